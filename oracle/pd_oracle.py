@@ -1,0 +1,410 @@
+"""NumPy restatement of the masked-component path (oracle only; float64 arithmetic).
+
+Every function cites the reference file it follows. Paths are relative to the
+reference repository root; `pd/` = `param_decomp/param_decomp/`.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+from scipy.special import erf
+
+from oracle import threefry
+
+ALPHA = 0.01
+SQRT1_2 = 1.0 / math.sqrt(2.0)
+INV_SQRT_2PI = 1.0 / math.sqrt(2.0 * math.pi)
+
+
+# ---------------------------------------------------------------- squashing
+def lower_leaky(x):
+    """`pd/core/ci_fn/squashing.py:8-14`: forward is `clip(x, 0, 1)`."""
+    return np.clip(x, 0.0, 1.0)
+
+
+def lower_leaky_vjp(x, g):
+    """`pd/core/ci_fn/squashing.py:17-19` (`_lhs_b`): leak `0.01*g` below zero only when
+    `g < 0`; pass `g` on (0, 1] (x=0 takes the lower branch, x=1 the middle); 0 above."""
+    leak = np.where(g < 0, ALPHA * g, 0.0)
+    return np.where(x <= 0, leak, np.where(x <= 1, g, 0.0))
+
+
+def upper_leaky(x):
+    """`pd/core/ci_fn/squashing.py:41-45`: `x>1 ? 1+0.01(x-1) : clip(x,0,1)`."""
+    return np.where(x > 1, 1 + ALPHA * (x - 1), np.clip(x, 0.0, 1.0))
+
+
+def upper_leaky_vjp(x, g):
+    """Plain autodiff of `upper_leaky` as JAX differentiates it: `where` routes the
+    cotangent; `clip` is `min(max(x, 0), 1)` and JAX's max/min JVP gives half the
+    cotangent to each operand at an exact tie, so x == 0 and x == 1 pass `0.5*g`."""
+    clip_grad = np.where((x > 0) & (x < 1), 1.0, np.where((x == 0) | (x == 1), 0.5, 0.0))
+    return np.where(x > 1, ALPHA * g, clip_grad * g)
+
+
+# ---------------------------------------------------------------- gate MLP (paper form)
+@dataclass
+class GateParams:
+    """Per-component gate MLP: `w_in, b_in, w_out` are `[C, H]`, `b_out` is `[C]`
+    (`papers/Stochastic_Parameter_Decomposition/spd_paper.md`, appendix "Architecture of
+    Causal Importance Function MLPs": one hidden GELU layer of width d_gate per
+    component, scalar input h_c, scalar output)."""
+
+    w_in: np.ndarray
+    b_in: np.ndarray
+    w_out: np.ndarray
+    b_out: np.ndarray
+
+
+def gelu(z):
+    """Exact (erf) GELU, the engine's choice (`pd/core/ci_fn/implementations/mlp.py:77`)."""
+    return 0.5 * z * (1.0 + erf(z * SQRT1_2))
+
+
+def gelu_grad(z):
+    return 0.5 * (1.0 + erf(z * SQRT1_2)) + z * INV_SQRT_2PI * np.exp(-0.5 * z * z)
+
+
+def gate_forward(h, p: GateParams):
+    """`g_raw[t,c] = b_out[c] + sum_j w_out[c,j] * GELU(w_in[c,j]*h[t,c] + b_in[c,j])`."""
+    z = h[..., None] * p.w_in + p.b_in
+    return np.sum(gelu(z) * p.w_out, axis=-1) + p.b_out
+
+
+def gate_backward(h, p: GateParams, dg_raw):
+    """VJP of `gate_forward`: returns (dh, dw_in, db_in, dw_out, db_out)."""
+    z = h[..., None] * p.w_in + p.b_in
+    lead = tuple(range(h.ndim - 1))
+    dz = dg_raw[..., None] * p.w_out * gelu_grad(z)
+    dh = np.sum(dz * p.w_in, axis=-1)
+    dw_in = np.sum(dz * h[..., None], axis=lead)
+    db_in = np.sum(dz, axis=lead)
+    dw_out = np.sum(dg_raw[..., None] * gelu(z), axis=lead)
+    db_out = np.sum(dg_raw, axis=lead)
+    return dh, dw_in, db_in, dw_out, db_out
+
+
+# ---------------------------------------------------------------- masks
+def component_mask(ci_lower, u):
+    """`pd/core/masking.py:135-136`: `m = g + (1 - g) * u`."""
+    return ci_lower + (1.0 - ci_lower) * u
+
+
+def site_keys(draw_key, site_idx: int, *, partitionable: bool = True):
+    """`pd/core/masking.py:148-167` (`materialize_masking`): `mask_key, delta_key =
+    split(draw_key)`, then `fold_in(., site_idx)` in CI insertion order."""
+    mask_key, delta_key = threefry.split(draw_key, 2, partitionable=partitionable)
+    return threefry.fold_in(mask_key, site_idx), threefry.fold_in(delta_key, site_idx)
+
+
+def draw_site_mask(ci_lower, draw_key, site_idx, dtype="bfloat16", *, with_delta=True, partitionable=True):
+    """Site mask and delta exactly as the toy targets draw them
+    (`pd/core/masking.py:162-167`; `pd/core/linear_plan.py:80-106`): uniforms in the CI
+    dtype, delta drops the trailing component axis."""
+    mk, dk = site_keys(draw_key, site_idx, partitionable=partitionable)
+    u = threefry.uniform(mk, ci_lower.shape, dtype, partitionable=partitionable)
+    m = component_mask(ci_lower, u)
+    d = threefry.uniform(dk, ci_lower.shape[:-1], dtype, partitionable=partitionable) if with_delta else None
+    return m, d, u
+
+
+# ---------------------------------------------------------------- decomposed linear
+def site_forward(x, W, V, U, mask, delta=None, route=None):
+    """`pd/core/decomposed_linear.py:142-175` with `:65-85`:
+    `where(route, ((x@V)*(m-d))@U + d*(x@W.T), x@W.T)`. Returns (output, x@V)."""
+    xV = x @ V
+    coef = mask if delta is None else mask - delta[..., None]
+    out = (xV * coef) @ U
+    if delta is None and route is None:
+        return out, xV
+    target = x @ W.T
+    blended = out if delta is None else out + delta[..., None] * target
+    if route is not None:
+        blended = np.where(route[..., None], blended, target)
+    return blended, xV
+
+
+def site_backward(x, W, V, U, mask, delta, route, dout):
+    """VJP of `site_forward` w.r.t. (x, V, U, mask) given the output cotangent."""
+    xV = x @ V
+    coef = mask if delta is None else mask - delta[..., None]
+    dcomp = dout if route is None else np.where(route[..., None], dout, 0.0)
+    acts = xV * coef
+    dU = acts.reshape(-1, acts.shape[-1]).T @ dcomp.reshape(-1, dcomp.shape[-1])
+    dacts = dcomp @ U.T
+    dmask = dacts * xV
+    dxV = dacts * coef
+    dV = x.reshape(-1, x.shape[-1]).T @ dxV.reshape(-1, dxV.shape[-1])
+    dx = dxV @ V.T
+    if delta is not None or route is not None:
+        dtarget = np.zeros_like(dout)
+        if delta is not None:
+            dtarget = dtarget + (dcomp * delta[..., None])
+        if route is not None:
+            dtarget = dtarget + np.where(route[..., None], 0.0, dout)
+        dx = dx + dtarget @ W
+    return dx, dV, dU, dmask
+
+
+# ---------------------------------------------------------------- losses
+def impmin_pnorm(ci_upper, p: float, eps: float = 0.0, beta: float = 0.0, world_size: int = 1):
+    """L_p importance minimality. Paper algorithm step 4
+    (`spd_paper.md`, "Algorithm"): `(1/B) sum_b sum_c |upper|^p`; with the `eps`/`beta`
+    extension of `nano_param_decomp/run.py:413-429`:
+    `sum_c [mean_c + beta*mean_c*log2(1 + sum_c*world_size)]`, values `(upper+eps)^p`."""
+    vals = (ci_upper + eps) ** p
+    flat = vals.reshape(-1, vals.shape[-1])
+    s = flat.sum(axis=0)
+    mean = s / flat.shape[0]
+    return float(np.sum(mean + beta * mean * np.log2(1.0 + s * world_size)))
+
+
+def impmin_pnorm_grad(ci_upper, p: float, eps: float = 0.0, beta: float = 0.0, world_size: int = 1):
+    """d impmin_pnorm / d ci_upper."""
+    vals = (ci_upper + eps) ** p
+    flat = vals.reshape(-1, vals.shape[-1])
+    n = flat.shape[0]
+    s = flat.sum(axis=0)
+    a = s * world_size
+    dsum = (1.0 / n) * (1.0 + beta * np.log2(1.0 + a)) + beta * (s / n) * world_size / ((1.0 + a) * math.log(2.0))
+    dvals = p * (ci_upper + eps) ** (p - 1.0)
+    return dvals * dsum
+
+
+def smooth_l0_psi(c, gamma: float, normalize_at_one: bool = False):
+    """`pd/core/losses.py:388-394`: `c^2/(c^2+gamma^2)` (times `1+gamma^2` when
+    normalized at one)."""
+    g2 = gamma * gamma
+    base = c * c / (c * c + g2)
+    return (1.0 + g2) * base if normalize_at_one else base
+
+
+def smooth_l0_psi_grad(c, gamma: float, normalize_at_one: bool = False):
+    g2 = gamma * gamma
+    d = 2.0 * c * g2 / (c * c + g2) ** 2
+    return (1.0 + g2) * d if normalize_at_one else d
+
+
+def importance_minimality_terms(ci_upper_sites, gamma, reference_datapoint_count=None, normalize_at_one=False):
+    """`pd/core/losses.py:462-485`: activity `sum_sites sum_c mean_t psi`, and the
+    frequency penalty `sum f*log2(1 + a'*f)` (`:375-386, 425-458`) when a reference
+    datapoint count is given."""
+    activity = 0.0
+    freq = 0.0
+    for v in ci_upper_sites:
+        f = smooth_l0_psi(v, gamma, normalize_at_one).reshape(-1, v.shape[-1]).mean(axis=0)
+        activity += float(f.sum())
+        if reference_datapoint_count is not None:
+            freq += float(np.sum(f * np.log2(1.0 + reference_datapoint_count * f)))
+    return activity, freq
+
+
+def mse(masked, clean):
+    """`pd/targets/tms.py:380-388`, `pd/targets/resid_mlp.py:411-418`:
+    `mean((masked - clean)^2)` in fp32."""
+    return float(np.mean((masked - clean) ** 2))
+
+
+def relative_squared_error(masked, clean):
+    """`pd/core/losses.py:60-76`: mean over positions of `|m-c|^2 / max(|c|^2, 1e-8)`."""
+    se = np.sum((masked - clean) ** 2, axis=-1)
+    sc = np.sum(clean**2, axis=-1)
+    return float(np.mean(se / np.maximum(sc, 1e-8)))
+
+
+def log_softmax(z):
+    z = z - z.max(axis=-1, keepdims=True)
+    return z - np.log(np.sum(np.exp(z), axis=-1, keepdims=True))
+
+
+def kl_per_position(masked_logits, clean_logits):
+    """`pd/core/losses.py:80-92`, `pd/targets/losses.py:50-60`: KL(clean || masked) per
+    position with the clean distribution frozen."""
+    lp = log_softmax(clean_logits)
+    lq = log_softmax(masked_logits)
+    return np.sum(np.exp(lp) * (lp - lq), axis=-1)
+
+
+def categorical_kl(masked_logits, clean_logits):
+    return float(np.mean(kl_per_position(masked_logits, clean_logits)))
+
+
+def categorical_kl_grad(masked_logits, clean_logits):
+    """d mean_pos KL / d masked_logits = (softmax(masked) - softmax(clean)) / n_pos."""
+    n = int(np.prod(masked_logits.shape[:-1]))
+    return (np.exp(log_softmax(masked_logits)) - np.exp(log_softmax(clean_logits))) / n
+
+
+# ---------------------------------------------------------------- dense fused step
+@dataclass
+class DenseStepResult:
+    loss: float
+    recon: float
+    imp: float
+    y: np.ndarray
+    h: np.ndarray
+    g_raw: np.ndarray
+    mask: np.ndarray
+    u: np.ndarray
+    delta: np.ndarray | None
+    dV: np.ndarray
+    dU: np.ndarray
+    dgate: tuple
+
+
+def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0, imp_coeff=1.0,
+                    recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True):
+    """One stochastic-recon + importance-minimality fwd+bwd for ONE decomposed site whose
+    input `x` is the clean input (the single-linear workload). It composes:
+    clean target `x@W.T` (`pd/core/train.py:578-606`, detached), CI gate on `h = x@V`
+    (paper form), lower/upper squashing (`pd/core/ci_fn/interface.py:35-41`), mask draw
+    (`pd/core/masking.py:148-167`), `site_forward`, MSE recon and p-norm imp-min, then
+    the gradients w.r.t. V, U and the gate parameters. The gate reads `h = x@V` with
+    `V` live, so dV carries both the masked product's and the gate's pullback
+    (`pd/core/train.py:624-655`: the CI VJP pulls back onto the prepared components)."""
+    T = x.shape[0]
+    y_t = x @ W.T
+    h = x @ V
+    g_raw = gate_forward(h, gate)
+    lo = lower_leaky(g_raw)
+    up = upper_leaky(g_raw)
+    m, d, u = draw_site_mask(lo, draw_key, site_idx, mask_dtype, with_delta=use_delta, partitionable=partitionable)
+    y, _ = site_forward(x, W, V, U, m, d, None)
+    recon = mse(y, y_t)
+    imp = impmin_pnorm(up, p)
+    loss = recon_coeff * recon + imp_coeff * imp
+    dy = recon_coeff * 2.0 * (y - y_t) / y.size
+    _, dV_direct, dU, dmask = site_backward(x, W, V, U, m, d, None, dy)
+    dlo = dmask * (1.0 - u)
+    dgraw = lower_leaky_vjp(g_raw, dlo)
+    dup = imp_coeff * impmin_pnorm_grad(up, p)
+    dgraw = dgraw + upper_leaky_vjp(g_raw, dup)
+    dh_gate, dwi, dbi, dwo, dbo = gate_backward(h, gate, dgraw)
+    dV = dV_direct + x.T @ dh_gate
+    del T
+    return DenseStepResult(loss, recon, imp, y, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo))
+
+
+# ---------------------------------------------------------------- MoE routing
+def softmax(z, axis=-1):
+    z = z - z.max(axis=axis, keepdims=True)
+    e = np.exp(z)
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+def select_experts(probs, k: int):
+    """`pd/targets/qwen36_moe.py:483-505`: the k most probable experts, descending,
+    lowest index on ties (a stable argsort of `-probs`)."""
+    order = np.argsort(-probs, axis=-1, kind="stable")
+    return order[..., :k].astype(np.int32)
+
+
+def expert_mixing_weights(probs, idx):
+    """`pd/targets/qwen36_moe.py:508-514`: gathered probabilities renormalized over k."""
+    sel = np.take_along_axis(probs, idx.astype(np.int64), axis=-1)
+    return sel / sel.sum(axis=-1, keepdims=True)
+
+
+@dataclass
+class RoutedJobs:
+    top_idx: np.ndarray
+    sort_idx: np.ndarray
+    inv_sort_idx: np.ndarray
+    group_sizes: np.ndarray
+
+
+def routed_jobs(top_idx, n_experts: int) -> RoutedJobs:
+    """`pd/routed/experts.py:115-123`: stable argsort of the flat expert-of-job vector,
+    its inverse permutation, and `bincount(length=E)`."""
+    flat = top_idx.reshape(-1)
+    sort_idx = np.argsort(flat, kind="stable").astype(np.int32)
+    inv = np.argsort(sort_idx, kind="stable").astype(np.int32)
+    sizes = np.bincount(flat, minlength=n_experts).astype(np.int32)
+    return RoutedJobs(top_idx, sort_idx, inv, sizes)
+
+
+def gather_tokens(x, jobs: RoutedJobs):
+    """`pd/routed/experts.py:127-166`: `x[sort_idx // k]`."""
+    k = jobs.top_idx.shape[-1]
+    return x[jobs.sort_idx // k]
+
+
+def gather_tokens_vjp(grad, jobs: RoutedJobs):
+    """`pd/routed/experts.py:135-138`: inverse gather plus a sum over the k slots."""
+    k = jobs.top_idx.shape[-1]
+    return grad[jobs.inv_sort_idx].reshape(-1, k, grad.shape[-1]).sum(axis=1)
+
+
+def unsort_jobs(y, jobs: RoutedJobs):
+    """`pd/routed/experts.py:169-172`: `y[inv_sort_idx]` reshaped `[T, k, n]`."""
+    T, k = jobs.top_idx.shape
+    return y[jobs.inv_sort_idx].reshape(T, k, y.shape[-1])
+
+
+def sort_jobs(values, jobs: RoutedJobs):
+    """`pd/routed/experts.py:175-178`."""
+    return values.reshape(-1)[jobs.sort_idx]
+
+
+def sort_job_values(values, jobs: RoutedJobs):
+    """`pd/routed/experts.py:192-199`: `[T, k, n]` rows in expert-sorted job order."""
+    T, k = jobs.top_idx.shape
+    return values.reshape(T * k, -1)[jobs.sort_idx]
+
+
+def sum_jobs(y, jobs: RoutedJobs):
+    """`pd/routed/experts.py:202-206`: fp32 sum over each token's k job rows."""
+    return unsort_jobs(y, jobs).sum(axis=1)
+
+
+def combine_jobs(y, jobs: RoutedJobs, weights):
+    """`pd/routed/experts.py:351-359`: routing-weighted fp32 sum over the k job rows."""
+    return (unsort_jobs(y, jobs) * weights[..., None]).sum(axis=1)
+
+
+def grouped_matmul(lhs, rhs, group_sizes):
+    """`pd/routed/experts.py:326-348` (`jax.lax.ragged_dot` semantics): the e-th
+    contiguous `group_sizes[e]`-row block of `lhs` times `rhs[e]`. Rows beyond
+    `sum(group_sizes)` are zero."""
+    out = np.zeros((lhs.shape[0], rhs.shape[-1]), dtype=np.float64)
+    start = 0
+    for e, n in enumerate(group_sizes):
+        n = int(n)
+        out[start:start + n] = lhs[start:start + n] @ rhs[e]
+        start += n
+    return out
+
+
+def transposed_grouped_matmul(lhs, dout, group_sizes):
+    """`pd/routed/experts.py:209-280`: `out[e] = lhs[block_e].T @ dout[block_e]`; empty
+    groups are exactly zero."""
+    E = len(group_sizes)
+    out = np.zeros((E, lhs.shape[1], dout.shape[1]), dtype=np.float64)
+    start = 0
+    for e, n in enumerate(group_sizes):
+        n = int(n)
+        if n:
+            out[e] = lhs[start:start + n].T @ dout[start:start + n]
+        start += n
+    return out
+
+
+def fold_routing_weights(gate, up, weights):
+    """`pd/targets/qwen36_moe.py:2272-2282`: `silu(gate) * up * weight` in fp32."""
+    return gate / (1.0 + np.exp(-gate)) * up * weights
+
+
+def routed_decomposed_site(x_jobs, V, U, group_sizes, mask_jobs, delta_jobs=None, frozen=None):
+    """One decomposed expert site in job space, `pd/targets/qwen36_moe.py:2790-2818`:
+    `acts = gmm(x_jobs, V) * (mask - delta)`; `out = gmm(acts, U) [+ delta*gmm(x, W)]`.
+    V is `[E, d_in, c]`, U is `[E, c, d_out]`, mask_jobs `[J, c]`, delta_jobs `[J]`."""
+    h = grouped_matmul(x_jobs, V, group_sizes)
+    coef = mask_jobs if delta_jobs is None else mask_jobs - delta_jobs[:, None]
+    acts = h * coef
+    out = grouped_matmul(acts, U, group_sizes)
+    if delta_jobs is not None:
+        out = out + delta_jobs[:, None] * grouped_matmul(x_jobs, frozen, group_sizes)
+    return out, h
