@@ -1,0 +1,206 @@
+/*
+ * pd_mi355x.h — C ABI of the MI355X (gfx950) masked-component kernels.
+ *
+ * The reference (goodfire-ai/param-decomp) is Python/JAX with no FFI layer; its seams
+ * are Python functions. Each entry point below replaces the arithmetic of one of those
+ * seams and cites it (paths relative to the reference root, pd/ =
+ * param_decomp/param_decomp/). A jax.ffi custom-call handler or a ctypes stub binds
+ * them one to one.
+ *
+ * Conventions (every entry point):
+ *  - All tensor arguments are DEVICE pointers owned by the caller; outputs are
+ *    preallocated by the caller. Row-major, densely packed unless a leading dimension
+ *    is given. Entry points that need scratch take a caller-provided `workspace` whose
+ *    size comes from the matching *_workspace_size query; nothing allocates.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Calls only enqueue work;
+ *    none synchronizes the host.
+ *  - Return PD_OK (0) or a PD_E* code; pd_last_error() gives the message (thread-local).
+ *    Invalid shapes are rejected on the host before any launch.
+ *  - Random keys are JAX threefry2x32 key words (k0, k1) as jax.random.PRNGKey /
+ *    split / fold_in produce them; draws follow jax.random.uniform in the chosen
+ *    counter layout.
+ */
+#ifndef PD_MI355X_H
+#define PD_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PD_OK 0
+#define PD_EINVAL 1
+#define PD_ELAUNCH 2
+#define PD_EUNSUPPORTED 3
+#define PD_EWORKSPACE 4
+
+#define PD_DTYPE_F32 0
+#define PD_DTYPE_BF16 1
+
+#define PD_LAYOUT_PARTITIONABLE 0 /* jax_threefry_partitionable=True (JAX >= 0.5 default) */
+#define PD_LAYOUT_ORIGINAL 1
+
+#define PD_IMPMIN_PNORM 0     /* (upper+eps)^p, paper / nano_param_decomp/run.py:413-429 */
+#define PD_IMPMIN_SMOOTH_L0 1 /* c^2/(c^2+gamma^2), pd/core/losses.py:388-394 */
+
+const char* pd_last_error(void);
+int pd_abi_version(void);
+
+/* ---- mask draw: jax.random.uniform (pd/core/linear_plan.py:80-106 uniform_like) ---- */
+/* out[i] = uniform(key)[i], i < n, drawn in draw_dtype, stored in out_dtype. */
+int pd_uniform(uint32_t k0, uint32_t k1, int64_t n, int draw_dtype, int layout, void* out, int out_dtype,
+               void* stream);
+
+/* ---- squashing: pd/core/ci_fn/squashing.py:8-45, CI.from_preactivations
+ *      (pd/core/ci_fn/interface.py:35-41). lower/upper may be NULL. ---- */
+int pd_squash_fwd(const void* pre, int dtype, int64_t n, void* lower, void* upper, void* stream);
+/* d_pre = lower_vjp(pre, g_lower) + upper_vjp(pre, g_upper); either g may be NULL. */
+int pd_squash_bwd(const void* pre, const void* g_lower, const void* g_upper, int dtype, int64_t n, void* d_pre,
+                  void* stream);
+
+/* ---- component mask: pd/core/masking.py:135-136 sample_component_mask
+ *      m = ci + (1-ci)*uniform(key, ci.shape, draw_dtype). ---- */
+int pd_component_mask_fwd(const void* ci, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype,
+                          int layout, void* mask, void* stream);
+/* d_ci = g_mask * (1 - u). */
+int pd_component_mask_bwd(const void* g_mask, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype,
+                          int layout, void* d_ci, void* stream);
+
+/* ---- per-component gate MLP (paper form, spd_paper.md appendix; engine GELU is exact
+ *      erf, pd/core/ci_fn/implementations/mlp.py:77):
+ *      g_raw[r,c] = b_out[c] + sum_j w_out[c,j]*GELU(w_in[c,j]*h[r,c] + b_in[c,j]).
+ *      h is [rows, C] (dtype), params fp32 [C,H] / [C]; H must be 16. ---- */
+int pd_gate_fwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const float* w_in, const float* b_in,
+                const float* w_out, const float* b_out, int precise, float* g_raw, void* stream);
+size_t pd_gate_bwd_workspace_size(int64_t rows, int64_t C, int H);
+/* dh (dtype) and fp32 parameter grads (overwritten) from dg_raw (fp32). */
+int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const float* w_in, const float* b_in,
+                const float* w_out, const float* b_out, const float* dg_raw, int precise, void* dh, float* dw_in,
+                float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- importance minimality over ci_upper [rows, C] (pd/core/losses.py:357-485;
+ *      nano_param_decomp/run.py:413-429). kind PD_IMPMIN_PNORM uses (p, eps, beta,
+ *      world_size); PD_IMPMIN_SMOOTH_L0 uses gamma, normalize_at_one and, when
+ *      ref_count > 0, the frequency term. out[0] = activity, out[1] = frequency term
+ *      (fp32, overwritten). grad (nullable, dtype of ci) = coeff_act*d act/d ci +
+ *      coeff_freq*d freq/d ci. ---- */
+size_t pd_impmin_workspace_size(int64_t rows, int64_t C);
+int pd_impmin(const void* ci_upper, int dtype, int64_t rows, int64_t C, int kind, float p, float eps, float beta,
+              float world_size, float gamma, int normalize_at_one, float ref_count, float coeff_act,
+              float coeff_freq, float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- recon losses ----
+ * MSE: pd/targets/tms.py:380-388, pd/targets/resid_mlp.py:411-418: mean((a-b)^2).
+ * out[0] = loss; grad_a (nullable, dtype) = coeff * 2(a-b)/n. */
+size_t pd_mse_workspace_size(int64_t n);
+int pd_mse(const void* a, const void* b, int dtype, int64_t n, float coeff, float* out, void* grad_a, void* workspace,
+           size_t workspace_bytes, void* stream);
+/* KL(clean || masked) per position, averaged over rows (pd/core/losses.py:80-92,
+ * pd/targets/losses.py:50-60). logits are [rows, V]; grad (nullable, dtype) =
+ * coeff * (softmax(masked) - softmax(clean)) / rows. */
+size_t pd_kl_workspace_size(int64_t rows);
+int pd_kl(const void* masked_logits, const void* clean_logits, int dtype, int64_t rows, int64_t vocab, float coeff,
+          float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- GEMM: C[M,N] = alpha * op(A) @ op(B) + beta * C, fp32 accumulation.
+ *      dtype PD_DTYPE_BF16 runs bf16 MFMA (A/B bf16; C bf16 or fp32 via c_dtype);
+ *      PD_DTYPE_F32 runs an fp32 kernel (A/B/C fp32). trans_a: A stored [K,M];
+ *      trans_b: B stored [N,K]. Backs every x@V, (xV*m)@U and their transposes in
+ *      site_forward (pd/core/decomposed_linear.py:142-175). ---- */
+int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B,
+            int64_t ldb, int trans_b, void* C, int64_t ldc, int c_dtype, float alpha, float beta, void* stream);
+
+/* ---- masked decomposed linear: pd/core/decomposed_linear.py:142-175 site_forward,
+ *      ((x@V)*(m-d))@U blended with d*(x@W^T) and route (:65-85).
+ *      x [T,d_in], V [d_in,C], U [C,d_out], W [d_out,d_in] (only read when delta or
+ *      route is given), mask [T,C], delta [T] (nullable), route [T] uint8 (nullable).
+ *      Outputs: out [T,d_out], xV [T,C]; acts [T,C] is the caller's residual buffer
+ *      holding (x@V)*(m-d) for the backward. ---- */
+int pd_masked_linear_fwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
+                         const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
+                         void* out, void* xV, void* acts, void* stream);
+/* VJP: given d_out_grad [T,d_out] -> dx [T,d_in] (nullable), dV, dU, dmask [T,C]
+ * (nullable). workspace holds two [T,C] and one [T,d_out] tensors of `dtype`. */
+size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, int64_t C);
+int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
+                         const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
+                         const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
+                         void* dmask, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- fused single-site stochastic-recon step (the dense hot path) ----
+ * One fwd+bwd of: clean target y_t = x@W^T (detached, pd/core/train.py:578-606);
+ * h = x@V; paper-form gate g_raw = gate(h); lower/upper squashing; mask
+ * m = lower + (1-lower)*uniform(mask key) (pd/core/masking.py:148-167); optional
+ * delta d = uniform(delta key, [T]); y = (h*(m-d))@U + d*y_t; recon = mean((y-y_t)^2);
+ * imp = sum_c mean_t (upper)^p; loss = recon_coeff*recon + imp_coeff*imp.
+ * Gradients (overwritten, fp32 for the fp32 masters): dV [d_in,C], dU [C,d_out], gate grads.
+ * losses[3] = {loss, recon, imp} fp32. mask_key / delta_key are the site's keys
+ * (already split/folded). dtype bf16: x,W,V,U bf16. */
+size_t pd_dense_step_workspace_size(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H);
+int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x, const void* W,
+                  const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
+                  const float* b_out, uint32_t mask_k0, uint32_t mask_k1, uint32_t delta_k0, uint32_t delta_k1,
+                  int use_delta, int draw_dtype, int layout, float p, float imp_coeff, float recon_coeff,
+                  float* losses, float* dV, float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* pd_dense_step with phase timing for measurement harnesses: `events` holds
+ * PD_DENSE_STEP_PHASES + 1 hipEvent_t handles recorded on `stream` at the phase
+ * boundaries: 0 target GEMM x@W^T, 1 GEMM h=x@V, 2 gate/mask fwd, 3 GEMM (h*m)@U,
+ * 4 recon residual, 5 loss finalize, 6 GEMM dU, 7 GEMM da=dy@U^T, 8 gate/mask bwd,
+ * 9 gate-grad reduce, 10 GEMM dV. Same arithmetic as pd_dense_step. */
+#define PD_DENSE_STEP_PHASES 11
+int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
+                        const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
+                        const float* w_out, const float* b_out, uint32_t mask_k0, uint32_t mask_k1,
+                        uint32_t delta_k0, uint32_t delta_k1, int use_delta, int draw_dtype, int layout, float p,
+                        float imp_coeff, float recon_coeff, float* losses, float* dV, float* dU, float* dw_in,
+                        float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes,
+                        void* stream, void** events);
+
+/* ---- MoE routing: pd/targets/qwen36_moe.py:473-514 (router softmax, select_experts
+ *      stable-descending lowest-index ties, expert_mixing_weights renormalized). ----
+ * logits [T,E] fp32 -> probs [T,E] fp32 (nullable), top_idx [T,k] int32,
+ * weights [T,k] fp32. E <= 64, k <= E. */
+int pd_router_topk(const float* logits, int64_t T, int E, int k, float* probs, int32_t* top_idx, float* weights,
+                   void* stream);
+
+/* ---- bucketing: pd/routed/experts.py:115-123 routed_jobs: sort_idx = stable argsort
+ *      of top_idx.reshape(-1), inv_sort_idx its inverse, group_sizes = bincount(E);
+ *      group_offsets [E+1] exclusive prefix (int32). Bit-exact, deterministic. ---- */
+size_t pd_routed_jobs_workspace_size(int64_t n_jobs, int E);
+int pd_routed_jobs(const int32_t* top_idx, int64_t T, int k, int E, int32_t* sort_idx, int32_t* inv_sort_idx,
+                   int32_t* group_sizes, int32_t* group_offsets, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* ---- job-space gathers (pd/routed/experts.py:127-206) ----
+ * out[j,:] = src[idx[j] / div, :] for j < n_out (gather_tokens: idx=sort_idx, div=k;
+ * sort_job_values / unsort: div=1). */
+int pd_gather_rows(const void* src, int dtype, int64_t width, const int32_t* idx, int div, int64_t n_out, void* out,
+                   void* stream);
+/* gather_tokens VJP (:135-138): out[t,:] = sum_s grad[inv_sort_idx[t*k+s], :]. */
+int pd_gather_rows_vjp(const void* grad, int dtype, int64_t width, const int32_t* inv_sort_idx, int64_t T, int k,
+                       void* out, void* stream);
+/* combine_jobs / sum_jobs (:202-206, :351-359): out[t,:] = sum_s w[t,s]*y[inv[t*k+s],:],
+ * fp32 accumulation; weights NULL = sum_jobs. */
+int pd_combine_jobs(const void* y, int dtype, int64_t width, const int32_t* inv_sort_idx, const float* weights,
+                    int64_t T, int k, void* out, void* stream);
+
+/* ---- grouped matmul: pd/routed/experts.py:326-348 grouped_matmul (backend "hip").
+ *      out[rows_e] = lhs[rows_e] @ rhs[e] over contiguous groups; rhs [E,K,N]
+ *      (trans_rhs=0) or [E,N,K] (trans_rhs=1, the d_input product). Rows past
+ *      sum(group_sizes) are zero-filled. group_offsets [E+1] from pd_routed_jobs.
+ *      bf16 operands, fp32 accumulation, out in out_dtype. ---- */
+int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* group_offsets, int64_t J, int E, int64_t K,
+                    int64_t N, int trans_rhs, void* out, int out_dtype, void* stream);
+/* transposed_grouped_matmul (:209-280): out[e] = lhs[rows_e]^T @ dout[rows_e],
+ * [E,K,N]; empty groups are exactly zero. */
+int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* group_offsets, int64_t J, int E, int64_t K,
+                       int64_t N, void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PD_MI355X_H */

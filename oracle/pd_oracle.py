@@ -255,8 +255,16 @@ class DenseStepResult:
     dgate: tuple
 
 
+def round_bf16(a):
+    """Round to bfloat16 (round-to-nearest-even), returned as float64."""
+    a32 = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    u = a32.view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
 def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0, imp_coeff=1.0,
-                    recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True):
+                    recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True, bf16_storage=False):
     """One stochastic-recon + importance-minimality fwd+bwd for ONE decomposed site whose
     input `x` is the clean input (the single-linear workload). It composes:
     clean target `x@W.T` (`pd/core/train.py:578-606`, detached), CI gate on `h = x@V`
@@ -264,28 +272,39 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     (`pd/core/masking.py:148-167`), `site_forward`, MSE recon and p-norm imp-min, then
     the gradients w.r.t. V, U and the gate parameters. The gate reads `h = x@V` with
     `V` live, so dV carries both the masked product's and the gate's pullback
-    (`pd/core/train.py:624-655`: the CI VJP pulls back onto the prepared components)."""
-    T = x.shape[0]
-    y_t = x @ W.T
-    h = x @ V
+    (`pd/core/train.py:624-655`: the CI VJP pulls back onto the prepared components).
+
+    `bf16_storage` rounds to bf16 every tensor the reference's bf16 compute stores in
+    bf16 (`pd/core/precision.py:9`; `pd/core/model.py:479-483` casts V/U to bf16, so
+    `x@V`, `(x@V)*coef`, `@U` and the clean output are bf16, and their cotangents come
+    back in bf16); products and reductions are exact (float64) in between. The gate
+    MLP itself is evaluated exactly on the bf16 `h` — finer than the reference's bf16
+    MLP arithmetic."""
+    rb = round_bf16 if bf16_storage else (lambda a: a)
+    y_t = rb(x @ W.T)
+    h = rb(x @ V)
     g_raw = gate_forward(h, gate)
     lo = lower_leaky(g_raw)
     up = upper_leaky(g_raw)
     m, d, u = draw_site_mask(lo, draw_key, site_idx, mask_dtype, with_delta=use_delta, partitionable=partitionable)
-    y, _ = site_forward(x, W, V, U, m, d, None)
-    recon = mse(y, y_t)
+    coef = m if d is None else m - d[:, None]
+    acts = rb(h * coef)
+    y = rb(acts @ U)
+    y_masked = y if d is None else y + d[:, None] * y_t
+    recon = mse(y_masked, y_t)
     imp = impmin_pnorm(up, p)
     loss = recon_coeff * recon + imp_coeff * imp
-    dy = recon_coeff * 2.0 * (y - y_t) / y.size
-    _, dV_direct, dU, dmask = site_backward(x, W, V, U, m, d, None, dy)
-    dlo = dmask * (1.0 - u)
+    dy = rb(recon_coeff * 2.0 * (y_masked - y_t) / y.size)
+    dU = acts.T @ dy
+    da = rb(dy @ U.T)
+    dh_direct = da * coef
+    dlo = da * h * (1.0 - u)
     dgraw = lower_leaky_vjp(g_raw, dlo)
     dup = imp_coeff * impmin_pnorm_grad(up, p)
     dgraw = dgraw + upper_leaky_vjp(g_raw, dup)
     dh_gate, dwi, dbi, dwo, dbo = gate_backward(h, gate, dgraw)
-    dV = dV_direct + x.T @ dh_gate
-    del T
-    return DenseStepResult(loss, recon, imp, y, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo))
+    dV = x.T @ rb(dh_direct + dh_gate)
+    return DenseStepResult(loss, recon, imp, y_masked, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo))
 
 
 # ---------------------------------------------------------------- MoE routing

@@ -1,0 +1,197 @@
+// Shared device helpers for the gfx950 masked-component kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/pd_mi355x.h"
+
+namespace pd {
+
+// ---------------------------------------------------------------- error state
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------- bf16
+typedef uint16_t bf16_t;
+
+__host__ __device__ inline float bf16_to_f32(bf16_t v) {
+  union {
+    uint32_t u;
+    float f;
+  } c;
+  c.u = (uint32_t)v << 16;
+  return c.f;
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__host__ __device__ inline bf16_t f32_to_bf16(float f) {
+  union {
+    uint32_t u;
+    float f;
+  } c;
+  c.f = f;
+  uint32_t u = c.u;
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T>
+__device__ inline float load_f(const T* p, int64_t i);
+template <>
+__device__ inline float load_f<float>(const float* p, int64_t i) {
+  return p[i];
+}
+template <>
+__device__ inline float load_f<bf16_t>(const bf16_t* p, int64_t i) {
+  return bf16_to_f32(p[i]);
+}
+template <typename T>
+__device__ inline void store_f(T* p, int64_t i, float v);
+template <>
+__device__ inline void store_f<float>(float* p, int64_t i, float v) {
+  p[i] = v;
+}
+template <>
+__device__ inline void store_f<bf16_t>(bf16_t* p, int64_t i, float v) {
+  p[i] = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------------------- Threefry-2x32-20
+// Salmon et al., SC'11; rotation constants (13,15,26,6,17,29,16,24), parity 0x1BD11BDA.
+__host__ __device__ inline uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+__host__ __device__ inline void threefry2x32(uint32_t k0, uint32_t k1, uint32_t& x0, uint32_t& x1) {
+  const uint32_t k2 = k0 ^ k1 ^ 0x1BD11BDAu;
+  x0 += k0;
+  x1 += k1;
+#define PD_TF_ROUND(r) \
+  x0 += x1;            \
+  x1 = rotl32(x1, r);  \
+  x1 ^= x0;
+  PD_TF_ROUND(13) PD_TF_ROUND(15) PD_TF_ROUND(26) PD_TF_ROUND(6)
+  x0 += k1; x1 += k2 + 1u;
+  PD_TF_ROUND(17) PD_TF_ROUND(29) PD_TF_ROUND(16) PD_TF_ROUND(24)
+  x0 += k2; x1 += k0 + 2u;
+  PD_TF_ROUND(13) PD_TF_ROUND(15) PD_TF_ROUND(26) PD_TF_ROUND(6)
+  x0 += k0; x1 += k1 + 3u;
+  PD_TF_ROUND(17) PD_TF_ROUND(29) PD_TF_ROUND(16) PD_TF_ROUND(24)
+  x0 += k1; x1 += k2 + 4u;
+  PD_TF_ROUND(13) PD_TF_ROUND(15) PD_TF_ROUND(26) PD_TF_ROUND(6)
+  x0 += k2; x1 += k0 + 5u;
+#undef PD_TF_ROUND
+}
+
+// Raw random bits of element `i` of an `n`-element jax.random draw of `nbits` (8 or
+// 32) under JAX's partitionable (PD_LAYOUT_PARTITIONABLE) or original counter layout.
+__device__ inline uint32_t draw_bits(uint32_t k0, uint32_t k1, int64_t i, int64_t n, int nbits, int layout) {
+  if (layout == PD_LAYOUT_PARTITIONABLE) {
+    uint32_t x0 = (uint32_t)((uint64_t)i >> 32), x1 = (uint32_t)i;
+    threefry2x32(k0, k1, x0, x1);
+    return x0 ^ x1;  // 8-bit draws keep the low byte
+  }
+  // original layout: the stream is threefry_2x32(key, iota(max_count))
+  int64_t max_count = (nbits == 32) ? n : (n + 3) / 4;
+  int64_t word = (nbits == 32) ? i : i / 4;
+  int64_t half = (max_count + 1) / 2;
+  uint32_t x0, x1;
+  bool first;
+  if (word < half) {
+    x0 = (uint32_t)word;
+    x1 = (half + word < max_count) ? (uint32_t)(half + word) : 0u;
+    first = true;
+  } else {
+    x0 = (uint32_t)(word - half);
+    x1 = (uint32_t)word;
+    first = false;
+  }
+  threefry2x32(k0, k1, x0, x1);
+  uint32_t w = first ? x0 : x1;
+  return (nbits == 32) ? w : (w >> (8 * (int)(i & 3)));
+}
+
+// jax.random.uniform's mantissa trick: fp32 keeps bits[31:9]; bf16 draws 8 bits and
+// keeps the top 7 of that byte.
+__device__ inline float bits_to_uniform(uint32_t b, int draw_dtype) {
+  return draw_dtype == PD_DTYPE_BF16 ? (float)((b & 0xFFu) >> 1) * (1.0f / 128.0f)
+                                     : (float)(b >> 9) * (1.0f / 8388608.0f);
+}
+
+__device__ inline float draw_uniform(uint32_t k0, uint32_t k1, int64_t i, int64_t n, int draw_dtype, int layout) {
+  return bits_to_uniform(draw_bits(k0, k1, i, n, draw_dtype == PD_DTYPE_BF16 ? 8 : 32, layout), draw_dtype);
+}
+
+// ---------------------------------------------------------------- squashing
+// lower: forward clip(x,0,1); VJP leaks 0.01*g below zero only for g<0.
+__device__ inline float lower_fwd(float x) { return fminf(fmaxf(x, 0.f), 1.f); }
+__device__ inline float lower_vjp(float x, float g) {
+  return x <= 0.f ? (g < 0.f ? 0.01f * g : 0.f) : (x <= 1.f ? g : 0.f);
+}
+// upper: x>1 ? 1+0.01(x-1) : clip(x,0,1); VJP of that expression under JAX autodiff
+// (clip's max/min split the cotangent evenly at exact ties x==0, x==1).
+__device__ inline float upper_fwd(float x) { return x > 1.f ? 1.f + 0.01f * (x - 1.f) : fminf(fmaxf(x, 0.f), 1.f); }
+__device__ inline float upper_vjp(float x, float g) {
+  float s = x > 1.f ? 0.01f : ((x > 0.f && x < 1.f) ? 1.f : ((x == 0.f || x == 1.f) ? 0.5f : 0.f));
+  return s * g;
+}
+
+// ---------------------------------------------------------------- GELU
+// Exact-erf GELU. PRECISE uses the device library's erff/expf. The fast form uses the
+// Abramowitz & Stegun 7.1.26 rational approximation of erf (|error| <= 1.5e-7), whose
+// exp(-z^2/2) factor is shared with the Gaussian density needed by the derivative.
+struct GeluOut {
+  float gelu, grad;
+};
+
+template <bool PRECISE>
+__device__ inline GeluOut gelu_and_grad(float z) {
+  if (PRECISE) {
+    float phi_cdf = 0.5f * (1.f + erff(z * 0.70710678118654752f));
+    float pdf = 0.39894228040143268f * expf(-0.5f * z * z);
+    return {z * phi_cdf, phi_cdf + z * pdf};
+  } else {
+    float az = fabsf(z) * 0.70710678118654752f;
+    float t = __frcp_rn(fmaf(0.3275911f, az, 1.f));
+    float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f),
+                          0.254829592f);
+    float e = __expf(-0.5f * z * z);
+    float q = 0.5f * poly * e;  // = 1 - Phi(|z|)
+    float phi_cdf = z >= 0.f ? 1.f - q : q;
+    return {z * phi_cdf, phi_cdf + z * (0.39894228040143268f * e)};
+  }
+}
+
+template <bool PRECISE>
+__device__ inline float gelu_only(float z) {
+  if (PRECISE) return 0.5f * z * (1.f + erff(z * 0.70710678118654752f));
+  float az = fabsf(z) * 0.70710678118654752f;
+  float t = __frcp_rn(fmaf(0.3275911f, az, 1.f));
+  float poly =
+      t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
+  float q = 0.5f * poly * __expf(-0.5f * z * z);
+  return z * (z >= 0.f ? 1.f - q : q);
+}
+
+// ---------------------------------------------------------------- reductions
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace pd

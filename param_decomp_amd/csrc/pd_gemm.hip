@@ -1,0 +1,352 @@
+// GEMM kernels for the masked-component path (gfx950).
+//
+// bf16 path: v_mfma_f32_32x32x16_bf16 on 128x128x64 block tiles, 4 waves (2x2) of
+// 64x64, LDS double-buffered through registers. LDS always holds both operands
+// K-contiguous ([rows][BK+pad]); an operand whose global layout is MN-contiguous is
+// transposed in registers (4 k-rows x 8 elements per thread) on its way into LDS, so
+// every MFMA fragment is one 16-byte LDS read.
+//
+// Three problem mappings share the kernel:
+//   DENSE     C = alpha*op(A)@op(B) + beta*C                  (x@V, acts@U, transposes)
+//   GROUPED   out[rows_e] = lhs[rows_e] @ rhs[e], ragged rows  (pd/routed/experts.py:326-348)
+//   GROUPED_K out[e] = lhs[rows_e]^T @ dout[rows_e]            (pd/routed/experts.py:209-280)
+// Group offsets live on the device; blocks locate their group by scanning them, so no
+// host synchronization is needed.
+#include <algorithm>
+
+#include "pd_common.hpp"
+
+namespace pd {
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short bf16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2 };
+
+constexpr int BM = 128, BN = 128, BK = 64, LDS_PAD = 8, LDS_STRIDE = BK + LDS_PAD;
+constexpr int GEMM_THREADS = 256;
+
+struct GemmArgs {
+  int64_t M, N, K;
+  const bf16_t* A;
+  int64_t lda;
+  const bf16_t* B;
+  int64_t ldb;
+  void* C;
+  int64_t ldc;
+  float alpha, beta;
+  const int32_t* offsets;  // [E+1] group offsets (grouped modes)
+  int E;
+  int64_t strideB;  // elements between consecutive groups' B (GROUPED)
+  int64_t strideC;  // elements between consecutive groups' C (GROUPED_K)
+};
+
+// Loads one operand tile (ROWS x BK, rows = M or N index) into registers.
+// KMAJ: global is [rows][K] (K contiguous): 4 chunks of 8 per thread.
+// !KMAJ: global is [K][rows] (rows contiguous): 4 k-rows x 8 rows per thread.
+template <bool KMAJ>
+struct TileLoader {
+  bf16x8 v[4];
+  __device__ inline void load(const bf16_t* __restrict__ g, int64_t ld, int64_t row0, int64_t nrows, int64_t k0,
+                              int64_t kmax, int tid) {
+    if (KMAJ) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int id = tid + GEMM_THREADS * i;
+        int r = id >> 3, kc = id & 7;
+        int64_t gr = row0 + r, gk = k0 + kc * 8;
+        if (gr < nrows && gk < kmax)
+          v[i] = *(const bf16x8*)(g + gr * ld + gk);
+        else
+          v[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    } else {
+      int rc = tid & 15, kg = tid >> 4;
+      int64_t gr = row0 + rc * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int64_t gk = k0 + kg * 4 + i;
+        if (gr < nrows && gk < kmax)
+          v[i] = *(const bf16x8*)(g + gk * ld + gr);
+        else
+          v[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+  }
+  __device__ inline void store(bf16_t* __restrict__ lds, int tid) {
+    if (KMAJ) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int id = tid + GEMM_THREADS * i;
+        int r = id >> 3, kc = id & 7;
+        *(bf16x8*)(lds + r * LDS_STRIDE + kc * 8) = v[i];
+      }
+    } else {
+      int rc = tid & 15, kg = tid >> 4;
+      // v[k][e]: k-row k, element e (row rc*8+e). Write row rc*8+e with its 4 k values.
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bf16x4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
+        *(bf16x4*)(lds + (rc * 8 + e) * LDS_STRIDE + kg * 4) = w;
+      }
+    }
+  }
+};
+
+template <typename TC>
+__device__ inline void store_out(TC* C, int64_t idx, float v, float beta);
+template <>
+__device__ inline void store_out<float>(float* C, int64_t idx, float v, float beta) {
+  C[idx] = beta != 0.f ? v + beta * C[idx] : v;
+}
+template <>
+__device__ inline void store_out<bf16_t>(bf16_t* C, int64_t idx, float v, float beta) {
+  C[idx] = f32_to_bf16(beta != 0.f ? v + beta * bf16_to_f32(C[idx]) : v);
+}
+
+template <bool A_KMAJ, bool B_KMAJ, typename TC, int MODE>
+__global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][(BM + BN) * LDS_STRIDE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int64_t M = p.M, N = p.N, K = p.K;
+  const bf16_t* A = p.A;
+  const bf16_t* B = p.B;
+  TC* C = (TC*)p.C;
+  int64_t m0 = (int64_t)blockIdx.y * BM;
+  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  int64_t kbeg = 0, kend = K;
+
+  if (MODE == MODE_GROUPED) {
+    // blockIdx.y enumerates row tiles over all groups in order
+    int64_t tile = blockIdx.y, acc = 0;
+    int e = 0;
+    for (; e < p.E; ++e) {
+      int64_t sz = p.offsets[e + 1] - p.offsets[e];
+      int64_t nt = (sz + BM - 1) / BM;
+      if (tile < acc + nt) break;
+      acc += nt;
+    }
+    if (e >= p.E) return;
+    int64_t off = p.offsets[e];
+    M = p.offsets[e + 1] < p.M ? p.offsets[e + 1] : p.M;  // absolute row bound, clamped to J
+    m0 = off + (tile - acc) * BM;
+    if (m0 < 0) return;
+    B = p.B + (int64_t)e * p.strideB;
+  } else if (MODE == MODE_GROUPED_K) {
+    int e = blockIdx.z;
+    kbeg = p.offsets[e] < 0 ? 0 : p.offsets[e];
+    kend = p.offsets[e + 1] < p.K ? p.offsets[e + 1] : p.K;  // clamped to J
+    if (kend < kbeg) kend = kbeg;
+    C = (TC*)p.C + (int64_t)e * p.strideC;
+  }
+  if (m0 >= M || n0 >= N) return;
+
+  TileLoader<A_KMAJ> la;
+  TileLoader<B_KMAJ> lb;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // grouped-K: K runs over absolute job rows [kbeg, kend); tiles start at kbeg
+  const int64_t nk = (kend - kbeg + BK - 1) / BK;
+  if (nk > 0) {
+    la.load(A, p.lda, m0, M, kbeg, kend, tid);
+    lb.load(B, p.ldb, n0, N, kbeg, kend, tid);
+    la.store(lds[0], tid);
+    lb.store(lds[0] + BM * LDS_STRIDE, tid);
+    __syncthreads();
+  }
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int s = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      int64_t k0 = kbeg + (kt + 1) * BK;
+      la.load(A, p.lda, m0, M, k0, kend, tid);
+      lb.load(B, p.ldb, n0, N, k0, kend, tid);
+    }
+    const bf16_t* As = lds[s];
+    const bf16_t* Bs = lds[s] + BM * LDS_STRIDE;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8 af[2], bfr[2];
+      const int kofs = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const bf16x8*)(As + (wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfr[j] = *(const bf16x8*)(Bs + (wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      la.store(lds[s ^ 1], tid);
+      lb.store(lds[s ^ 1] + BM * LDS_STRIDE, tid);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column (lane&31) and rows 8*(v/4) + 4*(lane>>5) + (v&3)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        int64_t row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row < M) store_out<TC>(C, row * p.ldc + col, p.alpha * acc[i][j][v], p.beta);
+      }
+    }
+}
+
+// fp32 kernel (fp32 toy configs): 64x64 tiles, 4x4 outputs per thread, any layout.
+constexpr int FT = 64, FK = 16;
+__global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
+                                                  int64_t lda, int ta, const float* __restrict__ B, int64_t ldb,
+                                                  int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta) {
+  __shared__ float As[FK][FT + 1], Bs[FK][FT + 1];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * FT, n0 = (int64_t)blockIdx.x * FT;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < K; k0 += FK) {
+    for (int e = tid; e < FK * FT; e += 256) {
+      int kk = e / FT, r = e % FT;
+      int64_t gm = m0 + r, gk = k0 + kk, gn = n0 + r;
+      As[kk][r] = (gm < M && gk < K) ? (ta ? A[gk * lda + gm] : A[gm * lda + gk]) : 0.f;
+      Bs[kk][r] = (gn < N && gk < K) ? (tb ? B[gn * ldb + gk] : B[gk * ldb + gn]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < FK; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int64_t r = m0 + ty * 4 + i, c = n0 + tx * 4 + j;
+      if (r < M && c < N) C[r * ldc + c] = alpha * acc[i][j] + (beta != 0.f ? beta * C[r * ldc + c] : 0.f);
+    }
+}
+
+__global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int64_t J, int64_t width, int out_bytes,
+                                 void* __restrict__ out) {
+  int64_t start = offsets[E];
+  int64_t n = (J - start) * width;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    if (out_bytes == 4)
+      ((float*)out)[start * width + i] = 0.f;
+    else
+      ((bf16_t*)out)[start * width + i] = 0;
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int MODE>
+static int launch_bf16(const GemmArgs& a, bool a_kmaj, bool b_kmaj, int c_dtype, dim3 grid, hipStream_t s) {
+#define PD_L(AK, BKM, TC) \
+  hipLaunchKernelGGL((k_gemm_bf16<AK, BKM, TC, MODE>), grid, dim3(GEMM_THREADS), 0, s, a)
+  if (c_dtype == PD_DTYPE_F32) {
+    if (a_kmaj && b_kmaj) PD_L(true, true, float);
+    else if (a_kmaj) PD_L(true, false, float);
+    else if (b_kmaj) PD_L(false, true, float);
+    else PD_L(false, false, float);
+  } else {
+    if (a_kmaj && b_kmaj) PD_L(true, true, bf16_t);
+    else if (a_kmaj) PD_L(true, false, bf16_t);
+    else if (b_kmaj) PD_L(false, true, bf16_t);
+    else PD_L(false, false, bf16_t);
+  }
+#undef PD_L
+  return check_launch("pd_gemm bf16");
+}
+
+// host-side validation of a bf16 operand: contiguous dim a multiple of 8 elements,
+// leading dim a multiple of 8, 16-byte aligned base.
+static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) {
+  return aligned16(ptr) && ld % 8 == 0 && contig_extent % 8 == 0;
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+extern "C" {
+
+int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B,
+            int64_t ldb, int trans_b, void* C, int64_t ldc, int c_dtype, float alpha, float beta, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || !A || !B || !C) return fail(PD_EINVAL, "pd_gemm: bad args");
+  if (M == 0 || N == 0) return PD_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (cdiv(M, FT) > 65535 || cdiv(N, FT) > 0x7FFFFFFFLL) return fail(PD_EUNSUPPORTED, "pd_gemm: too large");
+  if (dtype == PD_DTYPE_F32) {
+    if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm: fp32 path writes fp32");
+    dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT));
+    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, M, N, K, (const float*)A, lda, trans_a, (const float*)B,
+                       ldb, trans_b, (float*)C, ldc, alpha, beta);
+    return check_launch("pd_gemm f32");
+  }
+  if (dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_gemm: dtype");
+  bool a_kmaj = !trans_a, b_kmaj = trans_b;
+  if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N))
+    return fail(PD_EUNSUPPORTED, "pd_gemm: bf16 operands need 16B alignment and contiguous dims / ld % 8 == 0");
+  GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, 0, 0};
+  dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM));
+  return launch_bf16<MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype, grid, s);
+}
+
+int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
+                    int trans_rhs, void* out, int out_dtype, void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs || !rhs || !offsets || !out)
+    return fail(PD_EINVAL, "pd_grouped_gemm: bad args");
+  if (J == 0) return PD_OK;
+  bool b_kmaj = trans_rhs != 0;
+  if (!bf16_operand_ok(lhs, K, K) || !bf16_operand_ok(rhs, b_kmaj ? K : N, b_kmaj ? K : N))
+    return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: K and N must be multiples of 8 with 16B-aligned bases");
+  hipStream_t s = (hipStream_t)stream;
+  // zero rows past sum(group_sizes) (ragged_dot leaves them 0)
+  hipLaunchKernelGGL(k_zero_tail_rows, dim3(256), dim3(256), 0, s, offsets, E, J, N,
+                     out_dtype == PD_DTYPE_F32 ? 4 : 2, out);
+  GemmArgs a{J, N, K, (const bf16_t*)lhs, K, (const bf16_t*)rhs, b_kmaj ? K : N, out, N, 1.f, 0.f, offsets, E,
+             K * N, 0};
+  int64_t max_tiles = cdiv(J, BM) + E;
+  if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: too many rows");
+  dim3 grid((unsigned)cdiv(N, BN), (unsigned)max_tiles);
+  return launch_bf16<MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
+}
+
+int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets, int64_t J, int E, int64_t K,
+                       int64_t N, void* out, int out_dtype, void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs || !dout || !offsets || !out)
+    return fail(PD_EINVAL, "pd_grouped_gemm_dw: bad args");
+  if (!bf16_operand_ok(lhs, K, K) || !bf16_operand_ok(dout, N, N))
+    return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw: K and N must be multiples of 8 with 16B-aligned bases");
+  if (E > 65535 || cdiv(K, BM) > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw: E or K too large");
+  // out[e] (M=K_in x N) = lhs[rows_e]^T (A stored [J,K]: M-contiguous) @ dout[rows_e] ([J,N])
+  GemmArgs a{K, N, J, (const bf16_t*)lhs, K, (const bf16_t*)dout, N, out, N, 1.f, 0.f, offsets, E, 0, K * N};
+  dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(K, BM), (unsigned)E);
+  return launch_bf16<MODE_GROUPED_K>(a, false, false, out_dtype, grid, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+// MoE routing, deterministic bucketing and job-space gathers (gfx950).
+//
+//   pd_router_topk      softmax + select_experts + expert_mixing_weights
+//                       (pd/targets/qwen36_moe.py:473-514)
+//   pd_routed_jobs      stable argsort by expert, inverse, bincount
+//                       (pd/routed/experts.py:115-123) as a three-phase counting sort
+//   pd_gather_rows(_vjp), pd_combine_jobs   (pd/routed/experts.py:127-206, 351-359)
+#include "pd_common.hpp"
+
+namespace pd {
+
+// One wave per token, lane e holds expert e. Top-k by k rounds of a wave argmax that
+// prefers the larger probability and, on equal probabilities, the lower index — the
+// order of a stable descending sort.
+__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int64_t T, int E, int k,
+                                                     float* __restrict__ probs, int32_t* __restrict__ top_idx,
+                                                     float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float x = lane < E ? logits[t * E + lane] : -INFINITY;
+  float mx = wave_max(x);
+  float ex = lane < E ? expf(x - mx) : 0.f;
+  float z = wave_sum(ex);
+  float p = ex / z;
+  if (probs && lane < E) probs[t * E + lane] = p;
+  float cand = lane < E ? p : -INFINITY;
+  float sel_sum = 0.f, my_w = 0.f;
+  for (int s = 0; s < k; ++s) {
+    float bv = cand;
+    int bi = lane;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      float ov = __shfl_xor(bv, off, 64);
+      int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi >= E) bi = E - 1;  // only reachable with NaN probabilities
+    if (lane == bi) cand = -INFINITY;
+    if (lane == s) my_w = bv;
+    sel_sum += bv;
+    if (lane == 0) top_idx[t * k + s] = bi;
+  }
+  if (lane < k) weights[t * k + lane] = my_w / sel_sum;
+}
+
+// ---- counting sort. Phase 1: per-chunk histograms.
+constexpr int SORT_CHUNK = 2048;
+constexpr int SORT_MAX_E = 1024;
+
+// Expert ids outside [0, E) (only possible from corrupt routing input) are clamped
+// into range identically in every phase, so positions stay a permutation of [0, n).
+__device__ inline int clamp_key(int k, int E) { return k < 0 ? 0 : (k >= E ? E - 1 : k); }
+
+__global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ keys, int64_t n, int E,
+                                                   int32_t* __restrict__ counts) {
+  __shared__ int32_t h[SORT_MAX_E];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) h[e] = 0;
+  __syncthreads();
+  int64_t j0 = (int64_t)blockIdx.x * SORT_CHUNK;
+  for (int64_t j = j0 + threadIdx.x; j < n && j < j0 + SORT_CHUNK; j += blockDim.x)
+    atomicAdd(&h[clamp_key(keys[j], E)], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) counts[(int64_t)blockIdx.x * E + e] = h[e];
+}
+
+// Phase 2 (one block): group sizes, exclusive group offsets, and each chunk's base
+// position per expert (in place over counts).
+__global__ __launch_bounds__(1024) void k_sort_scan(int32_t* __restrict__ counts, int64_t nchunks, int E,
+                                                    int32_t* __restrict__ group_sizes,
+                                                    int32_t* __restrict__ group_offsets) {
+  __shared__ int32_t tot[SORT_MAX_E + 1];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int32_t s = 0;
+    for (int64_t b = 0; b < nchunks; ++b) {
+      int32_t c = counts[b * E + e];
+      counts[b * E + e] = s;  // exclusive prefix over chunks
+      s += c;
+    }
+    tot[e] = s;
+    group_sizes[e] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t acc = 0;
+    for (int e = 0; e < E; ++e) {
+      int32_t c = tot[e];
+      tot[e] = acc;
+      group_offsets[e] = acc;
+      acc += c;
+    }
+    group_offsets[E] = acc;
+    tot[E] = acc;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    for (int64_t b = 0; b < nchunks; ++b) counts[b * E + e] += tot[e];
+}
+
+// Phase 3: one wave per chunk walks it in 64-job steps; each lane's position is its
+// chunk base + the running count of its expert + the number of earlier lanes in the
+// step with the same expert. Stable by construction.
+__global__ __launch_bounds__(64) void k_sort_scatter(const int32_t* __restrict__ keys, int64_t n, int E,
+                                                     const int32_t* __restrict__ base, int32_t* __restrict__ sort_idx,
+                                                     int32_t* __restrict__ inv_sort_idx) {
+  __shared__ int32_t run[SORT_MAX_E];
+  __shared__ int32_t step_keys[64];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)blockIdx.x * E + e];
+  __syncthreads();
+  int64_t j0 = (int64_t)blockIdx.x * SORT_CHUNK;
+  int64_t j1 = j0 + SORT_CHUNK < n ? j0 + SORT_CHUNK : n;
+  for (int64_t s0 = j0; s0 < j1; s0 += 64) {
+    int64_t j = s0 + lane;
+    int key = j < j1 ? clamp_key(keys[j], E) : -1;
+    step_keys[lane] = key;
+    __syncthreads();
+    int before = 0;
+    for (int i = 0; i < lane; ++i) before += (step_keys[i] == key);
+    if (j < j1) {
+      int32_t pos = run[key] + before;
+      sort_idx[pos] = (int32_t)j;
+      inv_sort_idx[j] = pos;
+    }
+    __syncthreads();
+    // advance running counters: the last lane holding each expert adds its count
+    if (j < j1) {
+      bool last = true;
+      for (int i = lane + 1; i < 64 && s0 + i < j1; ++i)
+        if (step_keys[i] == key) {
+          last = false;
+          break;
+        }
+      if (last) run[key] += before + 1;
+    }
+    __syncthreads();
+  }
+}
+
+// ---- gathers (16-byte vectors when rows allow it)
+template <typename T>
+__global__ void k_gather_rows(const T* __restrict__ src, int64_t width, const int32_t* __restrict__ idx, int div,
+                              int64_t n_out, T* __restrict__ out) {
+  for (int64_t r = blockIdx.x; r < n_out; r += gridDim.x) {
+    int64_t srow = idx[r] / div;
+    const T* s = src + srow * width;
+    T* d = out + r * width;
+    if ((width * (int64_t)sizeof(T)) % 16 == 0 && ((uintptr_t)src % 16 == 0) && ((uintptr_t)out % 16 == 0)) {
+      int64_t nv = width * (int64_t)sizeof(T) / 16;
+      for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) ((uint4*)d)[i] = ((const uint4*)s)[i];
+    } else {
+      for (int64_t i = threadIdx.x; i < width; i += blockDim.x) d[i] = s[i];
+    }
+  }
+}
+
+template <typename T>
+__global__ void k_combine(const T* __restrict__ y, int64_t width, const int32_t* __restrict__ inv,
+                          const float* __restrict__ w, int64_t T_, int k, T* __restrict__ out) {
+  for (int64_t t = blockIdx.x; t < T_; t += gridDim.x) {
+    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
+      float acc = 0.f;
+      for (int s = 0; s < k; ++s) {
+        float v = load_f<T>(y, (int64_t)inv[t * k + s] * width + i);
+        acc = w ? fmaf(w[t * k + s], v, acc) : acc + v;
+      }
+      store_f<T>(out, t * width + i, acc);
+    }
+  }
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+extern "C" {
+
+int pd_router_topk(const float* logits, int64_t T, int E, int k, float* probs, int32_t* top_idx, float* weights,
+                   void* stream) {
+  if (T < 0 || E <= 0 || E > 64 || k <= 0 || k > E || !logits || !top_idx || !weights)
+    return fail(PD_EINVAL, "pd_router_topk: need 0 < k <= E <= 64");
+  if (T == 0) return PD_OK;
+  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T, E, k,
+                     probs, top_idx, weights);
+  return check_launch("pd_router_topk");
+}
+
+size_t pd_routed_jobs_workspace_size(int64_t n_jobs, int E) {
+  return (size_t)cdiv(n_jobs, SORT_CHUNK) * (size_t)E * sizeof(int32_t);
+}
+
+int pd_routed_jobs(const int32_t* top_idx, int64_t T, int k, int E, int32_t* sort_idx, int32_t* inv_sort_idx,
+                   int32_t* group_sizes, int32_t* group_offsets, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  if (T < 0 || k <= 0 || E <= 0 || E > SORT_MAX_E || !top_idx || !sort_idx || !inv_sort_idx || !group_sizes ||
+      !group_offsets)
+    return fail(PD_EINVAL, "pd_routed_jobs: bad args (E <= 1024)");
+  int64_t n = T * k;
+  if (n > 0x7FFFFFFF) return fail(PD_EUNSUPPORTED, "pd_routed_jobs: too many jobs");
+  if (!workspace || workspace_bytes < pd_routed_jobs_workspace_size(n, E))
+    return fail(PD_EWORKSPACE, "pd_routed_jobs: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  int64_t nchunks = cdiv(n, SORT_CHUNK);
+  int32_t* counts = (int32_t*)workspace;
+  if (nchunks > 0) hipLaunchKernelGGL(k_sort_hist, dim3((unsigned)nchunks), dim3(256), 0, s, top_idx, n, E, counts);
+  hipLaunchKernelGGL(k_sort_scan, dim3(1), dim3(1024), 0, s, counts, nchunks, E, group_sizes, group_offsets);
+  if (nchunks > 0)
+    hipLaunchKernelGGL(k_sort_scatter, dim3((unsigned)nchunks), dim3(64), 0, s, top_idx, n, E, counts, sort_idx,
+                       inv_sort_idx);
+  return check_launch("pd_routed_jobs");
+}
+
+int pd_gather_rows(const void* src, int dtype, int64_t width, const int32_t* idx, int div, int64_t n_out, void* out,
+                   void* stream) {
+  if (width <= 0 || n_out < 0 || div <= 0 || !src || !idx || !out) return fail(PD_EINVAL, "pd_gather_rows: bad args");
+  if (n_out == 0) return PD_OK;
+  unsigned blocks = (unsigned)std::min<int64_t>(n_out, 65535);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PD_DTYPE_F32)
+    hipLaunchKernelGGL(k_gather_rows<float>, dim3(blocks), dim3(128), 0, s, (const float*)src, width, idx, div, n_out,
+                       (float*)out);
+  else if (dtype == PD_DTYPE_BF16)
+    hipLaunchKernelGGL(k_gather_rows<bf16_t>, dim3(blocks), dim3(128), 0, s, (const bf16_t*)src, width, idx, div,
+                       n_out, (bf16_t*)out);
+  else
+    return fail(PD_EINVAL, "pd_gather_rows: dtype");
+  return check_launch("pd_gather_rows");
+}
+
+int pd_combine_jobs(const void* y, int dtype, int64_t width, const int32_t* inv, const float* weights, int64_t T,
+                    int k, void* out, void* stream) {
+  if (width <= 0 || T < 0 || k <= 0 || !y || !inv || !out) return fail(PD_EINVAL, "pd_combine_jobs: bad args");
+  if (T == 0) return PD_OK;
+  unsigned blocks = (unsigned)std::min<int64_t>(T, 65535);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PD_DTYPE_F32)
+    hipLaunchKernelGGL(k_combine<float>, dim3(blocks), dim3(256), 0, s, (const float*)y, width, inv, weights, T, k,
+                       (float*)out);
+  else if (dtype == PD_DTYPE_BF16)
+    hipLaunchKernelGGL(k_combine<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)y, width, inv, weights, T, k,
+                       (bf16_t*)out);
+  else
+    return fail(PD_EINVAL, "pd_combine_jobs: dtype");
+  return check_launch("pd_combine_jobs");
+}
+
+int pd_gather_rows_vjp(const void* grad, int dtype, int64_t width, const int32_t* inv, int64_t T, int k, void* out,
+                       void* stream) {
+  return pd_combine_jobs(grad, dtype, width, inv, nullptr, T, k, out, stream);
+}
+
+}  // extern "C"

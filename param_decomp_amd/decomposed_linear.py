@@ -1,0 +1,114 @@
+"""The decomposed-linear primitive on the GPU: `((x@V)*(m-d))@U + d*(x@W^T)`.
+
+Mirrors `param_decomp/param_decomp/core/decomposed_linear.py`:
+- `SiteWeights(W, V, U)` (`:96-107`; the placement fields are single-GPU and absent),
+- `site_forward(x, weights, mask, delta, route) -> SiteForward(output,
+  component_activation)` (`:142-175`), `site_out` (`:178-181`),
+- `component_coefficients` / `blend_target_output` semantics (`:65-85`): `delta` and
+  `route` carry the leading axes only; None is the identity (d = 0, every position
+  routed) and skips the target product.
+
+`site_forward` is differentiable w.r.t. x, V, U and mask (W is frozen; delta and route
+are samples). Forward and backward run as bf16 (or fp32) MFMA GEMMs through the C ABI.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from param_decomp_amd import _lib as L
+
+
+@dataclass(frozen=True)
+class SiteWeights:
+    W: torch.Tensor  # [d_out, d_in]
+    V: torch.Tensor  # [d_in, C]
+    U: torch.Tensor  # [C, d_out]
+
+
+@dataclass(frozen=True)
+class SiteForward:
+    output: torch.Tensor
+    component_activation: torch.Tensor
+
+
+def component_coefficients(mask: torch.Tensor, delta: torch.Tensor | None) -> torch.Tensor:
+    return mask if delta is None else mask - delta
+
+
+class _MaskedLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, V, U, mask, W, delta, route):
+        lead = x.shape[:-1]
+        T = int(math.prod(lead))
+        d_in, C = V.shape
+        d_out = U.shape[1]
+        dt = L.dtype_code(x.dtype)
+        x2 = x.reshape(T, d_in).contiguous()
+        m2 = mask.reshape(T, C).contiguous()
+        d2 = None if delta is None else delta.reshape(T).to(x.dtype).contiguous()
+        r2 = None if route is None else route.reshape(T).to(torch.uint8).contiguous()
+        Wc = None if W is None else W.contiguous()
+        out = torch.empty((T, d_out), dtype=x.dtype, device=x.device)
+        xV = torch.empty((T, C), dtype=x.dtype, device=x.device)
+        acts = torch.empty((T, C), dtype=x.dtype, device=x.device)
+        L.call("pd_masked_linear_fwd", dt, T, d_in, d_out, C, L.ptr(x2), L.ptr(V.contiguous()), L.ptr(U.contiguous()),
+               L.ptr(Wc), L.ptr(m2), L.ptr(d2), L.ptr(r2), L.ptr(out), L.ptr(xV), L.ptr(acts), L.stream())
+        ctx.save_for_backward(x2, V, U, m2, Wc if Wc is not None else torch.empty(0, device=x.device),
+                              d2 if d2 is not None else torch.empty(0, device=x.device),
+                              r2 if r2 is not None else torch.empty(0, device=x.device), xV, acts)
+        ctx.has = (W is not None, delta is not None, route is not None)
+        ctx.lead = lead
+        ctx.set_materialize_grads(False)
+        return out.reshape(*lead, d_out), xV.reshape(*lead, C)
+
+    @staticmethod
+    def backward(ctx, g_out, g_xV):
+        x2, V, U, m2, W, d2, r2, xV, acts = ctx.saved_tensors
+        has_w, has_d, has_r = ctx.has
+        W = W if has_w else None
+        d2 = d2 if has_d else None
+        r2 = r2 if has_r else None
+        T, d_in = x2.shape
+        C = V.shape[1]
+        d_out = U.shape[1]
+        dt = L.dtype_code(x2.dtype)
+        if g_out is None:
+            g_out = torch.zeros((T, d_out), dtype=x2.dtype, device=x2.device)
+        g = g_out.reshape(T, d_out).contiguous()
+        need_x, need_v, need_u, need_m = ctx.needs_input_grad[:4]
+        dx = torch.empty_like(x2) if need_x else None
+        dV = torch.empty((d_in, C), dtype=x2.dtype, device=x2.device)
+        dU = torch.empty((C, d_out), dtype=x2.dtype, device=x2.device)
+        dm = torch.empty_like(m2) if need_m else None
+        ws = L.workspace(L.load().pd_masked_linear_bwd_workspace_size(dt, T, d_out, C), x2.device)
+        L.call("pd_masked_linear_bwd", dt, T, d_in, d_out, C, L.ptr(x2), L.ptr(V.contiguous()), L.ptr(U.contiguous()),
+               L.ptr(W), L.ptr(m2), L.ptr(d2), L.ptr(r2), L.ptr(xV), L.ptr(acts), L.ptr(g), L.ptr(dx), L.ptr(dV),
+               L.ptr(dU), L.ptr(dm), L.ptr(ws), ws.numel(), L.stream())
+        if g_xV is not None:
+            # component_activation = x@V is also an output (the CI tap): its cotangent
+            # adds x^T g_xV to dV and g_xV V^T to dx.
+            from param_decomp_amd import ops
+
+            gx = g_xV.reshape(T, C).contiguous().to(x2.dtype)
+            ops.gemm(x2, gx, trans_a=True, out=dV, beta=1.0)
+            if dx is not None:
+                ops.gemm(gx, V.contiguous(), trans_b=True, out=dx, beta=1.0)
+        lead = ctx.lead
+        return (None if dx is None else dx.reshape(*lead, d_in), dV if need_v else None, dU if need_u else None,
+                None if dm is None else dm.reshape(*lead, C), None, None, None)
+
+
+def site_forward(x: torch.Tensor, weights: SiteWeights, mask: torch.Tensor, delta: torch.Tensor | None,
+                 route: torch.Tensor | None) -> SiteForward:
+    """`where(route, ((x@V)*m)@U + d*(x@(W - V@U)^T), x@W^T)` per position."""
+    W = weights.W if (delta is not None or route is not None) else None
+    out, xV = _MaskedLinear.apply(x, weights.V, weights.U, mask, W, delta, route)
+    return SiteForward(output=out, component_activation=xV)
+
+
+def site_out(x, weights, mask, delta, route) -> torch.Tensor:
+    return site_forward(x, weights, mask, delta, route).output

@@ -1,0 +1,181 @@
+"""Tensor-level wrappers over the C ABI: shape checks, output allocation, streams.
+
+Each function maps one-to-one onto an `include/pd_mi355x.h` entry point. Higher-level
+modules (`masking`, `decomposed_linear`, `losses`, `routed.experts`) add autograd.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from param_decomp_amd import _lib as L
+from param_decomp_amd.prng import Key
+
+
+def _flat_rows(t: torch.Tensor) -> tuple[int, int]:
+    return int(math.prod(t.shape[:-1])), int(t.shape[-1])
+
+
+def uniform(key: Key, shape, draw_dtype: torch.dtype, device, *, out_dtype: torch.dtype | None = None,
+            layout: int = L.LAYOUT_PARTITIONABLE) -> torch.Tensor:
+    out = torch.empty(tuple(shape), dtype=out_dtype or draw_dtype, device=device)
+    L.call("pd_uniform", key[0], key[1], out.numel(), L.dtype_code(draw_dtype), layout, L.ptr(out),
+           L.dtype_code(out.dtype), L.stream())
+    return out
+
+
+def squash_fwd(pre: torch.Tensor, lower: bool = True, upper: bool = True):
+    lo = torch.empty_like(pre) if lower else None
+    up = torch.empty_like(pre) if upper else None
+    L.call("pd_squash_fwd", L.ptr(pre), L.dtype_code(pre.dtype), pre.numel(), L.ptr(lo), L.ptr(up), L.stream())
+    return lo, up
+
+
+def squash_bwd(pre, g_lower, g_upper):
+    d = torch.empty_like(pre)
+    L.call("pd_squash_bwd", L.ptr(pre), L.ptr(g_lower), L.ptr(g_upper), L.dtype_code(pre.dtype), pre.numel(),
+           L.ptr(d), L.stream())
+    return d
+
+
+def component_mask_fwd(ci, key: Key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
+    m = torch.empty_like(ci)
+    L.call("pd_component_mask_fwd", L.ptr(ci), L.dtype_code(ci.dtype), ci.numel(), key[0], key[1],
+           L.dtype_code(draw_dtype), layout, L.ptr(m), L.stream())
+    return m
+
+
+def component_mask_bwd(g_mask, key: Key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
+    d = torch.empty_like(g_mask)
+    L.call("pd_component_mask_bwd", L.ptr(g_mask), L.dtype_code(g_mask.dtype), g_mask.numel(), key[0], key[1],
+           L.dtype_code(draw_dtype), layout, L.ptr(d), L.stream())
+    return d
+
+
+def gate_fwd(h, w_in, b_in, w_out, b_out, precise: bool):
+    rows, C = _flat_rows(h)
+    g = torch.empty(h.shape, dtype=torch.float32, device=h.device)
+    L.call("pd_gate_fwd", L.ptr(h), L.dtype_code(h.dtype), rows, C, w_in.shape[1], L.ptr(w_in), L.ptr(b_in),
+           L.ptr(w_out), L.ptr(b_out), int(precise), L.ptr(g), L.stream())
+    return g
+
+
+def gate_bwd(h, w_in, b_in, w_out, b_out, dg_raw, precise: bool):
+    rows, C = _flat_rows(h)
+    H = w_in.shape[1]
+    dh = torch.empty_like(h)
+    dwi, dbi, dwo = torch.empty_like(w_in), torch.empty_like(b_in), torch.empty_like(w_out)
+    dbo = torch.empty_like(b_out)
+    lib = L.load()
+    ws = L.workspace(lib.pd_gate_bwd_workspace_size(rows, C, H), h.device)
+    L.call("pd_gate_bwd", L.ptr(h), L.dtype_code(h.dtype), rows, C, H, L.ptr(w_in), L.ptr(b_in), L.ptr(w_out),
+           L.ptr(b_out), L.ptr(dg_raw.contiguous()), int(precise), L.ptr(dh), L.ptr(dwi), L.ptr(dbi), L.ptr(dwo),
+           L.ptr(dbo), L.ptr(ws), ws.numel(), L.stream())
+    return dh, dwi, dbi, dwo, dbo
+
+
+def impmin(ci_upper, *, kind: int, p=1.0, eps=0.0, beta=0.0, world_size=1.0, gamma=1.0, normalize_at_one=False,
+           ref_count=0.0, coeff_act=1.0, coeff_freq=0.0, want_grad=False):
+    rows, C = _flat_rows(ci_upper)
+    out = torch.empty(2, dtype=torch.float32, device=ci_upper.device)
+    grad = torch.empty_like(ci_upper) if want_grad else None
+    ws = L.workspace(L.load().pd_impmin_workspace_size(rows, C), ci_upper.device)
+    L.call("pd_impmin", L.ptr(ci_upper), L.dtype_code(ci_upper.dtype), rows, C, kind, p, eps, beta, world_size, gamma,
+           int(normalize_at_one), ref_count, coeff_act, coeff_freq, L.ptr(out), L.ptr(grad), L.ptr(ws), ws.numel(),
+           L.stream())
+    return out, grad
+
+
+def mse(a, b, coeff=1.0, want_grad=False):
+    out = torch.empty(1, dtype=torch.float32, device=a.device)
+    grad = torch.empty_like(a) if want_grad else None
+    ws = L.workspace(L.load().pd_mse_workspace_size(a.numel()), a.device)
+    L.call("pd_mse", L.ptr(a), L.ptr(b), L.dtype_code(a.dtype), a.numel(), coeff, L.ptr(out), L.ptr(grad), L.ptr(ws),
+           ws.numel(), L.stream())
+    return out, grad
+
+
+def kl(masked_logits, clean_logits, coeff=1.0, want_grad=False):
+    rows, V = _flat_rows(masked_logits)
+    out = torch.empty(1, dtype=torch.float32, device=masked_logits.device)
+    grad = torch.empty_like(masked_logits) if want_grad else None
+    ws = L.workspace(L.load().pd_kl_workspace_size(rows), masked_logits.device)
+    L.call("pd_kl", L.ptr(masked_logits), L.ptr(clean_logits), L.dtype_code(masked_logits.dtype), rows, V, coeff,
+           L.ptr(out), L.ptr(grad), L.ptr(ws), ws.numel(), L.stream())
+    return out, grad
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, trans_a=False, trans_b=False, out: torch.Tensor | None = None,
+         out_dtype: torch.dtype | None = None, alpha=1.0, beta=0.0) -> torch.Tensor:
+    """`alpha * op(a) @ op(b) + beta * out` for 2-D row-major tensors."""
+    M = a.shape[1] if trans_a else a.shape[0]
+    K = a.shape[0] if trans_a else a.shape[1]
+    N = b.shape[0] if trans_b else b.shape[1]
+    Kb = b.shape[1] if trans_b else b.shape[0]
+    if K != Kb:
+        raise L.PDError(f"gemm shape mismatch {tuple(a.shape)} {tuple(b.shape)}")
+    if a.dtype != b.dtype:
+        raise L.PDError("gemm operands must share a dtype")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or a.dtype, device=a.device)
+    L.call("pd_gemm", L.dtype_code(a.dtype), M, N, K, L.ptr(a), a.shape[1], int(trans_a), L.ptr(b), b.shape[1],
+           int(trans_b), L.ptr(out), N, L.dtype_code(out.dtype), alpha, beta, L.stream())
+    return out
+
+
+def router_topk(logits: torch.Tensor, k: int):
+    T, E = logits.shape
+    probs = torch.empty_like(logits)
+    idx = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    L.call("pd_router_topk", L.ptr(logits), T, E, k, L.ptr(probs), L.ptr(idx), L.ptr(w), L.stream())
+    return probs, idx, w
+
+
+def routed_jobs(top_idx: torch.Tensor, n_experts: int):
+    T, k = top_idx.shape
+    n = T * k
+    dev = top_idx.device
+    sort_idx = torch.empty(n, dtype=torch.int32, device=dev)
+    inv = torch.empty(n, dtype=torch.int32, device=dev)
+    sizes = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    ws = L.workspace(L.load().pd_routed_jobs_workspace_size(n, n_experts), dev)
+    L.call("pd_routed_jobs", L.ptr(top_idx), T, k, n_experts, L.ptr(sort_idx), L.ptr(inv), L.ptr(sizes),
+           L.ptr(offsets), L.ptr(ws), ws.numel(), L.stream())
+    return sort_idx, inv, sizes, offsets
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, div: int) -> torch.Tensor:
+    out = torch.empty((idx.numel(), src.shape[-1]), dtype=src.dtype, device=src.device)
+    L.call("pd_gather_rows", L.ptr(src), L.dtype_code(src.dtype), src.shape[-1], L.ptr(idx), div, idx.numel(),
+           L.ptr(out), L.stream())
+    return out
+
+
+def combine_jobs(y: torch.Tensor, inv: torch.Tensor, weights: torch.Tensor | None, T: int, k: int) -> torch.Tensor:
+    out = torch.empty((T, y.shape[-1]), dtype=y.dtype, device=y.device)
+    L.call("pd_combine_jobs", L.ptr(y), L.dtype_code(y.dtype), y.shape[-1], L.ptr(inv), L.ptr(weights), T, k,
+           L.ptr(out), L.stream())
+    return out
+
+
+def grouped_gemm(lhs, rhs, offsets, *, trans_rhs=False, out_dtype=None):
+    J, K = lhs.shape
+    E = rhs.shape[0]
+    N = rhs.shape[1] if trans_rhs else rhs.shape[2]
+    out = torch.empty((J, N), dtype=out_dtype or lhs.dtype, device=lhs.device)
+    L.call("pd_grouped_gemm", L.ptr(lhs), L.ptr(rhs), L.ptr(offsets), J, E, K, N, int(trans_rhs), L.ptr(out),
+           L.dtype_code(out.dtype), L.stream())
+    return out
+
+
+def grouped_gemm_dw(lhs, dout, offsets, n_groups: int, *, out_dtype=None):
+    J, K = lhs.shape
+    N = dout.shape[1]
+    out = torch.empty((n_groups, K, N), dtype=out_dtype or lhs.dtype, device=lhs.device)
+    L.call("pd_grouped_gemm_dw", L.ptr(lhs), L.ptr(dout), L.ptr(offsets), J, n_groups, K, N, L.ptr(out),
+           L.dtype_code(out.dtype), L.stream())
+    return out

@@ -1,0 +1,446 @@
+"""GPU parity: every C-ABI entry point against the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for Threefry bits/uniforms, routing indices and bucketing; fp32
+kernels within rtol 1e-5 (looser only where an fp32 reduction order differs, stated per
+test); bf16 kernels within rtol 2e-2 against a float64 oracle fed the same
+bf16-rounded inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pd_oracle as po
+from oracle import threefry as tf
+
+pytestmark = pytest.mark.gpu
+
+BF16_RTOL = 2e-2
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def bf(a, device):
+    return torch.tensor(np.asarray(a, np.float32), device=device).to(torch.bfloat16)
+
+
+def f32(a, device):
+    return torch.tensor(np.asarray(a, np.float32), device=device)
+
+
+def assert_close(got, want, rtol, atol_frac=1e-3, what=""):
+    """|got - want| <= rtol*|want| + atol_frac*max|want| (the absolute floor scales with
+    the tensor so near-zero entries of a bf16 product are judged at its precision)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    err = np.abs(got - want)
+    bound = rtol * np.abs(want) + atol_frac * scale
+    bad = err > bound
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} off; worst {err.max():.3e} (scale {scale:.3e})"
+
+
+# ------------------------------------------------------------------ Threefry draws
+
+
+@pytest.mark.parametrize("draw", ["float32", "bfloat16"])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003])
+def test_uniform_bit_exact(device, draw, layout, n):
+    from param_decomp_amd import ops
+
+    key = tf.fold_in(tf.split(tf.prng_key(42))[0], 3)
+    dt = torch.float32 if draw == "float32" else torch.bfloat16
+    got = ops.uniform(key, (n,), dt, device, out_dtype=torch.float32, layout=layout)
+    want = tf.uniform(key, (n,), draw, partitionable=(layout == 0))
+    np.testing.assert_array_equal(got.cpu().numpy().astype(np.float64), want)
+
+
+def test_prng_host_matches_oracle():
+    from param_decomp_amd import prng
+
+    for seed in (0, 1, 12345):
+        k = prng.PRNGKey(seed)
+        assert prng.split(k) == tf.split(tf.prng_key(seed))
+        assert prng.split(k, 3, partitionable=False) == tf.split(tf.prng_key(seed), 3, partitionable=False)
+        assert prng.fold_in(k, 77) == tf.fold_in(tf.prng_key(seed), 77)
+
+
+# ------------------------------------------------------------------ squashing / masks
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_squash_and_reference_cotangents(device, dtype):
+    from param_decomp_amd.squashing import lower_leaky_hard_sigmoid, upper_leaky_hard_sigmoid
+
+    xs = [-2.0, -2.0, 0.5, 0.5, 4.0, 4.0, 0.0, 0.0, 1.0, 1.0]
+    gs = [-3.0, 3.0, -3.0, 3.0, -3.0, 3.0, -3.0, 3.0, -3.0, 3.0]
+    x = torch.tensor(xs, device=device, dtype=dtype, requires_grad=True)
+    # fp32: exact equality with the float32 value of each known answer, as the
+    # reference's own test asserts (`cotangent == jnp.float32(expected)`)
+    rtol = 1e-2 if dtype == torch.bfloat16 else 0
+    cast = (lambda a: a) if dtype == torch.bfloat16 else (lambda a: np.asarray(a, np.float32).astype(np.float64))
+    lo = lower_leaky_hard_sigmoid(x)
+    (glo,) = torch.autograd.grad(lo, x, torch.tensor(gs, device=device, dtype=dtype))
+    np.testing.assert_allclose(np64(glo), cast(po.lower_leaky_vjp(np.array(xs), np.array(gs))), rtol=rtol)
+    up = upper_leaky_hard_sigmoid(x)
+    (gup,) = torch.autograd.grad(up, x, torch.tensor(gs, device=device, dtype=dtype))
+    # upper: 1 + 0.01*(x-1) is evaluated in fp32 (one rounding per op), so 1 ulp
+    rtol_up = 1e-2 if dtype == torch.bfloat16 else 1e-6
+    np.testing.assert_allclose(np64(up), po.upper_leaky(np.array(xs)), rtol=rtol_up)
+    np.testing.assert_allclose(np64(gup), po.upper_leaky_vjp(np.array(xs), np.array(gs)), rtol=rtol_up)
+
+
+def test_component_mask_fwd_bwd(device):
+    from param_decomp_amd.masking import sample_component_mask
+
+    rng = np.random.default_rng(0)
+    ci = rng.uniform(size=(33, 70)).astype(np.float32)
+    key = tf.fold_in(tf.prng_key(9), 1)
+    x = f32(ci, device).requires_grad_(True)
+    m = sample_component_mask(x, key)
+    u = tf.uniform(key, ci.shape, "float32")
+    np.testing.assert_allclose(np64(m), po.component_mask(ci.astype(np.float64), u), rtol=1e-6, atol=1e-7)
+    g = rng.normal(size=ci.shape)
+    (d,) = torch.autograd.grad(m, x, f32(g, device))
+    np.testing.assert_allclose(np64(d), g * (1 - u), rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ gate MLP
+
+
+def _gate_np(rng, C, H=16):
+    return po.GateParams(*(a.astype(np.float32).astype(np.float64) for a in (
+        rng.normal(size=(C, H)) * 1.4, rng.normal(size=(C, H)) * 0.2, rng.normal(size=(C, H)) * 0.35,
+        rng.normal(size=C) * 0.2 + 0.3)))
+
+
+@pytest.mark.parametrize("precise", [True, False])
+def test_gate_fwd_bwd_fp32(device, precise):
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(1)
+    T, C = 130, 75
+    gp = _gate_np(rng, C)
+    h = rng.normal(size=(T, C)).astype(np.float32).astype(np.float64)
+    tp = [f32(a, device) for a in (gp.w_in, gp.b_in, gp.w_out, gp.b_out)]
+    g = ops.gate_fwd(f32(h, device), *tp, precise)
+    want = po.gate_forward(h, gp)
+    # fast path: A&S 7.1.26 erf (|err| <= 1.5e-7) -> per-value error <= ~1e-6 absolute
+    assert_close(np64(g), want, 1e-5, 1e-6 if precise else 3e-6, "gate fwd")
+    dg = rng.normal(size=(T, C))
+    dh, dwi, dbi, dwo, dbo = ops.gate_bwd(f32(h, device), *tp, f32(dg, device), precise)
+    w = po.gate_backward(h, gp, dg)
+    for got, want_, name in zip((dh, dwi, dbi, dwo, dbo), w, ("dh", "dw_in", "db_in", "dw_out", "db_out")):
+        assert_close(np64(got), want_, 1e-4, 1e-5 if precise else 3e-5, name)
+
+
+def test_gate_bf16_h(device):
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(2)
+    T, C = 96, 128
+    gp = _gate_np(rng, C)
+    hb = bf(rng.normal(size=(T, C)), device)
+    tp = [f32(a, device) for a in (gp.w_in, gp.b_in, gp.w_out, gp.b_out)]
+    g = ops.gate_fwd(hb, *tp, False)
+    assert_close(np64(g), po.gate_forward(np64(hb), gp), BF16_RTOL, 1e-3, "gate fwd bf16")
+
+
+# ------------------------------------------------------------------ losses
+
+
+@pytest.mark.parametrize("p,beta", [(1.0, 0.0), (2.0, 0.0), (0.9, 0.2)])
+def test_impmin_pnorm(device, p, beta):
+    from param_decomp_amd import _lib as L
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(3)
+    up = rng.uniform(0.0, 1.2, size=(300, 37)).astype(np.float32).astype(np.float64)
+    out, grad = ops.impmin(f32(up, device), kind=L.IMPMIN_PNORM, p=p, eps=1e-3, beta=beta, world_size=2.0,
+                           want_grad=True)
+    assert float(out[0]) == pytest.approx(po.impmin_pnorm(up, p, 1e-3, beta, 2), rel=1e-5)
+    assert_close(np64(grad), po.impmin_pnorm_grad(up, p, 1e-3, beta, 2), 1e-4, 1e-6, "pnorm grad")
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+def test_impmin_smooth_l0(device, normalize):
+    from param_decomp_amd.losses import importance_minimality_terms
+
+    rng = np.random.default_rng(4)
+    a = rng.uniform(0.0, 1.1, size=(257, 40)).astype(np.float32).astype(np.float64)
+    b = rng.uniform(0.0, 1.1, size=(257, 9)).astype(np.float32).astype(np.float64)
+    ta, tb = f32(a, device).requires_grad_(True), f32(b, device).requires_grad_(True)
+    act, freq = importance_minimality_terms({"a": ta, "b": tb}, 0.3, 64, normalize_at_one=normalize)
+    wa, wf = po.importance_minimality_terms([a, b], 0.3, 64, normalize)
+    assert float(act) == pytest.approx(wa, rel=1e-5)
+    assert float(freq) == pytest.approx(wf, rel=1e-5)
+    (ga,) = torch.autograd.grad(act + 0.5 * freq, ta)
+    # finite differences of the oracle objective at a few entries
+    f = lambda arr: sum(po.importance_minimality_terms([arr, b], 0.3, 64, normalize) * np.array([1.0, 0.5]))
+    for idx in [(0, 0), (100, 17), (256, 39)]:
+        e = 1e-6
+        ap, am = a.copy(), a.copy()
+        ap[idx] += e
+        am[idx] -= e
+        assert float(ga[idx]) == pytest.approx((f(ap) - f(am)) / (2 * e), rel=1e-3, abs=1e-7)
+
+
+def test_reference_smooth_l0_closed_forms_on_gpu(device):
+    from param_decomp_amd.losses import importance_minimality_terms
+
+    act, freq = importance_minimality_terms({"a": f32([[1.0, 2.0], [3.0, 4.0]], device)}, 1.0, 8,
+                                            normalize_at_one=False)
+    f0, f1 = (1 / 2 + 9 / 10) / 2, (4 / 5 + 16 / 17) / 2
+    assert float(act) == pytest.approx(f0 + f1, rel=1e-6)
+    assert float(freq) == pytest.approx(f0 * np.log2(1 + 8 * f0) + f1 * np.log2(1 + 8 * f1), rel=1e-6)
+    act, _ = importance_minimality_terms({"a": f32([[1.0, 1.0]], device)}, 0.1, None, normalize_at_one=True)
+    assert float(act) == pytest.approx(2.0, rel=1e-6)
+
+
+def test_mse_and_kl(device):
+    from param_decomp_amd.losses import categorical_kl_from_logits, mse
+
+    rng = np.random.default_rng(5)
+    a, b = rng.normal(size=(50, 33)), rng.normal(size=(50, 33))
+    ta = f32(a, device).requires_grad_(True)
+    loss = mse(ta, f32(b, device))
+    a32, b32 = a.astype(np.float32).astype(np.float64), b.astype(np.float32).astype(np.float64)
+    assert float(loss) == pytest.approx(po.mse(a32, b32), rel=1e-5)
+    (g,) = torch.autograd.grad(loss, ta)
+    assert_close(np64(g), 2 * (a32 - b32) / a.size, 1e-5, 1e-7, "mse grad")
+    m, c = rng.normal(size=(9, 1001)) * 3, rng.normal(size=(9, 1001)) * 3
+    tm = f32(m, device).requires_grad_(True)
+    kl = categorical_kl_from_logits(tm, f32(c, device))
+    m32, c32 = m.astype(np.float32).astype(np.float64), c.astype(np.float32).astype(np.float64)
+    assert float(kl) == pytest.approx(po.categorical_kl(m32, c32), rel=1e-4)
+    (gk,) = torch.autograd.grad(kl, tm)
+    assert_close(np64(gk), po.categorical_kl_grad(m32, c32), 1e-4, 1e-6, "kl grad")
+
+
+# ------------------------------------------------------------------ GEMM
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 136, 72), (256, 384, 768), (8, 8, 8)])
+def test_gemm_bf16_layouts(device, ta, tb, M, N, K):
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(M + N + K + 2 * ta + tb)
+    A = rng.normal(size=(K, M) if ta else (M, K))
+    B = rng.normal(size=(N, K) if tb else (K, N))
+    Ab, Bb = bf(A, device), bf(B, device)
+    out = ops.gemm(Ab, Bb, trans_a=bool(ta), trans_b=bool(tb), out_dtype=torch.float32)
+    An, Bn = np64(Ab), np64(Bb)
+    want = (An.T if ta else An) @ (Bn.T if tb else Bn)
+    assert_close(np64(out), want, 1e-5, 1e-6, f"gemm ta={ta} tb={tb}")  # fp32 out: accumulation order only
+    out16 = ops.gemm(Ab, Bb, trans_a=bool(ta), trans_b=bool(tb))
+    assert_close(np64(out16), want, BF16_RTOL, 1e-3, "gemm bf16 out")
+
+
+def test_gemm_alpha_beta_and_fp32(device):
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(11)
+    A, B, C0 = rng.normal(size=(70, 50)), rng.normal(size=(50, 90)), rng.normal(size=(70, 90))
+    c = f32(C0, device)
+    ops.gemm(f32(A, device), f32(B, device), out=c, alpha=0.5, beta=2.0)
+    A32, B32, C32 = (x.astype(np.float32).astype(np.float64) for x in (A, B, C0))
+    assert_close(np64(c), 0.5 * A32 @ B32 + 2 * C32, 1e-5, 1e-6, "fp32 gemm")
+
+
+# ------------------------------------------------------------------ masked linear (site_forward)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_delta,with_route", [(False, False), (True, False), (True, True), (False, True)])
+def test_site_forward_and_backward(device, dtype, with_delta, with_route):
+    from param_decomp_amd.decomposed_linear import SiteWeights, site_forward
+
+    rng = np.random.default_rng(12)
+    B_, S, d_in, d_out, C = 3, 40, 64, 96, 128
+    x = rng.normal(size=(B_, S, d_in))
+    W = rng.normal(size=(d_out, d_in)) / 8
+    V = rng.normal(size=(d_in, C)) / 8
+    U = rng.normal(size=(C, d_out)) / 11
+    m = rng.uniform(size=(B_, S, C))
+    d = rng.uniform(size=(B_, S)) if with_delta else None
+    r = rng.uniform(size=(B_, S)) > 0.3 if with_route else None
+    cv = (lambda a: bf(a, device)) if dtype == torch.bfloat16 else (lambda a: f32(a, device))
+    tx, tV, tU, tm = (cv(a).requires_grad_(True) for a in (x, V, U, m))
+    tW = cv(W)
+    td = None if d is None else cv(d)
+    tr = None if r is None else torch.tensor(r, device=device)
+    res = site_forward(tx, SiteWeights(tW, tV, tU), tm, td, tr)
+    xs, Ws, Vs, Us, ms = (np64(t) for t in (tx, tW, tV, tU, tm))
+    ds = None if td is None else np64(td)
+    want, want_xV = po.site_forward(xs, Ws, Vs, Us, ms, ds, r)
+    rtol = 1e-5 if dtype == torch.float32 else BF16_RTOL
+    assert_close(np64(res.output), want, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "site out")
+    assert_close(np64(res.component_activation), want_xV, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "xV")
+    go = rng.normal(size=want.shape)
+    grads = torch.autograd.grad(res.output, (tx, tV, tU, tm), cv(go))
+    dx, dV, dU, dm = po.site_backward(xs, Ws, Vs, Us, ms, ds, r, np64(cv(go)))
+    for got, w, name in zip(grads, (dx, dV, dU, dm), ("dx", "dV", "dU", "dmask")):
+        assert_close(np64(got), w, rtol, 1e-4 if dtype == torch.float32 else 5e-3, name)
+
+
+# ------------------------------------------------------------------ fused dense step
+
+
+def _dense_inputs(rng, T, d_in, d_out, C):
+    x = rng.normal(size=(T, d_in))
+    W = rng.normal(size=(d_out, d_in)) / np.sqrt(d_in)
+    V = rng.normal(size=(d_in, C)) / np.sqrt(d_in)
+    U = rng.normal(size=(C, d_out)) / np.sqrt(C)
+    gp = po.GateParams(rng.normal(size=(C, 16)) * 1.4, np.zeros((C, 16)), rng.normal(size=(C, 16)) * 0.35,
+                       np.full(C, 0.3))
+    return x, W, V, U, gp
+
+
+@pytest.mark.parametrize("use_delta", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_step_matches_oracle(device, dtype, use_delta):
+    from param_decomp_amd.dense_step import DenseSiteStep
+
+    rng = np.random.default_rng(13)
+    T, d_in, d_out, C = 256, 64, 96, 192
+    x, W, V, U, gp = _dense_inputs(rng, T, d_in, d_out, C)
+    cv = (lambda a: bf(a, device)) if dtype == torch.bfloat16 else (lambda a: f32(a, device))
+    tx, tW, tV, tU = (cv(a) for a in (x, W, V, U))
+    gate = tuple(f32(a, device) for a in (gp.w_in, gp.b_in, gp.w_out, gp.b_out))
+    draw_key = tf.fold_in(tf.prng_key(5), 1)
+    step = DenseSiteStep(T, d_in, d_out, C, dtype=dtype, device=device, p=2.0, imp_coeff=0.7, recon_coeff=1.3,
+                         use_delta=use_delta)
+    mk, dk = step.site_keys(draw_key, 0)
+    g = step.step(tx, tW, tV, tU, gate, mk, dk)
+    torch.cuda.synchronize()
+    gp64 = po.GateParams(*(np64(t) for t in gate))
+    r = po.dense_site_step(np64(tx), np64(tW), np64(tV), np64(tU), gp64, draw_key, p=2.0, imp_coeff=0.7,
+                           recon_coeff=1.3, mask_dtype="bfloat16" if dtype == torch.bfloat16 else "float32",
+                           use_delta=use_delta, bf16_storage=dtype == torch.bfloat16)
+    rtol = 1e-4 if dtype == torch.float32 else BF16_RTOL
+    losses = g.losses.cpu().numpy()
+    np.testing.assert_allclose(losses, [r.loss, r.recon, r.imp], rtol=rtol)
+    floor = 1e-4 if dtype == torch.float32 else 1e-2
+    assert_close(np64(g.dU), r.dU, rtol, floor, "dU")
+    assert_close(np64(g.dV), r.dV, rtol, floor, "dV")
+    for got, want, name in zip((g.dw_in, g.db_in, g.dw_out, g.db_out), r.dgate, ("dw_in", "db_in", "dw_out", "db_out")):
+        assert_close(np64(got), want, rtol, floor, name)
+
+
+def test_dense_step_full_size_properties(device):
+    """At the full single-linear shape (T=4096, 768->3072, C=4096): the step is
+    deterministic run to run, losses are finite and positive, and the gradient of
+    the recon term scales linearly with recon_coeff (the MSE pullback is linear in its
+    coefficient and imp_coeff=0 removes the other term)."""
+    from param_decomp_amd.dense_step import DenseSiteStep
+
+    T, d_in, d_out, C = 4096, 768, 3072, 4096
+    gen = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(T, d_in, device=device, generator=gen).to(torch.bfloat16)
+    W = (torch.randn(d_out, d_in, device=device, generator=gen) / d_in**0.5).to(torch.bfloat16)
+    V = (torch.randn(d_in, C, device=device, generator=gen) / d_in**0.5).to(torch.bfloat16)
+    U = (torch.randn(C, d_out, device=device, generator=gen) / C**0.5).to(torch.bfloat16)
+    gate = (torch.randn(C, 16, device=device, generator=gen) * 1.4, torch.zeros(C, 16, device=device),
+            torch.randn(C, 16, device=device, generator=gen) * 0.35, torch.full((C,), 0.3, device=device))
+    mk, dk = DenseSiteStep.site_keys((0, 7), 0)
+    s1 = DenseSiteStep(T, d_in, d_out, C, device=device, imp_coeff=0.0, recon_coeff=1.0)
+    a = s1.step(x, W, V, U, gate, mk, dk)
+    dV1, dU1, l1 = a.dV.clone(), a.dU.clone(), a.losses.clone()
+    a = s1.step(x, W, V, U, gate, mk, dk)
+    assert torch.equal(a.dV, dV1) and torch.equal(a.dU, dU1) and torch.equal(a.losses, l1)
+    assert torch.isfinite(l1).all() and float(l1[1]) > 0
+    s2 = DenseSiteStep(T, d_in, d_out, C, device=device, imp_coeff=0.0, recon_coeff=2.0)
+    b = s2.step(x, W, V, U, gate, mk, dk)
+    torch.testing.assert_close(b.dU, 2 * dU1, rtol=2e-2, atol=1e-3 * float(dU1.abs().max()))
+
+
+# ------------------------------------------------------------------ routing
+
+
+def test_router_topk_bit_exact_indices(device):
+    from param_decomp_amd.routed.experts import route_tokens
+
+    rng = np.random.default_rng(14)
+    T, E, k = 1000, 42, 8
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    logits[3, [5, 9, 11]] = 2.5  # exact ties: lowest index first
+    logits[4, :] = 0.0
+    probs, idx, w = route_tokens(f32(logits, device), k)
+    p_or = po.softmax(logits.astype(np.float64))
+    want_idx = po.select_experts(p_or, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(probs.cpu().numpy(), p_or, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(w.cpu().numpy(), po.expert_mixing_weights(p_or, want_idx), rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,k,E", [(24, 2, 8), (8192, 8, 42), (1000, 3, 5), (7, 1, 64)])
+def test_routed_jobs_bit_exact(device, T, k, E):
+    from param_decomp_amd.routed.experts import routed_jobs
+
+    if (T, k, E) == (24, 2, 8):
+        first = np.arange(T) % (E - 2)
+        top = np.stack([first, (first + 1) % (E - 2)], axis=1).astype(np.int32)
+    else:
+        rng = np.random.default_rng(T)
+        top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    jobs = routed_jobs(torch.tensor(top, device=device), E)
+    want = po.routed_jobs(top, E)
+    np.testing.assert_array_equal(jobs.sort_idx.cpu().numpy(), want.sort_idx)
+    np.testing.assert_array_equal(jobs.inv_sort_idx.cpu().numpy(), want.inv_sort_idx)
+    np.testing.assert_array_equal(jobs.group_sizes.cpu().numpy(), want.group_sizes)
+    np.testing.assert_array_equal(jobs.group_offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(want.group_sizes)]))
+
+
+def test_gather_combine_and_vjp(device):
+    from param_decomp_amd.routed.experts import combine_jobs, gather_tokens, routed_jobs, sum_jobs
+
+    rng = np.random.default_rng(15)
+    T, k, E, D = 300, 4, 10, 48
+    top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    jobs = routed_jobs(torch.tensor(top, device=device), E)
+    oj = po.routed_jobs(top, E)
+    x = rng.normal(size=(T, D))
+    tx = f32(x, device).requires_grad_(True)
+    xj = gather_tokens(tx, jobs)
+    np.testing.assert_array_equal(np64(xj), po.gather_tokens(x.astype(np.float32).astype(np.float64), oj))
+    g = rng.normal(size=(T * k, D))
+    (gx,) = torch.autograd.grad(xj, tx, f32(g, device))
+    assert_close(np64(gx), po.gather_tokens_vjp(g.astype(np.float32).astype(np.float64), oj), 1e-6, 1e-7, "vjp")
+    y = rng.normal(size=(T * k, D)).astype(np.float32).astype(np.float64)
+    w = po.softmax(rng.normal(size=(T, k))).astype(np.float32).astype(np.float64)
+    assert_close(np64(sum_jobs(f32(y, device), jobs)), po.sum_jobs(y, oj), 1e-6, 1e-7, "sum_jobs")
+    assert_close(np64(combine_jobs(f32(y, device), jobs, f32(w, device))), po.combine_jobs(y, oj, w), 1e-6, 1e-7,
+                 "combine")
+
+
+@pytest.mark.parametrize("sizes", [[7, 0, 19, 1, 0, 26, 37, 0], [0, 0, 300, 5], [129, 128, 127, 1]])
+def test_grouped_matmul_fwd_bwd(device, sizes):
+    from param_decomp_amd.routed.experts import grouped_matmul, transposed_grouped_matmul
+
+    rng = np.random.default_rng(sum(sizes))
+    E, K, N = len(sizes), 64, 136
+    J = int(sum(sizes)) + 5  # 5 trailing rows past sum(group_sizes)
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = bf(rng.normal(size=(J, K)), device).requires_grad_(True)
+    rhs = bf(rng.normal(size=(E, K, N)) / 8, device).requires_grad_(True)
+    out = grouped_matmul(lhs, rhs, offsets)
+    want = po.grouped_matmul(np64(lhs), np64(rhs), sizes)
+    assert_close(np64(out), want, BF16_RTOL, 4e-3, "grouped fwd")
+    assert np.all(np64(out)[sum(sizes):] == 0)
+    g = bf(rng.normal(size=(J, N)), device)
+    dl, dr = torch.autograd.grad(out, (lhs, rhs), g)
+    gn = np64(g)
+    gn[sum(sizes):] = 0.0
+    want_dl = po.grouped_matmul(gn, np.transpose(np64(rhs), (0, 2, 1)), sizes)
+    assert_close(np64(dl), want_dl, BF16_RTOL, 4e-3, "grouped d_lhs")
+    want_dr = po.transposed_grouped_matmul(np64(lhs), gn, sizes)
+    assert_close(np64(dr), want_dr, BF16_RTOL, 4e-3, "grouped d_rhs")
+    dw = transposed_grouped_matmul(lhs.detach(), g, offsets, out_dtype=torch.float32)
+    assert_close(np64(dw), want_dr, 1e-5, 1e-6, "dw fp32")
+    for e, s in enumerate(sizes):
+        if s == 0:
+            assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dr[e]) == 0
