@@ -41,6 +41,7 @@ def phase_work(name, T, d_in, d_out, C, es):
     fused elementwise passes (fwd reads h and writes h*m; bwd reads h and d(h*m) and
     writes dh; u is regenerated, never stored)."""
     table = {
+        "transpose_inputs": ("byte", 2 * (T * d_in + d_in * C + C * d_out) * es),
         "gemm_target": ("flop", 2 * T * d_in * d_out),
         "gemm_xV": ("flop", 2 * T * d_in * C),
         "gate_mask_fwd": ("byte", 2 * T * C * es),

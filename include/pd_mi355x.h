@@ -148,10 +148,11 @@ int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, 
 
 /* pd_dense_step with phase timing for measurement harnesses: `events` holds
  * PD_DENSE_STEP_PHASES + 1 hipEvent_t handles recorded on `stream` at the phase
- * boundaries: 0 target GEMM x@W^T, 1 GEMM h=x@V, 2 gate/mask fwd, 3 GEMM (h*m)@U,
- * 4 recon residual, 5 loss finalize, 6 GEMM dU, 7 GEMM da=dy@U^T, 8 gate/mask bwd,
- * 9 gate-grad reduce, 10 GEMM dV. Same arithmetic as pd_dense_step. */
-#define PD_DENSE_STEP_PHASES 11
+ * boundaries: 0 operand transposes (x, V, U), 1 target GEMM x@W^T, 2 GEMM h=x@V,
+ * 3 gate/mask fwd, 4 GEMM (h*m)@U, 5 recon residual, 6 loss finalize, 7 GEMM dU,
+ * 8 GEMM da=dy@U^T, 9 gate/mask bwd, 10 gate-grad reduce, 11 GEMM dV. Same arithmetic
+ * as pd_dense_step. */
+#define PD_DENSE_STEP_PHASES 12
 int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
                         const float* w_out, const float* b_out, uint32_t mask_k0, uint32_t mask_k1,

@@ -1,0 +1,476 @@
+// The fused single-site stochastic-recon step (gfx950): one fwd+bwd of one decomposed
+// linear with the paper-form gate, mask draw, MSE recon and L_p imp-min
+// (pd/core/train.py:1126-1352 restricted to one site; pd/core/masking.py:148-167 draws;
+// pd/core/decomposed_linear.py:142-175; spd_paper.md appendix gate).
+//
+// Every GEMM of the step runs with both operands K-contiguous (the fastest MFMA
+// operand path): the inputs x, V, U are transposed once per step, and the elementwise
+// producers write the K-contiguous copies the weight-gradient GEMMs need (acts^T, dy^T,
+// dh^T) through 64x64 LDS tiles, so those stores stay coalesced.
+//
+//   yt  = x @ W^T          A=x [T,d_in]      B=W  [d_out,d_in]
+//   h   = x @ V            A=x               B=V^T [C,d_in]
+//   fwd elementwise: g_raw, squash, u, acts = h*(m-d)  -> acts [T,C], acts^T [C,T]
+//   y   = acts @ U         A=acts [T,C]      B=U^T [d_out,C]
+//   recon: e = y + d*yt - yt, dy = scale*e            -> dy [T,d_out], dy^T [d_out,T]
+//   dU  = acts^T @ dy      A=acts^T [C,T]    B=dy^T [d_out,T]
+//   da  = dy @ U^T         A=dy [T,d_out]    B=U [C,d_out]
+//   bwd elementwise: dh = da*(m-d) + gate pullback     -> dh^T [C,T]
+//   dV  = x^T @ dh         A=x^T [d_in,T]    B=dh^T [C,T]
+#include <algorithm>
+
+#include "pd_common.hpp"
+
+namespace pd {
+
+static constexpr int SITE_COLS = 64;  // components per block in the column-mapped kernels
+static constexpr int SITE_ROWS = 64;  // tokens per block chunk
+static constexpr int TP = 64;         // transpose tile
+
+struct StepParams {
+  int64_t T, C;
+  uint32_t mk0, mk1;
+  int draw_dtype, layout;
+  float p, imp_scale;     // imp_scale = imp_coeff / T
+  const float* delta;     // [T] per-token delta draw, or NULL (d = 0)
+  uint8_t* ubits;         // [T, C] bf16-draw uniforms as 7-bit integers (bf16 draws only)
+};
+
+__device__ inline float step_delta(const StepParams& s, int64_t t) { return s.delta ? s.delta[t] : 0.f; }
+
+__global__ void k_delta_fill(uint32_t k0, uint32_t k1, int64_t T, int draw_dtype, int layout, float* __restrict__ d) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < T; t += (int64_t)gridDim.x * blockDim.x)
+    d[t] = draw_uniform(k0, k1, t, T, draw_dtype, layout);
+}
+
+// A lane's run of consecutive-token values of one component, emitted to dstT [C, T] as
+// 16-byte stores: a sliding window of 8 bf16 (shifted with v_alignbit) or 4 fp32.
+template <typename T>
+struct RowPack;
+template <>
+struct RowPack<bf16_t> {
+  static constexpr int N = 8;
+  uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+  __device__ inline void push(float v) {
+    const uint32_t b = f32_to_bf16(v);
+    w0 = __builtin_amdgcn_alignbit(w1, w0, 16);
+    w1 = __builtin_amdgcn_alignbit(w2, w1, 16);
+    w2 = __builtin_amdgcn_alignbit(w3, w2, 16);
+    w3 = (w3 >> 16) | (b << 16);
+  }
+  __device__ inline void flush(bf16_t* dst) { *(uint4*)dst = make_uint4(w0, w1, w2, w3); }
+};
+template <>
+struct RowPack<float> {
+  static constexpr int N = 4;
+  float w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+  __device__ inline void push(float v) {
+    w0 = w1;
+    w1 = w2;
+    w2 = w3;
+    w3 = v;
+  }
+  __device__ inline void flush(float* dst) { *(float4*)dst = make_float4(w0, w1, w2, w3); }
+};
+
+__device__ inline float pow_p(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
+__device__ inline float dpow_p(float b, float p) {
+  return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f));
+}
+
+// dst[c][r] = src[r][c] for a [R, Cc] matrix; 64x64 tiles through LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ src, int64_t R, int64_t Cc,
+                                                   T* __restrict__ dst) {
+  __shared__ float tile[TP][TP + 1];
+  const int64_t r0 = (int64_t)blockIdx.y * TP, c0 = (int64_t)blockIdx.x * TP;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < TP; i += 4) {
+    int64_t r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < R && c < Cc) ? load_f<T>(src, r * Cc + c) : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < TP; i += 4) {
+    int64_t c = c0 + i, r = r0 + tx;
+    if (c < Cc && r < R) store_f<T>(dst, c * R + r, tile[tx][i]);
+  }
+}
+
+// The uniform of element i: bf16 draws are stored by the forward as the 7-bit integer
+// k (u = k/128) and re-read by the backward; fp32 draws are regenerated from the key.
+__device__ inline float step_uniform_fwd(const StepParams& s, int64_t i, int64_t n) {
+  if (s.draw_dtype == PD_DTYPE_BF16) {
+    const uint32_t k = (draw_bits(s.mk0, s.mk1, i, n, 8, s.layout) & 0xFFu) >> 1;
+    s.ubits[i] = (uint8_t)k;
+    return (float)k * (1.f / 128.f);
+  }
+  return draw_uniform(s.mk0, s.mk1, i, n, s.draw_dtype, s.layout);
+}
+__device__ inline float step_uniform_bwd(const StepParams& s, int64_t i, int64_t n) {
+  if (s.draw_dtype == PD_DTYPE_BF16) return (float)s.ubits[i] * (1.f / 128.f);
+  return draw_uniform(s.mk0, s.mk1, i, n, s.draw_dtype, s.layout);
+}
+
+// Forward, one component per lane over a 64-token chunk: gate MLP on h, squash, draw u,
+// acts = h*(m-d), imp-min partial of upper^p. Writes g_raw (fp32), acts, acts^T (the
+// lane's consecutive tokens of its component, packed into 16-byte stores).
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h, const float* __restrict__ w_in,
+                                                        const float* __restrict__ b_in,
+                                                        const float* __restrict__ w_out,
+                                                        const float* __restrict__ b_out, StepParams s,
+                                                        float* __restrict__ g_raw, T* __restrict__ acts,
+                                                        T* __restrict__ actsT, float* __restrict__ imp_partial) {
+  const int64_t c = (int64_t)blockIdx.x * SITE_COLS + threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * SITE_ROWS;
+  const int64_t r1 = r0 + SITE_ROWS < s.T ? r0 + SITE_ROWS : s.T;
+  float imp = 0.f;
+  if (c < s.C) {
+    float wi[16], bi[16], wo[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      wi[j] = w_in[c * 16 + j];
+      bi[j] = b_in[c * 16 + j];
+      wo[j] = w_out[c * 16 + j];
+    }
+    const float bo = b_out[c];
+    const int64_t n = s.T * s.C;
+    RowPack<T> pack;
+    for (int64_t t = r0; t < r1; ++t) {
+      const int64_t i = t * s.C + c;
+      const float hv = load_f<T>(h, i);
+      float g = bo;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) g = fmaf(wo[j], gelu_only<PRECISE>(fmaf(wi[j], hv, bi[j])), g);
+      g_raw[i] = g;
+      const float lo = lower_fwd(g);
+      imp += pow_p(upper_fwd(g), s.p);
+      const float u = step_uniform_fwd(s, i, n);
+      const float m = lo + (1.f - lo) * u;
+      const float a = hv * (m - step_delta(s, t));
+      store_f<T>(acts, i, a);
+      pack.push(a);
+      if (((t - r0) % RowPack<T>::N) == RowPack<T>::N - 1) pack.flush(actsT + c * s.T + t + 1 - RowPack<T>::N);
+    }
+  }
+  imp = wave_sum(imp);
+  if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = imp;
+}
+
+// Recon residual on a 64x64 tile: e = y + d*yt - yt; partial of e^2; dy = gscale*e
+// written as dy [T, D] and dy^T [D, T].
+template <typename T>
+__global__ __launch_bounds__(256) void k_step_recon(const T* __restrict__ y, const T* __restrict__ yt, StepParams s,
+                                                    int64_t D, float gscale, T* __restrict__ dy,
+                                                    T* __restrict__ dyT, float* __restrict__ partial) {
+  __shared__ float tile[TP][TP + 1];
+  __shared__ float sw[4];
+  const int64_t r0 = (int64_t)blockIdx.y * TP, c0 = (int64_t)blockIdx.x * TP;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  float acc = 0.f;
+  for (int i = ty; i < TP; i += 4) {
+    int64_t t = r0 + i, c = c0 + tx;
+    float g = 0.f;
+    if (t < s.T && c < D) {
+      const int64_t idx = t * D + c;
+      const float tv = load_f<T>(yt, idx);
+      const float e = load_f<T>(y, idx) + step_delta(s, t) * tv - tv;
+      acc = fmaf(e, e, acc);
+      g = gscale * e;
+      store_f<T>(dy, idx, g);
+    }
+    tile[i][tx] = g;
+  }
+  acc = wave_sum(acc);
+  if (tx == 0) sw[ty] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = sw[0] + sw[1] + sw[2] + sw[3];
+  for (int i = ty; i < TP; i += 4) {
+    int64_t c = c0 + i, t = r0 + tx;
+    if (c < D && t < s.T) store_f<T>(dyT, c * s.T + t, tile[tx][i]);
+  }
+}
+
+// Backward, one component per lane: from da = dy@U^T, h, g_raw and the regenerated u:
+// dh = da*(m-d) + gate pullback of dg_raw, where dg_raw = lower_vjp(g, da*h*(1-u))
+// + upper_vjp(g, imp_scale * d upper^p). Writes dh^T; gate parameter grads go to
+// per-chunk partials [chunk][49][C].
+template <typename T, bool PRECISE>
+__global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da, const T* __restrict__ h,
+                                                        const float* __restrict__ g_raw,
+                                                        const float* __restrict__ w_in,
+                                                        const float* __restrict__ b_in,
+                                                        const float* __restrict__ w_out, StepParams s,
+                                                        T* __restrict__ dhT, float* __restrict__ partial) {
+  const int64_t c = (int64_t)blockIdx.x * SITE_COLS + threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * SITE_ROWS;
+  const int64_t r1 = r0 + SITE_ROWS < s.T ? r0 + SITE_ROWS : s.T;
+  if (c < s.C) {
+    RowPack<T> pack;
+    float wi[16], bi[16], wo[16], a_wi[16], a_bi[16], a_wo[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      wi[j] = w_in[c * 16 + j];
+      bi[j] = b_in[c * 16 + j];
+      wo[j] = w_out[c * 16 + j];
+      a_wi[j] = a_bi[j] = a_wo[j] = 0.f;
+    }
+    float a_bo = 0.f;
+    const int64_t n = s.T * s.C;
+    for (int64_t t = r0; t < r1; ++t) {
+      const int64_t i = t * s.C + c;
+      const float hv = load_f<T>(h, i), g = g_raw[i], dav = load_f<T>(da, i);
+      const float lo = lower_fwd(g);
+      const float u = step_uniform_bwd(s, i, n);
+      const float m = lo + (1.f - lo) * u;
+      float dhv = dav * (m - step_delta(s, t));
+      const float dg = lower_vjp(g, dav * hv * (1.f - u)) + upper_vjp(g, s.imp_scale * dpow_p(upper_fwd(g), s.p));
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        GeluOut go = gelu_and_grad<PRECISE>(fmaf(wi[j], hv, bi[j]));
+        const float dz = dg * wo[j] * go.grad;
+        dhv = fmaf(dz, wi[j], dhv);
+        a_wi[j] = fmaf(dz, hv, a_wi[j]);
+        a_bi[j] += dz;
+        a_wo[j] = fmaf(dg, go.gelu, a_wo[j]);
+      }
+      a_bo += dg;
+      pack.push(dhv);
+      if (((t - r0) % RowPack<T>::N) == RowPack<T>::N - 1) pack.flush(dhT + c * s.T + t + 1 - RowPack<T>::N);
+    }
+    float* pp = partial + (int64_t)blockIdx.y * 49 * s.C;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      pp[(int64_t)j * s.C + c] = a_wi[j];
+      pp[(int64_t)(16 + j) * s.C + c] = a_bi[j];
+      pp[(int64_t)(32 + j) * s.C + c] = a_wo[j];
+    }
+    pp[(int64_t)48 * s.C + c] = a_bo;
+  }
+}
+
+__global__ void k_step_gate_reduce(const float* __restrict__ partial, int64_t chunks, int64_t C,
+                                   float* __restrict__ dw_in, float* __restrict__ db_in, float* __restrict__ dw_out,
+                                   float* __restrict__ db_out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= 49 * C) return;
+  const int64_t q = idx / C, c = idx % C;
+  float acc = 0.f;
+  for (int64_t k = 0; k < chunks; ++k) acc += partial[k * 49 * C + idx];
+  if (q < 16)
+    dw_in[c * 16 + q] = acc;
+  else if (q < 32)
+    db_in[c * 16 + q - 16] = acc;
+  else if (q < 48)
+    dw_out[c * 16 + q - 32] = acc;
+  else
+    db_out[c] = acc;
+}
+
+// losses[0..2] = {loss, recon, imp} from the two partial arrays (one block, fixed order)
+__global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec, const float* __restrict__ imp_part,
+                              int64_t n_imp, double rec_scale, double imp_scale, float recon_coeff, float imp_coeff,
+                              float* __restrict__ losses) {
+  __shared__ double sr[16], si[16];
+  double r = 0.0, m = 0.0;
+  for (int64_t i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
+  for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  r = wave_sum_d(r);
+  m = wave_sum_d(m);
+  if (threadIdx.x % 64 == 0) {
+    sr[threadIdx.x / 64] = r;
+    si[threadIdx.x / 64] = m;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double a = 0, b = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
+      a += sr[i];
+      b += si[i];
+    }
+    a *= rec_scale;
+    b *= imp_scale;
+    losses[0] = (float)(recon_coeff * a + imp_coeff * b);
+    losses[1] = (float)a;
+    losses[2] = (float)b;
+  }
+}
+
+struct StepWorkspace {
+  size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, total;
+};
+
+static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C) {
+  const size_t es = dtype == PD_DTYPE_BF16 ? 2 : 4;
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  StepWorkspace w{};
+  size_t o = 0;
+  auto take = [&](size_t& field, size_t bytes) {
+    field = o;
+    o += al(bytes);
+  };
+  take(w.xT, es * d_in * T);
+  take(w.VT, es * C * d_in);
+  take(w.UT, es * d_out * C);
+  take(w.yt, es * T * d_out);
+  take(w.h, es * T * C);
+  take(w.graw, 4 * T * C);
+  take(w.acts, es * T * C);
+  take(w.actsT, es * C * T);
+  take(w.y, es * T * d_out);
+  take(w.dy, es * T * d_out);
+  take(w.dyT, es * d_out * T);
+  take(w.da, es * T * C);
+  take(w.dhT, es * C * T);
+  take(w.imp, 4 * cdiv(T, SITE_ROWS) * cdiv(C, SITE_COLS));
+  take(w.rec, 4 * cdiv(T, TP) * cdiv(d_out, TP));
+  take(w.gate, 4 * cdiv(T, SITE_ROWS) * 49 * C);
+  take(w.delta, 4 * T);
+  take(w.ubits, (size_t)T * C);
+  w.total = o;
+  return w;
+}
+
+template <typename TT>
+static void launch_transpose(const void* src, int64_t R, int64_t Cc, void* dst, hipStream_t s) {
+  hipLaunchKernelGGL(k_transpose<TT>, dim3((unsigned)cdiv(Cc, TP), (unsigned)cdiv(R, TP)), dim3(256), 0, s,
+                     (const TT*)src, R, Cc, (TT*)dst);
+}
+
+// Phase boundaries recorded into caller events (events may be NULL); the phase order
+// is documented at pd_dense_step_timed in the header.
+static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
+                           const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
+                           const float* w_out, const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0,
+                           uint32_t dk1, int use_delta, int draw_dtype, int layout, float p, float imp_coeff,
+                           float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
+                           float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
+                           void** events) {
+#define PD_MARK(i) \
+  if (events) hipEventRecord((hipEvent_t)events[i], (hipStream_t)stream)
+  if (H != 16) return fail(PD_EUNSUPPORTED, "pd_dense_step: gate hidden width must be 16");
+  if (T <= 0 || d_in <= 0 || d_out <= 0 || C <= 0 || !x || !W || !V || !U || !w_in || !b_in || !w_out || !b_out ||
+      !losses || !dV || !dU || !dw_in || !db_in || !dw_out || !db_out)
+    return fail(PD_EINVAL, "pd_dense_step: bad args");
+  if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_dense_step: dtype");
+  if (draw_dtype != PD_DTYPE_F32 && draw_dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_dense_step: draw dtype");
+  StepWorkspace L = step_layout(dtype, T, d_in, d_out, C);
+  if (!workspace || workspace_bytes < L.total) return fail(PD_EWORKSPACE, "pd_dense_step: workspace too small");
+  if (cdiv(T, SITE_ROWS) > 65535 || cdiv(d_in, TP) > 65535 || cdiv(C, TP) > 65535)
+    return fail(PD_EUNSUPPORTED, "pd_dense_step: shape too large");
+  if (T % 8 != 0) return fail(PD_EUNSUPPORTED, "pd_dense_step: T must be a multiple of 8");
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  void *xT = ws + L.xT, *VT = ws + L.VT, *UT = ws + L.UT, *yt = ws + L.yt, *h = ws + L.h, *acts = ws + L.acts;
+  void *actsT = ws + L.actsT, *y = ws + L.y, *dy = ws + L.dy, *dyT = ws + L.dyT, *da = ws + L.da, *dhT = ws + L.dhT;
+  float* graw = (float*)(ws + L.graw);
+  float* imp_part = (float*)(ws + L.imp);
+  float* rec_part = (float*)(ws + L.rec);
+  float* gate_part = (float*)(ws + L.gate);
+  const bool bf = dtype == PD_DTYPE_BF16;
+  float* delta = use_delta ? (float*)(ws + L.delta) : nullptr;
+  StepParams sp{T, C, mk0, mk1, draw_dtype, layout, p, imp_coeff / (float)T, delta, (uint8_t*)(ws + L.ubits)};
+  const dim3 cgrid((unsigned)cdiv(C, SITE_COLS), (unsigned)cdiv(T, SITE_ROWS));
+  const dim3 rgrid((unsigned)cdiv(d_out, TP), (unsigned)cdiv(T, TP));
+  int rc;
+  PD_MARK(0);
+  if (bf) {
+    launch_transpose<bf16_t>(x, T, d_in, xT, s);
+    launch_transpose<bf16_t>(V, d_in, C, VT, s);
+    launch_transpose<bf16_t>(U, C, d_out, UT, s);
+  } else {
+    launch_transpose<float>(x, T, d_in, xT, s);
+    launch_transpose<float>(V, d_in, C, VT, s);
+    launch_transpose<float>(U, C, d_out, UT, s);
+  }
+  if (delta)
+    hipLaunchKernelGGL(k_delta_fill, dim3((unsigned)std::min<int64_t>(cdiv(T, 256), 1024)), dim3(256), 0, s, dk0, dk1,
+                       T, draw_dtype, layout, delta);
+  if ((rc = check_launch("pd_dense_step transpose"))) return rc;
+  PD_MARK(1);
+  if ((rc = pd_gemm(dtype, T, d_out, d_in, x, d_in, 0, W, d_in, 1, yt, d_out, dtype, 1.f, 0.f, stream))) return rc;
+  PD_MARK(2);
+  if ((rc = pd_gemm(dtype, T, C, d_in, x, d_in, 0, VT, d_in, 1, h, C, dtype, 1.f, 0.f, stream))) return rc;
+  PD_MARK(3);
+  if (bf)
+    hipLaunchKernelGGL((k_step_fwd<bf16_t, false>), cgrid, dim3(SITE_COLS), 0, s, (const bf16_t*)h, w_in, b_in,
+                       w_out, b_out, sp, graw, (bf16_t*)acts, (bf16_t*)actsT, imp_part);
+  else
+    hipLaunchKernelGGL((k_step_fwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)h, w_in, b_in, w_out,
+                       b_out, sp, graw, (float*)acts, (float*)actsT, imp_part);
+  if ((rc = check_launch("pd_dense_step fwd"))) return rc;
+  PD_MARK(4);
+  if ((rc = pd_gemm(dtype, T, d_out, C, acts, C, 0, UT, C, 1, y, d_out, dtype, 1.f, 0.f, stream))) return rc;
+  PD_MARK(5);
+  const float gscale = recon_coeff * 2.f / (float)(T * d_out);
+  if (bf)
+    hipLaunchKernelGGL(k_step_recon<bf16_t>, rgrid, dim3(256), 0, s, (const bf16_t*)y, (const bf16_t*)yt, sp, d_out,
+                       gscale, (bf16_t*)dy, (bf16_t*)dyT, rec_part);
+  else
+    hipLaunchKernelGGL(k_step_recon<float>, rgrid, dim3(256), 0, s, (const float*)y, (const float*)yt, sp, d_out,
+                       gscale, (float*)dy, (float*)dyT, rec_part);
+  if ((rc = check_launch("pd_dense_step recon"))) return rc;
+  PD_MARK(6);
+  hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), imp_part,
+                     (int64_t)(cgrid.x * cgrid.y), 1.0 / (double)(T * d_out), 1.0 / (double)T, recon_coeff, imp_coeff,
+                     losses);
+  PD_MARK(7);
+  if ((rc = pd_gemm(dtype, C, d_out, T, actsT, T, 0, dyT, T, 1, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
+    return rc;
+  PD_MARK(8);
+  if ((rc = pd_gemm(dtype, T, C, d_out, dy, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
+  PD_MARK(9);
+  if (bf)
+    hipLaunchKernelGGL((k_step_bwd<bf16_t, false>), cgrid, dim3(SITE_COLS), 0, s, (const bf16_t*)da, (const bf16_t*)h,
+                       graw, w_in, b_in, w_out, sp, (bf16_t*)dhT, gate_part);
+  else
+    hipLaunchKernelGGL((k_step_bwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)da, (const float*)h,
+                       graw, w_in, b_in, w_out, sp, (float*)dhT, gate_part);
+  if ((rc = check_launch("pd_dense_step bwd"))) return rc;
+  PD_MARK(10);
+  hipLaunchKernelGGL(k_step_gate_reduce, dim3((unsigned)cdiv(49 * C, 256)), dim3(256), 0, s, gate_part,
+                     (int64_t)cgrid.y, C, dw_in, db_in, dw_out, db_out);
+  if ((rc = check_launch("pd_dense_step gate reduce"))) return rc;
+  PD_MARK(11);
+  if ((rc = pd_gemm(dtype, d_in, C, T, xT, T, 0, dhT, T, 1, dV, C, PD_DTYPE_F32, 1.f, 0.f, stream))) return rc;
+  PD_MARK(12);
+  return PD_OK;
+#undef PD_MARK
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+extern "C" {
+
+size_t pd_dense_step_workspace_size(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H) {
+  (void)H;
+  return step_layout(dtype, T, d_in, d_out, C).total;
+}
+
+int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x, const void* W,
+                  const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
+                  const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0, uint32_t dk1, int use_delta,
+                  int draw_dtype, int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dV,
+                  float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
+                         use_delta, draw_dtype, layout, p, imp_coeff, recon_coeff, losses, dV, dU, dw_in, db_in,
+                         dw_out, db_out, workspace, workspace_bytes, stream, nullptr);
+}
+
+int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
+                        const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
+                        const float* w_out, const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0,
+                        uint32_t dk1, int use_delta, int draw_dtype, int layout, float p, float imp_coeff,
+                        float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
+                        float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
+                        void** events) {
+  if (!events) return fail(PD_EINVAL, "pd_dense_step_timed: events required");
+  return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
+                         use_delta, draw_dtype, layout, p, imp_coeff, recon_coeff, losses, dV, dU, dw_in, db_in,
+                         dw_out, db_out, workspace, workspace_bytes, stream, events);
+}
+
+}  // extern "C"

@@ -1,10 +1,20 @@
 // GEMM kernels for the masked-component path (gfx950).
 //
-// bf16 path: v_mfma_f32_32x32x16_bf16 on 128x128x64 block tiles, 4 waves (2x2) of
-// 64x64, LDS double-buffered through registers. LDS always holds both operands
-// K-contiguous ([rows][BK+pad]); an operand whose global layout is MN-contiguous is
-// transposed in registers (4 k-rows x 8 elements per thread) on its way into LDS, so
-// every MFMA fragment is one 16-byte LDS read.
+// bf16 path: v_mfma_f32_32x32x16_bf16, LDS double-buffered through registers. Two tile
+// configurations share one template:
+//   BIG   256x256x64, 8 waves (2x4), 128x64 per wave (4x2 MFMA tiles), 144 KB LDS —
+//         one block per CU; halves the L2 re-read per FLOP of a 128x128 tile.
+//   SMALL 128x128x64, 4 waves (2x2), 64x64 per wave — for grids the big tile leaves
+//         under-occupied (fewer than ~200 tiles on 256 CUs).
+// LDS holds both operands K-contiguous ([rows][BK+8]; the 144-byte row stride makes a
+// wave's 16-byte fragment reads of 16 consecutive rows hit 16 distinct 4-bank groups).
+// An operand whose global layout is MN-contiguous is transposed in registers (4 k-rows
+// x 8 elements per thread) on its way into LDS; the hot paths avoid that layout by
+// having producers write K-contiguous copies.
+//
+// Dense launches use an XCD-aware tile order: workgroups are dispatched round-robin
+// over the 8 XCDs, so the linear id is remapped so each XCD's share is a compact
+// 8-row-grouped region (fewer distinct A/B panels per XCD-local L2).
 //
 // Three problem mappings share the kernel:
 //   DENSE     C = alpha*op(A)@op(B) + beta*C                  (x@V, acts@U, transposes)
@@ -24,8 +34,7 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
 enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2 };
 
-constexpr int BM = 128, BN = 128, BK = 64, LDS_PAD = 8, LDS_STRIDE = BK + LDS_PAD;
-constexpr int GEMM_THREADS = 256;
+constexpr int BK = 64, LDS_PAD = 8, LDS_STRIDE = BK + LDS_PAD;
 
 struct GemmArgs {
   int64_t M, N, K;
@@ -42,18 +51,31 @@ struct GemmArgs {
   int64_t strideC;  // elements between consecutive groups' C (GROUPED_K)
 };
 
+template <int BM_, int BN_, int WM_, int WN_>
+struct TileCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int NT = WM_ * WN_ * 64;
+  static constexpr int TM = BM_ / WM_ / 32, TN = BN_ / WN_ / 32;
+  static constexpr int LDS_ELEMS = (BM_ + BN_) * LDS_STRIDE;
+};
+typedef TileCfg<256, 256, 2, 4> CfgBig;
+typedef TileCfg<128, 128, 2, 2> CfgSmall;
+
 // Loads one operand tile (ROWS x BK, rows = M or N index) into registers.
-// KMAJ: global is [rows][K] (K contiguous): 4 chunks of 8 per thread.
-// !KMAJ: global is [K][rows] (rows contiguous): 4 k-rows x 8 rows per thread.
-template <bool KMAJ>
+// KMAJ: global is [rows][K] (K contiguous): 16-byte chunks, 8 per row.
+// !KMAJ: global is [K][rows] (rows contiguous): groups of 4 k-rows x 8 rows.
+template <bool KMAJ, int ROWS, int NT>
 struct TileLoader {
-  bf16x8 v[4];
+  static constexpr int NCH = KMAJ ? ROWS * BK / 8 / NT : (BK / 4) * (ROWS / 8) / NT;
+  static constexpr int NV = KMAJ ? NCH : 4 * NCH;
+  static_assert(NCH >= 1, "tile too small for the thread count");
+  bf16x8 v[NV];
   __device__ inline void load(const bf16_t* __restrict__ g, int64_t ld, int64_t row0, int64_t nrows, int64_t k0,
                               int64_t kmax, int tid) {
     if (KMAJ) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int id = tid + GEMM_THREADS * i;
+      for (int i = 0; i < NCH; ++i) {
+        int id = tid + NT * i;
         int r = id >> 3, kc = id & 7;
         int64_t gr = row0 + r, gk = k0 + kc * 8;
         if (gr < nrows && gk < kmax)
@@ -62,33 +84,41 @@ struct TileLoader {
           v[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     } else {
-      int rc = tid & 15, kg = tid >> 4;
-      int64_t gr = row0 + rc * 8;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int64_t gk = k0 + kg * 4 + i;
-        if (gr < nrows && gk < kmax)
-          v[i] = *(const bf16x8*)(g + gk * ld + gr);
-        else
-          v[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < NCH; ++i) {
+        int id = tid + NT * i;
+        int rc = id % (ROWS / 8), kg = id / (ROWS / 8);
+        int64_t gr = row0 + rc * 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int64_t gk = k0 + kg * 4 + q;
+          if (gr < nrows && gk < kmax)
+            v[4 * i + q] = *(const bf16x8*)(g + gk * ld + gr);
+          else
+            v[4 * i + q] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
       }
     }
   }
   __device__ inline void store(bf16_t* __restrict__ lds, int tid) {
     if (KMAJ) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int id = tid + GEMM_THREADS * i;
+      for (int i = 0; i < NCH; ++i) {
+        int id = tid + NT * i;
         int r = id >> 3, kc = id & 7;
         *(bf16x8*)(lds + r * LDS_STRIDE + kc * 8) = v[i];
       }
     } else {
-      int rc = tid & 15, kg = tid >> 4;
-      // v[k][e]: k-row k, element e (row rc*8+e). Write row rc*8+e with its 4 k values.
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bf16x4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
-        *(bf16x4*)(lds + (rc * 8 + e) * LDS_STRIDE + kg * 4) = w;
+      for (int i = 0; i < NCH; ++i) {
+        int id = tid + NT * i;
+        int rc = id % (ROWS / 8), kg = id / (ROWS / 8);
+        // v[4i+q][e]: k-row q, element e (row rc*8+e). Write row rc*8+e with its 4 k values.
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bf16x4 w = {v[4 * i][e], v[4 * i + 1][e], v[4 * i + 2][e], v[4 * i + 3][e]};
+          *(bf16x4*)(lds + (rc * 8 + e) * LDS_STRIDE + kg * 4) = w;
+        }
       }
     }
   }
@@ -105,28 +135,50 @@ __device__ inline void store_out<bf16_t>(bf16_t* C, int64_t idx, float v, float 
   C[idx] = f32_to_bf16(beta != 0.f ? v + beta * bf16_to_f32(C[idx]) : v);
 }
 
-template <bool A_KMAJ, bool B_KMAJ, typename TC, int MODE>
-__global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2][(BM + BN) * LDS_STRIDE];
+// XCD-aware tile order for dense launches (see file comment).
+__device__ inline void dense_tile(int& my, int& nx) {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int total = gx * gy;
+  int L = blockIdx.y * gx + blockIdx.x;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  const int GROUP = 8;
+  const int g = L / (GROUP * gx);
+  const int first = g * GROUP;
+  const int gm = gy - first < GROUP ? gy - first : GROUP;
+  const int within = L - g * GROUP * gx;
+  my = first + within % gm;
+  nx = within / gm;
+}
+
+template <class CFG, bool A_KMAJ, bool B_KMAJ, typename TC, int MODE>
+__global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
+  constexpr int BM = CFG::BM, BN = CFG::BN, NT = CFG::NT, TM = CFG::TM, TN = CFG::TN;
+  constexpr int WTM = BM / CFG::WM, WTN = BN / CFG::WN;  // wave tile
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][CFG::LDS_ELEMS];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / CFG::WN, wn = wave % CFG::WN;
 
   int64_t M = p.M, N = p.N, K = p.K;
   const bf16_t* A = p.A;
   const bf16_t* B = p.B;
   TC* C = (TC*)p.C;
-  int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  int64_t m0, n0;
   int64_t kbeg = 0, kend = K;
 
-  if (MODE == MODE_GROUPED) {
+  if (MODE == MODE_DENSE) {
+    int my, nx;
+    dense_tile(my, nx);
+    m0 = (int64_t)my * BM;
+    n0 = (int64_t)nx * BN;
+  } else if (MODE == MODE_GROUPED) {
     // blockIdx.y enumerates row tiles over all groups in order
+    n0 = (int64_t)blockIdx.x * BN;
     int64_t tile = blockIdx.y, acc = 0;
     int e = 0;
     for (; e < p.E; ++e) {
       int64_t sz = p.offsets[e + 1] - p.offsets[e];
-      int64_t nt = (sz + BM - 1) / BM;
+      int64_t nt = sz > 0 ? (sz + BM - 1) / BM : 0;
       if (tile < acc + nt) break;
       acc += nt;
     }
@@ -136,7 +188,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
     m0 = off + (tile - acc) * BM;
     if (m0 < 0) return;
     B = p.B + (int64_t)e * p.strideB;
-  } else if (MODE == MODE_GROUPED_K) {
+  } else {
+    m0 = (int64_t)blockIdx.y * BM;
+    n0 = (int64_t)blockIdx.x * BN;
     int e = blockIdx.z;
     kbeg = p.offsets[e] < 0 ? 0 : p.offsets[e];
     kend = p.offsets[e + 1] < p.K ? p.offsets[e + 1] : p.K;  // clamped to J
@@ -145,17 +199,16 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
   }
   if (m0 >= M || n0 >= N) return;
 
-  TileLoader<A_KMAJ> la;
-  TileLoader<B_KMAJ> lb;
-  f32x16 acc[2][2];
+  TileLoader<A_KMAJ, BM, NT> la;
+  TileLoader<B_KMAJ, BN, NT> lb;
+  f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  // grouped-K: K runs over absolute job rows [kbeg, kend); tiles start at kbeg
   const int64_t nk = (kend - kbeg + BK - 1) / BK;
   if (nk > 0) {
     la.load(A, p.lda, m0, M, kbeg, kend, tid);
@@ -172,20 +225,19 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
       la.load(A, p.lda, m0, M, k0, kend, tid);
       lb.load(B, p.ldb, n0, N, k0, kend, tid);
     }
-    const bf16_t* As = lds[s];
-    const bf16_t* Bs = lds[s] + BM * LDS_STRIDE;
+    const bf16_t* As = lds[s] + (wm * WTM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
+    const bf16_t* Bs = lds[s] + (BM + wn * WTN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      bf16x8 af[2], bfr[2];
-      const int kofs = kk * 16 + (lane >> 5) * 8;
+      bf16x8 af[TM], bfr[TN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *(const bf16x8*)(As + (wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+      for (int i = 0; i < TM; ++i) af[i] = *(const bf16x8*)(As + i * 32 * LDS_STRIDE + kk * 16);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bfr[j] = *(const bf16x8*)(Bs + (wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+      for (int j = 0; j < TN; ++j) bfr[j] = *(const bf16x8*)(Bs + j * 32 * LDS_STRIDE + kk * 16);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
     if (more) {
       la.store(lds[s ^ 1], tid);
@@ -196,14 +248,14 @@ __global__ __launch_bounds__(GEMM_THREADS) void k_gemm_bf16(GemmArgs p) {
 
   // epilogue: lane holds column (lane&31) and rows 8*(v/4) + 4*(lane>>5) + (v&3)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < TN; ++j) {
+      int64_t col = n0 + wn * WTN + j * 32 + (lane & 31);
       if (col >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        int64_t row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        int64_t row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (row < M) store_out<TC>(C, row * p.ldc + col, p.alpha * acc[i][j][v], p.beta);
       }
     }
@@ -252,6 +304,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t 
 __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int64_t J, int64_t width, int out_bytes,
                                  void* __restrict__ out) {
   int64_t start = offsets[E];
+  if (start < 0) start = 0;
   int64_t n = (J - start) * width;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     if (out_bytes == 4)
@@ -263,10 +316,10 @@ __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-template <int MODE>
+template <class CFG, int MODE>
 static int launch_bf16(const GemmArgs& a, bool a_kmaj, bool b_kmaj, int c_dtype, dim3 grid, hipStream_t s) {
 #define PD_L(AK, BKM, TC) \
-  hipLaunchKernelGGL((k_gemm_bf16<AK, BKM, TC, MODE>), grid, dim3(GEMM_THREADS), 0, s, a)
+  hipLaunchKernelGGL((k_gemm_bf16<CFG, AK, BKM, TC, MODE>), grid, dim3(CFG::NT), 0, s, a)
   if (c_dtype == PD_DTYPE_F32) {
     if (a_kmaj && b_kmaj) PD_L(true, true, float);
     else if (a_kmaj) PD_L(true, false, float);
@@ -288,6 +341,9 @@ static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) 
   return aligned16(ptr) && ld % 8 == 0 && contig_extent % 8 == 0;
 }
 
+// The big tile needs enough tiles to occupy the 256 CUs; otherwise use the small one.
+static bool use_big_tile(int64_t M, int64_t N) { return cdiv(M, 256) * cdiv(N, 256) >= 192; }
+
 }  // namespace pd
 
 using namespace pd;
@@ -299,7 +355,7 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
   if (M < 0 || N < 0 || K < 0 || !A || !B || !C) return fail(PD_EINVAL, "pd_gemm: bad args");
   if (M == 0 || N == 0) return PD_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (cdiv(M, FT) > 65535 || cdiv(N, FT) > 0x7FFFFFFFLL) return fail(PD_EUNSUPPORTED, "pd_gemm: too large");
+  if (cdiv(M, FT) > 65535 || cdiv(N, FT) > 65535) return fail(PD_EUNSUPPORTED, "pd_gemm: too large");
   if (dtype == PD_DTYPE_F32) {
     if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm: fp32 path writes fp32");
     dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT));
@@ -312,8 +368,11 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
   if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N))
     return fail(PD_EUNSUPPORTED, "pd_gemm: bf16 operands need 16B alignment and contiguous dims / ld % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, 0, 0};
-  dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM));
-  return launch_bf16<MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype, grid, s);
+  if (use_big_tile(M, N))
+    return launch_bf16<CfgBig, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
+                                           dim3((unsigned)cdiv(N, 256), (unsigned)cdiv(M, 256)), s);
+  return launch_bf16<CfgSmall, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
+                                           dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128)), s);
 }
 
 int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
@@ -330,10 +389,10 @@ int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, in
                      out_dtype == PD_DTYPE_F32 ? 4 : 2, out);
   GemmArgs a{J, N, K, (const bf16_t*)lhs, K, (const bf16_t*)rhs, b_kmaj ? K : N, out, N, 1.f, 0.f, offsets, E,
              K * N, 0};
-  int64_t max_tiles = cdiv(J, BM) + E;
+  int64_t max_tiles = cdiv(J, CfgSmall::BM) + E;
   if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: too many rows");
-  dim3 grid((unsigned)cdiv(N, BN), (unsigned)max_tiles);
-  return launch_bf16<MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
+  dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)max_tiles);
+  return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
 int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets, int64_t J, int E, int64_t K,
@@ -342,11 +401,11 @@ int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets
     return fail(PD_EINVAL, "pd_grouped_gemm_dw: bad args");
   if (!bf16_operand_ok(lhs, K, K) || !bf16_operand_ok(dout, N, N))
     return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw: K and N must be multiples of 8 with 16B-aligned bases");
-  if (E > 65535 || cdiv(K, BM) > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw: E or K too large");
+  if (E > 65535 || cdiv(K, CfgSmall::BM) > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw: E or K too large");
   // out[e] (M=K_in x N) = lhs[rows_e]^T (A stored [J,K]: M-contiguous) @ dout[rows_e] ([J,N])
   GemmArgs a{K, N, J, (const bf16_t*)lhs, K, (const bf16_t*)dout, N, out, N, 1.f, 0.f, offsets, E, 0, K * N};
-  dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(K, BM), (unsigned)E);
-  return launch_bf16<MODE_GROUPED_K>(a, false, false, out_dtype, grid, (hipStream_t)stream);
+  dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)cdiv(K, CfgSmall::BM), (unsigned)E);
+  return launch_bf16<CfgSmall, MODE_GROUPED_K>(a, false, false, out_dtype, grid, (hipStream_t)stream);
 }
 
 }  // extern "C"
