@@ -1,16 +1,24 @@
 """Masked-component fwd+bwd throughput on one MI355X.
 
-Default workload: the single decomposed dense linear 768 -> 3072 (x bf16 [4096, 768] ~
-N(0,1), U/V ~ N(0, 1/d), C = 4096 components, per-component gate MLP hidden 16 with
-leaky-hard-sigmoid squashing, bf16 Threefry mask uniforms, fp32 accumulation, one fused
-fwd+bwd of stochastic-recon MSE + sum_c mean_t |g_upper|^2). A step is one call of
-`pd_dense_step` on resident inputs: clean target, h = x@V, gate/mask, (h*m)@U, MSE,
-imp-min, and the backward to dV, dU and the gate parameters.
+Workloads (synthetic data of the named shapes, random-init weights):
 
-Prints one JSON line: the throughput (tokens/s), the roofline of the dominant kernel
-(measured with HIP events on the kernels' own stream over the timed region), per-phase
-times, and the CPU baseline (the oracle's C restatement, OpenMP, on a bounded token
-sample, timed in this run on this host).
+- `qwen35moe4L` (default; the MoE stack the throughput target is quoted on): 4 layers of
+  width 512, 42 experts with top-8 softmax routing, SwiGLU experts 512->256->512, every
+  expert gate/up/down matrix decomposed with c=512 components per expert, 8192 tokens,
+  bf16. A step is one `pd_moe_stack_step`: clean forward on the frozen experts, masked
+  forward (grouped masked-component matmuls over bucketed tokens), MSE recon of the final
+  residual + L_p (p=2) imp-min over the selected CI, and the full backward.
+- `dense768x3072_C4096`: one decomposed dense linear 768->3072, x bf16 [4096, 768],
+  C=4096, per-component gate MLP hidden 16, bf16 Threefry mask uniforms, stochastic-
+  recon MSE + sum_c mean_t |g_upper|^2 fwd+bwd (`pd_dense_step`).
+
+Prints one JSON line: tokens/s, the roofline of the dominant kernel (its duration
+measured with HIP events on the kernels' own stream inside the timed region), per-phase
+times, and the CPU baseline (the oracle's restatement of the same step on a bounded
+token sample, timed in this run on this host).
+
+`python bench.py --rocprof-summary DB CMD` turns a rocprofv3 results DB into the
+per-kernel table kept under profiles/ (no GPU needed).
 """
 
 from __future__ import annotations
@@ -27,60 +35,14 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_BF16_FLOPS = 2.5e15
-PEAK_F32_FLOPS = 157.3e12
 PEAK_HBM = 8.0e12
-
-WORKLOADS = {
-    "dense768x3072_C4096": dict(T=4096, d_in=768, d_out=3072, C=4096),
-}
 METRIC = "masked-component fwd+bwd tokens/s on 1 MI355X; % of MFMA/HBM roofline"
-
-
-def phase_work(name, T, d_in, d_out, C, es):
-    """(kind, amount): algorithmic FLOPs for GEMM phases, algorithmic HBM bytes for the
-    fused elementwise passes (fwd reads h and writes h*m; bwd reads h and d(h*m) and
-    writes dh; u is regenerated, never stored)."""
-    table = {
-        "transpose_inputs": ("byte", 2 * (T * d_in + d_in * C + C * d_out) * es),
-        "gemm_target": ("flop", 2 * T * d_in * d_out),
-        "gemm_xV": ("flop", 2 * T * d_in * C),
-        "gate_mask_fwd": ("byte", 2 * T * C * es),
-        "gemm_actsU": ("flop", 2 * T * C * d_out),
-        "recon": ("byte", 3 * T * d_out * es),
-        "loss_final": ("byte", 0),
-        "gemm_dU": ("flop", 2 * T * C * d_out),
-        "gemm_da": ("flop", 2 * T * C * d_out),
-        "gate_mask_bwd": ("byte", 3 * T * C * es),
-        "gate_grad_reduce": ("byte", 0),
-        "gemm_dV": ("flop", 2 * T * d_in * C),
-    }
-    return table[name]
-
-
-def cpu_baseline(T_sample, d_in, d_out, C, reps=3):
-    import numpy as np
-
-    from oracle import cpu
-    from oracle import pd_oracle as po
-
-    rng = np.random.default_rng(0)
-    x = rng.normal(size=(T_sample, d_in)).astype(np.float32)
-    W = (rng.normal(size=(d_out, d_in)) / np.sqrt(d_in)).astype(np.float32)
-    V = (rng.normal(size=(d_in, C)) / np.sqrt(d_in)).astype(np.float32)
-    U = (rng.normal(size=(C, d_out)) / np.sqrt(C)).astype(np.float32)
-    gp = po.GateParams(rng.normal(size=(C, 16)).astype(np.float32) * 1.4, np.zeros((C, 16), np.float32),
-                       rng.normal(size=(C, 16)).astype(np.float32) * 0.35, np.full(C, 0.3, np.float32))
-    mk, dk = po.site_keys((0, 0), 0)
-    cpu.dense_step(x, W, V, U, gp, mk, dk)  # warmup
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        cpu.dense_step(x, W, V, U, gp, mk, dk)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": T_sample / med, "unit": "tokens/s", "cores": cpu.num_threads(), "kind": "port",
-            "sample": f"{T_sample} of the workload's tokens (same d_in/d_out/C), fp32 C+OpenMP restatement of the "
-                      f"same step, median of {reps} after 1 warmup; {med * 1e3:.1f} ms per sample step"}
+DENSE = "dense768x3072_C4096"
+MOE = "qwen35moe4L"
+WORKLOADS = {
+    DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
+    MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4),
+}
 
 
 def rocprof_summary(db_path: str, command: str) -> str:
@@ -100,31 +62,75 @@ def rocprof_summary(db_path: str, command: str) -> str:
     return "\n".join(out) + "\n"
 
 
-def main():
-    if "--rocprof-summary" in sys.argv:
-        i = sys.argv.index("--rocprof-summary")
-        db, cmd = sys.argv[i + 1], sys.argv[i + 2]
-        print(rocprof_summary(db, cmd))
-        return
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="dense768x3072_C4096", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-tokens", type=int, default=256)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every GPU box here has one MI355X; --gpus {args.gpus} is not run. "
-              "Multi-GPU sharding is described in DESIGN.md, not measured.", file=sys.stderr)
-        sys.exit(2)
+def roofline(kind, amount_per_launch, ms_per_launch, kernel, launches_per_step):
+    dur = ms_per_launch * 1e-3
+    if kind == "flop":
+        achieved = amount_per_launch / dur / 1e12
+        return {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / (PEAK_BF16_FLOPS / 1e12), "traffic": None, "kernel": kernel,
+                "avg_launch_ms": ms_per_launch, "work_per_launch": amount_per_launch,
+                "launches_per_step": launches_per_step}
+    achieved = amount_per_launch / dur / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": achieved / (PEAK_HBM / 1e9), "traffic": None, "kernel": kernel, "avg_launch_ms": ms_per_launch,
+            "work_per_launch": amount_per_launch, "launches_per_step": launches_per_step}
 
+
+# ============================================================== dense single site
+def dense_phase_work(name, T, d_in, d_out, C, es):
+    """(kind, amount): algorithmic FLOPs for GEMM phases, algorithmic HBM bytes for the
+    fused elementwise passes (fwd reads h and writes h*m; bwd reads h and d(h*m) and
+    writes dh; u is regenerated or byte-stored, never stored at full width)."""
+    table = {
+        "transpose_inputs": ("byte", 2 * (T * d_in + d_in * C + C * d_out) * es),
+        "gemm_target": ("flop", 2 * T * d_in * d_out),
+        "gemm_xV": ("flop", 2 * T * d_in * C),
+        "gate_mask_fwd": ("byte", 2 * T * C * es),
+        "gemm_actsU": ("flop", 2 * T * C * d_out),
+        "recon": ("byte", 3 * T * d_out * es),
+        "loss_final": ("byte", 0),
+        "gemm_dU": ("flop", 2 * T * C * d_out),
+        "gemm_da": ("flop", 2 * T * C * d_out),
+        "gate_mask_bwd": ("byte", 3 * T * C * es),
+        "gate_grad_reduce": ("byte", 0),
+        "gemm_dV": ("flop", 2 * T * d_in * C),
+    }
+    return table[name]
+
+
+def dense_cpu_baseline(T_sample, d_in, d_out, C, reps=3):
+    import numpy as np
+
+    from oracle import cpu
+    from oracle import pd_oracle as po
+
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=(T_sample, d_in)).astype(np.float32)
+    W = (rng.normal(size=(d_out, d_in)) / np.sqrt(d_in)).astype(np.float32)
+    V = (rng.normal(size=(d_in, C)) / np.sqrt(d_in)).astype(np.float32)
+    U = (rng.normal(size=(C, d_out)) / np.sqrt(C)).astype(np.float32)
+    gp = po.GateParams(rng.normal(size=(C, 16)).astype(np.float32) * 1.4, np.zeros((C, 16), np.float32),
+                       rng.normal(size=(C, 16)).astype(np.float32) * 0.35, np.full(C, 0.3, np.float32))
+    mk, dk = po.site_keys((0, 0), 0)
+    cpu.dense_step(x, W, V, U, gp, mk, dk)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cpu.dense_step(x, W, V, U, gp, mk, dk)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cpu.num_threads(), "kind": "port",
+            "sample": f"{T_sample} of the workload's tokens (same d_in/d_out/C), fp32 C+OpenMP restatement of the "
+                      f"same step, median of {reps} after 1 warmup; {med * 1e3:.1f} ms per sample step"}
+
+
+def run_dense(args):
     import torch
 
-    from param_decomp_amd import hip_events
+    from param_decomp_amd import hip_events, prng
     from param_decomp_amd.dense_step import DenseSiteStep
 
-    cfg = WORKLOADS[args.workload]
+    cfg = WORKLOADS[DENSE]
     T, d_in, d_out, C = cfg["T"], cfg["d_in"], cfg["d_out"], cfg["C"]
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -135,11 +141,9 @@ def main():
     gate = (torch.randn(C, 16, device=dev, generator=gen) * 2**0.5, torch.zeros(C, 16, device=dev),
             torch.randn(C, 16, device=dev, generator=gen) * (2 / 16) ** 0.5, torch.zeros(C, device=dev))
     step = DenseSiteStep(T, d_in, d_out, C, dtype=torch.bfloat16, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0)
-    draw_key = (0, 0)
-    from param_decomp_amd import prng
 
     def keys(i):
-        return step.site_keys(prng.fold_in(draw_key, i), 0)
+        return step.site_keys(prng.fold_in((0, 0), i), 0)
 
     for i in range(args.warmup):
         step.step(x, W, V, U, gate, *keys(i))
@@ -149,62 +153,197 @@ def main():
     stream = torch.cuda.current_stream().cuda_stream
     start, stop = hip_events.create(2)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     hip_events.record(start, stream)
     for i in range(args.steps):
         step.step(x, W, V, U, gate, *keys(args.warmup + i), events=arrs[i])
     hip_events.record(stop, stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = hip_events.elapsed_ms(start, stop)
-    ms_per_step = gpu_ms / args.steps
+    ms_per_step = hip_events.elapsed_ms(start, stop) / args.steps
     phase_ms = {p: 0.0 for p in DenseSiteStep.PHASES}
     for e in evs:
         for j, p in enumerate(DenseSiteStep.PHASES):
             phase_ms[p] += hip_events.elapsed_ms(e[j], e[j + 1]) / args.steps
-    for e in evs:
         hip_events.destroy(e)
     assert torch.isfinite(step.grads.losses).all(), step.grads.losses
     dom = max(phase_ms, key=phase_ms.get)
-    kind, amount = phase_work(dom, T, d_in, d_out, C, 2)
-    dur = phase_ms[dom] * 1e-3
-    if kind == "flop":
-        achieved = amount / dur / 1e12
-        roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / (PEAK_BF16_FLOPS / 1e12), "traffic": None, "kernel": dom,
-                "avg_launch_ms": phase_ms[dom], "work_per_launch": amount}
-    else:
-        achieved = amount / dur / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": achieved / (PEAK_HBM / 1e9), "traffic": None, "kernel": dom,
-                "avg_launch_ms": phase_ms[dom], "work_per_launch": amount}
+    kind, amount = dense_phase_work(dom, T, d_in, d_out, C, 2)
     in_proj, out_proj = 2 * T * d_in * C, 2 * T * C * d_out
-    step_flops = 2 * in_proj + 3 * out_proj  # reference rule: fwd in+out, bwd in + 2*out
-    result = {
+    step_flops = 2 * in_proj + 3 * out_proj  # reference rule: fwd in+out, bwd in + 2*out (input not mask-dependent)
+    res = {
+        "tokens": T, "ms_per_step": ms_per_step,
+        "config": {"workload": DENSE, "tokens": T, "d_in": d_in, "d_out": d_out, "C": C, "gate_hidden": 16,
+                   "imp_min": "p=2", "recon": "mse", "mask_draw": "threefry bf16 (partitionable)"},
+        "step_flops": step_flops, "phases_ms": phase_ms, "roofline": roofline(kind, amount, phase_ms[dom], dom, 1),
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = dense_cpu_baseline(args.cpu_tokens, d_in, d_out, C)
+    return res
+
+
+# ============================================================== MoE stack
+def moe_site_flops(J, d, f, c):
+    """Per-site (in_proj, out_proj) FLOPs: gate/up read width d and write f; down reads
+    f and writes d (reference rule, `pd/core/flops/target.py:39-93`)."""
+    return {"gate": (2 * J * d * c, 2 * J * c * f), "up": (2 * J * d * c, 2 * J * c * f),
+            "down": (2 * J * f * c, 2 * J * c * d)}
+
+
+def moe_step_flops(cfg):
+    J = cfg["T"] * cfg["k"]
+    per = moe_site_flops(J, cfg["d"], cfg["f"], cfg["c"])
+    total = 0
+    for layer in range(cfg["L"]):
+        for s, (i, o) in per.items():
+            dx = 0 if (layer == 0 and s != "down") else 1  # layer-0 gate/up inputs carry no mask dependence
+            total += (i + o) + i * (dx + 1) + o * 2
+    return total
+
+
+def moe_cpu_baseline(cfg, T_sample, reps=1):
+    import numpy as np
+
+    from oracle import moe_oracle as mo
+
+    mc = mo.MoEConfig(T=T_sample, d=cfg["d"], f=cfg["f"], E=cfg["E"], k=cfg["k"], c=cfg["c"], L=cfg["L"])
+    params, x0, ci = mo.init_moe(mc, np.random.default_rng(0))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        mo.moe_stack_step(mc, params, x0, ci, (0, 1))
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{T_sample} of the workload's 8192 tokens (full widths, 42 experts, 4 layers), NumPy float64 "
+                      f"restatement of the same step (BLAS-threaded matmuls), median of {reps}; "
+                      f"{med * 1e3:.0f} ms per sample step"}
+
+
+def run_moe(args):
+    import torch
+
+    from param_decomp_amd import hip_events, prng
+    from param_decomp_amd.moe_step import CATEGORIES, MoEStackStep, MoEWeights
+
+    cfg = WORKLOADS[MOE]
+    T, d, f, E, k, c, Ln = (cfg[x] for x in ("T", "d", "f", "E", "k", "c", "L"))
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, scale):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(torch.bfloat16)
+
+    w = MoEWeights(ln=torch.zeros(Ln, d, device=dev), router=rn(Ln, E, d, scale=d**-0.5),
+                   Wg=rn(Ln, E, d, f, scale=d**-0.5), Wu=rn(Ln, E, d, f, scale=d**-0.5),
+                   Wd=rn(Ln, E, f, d, scale=f**-0.5), Vg=rn(Ln, E, d, c, scale=d**-0.5),
+                   Ug=rn(Ln, E, c, f, scale=c**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
+                   Uu=rn(Ln, E, c, f, scale=c**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
+                   Ud=rn(Ln, E, c, d, scale=c**-0.5))
+    x0 = rn(T, d, scale=1.0)
+    ci = (torch.rand(Ln, 3, T, k, c, device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
+    step = MoEStackStep(T, d, f, E, k, c, Ln, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0)
+    for i in range(args.warmup):
+        step.step(x0, w, ci, prng.fold_in((0, 0), i))
+    cap = 1024
+    evs = [hip_events.create(cap) for _ in range(args.steps)]
+    arrs = [hip_events.array(e) for e in evs]
+    cats = [torch.zeros(cap, dtype=torch.int32) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    counts = []
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        counts.append(step.step_timed(x0, w, ci, prng.fold_in((0, 0), args.warmup + i), arrs[i], cats[i]))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms_per_step = hip_events.elapsed_ms(start, stop) / args.steps
+    cat_ms = {name: 0.0 for name in CATEGORIES}
+    cat_n = {name: 0 for name in CATEGORIES}
+    for e, cc, n in zip(evs, cats, counts):
+        for j in range(n - 1):
+            name = CATEGORIES[int(cc[j])]
+            cat_ms[name] += hip_events.elapsed_ms(e[j], e[j + 1]) / args.steps
+            cat_n[name] += 1
+        hip_events.destroy(e)
+    for name in cat_n:
+        cat_n[name] //= args.steps
+    assert torch.isfinite(step.losses).all(), step.losses
+    # algorithmic work per category (per step) for the roofline of the dominant one
+    J = T * k
+    per = moe_site_flops(J, d, f, c)
+    work = {
+        "gemm_fwd": ("flop", Ln * sum(i + o for i, o in per.values())),
+        "gemm_dx": ("flop", sum(o + (i if not (layer == 0 and s != "down") else i) for layer in range(Ln)
+                                for s, (i, o) in per.items())),
+        "gemm_dw": ("flop", Ln * sum(i + o for i, o in per.values())),
+        "mask_fwd": ("byte", Ln * 3 * J * c * (2 + 2 + 2 + 1)),   # read ci, h; write acts, u bits
+        "mask_bwd": ("byte", Ln * 3 * J * c * (2 + 2 + 1 + 2 + 2)),  # read ci, h, u, d_acts; write d_h, d_ci
+    }
+    dom = max((n for n in cat_ms if n in work), key=cat_ms.get)
+    kind, amount = work[dom]
+    launches = cat_n[dom]
+    roof = roofline(kind, amount / launches, cat_ms[dom] / launches, dom, launches)
+    res = {
+        "tokens": T, "ms_per_step": ms_per_step,
+        "config": {"workload": MOE, "tokens": T, "width": d, "experts": E, "top_k": k, "expert_ffn": f,
+                   "c_per_expert": c, "layers": Ln, "imp_min": "p=2", "recon": "mse(final residual)",
+                   "mask_draw": "threefry bf16 (partitionable)", "mixers_and_shared_expert": "excluded"},
+        "step_flops": moe_step_flops(cfg), "phases_ms": cat_ms, "launches_per_step": cat_n, "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = moe_cpu_baseline(cfg, args.cpu_tokens)
+    return res
+
+
+def main():
+    if "--rocprof-summary" in sys.argv:
+        i = sys.argv.index("--rocprof-summary")
+        print(rocprof_summary(sys.argv[i + 1], sys.argv[i + 2]))
+        return
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default=MOE, choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-tokens", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every GPU box here has one MI355X; --gpus {args.gpus} is not run. "
+              "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
+        sys.exit(2)
+    if args.cpu_tokens is None:
+        args.cpu_tokens = 64 if args.workload == MOE else 256
+    res = run_moe(args) if args.workload == MOE else run_dense(args)
+    ms = res["ms_per_step"]
+    out = {
         "metric": METRIC,
-        "value": T / (ms_per_step * 1e-3),
+        "value": res["tokens"] / (ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded torch.randn of the named shapes; random-init U/V/gate)",
-        "config": {"workload": args.workload, "tokens": T, "d_in": d_in, "d_out": d_out, "C": C, "gate_hidden": 16,
-                   "imp_min": "p=2", "recon": "mse", "mask_draw": "threefry bf16 (partitionable)",
-                   "parallelism": "single GPU"},
-        "step_mfma_frac": step_flops / (ms_per_step * 1e-3) / PEAK_BF16_FLOPS,
-        "step_tflops": step_flops / (ms_per_step * 1e-3) / 1e12,
-        "wall_ms_per_step": wall * 1e3 / args.steps,
-        "phases_ms": phase_ms,
-        "roofline": roof,
+        "data": "synthetic (seeded torch.randn / torch.rand of the named shapes; random-init target and components)",
+        "config": res["config"],
+        "step_tflops": res["step_flops"] / (ms * 1e-3) / 1e12,
+        "step_mfma_frac": res["step_flops"] / (ms * 1e-3) / PEAK_BF16_FLOPS,
+        "phases_ms": res["phases_ms"],
+        "roofline": res["roofline"],
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_tokens, d_in, d_out, C)
-    print(json.dumps(result))
+    if "launches_per_step" in res:
+        out["launches_per_step"] = res["launches_per_step"]
+    if "cpu_baseline" in res:
+        out["cpu_baseline"] = res["cpu_baseline"]
+    print(json.dumps(out))
 
 
 if __name__ == "__main__":

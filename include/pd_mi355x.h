@@ -201,6 +201,49 @@ int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* group_offse
 int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* group_offsets, int64_t J, int E, int64_t K,
                        int64_t N, void* out, int out_dtype, void* stream);
 
+/* ---- the decomposed MoE stack step (the routed-expert hot path end to end) ----
+ * L layers of: h2 = rms_norm_zero_centered(r) (target_ports/qwen3_5_moe.py:33-41),
+ * fp32 router softmax + top-k + renormalized weights (pd/targets/qwen36_moe.py:473-514),
+ * stable expert bucketing (pd/routed/experts.py:115-123), the three decomposed expert
+ * sites in job space (pd/targets/qwen36_moe.py:2752-2837: acts = gmm(x_jobs, V) * mask,
+ * out = gmm(acts, U), routing weights folded into the down input in fp32,
+ * :2272-2282), r += sum_jobs(down). A clean forward on the frozen expert weights W (its
+ * routing weights applied in the fp32 combine) pins each masked layer's expert indices
+ * (pd/targets/qwen36_moe.py:2923-2965). Masks m = lower(ci) + (1-lower(ci)) u are drawn
+ * per (kind, layer) with key fold_in(fold_in(split(draw_key)[0], kind), layer), kind =
+ * 11/12/13 for gate/up/down (pd/targets/qwen36_moe.py:3374-3401), over the selected-CI
+ * values [T, k*c] in bf16. Loss = recon_coeff * mean((r_L - rc_L)^2) + imp_coeff *
+ * sum over sites/layers of sum(upper(ci)^p)/T (the selected arm of
+ * pd/core/losses.py:357-372).
+ * Layouts (all bf16 unless noted): x0 [T,d]; ln fp32 [L,d]; router [L,E,d];
+ * Wg, Wu [L,E,d,f]; Wd [L,E,f,d]; Vg, Vu [L,E,d,c]; Ug, Uu [L,E,c,f]; Vd [L,E,f,c];
+ * Ud [L,E,c,d]; ci_pre [L,3,T,k,c] (site order gate, up, down; slot s = the token's
+ * s-th selected expert). Outputs: losses[3] = {loss, recon, imp}; the six V/U
+ * gradients fp32 in the V/U shapes; d_ci_pre bf16 [L,3,T,k,c]; top_idx_out int32
+ * [L,T,k] (nullable).
+ * E <= 64; d, f, c multiples of 8. */
+size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L);
+int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                      const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                      const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                      const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p, float imp_coeff,
+                      float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
+                      float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
+                      void* stream);
+/* pd_moe_stack_step recording a hipEvent_t before each launch group and one at the
+ * end; categories[i] labels the interval [i, i+1): 0 clean forward, 1 masked norm /
+ * router / bucketing / gather, 2 grouped GEMMs fwd, 3 mask fwd, 4 SwiGLU fold,
+ * 5 combine / loss / gathers, 6 grouped GEMMs d_input, 7 grouped GEMMs d_weight,
+ * 8 mask bwd, 9 router+norm token backward, 10 end. *n_recorded = events used. */
+int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                            const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                            const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p,
+                            float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
+                            float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
+                            void* workspace, size_t workspace_bytes, void* stream, void** events,
+                            int32_t* categories, int capacity, int* n_recorded);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,221 @@
+"""NumPy restatement of the decomposed MoE stack step (oracle only; float64 arithmetic).
+
+The stack is the reference's MoE layer with every routed expert matrix decomposed,
+mixers and the shared expert excluded: per layer
+`h2 = rms_norm_zero_centered(r)` (`param_decomp/param_decomp/target_ports/qwen3_5_moe.py:33-41`),
+fp32 router softmax, top-k (`pd/targets/qwen36_moe.py:473-514`), jobs schedule
+(`pd/routed/experts.py:115-123`), decomposed expert sites in job space
+(`pd/targets/qwen36_moe.py:2752-2837`: `acts = gmm(x_jobs, V) * mask_jobs`,
+`out = gmm(acts, U)`, routing weights folded into the down input in fp32,
+`_fold_routing_weights` `:2272-2282`, unweighted `sum_jobs`), `r += routed`. The clean
+forward runs the frozen expert weights with the weights applied to the down output in
+the fp32 combine (`combine_jobs`, `pd/routed/experts.py:351-359`) and pins the masked
+pass's expert indices (`_moe_forward`, `pd/targets/qwen36_moe.py:2923-2965`). Masks are
+drawn per (kind, layer) from `fold_in(fold_in(split(draw_key)[0], kind_index), layer)`
+(`pd/targets/qwen36_moe.py:3374-3401`) over the selected-CI values `[T, k*c]`
+(`SelectedCI`, `pd/core/components.py:81-114`). Loss: MSE between the masked and clean
+final residual streams plus the L_p imp-min over the selected upper CI values
+(`pd/core/losses.py:357-372` selected arm).
+
+`bf16_storage=True` rounds to bf16 exactly the tensors the GPU step stores in bf16;
+everything between is float64.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from oracle import pd_oracle as po
+from oracle import threefry as tf
+
+KIND_INDEX = {"gate": 11, "up": 12, "down": 13}
+SITES = ("gate", "up", "down")
+
+
+@dataclass
+class MoEConfig:
+    T: int
+    d: int
+    f: int
+    E: int
+    k: int
+    c: int
+    L: int
+    eps: float = 1e-6
+
+
+def sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def silu(x):
+    return x * sigmoid(x)
+
+
+def silu_grad(x):
+    s = sigmoid(x)
+    return s * (1.0 + x * (1.0 - s))
+
+
+def rms_norm_zero_centered(x, w, eps):
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * r * (1.0 + w), r
+
+
+def rms_norm_vjp(x, w, r, dy):
+    a = (1.0 + w) * dy
+    d = x.shape[-1]
+    return r * a - x * r**3 * np.sum(a * x, axis=-1, keepdims=True) / d
+
+
+def site_mask_keys(draw_key, layer):
+    src_base, _ = tf.split(draw_key)
+    return {s: tf.fold_in(tf.fold_in(src_base, KIND_INDEX[s]), layer) for s in SITES}
+
+
+def grouped_T(lhs, rhs, sizes):
+    """`lhs[rows_e] @ rhs[e].T` (the grouped matmul's d_input product)."""
+    return po.grouped_matmul(lhs, np.transpose(rhs, (0, 2, 1)), sizes)
+
+
+def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
+                   bf16_storage=False):
+    """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
+    ci_pre[l][site]: [T, k, c]. Returns dict(loss, recon, imp, grads, d_ci_pre,
+    top_idx, r_final, rc_final)."""
+    rb = po.round_bf16 if bf16_storage else (lambda a: a)
+    T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
+    # ---------------- clean forward (frozen weights)
+    rc = rb(x0)
+    tops = []
+    for l in range(cfg.L):
+        P = params[l]
+        h2c, _ = rms_norm_zero_centered(rc, P["ln"], cfg.eps)
+        h2c = rb(h2c)
+        probs = po.softmax(h2c @ P["router"].T)
+        idx = po.select_experts(probs, k)
+        w = po.expert_mixing_weights(probs, idx)
+        jobs = po.routed_jobs(idx, E)
+        xj = h2c[jobs.sort_idx // k]
+        g = rb(po.grouped_matmul(xj, P["Wg"], jobs.group_sizes))
+        u = rb(po.grouped_matmul(xj, P["Wu"], jobs.group_sizes))
+        din = rb(silu(g) * u)
+        down = rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes))
+        routed = rb(po.combine_jobs(down, jobs, w))
+        rc = rb(rc + routed)
+        tops.append(idx)
+    # ---------------- masked forward (pinned indices)
+    r = rb(x0)
+    saved = []
+    imp = 0.0
+    for l in range(cfg.L):
+        P = params[l]
+        h2, rinv = rms_norm_zero_centered(r, P["ln"], cfg.eps)
+        h2 = rb(h2)
+        probs = po.softmax(h2 @ P["router"].T)
+        idx = tops[l]
+        w = po.expert_mixing_weights(probs, idx)
+        jobs = po.routed_jobs(idx, E)
+        keys = site_mask_keys(draw_key, l)
+        xj = h2[jobs.sort_idx // k]
+        S = {}
+        for s in SITES:
+            pre = ci_pre[l][s]
+            lo = po.lower_leaky(pre)
+            up = po.upper_leaky(pre)
+            imp += float(np.sum(up**p)) / T
+            ut = tf.uniform(keys[s], (T, k * c), "bfloat16").reshape(T, k, c)
+            m_tok = lo + (1.0 - lo) * ut
+            S[s] = dict(pre=pre, lo=lo, up=up, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx])
+        wj = w.reshape(-1)[jobs.sort_idx]
+        for s in ("gate", "up"):
+            S[s]["h"] = rb(po.grouped_matmul(xj, P["V" + s[0]], jobs.group_sizes))
+            S[s]["acts"] = rb(S[s]["h"] * S[s]["m"])
+            S[s]["out"] = rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
+        gq, uq = S["gate"]["out"], S["up"]["out"]
+        din = rb(silu(gq) * uq * wj[:, None])
+        S["down"]["h"] = rb(po.grouped_matmul(din, P["Vd"], jobs.group_sizes))
+        S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["m"])
+        dout = rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
+        routed = rb(po.sum_jobs(dout, jobs))
+        saved.append(dict(r=r, rinv=rinv, h2=h2, probs=probs, w=w, wj=wj, jobs=jobs, xj=xj, S=S, din=din, idx=idx))
+        r = rb(r + routed)
+    n = T * cfg.d
+    recon = float(np.mean((r - rc) ** 2))
+    loss = recon_coeff * recon + imp_coeff * imp
+    # ---------------- backward
+    dr = rb(recon_coeff * 2.0 * (r - rc) / n)
+    grads = [dict() for _ in range(cfg.L)]
+    d_pre = [dict() for _ in range(cfg.L)]
+    for l in reversed(range(cfg.L)):
+        P, sv = params[l], saved[l]
+        jobs, S = sv["jobs"], sv["S"]
+        sizes = jobs.group_sizes
+        d_dout = dr[jobs.sort_idx // k]
+        # down site
+        Sd = S["down"]
+        d_acts = rb(grouped_T(d_dout, P["Ud"], sizes))
+        grads[l]["Ud"] = po.transposed_grouped_matmul(Sd["acts"], d_dout, sizes)
+        Sd["dm"] = d_acts * Sd["h"]
+        d_h = rb(d_acts * Sd["m"])
+        grads[l]["Vd"] = po.transposed_grouped_matmul(sv["din"], d_h, sizes)
+        d_din = rb(grouped_T(d_h, P["Vd"], sizes))
+        # SwiGLU fold
+        gq, uq, wj = S["gate"]["out"], S["up"]["out"], sv["wj"]
+        sg = silu(gq)
+        d_g = rb(d_din * uq * wj[:, None] * silu_grad(gq))
+        d_u = rb(d_din * sg * wj[:, None])
+        d_wj = np.sum(d_din * sg * uq, axis=-1)
+        d_xj = np.zeros_like(sv["xj"])
+        for s, dgo in (("gate", d_g), ("up", d_u)):
+            Ss = S[s]
+            d_acts = rb(grouped_T(dgo, P["U" + s[0]], sizes))
+            grads[l]["U" + s[0]] = po.transposed_grouped_matmul(Ss["acts"], dgo, sizes)
+            Ss["dm"] = d_acts * Ss["h"]
+            d_h = rb(d_acts * Ss["m"])
+            grads[l]["V" + s[0]] = po.transposed_grouped_matmul(sv["xj"], d_h, sizes)
+            d_xj = d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
+        # mask pullback to the CI preactivations (token-major)
+        for s in SITES:
+            Ss = S[s]
+            dm_tok = np.zeros((T * k, c))
+            dm_tok[jobs.sort_idx] = Ss["dm"]
+            dm_tok = dm_tok.reshape(T, k, c)
+            dlo = dm_tok * (1.0 - Ss["u"])
+            dup = imp_coeff * p * Ss["up"] ** (p - 1.0) / T
+            d_pre[l][s] = rb(po.lower_leaky_vjp(Ss["pre"], dlo) + po.upper_leaky_vjp(Ss["pre"], dup))
+        # routing weights -> probs -> logits -> h2
+        d_w = d_wj[jobs.inv_sort_idx].reshape(T, k)
+        w, probs, idx = sv["w"], sv["probs"], sv["idx"]
+        Ssum = np.take_along_axis(probs, idx.astype(np.int64), axis=-1).sum(-1, keepdims=True)
+        d_psel = (d_w - np.sum(d_w * w, axis=-1, keepdims=True)) / Ssum
+        d_probs = np.zeros_like(probs)
+        np.put_along_axis(d_probs, idx.astype(np.int64), d_psel, axis=-1)
+        d_logits = probs * (d_probs - np.sum(probs * d_probs, axis=-1, keepdims=True))
+        d_h2 = po.gather_tokens_vjp(d_xj, jobs) + d_logits @ P["router"]
+        dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
+        dr = rb(dr + dx)
+    return dict(loss=loss, recon=recon, imp=imp, grads=grads, d_ci_pre=d_pre, top_idx=tops, r_final=r,
+                rc_final=rc, dx0=dr)
+
+
+def init_moe(cfg: MoEConfig, rng):
+    """Random target and components of the stated shapes (the step's synthetic setup)."""
+    d, f, E, c = cfg.d, cfg.f, cfg.E, cfg.c
+
+    def rn(*shape, scale=1.0):
+        return rng.standard_normal(size=shape, dtype=np.float32).astype(np.float64) * scale
+
+    params = []
+    for _ in range(cfg.L):
+        P = dict(ln=rn(d, scale=0.1), router=rn(E, d, scale=d**-0.5),
+                 Wg=rn(E, d, f, scale=d**-0.5), Wu=rn(E, d, f, scale=d**-0.5), Wd=rn(E, f, d, scale=f**-0.5),
+                 Vg=rn(E, d, c, scale=d**-0.5), Ug=rn(E, c, f, scale=c**-0.5),
+                 Vu=rn(E, d, c, scale=d**-0.5), Uu=rn(E, c, f, scale=c**-0.5),
+                 Vd=rn(E, f, c, scale=f**-0.5), Ud=rn(E, c, d, scale=c**-0.5))
+        params.append(P)
+    x0 = rn(cfg.T, d)
+    ci = [{s: rng.uniform(-0.3, 1.3, size=(cfg.T, cfg.k, c)) for s in SITES} for _ in range(cfg.L)]
+    return params, x0, ci

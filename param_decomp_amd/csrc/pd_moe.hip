@@ -1,0 +1,705 @@
+// The decomposed MoE stack step (gfx950): L layers of
+//   h2 = rms_norm_zero_centered(r)        target_ports/qwen3_5_moe.py:33-41
+//   router softmax, top-k, mixing weights pd/targets/qwen36_moe.py:473-514, 2923-2965
+//   jobs = stable bucketing by expert     pd/routed/experts.py:115-123
+//   decomposed expert sites in job space  pd/targets/qwen36_moe.py:2752-2837
+//   r += sum_jobs(down)                   pd/routed/experts.py:202-206
+// with the clean forward on the frozen expert weights pinning every masked layer's
+// expert indices, stochastic masks drawn per (kind, layer) over the selected-CI values
+// (pd/targets/qwen36_moe.py:3374-3401), MSE between masked and clean final residuals,
+// L_p imp-min over the selected upper CI, and the full backward (V/U of every site, the
+// CI preactivations, through routing weights, router softmax and the norm).
+//
+// All contractions are the grouped bf16 MFMA GEMMs of pd_gemm.hip; the elementwise
+// passes below are one pass each over job space or token space.
+#include <algorithm>
+#include <vector>
+
+#include "pd_common.hpp"
+
+namespace pd {
+
+static constexpr int MOE_KIND_GATE = 11, MOE_KIND_UP = 12, MOE_KIND_DOWN = 13;  // KIND_ORDER indices
+
+static inline unsigned grid_for(int64_t n, int per_block) {
+  int64_t b = cdiv(n, per_block);
+  return (unsigned)(b < 1 ? 1 : (b > 16384 ? 16384 : b));
+}
+
+// ---------------------------------------------------------------- token-space kernels
+// One block (256 threads) per token row of width d (d <= 2048): y = x * rsqrt(mean x^2
+// + eps) * (1 + w), fp32 math, bf16 out; rinv saved for the backward.
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd(const bf16_t* __restrict__ x, int64_t T, int d,
+                                                     const float* __restrict__ w, float eps, bf16_t* __restrict__ y,
+                                                     float* __restrict__ rinv) {
+  const int64_t t = blockIdx.x;
+  if (t >= T) return;
+  __shared__ float red[4];
+  const bf16_t* xr = x + t * d;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    float v = bf16_to_f32(xr[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)d + eps);
+  if (threadIdx.x == 0 && rinv) rinv[t] = r;
+  for (int i = threadIdx.x; i < d; i += 256) y[t * d + i] = f32_to_bf16(bf16_to_f32(xr[i]) * r * (1.f + w[i]));
+}
+
+// Masked-layer routing weights at pinned indices: probs = softmax(logits) (saved),
+// w[t,s] = probs[idx[t,s]] / sum_s probs[idx[t,s]]. One wave per token, E <= 64.
+__global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__ logits, int64_t T, int E, int k,
+                                                       const int32_t* __restrict__ idx, float* __restrict__ probs,
+                                                       float* __restrict__ w) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float x = lane < E ? logits[t * E + lane] : -INFINITY;
+  float mx = wave_max(x);
+  float ex = lane < E ? expf(x - mx) : 0.f;
+  float p = ex / wave_sum(ex);
+  if (lane < E) probs[t * E + lane] = p;
+  // every lane takes part in the shuffle (a source lane must be active)
+  int e = lane < k ? idx[t * k + lane] : 0;
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+  const float sel = __shfl(p, e, 64);
+  float s = wave_sum(lane < k ? sel : 0.f);
+  if (lane < k) w[t * k + lane] = sel / s;
+}
+
+// r_out[t,:] = bf16(r[t,:] + sum_s wt[t,s] * y[inv[t*k+s],:]) with fp32 accumulation;
+// wt NULL = the unweighted sum_jobs.
+__global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restrict__ r, const bf16_t* __restrict__ y,
+                                                          const int32_t* __restrict__ inv,
+                                                          const float* __restrict__ wt, int64_t T, int k, int d,
+                                                          bf16_t* __restrict__ r_out) {
+  const int64_t t = blockIdx.x;
+  if (t >= T) return;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) {
+      float v = bf16_to_f32(y[(int64_t)inv[t * k + s] * d + i]);
+      acc = wt ? fmaf(wt[t * k + s], v, acc) : acc + v;
+    }
+    // the routed output is rounded to bf16 before the residual add (sum_jobs casts back)
+    r_out[t * d + i] = f32_to_bf16(bf16_to_f32(r[t * d + i]) + bf16_to_f32(f32_to_bf16(acc)));
+  }
+}
+
+// MSE between the masked and clean final residuals: partial sums of e^2 and
+// dr = bf16(scale * e).
+__global__ __launch_bounds__(256) void k_moe_recon(const bf16_t* __restrict__ r, const bf16_t* __restrict__ rc,
+                                                   int64_t n, float scale, bf16_t* __restrict__ dr,
+                                                   float* __restrict__ partial) {
+  float acc = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float e = bf16_to_f32(r[i]) - bf16_to_f32(rc[i]);
+    acc = fmaf(e, e, acc);
+    dr[i] = f32_to_bf16(scale * e);
+  }
+  __shared__ float red[4];
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// ---------------------------------------------------------------- job-space kernels
+struct SiteMaskArgs {
+  const bf16_t* ci_pre;  // [T, k, c] token-major (slot m = the token's m-th expert)
+  const int32_t* sort_idx;
+  int64_t J;
+  int c;
+  uint32_t k0, k1;
+  int layout;
+  float p;
+};
+
+// Forward mask in job space: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at
+// the job's token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16);
+// acts = bf16(h * m); u stored as its 7-bit integer; partial sums of upper(ci)^p.
+__global__ __launch_bounds__(256) void k_site_mask_fwd(SiteMaskArgs a, const bf16_t* __restrict__ h,
+                                                       bf16_t* __restrict__ acts, uint8_t* __restrict__ ubits,
+                                                       float* __restrict__ imp_partial) {
+  const int64_t n = a.J * a.c;
+  float imp = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t j = i / a.c;
+    const int q = (int)(i - j * a.c);
+    const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
+    const float pre = bf16_to_f32(a.ci_pre[src]);
+    const float lo = lower_fwd(pre), up = upper_fwd(pre);
+    imp += a.p == 2.f ? up * up : (a.p == 1.f ? up : powf(up, a.p));
+    const uint32_t kb = (draw_bits(a.k0, a.k1, src, n, 8, a.layout) & 0xFFu) >> 1;
+    ubits[i] = (uint8_t)kb;
+    const float m = lo + (1.f - lo) * ((float)kb * (1.f / 128.f));
+    acts[i] = f32_to_bf16(bf16_to_f32(h[i]) * m);
+  }
+  __shared__ float red[4];
+  imp = wave_sum(imp);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = imp;
+  __syncthreads();
+  if (threadIdx.x == 0) imp_partial[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Backward mask in job space: d_h = bf16(d_acts * m) (in place over d_acts) and the CI
+// pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
+// upper_vjp(pre, imp_scale * d upper^p) written token-major.
+__global__ __launch_bounds__(256) void k_site_mask_bwd(SiteMaskArgs a, const bf16_t* __restrict__ h,
+                                                       const uint8_t* __restrict__ ubits, float imp_scale,
+                                                       bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_pre) {
+  const int64_t n = a.J * a.c;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t j = i / a.c;
+    const int q = (int)(i - j * a.c);
+    const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
+    const float pre = bf16_to_f32(a.ci_pre[src]);
+    const float lo = lower_fwd(pre), up = upper_fwd(pre);
+    const float u = (float)ubits[i] * (1.f / 128.f);
+    const float m = lo + (1.f - lo) * u;
+    const float da = bf16_to_f32(d_acts[i]);
+    const float dup = imp_scale * (a.p == 2.f ? 2.f * up : (a.p == 1.f ? 1.f : a.p * powf(up, a.p - 1.f)));
+    d_pre[src] = f32_to_bf16(lower_vjp(pre, da * bf16_to_f32(h[i]) * (1.f - u)) + upper_vjp(pre, dup));
+    d_acts[i] = f32_to_bf16(da * m);
+  }
+}
+
+__device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math); wt NULL = frozen arm
+// (no weight), in which case sort_idx is unused.
+__global__ __launch_bounds__(256) void k_swiglu_fwd(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
+                                                    const float* __restrict__ wt, const int32_t* __restrict__ sort_idx,
+                                                    int64_t J, int f, bf16_t* __restrict__ din) {
+  const int64_t n = J * f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t j = i / f;
+    const float gv = bf16_to_f32(g[i]);
+    float v = gv * sigm(gv) * bf16_to_f32(u[i]);
+    if (wt) v *= wt[sort_idx[j]];
+    din[i] = f32_to_bf16(v);
+  }
+}
+
+// SwiGLU-fold backward, one wave per job row: d_g = bf16(d*u*w*silu'(g)),
+// d_u = bf16(d*silu(g)*w), d_w[j] = sum_f d*silu(g)*u.
+__global__ __launch_bounds__(256) void k_swiglu_bwd(const bf16_t* __restrict__ d_din, const bf16_t* __restrict__ g,
+                                                    const bf16_t* __restrict__ u, const float* __restrict__ wt,
+                                                    const int32_t* __restrict__ sort_idx, int64_t J, int f,
+                                                    bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_u,
+                                                    float* __restrict__ d_wj) {
+  const int lane = threadIdx.x & 63;
+  const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (j >= J) return;
+  const float w = wt[sort_idx[j]];
+  float acc = 0.f;
+  for (int q = lane; q < f; q += 64) {
+    const int64_t i = j * f + q;
+    const float dv = bf16_to_f32(d_din[i]), gv = bf16_to_f32(g[i]), uv = bf16_to_f32(u[i]);
+    const float sg = sigm(gv);
+    const float s = gv * sg;
+    d_g[i] = f32_to_bf16(dv * uv * w * sg * (1.f + gv * (1.f - sg)));
+    d_u[i] = f32_to_bf16(dv * s * w);
+    acc = fmaf(dv * s, uv, acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) d_wj[j] = acc;
+}
+
+// Token backward, one block (256 threads) per token:
+//   d_w[s] = d_wj[inv[t*k+s]]; through w = p_sel / sum p_sel and the router softmax to
+//   d_logits[E] (wave 0, lanes = experts); d_h2 = sum_s (dxa + dxb)[inv[t*k+s]] +
+//   d_logits @ router; d_r_out = bf16(d_r + rms_norm_vjp(r, d_h2)).
+__global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_wj, const int32_t* __restrict__ inv,
+                                                   const int32_t* __restrict__ idx, const float* __restrict__ probs,
+                                                   const float* __restrict__ w, const bf16_t* __restrict__ router,
+                                                   const bf16_t* __restrict__ dxa, const bf16_t* __restrict__ dxb,
+                                                   const bf16_t* __restrict__ r, const float* __restrict__ rinv,
+                                                   const float* __restrict__ ln, const bf16_t* __restrict__ d_r,
+                                                   int64_t T, int E, int k, int d, float* __restrict__ scratch_h2,
+                                                   bf16_t* __restrict__ d_r_out) {
+  const int64_t t = blockIdx.x;
+  if (t >= T) return;
+  __shared__ float dlog[64];
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave == 0) {
+    // d_w and the renormalization pullback over the k slots
+    float dw = lane < k ? d_wj[inv[t * k + lane]] : 0.f;
+    float wv = lane < k ? w[t * k + lane] : 0.f;
+    float dot = wave_sum(dw * wv);
+    int e_of_slot = lane < k ? idx[t * k + lane] : -1;
+    if (lane < k) e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
+    const float pe = lane < E ? probs[t * E + lane] : 0.f;
+    const float psel = __shfl(pe, lane < k ? e_of_slot : 0, 64);  // all lanes shuffle
+    float S = wave_sum(lane < k ? psel : 0.f);
+    float dps = lane < k ? (dw - dot) / S : 0.f;
+    // scatter d_psel to experts: lane e collects the slot that selected it (distinct)
+    float dpe = 0.f;
+    for (int s = 0; s < k; ++s) {
+      int es = __shfl(e_of_slot, s, 64);
+      float v = __shfl(dps, s, 64);
+      if (lane == es) dpe += v;
+    }
+    float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
+    if (lane < E) dlog[lane] = pe * (dpe - sdot);
+  }
+  __syncthreads();
+  // d_h2 and the norm pullback
+  const bf16_t* xr = r + t * d;
+  float* h2g = scratch_h2 + t * d;
+  float part = 0.f;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) {
+      int64_t row = (int64_t)inv[t * k + s] * d + i;
+      acc += bf16_to_f32(dxa[row]) + bf16_to_f32(dxb[row]);
+    }
+    for (int e = 0; e < E; ++e) acc = fmaf(dlog[e], bf16_to_f32(router[(int64_t)e * d + i]), acc);
+    const float a = (1.f + ln[i]) * acc;
+    h2g[i] = a;
+    part = fmaf(a, bf16_to_f32(xr[i]), part);
+  }
+  part = wave_sum(part);
+  if (lane == 0) red[wave] = part;
+  __syncthreads();
+  const float ax = red[0] + red[1] + red[2] + red[3];
+  const float rv = rinv[t];
+  const float c3 = rv * rv * rv * ax / (float)d;
+  for (int i = threadIdx.x; i < d; i += 256) {
+    const float dx = rv * h2g[i] - bf16_to_f32(xr[i]) * c3;
+    d_r_out[t * d + i] = f32_to_bf16(bf16_to_f32(d_r[t * d + i]) + dx);
+  }
+}
+
+__global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, const float* __restrict__ imp_part,
+                             int64_t n_imp, double rec_scale, double imp_scale, float recon_coeff, float imp_coeff,
+                             float* __restrict__ losses) {
+  __shared__ double sr[16], si[16];
+  double r = 0.0, m = 0.0;
+  for (int i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
+  for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  r = wave_sum_d(r);
+  m = wave_sum_d(m);
+  if (threadIdx.x % 64 == 0) {
+    sr[threadIdx.x / 64] = r;
+    si[threadIdx.x / 64] = m;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double a = 0, b = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
+      a += sr[i];
+      b += si[i];
+    }
+    a *= rec_scale;
+    b *= imp_scale;
+    losses[0] = (float)(recon_coeff * a + imp_coeff * b);
+    losses[1] = (float)a;
+    losses[2] = (float)b;
+  }
+}
+
+// ---------------------------------------------------------------- workspace plan
+static constexpr int MASK_BLOCKS = 2048;  // fixed partial count per site mask pass
+static constexpr int REC_BLOCKS = 1024;
+
+struct MoEDims {
+  int64_t T, J;
+  int d, f, E, k, c, L;
+};
+
+struct Arena {
+  char* base;
+  size_t off;
+  bool dry;
+  template <typename X>
+  X* take(size_t n) {
+    size_t bytes = (n * sizeof(X) + 255) & ~(size_t)255;
+    X* p = dry ? nullptr : (X*)(base + off);
+    off += bytes;
+    return p;
+  }
+};
+
+struct LayerSave {
+  bf16_t *r, *h2, *xj, *gout, *uout, *din;
+  float *rinv, *probs, *w;
+  int32_t *idx, *sort_idx, *inv, *sizes, *offsets;
+  bf16_t* h[3];
+  bf16_t* acts[3];
+  uint8_t* ub[3];
+};
+
+struct MoEPlan {
+  std::vector<LayerSave> layers;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xjc, *gc, *uc, *dinc, *downc, *down, *dr_a, *dr_b;
+  float *logits, *probsc, *wc, *rec_part, *imp_part, *h2g;
+  int32_t *idxc_scratch, *sort_ws;
+  bf16_t *d_dout, *d_acts, *d_din, *d_g, *d_u, *dxa, *dxb, *d_h;
+  float* d_wj;
+  size_t total;
+};
+
+static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
+  Arena A{base, 0, dry};
+  MoEPlan P;
+  const int64_t T = D.T, J = D.J;
+  P.layers.resize(D.L);
+  for (int l = 0; l < D.L; ++l) {
+    LayerSave& S = P.layers[l];
+    S.r = A.take<bf16_t>(T * D.d);
+    S.h2 = A.take<bf16_t>(T * D.d);
+    S.rinv = A.take<float>(T);
+    S.probs = A.take<float>(T * D.E);
+    S.w = A.take<float>(T * D.k);
+    S.idx = A.take<int32_t>(T * D.k);
+    S.sort_idx = A.take<int32_t>(J);
+    S.inv = A.take<int32_t>(J);
+    S.sizes = A.take<int32_t>(D.E);
+    S.offsets = A.take<int32_t>(D.E + 1);
+    S.xj = A.take<bf16_t>(J * D.d);
+    S.gout = A.take<bf16_t>(J * D.f);
+    S.uout = A.take<bf16_t>(J * D.f);
+    S.din = A.take<bf16_t>(J * D.f);
+    for (int s = 0; s < 3; ++s) {
+      S.h[s] = A.take<bf16_t>(J * D.c);
+      S.acts[s] = A.take<bf16_t>(J * D.c);
+      S.ub[s] = A.take<uint8_t>(J * D.c);
+    }
+  }
+  P.rc_a = A.take<bf16_t>(T * D.d);
+  P.rc_b = A.take<bf16_t>(T * D.d);
+  P.r_final = A.take<bf16_t>(T * D.d);
+  P.h2c = A.take<bf16_t>(T * D.d);
+  P.xjc = A.take<bf16_t>(J * D.d);
+  P.gc = A.take<bf16_t>(J * D.f);
+  P.uc = A.take<bf16_t>(J * D.f);
+  P.dinc = A.take<bf16_t>(J * D.f);
+  P.downc = A.take<bf16_t>(J * D.d);
+  P.down = A.take<bf16_t>(J * D.d);
+  P.dr_a = A.take<bf16_t>(T * D.d);
+  P.dr_b = A.take<bf16_t>(T * D.d);
+  P.logits = A.take<float>(T * D.E);
+  P.probsc = A.take<float>(T * D.E);
+  P.wc = A.take<float>(T * D.k);
+  P.rec_part = A.take<float>(REC_BLOCKS);
+  P.imp_part = A.take<float>((size_t)MASK_BLOCKS * 3 * D.L);
+  P.h2g = A.take<float>(T * D.d);
+  P.idxc_scratch = A.take<int32_t>(T * D.k);
+  P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
+  P.d_dout = A.take<bf16_t>(J * D.d);
+  P.d_acts = A.take<bf16_t>(J * D.c);
+  P.d_din = A.take<bf16_t>(J * D.f);
+  P.d_g = A.take<bf16_t>(J * D.f);
+  P.d_u = A.take<bf16_t>(J * D.f);
+  P.dxa = A.take<bf16_t>(J * D.d);
+  P.dxb = A.take<bf16_t>(J * D.d);
+  P.d_h = A.take<bf16_t>(J * D.f > J * D.d ? J * D.f : J * D.d);
+  P.d_wj = A.take<float>(J);
+  P.total = A.off;
+  return P;
+}
+
+struct Recorder {
+  void** ev;
+  int32_t* cat;
+  int cap, n;
+  hipStream_t s;
+  void mark(int category) {
+    if (!ev || n >= cap) return;
+    hipEventRecord((hipEvent_t)ev[n], s);
+    if (cat) cat[n] = category;
+    ++n;
+  }
+};
+
+}  // namespace pd
+
+using namespace pd;
+
+extern "C" {
+
+size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L) {
+  MoEDims D{T, T * k, d, f, E, k, c, L};
+  return plan(D, nullptr, true).total;
+}
+
+// Phase categories recorded by pd_moe_stack_step_timed (one event before each launch
+// group and one at the end; cat[i] labels the interval [i, i+1)).
+enum {
+  MOE_CAT_CLEAN = 0,       // clean forward (norm, router, bucketing, frozen grouped GEMMs, combine)
+  MOE_CAT_NORM_ROUTE = 1,  // masked-pass norm, router GEMM, pinned weights, bucketing, gather
+  MOE_CAT_GEMM_FWD = 2,    // grouped GEMMs of the decomposed sites, forward
+  MOE_CAT_MASK_FWD = 3,    // job-space mask passes, forward
+  MOE_CAT_SWIGLU = 4,      // SwiGLU fold fwd/bwd
+  MOE_CAT_COMBINE = 5,     // sum_jobs + residual, loss, gathers
+  MOE_CAT_GEMM_DX = 6,     // grouped GEMMs d_input
+  MOE_CAT_GEMM_DW = 7,     // grouped GEMMs d_weight (ragged contraction)
+  MOE_CAT_MASK_BWD = 8,    // job-space mask passes, backward
+  MOE_CAT_TOKEN_BWD = 9,   // router/norm token backward
+  MOE_CAT_END = 10
+};
+
+static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                         const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                         const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p, float imp_coeff,
+                         float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
+                         float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
+                         void* stream, Recorder& rec) {
+  if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 64 || k <= 0 || k > E || c <= 0 || L <= 0)
+    return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 64)");
+  if (d % 8 || f % 8 || c % 8) return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d, f, c must be multiples of 8");
+  if (d > 4096 || T * k > 0x7FFFFFFF) return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: shape too large");
+  if (!x0 || !ln || !router || !Wg || !Wu || !Wd || !Vg || !Ug || !Vu || !Uu || !Vd || !Ud || !ci_pre || !losses ||
+      !dVg || !dUg || !dVu || !dUu || !dVd || !dUd || !d_ci_pre)
+    return fail(PD_EINVAL, "pd_moe_stack_step: null pointer");
+  const MoEDims D{T, T * k, d, f, E, k, c, L};
+  if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
+    return fail(PD_EWORKSPACE, "pd_moe_stack_step: workspace too small");
+  MoEPlan P = plan(D, (char*)workspace, false);
+  hipStream_t s = (hipStream_t)stream;
+  rec.s = s;
+  const int64_t J = D.J;
+  const size_t szW = (size_t)E * d * f, szVg = (size_t)E * d * c, szUg = (size_t)E * c * f, szVd = (size_t)E * f * c,
+               szUd = (size_t)E * c * d;
+  const size_t szCI = (size_t)T * k * c;
+  auto bf = [](const void* base, size_t off) { return (const bf16_t*)base + off; };
+  int rc;
+  // ---- site keys: src_base = split(draw_key)[0]; key(kind, layer) = fold_in(fold_in(src_base, kind), layer)
+  // partitionable split: subkey 0 = block(key, (0, 0)); original split of 2 keys:
+  // subkey 0 = (block(key, (0, 2)).x0, block(key, (1, 3)).x0).
+  uint32_t sb0 = 0, sb1 = 0;
+  if (layout == PD_LAYOUT_PARTITIONABLE) {
+    threefry2x32(draw_k0, draw_k1, sb0, sb1);
+  } else {
+    uint32_t a0 = 0, a1 = 2, b0 = 1, b1 = 3;
+    threefry2x32(draw_k0, draw_k1, a0, a1);
+    threefry2x32(draw_k0, draw_k1, b0, b1);
+    sb0 = a0;
+    sb1 = b0;
+  }
+  auto site_key = [&](int kind, int layer, uint32_t& o0, uint32_t& o1) {
+    uint32_t x0_ = 0, x1_ = (uint32_t)kind;
+    threefry2x32(sb0, sb1, x0_, x1_);
+    uint32_t y0 = 0, y1 = (uint32_t)layer;
+    threefry2x32(x0_, x1_, y0, y1);
+    o0 = y0;
+    o1 = y1;
+  };
+
+  // ================= clean forward (frozen weights): pins the expert indices
+  rec.mark(MOE_CAT_CLEAN);
+  hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
+  bf16_t* rcur = P.rc_a;
+  bf16_t* rnext = P.rc_b;
+  for (int l = 0; l < L; ++l) {
+    LayerSave& S = P.layers[l];
+    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)T), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
+                       P.h2c, (float*)nullptr);
+    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, P.h2c, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
+                      PD_DTYPE_F32, 1.f, 0.f, stream)))
+      return rc;
+    if ((rc = pd_router_topk(P.logits, T, E, k, P.probsc, S.idx, P.wc, stream))) return rc;
+    if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
+                             pd_routed_jobs_workspace_size(J, E), stream)))
+      return rc;
+    if ((rc = pd_gather_rows(P.h2c, PD_DTYPE_BF16, d, S.sort_idx, k, J, P.xjc, stream))) return rc;
+    if ((rc = pd_grouped_gemm(P.xjc, bf(Wg, l * szW), S.offsets, J, E, d, f, 0, P.gc, PD_DTYPE_BF16, stream)))
+      return rc;
+    if ((rc = pd_grouped_gemm(P.xjc, bf(Wu, l * szW), S.offsets, J, E, d, f, 0, P.uc, PD_DTYPE_BF16, stream)))
+      return rc;
+    hipLaunchKernelGGL(k_swiglu_fwd, dim3(grid_for(J * f, 1024)), dim3(256), 0, s, P.gc, P.uc, (const float*)nullptr,
+                       S.sort_idx, J, f, P.dinc);
+    if ((rc = pd_grouped_gemm(P.dinc, bf(Wd, l * szW), S.offsets, J, E, f, d, 0, P.downc, PD_DTYPE_BF16, stream)))
+      return rc;
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
+                       rnext);
+    std::swap(rcur, rnext);
+    if (top_idx_out) hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+  }
+  bf16_t* rc_final = rcur;
+  if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
+
+  // ================= masked forward
+  const bf16_t* r_in = (const bf16_t*)x0;
+  for (int l = 0; l < L; ++l) {
+    LayerSave& S = P.layers[l];
+    rec.mark(MOE_CAT_NORM_ROUTE);
+    hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
+    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)T), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f, S.h2,
+                       S.rinv);
+    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
+                      PD_DTYPE_F32, 1.f, 0.f, stream)))
+      return rc;
+    hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
+                       S.probs, S.w);
+    if ((rc = pd_gather_rows(S.h2, PD_DTYPE_BF16, d, S.sort_idx, k, J, S.xj, stream))) return rc;
+    const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
+    bf16_t* outs[2] = {S.gout, S.uout};
+    const void* Vs[2] = {Vg, Vu};
+    const void* Us[2] = {Ug, Uu};
+    for (int si = 0; si < 3; ++si) {
+      if (si == 2) {
+        rec.mark(MOE_CAT_SWIGLU);
+        hipLaunchKernelGGL(k_swiglu_fwd, dim3(grid_for(J * f, 1024)), dim3(256), 0, s, S.gout, S.uout, S.w,
+                           S.sort_idx, J, f, S.din);
+      }
+      rec.mark(MOE_CAT_GEMM_FWD);
+      if (si < 2) {
+        if ((rc = pd_grouped_gemm(S.xj, bf(Vs[si], l * szVg), S.offsets, J, E, d, c, 0, S.h[si], PD_DTYPE_BF16,
+                                  stream)))
+          return rc;
+      } else {
+        if ((rc = pd_grouped_gemm(S.din, bf(Vd, l * szVd), S.offsets, J, E, f, c, 0, S.h[2], PD_DTYPE_BF16, stream)))
+          return rc;
+      }
+      rec.mark(MOE_CAT_MASK_FWD);
+      SiteMaskArgs ma;
+      ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
+      ma.sort_idx = S.sort_idx;
+      ma.J = J;
+      ma.c = c;
+      site_key(kinds[si], l, ma.k0, ma.k1);
+      ma.layout = layout;
+      ma.p = p;
+      hipLaunchKernelGGL(k_site_mask_fwd, dim3(MASK_BLOCKS), dim3(256), 0, s, ma, S.h[si], S.acts[si], S.ub[si],
+                         P.imp_part + ((size_t)l * 3 + si) * MASK_BLOCKS);
+      rec.mark(MOE_CAT_GEMM_FWD);
+      if (si < 2) {
+        if ((rc = pd_grouped_gemm(S.acts[si], bf(Us[si], l * szUg), S.offsets, J, E, c, f, 0, outs[si],
+                                  PD_DTYPE_BF16, stream)))
+          return rc;
+      } else {
+        if ((rc = pd_grouped_gemm(S.acts[2], bf(Ud, l * szUd), S.offsets, J, E, c, d, 0, P.down, PD_DTYPE_BF16,
+                                  stream)))
+          return rc;
+      }
+    }
+    rec.mark(MOE_CAT_COMBINE);
+    bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, S.r, P.down, S.inv,
+                       (const float*)nullptr, T, k, d, r_out);
+    r_in = r_out;
+    if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
+  }
+  // ================= loss
+  const int64_t nres = T * d;
+  hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
+                     recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
+  hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.imp_part,
+                     (int64_t)MASK_BLOCKS * 3 * L, 1.0 / (double)nres, 1.0 / (double)T, recon_coeff, imp_coeff,
+                     losses);
+  // ================= backward
+  bf16_t* dr = P.dr_a;
+  bf16_t* dr_next = P.dr_b;
+  const float imp_scale = imp_coeff / (float)T;
+  for (int l = L - 1; l >= 0; --l) {
+    LayerSave& S = P.layers[l];
+    const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
+    rec.mark(MOE_CAT_COMBINE);
+    if ((rc = pd_gather_rows(dr, PD_DTYPE_BF16, d, S.sort_idx, k, J, P.d_dout, stream))) return rc;
+    // ---- down site
+    rec.mark(MOE_CAT_GEMM_DX);
+    if ((rc = pd_grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts, PD_DTYPE_BF16, stream)))
+      return rc;
+    rec.mark(MOE_CAT_GEMM_DW);
+    if ((rc = pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd, PD_DTYPE_F32, stream)))
+      return rc;
+    rec.mark(MOE_CAT_MASK_BWD);
+    SiteMaskArgs ma;
+    ma.sort_idx = S.sort_idx;
+    ma.J = J;
+    ma.c = c;
+    ma.layout = layout;
+    ma.p = p;
+    ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
+    site_key(kinds[2], l, ma.k0, ma.k1);
+    hipLaunchKernelGGL(k_site_mask_bwd, dim3(grid_for(J * c, 1024)), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale,
+                       P.d_acts, (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    rec.mark(MOE_CAT_GEMM_DW);
+    if ((rc = pd_grouped_gemm_dw(S.din, P.d_acts, S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32, stream)))
+      return rc;
+    rec.mark(MOE_CAT_GEMM_DX);
+    if ((rc = pd_grouped_gemm(P.d_acts, bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream)))
+      return rc;
+    rec.mark(MOE_CAT_SWIGLU);
+    hipLaunchKernelGGL(k_swiglu_bwd, dim3((unsigned)cdiv(J, 4)), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w,
+                       S.sort_idx, J, f, P.d_g, P.d_u, P.d_wj);
+    // ---- gate and up sites
+    const void* Vs[2] = {Vg, Vu};
+    const void* Us[2] = {Ug, Uu};
+    float* dVs[2] = {dVg, dVu};
+    float* dUs[2] = {dUg, dUu};
+    bf16_t* douts[2] = {P.d_g, P.d_u};
+    bf16_t* dxs[2] = {P.dxa, P.dxb};
+    for (int si = 0; si < 2; ++si) {
+      rec.mark(MOE_CAT_GEMM_DX);
+      if ((rc = pd_grouped_gemm(douts[si], bf(Us[si], l * szUg), S.offsets, J, E, f, c, 1, P.d_acts, PD_DTYPE_BF16,
+                                stream)))
+        return rc;
+      rec.mark(MOE_CAT_GEMM_DW);
+      if ((rc = pd_grouped_gemm_dw(S.acts[si], douts[si], S.offsets, J, E, c, f, dUs[si] + l * szUg, PD_DTYPE_F32,
+                                   stream)))
+        return rc;
+      rec.mark(MOE_CAT_MASK_BWD);
+      ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
+      site_key(kinds[si], l, ma.k0, ma.k1);
+      hipLaunchKernelGGL(k_site_mask_bwd, dim3(grid_for(J * c, 1024)), dim3(256), 0, s, ma, S.h[si], S.ub[si],
+                         imp_scale, P.d_acts, (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
+      rec.mark(MOE_CAT_GEMM_DW);
+      if ((rc = pd_grouped_gemm_dw(S.xj, P.d_acts, S.offsets, J, E, d, c, dVs[si] + l * szVg, PD_DTYPE_F32, stream)))
+        return rc;
+      rec.mark(MOE_CAT_GEMM_DX);
+      if ((rc = pd_grouped_gemm(P.d_acts, bf(Vs[si], l * szVg), S.offsets, J, E, c, d, 1, dxs[si], PD_DTYPE_BF16,
+                                stream)))
+        return rc;
+    }
+    // ---- routing weights, router, gather VJP and the norm
+    rec.mark(MOE_CAT_TOKEN_BWD);
+    hipLaunchKernelGGL(k_token_bwd, dim3((unsigned)T), dim3(256), 0, s, P.d_wj, S.inv, S.idx, S.probs, S.w,
+                       bf(router, (size_t)l * E * d), P.dxa, P.dxb, S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d,
+                       P.h2g, dr_next);
+    std::swap(dr, dr_next);
+    if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
+  }
+  rec.mark(MOE_CAT_END);
+  return PD_OK;
+}
+
+int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                      const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                      const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
+                      uint32_t draw_k0, uint32_t draw_k1, int layout, float p, float imp_coeff, float recon_coeff,
+                      float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd,
+                      void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream) {
+  Recorder rec{nullptr, nullptr, 0, 0, nullptr};
+  return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
+                       draw_k1, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                       top_idx_out, workspace, workspace_bytes, stream, rec);
+}
+
+int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                            const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                            const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p,
+                            float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
+                            float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
+                            size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
+                            int* n_recorded) {
+  if (!events || !categories || capacity <= 0 || !n_recorded)
+    return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
+  Recorder rec{events, categories, capacity, 0, nullptr};
+  int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
+                         draw_k1, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                         top_idx_out, workspace, workspace_bytes, stream, rec);
+  *n_recorded = rec.n;
+  if (rc == PD_OK && rec.n >= capacity) return fail(PD_EINVAL, "pd_moe_stack_step_timed: event capacity too small");
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+"""The decomposed MoE stack step (the routed-expert hot path end to end) on the GPU.
+
+One call = the clean forward on the frozen experts (pinning each layer's expert
+indices), the masked forward with every routed expert matrix decomposed, MSE recon of
+the final residual + L_p imp-min over the selected CI, and the full backward to the
+V/U factors of every site and to the CI preactivations. See `pd_moe_stack_step` in
+include/pd_mi355x.h for the reference citations and layouts.
+
+All buffers are allocated once at construction; `step()` only enqueues kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from param_decomp_amd import _lib as L
+from param_decomp_amd.prng import Key
+
+SITE_NAMES = ("gate", "up", "down")
+CATEGORIES = ("clean_fwd", "norm_route", "gemm_fwd", "mask_fwd", "swiglu", "combine_loss", "gemm_dx", "gemm_dw",
+              "mask_bwd", "token_bwd")
+
+
+@dataclass
+class MoEWeights:
+    """bf16 tensors in the layouts of the C ABI (ln is fp32)."""
+
+    ln: torch.Tensor  # [L, d] fp32
+    router: torch.Tensor  # [L, E, d]
+    Wg: torch.Tensor  # [L, E, d, f]
+    Wu: torch.Tensor  # [L, E, d, f]
+    Wd: torch.Tensor  # [L, E, f, d]
+    Vg: torch.Tensor  # [L, E, d, c]
+    Ug: torch.Tensor  # [L, E, c, f]
+    Vu: torch.Tensor  # [L, E, d, c]
+    Uu: torch.Tensor  # [L, E, c, f]
+    Vd: torch.Tensor  # [L, E, f, c]
+    Ud: torch.Tensor  # [L, E, c, d]
+
+
+class MoEStackStep:
+    def __init__(self, T: int, d: int, f: int, E: int, k: int, c: int, n_layers: int, *, device="cuda",
+                 p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
+                 layout: int = L.LAYOUT_PARTITIONABLE):
+        self.dims = (T, d, f, E, k, c, n_layers)
+        self.p, self.imp_coeff, self.recon_coeff, self.layout = p, imp_coeff, recon_coeff, layout
+        dev = torch.device(device)
+        f32 = dict(dtype=torch.float32, device=dev)
+        Ln = n_layers
+        self.losses = torch.empty(3, **f32)
+        self.dV = {"gate": torch.empty(Ln, E, d, c, **f32), "up": torch.empty(Ln, E, d, c, **f32),
+                   "down": torch.empty(Ln, E, f, c, **f32)}
+        self.dU = {"gate": torch.empty(Ln, E, c, f, **f32), "up": torch.empty(Ln, E, c, f, **f32),
+                   "down": torch.empty(Ln, E, c, d, **f32)}
+        self.d_ci_pre = torch.empty(Ln, 3, T, k, c, dtype=torch.bfloat16, device=dev)
+        self.top_idx = torch.empty(Ln, T, k, dtype=torch.int32, device=dev)
+        self.workspace = L.workspace(L.load().pd_moe_stack_workspace_size(T, d, f, E, k, c, Ln), dev)
+
+    def _args(self, x0, w: MoEWeights, ci_pre, draw_key: Key):
+        T, d, f, E, k, c, Ln = self.dims
+        return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
+                L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
+                draw_key[0], draw_key[1], self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
+                L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
+                L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
+                L.ptr(self.workspace), self.workspace.numel(), L.stream()]
+
+    def step(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, draw_key: Key):
+        L.call("pd_moe_stack_step", *self._args(x0, w, ci_pre, draw_key))
+        return self
+
+    def step_timed(self, x0, w, ci_pre, draw_key, events: ctypes.Array, categories: torch.Tensor) -> int:
+        """Records phase events; returns the number recorded (categories is an int32 CPU
+        tensor of the events' capacity)."""
+        n = ctypes.c_int(0)
+        L.call("pd_moe_stack_step_timed", *self._args(x0, w, ci_pre, draw_key), events,
+               ctypes.c_void_p(categories.data_ptr()), len(events), ctypes.byref(n))
+        return n.value

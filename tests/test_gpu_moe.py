@@ -1,0 +1,103 @@
+"""GPU parity of the fused MoE stack step against the MoE oracle (same bf16 storage
+points): pinned routing bit-exact, losses and every gradient within rtol 2e-2."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as mo
+from oracle import pd_oracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, want, rtol, floor, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    bad = np.abs(got - want) > rtol * np.abs(want) + floor * scale
+    assert not bad.any(), f"{what}: {bad.sum()}/{bad.size} off, worst {np.abs(got - want).max():.3e} scale {scale:.3e}"
+
+
+def _make(cfg, seed, device):
+    rng = np.random.default_rng(seed)
+    params, x0, ci = mo.init_moe(cfg, rng)
+    rb = po.round_bf16
+    params = [{k: (v.astype(np.float32).astype(np.float64) if k == "ln" else rb(v)) for k, v in P.items()}
+              for P in params]
+    x0 = rb(x0)
+    ci = [{s: rb(v) for s, v in layer.items()} for layer in ci]
+    from param_decomp_amd.moe_step import MoEWeights
+
+    def stack(name, dt=torch.bfloat16):
+        return torch.tensor(np.stack([P[name] for P in params]).astype(np.float32), device=device).to(dt)
+
+    w = MoEWeights(ln=stack("ln", torch.float32), router=stack("router"), Wg=stack("Wg"), Wu=stack("Wu"),
+                   Wd=stack("Wd"), Vg=stack("Vg"), Ug=stack("Ug"), Vu=stack("Vu"), Uu=stack("Uu"), Vd=stack("Vd"),
+                   Ud=stack("Ud"))
+    ci_t = torch.tensor(np.stack([np.stack([layer[s] for s in mo.SITES]) for layer in ci]).astype(np.float32),
+                        device=device).to(torch.bfloat16)
+    x0_t = torch.tensor(x0.astype(np.float32), device=device).to(torch.bfloat16)
+    return params, x0, ci, w, ci_t, x0_t
+
+
+@pytest.mark.parametrize("cfg", [mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2),
+                                 mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3)])
+def test_moe_stack_step_matches_oracle(device, cfg):
+    from param_decomp_amd.moe_step import MoEStackStep
+
+    params, x0, ci, w, ci_t, x0_t = _make(cfg, 0, device)
+    key = (0, 17)
+    step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, p=2.0, imp_coeff=0.5,
+                        recon_coeff=1.5)
+    step.step(x0_t, w, ci_t, key)
+    torch.cuda.synchronize()
+    ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True)
+    for l in range(cfg.L):
+        np.testing.assert_array_equal(step.top_idx[l].cpu().numpy(), ref["top_idx"][l])
+    losses = step.losses.cpu().numpy()
+    np.testing.assert_allclose(losses, [ref["loss"], ref["recon"], ref["imp"]], rtol=2e-2)
+    for l in range(cfg.L):
+        for s, vn, un in (("gate", "Vg", "Ug"), ("up", "Vu", "Uu"), ("down", "Vd", "Ud")):
+            _close(step.dV[s][l].cpu().numpy(), ref["grads"][l][vn], 2e-2, 1e-2, f"{vn}[{l}]")
+            _close(step.dU[s][l].cpu().numpy(), ref["grads"][l][un], 2e-2, 1e-2, f"{un}[{l}]")
+        got = step.d_ci_pre[l].float().cpu().numpy()
+        for si, s in enumerate(mo.SITES):
+            _close(got[si], ref["d_ci_pre"][l][s], 2e-2, 1e-2, f"d_ci_pre[{l}][{s}]")
+
+
+def test_moe_stack_step_full_size_properties(device):
+    """The Qwen3.5-MoE-shaped stack (T=8192, width 512, 42 experts top-8, SwiGLU
+    512->256->512, c=512 per expert, 4 layers): finite losses, deterministic run to
+    run, and every expert's bucket size equals its routed job count (the per-layer
+    routing is a permutation: all T*k jobs land)."""
+    from param_decomp_amd.moe_step import MoEStackStep, MoEWeights
+
+    T, d, f, E, k, c, Ln = 8192, 512, 256, 42, 8, 512, 4
+    g = torch.Generator(device=device).manual_seed(0)
+
+    def rn(*shape, scale):
+        return (torch.randn(*shape, device=device, generator=g) * scale).to(torch.bfloat16)
+
+    w = MoEWeights(ln=torch.zeros(Ln, d, device=device), router=rn(Ln, E, d, scale=d**-0.5),
+                   Wg=rn(Ln, E, d, f, scale=d**-0.5), Wu=rn(Ln, E, d, f, scale=d**-0.5),
+                   Wd=rn(Ln, E, f, d, scale=f**-0.5), Vg=rn(Ln, E, d, c, scale=d**-0.5),
+                   Ug=rn(Ln, E, c, f, scale=c**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
+                   Uu=rn(Ln, E, c, f, scale=c**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
+                   Ud=rn(Ln, E, c, d, scale=c**-0.5))
+    x0 = rn(T, d, scale=1.0)
+    ci = (torch.rand(Ln, 3, T, k, c, device=device, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
+    step = MoEStackStep(T, d, f, E, k, c, Ln, device=device)
+    step.step(x0, w, ci, (0, 1))
+    l1 = step.losses.clone()
+    dv1 = step.dV["down"].clone()
+    dci1 = step.d_ci_pre.clone()
+    step.step(x0, w, ci, (0, 1))
+    assert torch.isfinite(l1).all() and float(l1[1]) > 0 and float(l1[2]) > 0
+    assert torch.equal(step.losses, l1) and torch.equal(step.dV["down"], dv1) and torch.equal(step.d_ci_pre, dci1)
+    for l in range(Ln):
+        counts = torch.bincount(step.top_idx[l].reshape(-1).long(), minlength=E)
+        assert int(counts.sum()) == T * k
+        # each token's k experts are distinct
+        srt, _ = torch.sort(step.top_idx[l], dim=-1)
+        assert bool((srt[:, 1:] != srt[:, :-1]).all())
