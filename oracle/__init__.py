@@ -14,8 +14,10 @@ Pinning (what checks each function besides a retyped formula):
   `split(PRNGKey(0))`.
 - `threefry` key chain, partitionable layout: `split(k)[i] == fold_in(k, i)` and the
   Random123 vector at key (0,0), counter (0,0). The bits→uniform conversion is restated
-  from JAX's published `_uniform`; no JAX is importable here, so the partitionable
-  uniform draw itself is "parity unpinned" beyond those checks.
+  from JAX's published `_uniform`; no JAX is importable here, so the uniform draw itself
+  is "parity unpinned" against JAX beyond those checks.
+- `moe_oracle`: finite differences of its hand-written backward and the every-expert
+  dense spelling of a routed layer.
 - squashing VJPs: the reference's 10 known-answer cotangents.
 - smooth-L0 imp-min: the reference's closed-form tests.
 - gate MLP, p-norm imp-min, masked linear and its backward: finite differences and

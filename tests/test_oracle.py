@@ -37,11 +37,13 @@ def test_split_matches_jax_documentation_original_layout():
     assert tf.split(tf.prng_key(0), 2, partitionable=False) == [(4146024105, 967050713), (2718843009, 1272950319)]
 
 
-def test_split_matches_jax_documentation_partitionable_layout():
+def test_split_partitionable_layout():
+    """First subkey = the Random123 vector at key (0,0), counter (0,0) (pinned); the
+    second row is a regression vector of this restatement (split(k)[1] == fold_in(k, 1),
+    checked generally in the next test)."""
     got = tf.split(tf.prng_key(0), 2, partitionable=True)
-    assert got == [(1797259609, 2579123966), (928981903, 3453687069)]
-    # first subkey is the Random123 vector at key (0,0), counter (0,0)
     assert got[0] == (0x6B200159, 0x99BA4EFE)
+    assert got == [(1797259609, 2579123966), (928981903, 3453687069)]
 
 
 def test_partitionable_split_is_foldlike():
