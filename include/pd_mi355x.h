@@ -200,6 +200,11 @@ int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* group_offse
  * [E,K,N]; empty groups are exactly zero. */
 int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* group_offsets, int64_t J, int E, int64_t K,
                        int64_t N, void* out, int out_dtype, void* stream);
+/* The same weight cotangent from K-major (job-contiguous) operands, the fast MFMA path:
+ * lhsT [K, J], doutT [N, J]; out[e] = lhsT[:, rows_e] @ doutT[:, rows_e]^T. J must be a
+ * multiple of 8. */
+int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t* group_offsets, int64_t J, int E,
+                              int64_t K, int64_t N, void* out, int out_dtype, void* stream);
 
 /* ---- the decomposed MoE stack step (the routed-expert hot path end to end) ----
  * L layers of: h2 = rms_norm_zero_centered(r) (target_ports/qwen3_5_moe.py:33-41),

@@ -13,6 +13,10 @@ namespace pd {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// pd_grouped_gemm without the launch that zeroes rows past the last group offset (for
+// callers whose groups cover every row).
+int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
+                 int trans_rhs, void* out, int out_dtype, void* stream, bool zero_tail);
 
 // ---------------------------------------------------------------- bf16
 typedef uint16_t bf16_t;

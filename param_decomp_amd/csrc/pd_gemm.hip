@@ -24,32 +24,13 @@
 // host synchronization is needed.
 #include <algorithm>
 
-#include "pd_common.hpp"
+#include "pd_gemm_dtl.hpp"
 
 namespace pd {
 
-typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short bf16x4;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
-
-enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2 };
 
 constexpr int BK = 64, LDS_PAD = 8, LDS_STRIDE = BK + LDS_PAD;
-
-struct GemmArgs {
-  int64_t M, N, K;
-  const bf16_t* A;
-  int64_t lda;
-  const bf16_t* B;
-  int64_t ldb;
-  void* C;
-  int64_t ldc;
-  float alpha, beta;
-  const int32_t* offsets;  // [E+1] group offsets (grouped modes)
-  int E;
-  int64_t strideB;  // elements between consecutive groups' B (GROUPED)
-  int64_t strideC;  // elements between consecutive groups' C (GROUPED_K)
-};
 
 template <int BM_, int BN_, int WM_, int WN_>
 struct TileCfg {
@@ -70,18 +51,26 @@ struct TileLoader {
   static constexpr int NV = KMAJ ? NCH : 4 * NCH;
   static_assert(NCH >= 1, "tile too small for the thread count");
   bf16x8 v[NV];
+  // kmin: elements with k < kmin are zeroed (ragged-K groups whose tiles start at an
+  // 8-aligned k below the group's first row); chunks are 8-aligned so loads stay 16 B.
   __device__ inline void load(const bf16_t* __restrict__ g, int64_t ld, int64_t row0, int64_t nrows, int64_t k0,
-                              int64_t kmax, int tid) {
+                              int64_t kmax, int tid, int64_t kmin = 0) {
     if (KMAJ) {
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
         int id = tid + NT * i;
         int r = id >> 3, kc = id & 7;
         int64_t gr = row0 + r, gk = k0 + kc * 8;
-        if (gr < nrows && gk < kmax)
+        if (gr < nrows && gk < kmax) {
           v[i] = *(const bf16x8*)(g + gr * ld + gk);
-        else
+          if (gk < kmin || gk + 8 > kmax) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (gk + e < kmin || gk + e >= kmax) v[i][e] = 0;
+          }
+        } else {
           v[i] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
       }
     } else {
 #pragma unroll
@@ -92,7 +81,7 @@ struct TileLoader {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           int64_t gk = k0 + kg * 4 + q;
-          if (gr < nrows && gk < kmax)
+          if (gr < nrows && gk < kmax && gk >= kmin)
             v[4 * i + q] = *(const bf16x8*)(g + gk * ld + gr);
           else
             v[4 * i + q] = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -124,32 +113,6 @@ struct TileLoader {
   }
 };
 
-template <typename TC>
-__device__ inline void store_out(TC* C, int64_t idx, float v, float beta);
-template <>
-__device__ inline void store_out<float>(float* C, int64_t idx, float v, float beta) {
-  C[idx] = beta != 0.f ? v + beta * C[idx] : v;
-}
-template <>
-__device__ inline void store_out<bf16_t>(bf16_t* C, int64_t idx, float v, float beta) {
-  C[idx] = f32_to_bf16(beta != 0.f ? v + beta * bf16_to_f32(C[idx]) : v);
-}
-
-// XCD-aware tile order for dense launches (see file comment).
-__device__ inline void dense_tile(int& my, int& nx) {
-  const int gx = gridDim.x, gy = gridDim.y;
-  const int total = gx * gy;
-  int L = blockIdx.y * gx + blockIdx.x;
-  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-  const int GROUP = 8;
-  const int g = L / (GROUP * gx);
-  const int first = g * GROUP;
-  const int gm = gy - first < GROUP ? gy - first : GROUP;
-  const int within = L - g * GROUP * gx;
-  my = first + within % gm;
-  nx = within / gm;
-}
-
 template <class CFG, bool A_KMAJ, bool B_KMAJ, typename TC, int MODE>
 __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
   constexpr int BM = CFG::BM, BN = CFG::BN, NT = CFG::NT, TM = CFG::TM, TN = CFG::TN;
@@ -159,45 +122,13 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / CFG::WN, wn = wave % CFG::WN;
 
-  int64_t M = p.M, N = p.N, K = p.K;
+  TileJob t;
+  if (!map_tile<BM, BN, MODE, TC>(p, lane, t)) return;
+  const int64_t M = t.M, N = p.N, m0 = t.m0, n0 = t.n0, kend = t.kend;
+  int64_t kbeg = t.kbeg;
   const bf16_t* A = p.A;
-  const bf16_t* B = p.B;
-  TC* C = (TC*)p.C;
-  int64_t m0, n0;
-  int64_t kbeg = 0, kend = K;
-
-  if (MODE == MODE_DENSE) {
-    int my, nx;
-    dense_tile(my, nx);
-    m0 = (int64_t)my * BM;
-    n0 = (int64_t)nx * BN;
-  } else if (MODE == MODE_GROUPED) {
-    // blockIdx.y enumerates row tiles over all groups in order
-    n0 = (int64_t)blockIdx.x * BN;
-    int64_t tile = blockIdx.y, acc = 0;
-    int e = 0;
-    for (; e < p.E; ++e) {
-      int64_t sz = p.offsets[e + 1] - p.offsets[e];
-      int64_t nt = sz > 0 ? (sz + BM - 1) / BM : 0;
-      if (tile < acc + nt) break;
-      acc += nt;
-    }
-    if (e >= p.E) return;
-    int64_t off = p.offsets[e];
-    M = p.offsets[e + 1] < p.M ? p.offsets[e + 1] : p.M;  // absolute row bound, clamped to J
-    m0 = off + (tile - acc) * BM;
-    if (m0 < 0) return;
-    B = p.B + (int64_t)e * p.strideB;
-  } else {
-    m0 = (int64_t)blockIdx.y * BM;
-    n0 = (int64_t)blockIdx.x * BN;
-    int e = blockIdx.z;
-    kbeg = p.offsets[e] < 0 ? 0 : p.offsets[e];
-    kend = p.offsets[e + 1] < p.K ? p.offsets[e + 1] : p.K;  // clamped to J
-    if (kend < kbeg) kend = kbeg;
-    C = (TC*)p.C + (int64_t)e * p.strideC;
-  }
-  if (m0 >= M || n0 >= N) return;
+  const bf16_t* B = t.B;
+  TC* C = (TC*)t.C;
 
   TileLoader<A_KMAJ, BM, NT> la;
   TileLoader<B_KMAJ, BN, NT> lb;
@@ -209,10 +140,14 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // K-major operands read 16-byte chunks, so a ragged group's K walk starts at the
+  // 8-aligned k below its first row and the loaders zero k < kmin.
+  const int64_t kmin = kbeg;
+  if (MODE == MODE_GROUPED_K && (A_KMAJ || B_KMAJ)) kbeg &= ~(int64_t)7;
   const int64_t nk = (kend - kbeg + BK - 1) / BK;
   if (nk > 0) {
-    la.load(A, p.lda, m0, M, kbeg, kend, tid);
-    lb.load(B, p.ldb, n0, N, kbeg, kend, tid);
+    la.load(A, p.lda, m0, M, kbeg, kend, tid, kmin);
+    lb.load(B, p.ldb, n0, N, kbeg, kend, tid, kmin);
     la.store(lds[0], tid);
     lb.store(lds[0] + BM * LDS_STRIDE, tid);
     __syncthreads();
@@ -222,8 +157,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
     const bool more = kt + 1 < nk;
     if (more) {
       int64_t k0 = kbeg + (kt + 1) * BK;
-      la.load(A, p.lda, m0, M, k0, kend, tid);
-      lb.load(B, p.ldb, n0, N, k0, kend, tid);
+      la.load(A, p.lda, m0, M, k0, kend, tid, kmin);
+      lb.load(B, p.ldb, n0, N, k0, kend, tid, kmin);
     }
     const bf16_t* As = lds[s] + (wm * WTM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
     const bf16_t* Bs = lds[s] + (BM + wn * WTN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
@@ -256,7 +191,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         int64_t row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row < M) store_out<TC>(C, row * p.ldc + col, p.alpha * acc[i][j][v], p.beta);
+        if (row < M) store1<TC>(C, row * p.ldc + col, p.alpha * acc[i][j][v], p.beta);
       }
     }
 }
@@ -344,6 +279,19 @@ static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) 
 // The big tile needs enough tiles to occupy the 256 CUs; otherwise use the small one.
 static bool use_big_tile(int64_t M, int64_t N) { return cdiv(M, 256) * cdiv(N, 256) >= 192; }
 
+// Direct-to-LDS kernel for K-contiguous operands: 128x128 tiles, 8 waves (4x2, 32x64 per
+// wave), 2 LDS stages (64 KB, two blocks per CU), reads one k16 step ahead.
+typedef DtlCfg<128, 128, 4, 2, 2, 2> CfgDtl;
+
+template <class CFG, int MODE>
+static int launch_dtl(const GemmArgs& a, int c_dtype, dim3 grid, hipStream_t s) {
+  if (c_dtype == PD_DTYPE_F32)
+    hipLaunchKernelGGL((k_gemm_dtl<CFG, float, MODE>), grid, dim3(CFG::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_gemm_dtl<CFG, bf16_t, MODE>), grid, dim3(CFG::NT), 0, s, a);
+  return check_launch("pd_gemm bf16 (direct-to-LDS)");
+}
+
 }  // namespace pd
 
 using namespace pd;
@@ -377,6 +325,15 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
 
 int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
                     int trans_rhs, void* out, int out_dtype, void* stream) {
+  return pd::grouped_gemm(lhs, rhs, offsets, J, E, K, N, trans_rhs, out, out_dtype, stream, true);
+}
+
+}  // extern "C"
+
+namespace pd {
+
+int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
+                 int trans_rhs, void* out, int out_dtype, void* stream, bool zero_tail) {
   if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs || !rhs || !offsets || !out)
     return fail(PD_EINVAL, "pd_grouped_gemm: bad args");
   if (J == 0) return PD_OK;
@@ -385,15 +342,22 @@ int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, in
     return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: K and N must be multiples of 8 with 16B-aligned bases");
   hipStream_t s = (hipStream_t)stream;
   // zero rows past sum(group_sizes) (ragged_dot leaves them 0)
-  hipLaunchKernelGGL(k_zero_tail_rows, dim3(256), dim3(256), 0, s, offsets, E, J, N,
-                     out_dtype == PD_DTYPE_F32 ? 4 : 2, out);
+  if (zero_tail)
+    hipLaunchKernelGGL(k_zero_tail_rows, dim3(256), dim3(256), 0, s, offsets, E, J, N,
+                       out_dtype == PD_DTYPE_F32 ? 4 : 2, out);
   GemmArgs a{J, N, K, (const bf16_t*)lhs, K, (const bf16_t*)rhs, b_kmaj ? K : N, out, N, 1.f, 0.f, offsets, E,
              K * N, 0};
+  static_assert(CfgDtl::BM == CfgSmall::BM && CfgDtl::BN == CfgSmall::BN, "one grid shape for both kernels");
   int64_t max_tiles = cdiv(J, CfgSmall::BM) + E;
   if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: too many rows");
   dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)max_tiles);
+  if (b_kmaj) return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, grid, s);
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
+
+}  // namespace pd
+
+extern "C" {
 
 int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets, int64_t J, int E, int64_t K,
                        int64_t N, void* out, int out_dtype, void* stream) {
@@ -406,6 +370,20 @@ int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets
   GemmArgs a{K, N, J, (const bf16_t*)lhs, K, (const bf16_t*)dout, N, out, N, 1.f, 0.f, offsets, E, 0, K * N};
   dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)cdiv(K, CfgSmall::BM), (unsigned)E);
   return launch_bf16<CfgSmall, MODE_GROUPED_K>(a, false, false, out_dtype, grid, (hipStream_t)stream);
+}
+
+int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t* offsets, int64_t J, int E,
+                              int64_t K, int64_t N, void* out, int out_dtype, void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhsT || !doutT || !offsets || !out)
+    return fail(PD_EINVAL, "pd_grouped_gemm_dw_kmajor: bad args");
+  if (!bf16_operand_ok(lhsT, J, J) || !bf16_operand_ok(doutT, J, J))
+    return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw_kmajor: J must be a multiple of 8 with 16B-aligned bases");
+  if (E > 65535 || cdiv(K, CfgDtl::BM) > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw_kmajor: size");
+  // (J == 0: every group has an empty k range, no loads are issued, out = 0)
+  // out[e] (M=K x N) = lhsT[:, rows_e] (A stored [K, J]: K-major) @ doutT[:, rows_e]^T (B stored [N, J])
+  GemmArgs a{K, N, J, (const bf16_t*)lhsT, J, (const bf16_t*)doutT, J, out, N, 1.f, 0.f, offsets, E, 0, K * N};
+  dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)E);
+  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, grid, (hipStream_t)stream);
 }
 
 }  // extern "C"

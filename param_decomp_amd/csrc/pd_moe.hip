@@ -10,8 +10,11 @@
 // L_p imp-min over the selected upper CI, and the full backward (V/U of every site, the
 // CI preactivations, through routing weights, router softmax and the norm).
 //
-// All contractions are the grouped bf16 MFMA GEMMs of pd_gemm.hip; the elementwise
-// passes below are one pass each over job space or token space.
+// Every grouped GEMM runs with both operands K-contiguous:
+//   forward  out = in @ W[e]      rhs = W^T copies [E, N, K] made once per step
+//   d_input  d_in = d_out @ W[e]^T rhs = W in its own layout [E, K_in, N_out]
+//   d_weight dW[e] = in^T @ d_out  both from job-contiguous copies [width, J] that the
+//                                  job-space producers write through 64x64 LDS tiles
 #include <algorithm>
 #include <vector>
 
@@ -20,15 +23,60 @@
 namespace pd {
 
 static constexpr int MOE_KIND_GATE = 11, MOE_KIND_UP = 12, MOE_KIND_DOWN = 13;  // KIND_ORDER indices
+static constexpr int TILE = 64;
 
-static inline unsigned grid_for(int64_t n, int per_block) {
-  int64_t b = cdiv(n, per_block);
-  return (unsigned)(b < 1 ? 1 : (b > 16384 ? 16384 : b));
+// ---------------------------------------------------------------- layout kernels
+// dst[b][c][r] = src[b][r][c] for B matrices of [R, Cc] (64x64 tiles through LDS).
+__global__ __launch_bounds__(256) void k_batched_transpose(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
+                                                           bf16_t* __restrict__ dst) {
+  __shared__ bf16_t tile[TILE][TILE + 2];
+  const int64_t b = blockIdx.z;
+  const bf16_t* s = src + b * R * Cc;
+  bf16_t* d = dst + b * R * Cc;
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < R && c < Cc) ? s[r * Cc + c] : (bf16_t)0;
+  }
+  __syncthreads();
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (c < Cc && r < R) d[c * R + r] = tile[tx][i];
+  }
+}
+
+// Job-space gather on 64x64 tiles: out[j][i] = src[idx[j] / div][i] and/or its
+// job-contiguous copy outT[i][j].
+__global__ __launch_bounds__(256) void k_gather_tile(const bf16_t* __restrict__ src, const int32_t* __restrict__ idx,
+                                                     int div, int64_t J, int w, bf16_t* __restrict__ out,
+                                                     bf16_t* __restrict__ outT) {
+  __shared__ bf16_t tile[TILE][TILE + 2];
+  const int64_t j0 = (int64_t)blockIdx.y * TILE;
+  const int c0 = blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t j = j0 + i;
+    const int c = c0 + tx;
+    bf16_t v = 0;
+    if (j < J && c < w) {
+      v = src[(int64_t)(idx[j] / div) * w + c];
+      if (out) out[j * w + c] = v;
+    }
+    tile[i][tx] = v;
+  }
+  if (!outT) return;
+  __syncthreads();
+  for (int i = ty; i < TILE; i += 4) {
+    const int c = c0 + i;
+    const int64_t j = j0 + tx;
+    if (c < w && j < J) outT[(int64_t)c * J + j] = tile[tx][i];
+  }
 }
 
 // ---------------------------------------------------------------- token-space kernels
-// One block (256 threads) per token row of width d (d <= 2048): y = x * rsqrt(mean x^2
-// + eps) * (1 + w), fp32 math, bf16 out; rinv saved for the backward.
+// One block (256 threads) per token row of width d: y = x * rsqrt(mean x^2 + eps) *
+// (1 + w), fp32 math, bf16 out; rinv saved for the backward.
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const bf16_t* __restrict__ x, int64_t T, int d,
                                                      const float* __restrict__ w, float eps, bf16_t* __restrict__ y,
                                                      float* __restrict__ rinv) {
@@ -70,8 +118,8 @@ __global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__
   if (lane < k) w[t * k + lane] = sel / s;
 }
 
-// r_out[t,:] = bf16(r[t,:] + sum_s wt[t,s] * y[inv[t*k+s],:]) with fp32 accumulation;
-// wt NULL = the unweighted sum_jobs.
+// r_out[t,:] = bf16(r[t,:] + bf16(sum_s wt[t,s] * y[inv[t*k+s],:])) with fp32
+// accumulation; wt NULL = the unweighted sum_jobs.
 __global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restrict__ r, const bf16_t* __restrict__ y,
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ wt, int64_t T, int k, int d,
@@ -84,7 +132,6 @@ __global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restri
       float v = bf16_to_f32(y[(int64_t)inv[t * k + s] * d + i]);
       acc = wt ? fmaf(wt[t * k + s], v, acc) : acc + v;
     }
-    // the routed output is rounded to bf16 before the residual add (sum_jobs casts back)
     r_out[t * d + i] = f32_to_bf16(bf16_to_f32(r[t * d + i]) + bf16_to_f32(f32_to_bf16(acc)));
   }
 }
@@ -107,7 +154,7 @@ __global__ __launch_bounds__(256) void k_moe_recon(const bf16_t* __restrict__ r,
   if (threadIdx.x == 0) partial[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
 }
 
-// ---------------------------------------------------------------- job-space kernels
+// ---------------------------------------------------------------- job-space kernels (64x64 tiles)
 struct SiteMaskArgs {
   const bf16_t* ci_pre;  // [T, k, c] token-major (slot m = the token's m-th expert)
   const int32_t* sort_idx;
@@ -118,144 +165,223 @@ struct SiteMaskArgs {
   float p;
 };
 
-// Forward mask in job space: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at
-// the job's token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16);
-// acts = bf16(h * m); u stored as its 7-bit integer; partial sums of upper(ci)^p.
-__global__ __launch_bounds__(256) void k_site_mask_fwd(SiteMaskArgs a, const bf16_t* __restrict__ h,
-                                                       bf16_t* __restrict__ acts, uint8_t* __restrict__ ubits,
-                                                       float* __restrict__ imp_partial) {
-  const int64_t n = a.J * a.c;
-  float imp = 0.f;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t j = i / a.c;
-    const int q = (int)(i - j * a.c);
-    const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
-    const float pre = bf16_to_f32(a.ci_pre[src]);
-    const float lo = lower_fwd(pre), up = upper_fwd(pre);
-    imp += a.p == 2.f ? up * up : (a.p == 1.f ? up : powf(up, a.p));
-    const uint32_t kb = (draw_bits(a.k0, a.k1, src, n, 8, a.layout) & 0xFFu) >> 1;
-    ubits[i] = (uint8_t)kb;
-    const float m = lo + (1.f - lo) * ((float)kb * (1.f / 128.f));
-    acts[i] = f32_to_bf16(bf16_to_f32(h[i]) * m);
-  }
+__device__ inline float powp(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
+__device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f)); }
+
+// Forward mask: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at the job's
+// token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16); acts =
+// bf16(h * m) written as acts [J,c] and acts^T [c,J]; u stored as its 7-bit integer;
+// per-block partial of upper(ci)^p.
+__global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
+                                                       bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
+                                                       uint8_t* __restrict__ ubits, float* __restrict__ imp_partial) {
+  __shared__ bf16_t tile[TILE][TILE + 2];
   __shared__ float red[4];
+  const int64_t j0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t n = a.J * a.c;
+  const int q = q0 + tx;
+  float imp = 0.f;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t j = j0 + i;
+    bf16_t out = 0;
+    if (j < a.J && q < a.c) {
+      const int64_t idx = j * a.c + q;
+      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
+      const float pre = bf16_to_f32(a.ci_pre[src]);
+      const float lo = lower_fwd(pre);
+      imp += powp(upper_fwd(pre), a.p);
+      const uint32_t kb = (draw_bits(a.k0, a.k1, src, n, 8, a.layout) & 0xFFu) >> 1;
+      ubits[idx] = (uint8_t)kb;
+      const float m = lo + (1.f - lo) * ((float)kb * (1.f / 128.f));
+      out = f32_to_bf16(bf16_to_f32(h[idx]) * m);
+      acts[idx] = out;
+    }
+    tile[i][tx] = out;
+  }
   imp = wave_sum(imp);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = imp;
+  if (tx == 0) red[ty] = imp;
   __syncthreads();
-  if (threadIdx.x == 0) imp_partial[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  for (int i = ty; i < TILE; i += 4) {
+    const int qq = q0 + i;
+    const int64_t j = j0 + tx;
+    if (qq < a.c && j < a.J) actsT[(int64_t)qq * a.J + j] = tile[tx][i];
+  }
 }
 
-// Backward mask in job space: d_h = bf16(d_acts * m) (in place over d_acts) and the CI
-// pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
-// upper_vjp(pre, imp_scale * d upper^p) written token-major.
-__global__ __launch_bounds__(256) void k_site_mask_bwd(SiteMaskArgs a, const bf16_t* __restrict__ h,
+// Backward mask: d_h = bf16(d_acts * m) (in place over d_acts, plus d_h^T [c,J]) and the
+// CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
+// upper_vjp(pre, imp_scale * d upper^p), written token-major.
+__global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
-                                                       bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_pre) {
-  const int64_t n = a.J * a.c;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t j = i / a.c;
-    const int q = (int)(i - j * a.c);
-    const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
-    const float pre = bf16_to_f32(a.ci_pre[src]);
-    const float lo = lower_fwd(pre), up = upper_fwd(pre);
-    const float u = (float)ubits[i] * (1.f / 128.f);
-    const float m = lo + (1.f - lo) * u;
-    const float da = bf16_to_f32(d_acts[i]);
-    const float dup = imp_scale * (a.p == 2.f ? 2.f * up : (a.p == 1.f ? 1.f : a.p * powf(up, a.p - 1.f)));
-    d_pre[src] = f32_to_bf16(lower_vjp(pre, da * bf16_to_f32(h[i]) * (1.f - u)) + upper_vjp(pre, dup));
-    d_acts[i] = f32_to_bf16(da * m);
+                                                       bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_hT,
+                                                       bf16_t* __restrict__ d_pre) {
+  __shared__ bf16_t tile[TILE][TILE + 2];
+  const int64_t j0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int q = q0 + tx;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t j = j0 + i;
+    bf16_t out = 0;
+    if (j < a.J && q < a.c) {
+      const int64_t idx = j * a.c + q;
+      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
+      const float pre = bf16_to_f32(a.ci_pre[src]);
+      const float lo = lower_fwd(pre), up = upper_fwd(pre);
+      const float u = (float)ubits[idx] * (1.f / 128.f);
+      const float m = lo + (1.f - lo) * u;
+      const float da = bf16_to_f32(d_acts[idx]);
+      d_pre[src] = f32_to_bf16(lower_vjp(pre, da * bf16_to_f32(h[idx]) * (1.f - u)) +
+                               upper_vjp(pre, imp_scale * dpowp(up, a.p)));
+      out = f32_to_bf16(da * m);
+      d_acts[idx] = out;
+    }
+    tile[i][tx] = out;
+  }
+  __syncthreads();
+  for (int i = ty; i < TILE; i += 4) {
+    const int qq = q0 + i;
+    const int64_t j = j0 + tx;
+    if (qq < a.c && j < a.J) d_hT[(int64_t)qq * a.J + j] = tile[tx][i];
   }
 }
 
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math); wt NULL = frozen arm
-// (no weight), in which case sort_idx is unused.
-__global__ __launch_bounds__(256) void k_swiglu_fwd(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
-                                                    const float* __restrict__ wt, const int32_t* __restrict__ sort_idx,
-                                                    int64_t J, int f, bf16_t* __restrict__ din) {
-  const int64_t n = J * f;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t j = i / f;
-    const float gv = bf16_to_f32(g[i]);
-    float v = gv * sigm(gv) * bf16_to_f32(u[i]);
-    if (wt) v *= wt[sort_idx[j]];
-    din[i] = f32_to_bf16(v);
+// din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math) and its job-contiguous copy;
+// wt NULL = the frozen arm (no weight, no copy needed).
+__global__ __launch_bounds__(256) void k_swiglu_fwd_tile(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
+                                                         const float* __restrict__ wt,
+                                                         const int32_t* __restrict__ sort_idx, int64_t J, int f,
+                                                         bf16_t* __restrict__ din, bf16_t* __restrict__ dinT) {
+  __shared__ bf16_t tile[TILE][TILE + 2];
+  const int64_t j0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int q = q0 + tx;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t j = j0 + i;
+    bf16_t out = 0;
+    if (j < J && q < f) {
+      const int64_t idx = j * f + q;
+      const float gv = bf16_to_f32(g[idx]);
+      float v = gv * sigm(gv) * bf16_to_f32(u[idx]);
+      if (wt) v *= wt[sort_idx[j]];
+      out = f32_to_bf16(v);
+      din[idx] = out;
+    }
+    tile[i][tx] = out;
+  }
+  if (!dinT) return;
+  __syncthreads();
+  for (int i = ty; i < TILE; i += 4) {
+    const int qq = q0 + i;
+    const int64_t j = j0 + tx;
+    if (qq < f && j < J) dinT[(int64_t)qq * J + j] = tile[tx][i];
   }
 }
 
-// SwiGLU-fold backward, one wave per job row: d_g = bf16(d*u*w*silu'(g)),
-// d_u = bf16(d*silu(g)*w), d_w[j] = sum_f d*silu(g)*u.
-__global__ __launch_bounds__(256) void k_swiglu_bwd(const bf16_t* __restrict__ d_din, const bf16_t* __restrict__ g,
-                                                    const bf16_t* __restrict__ u, const float* __restrict__ wt,
-                                                    const int32_t* __restrict__ sort_idx, int64_t J, int f,
-                                                    bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_u,
-                                                    float* __restrict__ d_wj) {
-  const int lane = threadIdx.x & 63;
-  const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (j >= J) return;
-  const float w = wt[sort_idx[j]];
-  float acc = 0.f;
-  for (int q = lane; q < f; q += 64) {
-    const int64_t i = j * f + q;
-    const float dv = bf16_to_f32(d_din[i]), gv = bf16_to_f32(g[i]), uv = bf16_to_f32(u[i]);
-    const float sg = sigm(gv);
-    const float s = gv * sg;
-    d_g[i] = f32_to_bf16(dv * uv * w * sg * (1.f + gv * (1.f - sg)));
-    d_u[i] = f32_to_bf16(dv * s * w);
-    acc = fmaf(dv * s, uv, acc);
+// SwiGLU-fold backward on 64x64 tiles: d_g = bf16(d*u*w*silu'(g)), d_u = bf16(d*silu(g)*w)
+// with their job-contiguous copies, and the per-(job, tile) partial of
+// d_w[j] = sum_f d*silu(g)*u into d_w_part [J, tiles].
+__global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restrict__ d_din,
+                                                         const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
+                                                         const float* __restrict__ wt,
+                                                         const int32_t* __restrict__ sort_idx, int64_t J, int f,
+                                                         bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_gT,
+                                                         bf16_t* __restrict__ d_u, bf16_t* __restrict__ d_uT,
+                                                         float* __restrict__ d_w_part) {
+  __shared__ bf16_t tg[TILE][TILE + 2];
+  __shared__ bf16_t tu[TILE][TILE + 2];
+  const int64_t j0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int q = q0 + tx;
+  for (int i = ty; i < TILE; i += 4) {
+    const int64_t j = j0 + i;
+    bf16_t og = 0, ou = 0;
+    float part = 0.f;
+    if (j < J) {
+      const float w = wt[sort_idx[j]];
+      if (q < f) {
+        const int64_t idx = j * f + q;
+        const float dv = bf16_to_f32(d_din[idx]), gv = bf16_to_f32(g[idx]), uv = bf16_to_f32(u[idx]);
+        const float sg = sigm(gv);
+        const float s = gv * sg;
+        og = f32_to_bf16(dv * uv * w * sg * (1.f + gv * (1.f - sg)));
+        ou = f32_to_bf16(dv * s * w);
+        d_g[idx] = og;
+        d_u[idx] = ou;
+        part = dv * s * uv;
+      }
+    }
+    part = wave_sum(part);  // one wave = one job row of this tile
+    if (tx == 0 && j < J) d_w_part[j * gridDim.x + blockIdx.x] = part;
+    tg[i][tx] = og;
+    tu[i][tx] = ou;
   }
-  acc = wave_sum(acc);
-  if (lane == 0) d_wj[j] = acc;
+  __syncthreads();
+  for (int i = ty; i < TILE; i += 4) {
+    const int qq = q0 + i;
+    const int64_t j = j0 + tx;
+    if (qq < f && j < J) {
+      d_gT[(int64_t)qq * J + j] = tg[tx][i];
+      d_uT[(int64_t)qq * J + j] = tu[tx][i];
+    }
+  }
 }
 
 // Token backward, one block (256 threads) per token:
-//   d_w[s] = d_wj[inv[t*k+s]]; through w = p_sel / sum p_sel and the router softmax to
-//   d_logits[E] (wave 0, lanes = experts); d_h2 = sum_s (dxa + dxb)[inv[t*k+s]] +
-//   d_logits @ router; d_r_out = bf16(d_r + rms_norm_vjp(r, d_h2)).
-__global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_wj, const int32_t* __restrict__ inv,
-                                                   const int32_t* __restrict__ idx, const float* __restrict__ probs,
-                                                   const float* __restrict__ w, const bf16_t* __restrict__ router,
-                                                   const bf16_t* __restrict__ dxa, const bf16_t* __restrict__ dxb,
-                                                   const bf16_t* __restrict__ r, const float* __restrict__ rinv,
-                                                   const float* __restrict__ ln, const bf16_t* __restrict__ d_r,
-                                                   int64_t T, int E, int k, int d, float* __restrict__ scratch_h2,
+//   d_w[s] = sum of the d_w_part tiles of job inv[t*k+s]; through w = p_sel / sum p_sel
+//   and the router softmax to d_logits[E] (wave 0, lanes = experts); d_h2 = sum_s
+//   (dxa + dxb)[inv[t*k+s]] + d_logits @ router; d_r_out = bf16(d_r + rms_norm_vjp).
+__global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w_part, int n_part,
+                                                   const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
+                                                   const float* __restrict__ probs, const float* __restrict__ w,
+                                                   const bf16_t* __restrict__ router, const bf16_t* __restrict__ dxa,
+                                                   const bf16_t* __restrict__ dxb, const bf16_t* __restrict__ r,
+                                                   const float* __restrict__ rinv, const float* __restrict__ ln,
+                                                   const bf16_t* __restrict__ d_r, int64_t T, int E, int k, int d,
                                                    bf16_t* __restrict__ d_r_out) {
   const int64_t t = blockIdx.x;
   if (t >= T) return;
   __shared__ float dlog[64];
   __shared__ float red[4];
+  __shared__ float h2g[4096];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (wave == 0) {
-    // d_w and the renormalization pullback over the k slots
-    float dw = lane < k ? d_wj[inv[t * k + lane]] : 0.f;
-    float wv = lane < k ? w[t * k + lane] : 0.f;
-    float dot = wave_sum(dw * wv);
+    float dw = 0.f;
+    if (lane < k) {
+      const int64_t jj = inv[t * k + lane];
+      for (int pp = 0; pp < n_part; ++pp) dw += d_w_part[jj * n_part + pp];
+    }
+    const float wv = lane < k ? w[t * k + lane] : 0.f;
+    const float dot = wave_sum(dw * wv);
     int e_of_slot = lane < k ? idx[t * k + lane] : -1;
     if (lane < k) e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
     const float pe = lane < E ? probs[t * E + lane] : 0.f;
     const float psel = __shfl(pe, lane < k ? e_of_slot : 0, 64);  // all lanes shuffle
-    float S = wave_sum(lane < k ? psel : 0.f);
-    float dps = lane < k ? (dw - dot) / S : 0.f;
-    // scatter d_psel to experts: lane e collects the slot that selected it (distinct)
+    const float S = wave_sum(lane < k ? psel : 0.f);
+    const float dps = lane < k ? (dw - dot) / S : 0.f;
     float dpe = 0.f;
     for (int s = 0; s < k; ++s) {
-      int es = __shfl(e_of_slot, s, 64);
-      float v = __shfl(dps, s, 64);
+      const int es = __shfl(e_of_slot, s, 64);
+      const float v = __shfl(dps, s, 64);
       if (lane == es) dpe += v;
     }
-    float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
+    const float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
     if (lane < E) dlog[lane] = pe * (dpe - sdot);
   }
   __syncthreads();
-  // d_h2 and the norm pullback
   const bf16_t* xr = r + t * d;
-  float* h2g = scratch_h2 + t * d;
   float part = 0.f;
   for (int i = threadIdx.x; i < d; i += 256) {
     float acc = 0.f;
     for (int s = 0; s < k; ++s) {
-      int64_t row = (int64_t)inv[t * k + s] * d + i;
+      const int64_t row = (int64_t)inv[t * k + s] * d + i;
       acc += bf16_to_f32(dxa[row]) + bf16_to_f32(dxb[row]);
     }
     for (int e = 0; e < E; ++e) acc = fmaf(dlog[e], bf16_to_f32(router[(int64_t)e * d + i]), acc);
@@ -304,7 +430,6 @@ __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, cons
 }
 
 // ---------------------------------------------------------------- workspace plan
-static constexpr int MASK_BLOCKS = 2048;  // fixed partial count per site mask pass
 static constexpr int REC_BLOCKS = 1024;
 
 struct MoEDims {
@@ -326,28 +451,30 @@ struct Arena {
 };
 
 struct LayerSave {
-  bf16_t *r, *h2, *xj, *gout, *uout, *din;
+  bf16_t *r, *h2, *xjT, *gout, *uout, *dinT;
   float *rinv, *probs, *w;
   int32_t *idx, *sort_idx, *inv, *sizes, *offsets;
   bf16_t* h[3];
-  bf16_t* acts[3];
+  bf16_t* actsT[3];
   uint8_t* ub[3];
 };
 
 struct MoEPlan {
   std::vector<LayerSave> layers;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xjc, *gc, *uc, *dinc, *downc, *down, *dr_a, *dr_b;
-  float *logits, *probsc, *wc, *rec_part, *imp_part, *h2g;
-  int32_t *idxc_scratch, *sort_ws;
-  bf16_t *d_dout, *d_acts, *d_din, *d_g, *d_u, *dxa, *dxb, *d_h;
-  float* d_wj;
-  size_t total;
+  // weight copies [L, E, N, K] for the forward products
+  bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
+  float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part;
+  int32_t* sort_ws;
+  bf16_t *d_dout, *d_doutT, *d_acts, *d_hT, *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
+  size_t imp_per_site, total;
 };
 
 static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   Arena A{base, 0, dry};
   MoEPlan P;
   const int64_t T = D.T, J = D.J;
+  const size_t E = D.E, L = D.L;
   P.layers.resize(D.L);
   for (int l = 0; l < D.L; ++l) {
     LayerSave& S = P.layers[l];
@@ -361,24 +488,34 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
     S.inv = A.take<int32_t>(J);
     S.sizes = A.take<int32_t>(D.E);
     S.offsets = A.take<int32_t>(D.E + 1);
-    S.xj = A.take<bf16_t>(J * D.d);
+    S.xjT = A.take<bf16_t>(J * D.d);
     S.gout = A.take<bf16_t>(J * D.f);
     S.uout = A.take<bf16_t>(J * D.f);
-    S.din = A.take<bf16_t>(J * D.f);
+    S.dinT = A.take<bf16_t>(J * D.f);
     for (int s = 0; s < 3; ++s) {
       S.h[s] = A.take<bf16_t>(J * D.c);
-      S.acts[s] = A.take<bf16_t>(J * D.c);
+      S.actsT[s] = A.take<bf16_t>(J * D.c);
       S.ub[s] = A.take<uint8_t>(J * D.c);
     }
   }
+  P.WgT = A.take<bf16_t>(L * E * D.d * D.f);
+  P.WuT = A.take<bf16_t>(L * E * D.d * D.f);
+  P.WdT = A.take<bf16_t>(L * E * D.d * D.f);
+  P.VgT = A.take<bf16_t>(L * E * D.d * D.c);
+  P.UgT = A.take<bf16_t>(L * E * D.c * D.f);
+  P.VuT = A.take<bf16_t>(L * E * D.d * D.c);
+  P.UuT = A.take<bf16_t>(L * E * D.c * D.f);
+  P.VdT = A.take<bf16_t>(L * E * D.f * D.c);
+  P.UdT = A.take<bf16_t>(L * E * D.c * D.d);
   P.rc_a = A.take<bf16_t>(T * D.d);
   P.rc_b = A.take<bf16_t>(T * D.d);
   P.r_final = A.take<bf16_t>(T * D.d);
   P.h2c = A.take<bf16_t>(T * D.d);
-  P.xjc = A.take<bf16_t>(J * D.d);
+  P.xj = A.take<bf16_t>(J * D.d);
+  P.acts = A.take<bf16_t>(J * D.c);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
-  P.dinc = A.take<bf16_t>(J * D.f);
+  P.din = A.take<bf16_t>(J * D.f);
   P.downc = A.take<bf16_t>(J * D.d);
   P.down = A.take<bf16_t>(J * D.d);
   P.dr_a = A.take<bf16_t>(T * D.d);
@@ -387,19 +524,21 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.probsc = A.take<float>(T * D.E);
   P.wc = A.take<float>(T * D.k);
   P.rec_part = A.take<float>(REC_BLOCKS);
-  P.imp_part = A.take<float>((size_t)MASK_BLOCKS * 3 * D.L);
-  P.h2g = A.take<float>(T * D.d);
-  P.idxc_scratch = A.take<int32_t>(T * D.k);
+  P.imp_per_site = (size_t)cdiv(D.c, TILE) * cdiv(J, TILE);
+  P.imp_part = A.take<float>(P.imp_per_site * 3 * D.L);
+  P.d_w_part = A.take<float>(J * cdiv(D.f, TILE));
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
+  P.d_doutT = A.take<bf16_t>(J * D.d);
   P.d_acts = A.take<bf16_t>(J * D.c);
+  P.d_hT = A.take<bf16_t>(J * D.c);
   P.d_din = A.take<bf16_t>(J * D.f);
   P.d_g = A.take<bf16_t>(J * D.f);
+  P.d_gT = A.take<bf16_t>(J * D.f);
   P.d_u = A.take<bf16_t>(J * D.f);
+  P.d_uT = A.take<bf16_t>(J * D.f);
   P.dxa = A.take<bf16_t>(J * D.d);
   P.dxb = A.take<bf16_t>(J * D.d);
-  P.d_h = A.take<bf16_t>(J * D.f > J * D.d ? J * D.f : J * D.d);
-  P.d_wj = A.take<float>(J);
   P.total = A.off;
   return P;
 }
@@ -417,6 +556,13 @@ struct Recorder {
   }
 };
 
+static void launch_batched_T(const void* src, int64_t B, int64_t R, int64_t Cc, bf16_t* dst, hipStream_t s) {
+  hipLaunchKernelGGL(k_batched_transpose, dim3((unsigned)cdiv(Cc, TILE), (unsigned)cdiv(R, TILE), (unsigned)B),
+                     dim3(256), 0, s, (const bf16_t*)src, R, Cc, dst);
+}
+
+static dim3 tile_grid(int64_t J, int w) { return dim3((unsigned)cdiv(w, TILE), (unsigned)cdiv(J, TILE)); }
+
 }  // namespace pd
 
 using namespace pd;
@@ -431,8 +577,8 @@ size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c,
 // Phase categories recorded by pd_moe_stack_step_timed (one event before each launch
 // group and one at the end; cat[i] labels the interval [i, i+1)).
 enum {
-  MOE_CAT_CLEAN = 0,       // clean forward (norm, router, bucketing, frozen grouped GEMMs, combine)
-  MOE_CAT_NORM_ROUTE = 1,  // masked-pass norm, router GEMM, pinned weights, bucketing, gather
+  MOE_CAT_CLEAN = 0,       // weight copies + clean forward (norm, router, bucketing, frozen GEMMs, combine)
+  MOE_CAT_NORM_ROUTE = 1,  // masked-pass norm, router GEMM, pinned weights, gather
   MOE_CAT_GEMM_FWD = 2,    // grouped GEMMs of the decomposed sites, forward
   MOE_CAT_MASK_FWD = 3,    // job-space mask passes, forward
   MOE_CAT_SWIGLU = 4,      // SwiGLU fold fwd/bwd
@@ -453,8 +599,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                          void* stream, Recorder& rec) {
   if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 64 || k <= 0 || k > E || c <= 0 || L <= 0)
     return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 64)");
-  if (d % 8 || f % 8 || c % 8) return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d, f, c must be multiples of 8");
-  if (d > 4096 || T * k > 0x7FFFFFFF) return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: shape too large");
+  if (d % 8 || f % 8 || c % 8 || (T * k) % 8)
+    return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d, f, c and T*k must be multiples of 8");
+  if (d > 4096 || T * k > 0x7FFFFFFF || cdiv(T * k, TILE) > 65535)
+    return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: shape too large");
   if (!x0 || !ln || !router || !Wg || !Wu || !Wd || !Vg || !Ug || !Vu || !Uu || !Vd || !Ud || !ci_pre || !losses ||
       !dVg || !dUg || !dVu || !dUu || !dVd || !dUd || !d_ci_pre)
     return fail(PD_EINVAL, "pd_moe_stack_step: null pointer");
@@ -491,9 +639,26 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     o0 = y0;
     o1 = y1;
   };
+  const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
+
+  // ================= K-contiguous weight copies for the forward products (once per step)
+  rec.mark(MOE_CAT_CLEAN);
+  const int64_t LE = (int64_t)L * E;
+  launch_batched_T(Wg, LE, d, f, P.WgT, s);
+  launch_batched_T(Wu, LE, d, f, P.WuT, s);
+  launch_batched_T(Wd, LE, f, d, P.WdT, s);
+  launch_batched_T(Vg, LE, d, c, P.VgT, s);
+  launch_batched_T(Ug, LE, c, f, P.UgT, s);
+  launch_batched_T(Vu, LE, d, c, P.VuT, s);
+  launch_batched_T(Uu, LE, c, f, P.UuT, s);
+  launch_batched_T(Vd, LE, f, c, P.VdT, s);
+  launch_batched_T(Ud, LE, c, d, P.UdT, s);
+  const bf16_t* VT[3] = {P.VgT, P.VuT, P.VdT};
+  const bf16_t* UT[3] = {P.UgT, P.UuT, P.UdT};
+  const size_t szV[3] = {szVg, szVg, szVd};
+  const size_t szU[3] = {szUg, szUg, szUd};
 
   // ================= clean forward (frozen weights): pins the expert indices
-  rec.mark(MOE_CAT_CLEAN);
   hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
   bf16_t* rcur = P.rc_a;
   bf16_t* rnext = P.rc_b;
@@ -508,19 +673,19 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
                              pd_routed_jobs_workspace_size(J, E), stream)))
       return rc;
-    if ((rc = pd_gather_rows(P.h2c, PD_DTYPE_BF16, d, S.sort_idx, k, J, P.xjc, stream))) return rc;
-    if ((rc = pd_grouped_gemm(P.xjc, bf(Wg, l * szW), S.offsets, J, E, d, f, 0, P.gc, PD_DTYPE_BF16, stream)))
-      return rc;
-    if ((rc = pd_grouped_gemm(P.xjc, bf(Wu, l * szW), S.offsets, J, E, d, f, 0, P.uc, PD_DTYPE_BF16, stream)))
-      return rc;
-    hipLaunchKernelGGL(k_swiglu_fwd, dim3(grid_for(J * f, 1024)), dim3(256), 0, s, P.gc, P.uc, (const float*)nullptr,
-                       S.sort_idx, J, f, P.dinc);
-    if ((rc = pd_grouped_gemm(P.dinc, bf(Wd, l * szW), S.offsets, J, E, f, d, 0, P.downc, PD_DTYPE_BF16, stream)))
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, P.h2c, S.sort_idx, k, J, d, P.xj,
+                       (bf16_t*)nullptr);
+    if ((rc = grouped_gemm(P.xj, P.WgT + l * szW, S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false))) return rc;
+    if ((rc = grouped_gemm(P.xj, P.WuT + l * szW, S.offsets, J, E, d, f, 1, P.uc, PD_DTYPE_BF16, stream, false))) return rc;
+    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, P.gc, P.uc, (const float*)nullptr,
+                       S.sort_idx, J, f, P.din, (bf16_t*)nullptr);
+    if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
       return rc;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
                        rnext);
     std::swap(rcur, rnext);
-    if (top_idx_out) hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+    if (top_idx_out)
+      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
   }
   bf16_t* rc_final = rcur;
   if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
@@ -530,7 +695,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
     rec.mark(MOE_CAT_NORM_ROUTE);
-    hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
+    if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
     hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)T), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f, S.h2,
                        S.rinv);
     if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
@@ -538,26 +703,21 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
                        S.probs, S.w);
-    if ((rc = pd_gather_rows(S.h2, PD_DTYPE_BF16, d, S.sort_idx, k, J, S.xj, stream))) return rc;
-    const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
-    bf16_t* outs[2] = {S.gout, S.uout};
-    const void* Vs[2] = {Vg, Vu};
-    const void* Us[2] = {Ug, Uu};
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
+    bf16_t* outs[3] = {S.gout, S.uout, P.down};
+    const int nout[3] = {f, f, d};
     for (int si = 0; si < 3; ++si) {
+      const bf16_t* in = si < 2 ? P.xj : P.din;
+      const int kin = si < 2 ? d : f;
       if (si == 2) {
         rec.mark(MOE_CAT_SWIGLU);
-        hipLaunchKernelGGL(k_swiglu_fwd, dim3(grid_for(J * f, 1024)), dim3(256), 0, s, S.gout, S.uout, S.w,
-                           S.sort_idx, J, f, S.din);
+        hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J,
+                           f, P.din, S.dinT);
       }
       rec.mark(MOE_CAT_GEMM_FWD);
-      if (si < 2) {
-        if ((rc = pd_grouped_gemm(S.xj, bf(Vs[si], l * szVg), S.offsets, J, E, d, c, 0, S.h[si], PD_DTYPE_BF16,
-                                  stream)))
-          return rc;
-      } else {
-        if ((rc = pd_grouped_gemm(S.din, bf(Vd, l * szVd), S.offsets, J, E, f, c, 0, S.h[2], PD_DTYPE_BF16, stream)))
-          return rc;
-      }
+      if ((rc = grouped_gemm(in, VT[si] + l * szV[si], S.offsets, J, E, kin, c, 1, S.h[si], PD_DTYPE_BF16,
+                                stream, false)))
+        return rc;
       rec.mark(MOE_CAT_MASK_FWD);
       SiteMaskArgs ma;
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
@@ -567,18 +727,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.layout = layout;
       ma.p = p;
-      hipLaunchKernelGGL(k_site_mask_fwd, dim3(MASK_BLOCKS), dim3(256), 0, s, ma, S.h[si], S.acts[si], S.ub[si],
-                         P.imp_part + ((size_t)l * 3 + si) * MASK_BLOCKS);
+      hipLaunchKernelGGL(k_mask_fwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], P.acts, S.actsT[si],
+                         S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
       rec.mark(MOE_CAT_GEMM_FWD);
-      if (si < 2) {
-        if ((rc = pd_grouped_gemm(S.acts[si], bf(Us[si], l * szUg), S.offsets, J, E, c, f, 0, outs[si],
-                                  PD_DTYPE_BF16, stream)))
-          return rc;
-      } else {
-        if ((rc = pd_grouped_gemm(S.acts[2], bf(Ud, l * szUd), S.offsets, J, E, c, d, 0, P.down, PD_DTYPE_BF16,
-                                  stream)))
-          return rc;
-      }
+      if ((rc = grouped_gemm(P.acts, UT[si] + l * szU[si], S.offsets, J, E, c, nout[si], 1, outs[si],
+                                PD_DTYPE_BF16, stream, false)))
+        return rc;
     }
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
@@ -592,78 +746,81 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
                      recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
   hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.imp_part,
-                     (int64_t)MASK_BLOCKS * 3 * L, 1.0 / (double)nres, 1.0 / (double)T, recon_coeff, imp_coeff,
+                     (int64_t)(P.imp_per_site * 3 * L), 1.0 / (double)nres, 1.0 / (double)T, recon_coeff, imp_coeff,
                      losses);
   // ================= backward
   bf16_t* dr = P.dr_a;
   bf16_t* dr_next = P.dr_b;
   const float imp_scale = imp_coeff / (float)T;
+  const int n_wpart = (int)cdiv(f, TILE);
   for (int l = L - 1; l >= 0; --l) {
     LayerSave& S = P.layers[l];
-    const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
     rec.mark(MOE_CAT_COMBINE);
-    if ((rc = pd_gather_rows(dr, PD_DTYPE_BF16, d, S.sort_idx, k, J, P.d_dout, stream))) return rc;
-    // ---- down site
-    rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = pd_grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts, PD_DTYPE_BF16, stream)))
-      return rc;
-    rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd, PD_DTYPE_F32, stream)))
-      return rc;
-    rec.mark(MOE_CAT_MASK_BWD);
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, dr, S.sort_idx, k, J, d, P.d_dout, P.d_doutT);
     SiteMaskArgs ma;
     ma.sort_idx = S.sort_idx;
     ma.J = J;
     ma.c = c;
     ma.layout = layout;
     ma.p = p;
+    // ---- down site
+    rec.mark(MOE_CAT_GEMM_DX);
+    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts, PD_DTYPE_BF16, stream, false)))
+      return rc;
+    rec.mark(MOE_CAT_GEMM_DW);
+    if ((rc = pd_grouped_gemm_dw_kmajor(S.actsT[2], P.d_doutT, S.offsets, J, E, c, d, dUd + l * szUd, PD_DTYPE_F32,
+                                        stream)))
+      return rc;
+    rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
-    hipLaunchKernelGGL(k_site_mask_bwd, dim3(grid_for(J * c, 1024)), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale,
-                       P.d_acts, (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale, P.d_acts,
+                       P.d_hT, (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = pd_grouped_gemm_dw(S.din, P.d_acts, S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32, stream)))
+    if ((rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT, S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = pd_grouped_gemm(P.d_acts, bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream)))
+    if ((rc = grouped_gemm(P.d_acts, bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_SWIGLU);
-    hipLaunchKernelGGL(k_swiglu_bwd, dim3((unsigned)cdiv(J, 4)), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w,
-                       S.sort_idx, J, f, P.d_g, P.d_u, P.d_wj);
+    hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
+                       J, f, P.d_g, P.d_gT, P.d_u, P.d_uT, P.d_w_part);
     // ---- gate and up sites
     const void* Vs[2] = {Vg, Vu};
     const void* Us[2] = {Ug, Uu};
     float* dVs[2] = {dVg, dVu};
     float* dUs[2] = {dUg, dUu};
     bf16_t* douts[2] = {P.d_g, P.d_u};
+    bf16_t* doutsT[2] = {P.d_gT, P.d_uT};
     bf16_t* dxs[2] = {P.dxa, P.dxb};
     for (int si = 0; si < 2; ++si) {
       rec.mark(MOE_CAT_GEMM_DX);
-      if ((rc = pd_grouped_gemm(douts[si], bf(Us[si], l * szUg), S.offsets, J, E, f, c, 1, P.d_acts, PD_DTYPE_BF16,
-                                stream)))
+      if ((rc = grouped_gemm(douts[si], bf(Us[si], l * szUg), S.offsets, J, E, f, c, 1, P.d_acts, PD_DTYPE_BF16,
+                                stream, false)))
         return rc;
       rec.mark(MOE_CAT_GEMM_DW);
-      if ((rc = pd_grouped_gemm_dw(S.acts[si], douts[si], S.offsets, J, E, c, f, dUs[si] + l * szUg, PD_DTYPE_F32,
-                                   stream)))
+      if ((rc = pd_grouped_gemm_dw_kmajor(S.actsT[si], doutsT[si], S.offsets, J, E, c, f, dUs[si] + l * szUg,
+                                          PD_DTYPE_F32, stream)))
         return rc;
       rec.mark(MOE_CAT_MASK_BWD);
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
-      hipLaunchKernelGGL(k_site_mask_bwd, dim3(grid_for(J * c, 1024)), dim3(256), 0, s, ma, S.h[si], S.ub[si],
-                         imp_scale, P.d_acts, (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
+      hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], S.ub[si], imp_scale,
+                         P.d_acts, P.d_hT, (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
       rec.mark(MOE_CAT_GEMM_DW);
-      if ((rc = pd_grouped_gemm_dw(S.xj, P.d_acts, S.offsets, J, E, d, c, dVs[si] + l * szVg, PD_DTYPE_F32, stream)))
+      if ((rc = pd_grouped_gemm_dw_kmajor(S.xjT, P.d_hT, S.offsets, J, E, d, c, dVs[si] + l * szVg, PD_DTYPE_F32,
+                                          stream)))
         return rc;
       rec.mark(MOE_CAT_GEMM_DX);
-      if ((rc = pd_grouped_gemm(P.d_acts, bf(Vs[si], l * szVg), S.offsets, J, E, c, d, 1, dxs[si], PD_DTYPE_BF16,
-                                stream)))
+      if ((rc = grouped_gemm(P.d_acts, bf(Vs[si], l * szVg), S.offsets, J, E, c, d, 1, dxs[si], PD_DTYPE_BF16,
+                                stream, false)))
         return rc;
     }
     // ---- routing weights, router, gather VJP and the norm
     rec.mark(MOE_CAT_TOKEN_BWD);
-    hipLaunchKernelGGL(k_token_bwd, dim3((unsigned)T), dim3(256), 0, s, P.d_wj, S.inv, S.idx, S.probs, S.w,
-                       bf(router, (size_t)l * E * d), P.dxa, P.dxb, S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d,
-                       P.h2g, dr_next);
+    hipLaunchKernelGGL(k_token_bwd, dim3((unsigned)T), dim3(256), 0, s, P.d_w_part, n_wpart, S.inv, S.idx, S.probs,
+                       S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb, S.r, S.rinv, ln + (size_t)l * d, dr, T, E,
+                       k, d, dr_next);
     std::swap(dr, dr_next);
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
   }

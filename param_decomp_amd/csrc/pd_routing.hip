@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 }
 
 // ---- counting sort. Phase 1: per-chunk histograms.
-constexpr int SORT_CHUNK = 2048;
+constexpr int SORT_CHUNK = 256;
 constexpr int SORT_MAX_E = 1024;
 
 // Expert ids outside [0, E) (only possible from corrupt routing input) are clamped
@@ -68,20 +68,30 @@ __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ k
 }
 
 // Phase 2 (one block): group sizes, exclusive group offsets, and each chunk's base
-// position per expert (in place over counts).
+// position per expert (in place over counts). One wave per expert scans the chunk
+// counts 64 at a time.
 __global__ __launch_bounds__(1024) void k_sort_scan(int32_t* __restrict__ counts, int64_t nchunks, int E,
                                                     int32_t* __restrict__ group_sizes,
                                                     int32_t* __restrict__ group_offsets) {
   __shared__ int32_t tot[SORT_MAX_E + 1];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int32_t s = 0;
-    for (int64_t b = 0; b < nchunks; ++b) {
-      int32_t c = counts[b * E + e];
-      counts[b * E + e] = s;  // exclusive prefix over chunks
-      s += c;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  for (int e = wave; e < E; e += nwaves) {
+    int32_t carry = 0;
+    for (int64_t b0 = 0; b0 < nchunks; b0 += 64) {
+      const int64_t b = b0 + lane;
+      const int32_t c = b < nchunks ? counts[b * E + e] : 0;
+      int32_t incl = c;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+      }
+      if (b < nchunks) counts[b * E + e] = carry + incl - c;  // exclusive prefix over chunks
+      carry += __shfl(incl, 63, 64);
     }
-    tot[e] = s;
-    group_sizes[e] = s;
+    if (lane == 0) {
+      tot[e] = carry;
+      group_sizes[e] = carry;
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -96,46 +106,43 @@ __global__ __launch_bounds__(1024) void k_sort_scan(int32_t* __restrict__ counts
     tot[E] = acc;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x)
-    for (int64_t b = 0; b < nchunks; ++b) counts[b * E + e] += tot[e];
+  for (int64_t i = threadIdx.x; i < nchunks * E; i += blockDim.x) counts[i] += tot[i % E];
 }
 
-// Phase 3: one wave per chunk walks it in 64-job steps; each lane's position is its
-// chunk base + the running count of its expert + the number of earlier lanes in the
-// step with the same expert. Stable by construction.
+// Phase 3: one wave per chunk walks it in 64-job steps. Lanes holding the same expert
+// find each other with one ballot per key bit; a lane's position is its chunk base +
+// the running count of its expert + the number of earlier lanes with that expert.
+// Stable by construction.
 __global__ __launch_bounds__(64) void k_sort_scatter(const int32_t* __restrict__ keys, int64_t n, int E,
                                                      const int32_t* __restrict__ base, int32_t* __restrict__ sort_idx,
                                                      int32_t* __restrict__ inv_sort_idx) {
   __shared__ int32_t run[SORT_MAX_E];
-  __shared__ int32_t step_keys[64];
   const int lane = threadIdx.x;
   for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)blockIdx.x * E + e];
   __syncthreads();
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
   int64_t j0 = (int64_t)blockIdx.x * SORT_CHUNK;
   int64_t j1 = j0 + SORT_CHUNK < n ? j0 + SORT_CHUNK : n;
   for (int64_t s0 = j0; s0 < j1; s0 += 64) {
-    int64_t j = s0 + lane;
-    int key = j < j1 ? clamp_key(keys[j], E) : -1;
-    step_keys[lane] = key;
-    __syncthreads();
-    int before = 0;
-    for (int i = 0; i < lane; ++i) before += (step_keys[i] == key);
-    if (j < j1) {
-      int32_t pos = run[key] + before;
+    const int64_t j = s0 + lane;
+    const bool valid = j < j1;
+    const int key = valid ? clamp_key(keys[j], E) : 0;
+    uint64_t same = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t ones = __ballot((key >> b) & 1);
+      same &= ((key >> b) & 1) ? ones : ~ones;
+    }
+    const int before = __popcll(same & lt);
+    const int32_t start = run[key];
+    if (valid) {
+      const int32_t pos = start + before;
       sort_idx[pos] = (int32_t)j;
       inv_sort_idx[j] = pos;
     }
-    __syncthreads();
-    // advance running counters: the last lane holding each expert adds its count
-    if (j < j1) {
-      bool last = true;
-      for (int i = lane + 1; i < 64 && s0 + i < j1; ++i)
-        if (step_keys[i] == key) {
-          last = false;
-          break;
-        }
-      if (last) run[key] += before + 1;
-    }
+    __syncthreads();  // every lane has read run[] before any lane advances it
+    if (valid && (same >> lane) == 1ull) run[key] = start + before + 1;  // last lane of its expert
     __syncthreads();
   }
 }

@@ -172,6 +172,16 @@ def grouped_gemm(lhs, rhs, offsets, *, trans_rhs=False, out_dtype=None):
     return out
 
 
+def grouped_gemm_dw_kmajor(lhsT, doutT, offsets, n_groups: int, *, out_dtype=None):
+    """`out[e] = lhsT[:, rows_e] @ doutT[:, rows_e]^T` from job-contiguous operands."""
+    K, J = lhsT.shape
+    N = doutT.shape[0]
+    out = torch.empty((n_groups, K, N), dtype=out_dtype or lhsT.dtype, device=lhsT.device)
+    L.call("pd_grouped_gemm_dw_kmajor", L.ptr(lhsT), L.ptr(doutT), L.ptr(offsets), J, n_groups, K, N, L.ptr(out),
+           L.dtype_code(out.dtype), L.stream())
+    return out
+
+
 def grouped_gemm_dw(lhs, dout, offsets, n_groups: int, *, out_dtype=None):
     J, K = lhs.shape
     N = dout.shape[1]

@@ -377,7 +377,7 @@ def test_router_topk_bit_exact_indices(device):
     np.testing.assert_allclose(w.cpu().numpy(), po.expert_mixing_weights(p_or, want_idx), rtol=1e-5)
 
 
-@pytest.mark.parametrize("T,k,E", [(24, 2, 8), (8192, 8, 42), (1000, 3, 5), (7, 1, 64)])
+@pytest.mark.parametrize("T,k,E", [(24, 2, 8), (8192, 8, 42), (1000, 3, 5), (7, 1, 64), (3001, 5, 1000)])
 def test_routed_jobs_bit_exact(device, T, k, E):
     from param_decomp_amd.routed.experts import routed_jobs
 
@@ -444,3 +444,51 @@ def test_grouped_matmul_fwd_bwd(device, sizes):
     for e, s in enumerate(sizes):
         if s == 0:
             assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dr[e]) == 0
+
+
+@pytest.mark.parametrize("sizes", [[7, 0, 19, 1, 0, 26, 37, 0], [0, 0, 300, 5], [129, 128, 127, 1]])
+@pytest.mark.parametrize("K", [72, 512])
+def test_grouped_gemm_kmajor_rhs(device, sizes, K):
+    """Grouped forward with the per-group weights stored [E, N, K] (K-contiguous): ragged
+    groups, a contraction that is not a multiple of the 64-wide k tile, trailing rows."""
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(11 + K + sum(sizes))
+    E, N = len(sizes), 136
+    used = int(sum(sizes))
+    J = used + 5
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = bf(rng.normal(size=(J, K)), device)
+    rhsT = bf(rng.normal(size=(E, N, K)) / 8, device)
+    out = ops.grouped_gemm(lhs, rhsT, offsets, trans_rhs=True)
+    want = po.grouped_matmul(np64(lhs)[:used], np.transpose(np64(rhsT), (0, 2, 1)), sizes)
+    assert_close(np64(out)[:used], want, BF16_RTOL, 4e-3, "grouped kmajor rhs")
+    assert np.all(np64(out)[used:] == 0)
+
+
+@pytest.mark.parametrize("sizes", [[7, 0, 19, 1, 0, 26, 37, 0], [0, 0, 300, 5], [129, 128, 127, 1], [3, 5]])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_grouped_gemm_dw_kmajor(device, sizes, out_dtype):
+    """Ragged-contraction dW from job-contiguous operands: unaligned group starts and
+    empty groups (exact zeros); trailing jobs past the last offset are ignored."""
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(7 + sum(sizes))
+    E, K, N = len(sizes), 72, 136
+    used = int(sum(sizes))
+    J = (used + 5 + 7) // 8 * 8
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = bf(rng.normal(size=(J, K)), device)
+    dout = bf(rng.normal(size=(J, N)), device)
+    dw = ops.grouped_gemm_dw_kmajor(lhs.t().contiguous(), dout.t().contiguous(), offsets, E, out_dtype=out_dtype)
+    want = po.transposed_grouped_matmul(np64(lhs)[:used], np64(dout)[:used], sizes)
+    if out_dtype == torch.float32:
+        assert_close(np64(dw), want, 1e-5, 1e-6, "dw kmajor fp32")
+    else:
+        assert_close(np64(dw), want, BF16_RTOL, 4e-3, "dw kmajor bf16")
+    ref = ops.grouped_gemm_dw(lhs, dout, offsets, E, out_dtype=torch.float32)
+    if out_dtype == torch.float32:
+        assert_close(np64(dw), np64(ref), 1e-6, 1e-6, "dw kmajor vs row-major")
+    for e, s in enumerate(sizes):
+        if s == 0:
+            assert torch.count_nonzero(dw[e]) == 0
