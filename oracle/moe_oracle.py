@@ -70,8 +70,8 @@ def rms_norm_vjp(x, w, r, dy):
     return r * a - x * r**3 * np.sum(a * x, axis=-1, keepdims=True) / d
 
 
-def site_mask_keys(draw_key, layer):
-    src_base, _ = tf.split(draw_key)
+def site_mask_keys(draw_key, layer, partitionable=True):
+    src_base, _ = tf.split(draw_key, partitionable=partitionable)
     return {s: tf.fold_in(tf.fold_in(src_base, KIND_INDEX[s]), layer) for s in SITES}
 
 
@@ -81,7 +81,7 @@ def grouped_T(lhs, rhs, sizes):
 
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                   bf16_storage=False):
+                   bf16_storage=False, partitionable=True):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. Returns dict(loss, recon, imp, grads, d_ci_pre,
     top_idx, r_final, rc_final)."""
@@ -118,7 +118,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         idx = tops[l]
         w = po.expert_mixing_weights(probs, idx)
         jobs = po.routed_jobs(idx, E)
-        keys = site_mask_keys(draw_key, l)
+        keys = site_mask_keys(draw_key, l, partitionable)
         xj = h2[jobs.sort_idx // k]
         S = {}
         for s in SITES:
@@ -126,7 +126,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             lo = po.lower_leaky(pre)
             up = po.upper_leaky(pre)
             imp += float(np.sum(up**p)) / T
-            ut = tf.uniform(keys[s], (T, k * c), "bfloat16").reshape(T, k, c)
+            ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
             m_tok = lo + (1.0 - lo) * ut
             S[s] = dict(pre=pre, lo=lo, up=up, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx])
         wj = w.reshape(-1)[jobs.sort_idx]

@@ -26,52 +26,85 @@ static constexpr int MOE_KIND_GATE = 11, MOE_KIND_UP = 12, MOE_KIND_DOWN = 13;  
 static constexpr int TILE = 64;
 
 // ---------------------------------------------------------------- layout kernels
-// dst[b][c][r] = src[b][r][c] for B matrices of [R, Cc] (64x64 tiles through LDS).
-__global__ __launch_bounds__(256) void k_batched_transpose(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
-                                                           bf16_t* __restrict__ dst) {
-  __shared__ bf16_t tile[TILE][TILE + 2];
-  const int64_t b = blockIdx.z;
-  const bf16_t* s = src + b * R * Cc;
-  bf16_t* d = dst + b * R * Cc;
-  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t r = r0 + i, c = c0 + tx;
-    tile[i][tx] = (r < R && c < Cc) ? s[r * Cc + c] : (bf16_t)0;
-  }
-  __syncthreads();
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t c = c0 + i, r = r0 + tx;
-    if (c < Cc && r < R) d[c * R + r] = tile[tx][i];
+// All job-space producers work on 64 (rows) x 64 (columns) tiles with 256 threads. A
+// thread moves 4 or 8 consecutive columns of a row with one 8- or 16-byte access; the
+// transposed copy goes through an LDS tile held transposed (tT[col][row], 144-byte rows)
+// so it leaves as 16-byte stores of 8 consecutive rows.
+struct TTile {
+  bf16_t v[TILE][TILE + 8];
+};
+
+// dst[(c0 + cc) * ld + r0 + rr ...] = tT[cc][rr ...]: rows r < nrows (nrows % 8 == 0),
+// columns c0 + cc < ncols.
+__device__ inline void ttile_store(const TTile& T, bf16_t* __restrict__ dst, int64_t ld, int64_t r0, int64_t nrows,
+                                   int64_t c0, int64_t ncols, int tid) {
+  const int cc = tid >> 2, rr = (tid & 3) * 16;
+  if (c0 + cc >= ncols) return;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r = r0 + rr + 8 * h;
+    if (r < nrows) *(uint4*)(dst + (c0 + cc) * ld + r) = *(const uint4*)&T.v[cc][rr + 8 * h];
   }
 }
 
-// Job-space gather on 64x64 tiles: out[j][i] = src[idx[j] / div][i] and/or its
-// job-contiguous copy outT[i][j].
+__device__ inline float bf_lo(uint32_t w) { return bf16_to_f32((bf16_t)(w & 0xFFFFu)); }
+__device__ inline float bf_hi(uint32_t w) { return bf16_to_f32((bf16_t)(w >> 16)); }
+__device__ inline uint32_t bf_pack(bf16_t a, bf16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
+
+// dst[b] = src[b]^T for B matrices of [R, Cc] (R, Cc multiples of 8).
+__global__ __launch_bounds__(256) void k_batched_transpose(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
+                                                           bf16_t* __restrict__ dst) {
+  __shared__ TTile T;
+  const int64_t b = blockIdx.z;
+  const bf16_t* s = src + b * R * Cc;
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const int tid = threadIdx.x, c8 = (tid & 7) * 8;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int r = (tid >> 3) + 32 * pass;
+    uint4 v = {0, 0, 0, 0};
+    if (r0 + r < R && c0 + c8 < Cc) v = *(const uint4*)(s + (r0 + r) * Cc + c0 + c8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      T.v[c8 + 2 * e][r] = (bf16_t)(w[e] & 0xFFFFu);
+      T.v[c8 + 2 * e + 1][r] = (bf16_t)(w[e] >> 16);
+    }
+  }
+  __syncthreads();
+  ttile_store(T, dst + b * R * Cc, R, r0, R, c0, Cc, tid);
+}
+
+// Job-space gather: out[j][:] = src[idx[j] / div][:] and/or its job-contiguous copy
+// outT[:][j] (w % 8 == 0, J % 8 == 0).
 __global__ __launch_bounds__(256) void k_gather_tile(const bf16_t* __restrict__ src, const int32_t* __restrict__ idx,
                                                      int div, int64_t J, int w, bf16_t* __restrict__ out,
                                                      bf16_t* __restrict__ outT) {
-  __shared__ bf16_t tile[TILE][TILE + 2];
+  __shared__ TTile T;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int c0 = blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t j = j0 + i;
-    const int c = c0 + tx;
-    bf16_t v = 0;
-    if (j < J && c < w) {
-      v = src[(int64_t)(idx[j] / div) * w + c];
-      if (out) out[j * w + c] = v;
+  const int tid = threadIdx.x, c8 = (tid & 7) * 8;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int r = (tid >> 3) + 32 * pass;
+    const int64_t j = j0 + r;
+    uint4 v = {0, 0, 0, 0};
+    if (j < J && c0 + c8 < w) {
+      v = *(const uint4*)(src + (int64_t)(idx[j] / div) * w + c0 + c8);
+      if (out) *(uint4*)(out + j * w + c0 + c8) = v;
     }
-    tile[i][tx] = v;
+    if (outT) {
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        T.v[c8 + 2 * e][r] = (bf16_t)(u[e] & 0xFFFFu);
+        T.v[c8 + 2 * e + 1][r] = (bf16_t)(u[e] >> 16);
+      }
+    }
   }
   if (!outT) return;
   __syncthreads();
-  for (int i = ty; i < TILE; i += 4) {
-    const int c = c0 + i;
-    const int64_t j = j0 + tx;
-    if (c < w && j < J) outT[(int64_t)c * J + j] = tile[tx][i];
-  }
+  ttile_store(T, outT, J, j0, J, c0, w, tid);
 }
 
 // ---------------------------------------------------------------- token-space kernels
@@ -168,47 +201,58 @@ struct SiteMaskArgs {
 __device__ inline float powp(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
 __device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f)); }
 
+// Thread -> (row (tid >> 4) + 16 * pass, columns q4 .. q4 + 3) of a 64x64 job-space tile.
+#define PD_TILE4_ROW(pass) ((threadIdx.x >> 4) + 16 * (pass))
+#define PD_TILE4_COL ((threadIdx.x & 15) * 4)
+
 // Forward mask: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at the job's
 // token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16); acts =
 // bf16(h * m) written as acts [J,c] and acts^T [c,J]; u stored as its 7-bit integer;
-// per-block partial of upper(ci)^p.
+// per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
+template <int LAYOUT>
 __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
                                                        uint8_t* __restrict__ ubits, float* __restrict__ imp_partial) {
-  __shared__ bf16_t tile[TILE][TILE + 2];
+  __shared__ TTile T;
   __shared__ float red[4];
+  const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
-  const int q0 = blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
   const int64_t n = a.J * a.c;
-  const int q = q0 + tx;
+  const bool qok = q0 + q4 < a.c;
   float imp = 0.f;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t j = j0 + i;
-    bf16_t out = 0;
-    if (j < a.J && q < a.c) {
-      const int64_t idx = j * a.c + q;
-      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
-      const float pre = bf16_to_f32(a.ci_pre[src]);
-      const float lo = lower_fwd(pre);
-      imp += powp(upper_fwd(pre), a.p);
-      const uint32_t kb = (draw_bits(a.k0, a.k1, src, n, 8, a.layout) & 0xFFu) >> 1;
-      ubits[idx] = (uint8_t)kb;
-      const float m = lo + (1.f - lo) * ((float)kb * (1.f / 128.f));
-      out = f32_to_bf16(bf16_to_f32(h[idx]) * m);
-      acts[idx] = out;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_TILE4_ROW(pass);
+    const int64_t j = j0 + r;
+    bf16_t o[4] = {0, 0, 0, 0};
+    if (j < a.J && qok) {
+      const int64_t idx = j * a.c + q0 + q4;
+      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q0 + q4;
+      const uint2 pw = *(const uint2*)(a.ci_pre + src);
+      const uint2 hw = *(const uint2*)(h + idx);
+      const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
+      const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
+      uint32_t ub = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lower_fwd(pre[e]);
+        imp += powp(upper_fwd(pre[e]), a.p);
+        const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
+        ub |= kb << (8 * e);
+        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * ((float)kb * (1.f / 128.f))));
+      }
+      *(uint32_t*)(ubits + idx) = ub;
+      *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     }
-    tile[i][tx] = out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
   imp = wave_sum(imp);
-  if (tx == 0) red[ty] = imp;
+  if ((tid & 63) == 0) red[tid >> 6] = imp;
   __syncthreads();
-  if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
-  for (int i = ty; i < TILE; i += 4) {
-    const int qq = q0 + i;
-    const int64_t j = j0 + tx;
-    if (qq < a.c && j < a.J) actsT[(int64_t)qq * a.J + j] = tile[tx][i];
-  }
+  if (tid == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  ttile_store(T, actsT, a.J, j0, a.J, q0, a.c, tid);
 }
 
 // Backward mask: d_h = bf16(d_acts * m) (in place over d_acts, plus d_h^T [c,J]) and the
@@ -218,70 +262,83 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
                                                        bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_hT,
                                                        bf16_t* __restrict__ d_pre) {
-  __shared__ bf16_t tile[TILE][TILE + 2];
+  __shared__ TTile T;
+  const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
-  const int q0 = blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int q = q0 + tx;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t j = j0 + i;
-    bf16_t out = 0;
-    if (j < a.J && q < a.c) {
-      const int64_t idx = j * a.c + q;
-      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q;
-      const float pre = bf16_to_f32(a.ci_pre[src]);
-      const float lo = lower_fwd(pre), up = upper_fwd(pre);
-      const float u = (float)ubits[idx] * (1.f / 128.f);
-      const float m = lo + (1.f - lo) * u;
-      const float da = bf16_to_f32(d_acts[idx]);
-      d_pre[src] = f32_to_bf16(lower_vjp(pre, da * bf16_to_f32(h[idx]) * (1.f - u)) +
-                               upper_vjp(pre, imp_scale * dpowp(up, a.p)));
-      out = f32_to_bf16(da * m);
-      d_acts[idx] = out;
+  const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
+  const bool qok = q0 + q4 < a.c;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_TILE4_ROW(pass);
+    const int64_t j = j0 + r;
+    bf16_t o[4] = {0, 0, 0, 0};
+    if (j < a.J && qok) {
+      const int64_t idx = j * a.c + q0 + q4;
+      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q0 + q4;
+      const uint2 pw = *(const uint2*)(a.ci_pre + src);
+      const uint2 hw = *(const uint2*)(h + idx);
+      const uint2 dw = *(const uint2*)(d_acts + idx);
+      const uint32_t ub = *(const uint32_t*)(ubits + idx);
+      const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
+      const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
+      const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
+      bf16_t dp[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
+        const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
+        const float m = lo + (1.f - lo) * u;
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
+                            upper_vjp(pre[e], imp_scale * dpowp(up, a.p)));
+        o[e] = f32_to_bf16(da[e] * m);
+      }
+      *(uint2*)(d_pre + src) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
+      *(uint2*)(d_acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     }
-    tile[i][tx] = out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
   __syncthreads();
-  for (int i = ty; i < TILE; i += 4) {
-    const int qq = q0 + i;
-    const int64_t j = j0 + tx;
-    if (qq < a.c && j < a.J) d_hT[(int64_t)qq * a.J + j] = tile[tx][i];
-  }
+  ttile_store(T, d_hT, a.J, j0, a.J, q0, a.c, tid);
 }
 
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
 // din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math) and its job-contiguous copy;
-// wt NULL = the frozen arm (no weight, no copy needed).
+// wt NULL = the frozen arm (no weight, no copy needed). f % 8 == 0.
 __global__ __launch_bounds__(256) void k_swiglu_fwd_tile(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
                                                          const float* __restrict__ wt,
                                                          const int32_t* __restrict__ sort_idx, int64_t J, int f,
                                                          bf16_t* __restrict__ din, bf16_t* __restrict__ dinT) {
-  __shared__ bf16_t tile[TILE][TILE + 2];
+  __shared__ TTile T;
+  const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
-  const int q0 = blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int q = q0 + tx;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t j = j0 + i;
-    bf16_t out = 0;
-    if (j < J && q < f) {
-      const int64_t idx = j * f + q;
-      const float gv = bf16_to_f32(g[idx]);
-      float v = gv * sigm(gv) * bf16_to_f32(u[idx]);
-      if (wt) v *= wt[sort_idx[j]];
-      out = f32_to_bf16(v);
-      din[idx] = out;
+  const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
+  const bool qok = q0 + q4 < f;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_TILE4_ROW(pass);
+    const int64_t j = j0 + r;
+    bf16_t o[4] = {0, 0, 0, 0};
+    if (j < J && qok) {
+      const int64_t idx = j * f + q0 + q4;
+      const uint2 gw = *(const uint2*)(g + idx);
+      const uint2 uw = *(const uint2*)(u + idx);
+      const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
+      const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
+      const float w = wt ? wt[sort_idx[j]] : 1.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(gv[e] * sigm(gv[e]) * uv[e] * w);
+      *(uint2*)(din + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     }
-    tile[i][tx] = out;
+    if (dinT) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
+    }
   }
   if (!dinT) return;
   __syncthreads();
-  for (int i = ty; i < TILE; i += 4) {
-    const int qq = q0 + i;
-    const int64_t j = j0 + tx;
-    if (qq < f && j < J) dinT[(int64_t)qq * J + j] = tile[tx][i];
-  }
+  ttile_store(T, dinT, J, j0, J, q0, f, tid);
 }
 
 // SwiGLU-fold backward on 64x64 tiles: d_g = bf16(d*u*w*silu'(g)), d_u = bf16(d*silu(g)*w)
@@ -294,44 +351,50 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
                                                          bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_gT,
                                                          bf16_t* __restrict__ d_u, bf16_t* __restrict__ d_uT,
                                                          float* __restrict__ d_w_part) {
-  __shared__ bf16_t tg[TILE][TILE + 2];
-  __shared__ bf16_t tu[TILE][TILE + 2];
+  __shared__ TTile Tg, Tu;
+  const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
-  const int q0 = blockIdx.x * TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int q = q0 + tx;
-  for (int i = ty; i < TILE; i += 4) {
-    const int64_t j = j0 + i;
-    bf16_t og = 0, ou = 0;
+  const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
+  const bool qok = q0 + q4 < f;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_TILE4_ROW(pass);
+    const int64_t j = j0 + r;
+    bf16_t og[4] = {0, 0, 0, 0}, ou[4] = {0, 0, 0, 0};
     float part = 0.f;
-    if (j < J) {
+    if (j < J && qok) {
+      const int64_t idx = j * f + q0 + q4;
       const float w = wt[sort_idx[j]];
-      if (q < f) {
-        const int64_t idx = j * f + q;
-        const float dv = bf16_to_f32(d_din[idx]), gv = bf16_to_f32(g[idx]), uv = bf16_to_f32(u[idx]);
-        const float sg = sigm(gv);
-        const float s = gv * sg;
-        og = f32_to_bf16(dv * uv * w * sg * (1.f + gv * (1.f - sg)));
-        ou = f32_to_bf16(dv * s * w);
-        d_g[idx] = og;
-        d_u[idx] = ou;
-        part = dv * s * uv;
+      const uint2 dw = *(const uint2*)(d_din + idx);
+      const uint2 gw = *(const uint2*)(g + idx);
+      const uint2 uw = *(const uint2*)(u + idx);
+      const float dv[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
+      const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
+      const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float sg = sigm(gv[e]);
+        const float s = gv[e] * sg;
+        og[e] = f32_to_bf16(dv[e] * uv[e] * w * sg * (1.f + gv[e] * (1.f - sg)));
+        ou[e] = f32_to_bf16(dv[e] * s * w);
+        part += dv[e] * s * uv[e];
       }
+      *(uint2*)(d_g + idx) = make_uint2(bf_pack(og[0], og[1]), bf_pack(og[2], og[3]));
+      *(uint2*)(d_u + idx) = make_uint2(bf_pack(ou[0], ou[1]), bf_pack(ou[2], ou[3]));
     }
-    part = wave_sum(part);  // one wave = one job row of this tile
-    if (tx == 0 && j < J) d_w_part[j * gridDim.x + blockIdx.x] = part;
-    tg[i][tx] = og;
-    tu[i][tx] = ou;
+    // the 16 lanes of one row sum their partials
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+    if ((tid & 15) == 0 && j < J) d_w_part[j * gridDim.x + blockIdx.x] = part;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Tg.v[q4 + e][r] = og[e];
+      Tu.v[q4 + e][r] = ou[e];
+    }
   }
   __syncthreads();
-  for (int i = ty; i < TILE; i += 4) {
-    const int qq = q0 + i;
-    const int64_t j = j0 + tx;
-    if (qq < f && j < J) {
-      d_gT[(int64_t)qq * J + j] = tg[tx][i];
-      d_uT[(int64_t)qq * J + j] = tu[tx][i];
-    }
-  }
+  ttile_store(Tg, d_gT, J, j0, J, q0, f, tid);
+  ttile_store(Tu, d_uT, J, j0, J, q0, f, tid);
 }
 
 // Token backward, one block (256 threads) per token:
@@ -606,6 +669,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   if (!x0 || !ln || !router || !Wg || !Wu || !Wd || !Vg || !Ug || !Vu || !Uu || !Vd || !Ud || !ci_pre || !losses ||
       !dVg || !dUg || !dVu || !dUu || !dVd || !dUd || !d_ci_pre)
     return fail(PD_EINVAL, "pd_moe_stack_step: null pointer");
+  if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
+    return fail(PD_EINVAL, "pd_moe_stack_step: unknown counter layout");
   const MoEDims D{T, T * k, d, f, E, k, c, L};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
     return fail(PD_EWORKSPACE, "pd_moe_stack_step: workspace too small");
@@ -727,8 +792,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.layout = layout;
       ma.p = p;
-      hipLaunchKernelGGL(k_mask_fwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], P.acts, S.actsT[si],
-                         S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
+      if (layout == PD_LAYOUT_PARTITIONABLE)
+        hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_PARTITIONABLE>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
+                           P.acts, S.actsT[si], S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
+      else
+        hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_ORIGINAL>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
+                           P.acts, S.actsT[si], S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
       rec.mark(MOE_CAT_GEMM_FWD);
       if ((rc = grouped_gemm(P.acts, UT[si] + l * szU[si], S.offsets, J, E, c, nout[si], 1, outs[si],
                                 PD_DTYPE_BF16, stream, false)))
