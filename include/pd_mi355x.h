@@ -161,6 +161,19 @@ int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64
                         float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes,
                         void* stream, void** events);
 
+/* ---- site routing samplers: pd/core/recon.py:218-252 (which sites take the decomposed
+ *      output at each position; AllRouting = no routes array). routes: uint8
+ *      [n_sites, n_positions], 1 = routed. ----
+ * UniformKRouting (:218-231): (k_key, perm_key) = split(key); k = randint(k_key, [N], 1,
+ * n_sites + 1) (randint splits k_key into high/low 32-bit draws, offset = (hi*2^32 + lo)
+ * mod n_sites); routes[j] = argsort(uniform_f32(perm_key, [n_sites, N]), axis 0, stable)[j]
+ * < k. n_sites <= 64. */
+int pd_route_uniform_k(uint32_t key0, uint32_t key1, int64_t n_positions, int n_sites, int layout, uint8_t* routes,
+                       void* stream);
+/* StaticProbabilityRouting (:233-244): routes[j] = uniform_f32(fold_in(key, j), [N]) < p. */
+int pd_route_static_p(uint32_t key0, uint32_t key1, int64_t n_positions, int n_sites, float p, int layout,
+                      uint8_t* routes, void* stream);
+
 /* ---- MoE routing: pd/targets/qwen36_moe.py:473-514 (router softmax, select_experts
  *      stable-descending lowest-index ties, expert_mixing_weights renormalized). ----
  * logits [T,E] fp32 -> probs [T,E] fp32 (nullable), top_idx [T,k] int32,

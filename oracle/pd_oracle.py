@@ -427,3 +427,26 @@ def routed_decomposed_site(x_jobs, V, U, group_sizes, mask_jobs, delta_jobs=None
     if delta_jobs is not None:
         out = out + delta_jobs[:, None] * grouped_matmul(x_jobs, frozen, group_sizes)
     return out, h
+
+
+# ---------------------------------------------------------------- routing samplers
+def uniform_k_routing(key, n_sites: int, leading_shape, *, partitionable: bool = True) -> np.ndarray:
+    """`UniformKRouting.__call__` (`param_decomp/param_decomp/core/recon.py:218-231`):
+    `k_key, perm_key = split(key)`; `k = randint(k_key, shape, 1, n_sites + 1)`;
+    `perms = argsort(uniform(perm_key, (n_sites, *shape)), axis=0)` (stable);
+    `routed[j] = perms[j] < k`. Returns bool `[n_sites, *shape]`."""
+    k_key, perm_key = threefry.split(key, partitionable=partitionable)
+    shape = tuple(int(s) for s in leading_shape)
+    k = threefry.randint(k_key, shape, 1, n_sites + 1, partitionable=partitionable)
+    u = threefry.uniform(perm_key, (n_sites, *shape), "float32", partitionable=partitionable)
+    perms = np.argsort(u, axis=0, kind="stable")
+    return perms < k[None]
+
+
+def static_probability_routing(key, n_sites: int, p: float, leading_shape, *, partitionable: bool = True) -> np.ndarray:
+    """`StaticProbabilityRouting.__call__` (`core/recon.py:233-244`):
+    `routed[j] = bernoulli(fold_in(key, j), p, shape)` = `uniform_f32 < float32(p)`."""
+    shape = tuple(int(s) for s in leading_shape)
+    p32 = float(np.float32(p))
+    return np.stack([threefry.uniform(threefry.fold_in(key, j), shape, "float32", partitionable=partitionable) < p32
+                     for j in range(n_sites)])

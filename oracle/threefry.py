@@ -136,3 +136,21 @@ def uniform(key: tuple[int, int], shape, dtype: str = "float32", *, partitionabl
     """`jax.random.uniform(key, shape, dtype)` on [0, 1), as exact float64 values."""
     nbits = {"float32": 32, "bfloat16": 8}[dtype]
     return uniform_bits_to_float(random_bits(key, nbits, shape, partitionable=partitionable), dtype)
+
+
+def randint(key: tuple[int, int], shape, minval: int, maxval: int, *, partitionable: bool = True) -> np.ndarray:
+    """`jax.random.randint(key, shape, minval, maxval)` for int32 (JAX's `_randint`):
+    `k1, k2 = split(key)`; 32 high and 32 low random bits from `k1` and `k2`; with
+    `span = maxval - minval` (1 when maxval <= minval) the offset is
+    `((hi % span) * m + lo % span) % span`, `m = (2^16 % span)^2 % span`, i.e. the
+    64-bit value `hi * 2^32 + lo` reduced mod span in 32-bit arithmetic.
+
+    The key/bit assignment follows the published JAX source; no golden vector exists
+    for it here (parity unpinned beyond the modular identity and range checks)."""
+    k1, k2 = split(key, partitionable=partitionable)
+    hi = random_bits(k1, 32, shape, partitionable=partitionable).astype(np.uint64)
+    lo = random_bits(k2, 32, shape, partitionable=partitionable).astype(np.uint64)
+    span = np.uint64(maxval - minval if maxval > minval else 1)
+    mult = (np.uint64(65536) % span) * (np.uint64(65536) % span) % span
+    off = ((hi % span) * mult + lo % span) % span
+    return (np.int64(minval) + off.astype(np.int64)).astype(np.int32)

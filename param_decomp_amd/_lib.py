@@ -51,6 +51,8 @@ _SIGNATURES = {
                       [_c_i32] * 3 + [_c_f32] * 3 + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),
     "pd_dense_step_timed": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 8 + [_c_u32] * 4 +
                             [_c_i32] * 3 + [_c_f32] * 3 + [_c_p] * 7 + [_c_p, _c_sz, _c_p, _c_p]),
+    "pd_route_uniform_k": (_c_i32, [_c_u32, _c_u32, _c_i64, _c_i32, _c_i32, _c_p, _c_p]),
+    "pd_route_static_p": (_c_i32, [_c_u32, _c_u32, _c_i64, _c_i32, _c_f32, _c_i32, _c_p, _c_p]),
     "pd_router_topk": (_c_i32, [_c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
     "pd_routed_jobs_workspace_size": (_c_sz, [_c_i64, _c_i32]),
     "pd_routed_jobs": (_c_i32, [_c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p]),

@@ -198,4 +198,21 @@ __device__ inline float wave_max(float v) {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// jax.random.split(key, 2) on the host: out = {key0.x0, key0.x1, key1.x0, key1.x1}.
+// partitionable: key i = block(key, (0, i)); original: the block outputs of the counter
+// pairs (0, 2) and (1, 3), concatenated word-wise and read as [2, 2].
+inline void split2(uint32_t k0, uint32_t k1, int layout, uint32_t out[4]) {
+  if (layout == PD_LAYOUT_PARTITIONABLE) {
+    uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 1;
+    threefry2x32(k0, k1, a0, a1);
+    threefry2x32(k0, k1, b0, b1);
+    out[0] = a0, out[1] = a1, out[2] = b0, out[3] = b1;
+  } else {
+    uint32_t a0 = 0, a1 = 2, b0 = 1, b1 = 3;
+    threefry2x32(k0, k1, a0, a1);
+    threefry2x32(k0, k1, b0, b1);
+    out[0] = a0, out[1] = b0, out[2] = a1, out[3] = b1;
+  }
+}
+
 }  // namespace pd

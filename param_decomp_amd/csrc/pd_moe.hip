@@ -684,18 +684,9 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   auto bf = [](const void* base, size_t off) { return (const bf16_t*)base + off; };
   int rc;
   // ---- site keys: src_base = split(draw_key)[0]; key(kind, layer) = fold_in(fold_in(src_base, kind), layer)
-  // partitionable split: subkey 0 = block(key, (0, 0)); original split of 2 keys:
-  // subkey 0 = (block(key, (0, 2)).x0, block(key, (1, 3)).x0).
-  uint32_t sb0 = 0, sb1 = 0;
-  if (layout == PD_LAYOUT_PARTITIONABLE) {
-    threefry2x32(draw_k0, draw_k1, sb0, sb1);
-  } else {
-    uint32_t a0 = 0, a1 = 2, b0 = 1, b1 = 3;
-    threefry2x32(draw_k0, draw_k1, a0, a1);
-    threefry2x32(draw_k0, draw_k1, b0, b1);
-    sb0 = a0;
-    sb1 = b0;
-  }
+  uint32_t halves[4];
+  split2(draw_k0, draw_k1, layout, halves);
+  const uint32_t sb0 = halves[0], sb1 = halves[1];
   auto site_key = [&](int kind, int layer, uint32_t& o0, uint32_t& o1) {
     uint32_t x0_ = 0, x1_ = (uint32_t)kind;
     threefry2x32(sb0, sb1, x0_, x1_);

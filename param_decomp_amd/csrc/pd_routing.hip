@@ -5,6 +5,8 @@
 //   pd_routed_jobs      stable argsort by expert, inverse, bincount
 //                       (pd/routed/experts.py:115-123) as a three-phase counting sort
 //   pd_gather_rows(_vjp), pd_combine_jobs   (pd/routed/experts.py:127-206, 351-359)
+#include <algorithm>
+
 #include "pd_common.hpp"
 
 namespace pd {
@@ -179,6 +181,51 @@ __global__ void k_combine(const T* __restrict__ y, int64_t width, const int32_t*
   }
 }
 
+// ---- routing samplers (which sites take the decomposed output at each position)
+constexpr int ROUTE_MAX_SITES = 64, ROUTE_BLOCK = 128;
+
+// Uniform-k subset: k = 1 + randint offset from 32 high bits (key hk) and 32 low bits
+// (key lk), the 64-bit value reduced mod n_sites in 32-bit steps; u[j] = fp32 uniform of
+// element j*N + pos of an [S, N] draw (key pk); routes[rank(j)][pos] = (j < k), with
+// rank(j) = j's place in the stable ascending order of u[:, pos].
+template <int LAYOUT>
+__global__ __launch_bounds__(ROUTE_BLOCK) void k_route_uniform_k(uint32_t hk0, uint32_t hk1, uint32_t lk0,
+                                                                 uint32_t lk1, uint32_t pk0, uint32_t pk1, int64_t N,
+                                                                 int S, uint8_t* __restrict__ routes) {
+  __shared__ float u[ROUTE_MAX_SITES][ROUTE_BLOCK];
+  const int64_t pos = (int64_t)blockIdx.x * ROUTE_BLOCK + threadIdx.x;
+  if (pos >= N) return;  // each thread only touches its own LDS column
+  const uint32_t span = (uint32_t)S;
+  const uint32_t hb = draw_bits(hk0, hk1, pos, N, 32, LAYOUT);
+  const uint32_t lb = draw_bits(lk0, lk1, pos, N, 32, LAYOUT);
+  const uint32_t m = ((65536u % span) * (65536u % span)) % span;
+  const uint32_t k = 1u + ((hb % span) * m + lb % span) % span;
+  for (int j = 0; j < S; ++j)
+    u[j][threadIdx.x] =
+        bits_to_uniform(draw_bits(pk0, pk1, (int64_t)j * N + pos, (int64_t)S * N, 32, LAYOUT), PD_DTYPE_F32);
+  for (int j = 0; j < S; ++j) {
+    const float uj = u[j][threadIdx.x];
+    int rank = 0;
+    for (int t = 0; t < S; ++t) {
+      const float ut = u[t][threadIdx.x];
+      rank += (ut < uj) || (ut == uj && t < j);
+    }
+    routes[(int64_t)rank * N + pos] = (uint8_t)((uint32_t)j < k);
+  }
+}
+
+// Static probability: routes[j][pos] = (fp32 uniform of fold_in(key, j) at pos) < p.
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void k_route_static_p(uint32_t k0, uint32_t k1, int64_t N, float p,
+                                                        uint8_t* __restrict__ routes) {
+  const int j = blockIdx.y;
+  uint32_t f0 = 0, f1 = (uint32_t)j;
+  threefry2x32(k0, k1, f0, f1);
+  for (int64_t pos = (int64_t)blockIdx.x * 256 + threadIdx.x; pos < N; pos += (int64_t)gridDim.x * 256)
+    routes[(int64_t)j * N + pos] =
+        (uint8_t)(bits_to_uniform(draw_bits(f0, f1, pos, N, 32, LAYOUT), PD_DTYPE_F32) < p);
+}
+
 }  // namespace pd
 
 using namespace pd;
@@ -257,6 +304,45 @@ int pd_combine_jobs(const void* y, int dtype, int64_t width, const int32_t* inv,
 int pd_gather_rows_vjp(const void* grad, int dtype, int64_t width, const int32_t* inv, int64_t T, int k, void* out,
                        void* stream) {
   return pd_combine_jobs(grad, dtype, width, inv, nullptr, T, k, out, stream);
+}
+
+
+int pd_route_uniform_k(uint32_t key0, uint32_t key1, int64_t n_positions, int n_sites, int layout, uint8_t* routes,
+                       void* stream) {
+  if (n_positions < 0 || n_sites < 1 || n_sites > ROUTE_MAX_SITES || !routes)
+    return fail(PD_EINVAL, "pd_route_uniform_k: need 1 <= n_sites <= 64 and an output");
+  if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
+    return fail(PD_EINVAL, "pd_route_uniform_k: unknown counter layout");
+  if (n_positions == 0) return PD_OK;
+  if (cdiv(n_positions, ROUTE_BLOCK) > 0x7FFFFFFF) return fail(PD_EUNSUPPORTED, "pd_route_uniform_k: too large");
+  uint32_t kp[4], hl[4];
+  split2(key0, key1, layout, kp);     // (k_key, perm_key)
+  split2(kp[0], kp[1], layout, hl);   // randint's (high-bits key, low-bits key)
+  const dim3 grid((unsigned)cdiv(n_positions, ROUTE_BLOCK));
+  if (layout == PD_LAYOUT_PARTITIONABLE)
+    hipLaunchKernelGGL(k_route_uniform_k<PD_LAYOUT_PARTITIONABLE>, grid, dim3(ROUTE_BLOCK), 0, (hipStream_t)stream,
+                       hl[0], hl[1], hl[2], hl[3], kp[2], kp[3], n_positions, n_sites, routes);
+  else
+    hipLaunchKernelGGL(k_route_uniform_k<PD_LAYOUT_ORIGINAL>, grid, dim3(ROUTE_BLOCK), 0, (hipStream_t)stream, hl[0],
+                       hl[1], hl[2], hl[3], kp[2], kp[3], n_positions, n_sites, routes);
+  return check_launch("pd_route_uniform_k");
+}
+
+int pd_route_static_p(uint32_t key0, uint32_t key1, int64_t n_positions, int n_sites, float p, int layout,
+                      uint8_t* routes, void* stream) {
+  if (n_positions < 0 || n_sites < 1 || n_sites > 65535 || !routes)
+    return fail(PD_EINVAL, "pd_route_static_p: need 1 <= n_sites <= 65535 and an output");
+  if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
+    return fail(PD_EINVAL, "pd_route_static_p: unknown counter layout");
+  if (n_positions == 0) return PD_OK;
+  const dim3 grid((unsigned)std::min<int64_t>(cdiv(n_positions, 256), 4096), (unsigned)n_sites);
+  if (layout == PD_LAYOUT_PARTITIONABLE)
+    hipLaunchKernelGGL(k_route_static_p<PD_LAYOUT_PARTITIONABLE>, grid, dim3(256), 0, (hipStream_t)stream, key0,
+                       key1, n_positions, p, routes);
+  else
+    hipLaunchKernelGGL(k_route_static_p<PD_LAYOUT_ORIGINAL>, grid, dim3(256), 0, (hipStream_t)stream, key0, key1,
+                       n_positions, p, routes);
+  return check_launch("pd_route_static_p");
 }
 
 }  // extern "C"

@@ -125,6 +125,18 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, trans_a=False, trans_b=False, out:
     return out
 
 
+def route_uniform_k(key: Key, n_sites: int, n_positions: int, device, layout: int = L.LAYOUT_PARTITIONABLE):
+    routes = torch.empty((n_sites, n_positions), dtype=torch.uint8, device=device)
+    L.call("pd_route_uniform_k", key[0], key[1], n_positions, n_sites, layout, L.ptr(routes), L.stream())
+    return routes
+
+
+def route_static_p(key: Key, n_sites: int, p: float, n_positions: int, device, layout: int = L.LAYOUT_PARTITIONABLE):
+    routes = torch.empty((n_sites, n_positions), dtype=torch.uint8, device=device)
+    L.call("pd_route_static_p", key[0], key[1], n_positions, n_sites, p, layout, L.ptr(routes), L.stream())
+    return routes
+
+
 def router_topk(logits: torch.Tensor, k: int):
     T, E = logits.shape
     probs = torch.empty_like(logits)

@@ -1,0 +1,192 @@
+"""Toy targets (TMS, ResidMLP) and their decomposition step on the GPU.
+
+Mirrors the reference's toy targets:
+- TMS (`param_decomp/param_decomp/targets/tms.py`): `clean_output` (`:254-258`),
+  `site_inputs` (`:261-271`), the masked forward `_run_masked` (`:311-359`:
+  `linear1` -> `linear2` + b2 -> ReLU, every site decomposed), `tms_mse` (`:380-388`),
+  the tied untrained target (`:569-581`) and `sample_sparse_features` (`:584-609`).
+- ResidMLP (`targets/resid_mlp.py`): `clean_output` / `site_inputs` (`:266-333`), the
+  masked forward (`:336-390`: `resid += mlp_out(act(mlp_in(resid)))`, `out = resid @
+  W_U`), `resid_mlp_mse` (`:411-418`), Kaiming-uniform blocks and the fixed unit-norm
+  embedding (`:596-628`), `sample_sparse_features` (`:643-662`).
+
+`ToyDecompositionStep.step` is one fwd+bwd of the stochastic-recon + importance-minimality
+objective (`core/train.py:1182-1258`): clean forward, per-site CI from the gate MLP on
+`clean_input @ V`, masks drawn from `split(draw_key)` -> `fold_in(., site_idx)`
+(`core/masking.py:148-167`), masked forward through `site_forward`, MSE recon, p-norm
+imp-min summed over sites, gradients left on V, U and the gate parameters. Every
+product, gate, squashing, mask and loss runs in the HIP library (fp32 kernels); ReLU,
+bias and residual adds are the only torch elementwise ops.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from param_decomp_amd import losses, masking, ops, prng
+from param_decomp_amd.ci_fn import ComponentGateMLP
+from param_decomp_amd.decomposed_linear import SiteWeights, site_out
+from param_decomp_amd.prng import Key
+from param_decomp_amd.squashing import lower_leaky_hard_sigmoid, upper_leaky_hard_sigmoid
+
+
+class _Product(torch.autograd.Function):
+    """`a @ b` through the HIP GEMM (fp32 or bf16), differentiable in both operands."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return ops.gemm(a.contiguous(), b.contiguous())
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        g = g.contiguous()
+        da = ops.gemm(g, b.contiguous(), trans_b=True) if ctx.needs_input_grad[0] else None
+        db = ops.gemm(a.contiguous(), g, trans_a=True) if ctx.needs_input_grad[1] else None
+        return da, db
+
+
+def product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return _Product.apply(a, b)
+
+
+@dataclass
+class ToySite:
+    """One decomposed site: frozen `W [d_out, d_in]`, trainable `V [d_in, C]`, `U [C, d_out]`
+    and the per-component gate."""
+
+    name: str
+    W: torch.Tensor
+    V: torch.Tensor
+    U: torch.Tensor
+    gate: ComponentGateMLP
+
+    def parameters(self):
+        return [self.V, self.U, *self.gate.parameters()]
+
+
+@dataclass
+class TMSTarget:
+    W1: torch.Tensor  # [n_hidden, n_features]; linear2's weight is W1^T (tied)
+    b2: torch.Tensor  # [n_features]
+
+
+@dataclass
+class ResidMLPTarget:
+    W_E: torch.Tensor  # [n_features, d_embed]
+    W_U: torch.Tensor  # [d_embed, n_features]
+    b_in: list = field(default_factory=list)  # per layer, None = no bias
+    b_out: list = field(default_factory=list)
+
+
+def make_site(name: str, W: torch.Tensor, C: int, *, generator=None) -> ToySite:
+    """V ~ N(0, 1/d_in), U ~ N(0, 1/C) (`core/components.py:650-677`)."""
+    d_out, d_in = W.shape
+    dev = W.device
+    V = (torch.randn(d_in, C, device=dev, generator=generator) / math.sqrt(d_in)).requires_grad_(True)
+    U = (torch.randn(C, d_out, device=dev, generator=generator) / math.sqrt(C)).requires_grad_(True)
+    return ToySite(name, W, V, U, ComponentGateMLP(C, device=dev, generator=generator))
+
+
+def init_tms(n_features: int = 5, n_hidden: int = 2, C: int = 20, *, device="cuda", generator=None):
+    """Untrained tied TMS target with zero bias (`tms.py:569-581`) and sites linear1, linear2."""
+    b = 1.0 / math.sqrt(n_features)
+    W1 = (torch.rand(n_hidden, n_features, device=device, generator=generator) * 2 - 1) * b
+    target = TMSTarget(W1, torch.zeros(n_features, device=device))
+    return target, [make_site("linear1", W1, C, generator=generator),
+                    make_site("linear2", W1.t().contiguous(), C, generator=generator)]
+
+
+def init_resid_mlp(n_features: int = 100, d_embed: int = 1000, d_mlp: int = 50, n_layers: int = 1, C: int = 100, *,
+                   device="cuda", generator=None):
+    """Fixed random unit-norm embedding (`W_U = W_E^T`) and Kaiming-uniform bias-free
+    blocks (`resid_mlp.py:596-628`); sites `layers.{i}.mlp_in`, `layers.{i}.mlp_out`."""
+    raw = torch.randn(n_features, d_embed, device=device, generator=generator)
+    W_E = raw / raw.norm(dim=-1, keepdim=True)
+    target = ResidMLPTarget(W_E, W_E.t().contiguous(), [None] * n_layers, [None] * n_layers)
+    sites = []
+    for i in range(n_layers):
+        bi, bo = 1.0 / math.sqrt(d_embed), 1.0 / math.sqrt(d_mlp)
+        W_in = (torch.rand(d_mlp, d_embed, device=device, generator=generator) * 2 - 1) * bi
+        W_out = (torch.rand(d_embed, d_mlp, device=device, generator=generator) * 2 - 1) * bo
+        sites += [make_site(f"layers.{i}.mlp_in", W_in, C, generator=generator),
+                  make_site(f"layers.{i}.mlp_out", W_out, C, generator=generator)]
+    return target, sites
+
+
+def sparse_features(batch: int, n_features: int, p: float, low: float, *, device="cuda", generator=None):
+    """`at_least_zero_active` batches: U(low, 1) values gated by U(0,1) < p (TMS low=0,
+    ResidMLP low=-1)."""
+    v = torch.rand(batch, n_features, device=device, generator=generator) * (1.0 - low) + low
+    return v * (torch.rand(batch, n_features, device=device, generator=generator) < p)
+
+
+def _bias(a, b):
+    return a if b is None else a + b
+
+
+@torch.no_grad()
+def clean_forward(target, sites, x):
+    """The all-frozen forward and each site's clean input."""
+    if isinstance(target, TMSTarget):
+        hidden = ops.gemm(x, sites[0].W, trans_b=True)
+        return torch.relu(ops.gemm(hidden, sites[1].W, trans_b=True) + target.b2), [x, hidden]
+    r = ops.gemm(x, target.W_E)
+    inputs = []
+    for i in range(len(sites) // 2):
+        hid = torch.relu(_bias(ops.gemm(r, sites[2 * i].W, trans_b=True), target.b_in[i]))
+        inputs += [r, hid]
+        r = r + _bias(ops.gemm(hid, sites[2 * i + 1].W, trans_b=True), target.b_out[i])
+    return ops.gemm(r, target.W_U), inputs
+
+
+def masked_forward(target, sites, x, masks, deltas=None, routes=None):
+    """The masked forward with every site decomposed (`tms.py:311-359`;
+    `resid_mlp.py:336-390`)."""
+    def site(i, a):
+        s = sites[i]
+        return site_out(a, SiteWeights(s.W, s.V, s.U), masks[i], None if deltas is None else deltas[i],
+                        None if routes is None else routes[i])
+
+    if isinstance(target, TMSTarget):
+        return torch.relu(site(1, site(0, x)) + target.b2)
+    r = ops.gemm(x, target.W_E)
+    for i in range(len(sites) // 2):
+        hid = torch.relu(_bias(site(2 * i, r), target.b_in[i]))
+        r = r + _bias(site(2 * i + 1, hid), target.b_out[i])
+    return product(r, target.W_U)
+
+
+class ToyDecompositionStep:
+    """One fwd+bwd of the toy decomposition objective; gradients accumulate into `.grad`
+    of each site's V, U and gate parameters (zeroed at the start of every step)."""
+
+    def __init__(self, target, sites, *, p: float = 1.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
+                 use_delta: bool = False):
+        self.target, self.sites = target, sites
+        self.p, self.imp_coeff, self.recon_coeff, self.use_delta = p, imp_coeff, recon_coeff, use_delta
+
+    def step(self, x: torch.Tensor, draw_key: Key, routes=None) -> dict:
+        for s in self.sites:
+            for prm in s.parameters():
+                prm.grad = None
+        clean, cin = clean_forward(self.target, self.sites, x)
+        g = [s.gate(product(cin[i], s.V)) for i, s in enumerate(self.sites)]
+        lower = [lower_leaky_hard_sigmoid(a) for a in g]
+        upper = {s.name: upper_leaky_hard_sigmoid(a) for s, a in zip(self.sites, g)}
+        mask_key, delta_key = prng.split(draw_key)
+        masks = [masking.sample_component_mask(lo, prng.fold_in(mask_key, i)) for i, lo in enumerate(lower)]
+        deltas = None
+        if self.use_delta:
+            deltas = [masking.sample_delta_mask(lo, prng.fold_in(delta_key, i)) for i, lo in enumerate(lower)]
+        out = masked_forward(self.target, self.sites, x, masks, deltas, routes)
+        recon = losses.mse(out, clean)
+        imp = losses.importance_minimality_pnorm(upper, self.p)
+        loss = self.recon_coeff * recon + self.imp_coeff * imp
+        loss.backward()
+        return {"loss": loss.detach(), "recon": recon.detach(), "imp": imp.detach(), "out": out.detach(),
+                "clean": clean, "g_raw": [a.detach() for a in g]}

@@ -377,6 +377,34 @@ def test_router_topk_bit_exact_indices(device):
     np.testing.assert_allclose(w.cpu().numpy(), po.expert_mixing_weights(p_or, want_idx), rtol=1e-5)
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("S,n", [(7, 1000), (24, 4096), (1, 5), (64, 300), (12, 8192)])
+def test_route_uniform_k_bit_exact(device, layout, S, n):
+    from param_decomp_amd.routing import UniformKRouting
+
+    key = (5, 77 + S)
+    sites = tuple(f"s{j}" for j in range(S))
+    got = UniformKRouting(sites, device, layout)(key, (n,))
+    want = po.uniform_k_routing(key, S, (n,), partitionable=layout == 0)
+    for j, name in enumerate(sites):
+        assert got[name].dtype == torch.bool
+        np.testing.assert_array_equal(got[name].cpu().numpy(), want[j], err_msg=name)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("p", [0.0, 0.3, 0.5, 1.0])
+def test_route_static_p_bit_exact(device, layout, p):
+    from param_decomp_amd.routing import AllRouting, StaticProbabilityRouting
+
+    key = (9, 31)
+    sites = ("a", "b", "c")
+    got = StaticProbabilityRouting(sites, p, device, layout)(key, (3, 700))
+    want = po.static_probability_routing(key, 3, p, (3, 700), partitionable=layout == 0)
+    for j, name in enumerate(sites):
+        np.testing.assert_array_equal(got[name].cpu().numpy(), want[j])
+    assert AllRouting()(key, (3, 700)) is None
+
+
 @pytest.mark.parametrize("T,k,E", [(24, 2, 8), (8192, 8, 42), (1000, 3, 5), (7, 1, 64), (3001, 5, 1000)])
 def test_routed_jobs_bit_exact(device, T, k, E):
     from param_decomp_amd.routed.experts import routed_jobs

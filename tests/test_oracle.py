@@ -460,3 +460,63 @@ def test_gather_tokens_vjp_is_the_adjoint():
     y = rng.normal(size=(T_R * K, 3))
     np.testing.assert_allclose(po.sum_jobs(y, jobs), np.stack(
         [sum(y[np.where(jobs.sort_idx == t * K + s)[0][0]] for s in range(K)) for t in range(T_R)]))
+
+
+# ---------------------------------------------------------------- routing samplers
+@pytest.mark.parametrize("partitionable", [True, False])
+@pytest.mark.parametrize("minval,maxval", [(1, 2), (1, 8), (0, 25), (3, 68), (5, 5), (7, 2)])
+def test_randint_is_the_64_bit_value_mod_span(partitionable, minval, maxval):
+    """randint's 32-bit remainder steps equal (hi * 2^32 + lo) mod span computed with
+    exact integers; span 1 (maxval <= minval) returns minval."""
+    key = (7, 1234)
+    n = 4000
+    k1, k2 = tf.split(key, partitionable=partitionable)
+    hi = tf.random_bits(k1, 32, (n,), partitionable=partitionable)
+    lo = tf.random_bits(k2, 32, (n,), partitionable=partitionable)
+    span = maxval - minval if maxval > minval else 1
+    want = np.array([minval + ((int(h) << 32) + int(l)) % span for h, l in zip(hi, lo)], dtype=np.int64)
+    got = tf.randint(key, (n,), minval, maxval, partitionable=partitionable)
+    assert got.dtype == np.int32
+    np.testing.assert_array_equal(got.astype(np.int64), want)
+
+
+@pytest.mark.parametrize("partitionable", [True, False])
+def test_uniform_k_routing_subset_sizes_and_uniformity(partitionable):
+    """Each position routes exactly k sites, k = randint(1, S + 1) from the first split
+    key; k is uniform over 1..S (chi-square) and each site is routed with probability
+    (S + 1) / (2 S)."""
+    S, n = 6, 30000
+    key = (0, 99)
+    routes = po.uniform_k_routing(key, S, (n,), partitionable=partitionable)
+    k_key, _ = tf.split(key, partitionable=partitionable)
+    k = tf.randint(k_key, (n,), 1, S + 1, partitionable=partitionable)
+    np.testing.assert_array_equal(routes.sum(axis=0), k)
+    counts = np.bincount(k, minlength=S + 1)[1:]
+    chi2 = float(np.sum((counts - n / S) ** 2 / (n / S)))
+    assert chi2 < 25.0  # 5 dof; p ~ 1e-4
+    np.testing.assert_allclose(routes.mean(axis=1), (S + 1) / (2 * S), atol=0.02)
+
+
+def test_uniform_k_routing_brute_force_small():
+    """S = 3 by hand: routed[j] = (index of the j-th smallest u) < k, stable on ties."""
+    key = (3, 4)
+    S, n = 3, 50
+    k_key, perm_key = tf.split(key)
+    k = tf.randint(k_key, (n,), 1, S + 1)
+    u = tf.uniform(perm_key, (S, n), "float32")
+    routes = po.uniform_k_routing(key, S, (n,))
+    for pos in range(n):
+        order = sorted(range(S), key=lambda s: (u[s, pos], s))
+        for j in range(S):
+            assert bool(routes[j, pos]) == (order[j] < k[pos])
+
+
+def test_static_probability_routing_limits_and_rate():
+    key = (1, 2)
+    n = 20000
+    assert not po.static_probability_routing(key, 3, 0.0, (n,)).any()
+    assert po.static_probability_routing(key, 3, 1.0, (n,)).all()
+    r = po.static_probability_routing(key, 4, 0.3, (n,))
+    np.testing.assert_allclose(r.mean(axis=1), 0.3, atol=0.015)
+    u1 = tf.uniform(tf.fold_in(key, 1), (n,), "float32")
+    np.testing.assert_array_equal(r[1], u1 < np.float32(0.3))
