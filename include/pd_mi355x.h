@@ -45,6 +45,9 @@ extern "C" {
 #define PD_IMPMIN_PNORM 0     /* (upper+eps)^p, paper / nano_param_decomp/run.py:413-429 */
 #define PD_IMPMIN_SMOOTH_L0 1 /* c^2/(c^2+gamma^2), pd/core/losses.py:388-394 */
 
+#define PD_BLOCK_FUSED_OUTPUT 0 /* BlockContraction "fused_output", pd/core/linear_plan.py:134-146 */
+#define PD_BLOCK_FUSED_INPUT 1  /* BlockContraction "fused_input" */
+
 const char* pd_last_error(void);
 int pd_abi_version(void);
 
@@ -103,6 +106,21 @@ int pd_mse(const void* a, const void* b, int dtype, int64_t n, float coeff, floa
 size_t pd_kl_workspace_size(int64_t rows);
 int pd_kl(const void* masked_logits, const void* clean_logits, int dtype, int64_t rows, int64_t vocab, float coeff,
           float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream);
+/* Streamed-vocab KL (pd/targets/losses.py:101-170 streamed_position_kl): per-position
+ * KL(softmax(act_clean @ head_clean^T) || softmax(act_masked @ head_masked^T)) streamed over
+ * n_chunks equal vocab chunks (V % n_chunks == 0) with the paired online-softmax
+ * accumulators; the logits never materialize. act [N,d], head [V,d] in `dtype` (bf16:
+ * d and V/n_chunks multiples of 8). fwd writes position_kl [N] and stats [N,5] =
+ * (m_p, s_p, a, m_q, s_q); bwd writes d_act_masked [N,d] fp32 = sum_v (q - p) g[n]
+ * head_masked[v] for the per-position cotangent g (the clean side is the target). */
+size_t pd_streamed_kl_workspace_size(int dtype, int64_t N, int64_t V, int n_chunks);
+int pd_streamed_kl_fwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks, const void* act_masked,
+                       const void* head_masked, const void* act_clean, const void* head_clean, float* position_kl,
+                       float* stats, void* workspace, size_t workspace_bytes, void* stream);
+int pd_streamed_kl_bwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks, const void* act_masked,
+                       const void* head_masked, const void* act_clean, const void* head_clean, const float* stats,
+                       const float* g_position, float* d_act_masked, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* ---- GEMM: C[M,N] = alpha * op(A) @ op(B) + beta * C, fp32 accumulation.
  *      dtype PD_DTYPE_BF16 runs bf16 MFMA (A/B bf16; C bf16 or fp32 via c_dtype);
@@ -111,6 +129,13 @@ int pd_kl(const void* masked_logits, const void* clean_logits, int dtype, int64_
  *      site_forward (pd/core/decomposed_linear.py:142-175). ---- */
 int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B,
             int64_t ldb, int trans_b, void* C, int64_t ldc, int c_dtype, float alpha, float beta, void* stream);
+/* Strided-batched pd_gemm: C[z] = alpha op(A[z]) op(B[z]) + beta C[z] for z < batch, each
+ * operand at base + z * stride (stride 0 = shared). The per-block einsums of the
+ * block-factored linears (pd/core/linear_plan.py:149-160). bf16: strides % 8 == 0. */
+int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                            int64_t stride_a, int trans_a, const void* B, int64_t ldb, int64_t stride_b, int trans_b,
+                            void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
+                            void* stream);
 
 /* ---- masked decomposed linear: pd/core/decomposed_linear.py:142-175 site_forward,
  *      ((x@V)*(m-d))@U blended with d*(x@W^T) and route (:65-85).
@@ -128,6 +153,25 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
                          void* dmask, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- block-factored site, dense over every block: pd/core/decomposed_linear.py:209-271
+ *      blocked_site_forward with the einsums of pd/core/linear_plan.py:149-160.
+ *      V [E,d_in,c], U [E,c,d_out] per block; mask [T,E*c] block-major; delta [T], route
+ *      [T] uint8 nullable (W read only with them).
+ *      PD_BLOCK_FUSED_OUTPUT (gate/up): x [T,d_in], W [E*d_out,d_in], out [T,E*d_out]
+ *        (block outputs concatenated); PD_BLOCK_FUSED_INPUT (down): x [T,E*d_in],
+ *        W [d_out,E*d_in], out [T,d_out] (block outputs summed).
+ *      Outputs xV [T,E*c] (the flat component activation) and acts [T,E*c] for the bwd.
+ *      bwd: dx (nullable, x's shape), dV, dU, dmask (nullable). bf16: d_in, d_out, c % 8. */
+int pd_blocked_site_fwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
+                        const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                        const uint8_t* route, void* out, void* xV, void* acts, void* stream);
+size_t pd_blocked_site_bwd_workspace_size(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in,
+                                          int64_t d_out, int64_t c);
+int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
+                        const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                        const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx, void* dV,
+                        void* dU, void* dmask, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- fused single-site stochastic-recon step (the dense hot path) ----
  * One fwd+bwd of: clean target y_t = x@W^T (detached, pd/core/train.py:578-606);

@@ -149,6 +149,95 @@ def site_backward(x, W, V, U, mask, delta, route, dout):
     return dx, dV, dU, dmask
 
 
+# ---------------------------------------------------------------- block-factored site
+def blocked_site_forward(x, W, V, U, mask, delta, route, contraction):
+    """`pd/core/decomposed_linear.py:209-271` dense over every block, with the einsums of
+    `pd/core/linear_plan.py:149-160`: fused_output `xV = einsum('ti,eij->tej')`,
+    `out = einsum('tej,ejk->tek')` flattened; fused_input `xV = einsum('tei,eij->tej')`,
+    `out = einsum('tej,ejk->tk')`. mask / delta / route as `site_forward` with the flat
+    block-major `C = E*c`. Returns (output, xV_flat)."""
+    E, d_in, c = V.shape
+    T = x.shape[0]
+    if contraction == "fused_output":
+        xV = np.einsum("ti,eij->tej", x, V)
+    else:
+        xV = np.einsum("tei,eij->tej", x.reshape(T, E, d_in), V)
+    xV_flat = xV.reshape(T, E * c)
+    coef = mask if delta is None else mask - delta[:, None]
+    acts = (xV_flat * coef).reshape(T, E, c)
+    if contraction == "fused_output":
+        out = np.einsum("tej,ejk->tek", acts, U).reshape(T, -1)
+    else:
+        out = np.einsum("tej,ejk->tk", acts, U)
+    if delta is None and route is None:
+        return out, xV_flat
+    target = x @ W.T
+    blended = out if delta is None else out + delta[:, None] * target
+    if route is not None:
+        blended = np.where(route[:, None], blended, target)
+    return blended, xV_flat
+
+
+def blocked_site_forward_loop(x, W, V, U, mask, delta, route, contraction):
+    """The same site written block by block (as `tests/core/test_blocked_factorization.py`'s
+    per-block loop reference): the second formulation the einsum form is checked against."""
+    E, d_in, c = V.shape
+    T = x.shape[0]
+    if contraction == "fused_output":
+        xV = np.stack([x @ V[e] for e in range(E)], axis=1)
+    else:
+        xe = x.reshape(T, E, d_in)
+        xV = np.stack([xe[:, e] @ V[e] for e in range(E)], axis=1)
+    xV_flat = xV.reshape(T, E * c)
+    coef = mask if delta is None else mask - delta[:, None]
+    acts = (xV_flat * coef).reshape(T, E, c)
+    if contraction == "fused_output":
+        out = np.concatenate([acts[:, e] @ U[e] for e in range(E)], axis=-1)
+    else:
+        out = sum(acts[:, e] @ U[e] for e in range(E))
+    frozen = x @ W.T
+    if delta is not None:
+        out = out + delta[:, None] * frozen
+    if route is not None:
+        out = np.where(route[:, None], out, frozen)
+    return out, xV_flat
+
+
+def blocked_site_backward(x, W, V, U, mask, delta, route, contraction, dout):
+    """VJP of `blocked_site_forward` w.r.t. (x, V, U, mask)."""
+    E, d_in, c = V.shape
+    T = x.shape[0]
+    fo = contraction == "fused_output"
+    xe = None if fo else x.reshape(T, E, d_in)
+    xV = np.einsum("ti,eij->tej", x, V) if fo else np.einsum("tei,eij->tej", xe, V)
+    coef = (mask if delta is None else mask - delta[:, None]).reshape(T, E, c)
+    dcomp = dout if route is None else np.where(route[:, None], dout, 0.0)
+    acts = xV * coef
+    if fo:
+        g = dcomp.reshape(T, E, -1)
+        dU = np.einsum("tej,tek->ejk", acts, g)
+        dacts = np.einsum("tek,ejk->tej", g, U)
+    else:
+        dU = np.einsum("tej,tk->ejk", acts, dcomp)
+        dacts = np.einsum("tk,ejk->tej", dcomp, U)
+    dmask = (dacts * xV).reshape(T, E * c)
+    dxV = dacts * coef
+    if fo:
+        dV = np.einsum("ti,tej->eij", x, dxV)
+        dx = np.einsum("tej,eij->ti", dxV, V)
+    else:
+        dV = np.einsum("tei,tej->eij", xe, dxV)
+        dx = np.einsum("tej,eij->tei", dxV, V).reshape(T, E * d_in)
+    if delta is not None or route is not None:
+        dtarget = np.zeros_like(dout)
+        if delta is not None:
+            dtarget = dtarget + dcomp * delta[:, None]
+        if route is not None:
+            dtarget = dtarget + np.where(route[:, None], 0.0, dout)
+        dx = dx + dtarget @ W
+    return dx, dV, dU, dmask
+
+
 # ---------------------------------------------------------------- losses
 def impmin_pnorm(ci_upper, p: float, eps: float = 0.0, beta: float = 0.0, world_size: int = 1):
     """L_p importance minimality. Paper algorithm step 4
@@ -236,6 +325,46 @@ def categorical_kl_grad(masked_logits, clean_logits):
     """d mean_pos KL / d masked_logits = (softmax(masked) - softmax(clean)) / n_pos."""
     n = int(np.prod(masked_logits.shape[:-1]))
     return (np.exp(log_softmax(masked_logits)) - np.exp(log_softmax(clean_logits))) / n
+
+
+def streamed_position_kl(act_masked, head_masked, act_clean, head_clean, n_chunks: int):
+    """`param_decomp/param_decomp/targets/losses.py:101-163` (`streamed_position_kl`):
+    per-position KL(softmax(clean) || softmax(masked)) with `z = act @ head.T` streamed
+    over `n_chunks` equal vocab chunks through the paired online-softmax accumulators
+    (running maxima m_p, m_q, rescaled sums s_p, s_q and the p-weighted cross term a):
+    `KL = a/s_p - (m_p + log s_p) + (m_q + log s_q)`. Returns (kl [N], stats [N, 5] =
+    (m_p, s_p, a, m_q, s_q))."""
+    V = head_masked.shape[0]
+    assert V % n_chunks == 0, (V, n_chunks)
+    ch = V // n_chunks
+    N = act_masked.shape[0]
+    m_p = np.full(N, -np.inf)
+    m_q = np.full(N, -np.inf)
+    s_p = np.zeros(N)
+    s_q = np.zeros(N)
+    a = np.zeros(N)
+    for c in range(n_chunks):
+        zp = act_clean @ head_clean[c * ch:(c + 1) * ch].T
+        zq = act_masked @ head_masked[c * ch:(c + 1) * ch].T
+        mp2 = np.maximum(m_p, zp.max(axis=-1))
+        mq2 = np.maximum(m_q, zq.max(axis=-1))
+        rp = np.exp(m_p - mp2)
+        ep = np.exp(zp - mp2[:, None])
+        s_p = s_p * rp + ep.sum(axis=-1)
+        a = a * rp + np.sum(ep * (zp - zq), axis=-1)
+        s_q = s_q * np.exp(m_q - mq2) + np.exp(zq - mq2[:, None]).sum(axis=-1)
+        m_p, m_q = mp2, mq2
+    kl = a / s_p - (m_p + np.log(s_p)) + (m_q + np.log(s_q))
+    return kl, np.stack([m_p, s_p, a, m_q, s_q], axis=-1)
+
+
+def streamed_position_kl_vjp(act_masked, head_masked, act_clean, head_clean, g_position):
+    """Cotangent of the masked activations: `sum_v (q_v - p_v) g_n head_masked[v]`
+    (the exact softmax cotangent the reference's checkpointed scan flows back; the clean
+    side is the stop-gradient target)."""
+    q = np.exp(log_softmax(act_masked @ head_masked.T))
+    p = np.exp(log_softmax(act_clean @ head_clean.T))
+    return ((q - p) * g_position[:, None]) @ head_masked
 
 
 # ---------------------------------------------------------------- dense fused step

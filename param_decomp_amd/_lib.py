@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 F32, BF16 = 0, 1
 LAYOUT_PARTITIONABLE, LAYOUT_ORIGINAL = 0, 1
 IMPMIN_PNORM, IMPMIN_SMOOTH_L0 = 0, 1
+BLOCK_FUSED_OUTPUT, BLOCK_FUSED_INPUT = 0, 1
 
 _c_i64, _c_i32, _c_u32, _c_f32, _c_p, _c_sz = (ctypes.c_int64, ctypes.c_int, ctypes.c_uint32, ctypes.c_float,
                                                 ctypes.c_void_p, ctypes.c_size_t)
@@ -41,8 +42,16 @@ _SIGNATURES = {
     "pd_mse": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "pd_kl_workspace_size": (_c_sz, [_c_i64]),
     "pd_kl": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "pd_streamed_kl_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i32]),
+    "pd_streamed_kl_fwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 6 + [_c_p, _c_sz, _c_p]),
+    "pd_streamed_kl_bwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),
     "pd_gemm": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_i32, _c_p, _c_i64,
                          _c_i32, _c_f32, _c_f32, _c_p]),
+    "pd_gemm_strided_batched": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_p,
+                                         _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_f32, _c_f32, _c_p]),
+    "pd_blocked_site_fwd": (_c_i32, [_c_i32, _c_i32] + [_c_i64] * 5 + [_c_p] * 11),
+    "pd_blocked_site_bwd_workspace_size": (_c_sz, [_c_i32, _c_i32] + [_c_i64] * 5),
+    "pd_blocked_site_bwd": (_c_i32, [_c_i32, _c_i32] + [_c_i64] * 5 + [_c_p] * 15 + [_c_sz, _c_p]),
     "pd_masked_linear_fwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 11),
     "pd_masked_linear_bwd_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
     "pd_masked_linear_bwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 14 + [_c_sz, _c_p]),

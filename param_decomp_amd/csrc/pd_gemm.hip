@@ -16,10 +16,12 @@
 // over the 8 XCDs, so the linear id is remapped so each XCD's share is a compact
 // 8-row-grouped region (fewer distinct A/B panels per XCD-local L2).
 //
-// Three problem mappings share the kernel:
+// Four problem mappings share the kernel:
 //   DENSE     C = alpha*op(A)@op(B) + beta*C                  (x@V, acts@U, transposes)
 //   GROUPED   out[rows_e] = lhs[rows_e] @ rhs[e], ragged rows  (pd/routed/experts.py:326-348)
 //   GROUPED_K out[e] = lhs[rows_e]^T @ dout[rows_e]            (pd/routed/experts.py:209-280)
+//   BATCHED   C[z] = op(A[z]) @ op(B[z]), per-operand strides  (per-block einsums,
+//                                                              pd/core/linear_plan.py:149-160)
 // Group offsets live on the device; blocks locate their group by scanning them, so no
 // host synchronization is needed.
 #include <algorithm>
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
   if (!map_tile<BM, BN, MODE, TC>(p, lane, t)) return;
   const int64_t M = t.M, N = p.N, m0 = t.m0, n0 = t.n0, kend = t.kend;
   int64_t kbeg = t.kbeg;
-  const bf16_t* A = p.A;
+  const bf16_t* A = t.A;
   const bf16_t* B = t.B;
   TC* C = (TC*)t.C;
 
@@ -196,12 +198,17 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
     }
 }
 
-// fp32 kernel (fp32 toy configs): 64x64 tiles, 4x4 outputs per thread, any layout.
+// fp32 kernel (fp32 toy configs): 64x64 tiles, 4x4 outputs per thread, any layout;
+// blockIdx.z = batch, each operand advancing by its own stride (0 = shared).
 constexpr int FT = 64, FK = 16;
 __global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
                                                   int64_t lda, int ta, const float* __restrict__ B, int64_t ldb,
-                                                  int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta) {
+                                                  int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta,
+                                                  int64_t sA, int64_t sB, int64_t sC) {
   __shared__ float As[FK][FT + 1], Bs[FK][FT + 1];
+  A += (int64_t)blockIdx.z * sA;
+  B += (int64_t)blockIdx.z * sB;
+  C += (int64_t)blockIdx.z * sC;
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const int64_t m0 = (int64_t)blockIdx.y * FT, n0 = (int64_t)blockIdx.x * FT;
   float acc[4][4] = {};
@@ -308,7 +315,7 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
     if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm: fp32 path writes fp32");
     dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT));
     hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, M, N, K, (const float*)A, lda, trans_a, (const float*)B,
-                       ldb, trans_b, (float*)C, ldc, alpha, beta);
+                       ldb, trans_b, (float*)C, ldc, alpha, beta, (int64_t)0, (int64_t)0, (int64_t)0);
     return check_launch("pd_gemm f32");
   }
   if (dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_gemm: dtype");
@@ -321,6 +328,35 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
                                            dim3((unsigned)cdiv(N, 256), (unsigned)cdiv(M, 256)), s);
   return launch_bf16<CfgSmall, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
                                            dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128)), s);
+}
+
+int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                            int64_t stride_a, int trans_a, const void* B, int64_t ldb, int64_t stride_b, int trans_b,
+                            void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
+                            void* stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0 || stride_a < 0 || stride_b < 0 || stride_c < 0 || !A || !B || !C)
+    return fail(PD_EINVAL, "pd_gemm_strided_batched: bad args");
+  if (batch == 0 || M == 0 || N == 0) return PD_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (batch > 65535 || cdiv(M, FT) > 65535 || cdiv(N, FT) > 65535)
+    return fail(PD_EUNSUPPORTED, "pd_gemm_strided_batched: too large");
+  if (dtype == PD_DTYPE_F32) {
+    if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm_strided_batched: fp32 path writes fp32");
+    dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
+    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, M, N, K, (const float*)A, lda, trans_a, (const float*)B,
+                       ldb, trans_b, (float*)C, ldc, alpha, beta, stride_a, stride_b, stride_c);
+    return check_launch("pd_gemm_strided_batched f32");
+  }
+  if (dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_gemm_strided_batched: dtype");
+  bool a_kmaj = !trans_a, b_kmaj = trans_b;
+  if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N) || stride_a % 8 ||
+      stride_b % 8)
+    return fail(PD_EUNSUPPORTED,
+                "pd_gemm_strided_batched: bf16 operands need 16B alignment, ld and batch strides % 8 == 0");
+  GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, stride_b,
+             stride_c, stride_a};
+  return launch_bf16<CfgSmall, MODE_BATCHED>(
+      a, a_kmaj, b_kmaj, c_dtype, dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)batch), s);
 }
 
 int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,

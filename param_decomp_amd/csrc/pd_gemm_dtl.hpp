@@ -29,7 +29,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2 };
+enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2, MODE_BATCHED = 3 };
 
 struct GemmArgs {
   int64_t M, N, K;
@@ -42,8 +42,9 @@ struct GemmArgs {
   float alpha, beta;
   const int32_t* offsets;  // [E+1] group offsets (grouped modes)
   int E;
-  int64_t strideB;  // elements between consecutive groups' B (GROUPED)
-  int64_t strideC;  // elements between consecutive groups' C (GROUPED_K)
+  int64_t strideB;  // elements between consecutive groups' B (GROUPED, BATCHED)
+  int64_t strideC;  // elements between consecutive groups' C (GROUPED_K, BATCHED)
+  int64_t strideA;  // elements between consecutive batches' A (BATCHED; 0 = shared)
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): give
@@ -90,14 +91,16 @@ __device__ inline void dense_tile(int& my, int& nx) {
 // columns from n0, contraction [kbeg, kend), and the operand/output bases.
 struct TileJob {
   int64_t m0, n0, M, kbeg, kend;
+  const bf16_t* A;
   const bf16_t* B;
   void* C;
 };
 
-// Maps this block to its tile (the three problem mappings); false = no work.
+// Maps this block to its tile (the four problem mappings); false = no work.
 template <int BM, int BN, int MODE, typename TC>
 __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   t.M = p.M;
+  t.A = p.A;
   t.B = p.B;
   t.C = p.C;
   t.kbeg = 0;
@@ -139,6 +142,14 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     t.m0 = off + (int64_t)(tile - before) * BM;
     if (t.m0 < 0) return false;
     t.B = p.B + (int64_t)e * p.strideB;
+  } else if (MODE == MODE_BATCHED) {
+    // blockIdx.z = batch; each operand advances by its own stride (0 = shared)
+    const int64_t z = blockIdx.z;
+    t.m0 = (int64_t)blockIdx.y * BM;
+    t.n0 = (int64_t)blockIdx.x * BN;
+    t.A = p.A + z * p.strideA;
+    t.B = p.B + z * p.strideB;
+    t.C = (TC*)p.C + z * p.strideC;
   } else {
     const int64_t gx = gridDim.x, gxy = gx * gridDim.y;
     const int64_t lin = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gx + blockIdx.x;
@@ -352,7 +363,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
   auto issue = [&](int64_t kt) {
     char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
     const int64_t k0 = kbeg + kt * 64;
-    dtl_issue<BM, NW>(st, p.A, p.lda, t.m0, p.M, k0, kcap, wave, lane);
+    dtl_issue<BM, NW>(st, t.A, p.lda, t.m0, p.M, k0, kcap, wave, lane);
     dtl_issue<CFG::BN, NW>(st + BM * 128, t.B, p.ldb, t.n0, p.N, k0, kcap, wave, lane);
   };
 

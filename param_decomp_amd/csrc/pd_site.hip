@@ -2,6 +2,7 @@
 //
 //   pd_masked_linear_fwd/bwd   pd/core/decomposed_linear.py:142-175 (site_forward),
 //                              :65-85 (component_coefficients, blend_target_output)
+//   pd_blocked_site_fwd/bwd    :209-271 (blocked_site_forward, dense over every block)
 #include "pd_common.hpp"
 
 namespace pd {
@@ -64,6 +65,19 @@ __global__ void k_ml_target_grad(const T* __restrict__ g, const T* __restrict__ 
     float s = r ? (delta ? load_f<T>(delta, t) : 0.f) : 1.f;
     store_f<T>(gt, i, load_f<T>(g, i) * s);
   }
+}
+
+
+__global__ void k_f32_to_bf16(const float* __restrict__ src, int64_t n, bf16_t* __restrict__ dst) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = f32_to_bf16(src[i]);
+}
+
+template <typename T>
+static void launch_acts(int dtype, const void* xV, const void* mask, const void* delta, const uint8_t* route,
+                        int64_t Tn, int64_t C, void* acts, hipStream_t s) {
+  hipLaunchKernelGGL(k_ml_acts<T>, dim3(ew_grid(Tn * C)), dim3(256), 0, s, (const T*)xV, (const T*)mask,
+                     (const T*)delta, route, Tn, C, (T*)acts);
 }
 
 }  // namespace pd
@@ -151,6 +165,155 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
                          (const bf16_t*)delta, route, T, d_out, (bf16_t*)gt);
     if ((rc = check_launch("pd_masked_linear_bwd target"))) return rc;
     if ((rc = pd_gemm(dtype, T, d_in, d_out, gt, d_out, 0, W, d_in, 0, dx, d_in, dtype, 1.f, 1.f, stream))) return rc;
+  }
+  return PD_OK;
+}
+
+
+// ---------------------------------------------------------------- block-factored site
+// pd/core/decomposed_linear.py:209-271 (blocked_site_forward), einsums of
+// pd/core/linear_plan.py:149-160. With C = E*c block-major:
+//   fused_output: xV[:, e] = x @ V[e]            out[:, e] = acts[:, e] @ U[e]   (concat)
+//   fused_input:  xV[:, e] = x[:, e] @ V[e]      out = sum_e acts[:, e] @ U[e]   (one GEMM)
+// acts = routed ? xV * (m - d) : 0; with delta/route the target x @ W^T is blended as in
+// site_forward. Per-block products run as strided-batched GEMMs.
+int pd_blocked_site_fwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
+                        const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                        const uint8_t* route, void* out, void* xV, void* acts, void* stream) {
+  if (T < 0 || E <= 0 || d_in <= 0 || d_out <= 0 || c <= 0 || !x || !V || !U || !mask || !out || !xV || !acts)
+    return fail(PD_EINVAL, "pd_blocked_site_fwd: bad args");
+  if (contraction != PD_BLOCK_FUSED_OUTPUT && contraction != PD_BLOCK_FUSED_INPUT)
+    return fail(PD_EINVAL, "pd_blocked_site_fwd: contraction");
+  if ((delta || route) && !W) return fail(PD_EINVAL, "pd_blocked_site_fwd: W required with delta/route");
+  if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_blocked_site_fwd: dtype");
+  if (dtype == PD_DTYPE_BF16 && (d_in % 8 || d_out % 8 || c % 8))
+    return fail(PD_EUNSUPPORTED, "pd_blocked_site_fwd: bf16 needs d_in, d_out, c multiples of 8");
+  if (T == 0) return PD_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bool fo = contraction == PD_BLOCK_FUSED_OUTPUT;
+  const int64_t C = E * c, DI = fo ? d_in : E * d_in, DO = fo ? E * d_out : d_out;
+  int rc = pd_gemm_strided_batched(dtype, E, T, c, d_in, x, DI, fo ? 0 : d_in, 0, V, c, d_in * c, 0, xV, C, c, dtype,
+                                   1.f, 0.f, stream);
+  if (rc) return rc;
+  if (dtype == PD_DTYPE_F32)
+    launch_acts<float>(dtype, xV, mask, delta, route, T, C, acts, s);
+  else
+    launch_acts<bf16_t>(dtype, xV, mask, delta, route, T, C, acts, s);
+  if ((rc = check_launch("pd_blocked_site_fwd acts"))) return rc;
+  float beta = 0.f;
+  if (delta || route) {
+    if ((rc = pd_gemm(dtype, T, DO, DI, x, DI, 0, W, DI, 1, out, DO, dtype, 1.f, 0.f, stream))) return rc;
+    if (dtype == PD_DTYPE_F32)
+      hipLaunchKernelGGL(k_ml_scale_target<float>, dim3(ew_grid(T * DO)), dim3(256), 0, s, (float*)out,
+                         (const float*)delta, route, T, DO);
+    else
+      hipLaunchKernelGGL(k_ml_scale_target<bf16_t>, dim3(ew_grid(T * DO)), dim3(256), 0, s, (bf16_t*)out,
+                         (const bf16_t*)delta, route, T, DO);
+    if ((rc = check_launch("pd_blocked_site_fwd target"))) return rc;
+    beta = 1.f;
+  }
+  if (fo)
+    return pd_gemm_strided_batched(dtype, E, T, d_out, c, acts, C, c, 0, U, d_out, c * d_out, 0, out, DO, d_out, dtype,
+                                   1.f, beta, stream);
+  return pd_gemm(dtype, T, d_out, C, acts, C, 0, U, d_out, 0, out, d_out, dtype, 1.f, beta, stream);
+}
+
+static size_t blocked_ws_plan(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
+                              size_t* off_gt, size_t* off_dx32) {
+  const size_t es = dtype == PD_DTYPE_BF16 ? 2 : 4;
+  const bool fo = contraction == PD_BLOCK_FUSED_OUTPUT;
+  const int64_t C = E * c, DI = fo ? d_in : E * d_in, DO = fo ? E * d_out : d_out;
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  size_t off = up(es * (size_t)T * C);  // da
+  *off_gt = off;
+  off += up(es * (size_t)T * DO);
+  *off_dx32 = off;
+  off += up(4 * (size_t)T * DI);
+  return off;
+}
+
+size_t pd_blocked_site_bwd_workspace_size(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in,
+                                          int64_t d_out, int64_t c) {
+  size_t a, b;
+  return blocked_ws_plan(dtype, contraction, T, E, d_in, d_out, c, &a, &b);
+}
+
+int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
+                        const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                        const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx, void* dV,
+                        void* dU, void* dmask, void* workspace, size_t workspace_bytes, void* stream) {
+  if (T <= 0 || E <= 0 || d_in <= 0 || d_out <= 0 || c <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out ||
+      !dV || !dU)
+    return fail(PD_EINVAL, "pd_blocked_site_bwd: bad args");
+  if (contraction != PD_BLOCK_FUSED_OUTPUT && contraction != PD_BLOCK_FUSED_INPUT)
+    return fail(PD_EINVAL, "pd_blocked_site_bwd: contraction");
+  if ((delta || route) && dx && !W) return fail(PD_EINVAL, "pd_blocked_site_bwd: W required for dx");
+  if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_blocked_site_bwd: dtype");
+  if (dtype == PD_DTYPE_BF16 && (d_in % 8 || d_out % 8 || c % 8))
+    return fail(PD_EUNSUPPORTED, "pd_blocked_site_bwd: bf16 needs d_in, d_out, c multiples of 8");
+  size_t off_gt, off_dx32;
+  if (!workspace ||
+      workspace_bytes < blocked_ws_plan(dtype, contraction, T, E, d_in, d_out, c, &off_gt, &off_dx32))
+    return fail(PD_EWORKSPACE, "pd_blocked_site_bwd: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  const bool fo = contraction == PD_BLOCK_FUSED_OUTPUT;
+  const int64_t C = E * c, DI = fo ? d_in : E * d_in, DO = fo ? E * d_out : d_out;
+  char* ws = (char*)workspace;
+  void* da = ws;
+  void* gt = ws + off_gt;
+  float* dx32 = (float*)(ws + off_dx32);
+  int rc;
+  if (fo) {
+    // dU[e] = acts[:, e]^T @ g[:, e];  da[:, e] = g[:, e] @ U[e]^T
+    if ((rc = pd_gemm_strided_batched(dtype, E, c, d_out, T, acts, C, c, 1, g_out, DO, d_out, 0, dU, d_out, c * d_out,
+                                      dtype, 1.f, 0.f, stream)))
+      return rc;
+    if ((rc = pd_gemm_strided_batched(dtype, E, T, c, d_out, g_out, DO, d_out, 0, U, d_out, c * d_out, 1, da, C, c,
+                                      dtype, 1.f, 0.f, stream)))
+      return rc;
+  } else {
+    if ((rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream))) return rc;
+    if ((rc = pd_gemm(dtype, T, C, d_out, g_out, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
+  }
+  if (dtype == PD_DTYPE_F32)
+    hipLaunchKernelGGL(k_ml_bwd_elem<float>, dim3(ew_grid(T * C)), dim3(256), 0, s, (float*)da, (const float*)xV,
+                       (const float*)mask, (const float*)delta, route, T, C, (float*)dmask);
+  else
+    hipLaunchKernelGGL(k_ml_bwd_elem<bf16_t>, dim3(ew_grid(T * C)), dim3(256), 0, s, (bf16_t*)da, (const bf16_t*)xV,
+                       (const bf16_t*)mask, (const bf16_t*)delta, route, T, C, (bf16_t*)dmask);
+  if ((rc = check_launch("pd_blocked_site_bwd elem"))) return rc;
+  // dV[e] = x_e^T @ dxV[:, e]
+  if ((rc = pd_gemm_strided_batched(dtype, E, d_in, c, T, x, DI, fo ? 0 : d_in, 1, da, C, c, 0, dV, c, d_in * c,
+                                    dtype, 1.f, 0.f, stream)))
+    return rc;
+  if (!dx) return PD_OK;
+  // dx accumulates in fp32 (per-block sums, the target term), then takes the site dtype
+  float* acc = dtype == PD_DTYPE_F32 ? (float*)dx : dx32;
+  if (fo) {
+    for (int64_t e = 0; e < E; ++e) {
+      const char* dae = (const char*)da + (size_t)e * c * (dtype == PD_DTYPE_BF16 ? 2 : 4);
+      const char* ve = (const char*)V + (size_t)e * d_in * c * (dtype == PD_DTYPE_BF16 ? 2 : 4);
+      if ((rc = pd_gemm(dtype, T, d_in, c, dae, C, 0, ve, c, 1, acc, d_in, PD_DTYPE_F32, 1.f, e ? 1.f : 0.f, stream)))
+        return rc;
+    }
+  } else {
+    if ((rc = pd_gemm_strided_batched(dtype, E, T, d_in, c, da, C, c, 0, V, c, d_in * c, 1, acc, DI, d_in,
+                                      PD_DTYPE_F32, 1.f, 0.f, stream)))
+      return rc;
+  }
+  if (delta || route) {
+    if (dtype == PD_DTYPE_F32)
+      hipLaunchKernelGGL(k_ml_target_grad<float>, dim3(ew_grid(T * DO)), dim3(256), 0, s, (const float*)g_out,
+                         (const float*)delta, route, T, DO, (float*)gt);
+    else
+      hipLaunchKernelGGL(k_ml_target_grad<bf16_t>, dim3(ew_grid(T * DO)), dim3(256), 0, s, (const bf16_t*)g_out,
+                         (const bf16_t*)delta, route, T, DO, (bf16_t*)gt);
+    if ((rc = check_launch("pd_blocked_site_bwd target"))) return rc;
+    if ((rc = pd_gemm(dtype, T, DI, DO, gt, DO, 0, W, DI, 0, acc, DI, PD_DTYPE_F32, 1.f, 1.f, stream))) return rc;
+  }
+  if (dtype == PD_DTYPE_BF16) {
+    hipLaunchKernelGGL(k_f32_to_bf16, dim3(ew_grid(T * DI)), dim3(256), 0, s, dx32, T * DI, (bf16_t*)dx);
+    return check_launch("pd_blocked_site_bwd dx");
   }
   return PD_OK;
 }

@@ -11,6 +11,8 @@ Mirrors:
 - `mse(masked, clean)` — `pd/targets/tms.py:380-388`, `pd/targets/resid_mlp.py:411-418`.
 - `categorical_kl_from_logits(masked, clean)` — KL(clean || masked) per position,
   clean frozen (`pd/core/losses.py:80-92`).
+- `streamed_position_kl` / `streamed_kl_per_position` — the same KL over the factored
+  lm-head edge, streamed over vocab chunks (`pd/targets/losses.py:101-170`).
 """
 
 from __future__ import annotations
@@ -96,3 +98,49 @@ class _KL(torch.autograd.Function):
 
 def categorical_kl_from_logits(masked_logits: torch.Tensor, clean_logits: torch.Tensor) -> torch.Tensor:
     return _KL.apply(masked_logits, clean_logits.detach())
+
+
+class _StreamedKL(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, act_masked, head_masked, act_clean, head_clean, n_chunks):
+        N, d = act_masked.shape
+        V = head_masked.shape[0]
+        dt = L.dtype_code(act_masked.dtype)
+        kl = torch.empty(N, dtype=torch.float32, device=act_masked.device)
+        stats = torch.empty((N, 5), dtype=torch.float32, device=act_masked.device)
+        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, V, n_chunks), act_masked.device)
+        args = (dt, N, d, V, n_chunks, L.ptr(act_masked), L.ptr(head_masked), L.ptr(act_clean), L.ptr(head_clean))
+        L.call("pd_streamed_kl_fwd", *args, L.ptr(kl), L.ptr(stats), L.ptr(ws), ws.numel(), L.stream())
+        ctx.save_for_backward(act_masked, head_masked, act_clean, head_clean, stats)
+        ctx.n_chunks = n_chunks
+        return kl
+
+    @staticmethod
+    def backward(ctx, g):
+        act_masked, head_masked, act_clean, head_clean, stats = ctx.saved_tensors
+        N, d = act_masked.shape
+        V = head_masked.shape[0]
+        dt = L.dtype_code(act_masked.dtype)
+        d_act = torch.empty((N, d), dtype=torch.float32, device=act_masked.device)
+        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, V, ctx.n_chunks), act_masked.device)
+        L.call("pd_streamed_kl_bwd", dt, N, d, V, ctx.n_chunks, L.ptr(act_masked), L.ptr(head_masked),
+               L.ptr(act_clean), L.ptr(head_clean), L.ptr(stats), L.ptr(g.float().contiguous()), L.ptr(d_act),
+               L.ptr(ws), ws.numel(), L.stream())
+        return d_act.to(act_masked.dtype), None, None, None, None
+
+
+def streamed_position_kl(act_masked: torch.Tensor, head_masked: torch.Tensor, act_clean: torch.Tensor,
+                         head_clean: torch.Tensor, n_chunks: int) -> torch.Tensor:
+    """Per-position KL(clean || masked) over the factored lm-head edge, streamed over
+    `n_chunks` vocab chunks (`param_decomp/param_decomp/targets/losses.py:101-163`);
+    differentiable w.r.t. the masked activations (the clean side is the target)."""
+    lead = act_masked.shape[:-1]
+    am = act_masked.reshape(-1, act_masked.shape[-1]).contiguous()
+    ac = act_clean.detach().reshape(-1, act_clean.shape[-1]).contiguous()
+    kl = _StreamedKL.apply(am, head_masked.detach().contiguous(), ac, head_clean.detach().contiguous(), int(n_chunks))
+    return kl.reshape(lead)
+
+
+def streamed_kl_per_position(act_masked, head_masked, act_clean, head_clean, n_chunks: int) -> torch.Tensor:
+    """`streamed_kl_per_position` (`targets/losses.py:166-170`): the mean over positions."""
+    return streamed_position_kl(act_masked, head_masked, act_clean, head_clean, n_chunks).mean()

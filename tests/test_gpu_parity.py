@@ -520,3 +520,110 @@ def test_grouped_gemm_dw_kmajor(device, sizes, out_dtype):
     for e, s in enumerate(sizes):
         if s == 0:
             assert torch.count_nonzero(dw[e]) == 0
+
+
+# ------------------------------------------------------------------ streamed-vocab KL
+
+
+@pytest.mark.parametrize("dtype,n_chunks", [(torch.float32, 1), (torch.float32, 3), (torch.float32, 8),
+                                            (torch.bfloat16, 8), (torch.bfloat16, 2)])
+def test_streamed_kl_fwd_bwd(device, dtype, n_chunks):
+    """Per-position KL and the masked-activation gradient against the float64 oracle on
+    the same (dtype-rounded) inputs. fp32: |err| <= 1e-4 |want| + 2e-6 max|want| (fp32
+    logits accumulated over d, exp/log in fp32). bf16: the gradient's (q - p) g passes
+    through bf16 on its way into the GEMM, so rtol 2e-2."""
+    from param_decomp_amd.losses import streamed_kl_per_position, streamed_position_kl
+
+    rng = np.random.default_rng(n_chunks)
+    N, d, V = (300, 64, 1200) if dtype == torch.float32 else (512, 128, 4096)
+    cast = (lambda a: f32(a, device)) if dtype == torch.float32 else (lambda a: bf(a, device))
+    aq = cast(rng.normal(size=(N, d)) * 0.5).requires_grad_(True)
+    ap = cast(rng.normal(size=(N, d)) * 0.5)
+    hq = cast(rng.normal(size=(V, d)) * 0.3)
+    hp = cast(rng.normal(size=(V, d)) * 0.3)
+    kl = streamed_position_kl(aq, hq, ap, hp, n_chunks)
+    want, _ = po.streamed_position_kl(np64(aq), np64(hq), np64(ap), np64(hp), n_chunks)
+    if dtype == torch.float32:
+        assert_close(np64(kl), want, 1e-4, 2e-6, "position kl")
+    else:
+        assert_close(np64(kl), want, 1e-3, 1e-4, "position kl bf16")
+    g = rng.normal(size=N)
+    (da,) = torch.autograd.grad(kl, aq, f32(g, device))
+    want_da = po.streamed_position_kl_vjp(np64(aq), np64(hq), np64(ap), np64(hp), g)
+    if dtype == torch.float32:
+        assert_close(np64(da), want_da, 1e-4, 1e-5, "d act_masked")
+    else:
+        assert_close(np64(da), want_da, BF16_RTOL, 1e-2, "d act_masked bf16")
+    mean = streamed_kl_per_position(aq, hq, ap, hp, n_chunks)
+    assert float(mean) == pytest.approx(float(np.mean(want)), rel=1e-3)
+
+
+# ------------------------------------------------------------------ strided-batched GEMM / blocked site
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ta,tb,shared_a", [(0, 0, False), (1, 0, True), (0, 1, False), (1, 1, False)])
+def test_gemm_strided_batched(device, dtype, ta, tb, shared_a):
+    from param_decomp_amd import _lib as L
+
+    rng = np.random.default_rng(ta * 4 + tb * 2 + int(shared_a))
+    Bt, M, N, K = 5, 72, 40, 56
+    cast = (lambda a: f32(a, device)) if dtype == torch.float32 else (lambda a: bf(a, device))
+    A = cast(rng.normal(size=(1 if shared_a else Bt,) + ((K, M) if ta else (M, K))))
+    B = cast(rng.normal(size=(Bt,) + ((N, K) if tb else (K, N))))
+    C = torch.empty((Bt, M, N), dtype=torch.float32, device=device)
+    lda = M if ta else K
+    ldb = K if tb else N
+    L.call("pd_gemm_strided_batched", L.dtype_code(dtype), Bt, M, N, K, L.ptr(A), lda, 0 if shared_a else M * K, ta,
+           L.ptr(B), ldb, N * K, tb, L.ptr(C), N, M * N, L.F32, 1.0, 0.0, L.stream())
+    a, b = np64(A), np64(B)
+    a = np.broadcast_to(a, (Bt,) + a.shape[1:])
+    want = np.einsum("zmk,zkn->zmn", np.swapaxes(a, 1, 2) if ta else a, np.swapaxes(b, 1, 2) if tb else b)
+    assert_close(np64(C), want, 1e-5 if dtype == torch.float32 else 1e-5, 1e-6, "batched")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("contraction", ["fused_output", "fused_input"])
+@pytest.mark.parametrize("with_delta_and_route", [False, True])
+def test_blocked_site_forward_backward(device, dtype, contraction, with_delta_and_route):
+    from param_decomp_amd.decomposed_linear import BlockedSiteWeights, blocked_site_forward
+
+    rng = np.random.default_rng(2 + int(with_delta_and_route))
+    E, d_in, d_out, c, T = 6, 32, 24, 16, 150
+    site_in = d_in * (E if contraction == "fused_input" else 1)
+    site_out = d_out * (E if contraction == "fused_output" else 1)
+    cast = (lambda a: f32(a, device)) if dtype == torch.float32 else (lambda a: bf(a, device))
+    x = cast(rng.normal(size=(T, site_in))).requires_grad_(True)
+    V = cast(rng.normal(size=(E, d_in, c)) / np.sqrt(d_in)).requires_grad_(True)
+    U = cast(rng.normal(size=(E, c, d_out)) / np.sqrt(E * c)).requires_grad_(True)
+    W = cast(rng.normal(size=(site_out, site_in)) / np.sqrt(site_in))
+    mask = cast(rng.uniform(size=(T, E * c))).requires_grad_(True)
+    delta = cast(rng.uniform(size=T)) if with_delta_and_route else None
+    route = torch.tensor(rng.uniform(size=T) < 0.6, device=device) if with_delta_and_route else None
+    sf = blocked_site_forward(x, BlockedSiteWeights(W, V, U), mask, delta, route, contraction)
+    want_out, want_xv = po.blocked_site_forward(np64(x), np64(W), np64(V), np64(U), np64(mask),
+                                                None if delta is None else np64(delta),
+                                                None if route is None else route.cpu().numpy(), contraction)
+    rt, fl = (1e-5, 1e-6) if dtype == torch.float32 else (BF16_RTOL, 4e-3)
+    assert_close(np64(sf.output), want_out, rt, fl, "blocked out")
+    assert_close(np64(sf.component_activation), want_xv, rt, fl, "blocked xV")
+    G = rng.normal(size=want_out.shape)
+    Gx = rng.normal(size=want_xv.shape) * 0.1
+    dx, dV, dU, dm = torch.autograd.grad((sf.output, sf.component_activation), (x, V, U, mask),
+                                         (cast(G), cast(Gx)))
+    wdx, wdV, wdU, wdm = po.blocked_site_backward(np64(x), np64(W), np64(V), np64(U), np64(mask),
+                                                  None if delta is None else np64(delta),
+                                                  None if route is None else route.cpu().numpy(), contraction,
+                                                  np64(cast(G)))
+    gx = np64(cast(Gx))
+    xe = np64(x) if contraction == "fused_output" else np64(x).reshape(T, E, d_in)
+    gxe = gx.reshape(T, E, c)
+    if contraction == "fused_output":
+        wdV = wdV + np.einsum("ti,tej->eij", xe, gxe)
+        wdx = wdx + np.einsum("tej,eij->ti", gxe, np64(V))
+    else:
+        wdV = wdV + np.einsum("tei,tej->eij", xe, gxe)
+        wdx = wdx + np.einsum("tej,eij->tei", gxe, np64(V)).reshape(T, -1)
+    rt, fl = (1e-4, 1e-5) if dtype == torch.float32 else (BF16_RTOL, 1e-2)
+    for got, want, name in ((dx, wdx, "dx"), (dV, wdV, "dV"), (dU, wdU, "dU"), (dm, wdm, "dmask")):
+        assert_close(np64(got), want, rt, fl, f"blocked {name}")

@@ -520,3 +520,94 @@ def test_static_probability_routing_limits_and_rate():
     np.testing.assert_allclose(r.mean(axis=1), 0.3, atol=0.015)
     u1 = tf.uniform(tf.fold_in(key, 1), (n,), "float32")
     np.testing.assert_array_equal(r[1], u1 < np.float32(0.3))
+
+
+# ---------------------------------------------------------------- streamed-vocab KL
+@pytest.mark.parametrize("n_chunks", [1, 3, 8])
+def test_streamed_kl_equals_materialized_kl(n_chunks):
+    """The paired online-softmax recurrence equals KL on the materialized logits, for
+    any chunking (the result is invariant to the running max)."""
+    rng = np.random.default_rng(n_chunks)
+    N, d, V = 37, 16, 48
+    aq, ap = rng.normal(size=(N, d)), rng.normal(size=(N, d))
+    head = rng.normal(size=(V, d))
+    kl, stats = po.streamed_position_kl(aq, head, ap, head, n_chunks)
+    want = po.kl_per_position(aq @ head.T, ap @ head.T)
+    np.testing.assert_allclose(kl, want, rtol=1e-10, atol=1e-13)
+    # stats: m_p is the row max, m_p + log s_p the clean log-partition
+    zp = ap @ head.T
+    np.testing.assert_allclose(stats[:, 0], zp.max(axis=-1), rtol=0, atol=0)
+    np.testing.assert_allclose(stats[:, 0] + np.log(stats[:, 1]), np.log(np.exp(zp).sum(axis=-1)), rtol=1e-12)
+    assert np.all(kl >= -1e-12)
+
+
+def test_streamed_kl_vjp_finite_differences():
+    rng = np.random.default_rng(0)
+    N, d, V = 5, 4, 12
+    aq, ap = rng.normal(size=(N, d)), rng.normal(size=(N, d))
+    hq, hp = rng.normal(size=(V, d)), rng.normal(size=(V, d))
+    g = rng.normal(size=N)
+    grad = po.streamed_position_kl_vjp(aq, hq, ap, hp, g)
+    eps = 1e-6
+    for n in range(N):
+        for j in range(d):
+            a1, a2 = aq.copy(), aq.copy()
+            a1[n, j] += eps
+            a2[n, j] -= eps
+            f1 = np.dot(g, po.streamed_position_kl(a1, hq, ap, hp, 3)[0])
+            f2 = np.dot(g, po.streamed_position_kl(a2, hq, ap, hp, 3)[0])
+            assert grad[n, j] == pytest.approx((f1 - f2) / (2 * eps), rel=1e-6, abs=1e-9)
+
+
+# ---------------------------------------------------------------- block-factored site
+@pytest.mark.parametrize("contraction", ["fused_output", "fused_input"])
+@pytest.mark.parametrize("with_delta_and_route", [False, True])
+def test_blocked_site_einsum_form_matches_per_block_loop(contraction, with_delta_and_route):
+    rng = np.random.default_rng(4)
+    E, d_in, d_out, c, T = 3, 5, 4, 2, 11
+    site_in = d_in * (E if contraction == "fused_input" else 1)
+    site_out = d_out * (E if contraction == "fused_output" else 1)
+    x = rng.normal(size=(T, site_in))
+    V = rng.normal(size=(E, d_in, c)) * 0.3
+    U = rng.normal(size=(E, c, d_out)) * 0.3
+    W = rng.normal(size=(site_out, site_in))
+    mask = rng.uniform(size=(T, E * c))
+    delta = rng.uniform(size=T) if with_delta_and_route else None
+    route = (rng.uniform(size=T) < 0.5) if with_delta_and_route else None
+    got = po.blocked_site_forward(x, W, V, U, mask, delta, route, contraction)
+    want = po.blocked_site_forward_loop(x, W, V, U, mask, delta, route, contraction)
+    np.testing.assert_allclose(got[0], want[0], rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(got[1], want[1], rtol=1e-12, atol=1e-13)
+
+
+@pytest.mark.parametrize("contraction", ["fused_output", "fused_input"])
+def test_blocked_site_backward_finite_differences(contraction):
+    rng = np.random.default_rng(9)
+    E, d_in, d_out, c, T = 2, 3, 4, 2, 5
+    site_in = d_in * (E if contraction == "fused_input" else 1)
+    site_out = d_out * (E if contraction == "fused_output" else 1)
+    x = rng.normal(size=(T, site_in))
+    V = rng.normal(size=(E, d_in, c))
+    U = rng.normal(size=(E, c, d_out))
+    W = rng.normal(size=(site_out, site_in))
+    mask = rng.uniform(size=(T, E * c))
+    delta = rng.uniform(size=T)
+    route = rng.uniform(size=T) < 0.6
+    G = rng.normal(size=(T, site_out))
+    grads = po.blocked_site_backward(x, W, V, U, mask, delta, route, contraction, G)
+
+    def f(x_, V_, U_, m_):
+        return float(np.sum(G * po.blocked_site_forward(x_, W, V_, U_, m_, delta, route, contraction)[0]))
+
+    for which, arr in enumerate((x, V, U, mask)):
+        for _ in range(4):
+            idx = tuple(rng.integers(0, n) for n in arr.shape)
+            args = [x, V, U, mask]
+            a1, a2 = arr.copy(), arr.copy()
+            a1[idx] += 1e-6
+            a2[idx] -= 1e-6
+            args[which] = a1
+            f1 = f(*args)
+            args[which] = a2
+            f2 = f(*args)
+            assert grads[(0, 1, 2, 3)[which]][idx] == pytest.approx((f1 - f2) / 2e-6, rel=1e-6, abs=1e-8)
