@@ -17,6 +17,15 @@ int check_launch(const char* what);
 // callers whose groups cover every row).
 int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
                  int trans_rhs, void* out, int out_dtype, void* stream, bool zero_tail);
+// Two grouped products of one shape and one set of group offsets in a single launch:
+// out_i = lhs_i [J,K] @ rhs_i[e] with rhs_i stored [E,N,K] (K-contiguous); no tail zeroing.
+int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,
+                      const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype, void* stream);
+// Two ragged-contraction weight gradients in one launch: out_i[e] = lhsT_i[:, rows_e] @
+// doutT_i[:, rows_e]^T from job-contiguous [K,J] / [N,J] operands.
+int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out1, const void* lhsT2,
+                                const void* doutT2, void* out2, const int32_t* offsets, int64_t J, int E, int64_t K,
+                                int64_t N, int out_dtype, void* stream);
 
 // ---------------------------------------------------------------- bf16
 typedef uint16_t bf16_t;

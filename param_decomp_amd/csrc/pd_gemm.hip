@@ -391,6 +391,38 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
+int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,
+                      const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype, void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs1 || !rhsT1 || !out1 || !lhs2 || !rhsT2 || !out2 || !offsets)
+    return fail(PD_EINVAL, "grouped_gemm_pair: bad args");
+  if (J == 0) return PD_OK;
+  if (!bf16_operand_ok(lhs1, K, K) || !bf16_operand_ok(rhsT1, K, K) || !bf16_operand_ok(lhs2, K, K) ||
+      !bf16_operand_ok(rhsT2, K, K))
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: K must be a multiple of 8 with 16B-aligned bases");
+  GemmArgs a{J, N, K, (const bf16_t*)lhs1, K, (const bf16_t*)rhsT1, K, out1, N, 1.f, 0.f, offsets, E, K * N, 0, 0,
+             (const bf16_t*)lhs2, (const bf16_t*)rhsT2, out2};
+  const int64_t max_tiles = cdiv(J, CfgDtl::BM) + E;
+  if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: too many rows");
+  return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)max_tiles, 2),
+                                          (hipStream_t)stream);
+}
+
+int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out1, const void* lhsT2,
+                                const void* doutT2, void* out2, const int32_t* offsets, int64_t J, int E, int64_t K,
+                                int64_t N, int out_dtype, void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhsT1 || !doutT1 || !out1 || !lhsT2 || !doutT2 || !out2 || !offsets)
+    return fail(PD_EINVAL, "grouped_gemm_dw_kmajor_pair: bad args");
+  if (!bf16_operand_ok(lhsT1, J, J) || !bf16_operand_ok(doutT1, J, J) || !bf16_operand_ok(lhsT2, J, J) ||
+      !bf16_operand_ok(doutT2, J, J))
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: J must be a multiple of 8 with 16B-aligned bases");
+  if (2 * (int64_t)E > 65535 || cdiv(K, CfgDtl::BM) > 65535)
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: size");
+  GemmArgs a{K, N, J, (const bf16_t*)lhsT1, J, (const bf16_t*)doutT1, J, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
+             (const bf16_t*)lhsT2, (const bf16_t*)doutT2, out2};
+  dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)(2 * E));
+  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, grid, (hipStream_t)stream);
+}
+
 }  // namespace pd
 
 extern "C" {

@@ -45,6 +45,11 @@ struct GemmArgs {
   int64_t strideB;  // elements between consecutive groups' B (GROUPED, BATCHED)
   int64_t strideC;  // elements between consecutive groups' C (GROUPED_K, BATCHED)
   int64_t strideA;  // elements between consecutive batches' A (BATCHED; 0 = shared)
+  // Grouped modes: a second problem of identical shape and group offsets in the same
+  // launch (gridDim.z doubles; the upper half uses A2/B2/C2). NULL = one problem.
+  const bf16_t* A2;
+  const bf16_t* B2;
+  void* C2;
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): give
@@ -118,9 +123,16 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     int real = 0;
     for (int g0 = 0; g0 < p.E; g0 += 64)
       real += __shfl(wave_incl_scan(group_tiles(p.offsets, g0 + lane, p.E, BM), lane), 63, 64);
-    const int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
-    if (lin >= (int64_t)real * gx) return false;
-    const int64_t lr = xcd_contiguous(lin, (int64_t)real * gx);
+    const int64_t per = (int64_t)real * gx;  // tiles of one problem
+    const int64_t lin = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gx + blockIdx.x;
+    if (lin >= per * gridDim.z) return false;
+    int64_t lr = xcd_contiguous(lin, per * gridDim.z);
+    if (lr >= per) {  // second problem of a paired launch
+      lr -= per;
+      t.A = p.A2;
+      t.B = p.B2;
+      t.C = p.C2;
+    }
     t.n0 = (lr % gx) * BN;
     const int tile = (int)(lr / gx);
     int e = -1, before = 0;
@@ -141,7 +153,7 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     t.M = p.offsets[e + 1] < p.M ? p.offsets[e + 1] : p.M;  // absolute row bound, clamped to J
     t.m0 = off + (int64_t)(tile - before) * BM;
     if (t.m0 < 0) return false;
-    t.B = p.B + (int64_t)e * p.strideB;
+    t.B += (int64_t)e * p.strideB;
   } else if (MODE == MODE_BATCHED) {
     // blockIdx.z = batch; each operand advances by its own stride (0 = shared)
     const int64_t z = blockIdx.z;
@@ -154,13 +166,19 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     const int64_t gx = gridDim.x, gxy = gx * gridDim.y;
     const int64_t lin = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gx + blockIdx.x;
     const int64_t lr = xcd_contiguous(lin, gxy * gridDim.z);
-    const int e = (int)(lr / gxy);
+    int e = (int)(lr / gxy);
+    if (e >= p.E) {  // second problem of a paired launch (gridDim.z = 2E)
+      e -= p.E;
+      t.A = p.A2;
+      t.B = p.B2;
+      t.C = p.C2;
+    }
     t.m0 = (lr % gxy) / gx * BM;
     t.n0 = (lr % gx) * BN;
     t.kbeg = p.offsets[e] < 0 ? 0 : p.offsets[e];
     t.kend = p.offsets[e + 1] < p.K ? p.offsets[e + 1] : p.K;  // clamped to J
     if (t.kend < t.kbeg) t.kend = t.kbeg;
-    t.C = (TC*)p.C + (int64_t)e * p.strideC;
+    t.C = (TC*)t.C + (int64_t)e * p.strideC;
   }
   return t.m0 < t.M && t.n0 < p.N;
 }

@@ -526,10 +526,10 @@ struct MoEPlan {
   std::vector<LayerSave> layers;
   // weight copies [L, E, N, K] for the forward products
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
   float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part;
   int32_t* sort_ws;
-  bf16_t *d_dout, *d_doutT, *d_acts, *d_hT, *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
+  bf16_t *d_dout, *d_doutT, *d_acts[2], *d_hT[2], *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
   size_t imp_per_site, total;
 };
 
@@ -575,7 +575,8 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.r_final = A.take<bf16_t>(T * D.d);
   P.h2c = A.take<bf16_t>(T * D.d);
   P.xj = A.take<bf16_t>(J * D.d);
-  P.acts = A.take<bf16_t>(J * D.c);
+  P.acts[0] = A.take<bf16_t>(J * D.c);
+  P.acts[1] = A.take<bf16_t>(J * D.c);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
   P.din = A.take<bf16_t>(J * D.f);
@@ -593,8 +594,10 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
   P.d_doutT = A.take<bf16_t>(J * D.d);
-  P.d_acts = A.take<bf16_t>(J * D.c);
-  P.d_hT = A.take<bf16_t>(J * D.c);
+  for (int i = 0; i < 2; ++i) {
+    P.d_acts[i] = A.take<bf16_t>(J * D.c);
+    P.d_hT[i] = A.take<bf16_t>(J * D.c);
+  }
   P.d_din = A.take<bf16_t>(J * D.f);
   P.d_g = A.take<bf16_t>(J * D.f);
   P.d_gT = A.take<bf16_t>(J * D.f);
@@ -731,8 +734,9 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, P.h2c, S.sort_idx, k, J, d, P.xj,
                        (bf16_t*)nullptr);
-    if ((rc = grouped_gemm(P.xj, P.WgT + l * szW, S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false))) return rc;
-    if ((rc = grouped_gemm(P.xj, P.WuT + l * szW, S.offsets, J, E, d, f, 1, P.uc, PD_DTYPE_BF16, stream, false))) return rc;
+    if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, P.gc, P.xj, P.WuT + l * szW, P.uc, S.offsets, J, E, d, f,
+                                PD_DTYPE_BF16, stream)))
+      return rc;
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, P.gc, P.uc, (const float*)nullptr,
                        S.sort_idx, J, f, P.din, (bf16_t*)nullptr);
     if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
@@ -760,21 +764,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
                        S.probs, S.w);
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
-    bf16_t* outs[3] = {S.gout, S.uout, P.down};
-    const int nout[3] = {f, f, d};
-    for (int si = 0; si < 3; ++si) {
-      const bf16_t* in = si < 2 ? P.xj : P.din;
-      const int kin = si < 2 ? d : f;
-      if (si == 2) {
-        rec.mark(MOE_CAT_SWIGLU);
-        hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J,
-                           f, P.din, S.dinT);
-      }
-      rec.mark(MOE_CAT_GEMM_FWD);
-      if ((rc = grouped_gemm(in, VT[si] + l * szV[si], S.offsets, J, E, kin, c, 1, S.h[si], PD_DTYPE_BF16,
-                                stream, false)))
-        return rc;
-      rec.mark(MOE_CAT_MASK_FWD);
+    auto mask_fwd = [&](int si, bf16_t* acts_out) {
       SiteMaskArgs ma;
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       ma.sort_idx = S.sort_idx;
@@ -783,17 +773,39 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.layout = layout;
       ma.p = p;
+      float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
       if (layout == PD_LAYOUT_PARTITIONABLE)
         hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_PARTITIONABLE>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
-                           P.acts, S.actsT[si], S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
+                           acts_out, S.actsT[si], S.ub[si], part);
       else
         hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_ORIGINAL>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
-                           P.acts, S.actsT[si], S.ub[si], P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site);
-      rec.mark(MOE_CAT_GEMM_FWD);
-      if ((rc = grouped_gemm(P.acts, UT[si] + l * szU[si], S.offsets, J, E, c, nout[si], 1, outs[si],
-                                PD_DTYPE_BF16, stream, false)))
-        return rc;
-    }
+                           acts_out, S.actsT[si], S.ub[si], part);
+    };
+    // ---- gate and up sites: both products of each stage in one paired launch
+    rec.mark(MOE_CAT_GEMM_FWD);
+    if ((rc = grouped_gemm_pair(P.xj, VT[0] + l * szV[0], S.h[0], P.xj, VT[1] + l * szV[1], S.h[1], S.offsets, J, E,
+                                d, c, PD_DTYPE_BF16, stream)))
+      return rc;
+    rec.mark(MOE_CAT_MASK_FWD);
+    mask_fwd(0, P.acts[0]);
+    mask_fwd(1, P.acts[1]);
+    rec.mark(MOE_CAT_GEMM_FWD);
+    if ((rc = grouped_gemm_pair(P.acts[0], UT[0] + l * szU[0], S.gout, P.acts[1], UT[1] + l * szU[1], S.uout,
+                                S.offsets, J, E, c, f, PD_DTYPE_BF16, stream)))
+      return rc;
+    // ---- down site
+    rec.mark(MOE_CAT_SWIGLU);
+    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J, f,
+                       P.din, S.dinT);
+    rec.mark(MOE_CAT_GEMM_FWD);
+    if ((rc = grouped_gemm(P.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
+      return rc;
+    rec.mark(MOE_CAT_MASK_FWD);
+    mask_fwd(2, P.acts[0]);
+    rec.mark(MOE_CAT_GEMM_FWD);
+    if ((rc = grouped_gemm(P.acts[0], UT[2] + l * szU[2], S.offsets, J, E, c, d, 1, P.down, PD_DTYPE_BF16, stream,
+                           false)))
+      return rc;
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, S.r, P.down, S.inv,
@@ -825,7 +837,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.p = p;
     // ---- down site
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts, PD_DTYPE_BF16, stream, false)))
+    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[0], PD_DTYPE_BF16, stream,
+                           false)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
     if ((rc = pd_grouped_gemm_dw_kmajor(S.actsT[2], P.d_doutT, S.offsets, J, E, c, d, dUd + l * szUd, PD_DTYPE_F32,
@@ -834,48 +847,43 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
-    hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale, P.d_acts,
-                       P.d_hT, (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale,
+                       P.d_acts[0], P.d_hT[0], (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT, S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32, stream)))
+    if ((rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT[0], S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32,
+                                        stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_acts, bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream, false)))
+    if ((rc = grouped_gemm(P.d_acts[0], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
+                           false)))
       return rc;
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
                        J, f, P.d_g, P.d_gT, P.d_u, P.d_uT, P.d_w_part);
-    // ---- gate and up sites
-    const void* Vs[2] = {Vg, Vu};
-    const void* Us[2] = {Ug, Uu};
-    float* dVs[2] = {dVg, dVu};
-    float* dUs[2] = {dUg, dUu};
-    bf16_t* douts[2] = {P.d_g, P.d_u};
-    bf16_t* doutsT[2] = {P.d_gT, P.d_uT};
-    bf16_t* dxs[2] = {P.dxa, P.dxb};
+    // ---- gate and up sites: paired launches
+    rec.mark(MOE_CAT_GEMM_DX);
+    if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
+                                J, E, f, c, PD_DTYPE_BF16, stream)))
+      return rc;
+    rec.mark(MOE_CAT_GEMM_DW);
+    if ((rc = grouped_gemm_dw_kmajor_pair(S.actsT[0], P.d_gT, dUg + l * szUg, S.actsT[1], P.d_uT, dUu + l * szUg,
+                                          S.offsets, J, E, c, f, PD_DTYPE_F32, stream)))
+      return rc;
+    rec.mark(MOE_CAT_MASK_BWD);
     for (int si = 0; si < 2; ++si) {
-      rec.mark(MOE_CAT_GEMM_DX);
-      if ((rc = grouped_gemm(douts[si], bf(Us[si], l * szUg), S.offsets, J, E, f, c, 1, P.d_acts, PD_DTYPE_BF16,
-                                stream, false)))
-        return rc;
-      rec.mark(MOE_CAT_GEMM_DW);
-      if ((rc = pd_grouped_gemm_dw_kmajor(S.actsT[si], doutsT[si], S.offsets, J, E, c, f, dUs[si] + l * szUg,
-                                          PD_DTYPE_F32, stream)))
-        return rc;
-      rec.mark(MOE_CAT_MASK_BWD);
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
       hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], S.ub[si], imp_scale,
-                         P.d_acts, P.d_hT, (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
-      rec.mark(MOE_CAT_GEMM_DW);
-      if ((rc = pd_grouped_gemm_dw_kmajor(S.xjT, P.d_hT, S.offsets, J, E, d, c, dVs[si] + l * szVg, PD_DTYPE_F32,
-                                          stream)))
-        return rc;
-      rec.mark(MOE_CAT_GEMM_DX);
-      if ((rc = grouped_gemm(P.d_acts, bf(Vs[si], l * szVg), S.offsets, J, E, c, d, 1, dxs[si], PD_DTYPE_BF16,
-                                stream, false)))
-        return rc;
+                         P.d_acts[si], P.d_hT[si], (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
     }
+    rec.mark(MOE_CAT_GEMM_DW);
+    if ((rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
+                                          S.offsets, J, E, d, c, PD_DTYPE_F32, stream)))
+      return rc;
+    rec.mark(MOE_CAT_GEMM_DX);
+    if ((rc = grouped_gemm_pair(P.d_acts[0], bf(Vg, l * szVg), P.dxa, P.d_acts[1], bf(Vu, l * szVg), P.dxb, S.offsets,
+                                J, E, c, d, PD_DTYPE_BF16, stream)))
+      return rc;
     // ---- routing weights, router, gather VJP and the norm
     rec.mark(MOE_CAT_TOKEN_BWD);
     hipLaunchKernelGGL(k_token_bwd, dim3((unsigned)T), dim3(256), 0, s, P.d_w_part, n_wpart, S.inv, S.idx, S.probs,
