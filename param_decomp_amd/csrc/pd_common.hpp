@@ -39,8 +39,12 @@ __host__ __device__ inline float bf16_to_f32(bf16_t v) {
   return c.f;
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN). On the device this is gfx950's
+// v_cvt_pk_bf16_f32; the host keeps the bit-level rounding.
 __host__ __device__ inline bf16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(bf16_t, (__bf16)f);
+#else
   union {
     uint32_t u;
     float f;
@@ -50,6 +54,14 @@ __host__ __device__ inline bf16_t f32_to_bf16(float f) {
   if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (bf16_t)((u >> 16) | 0x40);
   u += 0x7FFFu + ((u >> 16) & 1u);
   return (bf16_t)(u >> 16);
+#endif
+}
+
+// Two fp32 values -> packed bf16 pair (a in the low half) with one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 template <typename T>

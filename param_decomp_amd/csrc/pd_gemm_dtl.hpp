@@ -1,10 +1,12 @@
 // bf16 GEMM with both operands K-contiguous, fed by direct global->LDS loads (gfx950).
 //
-// Operand tiles (rows x 64 k) live in LDS as 128-byte rows without padding; the 16-byte
-// chunk c of row R sits at physical chunk c ^ (R & 7) ^ ((R >> 3) & 1), so the 8 or 16
-// consecutive rows a fragment read touches hit distinct bank groups. Each
-// global_load_lds_dwordx4 moves one 8-row x 128-byte block: lane l writes physical
-// chunk l & 7 of row l >> 3, so it fetches the logical chunk that the swizzle puts there.
+// Operand tiles (rows x BK k, BK = 64 or 32) live in LDS as 2*BK-byte rows without
+// padding. The 16-byte chunk c of row R sits at physical chunk c ^ swz(R), with
+// swz(R) = (R & 7) ^ ((R >> 3) & 1) for 128-byte rows and (R >> 2) & 3 for 64-byte rows,
+// so the 16 consecutive rows a quarter-wave fragment read touches cover all 64 banks.
+// Each global_load_lds_dwordx4 moves one 1 KB block of whole rows: lane l writes physical
+// chunk l % (BK/8) of row l / (BK/8), so it fetches the logical chunk the swizzle puts
+// there.
 //
 // NS LDS stages form a ring with NS-1 k-tiles in flight: iteration kt waits (vmcnt) until
 // its own tile has landed, one s_barrier makes it visible and frees the stage of tile
@@ -118,39 +120,60 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   } else if (MODE == MODE_GROUPED) {
     // Row tiles are enumerated over all groups in order. Every wave scans the groups'
     // tile counts 64 at a time (lane = group); the grid has a few spare rows of blocks,
-    // so the XCD remap runs over the tiles that exist.
+    // so the XCD remap runs over the tiles that exist. With E <= 64 one load of the
+    // offsets serves the count, the lookup and the group's row range.
     const int64_t gx = gridDim.x;
-    int real = 0;
-    for (int g0 = 0; g0 < p.E; g0 += 64)
-      real += __shfl(wave_incl_scan(group_tiles(p.offsets, g0 + lane, p.E, BM), lane), 63, 64);
-    const int64_t per = (int64_t)real * gx;  // tiles of one problem
     const int64_t lin = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gx + blockIdx.x;
-    if (lin >= per * gridDim.z) return false;
-    int64_t lr = xcd_contiguous(lin, per * gridDim.z);
-    if (lr >= per) {  // second problem of a paired launch
-      lr -= per;
-      t.A = p.A2;
-      t.B = p.B2;
-      t.C = p.C2;
-    }
-    t.n0 = (lr % gx) * BN;
-    const int tile = (int)(lr / gx);
-    int e = -1, before = 0;
-    for (int g0 = 0, base = 0; g0 < p.E; g0 += 64) {
-      const int nt = group_tiles(p.offsets, g0 + lane, p.E, BM);
-      const int incl = wave_incl_scan(nt, lane);
-      const unsigned long long hit = __ballot(base + incl > tile);
-      if (hit) {
-        const int ln = __ffsll(hit) - 1;
-        e = g0 + ln;
-        before = base + __shfl(incl - nt, ln, 64);
-        break;
+    int e = -1, before = 0, tile = 0;
+    int64_t off = 0, end = 0;
+    auto pick = [&](int64_t per) -> bool {  // this block's (problem, column, row tile)
+      if (lin >= per * gridDim.z) return false;
+      int64_t lr = xcd_contiguous(lin, per * gridDim.z);
+      if (lr >= per) {  // second problem of a paired launch
+        lr -= per;
+        t.A = p.A2;
+        t.B = p.B2;
+        t.C = p.C2;
       }
-      base += __shfl(incl, 63, 64);
+      t.n0 = (lr % gx) * BN;
+      tile = (int)(lr / gx);
+      return true;
+    };
+    if (p.E <= 64) {
+      const bool in = lane < p.E;
+      const int lo = in ? p.offsets[lane] : 0, hi = in ? p.offsets[lane + 1] : 0;
+      const int nt = in && hi > lo ? (hi - lo + BM - 1) / BM : 0;
+      const int incl = wave_incl_scan(nt, lane);
+      if (!pick((int64_t)__shfl(incl, 63, 64) * gx)) return false;
+      const unsigned long long hit = __ballot(incl > tile);
+      if (!hit) return false;
+      const int ln = __ffsll(hit) - 1;
+      e = ln;
+      before = __shfl(incl - nt, ln, 64);
+      off = __shfl(lo, ln, 64);
+      end = __shfl(hi, ln, 64);
+    } else {
+      int real = 0;
+      for (int g0 = 0; g0 < p.E; g0 += 64)
+        real += __shfl(wave_incl_scan(group_tiles(p.offsets, g0 + lane, p.E, BM), lane), 63, 64);
+      if (!pick((int64_t)real * gx)) return false;
+      for (int g0 = 0, base = 0; g0 < p.E; g0 += 64) {
+        const int nt = group_tiles(p.offsets, g0 + lane, p.E, BM);
+        const int incl = wave_incl_scan(nt, lane);
+        const unsigned long long hit = __ballot(base + incl > tile);
+        if (hit) {
+          const int ln = __ffsll(hit) - 1;
+          e = g0 + ln;
+          before = base + __shfl(incl - nt, ln, 64);
+          break;
+        }
+        base += __shfl(incl, 63, 64);
+      }
+      if (e < 0) return false;
+      off = p.offsets[e];
+      end = p.offsets[e + 1];
     }
-    if (e < 0) return false;
-    const int64_t off = p.offsets[e];
-    t.M = p.offsets[e + 1] < p.M ? p.offsets[e + 1] : p.M;  // absolute row bound, clamped to J
+    t.M = end < p.M ? end : p.M;  // absolute row bound, clamped to J
     t.m0 = off + (int64_t)(tile - before) * BM;
     if (t.m0 < 0) return false;
     t.B += (int64_t)e * p.strideB;
@@ -183,16 +206,19 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   return t.m0 < t.M && t.n0 < p.N;
 }
 
-template <int BM_, int BN_, int WM_, int WN_, int NS_, int RD_ = 0>
+template <int BM_, int BN_, int WM_, int WN_, int NS_, int RD_ = 0, int BK_ = 64>
 struct DtlCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, RD = RD_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, RD = RD_, BK = BK_;
   static constexpr int NW = WM_ * WN_, NT = NW * 64;
   static constexpr int WTM = BM_ / WM_, WTN = BN_ / WN_;  // wave tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int STAGE_BYTES = (BM_ + BN_) * 128;
-  static constexpr int A_INSTS = BM_ / (8 * NW), B_INSTS = BN_ / (8 * NW);  // 1 KB loads per wave per stage
+  static constexpr int ROWB = 2 * BK_, RPI = 1024 / ROWB;  // LDS row bytes, rows per 1 KB load
+  static constexpr int KK = BK_ / 16;                      // k16 MFMA steps per stage
+  static constexpr int STAGE_BYTES = (BM_ + BN_) * ROWB;
+  static constexpr int A_INSTS = BM_ / (RPI * NW), B_INSTS = BN_ / (RPI * NW);  // 1 KB loads per wave per stage
   static constexpr int INSTS = A_INSTS + B_INSTS;
-  static_assert(BM_ % (8 * NW) == 0 && BN_ % (8 * NW) == 0, "every wave moves whole 8-row blocks");
+  static_assert(BK_ == 64 || BK_ == 32, "stage depth");
+  static_assert(BM_ % (RPI * NW) == 0 && BN_ % (RPI * NW) == 0, "every wave moves whole 1 KB row blocks");
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile is a multiple of 32x32");
   static_assert(NS_ >= 2 && INSTS * (NS_ - 2) < 64, "vmcnt range");
   static_assert(NS_ * STAGE_BYTES <= 160 * 1024, "LDS");
@@ -206,22 +232,18 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Waits until at most `ahead` stages of this wave's loads are still in flight.
-template <int INSTS, int NS>
+// Waits until at most `ahead` (<= A) stages of this wave's loads are still in flight.
+template <int INSTS, int A>
 __device__ inline void wait_stages(int ahead) {
-  if constexpr (NS >= 4) {
-    if (ahead >= 2) {
-      wait_vmcnt<2 * INSTS>();
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vmcnt<A * INSTS>();
       return;
     }
+    wait_stages<INSTS, A - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
   }
-  if constexpr (NS >= 3) {
-    if (ahead >= 1) {
-      wait_vmcnt<INSTS>();
-      return;
-    }
-  }
-  wait_vmcnt<0>();
 }
 
 __device__ inline void lds_barrier() {
@@ -230,20 +252,27 @@ __device__ inline void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Issues this wave's share of one operand tile (ROWS x 64 k) into `dst`.
-template <int ROWS, int NW>
+// Physical-chunk swizzle of LDS row R (see the top of this file).
+template <int BK>
+__device__ inline int dtl_swz(int R) {
+  return BK == 64 ? (R & 7) ^ ((R >> 3) & 1) : (R >> 2) & 3;
+}
+
+// Issues this wave's share of one operand tile (ROWS x BK k) into `dst`.
+template <int ROWS, int NW, int BK>
 __device__ inline void dtl_issue(char* dst, const bf16_t* __restrict__ g, int64_t ld, int64_t row0, int64_t rows,
                                  int64_t k0, int64_t kcap, int wave, int lane) {
-  const int rsub = lane >> 3;
+  constexpr int CH = BK / 8, RPI = 64 / CH;
+  const int rsub = lane / CH;
 #pragma unroll
-  for (int q = 0; q < ROWS / (8 * NW); ++q) {
-    const int R0 = (q * NW + wave) * 8;
-    const int c = (lane & 7) ^ rsub ^ ((R0 >> 3) & 1);
+  for (int q = 0; q < ROWS / (RPI * NW); ++q) {
+    const int R0 = (q * NW + wave) * RPI;
+    const int c = (lane % CH) ^ dtl_swz<BK>(R0 + rsub);
     int64_t gr = row0 + R0 + rsub;
     gr = gr < rows ? gr : rows - 1;
     int64_t gk = k0 + c * 8;
     gk = gk < kcap ? gk : kcap;
-    __builtin_amdgcn_global_load_lds((const void*)(g + gr * ld + gk), (lds_void_t*)(dst + R0 * 128), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(g + gr * ld + gk), (lds_void_t*)(dst + R0 * 2 * BK), 16, 0, 0);
   }
 }
 
@@ -278,8 +307,8 @@ __device__ inline void store4<bf16_t>(bf16_t* C, int64_t idx, const float* v, fl
     o[3] += beta * bf16_to_f32((bf16_t)(c.y >> 16));
   }
   uint2 w;
-  w.x = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
-  w.y = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+  w.x = pack_bf16x2(o[0], o[1]);
+  w.y = pack_bf16x2(o[2], o[3]);
   *(uint2*)(C + idx) = w;
 }
 
@@ -294,7 +323,7 @@ __device__ inline void store1<bf16_t>(bf16_t* C, int64_t idx, float v, float bet
   C[idx] = f32_to_bf16(beta != 0.f ? v + beta * bf16_to_f32(C[idx]) : v);
 }
 
-// Consumes one 64-k stage (four k16 steps). CFG::RD picks the LDS read schedule:
+// Consumes one BK-k stage (BK/16 k16 steps). CFG::RD picks the LDS read schedule:
 //   0  each step reads its fragments, then runs its MFMAs
 //   1  all fragments of the stage are read before the first MFMA
 //   2  software pipeline: step kk+1's reads are issued ahead of step kk's MFMAs
@@ -304,9 +333,9 @@ __device__ inline void dtl_read(const char* st, int a_off, int b_off, int sw, in
                                 int64_t kmin, int64_t kend, bf16x8 (&af)[CFG::TM], bf16x8 (&bfr)[CFG::TN]) {
   const int coff = ((2 * kk + (lane >> 5)) ^ sw) << 4;
 #pragma unroll
-  for (int i = 0; i < CFG::TM; ++i) af[i] = *(const bf16x8*)(st + a_off + i * 32 * 128 + coff);
+  for (int i = 0; i < CFG::TM; ++i) af[i] = *(const bf16x8*)(st + a_off + i * 32 * CFG::ROWB + coff);
 #pragma unroll
-  for (int j = 0; j < CFG::TN; ++j) bfr[j] = *(const bf16x8*)(st + b_off + j * 32 * 128 + coff);
+  for (int j = 0; j < CFG::TN; ++j) bfr[j] = *(const bf16x8*)(st + b_off + j * 32 * CFG::ROWB + coff);
   if (EDGE) {
     const int64_t kf = k0 + kk * 16 + (lane >> 5) * 8;
 #pragma unroll
@@ -329,25 +358,25 @@ __device__ inline void dtl_mfma(const bf16x8 (&af)[CFG::TM], const bf16x8 (&bfr)
 template <class CFG, bool EDGE>
 __device__ inline void dtl_stage(const char* st, int a_off, int b_off, int sw, int lane, int64_t k0, int64_t kmin,
                                  int64_t kend, f32x16 (&acc)[CFG::TM][CFG::TN]) {
-  constexpr int TM = CFG::TM, TN = CFG::TN;
+  constexpr int TM = CFG::TM, TN = CFG::TN, KK = CFG::KK;
   if constexpr (CFG::RD == 1) {
-    bf16x8 af[4][TM], bfr[4][TN];
+    bf16x8 af[KK][TM], bfr[KK][TN];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af[kk], bfr[kk]);
+    for (int kk = 0; kk < KK; ++kk) dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af[kk], bfr[kk]);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) dtl_mfma<CFG>(af[kk], bfr[kk], acc);
+    for (int kk = 0; kk < KK; ++kk) dtl_mfma<CFG>(af[kk], bfr[kk], acc);
   } else if constexpr (CFG::RD == 2) {
     bf16x8 af[2][TM], bfr[2][TN];
     dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, 0, k0, kmin, kend, af[0], bfr[0]);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      if (kk + 1 < 4)
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK)
         dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk + 1, k0, kmin, kend, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
       dtl_mfma<CFG>(af[kk & 1], bfr[kk & 1], acc);
     }
   } else {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < KK; ++kk) {
       bf16x8 af[TM], bfr[TN];
       dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af, bfr);
       dtl_mfma<CFG>(af, bfr, acc);
@@ -368,7 +397,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
   const int64_t kbeg = t.kbeg & ~(int64_t)7;  // 16-byte chunks start 8-aligned
   const int64_t kend = t.kend;
   const int64_t kcap = p.K - 8;  // last in-bounds chunk of a row
-  const int64_t nk = (kend - kbeg + 63) / 64;
+  constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
+  const int64_t nk = (kend - kbeg + BK - 1) / BK;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -380,26 +410,26 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
 
   auto issue = [&](int64_t kt) {
     char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    const int64_t k0 = kbeg + kt * 64;
-    dtl_issue<BM, NW>(st, t.A, p.lda, t.m0, p.M, k0, kcap, wave, lane);
-    dtl_issue<CFG::BN, NW>(st + BM * 128, t.B, p.ldb, t.n0, p.N, k0, kcap, wave, lane);
+    const int64_t k0 = kbeg + kt * BK;
+    dtl_issue<BM, NW, BK>(st, t.A, p.lda, t.m0, p.M, k0, kcap, wave, lane);
+    dtl_issue<CFG::BN, NW, BK>(st + BM * ROWB, t.B, p.ldb, t.n0, p.N, k0, kcap, wave, lane);
   };
 
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
 
-  const int sw = (lane & 7) ^ ((lane >> 3) & 1);
-  const int a_off = (wm * CFG::WTM + (lane & 31)) * 128;
-  const int b_off = BM * 128 + (wn * CFG::WTN + (lane & 31)) * 128;
+  const int sw = dtl_swz<BK>(lane & 31);  // fragment rows sit at multiples of 32 plus lane & 31
+  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
+  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int64_t left = nk - 1 - kt;
-    wait_stages<CFG::INSTS, NS>((int)(left < NS - 2 ? left : NS - 2));
+    wait_stages<CFG::INSTS, NS - 2>((int)(left < NS - 2 ? left : NS - 2));
     lds_barrier();
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
     const char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    const int64_t k0 = kbeg + kt * 64;
-    if (k0 < kmin || k0 + 64 > kend)
+    const int64_t k0 = kbeg + kt * BK;
+    if (k0 < kmin || k0 + BK > kend)
       dtl_stage<CFG, true>(st, a_off, b_off, sw, lane, k0, kmin, kend, acc);
     else
       dtl_stage<CFG, false>(st, a_off, b_off, sw, lane, k0, kmin, kend, acc);

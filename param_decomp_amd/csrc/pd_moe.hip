@@ -51,6 +51,24 @@ __device__ inline float bf_lo(uint32_t w) { return bf16_to_f32((bf16_t)(w & 0xFF
 __device__ inline float bf_hi(uint32_t w) { return bf16_to_f32((bf16_t)(w >> 16)); }
 __device__ inline uint32_t bf_pack(bf16_t a, bf16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
+// 8 consecutive bf16 values <-> fp32 through one 16-byte access (p 16-byte aligned).
+__device__ inline void load8(const bf16_t* p, float f[8]) {
+  const uint4 v = *(const uint4*)p;
+  f[0] = bf_lo(v.x), f[1] = bf_hi(v.x), f[2] = bf_lo(v.y), f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z), f[5] = bf_hi(v.z), f[6] = bf_lo(v.w), f[7] = bf_hi(v.w);
+}
+__device__ inline void store8(bf16_t* p, const float f[8]) {
+  *(uint4*)p = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                          pack_bf16x2(f[6], f[7]));
+}
+__device__ inline void load8f(const float* p, float f[8]) {
+  const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+  f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+}
+// Token-space kernels run one wave per token row, 4 waves per block; the wave index is
+// read into a scalar register so per-token indices and weights come in as scalar loads.
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // dst[b] = src[b]^T for B matrices of [R, Cc] (R, Cc multiples of 8).
 __global__ __launch_bounds__(256) void k_batched_transpose(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
                                                            bf16_t* __restrict__ dst) {
@@ -108,26 +126,33 @@ __global__ __launch_bounds__(256) void k_gather_tile(const bf16_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------- token-space kernels
-// One block (256 threads) per token row of width d: y = x * rsqrt(mean x^2 + eps) *
-// (1 + w), fp32 math, bf16 out; rinv saved for the backward.
+// Rows of width d (d % 8 == 0), lane l owning columns 8l..8l+7 of each 512-column chunk.
+// y = x * rsqrt(mean x^2 + eps) * (1 + w), fp32 math, bf16 out; rinv saved for the
+// backward.
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const bf16_t* __restrict__ x, int64_t T, int d,
                                                      const float* __restrict__ w, float eps, bf16_t* __restrict__ y,
                                                      float* __restrict__ rinv) {
-  const int64_t t = blockIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
   if (t >= T) return;
-  __shared__ float red[4];
+  const int lane = threadIdx.x & 63;
   const bf16_t* xr = x + t * d;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    float v = bf16_to_f32(xr[i]);
-    ss = fmaf(v, v, ss);
+  for (int i = lane * 8; i < d; i += 512) {
+    float v[8];
+    load8(xr + i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
   }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)d + eps);
-  if (threadIdx.x == 0 && rinv) rinv[t] = r;
-  for (int i = threadIdx.x; i < d; i += 256) y[t * d + i] = f32_to_bf16(bf16_to_f32(xr[i]) * r * (1.f + w[i]));
+  const float r = rsqrtf(wave_sum(ss) / (float)d + eps);
+  if (lane == 0 && rinv) rinv[t] = r;
+  for (int i = lane * 8; i < d; i += 512) {
+    float v[8], g[8];
+    load8(xr + i, v);
+    load8f(w + i, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * r * (1.f + g[j]);
+    store8(y + t * d + i, v);
+  }
 }
 
 // Masked-layer routing weights at pinned indices: probs = softmax(logits) (saved),
@@ -152,20 +177,30 @@ __global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__
 }
 
 // r_out[t,:] = bf16(r[t,:] + bf16(sum_s wt[t,s] * y[inv[t*k+s],:])) with fp32
-// accumulation; wt NULL = the unweighted sum_jobs.
+// accumulation in slot order; wt NULL = the unweighted sum_jobs. One wave per token.
 __global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restrict__ r, const bf16_t* __restrict__ y,
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ wt, int64_t T, int k, int d,
                                                           bf16_t* __restrict__ r_out) {
-  const int64_t t = blockIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
   if (t >= T) return;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    float acc = 0.f;
+  for (int i = (threadIdx.x & 63) * 8; i < d; i += 512) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, v[8];
     for (int s = 0; s < k; ++s) {
-      float v = bf16_to_f32(y[(int64_t)inv[t * k + s] * d + i]);
-      acc = wt ? fmaf(wt[t * k + s], v, acc) : acc + v;
+      load8(y + (int64_t)inv[t * k + s] * d + i, v);
+      if (wt) {
+        const float ws = wt[t * k + s];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(ws, v[j], acc[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += v[j];
+      }
     }
-    r_out[t * d + i] = f32_to_bf16(bf16_to_f32(r[t * d + i]) + bf16_to_f32(f32_to_bf16(acc)));
+    load8(r + t * d + i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = v[j] + bf16_to_f32(f32_to_bf16(acc[j]));
+    store8(r_out + t * d + i, acc);
   }
 }
 
@@ -397,10 +432,42 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
   ttile_store(Tu, d_uT, J, j0, J, q0, f, tid);
 }
 
-// Token backward, one block (256 threads) per token:
-//   d_w[s] = sum of the d_w_part tiles of job inv[t*k+s]; through w = p_sel / sum p_sel
-//   and the router softmax to d_logits[E] (wave 0, lanes = experts); d_h2 = sum_s
-//   (dxa + dxb)[inv[t*k+s]] + d_logits @ router; d_r_out = bf16(d_r + rms_norm_vjp).
+// d_logits[t, lane] of one token (lanes = experts, 0 past E), all 64 lanes active:
+// d_w[s] = sum of the d_w_part tiles of job inv[t*k+s], through w = p_sel / sum p_sel
+// and the router softmax.
+__device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int n_part,
+                                         const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
+                                         const float* __restrict__ probs, const float* __restrict__ w, int64_t t,
+                                         int E, int k, int lane) {
+  float dw = 0.f;
+  if (lane < k) {
+    const int64_t jj = inv[t * k + lane];
+    for (int pp = 0; pp < n_part; ++pp) dw += d_w_part[jj * n_part + pp];
+  }
+  const float wv = lane < k ? w[t * k + lane] : 0.f;
+  const float dot = wave_sum(dw * wv);
+  int e_of_slot = lane < k ? idx[t * k + lane] : -1;
+  if (lane < k) e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
+  const float pe = lane < E ? probs[t * E + lane] : 0.f;
+  const float psel = __shfl(pe, lane < k ? e_of_slot : 0, 64);  // all lanes shuffle
+  const float S = wave_sum(lane < k ? psel : 0.f);
+  const float dps = lane < k ? (dw - dot) / S : 0.f;
+  float dpe = 0.f;
+  for (int s = 0; s < k; ++s) {
+    const int es = __shfl(e_of_slot, s, 64);
+    const float v = __shfl(dps, s, 64);
+    if (lane == es) dpe += v;
+  }
+  const float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
+  return lane < E ? pe * (dpe - sdot) : 0.f;
+}
+
+// Token backward, one wave per TPW consecutive tokens, lane l owning columns 8l..8l+7 of
+// each of the NCH 512-column chunks (d <= 512 * NCH, d % 8 == 0):
+//   d_h2 = sum_s (dxa + dxb)[inv[t*k+s]] + d_logits @ router (slot sums first, then the
+//   experts in order, fp32); d_r_out = bf16(d_r + rms_norm_vjp(d_h2)). The TPW tokens of
+//   a wave share each 16-byte router load.
+template <int TPW, int NCH>
 __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w_part, int n_part,
                                                    const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
                                                    const float* __restrict__ probs, const float* __restrict__ w,
@@ -409,59 +476,115 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
                                                    const float* __restrict__ rinv, const float* __restrict__ ln,
                                                    const bf16_t* __restrict__ d_r, int64_t T, int E, int k, int d,
                                                    bf16_t* __restrict__ d_r_out) {
-  const int64_t t = blockIdx.x;
-  if (t >= T) return;
-  __shared__ float dlog[64];
-  __shared__ float red[4];
-  __shared__ float h2g[4096];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (wave == 0) {
-    float dw = 0.f;
-    if (lane < k) {
-      const int64_t jj = inv[t * k + lane];
-      for (int pp = 0; pp < n_part; ++pp) dw += d_w_part[jj * n_part + pp];
-    }
-    const float wv = lane < k ? w[t * k + lane] : 0.f;
-    const float dot = wave_sum(dw * wv);
-    int e_of_slot = lane < k ? idx[t * k + lane] : -1;
-    if (lane < k) e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
-    const float pe = lane < E ? probs[t * E + lane] : 0.f;
-    const float psel = __shfl(pe, lane < k ? e_of_slot : 0, 64);  // all lanes shuffle
-    const float S = wave_sum(lane < k ? psel : 0.f);
-    const float dps = lane < k ? (dw - dot) / S : 0.f;
-    float dpe = 0.f;
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave_id()) * TPW;
+  if (t0 >= T) return;
+  const int lane = threadIdx.x & 63;
+  float dl[TPW], a[TPW][NCH][8];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int64_t t = t0 + u;
+    dl[u] = t < T ? router_logit_vjp(d_w_part, n_part, inv, idx, probs, w, t, E, k, lane) : 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[u][c][j] = 0.f;
+    if (t >= T) continue;
     for (int s = 0; s < k; ++s) {
-      const int es = __shfl(e_of_slot, s, 64);
-      const float v = __shfl(dps, s, 64);
-      if (lane == es) dpe += v;
+      const int64_t row = (int64_t)inv[t * k + s] * d;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int i = c * 512 + lane * 8;
+        if (i < d) {
+          float va[8], vb[8];
+          load8(dxa + row + i, va);
+          load8(dxb + row + i, vb);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) a[u][c][j] += va[j] + vb[j];
+        }
+      }
     }
-    const float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
-    if (lane < E) dlog[lane] = pe * (dpe - sdot);
   }
-  __syncthreads();
-  const bf16_t* xr = r + t * d;
-  float part = 0.f;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    float acc = 0.f;
-    for (int s = 0; s < k; ++s) {
-      const int64_t row = (int64_t)inv[t * k + s] * d + i;
-      acc += bf16_to_f32(dxa[row]) + bf16_to_f32(dxb[row]);
+  for (int e = 0; e < E; ++e) {
+    float de[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) de[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl[u]), e));
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 512 + lane * 8;
+      if (i < d) {
+        float rv[8];
+        load8(router + (int64_t)e * d + i, rv);
+#pragma unroll
+        for (int u = 0; u < TPW; ++u)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) a[u][c][j] = fmaf(de[u], rv[j], a[u][c][j]);
+      }
     }
-    for (int e = 0; e < E; ++e) acc = fmaf(dlog[e], bf16_to_f32(router[(int64_t)e * d + i]), acc);
-    const float a = (1.f + ln[i]) * acc;
-    h2g[i] = a;
-    part = fmaf(a, bf16_to_f32(xr[i]), part);
   }
-  part = wave_sum(part);
-  if (lane == 0) red[wave] = part;
-  __syncthreads();
-  const float ax = red[0] + red[1] + red[2] + red[3];
-  const float rv = rinv[t];
-  const float c3 = rv * rv * rv * ax / (float)d;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    const float dx = rv * h2g[i] - bf16_to_f32(xr[i]) * c3;
-    d_r_out[t * d + i] = f32_to_bf16(bf16_to_f32(d_r[t * d + i]) + dx);
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int64_t t = t0 + u;
+    if (t >= T) break;
+    const bf16_t* xr = r + t * d;
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 512 + lane * 8;
+      if (i < d) {
+        float g[8], xv[8];
+        load8f(ln + i, g);
+        load8(xr + i, xv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          a[u][c][j] = (1.f + g[j]) * a[u][c][j];
+          part = fmaf(a[u][c][j], xv[j], part);
+        }
+      }
+    }
+    const float ax = wave_sum(part);
+    const float rv = rinv[t];
+    const float c3 = rv * rv * rv * ax / (float)d;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 512 + lane * 8;
+      if (i < d) {
+        float xv[8], dv[8];
+        load8(xr + i, xv);
+        load8(d_r + t * d + i, dv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dv[j] = dv[j] + (rv * a[u][c][j] - xv[j] * c3);
+        store8(d_r_out + t * d + i, dv);
+      }
+    }
   }
+}
+
+template <int TPW, int NCH>
+static void launch_token_bwd_t(const float* d_w_part, int n_part, const int32_t* inv, const int32_t* idx,
+                               const float* probs, const float* w, const bf16_t* router, const bf16_t* dxa,
+                               const bf16_t* dxb, const bf16_t* r, const float* rinv, const float* ln,
+                               const bf16_t* d_r, int64_t T, int E, int k, int d, bf16_t* d_r_out, hipStream_t s) {
+  hipLaunchKernelGGL((k_token_bwd<TPW, NCH>), dim3((unsigned)cdiv(T, 4 * TPW)), dim3(256), 0, s, d_w_part, n_part,
+                     inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d, d_r_out);
+}
+
+// d <= 4096 (checked by the step): the column chunks per lane set the register tile.
+static void launch_token_bwd(const float* d_w_part, int n_part, const int32_t* inv, const int32_t* idx,
+                             const float* probs, const float* w, const bf16_t* router, const bf16_t* dxa,
+                             const bf16_t* dxb, const bf16_t* r, const float* rinv, const float* ln, const bf16_t* d_r,
+                             int64_t T, int E, int k, int d, bf16_t* d_r_out, hipStream_t s) {
+  if (d <= 512)
+    launch_token_bwd_t<2, 1>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
+                             d_r_out, s);
+  else if (d <= 1024)
+    launch_token_bwd_t<2, 2>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
+                             d_r_out, s);
+  else if (d <= 2048)
+    launch_token_bwd_t<1, 4>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
+                             d_r_out, s);
+  else
+    launch_token_bwd_t<1, 8>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
+                             d_r_out, s);
 }
 
 __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, const float* __restrict__ imp_part,
@@ -723,7 +846,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   bf16_t* rnext = P.rc_b;
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
-    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)T), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
+    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
                        P.h2c, (float*)nullptr);
     if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, P.h2c, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
                       PD_DTYPE_F32, 1.f, 0.f, stream)))
@@ -741,7 +864,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                        S.sort_idx, J, f, P.din, (bf16_t*)nullptr);
     if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
       return rc;
-    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
                        rnext);
     std::swap(rcur, rnext);
     if (top_idx_out)
@@ -756,7 +879,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     LayerSave& S = P.layers[l];
     rec.mark(MOE_CAT_NORM_ROUTE);
     if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
-    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)T), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f, S.h2,
+    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f, S.h2,
                        S.rinv);
     if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
                       PD_DTYPE_F32, 1.f, 0.f, stream)))
@@ -808,7 +931,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
-    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)T), dim3(256), 0, s, S.r, P.down, S.inv,
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, P.down, S.inv,
                        (const float*)nullptr, T, k, d, r_out);
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
@@ -886,9 +1009,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     // ---- routing weights, router, gather VJP and the norm
     rec.mark(MOE_CAT_TOKEN_BWD);
-    hipLaunchKernelGGL(k_token_bwd, dim3((unsigned)T), dim3(256), 0, s, P.d_w_part, n_wpart, S.inv, S.idx, S.probs,
-                       S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb, S.r, S.rinv, ln + (size_t)l * d, dr, T, E,
-                       k, d, dr_next);
+    launch_token_bwd(P.d_w_part, n_wpart, S.inv, S.idx, S.probs, S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb,
+                     S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, dr_next, s);
     std::swap(dr, dr_next);
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
   }
