@@ -1,22 +1,23 @@
-// GEMM kernels for the masked-component path (gfx950).
+// GEMM kernels for the masked-component path (gfx950), v_mfma_f32_32x32x16_bf16.
 //
-// bf16 path: v_mfma_f32_32x32x16_bf16, LDS double-buffered through registers. Two tile
-// configurations share one template:
-//   BIG   256x256x64, 8 waves (2x4), 128x64 per wave (4x2 MFMA tiles), 144 KB LDS —
-//         one block per CU; halves the L2 re-read per FLOP of a 128x128 tile.
-//   SMALL 128x128x64, 4 waves (2x2), 64x64 per wave — for grids the big tile leaves
+// Both operands K-contiguous (every hot-path product): the buffer-fed kernel of
+// pd_gemm_dtl.hpp, 128x128x64 tiles, 8 waves of 32x64, operands loaded straight into
+// LDS, two stages, two blocks per CU.
+//
+// Any other operand layout: the register-staged kernel below. LDS holds both operands
+// K-contiguous ([rows][BK+8]; the 144-byte row stride makes a wave's 16-byte fragment
+// reads of 16 consecutive rows hit 16 distinct 4-bank groups); an operand whose global
+// layout is MN-contiguous is transposed in registers (4 k-rows x 8 elements per thread)
+// on its way into LDS. Two tile configurations:
+//   BIG   256x256x64, 8 waves (2x4), 128x64 per wave (4x2 MFMA tiles), 144 KB LDS
+//   SMALL 128x128x64, 4 waves (2x2), 64x64 per wave, for grids the big tile leaves
 //         under-occupied (fewer than ~200 tiles on 256 CUs).
-// LDS holds both operands K-contiguous ([rows][BK+8]; the 144-byte row stride makes a
-// wave's 16-byte fragment reads of 16 consecutive rows hit 16 distinct 4-bank groups).
-// An operand whose global layout is MN-contiguous is transposed in registers (4 k-rows
-// x 8 elements per thread) on its way into LDS; the hot paths avoid that layout by
-// having producers write K-contiguous copies.
 //
 // Dense launches use an XCD-aware tile order: workgroups are dispatched round-robin
 // over the 8 XCDs, so the linear id is remapped so each XCD's share is a compact
 // 8-row-grouped region (fewer distinct A/B panels per XCD-local L2).
 //
-// Four problem mappings share the kernel:
+// Four problem mappings share the kernels:
 //   DENSE     C = alpha*op(A)@op(B) + beta*C                  (x@V, acts@U, transposes)
 //   GROUPED   out[rows_e] = lhs[rows_e] @ rhs[e], ragged rows  (pd/routed/experts.py:326-348)
 //   GROUPED_K out[e] = lhs[rows_e]^T @ dout[rows_e]            (pd/routed/experts.py:209-280)
@@ -286,17 +287,27 @@ static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) 
 // The big tile needs enough tiles to occupy the 256 CUs; otherwise use the small one.
 static bool use_big_tile(int64_t M, int64_t N) { return cdiv(M, 256) * cdiv(N, 256) >= 192; }
 
-// Direct-to-LDS kernel for K-contiguous operands: 128x128 tiles, 8 waves (4x2, 32x64 per
-// wave), 2 LDS stages (64 KB, two blocks per CU), reads one k16 step ahead.
-typedef DtlCfg<128, 128, 4, 2, 2, 2> CfgDtl;
+// Buffer-fed kernel for K-contiguous operands: 128x128 tiles, 8 waves (4x2, 32x64 per
+// wave), 2 LDS stages (64 KB, two blocks per CU).
+typedef DtlCfg<128, 128, 4, 2, 2> CfgDtl;
+
+// The kernel addresses each operand through a 31-bit buffer record count.
+static bool dtl_fits(int64_t rows_a, int64_t lda, int64_t rows_b, int64_t ldb) {
+  return rows_a * lda * 2 <= 0x7FFFFFFF && rows_b * ldb * 2 <= 0x7FFFFFFF;
+}
 
 template <class CFG, int MODE>
-static int launch_dtl(const GemmArgs& a, int c_dtype, dim3 grid, hipStream_t s) {
-  if (c_dtype == PD_DTYPE_F32)
-    hipLaunchKernelGGL((k_gemm_dtl<CFG, float, MODE>), grid, dim3(CFG::NT), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_gemm_dtl<CFG, bf16_t, MODE>), grid, dim3(CFG::NT), 0, s, a);
-  return check_launch("pd_gemm bf16 (direct-to-LDS)");
+static int launch_dtl(const GemmArgs& a, int c_dtype, bool kedge, dim3 grid, hipStream_t s) {
+#define PD_L(TC, KE) hipLaunchKernelGGL((k_gemm_dtl<CFG, TC, MODE, KE>), grid, dim3(CFG::NT), 0, s, a)
+  if (c_dtype == PD_DTYPE_F32) {
+    if (kedge) PD_L(float, true);
+    else PD_L(float, false);
+  } else {
+    if (kedge) PD_L(bf16_t, true);
+    else PD_L(bf16_t, false);
+  }
+#undef PD_L
+  return check_launch("pd_gemm bf16 (buffer-fed)");
 }
 
 }  // namespace pd
@@ -323,6 +334,9 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
   if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N))
     return fail(PD_EUNSUPPORTED, "pd_gemm: bf16 operands need 16B alignment and contiguous dims / ld % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, 0, 0};
+  if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
+    return launch_dtl<CfgDtl, MODE_DENSE>(a, c_dtype, K % CfgDtl::BK != 0,
+                                          dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(M, CfgDtl::BM)), s);
   if (use_big_tile(M, N))
     return launch_bf16<CfgBig, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
                                            dim3((unsigned)cdiv(N, 256), (unsigned)cdiv(M, 256)), s);
@@ -355,6 +369,10 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
                 "pd_gemm_strided_batched: bf16 operands need 16B alignment, ld and batch strides % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, stride_b,
              stride_c, stride_a};
+  if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
+    return launch_dtl<CfgDtl, MODE_BATCHED>(
+        a, c_dtype, K % CfgDtl::BK != 0, dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(M, CfgDtl::BM), (unsigned)batch),
+        s);
   return launch_bf16<CfgSmall, MODE_BATCHED>(
       a, a_kmaj, b_kmaj, c_dtype, dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)batch), s);
 }
@@ -387,7 +405,7 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
   int64_t max_tiles = cdiv(J, CfgSmall::BM) + E;
   if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: too many rows");
   dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)max_tiles);
-  if (b_kmaj) return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, grid, s);
+  if (b_kmaj && dtl_fits(J, K, N, K)) return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, K % CfgDtl::BK != 0, grid, s);
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
@@ -403,7 +421,9 @@ int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const voi
              (const bf16_t*)lhs2, (const bf16_t*)rhsT2, out2};
   const int64_t max_tiles = cdiv(J, CfgDtl::BM) + E;
   if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: too many rows");
-  return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)max_tiles, 2),
+  if (!dtl_fits(J, K, N, K)) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: operands of 2 GiB or more");
+  return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, K % CfgDtl::BK != 0,
+                                          dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)max_tiles, 2),
                                           (hipStream_t)stream);
 }
 
@@ -419,8 +439,9 @@ int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out
     return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: size");
   GemmArgs a{K, N, J, (const bf16_t*)lhsT1, J, (const bf16_t*)doutT1, J, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
              (const bf16_t*)lhsT2, (const bf16_t*)doutT2, out2};
+  if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: operands of 2 GiB or more");
   dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)(2 * E));
-  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, grid, (hipStream_t)stream);
+  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // namespace pd
@@ -450,8 +471,9 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
   // (J == 0: every group has an empty k range, no loads are issued, out = 0)
   // out[e] (M=K x N) = lhsT[:, rows_e] (A stored [K, J]: K-major) @ doutT[:, rows_e]^T (B stored [N, J])
   GemmArgs a{K, N, J, (const bf16_t*)lhsT, J, (const bf16_t*)doutT, J, out, N, 1.f, 0.f, offsets, E, 0, K * N};
+  if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw_kmajor: operands of 2 GiB or more");
   dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)E);
-  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, grid, (hipStream_t)stream);
+  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // extern "C"

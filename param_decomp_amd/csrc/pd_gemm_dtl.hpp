@@ -1,12 +1,17 @@
-// bf16 GEMM with both operands K-contiguous, fed by direct global->LDS loads (gfx950).
+// bf16 GEMM with both operands K-contiguous, fed into LDS by buffer loads
+// (buffer_load_dwordx4 ... lds, gfx950).
 //
-// Operand tiles (rows x BK k, BK = 64 or 32) live in LDS as 2*BK-byte rows without
-// padding. The 16-byte chunk c of row R sits at physical chunk c ^ swz(R), with
-// swz(R) = (R & 7) ^ ((R >> 3) & 1) for 128-byte rows and (R >> 2) & 3 for 64-byte rows,
+// Operand tiles (rows x 64 k) live in LDS as 128-byte rows without padding. The 16-byte
+// chunk c of row R sits at physical chunk c ^ swz(R), swz(R) = (R & 7) ^ ((R >> 3) & 1),
 // so the 16 consecutive rows a quarter-wave fragment read touches cover all 64 banks.
-// Each global_load_lds_dwordx4 moves one 1 KB block of whole rows: lane l writes physical
-// chunk l % (BK/8) of row l / (BK/8), so it fetches the logical chunk the swizzle puts
-// there.
+// Each load instruction moves one 1 KB block of whole rows: lane l writes physical chunk
+// l % 8 of row l / 8, so it fetches the logical chunk the swizzle puts there.
+//
+// Operand addressing: a tile's rows start at a per-tile buffer descriptor base (scalar
+// registers); each load's per-lane byte offset (row within the tile, swizzled chunk) is
+// computed once per kernel and the stage's k position is added to it. The descriptor's
+// record count ends at the operand's last row, so rows past the operand extent, and
+// chunks past the end of its last row, load as zeros; their outputs are never stored.
 //
 // NS LDS stages form a ring with NS-1 k-tiles in flight: iteration kt waits (vmcnt) until
 // its own tile has landed, one s_barrier makes it visible and frees the stage of tile
@@ -18,9 +23,8 @@
 // ends with 4 consecutive output columns of one row per 4 accumulators; the epilogue
 // writes them as one 8-byte (bf16) or 16-byte (fp32) store.
 //
-// Rows past the operand extent are clamped to the last row (their outputs are never
-// stored); k chunks past the row end are clamped in-bounds and, with k < kmin (ragged
-// contraction groups start at an 8-aligned k), zeroed in the fragments of the edge tiles.
+// Ragged contraction groups start at an 8-aligned k below the group's first row; k
+// outside [kmin, kend) is zeroed in the fragments of a tile's first and last stage.
 #pragma once
 
 #include "pd_common.hpp"
@@ -206,18 +210,18 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   return t.m0 < t.M && t.n0 < p.N;
 }
 
-template <int BM_, int BN_, int WM_, int WN_, int NS_, int RD_ = 0, int BK_ = 64>
+template <int BM_, int BN_, int WM_, int WN_, int NS_>
 struct DtlCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, RD = RD_, BK = BK_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, NS = NS_, BK = 64;
   static constexpr int NW = WM_ * WN_, NT = NW * 64;
   static constexpr int WTM = BM_ / WM_, WTN = BN_ / WN_;  // wave tile
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int ROWB = 2 * BK_, RPI = 1024 / ROWB;  // LDS row bytes, rows per 1 KB load
-  static constexpr int KK = BK_ / 16;                      // k16 MFMA steps per stage
+  static constexpr int ROWB = 128, RPI = 8;  // LDS row bytes, rows per 1 KB load
+  static constexpr int KK = BK / 16;         // k16 MFMA steps per stage
   static constexpr int STAGE_BYTES = (BM_ + BN_) * ROWB;
   static constexpr int A_INSTS = BM_ / (RPI * NW), B_INSTS = BN_ / (RPI * NW);  // 1 KB loads per wave per stage
   static constexpr int INSTS = A_INSTS + B_INSTS;
-  static_assert(BK_ == 64 || BK_ == 32, "stage depth");
+  static_assert(NW % 2 == 0, "the swizzle parity of a wave's rows must not depend on the load index");
   static_assert(BM_ % (RPI * NW) == 0 && BN_ % (RPI * NW) == 0, "every wave moves whole 1 KB row blocks");
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile is a multiple of 32x32");
   static_assert(NS_ >= 2 && INSTS * (NS_ - 2) < 64, "vmcnt range");
@@ -253,27 +257,47 @@ __device__ inline void lds_barrier() {
 }
 
 // Physical-chunk swizzle of LDS row R (see the top of this file).
-template <int BK>
-__device__ inline int dtl_swz(int R) {
-  return BK == 64 ? (R & 7) ^ ((R >> 3) & 1) : (R >> 2) & 3;
+__device__ inline int dtl_swz(int R) { return (R & 7) ^ ((R >> 3) & 1); }
+
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ inline int64_t uni64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// Issues this wave's share of one operand tile (ROWS x BK k) into `dst`.
-template <int ROWS, int NW, int BK>
-__device__ inline void dtl_issue(char* dst, const bf16_t* __restrict__ g, int64_t ld, int64_t row0, int64_t rows,
-                                 int64_t k0, int64_t kcap, int wave, int lane) {
-  constexpr int CH = BK / 8, RPI = 64 / CH;
-  const int rsub = lane / CH;
+// Record count (bytes) of a raw buffer descriptor, clamped to the 31-bit range (the
+// launchers keep every operand below 2 GiB).
+__device__ inline int32_t buf_bytes(int64_t bytes) {
+  return bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (bytes < 0 ? 0 : (int32_t)bytes);
+}
+
+// Per-lane byte offsets of a wave's 1 KB row-block loads of one operand tile (relative
+// to the tile's first row, k = 0): lane l fills physical chunk l % 8 of row l / 8 of the
+// block, i.e. logical chunk (l % 8) ^ swz(row); the block of load q starts at row
+// (q * NW + wave) * 8, so swz's parity bit is wave & 1 for every q.
+template <int ROWS, int NW>
+__device__ inline void dtl_offsets(uint32_t (&off)[ROWS / (8 * NW)], int64_t ld, int wave, int lane) {
+  const int rsub = lane >> 3;
+  const int c = (lane & 7) ^ rsub ^ (wave & 1);
 #pragma unroll
-  for (int q = 0; q < ROWS / (RPI * NW); ++q) {
-    const int R0 = (q * NW + wave) * RPI;
-    const int c = (lane % CH) ^ dtl_swz<BK>(R0 + rsub);
-    int64_t gr = row0 + R0 + rsub;
-    gr = gr < rows ? gr : rows - 1;
-    int64_t gk = k0 + c * 8;
-    gk = gk < kcap ? gk : kcap;
-    __builtin_amdgcn_global_load_lds((const void*)(g + gr * ld + gk), (lds_void_t*)(dst + R0 * 2 * BK), 16, 0, 0);
+  for (int q = 0; q < ROWS / (8 * NW); ++q) {
+    const int64_t row = (int64_t)(q * NW + wave) * 8 + rsub;
+    off[q] = (uint32_t)((row * ld + c * 8) * 2);
   }
+}
+
+// One stage of one operand at byte offset koff (the stage's k position) within each
+// row. The descriptor spans [base, base + bytes) (stride 0); the whole offset goes in the
+// per-lane register so the record-count check covers it.
+template <int ROWS, int NW>
+__device__ inline void dtl_issue(char* dst, const bf16_t* base, int32_t bytes, const uint32_t* off, uint32_t koff,
+                                 int wave) {
+  const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, bytes, 0x00020000);
+#pragma unroll
+  for (int q = 0; q < ROWS / (8 * NW); ++q)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst + (q * NW + wave) * 8 * 128), 16, off[q] + koff,
+                                             0, 0, 0);
 }
 
 __device__ inline void mask_frag(bf16x8& v, int64_t k, int64_t kmin, int64_t kend) {
@@ -323,11 +347,7 @@ __device__ inline void store1<bf16_t>(bf16_t* C, int64_t idx, float v, float bet
   C[idx] = f32_to_bf16(beta != 0.f ? v + beta * bf16_to_f32(C[idx]) : v);
 }
 
-// Consumes one BK-k stage (BK/16 k16 steps). CFG::RD picks the LDS read schedule:
-//   0  each step reads its fragments, then runs its MFMAs
-//   1  all fragments of the stage are read before the first MFMA
-//   2  software pipeline: step kk+1's reads are issued ahead of step kk's MFMAs
-// EDGE zeroes k outside [kmin, kend).
+// Fragment reads of k16 step kk of a stage; EDGE zeroes k outside [kmin, kend).
 template <class CFG, bool EDGE>
 __device__ inline void dtl_read(const char* st, int a_off, int b_off, int sw, int lane, int kk, int64_t k0,
                                 int64_t kmin, int64_t kend, bf16x8 (&af)[CFG::TM], bf16x8 (&bfr)[CFG::TN]) {
@@ -355,95 +375,33 @@ __device__ inline void dtl_mfma(const bf16x8 (&af)[CFG::TM], const bf16x8 (&bfr)
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
 }
 
+// Consumes one 64-k stage (4 k16 steps), reading step kk+1's fragments ahead of step
+// kk's MFMAs.
 template <class CFG, bool EDGE>
 __device__ inline void dtl_stage(const char* st, int a_off, int b_off, int sw, int lane, int64_t k0, int64_t kmin,
                                  int64_t kend, f32x16 (&acc)[CFG::TM][CFG::TN]) {
   constexpr int TM = CFG::TM, TN = CFG::TN, KK = CFG::KK;
-  if constexpr (CFG::RD == 1) {
-    bf16x8 af[KK][TM], bfr[KK][TN];
+  bf16x8 af[2][TM], bfr[2][TN];
+  dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, 0, k0, kmin, kend, af[0], bfr[0]);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af[kk], bfr[kk]);
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) dtl_mfma<CFG>(af[kk], bfr[kk], acc);
-  } else if constexpr (CFG::RD == 2) {
-    bf16x8 af[2][TM], bfr[2][TN];
-    dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, 0, k0, kmin, kend, af[0], bfr[0]);
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if (kk + 1 < KK)
-        dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk + 1, k0, kmin, kend, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
-      dtl_mfma<CFG>(af[kk & 1], bfr[kk & 1], acc);
-    }
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      bf16x8 af[TM], bfr[TN];
-      dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af, bfr);
-      dtl_mfma<CFG>(af, bfr, acc);
-    }
+  for (int kk = 0; kk < KK; ++kk) {
+    if (kk + 1 < KK)
+      dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk + 1, k0, kmin, kend, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
+    dtl_mfma<CFG>(af[kk & 1], bfr[kk & 1], acc);
   }
 }
 
-template <class CFG, typename TC, int MODE>
-__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
-  constexpr int BM = CFG::BM, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
-  __shared__ __attribute__((aligned(1024))) char smem[NS * CFG::STAGE_BYTES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / CFG::WN, wn = wave % CFG::WN;
-
-  TileJob t;
-  if (!map_tile<BM, CFG::BN, MODE, TC>(p, lane, t)) return;
-  const int64_t kmin = t.kbeg;
-  const int64_t kbeg = t.kbeg & ~(int64_t)7;  // 16-byte chunks start 8-aligned
-  const int64_t kend = t.kend;
-  const int64_t kcap = p.K - 8;  // last in-bounds chunk of a row
-  constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
-  const int64_t nk = (kend - kbeg + BK - 1) / BK;
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  auto issue = [&](int64_t kt) {
-    char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    const int64_t k0 = kbeg + kt * BK;
-    dtl_issue<BM, NW, BK>(st, t.A, p.lda, t.m0, p.M, k0, kcap, wave, lane);
-    dtl_issue<CFG::BN, NW, BK>(st + BM * ROWB, t.B, p.ldb, t.n0, p.N, k0, kcap, wave, lane);
-  };
-
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s);
-
-  const int sw = dtl_swz<BK>(lane & 31);  // fragment rows sit at multiples of 32 plus lane & 31
-  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
-  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int64_t left = nk - 1 - kt;
-    wait_stages<CFG::INSTS, NS - 2>((int)(left < NS - 2 ? left : NS - 2));
-    lds_barrier();
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
-    const char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    const int64_t k0 = kbeg + kt * BK;
-    if (k0 < kmin || k0 + BK > kend)
-      dtl_stage<CFG, true>(st, a_off, b_off, sw, lane, k0, kmin, kend, acc);
-    else
-      dtl_stage<CFG, false>(st, a_off, b_off, sw, lane, k0, kmin, kend, acc);
-  }
-
-  // lane holds row (lane & 31) of each 32x32 block and columns 8g + 4(lane >> 5) + 0..3
+template <class CFG, typename TC>
+__device__ inline void dtl_epilogue(const GemmArgs& p, const TileJob& t, int wm, int wn, int lane,
+                                    f32x16 (&acc)[CFG::TM][CFG::TN]) {
   TC* C = (TC*)t.C;
   const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)C & (4 * sizeof(TC) - 1)) == 0;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int i = 0; i < CFG::TM; ++i) {
     const int64_t row = t.m0 + wm * CFG::WTM + i * 32 + (lane & 31);
     if (row >= t.M) continue;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int j = 0; j < CFG::TN; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t col = t.n0 + wn * CFG::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
@@ -458,6 +416,84 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
       }
     }
   }
+}
+
+// KEDGE: some stages cover k outside [kmin, kend) and are masked (ragged contraction
+// groups, or K % 64 != 0). Only a tile's first and last stage can be such stages, so they
+// are peeled off the main loop, which then has a single body: a branch between a masked
+// and a plain stage inside the loop makes the compiler shuttle the accumulators between
+// AGPRs and VGPRs on every iteration.
+template <class CFG, typename TC, int MODE, bool KEDGE>
+__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
+  constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
+  constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
+  __shared__ __attribute__((aligned(1024))) char smem[NS * CFG::STAGE_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = uni(tid >> 6);
+  const int wm = wave / CFG::WN, wn = wave % CFG::WN;
+
+  TileJob t;
+  if (!map_tile<BM, BN, MODE, TC>(p, lane, t)) return;
+  // every tile field is wave-uniform; say so, so the descriptors stay in scalar registers
+  const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
+  const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
+  const int64_t kbeg = kmin & ~(int64_t)7;
+  const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
+  const bf16_t* abase = (const bf16_t*)uni64((int64_t)(t.A + m0 * p.lda));
+  const bf16_t* bbase = (const bf16_t*)uni64((int64_t)(t.B + n0 * p.ldb));
+  const int32_t abytes = buf_bytes((p.M - m0) * p.lda * 2), bbytes = buf_bytes((p.N - n0) * p.ldb * 2);
+  uint32_t offa[CFG::A_INSTS], offb[CFG::B_INSTS];
+  dtl_offsets<BM, NW>(offa, p.lda, wave, lane);
+  dtl_offsets<BN, NW>(offb, p.ldb, wave, lane);
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto issue = [&](int64_t kt) {
+    char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
+    const uint32_t koff = (uint32_t)((kbeg + kt * BK) * 2);
+    dtl_issue<BM, NW>(st, abase, abytes, offa, koff, wave);
+    dtl_issue<BN, NW>(st + BM * ROWB, bbase, bbytes, offb, koff, wave);
+  };
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+
+  const int sw = dtl_swz(lane & 31);  // fragment rows sit at multiples of 32 plus lane & 31
+  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
+  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
+  auto sync = [&](int64_t kt) {  // stage kt has landed and is visible; stage kt+NS-1 goes out
+    const int64_t left = nk - 1 - kt;
+    wait_stages<CFG::INSTS, NS - 2>((int)(left < NS - 2 ? left : NS - 2));
+    lds_barrier();
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+  };
+  auto st_of = [&](int64_t kt) { return smem + (int)(kt % NS) * CFG::STAGE_BYTES; };
+  if constexpr (KEDGE) {
+    if (nk > 0) {
+      sync(0);
+      dtl_stage<CFG, true>(st_of(0), a_off, b_off, sw, lane, kbeg, kmin, kend, acc);
+    }
+    for (int64_t kt = 1; kt < nk - 1; ++kt) {
+      sync(kt);
+      dtl_stage<CFG, false>(st_of(kt), a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
+    }
+    if (nk > 1) {
+      sync(nk - 1);
+      dtl_stage<CFG, true>(st_of(nk - 1), a_off, b_off, sw, lane, kbeg + (nk - 1) * BK, kmin, kend, acc);
+    }
+  } else {
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      sync(kt);
+      dtl_stage<CFG, false>(st_of(kt), a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
+    }
+  }
+  dtl_epilogue<CFG, TC>(p, t, wm, wn, lane, acc);
 }
 
 }  // namespace pd
