@@ -62,17 +62,49 @@ def rocprof_summary(db_path: str, command: str) -> str:
     return "\n".join(out) + "\n"
 
 
-def roofline(kind, amount_per_launch, ms_per_launch, kernel, launches_per_step):
+# The kernel behind each phase, as named in profiles/hbm_traffic_pmc.md (a prefix of the
+# demangled name: the phases of one kernel template share its per-dispatch average).
+PHASE_KERNEL = {
+    MOE: {"gemm_fwd": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 1,",
+          "gemm_dx": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 1,",
+          "gemm_dw": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 2,",
+          "mask_fwd": "pd::k_mask_fwd_tile", "mask_bwd": "pd::k_mask_bwd_tile"},
+    DENSE: {"gate_mask_fwd": "pd::k_step_fwd", "gate_mask_bwd": "pd::k_step_bwd", "recon": "pd::k_step_recon",
+            "gemm_xV": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
+            "gemm_actsU": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
+            "gemm_da": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
+            "gemm_dU": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 0,",
+            "gemm_dV": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 0,"},
+}
+
+
+def pmc_traffic(workload, phase):
+    """Calibrated HBM bytes per dispatch of the phase's kernel from the committed PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs scaled by a 1 GiB copy), or None."""
+    prefix = PHASE_KERNEL.get(workload, {}).get(phase)
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    if prefix is None or not os.path.exists(path):
+        return None
+    section = None
+    for line in open(path):
+        if line.startswith("## "):
+            section = line[3:].strip()
+        elif section == workload and line.startswith("| `") and line.split("`")[1].startswith(prefix):
+            return float(line.rstrip().rstrip("|").split("|")[-1])
+    return None
+
+
+def roofline(kind, amount_per_launch, ms_per_launch, kernel, launches_per_step, traffic=None):
     dur = ms_per_launch * 1e-3
     if kind == "flop":
         achieved = amount_per_launch / dur / 1e12
         return {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / (PEAK_BF16_FLOPS / 1e12), "traffic": None, "kernel": kernel,
+                "frac": achieved / (PEAK_BF16_FLOPS / 1e12), "traffic": traffic, "kernel": kernel,
                 "avg_launch_ms": ms_per_launch, "work_per_launch": amount_per_launch,
                 "launches_per_step": launches_per_step}
     achieved = amount_per_launch / dur / 1e9
     return {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": achieved / (PEAK_HBM / 1e9), "traffic": None, "kernel": kernel, "avg_launch_ms": ms_per_launch,
+            "frac": achieved / (PEAK_HBM / 1e9), "traffic": traffic, "kernel": kernel, "avg_launch_ms": ms_per_launch,
             "work_per_launch": amount_per_launch, "launches_per_step": launches_per_step}
 
 
@@ -173,7 +205,7 @@ def run_dense(args):
         "tokens": T, "ms_per_step": ms_per_step,
         "config": {"workload": DENSE, "tokens": T, "d_in": d_in, "d_out": d_out, "C": C, "gate_hidden": 16,
                    "imp_min": "p=2", "recon": "mse", "mask_draw": "threefry bf16 (partitionable)"},
-        "step_flops": step_flops, "phases_ms": phase_ms, "roofline": roofline(kind, amount, phase_ms[dom], dom, 1),
+        "step_flops": step_flops, "phases_ms": phase_ms, "roofline": roofline(kind, amount, phase_ms[dom], dom, 1, pmc_traffic(DENSE, dom)),
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = dense_cpu_baseline(args.cpu_tokens, d_in, d_out, C)
@@ -286,7 +318,7 @@ def run_moe(args):
     dom = max((n for n in cat_ms if n in work), key=cat_ms.get)
     kind, amount = work[dom]
     launches = cat_n[dom]
-    roof = roofline(kind, amount / launches, cat_ms[dom] / launches, dom, launches)
+    roof = roofline(kind, amount / launches, cat_ms[dom] / launches, dom, launches, pmc_traffic(MOE, dom))
     res = {
         "tokens": T, "ms_per_step": ms_per_step,
         "config": {"workload": MOE, "tokens": T, "width": d, "experts": E, "top_k": k, "expert_ffn": f,

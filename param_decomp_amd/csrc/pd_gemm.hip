@@ -287,18 +287,10 @@ static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) 
 // The big tile needs enough tiles to occupy the 256 CUs; otherwise use the small one.
 static bool use_big_tile(int64_t M, int64_t N) { return cdiv(M, 256) * cdiv(N, 256) >= 192; }
 
-// Buffer-fed kernel for K-contiguous operands: 128x128 tiles, 8 waves (4x2, 32x64 per
-// wave), 2 LDS stages (64 KB, two blocks per CU).
-typedef DtlCfg<128, 128, 4, 2, 2> CfgDtl;
-
-// The kernel addresses each operand through a 31-bit buffer record count.
-static bool dtl_fits(int64_t rows_a, int64_t lda, int64_t rows_b, int64_t ldb) {
-  return rows_a * lda * 2 <= 0x7FFFFFFF && rows_b * ldb * 2 <= 0x7FFFFFFF;
-}
-
 template <class CFG, int MODE>
 static int launch_dtl(const GemmArgs& a, int c_dtype, bool kedge, dim3 grid, hipStream_t s) {
-#define PD_L(TC, KE) hipLaunchKernelGGL((k_gemm_dtl<CFG, TC, MODE, KE>), grid, dim3(CFG::NT), 0, s, a)
+#define PD_L(TC, KE) \
+  hipLaunchKernelGGL((k_gemm_dtl<CFG, TC, MODE, KE>), grid, dim3(CFG::NT), 0, s, a, EpiStore::Args{})
   if (c_dtype == PD_DTYPE_F32) {
     if (kedge) PD_L(float, true);
     else PD_L(float, false);

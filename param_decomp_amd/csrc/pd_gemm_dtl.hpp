@@ -105,6 +105,8 @@ struct TileJob {
   const bf16_t* A;
   const bf16_t* B;
   void* C;
+  int prob;    // 0, or 1 for the second problem of a paired launch
+  int64_t lin;  // GROUPED: the tile's index within its problem, < (J / BM + E) * ceil(N / BN)
 };
 
 // Maps this block to its tile (the four problem mappings); false = no work.
@@ -116,6 +118,8 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   t.C = p.C;
   t.kbeg = 0;
   t.kend = p.K;
+  t.prob = 0;
+  t.lin = 0;
   if (MODE == MODE_DENSE) {
     int my, nx;
     dense_tile(my, nx);
@@ -138,8 +142,10 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
         t.A = p.A2;
         t.B = p.B2;
         t.C = p.C2;
+        t.prob = 1;
       }
       t.n0 = (lr % gx) * BN;
+      t.lin = lr;
       tile = (int)(lr / gx);
       return true;
     };
@@ -199,6 +205,7 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
       t.A = p.A2;
       t.B = p.B2;
       t.C = p.C2;
+      t.prob = 1;
     }
     t.m0 = (lr % gxy) / gx * BM;
     t.n0 = (lr % gx) * BN;
@@ -264,6 +271,14 @@ __device__ inline int64_t uni64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
   return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// 128x128x64 tiles, 8 waves (4x2, 32x64 per wave), 2 LDS stages (64 KB, two blocks per CU).
+typedef DtlCfg<128, 128, 4, 2, 2> CfgDtl;
+
+// The kernel addresses each operand through a 31-bit buffer record count.
+inline bool dtl_fits(int64_t rows_a, int64_t lda, int64_t rows_b, int64_t ldb) {
+  return rows_a * lda * 2 <= 0x7FFFFFFF && rows_b * ldb * 2 <= 0x7FFFFFFF;
 }
 
 // Record count (bytes) of a raw buffer descriptor, clamped to the 31-bit range (the
@@ -418,13 +433,25 @@ __device__ inline void dtl_epilogue(const GemmArgs& p, const TileJob& t, int wm,
   }
 }
 
+// The epilogue is a policy: EPI::run(p, args, tile, wm, wn, tid, acc, smem) runs after the
+// k loop with the LDS stage buffers still owned by the k loop (a policy that reuses
+// them starts with a barrier). EpiStore writes C = alpha * acc + beta * C.
+struct EpiStore {
+  struct Args {};
+  template <class CFG, typename TC>
+  __device__ static void run(const GemmArgs& p, const Args&, const TileJob& t, int wm, int wn, int tid,
+                             f32x16 (&acc)[CFG::TM][CFG::TN], char*) {
+    dtl_epilogue<CFG, TC>(p, t, wm, wn, tid & 63, acc);
+  }
+};
+
 // KEDGE: some stages cover k outside [kmin, kend) and are masked (ragged contraction
 // groups, or K % 64 != 0). Only a tile's first and last stage can be such stages, so they
 // are peeled off the main loop, which then has a single body: a branch between a masked
 // and a plain stage inside the loop makes the compiler shuttle the accumulators between
 // AGPRs and VGPRs on every iteration.
-template <class CFG, typename TC, int MODE, bool KEDGE>
-__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
+template <class CFG, typename TC, int MODE, bool KEDGE, class EPI = EpiStore>
+__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::Args ea) {
   constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
   constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
   __shared__ __attribute__((aligned(1024))) char smem[NS * CFG::STAGE_BYTES];
@@ -493,7 +520,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p) {
       dtl_stage<CFG, false>(st_of(kt), a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
     }
   }
-  dtl_epilogue<CFG, TC>(p, t, wm, wn, lane, acc);
+  EPI::template run<CFG, TC>(p, ea, t, wm, wn, tid, acc, smem);
 }
 
 }  // namespace pd
