@@ -157,6 +157,152 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
   if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = imp;
 }
 
+// ---------------------------------------------------------------- tabulated gate (bf16 step)
+// For one component c the gate preactivation g_c(h) = b_out + sum_j w_out_j GELU(w_in_j h +
+// b_in_j) is a smooth function of the scalar h, and the step draws all its h values
+// from x @ V before the forward pass. So the bf16 forward evaluates g_c from a per-step
+// table instead of 16 GELUs per element: GATE_KNOTS intervals spanning the component's
+// observed [min h, max h], exact g and g' at every knot, and the cubic Hermite
+// interpolant between knots. Its error is at most dx^4/384 max|g^(4)|, about 1e-5 of g
+// for unit-scale h and the paper's initialization (dx = range/128), far below bf16
+// resolution and below the reference's own bf16 arithmetic for this MLP. The forward
+// stores that g, so the backward's squashing branches agree with it; the backward keeps
+// the exact per-element pullback (it needs every hidden unit for the parameter
+// gradients anyway).
+static constexpr int GATE_KNOTS = 128;
+static constexpr int RANGE_ROWS = 256;   // tokens per block of the range pass
+static constexpr int FWD_WAVES = 8;      // waves per tabulated-forward block (each 64 tokens)
+
+// Partial per-component min/max of h over RANGE_ROWS tokens: rng_part[chunk][c] = (min, max).
+__global__ __launch_bounds__(256) void k_gate_range(const bf16_t* __restrict__ h, int64_t T, int64_t C,
+                                                    float2* __restrict__ rng_part) {
+  __shared__ float2 red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t t0 = (int64_t)blockIdx.y * RANGE_ROWS;
+  float lo = INFINITY, hi = -INFINITY;
+  if (c < C)
+    for (int64_t tb = t0 + w * 8; tb < t0 + RANGE_ROWS && tb < T; tb += 32) {  // 8 rows' loads at a time
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tb + e < T ? bf16_to_f32(h[(tb + e) * C + c]) : v[0];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lo = fminf(lo, v[e]);
+        hi = fmaxf(hi, v[e]);
+      }
+    }
+  red[w][lane] = make_float2(lo, hi);
+  __syncthreads();
+  if (w == 0 && c < C) {
+    for (int k = 1; k < 4; ++k) {
+      lo = fminf(lo, red[k][lane].x);
+      hi = fmaxf(hi, red[k][lane].y);
+    }
+    rng_part[(int64_t)blockIdx.y * C + c] = make_float2(lo, hi);
+  }
+}
+
+// One thread per (component, knot): tab[c][k] = (g(h_k), g'(h_k) * dx) with h_k = lo + k dx
+// evaluated exactly (device erff/expf), and rng[c] = (lo, 1 / dx, dx).
+__global__ __launch_bounds__(256) void k_gate_table(const float2* __restrict__ rng_part, int nchunk, int64_t C,
+                                                    const float* __restrict__ w_in, const float* __restrict__ b_in,
+                                                    const float* __restrict__ w_out, const float* __restrict__ b_out,
+                                                    float2* __restrict__ tab, float4* __restrict__ rng) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= C * (GATE_KNOTS + 1)) return;
+  const int64_t c = idx / (GATE_KNOTS + 1);
+  const int k = (int)(idx % (GATE_KNOTS + 1));
+  float lo = INFINITY, hi = -INFINITY;
+  for (int i = 0; i < nchunk; ++i) {
+    const float2 r = rng_part[(int64_t)i * C + c];
+    lo = fminf(lo, r.x);
+    hi = fmaxf(hi, r.y);
+  }
+  const float dx = fmaxf((hi - lo) / GATE_KNOTS, 1e-6f * fmaxf(fabsf(lo), 1.f));
+  const float hk = lo + k * dx;
+  float g = b_out[c], gp = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float wi = w_in[c * 16 + j], wo = w_out[c * 16 + j];
+    const GeluOut go = gelu_and_grad<true>(fmaf(wi, hk, b_in[c * 16 + j]));
+    g = fmaf(wo, go.gelu, g);
+    gp = fmaf(wo * wi, go.grad, gp);
+  }
+  tab[idx] = make_float2(g, gp * dx);
+  if (k == 0) rng[c] = make_float4(lo, 1.f / dx, dx, 0.f);
+}
+
+// g_c(h) from the component's table row tl (interval k, fraction f): the cubic Hermite
+// interpolant in power form.
+__device__ inline float gate_eval(const float* tl, float tt) {
+  const int k = min(max((int)tt, 0), GATE_KNOTS - 1);
+  const float f = tt - (float)k;
+  const float2 q0 = *(const float2*)(tl + 2 * k);  // (g_k, s_k), s = g' dx
+  const float2 q1 = *(const float2*)(tl + 2 * k + 2);
+  const float d = q1.x - q0.x;
+  const float b = 3.f * d - 2.f * q0.y - q1.y, cc = q0.y + q1.y - 2.f * d;
+  return fmaf(f, fmaf(f, fmaf(f, cc, b), q0.y), q0.x);
+}
+
+// The bf16 forward with the tabulated gate: block = 64 components x (FWD_WAVES * 64)
+// tokens; the 64 components' tables sit in LDS; each wave walks 64 consecutive tokens,
+// one component per lane. Otherwise as k_step_fwd.
+__global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* __restrict__ h,
+                                                                 const float2* __restrict__ tab,
+                                                                 const float4* __restrict__ rng, StepParams s,
+                                                                 float* __restrict__ g_raw, bf16_t* __restrict__ acts,
+                                                                 bf16_t* __restrict__ actsT,
+                                                                 float* __restrict__ imp_partial) {
+  constexpr int KS = GATE_KNOTS + 1;
+  __shared__ __attribute__((aligned(16))) float2 lt[64 * KS];
+  __shared__ float red[FWD_WAVES];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int nc = (int)(s.C - c0 < 64 ? s.C - c0 : 64);
+  for (int i = threadIdx.x; i < nc * KS; i += blockDim.x) lt[i] = tab[c0 * KS + i];
+  __syncthreads();
+  const int64_t c = c0 + lane;
+  const int64_t r0 = ((int64_t)blockIdx.y * FWD_WAVES + w) * 64;
+  const int64_t r1 = r0 + 64 < s.T ? r0 + 64 : s.T;
+  float imp = 0.f;
+  if (c < s.C && r0 < s.T) {
+    const float4 rg = rng[c];
+    const float* tl = (const float*)(lt + lane * KS);
+    const int64_t n = s.T * s.C;
+    RowPack<bf16_t> pack;
+    // 8 tokens per step: their h loads go out together, then the 8 elements are computed
+    for (int64_t t8 = r0; t8 < r1; t8 += 8) {
+      float hv8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hv8[e] = bf16_to_f32(h[(t8 + e) * s.C + c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t t = t8 + e, i = t * s.C + c;
+        const float hv = hv8[e];
+        const float g = gate_eval(tl, (hv - rg.x) * rg.y);
+        g_raw[i] = g;  // the backward's squashing branches see this exact value
+        const float lo = lower_fwd(g);
+        imp += pow_p(upper_fwd(g), s.p);
+        const float u = step_uniform_fwd(s, i, n);
+        const float m = lo + (1.f - lo) * u;
+        const float a = hv * (m - step_delta(s, t));
+        acts[i] = f32_to_bf16(a);
+        pack.push(a);
+      }
+      pack.flush(actsT + c * s.T + t8);
+    }
+  }
+  imp = wave_sum(imp);
+  if (lane == 0) red[w] = imp;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.f;
+    for (int k = 0; k < FWD_WAVES; ++k) sum += red[k];
+    imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = sum;
+  }
+}
+
 // Recon residual on a 64x64 tile: e = y + d*yt - yt; partial of e^2; dy = gscale*e
 // written as dy [T, D] and dy^T [D, T].
 template <typename T>
@@ -297,7 +443,8 @@ __global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec,
 }
 
 struct StepWorkspace {
-  size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, total;
+  size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, rng_part, rng, tab,
+      total;
 };
 
 static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C) {
@@ -327,6 +474,9 @@ static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_o
   take(w.gate, 4 * cdiv(T, SITE_ROWS) * 49 * C);
   take(w.delta, 4 * T);
   take(w.ubits, (size_t)T * C);
+  take(w.rng_part, 8 * cdiv(T, RANGE_ROWS) * C);
+  take(w.rng, 16 * C);
+  take(w.tab, 8 * C * (GATE_KNOTS + 1));
   w.total = o;
   return w;
 }
@@ -392,10 +542,19 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   PD_MARK(2);
   if ((rc = pd_gemm(dtype, T, C, d_in, x, d_in, 0, VT, d_in, 1, h, C, dtype, 1.f, 0.f, stream))) return rc;
   PD_MARK(3);
-  if (bf)
-    hipLaunchKernelGGL((k_step_fwd<bf16_t, false>), cgrid, dim3(SITE_COLS), 0, s, (const bf16_t*)h, w_in, b_in,
-                       w_out, b_out, sp, graw, (bf16_t*)acts, (bf16_t*)actsT, imp_part);
-  else
+  const dim3 fgrid((unsigned)cdiv(C, 64), (unsigned)cdiv(T, 64 * FWD_WAVES));
+  if (bf) {
+    float2* rng_part = (float2*)(ws + L.rng_part);
+    float4* rng = (float4*)(ws + L.rng);
+    float2* tab = (float2*)(ws + L.tab);
+    const int nchunk = (int)cdiv(T, RANGE_ROWS);
+    hipLaunchKernelGGL(k_gate_range, dim3((unsigned)cdiv(C, 64), (unsigned)nchunk), dim3(256), 0, s, (const bf16_t*)h,
+                       T, C, rng_part);
+    hipLaunchKernelGGL(k_gate_table, dim3((unsigned)cdiv(C * (GATE_KNOTS + 1), 256)), dim3(256), 0, s, rng_part,
+                       nchunk, C, w_in, b_in, w_out, b_out, tab, rng);
+    hipLaunchKernelGGL(k_step_fwd_tab, fgrid, dim3(64 * FWD_WAVES), 0, s, (const bf16_t*)h, tab, rng, sp, graw,
+                       (bf16_t*)acts, (bf16_t*)actsT, imp_part);
+  } else
     hipLaunchKernelGGL((k_step_fwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)h, w_in, b_in, w_out,
                        b_out, sp, graw, (float*)acts, (float*)actsT, imp_part);
   if ((rc = check_launch("pd_dense_step fwd"))) return rc;
@@ -411,9 +570,9 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
                        gscale, (float*)dy, (float*)dyT, rec_part);
   if ((rc = check_launch("pd_dense_step recon"))) return rc;
   PD_MARK(6);
+  const int64_t n_imp = bf ? (int64_t)fgrid.x * fgrid.y : (int64_t)cgrid.x * cgrid.y;
   hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), imp_part,
-                     (int64_t)(cgrid.x * cgrid.y), 1.0 / (double)(T * d_out), 1.0 / (double)T, recon_coeff, imp_coeff,
-                     losses);
+                     n_imp, 1.0 / (double)(T * d_out), 1.0 / (double)T, recon_coeff, imp_coeff, losses);
   PD_MARK(7);
   if ((rc = pd_gemm(dtype, C, d_out, T, actsT, T, 0, dyT, T, 1, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
     return rc;
