@@ -435,8 +435,10 @@ __device__ inline void dtl_epilogue(const GemmArgs& p, const TileJob& t, int wm,
 
 // The epilogue is a policy: EPI::run(p, args, tile, wm, wn, tid, acc, smem) runs after the
 // k loop with the LDS stage buffers still owned by the k loop (a policy that reuses
-// them starts with a barrier). EpiStore writes C = alpha * acc + beta * C.
+// them starts with a barrier); the block's LDS is max(stages, EPI::LDS_BYTES). EpiStore
+// writes C = alpha * acc + beta * C.
 struct EpiStore {
+  static constexpr int LDS_BYTES = 0;
   struct Args {};
   template <class CFG, typename TC>
   __device__ static void run(const GemmArgs& p, const Args&, const TileJob& t, int wm, int wn, int tid,
@@ -454,7 +456,8 @@ template <class CFG, typename TC, int MODE, bool KEDGE, class EPI = EpiStore>
 __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::Args ea) {
   constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
   constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
-  __shared__ __attribute__((aligned(1024))) char smem[NS * CFG::STAGE_BYTES];
+  constexpr int LDS = NS * CFG::STAGE_BYTES > EPI::LDS_BYTES ? NS * CFG::STAGE_BYTES : EPI::LDS_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = uni(tid >> 6);
   const int wm = wave / CFG::WN, wn = wave % CFG::WN;
 
