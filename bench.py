@@ -39,9 +39,15 @@ PEAK_HBM = 8.0e12
 METRIC = "masked-component fwd+bwd tokens/s on 1 MI355X; % of MFMA/HBM roofline"
 DENSE = "dense768x3072_C4096"
 MOE = "qwen35moe4L"
+CI_MLP = "ci_mlp768_h1024_C4096"
+CI_READOUT = "ci_readout_llama4L"
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
     MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4),
+    CI_MLP: dict(T=4096, dims=(768, 1024, 4096)),
+    # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
+    # readouts side by side: 4 * (4*768 + 2*3072) components
+    CI_READOUT: dict(T=8192, C=4 * (4 * 768 + 2 * 3072)),
 }
 
 
@@ -212,6 +218,110 @@ def run_dense(args):
     return res
 
 
+# ============================================================== CI functions
+def ci_cpu_baseline(workload, cfg, T_sample, reps=3):
+    import numpy as np
+
+    from oracle import ci_fn_oracle as co
+
+    rng = np.random.default_rng(0)
+    if workload == CI_MLP:
+        weights, biases = co.init_mlp_stack(cfg["dims"], rng)
+        x = rng.normal(size=(T_sample, cfg["dims"][0]))
+        g = rng.normal(size=(T_sample, cfg["dims"][-1]))
+        run = lambda: (co.site_mlp_fwd(x, weights, biases), co.site_mlp_bwd(x, weights, biases, g))
+        what = f"SiteMLP {cfg['dims']} fwd+bwd"
+    else:
+        C = cfg["C"]
+        h = rng.normal(size=(T_sample, C))
+        params = np.stack([np.ones(C), np.zeros(C), np.ones(C), np.ones(C), np.zeros(C), np.ones(C), np.zeros(C)])
+        g = rng.normal(size=(T_sample, C))
+        run = lambda: (co.readout_fwd(h, params, h), co.readout_bwd(h, params, g))
+        what = f"readout over {C} components fwd+bwd"
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{T_sample} tokens, NumPy float64 restatement of {what} (BLAS-threaded matmuls), median of "
+                      f"{reps} after 1 warmup; {med * 1e3:.1f} ms per sample"}
+
+
+def run_ci(args):
+    """The engine's CI functions: a SiteMLP fwd+bwd (GEMMs with fused bias/GELU epilogues)
+    or the component-activation readout fwd+bwd (one HBM-bound pass each way)."""
+    import torch
+
+    from param_decomp_amd import hip_events, ops
+
+    cfg = WORKLOADS[args.workload]
+    T = cfg["T"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    if args.workload == CI_MLP:
+        dims = cfg["dims"]
+        x = torch.randn(T, dims[0], device=dev, generator=gen).to(torch.bfloat16)
+        ws = [(torch.randn(a, b, device=dev, generator=gen) * (2 / a) ** 0.5).to(torch.bfloat16)
+              for a, b in zip(dims[:-1], dims[1:])]
+        bs = [torch.zeros(b, device=dev, dtype=torch.bfloat16) for b in dims[1:]]
+        g = torch.randn(T, dims[-1], device=dev, generator=gen).to(torch.bfloat16)
+        fwd = lambda: ops.ci_mlp_fwd(x, ws, bs)
+        bwd = lambda st: ops.ci_mlp_bwd(x, ws, g, st[1], False)
+        mm = sum(2 * T * a * b for a, b in zip(dims[:-1], dims[1:]))
+        work = {"fwd": ("flop", mm), "bwd": ("flop", 2 * mm - 2 * T * dims[0] * dims[1])}
+        kernels = {"fwd": "ci_mlp_fwd (a bias+GELU-epilogue GEMM per layer, W^T copies)",
+                   "bwd": "ci_mlp_bwd (dW GEMMs on K-contiguous copies, GELU'-epilogue d_a GEMMs, bias sums)"}
+        config = {"workload": args.workload, "tokens": T, "dims": list(dims), "gelu": "erf", "d_x": False}
+        step_flops = work["fwd"][1] + work["bwd"][1]
+    else:
+        C = cfg["C"]
+        h = torch.randn(T, C, device=dev, generator=gen).to(torch.bfloat16)
+        base = torch.randn(T, C, device=dev, generator=gen).to(torch.bfloat16)
+        g = torch.randn(T, C, device=dev, generator=gen).to(torch.bfloat16)
+        params = torch.stack([torch.rand(C, device=dev, generator=gen) + 0.5, torch.zeros(C, device=dev),
+                              torch.ones(C, device=dev), torch.rand(C, device=dev, generator=gen) + 0.5,
+                              torch.zeros(C, device=dev), torch.ones(C, device=dev), torch.zeros(C, device=dev)])
+        fwd = lambda: ops.ci_readout_fwd(h, params, base)
+        bwd = lambda st: ops.ci_readout_bwd(h, params, g)
+        n = T * C
+        work = {"fwd": ("byte", 6 * n), "bwd": ("byte", 6 * n)}  # fwd: h, base in, out; bwd: h, g in, d_h out
+        kernels = {"fwd": "k_readout_fwd", "bwd": "k_readout_bwd (+ k_sum_parts)"}
+        config = {"workload": args.workload, "tokens": T, "components": C, "base": True, "d_h": True}
+        step_flops = 0
+    for _ in range(args.warmup):
+        bwd(fwd())
+    evs = hip_events.create(3 * args.steps)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        hip_events.record(evs[3 * i], stream)
+        st = fwd()
+        hip_events.record(evs[3 * i + 1], stream)
+        bwd(st)
+        hip_events.record(evs[3 * i + 2], stream)
+    torch.cuda.synchronize()
+    phase = {"fwd": 0.0, "bwd": 0.0}
+    for i in range(args.steps):
+        phase["fwd"] += hip_events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) / args.steps
+        phase["bwd"] += hip_events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) / args.steps
+    hip_events.destroy(evs)
+    dom = max(phase, key=phase.get)
+    kind, amount = work[dom]
+    res = {"tokens": T, "ms_per_step": phase["fwd"] + phase["bwd"], "config": config, "step_flops": step_flops,
+           "phases_ms": phase, "roofline": roofline(kind, amount, phase[dom], kernels[dom], 1,
+                                                    pmc_traffic(args.workload, dom))}
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = ci_cpu_baseline(args.workload, cfg, args.cpu_tokens)
+    return res
+
+
 # ============================================================== MoE stack
 def moe_site_flops(J, d, f, c):
     """Per-site (in_proj, out_proj) FLOPs: gate/up read width d and write f; down reads
@@ -349,8 +459,13 @@ def main():
               "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = 64 if args.workload == MOE else 256
-    res = run_moe(args) if args.workload == MOE else run_dense(args)
+        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256}[args.workload]
+    if args.workload == MOE:
+        res = run_moe(args)
+    elif args.workload == DENSE:
+        res = run_dense(args)
+    else:
+        res = run_ci(args)
     ms = res["ms_per_step"]
     out = {
         "metric": METRIC,

@@ -306,6 +306,45 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
                             void* workspace, size_t workspace_bytes, void* stream, void** events,
                             int32_t* categories, int capacity, int* n_recorded);
 
+/* ---- the engine's CI functions ------------------------------------------------------
+ * SiteMLP (pd/core/ci_fn/implementations/mlp.py:57-78) of n_layers linears, as
+ * LayerwiseMLPCIFn.site_preactivations runs it per site
+ * (pd/core/ci_fn/implementations/layerwise_mlp.py:127-140): a_0 = x, z_i = a_i-1 @ W_i +
+ * b_i, a_i = GELU_erf(z_i) for every layer but the last, preact = z_n. dims[0..n_layers]
+ * are the widths (d_in, hidden..., C), each a positive multiple of 8; x bf16
+ * [n_tokens, dims[0]]; weights[i] bf16 [dims[i], dims[i+1]] (the reference's "i o"
+ * layout); biases[i] bf16 [dims[i+1]]; preact bf16 [n_tokens, dims[n]]. bf16 compute
+ * with fp32 accumulation, every product, bias sum and GELU rounded to bf16 as the
+ * engine's bf16 compute cast does. The forward keeps W^T copies and every hidden z_i and
+ * a_i in the workspace; pd_ci_mlp_bwd reads them, so it takes the forward's workspace
+ * unchanged. dims, weights, biases, d_weights and d_biases are HOST arrays of device
+ * pointers. All tensors 16-byte aligned. n_layers <= 16. */
+size_t pd_ci_mlp_workspace_size(int n_layers, const int64_t* dims, int64_t n_tokens);
+int pd_ci_mlp_fwd(int n_layers, const int64_t* dims, int64_t n_tokens, const void* x, const void* const* weights,
+                  const void* const* biases, void* preact, void* workspace, size_t workspace_bytes, void* stream);
+/* Backward of pd_ci_mlp_fwd from d_preact bf16 [n_tokens, dims[n]]: d_weights[i] fp32
+ * [dims[i], dims[i+1]], d_biases[i] fp32 [dims[i+1]] (overwritten; column sums in a fixed
+ * order, so repeated calls are bit-identical), d_x bf16 [n_tokens, dims[0]] (nullable). */
+int pd_ci_mlp_bwd(int n_layers, const int64_t* dims, int64_t n_tokens, const void* x, const void* const* weights,
+                  const void* d_preact, float* const* d_weights, float* const* d_biases, void* d_x, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* ComponentActivationReadout (pd/core/ci_fn/implementations/transformer/
+ * component_conditioning.py:215-245) with its ClampedAffineArm pair (:188-212):
+ * out = base + s+ sig(a+ h + b+) + s- sig(a- (-h) + b-) + bias per component, sig the
+ * symmetric leaky hard sigmoid (pd/core/ci_fn/squashing.py:25-38; forward clamp to
+ * [0, 1]). h, base, out bf16 [n_tokens, C] (base nullable); params fp32 [7, C] rows
+ * a+, b+, s+, a-, b-, s-, bias, each rounded to bf16 at use. */
+int pd_ci_readout_fwd(int64_t n_tokens, int64_t C, const void* h, const float* params, const void* base, void* out,
+                      void* stream);
+/* Backward: d_h bf16 [n_tokens, C] (nullable) and d_params fp32 [7, C] (overwritten,
+ * fixed-order sums) from d_out bf16; the d_base gradient is d_out itself. The clamp's
+ * pullback is the symmetric leaky form: inside (0, 1) the gradient, at or below 0 only
+ * a negative gradient scaled by 0.01, at or above 1 only a positive one scaled by 0.01. */
+size_t pd_ci_readout_workspace_size(int64_t n_tokens, int64_t C);
+int pd_ci_readout_bwd(int64_t n_tokens, int64_t C, const void* h, const float* params, const void* d_out, void* d_h,
+                      float* d_params, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

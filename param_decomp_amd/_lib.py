@@ -76,6 +76,12 @@ _SIGNATURES = {
                           [_c_p] * 9 + [_c_p, _c_sz, _c_p]),
     "pd_moe_stack_step_timed": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_u32, _c_u32, _c_i32] +
                                 [_c_f32] * 3 + [_c_p] * 9 + [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
+    "pd_ci_mlp_workspace_size": (_c_sz, [_c_i32, _c_p, _c_i64]),
+    "pd_ci_mlp_fwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 5 + [_c_sz, _c_p]),
+    "pd_ci_mlp_bwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 7 + [_c_sz, _c_p]),
+    "pd_ci_readout_fwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 5),
+    "pd_ci_readout_workspace_size": (_c_sz, [_c_i64, _c_i64]),
+    "pd_ci_readout_bwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 6 + [_c_sz, _c_p]),
 }
 
 _lib = None
@@ -128,6 +134,12 @@ def ptr(t: torch.Tensor | None) -> int | None:
     if not t.is_contiguous():
         raise PDError("pd kernels take contiguous tensors")
     return t.data_ptr()
+
+
+def host_array(ctype, values):
+    """A host array of `ctype` (the C ABI's `const int64_t*` / `const void* const*` lists)."""
+    values = list(values)
+    return (ctype * len(values))(*values)
 
 
 def stream() -> int:

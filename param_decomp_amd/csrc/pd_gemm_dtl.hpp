@@ -526,4 +526,19 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
   EPI::template run<CFG, TC>(p, ea, t, wm, wn, tid, acc, smem);
 }
 
+// Dense C = A [M, K] @ B^T (B stored [N, K], both K-contiguous, lda/ldb % 8 == 0, 16-byte
+// aligned) with the epilogue policy EPI (its Args carry everything beyond C's tile).
+template <class EPI, typename TC>
+inline int launch_dense_epi(const GemmArgs& a, const typename EPI::Args& ea, hipStream_t s, const char* what) {
+  if (!dtl_fits(a.M, a.lda, a.N, a.ldb)) return fail(PD_EUNSUPPORTED, std::string(what) + ": operands of 2 GiB or more");
+  if ((a.M + CfgDtl::BM - 1) / CfgDtl::BM > 65535 || (a.N + CfgDtl::BN - 1) / CfgDtl::BN > 65535)
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": too large");
+  const dim3 grid((unsigned)((a.N + CfgDtl::BN - 1) / CfgDtl::BN), (unsigned)((a.M + CfgDtl::BM - 1) / CfgDtl::BM));
+  if (a.K % CfgDtl::BK)
+    hipLaunchKernelGGL((k_gemm_dtl<CfgDtl, TC, MODE_DENSE, true, EPI>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
+  else
+    hipLaunchKernelGGL((k_gemm_dtl<CfgDtl, TC, MODE_DENSE, false, EPI>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
+  return check_launch(what);
+}
+
 }  // namespace pd

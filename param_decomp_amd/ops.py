@@ -6,6 +6,7 @@ modules (`masking`, `decomposed_linear`, `losses`, `routed.experts`) add autogra
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -201,3 +202,56 @@ def grouped_gemm_dw(lhs, dout, offsets, n_groups: int, *, out_dtype=None):
     L.call("pd_grouped_gemm_dw", L.ptr(lhs), L.ptr(dout), L.ptr(offsets), J, n_groups, K, N, L.ptr(out),
            L.dtype_code(out.dtype), L.stream())
     return out
+
+
+def ci_mlp_fwd(x: torch.Tensor, weights, biases):
+    """SiteMLP preactivations of bf16 `x` [..., d_0] with bf16 weights[i] [d_i, d_i+1] and
+    biases[i] [d_i+1]. Returns (preact [..., d_n], workspace); the workspace holds the
+    hidden activations and feeds `ci_mlp_bwd`."""
+    rows, d0 = _flat_rows(x)
+    dims = [d0] + [w.shape[1] for w in weights]
+    for i, w in enumerate(weights):
+        if w.shape[0] != dims[i] or biases[i].shape != (dims[i + 1],):
+            raise L.PDError(f"ci_mlp layer {i}: weight {tuple(w.shape)} / bias {tuple(biases[i].shape)} mismatch")
+    cdims = L.host_array(ctypes.c_int64, dims)
+    out = torch.empty((*x.shape[:-1], dims[-1]), dtype=torch.bfloat16, device=x.device)
+    ws = L.workspace(L.load().pd_ci_mlp_workspace_size(len(weights), cdims, rows), x.device)
+    L.call("pd_ci_mlp_fwd", len(weights), cdims, rows, L.ptr(x), L.host_array(ctypes.c_void_p, map(L.ptr, weights)),
+           L.host_array(ctypes.c_void_p, map(L.ptr, biases)), L.ptr(out), L.ptr(ws), ws.numel(), L.stream())
+    return out, ws
+
+
+def ci_mlp_bwd(x: torch.Tensor, weights, d_preact: torch.Tensor, ws: torch.Tensor, want_dx: bool):
+    """Gradients of `ci_mlp_fwd` from bf16 `d_preact`, reusing its workspace: fp32
+    d_weights and d_biases, and bf16 d_x (None unless asked)."""
+    rows, d0 = _flat_rows(x)
+    dims = [d0] + [w.shape[1] for w in weights]
+    cdims = L.host_array(ctypes.c_int64, dims)
+    dW = [torch.empty(w.shape, dtype=torch.float32, device=x.device) for w in weights]
+    db = [torch.empty(w.shape[1], dtype=torch.float32, device=x.device) for w in weights]
+    dx = torch.empty_like(x) if want_dx else None
+    L.call("pd_ci_mlp_bwd", len(weights), cdims, rows, L.ptr(x), L.host_array(ctypes.c_void_p, map(L.ptr, weights)),
+           L.ptr(d_preact), L.host_array(ctypes.c_void_p, map(L.ptr, dW)), L.host_array(ctypes.c_void_p, map(L.ptr, db)),
+           L.ptr(dx), L.ptr(ws), ws.numel(), L.stream())
+    return dW, db, dx
+
+
+def ci_readout_fwd(h: torch.Tensor, params: torch.Tensor, base: torch.Tensor | None = None) -> torch.Tensor:
+    """Component-activation readout of bf16 `h` [..., C] with fp32 params [7, C], added to
+    bf16 `base` when given."""
+    rows, C = _flat_rows(h)
+    if params.shape != (7, C) or params.dtype != torch.float32:
+        raise L.PDError("readout params must be fp32 [7, C]")
+    out = torch.empty_like(h)
+    L.call("pd_ci_readout_fwd", rows, C, L.ptr(h), L.ptr(params), L.ptr(base), L.ptr(out), L.stream())
+    return out
+
+
+def ci_readout_bwd(h: torch.Tensor, params: torch.Tensor, d_out: torch.Tensor, want_dh: bool = True):
+    rows, C = _flat_rows(h)
+    d_h = torch.empty_like(h) if want_dh else None
+    d_params = torch.empty((7, C), dtype=torch.float32, device=h.device)
+    ws = L.workspace(L.load().pd_ci_readout_workspace_size(rows, C), h.device)
+    L.call("pd_ci_readout_bwd", rows, C, L.ptr(h), L.ptr(params), L.ptr(d_out), L.ptr(d_h), L.ptr(d_params), L.ptr(ws),
+           ws.numel(), L.stream())
+    return d_h, d_params
