@@ -41,6 +41,9 @@ DENSE = "dense768x3072_C4096"
 MOE = "qwen35moe4L"
 CI_MLP = "ci_mlp768_h1024_C4096"
 CI_READOUT = "ci_readout_llama4L"
+FAITH_DENSE = "faith_dense768x3072_C4096"
+FAITH_MOE = "faith_qwen35moe4L"
+PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
     MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4),
@@ -48,6 +51,12 @@ WORKLOADS = {
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
     CI_READOUT: dict(T=8192, C=4 * (4 * 768 + 2 * 3072)),
+    # faithfulness of the dense site, and of every expert matrix of the MoE stack (per kind:
+    # 4 layers x 42 experts, each layer's experts one block-factored site)
+    FAITH_DENSE: dict(groups=[dict(n=1, per=1, d_in=768, d_out=3072, C=4096)]),
+    FAITH_MOE: dict(groups=[dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
+                            dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
+                            dict(n=4 * 42, per=42, d_in=256, d_out=512, C=512)]),
 }
 
 
@@ -102,6 +111,12 @@ def pmc_traffic(workload, phase):
 
 def roofline(kind, amount_per_launch, ms_per_launch, kernel, launches_per_step, traffic=None):
     dur = ms_per_launch * 1e-3
+    if kind == "flop32":
+        achieved = amount_per_launch / dur / 1e12
+        return {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / (PEAK_FP32_MFMA / 1e12), "traffic": traffic, "kernel": kernel,
+                "avg_launch_ms": ms_per_launch, "work_per_launch": amount_per_launch,
+                "launches_per_step": launches_per_step, "precision": "fp32 MFMA (dense fp32 peak)"}
     if kind == "flop":
         achieved = amount_per_launch / dur / 1e12
         return {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
@@ -322,6 +337,96 @@ def run_ci(args):
     return res
 
 
+# ============================================================== faithfulness
+def faith_cpu_baseline(groups, reps=3):
+    import numpy as np
+
+    from oracle import faith_oracle as fo
+
+    g0 = groups[0]
+    n = min(g0["n"], 4)
+    rng = np.random.default_rng(0)
+    W = rng.normal(size=(n, g0["d_out"], g0["d_in"])).astype(np.float32)
+    V = (rng.normal(size=(n, g0["d_in"], g0["C"])) / np.sqrt(g0["d_in"])).astype(np.float32)
+    U = (rng.normal(size=(n, g0["C"], g0["d_out"])) / np.sqrt(g0["C"])).astype(np.float32)
+    norms = (W.astype(np.float64) ** 2).reshape(n, -1).sum(1)
+    run = lambda: (fo.site_errors(W, V, U, norms), fo.grads(W, V, U, norms, 1.0))
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": n / med, "unit": "matrices/s", "cores": cores, "kind": "port",
+            "sample": f"{n} matrices of the first group ({g0['d_out']}x{g0['d_in']}, C={g0['C']}), NumPy float64 "
+                      f"restatement of loss + dV + dU (BLAS-threaded), median of {reps}; {med * 1e3:.1f} ms"}
+
+
+def run_faith(args):
+    """Faithfulness fwd+bwd over every group of the workload: fp32 MFMA products, the
+    delta and its squared norm fused into the forward GEMM's epilogue."""
+    import torch
+
+    from param_decomp_amd import hip_events, ops
+
+    groups = WORKLOADS[args.workload]["groups"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    stacks = []
+    for g in groups:
+        W = torch.randn(g["n"], g["d_out"], g["d_in"], device=dev, generator=gen).to(torch.bfloat16)
+        V = torch.randn(g["n"], g["d_in"], g["C"], device=dev, generator=gen) / g["d_in"] ** 0.5
+        U = torch.randn(g["n"], g["C"], g["d_out"], device=dev, generator=gen) / g["C"] ** 0.5
+        norms = (W.float() ** 2).reshape(g["n"] // g["per"], -1).sum(1)
+        stacks.append((W, V, U, norms, g["per"]))
+    n_sites = sum(g["n"] // g["per"] for g in groups)
+
+    def fwd():
+        return [ops.faithfulness_fwd(W, V, U, nt, per, 1.0 / n_sites, keep_delta=True) for W, V, U, nt, per in stacks]
+
+    def bwd(outs):
+        for (W, V, U, nt, per), (_, _, delta) in zip(stacks, outs):
+            ops.faithfulness_bwd(delta, V, U, nt, per, 1.0 / n_sites, None)
+
+    for _ in range(args.warmup):
+        bwd(fwd())
+    stream = torch.cuda.current_stream().cuda_stream
+    evs = hip_events.create(3 * args.steps)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        hip_events.record(evs[3 * i], stream)
+        outs = fwd()
+        hip_events.record(evs[3 * i + 1], stream)
+        bwd(outs)
+        hip_events.record(evs[3 * i + 2], stream)
+    torch.cuda.synchronize()
+    phase = {"fwd": 0.0, "bwd": 0.0}
+    for i in range(args.steps):
+        phase["fwd"] += hip_events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) / args.steps
+        phase["bwd"] += hip_events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) / args.steps
+    hip_events.destroy(evs)
+    mm = sum(2 * g["n"] * g["d_in"] * g["d_out"] * g["C"] for g in groups)
+    work = {"fwd": mm, "bwd": 2 * mm}
+    dom = max(phase, key=phase.get)
+    kern = {"fwd": "k_faith_gemm<EPI delta> (+ k_faith_reduce)", "bwd": "k_faith_gemm<EPI scale> x2 (dV, dU)"}[dom]
+    n_mats = sum(g["n"] for g in groups)
+    res = {"tokens": n_mats, "ms_per_step": phase["fwd"] + phase["bwd"],
+           "config": {"workload": args.workload, "groups": groups, "W": "bf16", "V_U": "fp32 masters",
+                      "unit_of_value": "matrices/s (a step is loss + dV + dU of every matrix)"},
+           "step_flops": 3 * mm, "phases_ms": phase,
+           "roofline": roofline("flop32", work[dom] / (len(groups) * (1 if dom == "fwd" else 2)),
+                                phase[dom] / (len(groups) * (1 if dom == "fwd" else 2)), kern,
+                                len(groups) * (1 if dom == "fwd" else 2))}
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = faith_cpu_baseline(groups)
+    return res
+
+
 # ============================================================== MoE stack
 def moe_site_flops(J, d, f, c):
     """Per-site (in_proj, out_proj) FLOPs: gate/up read width d and write f; down reads
@@ -459,18 +564,21 @@ def main():
               "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256}[args.workload]
+        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
     elif args.workload == DENSE:
         res = run_dense(args)
+    elif args.workload in (FAITH_DENSE, FAITH_MOE):
+        res = run_faith(args)
     else:
         res = run_ci(args)
     ms = res["ms_per_step"]
+    faith = args.workload in (FAITH_DENSE, FAITH_MOE)
     out = {
         "metric": METRIC,
         "value": res["tokens"] / (ms * 1e-3),
-        "unit": "tokens/s",
+        "unit": "matrices/s" if faith else "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -478,11 +586,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f32" if faith else "bf16",
         "data": "synthetic (seeded torch.randn / torch.rand of the named shapes; random-init target and components)",
         "config": res["config"],
         "step_tflops": res["step_flops"] / (ms * 1e-3) / 1e12,
-        "step_mfma_frac": res["step_flops"] / (ms * 1e-3) / PEAK_BF16_FLOPS,
+        "step_mfma_frac": res["step_flops"] / (ms * 1e-3) / (PEAK_FP32_MFMA if faith else PEAK_BF16_FLOPS),
         "phases_ms": res["phases_ms"],
         "roofline": res["roofline"],
     }

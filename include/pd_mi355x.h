@@ -345,6 +345,31 @@ size_t pd_ci_readout_workspace_size(int64_t n_tokens, int64_t C);
 int pd_ci_readout_bwd(int64_t n_tokens, int64_t C, const void* h, const float* params, const void* d_out, void* d_h,
                       float* d_params, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- faithfulness ---------------------------------------------------------------------
+ * Relative squared weight error (pd/core/faithfulness.py:16-75) of the fp32 deltas
+ * Delta = W - (V U)^T that the targets form per stack (pd/targets/transformer.py:2134-2184,
+ * protocol pd/core/model.py:430-449). n_mats matrices W bf16 or fp32 [n_mats, d_out, d_in],
+ * V fp32 [n_mats, d_in, C], U fp32 [n_mats, C, d_out]; every mats_per_site consecutive
+ * matrices form one site (1 for dense stacks, the expert count for block-factored ones,
+ * whose blocks partition the site matrix). w_sq_norms fp32 [n_mats / mats_per_site] =
+ * ||W_site||^2. Outputs (device): loss[0] = scale * sum_site ||Delta_site||^2 /
+ * ||W_site||^2 (scale = 1 / the number of sites of the whole model, so per-group calls
+ * add up to the reference's mean); site_errors [n_sites] the relative errors (nullable);
+ * delta fp32 [n_mats, d_out, d_in] (nullable; keep it for pd_faithfulness_bwd). fp32
+ * products on the matrix cores (v_mfma_f32_32x32x2f32), split over C into at most 8
+ * fixed chunks when the matrices alone fill fewer than 512 blocks; fixed-order
+ * reductions, so results are bit-identical from call to call. */
+size_t pd_faithfulness_workspace_size(int64_t n_mats, int64_t d_in, int64_t d_out, int64_t C);
+int pd_faithfulness_fwd(int64_t n_mats, int64_t mats_per_site, int64_t d_in, int64_t d_out, int64_t C, const void* W,
+                        int w_dtype, const float* V, const float* U, const float* w_sq_norms, float scale, float* loss,
+                        float* site_errors, float* delta, void* workspace, size_t workspace_bytes, void* stream);
+/* Gradients of pd_faithfulness_fwd's loss times *d_loss (a device scalar; NULL = 1):
+ * dV = -2 scale d_loss / ||W_site||^2 Delta^T U^T, dU = -2 scale d_loss / ||W_site||^2
+ * V^T Delta^T, fp32, overwritten. */
+int pd_faithfulness_bwd(int64_t n_mats, int64_t mats_per_site, int64_t d_in, int64_t d_out, int64_t C,
+                        const float* delta, const float* V, const float* U, const float* w_sq_norms, float scale,
+                        const float* d_loss, float* dV, float* dU, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,10 @@ _SIGNATURES = {
     "pd_ci_readout_fwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 5),
     "pd_ci_readout_workspace_size": (_c_sz, [_c_i64, _c_i64]),
     "pd_ci_readout_bwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 6 + [_c_sz, _c_p]),
+    "pd_faithfulness_workspace_size": (_c_sz, [_c_i64] * 4),
+    "pd_faithfulness_fwd": (_c_i32, [_c_i64] * 5 + [_c_p, _c_i32] + [_c_p] * 3 + [_c_f32] + [_c_p] * 4 +
+                            [_c_sz, _c_p]),
+    "pd_faithfulness_bwd": (_c_i32, [_c_i64] * 5 + [_c_p] * 4 + [_c_f32] + [_c_p] * 4),
 }
 
 _lib = None

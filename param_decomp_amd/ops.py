@@ -255,3 +255,31 @@ def ci_readout_bwd(h: torch.Tensor, params: torch.Tensor, d_out: torch.Tensor, w
     L.call("pd_ci_readout_bwd", rows, C, L.ptr(h), L.ptr(params), L.ptr(d_out), L.ptr(d_h), L.ptr(d_params), L.ptr(ws),
            ws.numel(), L.stream())
     return d_h, d_params
+
+
+def faithfulness_fwd(W, V, U, w_sq_norms, mats_per_site: int, scale: float, keep_delta: bool):
+    """Stacked faithfulness forward: W [n, d_out, d_in] (bf16/fp32), V fp32 [n, d_in, C],
+    U fp32 [n, C, d_out], w_sq_norms fp32 [n / mats_per_site]. Returns (loss [1],
+    site_errors, delta or None)."""
+    n, d_out, d_in = W.shape
+    C = V.shape[-1]
+    if V.shape != (n, d_in, C) or U.shape != (n, C, d_out) or V.dtype != torch.float32 or U.dtype != torch.float32:
+        raise L.PDError(f"faithfulness shapes: W {tuple(W.shape)} V {tuple(V.shape)} U {tuple(U.shape)} (fp32 V/U)")
+    dev = W.device
+    loss = torch.empty(1, dtype=torch.float32, device=dev)
+    site_err = torch.empty(n // mats_per_site, dtype=torch.float32, device=dev)
+    delta = torch.empty((n, d_out, d_in), dtype=torch.float32, device=dev) if keep_delta else None
+    ws = L.workspace(L.load().pd_faithfulness_workspace_size(n, d_in, d_out, C), dev)
+    L.call("pd_faithfulness_fwd", n, mats_per_site, d_in, d_out, C, L.ptr(W), L.dtype_code(W.dtype), L.ptr(V), L.ptr(U),
+           L.ptr(w_sq_norms), scale, L.ptr(loss), L.ptr(site_err), L.ptr(delta), L.ptr(ws), ws.numel(), L.stream())
+    return loss, site_err, delta
+
+
+def faithfulness_bwd(delta, V, U, w_sq_norms, mats_per_site: int, scale: float, d_loss: torch.Tensor | None):
+    n, d_out, d_in = delta.shape
+    C = V.shape[-1]
+    dV = torch.empty_like(V)
+    dU = torch.empty_like(U)
+    L.call("pd_faithfulness_bwd", n, mats_per_site, d_in, d_out, C, L.ptr(delta), L.ptr(V), L.ptr(U), L.ptr(w_sq_norms),
+           scale, L.ptr(d_loss), L.ptr(dV), L.ptr(dU), L.stream())
+    return dV, dU
