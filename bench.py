@@ -41,6 +41,7 @@ DENSE = "dense768x3072_C4096"
 MOE = "qwen35moe4L"
 CI_MLP = "ci_mlp768_h1024_C4096"
 CI_READOUT = "ci_readout_llama4L"
+PPGD_DENSE = "ppgd_dense768x3072_C4096"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
 PEAK_FP32_MFMA = 157.3e12
@@ -51,6 +52,10 @@ WORKLOADS = {
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
     CI_READOUT: dict(T=8192, C=4 * (4 * 768 + 2 * 3072)),
+    # persistent PGD on the dense site: per-token uint16 sources, momentum SGD, 2 warmup
+    # ascents (the reference's LM PPGD setting)
+    PPGD_DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096, n_warmup=2, source_shape="bsc", source_dtype="uint16",
+                     optimizer="momentum_sgd", momentum=0.9, lr=0.01),
     # faithfulness of the dense site, and of every expert matrix of the MoE stack (per kind:
     # 4 layers x 42 experts, each layer's experts one block-factored site)
     FAITH_DENSE: dict(groups=[dict(n=1, per=1, d_in=768, d_out=3072, C=4096)]),
@@ -337,6 +342,102 @@ def run_ci(args):
     return res
 
 
+# ============================================================== persistent PGD
+def ppgd_cpu_baseline(cfg, T_sample, reps=3):
+    import numpy as np
+
+    from oracle import pgd_oracle as po
+
+    rng = np.random.default_rng(0)
+    d_in, d_out, C = cfg["d_in"], cfg["d_out"], cfg["C"]
+    x = rng.normal(size=(T_sample, d_in))
+    V = rng.normal(size=(d_in, C)) / np.sqrt(d_in)
+    U = rng.normal(size=(C, d_out)) / np.sqrt(C)
+    ci = rng.uniform(size=(T_sample, C))
+    tgt = rng.normal(size=(T_sample, d_out))
+    src = rng.uniform(size=(T_sample, C))
+
+    def run():
+        s, vel = src.copy(), np.zeros_like(src)
+        for it in range(cfg["n_warmup"] + 1):
+            m = po.source_mask(ci, s, 1)
+            xV = x @ V
+            out = (xV * m) @ U
+            g = 2 * (out - tgt) / out.size
+            da = g @ U.T
+            d_src, _ = po.source_mask_vjp(da * xV, ci, s, 1)
+            if it == cfg["n_warmup"]:
+                _ = (xV * m).T @ g, x.T @ (da * m)
+            s, vel = po.momentum_sgd(s, d_src, vel, cfg["lr"], cfg["momentum"])
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{T_sample} tokens of the site (full widths), NumPy float64 restatement of the {cfg['n_warmup']} "
+                      f"warmup ascents + final recon/backward/ascent (BLAS-threaded), median of {reps}; "
+                      f"{med * 1e3:.1f} ms per sample step"}
+
+
+def run_ppgd(args):
+    """One persistent-PGD step of the dense site: n_warmup source ascents (masked forward,
+    MSE, mask-only backward, source pullback, projected ascent) and the final forward and
+    full backward with the final ascent."""
+    import torch
+
+    from param_decomp_amd import adversary as A
+    from param_decomp_amd import hip_events, prng
+
+    cfg = WORKLOADS[args.workload]
+    T, d_in, d_out, C = cfg["T"], cfg["d_in"], cfg["d_out"], cfg["C"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(T, d_in, device=dev, generator=gen).to(torch.bfloat16)
+    V = (torch.randn(d_in, C, device=dev, generator=gen) / d_in**0.5).to(torch.bfloat16)
+    U = (torch.randn(C, d_out, device=dev, generator=gen) / C**0.5).to(torch.bfloat16)
+    ci = torch.rand(T, C, device=dev, generator=gen).to(torch.bfloat16)
+    target = torch.randn(T, d_out, device=dev, generator=gen).to(torch.bfloat16)
+    src = A.store_unit_float(torch.rand(T, C, device=dev, generator=gen), torch.uint16)
+    adv = A.PersistentAdversary(src, A.MomentumSgdPGDConfig(cfg["momentum"]), cfg["n_warmup"], rows_per_source=1)
+    step = A.DenseSitePPGDStep(adv)
+    for i in range(args.warmup):
+        step.step(x, V, U, ci, target, cfg["lr"], prng.fold_in((0, 0), i))
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        res = step.step(x, V, U, ci, target, cfg["lr"], prng.fold_in((0, 0), args.warmup + i))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms = hip_events.elapsed_ms(start, stop) / args.steps
+    hip_events.destroy([start, stop])
+    assert torch.isfinite(res.loss).all()
+    xv, uo = 2 * T * d_in * C, 2 * T * C * d_out
+    warm = xv + 2 * uo          # fwd x@V, acts@U; bwd g@U^T only
+    final = 2 * xv + 3 * uo     # fwd x@V, acts@U; bwd dU, da, dV
+    step_flops = cfg["n_warmup"] * warm + final
+    res_d = {"tokens": T, "ms_per_step": ms,
+             "config": {"workload": args.workload, "tokens": T, "d_in": d_in, "d_out": d_out, "C": C,
+                        "n_warmup": cfg["n_warmup"], "source_shape": cfg["source_shape"],
+                        "source_dtype": cfg["source_dtype"], "optimizer": cfg["optimizer"],
+                        "recon": "mse (site output)"},
+             "step_flops": step_flops, "phases_ms": {"step": ms},
+             "roofline": roofline("flop", step_flops, ms, "the step's bf16 GEMMs (x@V, acts@U, g@U^T; dU, dV "
+                                  "in the final backward) with the source-mask and ascent passes", 1)}
+    if not args.no_cpu_baseline:
+        res_d["cpu_baseline"] = ppgd_cpu_baseline(cfg, args.cpu_tokens)
+    return res_d
+
+
 # ============================================================== faithfulness
 def faith_cpu_baseline(groups, reps=3):
     import numpy as np
@@ -564,13 +665,15 @@ def main():
               "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256}.get(args.workload, 0)
+        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
     elif args.workload == DENSE:
         res = run_dense(args)
     elif args.workload in (FAITH_DENSE, FAITH_MOE):
         res = run_faith(args)
+    elif args.workload == PPGD_DENSE:
+        res = run_ppgd(args)
     else:
         res = run_ci(args)
     ms = res["ms_per_step"]

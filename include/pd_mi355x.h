@@ -38,6 +38,12 @@ extern "C" {
 
 #define PD_DTYPE_F32 0
 #define PD_DTYPE_BF16 1
+#define PD_DTYPE_U16 2 /* unit-interval fixed point u / 65535 (adversarial source storage) */
+
+#define PD_PGD_SGD 0      /* source optimizers, pd/core/adversary.py:392-470 */
+#define PD_PGD_MOMENTUM 1
+#define PD_PGD_ADAM 2
+#define PD_PGD_SIGN 3     /* fresh-PGD sign ascent, pd/core/train.py:788-800 */
 
 #define PD_LAYOUT_PARTITIONABLE 0 /* jax_threefry_partitionable=True (JAX >= 0.5 default) */
 #define PD_LAYOUT_ORIGINAL 1
@@ -146,8 +152,9 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
 int pd_masked_linear_fwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          void* out, void* xV, void* acts, void* stream);
-/* VJP: given d_out_grad [T,d_out] -> dx [T,d_in] (nullable), dV, dU, dmask [T,C]
- * (nullable). workspace holds two [T,C] and one [T,d_out] tensors of `dtype`. */
+/* VJP: given d_out_grad [T,d_out] -> dx [T,d_in], dV, dU, dmask [T,C] (each nullable;
+ * an adversarial source ascent asks for dmask alone). workspace holds two [T,C] and one
+ * [T,d_out] tensors of `dtype`. */
 size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, int64_t C);
 int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
@@ -344,6 +351,36 @@ int pd_ci_readout_fwd(int64_t n_tokens, int64_t C, const void* h, const float* p
 size_t pd_ci_readout_workspace_size(int64_t n_tokens, int64_t C);
 int pd_ci_readout_bwd(int64_t n_tokens, int64_t C, const void* h, const float* params, const void* d_out, void* d_h,
                       float* d_params, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- adversarial sources (persistent and fresh PGD) ----------------------------------
+ * Source masks m = ci + (1 - ci) s (pd/core/source_mask.py:56-63; the source read into
+ * the CI's frame and dtype, pd/core/masking.py:260-272). ci and mask [rows, C] in dtype;
+ * sources [rows / rows_per_source, C] stored as src_dtype (F32, BF16 or U16 = u / 65535,
+ * pd/core/adversary.py:150-184). A source row covers rows_per_source consecutive CI rows:
+ * the reference's source shapes `bsc`, `bc` and `c` over (batch, positions) are 1, the
+ * positions of a sample, and every row. */
+int pd_source_mask_fwd(const void* ci, int dtype, int64_t rows, int64_t C, const void* sources, int src_dtype,
+                       int64_t rows_per_source, void* mask, void* stream);
+/* d_sources fp32 [rows / rows_per_source, C] = sum over covered rows of g (1 - ci), in a
+ * fixed order (overwritten); d_ci (nullable, dtype) = g (1 - s). */
+size_t pd_source_mask_bwd_workspace_size(int64_t rows, int64_t C, int64_t rows_per_source);
+int pd_source_mask_bwd(const void* g_mask, const void* ci, int dtype, int64_t rows, int64_t C, const void* sources,
+                       int src_dtype, int64_t rows_per_source, float* d_sources, void* d_ci, void* workspace,
+                       size_t workspace_bytes, void* stream);
+/* One projected ascent of n source values in place (pd/core/adversary.py:392-470 and the
+ * uint16 store with stochastic rounding, :186-214; fresh PGD's sign step,
+ * pd/core/train.py:788-800), projected to [0, 1]. grad fp32 is the gradient w.r.t. the
+ * float view. PD_PGD_SGD: s += lr g. PD_PGD_MOMENTUM: v = momentum v + g (state_a: fp32
+ * velocity for fp32 sources, bf16 otherwise), s += lr v. PD_PGD_ADAM: state_a/state_b =
+ * m, v at the source dtype (F32 or BF16), step_count = the step after this update (>= 1),
+ * s += lr m_hat / (sqrt(v_hat) + eps); beta1/beta2 are doubles so that 1 - beta is formed in
+ * double and rounded once, as the reference's Python-float arithmetic does.
+ * PD_PGD_SIGN (F32 sources): s += lr sign(g). Bf16
+ * storage rounds where the reference's bf16 arithmetic does; U16 storage quantizes with
+ * uniforms of key (k0, k1) (the per-leaf fold of the caller's key) under `layout`. */
+int pd_source_ascend(int opt, int src_dtype, int64_t n, void* sources, const float* grad, void* state_a,
+                     void* state_b, float step_count, float lr, double beta1, double beta2, float eps, float momentum,
+                     uint32_t k0, uint32_t k1, int layout, void* stream);
 
 /* ---- faithfulness ---------------------------------------------------------------------
  * Relative squared weight error (pd/core/faithfulness.py:16-75) of the fp32 deltas

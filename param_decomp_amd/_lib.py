@@ -14,7 +14,8 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpd_mi355x.so")
 
-F32, BF16 = 0, 1
+F32, BF16, U16 = 0, 1, 2
+PGD_SGD, PGD_MOMENTUM, PGD_ADAM, PGD_SIGN = 0, 1, 2, 3
 LAYOUT_PARTITIONABLE, LAYOUT_ORIGINAL = 0, 1
 IMPMIN_PNORM, IMPMIN_SMOOTH_L0 = 0, 1
 BLOCK_FUSED_OUTPUT, BLOCK_FUSED_INPUT = 0, 1
@@ -82,6 +83,12 @@ _SIGNATURES = {
     "pd_ci_readout_fwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 5),
     "pd_ci_readout_workspace_size": (_c_sz, [_c_i64, _c_i64]),
     "pd_ci_readout_bwd": (_c_i32, [_c_i64, _c_i64] + [_c_p] * 6 + [_c_sz, _c_p]),
+    "pd_source_mask_fwd": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_i32, _c_i64, _c_p, _c_p]),
+    "pd_source_mask_bwd_workspace_size": (_c_sz, [_c_i64] * 3),
+    "pd_source_mask_bwd": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_sz,
+                                    _c_p]),
+    "pd_source_ascend": (_c_i32, [_c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f32, _c_f32, ctypes.c_double,
+                                  ctypes.c_double, _c_f32, _c_f32, _c_u32, _c_u32, _c_i32, _c_p]),
     "pd_faithfulness_workspace_size": (_c_sz, [_c_i64] * 4),
     "pd_faithfulness_fwd": (_c_i32, [_c_i64] * 5 + [_c_p, _c_i32] + [_c_p] * 3 + [_c_f32] + [_c_p] * 4 +
                             [_c_sz, _c_p]),
@@ -127,6 +134,8 @@ def dtype_code(dt: torch.dtype) -> int:
         return F32
     if dt == torch.bfloat16:
         return BF16
+    if dt == torch.uint16:
+        return U16
     raise PDError(f"unsupported dtype {dt}")
 
 

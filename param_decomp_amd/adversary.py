@@ -1,0 +1,188 @@
+"""Adversarial sources on the GPU: persistent PGD (warmup ascents and the final ascent)
+and fresh PGD sign ascents.
+
+Mirrors `param_decomp/param_decomp/core/adversary.py`:
+- source storage `float32` / `bfloat16` / `uint16` (`u / 65535`, stored back with
+  unbiased stochastic rounding; `:150-214`), `source_values_to_float`, `velocity_dtype`;
+- the source optimizers `AdamPGDConfig`, `SgdPGDConfig`, `MomentumSgdPGDConfig`
+  (`pd/core/configs.py:347-375`) and their projected ascents (`:392-470`);
+- `PersistentAdversary.warmup_ascend` / `after_one_ascent` / `final_ascend` (`:487-560`);
+- fresh PGD's sign ascent (`pd/core/train.py:788-800`);
+and the source masks `ci + (1 - ci) s` (`pd/core/source_mask.py:56-63`).
+
+A source tensor is `[n_sources, C]`; each source row covers `rows_per_source`
+consecutive CI rows (`bsc`: 1, `bc`: the positions of a sample, `c`: every row).
+`DenseSitePPGDStep` runs the persistent-PGD step of one dense site through the
+masked-linear kernels: `n_warmup` source ascents on the detached reconstruction loss,
+then the final reconstruction (model gradients) whose source gradient makes the final
+ascent (`pd/core/train.py:693-811`).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from param_decomp_amd import _lib as L
+from param_decomp_amd import ops, prng
+
+UINT16_UNIT_SCALE = 65535.0
+
+
+@dataclass(frozen=True)
+class AdamPGDConfig:
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+
+
+@dataclass(frozen=True)
+class SgdPGDConfig:
+    pass
+
+
+@dataclass(frozen=True)
+class MomentumSgdPGDConfig:
+    momentum: float = 0.9
+
+
+def velocity_dtype(storage: torch.dtype) -> torch.dtype:
+    """fp32 velocity for fp32 sources, bf16 for either 16-bit storage (`:270-274`)."""
+    return torch.float32 if storage == torch.float32 else torch.bfloat16
+
+
+def store_unit_float(value: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Init-time store of [0, 1] values: uint16 rounds to nearest, floats cast (`:159-168`)."""
+    if dtype == torch.uint16:
+        return torch.round(value.float() * UINT16_UNIT_SCALE).to(torch.int32).to(torch.uint16)
+    return value.to(dtype)
+
+
+def source_values_to_float(sources: torch.Tensor) -> torch.Tensor:
+    """The float view: uint16 dequantizes to fp32 `u / 65535`; floats pass through."""
+    if sources.dtype == torch.uint16:
+        return sources.to(torch.int32).float() / UINT16_UNIT_SCALE
+    return sources
+
+
+def source_mask(ci: torch.Tensor, sources: torch.Tensor, rows_per_source: int) -> torch.Tensor:
+    return ops.source_mask_fwd(ci.contiguous(), sources, rows_per_source)
+
+
+def source_mask_grad(g_mask, ci, sources, rows_per_source: int, want_dci: bool = False):
+    """(d_sources fp32, d_ci): the pullback of `source_mask`."""
+    return ops.source_mask_bwd(g_mask.contiguous(), ci.contiguous(), sources, rows_per_source, want_dci)
+
+
+class PersistentAdversary:
+    """Persistent sources, optimizer state and ascent configuration of one source leaf."""
+
+    def __init__(self, sources: torch.Tensor, optimizer, n_warmup: int, rows_per_source: int, leaf_index: int = 0):
+        if isinstance(optimizer, AdamPGDConfig) and sources.dtype == torch.uint16:
+            raise ValueError("uint16 fixed-point source storage pairs with source optimizer sgd/momentum_sgd; "
+                             "adam stores its moments at the source dtype")
+        self.sources = sources.contiguous()
+        self.optimizer = optimizer
+        self.n_warmup = n_warmup
+        self.rows_per_source = rows_per_source
+        self.leaf_index = leaf_index
+        self.step_count = 0.0
+        self.state_a = self.state_b = None
+        if isinstance(optimizer, AdamPGDConfig):
+            self.state_a = torch.zeros_like(self.sources)
+            self.state_b = torch.zeros_like(self.sources)
+        elif isinstance(optimizer, MomentumSgdPGDConfig):
+            self.state_a = torch.zeros(self.sources.shape, dtype=velocity_dtype(self.sources.dtype),
+                                       device=self.sources.device)
+
+    @property
+    def float_sources(self) -> torch.Tensor:
+        return source_values_to_float(self.sources)
+
+    def mask(self, ci: torch.Tensor) -> torch.Tensor:
+        return source_mask(ci, self.sources, self.rows_per_source)
+
+    def after_one_ascent(self, grad: torch.Tensor, lr: float, key) -> "PersistentAdversary":
+        """One projected ascent along the float-view gradient; `key` is the ascent's key,
+        folded with this leaf's index for the uint16 rounding draw (`:197-214`)."""
+        opt = self.optimizer
+        leaf_key = prng.fold_in(key, self.leaf_index)
+        if isinstance(opt, AdamPGDConfig):
+            self.step_count += 1.0
+            ops.source_ascend(L.PGD_ADAM, self.sources, grad.contiguous(), self.state_a, self.state_b,
+                              step_count=self.step_count, lr=lr, beta1=opt.beta1, beta2=opt.beta2, eps=opt.eps,
+                              key=leaf_key)
+        elif isinstance(opt, MomentumSgdPGDConfig):
+            ops.source_ascend(L.PGD_MOMENTUM, self.sources, grad.contiguous(), self.state_a, lr=lr,
+                              momentum=opt.momentum, key=leaf_key)
+        else:
+            ops.source_ascend(L.PGD_SGD, self.sources, grad.contiguous(), lr=lr, key=leaf_key)
+        return self
+
+    def warmup_ascend(self, scoring_grad, lr: float, key) -> "PersistentAdversary":
+        """`n_warmup` projected ascents; `scoring_grad(self)` returns the source gradient of
+        the detached reconstruction loss at the current sources (`:519-539`)."""
+        for ascent_key in prng.split(key, self.n_warmup) if self.n_warmup else []:
+            self.after_one_ascent(scoring_grad(self), lr, ascent_key)
+        return self
+
+    final_ascend = after_one_ascent
+
+
+def fresh_pgd_ascend(sources: torch.Tensor, grad: torch.Tensor, step_size: float) -> torch.Tensor:
+    """`clip(s + step_size * sign(g), 0, 1)` in place (fp32 sources)."""
+    return ops.source_ascend(L.PGD_SIGN, sources, grad.contiguous(), lr=step_size)
+
+
+@dataclass
+class PPGDStepResult:
+    loss: torch.Tensor  # fp32 [1], the final reconstruction loss
+    dV: torch.Tensor
+    dU: torch.Tensor
+    d_ci: torch.Tensor
+    warmup_losses: list
+
+
+class DenseSitePPGDStep:
+    """The persistent-PGD reconstruction step of one dense site (bf16 compute):
+    `n_warmup` ascents of the adversary on `mse(site(x, m(s)), target)` with the model
+    detached (only the mask gradient is formed), then the final forward whose backward
+    gives dV, dU, the CI gradient and the source gradient of the final ascent. The loss and
+    gradients are the unscaled term's: the term coefficient scales only the model side
+    when the caller assembles the objective, so the sources ascend even at coefficient 0
+    (pd/core/adversary.py:553-560)."""
+
+    def __init__(self, adversary: PersistentAdversary):
+        self.adv = adversary
+
+    def _source_grad(self, x, V, U, ci, target):
+        mask = self.adv.mask(ci)
+        out, xV, acts = ops.masked_linear_fwd(x, V, U, mask)
+        loss, g_out = ops.mse(out, target, 1.0, want_grad=True)
+        _, _, _, dm = ops.masked_linear_bwd(x, V, U, mask, xV, acts, g_out, want_dvu=False)
+        d_src, _ = source_mask_grad(dm, ci, self.adv.sources, self.adv.rows_per_source)
+        return loss, d_src
+
+    def step(self, x, V, U, ci, target, lr: float, key, adv_index: int = 0) -> PPGDStepResult:
+        """`key` is the step's adversary key: the warmup ascents take
+        fold_in(fold_in(key, 0x51C), adv_index) (pd/core/train.py:746-753) and the final
+        ascent fold_in(fold_in(fold_in(key, 0x51C), 0x51D), adv_index) (:1004-1007, 1291)."""
+        quantize_key = prng.fold_in(key, 0x51C)
+        warm_key = prng.fold_in(quantize_key, adv_index)
+        final_key = prng.fold_in(prng.fold_in(quantize_key, 0x51D), adv_index)
+        warmup_losses = []
+
+        def scoring(_adv):
+            loss, d_src = self._source_grad(x, V, U, ci, target)
+            warmup_losses.append(loss)
+            return d_src
+
+        self.adv.warmup_ascend(scoring, lr, warm_key)
+        mask = self.adv.mask(ci)
+        out, xV, acts = ops.masked_linear_fwd(x, V, U, mask)
+        loss, g_out = ops.mse(out, target, 1.0, want_grad=True)
+        _, dV, dU, dm = ops.masked_linear_bwd(x, V, U, mask, xV, acts, g_out)
+        d_src, d_ci = source_mask_grad(dm, ci, self.adv.sources, self.adv.rows_per_source, want_dci=True)
+        self.adv.final_ascend(d_src, lr, final_key)
+        return PPGDStepResult(loss=loss, dV=dV, dU=dU, d_ci=d_ci, warmup_losses=warmup_losses)

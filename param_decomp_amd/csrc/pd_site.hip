@@ -129,7 +129,7 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
                          void* dmask, void* workspace, size_t workspace_bytes, void* stream) {
-  if (T <= 0 || d_in <= 0 || d_out <= 0 || C <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out || !dV || !dU)
+  if (T <= 0 || d_in <= 0 || d_out <= 0 || C <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out)
     return fail(PD_EINVAL, "pd_masked_linear_bwd: bad args");
   if ((delta || route) && dx && !W) return fail(PD_EINVAL, "pd_masked_linear_bwd: W required for dx");
   if (!workspace || workspace_bytes < pd_masked_linear_bwd_workspace_size(dtype, T, d_out, C))
@@ -141,7 +141,9 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
   void* gt = ws + ((es * T * C + 255) & ~(size_t)255);
   int rc;
   // dU = acts^T @ g (unrouted rows of acts are zero)
-  if ((rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream))) return rc;
+  if (dU && (rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream)))
+    return rc;
+  if (!dV && !dx && !dmask) return PD_OK;
   // da = g @ U^T
   if ((rc = pd_gemm(dtype, T, C, d_out, g_out, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
   if (dtype == PD_DTYPE_F32)
@@ -152,7 +154,7 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
                        (const bf16_t*)mask, (const bf16_t*)delta, route, T, C, (bf16_t*)dmask);
   if ((rc = check_launch("pd_masked_linear_bwd elem"))) return rc;
   // dV = x^T @ dxV
-  if ((rc = pd_gemm(dtype, d_in, C, T, x, d_in, 1, da, C, 0, dV, C, dtype, 1.f, 0.f, stream))) return rc;
+  if (dV && (rc = pd_gemm(dtype, d_in, C, T, x, d_in, 1, da, C, 0, dV, C, dtype, 1.f, 0.f, stream))) return rc;
   if (!dx) return PD_OK;
   // dx = dxV @ V^T (+ g_target @ W)
   if ((rc = pd_gemm(dtype, T, d_in, C, da, C, 0, V, C, 1, dx, d_in, dtype, 1.f, 0.f, stream))) return rc;

@@ -283,3 +283,59 @@ def faithfulness_bwd(delta, V, U, w_sq_norms, mats_per_site: int, scale: float, 
     L.call("pd_faithfulness_bwd", n, mats_per_site, d_in, d_out, C, L.ptr(delta), L.ptr(V), L.ptr(U), L.ptr(w_sq_norms),
            scale, L.ptr(d_loss), L.ptr(dV), L.ptr(dU), L.stream())
     return dV, dU
+
+
+def masked_linear_fwd(x, V, U, mask):
+    """`pd_masked_linear_fwd` without delta or route: (out, xV, acts) with acts = xV * mask."""
+    T, d_in = x.shape
+    C, d_out = U.shape
+    out = torch.empty((T, d_out), dtype=x.dtype, device=x.device)
+    xV = torch.empty((T, C), dtype=x.dtype, device=x.device)
+    acts = torch.empty((T, C), dtype=x.dtype, device=x.device)
+    L.call("pd_masked_linear_fwd", L.dtype_code(x.dtype), T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), None,
+           L.ptr(mask), None, None, L.ptr(out), L.ptr(xV), L.ptr(acts), L.stream())
+    return out, xV, acts
+
+
+def masked_linear_bwd(x, V, U, mask, xV, acts, g_out, *, want_dx=False, want_dvu=True, want_dmask=True):
+    """`pd_masked_linear_bwd` without delta or route; each output optional."""
+    T, d_in = x.shape
+    C, d_out = U.shape
+    dx = torch.empty_like(x) if want_dx else None
+    dV = torch.empty_like(V) if want_dvu else None
+    dU = torch.empty_like(U) if want_dvu else None
+    dm = torch.empty_like(mask) if want_dmask else None
+    dt = L.dtype_code(x.dtype)
+    ws = L.workspace(L.load().pd_masked_linear_bwd_workspace_size(dt, T, d_out, C), x.device)
+    L.call("pd_masked_linear_bwd", dt, T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), None, L.ptr(mask), None, None,
+           L.ptr(xV), L.ptr(acts), L.ptr(g_out), L.ptr(dx), L.ptr(dV), L.ptr(dU), L.ptr(dm), L.ptr(ws), ws.numel(),
+           L.stream())
+    return dx, dV, dU, dm
+
+
+def source_mask_fwd(ci, sources, rows_per_source: int):
+    """m = ci + (1 - ci) s for ci [rows, C] and sources [rows / rows_per_source, C]."""
+    rows, C = _flat_rows(ci)
+    mask = torch.empty_like(ci)
+    L.call("pd_source_mask_fwd", L.ptr(ci), L.dtype_code(ci.dtype), rows, C, L.ptr(sources),
+           L.dtype_code(sources.dtype), rows_per_source, L.ptr(mask), L.stream())
+    return mask
+
+
+def source_mask_bwd(g_mask, ci, sources, rows_per_source: int, want_dci: bool = False):
+    rows, C = _flat_rows(ci)
+    d_src = torch.empty((rows // rows_per_source, C), dtype=torch.float32, device=ci.device)
+    d_ci = torch.empty_like(ci) if want_dci else None
+    ws = L.workspace(L.load().pd_source_mask_bwd_workspace_size(rows, C, rows_per_source), ci.device)
+    L.call("pd_source_mask_bwd", L.ptr(g_mask), L.ptr(ci), L.dtype_code(ci.dtype), rows, C, L.ptr(sources),
+           L.dtype_code(sources.dtype), rows_per_source, L.ptr(d_src), L.ptr(d_ci), L.ptr(ws), ws.numel(), L.stream())
+    return d_src, d_ci
+
+
+def source_ascend(opt: int, sources, grad, state_a=None, state_b=None, *, step_count=0.0, lr=1.0, beta1=0.9,
+                  beta2=0.999, eps=1e-8, momentum=0.0, key: Key = (0, 0), layout: int = L.LAYOUT_PARTITIONABLE):
+    """One projected ascent of `sources` in place (see pd_source_ascend)."""
+    L.call("pd_source_ascend", opt, L.dtype_code(sources.dtype), sources.numel(), L.ptr(sources), L.ptr(grad),
+           L.ptr(state_a), L.ptr(state_b), step_count, lr, beta1, beta2, eps, momentum, key[0], key[1], layout,
+           L.stream())
+    return sources
