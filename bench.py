@@ -84,34 +84,34 @@ def rocprof_summary(db_path: str, command: str) -> str:
 
 # The kernel behind each phase, as named in profiles/hbm_traffic_pmc.md (a prefix of the
 # demangled name: the phases of one kernel template share its per-dispatch average).
+# Kernels of a timed phase (name prefixes as rocprofv3 prints them). A phase's traffic per
+# launch is the dispatch-weighted mean over its kernels in the committed PMC summary.
 PHASE_KERNEL = {
-    MOE: {"gemm_fwd": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 1,",
-          "gemm_dx": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 1,",
-          "gemm_dw": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 2,",
-          "mask_fwd": "pd::k_mask_fwd_tile", "mask_bwd": "pd::k_mask_bwd_tile"},
-    DENSE: {"gate_mask_fwd": "pd::k_step_fwd", "gate_mask_bwd": "pd::k_step_bwd", "recon": "pd::k_step_recon",
-            "gemm_xV": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
-            "gemm_actsU": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
-            "gemm_da": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, unsigned short, 0,",
-            "gemm_dU": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 0,",
-            "gemm_dV": "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2>, float, 0,"},
+    MOE: {"gemm_dw": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, float, 2,",
+                      "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 2,"),
+          "mask_fwd": ("pd::k_mask_fwd_tile",), "mask_bwd": ("pd::k_mask_bwd_tile",)},
+    DENSE: {"gate_mask_fwd": ("pd::k_step_fwd_tab",), "gate_mask_bwd": ("pd::k_step_bwd",),
+            "recon": ("pd::k_step_recon",)},
 }
 
 
 def pmc_traffic(workload, phase):
-    """Calibrated HBM bytes per dispatch of the phase's kernel from the committed PMC
+    """Calibrated HBM bytes per launch of the phase's kernels from the committed PMC
     summary (FETCH_SIZE and WRITE_SIZE runs scaled by a 1 GiB copy), or None."""
-    prefix = PHASE_KERNEL.get(workload, {}).get(phase)
+    prefixes = PHASE_KERNEL.get(workload, {}).get(phase)
     path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
-    if prefix is None or not os.path.exists(path):
+    if prefixes is None or not os.path.exists(path):
         return None
-    section = None
+    section, total, count = None, 0.0, 0
     for line in open(path):
         if line.startswith("## "):
             section = line[3:].strip()
-        elif section == workload and line.startswith("| `") and line.split("`")[1].startswith(prefix):
-            return float(line.rstrip().rstrip("|").split("|")[-1])
-    return None
+        elif section == workload and line.startswith("| `") and line.split("`")[1].startswith(prefixes):
+            cells = [c.strip() for c in line.rstrip().rstrip("|").split("|")]
+            n = int(cells[2])
+            total += float(cells[-1]) * n
+            count += n
+    return total / count if count else None
 
 
 def roofline(kind, amount_per_launch, ms_per_launch, kernel, launches_per_step, traffic=None):

@@ -327,8 +327,8 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
     return fail(PD_EUNSUPPORTED, "pd_gemm: bf16 operands need 16B alignment and contiguous dims / ld % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, 0, 0};
   if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
-    return launch_dtl<CfgDtl, MODE_DENSE>(a, c_dtype, K % CfgDtl::BK != 0,
-                                          dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(M, CfgDtl::BM)), s);
+    return launch_dtl<CfgDtlRA, MODE_DENSE>(a, c_dtype, K % CfgDtlRA::BK != 0,
+                                            dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM)), s);
   if (use_big_tile(M, N))
     return launch_bf16<CfgBig, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
                                            dim3((unsigned)cdiv(N, 256), (unsigned)cdiv(M, 256)), s);
@@ -362,8 +362,9 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, stride_b,
              stride_c, stride_a};
   if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
-    return launch_dtl<CfgDtl, MODE_BATCHED>(
-        a, c_dtype, K % CfgDtl::BK != 0, dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(M, CfgDtl::BM), (unsigned)batch),
+    return launch_dtl<CfgDtlRA, MODE_BATCHED>(
+        a, c_dtype, K % CfgDtlRA::BK != 0,
+        dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)batch),
         s);
   return launch_bf16<CfgSmall, MODE_BATCHED>(
       a, a_kmaj, b_kmaj, c_dtype, dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)batch), s);
@@ -397,7 +398,9 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
   int64_t max_tiles = cdiv(J, CfgSmall::BM) + E;
   if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm: too many rows");
   dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)max_tiles);
-  if (b_kmaj && dtl_fits(J, K, N, K)) return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, K % CfgDtl::BK != 0, grid, s);
+  static_assert(CfgDtlRA::BM == CfgSmall::BM && CfgDtlRA::BN == CfgSmall::BN, "one grid shape for both kernels");
+  if (b_kmaj && dtl_fits(J, K, N, K))
+    return launch_dtl<CfgDtlRA, MODE_GROUPED>(a, out_dtype, K % CfgDtlRA::BK != 0, grid, s);
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
@@ -411,12 +414,15 @@ int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const voi
     return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: K must be a multiple of 8 with 16B-aligned bases");
   GemmArgs a{J, N, K, (const bf16_t*)lhs1, K, (const bf16_t*)rhsT1, K, out1, N, 1.f, 0.f, offsets, E, K * N, 0, 0,
              (const bf16_t*)lhs2, (const bf16_t*)rhsT2, out2};
-  const int64_t max_tiles = cdiv(J, CfgDtl::BM) + E;
-  if (max_tiles > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: too many rows");
+  if (cdiv(J, CfgDtlRA::BM) + E > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: too many rows");
   if (!dtl_fits(J, K, N, K)) return fail(PD_EUNSUPPORTED, "grouped_gemm_pair: operands of 2 GiB or more");
-  return launch_dtl<CfgDtl, MODE_GROUPED>(a, out_dtype, K % CfgDtl::BK != 0,
-                                          dim3((unsigned)cdiv(N, CfgDtl::BN), (unsigned)max_tiles, 2),
-                                          (hipStream_t)stream);
+  if (N >= 512)  // 256x256 tiles: measured faster for the paired N=512 products
+    return launch_dtl<CfgDtlBig, MODE_GROUPED>(
+        a, out_dtype, K % CfgDtlBig::BK != 0,
+        dim3((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)(cdiv(J, CfgDtlBig::BM) + E), 2), (hipStream_t)stream);
+  return launch_dtl<CfgDtlRA, MODE_GROUPED>(
+      a, out_dtype, K % CfgDtlRA::BK != 0,
+      dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), 2), (hipStream_t)stream);
 }
 
 int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out1, const void* lhsT2,
@@ -432,8 +438,9 @@ int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out
   GemmArgs a{K, N, J, (const bf16_t*)lhsT1, J, (const bf16_t*)doutT1, J, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
              (const bf16_t*)lhsT2, (const bf16_t*)doutT2, out2};
   if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: operands of 2 GiB or more");
-  dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)(2 * E));
-  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
+  // 256x256 tiles: measured faster for both paired weight-gradient shapes
+  dim3 grid((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)cdiv(K, CfgDtlBig::BM), (unsigned)(2 * E));
+  return launch_dtl<CfgDtlBig, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // namespace pd
@@ -464,8 +471,8 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
   // out[e] (M=K x N) = lhsT[:, rows_e] (A stored [K, J]: K-major) @ doutT[:, rows_e]^T (B stored [N, J])
   GemmArgs a{K, N, J, (const bf16_t*)lhsT, J, (const bf16_t*)doutT, J, out, N, 1.f, 0.f, offsets, E, 0, K * N};
   if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "pd_grouped_gemm_dw_kmajor: operands of 2 GiB or more");
-  dim3 grid((unsigned)cdiv(N, CfgDtl::BN), (unsigned)cdiv(K, CfgDtl::BM), (unsigned)E);
-  return launch_dtl<CfgDtl, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
+  dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(K, CfgDtlRA::BM), (unsigned)E);
+  return launch_dtl<CfgDtlRA, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // extern "C"
