@@ -42,6 +42,7 @@ MOE = "qwen35moe4L"
 CI_MLP = "ci_mlp768_h1024_C4096"
 CI_READOUT = "ci_readout_llama4L"
 PPGD_DENSE = "ppgd_dense768x3072_C4096"
+KL_STREAM = "kl_stream_llama4L"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
 PEAK_FP32_MFMA = 157.3e12
@@ -52,6 +53,9 @@ WORKLOADS = {
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
     CI_READOUT: dict(T=8192, C=4 * (4 * 768 + 2 * 3072)),
+    # streamed-vocab KL over the factored lm-head edge of the 4-layer Llama-style target:
+    # 16 x 512 positions, d_model 768, vocab 50277 in 3 chunks (bf16)
+    KL_STREAM: dict(N=16 * 512, d=768, V=50277, n_chunks=3),
     # persistent PGD on the dense site: per-token uint16 sources, momentum SGD, 2 warmup
     # ascents (the reference's LM PPGD setting)
     PPGD_DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096, n_warmup=2, source_shape="bsc", source_dtype="uint16",
@@ -339,6 +343,85 @@ def run_ci(args):
                                                     pmc_traffic(args.workload, dom))}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = ci_cpu_baseline(args.workload, cfg, args.cpu_tokens)
+    return res
+
+
+# ============================================================== streamed-vocab KL
+def kl_cpu_baseline(cfg, N_sample, reps=3):
+    import numpy as np
+
+    from oracle import pd_oracle as po
+
+    rng = np.random.default_rng(0)
+    d, V = cfg["d"], cfg["V"]
+    aq, ap = rng.normal(size=(N_sample, d)) * 0.5, rng.normal(size=(N_sample, d)) * 0.5
+    hq, hp = rng.normal(size=(V, d)) * 0.05, rng.normal(size=(V, d)) * 0.05
+    g = np.full(N_sample, 1.0 / N_sample)
+    run = lambda: (po.streamed_position_kl(aq, hq, ap, hp, cfg["n_chunks"]),
+                   po.streamed_position_kl_vjp(aq, hq, ap, hp, g))
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": N_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{N_sample} positions (full d and vocab), NumPy float64 restatement of the streamed KL and "
+                      f"its input gradient (BLAS-threaded), median of {reps}; {med * 1e3:.1f} ms per sample"}
+
+
+def run_kl(args):
+    """Streamed-vocab KL fwd + bwd: per vocab chunk, the clean and masked logit blocks
+    from the bf16 GEMM, the paired online-softmax update, and in the backward the
+    re-derived logits' (q - p) g through the masked head."""
+    import torch
+
+    from param_decomp_amd import hip_events
+    from param_decomp_amd.losses import streamed_position_kl
+
+    cfg = WORKLOADS[args.workload]
+    N, d, V, nc = cfg["N"], cfg["d"], cfg["V"], cfg["n_chunks"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    aq = (torch.randn(N, d, device=dev, generator=gen) * 0.5).to(torch.bfloat16).requires_grad_(True)
+    ap = (torch.randn(N, d, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+    hq = (torch.randn(V, d, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+    hp = (torch.randn(V, d, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+    g = torch.full((N,), 1.0 / N, device=dev)
+    for _ in range(args.warmup):
+        torch.autograd.grad(streamed_position_kl(aq, hq, ap, hp, nc), aq, g)
+    stream = torch.cuda.current_stream().cuda_stream
+    evs = hip_events.create(3 * args.steps)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        hip_events.record(evs[3 * i], stream)
+        kl = streamed_position_kl(aq, hq, ap, hp, nc)
+        hip_events.record(evs[3 * i + 1], stream)
+        torch.autograd.grad(kl, aq, g)
+        hip_events.record(evs[3 * i + 2], stream)
+    torch.cuda.synchronize()
+    phase = {"fwd": 0.0, "bwd": 0.0}
+    for i in range(args.steps):
+        phase["fwd"] += hip_events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) / args.steps
+        phase["bwd"] += hip_events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) / args.steps
+    hip_events.destroy(evs)
+    assert torch.isfinite(kl).all()
+    mm = 2 * N * d * V
+    work = {"fwd": 2 * mm, "bwd": 3 * mm}
+    dom = max(phase, key=phase.get)
+    res = {"tokens": N, "ms_per_step": phase["fwd"] + phase["bwd"],
+           "config": {"workload": args.workload, "positions": N, "d_model": d, "vocab": V, "n_vocab_chunks": nc},
+           "step_flops": 5 * mm, "phases_ms": phase,
+           "roofline": roofline("flop", work[dom], phase[dom],
+                                {"fwd": "the chunk logit GEMMs (clean, masked) + k_kl_chunk",
+                                 "bwd": "the re-derived chunk logits + k_kl_grad + the input-gradient GEMM"}[dom], 1)}
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = kl_cpu_baseline(cfg, args.cpu_tokens)
     return res
 
 
@@ -665,7 +748,8 @@ def main():
               "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256}.get(args.workload, 0)
+        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
+                           KL_STREAM: 64}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
     elif args.workload == DENSE:
@@ -674,6 +758,8 @@ def main():
         res = run_faith(args)
     elif args.workload == PPGD_DENSE:
         res = run_ppgd(args)
+    elif args.workload == KL_STREAM:
+        res = run_kl(args)
     else:
         res = run_ci(args)
     ms = res["ms_per_step"]

@@ -115,11 +115,12 @@ int pd_kl(const void* masked_logits, const void* clean_logits, int dtype, int64_
 /* Streamed-vocab KL (pd/targets/losses.py:101-170 streamed_position_kl): per-position
  * KL(softmax(act_clean @ head_clean^T) || softmax(act_masked @ head_masked^T)) streamed over
  * n_chunks equal vocab chunks (V % n_chunks == 0) with the paired online-softmax
- * accumulators; the logits never materialize. act [N,d], head [V,d] in `dtype` (bf16:
- * d and V/n_chunks multiples of 8). fwd writes position_kl [N] and stats [N,5] =
+ * accumulators; the logits never materialize. act [N,d], head [V,d] in `dtype` (bf16: d
+ * a multiple of 8; bf16 chunks are V/n_chunks rounded up to a multiple of 8, the last one
+ * ragged, which the KL does not depend on). fwd writes position_kl [N] and stats [N,5] =
  * (m_p, s_p, a, m_q, s_q); bwd writes d_act_masked [N,d] fp32 = sum_v (q - p) g[n]
  * head_masked[v] for the per-position cotangent g (the clean side is the target). */
-size_t pd_streamed_kl_workspace_size(int dtype, int64_t N, int64_t V, int n_chunks);
+size_t pd_streamed_kl_workspace_size(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks);
 int pd_streamed_kl_fwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks, const void* act_masked,
                        const void* head_masked, const void* act_clean, const void* head_clean, float* position_kl,
                        float* stats, void* workspace, size_t workspace_bytes, void* stream);

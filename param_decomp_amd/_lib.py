@@ -43,7 +43,7 @@ _SIGNATURES = {
     "pd_mse": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "pd_kl_workspace_size": (_c_sz, [_c_i64]),
     "pd_kl": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
-    "pd_streamed_kl_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i32]),
+    "pd_streamed_kl_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
     "pd_streamed_kl_fwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 6 + [_c_p, _c_sz, _c_p]),
     "pd_streamed_kl_bwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),
     "pd_gemm": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_i32, _c_p, _c_i64,

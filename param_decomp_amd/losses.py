@@ -108,7 +108,7 @@ class _StreamedKL(torch.autograd.Function):
         dt = L.dtype_code(act_masked.dtype)
         kl = torch.empty(N, dtype=torch.float32, device=act_masked.device)
         stats = torch.empty((N, 5), dtype=torch.float32, device=act_masked.device)
-        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, V, n_chunks), act_masked.device)
+        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, d, V, n_chunks), act_masked.device)
         args = (dt, N, d, V, n_chunks, L.ptr(act_masked), L.ptr(head_masked), L.ptr(act_clean), L.ptr(head_clean))
         L.call("pd_streamed_kl_fwd", *args, L.ptr(kl), L.ptr(stats), L.ptr(ws), ws.numel(), L.stream())
         ctx.save_for_backward(act_masked, head_masked, act_clean, head_clean, stats)
@@ -122,7 +122,7 @@ class _StreamedKL(torch.autograd.Function):
         V = head_masked.shape[0]
         dt = L.dtype_code(act_masked.dtype)
         d_act = torch.empty((N, d), dtype=torch.float32, device=act_masked.device)
-        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, V, ctx.n_chunks), act_masked.device)
+        ws = L.workspace(L.load().pd_streamed_kl_workspace_size(dt, N, d, V, ctx.n_chunks), act_masked.device)
         L.call("pd_streamed_kl_bwd", dt, N, d, V, ctx.n_chunks, L.ptr(act_masked), L.ptr(head_masked),
                L.ptr(act_clean), L.ptr(head_clean), L.ptr(stats), L.ptr(g.float().contiguous()), L.ptr(d_act),
                L.ptr(ws), ws.numel(), L.stream())

@@ -525,17 +525,21 @@ def test_grouped_gemm_dw_kmajor(device, sizes, out_dtype):
 # ------------------------------------------------------------------ streamed-vocab KL
 
 
-@pytest.mark.parametrize("dtype,n_chunks", [(torch.float32, 1), (torch.float32, 3), (torch.float32, 8),
-                                            (torch.bfloat16, 8), (torch.bfloat16, 2)])
-def test_streamed_kl_fwd_bwd(device, dtype, n_chunks):
+@pytest.mark.parametrize("dtype,n_chunks,V", [(torch.float32, 1, 1200), (torch.float32, 3, 1200),
+                                              (torch.float32, 8, 1200), (torch.bfloat16, 8, 4096),
+                                              (torch.bfloat16, 2, 4096), (torch.bfloat16, 3, 4101),
+                                              (torch.bfloat16, 1, 2011)])
+def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V):
     """Per-position KL and the masked-activation gradient against the float64 oracle on
     the same (dtype-rounded) inputs. fp32: |err| <= 1e-4 |want| + 2e-6 max|want| (fp32
     logits accumulated over d, exp/log in fp32). bf16: the gradient's (q - p) g passes
-    through bf16 on its way into the GEMM, so rtol 2e-2."""
+    through bf16 on its way into the GEMM, so rtol 2e-2. V = 4101 (3 x 1367) and 2011 (prime)
+    give bf16 chunk widths that are not multiples of 8: the kernels stream 8-aligned chunks
+    and a ragged last one (the reference's LM vocab 50277 = 3 x 16759 is such a case)."""
     from param_decomp_amd.losses import streamed_kl_per_position, streamed_position_kl
 
-    rng = np.random.default_rng(n_chunks)
-    N, d, V = (300, 64, 1200) if dtype == torch.float32 else (512, 128, 4096)
+    rng = np.random.default_rng(n_chunks + V)
+    N, d = (300, 64) if dtype == torch.float32 else (512, 128)
     cast = (lambda a: f32(a, device)) if dtype == torch.float32 else (lambda a: bf(a, device))
     aq = cast(rng.normal(size=(N, d)) * 0.5).requires_grad_(True)
     ap = cast(rng.normal(size=(N, d)) * 0.5)
