@@ -27,6 +27,8 @@
 // outside [kmin, kend) is zeroed in the fragments of a tile's first and last stage.
 #pragma once
 
+#include <type_traits>
+
 #include "pd_common.hpp"
 
 namespace pd {
@@ -543,6 +545,94 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
     }
   }
   EPI::template run<CFG, TC>(p, ea, t, wm, wn, tid, acc, smem);
+}
+
+// Two products of one shape in one block, P1 = A @ B^T and P2 = A2 @ B2^T (dense, every
+// operand K-contiguous with the same lda / ldb), for epilogues that need both tiles of the
+// same (row, column) block at once. A stage holds A | B | A2 | B2 (B2 == B shares B's
+// rows and skips their loads). EPI::run(p, ea, tile, wm, wn, tid, acc1, acc2, smem).
+template <class CFG, bool KEDGE, class EPI>
+__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename EPI::Args ea) {
+  static_assert(CFG::NS == 2, "two LDS stages");
+  constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NW = CFG::NW;
+  constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
+  constexpr int SB = 2 * (BM + BN) * ROWB;
+  constexpr int LDS = 2 * SB > EPI::LDS_BYTES ? 2 * SB : EPI::LDS_BYTES;
+  static_assert(2 * SB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = uni(tid >> 6);
+  const int wm = wave / CFG::WN, wn = wave % CFG::WN;
+
+  TileJob t;
+  if (!map_tile<BM, BN, MODE_DENSE, float>(p, lane, t)) return;
+  const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
+  const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
+  const int64_t kbeg = kmin & ~(int64_t)7;
+  const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
+  const bool share_b = p.B2 == p.B;
+  const bf16_t* abase = (const bf16_t*)uni64((int64_t)(p.A + m0 * p.lda));
+  const bf16_t* a2base = (const bf16_t*)uni64((int64_t)(p.A2 + m0 * p.lda));
+  const bf16_t* bbase = (const bf16_t*)uni64((int64_t)(p.B + n0 * p.ldb));
+  const bf16_t* b2base = (const bf16_t*)uni64((int64_t)(p.B2 + n0 * p.ldb));
+  const int32_t abytes = buf_bytes((p.M - m0) * p.lda * 2), bbytes = buf_bytes((p.N - n0) * p.ldb * 2);
+  uint32_t offa[CFG::A_INSTS], offb[CFG::B_INSTS];
+  dtl_offsets<BM, NW>(offa, p.lda, wave, lane);
+  dtl_offsets<BN, NW>(offb, p.ldb, wave, lane);
+
+  f32x16 acc[TM][TN], acc2[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = acc2[i][j][v] = 0.f;
+
+  auto issue = [&](int64_t kt) {
+    char* st = smem + (int)(kt & 1) * SB;
+    const uint32_t koff = (uint32_t)((kbeg + kt * BK) * 2);
+    dtl_issue<BM, NW>(st, abase, abytes, offa, koff, wave);
+    dtl_issue<BN, NW>(st + BM * ROWB, bbase, bbytes, offb, koff, wave);
+    dtl_issue<BM, NW>(st + (BM + BN) * ROWB, a2base, abytes, offa, koff, wave);
+    if (!share_b) dtl_issue<BN, NW>(st + (2 * BM + BN) * ROWB, b2base, bbytes, offb, koff, wave);
+  };
+  if (nk > 0) issue(0);
+
+  const int sw = dtl_swz(lane & 31);
+  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
+  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
+  const int a2_off = a_off + (BM + BN) * ROWB;
+  const int b2_off = share_b ? b_off : b_off + (BM + BN) * ROWB;
+  auto sync = [&](int64_t kt) {
+    wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+  };
+  auto stage = [&](int64_t kt, auto edge) {
+    constexpr bool E = decltype(edge)::value;
+    const char* st = smem + (int)(kt & 1) * SB;
+    dtl_stage<CFG, E>(st, a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
+    dtl_stage<CFG, E>(st, a2_off, b2_off, sw, lane, kbeg + kt * BK, kmin, kend, acc2);
+  };
+  if constexpr (KEDGE) {
+    if (nk > 0) {
+      sync(0);
+      stage(0, std::true_type{});
+    }
+    for (int64_t kt = 1; kt < nk - 1; ++kt) {
+      sync(kt);
+      stage(kt, std::false_type{});
+    }
+    if (nk > 1) {
+      sync(nk - 1);
+      stage(nk - 1, std::true_type{});
+    }
+  } else {
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      sync(kt);
+      stage(kt, std::false_type{});
+    }
+  }
+  EPI::template run<CFG>(p, ea, t, wm, wn, tid, acc, acc2, smem);
 }
 
 // Dense C = A [M, K] @ B^T (B stored [N, K], both K-contiguous, lda/ldb % 8 == 0, 16-byte

@@ -525,11 +525,11 @@ def test_grouped_gemm_dw_kmajor(device, sizes, out_dtype):
 # ------------------------------------------------------------------ streamed-vocab KL
 
 
-@pytest.mark.parametrize("dtype,n_chunks,V", [(torch.float32, 1, 1200), (torch.float32, 3, 1200),
-                                              (torch.float32, 8, 1200), (torch.bfloat16, 8, 4096),
-                                              (torch.bfloat16, 2, 4096), (torch.bfloat16, 3, 4101),
-                                              (torch.bfloat16, 1, 2011)])
-def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V):
+@pytest.mark.parametrize("dtype,n_chunks,V,d", [(torch.float32, 1, 1200, 64), (torch.float32, 3, 1200, 64),
+                                                (torch.float32, 8, 1200, 64), (torch.bfloat16, 8, 4096, 128),
+                                                (torch.bfloat16, 2, 4096, 128), (torch.bfloat16, 3, 4101, 128),
+                                                (torch.bfloat16, 1, 2011, 128), (torch.bfloat16, 3, 999, 72)])
+def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V, d):
     """Per-position KL and the masked-activation gradient against the float64 oracle on
     the same (dtype-rounded) inputs. fp32: |err| <= 1e-4 |want| + 2e-6 max|want| (fp32
     logits accumulated over d, exp/log in fp32). bf16: the gradient's (q - p) g passes
@@ -539,7 +539,7 @@ def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V):
     from param_decomp_amd.losses import streamed_kl_per_position, streamed_position_kl
 
     rng = np.random.default_rng(n_chunks + V)
-    N, d = (300, 64) if dtype == torch.float32 else (512, 128)
+    N = 300 if dtype == torch.float32 else 512
     cast = (lambda a: f32(a, device)) if dtype == torch.float32 else (lambda a: bf(a, device))
     aq = cast(rng.normal(size=(N, d)) * 0.5).requires_grad_(True)
     ap = cast(rng.normal(size=(N, d)) * 0.5)
