@@ -6,8 +6,9 @@ Workloads (synthetic data of the named shapes, random-init weights):
   width 512, 42 experts with top-8 softmax routing, SwiGLU experts 512->256->512, every
   expert gate/up/down matrix decomposed with c=512 components per expert, 8192 tokens,
   bf16. A step is one `pd_moe_stack_step`: clean forward on the frozen experts, masked
-  forward (grouped masked-component matmuls over bucketed tokens), MSE recon of the final
-  residual + L_p (p=2) imp-min over the selected CI, and the full backward.
+  forward (grouped masked-component matmuls over bucketed tokens, with the frozen delta
+  channel of the reference's stochastic masking), MSE recon of the final residual + L_p
+  (p=2) imp-min over the selected CI, and the backward to every V/U and CI input.
 - `dense768x3072_C4096`: one decomposed dense linear 768->3072, x bf16 [4096, 768],
   C=4096, per-component gate MLP hidden 16, bf16 Threefry mask uniforms, stochastic-
   recon MSE + sum_c mean_t |g_upper|^2 fwd+bwd (`pd_dense_step`).
@@ -48,7 +49,8 @@ FAITH_MOE = "faith_qwen35moe4L"
 PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
-    MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4),
+    # with the frozen delta channel the reference's stochastic masking always draws
+    MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4, use_delta=True),
     CI_MLP: dict(T=4096, dims=(768, 1024, 4096)),
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
@@ -619,15 +621,31 @@ def moe_site_flops(J, d, f, c):
             "down": (2 * J * f * c, 2 * J * c * d)}
 
 
-def moe_step_flops(cfg):
-    J = cfg["T"] * cfg["k"]
-    per = moe_site_flops(J, cfg["d"], cfg["f"], cfg["c"])
-    total = 0
+def moe_gemm_flops(cfg):
+    """Per-category GEMM FLOPs of one step by the reference's linear rule
+    (`pd/core/flops/target.py:53-93`): a decomposed site costs in_proj + out_proj forward
+    (+ the frozen product W when the delta channel is on), and in backward in_proj per
+    gradient formed (input, components), out_proj twice (mask, components) and the frozen
+    product once more for the input gradient. Layer 0's gate/up inputs carry no mask
+    dependence: no input gradient there, and their frozen products are the clean pass's
+    (shared)."""
+    J, d, f, c, E, T = cfg["T"] * cfg["k"], cfg["d"], cfg["f"], cfg["c"], cfg["E"], cfg["T"]
+    per = moe_site_flops(J, d, f, c)
+    frozen = 2 * J * d * f if cfg.get("use_delta", True) else 0
+    fwd = dx = dw = 0
     for layer in range(cfg["L"]):
         for s, (i, o) in per.items():
-            dx = 0 if (layer == 0 and s != "down") else 1  # layer-0 gate/up inputs carry no mask dependence
-            total += (i + o) + i * (dx + 1) + o * 2
-    return total
+            changed = not (layer == 0 and s != "down")
+            fwd += i + o + frozen * changed
+            dx += o + (i + frozen) * changed
+            dw += i + o
+    clean = cfg["L"] * (2 * T * d * E + 3 * 2 * J * d * f)  # the clean pass's router and expert products
+    router = (cfg["L"] - 1) * 2 * (2 * T * d * E)  # masked-pass router fwd + input grad, layers >= 1
+    return {"gemm_fwd": fwd, "gemm_dx": dx, "gemm_dw": dw, "clean": clean, "router": router}
+
+
+def moe_step_flops(cfg):
+    return sum(moe_gemm_flops(cfg).values())
 
 
 def moe_cpu_baseline(cfg, T_sample, reps=1):
@@ -640,7 +658,7 @@ def moe_cpu_baseline(cfg, T_sample, reps=1):
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        mo.moe_stack_step(mc, params, x0, ci, (0, 1))
+        mo.moe_stack_step(mc, params, x0, ci, (0, 1), use_delta=cfg["use_delta"])
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     try:
@@ -675,7 +693,8 @@ def run_moe(args):
                    Ud=rn(Ln, E, c, d, scale=c**-0.5))
     x0 = rn(T, d, scale=1.0)
     ci = (torch.rand(Ln, 3, T, k, c, device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
-    step = MoEStackStep(T, d, f, E, k, c, Ln, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0)
+    step = MoEStackStep(T, d, f, E, k, c, Ln, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
+                        use_delta=cfg["use_delta"])
     for i in range(args.warmup):
         step.step(x0, w, ci, prng.fold_in((0, 0), i))
     cap = 1024
@@ -705,12 +724,11 @@ def run_moe(args):
     assert torch.isfinite(step.losses).all(), step.losses
     # algorithmic work per category (per step) for the roofline of the dominant one
     J = T * k
-    per = moe_site_flops(J, d, f, c)
+    gf = moe_gemm_flops(cfg)
     work = {
-        "gemm_fwd": ("flop", Ln * sum(i + o for i, o in per.values())),
-        "gemm_dx": ("flop", sum(o + (i if not (layer == 0 and s != "down") else i) for layer in range(Ln)
-                                for s, (i, o) in per.items())),
-        "gemm_dw": ("flop", Ln * sum(i + o for i, o in per.values())),
+        "gemm_fwd": ("flop", gf["gemm_fwd"]),
+        "gemm_dx": ("flop", gf["gemm_dx"]),
+        "gemm_dw": ("flop", gf["gemm_dw"]),
         "mask_fwd": ("byte", Ln * 3 * J * c * (2 + 2 + 2 + 1)),   # read ci, h; write acts, u bits
         "mask_bwd": ("byte", Ln * 3 * J * c * (2 + 2 + 1 + 2 + 2)),  # read ci, h, u, d_acts; write d_h, d_ci
     }
@@ -722,7 +740,8 @@ def run_moe(args):
         "tokens": T, "ms_per_step": ms_per_step,
         "config": {"workload": MOE, "tokens": T, "width": d, "experts": E, "top_k": k, "expert_ffn": f,
                    "c_per_expert": c, "layers": Ln, "imp_min": "p=2", "recon": "mse(final residual)",
-                   "mask_draw": "threefry bf16 (partitionable)", "mixers_and_shared_expert": "excluded"},
+                   "mask_draw": "threefry bf16 (partitionable)", "delta_channel": cfg["use_delta"],
+                   "mixers_and_shared_expert": "excluded"},
         "step_flops": moe_step_flops(cfg), "phases_ms": cat_ms, "launches_per_step": cat_n, "roofline": roof,
     }
     if not args.no_cpu_baseline:

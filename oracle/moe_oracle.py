@@ -13,8 +13,14 @@ the fp32 combine (`combine_jobs`, `pd/routed/experts.py:351-359`) and pins the m
 pass's expert indices (`_moe_forward`, `pd/targets/qwen36_moe.py:2923-2965`). Masks are
 drawn per (kind, layer) from `fold_in(fold_in(split(draw_key)[0], kind_index), layer)`
 (`pd/targets/qwen36_moe.py:3374-3401`) over the selected-CI values `[T, k*c]`
-(`SelectedCI`, `pd/core/components.py:81-114`). Loss: MSE between the masked and clean
-final residual streams plus the L_p imp-min over the selected upper CI values
+(`SelectedCI`, `pd/core/components.py:81-114`). The stochastic recipe also draws the
+frozen delta channel (`_entry_masking`, `pd/targets/qwen36_moe.py:2151-2160`): a
+per-token `d = uniform(fold_in(fold_in(split(draw_key)[1], kind_index), layer), [T])`
+in the CI dtype (`sample_delta_mask`, `pd/core/masking.py:139-140`), component
+coefficients `m - d` and site output `gmm(acts, U) + d * gmm(x_jobs, W[e])`
+(`pd/targets/qwen36_moe.py:2805-2815`, `pd/core/decomposed_linear.py:65-85`);
+`use_delta=False` is `d = 0`. Loss: MSE between the masked and clean final residual
+streams plus the L_p imp-min over the selected upper CI values
 (`pd/core/losses.py:357-372` selected arm).
 
 `bf16_storage=True` rounds to bf16 exactly the tensors the GPU step stores in bf16;
@@ -75,16 +81,22 @@ def site_mask_keys(draw_key, layer, partitionable=True):
     return {s: tf.fold_in(tf.fold_in(src_base, KIND_INDEX[s]), layer) for s in SITES}
 
 
+def site_delta_keys(draw_key, layer, partitionable=True):
+    _, delta_base = tf.split(draw_key, partitionable=partitionable)
+    return {s: tf.fold_in(tf.fold_in(delta_base, KIND_INDEX[s]), layer) for s in SITES}
+
+
 def grouped_T(lhs, rhs, sizes):
     """`lhs[rows_e] @ rhs[e].T` (the grouped matmul's d_input product)."""
     return po.grouped_matmul(lhs, np.transpose(rhs, (0, 2, 1)), sizes)
 
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                   bf16_storage=False, partitionable=True):
+                   bf16_storage=False, partitionable=True, use_delta=True, deltas=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
-    ci_pre[l][site]: [T, k, c]. Returns dict(loss, recon, imp, grads, d_ci_pre,
-    top_idx, r_final, rc_final)."""
+    ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
+    given. Returns dict(loss, recon, imp, grads, d_ci_pre, top_idx, r_final, rc_final,
+    deltas)."""
     rb = po.round_bf16 if bf16_storage else (lambda a: a)
     T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
     # ---------------- clean forward (frozen weights)
@@ -119,7 +131,9 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         w = po.expert_mixing_weights(probs, idx)
         jobs = po.routed_jobs(idx, E)
         keys = site_mask_keys(draw_key, l, partitionable)
+        dkeys = site_delta_keys(draw_key, l, partitionable)
         xj = h2[jobs.sort_idx // k]
+        tok = jobs.sort_idx // k
         S = {}
         for s in SITES:
             pre = ci_pre[l][s]
@@ -128,17 +142,28 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             imp += float(np.sum(up**p)) / T
             ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
             m_tok = lo + (1.0 - lo) * ut
-            S[s] = dict(pre=pre, lo=lo, up=up, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx])
+            if deltas is not None:
+                dt = np.asarray(deltas[l][s], np.float64)
+            elif use_delta:
+                dt = tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)
+            else:
+                dt = np.zeros(T)
+            dj = dt[tok][:, None]
+            S[s] = dict(pre=pre, lo=lo, up=up, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx], delta=dt, dj=dj)
+            S[s]["coef"] = S[s]["m"] - dj
         wj = w.reshape(-1)[jobs.sort_idx]
         for s in ("gate", "up"):
             S[s]["h"] = rb(po.grouped_matmul(xj, P["V" + s[0]], jobs.group_sizes))
-            S[s]["acts"] = rb(S[s]["h"] * S[s]["m"])
-            S[s]["out"] = rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
+            S[s]["acts"] = rb(S[s]["h"] * S[s]["coef"])
+            frozen = rb(po.grouped_matmul(xj, P["W" + s[0]], jobs.group_sizes))
+            S[s]["out"] = rb(rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
+                             + S[s]["dj"] * frozen)
         gq, uq = S["gate"]["out"], S["up"]["out"]
         din = rb(silu(gq) * uq * wj[:, None])
         S["down"]["h"] = rb(po.grouped_matmul(din, P["Vd"], jobs.group_sizes))
-        S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["m"])
-        dout = rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
+        S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["coef"])
+        dout = (rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
+                + S["down"]["dj"] * rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes)))
         routed = rb(po.sum_jobs(dout, jobs))
         saved.append(dict(r=r, rinv=rinv, h2=h2, probs=probs, w=w, wj=wj, jobs=jobs, xj=xj, S=S, din=din, idx=idx))
         r = rb(r + routed)
@@ -159,9 +184,9 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_acts = rb(grouped_T(d_dout, P["Ud"], sizes))
         grads[l]["Ud"] = po.transposed_grouped_matmul(Sd["acts"], d_dout, sizes)
         Sd["dm"] = d_acts * Sd["h"]
-        d_h = rb(d_acts * Sd["m"])
+        d_h = rb(d_acts * Sd["coef"])
         grads[l]["Vd"] = po.transposed_grouped_matmul(sv["din"], d_h, sizes)
-        d_din = rb(grouped_T(d_h, P["Vd"], sizes))
+        d_din = rb(grouped_T(d_h, P["Vd"], sizes)) + Sd["dj"] * rb(grouped_T(d_dout, P["Wd"], sizes))
         # SwiGLU fold
         gq, uq, wj = S["gate"]["out"], S["up"]["out"], sv["wj"]
         sg = silu(gq)
@@ -174,9 +199,10 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             d_acts = rb(grouped_T(dgo, P["U" + s[0]], sizes))
             grads[l]["U" + s[0]] = po.transposed_grouped_matmul(Ss["acts"], dgo, sizes)
             Ss["dm"] = d_acts * Ss["h"]
-            d_h = rb(d_acts * Ss["m"])
+            d_h = rb(d_acts * Ss["coef"])
             grads[l]["V" + s[0]] = po.transposed_grouped_matmul(sv["xj"], d_h, sizes)
-            d_xj = d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
+            d_xj = (d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
+                    + Ss["dj"] * rb(grouped_T(dgo, P["W" + s[0]], sizes)))
         # mask pullback to the CI preactivations (token-major)
         for s in SITES:
             Ss = S[s]
@@ -198,7 +224,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
         dr = rb(dr + dx)
     return dict(loss=loss, recon=recon, imp=imp, grads=grads, d_ci_pre=d_pre, top_idx=tops, r_final=r,
-                rc_final=rc, dx0=dr)
+                rc_final=rc, dx0=dr, deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
 
 
 def init_moe(cfg: MoEConfig, rng):

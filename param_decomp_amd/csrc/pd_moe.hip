@@ -177,10 +177,15 @@ __global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__
 }
 
 // r_out[t,:] = bf16(r[t,:] + bf16(sum_s wt[t,s] * y[inv[t*k+s],:])) with fp32
-// accumulation in slot order; wt NULL = the unweighted sum_jobs. One wave per token.
+// accumulation in slot order; wt NULL = the unweighted sum_jobs. With the frozen channel
+// (yd, delta non-NULL) the routed sum also takes delta[t] * sum_s yd[inv[t*k+s],:]: a
+// token's k jobs share its delta draw, so the slot sum of the frozen outputs is scaled
+// once (pd/core/decomposed_linear.py:72-85). One wave per token.
 __global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restrict__ r, const bf16_t* __restrict__ y,
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ wt, int64_t T, int k, int d,
+                                                          const bf16_t* __restrict__ yd,
+                                                          const float* __restrict__ delta,
                                                           bf16_t* __restrict__ r_out) {
   const int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
   if (t >= T) return;
@@ -196,6 +201,17 @@ __global__ __launch_bounds__(256) void k_combine_residual(const bf16_t* __restri
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] += v[j];
       }
+    }
+    if (yd) {
+      float fr[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < k; ++s) {
+        load8(yd + (int64_t)inv[t * k + s] * d + i, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fr[j] += v[j];
+      }
+      const float dt = delta[t];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(dt, fr[j], acc[j]);
     }
     load8(r + t * d + i, v);
 #pragma unroll
@@ -231,7 +247,11 @@ struct SiteMaskArgs {
   uint32_t k0, k1;
   int layout;
   float p;
+  const float* delta;  // [T] the site's per-token delta draw, or NULL (d = 0)
+  int k;               // experts per token: job j belongs to token sort_idx[j] / k
 };
+
+__device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
 
 __device__ inline float powp(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
 __device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f)); }
@@ -242,8 +262,9 @@ __device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p
 
 // Forward mask: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at the job's
 // token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16); acts =
-// bf16(h * m) written as acts [J,c] and acts^T [c,J]; u stored as its 7-bit integer;
-// per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
+// bf16(h * (m - delta)) (the component coefficients m - d, pd/core/decomposed_linear.py:65-69;
+// d = 0 without the frozen channel) written as acts [J,c] and acts^T [c,J]; u stored as
+// its 7-bit integer; per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
 template <int LAYOUT>
 __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
@@ -263,7 +284,9 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
     bf16_t o[4] = {0, 0, 0, 0};
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
-      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q0 + q4;
+      const int32_t slot = a.sort_idx[j];
+      const int64_t src = (int64_t)slot * a.c + q0 + q4;
+      const float dt = job_delta(a, slot);
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
@@ -275,7 +298,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
         imp += powp(upper_fwd(pre[e]), a.p);
         const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
         ub |= kb << (8 * e);
-        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * ((float)kb * (1.f / 128.f))));
+        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * ((float)kb * (1.f / 128.f)) - dt));
       }
       *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
@@ -290,7 +313,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
   ttile_store(T, actsT, a.J, j0, a.J, q0, a.c, tid);
 }
 
-// Backward mask: d_h = bf16(d_acts * m) (in place over d_acts, plus d_h^T [c,J]) and the
+// Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts, plus d_h^T [c,J]) and the
 // CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
 // upper_vjp(pre, imp_scale * d upper^p), written token-major.
 __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
@@ -309,7 +332,9 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
     bf16_t o[4] = {0, 0, 0, 0};
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
-      const int64_t src = (int64_t)a.sort_idx[j] * a.c + q0 + q4;
+      const int32_t slot = a.sort_idx[j];
+      const int64_t src = (int64_t)slot * a.c + q0 + q4;
+      const float dt = job_delta(a, slot);
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const uint2 dw = *(const uint2*)(d_acts + idx);
@@ -322,7 +347,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
         const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
-        const float m = lo + (1.f - lo) * u;
+        const float m = lo + (1.f - lo) * u - dt;
         dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
                             upper_vjp(pre[e], imp_scale * dpowp(up, a.p)));
         o[e] = f32_to_bf16(da[e] * m);
@@ -340,11 +365,17 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
 // din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math) and its job-contiguous copy;
-// wt NULL = the frozen arm (no weight, no copy needed). f % 8 == 0.
-__global__ __launch_bounds__(256) void k_swiglu_fwd_tile(const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
+// wt NULL = the frozen arm (no weight, no copy needed). With the frozen channel (fg, fu
+// non-NULL) the site outputs first take their delta share, g = bf16(g + dg[t] * fg) and
+// u = bf16(u + du[t] * fu) for the job's token t = sort_idx[j] / k
+// (pd/targets/qwen36_moe.py:2810-2815), written back over g and u for the backward.
+// f % 8 == 0.
+__global__ __launch_bounds__(256) void k_swiglu_fwd_tile(bf16_t* __restrict__ g, bf16_t* __restrict__ u,
                                                          const float* __restrict__ wt,
                                                          const int32_t* __restrict__ sort_idx, int64_t J, int f,
-                                                         bf16_t* __restrict__ din, bf16_t* __restrict__ dinT) {
+                                                         const bf16_t* __restrict__ fg, const bf16_t* __restrict__ fu,
+                                                         const float* __restrict__ dg, const float* __restrict__ du,
+                                                         int k, bf16_t* __restrict__ din, bf16_t* __restrict__ dinT) {
   __shared__ TTile T;
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
@@ -359,9 +390,27 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd_tile(const bf16_t* __restric
       const int64_t idx = j * f + q0 + q4;
       const uint2 gw = *(const uint2*)(g + idx);
       const uint2 uw = *(const uint2*)(u + idx);
-      const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
-      const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
-      const float w = wt ? wt[sort_idx[j]] : 1.f;
+      float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
+      float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
+      const int32_t slot = sort_idx[j];
+      if (fg) {
+        const float dgt = dg[slot / k], dut = du[slot / k];
+        const uint2 fgw = *(const uint2*)(fg + idx);
+        const uint2 fuw = *(const uint2*)(fu + idx);
+        const float fgv[4] = {bf_lo(fgw.x), bf_hi(fgw.x), bf_lo(fgw.y), bf_hi(fgw.y)};
+        const float fuv[4] = {bf_lo(fuw.x), bf_hi(fuw.x), bf_lo(fuw.y), bf_hi(fuw.y)};
+        bf16_t gb[4], ub[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gb[e] = f32_to_bf16(fmaf(dgt, fgv[e], gv[e]));
+          ub[e] = f32_to_bf16(fmaf(dut, fuv[e], uv[e]));
+          gv[e] = bf16_to_f32(gb[e]);
+          uv[e] = bf16_to_f32(ub[e]);
+        }
+        *(uint2*)(g + idx) = make_uint2(bf_pack(gb[0], gb[1]), bf_pack(gb[2], gb[3]));
+        *(uint2*)(u + idx) = make_uint2(bf_pack(ub[0], ub[1]), bf_pack(ub[2], ub[3]));
+      }
+      const float w = wt ? wt[slot] : 1.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(gv[e] * sigm(gv[e]) * uv[e] * w);
       *(uint2*)(din + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
@@ -378,12 +427,15 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd_tile(const bf16_t* __restric
 
 // SwiGLU-fold backward on 64x64 tiles: d_g = bf16(d*u*w*silu'(g)), d_u = bf16(d*silu(g)*w)
 // with their job-contiguous copies, and the per-(job, tile) partial of
-// d_w[j] = sum_f d*silu(g)*u into d_w_part [J, tiles].
+// d_w[j] = sum_f d*silu(g)*u into d_w_part [J, tiles]. With the down site's frozen channel
+// (gd non-NULL) the cotangent of the down input is d = d_din + dd[t] * gd, gd = d_out @
+// W_down[e]^T of the job, t = sort_idx[j] / k.
 __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restrict__ d_din,
                                                          const bf16_t* __restrict__ g, const bf16_t* __restrict__ u,
                                                          const float* __restrict__ wt,
                                                          const int32_t* __restrict__ sort_idx, int64_t J, int f,
-                                                         bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_gT,
+                                                         const bf16_t* __restrict__ gd, const float* __restrict__ dd,
+                                                         int k, bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_gT,
                                                          bf16_t* __restrict__ d_u, bf16_t* __restrict__ d_uT,
                                                          float* __restrict__ d_w_part) {
   __shared__ TTile Tg, Tu;
@@ -399,11 +451,19 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
     float part = 0.f;
     if (j < J && qok) {
       const int64_t idx = j * f + q0 + q4;
-      const float w = wt[sort_idx[j]];
+      const int32_t slot = sort_idx[j];
+      const float w = wt[slot];
       const uint2 dw = *(const uint2*)(d_din + idx);
       const uint2 gw = *(const uint2*)(g + idx);
       const uint2 uw = *(const uint2*)(u + idx);
-      const float dv[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
+      float dv[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
+      if (gd) {
+        const float ddt = dd[slot / k];
+        const uint2 fw = *(const uint2*)(gd + idx);
+        const float fv[4] = {bf_lo(fw.x), bf_hi(fw.x), bf_lo(fw.y), bf_hi(fw.y)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dv[e] = fmaf(ddt, fv[e], dv[e]);
+      }
       const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
       const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
 #pragma unroll
@@ -466,7 +526,9 @@ __device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int
 // each of the NCH 512-column chunks (d <= 512 * NCH, d % 8 == 0):
 //   d_h2 = sum_s (dxa + dxb)[inv[t*k+s]] + d_logits @ router (slot sums first, then the
 //   experts in order, fp32); d_r_out = bf16(d_r + rms_norm_vjp(d_h2)). The TPW tokens of
-//   a wave share each 16-byte router load.
+//   a wave share each 16-byte router load. With the frozen channel (fxa non-NULL) each
+//   slot also adds da[t] * fxa + db[t] * fxb, the gate and up frozen products' input
+//   cotangents scaled by the token's delta draws.
 template <int TPW, int NCH>
 __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w_part, int n_part,
                                                    const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
@@ -475,6 +537,8 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
                                                    const bf16_t* __restrict__ dxb, const bf16_t* __restrict__ r,
                                                    const float* __restrict__ rinv, const float* __restrict__ ln,
                                                    const bf16_t* __restrict__ d_r, int64_t T, int E, int k, int d,
+                                                   const bf16_t* __restrict__ fxa, const bf16_t* __restrict__ fxb,
+                                                   const float* __restrict__ da, const float* __restrict__ db,
                                                    bf16_t* __restrict__ d_r_out) {
   const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave_id()) * TPW;
   if (t0 >= T) return;
@@ -489,6 +553,7 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
 #pragma unroll
       for (int j = 0; j < 8; ++j) a[u][c][j] = 0.f;
     if (t >= T) continue;
+    const float dat = fxa ? da[t] : 0.f, dbt = fxa ? db[t] : 0.f;
     for (int s = 0; s < k; ++s) {
       const int64_t row = (int64_t)inv[t * k + s] * d;
 #pragma unroll
@@ -500,6 +565,12 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
           load8(dxb + row + i, vb);
 #pragma unroll
           for (int j = 0; j < 8; ++j) a[u][c][j] += va[j] + vb[j];
+          if (fxa) {
+            load8(fxa + row + i, va);
+            load8(fxb + row + i, vb);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[u][c][j] = fmaf(dat, va[j], fmaf(dbt, vb[j], a[u][c][j]));
+          }
         }
       }
     }
@@ -563,28 +634,30 @@ template <int TPW, int NCH>
 static void launch_token_bwd_t(const float* d_w_part, int n_part, const int32_t* inv, const int32_t* idx,
                                const float* probs, const float* w, const bf16_t* router, const bf16_t* dxa,
                                const bf16_t* dxb, const bf16_t* r, const float* rinv, const float* ln,
-                               const bf16_t* d_r, int64_t T, int E, int k, int d, bf16_t* d_r_out, hipStream_t s) {
+                               const bf16_t* d_r, int64_t T, int E, int k, int d, const bf16_t* fxa,
+                               const bf16_t* fxb, const float* da, const float* db, bf16_t* d_r_out, hipStream_t s) {
   hipLaunchKernelGGL((k_token_bwd<TPW, NCH>), dim3((unsigned)cdiv(T, 4 * TPW)), dim3(256), 0, s, d_w_part, n_part,
-                     inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d, d_r_out);
+                     inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d, fxa, fxb, da, db, d_r_out);
 }
 
 // d <= 4096 (checked by the step): the column chunks per lane set the register tile.
 static void launch_token_bwd(const float* d_w_part, int n_part, const int32_t* inv, const int32_t* idx,
                              const float* probs, const float* w, const bf16_t* router, const bf16_t* dxa,
                              const bf16_t* dxb, const bf16_t* r, const float* rinv, const float* ln, const bf16_t* d_r,
-                             int64_t T, int E, int k, int d, bf16_t* d_r_out, hipStream_t s) {
+                             int64_t T, int E, int k, int d, const bf16_t* fxa, const bf16_t* fxb, const float* da,
+                             const float* db, bf16_t* d_r_out, hipStream_t s) {
   if (d <= 512)
     launch_token_bwd_t<2, 1>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
-                             d_r_out, s);
+                             fxa, fxb, da, db, d_r_out, s);
   else if (d <= 1024)
     launch_token_bwd_t<2, 2>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
-                             d_r_out, s);
+                             fxa, fxb, da, db, d_r_out, s);
   else if (d <= 2048)
     launch_token_bwd_t<1, 4>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
-                             d_r_out, s);
+                             fxa, fxb, da, db, d_r_out, s);
   else
     launch_token_bwd_t<1, 8>(d_w_part, n_part, inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d,
-                             d_r_out, s);
+                             fxa, fxb, da, db, d_r_out, s);
 }
 
 __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, const float* __restrict__ imp_part,
@@ -613,6 +686,22 @@ __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, cons
     losses[1] = (float)a;
     losses[2] = (float)b;
   }
+}
+
+// Per-token delta draws of every (layer, site): delta[(l*3 + s)*T + t] =
+// uniform_bf16(fold_in(fold_in(delta_base, kind_s), l), [T])[t], the frozen channel's
+// sample_delta_mask (pd/core/masking.py:139-140) under the per-(kind, layer) keys of
+// pd/targets/qwen36_moe.py:3380-3398. Grid (cdiv(T, 256), 3L).
+__global__ __launch_bounds__(256) void k_delta_sites(uint32_t b0, uint32_t b1, int64_t T, int layout,
+                                                     float* __restrict__ delta) {
+  const int site = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  uint32_t x0 = 0, x1 = (uint32_t)(MOE_KIND_GATE + site % 3);
+  threefry2x32(b0, b1, x0, x1);
+  uint32_t k0 = 0, k1 = (uint32_t)(site / 3);
+  threefry2x32(x0, x1, k0, k1);
+  delta[(int64_t)site * T + t] = draw_uniform(k0, k1, t, T, PD_DTYPE_BF16, layout);
 }
 
 // ---------------------------------------------------------------- workspace plan
@@ -649,8 +738,8 @@ struct MoEPlan {
   std::vector<LayerSave> layers;
   // weight copies [L, E, N, K] for the forward products
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
-  float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *fg0, *fu0, *din, *downc, *down, *dr_a, *dr_b;
+  float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
   int32_t* sort_ws;
   bf16_t *d_dout, *d_doutT, *d_acts[2], *d_hT[2], *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
   size_t imp_per_site, total;
@@ -702,6 +791,8 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.acts[1] = A.take<bf16_t>(J * D.c);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
+  P.fg0 = A.take<bf16_t>(J * D.f);
+  P.fu0 = A.take<bf16_t>(J * D.f);
   P.din = A.take<bf16_t>(J * D.f);
   P.downc = A.take<bf16_t>(J * D.d);
   P.down = A.take<bf16_t>(J * D.d);
@@ -714,6 +805,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.imp_per_site = (size_t)cdiv(D.c, TILE) * cdiv(J, TILE);
   P.imp_part = A.take<float>(P.imp_per_site * 3 * D.L);
   P.d_w_part = A.take<float>(J * cdiv(D.f, TILE));
+  P.delta = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
   P.d_doutT = A.take<bf16_t>(J * D.d);
@@ -782,8 +874,8 @@ enum {
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p, float imp_coeff,
-                         float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
+                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout, float p,
+                         float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
                          float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
                          void* stream, Recorder& rec) {
   if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 64 || k <= 0 || k > E || c <= 0 || L <= 0)
@@ -809,10 +901,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const size_t szCI = (size_t)T * k * c;
   auto bf = [](const void* base, size_t off) { return (const bf16_t*)base + off; };
   int rc;
-  // ---- site keys: src_base = split(draw_key)[0]; key(kind, layer) = fold_in(fold_in(src_base, kind), layer)
+  // ---- site keys: src_base, delta_base = split(draw_key);
+  //      key(kind, layer) = fold_in(fold_in(base, kind), layer)
   uint32_t halves[4];
   split2(draw_k0, draw_k1, layout, halves);
   const uint32_t sb0 = halves[0], sb1 = halves[1];
+  const float* dlt[3] = {nullptr, nullptr, nullptr};  // the current layer's per-token delta draws
   auto site_key = [&](int kind, int layer, uint32_t& o0, uint32_t& o1) {
     uint32_t x0_ = 0, x1_ = (uint32_t)kind;
     threefry2x32(sb0, sb1, x0_, x1_);
@@ -840,7 +934,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const size_t szV[3] = {szVg, szVg, szVd};
   const size_t szU[3] = {szUg, szUg, szUd};
 
-  // ================= clean forward (frozen weights): pins the expert indices
+  if (use_delta)
+    hipLaunchKernelGGL(k_delta_sites, dim3((unsigned)cdiv(T, 256), (unsigned)(3 * L)), dim3(256), 0, s, halves[2],
+                       halves[3], T, layout, P.delta);
+  auto set_delta = [&](int l) {
+    for (int si = 0; si < 3; ++si) dlt[si] = use_delta ? P.delta + ((size_t)l * 3 + si) * T : nullptr;
+  };
+
+  // ================= clean forward (frozen weights): pins the expert indices. Layer 0's
+  // gate and up products are kept: the masked pass's layer-0 frozen channel reads the
+  // same inputs under the same routing.
   hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
   bf16_t* rcur = P.rc_a;
   bf16_t* rnext = P.rc_b;
@@ -857,15 +960,18 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, P.h2c, S.sort_idx, k, J, d, P.xj,
                        (bf16_t*)nullptr);
-    if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, P.gc, P.xj, P.WuT + l * szW, P.uc, S.offsets, J, E, d, f,
+    bf16_t* gcl = l == 0 ? P.fg0 : P.gc;
+    bf16_t* ucl = l == 0 ? P.fu0 : P.uc;
+    if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, gcl, P.xj, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
                                 PD_DTYPE_BF16, stream)))
       return rc;
-    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, P.gc, P.uc, (const float*)nullptr,
-                       S.sort_idx, J, f, P.din, (bf16_t*)nullptr);
+    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, gcl, ucl, (const float*)nullptr,
+                       S.sort_idx, J, f, (const bf16_t*)nullptr, (const bf16_t*)nullptr, (const float*)nullptr,
+                       (const float*)nullptr, k, P.din, (bf16_t*)nullptr);
     if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
       return rc;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
-                       rnext);
+                       (const bf16_t*)nullptr, (const float*)nullptr, rnext);
     std::swap(rcur, rnext);
     if (top_idx_out)
       hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
@@ -887,6 +993,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
                        S.probs, S.w);
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
+    set_delta(l);
     auto mask_fwd = [&](int si, bf16_t* acts_out) {
       SiteMaskArgs ma;
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
@@ -896,6 +1003,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.layout = layout;
       ma.p = p;
+      ma.delta = dlt[si];
+      ma.k = k;
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
       if (layout == PD_LAYOUT_PARTITIONABLE)
         hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_PARTITIONABLE>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
@@ -909,6 +1018,20 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = grouped_gemm_pair(P.xj, VT[0] + l * szV[0], S.h[0], P.xj, VT[1] + l * szV[1], S.h[1], S.offsets, J, E,
                                 d, c, PD_DTYPE_BF16, stream)))
       return rc;
+    // frozen channel of gate and up: x_jobs @ W[e] (layer 0: the clean pass's products)
+    const bf16_t* fg = nullptr;
+    const bf16_t* fu = nullptr;
+    if (use_delta) {
+      fg = P.fg0;
+      fu = P.fu0;
+      if (l > 0) {
+        if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, P.gc, P.xj, P.WuT + l * szW, P.uc, S.offsets, J, E, d, f,
+                                    PD_DTYPE_BF16, stream)))
+          return rc;
+        fg = P.gc;
+        fu = P.uc;
+      }
+    }
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(0, P.acts[0]);
     mask_fwd(1, P.acts[1]);
@@ -919,9 +1042,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     // ---- down site
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J, f,
-                       P.din, S.dinT);
+                       fg, fu, dlt[0], dlt[1], k, P.din, S.dinT);
     rec.mark(MOE_CAT_GEMM_FWD);
     if ((rc = grouped_gemm(P.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
+      return rc;
+    if (use_delta &&
+        (rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(2, P.acts[0]);
@@ -932,7 +1058,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, P.down, S.inv,
-                       (const float*)nullptr, T, k, d, r_out);
+                       (const float*)nullptr, T, k, d, use_delta ? P.downc : (const bf16_t*)nullptr, dlt[2], r_out);
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
@@ -958,6 +1084,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.c = c;
     ma.layout = layout;
     ma.p = p;
+    ma.k = k;
+    set_delta(l);
     // ---- down site
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[0], PD_DTYPE_BF16, stream,
@@ -970,6 +1098,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
+    ma.delta = dlt[2];
     hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale,
                        P.d_acts[0], P.d_hT[0], (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     rec.mark(MOE_CAT_GEMM_DW);
@@ -980,9 +1109,14 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = grouped_gemm(P.d_acts[0], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
                            false)))
       return rc;
+    // frozen channel of down: d_out @ W_down[e]^T, scaled by the token's delta in the fold
+    if (use_delta &&
+        (rc = grouped_gemm(P.d_dout, bf(Wd, l * szW), S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false)))
+      return rc;
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
-                       J, f, P.d_g, P.d_gT, P.d_u, P.d_uT, P.d_w_part);
+                       J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_gT, P.d_u, P.d_uT,
+                       P.d_w_part);
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
@@ -996,6 +1130,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     for (int si = 0; si < 2; ++si) {
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
+      ma.delta = dlt[si];
       hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], S.ub[si], imp_scale,
                          P.d_acts[si], P.d_hT[si], (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
     }
@@ -1003,15 +1138,24 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
                                           S.offsets, J, E, d, c, PD_DTYPE_F32, stream)))
       return rc;
-    rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm_pair(P.d_acts[0], bf(Vg, l * szVg), P.dxa, P.d_acts[1], bf(Vu, l * szVg), P.dxb, S.offsets,
-                                J, E, c, d, PD_DTYPE_BF16, stream)))
-      return rc;
-    // ---- routing weights, router, gather VJP and the norm
-    rec.mark(MOE_CAT_TOKEN_BWD);
-    launch_token_bwd(P.d_w_part, n_wpart, S.inv, S.idx, S.probs, S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb,
-                     S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, dr_next, s);
-    std::swap(dr, dr_next);
+    // The stack input carries no parameter gradient: layer 0 stops at its weight
+    // gradients (its gate/up input products and the token backward feed only d x0).
+    if (l > 0) {
+      rec.mark(MOE_CAT_GEMM_DX);
+      if ((rc = grouped_gemm_pair(P.d_acts[0], bf(Vg, l * szVg), P.dxa, P.d_acts[1], bf(Vu, l * szVg), P.dxb,
+                                  S.offsets, J, E, c, d, PD_DTYPE_BF16, stream)))
+        return rc;
+      // frozen channel of gate and up: d_g @ Wg[e]^T, d_u @ Wu[e]^T
+      if (use_delta && (rc = grouped_gemm_pair(P.d_g, bf(Wg, l * szW), P.downc, P.d_u, bf(Wu, l * szW), P.down,
+                                               S.offsets, J, E, f, d, PD_DTYPE_BF16, stream)))
+        return rc;
+      // ---- routing weights, router, gather VJP and the norm
+      rec.mark(MOE_CAT_TOKEN_BWD);
+      launch_token_bwd(P.d_w_part, n_wpart, S.inv, S.idx, S.probs, S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb,
+                       S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, use_delta ? P.downc : (const bf16_t*)nullptr,
+                       P.down, dlt[0], dlt[1], dr_next, s);
+      std::swap(dr, dr_next);
+    }
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
   }
   rec.mark(MOE_CAT_END);
@@ -1021,20 +1165,20 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
-                      uint32_t draw_k0, uint32_t draw_k1, int layout, float p, float imp_coeff, float recon_coeff,
-                      float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd,
+                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff,
+                      float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd,
                       void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                       draw_k1, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                       draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
                        top_idx_out, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int layout, float p,
-                            float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
+                            float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
                             float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
                             size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
                             int* n_recorded) {
@@ -1042,7 +1186,7 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
     return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
   Recorder rec{events, categories, capacity, 0, nullptr};
   int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                         draw_k1, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                         draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
                          top_idx_out, workspace, workspace_bytes, stream, rec);
   *n_recorded = rec.n;
   if (rc == PD_OK && rec.n >= capacity) return fail(PD_EINVAL, "pd_moe_stack_step_timed: event capacity too small");

@@ -1,7 +1,9 @@
 """The decomposed MoE stack step (the routed-expert hot path end to end) on the GPU.
 
 One call = the clean forward on the frozen experts (pinning each layer's expert
-indices), the masked forward with every routed expert matrix decomposed, MSE recon of
+indices), the masked forward with every routed expert matrix decomposed (with the
+frozen delta channel the reference's stochastic masking draws, unless `use_delta` is
+off), MSE recon of
 the final residual + L_p imp-min over the selected CI, and the full backward to the
 V/U factors of every site and to the CI preactivations. See `pd_moe_stack_step` in
 include/pd_mi355x.h for the reference citations and layouts.
@@ -44,9 +46,10 @@ class MoEWeights:
 class MoEStackStep:
     def __init__(self, T: int, d: int, f: int, E: int, k: int, c: int, n_layers: int, *, device="cuda",
                  p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
-                 layout: int = L.LAYOUT_PARTITIONABLE):
+                 layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True):
         self.dims = (T, d, f, E, k, c, n_layers)
         self.p, self.imp_coeff, self.recon_coeff, self.layout = p, imp_coeff, recon_coeff, layout
+        self.use_delta = bool(use_delta)
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
         Ln = n_layers
@@ -63,7 +66,7 @@ class MoEStackStep:
         T, d, f, E, k, c, Ln = self.dims
         return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
                 L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
-                draw_key[0], draw_key[1], self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
+                draw_key[0], draw_key[1], int(self.use_delta), self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]

@@ -1,6 +1,9 @@
 """Pins the MoE-stack oracle: central finite differences of its loss against its
 hand-written backward (V, U of every site, the CI preactivations and the stack input),
-and the routed forward against an every-expert dense spelling of the same layer."""
+the routed forward against a per-token, per-expert spelling of the same layer (mask,
+delta draws and frozen channel included), and the delta channel's defining identity:
+with every component live (m = 1) and V_e U_e = W_e the masked stack reproduces the
+clean one for any delta draw."""
 
 import numpy as np
 import pytest
@@ -84,21 +87,62 @@ def test_moe_layer_routed_equals_dense_spelling():
     probs = po.softmax(h2 @ P["router"].T)
     w = po.expert_mixing_weights(probs, idx)
     keys = mo.site_mask_keys((0, 3), 0)
+    dkeys = mo.site_delta_keys((0, 3), 0)
     from oracle import threefry as tf
 
-    m = {}
+    m, dl = {}, {}
     for s in mo.SITES:
         lo = po.lower_leaky(ci[0][s])
         u = tf.uniform(keys[s], (cfg.T, cfg.k * cfg.c), "bfloat16").reshape(cfg.T, cfg.k, cfg.c)
         m[s] = lo + (1 - lo) * u
+        # one bf16 draw per token, from the second half of the split draw key
+        dl[s] = tf.uniform(dkeys[s], (cfg.T,), "bfloat16")
+        assert np.all((dl[s] >= 0) & (dl[s] < 1)) and np.all(dl[s] * 128 == np.round(dl[s] * 128))
+        np.testing.assert_array_equal(res["deltas"][0][s], dl[s])
     out = x0.copy()
     for t in range(cfg.T):
         acc = np.zeros(cfg.d)
         for slot in range(cfg.k):
             e = idx[t, slot]
-            g = ((h2[t] @ P["Vg"][e]) * m["gate"][t, slot]) @ P["Ug"][e]
-            u_ = ((h2[t] @ P["Vu"][e]) * m["up"][t, slot]) @ P["Uu"][e]
+            g = (((h2[t] @ P["Vg"][e]) * (m["gate"][t, slot] - dl["gate"][t])) @ P["Ug"][e]
+                 + dl["gate"][t] * (h2[t] @ P["Wg"][e]))
+            u_ = (((h2[t] @ P["Vu"][e]) * (m["up"][t, slot] - dl["up"][t])) @ P["Uu"][e]
+                  + dl["up"][t] * (h2[t] @ P["Wu"][e]))
             din = mo.silu(g) * u_ * w[t, slot]
-            acc += ((din @ P["Vd"][e]) * m["down"][t, slot]) @ P["Ud"][e]
+            acc += (((din @ P["Vd"][e]) * (m["down"][t, slot] - dl["down"][t])) @ P["Ud"][e]
+                    + dl["down"][t] * (din @ P["Wd"][e]))
         out[t] += acc
     np.testing.assert_allclose(res["r_final"], out, rtol=1e-12, atol=1e-12)
+
+
+def test_moe_delta_channel_restores_the_target_when_every_component_is_live():
+    """ci >= 1 (lower(ci) = 1, m = 1) and exact factorizations V_e U_e = W_e: the site
+    output (h (1 - d)) U + d x W = x W whatever d is, so the masked stack equals the clean
+    one and the recon term vanishes. Dropping the frozen term, flipping the coefficient's
+    sign or using the mask draw for d all break it (the delta draws are far from 0)."""
+    cfg = mo.MoEConfig(T=16, d=8, f=6, E=4, k=2, c=8, L=2)
+    rng = np.random.default_rng(5)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    for P in params:
+        for s, (din_, dout_) in (("g", (cfg.d, cfg.f)), ("u", (cfg.d, cfg.f)), ("d", (cfg.f, cfg.d))):
+            V = P["V" + s][:, :din_, :]
+            # c >= d_in: V_e invertible on its leading d_in components; U_e solves V_e U_e = W_e
+            U = np.zeros((cfg.E, cfg.c, dout_))
+            for e in range(cfg.E):
+                U[e] = np.linalg.lstsq(V[e], P["W" + s][e], rcond=None)[0]
+            P["U" + s] = U
+            np.testing.assert_allclose(np.einsum("eic,eco->eio", V, U), P["W" + s], atol=1e-10)
+    ci = [{s: np.full((cfg.T, cfg.k, cfg.c), 1.2) for s in mo.SITES} for _ in range(cfg.L)]
+    res = mo.moe_stack_step(cfg, params, x0, ci, (0, 7), p=2.0, imp_coeff=0.0, recon_coeff=1.0)
+    assert min(float(d.max()) for layer in res["deltas"] for d in layer.values()) > 0.5
+    np.testing.assert_allclose(res["r_final"], res["rc_final"], rtol=1e-10, atol=1e-10)
+    assert res["recon"] < 1e-20
+    # a stack whose factorization is off reconstructs only approximately: the identity
+    # above is not vacuous
+    bent = [dict(P) for P in params]
+    bent[0]["Vg"] = bent[0]["Vg"] * 1.1
+    res2 = mo.moe_stack_step(cfg, bent, x0, ci, (0, 7), p=2.0, imp_coeff=0.0, recon_coeff=1.0)
+    assert res2["recon"] > 1e-6
+    # with the bent factorization the delta draw matters: d x (W - V U) differs per draw
+    res3 = mo.moe_stack_step(cfg, bent, x0, ci, (0, 7), p=2.0, imp_coeff=0.0, recon_coeff=1.0, use_delta=False)
+    assert abs(res3["recon"] - res2["recon"]) > 1e-3 * res2["recon"]
