@@ -153,14 +153,17 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
 int pd_masked_linear_fwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          void* out, void* xV, void* acts, void* stream);
-/* VJP: given d_out_grad [T,d_out] -> dx [T,d_in], dV, dU, dmask [T,C] (each nullable;
- * an adversarial source ascent asks for dmask alone). workspace holds two [T,C] and one
- * [T,d_out] tensors of `dtype`. */
+/* VJP: given d_out_grad [T,d_out] -> dx [T,d_in], dV, dU, dmask [T,C] and d_delta [T]
+ * (each nullable, of `dtype`; an adversarial source ascent asks for dmask and d_delta
+ * alone). d_delta[t] = routed ? sum_o g*(x@W^T) - sum_c (g@U^T)*xV : 0 is the weight-delta
+ * cotangent the reference's autodiff forms for delta sources (pd/core/source_mask.py:61-63,
+ * pd/core/adversary.py:74-82); it needs W, and is the gradient at d = 0 when delta is
+ * NULL. workspace holds two [T,C] and one [T,d_out] tensors of `dtype`. */
 size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, int64_t C);
 int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
-                         void* dmask, void* workspace, size_t workspace_bytes, void* stream);
+                         void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- block-factored site, dense over every block: pd/core/decomposed_linear.py:209-271
  *      blocked_site_forward with the einsums of pd/core/linear_plan.py:149-160.

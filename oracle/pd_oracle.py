@@ -149,6 +149,17 @@ def site_backward(x, W, V, U, mask, delta, route, dout):
     return dx, dV, dU, dmask
 
 
+def site_delta_grad(x, W, V, U, mask, delta, route, dout):
+    """VJP of `site_forward` w.r.t. the per-position delta (`[*lead]`): for a routed
+    position `sum_o dout * (x@W.T - (x@V*1)@U)`, i.e. `sum_o dout*target - sum_c
+    (dout@U.T)*xV`; 0 where unrouted. The weight-delta sources of adversarial masking
+    take this cotangent (`pd/core/source_mask.py:61-63`)."""
+    xV = x @ V
+    target = x @ W.T
+    g = np.sum(dout * target, axis=-1) - np.sum((dout @ U.T) * xV, axis=-1)
+    return g if route is None else np.where(route, g, 0.0)
+
+
 # ---------------------------------------------------------------- block-factored site
 def blocked_site_forward(x, W, V, U, mask, delta, route, contraction):
     """`pd/core/decomposed_linear.py:209-271` dense over every block, with the einsums of

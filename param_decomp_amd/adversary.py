@@ -151,38 +151,67 @@ class DenseSitePPGDStep:
     gives dV, dU, the CI gradient and the source gradient of the final ascent. The loss and
     gradients are the unscaled term's: the term coefficient scales only the model side
     when the caller assembles the objective, so the sources ascend even at coefficient 0
-    (pd/core/adversary.py:553-560)."""
+    (pd/core/adversary.py:553-560).
 
-    def __init__(self, adversary: PersistentAdversary):
+    `delta_adversary` adds the explicit weight-delta source of the site
+    (`SiteSource.delta`, pd/core/adversary.py:74-82): one value per token group, `[n_sources,
+    1]` with the components' `rows_per_source`, read as the site's delta mask
+    (`SourceMaskIngredients.delta_mask`, pd/core/source_mask.py:61-63), so the site output
+    becomes `(xV (m - d)) @ U + d (x @ W^T)`. It is the next leaf after the components
+    (`SourceStack` field order), so its uint16 rounding draws fold in `leaf_index + 1`.
+    The delta values are formed by the source-mask kernel at ci = 0 (`0 + (1 - 0) s = s`),
+    and their gradient is that kernel's pullback of the masked linear's delta cotangent."""
+
+    def __init__(self, adversary: PersistentAdversary, delta_adversary: PersistentAdversary | None = None):
         self.adv = adversary
+        self.dadv = delta_adversary
+        if delta_adversary is not None:
+            if delta_adversary.rows_per_source != adversary.rows_per_source or delta_adversary.n_warmup != adversary.n_warmup:
+                raise ValueError("delta sources share the component sources' shape and warmup count")
+            if delta_adversary.sources.shape[-1] != 1:
+                raise ValueError("delta sources are [n_sources, 1]: one value per token group")
 
-    def _source_grad(self, x, V, U, ci, target):
+    def _delta(self, zeros):
+        return None if self.dadv is None else source_mask(zeros, self.dadv.sources, self.dadv.rows_per_source)
+
+    def _grads(self, x, V, U, W, ci, target, zeros, *, final: bool):
         mask = self.adv.mask(ci)
-        out, xV, acts = ops.masked_linear_fwd(x, V, U, mask)
+        d = self._delta(zeros)
+        dvec = None if d is None else d.reshape(-1)
+        out, xV, acts = ops.masked_linear_fwd(x, V, U, mask, W=W, delta=dvec)
         loss, g_out = ops.mse(out, target, 1.0, want_grad=True)
-        _, _, _, dm = ops.masked_linear_bwd(x, V, U, mask, xV, acts, g_out, want_dvu=False)
-        d_src, _ = source_mask_grad(dm, ci, self.adv.sources, self.adv.rows_per_source)
-        return loss, d_src
+        _, dV, dU, dm, dd = ops.masked_linear_bwd(x, V, U, mask, xV, acts, g_out, W=W, delta=dvec, want_dvu=final,
+                                                  want_ddelta=d is not None)
+        d_src, d_ci = source_mask_grad(dm, ci, self.adv.sources, self.adv.rows_per_source, want_dci=final)
+        d_dsrc = None
+        if d is not None:
+            d_dsrc, _ = source_mask_grad(dd.reshape(-1, 1), zeros, self.dadv.sources, self.dadv.rows_per_source)
+        return loss, dV, dU, d_ci, d_src, d_dsrc
 
-    def step(self, x, V, U, ci, target, lr: float, key, adv_index: int = 0) -> PPGDStepResult:
+    def _ascend(self, d_src, d_dsrc, lr, key):
+        self.adv.after_one_ascent(d_src, lr, key)
+        if self.dadv is not None:
+            self.dadv.after_one_ascent(d_dsrc, lr, key)
+
+    def step(self, x, V, U, ci, target, lr: float, key, adv_index: int = 0, W=None) -> PPGDStepResult:
         """`key` is the step's adversary key: the warmup ascents take
         fold_in(fold_in(key, 0x51C), adv_index) (pd/core/train.py:746-753) and the final
-        ascent fold_in(fold_in(fold_in(key, 0x51C), 0x51D), adv_index) (:1004-1007, 1291)."""
+        ascent fold_in(fold_in(fold_in(key, 0x51C), 0x51D), adv_index) (:1004-1007, 1291).
+        W [d_out, d_in] is the site's target weight, needed with delta sources."""
+        if self.dadv is not None and W is None:
+            raise ValueError("delta sources need the site's target weight W")
         quantize_key = prng.fold_in(key, 0x51C)
         warm_key = prng.fold_in(quantize_key, adv_index)
         final_key = prng.fold_in(prng.fold_in(quantize_key, 0x51D), adv_index)
+        zeros = None
+        if self.dadv is not None:
+            zeros = torch.zeros((ci.shape[0], 1), dtype=ci.dtype, device=ci.device)
         warmup_losses = []
-
-        def scoring(_adv):
-            loss, d_src = self._source_grad(x, V, U, ci, target)
+        n = self.adv.n_warmup
+        for ascent_key in prng.split(warm_key, n) if n else []:
+            loss, _, _, _, d_src, d_dsrc = self._grads(x, V, U, W, ci, target, zeros, final=False)
             warmup_losses.append(loss)
-            return d_src
-
-        self.adv.warmup_ascend(scoring, lr, warm_key)
-        mask = self.adv.mask(ci)
-        out, xV, acts = ops.masked_linear_fwd(x, V, U, mask)
-        loss, g_out = ops.mse(out, target, 1.0, want_grad=True)
-        _, dV, dU, dm = ops.masked_linear_bwd(x, V, U, mask, xV, acts, g_out)
-        d_src, d_ci = source_mask_grad(dm, ci, self.adv.sources, self.adv.rows_per_source, want_dci=True)
-        self.adv.final_ascend(d_src, lr, final_key)
+            self._ascend(d_src, d_dsrc, lr, ascent_key)
+        loss, dV, dU, d_ci, d_src, d_dsrc = self._grads(x, V, U, W, ci, target, zeros, final=True)
+        self._ascend(d_src, d_dsrc, lr, final_key)
         return PPGDStepResult(loss=loss, dV=dV, dU=dU, d_ci=d_ci, warmup_losses=warmup_losses)

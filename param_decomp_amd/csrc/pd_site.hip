@@ -54,6 +54,24 @@ __global__ void k_ml_bwd_elem(T* __restrict__ da, const T* __restrict__ xV, cons
   }
 }
 
+// d_delta[t] = routed ? sum_o g[t,o] * yt[t,o] - sum_c da[t,c] * xV[t,c] : 0, the
+// derivative of (xV*(m - d))@U + d*yt with respect to d_t (da = g @ U^T before the
+// mask scaling). fp32 sums; one wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void k_ml_delta_grad(const T* __restrict__ g, const T* __restrict__ yt,
+                                                       const T* __restrict__ da, const T* __restrict__ xV,
+                                                       const uint8_t* __restrict__ route, int64_t Tn, int64_t D,
+                                                       int64_t C, T* __restrict__ d_delta) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const int lane = threadIdx.x & 63;
+  float part = 0.f;
+  for (int64_t o = lane; o < D; o += 64) part = fmaf(load_f<T>(g, t * D + o), load_f<T>(yt, t * D + o), part);
+  for (int64_t c = lane; c < C; c += 64) part = fmaf(-load_f<T>(da, t * C + c), load_f<T>(xV, t * C + c), part);
+  part = wave_sum(part);
+  if (lane == 0) store_f<T>(d_delta, t, (route ? route[t] != 0 : true) ? part : 0.f);
+}
+
 // g_target[t,:] = g[t,:] * (routed ? d_t : 1)
 template <typename T>
 __global__ void k_ml_target_grad(const T* __restrict__ g, const T* __restrict__ delta,
@@ -128,10 +146,11 @@ size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, 
 int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
-                         void* dmask, void* workspace, size_t workspace_bytes, void* stream) {
+                         void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream) {
   if (T <= 0 || d_in <= 0 || d_out <= 0 || C <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out)
     return fail(PD_EINVAL, "pd_masked_linear_bwd: bad args");
   if ((delta || route) && dx && !W) return fail(PD_EINVAL, "pd_masked_linear_bwd: W required for dx");
+  if (d_delta && !W) return fail(PD_EINVAL, "pd_masked_linear_bwd: W required for d_delta");
   if (!workspace || workspace_bytes < pd_masked_linear_bwd_workspace_size(dtype, T, d_out, C))
     return fail(PD_EWORKSPACE, "pd_masked_linear_bwd: workspace too small");
   hipStream_t s = (hipStream_t)stream;
@@ -143,9 +162,21 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
   // dU = acts^T @ g (unrouted rows of acts are zero)
   if (dU && (rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream)))
     return rc;
-  if (!dV && !dx && !dmask) return PD_OK;
+  if (!dV && !dx && !dmask && !d_delta) return PD_OK;
   // da = g @ U^T
   if ((rc = pd_gemm(dtype, T, C, d_out, g_out, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
+  if (d_delta) {
+    // the target x @ W^T into the target-gradient buffer, which is free until dx
+    if ((rc = pd_gemm(dtype, T, d_out, d_in, x, d_in, 0, W, d_in, 1, gt, d_out, dtype, 1.f, 0.f, stream))) return rc;
+    if (dtype == PD_DTYPE_F32)
+      hipLaunchKernelGGL(k_ml_delta_grad<float>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, (const float*)g_out,
+                         (const float*)gt, (const float*)da, (const float*)xV, route, T, d_out, C, (float*)d_delta);
+    else
+      hipLaunchKernelGGL(k_ml_delta_grad<bf16_t>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, (const bf16_t*)g_out,
+                         (const bf16_t*)gt, (const bf16_t*)da, (const bf16_t*)xV, route, T, d_out, C,
+                         (bf16_t*)d_delta);
+    if ((rc = check_launch("pd_masked_linear_bwd d_delta"))) return rc;
+  }
   if (dtype == PD_DTYPE_F32)
     hipLaunchKernelGGL(k_ml_bwd_elem<float>, dim3(ew_grid(T * C)), dim3(256), 0, s, (float*)da, (const float*)xV,
                        (const float*)mask, (const float*)delta, route, T, C, (float*)dmask);

@@ -80,14 +80,16 @@ class _MaskedLinear(torch.autograd.Function):
             g_out = torch.zeros((T, d_out), dtype=x2.dtype, device=x2.device)
         g = g_out.reshape(T, d_out).contiguous()
         need_x, need_v, need_u, need_m = ctx.needs_input_grad[:4]
+        need_d = ctx.needs_input_grad[5] and W is not None
         dx = torch.empty_like(x2) if need_x else None
+        dd = torch.empty((T,), dtype=x2.dtype, device=x2.device) if need_d else None
         dV = torch.empty((d_in, C), dtype=x2.dtype, device=x2.device)
         dU = torch.empty((C, d_out), dtype=x2.dtype, device=x2.device)
         dm = torch.empty_like(m2) if need_m else None
         ws = L.workspace(L.load().pd_masked_linear_bwd_workspace_size(dt, T, d_out, C), x2.device)
         L.call("pd_masked_linear_bwd", dt, T, d_in, d_out, C, L.ptr(x2), L.ptr(V.contiguous()), L.ptr(U.contiguous()),
                L.ptr(W), L.ptr(m2), L.ptr(d2), L.ptr(r2), L.ptr(xV), L.ptr(acts), L.ptr(g), L.ptr(dx), L.ptr(dV),
-               L.ptr(dU), L.ptr(dm), L.ptr(ws), ws.numel(), L.stream())
+               L.ptr(dU), L.ptr(dm), L.ptr(dd), L.ptr(ws), ws.numel(), L.stream())
         if g_xV is not None:
             # component_activation = x@V is also an output (the CI tap): its cotangent
             # adds x^T g_xV to dV and g_xV V^T to dx.
@@ -99,7 +101,7 @@ class _MaskedLinear(torch.autograd.Function):
                 ops.gemm(gx, V.contiguous(), trans_b=True, out=dx, beta=1.0)
         lead = ctx.lead
         return (None if dx is None else dx.reshape(*lead, d_in), dV if need_v else None, dU if need_u else None,
-                None if dm is None else dm.reshape(*lead, C), None, None, None)
+                None if dm is None else dm.reshape(*lead, C), None, None if dd is None else dd.reshape(lead), None)
 
 
 def site_forward(x: torch.Tensor, weights: SiteWeights, mask: torch.Tensor, delta: torch.Tensor | None,

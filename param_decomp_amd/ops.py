@@ -285,32 +285,36 @@ def faithfulness_bwd(delta, V, U, w_sq_norms, mats_per_site: int, scale: float, 
     return dV, dU
 
 
-def masked_linear_fwd(x, V, U, mask):
-    """`pd_masked_linear_fwd` without delta or route: (out, xV, acts) with acts = xV * mask."""
+def masked_linear_fwd(x, V, U, mask, W=None, delta=None):
+    """`pd_masked_linear_fwd` without route: (out, xV, acts) with acts = xV * (mask - delta)
+    and, with a delta [T], out = acts @ U + delta * (x @ W^T)."""
     T, d_in = x.shape
     C, d_out = U.shape
     out = torch.empty((T, d_out), dtype=x.dtype, device=x.device)
     xV = torch.empty((T, C), dtype=x.dtype, device=x.device)
     acts = torch.empty((T, C), dtype=x.dtype, device=x.device)
-    L.call("pd_masked_linear_fwd", L.dtype_code(x.dtype), T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), None,
-           L.ptr(mask), None, None, L.ptr(out), L.ptr(xV), L.ptr(acts), L.stream())
+    L.call("pd_masked_linear_fwd", L.dtype_code(x.dtype), T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), L.ptr(W),
+           L.ptr(mask), L.ptr(delta), None, L.ptr(out), L.ptr(xV), L.ptr(acts), L.stream())
     return out, xV, acts
 
 
-def masked_linear_bwd(x, V, U, mask, xV, acts, g_out, *, want_dx=False, want_dvu=True, want_dmask=True):
-    """`pd_masked_linear_bwd` without delta or route; each output optional."""
+def masked_linear_bwd(x, V, U, mask, xV, acts, g_out, *, W=None, delta=None, want_dx=False, want_dvu=True,
+                      want_dmask=True, want_ddelta=False):
+    """`pd_masked_linear_bwd` without route; each output optional. Returns
+    (dx, dV, dU, dmask, d_delta); d_delta [T] needs W."""
     T, d_in = x.shape
     C, d_out = U.shape
     dx = torch.empty_like(x) if want_dx else None
     dV = torch.empty_like(V) if want_dvu else None
     dU = torch.empty_like(U) if want_dvu else None
     dm = torch.empty_like(mask) if want_dmask else None
+    dd = torch.empty((T,), dtype=x.dtype, device=x.device) if want_ddelta else None
     dt = L.dtype_code(x.dtype)
     ws = L.workspace(L.load().pd_masked_linear_bwd_workspace_size(dt, T, d_out, C), x.device)
-    L.call("pd_masked_linear_bwd", dt, T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), None, L.ptr(mask), None, None,
-           L.ptr(xV), L.ptr(acts), L.ptr(g_out), L.ptr(dx), L.ptr(dV), L.ptr(dU), L.ptr(dm), L.ptr(ws), ws.numel(),
-           L.stream())
-    return dx, dV, dU, dm
+    L.call("pd_masked_linear_bwd", dt, T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), L.ptr(W), L.ptr(mask),
+           L.ptr(delta), None, L.ptr(xV), L.ptr(acts), L.ptr(g_out), L.ptr(dx), L.ptr(dV), L.ptr(dU), L.ptr(dm),
+           L.ptr(dd), L.ptr(ws), ws.numel(), L.stream())
+    return dx, dV, dU, dm, dd
 
 
 def source_mask_fwd(ci, sources, rows_per_source: int):

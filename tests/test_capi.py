@@ -39,6 +39,28 @@ def test_binding_covers_the_header():
     assert sorted(L.exported_symbols()) == header_symbols()
 
 
+def _header_arities():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"\b(pd_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_binding_arity_matches_the_header():
+    """Every ctypes signature has exactly the header's parameter count: an argument past
+    the declared argtypes would go through ctypes' variadic conversion (a 32-bit int in a
+    64-bit slot), which corrupts pointer arguments such as the stream."""
+    from param_decomp_amd import _lib as L
+
+    ar = _header_arities()
+    bad = {n: (ar.get(n), len(args)) for n, (_, args) in L._SIGNATURES.items() if ar.get(n) != len(args)}
+    assert not bad, bad
+
+
 def test_missing_library_raises(monkeypatch, tmp_path):
     from param_decomp_amd import _lib as L
 

@@ -271,7 +271,7 @@ def test_site_forward_and_backward(device, dtype, with_delta, with_route):
     cv = (lambda a: bf(a, device)) if dtype == torch.bfloat16 else (lambda a: f32(a, device))
     tx, tV, tU, tm = (cv(a).requires_grad_(True) for a in (x, V, U, m))
     tW = cv(W)
-    td = None if d is None else cv(d)
+    td = None if d is None else cv(d).requires_grad_(True)
     tr = None if r is None else torch.tensor(r, device=device)
     res = site_forward(tx, SiteWeights(tW, tV, tU), tm, td, tr)
     xs, Ws, Vs, Us, ms = (np64(t) for t in (tx, tW, tV, tU, tm))
@@ -281,9 +281,13 @@ def test_site_forward_and_backward(device, dtype, with_delta, with_route):
     assert_close(np64(res.output), want, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "site out")
     assert_close(np64(res.component_activation), want_xV, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "xV")
     go = rng.normal(size=want.shape)
-    grads = torch.autograd.grad(res.output, (tx, tV, tU, tm), cv(go))
+    inputs = (tx, tV, tU, tm) + (() if td is None else (td,))
+    grads = torch.autograd.grad(res.output, inputs, cv(go))
     dx, dV, dU, dm = po.site_backward(xs, Ws, Vs, Us, ms, ds, r, np64(cv(go)))
-    for got, w, name in zip(grads, (dx, dV, dU, dm), ("dx", "dV", "dU", "dmask")):
+    wants = (dx, dV, dU, dm)
+    if td is not None:  # the weight-delta cotangent (the delta sources of adversarial masking)
+        wants = wants + (po.site_delta_grad(xs, Ws, Vs, Us, ms, ds, r, np64(cv(go))),)
+    for got, w, name in zip(grads, wants, ("dx", "dV", "dU", "dmask", "d_delta")):
         assert_close(np64(got), w, rtol, 1e-4 if dtype == torch.float32 else 5e-3, name)
 
 

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import pd_oracle as pdo
 from oracle import pgd_oracle as po
 from oracle import threefry
 from param_decomp_amd import _lib as L
@@ -141,51 +142,78 @@ def test_adam_refuses_uint16_storage(device):
         A.PersistentAdversary(s.reshape(1, 8), A.AdamPGDConfig(), 2, 4)
 
 
-def _oracle_step(x, V, U, ci, target, src, rps, n_warmup, lr):
-    """float64 persistent-PGD step with Adam (fp32 storage): warmups then the final."""
-    T = x.shape[0]
+def _oracle_step(x, V, U, ci, target, src, rps, n_warmup, lr, W=None, dsrc=None):
+    """float64 persistent-PGD step with Adam (fp32 storage): warmups then the final. With
+    delta sources (dsrc [n_sources, 1]) the site output is (xV (m - d)) @ U + d (x @ W^T)
+    and the delta leaf ascends beside the components."""
 
-    def recon(s):
+    def recon(s, sd):
         m = po.source_mask(ci, s, rps)
         xV = x @ V
-        out = (xV * m) @ U
+        d = np.zeros(x.shape[0]) if sd is None else np.repeat(sd[:, 0], rps)
+        coef = m - d[:, None]
+        out = (xV * coef) @ U
+        if sd is not None:
+            out = out + d[:, None] * (x @ W.T)
         g_out = 2 * (out - target) / out.size
         da = g_out @ U.T
         dm = da * xV
         d_src, d_ci = po.source_mask_vjp(dm, ci, s, rps)
-        dU = (xV * m).T @ g_out
-        dV = x.T @ (da * m)
-        return float(((out - target) ** 2).mean()), d_src, d_ci, dV, dU
+        d_sd = None
+        if sd is not None:
+            dd = pdo.site_delta_grad(x, W, V, U, m, d, None, g_out)
+            d_sd = dd.reshape(-1, rps).sum(axis=1, keepdims=True)
+        dU = (xV * coef).T @ g_out
+        dV = x.T @ (da * coef)
+        return float(((out - target) ** 2).mean()), d_src, d_ci, dV, dU, d_sd
 
-    m_, v_ = np.zeros_like(src), np.zeros_like(src)
-    s, step = src.copy(), 0.0
+    state = {"s": (src.copy(), np.zeros_like(src), np.zeros_like(src))}
+    if dsrc is not None:
+        state["d"] = (dsrc.copy(), np.zeros_like(dsrc), np.zeros_like(dsrc))
+    step = 0.0
+
+    def ascend(d_src, d_sd):
+        s_, m_, v_ = state["s"]
+        state["s"] = po.adam(s_, d_src, m_, v_, step, lr=lr)
+        if dsrc is not None:
+            s_, m_, v_ = state["d"]
+            state["d"] = po.adam(s_, d_sd, m_, v_, step, lr=lr)
+
+    cur = lambda k: None if k not in state else state[k][0]
     for _ in range(n_warmup):
-        _, d_src, _, _, _ = recon(s)
+        _, d_src, _, _, _, d_sd = recon(cur("s"), cur("d"))
         step += 1
-        s, m_, v_ = po.adam(s, d_src, m_, v_, step, lr=lr)
-    loss, d_src, d_ci, dV, dU = recon(s)
+        ascend(d_src, d_sd)
+    loss, d_src, d_ci, dV, dU, d_sd = recon(cur("s"), cur("d"))
     step += 1
-    s_final, _, _ = po.adam(s, d_src, m_, v_, step, lr=lr)
-    return loss, dV, dU, d_ci, s_final
+    ascend(d_src, d_sd)
+    return loss, dV, dU, d_ci, cur("s"), cur("d")
 
 
-@pytest.mark.parametrize("rps", [256, 32, 1])
-def test_dense_site_ppgd_step_matches_oracle(device, rps):
-    print(f"ppgd step rps={rps}", flush=True)
+@pytest.mark.parametrize("rps,with_delta", [(256, False), (32, False), (1, False), (32, True), (1, True)])
+def test_dense_site_ppgd_step_matches_oracle(device, rps, with_delta):
+    print(f"ppgd step rps={rps} delta={with_delta}", flush=True)
     rng = np.random.default_rng(rps)
     T, d_in, d_out, C = 256, 64, 48, 96
     x = rng.normal(size=(T, d_in)).astype(np.float32)
     V = (rng.normal(size=(d_in, C)) / 8).astype(np.float32)
     U = (rng.normal(size=(C, d_out)) / 10).astype(np.float32)
+    W = (rng.normal(size=(d_out, d_in)) / 8).astype(np.float32)
     ci = rng.uniform(size=(T, C)).astype(np.float32)
     target = (x @ V @ U + rng.normal(size=(T, d_out)) * 0.1).astype(np.float32)
     src = rng.uniform(size=(T // rps, C)).astype(np.float32)
+    dsrc = rng.uniform(size=(T // rps, 1)).astype(np.float32) if with_delta else None
     f = lambda a: torch.tensor(a, device=device)
     adv = A.PersistentAdversary(f(src.copy()), A.AdamPGDConfig(), n_warmup=2, rows_per_source=rps)
-    res = A.DenseSitePPGDStep(adv).step(f(x), f(V), f(U), f(ci), f(target), lr=0.01, key=(0, 1))
+    dadv = None
+    if with_delta:
+        dadv = A.PersistentAdversary(f(dsrc.copy()), A.AdamPGDConfig(), n_warmup=2, rows_per_source=rps, leaf_index=1)
+    res = A.DenseSitePPGDStep(adv, dadv).step(f(x), f(V), f(U), f(ci), f(target), lr=0.01, key=(0, 1),
+                                              W=f(W) if with_delta else None)
     torch.cuda.synchronize()
-    d64 = lambda a: a.astype(np.float64)
-    loss, dV, dU, d_ci, s_final = _oracle_step(d64(x), d64(V), d64(U), d64(ci), d64(target), d64(src), rps, 2, 0.01)
+    d64 = lambda a: None if a is None else a.astype(np.float64)
+    loss, dV, dU, d_ci, s_final, d_final = _oracle_step(d64(x), d64(V), d64(U), d64(ci), d64(target), d64(src), rps,
+                                                        2, 0.01, W=d64(W), dsrc=d64(dsrc))
     assert float(res.loss[0]) == pytest.approx(loss, rel=1e-4)
     assert len(res.warmup_losses) == 2
     assert _rel(_np(res.dV), dV) < 1e-4 and _rel(_np(res.dU), dU) < 1e-4 and _rel(_np(res.d_ci), d_ci) < 1e-4
@@ -194,6 +222,11 @@ def test_dense_site_ppgd_step_matches_oracle(device, rps):
     off = np.abs(_np(adv.sources) - s_final) > 1e-3
     assert off.mean() <= 1e-3
     assert adv.step_count == 3.0
+    if with_delta:
+        # the delta leaf moved, and by the oracle's Adam steps
+        assert np.abs(_np(dadv.sources) - dsrc).max() > 5e-3
+        assert (np.abs(_np(dadv.sources) - d_final) > 1e-3).mean() <= 2e-2
+        assert dadv.step_count == 3.0
 
 
 def test_dense_site_ppgd_step_bf16_runs_at_full_site_shape(device):

@@ -311,6 +311,37 @@ def test_site_backward_finite_difference(with_delta, with_route):
             assert grad[idx] == pytest.approx((f(*a) - f(*b)) / (2 * eps), rel=1e-6, abs=1e-9)
 
 
+@pytest.mark.parametrize("with_route", [False, True])
+def test_site_delta_grad_finite_difference_and_exact_factorization(with_route):
+    """The delta cotangent: central differences of <site_forward, g> in each delta_t;
+    unrouted positions get 0; and with V@U = W^T the blend is delta-independent, so the
+    cotangent vanishes (a dropped target term or a sign flip breaks one of them)."""
+    rng = np.random.default_rng(8)
+    T, din, dout, C = 5, 3, 4, 6
+    x, W = rng.normal(size=(T, din)), rng.normal(size=(dout, din))
+    V, U = rng.normal(size=(din, C)), rng.normal(size=(C, dout))
+    m = rng.uniform(size=(T, C))
+    d = rng.uniform(size=T)
+    r = np.array([True, False, True, True, False]) if with_route else None
+    go = rng.normal(size=(T, dout))
+    dd = po.site_delta_grad(x, W, V, U, m, d, r, go)
+    eps = 1e-6
+    for t in range(T):
+        dp, dm_ = d.copy(), d.copy()
+        dp[t] += eps
+        dm_[t] -= eps
+        fd = (np.sum(po.site_forward(x, W, V, U, m, dp, r)[0] * go)
+              - np.sum(po.site_forward(x, W, V, U, m, dm_, r)[0] * go)) / (2 * eps)
+        assert dd[t] == pytest.approx(fd, rel=1e-6, abs=1e-9)
+    if with_route:
+        assert dd[1] == 0.0 and dd[4] == 0.0
+    # exact factorization: W^T = V @ U (C >= d_in, so V has a right inverse)
+    U2 = np.linalg.lstsq(V, W.T, rcond=None)[0]
+    np.testing.assert_allclose(V @ U2, W.T, atol=1e-10)
+    assert np.abs(po.site_delta_grad(x, W, V, U2, m, d, r, go)).max() < 1e-9
+    assert np.abs(dd).max() > 1e-3
+
+
 def test_dense_step_gradients_finite_difference():
     """The whole single-site step: loss(V, U, gate) with the mask uniforms fixed by the
     key — central differences on V, U and every gate parameter family. The lower
