@@ -666,7 +666,16 @@ __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, cons
   __shared__ double sr[16], si[16];
   double r = 0.0, m = 0.0;
   for (int i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
-  for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  // four independent chains keep four loads in flight per lane; combined in a fixed order
+  double m4[4] = {0.0, 0.0, 0.0, 0.0};
+  const int64_t step = blockDim.x;
+  int64_t i = threadIdx.x;
+  for (; i + 3 * step < n_imp; i += 4 * step) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m4[q] += imp_part[i + q * step];
+  }
+  for (; i < n_imp; i += step) m4[0] += imp_part[i];
+  m = (m4[0] + m4[1]) + (m4[2] + m4[3]);
   r = wave_sum_d(r);
   m = wave_sum_d(m);
   if (threadIdx.x % 64 == 0) {
@@ -941,28 +950,35 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     for (int si = 0; si < 3; ++si) dlt[si] = use_delta ? P.delta + ((size_t)l * 3 + si) * T : nullptr;
   };
 
-  // ================= clean forward (frozen weights): pins the expert indices. Layer 0's
-  // gate and up products are kept: the masked pass's layer-0 frozen channel reads the
-  // same inputs under the same routing.
+  // ================= clean forward (frozen weights): pins the expert indices. Layer 0 sees
+  // the masked pass's own input under the same routing, so its norm (h2, rinv), routing
+  // weights, gathered x_jobs (and copy) and the gate/up products of the frozen channel
+  // are written straight into the masked pass's buffers; later clean layers gather into
+  // a buffer the masked pass only uses afterwards.
   hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
   bf16_t* rcur = P.rc_a;
   bf16_t* rnext = P.rc_b;
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
+    bf16_t* h2l = l == 0 ? S.h2 : P.h2c;
     hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
-                       P.h2c, (float*)nullptr);
-    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, P.h2c, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
+                       h2l, l == 0 ? S.rinv : (float*)nullptr);
+    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, h2l, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
                       PD_DTYPE_F32, 1.f, 0.f, stream)))
       return rc;
     if ((rc = pd_router_topk(P.logits, T, E, k, P.probsc, S.idx, P.wc, stream))) return rc;
+    if (l == 0)
+      hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
+                         S.probs, S.w);
     if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
                              pd_routed_jobs_workspace_size(J, E), stream)))
       return rc;
-    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, P.h2c, S.sort_idx, k, J, d, P.xj,
-                       (bf16_t*)nullptr);
+    bf16_t* xjl = l == 0 ? P.xj : P.down;
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, h2l, S.sort_idx, k, J, d, xjl,
+                       l == 0 ? S.xjT : (bf16_t*)nullptr);
     bf16_t* gcl = l == 0 ? P.fg0 : P.gc;
     bf16_t* ucl = l == 0 ? P.fu0 : P.uc;
-    if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, gcl, P.xj, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
+    if ((rc = grouped_gemm_pair(xjl, P.WgT + l * szW, gcl, xjl, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
                                 PD_DTYPE_BF16, stream)))
       return rc;
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, gcl, ucl, (const float*)nullptr,
@@ -985,14 +1001,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     LayerSave& S = P.layers[l];
     rec.mark(MOE_CAT_NORM_ROUTE);
     if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
-    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f, S.h2,
-                       S.rinv);
-    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
-                      PD_DTYPE_F32, 1.f, 0.f, stream)))
-      return rc;
-    hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
-                       S.probs, S.w);
-    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
+    if (l > 0) {  // layer 0's were formed by the clean pass
+      hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, T, d, ln + (size_t)l * d, 1e-6f,
+                         S.h2, S.rinv);
+      if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
+                        PD_DTYPE_F32, 1.f, 0.f, stream)))
+        return rc;
+      hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
+                         S.probs, S.w);
+      hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
+    }
     set_delta(l);
     auto mask_fwd = [&](int si, bf16_t* acts_out) {
       SiteMaskArgs ma;
