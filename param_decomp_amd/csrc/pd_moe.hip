@@ -253,8 +253,21 @@ struct SiteMaskArgs {
 
 __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
 
-__device__ inline float powp(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
-__device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f)); }
+// b^p and d(b^p)/db with the exponent's common cases fixed at compile time (PM = 2: p = 2,
+// PM = 1: p = 1, PM = 0: any p), so no pow code sits beside the fast paths.
+template <int PM>
+__device__ inline float powp(float b, float p) {
+  if constexpr (PM == 2) return b * b;
+  else if constexpr (PM == 1) return b;
+  else return powf(b, p);
+}
+template <int PM>
+__device__ inline float dpowp(float b, float p) {
+  if constexpr (PM == 2) return 2.f * b;
+  else if constexpr (PM == 1) return 1.f;
+  else return p * powf(b, p - 1.f);
+}
+static int pow_mode(float p) { return p == 2.f ? 2 : (p == 1.f ? 1 : 0); }
 
 // Thread -> (row (tid >> 4) + 16 * pass, columns q4 .. q4 + 3) of a 64x64 job-space tile.
 #define PD_TILE4_ROW(pass) ((threadIdx.x >> 4) + 16 * (pass))
@@ -265,7 +278,7 @@ __device__ inline float dpowp(float b, float p) { return p == 2.f ? 2.f * b : (p
 // bf16(h * (m - delta)) (the component coefficients m - d, pd/core/decomposed_linear.py:65-69;
 // d = 0 without the frozen channel) written as acts [J,c] and acts^T [c,J]; u stored as
 // its 7-bit integer; per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
-template <int LAYOUT>
+template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
                                                        uint8_t* __restrict__ ubits, float* __restrict__ imp_partial) {
@@ -295,7 +308,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
-        imp += powp(upper_fwd(pre[e]), a.p);
+        imp += powp<PM>(upper_fwd(pre[e]), a.p);
         const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
         ub |= kb << (8 * e);
         o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * ((float)kb * (1.f / 128.f)) - dt));
@@ -316,6 +329,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 // Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts, plus d_h^T [c,J]) and the
 // CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
 // upper_vjp(pre, imp_scale * d upper^p), written token-major.
+template <int PM>
 __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
                                                        bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_hT,
@@ -349,7 +363,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
         const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
         const float m = lo + (1.f - lo) * u - dt;
         dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
-                            upper_vjp(pre[e], imp_scale * dpowp(up, a.p)));
+                            upper_vjp(pre[e], imp_scale * dpowp<PM>(up, a.p)));
         o[e] = f32_to_bf16(da[e] * m);
       }
       *(uint2*)(d_pre + src) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
@@ -713,6 +727,32 @@ __global__ __launch_bounds__(256) void k_delta_sites(uint32_t b0, uint32_t b1, i
   delta[(int64_t)site * T + t] = draw_uniform(k0, k1, t, T, PD_DTYPE_BF16, layout);
 }
 
+static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h, bf16_t* acts,
+                            bf16_t* actsT, uint8_t* ub, float* part) {
+#define PD_MF(LY, PMV) \
+  hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, actsT, ub, part)
+  if (ma.layout == PD_LAYOUT_PARTITIONABLE) {
+    if (pm == 2) PD_MF(PD_LAYOUT_PARTITIONABLE, 2);
+    else if (pm == 1) PD_MF(PD_LAYOUT_PARTITIONABLE, 1);
+    else PD_MF(PD_LAYOUT_PARTITIONABLE, 0);
+  } else {
+    if (pm == 2) PD_MF(PD_LAYOUT_ORIGINAL, 2);
+    else if (pm == 1) PD_MF(PD_LAYOUT_ORIGINAL, 1);
+    else PD_MF(PD_LAYOUT_ORIGINAL, 0);
+  }
+#undef PD_MF
+}
+
+static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h,
+                            const uint8_t* ub, float imp_scale, bf16_t* d_acts, bf16_t* d_hT, bf16_t* d_pre) {
+#define PD_MB(PMV) \
+  hipLaunchKernelGGL((k_mask_bwd_tile<PMV>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_hT, d_pre)
+  if (pm == 2) PD_MB(2);
+  else if (pm == 1) PD_MB(1);
+  else PD_MB(0);
+#undef PD_MB
+}
+
 // ---------------------------------------------------------------- workspace plan
 static constexpr int REC_BLOCKS = 1024;
 
@@ -925,6 +965,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     o1 = y1;
   };
   const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
+  const int pm = pow_mode(p);
 
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
@@ -1024,12 +1065,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.delta = dlt[si];
       ma.k = k;
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
-      if (layout == PD_LAYOUT_PARTITIONABLE)
-        hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_PARTITIONABLE>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
-                           acts_out, S.actsT[si], S.ub[si], part);
-      else
-        hipLaunchKernelGGL(k_mask_fwd_tile<PD_LAYOUT_ORIGINAL>, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si],
-                           acts_out, S.actsT[si], S.ub[si], part);
+      launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], acts_out, S.actsT[si], S.ub[si], part);
     };
     // ---- gate and up sites: both products of each stage in one paired launch
     rec.mark(MOE_CAT_GEMM_FWD);
@@ -1117,8 +1153,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
     ma.delta = dlt[2];
-    hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[2], S.ub[2], imp_scale,
-                       P.d_acts[0], P.d_hT[0], (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0], P.d_hT[0],
+                    (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     rec.mark(MOE_CAT_GEMM_DW);
     if ((rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT[0], S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32,
                                         stream)))
@@ -1149,8 +1185,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.delta = dlt[si];
-      hipLaunchKernelGGL(k_mask_bwd_tile, tile_grid(J, c), dim3(256), 0, s, ma, S.h[si], S.ub[si], imp_scale,
-                         P.d_acts[si], P.d_hT[si], (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
+      launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], P.d_hT[si],
+                      (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
     }
     rec.mark(MOE_CAT_GEMM_DW);
     if ((rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
