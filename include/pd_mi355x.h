@@ -173,7 +173,9 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
  *        (block outputs concatenated); PD_BLOCK_FUSED_INPUT (down): x [T,E*d_in],
  *        W [d_out,E*d_in], out [T,d_out] (block outputs summed).
  *      Outputs xV [T,E*c] (the flat component activation) and acts [T,E*c] for the bwd.
- *      bwd: dx (nullable, x's shape), dV, dU, dmask (nullable). bf16: d_in, d_out, c % 8. */
+ *      bwd: dx (nullable, x's shape), dV, dU, dmask (nullable), d_delta [T] (nullable; needs
+ *      W): the delta cotangent over the whole site output, as pd_masked_linear_bwd forms it.
+ *      bf16: d_in, d_out, c % 8. */
 int pd_blocked_site_fwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
                         const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
                         const uint8_t* route, void* out, void* xV, void* acts, void* stream);
@@ -182,7 +184,7 @@ size_t pd_blocked_site_bwd_workspace_size(int dtype, int contraction, int64_t T,
 int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
                         const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
                         const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx, void* dV,
-                        void* dU, void* dmask, void* workspace, size_t workspace_bytes, void* stream);
+                        void* dU, void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- fused single-site stochastic-recon step (the dense hot path) ----
  * One fwd+bwd of: clean target y_t = x@W^T (detached, pd/core/train.py:578-606);

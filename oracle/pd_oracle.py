@@ -250,6 +250,15 @@ def blocked_site_backward(x, W, V, U, mask, delta, route, contraction, dout):
 
 
 # ---------------------------------------------------------------- losses
+def blocked_site_delta_grad(x, W, V, U, mask, delta, route, contraction, dout):
+    """VJP of `blocked_site_forward` w.r.t. the per-position delta: for a routed position
+    `sum_o dout*(x@W.T) - sum_c dmask_c` (the mask cotangent `dacts*xV` of
+    `blocked_site_backward`, since the coefficients are `m - d`); 0 where unrouted."""
+    _, _, _, dmask = blocked_site_backward(x, W, V, U, mask, delta, route, contraction, dout)
+    g = np.sum(dout * (x @ W.T), axis=-1) - np.sum(dmask, axis=-1)
+    return g if route is None else np.where(route, g, 0.0)
+
+
 def impmin_pnorm(ci_upper, p: float, eps: float = 0.0, beta: float = 0.0, world_size: int = 1):
     """L_p importance minimality. Paper algorithm step 4
     (`spd_paper.md`, "Algorithm"): `(1/B) sum_b sum_c |upper|^p`; with the `eps`/`beta`

@@ -52,7 +52,7 @@ _SIGNATURES = {
                                          _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_f32, _c_f32, _c_p]),
     "pd_blocked_site_fwd": (_c_i32, [_c_i32, _c_i32] + [_c_i64] * 5 + [_c_p] * 11),
     "pd_blocked_site_bwd_workspace_size": (_c_sz, [_c_i32, _c_i32] + [_c_i64] * 5),
-    "pd_blocked_site_bwd": (_c_i32, [_c_i32, _c_i32] + [_c_i64] * 5 + [_c_p] * 15 + [_c_sz, _c_p]),
+    "pd_blocked_site_bwd": (_c_i32, [_c_i32, _c_i32] + [_c_i64] * 5 + [_c_p] * 16 + [_c_sz, _c_p]),
     "pd_masked_linear_fwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 11),
     "pd_masked_linear_bwd_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
     "pd_masked_linear_bwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 16 + [_c_sz, _c_p]),

@@ -274,10 +274,11 @@ size_t pd_blocked_site_bwd_workspace_size(int dtype, int contraction, int64_t T,
 int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_t d_in, int64_t d_out, int64_t c,
                         const void* x, const void* V, const void* U, const void* W, const void* mask, const void* delta,
                         const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx, void* dV,
-                        void* dU, void* dmask, void* workspace, size_t workspace_bytes, void* stream) {
+                        void* dU, void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream) {
   if (T <= 0 || E <= 0 || d_in <= 0 || d_out <= 0 || c <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out ||
       !dV || !dU)
     return fail(PD_EINVAL, "pd_blocked_site_bwd: bad args");
+  if (d_delta && !W) return fail(PD_EINVAL, "pd_blocked_site_bwd: W required for d_delta");
   if (contraction != PD_BLOCK_FUSED_OUTPUT && contraction != PD_BLOCK_FUSED_INPUT)
     return fail(PD_EINVAL, "pd_blocked_site_bwd: contraction");
   if ((delta || route) && dx && !W) return fail(PD_EINVAL, "pd_blocked_site_bwd: W required for dx");
@@ -307,6 +308,18 @@ int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_
   } else {
     if ((rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream))) return rc;
     if ((rc = pd_gemm(dtype, T, C, d_out, g_out, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
+  }
+  if (d_delta) {
+    // the delta cotangent over the whole site output: the target x @ W^T into the
+    // target-gradient buffer (free until dx), then the row sums of g*target - da*xV
+    if ((rc = pd_gemm(dtype, T, DO, DI, x, DI, 0, W, DI, 1, gt, DO, dtype, 1.f, 0.f, stream))) return rc;
+    if (dtype == PD_DTYPE_F32)
+      hipLaunchKernelGGL(k_ml_delta_grad<float>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, (const float*)g_out,
+                         (const float*)gt, (const float*)da, (const float*)xV, route, T, DO, C, (float*)d_delta);
+    else
+      hipLaunchKernelGGL(k_ml_delta_grad<bf16_t>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, (const bf16_t*)g_out,
+                         (const bf16_t*)gt, (const bf16_t*)da, (const bf16_t*)xV, route, T, DO, C, (bf16_t*)d_delta);
+    if ((rc = check_launch("pd_blocked_site_bwd d_delta"))) return rc;
   }
   if (dtype == PD_DTYPE_F32)
     hipLaunchKernelGGL(k_ml_bwd_elem<float>, dim3(ew_grid(T * C)), dim3(256), 0, s, (float*)da, (const float*)xV,

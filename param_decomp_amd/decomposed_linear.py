@@ -170,14 +170,16 @@ class _BlockedMaskedLinear(torch.autograd.Function):
             g_out = torch.zeros((T, DO), dtype=x2.dtype, device=x2.device)
         g = g_out.reshape(T, DO).contiguous()
         need_x, need_v, need_u, need_m = ctx.needs_input_grad[:4]
+        need_d = ctx.needs_input_grad[5] and W is not None
         dx = torch.empty_like(x2) if need_x else None
         dV = torch.empty_like(V)
         dU = torch.empty_like(U)
         dm = torch.empty_like(m2) if need_m else None
+        dd = torch.empty((T,), dtype=x2.dtype, device=x2.device) if need_d else None
         ws = L.workspace(L.load().pd_blocked_site_bwd_workspace_size(dt, code, T, E, d_in, d_out, c), x2.device)
         L.call("pd_blocked_site_bwd", dt, code, T, E, d_in, d_out, c, L.ptr(x2), L.ptr(V.contiguous()),
                L.ptr(U.contiguous()), L.ptr(W), L.ptr(m2), L.ptr(d2), L.ptr(r2), L.ptr(xV), L.ptr(acts), L.ptr(g),
-               L.ptr(dx), L.ptr(dV), L.ptr(dU), L.ptr(dm), L.ptr(ws), ws.numel(), L.stream())
+               L.ptr(dx), L.ptr(dV), L.ptr(dU), L.ptr(dm), L.ptr(dd), L.ptr(ws), ws.numel(), L.stream())
         if g_xV is not None:
             # the flat component activation is also an output (the CI tap)
             from param_decomp_amd import ops
@@ -196,7 +198,8 @@ class _BlockedMaskedLinear(torch.autograd.Function):
                     L.call("pd_gemm_strided_batched", dt, E, T, d_in, c, L.ptr(gx), E * c, c, 0,
                            L.ptr(V.contiguous()), c, d_in * c, 1, L.ptr(dx), DI, d_in, dt, 1.0, 1.0, L.stream())
         return (None if dx is None else dx.reshape(*lead, x2.shape[1]), dV if need_v else None,
-                dU if need_u else None, None if dm is None else dm.reshape(*lead, E * c), None, None, None, None)
+                dU if need_u else None, None if dm is None else dm.reshape(*lead, E * c), None,
+                None if dd is None else dd.reshape(lead), None, None)
 
 
 def blocked_site_forward(x: torch.Tensor, weights: BlockedSiteWeights, mask: torch.Tensor,

@@ -606,7 +606,7 @@ def test_blocked_site_forward_backward(device, dtype, contraction, with_delta_an
     U = cast(rng.normal(size=(E, c, d_out)) / np.sqrt(E * c)).requires_grad_(True)
     W = cast(rng.normal(size=(site_out, site_in)) / np.sqrt(site_in))
     mask = cast(rng.uniform(size=(T, E * c))).requires_grad_(True)
-    delta = cast(rng.uniform(size=T)) if with_delta_and_route else None
+    delta = cast(rng.uniform(size=T)).requires_grad_(True) if with_delta_and_route else None
     route = torch.tensor(rng.uniform(size=T) < 0.6, device=device) if with_delta_and_route else None
     sf = blocked_site_forward(x, BlockedSiteWeights(W, V, U), mask, delta, route, contraction)
     want_out, want_xv = po.blocked_site_forward(np64(x), np64(W), np64(V), np64(U), np64(mask),
@@ -635,3 +635,10 @@ def test_blocked_site_forward_backward(device, dtype, contraction, with_delta_an
     rt, fl = (1e-4, 1e-5) if dtype == torch.float32 else (BF16_RTOL, 1e-2)
     for got, want, name in ((dx, wdx, "dx"), (dV, wdV, "dV"), (dU, wdU, "dU"), (dm, wdm, "dmask")):
         assert_close(np64(got), want, rt, fl, f"blocked {name}")
+    if delta is not None:  # the weight-delta cotangent (delta sources of adversarial masking)
+        (dd,) = torch.autograd.grad(
+            blocked_site_forward(x, BlockedSiteWeights(W, V, U), mask, delta, route, contraction).output, (delta,),
+            cast(G))
+        want_dd = po.blocked_site_delta_grad(np64(x), np64(W), np64(V), np64(U), np64(mask), np64(delta),
+                                             route.cpu().numpy(), contraction, np64(cast(G)))
+        assert_close(np64(dd), want_dd, rt, fl, "blocked d_delta")

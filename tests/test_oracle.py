@@ -342,6 +342,29 @@ def test_site_delta_grad_finite_difference_and_exact_factorization(with_route):
     assert np.abs(dd).max() > 1e-3
 
 
+@pytest.mark.parametrize("contraction", ["fused_output", "fused_input"])
+def test_blocked_site_delta_grad_finite_difference(contraction):
+    rng = np.random.default_rng(9)
+    T, E, d_in, d_out, c = 4, 3, 2, 3, 2
+    site_in = d_in * (E if contraction == "fused_input" else 1)
+    site_out = d_out * (E if contraction == "fused_output" else 1)
+    x, W = rng.normal(size=(T, site_in)), rng.normal(size=(site_out, site_in))
+    V, U = rng.normal(size=(E, d_in, c)), rng.normal(size=(E, c, d_out))
+    m, d = rng.uniform(size=(T, E * c)), rng.uniform(size=T)
+    r = np.array([True, True, False, True])
+    go = rng.normal(size=(T, site_out))
+    dd = po.blocked_site_delta_grad(x, W, V, U, m, d, r, contraction, go)
+    eps = 1e-6
+    for t in range(T):
+        dp, dm_ = d.copy(), d.copy()
+        dp[t] += eps
+        dm_[t] -= eps
+        fd = (np.sum(po.blocked_site_forward(x, W, V, U, m, dp, r, contraction)[0] * go)
+              - np.sum(po.blocked_site_forward(x, W, V, U, m, dm_, r, contraction)[0] * go)) / (2 * eps)
+        assert dd[t] == pytest.approx(fd, rel=1e-6, abs=1e-9)
+    assert dd[2] == 0.0 and np.abs(dd).max() > 1e-3
+
+
 def test_dense_step_gradients_finite_difference():
     """The whole single-site step: loss(V, U, gate) with the mask uniforms fixed by the
     key — central differences on V, U and every gate parameter family. The lower
