@@ -291,7 +291,10 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
  * stochastic masking always draws (pd/targets/qwen36_moe.py:2151-2160, 2805-2815): a
  * per-token delta d = uniform_bf16(fold_in(fold_in(split(draw_key)[1], kind), layer), [T])
  * per site, component coefficients m - d and site output gmm(acts, U) + d * gmm(x_jobs,
- * W[e]) (pd/core/decomposed_linear.py:65-85); use_delta = 0 is d = 0. Loss = recon_coeff * mean((r_L - rc_L)^2) + imp_coeff *
+ * W[e]) (pd/core/decomposed_linear.py:65-85); use_delta = 0 is d = 0. source_value < 0
+ * draws as above (StochasticSources); source_value in [0, 1] is the reference's
+ * ConstantSources(v) (pd/core/objective.py:435-449): u = v everywhere and, with
+ * use_delta, d = v; 0 is the CI-masked reconstruction (m = lower(ci), d = 0). Loss = recon_coeff * mean((r_L - rc_L)^2) + imp_coeff *
  * sum over sites/layers of sum(upper(ci)^p)/T (the selected arm of
  * pd/core/losses.py:357-372).
  * Layouts (all bf16 unless noted): x0 [T,d]; ln fp32 [L,d]; router [L,E,d];
@@ -306,8 +309,8 @@ size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c,
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                      const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout, float p,
-                      float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
+                      const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
+                      int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
                       float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
                       void* stream);
 /* pd_moe_stack_step recording a hipEvent_t before each launch group and one at the
@@ -318,8 +321,8 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
-                            float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
+                            float source_value, int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
                             float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                             void* workspace, size_t workspace_bytes, void* stream, void** events,
                             int32_t* categories, int capacity, int* n_recorded);

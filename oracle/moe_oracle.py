@@ -19,7 +19,10 @@ per-token `d = uniform(fold_in(fold_in(split(draw_key)[1], kind_index), layer), 
 in the CI dtype (`sample_delta_mask`, `pd/core/masking.py:139-140`), component
 coefficients `m - d` and site output `gmm(acts, U) + d * gmm(x_jobs, W[e])`
 (`pd/targets/qwen36_moe.py:2805-2815`, `pd/core/decomposed_linear.py:65-85`);
-`use_delta=False` is `d = 0`. Loss: MSE between the masked and clean final residual
+`use_delta=False` is `d = 0`. `source_value=v` replaces the draws by the reference's
+`ConstantSources(v)` (`pd/core/objective.py:435-449`): `u = v` everywhere and `d = v`
+(`_constant_delta_mask`, `pd/core/masking.py:143-145`); `v = 0` is the CI-masked
+reconstruction. Loss: MSE between the masked and clean final residual
 streams plus the L_p imp-min over the selected upper CI values
 (`pd/core/losses.py:357-372` selected arm).
 
@@ -92,7 +95,7 @@ def grouped_T(lhs, rhs, sizes):
 
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                   bf16_storage=False, partitionable=True, use_delta=True, deltas=None):
+                   bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
     given. Returns dict(loss, recon, imp, grads, d_ci_pre, top_idx, r_final, rc_final,
@@ -140,10 +143,15 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             lo = po.lower_leaky(pre)
             up = po.upper_leaky(pre)
             imp += float(np.sum(up**p)) / T
-            ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
+            if source_value is None:
+                ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
+            else:
+                ut = np.full((T, k, c), float(source_value))
             m_tok = lo + (1.0 - lo) * ut
             if deltas is not None:
                 dt = np.asarray(deltas[l][s], np.float64)
+            elif use_delta and source_value is not None:
+                dt = np.full(T, float(source_value))
             elif use_delta:
                 dt = tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)
             else:

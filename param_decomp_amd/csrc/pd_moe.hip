@@ -249,7 +249,13 @@ struct SiteMaskArgs {
   float p;
   const float* delta;  // [T] the site's per-token delta draw, or NULL (d = 0)
   int k;               // experts per token: job j belongs to token sort_idx[j] / k
+  float uconst;        // MASK_CONST: the constant source value standing in for u
 };
+
+// Mask-source variant of the mask kernels beside the two Threefry layouts: every source
+// value is the constant SiteMaskArgs::uconst (the reference's ConstantSources; 0 is the
+// CI-masked reconstruction), nothing is drawn and no u bytes are kept.
+static constexpr int MASK_CONST = 2;
 
 __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
 
@@ -309,11 +315,17 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
         imp += powp<PM>(upper_fwd(pre[e]), a.p);
-        const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
-        ub |= kb << (8 * e);
-        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * ((float)kb * (1.f / 128.f)) - dt));
+        float u;
+        if constexpr (LAYOUT == MASK_CONST) {
+          u = a.uconst;
+        } else {
+          const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
+          ub |= kb << (8 * e);
+          u = (float)kb * (1.f / 128.f);
+        }
+        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt));
       }
-      *(uint32_t*)(ubits + idx) = ub;
+      if constexpr (LAYOUT != MASK_CONST) *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     }
 #pragma unroll
@@ -352,7 +364,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const uint2 dw = *(const uint2*)(d_acts + idx);
-      const uint32_t ub = *(const uint32_t*)(ubits + idx);
+      const uint32_t ub = a.uconst < 0.f ? *(const uint32_t*)(ubits + idx) : 0u;
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
@@ -360,7 +372,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-        const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
+        const float u = a.uconst < 0.f ? (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f) : a.uconst;
         const float m = lo + (1.f - lo) * u - dt;
         dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
                             upper_vjp(pre[e], imp_scale * dpowp<PM>(up, a.p)));
@@ -731,7 +743,11 @@ static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
                             bf16_t* actsT, uint8_t* ub, float* part) {
 #define PD_MF(LY, PMV) \
   hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, actsT, ub, part)
-  if (ma.layout == PD_LAYOUT_PARTITIONABLE) {
+  if (ma.uconst >= 0.f) {
+    if (pm == 2) PD_MF(MASK_CONST, 2);
+    else if (pm == 1) PD_MF(MASK_CONST, 1);
+    else PD_MF(MASK_CONST, 0);
+  } else if (ma.layout == PD_LAYOUT_PARTITIONABLE) {
     if (pm == 2) PD_MF(PD_LAYOUT_PARTITIONABLE, 2);
     else if (pm == 1) PD_MF(PD_LAYOUT_PARTITIONABLE, 1);
     else PD_MF(PD_LAYOUT_PARTITIONABLE, 0);
@@ -751,6 +767,11 @@ static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
   else if (pm == 1) PD_MB(1);
   else PD_MB(0);
 #undef PD_MB
+}
+
+// delta[0, n) = v (the constant sources' delta mask).
+__global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ out, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = v;
 }
 
 // ---------------------------------------------------------------- workspace plan
@@ -923,7 +944,8 @@ enum {
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout, float p,
+                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
+                         int layout, float p,
                          float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
                          float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
                          void* stream, Recorder& rec) {
@@ -938,6 +960,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     return fail(PD_EINVAL, "pd_moe_stack_step: null pointer");
   if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
     return fail(PD_EINVAL, "pd_moe_stack_step: unknown counter layout");
+  if (!(source_value <= 1.f)) return fail(PD_EINVAL, "pd_moe_stack_step: source_value must be < 0 (drawn) or in [0, 1]");
+  const float uconst = source_value >= 0.f ? source_value : -1.f;
   const MoEDims D{T, T * k, d, f, E, k, c, L};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
     return fail(PD_EWORKSPACE, "pd_moe_stack_step: workspace too small");
@@ -984,7 +1008,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const size_t szV[3] = {szVg, szVg, szVd};
   const size_t szU[3] = {szUg, szUg, szUd};
 
-  if (use_delta)
+  if (use_delta && uconst >= 0.f)  // constant sources: the delta mask is the constant too
+    hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)std::min<int64_t>(cdiv(3 * L * T, 256), 4096)), dim3(256), 0, s,
+                       P.delta, (int64_t)3 * L * T, uconst);
+  else if (use_delta)
     hipLaunchKernelGGL(k_delta_sites, dim3((unsigned)cdiv(T, 256), (unsigned)(3 * L)), dim3(256), 0, s, halves[2],
                        halves[3], T, layout, P.delta);
   auto set_delta = [&](int l) {
@@ -1064,6 +1091,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.p = p;
       ma.delta = dlt[si];
       ma.k = k;
+      ma.uconst = uconst;
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
       launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], acts_out, S.actsT[si], S.ub[si], part);
     };
@@ -1139,6 +1167,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.layout = layout;
     ma.p = p;
     ma.k = k;
+    ma.uconst = uconst;
     set_delta(l);
     // ---- down site
     rec.mark(MOE_CAT_GEMM_DX);
@@ -1219,19 +1248,22 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
-                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff,
+                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value, int layout, float p,
+                      float imp_coeff,
                       float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd,
                       void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                       draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                       draw_k1, use_delta, source_value, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
+                       dUd, d_ci_pre,
                        top_idx_out, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
+                            int layout,
                             float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
                             float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
                             size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
@@ -1240,7 +1272,8 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
     return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
   Recorder rec{events, categories, capacity, 0, nullptr};
   int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                         draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd, d_ci_pre,
+                         draw_k1, use_delta, source_value, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
+                         dUd, d_ci_pre,
                          top_idx_out, workspace, workspace_bytes, stream, rec);
   *n_recorded = rec.n;
   if (rc == PD_OK && rec.n >= capacity) return fail(PD_EINVAL, "pd_moe_stack_step_timed: event capacity too small");

@@ -46,10 +46,13 @@ class MoEWeights:
 class MoEStackStep:
     def __init__(self, T: int, d: int, f: int, E: int, k: int, c: int, n_layers: int, *, device="cuda",
                  p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
-                 layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True):
+                 layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, source_value: float = -1.0):
         self.dims = (T, d, f, E, k, c, n_layers)
         self.p, self.imp_coeff, self.recon_coeff, self.layout = p, imp_coeff, recon_coeff, layout
         self.use_delta = bool(use_delta)
+        # < 0: Threefry mask and delta draws (stochastic recon); v in [0, 1]: constant
+        # sources u = d = v (0: the CI-masked recon)
+        self.source_value = float(source_value)
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
         Ln = n_layers
@@ -66,7 +69,7 @@ class MoEStackStep:
         T, d, f, E, k, c, Ln = self.dims
         return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
                 L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
-                draw_key[0], draw_key[1], int(self.use_delta), self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
+                draw_key[0], draw_key[1], int(self.use_delta), self.source_value, self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]

@@ -41,13 +41,15 @@ def _make(cfg, seed, device):
     return params, x0, ci, w, ci_t, x0_t
 
 
-@pytest.mark.parametrize("cfg,partitionable,use_delta", [
-    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True),
-    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True),
-    (mo.MoEConfig(T=120, d=32, f=24, E=6, k=3, c=40, L=2), False, True),
-    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, False),
-    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), False, False)])
-def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta):
+@pytest.mark.parametrize("cfg,partitionable,use_delta,source_value", [
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None),
+    (mo.MoEConfig(T=120, d=32, f=24, E=6, k=3, c=40, L=2), False, True, None),
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, False, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), False, False, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, 0.0),
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, 0.375)])
+def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, source_value):
     from param_decomp_amd import _lib as L
     from param_decomp_amd.moe_step import MoEStackStep
 
@@ -55,11 +57,11 @@ def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta):
     key = (0, 17)
     step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, p=2.0, imp_coeff=0.5,
                         recon_coeff=1.5, layout=L.LAYOUT_PARTITIONABLE if partitionable else L.LAYOUT_ORIGINAL,
-                        use_delta=use_delta)
+                        use_delta=use_delta, source_value=-1.0 if source_value is None else source_value)
     step.step(x0_t, w, ci_t, key)
     torch.cuda.synchronize()
     ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True,
-                            partitionable=partitionable, use_delta=use_delta)
+                            partitionable=partitionable, use_delta=use_delta, source_value=source_value)
     for l in range(cfg.L):
         np.testing.assert_array_equal(step.top_idx[l].cpu().numpy(), ref["top_idx"][l])
     losses = step.losses.cpu().numpy()

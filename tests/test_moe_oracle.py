@@ -115,6 +115,44 @@ def test_moe_layer_routed_equals_dense_spelling():
     np.testing.assert_allclose(res["r_final"], out, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("v", [0.0, 0.375])
+def test_moe_constant_sources_gradients_and_ci_masked_form(v):
+    """Constant sources u = d = v: central differences of the loss in V, U and the CI,
+    and at v = 0 (the CI-masked recon) the masked layer is the per-token spelling with
+    m = lower(ci) and no frozen share."""
+    cfg, params, x0, ci = _setup(seed=4, L=1)
+    kw = dict(p=2.0, imp_coeff=0.3, recon_coeff=1.7, source_value=v)
+    res = mo.moe_stack_step(cfg, params, x0, ci, (0, 3), **kw)
+    eps = 1e-6
+    rng = np.random.default_rng(7)
+    for arr, grad in ((params[0]["Vg"], res["grads"][0]["Vg"]), (params[0]["Ud"], res["grads"][0]["Ud"]),
+                      (ci[0]["up"], res["d_ci_pre"][0]["up"])):
+        for _ in range(3):
+            idx = tuple(int(rng.integers(0, n)) for n in arr.shape)
+            old = arr[idx]
+            arr[idx] = old + eps
+            lp = mo.moe_stack_step(cfg, params, x0, ci, (0, 3), **kw)["loss"]
+            arr[idx] = old - eps
+            lm = mo.moe_stack_step(cfg, params, x0, ci, (0, 3), **kw)["loss"]
+            arr[idx] = old
+            assert grad[idx] == pytest.approx((lp - lm) / (2 * eps), rel=1e-5, abs=1e-9)
+    if v == 0.0:
+        P = params[0]
+        idx = res["top_idx"][0]
+        h2, _ = mo.rms_norm_zero_centered(x0, P["ln"], cfg.eps)
+        w = po.expert_mixing_weights(po.softmax(h2 @ P["router"].T), idx)
+        m = {s: po.lower_leaky(ci[0][s]) for s in mo.SITES}
+        out = x0.copy()
+        for t in range(cfg.T):
+            for slot in range(cfg.k):
+                e = idx[t, slot]
+                g = ((h2[t] @ P["Vg"][e]) * m["gate"][t, slot]) @ P["Ug"][e]
+                u_ = ((h2[t] @ P["Vu"][e]) * m["up"][t, slot]) @ P["Uu"][e]
+                din = mo.silu(g) * u_ * w[t, slot]
+                out[t] += ((din @ P["Vd"][e]) * m["down"][t, slot]) @ P["Ud"][e]
+        np.testing.assert_allclose(res["r_final"], out, rtol=1e-12, atol=1e-12)
+
+
 def test_moe_delta_channel_restores_the_target_when_every_component_is_live():
     """ci >= 1 (lower(ci) = 1, m = 1) and exact factorizations V_e U_e = W_e: the site
     output (h (1 - d)) U + d x W = x W whatever d is, so the masked stack equals the clean
