@@ -767,7 +767,7 @@ def main():
               "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = {MOE: 64, DENSE: 256, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
+        args.cpu_tokens = {MOE: 2048, DENSE: 4096, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
                            KL_STREAM: 64}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
