@@ -763,8 +763,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: every GPU box here has one MI355X; --gpus {args.gpus} is not run. "
-              "How the path would shard is described in DESIGN.md, not measured.", file=sys.stderr)
+        print(f"bench.py measures one GPU (one MI355X); --gpus {args.gpus} is not run. "
+              "How the path would shard is a design note, not a measurement.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
         args.cpu_tokens = {MOE: 2048, DENSE: 4096, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,

@@ -5,7 +5,7 @@ small C library (`oracle/cpu_step.c`), the arithmetic of goodfire-ai/param-decom
 masked-component path. Every function cites the reference file:line it follows.
 
 Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg may import
-it, and only as the checker (or the timed CPU baseline). The product path
+it, and only to check results (or as the timed CPU baseline). The product path
 (`param_decomp_amd`) never imports it and fails loudly when its HIP library is missing.
 
 Pinning (what checks each function besides a retyped formula):
