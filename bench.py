@@ -685,12 +685,14 @@ def run_moe(args):
     def rn(*shape, scale):
         return (torch.randn(*shape, device=dev, generator=g) * scale).to(torch.bfloat16)
 
+    # V by its per-block fan-in, U by the site's C = E*c (the reference's blocked init,
+    # BLOCKED_U_INIT_FAN_IN = "site", pd/core/components.py:639-677)
     w = MoEWeights(ln=torch.zeros(Ln, d, device=dev), router=rn(Ln, E, d, scale=d**-0.5),
                    Wg=rn(Ln, E, d, f, scale=d**-0.5), Wu=rn(Ln, E, d, f, scale=d**-0.5),
                    Wd=rn(Ln, E, f, d, scale=f**-0.5), Vg=rn(Ln, E, d, c, scale=d**-0.5),
-                   Ug=rn(Ln, E, c, f, scale=c**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
-                   Uu=rn(Ln, E, c, f, scale=c**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
-                   Ud=rn(Ln, E, c, d, scale=c**-0.5))
+                   Ug=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
+                   Uu=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
+                   Ud=rn(Ln, E, c, d, scale=(E * c)**-0.5))
     x0 = rn(T, d, scale=1.0)
     ci = (torch.rand(Ln, 3, T, k, c, device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
     step = MoEStackStep(T, d, f, E, k, c, Ln, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0,

@@ -3,7 +3,9 @@
 The stack is the reference's MoE layer with every routed expert matrix decomposed,
 mixers and the shared expert excluded: per layer
 `h2 = rms_norm_zero_centered(r)` (`param_decomp/param_decomp/target_ports/qwen3_5_moe.py:33-41`),
-fp32 router softmax, top-k (`pd/targets/qwen36_moe.py:473-514`), jobs schedule
+router softmax over the router product rounded to the bf16 matmul dtype and widened
+(`router_logits`, `pd/targets/qwen36_moe.py:473-475`; the rounding applies with
+`bf16_storage`), top-k (`:483-514`), jobs schedule
 (`pd/routed/experts.py:115-123`), decomposed expert sites in job space
 (`pd/targets/qwen36_moe.py:2752-2837`: `acts = gmm(x_jobs, V) * mask_jobs`,
 `out = gmm(acts, U)`, routing weights folded into the down input in fp32,
@@ -95,22 +97,31 @@ def grouped_T(lhs, rhs, sizes):
 
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                   bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None):
+                   bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None,
+                   pinned_top_idx=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
-    given. Returns dict(loss, recon, imp, grads, d_ci_pre, top_idx, r_final, rc_final,
-    deltas)."""
+    given. `pinned_top_idx[l]` ([T, k]) replaces the clean pass's own expert selection
+    (which is still computed and returned as `own_top_idx`, with the clean pass's router
+    products before rounding, `logits_raw`, and the sums of their terms' magnitudes,
+    `logits_mag`, that bound an fp32 accumulation's error). Returns dict(loss, recon,
+    imp, grads, d_ci_pre, top_idx, own_top_idx, logits_raw, logits_mag, r_final,
+    rc_final, deltas)."""
     rb = po.round_bf16 if bf16_storage else (lambda a: a)
     T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
     # ---------------- clean forward (frozen weights)
     rc = rb(x0)
-    tops = []
+    tops, own_tops, raws, mags = [], [], [], []
     for l in range(cfg.L):
         P = params[l]
         h2c, _ = rms_norm_zero_centered(rc, P["ln"], cfg.eps)
         h2c = rb(h2c)
-        probs = po.softmax(h2c @ P["router"].T)
-        idx = po.select_experts(probs, k)
+        raw = h2c @ P["router"].T
+        raws.append(raw)
+        mags.append(np.abs(h2c) @ np.abs(P["router"]).T)
+        probs = po.softmax(rb(raw))
+        own_tops.append(po.select_experts(probs, k))
+        idx = own_tops[-1] if pinned_top_idx is None else np.asarray(pinned_top_idx[l]).astype(own_tops[-1].dtype)
         w = po.expert_mixing_weights(probs, idx)
         jobs = po.routed_jobs(idx, E)
         xj = h2c[jobs.sort_idx // k]
@@ -129,7 +140,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         P = params[l]
         h2, rinv = rms_norm_zero_centered(r, P["ln"], cfg.eps)
         h2 = rb(h2)
-        probs = po.softmax(h2 @ P["router"].T)
+        probs = po.softmax(rb(h2 @ P["router"].T))
         idx = tops[l]
         w = po.expert_mixing_weights(probs, idx)
         jobs = po.routed_jobs(idx, E)
@@ -227,16 +238,55 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_psel = (d_w - np.sum(d_w * w, axis=-1, keepdims=True)) / Ssum
         d_probs = np.zeros_like(probs)
         np.put_along_axis(d_probs, idx.astype(np.int64), d_psel, axis=-1)
-        d_logits = probs * (d_probs - np.sum(probs * d_probs, axis=-1, keepdims=True))
+        d_logits = rb(probs * (d_probs - np.sum(probs * d_probs, axis=-1, keepdims=True)))
         d_h2 = po.gather_tokens_vjp(d_xj, jobs) + d_logits @ P["router"]
         dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
         dr = rb(dr + dx)
-    return dict(loss=loss, recon=recon, imp=imp, grads=grads, d_ci_pre=d_pre, top_idx=tops, r_final=r,
-                rc_final=rc, dx0=dr, deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
+    return dict(loss=loss, recon=recon, imp=imp, grads=grads, d_ci_pre=d_pre, top_idx=tops, own_top_idx=own_tops,
+                logits_raw=raws, logits_mag=mags, r_final=r, rc_final=rc, dx0=dr,
+                deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
+
+
+def selection_within_ulps(raw, got, k, n_ulp=1):
+    """True when the expert selection `got` ([k]) is the descending top-k, lowest index
+    on ties, of SOME logits within `n_ulp` bf16 ulps of the bf16-rounded router products
+    `raw` ([E]). Two products with the same exact value can round to adjacent bf16 values
+    when their fp32 accumulation orders (or a bf16 input one step upstream) differ, so a
+    selection from another correct implementation may differ from this oracle's exactly
+    where two logits are that close."""
+    r = po.round_bf16(np.asarray(raw, np.float64))
+    ulp = np.abs(r) * 2.0**-7
+    got = [int(e) for e in got]
+    if len(set(got)) != k:
+        return False
+    lo, hi = r - n_ulp * ulp, r + n_ulp * ulp
+    tiny = 1e-12
+
+    def lift(e, floor, floor_idx):
+        """Smallest admissible value of expert e ranked above a value `floor` held by
+        expert floor_idx (equal values rank the lower index first), or None."""
+        z = max(lo[e], floor)
+        if z == floor and floor_idx is not None and e > floor_idx:
+            z = floor + tiny
+        return z if z <= hi[e] else None
+
+    # the selected values must all stay at or above every unselected expert's lowest value
+    rest = [e for e in range(len(r)) if e not in got]
+    z, z_idx = -np.inf, None
+    for e in sorted(rest, key=lambda e: (lo[e], -e)):
+        z, z_idx = lo[e], e  # the binding constraint: the largest lower bound (lowest index on equal)
+    for e in reversed(got):  # then each selected expert above the next one down
+        zz = lift(e, z, z_idx)
+        if zz is None:
+            return False
+        z, z_idx = zz, e
+    return True
 
 
 def init_moe(cfg: MoEConfig, rng):
-    """Random target and components of the stated shapes (the step's synthetic setup)."""
+    """Random target and components of the stated shapes (the step's synthetic setup).
+    V scales by its per-block fan-in and each block's U by the site's C = E*c
+    (`BLOCKED_U_INIT_FAN_IN = "site"`, `pd/core/components.py:639-677`)."""
     d, f, E, c = cfg.d, cfg.f, cfg.E, cfg.c
 
     def rn(*shape, scale=1.0):
@@ -246,9 +296,9 @@ def init_moe(cfg: MoEConfig, rng):
     for _ in range(cfg.L):
         P = dict(ln=rn(d, scale=0.1), router=rn(E, d, scale=d**-0.5),
                  Wg=rn(E, d, f, scale=d**-0.5), Wu=rn(E, d, f, scale=d**-0.5), Wd=rn(E, f, d, scale=f**-0.5),
-                 Vg=rn(E, d, c, scale=d**-0.5), Ug=rn(E, c, f, scale=c**-0.5),
-                 Vu=rn(E, d, c, scale=d**-0.5), Uu=rn(E, c, f, scale=c**-0.5),
-                 Vd=rn(E, f, c, scale=f**-0.5), Ud=rn(E, c, d, scale=c**-0.5))
+                 Vg=rn(E, d, c, scale=d**-0.5), Ug=rn(E, c, f, scale=(E * c)**-0.5),
+                 Vu=rn(E, d, c, scale=d**-0.5), Uu=rn(E, c, f, scale=(E * c)**-0.5),
+                 Vd=rn(E, f, c, scale=f**-0.5), Ud=rn(E, c, d, scale=(E * c)**-0.5))
         params.append(P)
     x0 = rn(cfg.T, d)
     ci = [{s: rng.uniform(-0.3, 1.3, size=(cfg.T, cfg.k, c)) for s in SITES} for _ in range(cfg.L)]

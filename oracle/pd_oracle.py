@@ -405,11 +405,20 @@ class DenseStepResult:
 
 
 def round_bf16(a):
-    """Round to bfloat16 (round-to-nearest-even), returned as float64."""
+    """Round to bfloat16 (round-to-nearest-even), returned as float64. The float64 value
+    is first rounded to fp32 (as a bf16 store of an fp32 accumulator would see it);
+    NaNs stay NaN."""
     a32 = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
-    u = a32.view(np.uint32).astype(np.uint64)
-    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+    u = a32.view(np.uint32)
+    r = (u >> np.uint32(16)) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u  # uint32 arithmetic; only NaN payloads can wrap, and they are restored below
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32).astype(np.float64)
+    nan = np.isnan(a32)
+    if nan.any():
+        out[nan] = np.nan
+    return out
 
 
 def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0, imp_coeff=1.0,

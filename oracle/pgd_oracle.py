@@ -57,11 +57,31 @@ def momentum_sgd(values, g, velocity, lr, momentum):
 
 
 def adam(values, g, m, v, step_count, lr, beta1=0.9, beta2=0.999, eps=1e-8):
-    """`pd/core/adversary.py:463-484` (step_count is the count after this update)."""
+    """`pd/core/adversary.py:463-496` (step_count is the count after this update), exact
+    arithmetic: the fp32-moment form."""
     m = beta1 * m + (1 - beta1) * g
     v = beta2 * v + (1 - beta2) * g * g
     bc1, bc2 = 1 - beta1 ** step_count, 1 - beta2 ** step_count
     return np.clip(values + lr * (m / bc1) / (np.sqrt(v / bc2) + eps), 0.0, 1.0), m, v
+
+
+def adam_bf16(values, g, m, v, step_count, lr, beta1=0.9, beta2=0.999, eps=1e-8):
+    """The same ascent with bf16 sources and moments, rounding where the reference's
+    dtypes round (`pd/core/adversary.py:463-496`): the gradient is cast to the moment
+    dtype; the Python-float coefficients beta and (1 - beta) meet bf16 moments as weak
+    scalars and so are rounded to bf16 (bf16(0.9) = 0.8984375, bf16(0.999) = 1.0); every
+    bf16 product and sum rounds; the bias corrections are fp32 on fp32(beta); the update
+    is formed in fp32 and cast to bf16 before the add and the clip."""
+    rb = round_bf16
+    f32 = lambda a: np.asarray(a, np.float32).astype(np.float64)  # noqa: E731
+    g = rb(g)
+    b1, omb1, b2, omb2 = rb(beta1), rb(1.0 - beta1), rb(beta2), rb(1.0 - beta2)
+    m = rb(rb(b1 * m) + rb(omb1 * g))
+    v = rb(rb(b2 * v) + rb(rb(omb2 * g) * g))
+    bc1 = f32(1.0 - f32(f32(beta1) ** step_count))
+    bc2 = f32(1.0 - f32(f32(beta2) ** step_count))
+    upd = f32(f32(lr) * f32(f32(m) / bc1) / f32(f32(np.sqrt(f32(v / bc2))) + f32(eps)))
+    return np.clip(rb(values + rb(upd)), 0.0, 1.0), m, v
 
 
 def sign_ascent(values, g, step_size):

@@ -27,6 +27,12 @@ int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out
                                 const void* doutT2, void* out2, const int32_t* offsets, int64_t J, int E, int64_t K,
                                 int64_t N, int out_dtype, void* stream);
 
+// pd_router_topk with the logits first rounded to bf16 when round_bf16 is set (the
+// reference's router product runs in the target's bf16 matmul dtype and is widened to
+// fp32 afterwards, pd/targets/qwen36_moe.py:473-475).
+int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, float* probs, int32_t* top_idx,
+                float* weights, void* stream);
+
 // ---------------------------------------------------------------- bf16
 typedef uint16_t bf16_t;
 

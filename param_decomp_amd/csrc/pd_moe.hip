@@ -155,15 +155,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const bf16_t* __restrict__ 
   }
 }
 
-// Masked-layer routing weights at pinned indices: probs = softmax(logits) (saved),
-// w[t,s] = probs[idx[t,s]] / sum_s probs[idx[t,s]]. One wave per token, E <= 64.
+// Masked-layer routing weights at pinned indices: probs = softmax(bf16(logits))
+// (saved), w[t,s] = probs[idx[t,s]] / sum_s probs[idx[t,s]]. The fp32 product is
+// rounded to bf16 first: the reference's router product runs in the bf16 matmul dtype
+// (pd/targets/qwen36_moe.py:473-475). One wave per token, E <= 64.
 __global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__ logits, int64_t T, int E, int k,
                                                        const int32_t* __restrict__ idx, float* __restrict__ probs,
                                                        float* __restrict__ w) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float x = lane < E ? logits[t * E + lane] : -INFINITY;
+  float x = lane < E ? bf16_to_f32(f32_to_bf16(logits[t * E + lane])) : -INFINITY;
   float mx = wave_max(x);
   float ex = lane < E ? expf(x - mx) : 0.f;
   float p = ex / wave_sum(ex);
@@ -520,7 +522,7 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
 
 // d_logits[t, lane] of one token (lanes = experts, 0 past E), all 64 lanes active:
 // d_w[s] = sum of the d_w_part tiles of job inv[t*k+s], through w = p_sel / sum p_sel
-// and the router softmax.
+// and the router softmax, rounded to bf16.
 __device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int n_part,
                                          const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
                                          const float* __restrict__ probs, const float* __restrict__ w, int64_t t,
@@ -545,7 +547,9 @@ __device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int
     if (lane == es) dpe += v;
   }
   const float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
-  return lane < E ? pe * (dpe - sdot) : 0.f;
+  // the logits were widened from the bf16 router product: their cotangent narrows to
+  // bf16 on its way back into that product
+  return lane < E ? bf16_to_f32(f32_to_bf16(pe * (dpe - sdot))) : 0.f;
 }
 
 // Token backward, one wave per TPW consecutive tokens, lane l owning columns 8l..8l+7 of
@@ -1034,7 +1038,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, h2l, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
                       PD_DTYPE_F32, 1.f, 0.f, stream)))
       return rc;
-    if ((rc = pd_router_topk(P.logits, T, E, k, P.probsc, S.idx, P.wc, stream))) return rc;
+    if ((rc = router_topk(P.logits, T, E, k, true, P.probsc, S.idx, P.wc, stream))) return rc;
     if (l == 0)
       hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
                          S.probs, S.w);

@@ -218,9 +218,9 @@ struct AscendArgs {
   const float* grad;
   void* sa;  // adam m (storage dtype) or momentum velocity (fp32 for fp32 storage, else bf16)
   void* sb;  // adam v (storage dtype)
-  // beta and its complement are formed as the reference forms them: beta * moment takes
-  // beta rounded to fp32, (1 - beta) * g takes the double difference rounded to fp32,
-  // and the bias corrections 1 - beta^step are fp32 arithmetic on fp32(beta)
+  // beta and its complement as the reference's arithmetic sees them: rounded to the
+  // moment dtype (fp32, or bf16 for bf16 moments), (1 - beta) formed in double first;
+  // the bias corrections 1 - beta^step are fp32 arithmetic on fp32(beta)
   float lr, beta1, omb1, beta2, omb2, eps, momentum, bc1, bc2;
   uint32_t k0, k1;
   int layout;
@@ -410,9 +410,15 @@ int pd_source_ascend(int opt, int src_dtype, int64_t n, void* sources, const flo
     return fail(PD_EINVAL, "pd_source_ascend: adam needs m, v and a step count >= 1");
   if (opt < PD_PGD_SGD || opt > PD_PGD_SIGN) return fail(PD_EINVAL, "pd_source_ascend: optimizer");
   const float b1 = (float)beta1, b2 = (float)beta2;
+  // beta * moment and (1 - beta) * g take the Python-float coefficients at the moment
+  // dtype (JAX's weak typing, pd/core/adversary.py:475-480): fp32 for fp32 moments,
+  // bf16-rounded for bf16 moments (bf16(0.999) = 1, so v does not decay there). The bias
+  // corrections 1 - beta^step are fp32 on fp32(beta) in both.
+  const bool b16m = src_dtype == PD_DTYPE_BF16;
+  auto coef = [&](double c) { return b16m ? bf16_to_f32(f32_to_bf16((float)c)) : (float)c; };
   AscendArgs a{opt,      n,        sources,  grad,     state_a,
-               state_b,  lr,       b1,       (float)(1.0 - beta1),
-               b2,       (float)(1.0 - beta2), eps,    momentum,
+               state_b,  lr,       coef(beta1),        coef(1.0 - beta1),
+               coef(beta2),        coef(1.0 - beta2),  eps,    momentum,
                1.f - powf(b1, step_count),     1.f - powf(b2, step_count),
                k0,       k1,       layout};
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n, 256), 16384);

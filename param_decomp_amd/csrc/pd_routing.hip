@@ -13,7 +13,8 @@ namespace pd {
 
 // One wave per token, lane e holds expert e. Top-k by k rounds of a wave argmax that
 // prefers the larger probability and, on equal probabilities, the lower index — the
-// order of a stable descending sort.
+// order of a stable descending sort. ROUND: the logits are rounded to bf16 first.
+template <bool ROUND>
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int64_t T, int E, int k,
                                                      float* __restrict__ probs, int32_t* __restrict__ top_idx,
                                                      float* __restrict__ weights) {
@@ -21,6 +22,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (t >= T) return;
   float x = lane < E ? logits[t * E + lane] : -INFINITY;
+  if (ROUND && lane < E) x = bf16_to_f32(f32_to_bf16(x));
   float mx = wave_max(x);
   float ex = lane < E ? expf(x - mx) : 0.f;
   float z = wave_sum(ex);
@@ -226,6 +228,20 @@ __global__ __launch_bounds__(256) void k_route_static_p(uint32_t k0, uint32_t k1
         (uint8_t)(bits_to_uniform(draw_bits(f0, f1, pos, N, 32, LAYOUT), PD_DTYPE_F32) < p);
 }
 
+int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, float* probs, int32_t* top_idx,
+                float* weights, void* stream) {
+  if (T < 0 || E <= 0 || E > 64 || k <= 0 || k > E || !logits || !top_idx || !weights)
+    return fail(PD_EINVAL, "pd_router_topk: need 0 < k <= E <= 64");
+  if (T == 0) return PD_OK;
+  if (round_bf16)
+    hipLaunchKernelGGL(k_router_topk<true>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T,
+                       E, k, probs, top_idx, weights);
+  else
+    hipLaunchKernelGGL(k_router_topk<false>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T,
+                       E, k, probs, top_idx, weights);
+  return check_launch("pd_router_topk");
+}
+
 }  // namespace pd
 
 using namespace pd;
@@ -234,12 +250,7 @@ extern "C" {
 
 int pd_router_topk(const float* logits, int64_t T, int E, int k, float* probs, int32_t* top_idx, float* weights,
                    void* stream) {
-  if (T < 0 || E <= 0 || E > 64 || k <= 0 || k > E || !logits || !top_idx || !weights)
-    return fail(PD_EINVAL, "pd_router_topk: need 0 < k <= E <= 64");
-  if (T == 0) return PD_OK;
-  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T, E, k,
-                     probs, top_idx, weights);
-  return check_launch("pd_router_topk");
+  return router_topk(logits, T, E, k, false, probs, top_idx, weights, stream);
 }
 
 size_t pd_routed_jobs_workspace_size(int64_t n_jobs, int E) {

@@ -39,6 +39,26 @@ def component_coefficients(mask: torch.Tensor, delta: torch.Tensor | None) -> to
     return mask if delta is None else mask - delta
 
 
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise L.PDError(msg)
+
+
+def _check_operands(x, V, U, W, mask, v_shape, u_shape, w_shape, c_total):
+    """The kernels read every operand in x's dtype: the factors and the target weight
+    must already be in it (the reference casts them once per step,
+    `pd/core/model.py:479-483`); the mask and delta are cast here, as the reference's
+    arithmetic promotes them (`pd/core/decomposed_linear.py:65-85`)."""
+    for name, t, shape in (("V", V, v_shape), ("U", U, u_shape), ("W", W, w_shape)):
+        if t is None:
+            continue
+        _require(t.dtype == x.dtype, f"site_forward: {name} is {t.dtype}, x is {x.dtype}")
+        _require(tuple(t.shape) == tuple(shape), f"site_forward: {name} has shape {tuple(t.shape)}, expected "
+                                                 f"{tuple(shape)}")
+    _require(mask.shape[-1] == c_total and mask.numel() == x.numel() // x.shape[-1] * c_total,
+             f"site_forward: mask shape {tuple(mask.shape)} does not match x {tuple(x.shape)} and C={c_total}")
+
+
 class _MaskedLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, V, U, mask, W, delta, route):
@@ -47,8 +67,10 @@ class _MaskedLinear(torch.autograd.Function):
         d_in, C = V.shape
         d_out = U.shape[1]
         dt = L.dtype_code(x.dtype)
+        _require(x.shape[-1] == d_in, f"site_forward: x has {x.shape[-1]} features, V expects {d_in}")
+        _check_operands(x, V, U, W, mask, (d_in, C), (C, d_out), (d_out, d_in), C)
         x2 = x.reshape(T, d_in).contiguous()
-        m2 = mask.reshape(T, C).contiguous()
+        m2 = mask.reshape(T, C).to(x.dtype).contiguous()
         d2 = None if delta is None else delta.reshape(T).to(x.dtype).contiguous()
         r2 = None if route is None else route.reshape(T).to(torch.uint8).contiguous()
         Wc = None if W is None else W.contiguous()
@@ -138,8 +160,13 @@ class _BlockedMaskedLinear(torch.autograd.Function):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1]).contiguous()
         T = x2.shape[0]
-        m2 = mask.reshape(T, E * c).contiguous()
-        d2 = None if delta is None else delta.reshape(T).contiguous()
+        fo = contraction == "fused_output"
+        _require(x.shape[-1] == (d_in if fo else E * d_in),
+                 f"blocked_site_forward: x has {x.shape[-1]} features for {E} blocks of d_in={d_in} ({contraction})")
+        _check_operands(x, V, U, W, mask, (E, d_in, c), (E, c, d_out),
+                        (E * d_out, d_in) if fo else (d_out, E * d_in), E * c)
+        m2 = mask.reshape(T, E * c).to(x.dtype).contiguous()
+        d2 = None if delta is None else delta.reshape(T).to(x.dtype).contiguous()
         r2 = None if route is None else route.reshape(T).to(torch.uint8).contiguous()
         Wc = None if W is None else W.contiguous()
         code = _CONTRACTIONS[contraction]

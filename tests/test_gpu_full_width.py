@@ -1,0 +1,149 @@
+"""GPU parity at the widths the measured workloads run, so every kernel instantiation
+those workloads select is compared against the oracle, not only checked for finiteness:
+
+- the MoE stack at its full widths (d=512, f=256, c=512, 42 experts, top-8): the
+  256x256 grouped tiles of the N=512 component products (`grouped_gemm_pair`) and of
+  every paired weight gradient (`grouped_gemm_dw_kmajor_pair`), K=512 main loops over
+  several k stages, and ragged per-expert contraction lengths;
+- the register-staged 256x256 dense tile (`k_gemm_bf16` on `TileCfg<256,256>`, taken
+  for operands that are not both K-contiguous once the grid has >= 192 such tiles);
+- the public grouped products at K = N = 512 with ragged and empty groups.
+
+Reference semantics: `pd/targets/qwen36_moe.py:2752-2837` (decomposed experts in job
+space), `pd/routed/experts.py:209-348` (grouped products and the ragged dW).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as mo
+from oracle import pd_oracle as po
+from routing_checks import assert_routing_matches
+
+pytestmark = pytest.mark.gpu
+
+BF16_RTOL = 2e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _bf(a, device):
+    return torch.tensor(np.asarray(a, np.float32), device=device).to(torch.bfloat16)
+
+
+def _close(got, want, rtol, floor, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    err = np.abs(got - want)
+    bad = err > rtol * np.abs(want) + floor * scale
+    assert not bad.any(), f"{what}: {bad.sum()}/{bad.size} off, worst {err.max():.3e} scale {scale:.3e}"
+
+
+def test_moe_stack_step_full_width_matches_oracle(device):
+    """T=1024 tokens through 2 layers at the benchmark's widths, with the frozen delta
+    channel: routing bit-exact up to bf16 near-ties of the router products, losses and
+    every gradient within rtol 2e-2 of the oracle's bf16-storage model on the same
+    routing. About 20 s of oracle time."""
+    from param_decomp_amd import _lib as L
+    from param_decomp_amd.moe_step import MoEStackStep, MoEWeights
+
+    cfg = mo.MoEConfig(T=1024, d=512, f=256, E=42, k=8, c=512, L=2)
+    rng = np.random.default_rng(21)
+    params, x0, ci = mo.init_moe(cfg, rng)
+    rb = po.round_bf16
+    params = [{k: (v.astype(np.float32).astype(np.float64) if k == "ln" else rb(v)) for k, v in P.items()}
+              for P in params]
+    x0 = rb(x0)
+    ci = [{s: rb(v) for s, v in layer.items()} for layer in ci]
+
+    def stack(name, dt=torch.bfloat16):
+        return torch.tensor(np.stack([P[name] for P in params]).astype(np.float32), device=device).to(dt)
+
+    w = MoEWeights(ln=stack("ln", torch.float32), router=stack("router"), Wg=stack("Wg"), Wu=stack("Wu"),
+                   Wd=stack("Wd"), Vg=stack("Vg"), Ug=stack("Ug"), Vu=stack("Vu"), Uu=stack("Uu"), Vd=stack("Vd"),
+                   Ud=stack("Ud"))
+    ci_t = _bf(np.stack([np.stack([layer[s] for s in mo.SITES]) for layer in ci]), device)
+    x0_t = _bf(x0, device)
+    key = (3, 29)
+    step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, p=2.0, imp_coeff=0.5,
+                        recon_coeff=1.5, layout=L.LAYOUT_PARTITIONABLE, use_delta=True)
+    step.step(x0_t, w, ci_t, key)
+    torch.cuda.synchronize()
+    got_idx = step.top_idx.cpu().numpy()
+    ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True,
+                            partitionable=True, use_delta=True, pinned_top_idx=got_idx)
+    for l in range(cfg.L):
+        assert_routing_matches(got_idx[l], ref, l, cfg.k)
+        sizes = np.bincount(got_idx[l].ravel(), minlength=cfg.E)
+        assert sizes.min() > 64  # every expert's rows span several 64-deep k stages of the dW
+    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"]], rtol=2e-2)
+    for l in range(cfg.L):
+        for s, vn, un in (("gate", "Vg", "Ug"), ("up", "Vu", "Uu"), ("down", "Vd", "Ud")):
+            _close(step.dV[s][l].cpu().numpy(), ref["grads"][l][vn], BF16_RTOL, 1e-2, f"{vn}[{l}]")
+            _close(step.dU[s][l].cpu().numpy(), ref["grads"][l][un], BF16_RTOL, 1e-2, f"{un}[{l}]")
+        got = step.d_ci_pre[l].float().cpu().numpy()
+        for si, s in enumerate(mo.SITES):
+            _close(got[si], ref["d_ci_pre"][l][s], BF16_RTOL, 1e-2, f"d_ci_pre[{l}][{s}]")
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 768), (4000, 3000, 776)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (1, 1)])
+def test_gemm_register_staged_big_tile(device, ta, tb, M, N, K):
+    """The dense site's shapes with operand layouts the buffer-fed kernel does not take
+    (it needs both operands K-contiguous: ta=0, tb=1): >= 192 256x256 tiles select the
+    register-staged 256x256 kernel. fp32 output within fp32 accumulation-order error of
+    a float64 product; bf16 output within bf16 rounding."""
+    from param_decomp_amd import ops
+
+    assert -(-M // 256) * -(-N // 256) >= 192
+    rng = np.random.default_rng(M + N + K + 2 * ta + tb)
+    A = _bf(rng.normal(size=(K, M) if ta else (M, K)), device)
+    B = _bf(rng.normal(size=(N, K) if tb else (K, N)), device)
+    An, Bn = _np(A), _np(B)
+    want = (An.T if ta else An) @ (Bn.T if tb else Bn)
+    out = ops.gemm(A, B, trans_a=bool(ta), trans_b=bool(tb), out_dtype=torch.float32)
+    _close(_np(out), want, 1e-5, 1e-6, f"gemm fp32 out ta={ta} tb={tb}")
+    out16 = ops.gemm(A, B, trans_a=bool(ta), trans_b=bool(tb))
+    _close(_np(out16), want, BF16_RTOL, 1e-3, f"gemm bf16 out ta={ta} tb={tb}")
+
+
+def test_grouped_products_at_k_n_512(device):
+    """Forward (both rhs layouts), d_input and both dW forms at K = N = 512 over 42
+    groups with ragged sizes, three empty groups and trailing rows past the last offset."""
+    from param_decomp_amd import ops
+    from param_decomp_amd.routed.experts import grouped_matmul, transposed_grouped_matmul
+
+    rng = np.random.default_rng(5)
+    E, K, N = 42, 512, 512
+    sizes = rng.integers(1, 400, size=E)
+    sizes[[3, 17, 41]] = 0
+    used = int(sizes.sum())
+    J = (used + 13 + 7) // 8 * 8
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = _bf(rng.normal(size=(J, K)), device).requires_grad_(True)
+    rhs = _bf(rng.normal(size=(E, K, N)) / 16, device).requires_grad_(True)
+    out = grouped_matmul(lhs, rhs, offsets)
+    want = po.grouped_matmul(_np(lhs)[:used], _np(rhs), sizes)
+    _close(_np(out)[:used], want, BF16_RTOL, 4e-3, "grouped fwd")
+    assert torch.count_nonzero(out[used:]) == 0
+    outT = ops.grouped_gemm(lhs.detach(), rhs.detach().transpose(1, 2).contiguous(), offsets, trans_rhs=True)
+    _close(_np(outT)[:used], want, BF16_RTOL, 4e-3, "grouped fwd, K-contiguous rhs")
+    g = _bf(rng.normal(size=(J, N)), device)
+    dl, dr = torch.autograd.grad(out, (lhs, rhs), g)
+    gn = _np(g)
+    gn[used:] = 0.0
+    _close(_np(dl)[:used], po.grouped_matmul(gn[:used], np.transpose(_np(rhs), (0, 2, 1)), sizes), BF16_RTOL, 4e-3,
+           "grouped d_lhs")
+    want_dw = po.transposed_grouped_matmul(_np(lhs)[:used], gn[:used], sizes)
+    _close(_np(dr), want_dw, BF16_RTOL, 4e-3, "grouped d_rhs")
+    dw = transposed_grouped_matmul(lhs.detach(), g, offsets, out_dtype=torch.float32)
+    _close(_np(dw), want_dw, 1e-5, 1e-6, "dw fp32")
+    dwk = ops.grouped_gemm_dw_kmajor(lhs.detach().t().contiguous(), g.t().contiguous(), offsets, E,
+                                     out_dtype=torch.float32)
+    _close(_np(dwk), want_dw, 1e-5, 1e-6, "dw kmajor fp32")
+    for e in (3, 17, 41):
+        assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dwk[e]) == 0

@@ -1,5 +1,6 @@
 """GPU parity of the fused MoE stack step against the MoE oracle (same bf16 storage
-points): pinned routing bit-exact, losses and every gradient within rtol 2e-2."""
+points): routing bit-exact up to bf16 near-ties of the router products, losses and
+every gradient within rtol 2e-2 on the same routing."""
 
 import numpy as np
 import pytest
@@ -7,6 +8,7 @@ import torch
 
 from oracle import moe_oracle as mo
 from oracle import pd_oracle as po
+from routing_checks import assert_routing_matches
 
 pytestmark = pytest.mark.gpu
 
@@ -60,10 +62,12 @@ def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, so
                         use_delta=use_delta, source_value=-1.0 if source_value is None else source_value)
     step.step(x0_t, w, ci_t, key)
     torch.cuda.synchronize()
+    got_idx = step.top_idx.cpu().numpy()
     ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True,
-                            partitionable=partitionable, use_delta=use_delta, source_value=source_value)
+                            partitionable=partitionable, use_delta=use_delta, source_value=source_value,
+                            pinned_top_idx=got_idx)
     for l in range(cfg.L):
-        np.testing.assert_array_equal(step.top_idx[l].cpu().numpy(), ref["top_idx"][l])
+        assert_routing_matches(got_idx[l], ref, l, cfg.k)
     losses = step.losses.cpu().numpy()
     np.testing.assert_allclose(losses, [ref["loss"], ref["recon"], ref["imp"]], rtol=2e-2)
     for l in range(cfg.L):
@@ -91,9 +95,9 @@ def test_moe_stack_step_full_size_properties(device):
     w = MoEWeights(ln=torch.zeros(Ln, d, device=device), router=rn(Ln, E, d, scale=d**-0.5),
                    Wg=rn(Ln, E, d, f, scale=d**-0.5), Wu=rn(Ln, E, d, f, scale=d**-0.5),
                    Wd=rn(Ln, E, f, d, scale=f**-0.5), Vg=rn(Ln, E, d, c, scale=d**-0.5),
-                   Ug=rn(Ln, E, c, f, scale=c**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
-                   Uu=rn(Ln, E, c, f, scale=c**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
-                   Ud=rn(Ln, E, c, d, scale=c**-0.5))
+                   Ug=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
+                   Uu=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
+                   Ud=rn(Ln, E, c, d, scale=(E * c)**-0.5))
     x0 = rn(T, d, scale=1.0)
     ci = (torch.rand(Ln, 3, T, k, c, device=device, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
     step = MoEStackStep(T, d, f, E, k, c, Ln, device=device)

@@ -291,6 +291,42 @@ def test_site_forward_and_backward(device, dtype, with_delta, with_route):
         assert_close(np64(got), w, rtol, 1e-4 if dtype == torch.float32 else 5e-3, name)
 
 
+@pytest.mark.parametrize("blocked", [False, True])
+def test_site_forward_casts_fp32_mask_and_delta_to_bf16(device, blocked):
+    """An fp32 mask or delta (e.g. uniforms drawn in fp32) with bf16 activations is cast
+    to x's dtype, as the reference's arithmetic promotes it: the result equals the
+    all-bf16 call bit for bit, gradients included (returned in the input's dtype)."""
+    from param_decomp_amd.decomposed_linear import (BlockedSiteWeights, SiteWeights, blocked_site_forward,
+                                                    site_forward)
+
+    rng = np.random.default_rng(31)
+    T, d_in, d_out = 48, 64, 80
+    if blocked:
+        E, c = 3, 16
+        C = E * c
+        W, V, U = rng.normal(size=(E * d_out, d_in)) / 8, rng.normal(size=(E, d_in, c)) / 8, rng.normal(
+            size=(E, c, d_out)) / 8
+        run = lambda x, m, d: blocked_site_forward(x, BlockedSiteWeights(tW, tV, tU), m, d, None,  # noqa: E731
+                                                   "fused_output").output
+    else:
+        C = 96
+        W, V, U = rng.normal(size=(d_out, d_in)) / 8, rng.normal(size=(d_in, C)) / 8, rng.normal(size=(C, d_out)) / 8
+        run = lambda x, m, d: site_forward(x, SiteWeights(tW, tV, tU), m, d, None).output  # noqa: E731
+    tW, tV, tU = bf(W, device), bf(V, device), bf(U, device)
+    x = bf(rng.normal(size=(T, d_in)), device)
+    m32 = f32(po.round_bf16(rng.uniform(size=(T, C))), device).requires_grad_(True)
+    d32 = f32(po.round_bf16(rng.uniform(size=T)), device).requires_grad_(True)
+    m16 = m32.detach().to(torch.bfloat16).requires_grad_(True)
+    d16 = d32.detach().to(torch.bfloat16).requires_grad_(True)
+    y32, y16 = run(x, m32, d32), run(x, m16, d16)
+    assert torch.equal(y32, y16)
+    g = bf(rng.normal(size=tuple(y16.shape)), device)
+    gm32, gd32 = torch.autograd.grad(y32, (m32, d32), g)
+    gm16, gd16 = torch.autograd.grad(y16, (m16, d16), g)
+    assert gm32.dtype == torch.float32 and gd32.dtype == torch.float32
+    assert torch.equal(gm32, gm16.float()) and torch.equal(gd32, gd16.float())
+
+
 # ------------------------------------------------------------------ fused dense step
 
 

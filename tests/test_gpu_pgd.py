@@ -113,6 +113,31 @@ def test_source_ascents_bf16_storage(device):
     assert np.abs(_np(s2) - want2).max() <= 2 ** -8
 
 
+def test_adam_bf16_moments_over_several_steps(device):
+    """bf16 sources and moments over four steps from nonzero moments, against the
+    oracle's bf16 Adam (coefficients at the moment dtype: bf16(0.999) = 1, so v does not
+    decay; a one-step test from zero moments cannot tell this from fp32 coefficients)."""
+    rng = np.random.default_rng(6)
+    n = 5000
+    vals = po.round_bf16(rng.uniform(0.2, 0.8, size=n))
+    m0 = po.round_bf16(rng.normal(size=n) * 0.05)
+    v0 = po.round_bf16(rng.uniform(0.0, 0.01, size=n))
+    bf = lambda a: torch.tensor(np.asarray(a, np.float32), device=device).to(torch.bfloat16)  # noqa: E731
+    s, m, v = bf(vals), bf(m0), bf(v0)
+    w, mm, vv = vals, m0, v0
+    for step in (3.0, 4.0, 5.0, 6.0):
+        g = rng.normal(size=n) * 0.3
+        ops.source_ascend(L.PGD_ADAM, s, torch.tensor(g, dtype=torch.float32, device=device), m, v,
+                          step_count=step, lr=0.01)
+        w, mm, vv = po.adam_bf16(w, g, mm, vv, step, lr=0.01)
+    assert np.abs(_np(m) - mm).max() <= 1e-6 * np.abs(mm).max() + 1e-30
+    assert np.abs(_np(v) - vv).max() <= 1e-6 * np.abs(vv).max()
+    assert np.abs(_np(s) - w).max() <= 2 ** -8  # one bf16 ulp on [0, 1]
+    # the fp32-coefficient spelling would have decayed v: it is measurably different
+    _, _, v_f32 = po.adam(vals, po.round_bf16(g), m0, v0, 3.0, lr=0.01)
+    assert np.abs(v_f32 - po.adam_bf16(vals, g, m0, v0, 3.0, lr=0.01)[2]).max() > 1e-6
+
+
 @pytest.mark.parametrize("opt", [L.PGD_SGD, L.PGD_MOMENTUM])
 def test_uint16_storage_rounds_stochastically_with_the_leaf_key(device, opt):
     rng = np.random.default_rng(5)

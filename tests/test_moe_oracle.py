@@ -184,3 +184,32 @@ def test_moe_delta_channel_restores_the_target_when_every_component_is_live():
     # with the bent factorization the delta draw matters: d x (W - V U) differs per draw
     res3 = mo.moe_stack_step(cfg, bent, x0, ci, (0, 7), p=2.0, imp_coeff=0.0, recon_coeff=1.0, use_delta=False)
     assert abs(res3["recon"] - res2["recon"]) > 1e-3 * res2["recon"]
+
+
+def test_selection_within_ulps_accepts_only_near_ties():
+    # 0.999 rounds to bf16 1.0: experts 0 and 2 tie, so either order is a valid top-2
+    raw = np.array([1.0, 0.5, 0.999, 0.2, -1.0])
+    assert mo.selection_within_ulps(raw, [0, 2], 2) and mo.selection_within_ulps(raw, [2, 0], 2)
+    # 0.9 is 13 ulps below 1.0: only the exact order is accepted
+    raw = np.array([1.0, 0.5, 0.9, 0.2, -1.0])
+    assert mo.selection_within_ulps(raw, [0, 2], 2)
+    assert not mo.selection_within_ulps(raw, [2, 0], 2)
+    assert not mo.selection_within_ulps(raw, [0, 1], 2)  # a wrong member
+    assert not mo.selection_within_ulps(raw, [0, 0], 2)  # a repeated expert
+    # each logit may move one ulp, so values one or two ulps apart may swap; three may not
+    raw = np.array([1.0, 1.0078125, 1.0234375, -3.0])
+    assert mo.selection_within_ulps(raw, [2, 1, 0], 3) and mo.selection_within_ulps(raw, [2, 0, 1], 3)
+    assert mo.selection_within_ulps(raw, [1, 2, 0], 3)  # two ulps: a tie, broken by the lower index
+    assert not mo.selection_within_ulps(raw, [0, 2, 1], 3)  # three ulps apart
+    assert not mo.selection_within_ulps(raw, [0, 1, 2], 3)
+
+
+def test_pinned_routing_reproduces_the_oracles_own_step():
+    cfg = mo.MoEConfig(T=40, d=16, f=8, E=6, k=2, c=4, L=2)
+    params, x0, ci = mo.init_moe(cfg, np.random.default_rng(3))
+    a = mo.moe_stack_step(cfg, params, x0, ci, (1, 2), bf16_storage=True)
+    b = mo.moe_stack_step(cfg, params, x0, ci, (1, 2), bf16_storage=True, pinned_top_idx=a["own_top_idx"])
+    assert a["loss"] == b["loss"]
+    for l in range(cfg.L):
+        np.testing.assert_array_equal(a["top_idx"][l], b["top_idx"][l])
+        np.testing.assert_array_equal(a["grads"][l]["Vd"], b["grads"][l]["Vd"])

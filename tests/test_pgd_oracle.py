@@ -43,6 +43,24 @@ def test_first_adam_step_moves_by_lr_times_sign():
     np.testing.assert_allclose(v, 0.001 * g * g)
 
 
+def test_bf16_adam_takes_the_coefficients_at_the_moment_dtype():
+    # bf16 moments meet the Python-float betas as weak scalars: bf16(0.9) = 0.8984375,
+    # bf16(0.1) = 0.10009765625, bf16(0.999) = 1.0, bf16(0.001) = 131/128 * 2^-10 = 0.00099945068359375.
+    # Hand-rounded values for g = 1 over two steps from zero moments:
+    #   m1 = 0.10009765625; v1 = 0.00099945068359375
+    #   m2 = bf16(bf16(0.8984375 * m1) + m1) = bf16(0.08984375 + 0.10009765625)
+    #      = bf16(0.18994140625) = 0.189453125 (a tie, to even)
+    #   v2 = bf16(1.0 * v1 + v1) = 2 v1 exactly: v never decays
+    g = np.array([1.0])
+    s1, m1, v1 = po.adam_bf16(np.array([0.25]), g, np.zeros(1), np.zeros(1), 1.0, lr=0.01)
+    assert m1[0] == 0.10009765625 and v1[0] == 0.00099945068359375
+    s2, m2, v2 = po.adam_bf16(s1, g, m1, v1, 2.0, lr=0.01)
+    assert m2[0] == 0.189453125 and v2[0] == 2 * v1[0]
+    # the exact (fp32-moment) form differs exactly where the rounding bites
+    _, me, ve = po.adam(np.array([0.25]), g, np.array([0.1]), np.array([0.001]), 2.0, lr=0.01)
+    assert me[0] == pytest.approx(0.19) and ve[0] == pytest.approx(0.001999)
+
+
 def test_sgd_momentum_sign_and_projection():
     vals = np.array([0.0, 0.5, 0.95, 1.0])
     g = np.array([-1.0, 2.0, 1.0, 3.0])
