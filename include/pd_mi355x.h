@@ -164,6 +164,20 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
                          const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
                          const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
                          void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream);
+/* pd_masked_linear_bwd without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. Same arguments, kernels and results as
+ * pd_masked_linear_bwd; its scratch is a fixed device region of
+ * PD_MASKED_LINEAR_BWD_NOALLOC_MAX_BYTES per GPU inside the library, located once per
+ * device on the first call and held until the process ends. Calls whose
+ * pd_masked_linear_bwd_workspace_size exceeds it return PD_EUNSUPPORTED. No allocation
+ * happens in the call. Every call on one GPU shares that GPU's region: calls that overlap
+ * on one GPU (different streams, or host threads without ordering) race. */
+#define PD_MASKED_LINEAR_BWD_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int pd_masked_linear_bwd_noalloc(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x,
+                                 const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                                 const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx,
+                                 void* dV, void* dU, void* dmask, void* d_delta, void* stream);
 
 /* ---- block-factored site, dense over every block: pd/core/decomposed_linear.py:209-271
  *      blocked_site_forward with the einsums of pd/core/linear_plan.py:149-160.

@@ -56,6 +56,7 @@ _SIGNATURES = {
     "pd_masked_linear_fwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 11),
     "pd_masked_linear_bwd_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
     "pd_masked_linear_bwd": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 16 + [_c_sz, _c_p]),
+    "pd_masked_linear_bwd_noalloc": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 16),
     "pd_dense_step_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32]),
     "pd_dense_step": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 8 + [_c_u32] * 4 +
                       [_c_i32] * 3 + [_c_f32] * 3 + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),

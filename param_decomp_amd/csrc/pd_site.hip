@@ -3,6 +3,9 @@
 //   pd_masked_linear_fwd/bwd   pd/core/decomposed_linear.py:142-175 (site_forward),
 //                              :65-85 (component_coefficients, blend_target_output)
 //   pd_blocked_site_fwd/bwd    :209-271 (blocked_site_forward, dense over every block)
+#include <mutex>
+#include <string>
+
 #include "pd_common.hpp"
 
 namespace pd {
@@ -143,16 +146,26 @@ size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, 
   return es * (size_t)T * (size_t)C + es * (size_t)T * (size_t)d_out + 512;
 }
 
-int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
-                         const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
-                         const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
-                         void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace pd {
+
+// The masked-linear backward over a caller-sized scratch region `workspace` (at least
+// pd_masked_linear_bwd_workspace_size bytes, 256-byte aligned). Every byte of the
+// scratch it reads is written first in the same call (both regions are full GEMM
+// outputs with beta = 0), so it needs no clearing between calls.
+static int masked_linear_bwd_impl(const char* what, int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C,
+                                  const void* x, const void* V, const void* U, const void* W, const void* mask,
+                                  const void* delta, const uint8_t* route, const void* xV, const void* acts,
+                                  const void* g_out, void* dx, void* dV, void* dU, void* dmask, void* d_delta,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   if (T <= 0 || d_in <= 0 || d_out <= 0 || C <= 0 || !x || !V || !U || !mask || !xV || !acts || !g_out)
-    return fail(PD_EINVAL, "pd_masked_linear_bwd: bad args");
-  if ((delta || route) && dx && !W) return fail(PD_EINVAL, "pd_masked_linear_bwd: W required for dx");
-  if (d_delta && !W) return fail(PD_EINVAL, "pd_masked_linear_bwd: W required for d_delta");
+    return fail(PD_EINVAL, std::string(what) + ": bad args");
+  if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, std::string(what) + ": dtype");
+  if ((delta || route) && dx && !W) return fail(PD_EINVAL, std::string(what) + ": W required for dx");
+  if (d_delta && !W) return fail(PD_EINVAL, std::string(what) + ": W required for d_delta");
   if (!workspace || workspace_bytes < pd_masked_linear_bwd_workspace_size(dtype, T, d_out, C))
-    return fail(PD_EWORKSPACE, "pd_masked_linear_bwd: workspace too small");
+    return fail(PD_EWORKSPACE, std::string(what) + ": workspace too small");
   hipStream_t s = (hipStream_t)stream;
   size_t es = dtype == PD_DTYPE_BF16 ? 2 : 4;
   char* ws = (char*)workspace;
@@ -200,6 +213,65 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
     if ((rc = pd_gemm(dtype, T, d_in, d_out, gt, d_out, 0, W, d_in, 0, dx, d_in, dtype, 1.f, 1.f, stream))) return rc;
   }
   return PD_OK;
+}
+
+// Scratch of the allocation-free backward: one region per GPU, file scope, held by each
+// device the library runs on until the process ends. Host code reaches its device
+// address only through noalloc_scratch(), never through the symbol itself.
+constexpr size_t NOALLOC_SCRATCH_BYTES = PD_MASKED_LINEAR_BWD_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with that device
+// current) by hipGetSymbolAddress; nullptr (and the error state set) on failure.
+static void* noalloc_scratch(const char* what) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    fail(PD_ELAUNCH, std::string(what) + ": no current HIP device in range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(PD_ELAUNCH, std::string(what) + ": hipGetSymbolAddress(scratch) failed: " + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace pd
+
+extern "C" {
+
+int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
+                         const void* U, const void* W, const void* mask, const void* delta, const uint8_t* route,
+                         const void* xV, const void* acts, const void* g_out, void* dx, void* dV, void* dU,
+                         void* dmask, void* d_delta, void* workspace, size_t workspace_bytes, void* stream) {
+  return masked_linear_bwd_impl("pd_masked_linear_bwd", dtype, T, d_in, d_out, C, x, V, U, W, mask, delta, route, xV,
+                                acts, g_out, dx, dV, dU, dmask, d_delta, workspace, workspace_bytes, stream);
+}
+
+int pd_masked_linear_bwd_noalloc(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x,
+                                 const void* V, const void* U, const void* W, const void* mask, const void* delta,
+                                 const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx,
+                                 void* dV, void* dU, void* dmask, void* d_delta, void* stream) {
+  const char* what = "pd_masked_linear_bwd_noalloc";
+  if (T > 0 && C > 0 && d_out > 0 && pd_masked_linear_bwd_workspace_size(dtype, T, d_out, C) > NOALLOC_SCRATCH_BYTES)
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": needs " +
+                                     std::to_string(pd_masked_linear_bwd_workspace_size(dtype, T, d_out, C)) +
+                                     " scratch bytes (T*C + T*d_out elements + 512), above the fixed " +
+                                     std::to_string(NOALLOC_SCRATCH_BYTES) + "; use pd_masked_linear_bwd");
+  void* ws = noalloc_scratch(what);
+  if (!ws) return PD_ELAUNCH;
+  return masked_linear_bwd_impl(what, dtype, T, d_in, d_out, C, x, V, U, W, mask, delta, route, xV, acts, g_out, dx, dV,
+                                dU, dmask, d_delta, ws, NOALLOC_SCRATCH_BYTES, stream);
 }
 
 
