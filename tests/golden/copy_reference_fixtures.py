@@ -1,0 +1,41 @@
+"""Copies the reference's own frozen test fixtures (data only: inputs and expected
+outputs) into tests/golden/ and records their provenance in MANIFEST.txt. Run in the
+build container, where the reference is mounted read-only at /root/reference:
+
+    python tests/golden/copy_reference_fixtures.py
+
+- equivalence_fixtures.npz + equivalence_torch_reference.json:
+  param_decomp/param_decomp/tests/targets/equivalence/{fixtures.npz,torch_reference.json}
+  (a tiny GLU-MLP suffix with zeroed attention, pre-drawn masks and PPGD sources; the
+  frozen torch-era loss goldens).
+- simple_mlp_tiny_fixture.npz:
+  param_decomp/param_decomp/tests/targets/simple_mlp_equivalence/tiny_fixture.npz
+  (a 3-layer LlamaSimpleMLP state dict, token ids and the torch fp32 logits).
+"""
+
+import hashlib
+import os
+import shutil
+
+REF = "/root/reference/param_decomp/param_decomp/tests/targets"
+HERE = os.path.dirname(os.path.abspath(__file__))
+FILES = [
+    ("equivalence/fixtures.npz", "equivalence_fixtures.npz"),
+    ("equivalence/torch_reference.json", "equivalence_torch_reference.json"),
+    ("simple_mlp_equivalence/tiny_fixture.npz", "simple_mlp_tiny_fixture.npz"),
+]
+
+
+def main() -> None:
+    lines = []
+    for src, dst in FILES:
+        shutil.copyfile(os.path.join(REF, src), os.path.join(HERE, dst))
+        digest = hashlib.sha256(open(os.path.join(HERE, dst), "rb").read()).hexdigest()
+        lines.append(f"{dst}  sha256={digest}  from param_decomp/param_decomp/tests/targets/{src}")
+    with open(os.path.join(HERE, "MANIFEST.txt"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+if __name__ == "__main__":
+    main()

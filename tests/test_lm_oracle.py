@@ -1,0 +1,199 @@
+"""Pins of the LM oracle (oracle/lm_oracle.py) against the reference's own frozen
+goldens, library routines and finite differences (CPU)."""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lm_oracle as lo
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _t(a):
+    return torch.tensor(np.asarray(a, np.float64), dtype=torch.float64)
+
+
+def test_tiny_llama_simple_mlp_logits_match_the_reference_fixture():
+    """The reference's frozen fp32 logits of a 3-layer LlamaSimpleMLP (GQA repeat 2,
+    rotate-half RoPE, GELU-tanh MLP, tied head), held to the reference test's own bound
+    (`pd/tests/targets/simple_mlp_equivalence/test_torch_equivalence.py`: max abs 1e-5)."""
+    f = np.load(os.path.join(GOLDEN, "simple_mlp_tiny_fixture.npz"))
+    c = json.loads(str(f["config_json"]))
+    cfg = lo.LMConfig(n_layers=c["n_layer"], d=c["n_embd"], n_head=c["n_head"], n_kv_head=c["n_key_value_heads"],
+                      d_mlp=c["n_intermediate"], vocab=c["vocab_size"], mlp="plain", eps=c["rms_norm_eps"],
+                      rope_base=c["rotary_base"])
+    assert c["rotary_dim"] == cfg.head_dim and not c["rotary_adjacent_pairs"]
+    w = lambda k: _t(f["weights." + k])  # noqa: E731
+    params = {"head": w("lm_head.weight"), "norm": w("ln_f.weight"), "layers": []}
+    for i in range(cfg.n_layers):
+        params["layers"].append({
+            "ln1": w(f"h.{i}.rms_1.weight"), "ln2": w(f"h.{i}.rms_2.weight"),
+            "W_q_proj": w(f"h.{i}.attn.q_proj.weight"), "W_k_proj": w(f"h.{i}.attn.k_proj.weight"),
+            "W_v_proj": w(f"h.{i}.attn.v_proj.weight"), "W_o_proj": w(f"h.{i}.attn.o_proj.weight"),
+            "W_c_fc": w(f"h.{i}.mlp.c_fc.weight"), "W_down_proj": w(f"h.{i}.mlp.down_proj.weight")})
+    idx = torch.as_tensor(f["idx"])
+    r0 = w("wte.weight")[idx]
+    got = lo.logits(params, lo.forward(cfg, params, r0)).numpy()
+    assert got.shape == f["logits"].shape
+    assert np.abs(got - f["logits"]).max() < 1e-5
+
+
+def _equivalence_model():
+    f = np.load(os.path.join(GOLDEN, "equivalence_fixtures.npz"))
+    s = lambda k: f["_scalar_" + k].item()  # noqa: E731
+    d, di, n_dec, n_tail, C = s("N_EMBD"), s("N_INTERMEDIATE"), s("N_DECOMP_LAYERS"), s("N_TAIL"), s("C")
+    kinds = {"gate": "gate_proj", "up": "up_proj", "down": "down_proj"}
+    cfg = lo.LMConfig(n_layers=n_dec + n_tail, d=d, n_head=2, n_kv_head=1, d_mlp=di, vocab=f["lm_head"].shape[0],
+                      C={k: C for k in kinds.values()}, mlp="glu", eps=s("EPS"))
+    z = lambda r, c: torch.zeros(r, c, dtype=torch.float64)  # noqa: E731 (the fixtures zero every attention projection)
+    hd = d // 2
+    layers = []
+    for i in range(n_dec + n_tail):
+        pre = "" if i < n_dec else "tail_"
+        j = i if i < n_dec else i - n_dec
+        P = {"ln1": _t(f[f"{pre}ln1_{j}"]), "ln2": _t(f[f"{pre}ln2_{j}"]), "W_q_proj": z(2 * hd, d),
+             "W_k_proj": z(hd, d), "W_v_proj": z(hd, d), "W_o_proj": z(d, 2 * hd),
+             "W_gate_proj": _t(f[f"{pre}Wg_{j}"]), "W_up_proj": _t(f[f"{pre}Wu_{j}"]),
+             "W_down_proj": _t(f[f"{pre}Wd_{j}"])}
+        if i < n_dec:
+            for short, kind in kinds.items():
+                P["V_" + kind] = _t(f[f"V{short[0]}_{i}"])
+                P["U_" + kind] = _t(f[f"U{short[0]}_{i}"])
+        layers.append(P)
+    params = {"head": _t(f["lm_head"]), "norm": _t(f["norm"]), "layers": layers}
+    return f, cfg, params, kinds, n_dec
+
+
+def test_ppgd_loss_matches_the_reference_golden():
+    """`pd/tests/targets/equivalence/jax_equivalence.py:160-196`: masks composed from the
+    lower CI and the fixed PPGD sources, `m = ci + (1 - ci) * s[..., :C]`, weight-delta
+    mask `s[..., C]` (broadcast over the batch), every decomposed GLU site masked, then
+    final norm, head and the per-position KL against the frozen forward. The golden is
+    the reference's torch-era value, compared at the reference test's RTOL 2e-4 / ATOL
+    1e-5."""
+    f, cfg, params, kinds, n_dec = _equivalence_model()
+    ref = json.load(open(os.path.join(GOLDEN, "equivalence_torch_reference.json")))
+    r0 = _t(f["resid"])
+    b, t, _ = r0.shape
+    masks, deltas = [], []
+    for i in range(cfg.n_layers):
+        masks.append({})
+        deltas.append({})
+        if i >= n_dec:
+            continue
+        for short, kind in kinds.items():
+            ci = _t(f[f"ci_lower_{short}"][:, :, i])
+            src = _t(np.broadcast_to(f[f"ppgd_source_{short}"][:, :, i], (b, t, cfg.C[kind] + 1)))
+            masks[i][kind] = ci + (1.0 - ci) * src[..., :-1]
+            deltas[i][kind] = src[..., -1]
+    clean = lo.logits(params, lo.forward(cfg, params, r0))
+    masked = lo.logits(params, lo.forward(cfg, params, r0, masks, deltas))
+    ppgd = float(lo.kl_per_position(masked, clean))
+    assert abs(ppgd - ref["ppgd"]) <= 1e-5 + 2e-4 * abs(ref["ppgd"]), (ppgd, ref["ppgd"])
+    # a dropped delta channel or an unbroadcast source would move it far outside the bound
+    no_delta = float(lo.kl_per_position(lo.logits(params, lo.forward(
+        cfg, params, r0, masks, [{k: None for k in m} for m in masks])), clean))
+    assert abs(no_delta - ref["ppgd"]) > 1e-2 * ref["ppgd"]
+
+
+def test_attention_matches_torch_sdpa_with_gqa():
+    """The oracle's causal GQA attention equals torch's scaled_dot_product_attention on
+    the same RoPE-rotated heads."""
+    rng = np.random.default_rng(0)
+    b, t, H, KV, hd = 2, 9, 4, 2, 8
+    q, k, v = (_t(rng.normal(size=(b, t, n * hd))) for n in (H, KV, KV))
+    got = lo.causal_attention(q, k, v, H, KV, 10000.0)
+    cos, sin = lo.rope_cos_sin(t, hd, 10000.0)
+    qh = lo.apply_rope(q.reshape(b, t, H, hd).transpose(1, 2), cos, sin)
+    kh = lo.apply_rope(k.reshape(b, t, KV, hd).transpose(1, 2), cos, sin).repeat_interleave(H // KV, 1)
+    vh = v.reshape(b, t, KV, hd).transpose(1, 2).repeat_interleave(H // KV, 1)
+    want = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
+    np.testing.assert_allclose(got.numpy(), want.transpose(1, 2).reshape(b, t, H * hd).numpy(), rtol=1e-12,
+                               atol=1e-12)
+
+
+def test_rope_is_a_rotation_with_relative_position_scores():
+    # head_dim 2: inv_freq = [1], so position p rotates (x0, x1) by p radians
+    cos, sin = lo.rope_cos_sin(3, 2, 10000.0)
+    x = _t([[[[1.0, 0.0], [1.0, 0.0], [0.0, 1.0]]]])
+    y = lo.apply_rope(x, cos, sin)[0, 0].numpy()
+    np.testing.assert_allclose(y[1], [math.cos(1.0), math.sin(1.0)], atol=1e-15)
+    np.testing.assert_allclose(y[2], [-math.sin(2.0), math.cos(2.0)], atol=1e-15)
+    # scores depend only on the offset between query and key positions
+    rng = np.random.default_rng(1)
+    hd, T = 16, 12
+    q, k = _t(rng.normal(size=(1, 1, 1, hd))), _t(rng.normal(size=(1, 1, 1, hd)))
+    cos, sin = lo.rope_cos_sin(T, hd, 10000.0)
+    qs = lo.apply_rope(q.expand(1, 1, T, hd), cos, sin)[0, 0]
+    ks = lo.apply_rope(k.expand(1, 1, T, hd), cos, sin)[0, 0]
+    s = (qs @ ks.T).numpy()
+    for off in range(-3, 4):
+        diag = np.diagonal(s, offset=off)
+        np.testing.assert_allclose(diag, diag[0], rtol=1e-10)
+
+
+def _small():
+    cfg = lo.LMConfig(n_layers=2, d=16, n_head=4, n_kv_head=4, d_mlp=24, vocab=40,
+                      C={"q_proj": 6, "k_proj": 5, "v_proj": 6, "o_proj": 4, "c_fc": 8, "down_proj": 7})
+    rng = np.random.default_rng(3)
+    params = lo.init_lm(cfg, rng)
+    tokens = rng.integers(0, cfg.vocab, size=(2, 5))
+    ci = lo.init_ci(cfg, 10, rng, 0.05, 0.95)
+    return cfg, params, tokens, ci
+
+
+def test_step_gradients_match_finite_differences():
+    """float64 step: dV, dU and the CI-preactivation gradients against central
+    differences of the loss (CI kept inside (0, 1), where the custom lower VJP is the
+    derivative), with the stochastic masks and the weight-delta channel on."""
+    cfg, params, tokens, ci = _small()
+    key = (7, 11)
+    kw = dict(p=2.0, imp_coeff=0.3, recon_coeff=1.7)
+    base = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)
+    rng = np.random.default_rng(5)
+    eps = 1e-6
+    for l, kind in ((0, "q_proj"), (0, "k_proj"), (1, "o_proj"), (1, "c_fc"), (0, "down_proj")):
+        for name, grad in (("V_", base["dV"][l][kind]), ("U_", base["dU"][l][kind])):
+            arr = params["layers"][l][name + kind]
+            for _ in range(2):
+                i = tuple(int(rng.integers(0, s)) for s in arr.shape)
+                old = arr[i]
+                arr[i] = old + eps
+                up = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)["loss"]
+                arr[i] = old - eps
+                dn = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)["loss"]
+                arr[i] = old
+                assert (up - dn) / (2 * eps) == pytest.approx(grad[i], rel=1e-5, abs=1e-9), (name, kind, l, i)
+    for l, kind in ((0, "v_proj"), (1, "down_proj")):
+        arr = ci[l][kind]
+        for _ in range(3):
+            i = tuple(int(rng.integers(0, s)) for s in arr.shape)
+            old = arr[i]
+            arr[i] = old + eps
+            up = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)["loss"]
+            arr[i] = old - eps
+            dn = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)["loss"]
+            arr[i] = old
+            assert (up - dn) / (2 * eps) == pytest.approx(base["d_ci_pre"][l][kind][i], rel=1e-5, abs=1e-9)
+
+
+def test_full_masks_reproduce_the_clean_forward():
+    """CI = 1 everywhere makes every mask 1: with d = 0 the masked forward must equal
+    the clean one exactly when V@U = W^T (here: an exact rank-C factorization), so the
+    KL is 0 (the decomposition identity)."""
+    cfg = lo.LMConfig(n_layers=1, d=8, n_head=2, n_kv_head=2, d_mlp=8, vocab=11,
+                      C={"q_proj": 8, "c_fc": 8})
+    rng = np.random.default_rng(9)
+    params = lo.init_lm(cfg, rng)
+    for kind in cfg.C:
+        L_ = params["layers"][0]
+        L_["U_" + kind] = np.linalg.solve(L_["V_" + kind], L_["W_" + kind].T)  # V square: V U = W^T
+    tokens = rng.integers(0, cfg.vocab, size=(1, 6))
+    ci = [{k: np.full((6, cfg.C[k]), 1.0) for k in cfg.C}]
+    out = lo.lm_stack_step(cfg, params, tokens, ci, (1, 2), use_delta=False, imp_coeff=0.0)
+    assert abs(out["recon"]) < 1e-12
