@@ -9,6 +9,11 @@ Workloads (synthetic data of the named shapes, random-init weights):
   forward (grouped masked-component matmuls over bucketed tokens, with the frozen delta
   channel of the reference's stochastic masking), MSE recon of the final residual + L_p
   (p=2) imp-min over the selected CI, and the backward to every V/U and CI input.
+- `llama4L`: the 4-layer Llama-style simple-MLP target (d_model 768, 12 heads, d_mlp
+  3072, vocab 50277), every q/k/v/o (C=1024) and c_fc/down (C=4096) matrix decomposed,
+  16 x 512 tokens, bf16. A step is one `pd_lm_stack_step`: frozen forward, masked
+  forward with in-block mask and weight-delta draws, frozen causal attention, streamed
+  KL over the tied head + L_p (p=2) imp-min, and the backward to every V/U and CI input.
 - `dense768x3072_C4096`: one decomposed dense linear 768->3072, x bf16 [4096, 768],
   C=4096, per-component gate MLP hidden 16, bf16 Threefry mask uniforms, stochastic-
   recon MSE + sum_c mean_t |g_upper|^2 fwd+bwd (`pd_dense_step`).
@@ -46,11 +51,18 @@ PPGD_DENSE = "ppgd_dense768x3072_C4096"
 KL_STREAM = "kl_stream_llama4L"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
+LLAMA = "llama4L"
 PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
     # with the frozen delta channel the reference's stochastic masking always draws
     MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4, use_delta=True),
+    # the 4-layer Llama-style simple-MLP target: d_model 768, 12 heads (head_dim 64), d_mlp
+    # 3072, vocab 50277, C = 1024 per attention matrix and 4096 per MLP matrix, 16 x 512
+    # tokens, with the weight-delta channel of stochastic masking; KL over 3 vocab chunks
+    LLAMA: dict(B=16, T=512, d=768, H=12, KV=12, f=3072, V=50277, L=4,
+                C={"q_proj": 1024, "k_proj": 1024, "v_proj": 1024, "o_proj": 1024, "c_fc": 4096,
+                   "down_proj": 4096}, n_chunks=3, use_delta=True),
     CI_MLP: dict(T=4096, dims=(768, 1024, 4096)),
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
@@ -751,6 +763,153 @@ def run_moe(args):
     return res
 
 
+# ============================================================== Llama-style LM stack
+def lm_site_dims(cfg):
+    qd, kvd = cfg["H"] * 64, cfg["KV"] * 64
+    d, f = cfg["d"], cfg["f"]
+    return {"q_proj": (d, qd), "k_proj": (d, kvd), "v_proj": (d, kvd), "o_proj": (qd, d), "c_fc": (d, f),
+            "down_proj": (f, d)}
+
+
+def lm_gemm_flops(cfg):
+    """Per-category FLOPs of one step by the reference's linear rule
+    (`pd/core/flops/target.py:39-93`, frozen paths included with the weight-delta channel):
+    forward in + out (+ frozen); backward in * (input grad + component grad) + out * 2
+    (+ frozen for the input gradient). Layer 0's q/k/v read the embedding: no input
+    gradient there. Attention is a frozen product pair, full T x T per head, forward and
+    backward."""
+    N = cfg["B"] * cfg["T"]
+    fwd = dx = dw = 0
+    frozen_on = cfg.get("use_delta", True)
+    for layer in range(cfg["L"]):
+        for k, (din, dout) in lm_site_dims(cfg).items():
+            C = cfg["C"][k]
+            i, o, fr = 2 * N * din * C, 2 * N * C * dout, 2 * N * din * dout * frozen_on
+            ig = not (layer == 0 and k in ("q_proj", "k_proj", "v_proj"))
+            fwd += i + o + fr
+            dx += o + (i + fr) * ig
+            dw += i + o
+    attn_one = 2 * cfg["B"] * cfg["H"] * cfg["T"] * cfg["T"] * 64  # one T x T x 64 product over all heads
+    clean = sum(2 * N * din * dout for din, dout in lm_site_dims(cfg).values()) * cfg["L"] + 2 * attn_one * cfg["L"]
+    kl = 2 * N * cfg["d"] * cfg["V"] * 5  # fwd: clean + masked logits; bwd: both again + the input gradient
+    return {"gemm_fwd": fwd, "gemm_dx": dx, "gemm_dw": dw, "attention": 6 * attn_one * cfg["L"], "clean": clean,
+            "kl": kl}
+
+
+def lm_cpu_baseline(cfg, n_sample, reps=3):
+    """The LM oracle's step in fp32 (torch on the host cores) on `n_sample` tokens of one
+    sequence at the workload's full widths."""
+    import numpy as np
+    import torch
+
+    from oracle import lm_oracle as lo
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    torch.set_num_threads(cores)
+    lc = lo.LMConfig(n_layers=cfg["L"], d=cfg["d"], n_head=cfg["H"], n_kv_head=cfg["KV"], d_mlp=cfg["f"],
+                     vocab=cfg["V"], C=dict(cfg["C"]))
+    rng = np.random.default_rng(0)
+    params = lo.init_lm(lc, rng)
+    tokens = rng.integers(0, lc.vocab, size=(1, n_sample))
+    ci = lo.init_ci(lc, n_sample, rng)
+    run = lambda: lo.lm_stack_step(lc, params, tokens, ci, (0, 1), use_delta=cfg["use_delta"], dtype=torch.float32)
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": n_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one sequence of {n_sample} tokens at the full widths (4 layers, vocab 50277), the oracle's "
+                      f"torch fp32 CPU restatement of the same step (autograd backward), median of {reps} after 1 "
+                      f"warmup; {med * 1e3:.0f} ms per sample step"}
+
+
+def run_llama(args):
+    import torch
+
+    from param_decomp_amd import hip_events, prng
+    from param_decomp_amd.lm_step import CATEGORIES, KINDS, LMStackStep, LMWeights
+
+    cfg = WORKLOADS[LLAMA]
+    B, T, d, H, KV, f, V, Ln = (cfg[x] for x in ("B", "T", "d", "H", "KV", "f", "V", "L"))
+    C = cfg["C"]
+    N = B * T
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, scale):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(torch.bfloat16)
+
+    dims = lm_site_dims(cfg)
+    # target N(0, d_in^-1/2); components V by d_in^-1/2, U by C^-1/2 (pd/core/components.py:650-677)
+    w = LMWeights(wte=rn(V, d, scale=d**-0.5), ln1=torch.ones(Ln, d, device=dev), ln2=torch.ones(Ln, d, device=dev),
+                  norm=torch.ones(d, device=dev),
+                  W={k: rn(Ln, dims[k][1], dims[k][0], scale=dims[k][0]**-0.5) for k in KINDS},
+                  V={k: rn(Ln, dims[k][0], C[k], scale=dims[k][0]**-0.5) for k in KINDS},
+                  U={k: rn(Ln, C[k], dims[k][1], scale=C[k]**-0.5) for k in KINDS})
+    ci = {k: (torch.rand(Ln, N, C[k], device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16) for k in KINDS}
+    tok = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+    step = LMStackStep(B, T, d, H, KV, f, V, Ln, C, device=dev, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
+                       use_delta=cfg["use_delta"], n_kl_chunks=cfg["n_chunks"])
+    for i in range(args.warmup):
+        step.step(tok, w, ci, prng.fold_in((0, 0), i))
+    cap = 2048
+    evs = [hip_events.create(cap) for _ in range(args.steps)]
+    arrs = [hip_events.array(e) for e in evs]
+    cats = [torch.zeros(cap, dtype=torch.int32) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    counts = []
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        counts.append(step.step_timed(tok, w, ci, prng.fold_in((0, 0), args.warmup + i), arrs[i], cats[i]))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms_per_step = hip_events.elapsed_ms(start, stop) / args.steps
+    cat_ms = {name: 0.0 for name in CATEGORIES}
+    cat_n = {name: 0 for name in CATEGORIES}
+    for e, cc, n in zip(evs, cats, counts):
+        for j in range(n - 1):
+            name = CATEGORIES[int(cc[j])]
+            cat_ms[name] += hip_events.elapsed_ms(e[j], e[j + 1]) / args.steps
+            cat_n[name] += 1
+        hip_events.destroy(e)
+    for name in cat_n:
+        cat_n[name] //= args.steps
+    assert torch.isfinite(step.losses).all(), step.losses
+    gf = lm_gemm_flops(cfg)
+    sumC = sum(C[k] for k in KINDS) * Ln
+    work = {
+        "gemm_fwd": ("flop", gf["gemm_fwd"]),
+        "gemm_dx": ("flop", gf["gemm_dx"]),
+        "gemm_dw": ("flop", gf["gemm_dw"]),
+        "mask_fwd": ("byte", N * sumC * (2 + 2 + 2 + 1)),   # read ci, xV; write acts, u bits
+        "mask_bwd": ("byte", N * sumC * (2 + 2 + 1 + 2 + 2)),  # read ci, xV, u, d_acts; write d_xV, d_ci
+    }
+    dom = max((n for n in cat_ms if n in work), key=cat_ms.get)
+    kind, amount = work[dom]
+    launches = cat_n[dom]
+    roof = roofline(kind, amount / launches, cat_ms[dom] / launches, dom, launches, pmc_traffic(LLAMA, dom))
+    res = {
+        "tokens": N, "ms_per_step": ms_per_step,
+        "config": {"workload": LLAMA, "batch": B, "seq_len": T, "d_model": d, "heads": H, "kv_heads": KV,
+                   "d_mlp": f, "vocab": V, "layers": Ln, "C": dict(C), "imp_min": "p=2",
+                   "recon": "kl(clean || masked), streamed over 3 vocab chunks", "mask_draw":
+                   "threefry bf16 (partitionable)", "delta_channel": cfg["use_delta"], "attention": "frozen, causal"},
+        "step_flops": sum(gf.values()), "phases_ms": cat_ms, "launches_per_step": cat_n, "roofline": roof,
+        "reference_rule_flops": gf["gemm_fwd"] + gf["gemm_dx"] + gf["gemm_dw"],
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = lm_cpu_baseline(cfg, args.cpu_tokens)
+    return res
+
+
 def main():
     if "--rocprof-summary" in sys.argv:
         i = sys.argv.index("--rocprof-summary")
@@ -770,9 +929,11 @@ def main():
         sys.exit(2)
     if args.cpu_tokens is None:
         args.cpu_tokens = {MOE: 2048, DENSE: 4096, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
-                           KL_STREAM: 64}.get(args.workload, 0)
+                           KL_STREAM: 64, LLAMA: 128}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
+    elif args.workload == LLAMA:
+        res = run_llama(args)
     elif args.workload == DENSE:
         res = run_dense(args)
     elif args.workload in (FAITH_DENSE, FAITH_MOE):
@@ -806,6 +967,8 @@ def main():
     }
     if "launches_per_step" in res:
         out["launches_per_step"] = res["launches_per_step"]
+    if "reference_rule_flops" in res:
+        out["reference_rule_tflops"] = res["reference_rule_flops"] / (ms * 1e-3) / 1e12
     if "cpu_baseline" in res:
         out["cpu_baseline"] = res["cpu_baseline"]
     print(json.dumps(out))

@@ -341,6 +341,47 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
                             void* workspace, size_t workspace_bytes, void* stream, void** events,
                             int32_t* categories, int capacity, int* n_recorded);
 
+/* ---- the decomposed Llama-style LM step (one stochastic-recon KL step, fwd + bwd) -----
+ * The pre-RMSNorm transformer of pd/targets/transformer.py:1031-1140 in its
+ * LlamaSimpleMLP form (pd/targets/llama_simple_mlp.py: rotate-half RoPE, causal GQA
+ * attention, GELU-tanh MLP c_fc -> down_proj, tied embedding/head, no biases), with every
+ * one of the six matrices per layer (KIND_ORDER q_proj, k_proj, v_proj, o_proj, c_fc,
+ * down_proj = kinds 0..5) decomposed: site = ((x@V) * (m - d)) @ U + d * (x @ W^T)
+ * (pd/core/decomposed_linear.py:142-175). Masks are drawn in-block per (kind, layer):
+ * m = lower(ci) + (1 - lower(ci)) uniform(fold_in(fold_in(split(draw_key)[0], kind),
+ * layer), [N, C]) and d = uniform(fold_in(fold_in(split(draw_key)[1], kind), layer), [N])
+ * in bf16 (pd/targets/transformer.py:1048-1058, 1424-1451); use_delta = 0 is d = 0.
+ * Loss: recon_coeff * mean KL(softmax(clean logits) || softmax(masked logits)) (the
+ * streamed form, pd/targets/losses.py:102-163, over n_kl_chunks vocab chunks) + imp_coeff *
+ * sum_sites sum_c mean_tokens upper(ci)^p.
+ * Shapes: N = B*T tokens (int32 ids [N], T % 64 == 0); head_dim 64 (d = 64 n_head);
+ * n_head % n_kv_head == 0; d, d_mlp % 64 == 0; C[6] each % 8 == 0; vocab % n_kl_chunks == 0.
+ * wte [vocab, d] bf16 (embedding and head); ln1, ln2 [L, d], norm [d] fp32 (values the
+ * bf16 weights hold); per kind k: W[k] [L, d_out, d_in], V[k] [L, d_in, C_k], U[k]
+ * [L, C_k, d_out] bf16; ci_pre[k] [L, N, C_k] bf16. Outputs: losses [3] = (total, kl,
+ * imp) fp32; dV[k], dU[k] fp32 in V/U's layouts; d_ci_pre[k] bf16 in ci_pre's layout. */
+size_t pd_lm_stack_workspace_size(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab,
+                                  int L, const int32_t* C, int use_delta, int n_kl_chunks);
+int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                     const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
+                     const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
+                     const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
+                     int use_delta, int layout, float p, float imp_coeff, float recon_coeff, int n_kl_chunks,
+                     float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
+                     size_t workspace_bytes, void* stream);
+/* pd_lm_stack_step recording HIP events at phase boundaries (categories: 0 per-step weight
+ * copies and delta draws, 1 frozen forward, 2 site products fwd, 3 mask fwd, 4 attention,
+ * 5 norms / adds / GELU / transposes, 6 streamed KL, 7 d_acts and d_input products, 8 dU
+ * and dV products, 9 mask bwd, 10 end). */
+int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                           const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
+                           const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
+                           const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
+                           uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff, float recon_coeff,
+                           int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                           void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
+                           void** events, int32_t* categories, int capacity, int* n_recorded);
+
 /* ---- the engine's CI functions ------------------------------------------------------
  * SiteMLP (pd/core/ci_fn/implementations/mlp.py:57-78) of n_layers linears, as
  * LayerwiseMLPCIFn.site_preactivations runs it per site

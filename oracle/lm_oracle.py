@@ -102,8 +102,18 @@ class _RoundBF16(torch.autograd.Function):
         return _round_t(g)
 
 
+class _Rounder:
+    """The storage model: bf16 rounding (value and cotangent) or the identity."""
+
+    def __init__(self, bf16: bool):
+        self.bf16 = bf16
+
+    def __call__(self, t):
+        return _RoundBF16.apply(t) if self.bf16 else t
+
+
 def _rounder(bf16_storage: bool):
-    return _RoundBF16.apply if bf16_storage else (lambda t: t)
+    return _Rounder(bf16_storage)
 
 
 # ---------------------------------------------------------------- squashing with the reference VJPs
@@ -118,7 +128,7 @@ class _LowerLeaky(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         (x,) = ctx.saved_tensors
-        return torch.from_numpy(po.lower_leaky_vjp(x.numpy(), g.numpy()))
+        return torch.from_numpy(np.asarray(po.lower_leaky_vjp(x.numpy(), g.numpy()))).to(x.dtype)
 
 
 class _UpperLeaky(torch.autograd.Function):
@@ -127,18 +137,19 @@ class _UpperLeaky(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x):
         ctx.save_for_backward(x)
-        return torch.from_numpy(po.upper_leaky(x.numpy()))
+        return torch.from_numpy(np.asarray(po.upper_leaky(x.numpy()))).to(x.dtype)
 
     @staticmethod
     def backward(ctx, g):
         (x,) = ctx.saved_tensors
-        return torch.from_numpy(po.upper_leaky_vjp(x.numpy(), g.numpy()))
+        return torch.from_numpy(np.asarray(po.upper_leaky_vjp(x.numpy(), g.numpy()))).to(x.dtype)
 
 
 # ---------------------------------------------------------------- target pieces
-def rms_norm(x, w, eps):
-    """`pd/target_ports/llama.py:90-97`: `w * (x * rsqrt(mean(x^2) + eps))`."""
-    return w * (x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps))
+def rms_norm(x, w, eps, rb=lambda t: t):
+    """`pd/target_ports/llama.py:90-97`: `w * (x * rsqrt(mean(x^2) + eps))`, the normalized
+    value cast to the activation dtype before the weight multiply (`rb`)."""
+    return w * rb(x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps))
 
 
 def rope_cos_sin(T: int, head_dim: int, base: float):
@@ -160,6 +171,32 @@ def apply_rope(x, cos, sin):
     return x * cos + rotate_half(x) * sin
 
 
+class _CausalCore(torch.autograd.Function):
+    """softmax(q k^T * scale, causal) v on head-major [b, H, t, hd] operands, with the
+    backward spelled out: dP = dO V^T, dS = P (dP - rowsum(P dP)) scale, dQ = dS K,
+    dK = dS^T Q, dV = P^T dO. `bf16` rounds P, dS, dQ, dK and dV (the tensors a fused bf16
+    attention stores) and nothing else."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bf16):
+        t, hd = q.shape[-2], q.shape[-1]
+        rb = _round_t if bf16 else (lambda x: x)
+        s = (q @ k.transpose(-1, -2)) * hd**-0.5
+        causal = torch.ones(t, t, dtype=torch.bool).tril()
+        p = rb(torch.softmax(s.masked_fill(~causal, float("-inf")), dim=-1))
+        ctx.save_for_backward(q, k, v, p)
+        ctx.bf16 = bf16
+        return p @ v
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, p = ctx.saved_tensors
+        rb = _round_t if ctx.bf16 else (lambda x: x)
+        dp = do @ v.transpose(-1, -2)
+        ds = rb(p * (dp - (p * dp).sum(-1, keepdim=True)) * q.shape[-1] ** -0.5)
+        return rb(ds @ k), rb(ds.transpose(-1, -2) @ q), rb(p.transpose(-1, -2) @ do), None
+
+
 def causal_attention(q, k, v, n_head: int, n_kv_head: int, base: float, rb=lambda t: t):
     """q [b, t, H*hd], k/v [b, t, KV*hd] -> [b, t, H*hd]: RoPE on q and k, then causal
     softmax(q k^T / sqrt(hd)) v with each kv head serving H/KV query heads."""
@@ -170,14 +207,11 @@ def causal_attention(q, k, v, n_head: int, n_kv_head: int, base: float, rb=lambd
     kh = k.reshape(b, t, n_kv_head, hd).transpose(1, 2)
     vh = v.reshape(b, t, n_kv_head, hd).transpose(1, 2)
     cos, sin = rope_cos_sin(t, hd, base)
+    cos, sin = rb(cos.to(q.dtype)), rb(sin.to(q.dtype))  # the tables are cast to the activation dtype
     qh, kh = rb(apply_rope(qh, cos, sin)), rb(apply_rope(kh, cos, sin))
     kh = kh.repeat_interleave(rep, dim=1)
     vh = vh.repeat_interleave(rep, dim=1)
-    s = (qh @ kh.transpose(-1, -2)) * hd**-0.5
-    causal = torch.ones(t, t, dtype=torch.bool).tril()
-    s = s.masked_fill(~causal, float("-inf"))
-    p = rb(torch.softmax(s, dim=-1))
-    o = p @ vh
+    o = _CausalCore.apply(qh, kh, vh, bool(getattr(rb, "bf16", False)))
     return o.transpose(1, 2).reshape(b, t, qd)
 
 
@@ -194,10 +228,10 @@ def site(x, W, V=None, U=None, mask=None, delta=None, rb=lambda t: t):
     xV = rb(x @ V)
     coef = mask if delta is None else mask - delta[..., None]
     acts = rb(xV * coef)
-    out = rb(acts @ U)
-    if delta is not None:
-        out = rb(out + delta[..., None] * rb(x @ W.T))
-    return out
+    if delta is None:
+        return rb(acts @ U)
+    # d * (x @ W^T) = (d * x) @ W^T per row: one accumulation with acts @ U, d * x stored bf16
+    return rb(acts @ U + rb(delta[..., None] * x) @ W.T)
 
 
 def block(cfg: LMConfig, P: dict, r, masks=None, deltas=None, rb=lambda t: t, layer=0):
@@ -212,11 +246,11 @@ def block(cfg: LMConfig, P: dict, r, masks=None, deltas=None, rb=lambda t: t, la
             return site(x, P["W_" + kind], P["V_" + kind], P["U_" + kind], masks[kind], deltas.get(kind), rb=rb)
         return site(x, P["W_" + kind], rb=rb)
 
-    h = rb(rms_norm(r, P["ln1"], cfg.eps))
+    h = rb(rms_norm(r, P["ln1"], cfg.eps, rb))
     q, k, v = run("q_proj", h), run("k_proj", h), run("v_proj", h)
     a = rb(causal_attention(q, k, v, cfg.n_head, cfg.n_kv_head, cfg.rope_base, rb=rb))
     r = rb(r + run("o_proj", a))
-    h2 = rb(rms_norm(r, P["ln2"], cfg.eps))
+    h2 = rb(rms_norm(r, P["ln2"], cfg.eps, rb))
     if cfg.mlp == "plain":
         down_in = rb(gelu_tanh(run("c_fc", h2)))
     else:
@@ -225,7 +259,7 @@ def block(cfg: LMConfig, P: dict, r, masks=None, deltas=None, rb=lambda t: t, la
 
 
 def final_act(cfg: LMConfig, params: dict, r, rb=lambda t: t):
-    return rb(rms_norm(r, params["norm"], cfg.eps))
+    return rb(rms_norm(r, params["norm"], cfg.eps, rb))
 
 
 def forward(cfg: LMConfig, params: dict, r0, masks=None, deltas=None, rb=lambda t: t):
@@ -259,18 +293,20 @@ def site_keys(draw_key, cfg: LMConfig, kind: str, layer: int, partitionable=True
 
 
 def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None):
+                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64):
     """One stochastic-recon KL + L_p imp-min step, forward and backward.
 
     params: wte [V, d] (the embedding and the tied head), norm [d], layers: list of
     dicts (ln1, ln2, W_<kind> [d_out, d_in], V_<kind> [d_in, C], U_<kind> [C, d_out])
     as float64 numpy arrays; tokens [b, t] int; ci_pre[l][kind] [b*t, C_kind].
     `uniforms[l][kind] = (u [b*t, C], d [b*t])` replaces the Threefry draws when given.
+    `dtype` torch.float32 runs the same arithmetic in fp32 (the CPU baseline's timing
+    form; the float64 default is the checker).
     Returns dict(loss, recon, imp, dV[l][kind], dU[l][kind], d_ci_pre[l][kind], u, delta)."""
     rb = _rounder(bf16_storage)
     b, t = tokens.shape
     N = b * t
-    T = lambda a, g=False: torch.tensor(np.asarray(a, np.float64), dtype=F64, requires_grad=g)  # noqa: E731
+    T = lambda a, g=False: torch.tensor(np.asarray(a, np.float64), dtype=dtype, requires_grad=g)  # noqa: E731
     prm = {"head": T(params["wte"]), "norm": T(params["norm"]), "layers": []}
     leaves = []
     for l, L_ in enumerate(params["layers"]):
@@ -286,7 +322,7 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
         act_c = forward(cfg, prm, r0, rb=rb)
         clean_logits = logits(prm, act_c)
     masks, deltas, pres, us, ds = [], [], {}, {}, {}
-    imp = torch.zeros((), dtype=F64)
+    imp = torch.zeros((), dtype=dtype)
     for l in range(cfg.n_layers):
         masks.append({})
         deltas.append({})

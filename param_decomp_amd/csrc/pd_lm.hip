@@ -1,0 +1,1088 @@
+// The decomposed Llama-style LM step (gfx950): L pre-RMSNorm transformer blocks
+//   h = rms_norm(r, ln1)                        pd/target_ports/llama.py:90-97
+//   q, k, v = site(h); a = causal_attention(rope(q), rope(k), v)
+//                                               pd/targets/transformer.py:701-747, 1085-1100
+//   r1 = r + site_o(a); h2 = rms_norm(r1, ln2)
+//   r2 = r1 + site_down(gelu_tanh(site_fc(h2))) pd/targets/transformer.py:1101-1140, 802-805
+// with every q/k/v/o/c_fc/down matrix decomposed (site = ((x@V) * (m - d)) @ U + d * (x @ W^T),
+// pd/core/decomposed_linear.py:142-175), stochastic masks drawn in-block per (kind, layer)
+// (pd/targets/transformer.py:1048-1058, 1424-1451), the final norm and the tied head, the
+// streamed per-position KL against the frozen forward (pd/targets/losses.py:102-163), the
+// L_p imp-min over the upper CI, and the full backward to every site's V/U and CI
+// preactivations (the attention is frozen: gradients flow through it).
+//
+// Layouts: activations row-major [N = B*T, width] bf16. Every product runs on the
+// buffer-fed MFMA kernel with both operands K-contiguous:
+//   x @ V            B^T = V^T [C, d_in]                     (per-step transposed copy)
+//   out              [acts | d*x] @ [U ; W^T]: one product over K = C + d_in, its B^T =
+//                    [U^T | W] [d_out, C + d_in] (per-step copy); the weight-delta blend
+//                    d * (x @ W^T) rides in the same accumulation
+//   d_acts           g @ U^T: B^T = U as stored
+//   dU = acts^T g    A = acts^T [C, N] (written by the mask pass), B^T = g^T [d_out, N]
+//   dV = x^T dxV     A = x^T [d_in, N], B^T = dxV^T [C, N] (written by the mask pass)
+//   d_input          [dxV | d*g] @ [V^T ; W]: B^T = [V | W^T] [d_in, C + d_out]
+// Attention is materialized per (batch, head) at hd = 64: S = Q K^T (fp32), causal softmax
+// to bf16 P, O = P V; the backward forms dP, dS = P (dP - rowsum(P dP)) / sqrt(hd), dQ = dS K,
+// dK = dS^T Q, dV = P^T dO. It is about 1% of the step's work at the benchmark shape.
+#include <algorithm>
+#include <vector>
+
+#include "pd_common.hpp"
+#include "pd_tiles.hpp"
+
+namespace pd {
+
+enum { LK_Q = 0, LK_K = 1, LK_V = 2, LK_O = 3, LK_FC = 4, LK_DOWN = 5, LM_NK = 6 };  // KIND_ORDER indices
+static constexpr int LM_HD = 64;
+
+// ---------------------------------------------------------------- token-space kernels
+// r[n, :] = wte[tok[n], :] (ids clamped into [0, V)); one wave per token, d % 8 == 0.
+__global__ __launch_bounds__(256) void k_lm_embed(const int32_t* __restrict__ tok, const bf16_t* __restrict__ wte,
+                                                  int64_t N, int d, int64_t V, bf16_t* __restrict__ r) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + wave_id();
+  if (n >= N) return;
+  int64_t t = tok[n];
+  t = t < 0 ? 0 : (t >= V ? V - 1 : t);
+  for (int i = (threadIdx.x & 63) * 8; i < d; i += 512) *(uint4*)(r + n * d + i) = *(const uint4*)(wte + t * d + i);
+}
+
+// y = bf16(w * bf16(x * rinv)), rinv = rsqrt(mean x^2 + eps) kept for the backward
+// (the reference rounds the normalized value to the activation dtype before the weight
+// multiply). One wave per token.
+__global__ __launch_bounds__(256) void k_lm_rms_fwd(const bf16_t* __restrict__ x, int64_t N, int d,
+                                                    const float* __restrict__ w, float eps, bf16_t* __restrict__ y,
+                                                    float* __restrict__ rinv) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + wave_id();
+  if (n >= N) return;
+  const int lane = threadIdx.x & 63;
+  const bf16_t* xr = x + n * d;
+  float ss = 0.f, v[8];
+  for (int i = lane * 8; i < d; i += 512) {
+    load8(xr + i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+  }
+  const float r = rsqrtf(wave_sum(ss) / (float)d + eps);
+  if (rinv && lane == 0) rinv[n] = r;
+  for (int i = lane * 8; i < d; i += 512) {
+    float g[8];
+    load8(xr + i, v);
+    load8f(w + i, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = g[j] * bf16_to_f32(f32_to_bf16(v[j] * r));
+    store8(y + n * d + i, v);
+  }
+}
+
+// RMSNorm pullback added into the residual cotangent:
+//   d_out[n,:] = bf16(d_in[n,:] + rinv * (w dy) - x * rinv^3 * mean((w dy) x))
+// with dy fp32 (the straight-through derivative of the bf16 rounding of x * rinv).
+// d_in NULL = 0. One wave per token.
+__global__ __launch_bounds__(256) void k_lm_rms_bwd(const float* __restrict__ dy, const bf16_t* __restrict__ x,
+                                                    const float* __restrict__ rinv, const float* __restrict__ w,
+                                                    int64_t N, int d, const bf16_t* __restrict__ d_in,
+                                                    bf16_t* __restrict__ d_out) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + wave_id();
+  if (n >= N) return;
+  const int lane = threadIdx.x & 63;
+  const float r = rinv[n];
+  float dot = 0.f, xv[8], gv[8], wv[8];
+  for (int i = lane * 8; i < d; i += 512) {
+    load8(x + n * d + i, xv);
+    load8f(dy + n * d + i, gv);
+    load8f(w + i, wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dot = fmaf(wv[j] * gv[j], xv[j], dot);
+  }
+  const float c = wave_sum(dot) / (float)d * r * r * r;
+  for (int i = lane * 8; i < d; i += 512) {
+    float o[8], di[8];
+    load8(x + n * d + i, xv);
+    load8f(dy + n * d + i, gv);
+    load8f(w + i, wv);
+    if (d_in) load8(d_in + n * d + i, di);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (d_in ? di[j] : 0.f) + r * wv[j] * gv[j] - xv[j] * c;
+    store8(d_out + n * d + i, o);
+  }
+}
+
+// out = bf16(a + b), 8 elements per thread (n % 8 == 0).
+__global__ __launch_bounds__(256) void k_lm_add(const bf16_t* __restrict__ a, const bf16_t* __restrict__ b, int64_t n,
+                                                bf16_t* __restrict__ out) {
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (int64_t)gridDim.x * 256 * 8) {
+    float x[8], y[8];
+    load8(a + i, x);
+    load8(b + i, y);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] += y[j];
+    store8(out + i, x);
+  }
+}
+
+// dst[c * ld + r] = src[r * Cc + c] (src [R, Cc]; R, Cc, ld multiples of 8, dst 16-byte
+// aligned): 64x64 tiles through a transposed LDS tile.
+__global__ __launch_bounds__(256) void k_lm_transpose(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
+                                                      bf16_t* __restrict__ dst, int64_t ld) {
+  __shared__ TTile Tt;
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const int tid = threadIdx.x, c8 = (tid & 7) * 8;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int r = (tid >> 3) + 32 * pass;
+    uint4 v = {0, 0, 0, 0};
+    if (r0 + r < R && c0 + c8 < Cc) v = *(const uint4*)(src + (r0 + r) * Cc + c0 + c8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Tt.v[c8 + 2 * e][r] = (bf16_t)(w[e] & 0xFFFFu);
+      Tt.v[c8 + 2 * e + 1][r] = (bf16_t)(w[e] >> 16);
+    }
+  }
+  __syncthreads();
+  ttile_store(Tt, dst, ld, r0, R, c0, Cc, tid);
+}
+
+// dst[r * ld + c] = s[r] * src[r * w + c] (s NULL: a plain copy) for r < R, c < w; w % 8
+// == 0, ld % 8 == 0. One wave per row.
+__global__ __launch_bounds__(256) void k_lm_copy_rows(const bf16_t* __restrict__ src, int64_t R, int w,
+                                                      const float* __restrict__ s, bf16_t* __restrict__ dst,
+                                                      int64_t ld) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave_id();
+  if (r >= R) return;
+  const float sc = s ? s[r] : 1.f;
+  for (int i = (threadIdx.x & 63) * 8; i < w; i += 512) {
+    if (s) {
+      float v[8];
+      load8(src + r * w + i, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] *= sc;
+      store8(dst + r * ld + i, v);
+    } else {
+      *(uint4*)(dst + r * ld + i) = *(const uint4*)(src + r * w + i);
+    }
+  }
+}
+
+// Per-token delta draws of every (layer, kind): delta[(l * 6 + k) * N + n] =
+// uniform_bf16(fold_in(fold_in(delta_base, k), l), [N])[n] (pd/core/masking.py:139-140
+// under the keys of pd/targets/transformer.py:1424-1451). Grid (cdiv(N, 256), 6L).
+__global__ __launch_bounds__(256) void k_lm_deltas(uint32_t b0, uint32_t b1, int64_t N, int layout,
+                                                   float* __restrict__ delta) {
+  const int site = blockIdx.y;
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  uint32_t x0 = 0, x1 = (uint32_t)(site % LM_NK);
+  threefry2x32(b0, b1, x0, x1);
+  uint32_t k0 = 0, k1 = (uint32_t)(site / LM_NK);
+  threefry2x32(x0, x1, k0, k1);
+  delta[(int64_t)site * N + n] = draw_uniform(k0, k1, n, N, PD_DTYPE_BF16, layout);
+}
+
+// ---------------------------------------------------------------- site mask passes (64x64 tiles)
+struct LMMaskArgs {
+  const bf16_t* ci_pre;  // [N, C] bf16
+  int64_t N;
+  int C;
+  uint32_t k0, k1;
+  float p;
+  const float* delta;  // [N] or NULL (d = 0)
+  int64_t ld;          // row stride of acts / d_xV (the concatenated operand)
+};
+
+#define PD_LM_ROW(pass) ((threadIdx.x >> 4) + 16 * (pass))
+#define PD_LM_COL ((threadIdx.x & 15) * 4)
+
+// m = lower(ci) + (1 - lower(ci)) u (u drawn in bf16 over [N, C], counter n*C + c);
+// acts = bf16(xV * (m - d)) into acts[n * ld + c] and acts^T [C, N]; u kept as its 7-bit
+// integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0.
+template <int LAYOUT, int PM>
+__global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
+                                                     bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
+                                                     uint8_t* __restrict__ ubits, float* __restrict__ imp_part) {
+  __shared__ TTile Tt;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE, q4 = PD_LM_COL;
+  const int64_t total = a.N * a.C;
+  const bool qok = q0 + q4 < a.C;
+  float imp = 0.f;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_LM_ROW(pass);
+    const int64_t n = n0 + r;
+    bf16_t o[4] = {0, 0, 0, 0};
+    if (n < a.N && qok) {
+      const int64_t idx = n * a.C + q0 + q4;
+      const float dt = a.delta ? a.delta[n] : 0.f;
+      const uint2 pw = *(const uint2*)(a.ci_pre + idx);
+      const uint2 hw = *(const uint2*)(xV + idx);
+      const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
+      const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
+      uint32_t ub = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lower_fwd(pre[e]);
+        imp += powp<PM>(upper_fwd(pre[e]), a.p);
+        const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
+        ub |= kb << (8 * e);
+        const float u = (float)kb * (1.f / 128.f);
+        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt));
+      }
+      *(uint32_t*)(ubits + idx) = ub;
+      *(uint2*)(acts + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
+  }
+  imp = wave_sum(imp);
+  if ((tid & 63) == 0) red[tid >> 6] = imp;
+  __syncthreads();
+  if (tid == 0) imp_part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  ttile_store(Tt, actsT, a.N, n0, a.N, q0, a.C, tid);
+}
+
+// d_xV = bf16(d_acts * (m - d)) into d_xV[n * ld + c] and d_xV^T [C, N]; the CI pullback
+// d_pre = lower_vjp(pre, d_acts * xV * (1 - u)) + upper_vjp(pre, imp_scale * d upper^p).
+template <int PM>
+__global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
+                                                     const uint8_t* __restrict__ ubits, float imp_scale,
+                                                     const bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_xV,
+                                                     bf16_t* __restrict__ d_xVT, bf16_t* __restrict__ d_pre) {
+  __shared__ TTile Tt;
+  const int tid = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.y * TILE;
+  const int q0 = blockIdx.x * TILE, q4 = PD_LM_COL;
+  const bool qok = q0 + q4 < a.C;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int r = PD_LM_ROW(pass);
+    const int64_t n = n0 + r;
+    bf16_t o[4] = {0, 0, 0, 0};
+    if (n < a.N && qok) {
+      const int64_t idx = n * a.C + q0 + q4;
+      const float dt = a.delta ? a.delta[n] : 0.f;
+      const uint2 pw = *(const uint2*)(a.ci_pre + idx);
+      const uint2 hw = *(const uint2*)(xV + idx);
+      const uint2 dw = *(const uint2*)(d_acts + idx);
+      const uint32_t ub = *(const uint32_t*)(ubits + idx);
+      const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
+      const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
+      const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
+      bf16_t dp[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
+        const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
+        const float m = lo + (1.f - lo) * u - dt;
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
+                            upper_vjp(pre[e], imp_scale * dpowp<PM>(up, a.p)));
+        o[e] = f32_to_bf16(da[e] * m);
+      }
+      *(uint2*)(d_pre + idx) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
+      *(uint2*)(d_xV + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
+  }
+  __syncthreads();
+  ttile_store(Tt, d_xVT, a.N, n0, a.N, q0, a.C, tid);
+}
+
+// ---------------------------------------------------------------- attention (hd = 64)
+// RoPE angle table value for position t and pair c: cos/sin of t * base^(-2c/64), computed
+// in fp32 and rounded to bf16 as the reference's tables are (pd/target_ports/llama.py:100-105).
+__device__ inline void rope_cs(int64_t t, int c, float log2_base, float& cs, float& sn) {
+  const float inv = exp2f(-(float)(2 * c) / (float)LM_HD * log2_base);
+  float sv, cv;
+  sincosf((float)t * inv, &sv, &cv);
+  cs = bf16_to_f32(f32_to_bf16(cv));
+  sn = bf16_to_f32(f32_to_bf16(sv));
+}
+
+// Head-major copies of one (batch, head, 64-token) tile: Qh, Kh, Vh [B*H, T, 64] (q and k
+// rotated; a kv head serves H/KV query heads, so its k and v are repeated), and the
+// transposed Kh^T, Vh^T [B*H, 64, T] for the products that contract over tokens.
+// Grid (T/64, H, B); thread = (token tid / 4, pairs 8 (tid % 4) .. +8).
+__global__ __launch_bounds__(256) void k_lm_attn_in(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                    const bf16_t* __restrict__ v, int64_t T, int H, int KV,
+                                                    float log2_base, bf16_t* __restrict__ Qh, bf16_t* __restrict__ Kh,
+                                                    bf16_t* __restrict__ KhT, bf16_t* __restrict__ Vh,
+                                                    bf16_t* __restrict__ VhT) {
+  __shared__ TTile Tk, Tv;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.y, g = h / (H / KV);
+  const int64_t b = blockIdx.z, t0 = (int64_t)blockIdx.x * TILE;
+  const int r = tid >> 2, cp = (tid & 3) * 8;
+  const int64_t t = t0 + r, n = b * T + t;
+  const int64_t bh = b * H + h;
+  float q1[8], q2[8], k1[8], k2[8], v1[8], v2[8];
+  load8(q + n * (int64_t)H * LM_HD + h * LM_HD + cp, q1);
+  load8(q + n * (int64_t)H * LM_HD + h * LM_HD + cp + 32, q2);
+  load8(k + n * (int64_t)KV * LM_HD + g * LM_HD + cp, k1);
+  load8(k + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, k2);
+  load8(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp, v1);
+  load8(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, v2);
+  float qa[8], qb[8], ka[8], kb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float cs, sn;
+    rope_cs(t, cp + j, log2_base, cs, sn);
+    qa[j] = q1[j] * cs - q2[j] * sn;
+    qb[j] = q2[j] * cs + q1[j] * sn;
+    ka[j] = k1[j] * cs - k2[j] * sn;
+    kb[j] = k2[j] * cs + k1[j] * sn;
+  }
+  const int64_t row = (bh * T + t) * LM_HD;
+  store8(Qh + row + cp, qa);
+  store8(Qh + row + cp + 32, qb);
+  store8(Kh + row + cp, ka);
+  store8(Kh + row + cp + 32, kb);
+  store8(Vh + row + cp, v1);
+  store8(Vh + row + cp + 32, v2);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    Tk.v[cp + j][r] = f32_to_bf16(ka[j]);
+    Tk.v[cp + 32 + j][r] = f32_to_bf16(kb[j]);
+    Tv.v[cp + j][r] = f32_to_bf16(v1[j]);
+    Tv.v[cp + 32 + j][r] = f32_to_bf16(v2[j]);
+  }
+  __syncthreads();
+  ttile_store(Tk, KhT + bh * LM_HD * T, T, t0, T, 0, LM_HD, tid);
+  ttile_store(Tv, VhT + bh * LM_HD * T, T, t0, T, 0, LM_HD, tid);
+}
+
+// P = softmax(scale * S) over keys j <= i (causal), bf16; one wave per row of S [rows, T].
+__global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict__ S, int64_t rows, int T, float scale,
+                                                        bf16_t* __restrict__ P) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;
+  const int i = (int)(row % T), lane = threadIdx.x & 63;
+  const float* s = S + row * T;
+  float mx = -INFINITY;
+  for (int j = lane; j <= i; j += 64) mx = fmaxf(mx, s[j] * scale);
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = lane; j <= i; j += 64) sum += __expf(s[j] * scale - mx);
+  const float inv = 1.f / wave_sum(sum);
+  for (int j = lane; j < T; j += 64) P[row * T + j] = f32_to_bf16(j <= i ? __expf(s[j] * scale - mx) * inv : 0.f);
+}
+
+// dS = bf16(P * (dP - sum_j P dP) * scale) (causal zeros stay zero); one wave per row.
+__global__ __launch_bounds__(256) void k_lm_softmax_bwd(const bf16_t* __restrict__ P, const float* __restrict__ dP,
+                                                        int64_t rows, int T, float scale, bf16_t* __restrict__ dS) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;
+  const int i = (int)(row % T), lane = threadIdx.x & 63;
+  float dot = 0.f;
+  for (int j = lane; j <= i; j += 64) dot = fmaf(bf16_to_f32(P[row * T + j]), dP[row * T + j], dot);
+  dot = wave_sum(dot);
+  for (int j = lane; j < T; j += 64) {
+    const float pj = bf16_to_f32(P[row * T + j]);
+    dS[row * T + j] = f32_to_bf16(j <= i ? pj * (dP[row * T + j] - dot) * scale : 0.f);
+  }
+}
+
+// a[b*T + t, h*64 + c] = Oh[(b*H + h)*T + t, c] (dir = 0) or the inverse copy (dir = 1);
+// 8 elements per thread.
+__global__ __launch_bounds__(256) void k_lm_heads(bf16_t* __restrict__ rowmajor, bf16_t* __restrict__ headmajor,
+                                                  int64_t B, int64_t T, int H, int dir) {
+  const int64_t total = B * T * H * (LM_HD / 8);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int c8 = (int)(i % (LM_HD / 8)) * 8;
+    const int64_t rest = i / (LM_HD / 8);
+    const int h = (int)(rest % H);
+    const int64_t n = rest / H, b = n / T, t = n % T;
+    bf16_t* rm = rowmajor + n * (int64_t)H * LM_HD + h * LM_HD + c8;
+    bf16_t* hm = headmajor + ((b * H + h) * T + t) * LM_HD + c8;
+    if (dir == 0) *(uint4*)rm = *(const uint4*)hm;
+    else *(uint4*)hm = *(const uint4*)rm;
+  }
+}
+
+// Cotangents of q, k, v from the head-major dQh, dKh, dVh [B*H, T, 64]: the inverse RoPE
+// rotation on dq and dk (rope is orthogonal per pair: dx = dy cos - rot(dy) sin, the
+// transpose of the forward rotation) and, for k and v, the sum over the H/KV query heads
+// sharing a kv head. Grid (T/64, KV, B); thread = (token tid / 4, pairs 8 (tid % 4) .. +8).
+__global__ __launch_bounds__(256) void k_lm_attn_out_grads(const bf16_t* __restrict__ dQh,
+                                                           const bf16_t* __restrict__ dKh,
+                                                           const bf16_t* __restrict__ dVh, int64_t T, int H, int KV,
+                                                           float log2_base, bf16_t* __restrict__ dq,
+                                                           bf16_t* __restrict__ dk, bf16_t* __restrict__ dv) {
+  const int tid = threadIdx.x;
+  const int g = blockIdx.y, rep = H / KV;
+  const int64_t b = blockIdx.z, t0 = (int64_t)blockIdx.x * TILE;
+  const int r = tid >> 2, cp = (tid & 3) * 8;
+  const int64_t t = t0 + r, n = b * T + t;
+  float cs[8], sn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rope_cs(t, cp + j, log2_base, cs[j], sn[j]);
+  float ka[8] = {0, 0, 0, 0, 0, 0, 0, 0}, kb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float va[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < rep; ++i) {
+    const int h = g * rep + i;
+    const int64_t row = ((b * H + h) * T + t) * LM_HD;
+    float y1[8], y2[8], o1[8], o2[8];
+    load8(dQh + row + cp, y1);
+    load8(dQh + row + cp + 32, y2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o1[j] = y1[j] * cs[j] + y2[j] * sn[j];
+      o2[j] = y2[j] * cs[j] - y1[j] * sn[j];
+    }
+    store8(dq + n * (int64_t)H * LM_HD + h * LM_HD + cp, o1);
+    store8(dq + n * (int64_t)H * LM_HD + h * LM_HD + cp + 32, o2);
+    load8(dKh + row + cp, y1);
+    load8(dKh + row + cp + 32, y2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ka[j] += y1[j] * cs[j] + y2[j] * sn[j];
+      kb[j] += y2[j] * cs[j] - y1[j] * sn[j];
+    }
+    load8(dVh + row + cp, y1);
+    load8(dVh + row + cp + 32, y2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      va[j] += y1[j];
+      vb[j] += y2[j];
+    }
+  }
+  store8(dk + n * (int64_t)KV * LM_HD + g * LM_HD + cp, ka);
+  store8(dk + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, kb);
+  store8(dv + n * (int64_t)KV * LM_HD + g * LM_HD + cp, va);
+  store8(dv + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, vb);
+}
+
+// ---------------------------------------------------------------- GELU (tanh form)
+__device__ inline void gelu_tanh_fg(float x, float& f, float& g) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float u = k0 * (x + k1 * x * x * x);
+  const float th = tanhf(u);
+  f = 0.5f * x * (1.f + th);
+  g = 0.5f * (1.f + th) + 0.5f * x * (1.f - th * th) * k0 * (1.f + 3.f * k1 * x * x);
+}
+
+// y = bf16(gelu_tanh(x)), 8 elements per thread.
+__global__ __launch_bounds__(256) void k_lm_gelu_fwd(const bf16_t* __restrict__ x, int64_t n, bf16_t* __restrict__ y) {
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (int64_t)gridDim.x * 256 * 8) {
+    float v[8];
+    load8(x + i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float f, g;
+      gelu_tanh_fg(v[j], f, g);
+      v[j] = f;
+    }
+    store8(y + i, v);
+  }
+}
+
+// dx = bf16(dy * gelu_tanh'(x)).
+__global__ __launch_bounds__(256) void k_lm_gelu_bwd(const bf16_t* __restrict__ x, const bf16_t* __restrict__ dy,
+                                                     int64_t n, bf16_t* __restrict__ dx) {
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (int64_t)gridDim.x * 256 * 8) {
+    float v[8], d[8];
+    load8(x + i, v);
+    load8(dy + i, d);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float f, g;
+      gelu_tanh_fg(v[j], f, g);
+      v[j] = d[j] * g;
+    }
+    store8(dx + i, v);
+  }
+}
+
+// losses[0..2] = (recon_coeff * kl + imp_coeff * imp, kl, imp) with kl = mean of the
+// position KLs and imp = sum of the partials / N, each added in a fixed order in double.
+__global__ void k_lm_losses(const float* __restrict__ pos_kl, int64_t N, const float* __restrict__ imp_part,
+                            int64_t n_imp, float recon_coeff, float imp_coeff, float* __restrict__ losses) {
+  __shared__ double sr[16], si[16];
+  double r = 0.0, m = 0.0;
+  for (int64_t i = threadIdx.x; i < N; i += blockDim.x) r += pos_kl[i];
+  for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  r = wave_sum_d(r);
+  m = wave_sum_d(m);
+  if (threadIdx.x % 64 == 0) {
+    sr[threadIdx.x / 64] = r;
+    si[threadIdx.x / 64] = m;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double a = 0, c = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
+      a += sr[i];
+      c += si[i];
+    }
+    a /= (double)N;
+    c /= (double)N;
+    losses[0] = (float)(recon_coeff * a + imp_coeff * c);
+    losses[1] = (float)a;
+    losses[2] = (float)c;
+  }
+}
+
+// g[n] = v (the per-position cotangent of the mean KL).
+__global__ __launch_bounds__(256) void k_lm_fill(float* __restrict__ g, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) g[i] = v;
+}
+
+// ---------------------------------------------------------------- workspace plan
+struct LMDims {
+  int64_t B, T, N, V;
+  int d, H, KV, f, L, n_chunks;
+  int C[LM_NK], din[LM_NK], dout[LM_NK];
+  bool use_delta;
+  int64_t BH() const { return B * H; }
+  int64_t kcat(int k) const { return C[k] + (use_delta ? din[k] : 0); }   // forward product depth
+  int64_t kcat2(int k) const { return C[k] + (use_delta ? dout[k] : 0); } // d_input product depth
+};
+
+struct Arena {
+  char* base;
+  size_t off;
+  bool dry;
+  template <typename X>
+  X* take(size_t n) {
+    size_t bytes = (n * sizeof(X) + 255) & ~(size_t)255;
+    X* p = dry ? nullptr : (X*)(base + off);
+    off += bytes;
+    return p;
+  }
+};
+
+struct LMSiteSave {
+  bf16_t *xV, *acat, *actsT;
+  uint8_t* ub;
+};
+
+struct LMLayerSave {
+  bf16_t *r, *h, *hT, *r1, *h2, *h2T, *a, *aT, *fc, *g, *gT;
+  float *rinv1, *rinv2;
+  bf16_t *Qh, *Kh, *KhT, *Vh, *VhT, *P;
+  LMSiteSave site[LM_NK];
+};
+
+struct LMPlan {
+  std::vector<LMLayerSave> layers;
+  bf16_t *VT[LM_NK], *BtF[LM_NK], *BtB[LM_NK];  // per layer blocks of the per-step weight copies
+  bf16_t *rc_a, *rc_b, *rL, *act_m, *act_c, *hc, *qc, *kc, *vc, *ac, *Oh, *fcc, *gc;
+  bf16_t *q, *k, *v;
+  float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
+  bf16_t *dr_a, *dr_b, *drT, *dacts, *dcat, *dxVT, *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
+  char* kl_ws;
+  size_t kl_ws_bytes, imp_per_site[LM_NK], imp_total, total;
+};
+
+static size_t site_imp_blocks(const LMDims& D, int k) { return (size_t)cdiv(D.C[k], TILE) * cdiv(D.N, TILE); }
+
+static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
+  Arena A{base, 0, dry};
+  LMPlan P;
+  const int64_t N = D.N, d = D.d, f = D.f, BH = D.BH(), T = D.T;
+  const int64_t qd = (int64_t)D.H * LM_HD;
+  P.layers.resize(D.L);
+  for (int l = 0; l < D.L; ++l) {
+    LMLayerSave& S = P.layers[l];
+    S.r = A.take<bf16_t>(N * d);
+    S.h = A.take<bf16_t>(N * d);
+    S.hT = A.take<bf16_t>(N * d);
+    S.r1 = A.take<bf16_t>(N * d);
+    S.h2 = A.take<bf16_t>(N * d);
+    S.h2T = A.take<bf16_t>(N * d);
+    S.a = A.take<bf16_t>(N * qd);
+    S.aT = A.take<bf16_t>(N * qd);
+    S.fc = A.take<bf16_t>(N * f);
+    S.g = A.take<bf16_t>(N * f);
+    S.gT = A.take<bf16_t>(N * f);
+    S.rinv1 = A.take<float>(N);
+    S.rinv2 = A.take<float>(N);
+    S.Qh = A.take<bf16_t>(BH * T * LM_HD);
+    S.Kh = A.take<bf16_t>(BH * T * LM_HD);
+    S.KhT = A.take<bf16_t>(BH * T * LM_HD);
+    S.Vh = A.take<bf16_t>(BH * T * LM_HD);
+    S.VhT = A.take<bf16_t>(BH * T * LM_HD);
+    S.P = A.take<bf16_t>(BH * T * T);
+    for (int k = 0; k < LM_NK; ++k) {
+      S.site[k].xV = A.take<bf16_t>(N * D.C[k]);
+      S.site[k].acat = A.take<bf16_t>(N * D.kcat(k));
+      S.site[k].actsT = A.take<bf16_t>(N * D.C[k]);
+      S.site[k].ub = A.take<uint8_t>(N * D.C[k]);
+    }
+  }
+  for (int k = 0; k < LM_NK; ++k) {
+    P.VT[k] = A.take<bf16_t>((size_t)D.L * D.C[k] * D.din[k]);
+    P.BtF[k] = A.take<bf16_t>((size_t)D.L * D.dout[k] * D.kcat(k));
+    P.BtB[k] = A.take<bf16_t>((size_t)D.L * D.din[k] * D.kcat2(k));
+  }
+  int64_t maxw = std::max<int64_t>(d, f), maxC = 0, maxcat2 = 0;
+  for (int k = 0; k < LM_NK; ++k) {
+    maxC = std::max<int64_t>(maxC, D.C[k]);
+    maxcat2 = std::max<int64_t>(maxcat2, D.kcat2(k));
+  }
+  P.rc_a = A.take<bf16_t>(N * d);
+  P.rc_b = A.take<bf16_t>(N * d);
+  P.rL = A.take<bf16_t>(N * d);
+  P.act_m = A.take<bf16_t>(N * d);
+  P.act_c = A.take<bf16_t>(N * d);
+  P.hc = A.take<bf16_t>(N * d);
+  P.qc = A.take<bf16_t>(N * qd);
+  P.kc = A.take<bf16_t>(N * qd);
+  P.vc = A.take<bf16_t>(N * qd);
+  P.ac = A.take<bf16_t>(N * qd);
+  P.Oh = A.take<bf16_t>(BH * T * LM_HD);
+  P.fcc = A.take<bf16_t>(N * f);
+  P.gc = A.take<bf16_t>(N * f);
+  P.q = A.take<bf16_t>(N * qd);
+  P.k = A.take<bf16_t>(N * qd);
+  P.v = A.take<bf16_t>(N * qd);
+  P.rinvF = A.take<float>(N);
+  P.S = A.take<float>(BH * T * T);
+  P.delta = A.take<float>((size_t)D.L * LM_NK * N);
+  P.imp_total = 0;
+  for (int k = 0; k < LM_NK; ++k) {
+    P.imp_per_site[k] = site_imp_blocks(D, k);
+    P.imp_total += P.imp_per_site[k] * D.L;
+  }
+  P.imp_part = A.take<float>(P.imp_total);
+  P.pos_kl = A.take<float>(N);
+  P.stats = A.take<float>(N * 5);
+  P.gpos = A.take<float>(N);
+  P.d_act = A.take<float>(N * d);
+  P.dhf = A.take<float>(N * maxw);
+  P.dr_a = A.take<bf16_t>(N * d);
+  P.dr_b = A.take<bf16_t>(N * d);
+  P.drT = A.take<bf16_t>(N * maxw);
+  P.dacts = A.take<bf16_t>(N * maxC);
+  P.dcat = A.take<bf16_t>(N * maxcat2);
+  P.dxVT = A.take<bf16_t>(N * maxC);
+  for (int i = 0; i < 3; ++i) P.dqkv[i] = A.take<bf16_t>(N * qd);
+  P.dqkvT = A.take<bf16_t>(N * qd);
+  P.da = A.take<bf16_t>(N * qd);
+  P.dOh = A.take<bf16_t>(BH * T * LM_HD);
+  P.dQh = A.take<bf16_t>(BH * T * LM_HD);
+  P.dKh = A.take<bf16_t>(BH * T * LM_HD);
+  P.dVh = A.take<bf16_t>(BH * T * LM_HD);
+  P.dS = A.take<bf16_t>(BH * T * T);
+  P.dg = A.take<bf16_t>(N * f);
+  P.dfc = A.take<bf16_t>(N * f);
+  P.kl_ws_bytes = pd_streamed_kl_workspace_size(PD_DTYPE_BF16, N, d, D.V, D.n_chunks);
+  P.kl_ws = A.take<char>(P.kl_ws_bytes);
+  P.total = A.off;
+  return P;
+}
+
+struct LMRecorder {
+  void** ev;
+  int32_t* cat;
+  int cap, n;
+  hipStream_t s;
+  void mark(int category) {
+    if (!ev || n >= cap) return;
+    (void)hipEventRecord((hipEvent_t)ev[n], s);
+    if (cat) cat[n] = category;
+    ++n;
+  }
+};
+
+static unsigned ew_blocks(int64_t n8) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(n8, 256), 8192)); }
+
+static void transpose(const bf16_t* src, int64_t R, int64_t Cc, bf16_t* dst, int64_t ld, hipStream_t s) {
+  hipLaunchKernelGGL(k_lm_transpose, dim3((unsigned)cdiv(Cc, TILE), (unsigned)cdiv(R, TILE)), dim3(256), 0, s, src,
+                     R, Cc, dst, ld);
+}
+
+static void copy_rows(const bf16_t* src, int64_t R, int w, const float* sc, bf16_t* dst, int64_t ld, hipStream_t s) {
+  hipLaunchKernelGGL(k_lm_copy_rows, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, src, R, w, sc, dst, ld);
+}
+
+// C = A @ B^T with both operands K-contiguous (the buffer-fed kernel).
+static int gemm_nt(int64_t M, int64_t Nn, int64_t K, const bf16_t* A, int64_t lda, const bf16_t* Bt, int64_t ldb,
+                   void* C, int64_t ldc, int c_dtype, float beta, hipStream_t s) {
+  return pd_gemm(PD_DTYPE_BF16, M, Nn, K, A, lda, 0, Bt, ldb, 1, C, ldc, c_dtype, 1.f, beta, s);
+}
+
+}  // namespace pd
+
+using namespace pd;
+
+extern "C" {
+
+size_t pd_lm_stack_workspace_size(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab,
+                                  int L, const int32_t* C, int use_delta, int n_kl_chunks) {
+  if (B <= 0 || T <= 0 || d <= 0 || n_head <= 0 || n_kv_head <= 0 || d_mlp <= 0 || vocab <= 0 || L <= 0 || !C ||
+      n_kl_chunks <= 0)
+    return 0;
+  LMDims D{B, T, B * T, vocab, d, n_head, n_kv_head, d_mlp, L, n_kl_chunks, {}, {}, {}, use_delta != 0};
+  const int qd = n_head * LM_HD, kvd = n_kv_head * LM_HD;
+  const int din[LM_NK] = {d, d, d, qd, d, d_mlp}, dout[LM_NK] = {qd, kvd, kvd, d, d_mlp, d};
+  for (int k = 0; k < LM_NK; ++k) {
+    D.C[k] = C[k];
+    D.din[k] = din[k];
+    D.dout[k] = dout[k];
+  }
+  return lm_plan(D, nullptr, true).total;
+}
+
+enum {
+  LM_CAT_PREP = 0,     // per-step weight copies, delta draws
+  LM_CAT_CLEAN = 1,    // frozen forward
+  LM_CAT_GEMM_FWD = 2, // masked-forward site products
+  LM_CAT_MASK_FWD = 3, // mask passes (forward)
+  LM_CAT_ATTN = 4,     // attention forward and backward
+  LM_CAT_ELEM = 5,     // norms, residual adds, GELU, transposes
+  LM_CAT_KL = 6,       // streamed KL forward and backward
+  LM_CAT_GEMM_DX = 7,  // d_acts and d_input products
+  LM_CAT_GEMM_DW = 8,  // dU and dV products
+  LM_CAT_MASK_BWD = 9, // mask passes (backward)
+  LM_CAT_END = 10
+};
+
+static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64_t V, int L, const int32_t* Cs,
+                        const int32_t* tokens, const void* wte, const float* ln1, const float* ln2, const float* norm,
+                        float eps, float rope_base, const void* const* W, const void* const* Vf, const void* const* Uf,
+                        const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
+                        float p, float imp_coeff, float recon_coeff, int n_chunks, float* losses, float* const* dV,
+                        float* const* dU, void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
+                        LMRecorder& rec) {
+  const char* what = "pd_lm_stack_step";
+  if (B <= 0 || T <= 0 || d <= 0 || H <= 0 || KV <= 0 || f <= 0 || V <= 0 || L <= 0 || n_chunks <= 0 || !Cs)
+    return fail(PD_EINVAL, std::string(what) + ": bad dims");
+  if (H % KV) return fail(PD_EINVAL, std::string(what) + ": n_head must be a multiple of n_kv_head");
+  if (d != H * LM_HD) return fail(PD_EUNSUPPORTED, std::string(what) + ": head_dim must be 64 (d = 64 * n_head)");
+  if (T % TILE || d % 64 || f % 64 || V % n_chunks || T > 8192 || d > 4096 || f > 65536)
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": need T % 64 == 0 (T <= 8192), d and d_mlp multiples of 64, "
+                                                     "vocab % n_chunks == 0");
+  for (int k = 0; k < LM_NK; ++k)
+    if (Cs[k] <= 0 || Cs[k] % 8) return fail(PD_EUNSUPPORTED, std::string(what) + ": every C must be a positive multiple of 8");
+  if (!tokens || !wte || !ln1 || !ln2 || !norm || !W || !Vf || !Uf || !ci_pre || !losses || !dV || !dU || !d_ci_pre)
+    return fail(PD_EINVAL, std::string(what) + ": null pointer");
+  for (int k = 0; k < LM_NK; ++k)
+    if (!W[k] || !Vf[k] || !Uf[k] || !ci_pre[k] || !dV[k] || !dU[k] || !d_ci_pre[k])
+      return fail(PD_EINVAL, std::string(what) + ": null per-kind pointer");
+  if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
+    return fail(PD_EINVAL, std::string(what) + ": unknown counter layout");
+  LMDims D{B, T, B * T, V, d, H, KV, f, L, n_chunks, {}, {}, {}, use_delta != 0};
+  const int qd = H * LM_HD, kvd = KV * LM_HD;
+  {
+    const int din[LM_NK] = {d, d, d, qd, d, f}, dout[LM_NK] = {qd, kvd, kvd, d, f, d};
+    for (int k = 0; k < LM_NK; ++k) {
+      D.C[k] = Cs[k];
+      D.din[k] = din[k];
+      D.dout[k] = dout[k];
+    }
+  }
+  if (!workspace || workspace_bytes < lm_plan(D, nullptr, true).total)
+    return fail(PD_EWORKSPACE, std::string(what) + ": workspace too small");
+  if (D.N * (int64_t)std::max<int64_t>(f, 4096) > ((int64_t)1 << 31) / 2 || D.BH() * T * T > ((int64_t)1 << 31))
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": activations of 2 GiB or more");
+  LMPlan P = lm_plan(D, (char*)workspace, false);
+  hipStream_t s = (hipStream_t)stream;
+  rec.s = s;
+  const int64_t N = D.N, BH = D.BH();
+  const float log2b = log2f(rope_base), att_scale = 1.f / sqrtf((float)LM_HD);
+  const int pm = pow_mode(p);
+  int rc;
+  auto bfp = [](const void* base, size_t off) { return (const bf16_t*)base + off; };
+  auto rows4 = [](int64_t n) { return dim3((unsigned)cdiv(n, 4)); };
+  auto tgrid = [](int64_t rows, int64_t cols) { return dim3((unsigned)cdiv(cols, TILE), (unsigned)cdiv(rows, TILE)); };
+
+  // ---- keys: src_base, delta_base = split(draw_key); key(kind, layer) = fold_in(fold_in(base, kind), layer)
+  uint32_t halves[4];
+  split2(draw_k0, draw_k1, layout, halves);
+  auto site_key = [&](int kind, int layer, uint32_t& o0, uint32_t& o1) {
+    uint32_t x0 = 0, x1 = (uint32_t)kind;
+    threefry2x32(halves[0], halves[1], x0, x1);
+    uint32_t y0 = 0, y1 = (uint32_t)layer;
+    threefry2x32(x0, x1, y0, y1);
+    o0 = y0;
+    o1 = y1;
+  };
+
+  // ================= per-step weight copies (every product K-contiguous)
+  rec.mark(LM_CAT_PREP);
+  for (int k = 0; k < LM_NK; ++k) {
+    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc = D.kcat(k), kc2 = D.kcat2(k);
+    for (int l = 0; l < L; ++l) {
+      const bf16_t* Vl = bfp(Vf[k], (size_t)l * di * C);
+      const bf16_t* Ul = bfp(Uf[k], (size_t)l * C * dout);
+      const bf16_t* Wl = bfp(W[k], (size_t)l * dout * di);
+      bf16_t* vt = P.VT[k] + (size_t)l * C * di;
+      bf16_t* bf = P.BtF[k] + (size_t)l * dout * kc;
+      bf16_t* bb = P.BtB[k] + (size_t)l * di * kc2;
+      transpose(Vl, di, C, vt, di, s);                       // V^T [C, d_in]
+      transpose(Ul, C, dout, bf, kc, s);                     // U^T into [U^T | W]
+      if (D.use_delta) copy_rows(Wl, dout, (int)di, nullptr, bf + C, kc, s);  // W
+      copy_rows(Vl, di, (int)C, nullptr, bb, kc2, s);        // V into [V | W^T]
+      if (D.use_delta) transpose(Wl, dout, di, bb + C, kc2, s);  // W^T
+    }
+  }
+  if (D.use_delta)
+    hipLaunchKernelGGL(k_lm_deltas, dim3((unsigned)cdiv(N, 256), (unsigned)(LM_NK * L)), dim3(256), 0, s, halves[2],
+                       halves[3], N, layout, P.delta);
+  if ((rc = check_launch("pd_lm_stack_step prep"))) return rc;
+
+  // ================= attention forward on head-major copies
+  auto attn_fwd = [&](const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* Qh, bf16_t* Kh, bf16_t* KhT,
+                      bf16_t* Vh, bf16_t* VhT, bf16_t* Pm, bf16_t* a) -> int {
+    hipLaunchKernelGGL(k_lm_attn_in, dim3((unsigned)(T / TILE), (unsigned)H, (unsigned)B), dim3(256), 0, s, q, k, v,
+                       T, H, KV, log2b, Qh, Kh, KhT, Vh, VhT);
+    int r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, T, LM_HD, Qh, LM_HD, T * LM_HD, 0, Kh, LM_HD, T * LM_HD, 1,
+                                    P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s);
+    if (r) return r;
+    hipLaunchKernelGGL(k_lm_softmax_fwd, rows4(BH * T), dim3(256), 0, s, P.S, BH * T, (int)T, att_scale, Pm);
+    if ((r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, P.Oh,
+                                     LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+      return r;
+    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, a, P.Oh, B, T, H, 0);
+    return check_launch("pd_lm_stack_step attention");
+  };
+
+  // ================= clean forward (frozen target): act_c
+  rec.mark(LM_CAT_CLEAN);
+  hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, s, tokens, (const bf16_t*)wte, N, d, V, P.rc_a);
+  {
+    bf16_t* rcur = P.rc_a;
+    bf16_t* rnext = P.rc_b;
+    for (int l = 0; l < L; ++l) {
+      auto Wk = [&](int k) { return bfp(W[k], (size_t)l * D.dout[k] * D.din[k]); };
+      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, ln1 + (size_t)l * d, eps, P.hc,
+                         (float*)nullptr);
+      if ((rc = gemm_nt(N, qd, d, P.hc, d, Wk(LK_Q), d, P.qc, qd, PD_DTYPE_BF16, 0.f, s))) return rc;
+      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_K), d, P.kc, kvd, PD_DTYPE_BF16, 0.f, s))) return rc;
+      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_V), d, P.vc, kvd, PD_DTYPE_BF16, 0.f, s))) return rc;
+      // the clean pass borrows layer 0's attention saves, which the masked pass rewrites
+      LMLayerSave& S0 = P.layers[0];
+      if ((rc = attn_fwd(P.qc, P.kc, P.vc, S0.Qh, S0.Kh, S0.KhT, S0.Vh, S0.VhT, S0.P, P.ac))) return rc;
+      if ((rc = gemm_nt(N, d, qd, P.ac, qd, Wk(LK_O), qd, P.hc, d, PD_DTYPE_BF16, 0.f, s))) return rc;
+      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, rcur, P.hc, N * d, rnext);
+      std::swap(rcur, rnext);
+      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, ln2 + (size_t)l * d, eps, P.hc,
+                         (float*)nullptr);
+      if ((rc = gemm_nt(N, f, d, P.hc, d, Wk(LK_FC), d, P.fcc, f, PD_DTYPE_BF16, 0.f, s))) return rc;
+      hipLaunchKernelGGL(k_lm_gelu_fwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, P.fcc, N * f, P.gc);
+      if ((rc = gemm_nt(N, d, f, P.gc, f, Wk(LK_DOWN), f, P.hc, d, PD_DTYPE_BF16, 0.f, s))) return rc;
+      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, rcur, P.hc, N * d, rnext);
+      std::swap(rcur, rnext);
+    }
+    hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, norm, eps, P.act_c, (float*)nullptr);
+  }
+  if ((rc = check_launch("pd_lm_stack_step clean"))) return rc;
+
+  // ================= masked forward
+  auto mask_args = [&](int k, int l) {
+    LMMaskArgs ma;
+    ma.ci_pre = bfp(ci_pre[k], (size_t)l * N * D.C[k]);
+    ma.N = N;
+    ma.C = D.C[k];
+    site_key(k, l, ma.k0, ma.k1);
+    ma.p = p;
+    ma.delta = D.use_delta ? P.delta + ((size_t)l * LM_NK + k) * N : nullptr;
+    ma.ld = D.kcat(k);
+    return ma;
+  };
+  // site forward: x [N, d_in] (and the site's saves) -> out [N, d_out]
+  auto site_fwd = [&](int k, int l, const bf16_t* x, bf16_t* out) -> int {
+    LMSiteSave& S = P.layers[l].site[k];
+    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc = D.kcat(k);
+    rec.mark(LM_CAT_GEMM_FWD);
+    int r = gemm_nt(N, C, di, x, di, P.VT[k] + (size_t)l * C * di, di, S.xV, C, PD_DTYPE_BF16, 0.f, s);
+    if (r) return r;
+    rec.mark(LM_CAT_MASK_FWD);
+    const LMMaskArgs ma = mask_args(k, l);
+    if (D.use_delta) copy_rows(x, N, (int)di, ma.delta, S.acat + C, kc, s);
+    float* part = P.imp_part + [&] {
+      size_t o = 0;
+      for (int ll = 0; ll < l; ++ll)
+        for (int kk = 0; kk < LM_NK; ++kk) o += P.imp_per_site[kk];
+      for (int kk = 0; kk < k; ++kk) o += P.imp_per_site[kk];
+      return o;
+    }();
+#define PD_LMF(LY, PMV) \
+  hipLaunchKernelGGL((k_lm_mask_fwd<LY, PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.acat, S.actsT, S.ub, part)
+    if (layout == PD_LAYOUT_PARTITIONABLE) {
+      if (pm == 2) PD_LMF(PD_LAYOUT_PARTITIONABLE, 2);
+      else if (pm == 1) PD_LMF(PD_LAYOUT_PARTITIONABLE, 1);
+      else PD_LMF(PD_LAYOUT_PARTITIONABLE, 0);
+    } else {
+      if (pm == 2) PD_LMF(PD_LAYOUT_ORIGINAL, 2);
+      else if (pm == 1) PD_LMF(PD_LAYOUT_ORIGINAL, 1);
+      else PD_LMF(PD_LAYOUT_ORIGINAL, 0);
+    }
+#undef PD_LMF
+    rec.mark(LM_CAT_GEMM_FWD);
+    return gemm_nt(N, dout, kc, S.acat, kc, P.BtF[k] + (size_t)l * dout * kc, kc, out, dout, PD_DTYPE_BF16, 0.f, s);
+  };
+
+  hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, s, tokens, (const bf16_t*)wte, N, d, V, P.layers[0].r);
+  for (int l = 0; l < L; ++l) {
+    LMLayerSave& S = P.layers[l];
+    rec.mark(LM_CAT_ELEM);
+    hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, S.r, N, d, ln1 + (size_t)l * d, eps, S.h, S.rinv1);
+    transpose(S.h, N, d, S.hT, N, s);
+    if ((rc = site_fwd(LK_Q, l, S.h, P.q))) return rc;
+    if ((rc = site_fwd(LK_K, l, S.h, P.k))) return rc;
+    if ((rc = site_fwd(LK_V, l, S.h, P.v))) return rc;
+    rec.mark(LM_CAT_ATTN);
+    if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.KhT, S.Vh, S.VhT, S.P, S.a))) return rc;
+    rec.mark(LM_CAT_ELEM);
+    transpose(S.a, N, qd, S.aT, N, s);
+    if ((rc = site_fwd(LK_O, l, S.a, P.q))) return rc;  // o output into the q scratch
+    rec.mark(LM_CAT_ELEM);
+    hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, S.r, P.q, N * d, S.r1);
+    hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, S.r1, N, d, ln2 + (size_t)l * d, eps, S.h2, S.rinv2);
+    transpose(S.h2, N, d, S.h2T, N, s);
+    if ((rc = site_fwd(LK_FC, l, S.h2, S.fc))) return rc;
+    rec.mark(LM_CAT_ELEM);
+    hipLaunchKernelGGL(k_lm_gelu_fwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, S.fc, N * f, S.g);
+    transpose(S.g, N, f, S.gT, N, s);
+    if ((rc = site_fwd(LK_DOWN, l, S.g, P.q))) return rc;
+    rec.mark(LM_CAT_ELEM);
+    bf16_t* rnext = l + 1 < L ? P.layers[l + 1].r : P.rL;
+    hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, S.r1, P.q, N * d, rnext);
+  }
+  hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, P.rL, N, d, norm, eps, P.act_m, P.rinvF);
+  if ((rc = check_launch("pd_lm_stack_step masked forward"))) return rc;
+
+  // ================= streamed KL (clean || masked) over the tied head, and its cotangent
+  rec.mark(LM_CAT_KL);
+  if ((rc = pd_streamed_kl_fwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.pos_kl, P.stats,
+                               P.kl_ws, P.kl_ws_bytes, s)))
+    return rc;
+  hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.imp_part, (int64_t)P.imp_total,
+                     recon_coeff, imp_coeff, losses);
+  hipLaunchKernelGGL(k_lm_fill, dim3(ew_blocks(N)), dim3(256), 0, s, P.gpos, N, recon_coeff / (float)N);
+  if ((rc = pd_streamed_kl_bwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.stats, P.gpos,
+                               P.d_act, P.kl_ws, P.kl_ws_bytes, s)))
+    return rc;
+  rec.mark(LM_CAT_ELEM);
+  hipLaunchKernelGGL(k_lm_rms_bwd, rows4(N), dim3(256), 0, s, P.d_act, P.rL, P.rinvF, norm, N, d,
+                     (const bf16_t*)nullptr, P.dr_a);
+  if ((rc = check_launch("pd_lm_stack_step loss"))) return rc;
+
+  // ================= backward
+  const float imp_scale = imp_coeff / (float)N;
+  // site backward: g [N, d_out] (the output cotangent), the site input's transpose xT
+  // [d_in, N] -> dU, dV, d_ci_pre, and d_input (+)= into din_out (fp32 accumulate when
+  // din_f32, else bf16 written).
+  auto site_bwd = [&](int k, int l, const bf16_t* g, const bf16_t* xT, void* din_out, bool din_f32,
+                      float din_beta) -> int {
+    // din_out NULL: the site's input carries no gradient (layer 0's q/k/v read the
+    // embedding), so its d_input product is not formed (nor counted by the reference's
+    // FLOP rule, pd/core/flops/target.py:53-93)
+    LMSiteSave& S = P.layers[l].site[k];
+    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc2 = D.kcat2(k);
+    const LMMaskArgs ma0 = mask_args(k, l);
+    LMMaskArgs ma = ma0;
+    ma.ld = kc2;
+    rec.mark(LM_CAT_ELEM);
+    transpose(g, N, dout, P.drT, N, s);  // g^T [d_out, N]
+    if (D.use_delta && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s);
+    rec.mark(LM_CAT_GEMM_DX);
+    int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
+    if (r) return r;
+    rec.mark(LM_CAT_GEMM_DW);
+    if ((r = gemm_nt(C, dout, N, S.actsT, N, P.drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f, s)))
+      return r;
+    rec.mark(LM_CAT_MASK_BWD);
+    bf16_t* dpre = (bf16_t*)d_ci_pre[k] + (size_t)l * N * C;
+#define PD_LMB(PMV)                                                                                          \
+  hipLaunchKernelGGL((k_lm_mask_bwd<PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
+                     P.dcat, P.dxVT, dpre)
+    if (pm == 2) PD_LMB(2);
+    else if (pm == 1) PD_LMB(1);
+    else PD_LMB(0);
+#undef PD_LMB
+    rec.mark(LM_CAT_GEMM_DW);
+    if ((r = gemm_nt(di, C, N, xT, N, P.dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, s))) return r;
+    if (!din_out) return PD_OK;
+    rec.mark(LM_CAT_GEMM_DX);
+    return gemm_nt(N, di, kc2, P.dcat, kc2, P.BtB[k] + (size_t)l * di * kc2, kc2, din_out, di,
+                   din_f32 ? PD_DTYPE_F32 : PD_DTYPE_BF16, din_beta, s);
+  };
+
+  bf16_t* dr = P.dr_a;     // cotangent of the residual leaving layer l
+  bf16_t* dr_o = P.dr_b;
+  for (int l = L - 1; l >= 0; --l) {
+    LMLayerSave& S = P.layers[l];
+    // down site: input g, output cotangent dr
+    if ((rc = site_bwd(LK_DOWN, l, dr, S.gT, P.dg, false, 0.f))) return rc;
+    rec.mark(LM_CAT_ELEM);
+    hipLaunchKernelGGL(k_lm_gelu_bwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, S.fc, P.dg, N * f, P.dfc);
+    // fc site: input h2 -> d_h2 (fp32) -> norm pullback added to dr
+    if ((rc = site_bwd(LK_FC, l, P.dfc, S.h2T, P.dhf, true, 0.f))) return rc;
+    rec.mark(LM_CAT_ELEM);
+    hipLaunchKernelGGL(k_lm_rms_bwd, rows4(N), dim3(256), 0, s, P.dhf, S.r1, S.rinv2, ln2 + (size_t)l * d, N, d, dr,
+                       dr_o);
+    std::swap(dr, dr_o);  // dr: cotangent of r1
+    // o site: input a, output cotangent dr -> d_a
+    if ((rc = site_bwd(LK_O, l, dr, S.aT, P.da, false, 0.f))) return rc;
+    // attention backward
+    rec.mark(LM_CAT_ATTN);
+    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, P.da, P.dOh, B, T, H, 1);
+    // dP = dO @ V^T (fp32), dS
+    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, T, LM_HD, P.dOh, LM_HD, T * LM_HD, 0, S.Vh, LM_HD,
+                                      T * LM_HD, 1, P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s)))
+      return rc;
+    hipLaunchKernelGGL(k_lm_softmax_bwd, rows4(BH * T), dim3(256), 0, s, S.P, P.S, BH * T, (int)T, att_scale, P.dS);
+    // dQ = dS @ K (B^T = K^T), dK = dS^T @ Q, dV = P^T @ dO
+    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 0, S.KhT, T, LM_HD * T, 1, P.dQh,
+                                      LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+      return rc;
+    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 1, S.Qh, LM_HD, T * LM_HD, 0,
+                                      P.dKh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+      return rc;
+    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, S.P, T, T * T, 1, P.dOh, LM_HD, T * LM_HD, 0,
+                                      P.dVh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+      return rc;
+    hipLaunchKernelGGL(k_lm_attn_out_grads, dim3((unsigned)(T / TILE), (unsigned)KV, (unsigned)B), dim3(256), 0, s,
+                       P.dQh, P.dKh, P.dVh, T, H, KV, log2b, P.dqkv[0], P.dqkv[1], P.dqkv[2]);
+    if ((rc = check_launch("pd_lm_stack_step attention backward"))) return rc;
+    // q, k, v sites: input h, d_h accumulated in fp32 (none for layer 0: the embedding)
+    float* dh = l > 0 ? P.dhf : nullptr;
+    if ((rc = site_bwd(LK_Q, l, P.dqkv[0], S.hT, dh, true, 0.f))) return rc;
+    if ((rc = site_bwd(LK_K, l, P.dqkv[1], S.hT, dh, true, 1.f))) return rc;
+    if ((rc = site_bwd(LK_V, l, P.dqkv[2], S.hT, dh, true, 1.f))) return rc;
+    if (l > 0) {
+      rec.mark(LM_CAT_ELEM);
+      hipLaunchKernelGGL(k_lm_rms_bwd, rows4(N), dim3(256), 0, s, P.dhf, S.r, S.rinv1, ln1 + (size_t)l * d, N, d, dr,
+                         dr_o);
+      std::swap(dr, dr_o);  // dr: cotangent of layer l's input
+    }
+  }
+  rec.mark(LM_CAT_END);
+  return check_launch("pd_lm_stack_step backward");
+}
+
+int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                     const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
+                     const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
+                     const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
+                     int use_delta, int layout, float p, float imp_coeff, float recon_coeff, int n_kl_chunks,
+                     float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  LMRecorder rec{nullptr, nullptr, 0, 0, nullptr};
+  return lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base, W,
+                      V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, n_kl_chunks,
+                      losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
+}
+
+int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                           const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
+                           const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
+                           const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
+                           uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff, float recon_coeff,
+                           int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                           void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
+                           void** events, int32_t* categories, int capacity, int* n_recorded) {
+  LMRecorder rec{events, categories, capacity, 0, nullptr};
+  int rc = lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base,
+                        W, V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, n_kl_chunks,
+                        losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
+  if (n_recorded) *n_recorded = rec.n;
+  return rc;
+}
+
+}  // extern "C"
