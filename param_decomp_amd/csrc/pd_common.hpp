@@ -33,6 +33,15 @@ int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out
 int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, float* probs, int32_t* top_idx,
                 float* weights, void* stream);
 
+// C = A @ Bt^T (bf16, both operands K-contiguous: A [M, K] ld lda, Bt [N, K] ld ldb) with
+// the contraction split into slices when the output alone has too few tiles to occupy
+// the GPU: each slice's fp32 partial goes to `ws` and a second pass adds the slices in
+// order (deterministic), writing C (+ beta * C) in c_dtype. gemm_splitk_ws_bytes gives the
+// scratch the same call needs (0: no split; the call then needs no scratch).
+size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K);
+int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
+                   int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream);
+
 // ---------------------------------------------------------------- bf16
 typedef uint16_t bf16_t;
 

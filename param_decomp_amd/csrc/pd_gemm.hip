@@ -404,6 +404,66 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
+// ---------------------------------------------------------------- split contraction
+// Slices: enough (tiles x slices >= 512, two blocks per CU) when the output has fewer than
+// 384 128x128 tiles, each slice at least 512 deep, at most 16 slices.
+static int64_t splitk_slice(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, CfgDtlRA::BM) * cdiv(N, CfgDtlRA::BN);
+  if (tiles >= 384 || K < 1024) return 0;
+  int64_t splits = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), K / 512), 16);
+  if (splits < 2) return 0;
+  return cdiv(cdiv(K, splits), 64) * 64;
+}
+
+size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  const int64_t kc = splitk_slice(M, N, K);
+  return kc ? (size_t)cdiv(K, kc) * M * N * sizeof(float) : 0;
+}
+
+// C[m, n] = sum_z part[z][m, n] (+ beta * C), slices added in order; 4 columns per thread.
+template <typename TC>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int64_t M, int64_t N,
+                                                       int splits, TC* __restrict__ C, int64_t ldc, float beta) {
+  const int64_t n4 = N / 4, total = M * n4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / n4, c = (i % n4) * 4;
+    float4 acc = *(const float4*)(part + m * N + c);
+    for (int z = 1; z < splits; ++z) {
+      const float4 v = *(const float4*)(part + ((int64_t)z * M + m) * N + c);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    const float o[4] = {acc.x, acc.y, acc.z, acc.w};
+    store4<TC>(C, m * ldc + c, o, 1.f, beta);
+  }
+}
+
+int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
+                   int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream) {
+  const int64_t kc = splitk_slice(M, N, K);
+  if (!kc || N % 4 || ldc % 4 || !aligned16(C))
+    return pd_gemm(PD_DTYPE_BF16, M, N, K, A, lda, 0, Bt, ldb, 1, C, ldc, c_dtype, 1.f, beta, stream);
+  if (!bf16_operand_ok(A, lda, K) || !bf16_operand_ok(Bt, ldb, K) || !dtl_fits(M, lda, N, ldb))
+    return fail(PD_EUNSUPPORTED, "gemm_nt_splitk: operands");
+  const int splits = (int)cdiv(K, kc);
+  if (!ws || ws_bytes < (size_t)splits * M * N * sizeof(float)) return fail(PD_EWORKSPACE, "gemm_nt_splitk: scratch");
+  hipStream_t s = (hipStream_t)stream;
+  GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)Bt, ldb, ws, N, 1.f, 0.f, nullptr, 0, 0, M * N, kc};
+  const dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)splits);
+  int rc = launch_dtl<CfgDtlRA, MODE_SPLITK>(a, PD_DTYPE_F32, K % CfgDtlRA::BK != 0, grid, s);
+  if (rc) return rc;
+  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(M * N / 4, 256), 8192));
+  if (c_dtype == PD_DTYPE_F32)
+    hipLaunchKernelGGL(k_splitk_reduce<float>, dim3(blocks), dim3(256), 0, s, (const float*)ws, M, N, splits,
+                       (float*)C, ldc, beta);
+  else
+    hipLaunchKernelGGL(k_splitk_reduce<bf16_t>, dim3(blocks), dim3(256), 0, s, (const float*)ws, M, N, splits,
+                       (bf16_t*)C, ldc, beta);
+  return check_launch("gemm_nt_splitk reduce");
+}
+
 int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,
                       const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype, void* stream) {
   if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs1 || !rhsT1 || !out1 || !lhs2 || !rhsT2 || !out2 || !offsets)

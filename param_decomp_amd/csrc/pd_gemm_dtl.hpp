@@ -37,7 +37,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2, MODE_BATCHED = 3 };
+enum GemmMode { MODE_DENSE = 0, MODE_GROUPED = 1, MODE_GROUPED_K = 2, MODE_BATCHED = 3, MODE_SPLITK = 4 };
 
 struct GemmArgs {
   int64_t M, N, K;
@@ -189,6 +189,17 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     t.m0 = off + (int64_t)(tile - before) * BM;
     if (t.m0 < 0) return false;
     t.B += (int64_t)e * p.strideB;
+  } else if (MODE == MODE_SPLITK) {
+    // a dense tile, over the contraction slice blockIdx.z of gridDim.z equal slices of
+    // p.strideA k each (a multiple of 64); slice z writes its partial sum to
+    // C + z * strideC (the caller adds the slices in order)
+    int my, nx;
+    dense_tile(my, nx);
+    t.m0 = (int64_t)my * BM;
+    t.n0 = (int64_t)nx * BN;
+    t.kbeg = (int64_t)blockIdx.z * p.strideA;
+    t.kend = t.kbeg + p.strideA < p.K ? t.kbeg + p.strideA : p.K;
+    t.C = (TC*)p.C + (int64_t)blockIdx.z * p.strideC;
   } else if (MODE == MODE_BATCHED) {
     // blockIdx.z = batch; each operand advances by its own stride (0 = shared)
     const int64_t z = blockIdx.z;

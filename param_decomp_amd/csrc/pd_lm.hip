@@ -572,8 +572,8 @@ struct LMPlan {
   bf16_t *q, *k, *v;
   float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
   bf16_t *dr_a, *dr_b, *drT, *dacts, *dcat, *dxVT, *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
-  char* kl_ws;
-  size_t kl_ws_bytes, imp_per_site[LM_NK], imp_total, total;
+  char *kl_ws, *sk_ws;
+  size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
 };
 
 static size_t site_imp_blocks(const LMDims& D, int k) { return (size_t)cdiv(D.C[k], TILE) * cdiv(D.N, TILE); }
@@ -670,6 +670,11 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.dfc = A.take<bf16_t>(N * f);
   P.kl_ws_bytes = pd_streamed_kl_workspace_size(PD_DTYPE_BF16, N, d, D.V, D.n_chunks);
   P.kl_ws = A.take<char>(P.kl_ws_bytes);
+  P.sk_ws_bytes = 0;  // split-contraction partials of the weight-gradient products
+  for (int k = 0; k < LM_NK; ++k)
+    P.sk_ws_bytes = std::max({P.sk_ws_bytes, gemm_splitk_ws_bytes(D.C[k], D.dout[k], N),
+                              gemm_splitk_ws_bytes(D.din[k], D.C[k], N)});
+  P.sk_ws = A.take<char>(P.sk_ws_bytes);
   P.total = A.off;
   return P;
 }
@@ -984,7 +989,8 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
     rec.mark(LM_CAT_GEMM_DW);
-    if ((r = gemm_nt(C, dout, N, S.actsT, N, P.drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f, s)))
+    if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, P.drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
+                            P.sk_ws, P.sk_ws_bytes, s)))
       return r;
     rec.mark(LM_CAT_MASK_BWD);
     bf16_t* dpre = (bf16_t*)d_ci_pre[k] + (size_t)l * N * C;
@@ -996,7 +1002,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     else PD_LMB(0);
 #undef PD_LMB
     rec.mark(LM_CAT_GEMM_DW);
-    if ((r = gemm_nt(di, C, N, xT, N, P.dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, s))) return r;
+    if ((r = gemm_nt_splitk(di, C, N, xT, N, P.dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
+                            P.sk_ws_bytes, s)))
+      return r;
     if (!din_out) return PD_OK;
     rec.mark(LM_CAT_GEMM_DX);
     return gemm_nt(N, di, kc2, P.dcat, kc2, P.BtB[k] + (size_t)l * di * kc2, kc2, din_out, di,

@@ -60,12 +60,15 @@ def _setup(cfg, B, T, seed, device):
     return params, tokens, ci, w, ci_t, tok_t
 
 
-@pytest.mark.parametrize("n_kv,use_delta,partitionable", [(2, True, True), (1, True, False), (2, False, True)])
-def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable):
+@pytest.mark.parametrize("n_kv,use_delta,partitionable,T", [(2, True, True, 64), (1, True, False, 64),
+                                                           (2, False, True, 64), (2, True, True, 512)])
+def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T):
+    """T = 512 (1024 tokens) puts the weight-gradient products on the split-contraction
+    path (slices of the token axis added in order)."""
     from param_decomp_amd import _lib as L
     from param_decomp_amd.lm_step import LMStackStep
 
-    B, T = 2, 64
+    B = 2
     cfg = lo.LMConfig(n_layers=2, d=128, n_head=2, n_kv_head=n_kv, d_mlp=256, vocab=384,
                       C={"q_proj": 64, "k_proj": 48, "v_proj": 64, "o_proj": 32, "c_fc": 128, "down_proj": 96})
     params, tokens, ci, w, ci_t, tok_t = _setup(cfg, B, T, 4 + n_kv, device)
