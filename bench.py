@@ -52,6 +52,8 @@ KL_STREAM = "kl_stream_llama4L"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
 LLAMA = "llama4L"
+TMS = "tms5_2"
+RESID = "resid_mlp1L"
 PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
@@ -63,6 +65,12 @@ WORKLOADS = {
     LLAMA: dict(B=16, T=512, d=768, H=12, KV=12, f=3072, V=50277, L=4,
                 C={"q_proj": 1024, "k_proj": 1024, "v_proj": 1024, "o_proj": 1024, "c_fc": 4096,
                    "down_proj": 4096}, n_chunks=3, use_delta=True),
+    # the toy targets (fp32): TMS 5-2 (C=20, batch 4096, feature probability 0.05, p=1
+    # imp-min) and ResidualMLP 1 layer (100 features in a 1000-d residual, MLP 1000->50->1000,
+    # C=100 per matrix, batch 2048, probability 0.01, p=2 imp-min); per-component gate MLPs
+    # hidden 16, stochastic recon MSE
+    TMS: dict(B=4096, n_features=5, n_hidden=2, C=20, p_feat=0.05, low=0.0, p=1.0),
+    RESID: dict(B=2048, n_features=100, d_embed=1000, d_mlp=50, C=100, p_feat=0.01, low=-1.0, p=2.0),
     CI_MLP: dict(T=4096, dims=(768, 1024, 4096)),
     # every q/k/v/o (C=768) and c_fc/down (C=3072) site of the 4-layer Llama-style target,
     # readouts side by side: 4 * (4*768 + 2*3072) components
@@ -660,27 +668,30 @@ def moe_step_flops(cfg):
     return sum(moe_gemm_flops(cfg).values())
 
 
-def moe_cpu_baseline(cfg, T_sample, reps=1):
+def moe_cpu_baseline(cfg, T_sample, reps=5, warmup=2):
+    """The compiled fp32 C/OpenMP restatement of the same step (`oracle/cpu_step.c`
+    `or_moe_step`, checked against the NumPy oracle) on `T_sample` tokens at the full
+    widths; inputs packed once outside the timed calls."""
     import numpy as np
 
+    from oracle import cpu
     from oracle import moe_oracle as mo
 
     mc = mo.MoEConfig(T=T_sample, d=cfg["d"], f=cfg["f"], E=cfg["E"], k=cfg["k"], c=cfg["c"], L=cfg["L"])
     params, x0, ci = mo.init_moe(mc, np.random.default_rng(0))
+    st = cpu.pack_moe(mc, params, x0, ci, (0, 1))
+    for _ in range(warmup):
+        cpu.run_moe(mc, st, use_delta=cfg["use_delta"])
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        mo.moe_stack_step(mc, params, x0, ci, (0, 1), use_delta=cfg["use_delta"])
+        cpu.run_moe(mc, st, use_delta=cfg["use_delta"])
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count()
-    return {"value": T_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{T_sample} of the workload's 8192 tokens (full widths, 42 experts, 4 layers), NumPy float64 "
-                      f"restatement of the same step (BLAS-threaded matmuls), median of {reps}; "
-                      f"{med * 1e3:.0f} ms per sample step"}
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": cpu.num_threads(), "kind": "port",
+            "sample": f"{T_sample} of the workload's 8192 tokens (full widths, 42 experts, 4 layers), the fp32 "
+                      f"C/OpenMP restatement of the same step (oracle/cpu_step.c), median of {reps} after {warmup} "
+                      f"warmups; {med * 1e3:.0f} ms per sample step"}
 
 
 def run_moe(args):
@@ -761,6 +772,102 @@ def run_moe(args):
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = moe_cpu_baseline(cfg, args.cpu_tokens)
     return res
+
+
+# ============================================================== toy targets
+def toy_flops(workload, cfg):
+    """Reference rule per site (`pd/core/flops/target.py:39-93`): forward in + out, backward
+    in (component gradient; the toys' first site reads the data) or 2 in (later sites)
+    + 2 out, plus the per-component gate MLP's 2 * 2 * 16 multiply-adds per (row, component)
+    forward and twice that backward (elementwise by the rule, counted here as work)."""
+    B = cfg["B"]
+    if workload == TMS:
+        sites = [(cfg["n_features"], cfg["n_hidden"], False), (cfg["n_hidden"], cfg["n_features"], True)]
+    else:
+        sites = [(cfg["d_embed"], cfg["d_mlp"], False), (cfg["d_mlp"], cfg["d_embed"], True)]
+    total = 0
+    for din, dout, dx in sites:
+        i, o = 2 * B * din * cfg["C"], 2 * B * cfg["C"] * dout
+        total += (i + o) + (i * (1 + dx) + 2 * o)
+    return total
+
+
+def toy_cpu_baseline(workload, cfg, reps=5):
+    import numpy as np
+
+    from oracle import toy_oracle as to
+
+    rng = np.random.default_rng(0)
+    if workload == TMS:
+        tc = to.TMSConfig(n_features=cfg["n_features"], n_hidden=cfg["n_hidden"], C=cfg["C"], batch=cfg["B"])
+        target, sites = to.tms_init(tc, rng)
+        x = to.tms_batch(tc, rng)
+        kind = "tms"
+    else:
+        rc = to.ResidMLPConfig(n_features=cfg["n_features"], d_embed=cfg["d_embed"], d_mlp=cfg["d_mlp"], n_layers=1,
+                               C=cfg["C"], batch=cfg["B"])
+        target, sites = to.resid_mlp_init(rc, rng)
+        x = to.resid_mlp_batch(rc, rng)
+        kind = "resid_mlp"
+    run = lambda: to.toy_step(kind, target, sites, x, (0, 1), p=cfg["p"])
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {"value": cfg["B"] / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"the whole {cfg['B']}-row batch, the toy oracle's NumPy float64 restatement of the same step "
+                      f"(BLAS-threaded matmuls), median of {reps} after 1 warmup; {med * 1e3:.2f} ms per step"}
+
+
+def run_toy(args):
+    """The toy decomposition step: clean forward, per-site gate MLPs and CI, Threefry
+    masks (fp32 draws), masked forward, MSE + L_p imp-min, backward through the HIP
+    kernels under torch autograd. Launch-latency bound at these sizes."""
+    import torch
+
+    from param_decomp_amd import hip_events, prng, toys
+
+    cfg = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    if args.workload == TMS:
+        target, sites = toys.init_tms(cfg["n_features"], cfg["n_hidden"], cfg["C"], device=dev, generator=g)
+    else:
+        target, sites = toys.init_resid_mlp(cfg["n_features"], cfg["d_embed"], cfg["d_mlp"], 1, cfg["C"],
+                                            device=dev, generator=g)
+    x = toys.sparse_features(cfg["B"], cfg["n_features"], cfg["p_feat"], cfg["low"], device=dev, generator=g)
+    step = toys.ToyDecompositionStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
+    for i in range(args.warmup):
+        step.step(x, prng.fold_in((0, 0), i))
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        res = step.step(x, prng.fold_in((0, 0), args.warmup + i))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms = hip_events.elapsed_ms(start, stop) / args.steps
+    hip_events.destroy([start, stop])
+    assert torch.isfinite(res["loss"]).all()
+    flops = toy_flops(args.workload, cfg)
+    out = {"tokens": cfg["B"], "ms_per_step": ms,
+           "config": {"workload": args.workload, **{k: v for k, v in cfg.items()}, "dtype": "fp32",
+                      "gate_hidden": 16, "recon": "mse", "mask_draw": "threefry fp32 (partitionable)"},
+           "step_flops": flops, "phases_ms": {"step": ms},
+           "roofline": dict(roofline("flop32", flops, ms, "whole step (fp32; launch-latency bound)", 1),
+                            note="the step is a few dozen small launches; its contractions are microseconds of "
+                                 "fp32 MFMA work")}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = toy_cpu_baseline(args.workload, cfg)
+    return out
 
 
 # ============================================================== Llama-style LM stack
@@ -934,6 +1041,8 @@ def main():
         res = run_moe(args)
     elif args.workload == LLAMA:
         res = run_llama(args)
+    elif args.workload in (TMS, RESID):
+        res = run_toy(args)
     elif args.workload == DENSE:
         res = run_dense(args)
     elif args.workload in (FAITH_DENSE, FAITH_MOE):
@@ -946,6 +1055,7 @@ def main():
         res = run_ci(args)
     ms = res["ms_per_step"]
     faith = args.workload in (FAITH_DENSE, FAITH_MOE)
+    fp32_work = faith or args.workload in (TMS, RESID)
     out = {
         "metric": METRIC,
         "value": res["tokens"] / (ms * 1e-3),
@@ -957,11 +1067,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if faith else "bf16",
+        "dtype": "f32" if fp32_work else "bf16",
         "data": "synthetic (seeded torch.randn / torch.rand of the named shapes; random-init target and components)",
         "config": res["config"],
         "step_tflops": res["step_flops"] / (ms * 1e-3) / 1e12,
-        "step_mfma_frac": res["step_flops"] / (ms * 1e-3) / (PEAK_FP32_MFMA if faith else PEAK_BF16_FLOPS),
+        "step_mfma_frac": res["step_flops"] / (ms * 1e-3) / (PEAK_FP32_MFMA if fp32_work else PEAK_BF16_FLOPS),
         "phases_ms": res["phases_ms"],
         "roofline": res["roofline"],
     }

@@ -33,6 +33,10 @@ def lib():
             ctypes.c_float] * 3 + [f32p] * 4
         _lib.or_dense_step.restype = ctypes.c_int
         _lib.or_num_threads.restype = ctypes.c_int
+        i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+        _lib.or_moe_step.argtypes = [ctypes.c_int] * 7 + [f32p] * 13 + [u32p, u32p, ctypes.c_int] + [
+            ctypes.c_float] * 3 + [f32p] * 8 + [i32p]
+        _lib.or_moe_step.restype = ctypes.c_int
     return _lib
 
 
@@ -67,3 +71,48 @@ def dense_step(x, W, V, U, gate, mask_key, delta_key, *, use_delta=False, bf16_m
     dg = (dgate[:CH].reshape(C, H), dgate[CH:2 * CH].reshape(C, H), dgate[2 * CH:3 * CH].reshape(C, H),
           dgate[3 * CH:])
     return losses, dV, dU, dg
+
+
+def pack_moe(cfg, params, x0, ci_pre, draw_key):
+    """The fp32 arrays `or_moe_step` reads (stacked over layers) and the per-(layer, site)
+    mask and delta keys (partitionable counter layout)."""
+    from oracle import moe_oracle as mo
+
+    f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+    L = cfg.L
+    st = {n: f32(np.stack([P[n] for P in params])) for n in ("ln", "router", "Wg", "Wu", "Wd", "Vg", "Ug", "Vu",
+                                                               "Uu", "Vd", "Ud")}
+    st["x0"] = f32(x0)
+    st["ci"] = f32(np.stack([np.stack([ci_pre[l][s] for s in mo.SITES]) for l in range(L)]))
+    st["mkeys"] = np.array([[mo.site_mask_keys(draw_key, l)[s] for s in mo.SITES] for l in range(L)],
+                           np.uint32).reshape(-1)
+    st["dkeys"] = np.array([[mo.site_delta_keys(draw_key, l)[s] for s in mo.SITES] for l in range(L)],
+                           np.uint32).reshape(-1)
+    return st
+
+
+def run_moe(cfg, st, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0, use_delta=True):
+    """`or_moe_step` on packed inputs; returns dict(loss, recon, imp, grads, d_ci_pre, top_idx)."""
+    from oracle import moe_oracle as mo
+
+    T, d, f, E, k, c, L = cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L
+    losses = np.zeros(3, np.float32)
+    g = {n: np.zeros(st[n].shape, np.float32) for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud")}
+    d_ci = np.zeros_like(st["ci"])
+    top = np.zeros((L, T, k), np.int32)
+    rc = lib().or_moe_step(T, d, f, E, k, c, L, st["x0"], st["ln"], st["router"], st["Wg"], st["Wu"], st["Wd"],
+                           st["Vg"], st["Ug"], st["Vu"], st["Uu"], st["Vd"], st["Ud"], st["ci"], st["mkeys"],
+                           st["dkeys"], int(use_delta), p, imp_coeff, recon_coeff, losses, g["Vg"], g["Ug"], g["Vu"],
+                           g["Uu"], g["Vd"], g["Ud"], d_ci, top)
+    assert rc == 0
+    grads = [{n: g[n][l] for n in g} for l in range(L)]
+    return dict(loss=float(losses[0]), recon=float(losses[1]), imp=float(losses[2]), grads=grads,
+                d_ci_pre=[{s: d_ci[l, i] for i, s in enumerate(mo.SITES)} for l in range(L)], top_idx=top)
+
+
+def moe_step(cfg, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0, use_delta=True):
+    """Runs `or_moe_step` (the fp32 C restatement of oracle.moe_oracle.moe_stack_step
+    without the bf16 storage model; partitionable counter layout). params / ci_pre as
+    moe_stack_step takes them."""
+    return run_moe(cfg, pack_moe(cfg, params, x0, ci_pre, draw_key), p=p, imp_coeff=imp_coeff,
+                   recon_coeff=recon_coeff, use_delta=use_delta)

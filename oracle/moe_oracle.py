@@ -303,3 +303,94 @@ def init_moe(cfg: MoEConfig, rng):
     x0 = rn(cfg.T, d)
     ci = [{s: rng.uniform(-0.3, 1.3, size=(cfg.T, cfg.k, c)) for s in SITES} for _ in range(cfg.L)]
     return params, x0, ci
+
+
+def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
+                         use_delta=True, partitionable=True, dtype=None, threads=None):
+    """The same step as `moe_stack_step` (no bf16 storage model) in torch on the CPU, its
+    backward by autograd: the CPU baseline's timing form in fp32 (`dtype`
+    torch.float32; the default float64 is what pins it to `moe_stack_step`). The expert
+    selection and Threefry draws are computed as in `moe_stack_step` (integer and
+    bit-level work, outside autograd). Returns dict(loss, recon, imp, grads, d_ci_pre,
+    top_idx)."""
+    import torch
+
+    if threads:
+        torch.set_num_threads(threads)
+    dt = dtype or torch.float64
+    T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
+    t = lambda a, g=False: torch.tensor(np.asarray(a, np.float64), dtype=dt, requires_grad=g)  # noqa: E731
+
+    def norm(x, w):
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + cfg.eps) * (1.0 + w)
+
+    def gmm(lhs, rhs, offs):
+        return torch.cat([lhs[offs[e]:offs[e + 1]] @ rhs[e] for e in range(E)], 0)
+
+    P = [{n: t(v, n[0] in "VU") for n, v in layer.items()} for layer in params]
+    pre = [{s: t(ci_pre[l][s], True) for s in SITES} for l in range(cfg.L)]
+    # clean pass: the expert selection (no gradient)
+    with torch.no_grad():
+        rc = t(x0)
+        tops = []
+        for l in range(cfg.L):
+            h2 = norm(rc, P[l]["ln"])
+            probs = torch.softmax(h2 @ P[l]["router"].T, -1)
+            idx = po.select_experts(probs.double().numpy(), k)
+            tops.append(idx)
+            jobs = po.routed_jobs(idx, E)
+            offs = np.concatenate([[0], np.cumsum(jobs.group_sizes)]).tolist()
+            xj = h2[torch.as_tensor(jobs.sort_idx // k, dtype=torch.long)]
+            din = torch.nn.functional.silu(gmm(xj, P[l]["Wg"], offs)) * gmm(xj, P[l]["Wu"], offs)
+            down = gmm(din, P[l]["Wd"], offs)
+            w = torch.gather(probs, 1, torch.as_tensor(idx, dtype=torch.long))
+            w = w / w.sum(-1, keepdim=True)
+            inv = torch.as_tensor(jobs.inv_sort_idx, dtype=torch.long)
+            rc = rc + (down[inv].reshape(T, k, -1) * w[..., None]).sum(1)
+    r = t(x0)
+    imp = 0.0
+    for l in range(cfg.L):
+        h2 = norm(r, P[l]["ln"])
+        probs = torch.softmax(h2 @ P[l]["router"].T, -1)
+        idx = torch.as_tensor(tops[l], dtype=torch.long)
+        w = torch.gather(probs, 1, idx)
+        w = w / w.sum(-1, keepdim=True)
+        jobs = po.routed_jobs(tops[l], E)
+        offs = np.concatenate([[0], np.cumsum(jobs.group_sizes)]).tolist()
+        sidx = torch.as_tensor(jobs.sort_idx, dtype=torch.long)
+        tok = sidx // k
+        xj = h2[tok]
+        keys, dkeys = site_mask_keys(draw_key, l, partitionable), site_delta_keys(draw_key, l, partitionable)
+        coef = {}
+        for s in SITES:
+            lo = pre[l][s].clamp(0.0, 1.0)  # forward of the lower leaky hard sigmoid
+            up = torch.where(pre[l][s] > 1.0, 1.0 + 0.01 * (pre[l][s] - 1.0), pre[l][s].clamp(0.0, 1.0))
+            imp = imp + (up**p).sum() / T
+            u = t(tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c))
+            dlt = (t(tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)) if use_delta
+                   else torch.zeros(T, dtype=dt))
+            m = (lo + (1.0 - lo) * u).reshape(T * k, c)[sidx]
+            coef[s] = (m - dlt[tok][:, None], dlt[tok][:, None])
+        wj = w.reshape(-1)[sidx]
+        out = {}
+        for s in ("gate", "up"):
+            acts = gmm(xj, P[l]["V" + s[0]], offs) * coef[s][0]
+            out[s] = gmm(acts, P[l]["U" + s[0]], offs) + coef[s][1] * gmm(xj, P[l]["W" + s[0]], offs)
+        din = torch.nn.functional.silu(out["gate"]) * out["up"] * wj[:, None]
+        acts = gmm(din, P[l]["Vd"], offs) * coef["down"][0]
+        dout = gmm(acts, P[l]["Ud"], offs) + coef["down"][1] * gmm(din, P[l]["Wd"], offs)
+        inv = torch.as_tensor(jobs.inv_sort_idx, dtype=torch.long)
+        r = r + dout[inv].reshape(T, k, -1).sum(1)
+    recon = ((r - rc) ** 2).mean()
+    loss = recon_coeff * recon + imp_coeff * imp
+    names = [(l, n) for l in range(cfg.L) for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud")]
+    wrt = [P[l][n] for l, n in names] + [pre[l][s] for l in range(cfg.L) for s in SITES]
+    g = torch.autograd.grad(loss, wrt)
+    grads = [dict() for _ in range(cfg.L)]
+    for (l, n), v in zip(names, g[:len(names)]):
+        grads[l][n] = v.double().numpy()
+    d_ci = [dict() for _ in range(cfg.L)]
+    for i, (l, s) in enumerate((l, s) for l in range(cfg.L) for s in SITES):
+        d_ci[l][s] = g[len(names) + i].double().numpy()
+    return dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()), grads=grads,
+                d_ci_pre=d_ci, top_idx=tops)

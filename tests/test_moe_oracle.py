@@ -213,3 +213,47 @@ def test_pinned_routing_reproduces_the_oracles_own_step():
     for l in range(cfg.L):
         np.testing.assert_array_equal(a["top_idx"][l], b["top_idx"][l])
         np.testing.assert_array_equal(a["grads"][l]["Vd"], b["grads"][l]["Vd"])
+
+
+def test_torch_restatement_matches_the_numpy_oracle():
+    """The torch (autograd) restatement used for the CPU baseline equals the NumPy
+    oracle's hand-written backward in float64: loss, every V/U gradient and the CI
+    preactivation gradients (CI kept away from the squashing kinks, where the torch
+    form's plain clamp derivative and the reference's custom lower VJP agree)."""
+    cfg = mo.MoEConfig(T=48, d=16, f=8, E=6, k=2, c=4, L=2)
+    rng = np.random.default_rng(11)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.5, recon_coeff=1.5)
+    b = mo.moe_stack_step_torch(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.5, recon_coeff=1.5)
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-10)
+    for l in range(cfg.L):
+        np.testing.assert_array_equal(a["top_idx"][l], b["top_idx"][l])
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            np.testing.assert_allclose(b["grads"][l][n], a["grads"][l][n], rtol=1e-8, atol=1e-12)
+        for s in mo.SITES:
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
+
+
+def test_c_restatement_matches_the_numpy_oracle():
+    """The compiled fp32 C/OpenMP restatement (the CPU baseline) against the NumPy
+    oracle in float64: same expert selection, losses and every gradient to fp32
+    precision (CI away from the squashing kinks)."""
+    from oracle import cpu
+
+    cfg = mo.MoEConfig(T=64, d=32, f=16, E=7, k=3, c=8, L=2)
+    rng = np.random.default_rng(12)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.5, recon_coeff=1.5)
+    b = cpu.moe_step(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.5, recon_coeff=1.5)
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-5)
+    assert b["recon"] == pytest.approx(a["recon"], rel=1e-4)
+    for l in range(cfg.L):
+        np.testing.assert_array_equal(b["top_idx"][l], a["top_idx"][l])
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            w = a["grads"][l][n]
+            np.testing.assert_allclose(b["grads"][l][n], w, rtol=2e-4, atol=2e-5 * np.abs(w).max())
+        for s in mo.SITES:
+            w = a["d_ci_pre"][l][s]
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], w, rtol=2e-4, atol=2e-5 * np.abs(w).max())
