@@ -108,6 +108,65 @@ def rocprof_summary(db_path: str, command: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def rocprof_csv_summary(stats_csv: str, command: str) -> str:
+    """The per-kernel table of a rocprofv3 `--kernel-trace --stats` run's
+    `*_kernel_stats.csv` (calls, total/avg/min/max us, share)."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    total = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+    out = [f"command: `{command}`", "", "| kernel | calls | total us | avg us | min us | max us | % |",
+           "|---|---|---|---|---|---|---|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        short = r["Name"].split("(")[0].replace("void ", "")
+        out.append(f"| `{short}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e3:.1f} | "
+                   f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                   f"{float(r['MaxNs']) / 1e3:.2f} | {100 * float(r['TotalDurationNs']) / total:.1f} |")
+    return "\n".join(out) + "\n"
+
+
+def pmc_mfma_summary(csv1: str, csv2: str, command: str, n_xcd: int = 8, n_simd: int = 1024) -> str:
+    """Per-kernel MFMA utilisation and instruction mix from two `--pmc` runs' counter
+    CSVs: run 1 SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CU_CYCLES, GRBM_GUI_ACTIVE; run 2
+    SQ_INSTS_MFMA, SQ_INSTS_LDS, SQ_WAIT_INST_ANY, SQ_WAVE_CYCLES, SQ_INSTS_VALU.
+    MFMA utilisation = MFMA busy cycles over (GPU-active cycles per XCD x SIMDs):
+    GRBM_GUI_ACTIVE is summed over the 8 XCDs, and MI355X has 256 CUs x 4 SIMDs."""
+    import collections
+    import csv
+
+    def load(path):
+        per = collections.defaultdict(lambda: collections.defaultdict(float))
+        name = {}
+        for r in csv.DictReader(open(path)):
+            d = int(r["Dispatch_Id"])
+            per[d][r["Counter_Name"]] += float(r["Counter_Value"])
+            per[d]["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            name[d] = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        agg = collections.defaultdict(lambda: collections.defaultdict(float))
+        for d, v in per.items():
+            for c, x in v.items():
+                agg[name[d]][c] += x
+            agg[name[d]]["calls"] += 1
+        return agg
+
+    a, b = load(csv1), load(csv2)
+    out = [f"command: `{command}`", "",
+           "| kernel | calls | avg us | MFMA util % | MFMA insts / call | LDS insts / MFMA | VALU insts / MFMA | "
+           "wave cycles waiting % |", "|---|---|---|---|---|---|---|---|"]
+    for n, v in sorted(a.items(), key=lambda kv: -kv[1]["ns"]):
+        w = b.get(n, {})
+        mf = w.get("SQ_INSTS_MFMA", 0.0)
+        if not mf and not v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0):
+            continue
+        util = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (v["GRBM_GUI_ACTIVE"] / n_xcd * n_simd) if v["GRBM_GUI_ACTIVE"] else 0
+        calls = int(v["calls"])
+        out.append(f"| `{n}` | {calls} | {v['ns'] / calls / 1e3:.1f} | {100 * util:.1f} | "
+                   f"{mf / max(w.get('calls', 1), 1):.3g} | {w.get('SQ_INSTS_LDS', 0) / mf if mf else 0:.2f} | "
+                   f"{w.get('SQ_INSTS_VALU', 0) / mf if mf else 0:.2f} | "
+                   f"{100 * w.get('SQ_WAIT_INST_ANY', 0) / max(w.get('SQ_WAVE_CYCLES', 1), 1):.0f} |")
+    return "\n".join(out) + "\n"
+
+
 # The kernel behind each phase, as named in profiles/hbm_traffic_pmc.md (a prefix of the
 # demangled name: the phases of one kernel template share its per-dispatch average).
 # Kernels of a timed phase (name prefixes as rocprofv3 prints them). A phase's traffic per
@@ -1021,6 +1080,14 @@ def main():
     if "--rocprof-summary" in sys.argv:
         i = sys.argv.index("--rocprof-summary")
         print(rocprof_summary(sys.argv[i + 1], sys.argv[i + 2]))
+        return
+    if "--rocprof-csv-summary" in sys.argv:
+        i = sys.argv.index("--rocprof-csv-summary")
+        print(rocprof_csv_summary(sys.argv[i + 1], sys.argv[i + 2]))
+        return
+    if "--pmc-mfma-summary" in sys.argv:
+        i = sys.argv.index("--pmc-mfma-summary")
+        print(pmc_mfma_summary(sys.argv[i + 1], sys.argv[i + 2], sys.argv[i + 3]))
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)

@@ -307,12 +307,11 @@ def init_moe(cfg: MoEConfig, rng):
 
 def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                          use_delta=True, partitionable=True, dtype=None, threads=None):
-    """The same step as `moe_stack_step` (no bf16 storage model) in torch on the CPU, its
-    backward by autograd: the CPU baseline's timing form in fp32 (`dtype`
-    torch.float32; the default float64 is what pins it to `moe_stack_step`). The expert
-    selection and Threefry draws are computed as in `moe_stack_step` (integer and
-    bit-level work, outside autograd). Returns dict(loss, recon, imp, grads, d_ci_pre,
-    top_idx)."""
+    """The same step as `moe_stack_step` (no bf16 storage model) written as a torch
+    forward whose backward is torch autograd: in float64 it pins `moe_stack_step`'s
+    hand-written backward (tests/test_moe_oracle.py). The expert selection and Threefry
+    draws are computed as in `moe_stack_step` (integer and bit-level work, outside
+    autograd). Returns dict(loss, recon, imp, grads, d_ci_pre, top_idx)."""
     import torch
 
     if threads:
