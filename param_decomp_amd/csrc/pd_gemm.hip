@@ -287,10 +287,10 @@ static bool bf16_operand_ok(const void* ptr, int64_t ld, int64_t contig_extent) 
 // The big tile needs enough tiles to occupy the 256 CUs; otherwise use the small one.
 static bool use_big_tile(int64_t M, int64_t N) { return cdiv(M, 256) * cdiv(N, 256) >= 192; }
 
-template <class CFG, int MODE>
+template <class CFG, int MODE, bool AMN = false, bool BMN = false>
 static int launch_dtl(const GemmArgs& a, int c_dtype, bool kedge, dim3 grid, hipStream_t s) {
 #define PD_L(TC, KE) \
-  hipLaunchKernelGGL((k_gemm_dtl<CFG, TC, MODE, KE>), grid, dim3(CFG::NT), 0, s, a, EpiStore::Args{})
+  hipLaunchKernelGGL((k_gemm_dtl<CFG, TC, MODE, KE, EpiStore, AMN, BMN>), grid, dim3(CFG::NT), 0, s, a, EpiStore::Args{})
   if (c_dtype == PD_DTYPE_F32) {
     if (kedge) PD_L(float, true);
     else PD_L(float, false);
@@ -300,6 +300,22 @@ static int launch_dtl(const GemmArgs& a, int c_dtype, bool kedge, dim3 grid, hip
   }
 #undef PD_L
   return check_launch("pd_gemm bf16 (buffer-fed)");
+}
+
+// Any operand layout through the buffer-fed kernel (a_kmaj / b_kmaj: K-contiguous).
+template <class CFG, int MODE>
+static int launch_dtl_any(const GemmArgs& a, bool a_kmaj, bool b_kmaj, int c_dtype, bool kedge, dim3 grid,
+                          hipStream_t s) {
+  if (a_kmaj && b_kmaj) return launch_dtl<CFG, MODE, false, false>(a, c_dtype, kedge, grid, s);
+  if (a_kmaj) return launch_dtl<CFG, MODE, false, true>(a, c_dtype, kedge, grid, s);
+  if (b_kmaj) return launch_dtl<CFG, MODE, true, false>(a, c_dtype, kedge, grid, s);
+  return launch_dtl<CFG, MODE, true, true>(a, c_dtype, kedge, grid, s);
+}
+
+// Every operand of the buffer-fed kernel within its 31-bit addressing range.
+static bool dtl_fits_any(int64_t M, int64_t N, int64_t K, int64_t lda, bool a_kmaj, int64_t ldb, bool b_kmaj) {
+  return (a_kmaj ? M * lda * 2 <= 0x7FFFFFFF : dtl_fits_mn(K, lda)) &&
+         (b_kmaj ? N * ldb * 2 <= 0x7FFFFFFF : dtl_fits_mn(K, ldb));
 }
 
 }  // namespace pd
@@ -326,9 +342,10 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
   if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N))
     return fail(PD_EUNSUPPORTED, "pd_gemm: bf16 operands need 16B alignment and contiguous dims / ld % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, 0, 0};
-  if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
-    return launch_dtl<CfgDtlRA, MODE_DENSE>(a, c_dtype, K % CfgDtlRA::BK != 0,
-                                            dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM)), s);
+  if (dtl_fits_any(M, N, K, lda, a_kmaj, ldb, b_kmaj))
+    return launch_dtl_any<CfgDtlRA, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype, K % CfgDtlRA::BK != 0,
+                                                dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM)),
+                                                s);
   if (use_big_tile(M, N))
     return launch_bf16<CfgBig, MODE_DENSE>(a, a_kmaj, b_kmaj, c_dtype,
                                            dim3((unsigned)cdiv(N, 256), (unsigned)cdiv(M, 256)), s);
@@ -361,9 +378,9 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
                 "pd_gemm_strided_batched: bf16 operands need 16B alignment, ld and batch strides % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, stride_b,
              stride_c, stride_a};
-  if (a_kmaj && b_kmaj && dtl_fits(M, lda, N, ldb))
-    return launch_dtl<CfgDtlRA, MODE_BATCHED>(
-        a, c_dtype, K % CfgDtlRA::BK != 0,
+  if (dtl_fits_any(M, N, K, lda, a_kmaj, ldb, b_kmaj))
+    return launch_dtl_any<CfgDtlRA, MODE_BATCHED>(
+        a, a_kmaj, b_kmaj, c_dtype, K % CfgDtlRA::BK != 0,
         dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)batch),
         s);
   return launch_bf16<CfgSmall, MODE_BATCHED>(
@@ -401,6 +418,8 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
   static_assert(CfgDtlRA::BM == CfgSmall::BM && CfgDtlRA::BN == CfgSmall::BN, "one grid shape for both kernels");
   if (b_kmaj && dtl_fits(J, K, N, K))
     return launch_dtl<CfgDtlRA, MODE_GROUPED>(a, out_dtype, K % CfgDtlRA::BK != 0, grid, s);
+  if (!b_kmaj && dtl_fits(J, K, 0, 0) && dtl_fits_mn(K, N))  // each expert's rhs stored [K][N]
+    return launch_dtl<CfgDtlRA, MODE_GROUPED, false, true>(a, out_dtype, K % CfgDtlRA::BK != 0, grid, s);
   return launch_bf16<CfgSmall, MODE_GROUPED>(a, true, b_kmaj, out_dtype, grid, s);
 }
 
@@ -517,6 +536,9 @@ int pd_grouped_gemm_dw(const void* lhs, const void* dout, const int32_t* offsets
   // out[e] (M=K_in x N) = lhs[rows_e]^T (A stored [J,K]: M-contiguous) @ dout[rows_e] ([J,N])
   GemmArgs a{K, N, J, (const bf16_t*)lhs, K, (const bf16_t*)dout, N, out, N, 1.f, 0.f, offsets, E, 0, K * N};
   dim3 grid((unsigned)cdiv(N, CfgSmall::BN), (unsigned)cdiv(K, CfgSmall::BM), (unsigned)E);
+  static_assert(CfgDtlRA::BM == CfgSmall::BM && CfgDtlRA::BN == CfgSmall::BN, "one grid shape for both kernels");
+  if (dtl_fits_mn(J, K) && dtl_fits_mn(J, N))  // both operands MN-major: rows of lhs / dout are k
+    return launch_dtl<CfgDtlRA, MODE_GROUPED_K, true, true>(a, out_dtype, true, grid, (hipStream_t)stream);
   return launch_bf16<CfgSmall, MODE_GROUPED_K>(a, false, false, out_dtype, grid, (hipStream_t)stream);
 }
 

@@ -25,6 +25,19 @@
 //
 // Ragged contraction groups start at an 8-aligned k below the group's first row; k
 // outside [kmin, kend) is zeroed in the fragments of a tile's first and last stage.
+//
+// MN-major operands (stored [K][rows], rows contiguous: the B of x @ V and acts @ U, both
+// operands of a weight gradient x^T @ g). A stage of such an operand holds its 64 k-rows
+// of R = BM (or BN) elements, 2R bytes each; the 16-byte chunk c of k-row r sits at
+// physical chunk c ^ (4 * (r & 3)). One 1 KB load moves 1024 / 2R whole k-rows (lane l
+// writes physical chunk l % (R / 8) of k-row l / (R / 8)). Fragments come out of LDS
+// already transposed by ds_read_b64_tr_b16: within each 16-lane group, output lane
+// 4a + b receives element b of the 8 bytes read by source lanes a, a + 4, a + 8, a + 12.
+// Source lane 16g + 4e + a reads k-row 8 (g >> 1) + 4h + e (h = 0, 1: the fragment's two
+// halves), elements 16 (g & 1) + 4a .. + 3 of the fragment's 32 rows, so output lane l
+// holds rows l & 31 at k 8 (l >> 5) + 4h .. + 3: the same fragment the K-major path reads
+// with one ds_read_b128. The four k-rows one 16-lane group reads (r & 3 = e = 0..3) sit in
+// four distinct 64-byte bank groups, so a half-wave's 256 bytes are conflict-free.
 #pragma once
 
 #include <type_traits>
@@ -298,10 +311,13 @@ typedef DtlCfg<128, 128, 4, 2, 2, true> CfgDtlRA;
 // bytes per MFMA; faster for the paired N=512 products and the paired weight gradients.
 typedef DtlCfg<256, 256, 4, 2, 2> CfgDtlBig;
 
-// The kernel addresses each operand through a 31-bit buffer record count.
+// The kernel addresses each operand through a 31-bit buffer record count (rows = M or N
+// for a K-major operand; for an MN-major one, K plus the 128 k-rows a last stage may
+// reach past it).
 inline bool dtl_fits(int64_t rows_a, int64_t lda, int64_t rows_b, int64_t ldb) {
   return rows_a * lda * 2 <= 0x7FFFFFFF && rows_b * ldb * 2 <= 0x7FFFFFFF;
 }
+inline bool dtl_fits_mn(int64_t K, int64_t ld) { return (K + 128) * ld * 2 <= 0x7FFFFFFF; }
 
 // Record count (bytes) of a raw buffer descriptor, clamped to the 31-bit range (the
 // launchers keep every operand below 2 GiB).
@@ -323,6 +339,68 @@ __device__ inline void dtl_offsets(uint32_t (&off)[ROWS / (8 * NW)], int64_t ld,
     off[q] = (uint32_t)((row * ld + c * 8) * 2);
   }
 }
+
+// Per-lane byte offsets of a wave's 1 KB loads of an MN-major operand tile (R elements
+// per k-row, relative to the tile's first column, k = 0): load q covers k-rows
+// (q * NW + wave) * RPL .. + RPL - 1; lane l fills physical chunk l % CPR of k-row l / CPR.
+template <int R, int NW>
+__device__ inline void dtl_offsets_mn(uint32_t (&off)[R / (8 * NW)], int64_t ld, int wave, int lane) {
+  static_assert(R >= 128 && R <= 512, "an MN-major tile row is 256..1024 bytes");
+  constexpr int CPR = R / 8, RPL = 1024 / (2 * R);
+  const int rsub = lane / CPR, pc = lane % CPR;
+#pragma unroll
+  for (int q = 0; q < R / (8 * NW); ++q) {
+    const int64_t row = (int64_t)(q * NW + wave) * RPL + rsub;
+    const int c = pc ^ (4 * (int)(row & 3));
+    off[q] = (uint32_t)((row * ld + c * 8) * 2);
+  }
+}
+
+// LDS byte offset (within the operand's stage region, kk = 0, first half) of the
+// transposing reads of fragment i of an MN-major tile of R elements per k-row; wave_r =
+// the wave tile's first element within the block tile (a multiple of 32).
+template <int R>
+__device__ inline int mn_frag_off(int wave_r, int i, int lane) {
+  constexpr int RB = 2 * R;
+  const int g = lane >> 4, e = (lane >> 2) & 3, a = lane & 3;
+  const int c = ((wave_r >> 3) + 4 * i) ^ (4 * e);
+  return (8 * (g >> 1) + e) * RB + (c + 2 * (g & 1) + (a >> 1)) * 16 + (a & 1) * 8;
+}
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t* lds_v4i16_ptr;
+
+// One fragment (rows lane & 31, k 8 (lane >> 5) .. + 7 of k16 step kk): MN: two transposing
+// 8-byte reads; K-major: one 16-byte read at the lane's swizzled chunk coff.
+template <bool MN, int R>
+__device__ inline bf16x8 frag_load(const char* st, int off, int kk, int coff) {
+  if constexpr (MN) {
+    constexpr int RB = 2 * R;
+    const char* q = st + off + kk * 16 * RB;
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(q));
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(q + 4 * RB));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  } else {
+    return *(const bf16x8*)(st + off + coff);
+  }
+}
+
+// A wave's fragment offsets within a stage (A region first, then B), per operand layout.
+template <class CFG, bool AMN, bool BMN>
+struct FragOffs {
+  int a[CFG::TM], b[CFG::TN];
+  int sw;
+  __device__ inline FragOffs(int wm, int wn, int lane) {
+    sw = dtl_swz(lane & 31);  // K-major fragment rows sit at multiples of 32 plus lane & 31
+#pragma unroll
+    for (int i = 0; i < CFG::TM; ++i)
+      a[i] = AMN ? mn_frag_off<CFG::BM>(wm * CFG::WTM, i, lane) : (wm * CFG::WTM + i * 32 + (lane & 31)) * CFG::ROWB;
+#pragma unroll
+    for (int j = 0; j < CFG::TN; ++j)
+      b[j] = CFG::BM * CFG::ROWB +
+             (BMN ? mn_frag_off<CFG::BN>(wn * CFG::WTN, j, lane) : (wn * CFG::WTN + j * 32 + (lane & 31)) * CFG::ROWB);
+  }
+};
 
 // One stage of one operand at byte offset koff (the stage's k position) within each
 // row. The descriptor spans [base, base + bytes) (stride 0); the whole offset goes in the
@@ -385,14 +463,14 @@ __device__ inline void store1<bf16_t>(bf16_t* C, int64_t idx, float v, float bet
 }
 
 // Fragment reads of k16 step kk of a stage; EDGE zeroes k outside [kmin, kend).
-template <class CFG, bool EDGE>
-__device__ inline void dtl_read(const char* st, int a_off, int b_off, int sw, int lane, int kk, int64_t k0,
+template <class CFG, bool EDGE, bool AMN, bool BMN>
+__device__ inline void dtl_read(const char* st, const FragOffs<CFG, AMN, BMN>& fo, int lane, int kk, int64_t k0,
                                 int64_t kmin, int64_t kend, bf16x8 (&af)[CFG::TM], bf16x8 (&bfr)[CFG::TN]) {
-  const int coff = ((2 * kk + (lane >> 5)) ^ sw) << 4;
+  const int coff = ((2 * kk + (lane >> 5)) ^ fo.sw) << 4;
 #pragma unroll
-  for (int i = 0; i < CFG::TM; ++i) af[i] = *(const bf16x8*)(st + a_off + i * 32 * CFG::ROWB + coff);
+  for (int i = 0; i < CFG::TM; ++i) af[i] = frag_load<AMN, CFG::BM>(st, fo.a[i], kk, coff);
 #pragma unroll
-  for (int j = 0; j < CFG::TN; ++j) bfr[j] = *(const bf16x8*)(st + b_off + j * 32 * CFG::ROWB + coff);
+  for (int j = 0; j < CFG::TN; ++j) bfr[j] = frag_load<BMN, CFG::BN>(st, fo.b[j], kk, coff);
   if (EDGE) {
     const int64_t kf = k0 + kk * 16 + (lane >> 5) * 8;
 #pragma unroll
@@ -414,26 +492,26 @@ __device__ inline void dtl_mfma(const bf16x8 (&af)[CFG::TM], const bf16x8 (&bfr)
 
 // Consumes one 64-k stage (4 k16 steps), reading step kk+1's fragments ahead of step
 // kk's MFMAs.
-template <class CFG, bool EDGE>
-__device__ inline void dtl_stage(const char* st, int a_off, int b_off, int sw, int lane, int64_t k0, int64_t kmin,
-                                 int64_t kend, f32x16 (&acc)[CFG::TM][CFG::TN]) {
+template <class CFG, bool EDGE, bool AMN, bool BMN>
+__device__ inline void dtl_stage(const char* st, const FragOffs<CFG, AMN, BMN>& fo, int lane, int64_t k0,
+                                 int64_t kmin, int64_t kend, f32x16 (&acc)[CFG::TM][CFG::TN]) {
   constexpr int TM = CFG::TM, TN = CFG::TN, KK = CFG::KK;
   if constexpr (CFG::READ_ALL) {
     // every fragment of the stage in flight at once; each MFMA then waits only for its
     // own reads, so the LDS latency of later steps hides behind earlier MFMAs
     bf16x8 af[KK][TM], bfr[KK][TN];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk, k0, kmin, kend, af[kk], bfr[kk]);
+    for (int kk = 0; kk < KK; ++kk) dtl_read<CFG, EDGE>(st, fo, lane, kk, k0, kmin, kend, af[kk], bfr[kk]);
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) dtl_mfma<CFG>(af[kk], bfr[kk], acc);
     return;
   }
   bf16x8 af[2][TM], bfr[2][TN];
-  dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, 0, k0, kmin, kend, af[0], bfr[0]);
+  dtl_read<CFG, EDGE>(st, fo, lane, 0, k0, kmin, kend, af[0], bfr[0]);
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
     if (kk + 1 < KK)
-      dtl_read<CFG, EDGE>(st, a_off, b_off, sw, lane, kk + 1, k0, kmin, kend, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
+      dtl_read<CFG, EDGE>(st, fo, lane, kk + 1, k0, kmin, kend, af[(kk + 1) & 1], bfr[(kk + 1) & 1]);
     dtl_mfma<CFG>(af[kk & 1], bfr[kk & 1], acc);
   }
 }
@@ -484,7 +562,10 @@ struct EpiStore {
 // are peeled off the main loop, which then has a single body: a branch between a masked
 // and a plain stage inside the loop makes the compiler shuttle the accumulators between
 // AGPRs and VGPRs on every iteration.
-template <class CFG, typename TC, int MODE, bool KEDGE, class EPI = EpiStore>
+//
+// AMN / BMN: A (or B) is MN-major, stored [K][M] (or [K][N]) with leading dimension lda
+// (ldb) between k-rows.
+template <class CFG, typename TC, int MODE, bool KEDGE, class EPI = EpiStore, bool AMN = false, bool BMN = false>
 __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::Args ea) {
   constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
   constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
@@ -500,12 +581,20 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
   const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
   const int64_t kbeg = kmin & ~(int64_t)7;
   const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
-  const bf16_t* abase = (const bf16_t*)uni64((int64_t)(t.A + m0 * p.lda));
-  const bf16_t* bbase = (const bf16_t*)uni64((int64_t)(t.B + n0 * p.ldb));
-  const int32_t abytes = buf_bytes((p.M - m0) * p.lda * 2), bbytes = buf_bytes((p.N - n0) * p.ldb * 2);
+  // a K-major tile starts at its first row, an MN-major one at its first column; either
+  // descriptor ends at the operand's end (rows past M / N, or k-rows past K, load zeros;
+  // an MN-major tile's columns past M / N only feed outputs that are never stored)
+  const bf16_t* abase = (const bf16_t*)uni64((int64_t)(AMN ? t.A + m0 : t.A + m0 * p.lda));
+  const bf16_t* bbase = (const bf16_t*)uni64((int64_t)(BMN ? t.B + n0 : t.B + n0 * p.ldb));
+  const int32_t abytes = buf_bytes(AMN ? (p.K * p.lda - m0) * 2 : (p.M - m0) * p.lda * 2);
+  const int32_t bbytes = buf_bytes(BMN ? (p.K * p.ldb - n0) * 2 : (p.N - n0) * p.ldb * 2);
   uint32_t offa[CFG::A_INSTS], offb[CFG::B_INSTS];
-  dtl_offsets<BM, NW>(offa, p.lda, wave, lane);
-  dtl_offsets<BN, NW>(offb, p.ldb, wave, lane);
+  if constexpr (AMN) dtl_offsets_mn<BM, NW>(offa, p.lda, wave, lane);
+  else dtl_offsets<BM, NW>(offa, p.lda, wave, lane);
+  if constexpr (BMN) dtl_offsets_mn<BN, NW>(offb, p.ldb, wave, lane);
+  else dtl_offsets<BN, NW>(offb, p.ldb, wave, lane);
+  // a stage's k position as a byte offset: along the row (K-major) or down k-rows (MN)
+  const uint32_t kstep_a = AMN ? (uint32_t)(p.lda * 2) : 2u, kstep_b = BMN ? (uint32_t)(p.ldb * 2) : 2u;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -517,18 +606,16 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
 
   auto issue = [&](int64_t kt) {
     char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    const uint32_t koff = (uint32_t)((kbeg + kt * BK) * 2);
-    dtl_issue<BM, NW>(st, abase, abytes, offa, koff, wave);
-    dtl_issue<BN, NW>(st + BM * ROWB, bbase, bbytes, offb, koff, wave);
+    const uint32_t kpos = (uint32_t)(kbeg + kt * BK);
+    dtl_issue<BM, NW>(st, abase, abytes, offa, kpos * kstep_a, wave);
+    dtl_issue<BN, NW>(st + BM * ROWB, bbase, bbytes, offb, kpos * kstep_b, wave);
   };
 
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
 
-  const int sw = dtl_swz(lane & 31);  // fragment rows sit at multiples of 32 plus lane & 31
-  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
-  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
+  const FragOffs<CFG, AMN, BMN> fo(wm, wn, lane);
   auto sync = [&](int64_t kt) {  // stage kt has landed and is visible; stage kt+NS-1 goes out
     const int64_t left = nk - 1 - kt;
     wait_stages<CFG::INSTS, NS - 2>((int)(left < NS - 2 ? left : NS - 2));
@@ -539,20 +626,20 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
   if constexpr (KEDGE) {
     if (nk > 0) {
       sync(0);
-      dtl_stage<CFG, true>(st_of(0), a_off, b_off, sw, lane, kbeg, kmin, kend, acc);
+      dtl_stage<CFG, true>(st_of(0), fo, lane, kbeg, kmin, kend, acc);
     }
     for (int64_t kt = 1; kt < nk - 1; ++kt) {
       sync(kt);
-      dtl_stage<CFG, false>(st_of(kt), a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
+      dtl_stage<CFG, false>(st_of(kt), fo, lane, kbeg + kt * BK, kmin, kend, acc);
     }
     if (nk > 1) {
       sync(nk - 1);
-      dtl_stage<CFG, true>(st_of(nk - 1), a_off, b_off, sw, lane, kbeg + (nk - 1) * BK, kmin, kend, acc);
+      dtl_stage<CFG, true>(st_of(nk - 1), fo, lane, kbeg + (nk - 1) * BK, kmin, kend, acc);
     }
   } else {
     for (int64_t kt = 0; kt < nk; ++kt) {
       sync(kt);
-      dtl_stage<CFG, false>(st_of(kt), a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
+      dtl_stage<CFG, false>(st_of(kt), fo, lane, kbeg + kt * BK, kmin, kend, acc);
     }
   }
   EPI::template run<CFG, TC>(p, ea, t, wm, wn, tid, acc, smem);
@@ -608,11 +695,12 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
   };
   if (nk > 0) issue(0);
 
-  const int sw = dtl_swz(lane & 31);
-  const int a_off = (wm * CFG::WTM + (lane & 31)) * ROWB;
-  const int b_off = BM * ROWB + (wn * CFG::WTN + (lane & 31)) * ROWB;
-  const int a2_off = a_off + (BM + BN) * ROWB;
-  const int b2_off = share_b ? b_off : b_off + (BM + BN) * ROWB;
+  const FragOffs<CFG, false, false> fo(wm, wn, lane);
+  FragOffs<CFG, false, false> fo2 = fo;  // the second problem's A (and B) sit after the first's
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fo2.a[i] += (BM + BN) * ROWB;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fo2.b[j] += share_b ? 0 : (BM + BN) * ROWB;
   auto sync = [&](int64_t kt) {
     wait_vmcnt<0>();
     lds_barrier();
@@ -621,8 +709,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
   auto stage = [&](int64_t kt, auto edge) {
     constexpr bool E = decltype(edge)::value;
     const char* st = smem + (int)(kt & 1) * SB;
-    dtl_stage<CFG, E>(st, a_off, b_off, sw, lane, kbeg + kt * BK, kmin, kend, acc);
-    dtl_stage<CFG, E>(st, a2_off, b2_off, sw, lane, kbeg + kt * BK, kmin, kend, acc2);
+    dtl_stage<CFG, E>(st, fo, lane, kbeg + kt * BK, kmin, kend, acc);
+    dtl_stage<CFG, E>(st, fo2, lane, kbeg + kt * BK, kmin, kend, acc2);
   };
   if constexpr (KEDGE) {
     if (nk > 0) {
@@ -646,18 +734,151 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
   EPI::template run<CFG>(p, ea, t, wm, wn, tid, acc, acc2, smem);
 }
 
+// Two contractions into one accumulator, C = rs (.) (A1 @ op(B1)) + A2 @ op(B2): the
+// k loop runs over A1's K1 columns, then A2's K2 (p.K), with rs, the per-row scale of
+// the first product, applied to the accumulators in between. Every lane's 16 accumulators
+// of a 32x32 MFMA tile sit in one output row, so the scale is one multiply per register.
+// rs(t) = routed(t) ? (delta ? delta[t] : 0) : 1, routed(t) = !route || route[t]: the
+// blend weight of the target output x @ W^T in the masked linear (and of its cotangent).
+// A1 and A2 are K-contiguous; B1MN / B2MN: the B operand is MN-major. The LDS stage ring
+// runs straight through the segment boundary, so the second product's first stages
+// load while the first product's last stage is consumed.
+struct KcatArgs {
+  const bf16_t* A1;
+  int64_t lda1;
+  const bf16_t* B1;
+  int64_t ldb1;
+  int64_t K1;
+  const bf16_t* delta;
+  const uint8_t* route;
+};
+
+template <class CFG, typename TC, bool B1MN, bool B2MN, class EPI = EpiStore>
+__global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs q, typename EPI::Args ea) {
+  constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
+  constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
+  constexpr int LDS = NS * CFG::STAGE_BYTES > EPI::LDS_BYTES ? NS * CFG::STAGE_BYTES : EPI::LDS_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = uni(tid >> 6);
+  const int wm = wave / CFG::WN, wn = wave % CFG::WN;
+
+  TileJob t;
+  if (!map_tile<BM, BN, MODE_DENSE, TC>(p, lane, t)) return;
+  const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
+  const int64_t K1 = q.K1, K2 = p.K;
+  const int64_t nk1 = (K1 + BK - 1) / BK, nk = nk1 + (K2 + BK - 1) / BK;
+  const bf16_t* a1 = (const bf16_t*)uni64((int64_t)(q.A1 + m0 * q.lda1));
+  const bf16_t* b1 = (const bf16_t*)uni64((int64_t)(B1MN ? q.B1 + n0 : q.B1 + n0 * q.ldb1));
+  const bf16_t* a2 = (const bf16_t*)uni64((int64_t)(p.A + m0 * p.lda));
+  const bf16_t* b2 = (const bf16_t*)uni64((int64_t)(B2MN ? p.B + n0 : p.B + n0 * p.ldb));
+  const int32_t a1bytes = buf_bytes((p.M - m0) * q.lda1 * 2), a2bytes = buf_bytes((p.M - m0) * p.lda * 2);
+  const int32_t b1bytes = buf_bytes(B1MN ? (K1 * q.ldb1 - n0) * 2 : (p.N - n0) * q.ldb1 * 2);
+  const int32_t b2bytes = buf_bytes(B2MN ? (K2 * p.ldb - n0) * 2 : (p.N - n0) * p.ldb * 2);
+  uint32_t oa1[CFG::A_INSTS], ob1[CFG::B_INSTS], oa2[CFG::A_INSTS], ob2[CFG::B_INSTS];
+  dtl_offsets<BM, NW>(oa1, q.lda1, wave, lane);
+  dtl_offsets<BM, NW>(oa2, p.lda, wave, lane);
+  if constexpr (B1MN) dtl_offsets_mn<BN, NW>(ob1, q.ldb1, wave, lane);
+  else dtl_offsets<BN, NW>(ob1, q.ldb1, wave, lane);
+  if constexpr (B2MN) dtl_offsets_mn<BN, NW>(ob2, p.ldb, wave, lane);
+  else dtl_offsets<BN, NW>(ob2, p.ldb, wave, lane);
+  const uint32_t ks1 = B1MN ? (uint32_t)(q.ldb1 * 2) : 2u, ks2 = B2MN ? (uint32_t)(p.ldb * 2) : 2u;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto issue = [&](int64_t kt) {
+    char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
+    if (kt < nk1) {
+      const uint32_t kpos = (uint32_t)(kt * BK);
+      dtl_issue<BM, NW>(st, a1, a1bytes, oa1, kpos * 2, wave);
+      dtl_issue<BN, NW>(st + BM * ROWB, b1, b1bytes, ob1, kpos * ks1, wave);
+    } else {
+      const uint32_t kpos = (uint32_t)((kt - nk1) * BK);
+      dtl_issue<BM, NW>(st, a2, a2bytes, oa2, kpos * 2, wave);
+      dtl_issue<BN, NW>(st + BM * ROWB, b2, b2bytes, ob2, kpos * ks2, wave);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+
+  const FragOffs<CFG, false, B1MN> fo1(wm, wn, lane);
+  const FragOffs<CFG, false, B2MN> fo2(wm, wn, lane);
+  auto sync = [&](int64_t kt) {
+    const int64_t left = nk - 1 - kt;
+    wait_stages<CFG::INSTS, NS - 2>((int)(left < NS - 2 ? left : NS - 2));
+    lds_barrier();
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+  };
+  auto st_of = [&](int64_t kt) { return smem + (int)(kt % NS) * CFG::STAGE_BYTES; };
+  // segment 1 (k tail masked in its last stage)
+  const bool tail1 = (K1 % BK) != 0;
+  for (int64_t kt = 0; kt < nk1 - (tail1 ? 1 : 0); ++kt) {
+    sync(kt);
+    dtl_stage<CFG, false>(st_of(kt), fo1, lane, kt * BK, 0, K1, acc);
+  }
+  if (tail1) {
+    sync(nk1 - 1);
+    dtl_stage<CFG, true>(st_of(nk1 - 1), fo1, lane, (nk1 - 1) * BK, 0, K1, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = m0 + wm * CFG::WTM + i * 32 + (lane & 31);
+    float rs = 1.f;
+    if (row < p.M && (!q.route || q.route[row])) rs = q.delta ? bf16_to_f32(q.delta[row]) : 0.f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] *= rs;
+  }
+  // segment 2
+  const bool tail2 = (K2 % BK) != 0;
+  for (int64_t kt = nk1; kt < nk - (tail2 ? 1 : 0); ++kt) {
+    sync(kt);
+    dtl_stage<CFG, false>(st_of(kt), fo2, lane, (kt - nk1) * BK, 0, K2, acc);
+  }
+  if (tail2) {
+    sync(nk - 1);
+    dtl_stage<CFG, true>(st_of(nk - 1), fo2, lane, (nk - 1 - nk1) * BK, 0, K2, acc);
+  }
+  EPI::template run<CFG, TC>(p, ea, t, wm, wn, tid, acc, smem);
+}
+
 // Dense C = A [M, K] @ B^T (B stored [N, K], both K-contiguous, lda/ldb % 8 == 0, 16-byte
 // aligned) with the epilogue policy EPI (its Args carry everything beyond C's tile).
-template <class EPI, typename TC>
+template <class EPI, typename TC, bool BMN = false>
 inline int launch_dense_epi(const GemmArgs& a, const typename EPI::Args& ea, hipStream_t s, const char* what) {
-  if (!dtl_fits(a.M, a.lda, a.N, a.ldb)) return fail(PD_EUNSUPPORTED, std::string(what) + ": operands of 2 GiB or more");
+  if (a.M * a.lda * 2 > 0x7FFFFFFF || !(BMN ? dtl_fits_mn(a.K, a.ldb) : a.N * a.ldb * 2 <= 0x7FFFFFFF))
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": operands of 2 GiB or more");
   if ((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM > 65535 || (a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN > 65535)
     return fail(PD_EUNSUPPORTED, std::string(what) + ": too large");
   const dim3 grid((unsigned)((a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN), (unsigned)((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM));
   if (a.K % CfgDtlRA::BK)
-    hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, TC, MODE_DENSE, true, EPI>), grid, dim3(CfgDtlRA::NT), 0, s, a, ea);
+    hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, TC, MODE_DENSE, true, EPI, false, BMN>), grid, dim3(CfgDtlRA::NT), 0, s,
+                       a, ea);
   else
-    hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, TC, MODE_DENSE, false, EPI>), grid, dim3(CfgDtlRA::NT), 0, s, a, ea);
+    hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, TC, MODE_DENSE, false, EPI, false, BMN>), grid, dim3(CfgDtlRA::NT), 0, s,
+                       a, ea);
+  return check_launch(what);
+}
+
+// C = rs (.) (A1 @ op(B1)) + A2 @ op(B2) (k_gemm_dtl_kcat) with the epilogue policy EPI.
+template <class EPI, typename TC, bool B1MN, bool B2MN>
+inline int launch_kcat_epi(const GemmArgs& a, const KcatArgs& q, const typename EPI::Args& ea, hipStream_t s,
+                           const char* what) {
+  if (a.M * a.lda * 2 > 0x7FFFFFFF || a.M * q.lda1 * 2 > 0x7FFFFFFF ||
+      !(B1MN ? dtl_fits_mn(q.K1, q.ldb1) : a.N * q.ldb1 * 2 <= 0x7FFFFFFF) ||
+      !(B2MN ? dtl_fits_mn(a.K, a.ldb) : a.N * a.ldb * 2 <= 0x7FFFFFFF))
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": operands of 2 GiB or more");
+  if ((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM > 65535 || (a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN > 65535)
+    return fail(PD_EUNSUPPORTED, std::string(what) + ": too large");
+  const dim3 grid((unsigned)((a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN), (unsigned)((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM));
+  hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlRA, TC, B1MN, B2MN, EPI>), grid, dim3(CfgDtlRA::NT), 0, s, a, q, ea);
   return check_launch(what);
 }
 

@@ -3,10 +3,11 @@
 //   pd_masked_linear_fwd/bwd   pd/core/decomposed_linear.py:142-175 (site_forward),
 //                              :65-85 (component_coefficients, blend_target_output)
 //   pd_blocked_site_fwd/bwd    :209-271 (blocked_site_forward, dense over every block)
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
-#include "pd_common.hpp"
+#include "pd_gemm_dtl.hpp"
 
 namespace pd {
 
@@ -94,6 +95,160 @@ __global__ void k_f32_to_bf16(const float* __restrict__ src, int64_t n, bf16_t* 
     dst[i] = f32_to_bf16(src[i]);
 }
 
+// ---------------------------------------------------------------- fused bf16 seam
+// Every bf16 call whose widths are multiples of 8 (16-byte aligned operands) runs in
+// GEMM launches with the elementwise work in their prologue/epilogue:
+//   forward   xV = x @ V, epilogue acts = routed ? xV * (m - d) : 0          (1 launch)
+//             out = rs (.) (x @ W^T) + acts @ U, one k loop over [W^T ; U]    (1 launch)
+//   backward  dU = acts^T @ g                                                  (1 launch)
+//             da = g @ U^T, epilogue dmask = da * xV, dxV = da * (m - d)       (1 launch)
+//             dV = x^T @ dxV                                                   (1 launch)
+//             dx = rs (.) (g @ W) + dxV @ V^T, one k loop                      (1 launch)
+// rs = routed ? d : 1 blends the target output (and its cotangent). Each epilogue rounds
+// the accumulator to bf16 before the elementwise step, as the unfused passes do when
+// they read the stored bf16 product back, so both paths agree bit for bit there.
+
+// Row facts of the masked linear: d_t (0 without a delta) and routed(t).
+__device__ inline void ml_row(const bf16_t* delta, const uint8_t* route, int64_t row, float& d, bool& r) {
+  d = delta ? bf16_to_f32(delta[row]) : 0.f;
+  r = route ? route[row] != 0 : true;
+}
+
+__device__ inline void unpack4(uint2 u, float (&f)[4]) {
+  f[0] = bf16_to_f32((bf16_t)(u.x & 0xFFFF));
+  f[1] = bf16_to_f32((bf16_t)(u.x >> 16));
+  f[2] = bf16_to_f32((bf16_t)(u.y & 0xFFFF));
+  f[3] = bf16_to_f32((bf16_t)(u.y >> 16));
+}
+
+__device__ inline uint2 pack4(const float (&f)[4]) { return uint2{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])}; }
+
+// Visits the lane's output groups of 4 consecutive columns (row, col, the 4 fp32
+// accumulators rounded to bf16) of a k_gemm_dtl tile; N % 4 == 0 is required.
+template <class CFG, class F>
+__device__ inline void epi_groups(const GemmArgs& p, const TileJob& t, int wm, int wn, int lane,
+                                  f32x16 (&acc)[CFG::TM][CFG::TN], F&& f) {
+#pragma unroll
+  for (int i = 0; i < CFG::TM; ++i) {
+    const int64_t row = t.m0 + wm * CFG::WTM + i * 32 + (lane & 31);
+    if (row >= t.M) continue;
+#pragma unroll
+    for (int j = 0; j < CFG::TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = t.n0 + wn * CFG::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+        if (col >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = bf16_to_f32(f32_to_bf16(acc[i][j][4 * g + e]));
+        f(row, col, v);
+      }
+  }
+}
+
+// C = xV (bf16); acts = routed ? xV * (m - d) : 0
+struct EpiActs {
+  static constexpr int LDS_BYTES = 0;
+  struct Args {
+    const bf16_t* mask;
+    const bf16_t* delta;
+    const uint8_t* route;
+    bf16_t* acts;
+  };
+  template <class CFG, typename TC>
+  __device__ static void run(const GemmArgs& p, const Args& a, const TileJob& t, int wm, int wn, int tid,
+                             f32x16 (&acc)[CFG::TM][CFG::TN], char*) {
+    bf16_t* xV = (bf16_t*)t.C;
+    epi_groups<CFG>(p, t, wm, wn, tid & 63, acc, [&](int64_t row, int64_t col, const float (&v)[4]) {
+      float d;
+      bool r;
+      ml_row(a.delta, a.route, row, d, r);
+      const int64_t idx = row * p.ldc + col;
+      *(uint2*)(xV + idx) = pack4(v);
+      float m[4], o[4];
+      unpack4(*(const uint2*)(a.mask + idx), m);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = r ? v[e] * (m[e] - d) : 0.f;
+      *(uint2*)(a.acts + idx) = pack4(o);
+    });
+  }
+};
+
+// da = g @ U^T rounded; dmask = routed ? da * xV : 0 (if wanted); C = dxV = routed ? da * (m - d) : 0
+struct EpiMaskedBwd {
+  static constexpr int LDS_BYTES = 0;
+  struct Args {
+    const bf16_t* xV;
+    const bf16_t* mask;
+    const bf16_t* delta;
+    const uint8_t* route;
+    bf16_t* dmask;
+  };
+  template <class CFG, typename TC>
+  __device__ static void run(const GemmArgs& p, const Args& a, const TileJob& t, int wm, int wn, int tid,
+                             f32x16 (&acc)[CFG::TM][CFG::TN], char*) {
+    bf16_t* dxV = (bf16_t*)t.C;
+    epi_groups<CFG>(p, t, wm, wn, tid & 63, acc, [&](int64_t row, int64_t col, const float (&v)[4]) {
+      float d;
+      bool r;
+      ml_row(a.delta, a.route, row, d, r);
+      const int64_t idx = row * p.ldc + col;
+      float m[4], o[4];
+      if (a.dmask) {
+        float xv[4];
+        unpack4(*(const uint2*)(a.xV + idx), xv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = r ? v[e] * xv[e] : 0.f;
+        *(uint2*)(a.dmask + idx) = pack4(o);
+      }
+      unpack4(*(const uint2*)(a.mask + idx), m);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = r ? v[e] * (m[e] - d) : 0.f;
+      *(uint2*)(dxV + idx) = pack4(o);
+    });
+  }
+};
+
+// d_delta[t] = routed ? sum_o g[t,o] * yt[t,o] - sum_c dmask[t,c] : 0 (dmask = da * xV is
+// the per-component term of the delta derivative); fp32 sums, one wave per row.
+__global__ __launch_bounds__(256) void k_ml_delta_grad_dm(const bf16_t* __restrict__ g, const bf16_t* __restrict__ yt,
+                                                          const bf16_t* __restrict__ dmask,
+                                                          const uint8_t* __restrict__ route, int64_t Tn, int64_t D,
+                                                          int64_t C, bf16_t* __restrict__ d_delta) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const int lane = threadIdx.x & 63;
+  float part = 0.f;
+  for (int64_t o = lane; o < D; o += 64) part = fmaf(bf16_to_f32(g[t * D + o]), bf16_to_f32(yt[t * D + o]), part);
+  for (int64_t c = lane; c < C; c += 64) part -= bf16_to_f32(dmask[t * C + c]);
+  part = wave_sum(part);
+  if (lane == 0) d_delta[t] = f32_to_bf16((route ? route[t] != 0 : true) ? part : 0.f);
+}
+
+static bool a16(const void* p) { return !p || ((uintptr_t)p & 15) == 0; }
+
+// The fused seam applies: bf16, widths multiples of 8, 16-byte aligned operands.
+static bool fused_seam(int dtype, int64_t d_in, int64_t d_out, int64_t C, std::initializer_list<const void*> ptrs) {
+  if (dtype != PD_DTYPE_BF16 || d_in % 8 || d_out % 8 || C % 8) return false;
+  for (const void* q : ptrs)
+    if (!a16(q)) return false;
+  return true;
+}
+
+static int masked_linear_fwd_fused(int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
+                                   const void* U, const void* W, const void* mask, const void* delta,
+                                   const uint8_t* route, void* out, void* xV, void* acts, hipStream_t s) {
+  GemmArgs g1{T, C, d_in, (const bf16_t*)x, d_in, (const bf16_t*)V, C, xV, C, 1.f, 0.f, nullptr, 0, 0, 0};
+  int rc = launch_dense_epi<EpiActs, bf16_t, true>(
+      g1, EpiActs::Args{(const bf16_t*)mask, (const bf16_t*)delta, route, (bf16_t*)acts}, s, "pd_masked_linear_fwd xV");
+  if (rc) return rc;
+  if (!delta && !route)
+    return pd_gemm(PD_DTYPE_BF16, T, d_out, C, acts, C, 0, U, d_out, 0, out, d_out, PD_DTYPE_BF16, 1.f, 0.f, s);
+  GemmArgs g2{T, d_out, C, (const bf16_t*)acts, C, (const bf16_t*)U, d_out, out, d_out, 1.f, 0.f, nullptr, 0, 0, 0};
+  KcatArgs q{(const bf16_t*)x, d_in, (const bf16_t*)W, d_in, d_in, (const bf16_t*)delta, route};
+  return launch_kcat_epi<EpiStore, bf16_t, false, true>(g2, q, EpiStore::Args{}, s, "pd_masked_linear_fwd out");
+}
+
 template <typename T>
 static void launch_acts(int dtype, const void* xV, const void* mask, const void* delta, const uint8_t* route,
                         int64_t Tn, int64_t C, void* acts, hipStream_t s) {
@@ -116,6 +271,8 @@ int pd_masked_linear_fwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
   if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_masked_linear_fwd: dtype");
   if (T == 0) return PD_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (fused_seam(dtype, d_in, d_out, C, {x, V, U, W, mask, out, xV, acts}))
+    return masked_linear_fwd_fused(T, d_in, d_out, C, x, V, U, W, mask, delta, route, out, xV, acts, s);
   int rc = pd_gemm(dtype, T, C, d_in, x, d_in, 0, V, C, 0, xV, C, dtype, 1.f, 0.f, stream);
   if (rc) return rc;
   if (dtype == PD_DTYPE_F32)
@@ -150,6 +307,41 @@ size_t pd_masked_linear_bwd_workspace_size(int dtype, int64_t T, int64_t d_out, 
 
 namespace pd {
 
+// The fused bf16 backward (see the seam above); da and gt are the two scratch regions of
+// the unfused path (T x C and T x d_out elements).
+static int masked_linear_bwd_fused(int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x, const void* V,
+                                   const void* U, const void* W, const void* mask, const void* delta,
+                                   const uint8_t* route, const void* xV, const void* acts, const void* g_out, void* dx,
+                                   void* dV, void* dU, void* dmask, void* d_delta, void* da, void* gt,
+                                   hipStream_t s) {
+  const int BF = PD_DTYPE_BF16;
+  int rc;
+  // dU = acts^T @ g (both operands token-row-major: MN-major in the contraction)
+  if (dU && (rc = pd_gemm(BF, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, BF, 1.f, 0.f, s))) return rc;
+  if (!dV && !dx && !dmask && !d_delta) return PD_OK;
+  GemmArgs g{T, C, d_out, (const bf16_t*)g_out, d_out, (const bf16_t*)U, d_out, da, C, 1.f, 0.f, nullptr, 0, 0, 0};
+  rc = launch_dense_epi<EpiMaskedBwd, bf16_t, false>(
+      g, EpiMaskedBwd::Args{(const bf16_t*)xV, (const bf16_t*)mask, (const bf16_t*)delta, route, (bf16_t*)dmask}, s,
+      "pd_masked_linear_bwd da");
+  if (rc) return rc;
+  if (d_delta) {
+    // the target x @ W^T, then the row sums
+    if ((rc = pd_gemm(BF, T, d_out, d_in, x, d_in, 0, W, d_in, 1, gt, d_out, BF, 1.f, 0.f, s))) return rc;
+    hipLaunchKernelGGL(k_ml_delta_grad_dm, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, (const bf16_t*)g_out,
+                       (const bf16_t*)gt, (const bf16_t*)dmask, route, T, d_out, C, (bf16_t*)d_delta);
+    if ((rc = check_launch("pd_masked_linear_bwd d_delta"))) return rc;
+  }
+  // dV = x^T @ dxV
+  if (dV && (rc = pd_gemm(BF, d_in, C, T, x, d_in, 1, da, C, 0, dV, C, BF, 1.f, 0.f, s))) return rc;
+  if (!dx) return PD_OK;
+  if (!delta && !route)  // dx = dxV @ V^T
+    return pd_gemm(BF, T, d_in, C, da, C, 0, V, C, 1, dx, d_in, BF, 1.f, 0.f, s);
+  // dx = rs (.) (g @ W) + dxV @ V^T: W [d_out, d_in] is the MN-major B of the first product
+  GemmArgs g2{T, d_in, C, (const bf16_t*)da, C, (const bf16_t*)V, C, dx, d_in, 1.f, 0.f, nullptr, 0, 0, 0};
+  KcatArgs q{(const bf16_t*)g_out, d_out, (const bf16_t*)W, d_in, d_out, (const bf16_t*)delta, route};
+  return launch_kcat_epi<EpiStore, bf16_t, true, false>(g2, q, EpiStore::Args{}, s, "pd_masked_linear_bwd dx");
+}
+
 // The masked-linear backward over a caller-sized scratch region `workspace` (at least
 // pd_masked_linear_bwd_workspace_size bytes, 256-byte aligned). Every byte of the
 // scratch it reads is written first in the same call (both regions are full GEMM
@@ -172,6 +364,9 @@ static int masked_linear_bwd_impl(const char* what, int dtype, int64_t T, int64_
   void* da = ws;
   void* gt = ws + ((es * T * C + 255) & ~(size_t)255);
   int rc;
+  if (fused_seam(dtype, d_in, d_out, C, {x, V, U, W, mask, xV, acts, g_out, dx, dmask}) && (!d_delta || dmask))
+    return masked_linear_bwd_fused(T, d_in, d_out, C, x, V, U, W, mask, delta, route, xV, acts, g_out, dx, dV, dU,
+                                   dmask, d_delta, da, gt, s);
   // dU = acts^T @ g (unrouted rows of acts are zero)
   if (dU && (rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, g_out, d_out, 0, dU, d_out, dtype, 1.f, 0.f, stream)))
     return rc;

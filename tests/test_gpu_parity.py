@@ -224,8 +224,11 @@ def test_mse_and_kl(device):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 136, 72), (256, 384, 768), (8, 8, 8)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 136, 72), (256, 384, 768), (8, 8, 8), (1000, 776, 1096),
+                                   (136, 264, 520)])
 def test_gemm_bf16_layouts(device, ta, tb, M, N, K):
+    """Every operand layout runs the buffer-fed kernel (an MN-major operand's fragments
+    transposed on their way out of LDS); ragged tiles and a k-tail stage."""
     from param_decomp_amd import ops
 
     rng = np.random.default_rng(M + N + K + 2 * ta + tb)
@@ -238,6 +241,26 @@ def test_gemm_bf16_layouts(device, ta, tb, M, N, K):
     assert_close(np64(out), want, 1e-5, 1e-6, f"gemm ta={ta} tb={tb}")  # fp32 out: accumulation order only
     out16 = ops.gemm(Ab, Bb, trans_a=bool(ta), trans_b=bool(tb))
     assert_close(np64(out16), want, BF16_RTOL, 1e-3, "gemm bf16 out")
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1), (0, 0)])
+def test_gemm_bf16_padded_leading_dims(device, ta, tb):
+    """Leading dimensions past the operand extents (column blocks of wider tensors): the
+    columns an MN-major tile reads past M or N only feed outputs that are never stored."""
+    from param_decomp_amd import _lib as L
+
+    rng = np.random.default_rng(40 + 2 * ta + tb)
+    M, N, K, pad = 264, 200, 328, 24
+    A = bf(rng.normal(size=(K, M + pad) if ta else (M, K + pad)), device)
+    B = bf(rng.normal(size=(N, K + pad) if tb else (K, N + pad)), device)
+    C = torch.full((M, N + 8), 7.0, dtype=torch.float32, device=device)
+    L.call("pd_gemm", L.BF16, M, N, K, L.ptr(A), A.shape[1], ta, L.ptr(B), B.shape[1], tb, L.ptr(C), N + 8, L.F32,
+           1.0, 0.0, L.stream())
+    a, b = np64(A), np64(B)
+    a = a[:, :M].T if ta else a[:, :K]
+    b = b[:, :K].T if tb else b[:, :N]
+    assert_close(np64(C)[:, :N], a @ b, 1e-5, 1e-6, f"padded gemm ta={ta} tb={tb}")
+    assert torch.all(C[:, N:] == 7.0)
 
 
 def test_gemm_alpha_beta_and_fp32(device):
@@ -256,11 +279,15 @@ def test_gemm_alpha_beta_and_fp32(device):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("with_delta,with_route", [(False, False), (True, False), (True, True), (False, True)])
-def test_site_forward_and_backward(device, dtype, with_delta, with_route):
+@pytest.mark.parametrize("shape", [(3, 40, 64, 96, 128), (2, 150, 200, 136, 520)])
+def test_site_forward_and_backward(device, dtype, with_delta, with_route, shape):
+    """bf16 runs the fused seam (the mask step in the x @ V and g @ U^T epilogues, the
+    target blend inside one k loop over [W^T ; U]); the second shape has several k
+    stages and k tails in every product."""
     from param_decomp_amd.decomposed_linear import SiteWeights, site_forward
 
     rng = np.random.default_rng(12)
-    B_, S, d_in, d_out, C = 3, 40, 64, 96, 128
+    B_, S, d_in, d_out, C = shape
     x = rng.normal(size=(B_, S, d_in))
     W = rng.normal(size=(d_out, d_in)) / 8
     V = rng.normal(size=(d_in, C)) / 8
@@ -560,6 +587,46 @@ def test_grouped_gemm_dw_kmajor(device, sizes, out_dtype):
     for e, s in enumerate(sizes):
         if s == 0:
             assert torch.count_nonzero(dw[e]) == 0
+
+
+@pytest.mark.parametrize("sizes", [[700, 0, 300, 1025], [7, 0, 19, 1, 0, 26, 37, 0], [129, 128, 127, 1]])
+def test_grouped_gemm_dw_row_major(device, sizes):
+    """Ragged-contraction dW straight from the token-row operands (both MN-major: the
+    k axis is the row index): multi-stage groups, unaligned starts, empty groups."""
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(70 + sum(sizes))
+    E, K, N = len(sizes), 200, 264
+    used = int(sum(sizes))
+    J = used + 3
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = bf(rng.normal(size=(J, K)), device)
+    dout = bf(rng.normal(size=(J, N)), device)
+    dw = ops.grouped_gemm_dw(lhs, dout, offsets, E, out_dtype=torch.float32)
+    want = po.transposed_grouped_matmul(np64(lhs)[:used], np64(dout)[:used], sizes)
+    assert_close(np64(dw), want, 1e-5, 1e-6, "dw row-major fp32")
+    for e, s_ in enumerate(sizes):
+        if s_ == 0:
+            assert torch.count_nonzero(dw[e]) == 0
+
+
+@pytest.mark.parametrize("K", [200, 520])
+def test_grouped_gemm_mn_rhs_multistage(device, K):
+    """Grouped forward with each expert's weight stored [K, N] (MN-major) over several k
+    stages and a k tail."""
+    from param_decomp_amd import ops
+
+    sizes = [300, 0, 129, 77]
+    rng = np.random.default_rng(K)
+    E, N = len(sizes), 392
+    used = int(sum(sizes))
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=device)
+    lhs = bf(rng.normal(size=(used + 4, K)), device)
+    rhs = bf(rng.normal(size=(E, K, N)) / 8, device)
+    out = ops.grouped_gemm(lhs, rhs, offsets, trans_rhs=False, out_dtype=torch.float32)
+    want = po.grouped_matmul(np64(lhs)[:used], np64(rhs), sizes)
+    assert_close(np64(out)[:used], want, 1e-5, 1e-6, "grouped mn rhs")
+    assert torch.count_nonzero(out[used:]) == 0
 
 
 # ------------------------------------------------------------------ streamed-vocab KL
