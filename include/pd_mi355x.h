@@ -308,13 +308,20 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
  * W[e]) (pd/core/decomposed_linear.py:65-85); use_delta = 0 is d = 0. source_value < 0
  * draws as above (StochasticSources); source_value in [0, 1] is the reference's
  * ConstantSources(v) (pd/core/objective.py:435-449): u = v everywhere and, with
- * use_delta, d = v; 0 is the CI-masked reconstruction (m = lower(ci), d = 0). Loss = recon_coeff * mean((r_L - rc_L)^2) + imp_coeff *
- * sum over sites/layers of sum(upper(ci)^p)/T (the selected arm of
- * pd/core/losses.py:357-372).
+ * use_delta, d = v; 0 is the CI-masked reconstruction (m = lower(ci), d = 0).
+ * Loss = recon_coeff * mean((r_L - rc_L)^2) + the imp-min term over every site/layer's
+ * selected upper CI: imp_kind PD_IMPMIN_PNORM: imp_coeff * sum(upper^p) / T (the selected
+ * arm of pd/core/losses.py:357-372); PD_IMPMIN_SMOOTH_L0: the engine's term
+ * (pd/core/objective.py:101-131) imp_coeff * sum_c f_c + freq_coeff * sum_c f_c
+ * log2(1 + ref_count f_c), f_c = sum psi(upper) / T over the site's [E*c] components
+ * (values scattered to their expert's block, pd/core/losses.py:316-330), psi =
+ * c^2/(c^2 + gamma^2) (times 1 + gamma^2 when normalize_at_one); ref_count = 0 drops
+ * the frequency term (the single-batch estimate: no EMA state).
  * Layouts (all bf16 unless noted): x0 [T,d]; ln fp32 [L,d]; router [L,E,d];
  * Wg, Wu [L,E,d,f]; Wd [L,E,f,d]; Vg, Vu [L,E,d,c]; Ug, Uu [L,E,c,f]; Vd [L,E,f,c];
  * Ud [L,E,c,d]; ci_pre [L,3,T,k,c] (site order gate, up, down; slot s = the token's
- * s-th selected expert). Outputs: losses[3] = {loss, recon, imp}; the six V/U
+ * s-th selected expert). Outputs: losses[4] = {loss, recon, activity (the L_p sum or
+ * sum f_c), frequency (0 for L_p)}; the six V/U
  * gradients fp32 in the V/U shapes; d_ci_pre bf16 [L,3,T,k,c]; top_idx_out int32
  * [L,T,k] (nullable). The stack input's gradient is not formed (layer 0 stops at its
  * weight and CI gradients).
@@ -324,9 +331,10 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                       const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                      int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
-                      float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
-                      void* stream);
+                      int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
+                      float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dVg, float* dUg,
+                      float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
+                      void* workspace, size_t workspace_bytes, void* stream);
 /* pd_moe_stack_step recording a hipEvent_t before each launch group and one at the
  * end; categories[i] labels the interval [i, i+1): 0 clean forward, 1 masked norm /
  * router / bucketing / gather, 2 grouped GEMMs fwd, 3 mask fwd, 4 SwiGLU fold,
@@ -336,8 +344,10 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                             const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
-                            float source_value, int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
-                            float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
+                            float source_value, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                            float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, float* losses,
+                            float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                            int32_t* top_idx_out,
                             void* workspace, size_t workspace_bytes, void* stream, void** events,
                             int32_t* categories, int capacity, int* n_recorded);
 

@@ -98,7 +98,7 @@ def grouped_T(lhs, rhs, sizes):
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                    bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None,
-                   pinned_top_idx=None):
+                   pinned_top_idx=None, imp_min=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
     given. `pinned_top_idx[l]` ([T, k]) replaces the clean pass's own expert selection
@@ -106,8 +106,11 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     products before rounding, `logits_raw`, and the sums of their terms' magnitudes,
     `logits_mag`, that bound an fp32 accumulation's error). Returns dict(loss, recon,
     imp, grads, d_ci_pre, top_idx, own_top_idx, logits_raw, logits_mag, r_final,
-    rc_final, deltas)."""
+    rc_final, deltas). `imp_min` (a `pd_oracle.ImpMin`) replaces the L_p term given by
+    p / imp_coeff; each site's selected values map to their expert's block of the
+    [E * c] component vector; `freq` is the frequency term."""
     rb = po.round_bf16 if bf16_storage else (lambda a: a)
+    spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
     T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
     # ---------------- clean forward (frozen weights)
     rc = rb(x0)
@@ -136,6 +139,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     r = rb(x0)
     saved = []
     imp = 0.0
+    freq = 0.0
     for l in range(cfg.L):
         P = params[l]
         h2, rinv = rms_norm_zero_centered(r, P["ln"], cfg.eps)
@@ -153,7 +157,9 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             pre = ci_pre[l][s]
             lo = po.lower_leaky(pre)
             up = po.upper_leaky(pre)
-            imp += float(np.sum(up**p)) / T
+            a_, f_, dup = po.impmin_site_terms(up, spec, T, idx, E)
+            imp += a_
+            freq += f_
             if source_value is None:
                 ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
             else:
@@ -168,7 +174,8 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             else:
                 dt = np.zeros(T)
             dj = dt[tok][:, None]
-            S[s] = dict(pre=pre, lo=lo, up=up, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx], delta=dt, dj=dj)
+            S[s] = dict(pre=pre, lo=lo, up=up, dup=dup, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx], delta=dt,
+                        dj=dj)
             S[s]["coef"] = S[s]["m"] - dj
         wj = w.reshape(-1)[jobs.sort_idx]
         for s in ("gate", "up"):
@@ -188,7 +195,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         r = rb(r + routed)
     n = T * cfg.d
     recon = float(np.mean((r - rc) ** 2))
-    loss = recon_coeff * recon + imp_coeff * imp
+    loss = recon_coeff * recon + spec.loss(imp, freq)
     # ---------------- backward
     dr = rb(recon_coeff * 2.0 * (r - rc) / n)
     grads = [dict() for _ in range(cfg.L)]
@@ -229,8 +236,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             dm_tok[jobs.sort_idx] = Ss["dm"]
             dm_tok = dm_tok.reshape(T, k, c)
             dlo = dm_tok * (1.0 - Ss["u"])
-            dup = imp_coeff * p * Ss["up"] ** (p - 1.0) / T
-            d_pre[l][s] = rb(po.lower_leaky_vjp(Ss["pre"], dlo) + po.upper_leaky_vjp(Ss["pre"], dup))
+            d_pre[l][s] = rb(po.lower_leaky_vjp(Ss["pre"], dlo) + po.upper_leaky_vjp(Ss["pre"], Ss["dup"]))
         # routing weights -> probs -> logits -> h2
         d_w = d_wj[jobs.inv_sort_idx].reshape(T, k)
         w, probs, idx = sv["w"], sv["probs"], sv["idx"]
@@ -242,7 +248,8 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_h2 = po.gather_tokens_vjp(d_xj, jobs) + d_logits @ P["router"]
         dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
         dr = rb(dr + dx)
-    return dict(loss=loss, recon=recon, imp=imp, grads=grads, d_ci_pre=d_pre, top_idx=tops, own_top_idx=own_tops,
+    return dict(loss=loss, recon=recon, imp=imp, freq=freq, grads=grads, d_ci_pre=d_pre, top_idx=tops,
+                own_top_idx=own_tops,
                 logits_raw=raws, logits_mag=mags, r_final=r, rc_final=rc, dx0=dr,
                 deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
 
@@ -306,13 +313,18 @@ def init_moe(cfg: MoEConfig, rng):
 
 
 def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                         use_delta=True, partitionable=True, dtype=None, threads=None):
+                         use_delta=True, partitionable=True, dtype=None, threads=None, imp_min=None):
     """The same step as `moe_stack_step` (no bf16 storage model) written as a torch
     forward whose backward is torch autograd: in float64 it pins `moe_stack_step`'s
     hand-written backward (tests/test_moe_oracle.py). The expert selection and Threefry
     draws are computed as in `moe_stack_step` (integer and bit-level work, outside
-    autograd). Returns dict(loss, recon, imp, grads, d_ci_pre, top_idx)."""
+    autograd). The smooth-L0 imp-min (`imp_min`) is written as the reference writes it, a
+    scatter-add of psi into the [E, c] component frequencies, so autograd differentiates
+    the frequency penalty through the scatter. Returns dict(loss, recon, imp, freq,
+    grads, d_ci_pre, top_idx)."""
     import torch
+
+    spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
 
     if threads:
         torch.set_num_threads(threads)
@@ -348,6 +360,7 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
             rc = rc + (down[inv].reshape(T, k, -1) * w[..., None]).sum(1)
     r = t(x0)
     imp = 0.0
+    freq = 0.0
     for l in range(cfg.L):
         h2 = norm(r, P[l]["ln"])
         probs = torch.softmax(h2 @ P[l]["router"].T, -1)
@@ -364,7 +377,16 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
         for s in SITES:
             lo = pre[l][s].clamp(0.0, 1.0)  # forward of the lower leaky hard sigmoid
             up = torch.where(pre[l][s] > 1.0, 1.0 + 0.01 * (pre[l][s] - 1.0), pre[l][s].clamp(0.0, 1.0))
-            imp = imp + (up**p).sum() / T
+            if spec.kind == "pnorm":
+                imp = imp + (up**spec.p).sum() / T
+            else:
+                g2 = spec.gamma**2
+                psi = up**2 / (up**2 + g2) * ((1.0 + g2) if spec.normalize_at_one else 1.0)
+                F = torch.zeros(E, c, dtype=dt).index_add(0, idx.reshape(-1), psi.reshape(-1, c))
+                fr = F / T
+                imp = imp + fr.sum()
+                if spec.ref_count > 0:
+                    freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
             u = t(tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c))
             dlt = (t(tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)) if use_delta
                    else torch.zeros(T, dtype=dt))
@@ -381,7 +403,7 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
         inv = torch.as_tensor(jobs.inv_sort_idx, dtype=torch.long)
         r = r + dout[inv].reshape(T, k, -1).sum(1)
     recon = ((r - rc) ** 2).mean()
-    loss = recon_coeff * recon + imp_coeff * imp
+    loss = recon_coeff * recon + spec.coeff * imp + (spec.freq_coeff * freq if spec.kind == "smooth_l0" else 0.0)
     names = [(l, n) for l in range(cfg.L) for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud")]
     wrt = [P[l][n] for l, n in names] + [pre[l][s] for l in range(cfg.L) for s in SITES]
     g = torch.autograd.grad(loss, wrt)
@@ -391,5 +413,5 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
     d_ci = [dict() for _ in range(cfg.L)]
     for i, (l, s) in enumerate((l, s) for l in range(cfg.L) for s in SITES):
         d_ci[l][s] = g[len(names) + i].double().numpy()
-    return dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()), grads=grads,
-                d_ci_pre=d_ci, top_idx=tops)
+    return dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()),
+                freq=float(freq.detach()) if torch.is_tensor(freq) else freq, grads=grads, d_ci_pre=d_ci, top_idx=tops)

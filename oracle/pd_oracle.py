@@ -311,6 +311,58 @@ def importance_minimality_terms(ci_upper_sites, gamma, reference_datapoint_count
     return activity, freq
 
 
+@dataclass(frozen=True)
+class ImpMin:
+    """The imp-min term of a fused step. `kind="pnorm"`: `coeff * sum upper^p / n` (the
+    paper's L_p, the selected arm of `pd/core/losses.py:357-372` for p = smooth-L0's
+    stand-in). `kind="smooth_l0"`: the engine's term (`pd/core/objective.py:101-131`):
+    `coeff * sum_c f_c + freq_coeff * sum_c f_c log2(1 + ref_count f_c)` with
+    `f_c = sum psi(upper) / n` (`pd/core/losses.py:316-330, 375-394`), the frequency term
+    off when `ref_count` is 0. `n` is the token count of the batch."""
+
+    kind: str = "pnorm"
+    p: float = 2.0
+    coeff: float = 1.0
+    gamma: float = 1.0
+    normalize_at_one: bool = False
+    freq_coeff: float = 0.0
+    ref_count: float = 0.0
+
+    def loss(self, activity: float, frequency: float) -> float:
+        return self.coeff * activity + (self.freq_coeff * frequency if self.kind == "smooth_l0" else 0.0)
+
+
+def impmin_site_terms(up, spec: ImpMin, n: int, groups=None, n_groups: int = 1):
+    """One site's `(activity, frequency, d loss / d up)` for its upper CI `up` [..., c].
+    `groups` (the leading shape of `up`) maps each row to its block of the full
+    `[n_groups * c]` component vector, as a selected-emitting site's values map to their
+    expert's components (`pd/core/losses.py:316-330`: scatter-add of psi, divided by the
+    token count n; unselected pairs add psi(0) = 0). The gradient includes the
+    coefficients: `coeff * p up^(p-1) / n` (L_p) or
+    `(coeff + freq_coeff * Phi'(f_c)) / n * psi'(up)` (smooth-L0, `Phi'` of
+    `pd/core/losses.py:380-386`)."""
+    up = np.asarray(up, np.float64)
+    if spec.kind == "pnorm":
+        return float(np.sum(up**spec.p)) / n, 0.0, spec.coeff * spec.p * up ** (spec.p - 1.0) / n
+    if spec.kind != "smooth_l0":
+        raise ValueError(spec.kind)
+    c = up.shape[-1]
+    psi = smooth_l0_psi(up, spec.gamma, spec.normalize_at_one).reshape(-1, c)
+    g = np.zeros(psi.shape[0], np.int64) if groups is None else np.asarray(groups).reshape(-1).astype(np.int64)
+    F = np.zeros((n_groups, c))
+    np.add.at(F, g, psi)
+    f = F / n
+    act = float(f.sum())
+    freq = 0.0
+    slope = np.full_like(f, spec.coeff)
+    if spec.ref_count > 0:
+        af = spec.ref_count * f
+        freq = float(np.sum(f * np.log2(1.0 + af)))
+        slope = slope + spec.freq_coeff * (np.log2(1.0 + af) + af / ((1.0 + af) * math.log(2.0)))
+    grad = (slope / n)[g].reshape(up.shape) * smooth_l0_psi_grad(up, spec.gamma, spec.normalize_at_one)
+    return act, freq, grad
+
+
 def mse(masked, clean):
     """`pd/targets/tms.py:380-388`, `pd/targets/resid_mlp.py:411-418`:
     `mean((masked - clean)^2)` in fp32."""

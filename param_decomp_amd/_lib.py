@@ -24,6 +24,9 @@ _c_i64, _c_i32, _c_u32, _c_f32, _c_p, _c_sz = (ctypes.c_int64, ctypes.c_int, cty
                                                 ctypes.c_void_p, ctypes.c_size_t)
 
 # name -> (restype, argtypes)
+# imp-min arguments of the fused steps: kind, p, gamma, normalize_at_one, coeff, freq_coeff, ref_count
+_IMP_ARGS = [_c_i32, _c_f32, _c_f32, _c_i32, _c_f32, _c_f32, _c_f32]
+
 _SIGNATURES = {
     "pd_last_error": (ctypes.c_char_p, []),
     "pd_abi_version": (_c_i32, []),
@@ -75,10 +78,9 @@ _SIGNATURES = {
     "pd_grouped_gemm_dw_kmajor": (_c_i32, [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i32, _c_p]),
     "pd_moe_stack_workspace_size": (_c_sz, [_c_i64] + [_c_i32] * 6),
     "pd_moe_stack_step": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_u32, _c_u32, _c_i32, _c_f32, _c_i32] +
-                          [_c_f32] * 3 +
-                          [_c_p] * 9 + [_c_p, _c_sz, _c_p]),
+                          _IMP_ARGS + [_c_f32] + [_c_p] * 9 + [_c_p, _c_sz, _c_p]),
     "pd_moe_stack_step_timed": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_u32, _c_u32, _c_i32, _c_f32, _c_i32] +
-                                [_c_f32] * 3 + [_c_p] * 9 + [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
+                                _IMP_ARGS + [_c_f32] + [_c_p] * 9 + [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
     "pd_lm_stack_workspace_size": (_c_sz, [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32, _c_p, _c_i32, _c_i32]),
     "pd_lm_stack_step": (_c_i32,
                          [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +

@@ -19,7 +19,7 @@
 #include <vector>
 
 #include "pd_common.hpp"
-#include "pd_tiles.hpp"
+#include "pd_impmin.hpp"
 
 namespace pd {
 
@@ -207,6 +207,14 @@ struct SiteMaskArgs {
   const float* delta;  // [T] the site's per-token delta draw, or NULL (d = 0)
   int k;               // experts per token: job j belongs to token sort_idx[j] / k
   float uconst;        // MASK_CONST: the constant source value standing in for u
+  // smooth-L0 imp-min (PM_SL0): psi = psis * v^2 / (v^2 + g2); the forward writes the
+  // per-(tile, expert) column sums of psi to colpart, the backward reads the per-(expert,
+  // component) slope; offsets [E + 1] locate each job's expert
+  const int32_t* offsets;
+  int E;
+  float g2, psis;
+  float* colpart;
+  const float* slope;
 };
 
 // Mask-source variant of the mask kernels beside the two Threefry layouts: every source
@@ -232,11 +240,13 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
                                                        uint8_t* __restrict__ ubits, float* __restrict__ imp_partial) {
   __shared__ TTile T;
   __shared__ float red[4];
+  __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
   const int64_t n = a.J * a.c;
   const bool qok = q0 + q4 < a.c;
+  if constexpr (PM == PM_SL0) sl0_tile_groups(SLv, a.offsets, a.E, j0, a.J, tid);
   float imp = 0.f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
@@ -256,7 +266,8 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
-        imp += powp<PM>(upper_fwd(pre[e]), a.p);
+        if constexpr (PM == PM_SL0) SLv.ps[r][q4 + e] = sl0_psi(upper_fwd(pre[e]), a.g2, a.psis);
+        else imp += powp<PM>(upper_fwd(pre[e]), a.p);
         float u;
         if constexpr (LAYOUT == MASK_CONST) {
           u = a.uconst;
@@ -269,14 +280,22 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
       }
       if constexpr (LAYOUT != MASK_CONST) *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    } else if constexpr (PM == PM_SL0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) SLv.ps[r][q4 + e] = 0.f;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
-  imp = wave_sum(imp);
-  if ((tid & 63) == 0) red[tid >> 6] = imp;
-  __syncthreads();
-  if (tid == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  if constexpr (PM == PM_SL0) {
+    __syncthreads();
+    sl0_tile_colsums(SLv, blockIdx.y, q0, a.c, a.colpart, tid);
+  } else {
+    imp = wave_sum(imp);
+    if ((tid & 63) == 0) red[tid >> 6] = imp;
+    __syncthreads();
+    if (tid == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  }
   ttile_store(T, actsT, a.J, j0, a.J, q0, a.c, tid);
 }
 
@@ -311,13 +330,23 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
       bf16_t dp[4];
+      float slope4[4] = {imp_scale, imp_scale, imp_scale, imp_scale};
+      if constexpr (PM == PM_SL0) {
+        const float4 sl = *(const float4*)(a.slope + (int64_t)row_group(a.offsets, a.E, j) * a.c + q0 + q4);
+        slope4[0] = sl.x;
+        slope4[1] = sl.y;
+        slope4[2] = sl.z;
+        slope4[3] = sl.w;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
         const float u = a.uconst < 0.f ? (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f) : a.uconst;
         const float m = lo + (1.f - lo) * u - dt;
-        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
-                            upper_vjp(pre[e], imp_scale * dpowp<PM>(up, a.p)));
+        float dimp;
+        if constexpr (PM == PM_SL0) dimp = slope4[e] * sl0_dpsi(up, a.g2, a.psis);
+        else dimp = imp_scale * dpowp<PM>(up, a.p);
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp));
         o[e] = f32_to_bf16(da[e] * m);
       }
       *(uint2*)(d_pre + src) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
@@ -630,12 +659,18 @@ static void launch_token_bwd(const float* d_w_part, int n_part, const int32_t* i
                              fxa, fxb, da, db, d_r_out, s);
 }
 
+// losses[0..3] = {loss, recon, activity, frequency}: recon = rec_scale * sum(rec_part),
+// activity = imp_scale * sum(imp_part), frequency = sum(freq_part) (n_freq = 0: none),
+// loss = recon_coeff recon + imp_coeff activity + freq_coeff frequency; every sum in a
+// fixed order in double.
 __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, const float* __restrict__ imp_part,
-                             int64_t n_imp, double rec_scale, double imp_scale, float recon_coeff, float imp_coeff,
+                             int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double rec_scale,
+                             double imp_scale, float recon_coeff, float imp_coeff, float freq_coeff,
                              float* __restrict__ losses) {
-  __shared__ double sr[16], si[16];
-  double r = 0.0, m = 0.0;
+  __shared__ double sr[16], si[16], sq[16];
+  double r = 0.0, m = 0.0, fq = 0.0;
   for (int i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
+  for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
   // four independent chains keep four loads in flight per lane; combined in a fixed order
   double m4[4] = {0.0, 0.0, 0.0, 0.0};
   const int64_t step = blockDim.x;
@@ -648,22 +683,26 @@ __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, cons
   m = (m4[0] + m4[1]) + (m4[2] + m4[3]);
   r = wave_sum_d(r);
   m = wave_sum_d(m);
+  fq = wave_sum_d(fq);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
+    sq[threadIdx.x / 64] = fq;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, b = 0;
+    double a = 0, b = 0, q = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       b += si[i];
+      q += sq[i];
     }
     a *= rec_scale;
     b *= imp_scale;
-    losses[0] = (float)(recon_coeff * a + imp_coeff * b);
+    losses[0] = (float)(recon_coeff * a + imp_coeff * b + freq_coeff * q);
     losses[1] = (float)a;
     losses[2] = (float)b;
+    losses[3] = (float)q;
   }
 }
 
@@ -688,15 +727,18 @@ static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
 #define PD_MF(LY, PMV) \
   hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, actsT, ub, part)
   if (ma.uconst >= 0.f) {
-    if (pm == 2) PD_MF(MASK_CONST, 2);
+    if (pm == PM_SL0) PD_MF(MASK_CONST, PM_SL0);
+    else if (pm == 2) PD_MF(MASK_CONST, 2);
     else if (pm == 1) PD_MF(MASK_CONST, 1);
     else PD_MF(MASK_CONST, 0);
   } else if (ma.layout == PD_LAYOUT_PARTITIONABLE) {
-    if (pm == 2) PD_MF(PD_LAYOUT_PARTITIONABLE, 2);
+    if (pm == PM_SL0) PD_MF(PD_LAYOUT_PARTITIONABLE, PM_SL0);
+    else if (pm == 2) PD_MF(PD_LAYOUT_PARTITIONABLE, 2);
     else if (pm == 1) PD_MF(PD_LAYOUT_PARTITIONABLE, 1);
     else PD_MF(PD_LAYOUT_PARTITIONABLE, 0);
   } else {
-    if (pm == 2) PD_MF(PD_LAYOUT_ORIGINAL, 2);
+    if (pm == PM_SL0) PD_MF(PD_LAYOUT_ORIGINAL, PM_SL0);
+    else if (pm == 2) PD_MF(PD_LAYOUT_ORIGINAL, 2);
     else if (pm == 1) PD_MF(PD_LAYOUT_ORIGINAL, 1);
     else PD_MF(PD_LAYOUT_ORIGINAL, 0);
   }
@@ -707,7 +749,8 @@ static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
                             const uint8_t* ub, float imp_scale, bf16_t* d_acts, bf16_t* d_hT, bf16_t* d_pre) {
 #define PD_MB(PMV) \
   hipLaunchKernelGGL((k_mask_bwd_tile<PMV>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_hT, d_pre)
-  if (pm == 2) PD_MB(2);
+  if (pm == PM_SL0) PD_MB(PM_SL0);
+  else if (pm == 2) PD_MB(2);
   else if (pm == 1) PD_MB(1);
   else PD_MB(0);
 #undef PD_MB
@@ -754,6 +797,8 @@ struct MoEPlan {
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
   bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *fg0, *fu0, *din, *downc, *down, *dr_a, *dr_b;
   float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
+  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
+  size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
   bf16_t *d_dout, *d_doutT, *d_acts[2], *d_hT[2], *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
   size_t imp_per_site, total;
@@ -818,6 +863,13 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.rec_part = A.take<float>(REC_BLOCKS);
   P.imp_per_site = (size_t)cdiv(D.c, TILE) * cdiv(J, TILE);
   P.imp_part = A.take<float>(P.imp_per_site * 3 * D.L);
+  P.sl0_col_per_site = (size_t)(cdiv(J, TILE) + D.E) * D.c;
+  P.sl0_slope_per_site = (size_t)D.E * D.c;
+  P.sl0_blocks_per_site = sl0_blocks(D.E, D.c);
+  P.sl0_col = A.take<float>(P.sl0_col_per_site * 3 * L);
+  P.sl0_slope = A.take<float>(P.sl0_slope_per_site * 3 * L);
+  P.sl0_act = A.take<float>(P.sl0_blocks_per_site * 3 * L);
+  P.sl0_freq = A.take<float>(P.sl0_blocks_per_site * 3 * L);
   P.d_w_part = A.take<float>(J * cdiv(D.f, TILE));
   P.delta = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
@@ -889,10 +941,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                          const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                         int layout, float p,
-                         float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
-                         float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
-                         void* stream, Recorder& rec) {
+                         int layout, const ImpSpec& imp, float recon_coeff, float* losses, float* dVg, float* dUg,
+                         float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
+                         void* workspace, size_t workspace_bytes, void* stream, Recorder& rec) {
+  int rc0;
   if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 64 || k <= 0 || k > E || c <= 0 || L <= 0)
     return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 64)");
   if (d % 8 || f % 8 || c % 8 || (T * k) % 8)
@@ -905,6 +957,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
     return fail(PD_EINVAL, "pd_moe_stack_step: unknown counter layout");
   if (!(source_value <= 1.f)) return fail(PD_EINVAL, "pd_moe_stack_step: source_value must be < 0 (drawn) or in [0, 1]");
+  if ((rc0 = check_imp_spec(imp, "pd_moe_stack_step"))) return rc0;
   const float uconst = source_value >= 0.f ? source_value : -1.f;
   const MoEDims D{T, T * k, d, f, E, k, c, L};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
@@ -933,7 +986,17 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     o1 = y1;
   };
   const int kinds[3] = {MOE_KIND_GATE, MOE_KIND_UP, MOE_KIND_DOWN};
-  const int pm = pow_mode(p);
+  const int pm = imp_mode(imp);
+  const bool sl0 = pm == PM_SL0;
+  auto sl0_fill = [&](SiteMaskArgs& ma, const LayerSave& S, int l, int si) {
+    const size_t sl = (size_t)l * 3 + si;
+    ma.offsets = S.offsets;
+    ma.E = E;
+    ma.g2 = imp.g2();
+    ma.psis = imp.psi_scale();
+    ma.colpart = P.sl0_col + sl * P.sl0_col_per_site;
+    ma.slope = P.sl0_slope + sl * P.sl0_slope_per_site;
+  };
 
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
@@ -1032,12 +1095,19 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.c = c;
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.layout = layout;
-      ma.p = p;
+      ma.p = imp.p;
       ma.delta = dlt[si];
       ma.k = k;
       ma.uconst = uconst;
+      sl0_fill(ma, S, l, si);
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
       launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], acts_out, S.actsT[si], S.ub[si], part);
+      if (sl0) {  // this site's frequencies, loss partials and backward slopes
+        const size_t sl = (size_t)l * 3 + si;
+        hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(E, c)), dim3(256), 0, s, ma.colpart, S.offsets, E, J, c,
+                           1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count, P.sl0_slope + sl * P.sl0_slope_per_site,
+                           P.sl0_act + sl * P.sl0_blocks_per_site, P.sl0_freq + sl * P.sl0_blocks_per_site);
+      }
     };
     // ---- gate and up sites: both products of each stage in one paired launch
     rec.mark(MOE_CAT_GEMM_FWD);
@@ -1092,13 +1162,19 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const int64_t nres = T * d;
   hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
                      recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
-  hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.imp_part,
-                     (int64_t)(P.imp_per_site * 3 * L), 1.0 / (double)nres, 1.0 / (double)T, recon_coeff, imp_coeff,
-                     losses);
+  if (sl0)
+    hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.sl0_act,
+                       (int64_t)(P.sl0_blocks_per_site * 3 * L), P.sl0_freq,
+                       imp.ref_count > 0.f ? (int64_t)(P.sl0_blocks_per_site * 3 * L) : (int64_t)0,
+                       1.0 / (double)nres, 1.0, recon_coeff, imp.coeff, imp.freq_coeff, losses);
+  else
+    hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.imp_part,
+                       (int64_t)(P.imp_per_site * 3 * L), (const float*)nullptr, (int64_t)0, 1.0 / (double)nres,
+                       1.0 / (double)T, recon_coeff, imp.coeff, 0.f, losses);
   // ================= backward
   bf16_t* dr = P.dr_a;
   bf16_t* dr_next = P.dr_b;
-  const float imp_scale = imp_coeff / (float)T;
+  const float imp_scale = imp.coeff / (float)T;
   const int n_wpart = (int)cdiv(f, TILE);
   for (int l = L - 1; l >= 0; --l) {
     LayerSave& S = P.layers[l];
@@ -1109,7 +1185,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.J = J;
     ma.c = c;
     ma.layout = layout;
-    ma.p = p;
+    ma.p = imp.p;
     ma.k = k;
     ma.uconst = uconst;
     set_delta(l);
@@ -1126,6 +1202,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
     ma.delta = dlt[2];
+    sl0_fill(ma, S, l, 2);
     launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0], P.d_hT[0],
                     (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     rec.mark(MOE_CAT_GEMM_DW);
@@ -1158,6 +1235,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.delta = dlt[si];
+      sl0_fill(ma, S, l, si);
       launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], P.d_hT[si],
                       (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
     }
@@ -1192,33 +1270,34 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
-                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value, int layout, float p,
-                      float imp_coeff,
-                      float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd,
-                      void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream) {
+                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value, int layout, int imp_kind,
+                      float p, float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                      float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
+                      float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                       draw_k1, use_delta, source_value, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
-                       dUd, d_ci_pre,
-                       top_idx_out, workspace, workspace_bytes, stream, rec);
+                       draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd,
+                       d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                             const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                            int layout,
-                            float p, float imp_coeff, float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu,
-                            float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
-                            size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
-                            int* n_recorded) {
+                            int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
+                            float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dVg,
+                            float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                            int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream,
+                            void** events, int32_t* categories, int capacity, int* n_recorded) {
   if (!events || !categories || capacity <= 0 || !n_recorded)
     return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
   Recorder rec{events, categories, capacity, 0, nullptr};
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                         draw_k1, use_delta, source_value, layout, p, imp_coeff, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
-                         dUd, d_ci_pre,
-                         top_idx_out, workspace, workspace_bytes, stream, rec);
+                         draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
+                         dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
   *n_recorded = rec.n;
   if (rc == PD_OK && rec.n >= capacity) return fail(PD_EINVAL, "pd_moe_stack_step_timed: event capacity too small");
   return rc;

@@ -17,10 +17,46 @@ Mirrors:
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from param_decomp_amd import _lib as L
 from param_decomp_amd import ops
+
+
+@dataclass(frozen=True)
+class ImpMin:
+    """The imp-min term of the fused steps (`pd_dense_step`, `pd_moe_stack_step`,
+    `pd_lm_stack_step`). `kind="pnorm"`: `coeff * sum upper^p / n`. `kind="smooth_l0"`:
+    the engine's `ImportanceMinimalityLoss` (`pd/core/configs.py:186-206`,
+    `pd/core/objective.py:101-131`): `coeff * sum_c f_c + frequency_coeff * sum_c f_c
+    log2(1 + reference_datapoint_count * f_c)` with `f_c = sum psi(upper) / n`,
+    `psi = c^2 / (c^2 + gamma^2)` (times `1 + gamma^2` with `normalize_at_one`), the
+    frequency term off when `reference_datapoint_count` is 0 (a single-batch estimate:
+    the EMA estimator's state lives outside the step). gamma is the schedule's value
+    at this step."""
+
+    kind: str = "pnorm"
+    p: float = 2.0
+    coeff: float = 1.0
+    gamma: float = 1.0
+    normalize_at_one: bool = False
+    frequency_coeff: float = 0.0
+    reference_datapoint_count: float = 0.0
+
+    @classmethod
+    def smooth_l0(cls, coeff: float, gamma: float, *, normalize_at_one: bool = False, frequency_coeff: float = 0.0,
+                  reference_datapoint_count: float = 0.0) -> "ImpMin":
+        return cls("smooth_l0", 2.0, coeff, gamma, normalize_at_one, frequency_coeff, reference_datapoint_count)
+
+    def c_args(self) -> list:
+        """(kind, p, gamma, normalize_at_one, coeff, freq_coeff, ref_count) for the C ABI."""
+        if self.kind not in ("pnorm", "smooth_l0"):
+            raise L.PDError(f"ImpMin: unknown kind {self.kind!r}")
+        kind = L.IMPMIN_SMOOTH_L0 if self.kind == "smooth_l0" else L.IMPMIN_PNORM
+        return [kind, float(self.p), float(self.gamma), int(self.normalize_at_one), float(self.coeff),
+                float(self.frequency_coeff), float(self.reference_datapoint_count)]
 
 
 class _ImpMin(torch.autograd.Function):

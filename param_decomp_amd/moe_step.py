@@ -4,7 +4,8 @@ One call = the clean forward on the frozen experts (pinning each layer's expert
 indices), the masked forward with every routed expert matrix decomposed (with the
 frozen delta channel the reference's stochastic masking draws, unless `use_delta` is
 off), MSE recon of
-the final residual + L_p imp-min over the selected CI, and the full backward to the
+the final residual + the imp-min term over the selected CI (L_p or the engine's
+smooth-L0 with its frequency penalty), and the full backward to the
 V/U factors of every site and to the CI preactivations. See `pd_moe_stack_step` in
 include/pd_mi355x.h for the reference citations and layouts.
 
@@ -19,6 +20,7 @@ from dataclasses import dataclass
 import torch
 
 from param_decomp_amd import _lib as L
+from param_decomp_amd.losses import ImpMin
 from param_decomp_amd.prng import Key
 
 SITE_NAMES = ("gate", "up", "down")
@@ -46,9 +48,12 @@ class MoEWeights:
 class MoEStackStep:
     def __init__(self, T: int, d: int, f: int, E: int, k: int, c: int, n_layers: int, *, device="cuda",
                  p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
-                 layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, source_value: float = -1.0):
+                 layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, source_value: float = -1.0,
+                 imp_min: ImpMin | None = None):
         self.dims = (T, d, f, E, k, c, n_layers)
-        self.p, self.imp_coeff, self.recon_coeff, self.layout = p, imp_coeff, recon_coeff, layout
+        # the imp-min term: L_p (p, imp_coeff) unless a smooth-L0 ImpMin is given
+        self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
+        self.recon_coeff, self.layout = recon_coeff, layout
         self.use_delta = bool(use_delta)
         # < 0: Threefry mask and delta draws (stochastic recon); v in [0, 1]: constant
         # sources u = d = v (0: the CI-masked recon)
@@ -56,7 +61,7 @@ class MoEStackStep:
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
         Ln = n_layers
-        self.losses = torch.empty(3, **f32)
+        self.losses = torch.empty(4, **f32)  # loss, recon, activity, frequency
         self.dV = {"gate": torch.empty(Ln, E, d, c, **f32), "up": torch.empty(Ln, E, d, c, **f32),
                    "down": torch.empty(Ln, E, f, c, **f32)}
         self.dU = {"gate": torch.empty(Ln, E, c, f, **f32), "up": torch.empty(Ln, E, c, f, **f32),
@@ -69,7 +74,8 @@ class MoEStackStep:
         T, d, f, E, k, c, Ln = self.dims
         return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
                 L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
-                draw_key[0], draw_key[1], int(self.use_delta), self.source_value, self.layout, self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.losses),
+                draw_key[0], draw_key[1], int(self.use_delta), self.source_value, self.layout,
+                *self.imp_min.c_args(), self.recon_coeff, L.ptr(self.losses),
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]

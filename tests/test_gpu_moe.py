@@ -43,33 +43,45 @@ def _make(cfg, seed, device):
     return params, x0, ci, w, ci_t, x0_t
 
 
-@pytest.mark.parametrize("cfg,partitionable,use_delta,source_value", [
-    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, None),
-    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None),
-    (mo.MoEConfig(T=120, d=32, f=24, E=6, k=3, c=40, L=2), False, True, None),
-    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, False, None),
-    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), False, False, None),
-    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, 0.0),
-    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, 0.375)])
-def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, source_value):
+# the engine's smooth-L0 imp-min with its frequency penalty (per-expert component frequencies)
+SL0 = dict(kind="smooth_l0", coeff=0.5, gamma=0.3, normalize_at_one=True, freq_coeff=0.25, ref_count=4096.0)
+
+
+@pytest.mark.parametrize("cfg,partitionable,use_delta,source_value,sl0", [
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, None, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None, None),
+    (mo.MoEConfig(T=120, d=32, f=24, E=6, k=3, c=40, L=2), False, True, None, None),
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, False, None, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), False, False, None, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, 0.0, None),
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, 0.375, None),
+    (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None, SL0),
+    (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=72, L=2), False, True, None, dict(SL0, ref_count=0.0,
+                                                                                 normalize_at_one=False))])
+def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, source_value, sl0):
+    """sl0: the smooth-L0 term (per (tile, expert) column sums of psi in the mask pass,
+    per-expert frequencies and slopes in between, the slope in the mask backward)."""
     from param_decomp_amd import _lib as L
+    from param_decomp_amd.losses import ImpMin
     from param_decomp_amd.moe_step import MoEStackStep
 
     params, x0, ci, w, ci_t, x0_t = _make(cfg, 0, device)
     key = (0, 17)
-    step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, p=2.0, imp_coeff=0.5,
-                        recon_coeff=1.5, layout=L.LAYOUT_PARTITIONABLE if partitionable else L.LAYOUT_ORIGINAL,
-                        use_delta=use_delta, source_value=-1.0 if source_value is None else source_value)
+    spec = po.ImpMin(**sl0) if sl0 else po.ImpMin("pnorm", p=2.0, coeff=0.5)
+    imp = ImpMin(spec.kind, spec.p, spec.coeff, spec.gamma, spec.normalize_at_one, spec.freq_coeff, spec.ref_count)
+    step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, recon_coeff=1.5,
+                        layout=L.LAYOUT_PARTITIONABLE if partitionable else L.LAYOUT_ORIGINAL,
+                        use_delta=use_delta, source_value=-1.0 if source_value is None else source_value, imp_min=imp)
     step.step(x0_t, w, ci_t, key)
     torch.cuda.synchronize()
     got_idx = step.top_idx.cpu().numpy()
-    ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True,
+    ref = mo.moe_stack_step(cfg, params, x0, ci, key, recon_coeff=1.5, bf16_storage=True,
                             partitionable=partitionable, use_delta=use_delta, source_value=source_value,
-                            pinned_top_idx=got_idx)
+                            pinned_top_idx=got_idx, imp_min=spec)
     for l in range(cfg.L):
         assert_routing_matches(got_idx[l], ref, l, cfg.k)
     losses = step.losses.cpu().numpy()
-    np.testing.assert_allclose(losses, [ref["loss"], ref["recon"], ref["imp"]], rtol=2e-2)
+    np.testing.assert_allclose(losses, [ref["loss"], ref["recon"], ref["imp"], ref["freq"]], rtol=2e-2, atol=1e-7)
     for l in range(cfg.L):
         for s, vn, un in (("gate", "Vg", "Ug"), ("up", "Vu", "Uu"), ("down", "Vd", "Ud")):
             _close(step.dV[s][l].cpu().numpy(), ref["grads"][l][vn], 2e-2, 1e-2, f"{vn}[{l}]")

@@ -235,6 +235,60 @@ def test_torch_restatement_matches_the_numpy_oracle():
             np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
 
 
+@pytest.mark.parametrize("normalize", [False, True])
+@pytest.mark.parametrize("ref_count", [0.0, 64.0])
+def test_selected_smooth_l0_equals_the_dense_reference_form(normalize, ref_count):
+    """A selected-emitting site's smooth-L0 terms (values [T, k, c] scattered to their
+    expert's block of the [E * c] components) equal the reference's dense formula on the
+    scattered [T, E * c] upper CI (zeros where unselected, psi(0) = 0), and the gradient
+    matches central differences of activity + frequency."""
+    rng = np.random.default_rng(5)
+    T, k, c, E = 40, 3, 4, 6
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    up = rng.uniform(0.0, 1.2, size=(T, k, c))
+    spec = po.ImpMin("smooth_l0", coeff=0.7, gamma=0.3, normalize_at_one=normalize, freq_coeff=0.4,
+                     ref_count=ref_count)
+    act, freq, grad = po.impmin_site_terms(up, spec, T, idx, E)
+    dense = np.zeros((T, E, c))
+    for t in range(T):
+        for s_ in range(k):
+            dense[t, idx[t, s_]] = up[t, s_]
+    wa, wf = po.importance_minimality_terms([dense.reshape(T, E * c)], 0.3, ref_count if ref_count else None,
+                                            normalize)
+    assert act == pytest.approx(wa, rel=1e-12) and freq == pytest.approx(wf, rel=1e-12, abs=1e-15)
+
+    def loss(u):
+        a_, f_, _ = po.impmin_site_terms(u, spec, T, idx, E)
+        return spec.loss(a_, f_)
+
+    for ii in [(0, 0, 0), (7, 2, 3), (39, 1, 1), (12, 0, 2)]:
+        e = 1e-6
+        upp, upm = up.copy(), up.copy()
+        upp[ii] += e
+        upm[ii] -= e
+        assert grad[ii] == pytest.approx((loss(upp) - loss(upm)) / (2 * e), rel=1e-5, abs=1e-9)
+
+
+def test_smooth_l0_moe_step_matches_the_autograd_restatement():
+    """The NumPy oracle's smooth-L0 + frequency backward (per-expert frequency slopes)
+    against torch autograd through the reference's scatter form, in float64."""
+    cfg = mo.MoEConfig(T=48, d=16, f=8, E=6, k=2, c=4, L=2)
+    rng = np.random.default_rng(13)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    spec = po.ImpMin("smooth_l0", coeff=0.5, gamma=0.2, normalize_at_one=True, freq_coeff=0.3, ref_count=96.0)
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), recon_coeff=1.5, imp_min=spec)
+    b = mo.moe_stack_step_torch(cfg, params, x0, ci, (3, 4), recon_coeff=1.5, imp_min=spec)
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-10)
+    assert b["imp"] == pytest.approx(a["imp"], rel=1e-10) and b["freq"] == pytest.approx(a["freq"], rel=1e-10)
+    assert a["freq"] > 0
+    for l in range(cfg.L):
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            np.testing.assert_allclose(b["grads"][l][n], a["grads"][l][n], rtol=1e-8, atol=1e-12)
+        for s in mo.SITES:
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
+
+
 def test_c_restatement_matches_the_numpy_oracle():
     """The compiled fp32 C/OpenMP restatement (the CPU baseline) against the NumPy
     oracle in float64: same expert selection, losses and every gradient to fp32
