@@ -205,15 +205,20 @@ int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_
  * h = x@V; paper-form gate g_raw = gate(h); lower/upper squashing; mask
  * m = lower + (1-lower)*uniform(mask key) (pd/core/masking.py:148-167); optional
  * delta d = uniform(delta key, [T]); y = (h*(m-d))@U + d*y_t; recon = mean((y-y_t)^2);
- * imp = sum_c mean_t (upper)^p; loss = recon_coeff*recon + imp_coeff*imp.
+ * imp-min (imp_kind): PD_IMPMIN_PNORM imp = sum_c mean_t (upper)^p, loss = recon_coeff*recon
+ * + imp_coeff*imp; PD_IMPMIN_SMOOTH_L0 the engine's term imp_coeff * sum_c f_c +
+ * freq_coeff * sum_c f_c log2(1 + ref_count f_c), f_c = mean_t psi(upper), psi =
+ * c^2/(c^2 + gamma^2) (times 1 + gamma^2 when normalize_at_one; pd/core/losses.py:340-394,
+ * pd/core/objective.py:101-131; ref_count 0 = no frequency term).
  * Gradients (overwritten, fp32 for the fp32 masters): dV [d_in,C], dU [C,d_out], gate grads.
- * losses[3] = {loss, recon, imp} fp32. mask_key / delta_key are the site's keys
- * (already split/folded). dtype bf16: x,W,V,U bf16. */
+ * losses[4] = {loss, recon, activity, frequency} fp32. mask_key / delta_key are the site's
+ * keys (already split/folded). dtype bf16: x,W,V,U bf16. */
 size_t pd_dense_step_workspace_size(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H);
 int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x, const void* W,
                   const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
                   const float* b_out, uint32_t mask_k0, uint32_t mask_k1, uint32_t delta_k0, uint32_t delta_k1,
-                  int use_delta, int draw_dtype, int layout, float p, float imp_coeff, float recon_coeff,
+                  int use_delta, int draw_dtype, int layout, int imp_kind, float p, float gamma,
+                  int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count, float recon_coeff,
                   float* losses, float* dV, float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out,
                   void* workspace, size_t workspace_bytes, void* stream);
 
@@ -227,8 +232,9 @@ int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, 
 int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
                         const float* w_out, const float* b_out, uint32_t mask_k0, uint32_t mask_k1,
-                        uint32_t delta_k0, uint32_t delta_k1, int use_delta, int draw_dtype, int layout, float p,
-                        float imp_coeff, float recon_coeff, float* losses, float* dV, float* dU, float* dw_in,
+                        uint32_t delta_k0, uint32_t delta_k1, int use_delta, int draw_dtype, int layout,
+                        int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff, float freq_coeff,
+                        float ref_count, float recon_coeff, float* losses, float* dV, float* dU, float* dw_in,
                         float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes,
                         void* stream, void** events);
 
@@ -362,21 +368,26 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
  * layer), [N, C]) and d = uniform(fold_in(fold_in(split(draw_key)[1], kind), layer), [N])
  * in bf16 (pd/targets/transformer.py:1048-1058, 1424-1451); use_delta = 0 is d = 0.
  * Loss: recon_coeff * mean KL(softmax(clean logits) || softmax(masked logits)) (the
- * streamed form, pd/targets/losses.py:102-163, over n_kl_chunks vocab chunks) + imp_coeff *
- * sum_sites sum_c mean_tokens upper(ci)^p.
+ * streamed form, pd/targets/losses.py:102-163, over n_kl_chunks vocab chunks) + the
+ * imp-min term: PD_IMPMIN_PNORM: imp_coeff * sum_sites sum_c mean_tokens upper(ci)^p;
+ * PD_IMPMIN_SMOOTH_L0: imp_coeff * sum_sites sum_c f_c + freq_coeff * sum f_c log2(1 +
+ * ref_count f_c), f_c = mean_tokens psi(upper) (as pd_moe_stack_step, one component
+ * block per site).
  * Shapes: N = B*T tokens (int32 ids [N], T % 64 == 0); head_dim 64 (d = 64 n_head);
  * n_head % n_kv_head == 0; d, d_mlp % 64 == 0; C[6] each % 8 == 0; vocab % n_kl_chunks == 0.
  * wte [vocab, d] bf16 (embedding and head); ln1, ln2 [L, d], norm [d] fp32 (values the
  * bf16 weights hold); per kind k: W[k] [L, d_out, d_in], V[k] [L, d_in, C_k], U[k]
- * [L, C_k, d_out] bf16; ci_pre[k] [L, N, C_k] bf16. Outputs: losses [3] = (total, kl,
- * imp) fp32; dV[k], dU[k] fp32 in V/U's layouts; d_ci_pre[k] bf16 in ci_pre's layout. */
+ * [L, C_k, d_out] bf16; ci_pre[k] [L, N, C_k] bf16. Outputs: losses [4] = (total, kl,
+ * activity, frequency) fp32; dV[k], dU[k] fp32 in V/U's layouts; d_ci_pre[k] bf16 in
+ * ci_pre's layout. */
 size_t pd_lm_stack_workspace_size(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab,
                                   int L, const int32_t* C, int use_delta, int n_kl_chunks);
 int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
                      const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
-                     int use_delta, int layout, float p, float imp_coeff, float recon_coeff, int n_kl_chunks,
+                     int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                     float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, int n_kl_chunks,
                      float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
                      size_t workspace_bytes, void* stream);
 /* pd_lm_stack_step recording HIP events at phase boundaries (categories: 0 per-step weight
@@ -387,8 +398,9 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                            const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
                            const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
-                           uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff, float recon_coeff,
-                           int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                           uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
+                           int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                            void** events, int32_t* categories, int capacity, int* n_recorded);
 

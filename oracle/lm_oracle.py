@@ -293,8 +293,11 @@ def site_keys(draw_key, cfg: LMConfig, kind: str, layer: int, partitionable=True
 
 
 def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64):
-    """One stochastic-recon KL + L_p imp-min step, forward and backward.
+                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64, imp_min=None):
+    """One stochastic-recon KL + imp-min step, forward and backward. The imp-min term is
+    L_p (p, imp_coeff) or `imp_min` (a `pd_oracle.ImpMin`; smooth-L0 with the frequency
+    penalty as the reference writes it, `pd/core/losses.py:340-394`: per-site means of
+    psi over the tokens, differentiated by autograd).
 
     params: wte [V, d] (the embedding and the tied head), norm [d], layers: list of
     dicts (ln1, ln2, W_<kind> [d_out, d_in], V_<kind> [d_in, C], U_<kind> [C, d_out])
@@ -302,8 +305,9 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
     `uniforms[l][kind] = (u [b*t, C], d [b*t])` replaces the Threefry draws when given.
     `dtype` torch.float32 runs the same arithmetic in fp32 (the CPU baseline's timing
     form; the float64 default is the checker).
-    Returns dict(loss, recon, imp, dV[l][kind], dU[l][kind], d_ci_pre[l][kind], u, delta)."""
+    Returns dict(loss, recon, imp, freq, dV[l][kind], dU[l][kind], d_ci_pre[l][kind], u, delta)."""
     rb = _rounder(bf16_storage)
+    spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
     b, t = tokens.shape
     N = b * t
     T = lambda a, g=False: torch.tensor(np.asarray(a, np.float64), dtype=dtype, requires_grad=g)  # noqa: E731
@@ -323,6 +327,7 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
         clean_logits = logits(prm, act_c)
     masks, deltas, pres, us, ds = [], [], {}, {}, {}
     imp = torch.zeros((), dtype=dtype)
+    freq = torch.zeros((), dtype=dtype)
     for l in range(cfg.n_layers):
         masks.append({})
         deltas.append({})
@@ -343,17 +348,26 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
             us[(l, kind)], ds[(l, kind)] = u, dl
             lo = _LowerLeaky.apply(pre)
             up = _UpperLeaky.apply(pre)
-            imp = imp + (up**p).sum() / N
+            if spec.kind == "pnorm":
+                imp = imp + (up**spec.p).sum() / N
+            else:
+                g2 = spec.gamma**2
+                psi = up**2 / (up**2 + g2) * ((1.0 + g2) if spec.normalize_at_one else 1.0)
+                fr = psi.mean(0)
+                imp = imp + fr.sum()
+                if spec.ref_count > 0:
+                    freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
             masks[l][kind] = (lo + (1.0 - lo) * T(u)).reshape(b, t, C)
             deltas[l][kind] = T(dl).reshape(b, t) if use_delta else None
     act_m = forward(cfg, prm, r0, masks, deltas, rb=rb)
     recon = kl_per_position(logits(prm, act_m), clean_logits)
-    loss = recon_coeff * recon + imp_coeff * imp
+    loss = recon_coeff * recon + spec.coeff * imp + (spec.freq_coeff * freq if spec.kind == "smooth_l0" else 0.0)
     wrt = [prm["layers"][l]["V_" + k] for l, k in leaves] + [prm["layers"][l]["U_" + k] for l, k in leaves] + [
         pres[key] for key in pres]
     grads = torch.autograd.grad(loss, wrt)
     n = len(leaves)
     out = dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()),
+               freq=float(freq.detach()),
                dV=[{} for _ in range(cfg.n_layers)],
                dU=[{} for _ in range(cfg.n_layers)], d_ci_pre=[{} for _ in range(cfg.n_layers)], u=us, delta=ds)
     for i, (l, k) in enumerate(leaves):

@@ -454,6 +454,7 @@ class DenseStepResult:
     dV: np.ndarray
     dU: np.ndarray
     dgate: tuple
+    freq: float = 0.0
 
 
 def round_bf16(a):
@@ -474,7 +475,8 @@ def round_bf16(a):
 
 
 def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0, imp_coeff=1.0,
-                    recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True, bf16_storage=False):
+                    recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True, bf16_storage=False,
+                    imp_min=None):
     """One stochastic-recon + importance-minimality fwd+bwd for ONE decomposed site whose
     input `x` is the clean input (the single-linear workload). It composes:
     clean target `x@W.T` (`pd/core/train.py:578-606`, detached), CI gate on `h = x@V`
@@ -489,8 +491,9 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     `x@V`, `(x@V)*coef`, `@U` and the clean output are bf16, and their cotangents come
     back in bf16); products and reductions are exact (float64) in between. The gate
     MLP itself is evaluated exactly on the bf16 `h` — finer than the reference's bf16
-    MLP arithmetic."""
+    MLP arithmetic. `imp_min` (an `ImpMin`) replaces the L_p term of p / imp_coeff."""
     rb = round_bf16 if bf16_storage else (lambda a: a)
+    spec = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
     y_t = rb(x @ W.T)
     h = rb(x @ V)
     g_raw = gate_forward(h, gate)
@@ -502,19 +505,18 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     y = rb(acts @ U)
     y_masked = y if d is None else y + d[:, None] * y_t
     recon = mse(y_masked, y_t)
-    imp = impmin_pnorm(up, p)
-    loss = recon_coeff * recon + imp_coeff * imp
+    imp, freq, dup = impmin_site_terms(up, spec, up.shape[0])
+    loss = recon_coeff * recon + spec.loss(imp, freq)
     dy = rb(recon_coeff * 2.0 * (y_masked - y_t) / y.size)
     dU = acts.T @ dy
     da = rb(dy @ U.T)
     dh_direct = da * coef
     dlo = da * h * (1.0 - u)
     dgraw = lower_leaky_vjp(g_raw, dlo)
-    dup = imp_coeff * impmin_pnorm_grad(up, p)
     dgraw = dgraw + upper_leaky_vjp(g_raw, dup)
     dh_gate, dwi, dbi, dwo, dbo = gate_backward(h, gate, dgraw)
     dV = x.T @ rb(dh_direct + dh_gate)
-    return DenseStepResult(loss, recon, imp, y_masked, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo))
+    return DenseStepResult(loss, recon, imp, y_masked, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo), freq)
 
 
 # ---------------------------------------------------------------- MoE routing

@@ -62,9 +62,9 @@ _SIGNATURES = {
     "pd_masked_linear_bwd_noalloc": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64] + [_c_p] * 16),
     "pd_dense_step_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32]),
     "pd_dense_step": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 8 + [_c_u32] * 4 +
-                      [_c_i32] * 3 + [_c_f32] * 3 + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),
+                      [_c_i32] * 3 + _IMP_ARGS + [_c_f32] + [_c_p] * 7 + [_c_p, _c_sz, _c_p]),
     "pd_dense_step_timed": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32] + [_c_p] * 8 + [_c_u32] * 4 +
-                            [_c_i32] * 3 + [_c_f32] * 3 + [_c_p] * 7 + [_c_p, _c_sz, _c_p, _c_p]),
+                            [_c_i32] * 3 + _IMP_ARGS + [_c_f32] + [_c_p] * 7 + [_c_p, _c_sz, _c_p, _c_p]),
     "pd_route_uniform_k": (_c_i32, [_c_u32, _c_u32, _c_i64, _c_i32, _c_i32, _c_p, _c_p]),
     "pd_route_static_p": (_c_i32, [_c_u32, _c_u32, _c_i64, _c_i32, _c_f32, _c_i32, _c_p, _c_p]),
     "pd_router_topk": (_c_i32, [_c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
@@ -84,12 +84,12 @@ _SIGNATURES = {
     "pd_lm_stack_workspace_size": (_c_sz, [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32, _c_p, _c_i32, _c_i32]),
     "pd_lm_stack_step": (_c_i32,
                          [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
-                         [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + [_c_f32] * 3 + [_c_i32] + [_c_p] * 5 +
+                         [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] + [_c_p] * 5 +
                          [_c_sz, _c_p]),
     "pd_lm_stack_step_timed": (_c_i32,
                                [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
-                               [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + [_c_f32] * 3 + [_c_i32] + [_c_p] * 5 +
-                               [_c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
+                               [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] +
+                               [_c_p] * 5 + [_c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
     "pd_ci_mlp_workspace_size": (_c_sz, [_c_i32, _c_p, _c_i64]),
     "pd_ci_mlp_fwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 5 + [_c_sz, _c_p]),
     "pd_ci_mlp_bwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 7 + [_c_sz, _c_p]),

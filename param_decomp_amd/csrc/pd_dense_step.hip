@@ -19,7 +19,7 @@
 //   dV  = x^T @ dh         A=x^T [d_in,T]    B=dh^T [C,T]
 #include <algorithm>
 
-#include "pd_common.hpp"
+#include "pd_impmin.hpp"
 
 namespace pd {
 
@@ -34,7 +34,15 @@ struct StepParams {
   float p, imp_scale;     // imp_scale = imp_coeff / T
   const float* delta;     // [T] per-token delta draw, or NULL (d = 0)
   uint8_t* ubits;         // [T, C] bf16-draw uniforms as 7-bit integers (bf16 draws only)
+  // smooth-L0 imp-min (sl0 != 0): psi = psis * v^2 / (v^2 + g2); the forward writes each
+  // 64-token chunk's column sums of psi to colpart [chunk][C], the backward reads the
+  // per-component slope [C]
+  int sl0;
+  float g2, psis;
+  float* colpart;
+  const float* slope;
 };
+
 
 __device__ inline float step_delta(const StepParams& s, int64_t t) { return s.delta ? s.delta[t] : 0.f; }
 
@@ -76,6 +84,14 @@ struct RowPack<float> {
 __device__ inline float pow_p(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
 __device__ inline float dpow_p(float b, float p) {
   return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f));
+}
+
+// The per-element imp-min value (psi or upper^p) and its derivative's factor.
+__device__ inline float step_imp(const StepParams& s, float up) {
+  return s.sl0 ? sl0_psi(up, s.g2, s.psis) : pow_p(up, s.p);
+}
+__device__ inline float step_dimp(const StepParams& s, int64_t c, float up) {
+  return s.sl0 ? s.slope[c] * sl0_dpsi(up, s.g2, s.psis) : s.imp_scale * dpow_p(up, s.p);
 }
 
 // dst[c][r] = src[r][c] for a [R, Cc] matrix; 64x64 tiles through LDS.
@@ -124,7 +140,7 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
   const int64_t c = (int64_t)blockIdx.x * SITE_COLS + threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.y * SITE_ROWS;
   const int64_t r1 = r0 + SITE_ROWS < s.T ? r0 + SITE_ROWS : s.T;
-  float imp = 0.f;
+  float imp = 0.f, col = 0.f;
   if (c < s.C) {
     float wi[16], bi[16], wo[16];
 #pragma unroll
@@ -144,7 +160,9 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
       for (int j = 0; j < 16; ++j) g = fmaf(wo[j], gelu_only<PRECISE>(fmaf(wi[j], hv, bi[j])), g);
       g_raw[i] = g;
       const float lo = lower_fwd(g);
-      imp += pow_p(upper_fwd(g), s.p);
+      const float iv = step_imp(s, upper_fwd(g));
+      imp += iv;
+      col += iv;
       const float u = step_uniform_fwd(s, i, n);
       const float m = lo + (1.f - lo) * u;
       const float a = hv * (m - step_delta(s, t));
@@ -152,6 +170,7 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
       pack.push(a);
       if (((t - r0) % RowPack<T>::N) == RowPack<T>::N - 1) pack.flush(actsT + c * s.T + t + 1 - RowPack<T>::N);
     }
+    if (s.sl0) s.colpart[(int64_t)blockIdx.y * s.C + c] = col;
   }
   imp = wave_sum(imp);
   if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = imp;
@@ -265,7 +284,7 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
   const int64_t c = c0 + lane;
   const int64_t r0 = ((int64_t)blockIdx.y * FWD_WAVES + w) * 64;
   const int64_t r1 = r0 + 64 < s.T ? r0 + 64 : s.T;
-  float imp = 0.f;
+  float imp = 0.f, col = 0.f;
   if (c < s.C && r0 < s.T) {
     const float4 rg = rng[c];
     const float* tl = (const float*)(lt + lane * KS);
@@ -283,7 +302,9 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
         const float g = gate_eval(tl, (hv - rg.x) * rg.y);
         g_raw[i] = g;  // the backward's squashing branches see this exact value
         const float lo = lower_fwd(g);
-        imp += pow_p(upper_fwd(g), s.p);
+        const float iv = step_imp(s, upper_fwd(g));
+        imp += iv;
+        col += iv;
         const float u = step_uniform_fwd(s, i, n);
         const float m = lo + (1.f - lo) * u;
         const float a = hv * (m - step_delta(s, t));
@@ -292,6 +313,7 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
       }
       pack.flush(actsT + c * s.T + t8);
     }
+    if (s.sl0) s.colpart[(r0 / 64) * s.C + c] = col;
   }
   imp = wave_sum(imp);
   if (lane == 0) red[w] = imp;
@@ -370,7 +392,7 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da
       const float u = step_uniform_bwd(s, i, n);
       const float m = lo + (1.f - lo) * u;
       float dhv = dav * (m - step_delta(s, t));
-      const float dg = lower_vjp(g, dav * hv * (1.f - u)) + upper_vjp(g, s.imp_scale * dpow_p(upper_fwd(g), s.p));
+      const float dg = lower_vjp(g, dav * hv * (1.f - u)) + upper_vjp(g, step_dimp(s, c, upper_fwd(g)));
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         GeluOut go = gelu_and_grad<PRECISE>(fmaf(wi[j], hv, bi[j]));
@@ -413,38 +435,45 @@ __global__ void k_step_gate_reduce(const float* __restrict__ partial, int64_t ch
     db_out[c] = acc;
 }
 
-// losses[0..2] = {loss, recon, imp} from the two partial arrays (one block, fixed order)
+// losses[0..3] = {loss, recon, activity, frequency} from the partial arrays (one block,
+// fixed order): activity = imp_scale * sum(imp_part), frequency = sum(freq_part).
 __global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec, const float* __restrict__ imp_part,
-                              int64_t n_imp, double rec_scale, double imp_scale, float recon_coeff, float imp_coeff,
+                              int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double rec_scale,
+                              double imp_scale, float recon_coeff, float imp_coeff, float freq_coeff,
                               float* __restrict__ losses) {
-  __shared__ double sr[16], si[16];
-  double r = 0.0, m = 0.0;
+  __shared__ double sr[16], si[16], sq[16];
+  double r = 0.0, m = 0.0, fq = 0.0;
   for (int64_t i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
   for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
   r = wave_sum_d(r);
   m = wave_sum_d(m);
+  fq = wave_sum_d(fq);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
+    sq[threadIdx.x / 64] = fq;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, b = 0;
+    double a = 0, b = 0, q = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       b += si[i];
+      q += sq[i];
     }
     a *= rec_scale;
     b *= imp_scale;
-    losses[0] = (float)(recon_coeff * a + imp_coeff * b);
+    losses[0] = (float)(recon_coeff * a + imp_coeff * b + freq_coeff * q);
     losses[1] = (float)a;
     losses[2] = (float)b;
+    losses[3] = (float)q;
   }
 }
 
 struct StepWorkspace {
   size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, rng_part, rng, tab,
-      total;
+      sl0_col, sl0_slope, sl0_act, sl0_freq, total;
 };
 
 static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C) {
@@ -477,6 +506,10 @@ static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_o
   take(w.rng_part, 8 * cdiv(T, RANGE_ROWS) * C);
   take(w.rng, 16 * C);
   take(w.tab, 8 * C * (GATE_KNOTS + 1));
+  take(w.sl0_col, 4 * (size_t)(cdiv(T, 64) + 1) * C);
+  take(w.sl0_slope, 4 * (size_t)C);
+  take(w.sl0_act, 4 * (size_t)sl0_blocks(1, (int)C));
+  take(w.sl0_freq, 4 * (size_t)sl0_blocks(1, (int)C));
   w.total = o;
   return w;
 }
@@ -492,7 +525,7 @@ static void launch_transpose(const void* src, int64_t R, int64_t Cc, void* dst, 
 static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                            const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
                            const float* w_out, const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0,
-                           uint32_t dk1, int use_delta, int draw_dtype, int layout, float p, float imp_coeff,
+                           uint32_t dk1, int use_delta, int draw_dtype, int layout, const ImpSpec& imp,
                            float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
                            float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
                            void** events) {
@@ -504,6 +537,7 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
     return fail(PD_EINVAL, "pd_dense_step: bad args");
   if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_dense_step: dtype");
   if (draw_dtype != PD_DTYPE_F32 && draw_dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_dense_step: draw dtype");
+  if (int e = check_imp_spec(imp, "pd_dense_step")) return e;
   StepWorkspace L = step_layout(dtype, T, d_in, d_out, C);
   if (!workspace || workspace_bytes < L.total) return fail(PD_EWORKSPACE, "pd_dense_step: workspace too small");
   if (cdiv(T, SITE_ROWS) > 65535 || cdiv(d_in, TP) > 65535 || cdiv(C, TP) > 65535)
@@ -519,7 +553,12 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   float* gate_part = (float*)(ws + L.gate);
   const bool bf = dtype == PD_DTYPE_BF16;
   float* delta = use_delta ? (float*)(ws + L.delta) : nullptr;
-  StepParams sp{T, C, mk0, mk1, draw_dtype, layout, p, imp_coeff / (float)T, delta, (uint8_t*)(ws + L.ubits)};
+  const bool sl0 = imp.kind == PD_IMPMIN_SMOOTH_L0;
+  float* sl0_slope = (float*)(ws + L.sl0_slope);
+  float* sl0_act = (float*)(ws + L.sl0_act);
+  float* sl0_freq = (float*)(ws + L.sl0_freq);
+  StepParams sp{T, C, mk0, mk1, draw_dtype, layout, imp.p, imp.coeff / (float)T, delta, (uint8_t*)(ws + L.ubits),
+                sl0 ? 1 : 0, imp.g2(), imp.psi_scale(), (float*)(ws + L.sl0_col), sl0_slope};
   const dim3 cgrid((unsigned)cdiv(C, SITE_COLS), (unsigned)cdiv(T, SITE_ROWS));
   const dim3 rgrid((unsigned)cdiv(d_out, TP), (unsigned)cdiv(T, TP));
   int rc;
@@ -557,6 +596,10 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   } else
     hipLaunchKernelGGL((k_step_fwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)h, w_in, b_in, w_out,
                        b_out, sp, graw, (float*)acts, (float*)actsT, imp_part);
+  if (sl0)  // per-component frequencies, loss partials and backward slopes
+    hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(1, (int)C)), dim3(256), 0, s, sp.colpart,
+                       (const int32_t*)nullptr, 1, T, (int)C, 1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count,
+                       sl0_slope, sl0_act, sl0_freq);
   if ((rc = check_launch("pd_dense_step fwd"))) return rc;
   PD_MARK(4);
   if ((rc = pd_gemm(dtype, T, d_out, C, acts, C, 0, UT, C, 1, y, d_out, dtype, 1.f, 0.f, stream))) return rc;
@@ -571,8 +614,15 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   if ((rc = check_launch("pd_dense_step recon"))) return rc;
   PD_MARK(6);
   const int64_t n_imp = bf ? (int64_t)fgrid.x * fgrid.y : (int64_t)cgrid.x * cgrid.y;
-  hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), imp_part,
-                     n_imp, 1.0 / (double)(T * d_out), 1.0 / (double)T, recon_coeff, imp_coeff, losses);
+  const int64_t n_sl0 = sl0_blocks(1, (int)C);
+  if (sl0)
+    hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), sl0_act,
+                       n_sl0, sl0_freq, imp.ref_count > 0.f ? n_sl0 : (int64_t)0, 1.0 / (double)(T * d_out), 1.0,
+                       recon_coeff, imp.coeff, imp.freq_coeff, losses);
+  else
+    hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), imp_part,
+                       n_imp, (const float*)nullptr, (int64_t)0, 1.0 / (double)(T * d_out), 1.0 / (double)T,
+                       recon_coeff, imp.coeff, 0.f, losses);
   PD_MARK(7);
   if ((rc = pd_gemm(dtype, C, d_out, T, actsT, T, 0, dyT, T, 1, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
     return rc;
@@ -611,25 +661,28 @@ size_t pd_dense_step_workspace_size(int dtype, int64_t T, int64_t d_in, int64_t 
 int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x, const void* W,
                   const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
                   const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0, uint32_t dk1, int use_delta,
-                  int draw_dtype, int layout, float p, float imp_coeff, float recon_coeff, float* losses, float* dV,
+                  int draw_dtype, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                  float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dV,
                   float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out, void* workspace,
                   size_t workspace_bytes, void* stream) {
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
-                         use_delta, draw_dtype, layout, p, imp_coeff, recon_coeff, losses, dV, dU, dw_in, db_in,
-                         dw_out, db_out, workspace, workspace_bytes, stream, nullptr);
+                         use_delta, draw_dtype, layout, imp, recon_coeff, losses, dV, dU, dw_in, db_in, dw_out, db_out,
+                         workspace, workspace_bytes, stream, nullptr);
 }
 
 int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
                         const float* w_out, const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0,
-                        uint32_t dk1, int use_delta, int draw_dtype, int layout, float p, float imp_coeff,
-                        float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
-                        float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
-                        void** events) {
+                        uint32_t dk1, int use_delta, int draw_dtype, int layout, int imp_kind, float p, float gamma,
+                        int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count, float recon_coeff,
+                        float* losses, float* dV, float* dU, float* dw_in, float* db_in, float* dw_out,
+                        float* db_out, void* workspace, size_t workspace_bytes, void* stream, void** events) {
   if (!events) return fail(PD_EINVAL, "pd_dense_step_timed: events required");
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
-                         use_delta, draw_dtype, layout, p, imp_coeff, recon_coeff, losses, dV, dU, dw_in, db_in,
-                         dw_out, db_out, workspace, workspace_bytes, stream, events);
+                         use_delta, draw_dtype, layout, imp, recon_coeff, losses, dV, dU, dw_in, db_in, dw_out, db_out,
+                         workspace, workspace_bytes, stream, events);
 }
 
 }  // extern "C"

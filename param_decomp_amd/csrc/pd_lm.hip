@@ -28,7 +28,7 @@
 #include <vector>
 
 #include "pd_common.hpp"
-#include "pd_tiles.hpp"
+#include "pd_impmin.hpp"
 
 namespace pd {
 
@@ -188,6 +188,11 @@ struct LMMaskArgs {
   float p;
   const float* delta;  // [N] or NULL (d = 0)
   int64_t ld;          // row stride of acts / d_xV (the concatenated operand)
+  // smooth-L0 imp-min (PM_SL0): psi = psis * v^2 / (v^2 + g2); per-tile column sums of
+  // psi out (colpart), per-component slopes in (slope)
+  float g2, psis;
+  float* colpart;
+  const float* slope;
 };
 
 #define PD_LM_ROW(pass) ((threadIdx.x >> 4) + 16 * (pass))
@@ -202,11 +207,13 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
                                                      uint8_t* __restrict__ ubits, float* __restrict__ imp_part) {
   __shared__ TTile Tt;
   __shared__ float red[4];
+  __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
   const int tid = threadIdx.x;
   const int64_t n0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_LM_COL;
   const int64_t total = a.N * a.C;
   const bool qok = q0 + q4 < a.C;
+  if constexpr (PM == PM_SL0) sl0_tile_groups(SLv, nullptr, 1, n0, a.N, tid);
   float imp = 0.f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
@@ -224,7 +231,8 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
-        imp += powp<PM>(upper_fwd(pre[e]), a.p);
+        if constexpr (PM == PM_SL0) SLv.ps[r][q4 + e] = sl0_psi(upper_fwd(pre[e]), a.g2, a.psis);
+        else imp += powp<PM>(upper_fwd(pre[e]), a.p);
         const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
         ub |= kb << (8 * e);
         const float u = (float)kb * (1.f / 128.f);
@@ -232,14 +240,22 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
       }
       *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    } else if constexpr (PM == PM_SL0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) SLv.ps[r][q4 + e] = 0.f;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
   }
-  imp = wave_sum(imp);
-  if ((tid & 63) == 0) red[tid >> 6] = imp;
-  __syncthreads();
-  if (tid == 0) imp_part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  if constexpr (PM == PM_SL0) {
+    __syncthreads();
+    sl0_tile_colsums(SLv, blockIdx.y, q0, a.C, a.colpart, tid);
+  } else {
+    imp = wave_sum(imp);
+    if ((tid & 63) == 0) red[tid >> 6] = imp;
+    __syncthreads();
+    if (tid == 0) imp_part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+  }
   ttile_store(Tt, actsT, a.N, n0, a.N, q0, a.C, tid);
 }
 
@@ -271,13 +287,23 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
       bf16_t dp[4];
+      float slope4[4] = {imp_scale, imp_scale, imp_scale, imp_scale};
+      if constexpr (PM == PM_SL0) {
+        const float4 sl = *(const float4*)(a.slope + q0 + q4);
+        slope4[0] = sl.x;
+        slope4[1] = sl.y;
+        slope4[2] = sl.z;
+        slope4[3] = sl.w;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
         const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
         const float m = lo + (1.f - lo) * u - dt;
-        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) +
-                            upper_vjp(pre[e], imp_scale * dpowp<PM>(up, a.p)));
+        float dimp;
+        if constexpr (PM == PM_SL0) dimp = slope4[e] * sl0_dpsi(up, a.g2, a.psis);
+        else dimp = imp_scale * dpowp<PM>(up, a.p);
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp));
         o[e] = f32_to_bf16(da[e] * m);
       }
       *(uint2*)(d_pre + idx) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
@@ -495,32 +521,39 @@ __global__ __launch_bounds__(256) void k_lm_gelu_bwd(const bf16_t* __restrict__ 
   }
 }
 
-// losses[0..2] = (recon_coeff * kl + imp_coeff * imp, kl, imp) with kl = mean of the
-// position KLs and imp = sum of the partials / N, each added in a fixed order in double.
+// losses[0..3] = (recon_coeff kl + imp_coeff act + freq_coeff freq, kl, act, freq) with
+// kl = mean of the position KLs, act = imp_scale * sum of the imp partials, freq = sum
+// of the frequency partials (none when n_freq = 0), each added in a fixed order in double.
 __global__ void k_lm_losses(const float* __restrict__ pos_kl, int64_t N, const float* __restrict__ imp_part,
-                            int64_t n_imp, float recon_coeff, float imp_coeff, float* __restrict__ losses) {
-  __shared__ double sr[16], si[16];
-  double r = 0.0, m = 0.0;
+                            int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double imp_scale,
+                            float recon_coeff, float imp_coeff, float freq_coeff, float* __restrict__ losses) {
+  __shared__ double sr[16], si[16], sq[16];
+  double r = 0.0, m = 0.0, fq = 0.0;
   for (int64_t i = threadIdx.x; i < N; i += blockDim.x) r += pos_kl[i];
   for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
+  for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
   r = wave_sum_d(r);
   m = wave_sum_d(m);
+  fq = wave_sum_d(fq);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
+    sq[threadIdx.x / 64] = fq;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, c = 0;
+    double a = 0, c = 0, q = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       c += si[i];
+      q += sq[i];
     }
     a /= (double)N;
-    c /= (double)N;
-    losses[0] = (float)(recon_coeff * a + imp_coeff * c);
+    c *= imp_scale;
+    losses[0] = (float)(recon_coeff * a + imp_coeff * c + freq_coeff * q);
     losses[1] = (float)a;
     losses[2] = (float)c;
+    losses[3] = (float)q;
   }
 }
 
@@ -556,6 +589,8 @@ struct Arena {
 struct LMSiteSave {
   bf16_t *xV, *acat, *actsT;
   uint8_t* ub;
+  // smooth-L0: tile column sums of psi, per-component slopes, loss partials (act, freq)
+  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;
 };
 
 struct LMLayerSave {
@@ -574,6 +609,8 @@ struct LMPlan {
   bf16_t *dr_a, *dr_b, *drT, *dacts, *dcat, *dxVT, *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
   char *kl_ws, *sk_ws;
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
+  float *sl0_act, *sl0_freq;  // every site's smooth-L0 loss partials, contiguous
+  size_t sl0_blocks_total;
 };
 
 static size_t site_imp_blocks(const LMDims& D, int k) { return (size_t)cdiv(D.C[k], TILE) * cdiv(D.N, TILE); }
@@ -647,6 +684,22 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
     P.imp_total += P.imp_per_site[k] * D.L;
   }
   P.imp_part = A.take<float>(P.imp_total);
+  size_t nblk = 0;
+  for (int l = 0; l < D.L; ++l)
+    for (int k = 0; k < LM_NK; ++k) nblk += sl0_blocks(1, D.C[k]);
+  P.sl0_blocks_total = nblk;
+  P.sl0_act = A.take<float>(nblk);
+  P.sl0_freq = A.take<float>(nblk);
+  nblk = 0;
+  for (int l = 0; l < D.L; ++l)
+    for (int k = 0; k < LM_NK; ++k) {
+      LMSiteSave& S = P.layers[l].site[k];
+      S.sl0_col = A.take<float>((size_t)(cdiv(N, TILE) + 1) * D.C[k]);
+      S.sl0_slope = A.take<float>(D.C[k]);
+      S.sl0_act = P.sl0_act ? P.sl0_act + nblk : nullptr;
+      S.sl0_freq = P.sl0_freq ? P.sl0_freq + nblk : nullptr;
+      nblk += sl0_blocks(1, D.C[k]);
+    }
   P.pos_kl = A.take<float>(N);
   P.stats = A.take<float>(N * 5);
   P.gpos = A.take<float>(N);
@@ -749,10 +802,11 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                         const int32_t* tokens, const void* wte, const float* ln1, const float* ln2, const float* norm,
                         float eps, float rope_base, const void* const* W, const void* const* Vf, const void* const* Uf,
                         const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
-                        float p, float imp_coeff, float recon_coeff, int n_chunks, float* losses, float* const* dV,
+                        const ImpSpec& imp, float recon_coeff, int n_chunks, float* losses, float* const* dV,
                         float* const* dU, void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                         LMRecorder& rec) {
   const char* what = "pd_lm_stack_step";
+  if (int e = check_imp_spec(imp, what)) return e;
   if (B <= 0 || T <= 0 || d <= 0 || H <= 0 || KV <= 0 || f <= 0 || V <= 0 || L <= 0 || n_chunks <= 0 || !Cs)
     return fail(PD_EINVAL, std::string(what) + ": bad dims");
   if (H % KV) return fail(PD_EINVAL, std::string(what) + ": n_head must be a multiple of n_kv_head");
@@ -788,7 +842,8 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   rec.s = s;
   const int64_t N = D.N, BH = D.BH();
   const float log2b = log2f(rope_base), att_scale = 1.f / sqrtf((float)LM_HD);
-  const int pm = pow_mode(p);
+  const int pm = imp_mode(imp);
+  const bool sl0 = pm == PM_SL0;
   int rc;
   auto bfp = [](const void* base, size_t off) { return (const bf16_t*)base + off; };
   auto rows4 = [](int64_t n) { return dim3((unsigned)cdiv(n, 4)); };
@@ -883,9 +938,13 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     ma.N = N;
     ma.C = D.C[k];
     site_key(k, l, ma.k0, ma.k1);
-    ma.p = p;
+    ma.p = imp.p;
     ma.delta = D.use_delta ? P.delta + ((size_t)l * LM_NK + k) * N : nullptr;
     ma.ld = D.kcat(k);
+    ma.g2 = imp.g2();
+    ma.psis = imp.psi_scale();
+    ma.colpart = P.layers[l].site[k].sl0_col;
+    ma.slope = P.layers[l].site[k].sl0_slope;
     return ma;
   };
   // site forward: x [N, d_in] (and the site's saves) -> out [N, d_out]
@@ -908,15 +967,21 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 #define PD_LMF(LY, PMV) \
   hipLaunchKernelGGL((k_lm_mask_fwd<LY, PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.acat, S.actsT, S.ub, part)
     if (layout == PD_LAYOUT_PARTITIONABLE) {
-      if (pm == 2) PD_LMF(PD_LAYOUT_PARTITIONABLE, 2);
+      if (pm == PM_SL0) PD_LMF(PD_LAYOUT_PARTITIONABLE, PM_SL0);
+      else if (pm == 2) PD_LMF(PD_LAYOUT_PARTITIONABLE, 2);
       else if (pm == 1) PD_LMF(PD_LAYOUT_PARTITIONABLE, 1);
       else PD_LMF(PD_LAYOUT_PARTITIONABLE, 0);
     } else {
-      if (pm == 2) PD_LMF(PD_LAYOUT_ORIGINAL, 2);
+      if (pm == PM_SL0) PD_LMF(PD_LAYOUT_ORIGINAL, PM_SL0);
+      else if (pm == 2) PD_LMF(PD_LAYOUT_ORIGINAL, 2);
       else if (pm == 1) PD_LMF(PD_LAYOUT_ORIGINAL, 1);
       else PD_LMF(PD_LAYOUT_ORIGINAL, 0);
     }
 #undef PD_LMF
+    if (sl0)  // the site's frequencies, loss partials and backward slopes
+      hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(1, (int)C)), dim3(256), 0, s, S.sl0_col,
+                         (const int32_t*)nullptr, 1, N, (int)C, 1.f / (float)N, imp.coeff, imp.freq_coeff,
+                         imp.ref_count, S.sl0_slope, S.sl0_act, S.sl0_freq);
     rec.mark(LM_CAT_GEMM_FWD);
     return gemm_nt(N, dout, kc, S.acat, kc, P.BtF[k] + (size_t)l * dout * kc, kc, out, dout, PD_DTYPE_BF16, 0.f, s);
   };
@@ -956,8 +1021,13 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   if ((rc = pd_streamed_kl_fwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.pos_kl, P.stats,
                                P.kl_ws, P.kl_ws_bytes, s)))
     return rc;
-  hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.imp_part, (int64_t)P.imp_total,
-                     recon_coeff, imp_coeff, losses);
+  if (sl0)
+    hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.sl0_act, (int64_t)P.sl0_blocks_total,
+                       P.sl0_freq, imp.ref_count > 0.f ? (int64_t)P.sl0_blocks_total : (int64_t)0, 1.0, recon_coeff,
+                       imp.coeff, imp.freq_coeff, losses);
+  else
+    hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.imp_part, (int64_t)P.imp_total,
+                       (const float*)nullptr, (int64_t)0, 1.0 / (double)N, recon_coeff, imp.coeff, 0.f, losses);
   hipLaunchKernelGGL(k_lm_fill, dim3(ew_blocks(N)), dim3(256), 0, s, P.gpos, N, recon_coeff / (float)N);
   if ((rc = pd_streamed_kl_bwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.stats, P.gpos,
                                P.d_act, P.kl_ws, P.kl_ws_bytes, s)))
@@ -968,7 +1038,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   if ((rc = check_launch("pd_lm_stack_step loss"))) return rc;
 
   // ================= backward
-  const float imp_scale = imp_coeff / (float)N;
+  const float imp_scale = imp.coeff / (float)N;
   // site backward: g [N, d_out] (the output cotangent), the site input's transpose xT
   // [d_in, N] -> dU, dV, d_ci_pre, and d_input (+)= into din_out (fp32 accumulate when
   // din_f32, else bf16 written).
@@ -997,7 +1067,8 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 #define PD_LMB(PMV)                                                                                          \
   hipLaunchKernelGGL((k_lm_mask_bwd<PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
                      P.dcat, P.dxVT, dpre)
-    if (pm == 2) PD_LMB(2);
+    if (pm == PM_SL0) PD_LMB(PM_SL0);
+    else if (pm == 2) PD_LMB(2);
     else if (pm == 1) PD_LMB(1);
     else PD_LMB(0);
 #undef PD_LMB
@@ -1068,27 +1139,31 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
-                     int use_delta, int layout, float p, float imp_coeff, float recon_coeff, int n_kl_chunks,
+                     int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                     float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, int n_kl_chunks,
                      float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
                      size_t workspace_bytes, void* stream) {
   LMRecorder rec{nullptr, nullptr, 0, 0, nullptr};
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   return lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base, W,
-                      V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, n_kl_chunks,
-                      losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
+                      V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses, dV, dU,
+                      d_ci_pre, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
                            const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
                            const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
-                           uint32_t draw_k1, int use_delta, int layout, float p, float imp_coeff, float recon_coeff,
-                           int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                           uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
+                           int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                            void** events, int32_t* categories, int capacity, int* n_recorded) {
   LMRecorder rec{events, categories, capacity, 0, nullptr};
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   int rc = lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base,
-                        W, V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, p, imp_coeff, recon_coeff, n_kl_chunks,
-                        losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
+                        W, V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses,
+                        dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
   if (n_recorded) *n_recorded = rec.n;
   return rc;
 }

@@ -4,7 +4,8 @@ One call = one fwd+bwd of one decomposed linear whose input is the clean input:
 clean target `x@W^T` (detached), inner activations `h = x@V`, paper-form gate on h,
 lower/upper squashing, mask `m = lower + (1-lower)*u` with u drawn from the site's
 mask key (`pd/core/masking.py:148-167` key chain), optional weight-delta channel,
-`y = (h*(m-d))@U + d*(x@W^T)`, MSE recon, L_p imp-min, and the gradients w.r.t. V, U
+`y = (h*(m-d))@U + d*(x@W^T)`, MSE recon, the imp-min term (L_p, or the engine's
+smooth-L0 with its frequency penalty), and the gradients w.r.t. V, U
 and the gate parameters (the gate reads `h = x@V` with V live, so dV carries both
 pullbacks, as `pd/core/train.py:624-655` pulls the CI VJP back onto the components).
 
@@ -19,6 +20,7 @@ import torch
 
 from param_decomp_amd import _lib as L
 from param_decomp_amd import prng
+from param_decomp_amd.losses import ImpMin
 from param_decomp_amd.prng import Key
 
 
@@ -30,24 +32,27 @@ class DenseStepGrads:
     db_in: torch.Tensor
     dw_out: torch.Tensor
     db_out: torch.Tensor
-    losses: torch.Tensor  # [3] fp32: loss, recon, imp
+    losses: torch.Tensor  # [4] fp32: loss, recon, activity, frequency
 
 
 class DenseSiteStep:
     def __init__(self, T: int, d_in: int, d_out: int, C: int, *, dtype=torch.bfloat16, device="cuda", H: int = 16,
                  p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0, use_delta: bool = False,
-                 draw_dtype: torch.dtype | None = None, layout: int = L.LAYOUT_PARTITIONABLE):
+                 draw_dtype: torch.dtype | None = None, layout: int = L.LAYOUT_PARTITIONABLE,
+                 imp_min: ImpMin | None = None):
         self.T, self.d_in, self.d_out, self.C, self.H = T, d_in, d_out, C, H
         self.dtype = dtype
         self.dt = L.dtype_code(dtype)
         self.draw = L.dtype_code(draw_dtype or dtype)
         self.layout = layout
-        self.p, self.imp_coeff, self.recon_coeff, self.use_delta = p, imp_coeff, recon_coeff, use_delta
+        self.recon_coeff, self.use_delta = recon_coeff, use_delta
+        # the imp-min term: L_p (p, imp_coeff) unless a smooth-L0 ImpMin is given
+        self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
         self.grads = DenseStepGrads(torch.empty(d_in, C, **f32), torch.empty(C, d_out, **f32), torch.empty(C, H, **f32),
                                     torch.empty(C, H, **f32), torch.empty(C, H, **f32), torch.empty(C, **f32),
-                                    torch.empty(3, **f32))
+                                    torch.empty(4, **f32))
         nbytes = L.load().pd_dense_step_workspace_size(self.dt, T, d_in, d_out, C, H)
         self.workspace = L.workspace(nbytes, dev)
 
@@ -61,7 +66,7 @@ class DenseSiteStep:
         g = self.grads
         args = [self.dt, self.T, self.d_in, self.d_out, self.C, self.H, L.ptr(x), L.ptr(W), L.ptr(V), L.ptr(U),
                 L.ptr(w_in), L.ptr(b_in), L.ptr(w_out), L.ptr(b_out), mask_key[0], mask_key[1], delta_key[0],
-                delta_key[1], int(self.use_delta), self.draw, self.layout, self.p, self.imp_coeff, self.recon_coeff,
+                delta_key[1], int(self.use_delta), self.draw, self.layout, *self.imp_min.c_args(), self.recon_coeff,
                 L.ptr(g.losses), L.ptr(g.dV), L.ptr(g.dU), L.ptr(g.dw_in), L.ptr(g.db_in), L.ptr(g.dw_out),
                 L.ptr(g.db_out), L.ptr(self.workspace), self.workspace.numel(), L.stream()]
         if events is None:

@@ -18,6 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from param_decomp_amd import _lib as L
+from param_decomp_amd.losses import ImpMin
 from param_decomp_amd.prng import Key
 
 KINDS = ("q_proj", "k_proj", "v_proj", "o_proj", "c_fc", "down_proj")  # KIND_ORDER (pd/targets/llama_simple_mlp.py)
@@ -49,17 +50,19 @@ class LMStackStep:
     def __init__(self, B: int, T: int, d: int, n_head: int, n_kv_head: int, d_mlp: int, vocab: int, n_layers: int,
                  C: dict, *, device="cuda", p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
                  layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, n_kl_chunks: int = 1,
-                 eps: float = 1e-6, rope_base: float = 10000.0):
+                 eps: float = 1e-6, rope_base: float = 10000.0, imp_min: ImpMin | None = None):
         if d != n_head * HEAD_DIM:
             raise L.PDError(f"LMStackStep: head_dim must be {HEAD_DIM} (d = {HEAD_DIM} * n_head)")
         self.dims = (B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers)
         self.C = {k: int(C[k]) for k in KINDS}
-        self.p, self.imp_coeff, self.recon_coeff, self.layout = p, imp_coeff, recon_coeff, layout
+        # the imp-min term: L_p (p, imp_coeff) unless a smooth-L0 ImpMin is given
+        self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
+        self.recon_coeff, self.layout = recon_coeff, layout
         self.use_delta, self.n_kl_chunks, self.eps, self.rope_base = bool(use_delta), n_kl_chunks, eps, rope_base
         dev = torch.device(device)
         N = B * T
         f32 = dict(dtype=torch.float32, device=dev)
-        self.losses = torch.empty(3, **f32)
+        self.losses = torch.empty(4, **f32)  # total, kl, activity, frequency
         self.dV, self.dU, self.d_ci_pre = {}, {}, {}
         for k in KINDS:
             din, dout = site_dims(k, d, n_head, n_kv_head, d_mlp)
@@ -89,7 +92,7 @@ class LMStackStep:
         Wa, Va, Ua, Ca = self._keep
         return [B, T, d, H, KV, f, V, Ln, self._cs, L.ptr(tokens), L.ptr(w.wte), L.ptr(w.ln1), L.ptr(w.ln2),
                 L.ptr(w.norm), self.eps, self.rope_base, Wa, Va, Ua, Ca, draw_key[0], draw_key[1], int(self.use_delta),
-                self.layout, self.p, self.imp_coeff, self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
+                self.layout, *self.imp_min.c_args(), self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
                 self._dU, self._dci, L.ptr(self.workspace), self.workspace.numel(), L.stream()]
 
     def step(self, tokens: torch.Tensor, w: LMWeights, ci_pre: dict, draw_key: Key):

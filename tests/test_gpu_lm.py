@@ -60,12 +60,18 @@ def _setup(cfg, B, T, seed, device):
     return params, tokens, ci, w, ci_t, tok_t
 
 
-@pytest.mark.parametrize("n_kv,use_delta,partitionable,T", [(2, True, True, 64), (1, True, False, 64),
-                                                           (2, False, True, 64), (2, True, True, 512)])
-def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T):
+# the engine's smooth-L0 imp-min with its frequency penalty
+SL0 = dict(kind="smooth_l0", coeff=0.05, gamma=0.4, normalize_at_one=False, freq_coeff=0.02, ref_count=2048.0)
+
+
+@pytest.mark.parametrize("n_kv,use_delta,partitionable,T,sl0", [(2, True, True, 64, None), (1, True, False, 64, None),
+                                                               (2, False, True, 64, None), (2, True, True, 512, None),
+                                                               (2, True, True, 128, SL0)])
+def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T, sl0):
     """T = 512 (1024 tokens) puts the weight-gradient products on the split-contraction
-    path (slices of the token axis added in order)."""
+    path (slices of the token axis added in order); sl0 runs the smooth-L0 term."""
     from param_decomp_amd import _lib as L
+    from param_decomp_amd.losses import ImpMin
     from param_decomp_amd.lm_step import LMStackStep
 
     B = 2
@@ -73,15 +79,17 @@ def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T)
                       C={"q_proj": 64, "k_proj": 48, "v_proj": 64, "o_proj": 32, "c_fc": 128, "down_proj": 96})
     params, tokens, ci, w, ci_t, tok_t = _setup(cfg, B, T, 4 + n_kv, device)
     key = (5, 23)
-    kw = dict(p=2.0, imp_coeff=0.05, recon_coeff=3.0)
+    spec = po.ImpMin(**sl0) if sl0 else po.ImpMin("pnorm", p=2.0, coeff=0.05)
+    imp = ImpMin(spec.kind, spec.p, spec.coeff, spec.gamma, spec.normalize_at_one, spec.freq_coeff, spec.ref_count)
     step = LMStackStep(B, T, cfg.d, cfg.n_head, cfg.n_kv_head, cfg.d_mlp, cfg.vocab, cfg.n_layers, cfg.C,
                        device=device, layout=L.LAYOUT_PARTITIONABLE if partitionable else L.LAYOUT_ORIGINAL,
-                       use_delta=use_delta, n_kl_chunks=3, **kw)
+                       use_delta=use_delta, n_kl_chunks=3, recon_coeff=3.0, imp_min=imp)
     step.step(tok_t, w, ci_t, key)
     torch.cuda.synchronize()
     ref = lo.lm_stack_step(cfg, params, tokens, ci, key, bf16_storage=True, partitionable=partitionable,
-                           use_delta=use_delta, **kw)
-    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"]], rtol=2e-2)
+                           use_delta=use_delta, recon_coeff=3.0, imp_min=spec)
+    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"], ref["freq"]],
+                               rtol=2e-2, atol=1e-7)
     stats = []
     for l in range(cfg.n_layers):
         for k in KINDS:

@@ -367,10 +367,14 @@ def _dense_inputs(rng, T, d_in, d_out, C):
     return x, W, V, U, gp
 
 
-@pytest.mark.parametrize("use_delta", [False, True])
+@pytest.mark.parametrize("use_delta,sl0", [(False, False), (True, False), (True, True)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_dense_step_matches_oracle(device, dtype, use_delta):
+def test_dense_step_matches_oracle(device, dtype, use_delta, sl0):
+    """sl0: the engine's smooth-L0 term with its frequency penalty (each 64-token chunk's
+    column sums of psi in the gate pass, frequencies and slopes in between, the slope in
+    the gate backward)."""
     from param_decomp_amd.dense_step import DenseSiteStep
+    from param_decomp_amd.losses import ImpMin
 
     rng = np.random.default_rng(13)
     T, d_in, d_out, C = 256, 64, 96, 192
@@ -379,18 +383,21 @@ def test_dense_step_matches_oracle(device, dtype, use_delta):
     tx, tW, tV, tU = (cv(a) for a in (x, W, V, U))
     gate = tuple(f32(a, device) for a in (gp.w_in, gp.b_in, gp.w_out, gp.b_out))
     draw_key = tf.fold_in(tf.prng_key(5), 1)
-    step = DenseSiteStep(T, d_in, d_out, C, dtype=dtype, device=device, p=2.0, imp_coeff=0.7, recon_coeff=1.3,
-                         use_delta=use_delta)
+    spec = (po.ImpMin("smooth_l0", coeff=0.7, gamma=0.2, normalize_at_one=True, freq_coeff=0.4, ref_count=300.0)
+            if sl0 else po.ImpMin("pnorm", p=2.0, coeff=0.7))
+    imp = ImpMin(spec.kind, spec.p, spec.coeff, spec.gamma, spec.normalize_at_one, spec.freq_coeff, spec.ref_count)
+    step = DenseSiteStep(T, d_in, d_out, C, dtype=dtype, device=device, recon_coeff=1.3, use_delta=use_delta,
+                         imp_min=imp)
     mk, dk = step.site_keys(draw_key, 0)
     g = step.step(tx, tW, tV, tU, gate, mk, dk)
     torch.cuda.synchronize()
     gp64 = po.GateParams(*(np64(t) for t in gate))
-    r = po.dense_site_step(np64(tx), np64(tW), np64(tV), np64(tU), gp64, draw_key, p=2.0, imp_coeff=0.7,
-                           recon_coeff=1.3, mask_dtype="bfloat16" if dtype == torch.bfloat16 else "float32",
-                           use_delta=use_delta, bf16_storage=dtype == torch.bfloat16)
+    r = po.dense_site_step(np64(tx), np64(tW), np64(tV), np64(tU), gp64, draw_key, recon_coeff=1.3,
+                           mask_dtype="bfloat16" if dtype == torch.bfloat16 else "float32",
+                           use_delta=use_delta, bf16_storage=dtype == torch.bfloat16, imp_min=spec)
     rtol = 1e-4 if dtype == torch.float32 else BF16_RTOL
     losses = g.losses.cpu().numpy()
-    np.testing.assert_allclose(losses, [r.loss, r.recon, r.imp], rtol=rtol)
+    np.testing.assert_allclose(losses, [r.loss, r.recon, r.imp, r.freq], rtol=rtol, atol=1e-7)
     floor = 1e-4 if dtype == torch.float32 else 1e-2
     assert_close(np64(g.dU), r.dU, rtol, floor, "dU")
     assert_close(np64(g.dV), r.dV, rtol, floor, "dV")

@@ -197,3 +197,24 @@ def test_full_masks_reproduce_the_clean_forward():
     ci = [{k: np.full((6, cfg.C[k]), 1.0) for k in cfg.C}]
     out = lo.lm_stack_step(cfg, params, tokens, ci, (1, 2), use_delta=False, imp_coeff=0.0)
     assert abs(out["recon"]) < 1e-12
+
+
+def test_smooth_l0_terms_and_gradient_match_the_reference_formula():
+    """The step's smooth-L0 activity and frequency equal the reference formula
+    (pd_oracle.importance_minimality_terms, pinned by the reference's closed forms) on
+    every site's upper CI, and with recon_coeff = 0 the CI gradient is exactly the
+    imp-min pullback (the per-component slope times psi', through the upper VJP)."""
+    from oracle import pd_oracle as po
+
+    cfg, params, tokens, ci = _small()
+    spec = po.ImpMin("smooth_l0", coeff=0.7, gamma=0.25, normalize_at_one=True, freq_coeff=0.3, ref_count=50.0)
+    out = lo.lm_stack_step(cfg, params, tokens, ci, (7, 11), recon_coeff=0.0, imp_min=spec)
+    ups = [po.upper_leaky(ci[l][k]) for l in range(cfg.n_layers) for k in cfg.kinds if k in cfg.C]
+    act, freq = po.importance_minimality_terms(ups, 0.25, 50.0, True)
+    assert out["imp"] == pytest.approx(act, rel=1e-12) and out["freq"] == pytest.approx(freq, rel=1e-12)
+    assert out["loss"] == pytest.approx(0.7 * act + 0.3 * freq, rel=1e-12)
+    for l in range(cfg.n_layers):
+        for k in cfg.C:
+            _, _, dup = po.impmin_site_terms(po.upper_leaky(ci[l][k]), spec, 10)
+            want = po.upper_leaky_vjp(ci[l][k], dup)
+            np.testing.assert_allclose(out["d_ci_pre"][l][k], want, rtol=1e-10, atol=1e-14)
