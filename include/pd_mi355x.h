@@ -254,7 +254,7 @@ int pd_route_static_p(uint32_t key0, uint32_t key1, int64_t n_positions, int n_s
 /* ---- MoE routing: pd/targets/qwen36_moe.py:473-514 (router softmax, select_experts
  *      stable-descending lowest-index ties, expert_mixing_weights renormalized). ----
  * logits [T,E] fp32 -> probs [T,E] fp32 (nullable), top_idx [T,k] int32,
- * weights [T,k] fp32. E <= 64, k <= E. */
+ * weights [T,k] fp32. E <= 512, k <= min(E, 64). */
 int pd_router_topk(const float* logits, int64_t T, int E, int k, float* probs, int32_t* top_idx, float* weights,
                    void* stream);
 
@@ -331,7 +331,7 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
  * gradients fp32 in the V/U shapes; d_ci_pre bf16 [L,3,T,k,c]; top_idx_out int32
  * [L,T,k] (nullable). The stack input's gradient is not formed (layer 0 stops at its
  * weight and CI gradients).
- * E <= 64; d, f, c multiples of 8. */
+ * E <= 512, k <= 64; d, f, c multiples of 8. */
 size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L);
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,

@@ -110,27 +110,67 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(const bf16_t* __restrict__ 
   }
 }
 
+// The value v[e >> 6] of lane e & 63 (an expert-e quantity of the lane-strided layout
+// lane l <-> experts l + 64 i) for every lane; every lane takes part in the shuffles.
+template <int EPL>
+__device__ inline float expert_value(const float (&v)[EPL], int e) {
+  float out = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const float x = __shfl(v[i], e & 63, 64);
+    if ((e >> 6) == i) out = x;
+  }
+  return out;
+}
+
 // Masked-layer routing weights at pinned indices: probs = softmax(bf16(logits))
 // (saved), w[t,s] = probs[idx[t,s]] / sum_s probs[idx[t,s]]. The fp32 product is
 // rounded to bf16 first: the reference's router product runs in the bf16 matmul dtype
-// (pd/targets/qwen36_moe.py:473-475). One wave per token, E <= 64.
+// (pd/targets/qwen36_moe.py:473-475). One wave per token; lane l holds experts
+// l + 64 i (E <= 64 EPL).
+template <int EPL>
 __global__ __launch_bounds__(256) void k_router_pinned(const float* __restrict__ logits, int64_t T, int E, int k,
                                                        const int32_t* __restrict__ idx, float* __restrict__ probs,
                                                        float* __restrict__ w) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float x = lane < E ? bf16_to_f32(f32_to_bf16(logits[t * E + lane])) : -INFINITY;
-  float mx = wave_max(x);
-  float ex = lane < E ? expf(x - mx) : 0.f;
-  float p = ex / wave_sum(ex);
-  if (lane < E) probs[t * E + lane] = p;
-  // every lane takes part in the shuffle (a source lane must be active)
+  float x[EPL];
+  float mxl = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    x[i] = e < E ? bf16_to_f32(f32_to_bf16(logits[t * E + e])) : -INFINITY;
+    mxl = fmaxf(mxl, x[i]);
+  }
+  const float mx = wave_max(mxl);
+  float zl = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    x[i] = lane + 64 * i < E ? expf(x[i] - mx) : 0.f;
+    zl += x[i];
+  }
+  const float z = wave_sum(zl);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    x[i] = x[i] / z;
+    if (e < E) probs[t * E + e] = x[i];
+  }
   int e = lane < k ? idx[t * k + lane] : 0;
   e = e < 0 ? 0 : (e >= E ? E - 1 : e);
-  const float sel = __shfl(p, e, 64);
+  const float sel = expert_value<EPL>(x, e);
   float s = wave_sum(lane < k ? sel : 0.f);
   if (lane < k) w[t * k + lane] = sel / s;
+}
+
+static void launch_router_pinned(const float* logits, int64_t T, int E, int k, const int32_t* idx, float* probs,
+                                 float* w, hipStream_t s) {
+  const dim3 grid((unsigned)cdiv(T, 4));
+  if (E <= 64) hipLaunchKernelGGL(k_router_pinned<1>, grid, dim3(256), 0, s, logits, T, E, k, idx, probs, w);
+  else if (E <= 128) hipLaunchKernelGGL(k_router_pinned<2>, grid, dim3(256), 0, s, logits, T, E, k, idx, probs, w);
+  else if (E <= 256) hipLaunchKernelGGL(k_router_pinned<4>, grid, dim3(256), 0, s, logits, T, E, k, idx, probs, w);
+  else hipLaunchKernelGGL(k_router_pinned<8>, grid, dim3(256), 0, s, logits, T, E, k, idx, probs, w);
 }
 
 // r_out[t,:] = bf16(r[t,:] + bf16(sum_s wt[t,s] * y[inv[t*k+s],:])) with fp32
@@ -489,13 +529,14 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
   ttile_store(Tu, d_uT, J, j0, J, q0, f, tid);
 }
 
-// d_logits[t, lane] of one token (lanes = experts, 0 past E), all 64 lanes active:
-// d_w[s] = sum of the d_w_part tiles of job inv[t*k+s], through w = p_sel / sum p_sel
-// and the router softmax, rounded to bf16.
-__device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int n_part,
-                                         const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
-                                         const float* __restrict__ probs, const float* __restrict__ w, int64_t t,
-                                         int E, int k, int lane) {
+// d_logits of one token in the lane-strided layout (dl[i] = expert lane + 64 i, 0 past
+// E), all 64 lanes active: d_w[s] = sum of the d_w_part tiles of job inv[t*k+s], through
+// w = p_sel / sum p_sel and the router softmax, rounded to bf16.
+template <int EPL>
+__device__ inline void router_logit_vjp(const float* __restrict__ d_w_part, int n_part,
+                                        const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
+                                        const float* __restrict__ probs, const float* __restrict__ w, int64_t t,
+                                        int E, int k, int lane, float (&dl)[EPL]) {
   float dw = 0.f;
   if (lane < k) {
     const int64_t jj = inv[t * k + lane];
@@ -503,22 +544,33 @@ __device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int
   }
   const float wv = lane < k ? w[t * k + lane] : 0.f;
   const float dot = wave_sum(dw * wv);
-  int e_of_slot = lane < k ? idx[t * k + lane] : -1;
-  if (lane < k) e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
-  const float pe = lane < E ? probs[t * E + lane] : 0.f;
-  const float psel = __shfl(pe, lane < k ? e_of_slot : 0, 64);  // all lanes shuffle
+  int e_of_slot = lane < k ? idx[t * k + lane] : 0;
+  e_of_slot = e_of_slot < 0 ? 0 : (e_of_slot >= E ? E - 1 : e_of_slot);
+  float pe[EPL], dpe[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    pe[i] = lane + 64 * i < E ? probs[t * E + lane + 64 * i] : 0.f;
+    dpe[i] = 0.f;
+  }
+  const float psel = expert_value<EPL>(pe, e_of_slot);
   const float S = wave_sum(lane < k ? psel : 0.f);
   const float dps = lane < k ? (dw - dot) / S : 0.f;
-  float dpe = 0.f;
   for (int s = 0; s < k; ++s) {
     const int es = __shfl(e_of_slot, s, 64);
     const float v = __shfl(dps, s, 64);
-    if (lane == es) dpe += v;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i == es) dpe[i] += v;
   }
-  const float sdot = wave_sum(lane < E ? pe * dpe : 0.f);
+  float sl = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) sl += lane + 64 * i < E ? pe[i] * dpe[i] : 0.f;
+  const float sdot = wave_sum(sl);
   // the logits were widened from the bf16 router product: their cotangent narrows to
   // bf16 on its way back into that product
-  return lane < E ? bf16_to_f32(f32_to_bf16(pe * (dpe - sdot))) : 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    dl[i] = lane + 64 * i < E ? bf16_to_f32(f32_to_bf16(pe[i] * (dpe[i] - sdot))) : 0.f;
 }
 
 // Token backward, one wave per TPW consecutive tokens, lane l owning columns 8l..8l+7 of
@@ -528,7 +580,7 @@ __device__ inline float router_logit_vjp(const float* __restrict__ d_w_part, int
 //   a wave share each 16-byte router load. With the frozen channel (fxa non-NULL) each
 //   slot also adds da[t] * fxa + db[t] * fxb, the gate and up frozen products' input
 //   cotangents scaled by the token's delta draws.
-template <int TPW, int NCH>
+template <int TPW, int NCH, int EPL>
 __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w_part, int n_part,
                                                    const int32_t* __restrict__ inv, const int32_t* __restrict__ idx,
                                                    const float* __restrict__ probs, const float* __restrict__ w,
@@ -542,11 +594,16 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
   const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave_id()) * TPW;
   if (t0 >= T) return;
   const int lane = threadIdx.x & 63;
-  float dl[TPW], a[TPW][NCH][8];
+  float dl[TPW][EPL], a[TPW][NCH][8];
 #pragma unroll
   for (int u = 0; u < TPW; ++u) {
     const int64_t t = t0 + u;
-    dl[u] = t < T ? router_logit_vjp(d_w_part, n_part, inv, idx, probs, w, t, E, k, lane) : 0.f;
+    if (t < T) {
+      router_logit_vjp<EPL>(d_w_part, n_part, inv, idx, probs, w, t, E, k, lane, dl[u]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) dl[u][i] = 0.f;
+    }
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
@@ -574,20 +631,25 @@ __global__ __launch_bounds__(256) void k_token_bwd(const float* __restrict__ d_w
       }
     }
   }
-  for (int e = 0; e < E; ++e) {
-    float de[TPW];
 #pragma unroll
-    for (int u = 0; u < TPW; ++u) de[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl[u]), e));
+  for (int blk = 0; blk < EPL; ++blk) {
+    for (int el = 0; el < 64 && blk * 64 + el < E; ++el) {
+      const int e = blk * 64 + el;
+      float de[TPW];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int i = c * 512 + lane * 8;
-      if (i < d) {
-        float rv[8];
-        load8(router + (int64_t)e * d + i, rv);
+      for (int u = 0; u < TPW; ++u)
+        de[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl[u][blk]), el));
 #pragma unroll
-        for (int u = 0; u < TPW; ++u)
+      for (int c = 0; c < NCH; ++c) {
+        const int i = c * 512 + lane * 8;
+        if (i < d) {
+          float rv[8];
+          load8(router + (int64_t)e * d + i, rv);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) a[u][c][j] = fmaf(de[u], rv[j], a[u][c][j]);
+          for (int u = 0; u < TPW; ++u)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[u][c][j] = fmaf(de[u], rv[j], a[u][c][j]);
+        }
       }
     }
   }
@@ -635,8 +697,15 @@ static void launch_token_bwd_t(const float* d_w_part, int n_part, const int32_t*
                                const bf16_t* dxb, const bf16_t* r, const float* rinv, const float* ln,
                                const bf16_t* d_r, int64_t T, int E, int k, int d, const bf16_t* fxa,
                                const bf16_t* fxb, const float* da, const float* db, bf16_t* d_r_out, hipStream_t s) {
-  hipLaunchKernelGGL((k_token_bwd<TPW, NCH>), dim3((unsigned)cdiv(T, 4 * TPW)), dim3(256), 0, s, d_w_part, n_part,
-                     inv, idx, probs, w, router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d, fxa, fxb, da, db, d_r_out);
+  const dim3 grid((unsigned)cdiv(T, 4 * TPW));
+#define PD_TB(EPL)                                                                                                \
+  hipLaunchKernelGGL((k_token_bwd<TPW, NCH, EPL>), grid, dim3(256), 0, s, d_w_part, n_part, inv, idx, probs, w, \
+                     router, dxa, dxb, r, rinv, ln, d_r, T, E, k, d, fxa, fxb, da, db, d_r_out)
+  if (E <= 64) PD_TB(1);
+  else if (E <= 128) PD_TB(2);
+  else if (E <= 256) PD_TB(4);
+  else PD_TB(8);
+#undef PD_TB
 }
 
 // d <= 4096 (checked by the step): the column chunks per lane set the register tile.
@@ -945,8 +1014,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                          float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                          void* workspace, size_t workspace_bytes, void* stream, Recorder& rec) {
   int rc0;
-  if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 64 || k <= 0 || k > E || c <= 0 || L <= 0)
-    return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 64)");
+  if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 512 || k <= 0 || k > E || k > 64 || c <= 0 || L <= 0)
+    return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 512, k <= 64)");
   if (d % 8 || f % 8 || c % 8 || (T * k) % 8)
     return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d, f, c and T*k must be multiples of 8");
   if (d > 4096 || T * k > 0x7FFFFFFF || cdiv(T * k, TILE) > 65535)
@@ -1043,8 +1112,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     if ((rc = router_topk(P.logits, T, E, k, true, P.probsc, S.idx, P.wc, stream))) return rc;
     if (l == 0)
-      hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
-                         S.probs, S.w);
+      launch_router_pinned(P.logits, T, E, k, S.idx, S.probs, S.w, s);
     if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
                              pd_routed_jobs_workspace_size(J, E), stream)))
       return rc;
@@ -1082,8 +1150,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, S.h2, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
                         PD_DTYPE_F32, 1.f, 0.f, stream)))
         return rc;
-      hipLaunchKernelGGL(k_router_pinned, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, P.logits, T, E, k, S.idx,
-                         S.probs, S.w);
+      launch_router_pinned(P.logits, T, E, k, S.idx, S.probs, S.w, s);
       hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
     }
     set_delta(l);

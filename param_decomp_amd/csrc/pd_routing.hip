@@ -11,28 +11,51 @@
 
 namespace pd {
 
-// One wave per token, lane e holds expert e. Top-k by k rounds of a wave argmax that
-// prefers the larger probability and, on equal probabilities, the lower index — the
-// order of a stable descending sort. ROUND: the logits are rounded to bf16 first.
-template <bool ROUND>
+// One wave per token; lane l holds experts l + 64 i (i < EPL, E <= 64 EPL). Top-k by k
+// rounds of a wave argmax that prefers the larger probability and, on equal
+// probabilities, the lower index: the order of a stable descending sort. ROUND: the
+// logits are rounded to bf16 first. k <= 64.
+template <bool ROUND, int EPL>
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int64_t T, int E, int k,
                                                      float* __restrict__ probs, int32_t* __restrict__ top_idx,
                                                      float* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (t >= T) return;
-  float x = lane < E ? logits[t * E + lane] : -INFINITY;
-  if (ROUND && lane < E) x = bf16_to_f32(f32_to_bf16(x));
-  float mx = wave_max(x);
-  float ex = lane < E ? expf(x - mx) : 0.f;
-  float z = wave_sum(ex);
-  float p = ex / z;
-  if (probs && lane < E) probs[t * E + lane] = p;
-  float cand = lane < E ? p : -INFINITY;
+  float x[EPL], cand[EPL];
+  float mxl = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    x[i] = e < E ? logits[t * E + e] : -INFINITY;
+    if (ROUND && e < E) x[i] = bf16_to_f32(f32_to_bf16(x[i]));
+    mxl = fmaxf(mxl, x[i]);
+  }
+  const float mx = wave_max(mxl);
+  float zl = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    x[i] = lane + 64 * i < E ? expf(x[i] - mx) : 0.f;
+    zl += x[i];
+  }
+  const float z = wave_sum(zl);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    const float p = x[i] / z;
+    if (probs && e < E) probs[t * E + e] = p;
+    cand[i] = e < E ? p : -INFINITY;
+  }
   float sel_sum = 0.f, my_w = 0.f;
   for (int s = 0; s < k; ++s) {
-    float bv = cand;
+    float bv = cand[0];
     int bi = lane;
+#pragma unroll
+    for (int i = 1; i < EPL; ++i)
+      if (cand[i] > bv) {  // strict: the lower index keeps a tie
+        bv = cand[i];
+        bi = lane + 64 * i;
+      }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       float ov = __shfl_xor(bv, off, 64);
@@ -43,7 +66,9 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
       }
     }
     if (bi >= E) bi = E - 1;  // only reachable with NaN probabilities
-    if (lane == bi) cand = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i == bi) cand[i] = -INFINITY;
     if (lane == s) my_w = bv;
     sel_sum += bv;
     if (lane == 0) top_idx[t * k + s] = bi;
@@ -230,15 +255,25 @@ __global__ __launch_bounds__(256) void k_route_static_p(uint32_t k0, uint32_t k1
 
 int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, float* probs, int32_t* top_idx,
                 float* weights, void* stream) {
-  if (T < 0 || E <= 0 || E > 64 || k <= 0 || k > E || !logits || !top_idx || !weights)
-    return fail(PD_EINVAL, "pd_router_topk: need 0 < k <= E <= 64");
+  if (T < 0 || E <= 0 || E > 512 || k <= 0 || k > E || k > 64 || !logits || !top_idx || !weights)
+    return fail(PD_EINVAL, "pd_router_topk: need 0 < k <= min(E, 64), E <= 512");
   if (T == 0) return PD_OK;
-  if (round_bf16)
-    hipLaunchKernelGGL(k_router_topk<true>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T,
-                       E, k, probs, top_idx, weights);
-  else
-    hipLaunchKernelGGL(k_router_topk<false>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, (hipStream_t)stream, logits, T,
-                       E, k, probs, top_idx, weights);
+  const dim3 grid((unsigned)cdiv(T, 4));
+  hipStream_t s = (hipStream_t)stream;
+#define PD_RT(EPL)                                                                                           \
+  do {                                                                                                       \
+    if (round_bf16)                                                                                          \
+      hipLaunchKernelGGL((k_router_topk<true, EPL>), grid, dim3(256), 0, s, logits, T, E, k, probs, top_idx, \
+                         weights);                                                                           \
+    else                                                                                                     \
+      hipLaunchKernelGGL((k_router_topk<false, EPL>), grid, dim3(256), 0, s, logits, T, E, k, probs,        \
+                         top_idx, weights);                                                                  \
+  } while (0)
+  if (E <= 64) PD_RT(1);
+  else if (E <= 128) PD_RT(2);
+  else if (E <= 256) PD_RT(4);
+  else PD_RT(8);
+#undef PD_RT
   return check_launch("pd_router_topk");
 }
 

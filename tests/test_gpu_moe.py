@@ -57,7 +57,11 @@ SL0 = dict(kind="smooth_l0", coeff=0.5, gamma=0.3, normalize_at_one=True, freq_c
     (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, 0.375, None),
     (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None, SL0),
     (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=72, L=2), False, True, None, dict(SL0, ref_count=0.0,
-                                                                                 normalize_at_one=False))])
+                                                                                 normalize_at_one=False)),
+    # more than 64 experts: several experts per lane in the router, pinned-weight and
+    # token-backward kernels; the grouped products' group scan in 64-expert steps
+    (mo.MoEConfig(T=256, d=64, f=32, E=100, k=6, c=16, L=2), True, True, None, None),
+    (mo.MoEConfig(T=192, d=32, f=16, E=300, k=8, c=8, L=2), True, True, None, SL0)])
 def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, source_value, sl0):
     """sl0: the smooth-L0 term (per (tile, expert) column sums of psi in the mask pass,
     per-expert frequencies and slopes in between, the slope in the mask backward)."""

@@ -435,11 +435,13 @@ def test_dense_step_full_size_properties(device):
 # ------------------------------------------------------------------ routing
 
 
-def test_router_topk_bit_exact_indices(device):
+@pytest.mark.parametrize("E,k", [(42, 8), (100, 6), (256, 8), (500, 16)])
+def test_router_topk_bit_exact_indices(device, E, k):
+    """E > 64 puts several experts on each lane (lane l holds experts l + 64 i)."""
     from param_decomp_amd.routed.experts import route_tokens
 
-    rng = np.random.default_rng(14)
-    T, E, k = 1000, 42, 8
+    rng = np.random.default_rng(14 + E)
+    T = 1000
     logits = rng.normal(size=(T, E)).astype(np.float32)
     logits[3, [5, 9, 11]] = 2.5  # exact ties: lowest index first
     logits[4, :] = 0.0
