@@ -48,6 +48,7 @@ MOE = "qwen35moe4L"
 CI_MLP = "ci_mlp768_h1024_C4096"
 CI_READOUT = "ci_readout_llama4L"
 PPGD_DENSE = "ppgd_dense768x3072_C4096"
+PPGD_MOE = "ppgd_qwen35moe4L"
 KL_STREAM = "kl_stream_llama4L"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
@@ -82,6 +83,10 @@ WORKLOADS = {
     # ascents (the reference's LM PPGD setting)
     PPGD_DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096, n_warmup=2, source_shape="bsc", source_dtype="uint16",
                      optimizer="momentum_sgd", momentum=0.9, lr=0.01),
+    # persistent PGD over every expert site of the MoE stack: per-sample (bc) uint16 source
+    # tables of 16 samples x 512 positions, momentum SGD, 2 warmup ascents
+    PPGD_MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4, rows_per_source=512, n_warmup=2,
+                   source_dtype="uint16", optimizer="momentum_sgd", momentum=0.9, lr=0.01),
     # faithfulness of the dense site, and of every expert matrix of the MoE stack (per kind:
     # 4 layers x 42 experts, each layer's experts one block-factored site)
     FAITH_DENSE: dict(groups=[dict(n=1, per=1, d_in=768, d_out=3072, C=4096)]),
@@ -602,6 +607,69 @@ def run_ppgd(args):
     return res_d
 
 
+def run_ppgd_moe(args):
+    """One persistent-PGD step over every expert site of the MoE stack: n_warmup
+    source-only steps (masked forward, recon, backward to the sources, no weight
+    gradients) each followed by a projected ascent of both source leaves, then the final
+    step with every gradient and the final ascent."""
+    import torch
+
+    from param_decomp_amd import adversary as A
+    from param_decomp_amd import hip_events, prng
+    from param_decomp_amd.moe_step import MoEStackStep, MoEWeights
+
+    cfg = WORKLOADS[PPGD_MOE]
+    T, d, f, E, k, c, Ln = (cfg[x] for x in ("T", "d", "f", "E", "k", "c", "L"))
+    rps = cfg["rows_per_source"]
+    S = T // rps
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, scale):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(torch.bfloat16)
+
+    w = MoEWeights(ln=torch.zeros(Ln, d, device=dev), router=rn(Ln, E, d, scale=d**-0.5),
+                   Wg=rn(Ln, E, d, f, scale=d**-0.5), Wu=rn(Ln, E, d, f, scale=d**-0.5),
+                   Wd=rn(Ln, E, f, d, scale=f**-0.5), Vg=rn(Ln, E, d, c, scale=d**-0.5),
+                   Ug=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vu=rn(Ln, E, d, c, scale=d**-0.5),
+                   Uu=rn(Ln, E, c, f, scale=(E * c)**-0.5), Vd=rn(Ln, E, f, c, scale=f**-0.5),
+                   Ud=rn(Ln, E, c, d, scale=(E * c)**-0.5))
+    x0 = rn(T, d, scale=1.0)
+    ci = (torch.rand(Ln, 3, T, k, c, device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16)
+    step = MoEStackStep(T, d, f, E, k, c, Ln, device=dev, p=2.0, imp_coeff=0.0, recon_coeff=1.0, rows_per_source=rps)
+    opt = A.MomentumSgdPGDConfig(cfg["momentum"])
+    src = A.store_unit_float(torch.rand(Ln, 3, S, E, c, device=dev, generator=g), torch.uint16)
+    srcd = A.store_unit_float(torch.rand(Ln, 3, S, device=dev, generator=g), torch.uint16)
+    adv = A.PersistentAdversary(src, opt, cfg["n_warmup"], rows_per_source=rps)
+    dadv = A.PersistentAdversary(srcd, opt, cfg["n_warmup"], rows_per_source=rps, leaf_index=1)
+    ppgd = A.MoEPPGDStep(step, adv, dadv)
+    for i in range(args.warmup):
+        ppgd.step(x0, w, ci, cfg["lr"], prng.fold_in((0, 0), i))
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        res = ppgd.step(x0, w, ci, cfg["lr"], prng.fold_in((0, 0), args.warmup + i))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms = hip_events.elapsed_ms(start, stop) / args.steps
+    hip_events.destroy([start, stop])
+    assert torch.isfinite(res.loss).all()
+    gf = moe_gemm_flops(dict(cfg, use_delta=True))
+    # a warmup step runs everything but the weight-gradient products
+    step_flops = cfg["n_warmup"] * (sum(gf.values()) - gf["gemm_dw"]) + sum(gf.values())
+    return {"tokens": T, "ms_per_step": ms,
+            "config": {"workload": PPGD_MOE, "tokens": T, "width": d, "experts": E, "top_k": k, "expert_ffn": f,
+                       "c_per_expert": c, "layers": Ln, "source_shape": "bc", "rows_per_source": rps,
+                       "source_dtype": cfg["source_dtype"], "optimizer": cfg["optimizer"],
+                       "n_warmup": cfg["n_warmup"], "recon": "mse(final residual)", "delta_source": True,
+                       "mixers_and_shared_expert": "excluded"},
+            "step_flops": step_flops, "phases_ms": {"step": ms},
+            "roofline": roofline("flop", step_flops, ms, "the step's bf16 grouped GEMMs (warmup steps without "
+                                 "the weight-gradient products) with the source-table mask passes and ascents", 1)}
+
+
 # ============================================================== faithfulness
 def faith_cpu_baseline(groups, reps=3):
     import numpy as np
@@ -1116,6 +1184,8 @@ def main():
         res = run_faith(args)
     elif args.workload == PPGD_DENSE:
         res = run_ppgd(args)
+    elif args.workload == PPGD_MOE:
+        res = run_ppgd_moe(args)
     elif args.workload == KL_STREAM:
         res = run_kl(args)
     else:

@@ -341,6 +341,34 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
                       float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dVg, float* dUg,
                       float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                       void* workspace, size_t workspace_bytes, void* stream);
+/* pd_moe_stack_step with persistent (adversarial) source tables in place of the draws:
+ * the reference's SourceMaskIngredients arm (pd/targets/qwen36_moe.py:2151-2163,
+ * pd/core/source_mask.py:56-63) over block-factored sources read at each selected value's
+ * expert (pd/core/masking.py:43-68), the source half of persistent PGD
+ * (pd/core/train.py:693-811, pd/core/adversary.py:463-567). src [L, 3, S, E, c]
+ * (src_dtype F32, BF16 or U16 = u / 65535), every source row covering rows_per_source
+ * consecutive tokens (S = T / rows_per_source: rows_per_source = T is the `c` shape, the
+ * positions of a sample `bc`, 1 `bsc`); m = lower + (1 - lower) bf16(src[t / rps, e, :]);
+ * src_delta [L, 3, S] (its own dtype; NULL = no delta channel) gives each token's delta,
+ * d = bf16(src_delta[t / rps]). Outputs as pd_moe_stack_step (the weight gradients only
+ * when want_weight_grads; NULL allowed otherwise: the warmup ascents need only the
+ * sources' gradient), plus d_src fp32 [L, 3, S, E, c] = the sum over each row's selected
+ * values of dm (1 - lower) (unselected entries 0), and d_src_delta fp32 [L, 3, S] = the sum
+ * over each row's tokens and their jobs of the delta cotangent sum_o g_out frozen -
+ * sum_c dm. Every sum is in a fixed order. Workspace:
+ * pd_moe_stack_sources_workspace_size. */
+size_t pd_moe_stack_sources_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L,
+                                           int64_t rows_per_source);
+int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                              const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                              const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                              const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
+                              int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
+                              int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                              float recon_coeff, int want_weight_grads, float* losses, float* dVg, float* dUg,
+                              float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, float* d_src,
+                              float* d_src_delta, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
+                              void* stream);
 /* pd_moe_stack_step recording a hipEvent_t before each launch group and one at the
  * end; categories[i] labels the interval [i, i+1): 0 clean forward, 1 masked norm /
  * router / bucketing / gather, 2 grouped GEMMs fwd, 3 mask fwd, 4 SwiGLU fold,

@@ -98,7 +98,7 @@ def grouped_T(lhs, rhs, sizes):
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                    bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None,
-                   pinned_top_idx=None, imp_min=None):
+                   pinned_top_idx=None, imp_min=None, sources=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
     given. `pinned_top_idx[l]` ([T, k]) replaces the clean pass's own expert selection
@@ -108,7 +108,19 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     imp, grads, d_ci_pre, top_idx, own_top_idx, logits_raw, logits_mag, r_final,
     rc_final, deltas). `imp_min` (a `pd_oracle.ImpMin`) replaces the L_p term given by
     p / imp_coeff; each site's selected values map to their expert's block of the
-    [E * c] component vector; `freq` is the frequency term."""
+    [E * c] component vector; `freq` is the frequency term.
+
+    `sources = (src, src_delta, rows_per_source)` replaces the draws by persistent
+    (adversarial) source tables, the reference's `SourceMaskIngredients` arm
+    (`pd/targets/qwen36_moe.py:2151-2163`, `pd/core/source_mask.py:56-63`,
+    `pd/core/masking.py:43-68`): src[l][site] [S, E, c], src_delta[l][site] [S], every
+    source row covering rows_per_source consecutive tokens (S = T / rows_per_source: the
+    `c`, `bc` and `bsc` shapes). A selected value reads its expert's row,
+    m = lower + (1 - lower) src[t // rps, idx[t, slot], :], and the site's delta is
+    src_delta[t // rps]. The result then also holds the source gradients d_src[l][site]
+    (scatter of dm (1 - lower) into [S, E, c]) and d_src_delta[l][site] [S] (the delta
+    cotangent sum_o g_out frozen - sum_c dm of every job, summed over each source row's
+    tokens)."""
     rb = po.round_bf16 if bf16_storage else (lambda a: a)
     spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
     T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
@@ -160,12 +172,18 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             a_, f_, dup = po.impmin_site_terms(up, spec, T, idx, E)
             imp += a_
             freq += f_
-            if source_value is None:
+            if sources is not None:
+                src_t, src_d, rps = sources
+                # the table is cast to the CI dtype before the select (pd/core/masking.py:57)
+                ut = rb(np.asarray(src_t[l][s], np.float64))[(np.arange(T) // rps)[:, None], idx.astype(np.int64)]
+            elif source_value is None:
                 ut = tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c)
             else:
                 ut = np.full((T, k, c), float(source_value))
             m_tok = lo + (1.0 - lo) * ut
-            if deltas is not None:
+            if sources is not None:
+                dt = rb(np.asarray(sources[1][l][s], np.float64))[np.arange(T) // sources[2]]
+            elif deltas is not None:
                 dt = np.asarray(deltas[l][s], np.float64)
             elif use_delta and source_value is not None:
                 dt = np.full(T, float(source_value))
@@ -182,14 +200,16 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             S[s]["h"] = rb(po.grouped_matmul(xj, P["V" + s[0]], jobs.group_sizes))
             S[s]["acts"] = rb(S[s]["h"] * S[s]["coef"])
             frozen = rb(po.grouped_matmul(xj, P["W" + s[0]], jobs.group_sizes))
+            S[s]["frozen"] = frozen
             S[s]["out"] = rb(rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
                              + S[s]["dj"] * frozen)
         gq, uq = S["gate"]["out"], S["up"]["out"]
         din = rb(silu(gq) * uq * wj[:, None])
         S["down"]["h"] = rb(po.grouped_matmul(din, P["Vd"], jobs.group_sizes))
         S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["coef"])
+        S["down"]["frozen"] = rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes))
         dout = (rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
-                + S["down"]["dj"] * rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes)))
+                + S["down"]["dj"] * S["down"]["frozen"])
         routed = rb(po.sum_jobs(dout, jobs))
         saved.append(dict(r=r, rinv=rinv, h2=h2, probs=probs, w=w, wj=wj, jobs=jobs, xj=xj, S=S, din=din, idx=idx))
         r = rb(r + routed)
@@ -200,6 +220,8 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     dr = rb(recon_coeff * 2.0 * (r - rc) / n)
     grads = [dict() for _ in range(cfg.L)]
     d_pre = [dict() for _ in range(cfg.L)]
+    d_src = [dict() for _ in range(cfg.L)]
+    d_src_delta = [dict() for _ in range(cfg.L)]
     for l in reversed(range(cfg.L)):
         P, sv = params[l], saved[l]
         jobs, S = sv["jobs"], sv["S"]
@@ -207,6 +229,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_dout = dr[jobs.sort_idx // k]
         # down site
         Sd = S["down"]
+        Sd["gout"] = d_dout
         d_acts = rb(grouped_T(d_dout, P["Ud"], sizes))
         grads[l]["Ud"] = po.transposed_grouped_matmul(Sd["acts"], d_dout, sizes)
         Sd["dm"] = d_acts * Sd["h"]
@@ -222,6 +245,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_xj = np.zeros_like(sv["xj"])
         for s, dgo in (("gate", d_g), ("up", d_u)):
             Ss = S[s]
+            Ss["gout"] = dgo
             d_acts = rb(grouped_T(dgo, P["U" + s[0]], sizes))
             grads[l]["U" + s[0]] = po.transposed_grouped_matmul(Ss["acts"], dgo, sizes)
             Ss["dm"] = d_acts * Ss["h"]
@@ -237,6 +261,18 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             dm_tok = dm_tok.reshape(T, k, c)
             dlo = dm_tok * (1.0 - Ss["u"])
             d_pre[l][s] = rb(po.lower_leaky_vjp(Ss["pre"], dlo) + po.upper_leaky_vjp(Ss["pre"], Ss["dup"]))
+            if sources is not None:
+                rps = sources[2]
+                Sn = T // rps
+                ds = np.zeros((Sn, E, c))
+                np.add.at(ds, ((np.arange(T) // rps)[:, None], sv["idx"].astype(np.int64)),
+                          dm_tok * (1.0 - Ss["lo"]))
+                d_src[l][s] = ds
+                # the delta cotangent per job (d enters as acts = h (m - d) and + d frozen)
+                qj = np.sum(Ss["gout"] * Ss["frozen"], axis=-1) - np.sum(Ss["dm"], axis=-1)
+                d_tok = np.zeros(T)
+                np.add.at(d_tok, jobs.sort_idx // k, qj)
+                d_src_delta[l][s] = d_tok.reshape(Sn, rps).sum(axis=1)
         # routing weights -> probs -> logits -> h2
         d_w = d_wj[jobs.inv_sort_idx].reshape(T, k)
         w, probs, idx = sv["w"], sv["probs"], sv["idx"]
@@ -249,7 +285,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
         dr = rb(dr + dx)
     return dict(loss=loss, recon=recon, imp=imp, freq=freq, grads=grads, d_ci_pre=d_pre, top_idx=tops,
-                own_top_idx=own_tops,
+                d_src=d_src, d_src_delta=d_src_delta, own_top_idx=own_tops,
                 logits_raw=raws, logits_mag=mags, r_final=r, rc_final=rc, dx0=dr,
                 deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
 
@@ -313,7 +349,8 @@ def init_moe(cfg: MoEConfig, rng):
 
 
 def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                         use_delta=True, partitionable=True, dtype=None, threads=None, imp_min=None):
+                         use_delta=True, partitionable=True, dtype=None, threads=None, imp_min=None,
+                         sources=None):
     """The same step as `moe_stack_step` (no bf16 storage model) written as a torch
     forward whose backward is torch autograd: in float64 it pins `moe_stack_step`'s
     hand-written backward (tests/test_moe_oracle.py). The expert selection and Threefry
@@ -340,6 +377,11 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
 
     P = [{n: t(v, n[0] in "VU") for n, v in layer.items()} for layer in params]
     pre = [{s: t(ci_pre[l][s], True) for s in SITES} for l in range(cfg.L)]
+    if sources is not None:  # persistent source tables as autograd leaves
+        src = [{s: t(sources[0][l][s], True) for s in SITES} for l in range(cfg.L)]
+        srcd = [{s: t(sources[1][l][s], True) for s in SITES} for l in range(cfg.L)]
+        rps = sources[2]
+        doc = torch.as_tensor(np.arange(T) // rps, dtype=torch.long)
     # clean pass: the expert selection (no gradient)
     with torch.no_grad():
         rc = t(x0)
@@ -387,9 +429,13 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
                 imp = imp + fr.sum()
                 if spec.ref_count > 0:
                     freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
-            u = t(tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c))
-            dlt = (t(tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)) if use_delta
-                   else torch.zeros(T, dtype=dt))
+            if sources is not None:
+                u = src[l][s][doc[:, None], idx]
+                dlt = srcd[l][s][doc]
+            else:
+                u = t(tf.uniform(keys[s], (T, k * c), "bfloat16", partitionable=partitionable).reshape(T, k, c))
+                dlt = (t(tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)) if use_delta
+                       else torch.zeros(T, dtype=dt))
             m = (lo + (1.0 - lo) * u).reshape(T * k, c)[sidx]
             coef[s] = (m - dlt[tok][:, None], dlt[tok][:, None])
         wj = w.reshape(-1)[sidx]
@@ -406,12 +452,21 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
     loss = recon_coeff * recon + spec.coeff * imp + (spec.freq_coeff * freq if spec.kind == "smooth_l0" else 0.0)
     names = [(l, n) for l in range(cfg.L) for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud")]
     wrt = [P[l][n] for l, n in names] + [pre[l][s] for l in range(cfg.L) for s in SITES]
+    if sources is not None:
+        wrt += [src[l][s] for l in range(cfg.L) for s in SITES] + [srcd[l][s] for l in range(cfg.L) for s in SITES]
     g = torch.autograd.grad(loss, wrt)
     grads = [dict() for _ in range(cfg.L)]
     for (l, n), v in zip(names, g[:len(names)]):
         grads[l][n] = v.double().numpy()
     d_ci = [dict() for _ in range(cfg.L)]
+    d_src = [dict() for _ in range(cfg.L)]
+    d_srcd = [dict() for _ in range(cfg.L)]
+    nls = cfg.L * len(SITES)
     for i, (l, s) in enumerate((l, s) for l in range(cfg.L) for s in SITES):
         d_ci[l][s] = g[len(names) + i].double().numpy()
+        if sources is not None:
+            d_src[l][s] = g[len(names) + nls + i].double().numpy()
+            d_srcd[l][s] = g[len(names) + 2 * nls + i].double().numpy()
     return dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()),
-                freq=float(freq.detach()) if torch.is_tensor(freq) else freq, grads=grads, d_ci_pre=d_ci, top_idx=tops)
+                freq=float(freq.detach()) if torch.is_tensor(freq) else freq, grads=grads, d_ci_pre=d_ci, top_idx=tops,
+                d_src=d_src, d_src_delta=d_srcd)

@@ -215,3 +215,50 @@ class DenseSitePPGDStep:
         loss, dV, dU, d_ci, d_src, d_dsrc = self._grads(x, V, U, W, ci, target, zeros, final=True)
         self._ascend(d_src, d_dsrc, lr, final_key)
         return PPGDStepResult(loss=loss, dV=dV, dU=dU, d_ci=d_ci, warmup_losses=warmup_losses)
+
+
+class MoEPPGDStep:
+    """The persistent-PGD reconstruction step over every expert site of the MoE stack
+    (`pd/core/train.py:693-811`, `pd/core/adversary.py:463-567`, the source-masking arm of
+    `pd/targets/qwen36_moe.py:2151-2163`), on `pd_moe_stack_step_sources`: `n_warmup`
+    ascents of the adversary on the detached reconstruction loss (only the source
+    gradients are formed), then the final step, whose backward gives the model and CI
+    gradients and the source gradients of the final ascent.
+
+    `adversary.sources` is the stacked component-source leaf [L, 3, S, E, c] (sites gate,
+    up, down; every row covering `step.rows_per_source` tokens), `delta_adversary.sources`
+    the delta leaf [L, 3, S] (the next leaf, so its uint16 rounding draws fold in
+    `leaf_index + 1`). Keys as `DenseSitePPGDStep.step`."""
+
+    def __init__(self, step, adversary: PersistentAdversary, delta_adversary: PersistentAdversary | None = None):
+        self.step_fn = step
+        self.adv = adversary
+        self.dadv = delta_adversary
+        if step.rows_per_source is None:
+            raise ValueError("the MoE step must be constructed with rows_per_source")
+        if delta_adversary is not None and delta_adversary.n_warmup != adversary.n_warmup:
+            raise ValueError("delta sources share the component sources' warmup count")
+
+    def _run(self, x0, w, ci_pre, final: bool):
+        self.step_fn.step_sources(x0, w, ci_pre, self.adv.sources, None if self.dadv is None else self.dadv.sources,
+                                  want_weight_grads=final)
+        return self.step_fn.losses[0].clone()
+
+    def _ascend(self, lr, key):
+        self.adv.after_one_ascent(self.step_fn.d_src, lr, key)
+        if self.dadv is not None:
+            self.dadv.after_one_ascent(self.step_fn.d_src_delta, lr, key)
+
+    def step(self, x0, w, ci_pre, lr: float, key, adv_index: int = 0) -> PPGDStepResult:
+        quantize_key = prng.fold_in(key, 0x51C)
+        warm_key = prng.fold_in(quantize_key, adv_index)
+        final_key = prng.fold_in(prng.fold_in(quantize_key, 0x51D), adv_index)
+        warmup_losses = []
+        n = self.adv.n_warmup
+        for ascent_key in prng.split(warm_key, n) if n else []:
+            warmup_losses.append(self._run(x0, w, ci_pre, final=False))
+            self._ascend(lr, ascent_key)
+        loss = self._run(x0, w, ci_pre, final=True)
+        self._ascend(lr, final_key)
+        s = self.step_fn
+        return PPGDStepResult(loss=loss, dV=s.dV, dU=s.dU, d_ci=s.d_ci_pre, warmup_losses=warmup_losses)

@@ -255,12 +255,40 @@ struct SiteMaskArgs {
   float g2, psis;
   float* colpart;
   const float* slope;
+  // persistent source tables (MASK_SRC): src [S, E, c] of this (layer, site), S = T / rps
+  // rows of rps consecutive tokens; the backward writes the tables' gradient as
+  // per-(tile, group) column sums colsrc (group = expert * S + row, rps > 1) or straight
+  // into dsrc [T, E, c] (rps = 1), and each job's per-tile row sums of dm into rowdm
+  const void* src;
+  int src_dtype;
+  int64_t rps, S;
+  float* colsrc;
+  float* dsrc;
+  float* rowdm;
 };
 
 // Mask-source variant of the mask kernels beside the two Threefry layouts: every source
 // value is the constant SiteMaskArgs::uconst (the reference's ConstantSources; 0 is the
 // CI-masked reconstruction), nothing is drawn and no u bytes are kept.
 static constexpr int MASK_CONST = 2;
+// Persistent (adversarial) source tables: a selected value reads its expert's row of the
+// table, u = src[(t / rps) E c + e c + q] (the reference's SourceMaskIngredients,
+// pd/core/masking.py:43-68), cast to bf16 as the reference casts the table to the CI
+// dtype before the select; no u bytes are kept.
+static constexpr int MASK_SRC = 3;
+
+__device__ inline float src_value(const void* src, int dtype, int64_t i) {
+  float v;
+  if (dtype == PD_DTYPE_F32) v = ((const float*)src)[i];
+  else if (dtype == PD_DTYPE_BF16) v = bf16_to_f32(((const bf16_t*)src)[i]);
+  else v = (float)((const uint16_t*)src)[i] * (1.f / 65535.f);
+  return bf16_to_f32(f32_to_bf16(v));
+}
+
+// The table index of job j's element (q): source row of its token, its expert.
+__device__ inline int64_t src_index(const SiteMaskArgs& a, int32_t slot, int e, int q) {
+  return (((int64_t)(slot / a.k) / a.rps) * a.E + e) * a.c + q;
+}
 
 __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
 
@@ -303,6 +331,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       uint32_t ub = 0;
+      const int ej = LAYOUT == MASK_SRC ? row_group(a.offsets, a.E, j) : 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
@@ -311,6 +340,8 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
         float u;
         if constexpr (LAYOUT == MASK_CONST) {
           u = a.uconst;
+        } else if constexpr (LAYOUT == MASK_SRC) {
+          u = src_value(a.src, a.src_dtype, src_index(a, slot, ej, q0 + q4 + e));
         } else {
           const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
           ub |= kb << (8 * e);
@@ -318,7 +349,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
         }
         o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt));
       }
-      if constexpr (LAYOUT != MASK_CONST) *(uint32_t*)(ubits + idx) = ub;
+      if constexpr (LAYOUT != MASK_CONST && LAYOUT != MASK_SRC) *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     } else if constexpr (PM == PM_SL0) {
 #pragma unroll
@@ -342,21 +373,31 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 // Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts, plus d_h^T [c,J]) and the
 // CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
 // upper_vjp(pre, imp_scale * d upper^p), written token-major.
-template <int PM>
+// SRC: the sources are tables (MASK_SRC): u is read back from the table, and the tables'
+// gradient dm (1 - lower) (dm = d_acts h) and each job's row sums of dm are written.
+template <int PM, bool SRC>
 __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
                                                        bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_hT,
                                                        bf16_t* __restrict__ d_pre) {
   __shared__ TTile T;
+  __shared__ typename std::conditional<SRC, Sl0Tile, NoSl0Tile>::type SG;
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
   const bool qok = q0 + q4 < a.c;
+  if constexpr (SRC) {
+    if (tid < 64) {  // each row's (expert, source row) group; rows are sorted by it
+      const int64_t j = j0 + tid;
+      SG.grp[tid] = j < a.J ? row_group(a.offsets, a.E, j) * (int)a.S + (int)((a.sort_idx[j] / a.k) / a.rps) : -1;
+    }
+  }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int r = PD_TILE4_ROW(pass);
     const int64_t j = j0 + r;
     bf16_t o[4] = {0, 0, 0, 0};
+    float dmsum = 0.f;
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
       const int32_t slot = a.sort_idx[j];
@@ -365,7 +406,8 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const uint2 dw = *(const uint2*)(d_acts + idx);
-      const uint32_t ub = a.uconst < 0.f ? *(const uint32_t*)(ubits + idx) : 0u;
+      const uint32_t ub = !SRC && a.uconst < 0.f ? *(const uint32_t*)(ubits + idx) : 0u;
+      const int ej = SRC ? row_group(a.offsets, a.E, j) : 0;
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
@@ -381,21 +423,43 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-        const float u = a.uconst < 0.f ? (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f) : a.uconst;
+        float u;
+        if constexpr (SRC) u = src_value(a.src, a.src_dtype, src_index(a, slot, ej, q0 + q4 + e));
+        else u = a.uconst < 0.f ? (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f) : a.uconst;
         const float m = lo + (1.f - lo) * u - dt;
         float dimp;
         if constexpr (PM == PM_SL0) dimp = slope4[e] * sl0_dpsi(up, a.g2, a.psis);
         else dimp = imp_scale * dpowp<PM>(up, a.p);
-        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp));
+        const float dm = da[e] * hv[e];
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], dm * (1.f - u)) + upper_vjp(pre[e], dimp));
         o[e] = f32_to_bf16(da[e] * m);
+        if constexpr (SRC) {
+          dmsum += dm;
+          const float gs = dm * (1.f - lo);
+          if (a.rps == 1) a.dsrc[src_index(a, slot, ej, q0 + q4 + e)] = gs;
+          else SG.ps[r][q4 + e] = gs;
+        }
       }
       *(uint2*)(d_pre + src) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
       *(uint2*)(d_acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    } else if constexpr (SRC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) SG.ps[r][q4 + e] = 0.f;
+    }
+    if constexpr (SRC) {  // the 16 lanes of a row add their columns in a fixed tree (all lanes)
+      dmsum += __shfl_xor(dmsum, 1, 64);
+      dmsum += __shfl_xor(dmsum, 2, 64);
+      dmsum += __shfl_xor(dmsum, 4, 64);
+      dmsum += __shfl_xor(dmsum, 8, 64);
+      if (j < a.J && (tid & 15) == 0) a.rowdm[j * gridDim.x + blockIdx.x] = dmsum;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
   __syncthreads();
+  if constexpr (SRC) {
+    if (a.rps > 1) sl0_tile_colsums(SG, blockIdx.y, q0, a.c, a.colsrc, tid);
+  }
   ttile_store(T, d_hT, a.J, j0, a.J, q0, a.c, tid);
 }
 
@@ -791,11 +855,116 @@ __global__ __launch_bounds__(256) void k_delta_sites(uint32_t b0, uint32_t b1, i
   delta[(int64_t)site * T + t] = draw_uniform(k0, k1, t, T, PD_DTYPE_BF16, layout);
 }
 
+// ---------------------------------------------------------------- persistent sources
+// delta[(l*3 + s)*T + t] = bf16(src_delta[(l*3 + s)*S + t / rps]): each token's delta is
+// its source row's value, cast to the CI dtype as the reference casts the delta table.
+__global__ __launch_bounds__(256) void k_src_delta_fill(const void* __restrict__ src_delta, int dtype, int64_t S,
+                                                        int64_t rps, int64_t T, int n_sites,
+                                                        float* __restrict__ delta) {
+  const int64_t n = (int64_t)n_sites * T;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t site = i / T, t = i % T;
+    delta[i] = src_value(src_delta, dtype, site * S + t / rps);
+  }
+}
+
+// goff[g] for g = e * S + row: the first job of expert e whose token lies in source row
+// `row` or later (jobs of an expert are in token order), goff[E * S] = J.
+__global__ __launch_bounds__(256) void k_src_group_offsets(const int32_t* __restrict__ off,
+                                                           const int32_t* __restrict__ sort_idx, int E, int k,
+                                                           int64_t S, int64_t rps, int64_t J,
+                                                           int32_t* __restrict__ goff) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t G = (int64_t)E * S;
+  if (g > G) return;
+  if (g == G) {
+    goff[G] = (int32_t)J;
+    return;
+  }
+  const int e = (int)(g / S);
+  const int64_t row = g % S;
+  int64_t lo = off[e], hi = off[e + 1];
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)(sort_idx[mid] / k) / rps >= row) hi = mid;
+    else lo = mid + 1;
+  }
+  goff[g] = (int32_t)lo;
+}
+
+// d_src[(row * E + e) * c + q] = the sum, in tile order, of the column partials of group
+// g = e * S + row over the tiles its jobs [goff[g], goff[g+1]) touch (0 when it has none).
+__global__ __launch_bounds__(256) void k_src_finalize(const float* __restrict__ colsrc,
+                                                      const int32_t* __restrict__ goff, int E, int64_t S, int c,
+                                                      float* __restrict__ d_src) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)E * S * c) return;
+  const int64_t g = i / c;
+  const int q = (int)(i % c);
+  const int64_t lo = goff[g], hi = goff[g + 1];
+  float F = 0.f;
+  if (hi > lo)
+    for (int64_t t = lo / 64; t <= (hi - 1) / 64; ++t) F += colsrc[(t + g) * c + q];
+  const int e = (int)(g / S);
+  const int64_t row = g % S;
+  d_src[(row * E + e) * c + q] = F;
+}
+
+// q[j] = sum_o gout[j,o] frozen[j,o] - sum_p rowdm[j, p]: the delta cotangent of job j's
+// site (d enters the site as acts = h (m - d) and as + d frozen). One wave per job, fp32.
+__global__ __launch_bounds__(256) void k_job_delta_cot(const bf16_t* __restrict__ gout,
+                                                       const bf16_t* __restrict__ frozen,
+                                                       const float* __restrict__ rowdm, int n_parts, int64_t J,
+                                                       int w, float* __restrict__ q) {
+  const int64_t j = (int64_t)blockIdx.x * 4 + wave_id();
+  if (j >= J) return;
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int i = lane * 8; i < w; i += 512) {
+    float a[8], b[8];
+    load8(gout + j * w + i, a);
+    load8(frozen + j * w + i, b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(a[e], b[e], acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    float dm = 0.f;
+    for (int p = 0; p < n_parts; ++p) dm += rowdm[j * n_parts + p];
+    q[j] = acc - dm;
+  }
+}
+
+// d_src_delta[row] = sum over the row's tokens t of sum_s q[inv[t*k + s]]. One wave per
+// source row, a fixed order (lane-strided tokens, then the wave tree).
+__global__ __launch_bounds__(256) void k_src_delta_grad(const float* __restrict__ q, const int32_t* __restrict__ inv,
+                                                        int64_t S, int64_t rps, int k,
+                                                        float* __restrict__ d_src_delta) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= S) return;
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int64_t t = row * rps + lane; t < (row + 1) * rps; t += 64)
+    for (int s = 0; s < k; ++s) acc += q[inv[t * k + s]];
+  acc = wave_sum(acc);
+  if (lane == 0) d_src_delta[row] = acc;
+}
+
+// out[0, n) = 0.
+__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
+}
+
 static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h, bf16_t* acts,
                             bf16_t* actsT, uint8_t* ub, float* part) {
 #define PD_MF(LY, PMV) \
   hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, actsT, ub, part)
-  if (ma.uconst >= 0.f) {
+  if (ma.src) {
+    if (pm == PM_SL0) PD_MF(MASK_SRC, PM_SL0);
+    else if (pm == 2) PD_MF(MASK_SRC, 2);
+    else if (pm == 1) PD_MF(MASK_SRC, 1);
+    else PD_MF(MASK_SRC, 0);
+  } else if (ma.uconst >= 0.f) {
     if (pm == PM_SL0) PD_MF(MASK_CONST, PM_SL0);
     else if (pm == 2) PD_MF(MASK_CONST, 2);
     else if (pm == 1) PD_MF(MASK_CONST, 1);
@@ -816,12 +985,19 @@ static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
 
 static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h,
                             const uint8_t* ub, float imp_scale, bf16_t* d_acts, bf16_t* d_hT, bf16_t* d_pre) {
-#define PD_MB(PMV) \
-  hipLaunchKernelGGL((k_mask_bwd_tile<PMV>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_hT, d_pre)
-  if (pm == PM_SL0) PD_MB(PM_SL0);
-  else if (pm == 2) PD_MB(2);
-  else if (pm == 1) PD_MB(1);
-  else PD_MB(0);
+#define PD_MB(PMV, SRC) \
+  hipLaunchKernelGGL((k_mask_bwd_tile<PMV, SRC>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_hT, d_pre)
+  if (ma.src) {
+    if (pm == PM_SL0) PD_MB(PM_SL0, true);
+    else if (pm == 2) PD_MB(2, true);
+    else if (pm == 1) PD_MB(1, true);
+    else PD_MB(0, true);
+  } else {
+    if (pm == PM_SL0) PD_MB(PM_SL0, false);
+    else if (pm == 2) PD_MB(2, false);
+    else if (pm == 1) PD_MB(1, false);
+    else PD_MB(0, false);
+  }
 #undef PD_MB
 }
 
@@ -836,6 +1012,7 @@ static constexpr int REC_BLOCKS = 1024;
 struct MoEDims {
   int64_t T, J;
   int d, f, E, k, c, L;
+  int64_t S;  // persistent-source rows (0: no source tables)
 };
 
 struct Arena {
@@ -853,6 +1030,7 @@ struct Arena {
 
 struct LayerSave {
   bf16_t *r, *h2, *xjT, *gout, *uout, *dinT;
+  bf16_t *fg, *fu, *fd;  // the frozen channel's products x_jobs @ Wg/Wu[e], din @ Wd[e]
   float *rinv, *probs, *w;
   int32_t *idx, *sort_idx, *inv, *sizes, *offsets;
   bf16_t* h[3];
@@ -864,7 +1042,9 @@ struct MoEPlan {
   std::vector<LayerSave> layers;
   // weight copies [L, E, N, K] for the forward products
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *fg0, *fu0, *din, *downc, *down, *dr_a, *dr_b;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
+  float *colsrc, *rowdm, *qjob;  // persistent sources: group column sums, job row sums, job delta cotangents
+  int32_t* goff;
   float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
@@ -895,6 +1075,9 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
     S.gout = A.take<bf16_t>(J * D.f);
     S.uout = A.take<bf16_t>(J * D.f);
     S.dinT = A.take<bf16_t>(J * D.f);
+    S.fg = A.take<bf16_t>(J * D.f);
+    S.fu = A.take<bf16_t>(J * D.f);
+    S.fd = A.take<bf16_t>(J * D.d);
     for (int s = 0; s < 3; ++s) {
       S.h[s] = A.take<bf16_t>(J * D.c);
       S.actsT[s] = A.take<bf16_t>(J * D.c);
@@ -919,8 +1102,6 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.acts[1] = A.take<bf16_t>(J * D.c);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
-  P.fg0 = A.take<bf16_t>(J * D.f);
-  P.fu0 = A.take<bf16_t>(J * D.f);
   P.din = A.take<bf16_t>(J * D.f);
   P.downc = A.take<bf16_t>(J * D.d);
   P.down = A.take<bf16_t>(J * D.d);
@@ -939,6 +1120,10 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.sl0_slope = A.take<float>(P.sl0_slope_per_site * 3 * L);
   P.sl0_act = A.take<float>(P.sl0_blocks_per_site * 3 * L);
   P.sl0_freq = A.take<float>(P.sl0_blocks_per_site * 3 * L);
+  P.colsrc = A.take<float>(D.S && D.S < T ? (size_t)(cdiv(J, TILE) + (int64_t)D.E * D.S) * D.c : 1);
+  P.rowdm = A.take<float>(D.S ? (size_t)J * cdiv(D.c, TILE) : 1);
+  P.qjob = A.take<float>(D.S ? (size_t)J : 1);
+  P.goff = A.take<int32_t>(D.S ? (size_t)D.E * D.S + 1 : 1);
   P.d_w_part = A.take<float>(J * cdiv(D.f, TILE));
   P.delta = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
@@ -986,7 +1171,14 @@ using namespace pd;
 extern "C" {
 
 size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L) {
-  MoEDims D{T, T * k, d, f, E, k, c, L};
+  MoEDims D{T, T * k, d, f, E, k, c, L, 0};
+  return plan(D, nullptr, true).total;
+}
+
+size_t pd_moe_stack_sources_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L,
+                                           int64_t rows_per_source) {
+  if (rows_per_source <= 0 || T % rows_per_source) return 0;
+  MoEDims D{T, T * k, d, f, E, k, c, L, T / rows_per_source};
   return plan(D, nullptr, true).total;
 }
 
@@ -1006,13 +1198,26 @@ enum {
   MOE_CAT_END = 10
 };
 
+// Persistent (adversarial) source tables for pd_moe_stack_step_sources.
+struct SrcArgs {
+  const void* src;    // [L, 3, S, E, c]
+  int src_dtype;
+  const void* delta;  // [L, 3, S] or NULL (no delta channel)
+  int delta_dtype;
+  int64_t rps;        // tokens per source row (S = T / rps)
+  int want_wgrads;    // 0: only the source gradients (warmup ascents)
+  float* d_src;       // fp32 [L, 3, S, E, c]
+  float* d_src_delta; // fp32 [L, 3, S]
+};
+
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                          const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
                          int layout, const ImpSpec& imp, float recon_coeff, float* losses, float* dVg, float* dUg,
                          float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
-                         void* workspace, size_t workspace_bytes, void* stream, Recorder& rec) {
+                         void* workspace, size_t workspace_bytes, void* stream, Recorder& rec,
+                         const SrcArgs* srcs = nullptr) {
   int rc0;
   if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 512 || k <= 0 || k > E || k > 64 || c <= 0 || L <= 0)
     return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 512, k <= 64)");
@@ -1021,14 +1226,25 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   if (d > 4096 || T * k > 0x7FFFFFFF || cdiv(T * k, TILE) > 65535)
     return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: shape too large");
   if (!x0 || !ln || !router || !Wg || !Wu || !Wd || !Vg || !Ug || !Vu || !Uu || !Vd || !Ud || !ci_pre || !losses ||
-      !dVg || !dUg || !dVu || !dUu || !dVd || !dUd || !d_ci_pre)
+      !d_ci_pre)
     return fail(PD_EINVAL, "pd_moe_stack_step: null pointer");
+  if ((!srcs || srcs->want_wgrads) && (!dVg || !dUg || !dVu || !dUu || !dVd || !dUd))
+    return fail(PD_EINVAL, "pd_moe_stack_step: null weight-gradient output");
   if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
     return fail(PD_EINVAL, "pd_moe_stack_step: unknown counter layout");
   if (!(source_value <= 1.f)) return fail(PD_EINVAL, "pd_moe_stack_step: source_value must be < 0 (drawn) or in [0, 1]");
   if ((rc0 = check_imp_spec(imp, "pd_moe_stack_step"))) return rc0;
   const float uconst = source_value >= 0.f ? source_value : -1.f;
-  const MoEDims D{T, T * k, d, f, E, k, c, L};
+  if (srcs) {
+    if (!srcs->src || srcs->rps <= 0 || T % srcs->rps || !srcs->d_src || (srcs->delta && !srcs->d_src_delta))
+      return fail(PD_EINVAL, "pd_moe_stack_step_sources: source tables, rows_per_source | T and outputs required");
+    for (int dt : {srcs->src_dtype, srcs->delta ? srcs->delta_dtype : PD_DTYPE_F32})
+      if (dt != PD_DTYPE_F32 && dt != PD_DTYPE_BF16 && dt != PD_DTYPE_U16)
+        return fail(PD_EINVAL, "pd_moe_stack_step_sources: source dtype");
+    use_delta = srcs->delta ? 1 : 0;
+  }
+  const bool want_wgrads = !srcs || srcs->want_wgrads;
+  const MoEDims D{T, T * k, d, f, E, k, c, L, srcs ? T / srcs->rps : 0};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
     return fail(PD_EWORKSPACE, "pd_moe_stack_step: workspace too small");
   MoEPlan P = plan(D, (char*)workspace, false);
@@ -1066,6 +1282,24 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.colpart = P.sl0_col + sl * P.sl0_col_per_site;
     ma.slope = P.sl0_slope + sl * P.sl0_slope_per_site;
   };
+  // the (layer, site)'s source table, or none
+  const size_t src_site = (size_t)D.S * E * c;
+  auto src_fill = [&](SiteMaskArgs& ma, int l, int si) {
+    ma.src = nullptr;
+    ma.src_dtype = PD_DTYPE_F32;
+    ma.rps = 1;
+    ma.S = 0;
+    ma.colsrc = ma.dsrc = ma.rowdm = nullptr;
+    if (!srcs) return;
+    const size_t es = srcs->src_dtype == PD_DTYPE_F32 ? 4 : 2;
+    ma.src = (const char*)srcs->src + ((size_t)l * 3 + si) * src_site * es;
+    ma.src_dtype = srcs->src_dtype;
+    ma.rps = srcs->rps;
+    ma.S = D.S;
+    ma.colsrc = P.colsrc;
+    ma.dsrc = srcs->d_src + ((size_t)l * 3 + si) * src_site;
+    ma.rowdm = P.rowdm;
+  };
 
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
@@ -1084,7 +1318,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const size_t szV[3] = {szVg, szVg, szVd};
   const size_t szU[3] = {szUg, szUg, szUd};
 
-  if (use_delta && uconst >= 0.f)  // constant sources: the delta mask is the constant too
+  if (srcs && use_delta)  // persistent sources: each token's delta is its source row's
+    hipLaunchKernelGGL(k_src_delta_fill, dim3((unsigned)std::min<int64_t>(cdiv(3 * L * T, 256), 4096)), dim3(256), 0,
+                       s, srcs->delta, srcs->delta_dtype, D.S, srcs->rps, T, 3 * L, P.delta);
+  else if (use_delta && uconst >= 0.f)  // constant sources: the delta mask is the constant too
     hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)std::min<int64_t>(cdiv(3 * L * T, 256), 4096)), dim3(256), 0, s,
                        P.delta, (int64_t)3 * L * T, uconst);
   else if (use_delta)
@@ -1119,8 +1356,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     bf16_t* xjl = l == 0 ? P.xj : P.down;
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, h2l, S.sort_idx, k, J, d, xjl,
                        l == 0 ? S.xjT : (bf16_t*)nullptr);
-    bf16_t* gcl = l == 0 ? P.fg0 : P.gc;
-    bf16_t* ucl = l == 0 ? P.fu0 : P.uc;
+    bf16_t* gcl = l == 0 ? S.fg : P.gc;
+    bf16_t* ucl = l == 0 ? S.fu : P.uc;
     if ((rc = grouped_gemm_pair(xjl, P.WgT + l * szW, gcl, xjl, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
                                 PD_DTYPE_BF16, stream)))
       return rc;
@@ -1167,6 +1404,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.k = k;
       ma.uconst = uconst;
       sl0_fill(ma, S, l, si);
+      src_fill(ma, l, si);
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
       launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], acts_out, S.actsT[si], S.ub[si], part);
       if (sl0) {  // this site's frequencies, loss partials and backward slopes
@@ -1185,15 +1423,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     const bf16_t* fg = nullptr;
     const bf16_t* fu = nullptr;
     if (use_delta) {
-      fg = P.fg0;
-      fu = P.fu0;
-      if (l > 0) {
-        if ((rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, P.gc, P.xj, P.WuT + l * szW, P.uc, S.offsets, J, E, d, f,
-                                    PD_DTYPE_BF16, stream)))
-          return rc;
-        fg = P.gc;
-        fu = P.uc;
-      }
+      fg = S.fg;
+      fu = S.fu;
+      if (l > 0 &&
+          (rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, S.fg, P.xj, P.WuT + l * szW, S.fu, S.offsets, J, E, d, f,
+                                  PD_DTYPE_BF16, stream)))
+        return rc;
     }
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(0, P.acts[0]);
@@ -1210,7 +1445,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = grouped_gemm(P.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
       return rc;
     if (use_delta &&
-        (rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
+        (rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, S.fd, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(2, P.acts[0]);
@@ -1221,7 +1456,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, P.down, S.inv,
-                       (const float*)nullptr, T, k, d, use_delta ? P.downc : (const bf16_t*)nullptr, dlt[2], r_out);
+                       (const float*)nullptr, T, k, d, use_delta ? S.fd : (const bf16_t*)nullptr, dlt[2], r_out);
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
@@ -1256,25 +1491,52 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.k = k;
     ma.uconst = uconst;
     set_delta(l);
+    if (srcs && srcs->rps > 1)  // each (expert, source row) group's job range, for the tables' gradient
+      hipLaunchKernelGGL(k_src_group_offsets, dim3((unsigned)cdiv((int64_t)E * D.S + 1, 256)), dim3(256), 0, s,
+                         S.offsets, S.sort_idx, E, k, D.S, srcs->rps, J, P.goff);
+    // the source tables' gradient of site si, after its mask backward: the group sums in
+    // tile order (or, one token per row, the entries the mask pass wrote), then the delta
+    // table's gradient from each job's delta cotangent
+    auto src_grads = [&](int si, const bf16_t* gout, const bf16_t* frozen, int width) {
+      if (!srcs) return;
+      float* dsrc = srcs->d_src + ((size_t)l * 3 + si) * src_site;
+      if (srcs->rps > 1)
+        hipLaunchKernelGGL(k_src_finalize, dim3((unsigned)cdiv((int64_t)src_site, 256)), dim3(256), 0, s, P.colsrc,
+                           P.goff, E, D.S, c, dsrc);
+      if (use_delta) {
+        hipLaunchKernelGGL(k_job_delta_cot, dim3((unsigned)cdiv(J, 4)), dim3(256), 0, s, gout, frozen, P.rowdm,
+                           (int)cdiv(c, TILE), J, width, P.qjob);
+        hipLaunchKernelGGL(k_src_delta_grad, dim3((unsigned)cdiv(D.S, 4)), dim3(256), 0, s, P.qjob, S.inv, D.S,
+                           srcs->rps, k, srcs->d_src_delta + ((size_t)l * 3 + si) * D.S);
+      }
+    };
+    auto src_zero = [&](int si) {  // one token per row: the mask pass writes only the selected entries
+      if (srcs && srcs->rps == 1)
+        hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)std::min<int64_t>(cdiv((int64_t)src_site, 256), 8192)),
+                           dim3(256), 0, s, srcs->d_src + ((size_t)l * 3 + si) * src_site, (int64_t)src_site);
+    };
     // ---- down site
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[0], PD_DTYPE_BF16, stream,
                            false)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = pd_grouped_gemm_dw_kmajor(S.actsT[2], P.d_doutT, S.offsets, J, E, c, d, dUd + l * szUd, PD_DTYPE_F32,
-                                        stream)))
+    if (want_wgrads && (rc = pd_grouped_gemm_dw_kmajor(S.actsT[2], P.d_doutT, S.offsets, J, E, c, d, dUd + l * szUd,
+                                                       PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
     ma.delta = dlt[2];
     sl0_fill(ma, S, l, 2);
+    src_fill(ma, l, 2);
+    src_zero(2);
     launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0], P.d_hT[0],
                     (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    src_grads(2, P.d_dout, S.fd, d);
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT[0], S.offsets, J, E, f, c, dVd + l * szVd, PD_DTYPE_F32,
-                                        stream)))
+    if (want_wgrads && (rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT[0], S.offsets, J, E, f, c, dVd + l * szVd,
+                                                       PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm(P.d_acts[0], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
@@ -1294,7 +1556,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                                 J, E, f, c, PD_DTYPE_BF16, stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = grouped_gemm_dw_kmajor_pair(S.actsT[0], P.d_gT, dUg + l * szUg, S.actsT[1], P.d_uT, dUu + l * szUg,
+    if (want_wgrads &&
+        (rc = grouped_gemm_dw_kmajor_pair(S.actsT[0], P.d_gT, dUg + l * szUg, S.actsT[1], P.d_uT, dUu + l * szUg,
                                           S.offsets, J, E, c, f, PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
@@ -1303,11 +1566,15 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.delta = dlt[si];
       sl0_fill(ma, S, l, si);
+      src_fill(ma, l, si);
+      src_zero(si);
       launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], P.d_hT[si],
                       (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
+      src_grads(si, si == 0 ? P.d_g : P.d_u, si == 0 ? S.fg : S.fu, f);
     }
     rec.mark(MOE_CAT_GEMM_DW);
-    if ((rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
+    if (want_wgrads &&
+        (rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
                                           S.offsets, J, E, d, c, PD_DTYPE_F32, stream)))
       return rc;
     // The stack input carries no parameter gradient: layer 0 stops at its weight
@@ -1347,6 +1614,29 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
                        draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd,
                        d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
+}
+
+int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
+                              const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
+                              const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
+                              const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
+                              int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
+                              int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                              float recon_coeff, int want_weight_grads, float* losses, float* dVg, float* dUg,
+                              float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, float* d_src,
+                              float* d_src_delta, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  Recorder rec{nullptr, nullptr, 0, 0, nullptr};
+  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  const SrcArgs sa{src, src_dtype, src_delta, delta_dtype, rows_per_source, want_weight_grads, d_src, d_src_delta};
+  if (rows_per_source <= 0 || T % rows_per_source)
+    return fail(PD_EINVAL, "pd_moe_stack_step_sources: rows_per_source must divide T");
+  const MoEDims D{T, T * k, d, f, E, k, c, L, T / rows_per_source};
+  if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
+    return fail(PD_EWORKSPACE, "pd_moe_stack_step_sources: workspace too small");
+  return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, 0, 0,
+                       src_delta != nullptr, -1.f, PD_LAYOUT_PARTITIONABLE, imp, recon_coeff, losses, dVg, dUg, dVu,
+                       dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec, &sa);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,

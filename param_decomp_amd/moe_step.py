@@ -49,7 +49,9 @@ class MoEStackStep:
     def __init__(self, T: int, d: int, f: int, E: int, k: int, c: int, n_layers: int, *, device="cuda",
                  p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
                  layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, source_value: float = -1.0,
-                 imp_min: ImpMin | None = None):
+                 imp_min: ImpMin | None = None, rows_per_source: int | None = None):
+        """rows_per_source: tokens per row of persistent source tables (`step_sources`; T
+        is the `c` shape, a sample's positions `bc`, 1 `bsc`)."""
         self.dims = (T, d, f, E, k, c, n_layers)
         # the imp-min term: L_p (p, imp_coeff) unless a smooth-L0 ImpMin is given
         self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
@@ -68,7 +70,17 @@ class MoEStackStep:
                    "down": torch.empty(Ln, E, c, d, **f32)}
         self.d_ci_pre = torch.empty(Ln, 3, T, k, c, dtype=torch.bfloat16, device=dev)
         self.top_idx = torch.empty(Ln, T, k, dtype=torch.int32, device=dev)
-        self.workspace = L.workspace(L.load().pd_moe_stack_workspace_size(T, d, f, E, k, c, Ln), dev)
+        self.rows_per_source = rows_per_source
+        if rows_per_source is None:
+            nbytes = L.load().pd_moe_stack_workspace_size(T, d, f, E, k, c, Ln)
+        else:
+            if rows_per_source <= 0 or T % rows_per_source:
+                raise L.PDError("MoEStackStep: rows_per_source must divide T")
+            S = T // rows_per_source
+            nbytes = L.load().pd_moe_stack_sources_workspace_size(T, d, f, E, k, c, Ln, rows_per_source)
+            self.d_src = torch.empty(Ln, 3, S, E, c, **f32)
+            self.d_src_delta = torch.empty(Ln, 3, S, **f32)
+        self.workspace = L.workspace(nbytes, dev)
 
     def _args(self, x0, w: MoEWeights, ci_pre, draw_key: Key):
         T, d, f, E, k, c, Ln = self.dims
@@ -79,6 +91,31 @@ class MoEStackStep:
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]
+
+    def step_sources(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, src: torch.Tensor,
+                     src_delta: torch.Tensor | None = None, *, want_weight_grads: bool = True):
+        """The step with persistent source tables in place of the draws: src [L, 3, S, E, c]
+        and src_delta [L, 3, S] (float32, bfloat16 or uint16 storage; None = no delta
+        channel). Fills `d_src`, `d_src_delta` (and the model gradients when
+        `want_weight_grads`)."""
+        if self.rows_per_source is None:
+            raise L.PDError("MoEStackStep: construct with rows_per_source for source tables")
+        T, d, f, E, k, c, Ln = self.dims
+        S = T // self.rows_per_source
+        if tuple(src.shape) != (Ln, 3, S, E, c) or (src_delta is not None and tuple(src_delta.shape) != (Ln, 3, S)):
+            raise L.PDError("step_sources: src [L, 3, S, E, c], src_delta [L, 3, S]")
+        g = want_weight_grads
+        P = lambda t: L.ptr(t) if g else None  # noqa: E731
+        L.call("pd_moe_stack_step_sources", T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router),
+               L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd), L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd),
+               L.ptr(w.Ud), L.ptr(ci_pre), L.ptr(src), L.dtype_code(src.dtype),
+               None if src_delta is None else L.ptr(src_delta),
+               L.F32 if src_delta is None else L.dtype_code(src_delta.dtype), self.rows_per_source,
+               *self.imp_min.c_args(), self.recon_coeff, int(g), L.ptr(self.losses), P(self.dV["gate"]),
+               P(self.dU["gate"]), P(self.dV["up"]), P(self.dU["up"]), P(self.dV["down"]), P(self.dU["down"]),
+               L.ptr(self.d_ci_pre), L.ptr(self.d_src), L.ptr(self.d_src_delta), L.ptr(self.top_idx),
+               L.ptr(self.workspace), self.workspace.numel(), L.stream())
+        return self
 
     def step(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, draw_key: Key):
         L.call("pd_moe_stack_step", *self._args(x0, w, ci_pre, draw_key))

@@ -289,6 +289,41 @@ def test_smooth_l0_moe_step_matches_the_autograd_restatement():
             np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
 
 
+@pytest.mark.parametrize("rps", [48, 12, 1])
+def test_persistent_sources_match_the_autograd_restatement(rps):
+    """Persistent source tables (the `c`, `bc` and `bsc` shapes: 48, 12 and 1 tokens per
+    source row): the hand-written source gradients (the scatter of dm (1 - lower) into
+    each row's [E, c] table and the delta cotangent summed over each row's tokens) and
+    every model gradient equal torch autograd with the tables as leaves, in float64."""
+    cfg = mo.MoEConfig(T=48, d=16, f=8, E=6, k=2, c=4, L=2)
+    rng = np.random.default_rng(21)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    S = cfg.T // rps
+    src = [{s: rng.uniform(size=(S, cfg.E, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    srcd = [{s: rng.uniform(size=S) for s in mo.SITES} for _ in range(cfg.L)]
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.0, recon_coeff=1.5,
+                          sources=(src, srcd, rps))
+    b = mo.moe_stack_step_torch(cfg, params, x0, ci, (3, 4), p=2.0, imp_coeff=0.0, recon_coeff=1.5,
+                                sources=(src, srcd, rps))
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-10)
+    for l in range(cfg.L):
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            np.testing.assert_allclose(b["grads"][l][n], a["grads"][l][n], rtol=1e-8, atol=1e-12)
+        for s in mo.SITES:
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
+            np.testing.assert_allclose(b["d_src"][l][s], a["d_src"][l][s], rtol=1e-8, atol=1e-12)
+            np.testing.assert_allclose(b["d_src_delta"][l][s], a["d_src_delta"][l][s], rtol=1e-8, atol=1e-12)
+    # the tables were really read: a source row's gradient is nonzero only where its
+    # tokens routed, and unselected experts of a bsc row stay exactly zero
+    if rps == 1:
+        for s in mo.SITES:
+            sel = np.zeros((cfg.T, cfg.E), bool)
+            for t in range(cfg.T):
+                sel[t, a["top_idx"][0][t]] = True
+            assert np.all(a["d_src"][0][s][~sel] == 0.0)
+
+
 def test_c_restatement_matches_the_numpy_oracle():
     """The compiled fp32 C/OpenMP restatement (the CPU baseline) against the NumPy
     oracle in float64: same expert selection, losses and every gradient to fp32
