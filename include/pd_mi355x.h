@@ -385,6 +385,25 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
                             void* workspace, size_t workspace_bytes, void* stream, void** events,
                             int32_t* categories, int capacity, int* n_recorded);
 
+/* ---- the TMS toy decomposition step as one fused launch (pd/targets/tms.py:254-388) ----
+ * target hid = x W1^T, out = relu(hid W1 + b2); both sites (linear1: W1 [H,F], linear2:
+ * W1^T) decomposed with the paper-form gate on the clean input's x @ V, fp32 Threefry
+ * masks m = lower + (1 - lower) u under the site keys fold_in(split(draw_key)[0], site)
+ * (pd/core/masking.py:148-167), the delta channel under fold_in(split(draw_key)[1], site)
+ * when use_delta, routes [2, B] uint8 (NULL = every row routed); loss = recon_coeff mse(out,
+ * clean) + imp_coeff sum_sites sum_c mean_b upper^p. x [B,F], W1 [H,F], b2 [F], V1 [F,C],
+ * U1 [C,H], V2 [H,C], U2 [C,F] fp32; gates = 8 pointers (per site w_in [C,16], b_in
+ * [C,16], w_out [C,16], b_out [C]). grads fp32 (pd_tms_step_grads_size floats): dV1 |
+ * dU1 | dV2 | dU2 | site 1 gate (w_in, b_in, w_out, b_out) | site 2 gate; losses[3] =
+ * {loss, recon, imp}. Deterministic. Compiled for F = 5, H = 2, C = 20. */
+size_t pd_tms_step_workspace_size(int64_t B, int F, int H, int C);
+int pd_tms_step_grads_size(int F, int H, int C);
+int pd_tms_step(int64_t B, int F, int H, int C, const float* x, const float* W1, const float* b2, const float* V1,
+                const float* U1, const float* V2, const float* U2, const float* const* gates, uint32_t draw_k0,
+                uint32_t draw_k1, int use_delta, int layout, const uint8_t* routes, float p, float imp_coeff,
+                float recon_coeff, float* grads, float* losses, void* workspace, size_t workspace_bytes,
+                void* stream);
+
 /* ---- the decomposed Llama-style LM step (one stochastic-recon KL step, fwd + bwd) -----
  * The pre-RMSNorm transformer of pd/targets/transformer.py:1031-1140 in its
  * LlamaSimpleMLP form (pd/targets/llama_simple_mlp.py: rotate-half RoPE, causal GQA

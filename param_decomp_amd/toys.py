@@ -190,3 +190,80 @@ class ToyDecompositionStep:
         loss.backward()
         return {"loss": loss.detach(), "recon": recon.detach(), "imp": imp.detach(), "out": out.detach(),
                 "clean": clean, "g_raw": [a.detach() for a in g]}
+
+
+class TMSFusedStep:
+    """The TMS decomposition step of `ToyDecompositionStep` (same objective, draws and
+    gradients) as one fused launch plus one reduction (`pd_tms_step`): each wave owns 64
+    batch rows end to end, parameters in LDS, gradients summed over rows in a fixed order.
+    Compiled for the 5-2 target with 20 components per site; the gradients land in the
+    sites' `.grad` as views of one flat buffer."""
+
+    F, H, C = 5, 2, 20
+
+    def __init__(self, target: TMSTarget, sites, *, p: float = 1.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
+                 use_delta: bool = False, layout: int | None = None):
+        from param_decomp_amd import _lib as L
+
+        H, F = target.W1.shape
+        C = sites[0].V.shape[1]
+        if (F, H, C) != (self.F, self.H, self.C) or len(sites) != 2:
+            raise L.PDError(f"TMSFusedStep: compiled for the 5-2 target with 20 components (got {F}-{H}, C={C})")
+        self.target, self.sites = target, sites
+        self.p, self.imp_coeff, self.recon_coeff, self.use_delta = p, imp_coeff, recon_coeff, use_delta
+        self.layout = L.LAYOUT_PARTITIONABLE if layout is None else layout
+        dev = target.W1.device
+        n = L.load().pd_tms_step_grads_size(F, H, C)
+        self.flat = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.losses = torch.zeros(3, dtype=torch.float32, device=dev)
+        G = 16
+        o = 0
+        views = []
+        for shape in ((F, C), (C, H), (H, C), (C, F)):
+            views.append(self.flat[o:o + shape[0] * shape[1]].view(*shape))
+            o += shape[0] * shape[1]
+        self.gate_views = []
+        for _ in range(2):
+            gv = []
+            for shape in ((C, G), (C, G), (C, G), (C,)):
+                k = shape[0] * (shape[1] if len(shape) > 1 else 1)
+                gv.append(self.flat[o:o + k].view(*shape))
+                o += k
+            self.gate_views.append(gv)
+        self.dV = [views[0], views[2]]
+        self.dU = [views[1], views[3]]
+        self._ws = None
+        self._keep = None
+
+    def _workspace(self, B, dev):
+        from param_decomp_amd import _lib as L
+
+        nbytes = L.load().pd_tms_step_workspace_size(B, self.F, self.H, self.C)
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = L.workspace(nbytes, dev)
+        return self._ws
+
+    def step(self, x: torch.Tensor, draw_key: Key, routes=None) -> dict:
+        import ctypes
+
+        from param_decomp_amd import _lib as L
+
+        B = x.shape[0]
+        s0, s1 = self.sites
+        gates = L.host_array(ctypes.c_void_p, [L.ptr(t) for s in self.sites for t in
+                                              (s.gate.w_in, s.gate.b_in, s.gate.w_out, s.gate.b_out)])
+        rt = None
+        if routes is not None:
+            rt = torch.stack([r.to(torch.uint8) for r in routes]).contiguous()
+        self._keep = (gates, rt)
+        ws = self._workspace(B, x.device)
+        # the library derives the sites' mask / delta keys from draw_key on the host side
+        L.call("pd_tms_step", B, self.F, self.H, self.C, L.ptr(x.contiguous()), L.ptr(self.target.W1),
+               L.ptr(self.target.b2), L.ptr(s0.V), L.ptr(s0.U), L.ptr(s1.V), L.ptr(s1.U), gates, draw_key[0],
+               draw_key[1], int(self.use_delta), self.layout, None if rt is None else L.ptr(rt), self.p, self.imp_coeff,
+               self.recon_coeff, L.ptr(self.flat), L.ptr(self.losses), L.ptr(ws), ws.numel(), L.stream())
+        for i, s in enumerate(self.sites):
+            s.V.grad, s.U.grad = self.dV[i], self.dU[i]
+            for prm, g in zip(s.gate.parameters(), self.gate_views[i]):
+                prm.grad = g
+        return {"loss": self.losses[0], "recon": self.losses[1], "imp": self.losses[2]}

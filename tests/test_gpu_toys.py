@@ -78,6 +78,45 @@ def test_tms_5_2_step_matches_oracle(device, use_delta, routed):
     _compare(res, sites, want)
 
 
+@pytest.mark.parametrize("use_delta,routed,B", [(False, False, 4096), (True, False, 4096), (True, True, 4096),
+                                                (False, False, 1000)])
+def test_tms_fused_step_matches_oracle(device, use_delta, routed, B):
+    """The one-launch TMS step (pd_tms_step) against the same oracle, incl. a batch that
+    is not a multiple of the 64-row wave; then bit-identical on a second call."""
+    from param_decomp_amd import toys
+    from param_decomp_amd.routing import UniformKRouting
+
+    g = torch.Generator(device=device).manual_seed(0)
+    target, sites = toys.init_tms(5, 2, 20, device=device, generator=g)
+    with torch.no_grad():
+        target.b2.copy_(torch.randn(5, device=device, generator=g) * 0.1)
+    _vary_gates(sites, g)
+    x = toys.sparse_features(B, 5, 0.05, 0.0, device=device, generator=g)
+    key = (0, 2024)
+    routes = None
+    if routed:
+        r = UniformKRouting(tuple(s.name for s in sites), device)((7, 8), (B,))
+        routes = [r[s.name] for s in sites]
+    step = toys.TMSFusedStep(target, sites, p=1.0, imp_coeff=0.3, recon_coeff=1.0, use_delta=use_delta)
+    res = step.step(x, key, routes)
+    torch.cuda.synchronize()
+    want = to.toy_step("tms", {"W1": _np(target.W1), "b2": _np(target.b2)}, _oracle_sites(sites), _np(x), key, p=1.0,
+                       imp_coeff=0.3, recon_coeff=1.0, use_delta=use_delta,
+                       routes=None if routes is None else [r.cpu().numpy() for r in routes])
+    for k in ("loss", "recon", "imp"):
+        assert float(res[k]) == pytest.approx(want[k], rel=1e-5), k
+    for i, s in enumerate(sites):
+        _close(_np(s.V.grad), want["dV"][i], 1e-4, 1e-4, f"{s.name} dV")
+        _close(_np(s.U.grad), want["dU"][i], 1e-4, 1e-4, f"{s.name} dU")
+        for prm, w, nm in zip((s.gate.w_in, s.gate.b_in, s.gate.w_out, s.gate.b_out), want["dgate"][i],
+                              ("w_in", "b_in", "w_out", "b_out")):
+            _close(_np(prm.grad), w, 1e-4, 1e-4, f"{s.name} gate {nm}")
+    flat = step.flat.clone()
+    step.step(x, key, routes)
+    torch.cuda.synchronize()
+    assert torch.equal(step.flat, flat)
+
+
 @pytest.mark.parametrize("use_delta", [False, True])
 def test_resid_mlp_1l_step_matches_oracle(device, use_delta):
     from param_decomp_amd import toys
