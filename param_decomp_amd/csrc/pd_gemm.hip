@@ -517,9 +517,10 @@ int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out
   GemmArgs a{K, N, J, (const bf16_t*)lhsT1, J, (const bf16_t*)doutT1, J, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
              (const bf16_t*)lhsT2, (const bf16_t*)doutT2, out2};
   if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: operands of 2 GiB or more");
-  // 256x256 tiles: measured faster for both paired weight-gradient shapes
-  dim3 grid((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)cdiv(K, CfgDtlBig::BM), (unsigned)(2 * E));
-  return launch_dtl<CfgDtlBig, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
+  // 128x128 tiles, two blocks per CU: with line-aligned stages they beat 256x256 on every
+  // paired weight-gradient shape (which the 256x256 tile won with 8-aligned starts)
+  dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(K, CfgDtlRA::BM), (unsigned)(2 * E));
+  return launch_dtl<CfgDtlRA, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // namespace pd

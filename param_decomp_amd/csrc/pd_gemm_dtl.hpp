@@ -23,7 +23,9 @@
 // ends with 4 consecutive output columns of one row per 4 accumulators; the epilogue
 // writes them as one 8-byte (bf16) or 16-byte (fp32) store.
 //
-// Ragged contraction groups start at an 8-aligned k below the group's first row; k
+// Ragged contraction groups start at the 64-aligned k below the group's first row, so
+// every 128-byte piece of a K-major row a stage loads is one whole cache line (from an
+// 8-aligned start each piece straddled two lines: 20-25% slower weight gradients); k
 // outside [kmin, kend) is zeroed in the fragments of a tile's first and last stage.
 //
 // MN-major operands (stored [K][rows], rows contiguous: the B of x @ V and acts @ U, both
@@ -286,8 +288,23 @@ __device__ inline void wait_stages(int ahead) {
   }
 }
 
+// A bare s_barrier: it orders the waves but waits for none of this wave's memory
+// operations (gfx950 inserts no wait before s_barrier). It suffices where the LDS data
+// the barrier publishes arrived by buffer-to-LDS loads already waited for (vmcnt), or
+// where it only frees LDS whose reads this wave has consumed.
 __device__ inline void lds_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// A barrier after which every LDS access (ds_read / ds_write) any wave made before it has
+// completed: LDS written before it is visible to all, LDS read before it is free to
+// overwrite. This wave's LDS operations complete first (lgkmcnt = 0; the gfx9 s_waitcnt
+// fields vmcnt [3:0] + [15:14] and expcnt [6:4] stay at their maxima), then the s_barrier.
+__device__ inline void lds_write_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
@@ -543,36 +560,43 @@ __device__ inline void dtl_epilogue(const GemmArgs& p, const TileJob& t, int wm,
   }
 }
 
-// A bf16 tile written through LDS: the accumulators go to a row-major LDS image (rows
-// padded by 16 bytes, so the 32 rows one store instruction touches spread over the banks),
-// then every lane stores 16 contiguous bytes and each instruction covers whole output
-// rows. Straight from the MFMA layout a store instruction writes 16 bytes into each of 32
-// rows; through LDS the tile's 128-byte lines are written whole, which measured 13-25%
-// faster on the grouped products with bf16 outputs. The image holds BM / PASSES rows at a
-// time (the stage ring is the space); in pass q the waves whose rows fall in it write.
-// Values are rounded exactly as the register path rounds them (alpha * acc, beta == 0).
-template <class CFG>
+// A tile written through LDS: the accumulators go to a row-major LDS image (rows padded
+// by 16 bytes, so the 32 rows one write instruction touches spread over the banks), then
+// every lane stores 16 contiguous bytes and each instruction covers whole output rows.
+// Straight from the MFMA layout a store instruction writes 16 (bf16) or 32 (fp32) bytes
+// into each of 32 rows; through LDS the tile's 128-byte lines are written whole, which
+// measured 13-25% faster on the grouped products with bf16 outputs. The image holds
+// BM / PASSES rows at a time (the stage ring is the space); in pass q the waves whose
+// rows fall in it write. Values are rounded as the register path rounds them: the bf16
+// image holds round(alpha * acc) (so beta must be 0), the fp32 image alpha * acc, to
+// which the store pass adds beta * C.
+template <class CFG, int ES>
 struct StagedStore {
-  static constexpr int RSB = CFG::BN * 2 + 16;  // LDS bytes per image row
+  static constexpr int RSB = CFG::BN * ES + 16;  // LDS bytes per image row
   static constexpr int RING = CFG::NS * CFG::STAGE_BYTES;
-  static constexpr int PASSES = CFG::BM * RSB <= RING ? 1 : (CFG::BM / 2 * RSB <= RING ? 2 : 0);
+  static constexpr int PASSES = CFG::BM * RSB <= RING           ? 1
+                                : CFG::BM / 2 * RSB <= RING     ? 2
+                                : CFG::BM / 4 * RSB <= RING     ? 4
+                                                                : 0;
   static constexpr int ROWS = PASSES ? CFG::BM / PASSES : 0;
-  static_assert(PASSES == 0 || ROWS % CFG::WTM == 0, "a wave's rows fall in one pass");
+  static constexpr bool OK = PASSES > 0 && ROWS % CFG::WTM == 0;  // a wave's rows fall in one pass
 };
 
-template <class CFG>
+template <class CFG, typename TC>
 __device__ inline void dtl_epilogue_staged(const GemmArgs& p, const TileJob& t, int wm, int wn, int tid,
                                            f32x16 (&acc)[CFG::TM][CFG::TN], char* smem) {
-  typedef StagedStore<CFG> SS;
-  constexpr int CPR = CFG::BN / 8;          // 16-byte chunks per output row
+  constexpr int ES = sizeof(TC);
+  typedef StagedStore<CFG, ES> SS;
+  constexpr int EPC = 16 / ES;              // elements per 16-byte chunk
+  constexpr int CPR = CFG::BN / EPC;        // chunks per output row
   constexpr int RPP = CFG::NT / CPR;        // rows one pass of the block's stores covers
   static_assert(CFG::NT % CPR == 0 && SS::ROWS % RPP == 0, "store passes");
   const int lane = tid & 63, rr = tid / CPR, cc = tid % CPR;
-  bf16_t* C = (bf16_t*)t.C;
-  const int64_t col = t.n0 + cc * 8;
+  TC* C = (TC*)t.C;
+  const int64_t col = t.n0 + cc * EPC;
 #pragma unroll
   for (int q = 0; q < SS::PASSES; ++q) {
-    lds_barrier();  // the k loop's last reads (or the previous pass's stores) are done
+    lds_write_barrier();  // the k loop's last reads (or the previous pass's stores) are done
     const int r0 = wm * CFG::WTM - q * SS::ROWS;
     if (r0 >= 0 && r0 < SS::ROWS) {
 #pragma unroll
@@ -583,19 +607,34 @@ __device__ inline void dtl_epilogue_staged(const GemmArgs& p, const TileJob& t, 
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int c = wn * CFG::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
-            uint2 w;
-            w.x = pack_bf16x2(p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1]);
-            w.y = pack_bf16x2(p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]);
-            *(uint2*)(rowp + c * 2) = w;
+            const float v0 = p.alpha * acc[i][j][4 * g], v1 = p.alpha * acc[i][j][4 * g + 1];
+            const float v2 = p.alpha * acc[i][j][4 * g + 2], v3 = p.alpha * acc[i][j][4 * g + 3];
+            if constexpr (ES == 2) {
+              *(uint2*)(rowp + c * 2) = uint2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+            } else {
+              *(float4*)(rowp + c * 4) = float4{v0, v1, v2, v3};
+            }
           }
       }
     }
-    lds_barrier();
+    lds_write_barrier();
 #pragma unroll
     for (int r = rr; r < SS::ROWS; r += RPP) {
       const int64_t row = t.m0 + q * SS::ROWS + r;
-      const uint4 v = *(const uint4*)(smem + r * SS::RSB + cc * 16);
-      if (row < t.M && col < p.N) *(uint4*)(C + row * p.ldc + col) = v;
+      if (row >= t.M || col >= p.N) continue;
+      if constexpr (ES == 2) {
+        *(uint4*)(C + row * p.ldc + col) = *(const uint4*)(smem + r * SS::RSB + cc * 16);
+      } else {
+        float4 o = *(const float4*)(smem + r * SS::RSB + cc * 16);
+        if (p.beta != 0.f) {
+          const float4 c = *(const float4*)(C + row * p.ldc + col);
+          o.x += p.beta * c.x;
+          o.y += p.beta * c.y;
+          o.z += p.beta * c.z;
+          o.w += p.beta * c.w;
+        }
+        *(float4*)(C + row * p.ldc + col) = o;
+      }
     }
   }
 }
@@ -603,17 +642,19 @@ __device__ inline void dtl_epilogue_staged(const GemmArgs& p, const TileJob& t, 
 // The epilogue is a policy: EPI::run(p, args, tile, wm, wn, tid, acc, smem) runs after the
 // k loop with the LDS stage buffers still owned by the k loop (a policy that reuses
 // them starts with a barrier); the block's LDS is max(stages, EPI::LDS_BYTES). EpiStore
-// writes C = alpha * acc + beta * C: a bf16 C with beta == 0, 16-byte aligned rows and
-// N % 8 == 0 goes through the staged store, anything else straight from the registers.
+// writes C = alpha * acc + beta * C: with 16-byte aligned rows and N a whole number of
+// 16-byte chunks (and beta == 0 for a bf16 C) through the staged store, otherwise
+// straight from the registers.
 struct EpiStore {
   static constexpr int LDS_BYTES = 0;
   struct Args {};
   template <class CFG, typename TC>
   __device__ static void run(const GemmArgs& p, const Args&, const TileJob& t, int wm, int wn, int tid,
                              f32x16 (&acc)[CFG::TM][CFG::TN], char* smem) {
-    if constexpr (std::is_same<TC, bf16_t>::value && StagedStore<CFG>::PASSES > 0) {
-      if (p.beta == 0.f && (p.ldc & 7) == 0 && (p.N & 7) == 0 && ((uintptr_t)t.C & 15) == 0) {
-        dtl_epilogue_staged<CFG>(p, t, wm, wn, tid, acc, smem);
+    constexpr int EPC = 16 / sizeof(TC);
+    if constexpr (StagedStore<CFG, sizeof(TC)>::OK) {
+      if ((sizeof(TC) == 4 || p.beta == 0.f) && p.ldc % EPC == 0 && p.N % EPC == 0 && ((uintptr_t)t.C & 15) == 0) {
+        dtl_epilogue_staged<CFG, TC>(p, t, wm, wn, tid, acc, smem);
         return;
       }
     }
@@ -643,7 +684,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
   // every tile field is wave-uniform; say so, so the descriptors stay in scalar registers
   const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
   const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
-  const int64_t kbeg = kmin & ~(int64_t)7;
+  const int64_t kbeg = kmin & ~(int64_t)63;
   const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
   // a K-major tile starts at its first row, an MN-major one at its first column; either
   // descriptor ends at the operand's end (rows past M / N, or k-rows past K, load zeros;
@@ -729,7 +770,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
   if (!map_tile<BM, BN, MODE_DENSE, float>(p, lane, t)) return;
   const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
   const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
-  const int64_t kbeg = kmin & ~(int64_t)7;
+  const int64_t kbeg = kmin & ~(int64_t)63;
   const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
   const bool share_b = p.B2 == p.B;
   const bf16_t* abase = (const bf16_t*)uni64((int64_t)(p.A + m0 * p.lda));

@@ -209,12 +209,12 @@ struct EpiKLStats {
     mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
     mq = fmaxf(mq, __shfl_xor(mq, 32, 64));
     float* red = (float*)smem;  // [WM][2][32][3]
-    lds_barrier();              // the k loop's stage buffers are free
+    lds_write_barrier();        // the k loop's stage buffers are free
     if (lane < 32) {
       red[((wm * 2 + wn) * 32 + lane) * 3 + 0] = mp;
       red[((wm * 2 + wn) * 32 + lane) * 3 + 1] = mq;
     }
-    lds_barrier();
+    lds_write_barrier();
     const int rl = lane & 31;
     mp = fmaxf(red[((wm * 2) * 32 + rl) * 3 + 0], red[((wm * 2 + 1) * 32 + rl) * 3 + 0]);
     mq = fmaxf(red[((wm * 2) * 32 + rl) * 3 + 1], red[((wm * 2 + 1) * 32 + rl) * 3 + 1]);
@@ -237,13 +237,13 @@ struct EpiKLStats {
     sp += __shfl_xor(sp, 32, 64);
     sa += __shfl_xor(sa, 32, 64);
     sq += __shfl_xor(sq, 32, 64);
-    lds_barrier();
+    lds_write_barrier();
     if (lane < 32) {
       red[((wm * 2 + wn) * 32 + lane) * 3 + 0] = sp;
       red[((wm * 2 + wn) * 32 + lane) * 3 + 1] = sa;
       red[((wm * 2 + wn) * 32 + lane) * 3 + 2] = sq;
     }
-    lds_barrier();
+    lds_write_barrier();
     const int64_t row = t.m0 + wm * 32 + rl;
     if (wn == 0 && lane < 32 && row < t.M) {
       const float* r0 = red + ((wm * 2) * 32 + rl) * 3;
