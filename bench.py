@@ -955,8 +955,9 @@ def toy_cpu_baseline(workload, cfg, reps=5):
 
 def run_toy(args):
     """The toy decomposition step: clean forward, per-site gate MLPs and CI, Threefry
-    masks (fp32 draws), masked forward, MSE + L_p imp-min, backward through the HIP
-    kernels under torch autograd. Launch-latency bound at these sizes."""
+    masks (fp32 draws), masked forward, MSE + L_p imp-min and the backward. TMS runs as one
+    fused kernel (pd_tms_step); ResidMLP through the HIP primitives under torch autograd,
+    launch-latency bound at its sizes."""
     import torch
 
     from param_decomp_amd import hip_events, prng, toys
@@ -993,8 +994,12 @@ def run_toy(args):
            "config": {"workload": args.workload, **{k: v for k, v in cfg.items()}, "dtype": "fp32",
                       "gate_hidden": 16, "recon": "mse", "mask_draw": "threefry fp32 (partitionable)"},
            "step_flops": flops, "phases_ms": {"step": ms},
-           "roofline": dict(roofline("flop32", flops, ms, "whole step (fp32; launch-latency bound)", 1),
-                            note="the step is a few dozen small launches; its contractions are microseconds of "
+           "roofline": dict(roofline("flop32", flops, ms, "whole step" if args.workload == TMS else
+                                     "whole step (fp32; launch-latency bound)", 1),
+                            note="TMS: one fused launch (k_tms_step) plus one reduction per step, bound by the "
+                                 "CI gates' exact-erf GELUs and the Threefry draws on the vector ALUs; the FLOPs "
+                                 "counted (the reference rule) are only its tiny contractions" if args.workload == TMS
+                            else "the step is a few dozen small launches; its contractions are microseconds of "
                                  "fp32 MFMA work")}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = toy_cpu_baseline(args.workload, cfg)
