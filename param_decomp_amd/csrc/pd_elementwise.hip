@@ -91,13 +91,20 @@ __global__ void k_mask_bwd(const T* gm, int64_t n, uint32_t k0, uint32_t k1, int
 // lane keeps its component's 49 gate parameters in registers and the row loop reads
 // h coalesced across lanes.
 static constexpr int GATE_COLS = 64;
-static constexpr int GATE_ROWS = 64;  // rows per block chunk (also the bwd partial granularity)
+// Rows per block chunk (also the bwd partial granularity): 64, or fewer (down to 4) when
+// there are few components, so the grid has about 2048 blocks (C = 100 components over
+// 2048 rows: 4-row chunks instead of 64 one-wave blocks each walking 64 rows).
+static int64_t gate_rows(int64_t rows, int64_t C) {
+  const int64_t r = cdiv(rows * cdiv(C, GATE_COLS), 2048);
+  return r < 4 ? 4 : (r > 64 ? 64 : r);
+}
 
 template <typename T, bool PRECISE>
 __global__ __launch_bounds__(GATE_COLS) void k_gate_fwd(const T* __restrict__ h, int64_t rows, int64_t C,
                                                         const float* __restrict__ w_in, const float* __restrict__ b_in,
                                                         const float* __restrict__ w_out,
-                                                        const float* __restrict__ b_out, float* __restrict__ g_raw) {
+                                                        const float* __restrict__ b_out, float* __restrict__ g_raw,
+                                                        int64_t chunk_rows) {
   int64_t c = (int64_t)blockIdx.x * GATE_COLS + threadIdx.x;
   if (c >= C) return;
   float wi[16], bi[16], wo[16];
@@ -108,8 +115,8 @@ __global__ __launch_bounds__(GATE_COLS) void k_gate_fwd(const T* __restrict__ h,
     wo[j] = w_out[c * 16 + j];
   }
   float bo = b_out[c];
-  int64_t r0 = (int64_t)blockIdx.y * GATE_ROWS;
-  int64_t r1 = r0 + GATE_ROWS < rows ? r0 + GATE_ROWS : rows;
+  int64_t r0 = (int64_t)blockIdx.y * chunk_rows;
+  int64_t r1 = r0 + chunk_rows < rows ? r0 + chunk_rows : rows;
   for (int64_t r = r0; r < r1; ++r) {
     float hv = load_f<T>(h, r * C + c);
     float g = bo;
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(GATE_COLS) void k_gate_bwd(const T* __restrict__ h,
                                                         const float* __restrict__ w_in, const float* __restrict__ b_in,
                                                         const float* __restrict__ w_out,
                                                         const float* __restrict__ dg_raw, T* __restrict__ dh,
-                                                        float* __restrict__ partial) {
+                                                        float* __restrict__ partial, int64_t chunk_rows) {
   int64_t c = (int64_t)blockIdx.x * GATE_COLS + threadIdx.x;
   if (c >= C) return;
   float wi[16], bi[16], wo[16], a_wi[16], a_bi[16], a_wo[16];
@@ -136,8 +143,8 @@ __global__ __launch_bounds__(GATE_COLS) void k_gate_bwd(const T* __restrict__ h,
     a_wi[j] = a_bi[j] = a_wo[j] = 0.f;
   }
   float a_bo = 0.f;
-  int64_t r0 = (int64_t)blockIdx.y * GATE_ROWS;
-  int64_t r1 = r0 + GATE_ROWS < rows ? r0 + GATE_ROWS : rows;
+  int64_t r0 = (int64_t)blockIdx.y * chunk_rows;
+  int64_t r1 = r0 + chunk_rows < rows ? r0 + chunk_rows : rows;
   for (int64_t r = r0; r < r1; ++r) {
     float hv = load_f<T>(h, r * C + c);
     float dg = dg_raw[r * C + c];
@@ -212,15 +219,20 @@ __device__ inline float imp_dpsi(float v, const ImpParams& q) {
   return q.normalize_at_one ? (1.f + g2) * d : d;
 }
 
-static constexpr int COL_ROWS = 256;  // rows per partial chunk in column reductions
+// Rows per partial chunk in column reductions: rows / 128 within [8, 256], so short
+// batches still spread over ~128 row chunks (a thread's rows are a serial chain of loads).
+static int64_t col_rows(int64_t rows) {
+  const int64_t r = cdiv(rows, 128);
+  return r < 8 ? 8 : (r > 256 ? 256 : r);
+}
 
 template <typename T>
 __global__ void k_imp_colsum_partial(const T* __restrict__ ci, int64_t rows, int64_t C, ImpParams q,
-                                     float* __restrict__ partial) {
+                                     float* __restrict__ partial, int64_t chunk_rows) {
   int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
-  int64_t r0 = (int64_t)blockIdx.y * COL_ROWS;
-  int64_t r1 = r0 + COL_ROWS < rows ? r0 + COL_ROWS : rows;
+  int64_t r0 = (int64_t)blockIdx.y * chunk_rows;
+  int64_t r1 = r0 + chunk_rows < rows ? r0 + chunk_rows : rows;
   float s = 0.f;
   for (int64_t r = r0; r < r1; ++r) s += imp_psi(load_f<T>(ci, r * C + c), q);
   partial[(int64_t)blockIdx.y * C + c] = s;
@@ -476,23 +488,24 @@ int pd_gate_fwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const 
   if (H != 16) return fail(PD_EUNSUPPORTED, "pd_gate_fwd: gate hidden width must be 16");
   if (rows < 0 || C < 0 || !h || !g_raw) return fail(PD_EINVAL, "pd_gate_fwd: bad args");
   if (rows == 0 || C == 0) return PD_OK;
-  if (cdiv(rows, GATE_ROWS) > 65535) return fail(PD_EUNSUPPORTED, "pd_gate_fwd: too many rows");
-  dim3 grid((unsigned)cdiv(C, GATE_COLS), (unsigned)cdiv(rows, GATE_ROWS));
+  const int64_t cr = gate_rows(rows, C);
+  if (cdiv(rows, cr) > 65535) return fail(PD_EUNSUPPORTED, "pd_gate_fwd: too many rows");
+  dim3 grid((unsigned)cdiv(C, GATE_COLS), (unsigned)cdiv(rows, cr));
   hipStream_t s = (hipStream_t)stream;
   PD_DISPATCH_DTYPE(dtype, T, {
     if (precise)
       hipLaunchKernelGGL((k_gate_fwd<T, true>), grid, dim3(GATE_COLS), 0, s, (const T*)h, rows, C, w_in, b_in, w_out,
-                         b_out, g_raw);
+                         b_out, g_raw, cr);
     else
       hipLaunchKernelGGL((k_gate_fwd<T, false>), grid, dim3(GATE_COLS), 0, s, (const T*)h, rows, C, w_in, b_in,
-                         w_out, b_out, g_raw);
+                         w_out, b_out, g_raw, cr);
   });
   return check_launch("pd_gate_fwd");
 }
 
 size_t pd_gate_bwd_workspace_size(int64_t rows, int64_t C, int H) {
   (void)H;
-  return (size_t)cdiv(rows, GATE_ROWS) * 49 * (size_t)C * sizeof(float);
+  return rows > 0 && C > 0 ? (size_t)cdiv(rows, gate_rows(rows, C)) * 49 * (size_t)C * sizeof(float) : 0;
 }
 
 int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const float* w_in, const float* b_in,
@@ -503,7 +516,7 @@ int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const 
   if (rows <= 0 || C <= 0 || !h || !dg_raw || !dh) return fail(PD_EINVAL, "pd_gate_bwd: bad args");
   if (workspace_bytes < pd_gate_bwd_workspace_size(rows, C, H) || !workspace)
     return fail(PD_EWORKSPACE, "pd_gate_bwd: workspace too small");
-  int64_t chunks = cdiv(rows, GATE_ROWS);
+  const int64_t cr = gate_rows(rows, C), chunks = cdiv(rows, cr);
   if (chunks > 65535) return fail(PD_EUNSUPPORTED, "pd_gate_bwd: too many rows");
   dim3 grid((unsigned)cdiv(C, GATE_COLS), (unsigned)chunks);
   hipStream_t s = (hipStream_t)stream;
@@ -511,10 +524,10 @@ int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const 
   PD_DISPATCH_DTYPE(dtype, T, {
     if (precise)
       hipLaunchKernelGGL((k_gate_bwd<T, true>), grid, dim3(GATE_COLS), 0, s, (const T*)h, rows, C, w_in, b_in, w_out,
-                         dg_raw, (T*)dh, part);
+                         dg_raw, (T*)dh, part, cr);
     else
       hipLaunchKernelGGL((k_gate_bwd<T, false>), grid, dim3(GATE_COLS), 0, s, (const T*)h, rows, C, w_in, b_in,
-                         w_out, dg_raw, (T*)dh, part);
+                         w_out, dg_raw, (T*)dh, part, cr);
   });
   int rc = check_launch("pd_gate_bwd");
   if (rc) return rc;
@@ -524,7 +537,7 @@ int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const 
 }
 
 size_t pd_impmin_workspace_size(int64_t rows, int64_t C) {
-  return ((size_t)cdiv(rows, COL_ROWS) + 1) * (size_t)C * sizeof(float);
+  return rows > 0 && C > 0 ? ((size_t)cdiv(rows, col_rows(rows)) + 1) * (size_t)C * sizeof(float) : 0;
 }
 
 int pd_impmin(const void* ci, int dtype, int64_t rows, int64_t C, int kind, float p, float eps, float beta,
@@ -535,14 +548,14 @@ int pd_impmin(const void* ci, int dtype, int64_t rows, int64_t C, int kind, floa
   if (!workspace || workspace_bytes < pd_impmin_workspace_size(rows, C))
     return fail(PD_EWORKSPACE, "pd_impmin: workspace too small");
   ImpParams q{kind, p, eps, beta, world_size, gamma, normalize_at_one, ref_count, coeff_act, coeff_freq};
-  int64_t chunks = cdiv(rows, COL_ROWS);
+  const int64_t cr = col_rows(rows), chunks = cdiv(rows, cr);
   if (chunks > 65535) return fail(PD_EUNSUPPORTED, "pd_impmin: too many rows");
   float* part = (float*)workspace;
   float* colsum = part + chunks * C;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)cdiv(C, 256), (unsigned)chunks);
   PD_DISPATCH_DTYPE(dtype, T,
-                    hipLaunchKernelGGL(k_imp_colsum_partial<T>, grid, dim3(256), 0, s, (const T*)ci, rows, C, q, part));
+                    hipLaunchKernelGGL(k_imp_colsum_partial<T>, grid, dim3(256), 0, s, (const T*)ci, rows, C, q, part, cr));
   hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, part, chunks, C, colsum);
   hipLaunchKernelGGL(k_imp_scalar, dim3(1), dim3(1024), 0, s, colsum, rows, C, q, out);
   if (grad) {

@@ -199,49 +199,74 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
     }
 }
 
-// fp32 kernel (fp32 toy configs): 64x64 tiles, 4x4 outputs per thread, any layout;
+// fp32 GEMM on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), any operand layout;
 // blockIdx.z = batch, each operand advancing by its own stride (0 = shared).
-constexpr int FT = 64, FK = 16;
+//
+// A block computes one 32x32 output tile; its 4 waves split the contraction into 4
+// consecutive k ranges (multiples of 16), each wave streaming its own 32x16 A and 16x32 B
+// chunks through a private LDS slice (coalesced loads along whichever dimension is
+// contiguous, k-major in LDS so each MFMA operand read is one conflict-free float per
+// lane). The waves' partial tiles are added in wave order through LDS, so results are
+// deterministic and no workspace is needed. Small-output, long-contraction shapes (the
+// weight gradients of the toy targets, e.g. 1000x100 over 2048 rows) still get 4 waves
+// per 32x32 tile; large outputs get one block per tile.
+constexpr int FT = 32, FK = 16, FW = 4;
 __global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
                                                   int64_t lda, int ta, const float* __restrict__ B, int64_t ldb,
                                                   int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta,
                                                   int64_t sA, int64_t sB, int64_t sC) {
-  __shared__ float As[FK][FT + 1], Bs[FK][FT + 1];
+  __shared__ float As[FW][FK][FT], Bs[FW][FK][FT];  // [wave][k][m or n]
+  __shared__ float red[FW][FT * FT];
   A += (int64_t)blockIdx.z * sA;
   B += (int64_t)blockIdx.z * sB;
   C += (int64_t)blockIdx.z * sC;
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t m0 = (int64_t)blockIdx.y * FT, n0 = (int64_t)blockIdx.x * FT;
-  float acc[4][4] = {};
-  for (int64_t k0 = 0; k0 < K; k0 += FK) {
-    for (int e = tid; e < FK * FT; e += 256) {
-      int kk = e / FT, r = e % FT;
-      int64_t gm = m0 + r, gk = k0 + kk, gn = n0 + r;
-      As[kk][r] = (gm < M && gk < K) ? (ta ? A[gk * lda + gm] : A[gm * lda + gk]) : 0.f;
-      Bs[kk][r] = (gn < N && gk < K) ? (tb ? B[gn * ldb + gk] : B[gk * ldb + gn]) : 0.f;
+  const int64_t kq = (K + FW * FK - 1) / (FW * FK) * FK;  // each wave's k range, a multiple of FK
+  const int64_t kb = (int64_t)w * kq, ke = kb + kq < K ? kb + kq : K;
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+  // a lane's 8 loads of a chunk: along k (K-contiguous rows: row l/2, k (l%2)*8 + e) or
+  // along m / n (MN-contiguous k-rows: k l/4, column (l%4)*8 + e)
+  const int r_k = lane >> 1, c_k = (lane & 1) * 8, r_mn = lane >> 2, c_mn = (lane & 3) * 8;
+  for (int64_t k0 = kb; k0 < ke; k0 += FK) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!ta) {  // A [M, K]
+        const int64_t m = m0 + r_k, k = k0 + c_k + e;
+        As[w][c_k + e][r_k] = (m < M && k < ke) ? A[m * lda + k] : 0.f;
+      } else {  // A [K, M]
+        const int64_t k = k0 + r_mn, m = m0 + c_mn + e;
+        As[w][r_mn][c_mn + e] = (m < M && k < ke) ? A[k * lda + m] : 0.f;
+      }
+      if (tb) {  // B [N, K]
+        const int64_t n = n0 + r_k, k = k0 + c_k + e;
+        Bs[w][c_k + e][r_k] = (n < N && k < ke) ? B[n * ldb + k] : 0.f;
+      } else {  // B [K, N]
+        const int64_t k = k0 + r_mn, n = n0 + c_mn + e;
+        Bs[w][r_mn][c_mn + e] = (n < N && k < ke) ? B[k * ldb + n] : 0.f;
+      }
     }
-    __syncthreads();
+    // the slice is this wave's alone: its LDS writes and reads stay in program order
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int kk = 0; kk < FK; ++kk) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-    }
-    __syncthreads();
+    for (int kk = 0; kk < FK; kk += 2)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[w][kk + (lane >> 5)][lane & 31], Bs[w][kk + (lane >> 5)][lane & 31],
+                                                 acc, 0, 0, 0);
+    asm volatile("" ::: "memory");
   }
+  // lane holds column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4 of the tile
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int v = 0; v < 16; ++v) red[w][(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * FT + (lane & 31)] = acc[v];
+  __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int64_t r = m0 + ty * 4 + i, c = n0 + tx * 4 + j;
-      if (r < M && c < N) C[r * ldc + c] = alpha * acc[i][j] + (beta != 0.f ? beta * C[r * ldc + c] : 0.f);
-    }
+  for (int q = 0; q < FT * FT / 256; ++q) {
+    const int i = q * 256 + tid, r = i / FT, c = i % FT;
+    const float sum = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+    const int64_t gr = m0 + r, gc = n0 + c;
+    if (gr < M && gc < N) C[gr * ldc + gc] = alpha * sum + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+  }
 }
 
 __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int64_t J, int64_t width, int out_bytes,

@@ -274,6 +274,26 @@ def test_gemm_alpha_beta_and_fp32(device):
     assert_close(np64(c), 0.5 * A32 @ B32 + 2 * C32, 1e-5, 1e-6, "fp32 gemm")
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(2048, 100, 1000), (1000, 100, 2048), (100, 1000, 2048), (2048, 1000, 100),
+                                   (70, 50, 5), (33, 65, 97), (2048, 50, 1000)])
+def test_gemm_fp32_matrix_core_layouts(device, ta, tb, M, N, K):
+    """The fp32 MFMA kernel at the residual-MLP target's product shapes (its forward
+    contractions and weight gradients over 2048 rows) and ragged edges in every
+    dimension, every operand layout: fp32 accumulation-order error of a float64 product."""
+    from param_decomp_amd import ops
+
+    rng = np.random.default_rng(M * 7 + N * 3 + K + 2 * ta + tb)
+    A = f32(rng.normal(size=(K, M) if ta else (M, K)), device)
+    B = f32(rng.normal(size=(N, K) if tb else (K, N)), device)
+    out = ops.gemm(A, B, trans_a=bool(ta), trans_b=bool(tb))
+    An, Bn = np64(A), np64(B)
+    want = (An.T if ta else An) @ (Bn.T if tb else Bn)
+    assert_close(np64(out), want, 1e-5, 1e-6, f"fp32 gemm ta={ta} tb={tb} {M}x{N}x{K}")
+    again = ops.gemm(A, B, trans_a=bool(ta), trans_b=bool(tb))
+    assert torch.equal(out, again)  # fixed summation order
+
+
 # ------------------------------------------------------------------ masked linear (site_forward)
 
 
