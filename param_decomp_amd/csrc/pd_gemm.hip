@@ -202,52 +202,78 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
 // fp32 GEMM on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), any operand layout;
 // blockIdx.z = batch, each operand advancing by its own stride (0 = shared).
 //
-// A block computes one 32x32 output tile; its 4 waves split the contraction into 4
-// consecutive k ranges (multiples of 16), each wave streaming its own 32x16 A and 16x32 B
-// chunks through a private LDS slice (coalesced loads along whichever dimension is
-// contiguous, k-major in LDS so each MFMA operand read is one conflict-free float per
-// lane). The waves' partial tiles are added in wave order through LDS, so results are
-// deterministic and no workspace is needed. Small-output, long-contraction shapes (the
-// weight gradients of the toy targets, e.g. 1000x100 over 2048 rows) still get 4 waves
-// per 32x32 tile; large outputs get one block per tile.
-constexpr int FT = 32, FK = 16, FW = 4;
-__global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
+// Every wave computes a 32x32 output tile from 32x16 A and 16x32 B chunks it streams
+// through a private LDS slice: coalesced loads along whichever dimension is contiguous,
+// stored k-major so each MFMA operand read is one conflict-free float per lane; the next
+// chunk's loads are in flight (registers) while the current chunk's MFMAs run. Two block
+// forms of 4 waves:
+//   KW > 1  one 32x32 tile per block of KW waves, the contraction cut into KW consecutive
+//           k ranges (multiples of 16), the waves' partial tiles added in wave order
+//           through LDS: for small outputs over long contractions (the toy targets' weight
+//           gradients, e.g. 1000x100 over 2048 rows), which would otherwise leave most
+//           CUs idle (KW = 8 from K = 1024 on, else 4);
+//   KW = 1  a 64x64 tile per block of 4 waves, each one 32x32 quarter over the whole
+//           contraction.
+// Either way the summation order is fixed: results are deterministic, no workspace.
+constexpr int FT = 32, FK = 16;
+template <int KW>
+__global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
                                                   int64_t lda, int ta, const float* __restrict__ B, int64_t ldb,
                                                   int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta,
                                                   int64_t sA, int64_t sB, int64_t sC) {
-  __shared__ float As[FW][FK][FT], Bs[FW][FK][FT];  // [wave][k][m or n]
-  __shared__ float red[FW][FT * FT];
+  constexpr bool SPLIT = KW > 1;
+  constexpr int NWV = SPLIT ? KW : 4, NT = 64 * NWV;
+  __shared__ float As[NWV][FK][FT], Bs[NWV][FK][FT];  // [wave][k][m or n]
+  __shared__ float red[SPLIT ? KW : 1][SPLIT ? FT * FT : 1];
   A += (int64_t)blockIdx.z * sA;
   B += (int64_t)blockIdx.z * sB;
   C += (int64_t)blockIdx.z * sC;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t m0 = (int64_t)blockIdx.y * FT, n0 = (int64_t)blockIdx.x * FT;
-  const int64_t kq = (K + FW * FK - 1) / (FW * FK) * FK;  // each wave's k range, a multiple of FK
-  const int64_t kb = (int64_t)w * kq, ke = kb + kq < K ? kb + kq : K;
+  const int64_t bt = SPLIT ? FT : 2 * FT;
+  const int64_t m0 = (int64_t)blockIdx.y * bt + (SPLIT ? 0 : (w >> 1) * FT);
+  const int64_t n0 = (int64_t)blockIdx.x * bt + (SPLIT ? 0 : (w & 1) * FT);
+  int64_t kb = 0, ke = K;
+  if (SPLIT) {
+    const int64_t kq = (K + KW * FK - 1) / (KW * FK) * FK;  // each wave's k range, a multiple of FK
+    kb = (int64_t)w * kq;
+    ke = kb + kq < K ? kb + kq : K;
+  }
   f32x16 acc;
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc[v] = 0.f;
   // a lane's 8 loads of a chunk: along k (K-contiguous rows: row l/2, k (l%2)*8 + e) or
   // along m / n (MN-contiguous k-rows: k l/4, column (l%4)*8 + e)
   const int r_k = lane >> 1, c_k = (lane & 1) * 8, r_mn = lane >> 2, c_mn = (lane & 3) * 8;
-  for (int64_t k0 = kb; k0 < ke; k0 += FK) {
+  float ra[8], rb[8];
+  auto load = [&](int64_t k0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       if (!ta) {  // A [M, K]
         const int64_t m = m0 + r_k, k = k0 + c_k + e;
-        As[w][c_k + e][r_k] = (m < M && k < ke) ? A[m * lda + k] : 0.f;
+        ra[e] = (m < M && k < ke) ? A[m * lda + k] : 0.f;
       } else {  // A [K, M]
         const int64_t k = k0 + r_mn, m = m0 + c_mn + e;
-        As[w][r_mn][c_mn + e] = (m < M && k < ke) ? A[k * lda + m] : 0.f;
+        ra[e] = (m < M && k < ke) ? A[k * lda + m] : 0.f;
       }
       if (tb) {  // B [N, K]
         const int64_t n = n0 + r_k, k = k0 + c_k + e;
-        Bs[w][c_k + e][r_k] = (n < N && k < ke) ? B[n * ldb + k] : 0.f;
+        rb[e] = (n < N && k < ke) ? B[n * ldb + k] : 0.f;
       } else {  // B [K, N]
         const int64_t k = k0 + r_mn, n = n0 + c_mn + e;
-        Bs[w][r_mn][c_mn + e] = (n < N && k < ke) ? B[k * ldb + n] : 0.f;
+        rb[e] = (n < N && k < ke) ? B[k * ldb + n] : 0.f;
       }
     }
+  };
+  if (kb < ke) load(kb);
+  for (int64_t k0 = kb; k0 < ke; k0 += FK) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!ta) As[w][c_k + e][r_k] = ra[e];
+      else As[w][r_mn][c_mn + e] = ra[e];
+      if (tb) Bs[w][c_k + e][r_k] = rb[e];
+      else Bs[w][r_mn][c_mn + e] = rb[e];
+    }
+    if (k0 + FK < ke) load(k0 + FK);  // in flight during this chunk's MFMAs
     // the slice is this wave's alone: its LDS writes and reads stay in program order
     asm volatile("" ::: "memory");
 #pragma unroll
@@ -256,17 +282,45 @@ __global__ __launch_bounds__(256) void k_gemm_f32(int64_t M, int64_t N, int64_t 
                                                  acc, 0, 0, 0);
     asm volatile("" ::: "memory");
   }
-  // lane holds column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4 of the tile
+  // lane holds column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4 of its tile
+  if constexpr (SPLIT) {
 #pragma unroll
-  for (int v = 0; v < 16; ++v) red[w][(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * FT + (lane & 31)] = acc[v];
-  __syncthreads();
+    for (int v = 0; v < 16; ++v) red[w][(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * FT + (lane & 31)] = acc[v];
+    __syncthreads();
 #pragma unroll
-  for (int q = 0; q < FT * FT / 256; ++q) {
-    const int i = q * 256 + tid, r = i / FT, c = i % FT;
-    const float sum = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
-    const int64_t gr = m0 + r, gc = n0 + c;
-    if (gr < M && gc < N) C[gr * ldc + gc] = alpha * sum + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+    for (int q = 0; q < FT * FT / NT; ++q) {
+      const int i = q * NT + tid, r = i / FT, c = i % FT;
+      float sum = red[0][i];
+#pragma unroll
+      for (int x = 1; x < KW; ++x) sum += red[x][i];
+      const int64_t gr = m0 + r, gc = n0 + c;
+      if (gr < M && gc < N) C[gr * ldc + gc] = alpha * sum + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+    }
+  } else {
+    const int64_t gc = n0 + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t gr = m0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (gr < M && gc < N) C[gr * ldc + gc] = alpha * acc[v] + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+    }
   }
+}
+
+// The fp32 block form: whole-contraction 64x64 tiles once they alone give >= 512 blocks,
+// else 32x32 tiles with the contraction split over 8 (K >= 1024) or 4 waves.
+static void launch_gemm_f32(int64_t batch, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, int ta,
+                            const float* B, int64_t ldb, int tb, float* C, int64_t ldc, float alpha, float beta,
+                            int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
+  const dim3 g32((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
+  if (cdiv(M, 2 * FT) * cdiv(N, 2 * FT) * batch >= 512)
+    hipLaunchKernelGGL(k_gemm_f32<1>, dim3((unsigned)cdiv(N, 2 * FT), (unsigned)cdiv(M, 2 * FT), (unsigned)batch),
+                       dim3(256), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA, sB, sC);
+  else if (K >= 1024)
+    hipLaunchKernelGGL(k_gemm_f32<8>, g32, dim3(512), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA,
+                       sB, sC);
+  else
+    hipLaunchKernelGGL(k_gemm_f32<4>, g32, dim3(256), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA,
+                       sB, sC);
 }
 
 __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int64_t J, int64_t width, int out_bytes,
@@ -357,9 +411,8 @@ int pd_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t l
   if (cdiv(M, FT) > 65535 || cdiv(N, FT) > 65535) return fail(PD_EUNSUPPORTED, "pd_gemm: too large");
   if (dtype == PD_DTYPE_F32) {
     if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm: fp32 path writes fp32");
-    dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT));
-    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, M, N, K, (const float*)A, lda, trans_a, (const float*)B,
-                       ldb, trans_b, (float*)C, ldc, alpha, beta, (int64_t)0, (int64_t)0, (int64_t)0);
+    launch_gemm_f32(1, M, N, K, (const float*)A, lda, trans_a, (const float*)B, ldb, trans_b, (float*)C, ldc, alpha,
+                    beta, 0, 0, 0, s);
     return check_launch("pd_gemm f32");
   }
   if (dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_gemm: dtype");
@@ -390,9 +443,8 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
     return fail(PD_EUNSUPPORTED, "pd_gemm_strided_batched: too large");
   if (dtype == PD_DTYPE_F32) {
     if (c_dtype != PD_DTYPE_F32) return fail(PD_EINVAL, "pd_gemm_strided_batched: fp32 path writes fp32");
-    dim3 grid((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
-    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, M, N, K, (const float*)A, lda, trans_a, (const float*)B,
-                       ldb, trans_b, (float*)C, ldc, alpha, beta, stride_a, stride_b, stride_c);
+    launch_gemm_f32(batch, M, N, K, (const float*)A, lda, trans_a, (const float*)B, ldb, trans_b, (float*)C, ldc,
+                    alpha, beta, stride_a, stride_b, stride_c, s);
     return check_launch("pd_gemm_strided_batched f32");
   }
   if (dtype != PD_DTYPE_BF16) return fail(PD_EINVAL, "pd_gemm_strided_batched: dtype");
