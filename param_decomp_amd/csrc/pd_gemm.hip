@@ -216,10 +216,10 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_bf16(GemmArgs p) {
 //           contraction.
 // Either way the summation order is fixed: results are deterministic, no workspace.
 constexpr int FT = 32, FK = 16;
-template <int KW>
+template <int KW, bool TA, bool TB>
 __global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32(int64_t M, int64_t N, int64_t K, const float* __restrict__ A,
-                                                  int64_t lda, int ta, const float* __restrict__ B, int64_t ldb,
-                                                  int tb, float* __restrict__ C, int64_t ldc, float alpha, float beta,
+                                                  int64_t lda, const float* __restrict__ B, int64_t ldb,
+                                                  float* __restrict__ C, int64_t ldc, float alpha, float beta,
                                                   int64_t sA, int64_t sB, int64_t sC) {
   constexpr bool SPLIT = KW > 1;
   constexpr int NWV = SPLIT ? KW : 4, NT = 64 * NWV;
@@ -245,33 +245,49 @@ __global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32(int64_t M, 
   // along m / n (MN-contiguous k-rows: k l/4, column (l%4)*8 + e)
   const int r_k = lane >> 1, c_k = (lane & 1) * 8, r_mn = lane >> 2, c_mn = (lane & 3) * 8;
   float ra[8], rb[8];
+  uint32_t okm = 0;  // bit e: ra[e] in range; bit 8 + e: rb[e]
+  // out-of-range elements load the operand's first element (always valid) and are zeroed
+  // when stored to LDS: no branches, and nothing waits for the loads until the next
+  // chunk's stores, so all 16 loads are in flight during this chunk's MFMAs
   auto load = [&](int64_t k0) {
+    okm = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if (!ta) {  // A [M, K]
+      int64_t off;
+      bool ok;
+      if constexpr (!TA) {  // A [M, K]
         const int64_t m = m0 + r_k, k = k0 + c_k + e;
-        ra[e] = (m < M && k < ke) ? A[m * lda + k] : 0.f;
+        ok = m < M && k < ke;
+        off = m * lda + k;
       } else {  // A [K, M]
         const int64_t k = k0 + r_mn, m = m0 + c_mn + e;
-        ra[e] = (m < M && k < ke) ? A[k * lda + m] : 0.f;
+        ok = m < M && k < ke;
+        off = k * lda + m;
       }
-      if (tb) {  // B [N, K]
+      ra[e] = A[ok ? off : 0];
+      okm |= (uint32_t)ok << e;
+      if constexpr (TB) {  // B [N, K]
         const int64_t n = n0 + r_k, k = k0 + c_k + e;
-        rb[e] = (n < N && k < ke) ? B[n * ldb + k] : 0.f;
+        ok = n < N && k < ke;
+        off = n * ldb + k;
       } else {  // B [K, N]
         const int64_t k = k0 + r_mn, n = n0 + c_mn + e;
-        rb[e] = (n < N && k < ke) ? B[k * ldb + n] : 0.f;
+        ok = n < N && k < ke;
+        off = k * ldb + n;
       }
+      rb[e] = B[ok ? off : 0];
+      okm |= (uint32_t)ok << (8 + e);
     }
   };
   if (kb < ke) load(kb);
   for (int64_t k0 = kb; k0 < ke; k0 += FK) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if (!ta) As[w][c_k + e][r_k] = ra[e];
-      else As[w][r_mn][c_mn + e] = ra[e];
-      if (tb) Bs[w][c_k + e][r_k] = rb[e];
-      else Bs[w][r_mn][c_mn + e] = rb[e];
+      const float av = (okm >> e) & 1u ? ra[e] : 0.f, bv = (okm >> (8 + e)) & 1u ? rb[e] : 0.f;
+      if constexpr (!TA) As[w][c_k + e][r_k] = av;
+      else As[w][r_mn][c_mn + e] = av;
+      if constexpr (TB) Bs[w][c_k + e][r_k] = bv;
+      else Bs[w][r_mn][c_mn + e] = bv;
     }
     if (k0 + FK < ke) load(k0 + FK);  // in flight during this chunk's MFMAs
     // the slice is this wave's alone: its LDS writes and reads stay in program order
@@ -308,19 +324,30 @@ __global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32(int64_t M, 
 
 // The fp32 block form: whole-contraction 64x64 tiles once they alone give >= 512 blocks,
 // else 32x32 tiles with the contraction split over 8 (K >= 1024) or 4 waves.
+template <bool TA, bool TB>
+static void launch_gemm_f32_l(int64_t batch, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+                              const float* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta, int64_t sA,
+                              int64_t sB, int64_t sC, hipStream_t s) {
+  const dim3 g32((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
+  if (cdiv(M, 2 * FT) * cdiv(N, 2 * FT) * batch >= 512)
+    hipLaunchKernelGGL((k_gemm_f32<1, TA, TB>),
+                       dim3((unsigned)cdiv(N, 2 * FT), (unsigned)cdiv(M, 2 * FT), (unsigned)batch), dim3(256), 0, s, M,
+                       N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC);
+  else if (K >= 1024)
+    hipLaunchKernelGGL((k_gemm_f32<8, TA, TB>), g32, dim3(512), 0, s, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA,
+                       sB, sC);
+  else
+    hipLaunchKernelGGL((k_gemm_f32<4, TA, TB>), g32, dim3(256), 0, s, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA,
+                       sB, sC);
+}
+
 static void launch_gemm_f32(int64_t batch, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, int ta,
                             const float* B, int64_t ldb, int tb, float* C, int64_t ldc, float alpha, float beta,
                             int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
-  const dim3 g32((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
-  if (cdiv(M, 2 * FT) * cdiv(N, 2 * FT) * batch >= 512)
-    hipLaunchKernelGGL(k_gemm_f32<1>, dim3((unsigned)cdiv(N, 2 * FT), (unsigned)cdiv(M, 2 * FT), (unsigned)batch),
-                       dim3(256), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA, sB, sC);
-  else if (K >= 1024)
-    hipLaunchKernelGGL(k_gemm_f32<8>, g32, dim3(512), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA,
-                       sB, sC);
-  else
-    hipLaunchKernelGGL(k_gemm_f32<4>, g32, dim3(256), 0, s, M, N, K, A, lda, ta, B, ldb, tb, C, ldc, alpha, beta, sA,
-                       sB, sC);
+  if (ta && tb) launch_gemm_f32_l<true, true>(batch, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC, s);
+  else if (ta) launch_gemm_f32_l<true, false>(batch, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC, s);
+  else if (tb) launch_gemm_f32_l<false, true>(batch, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC, s);
+  else launch_gemm_f32_l<false, false>(batch, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC, s);
 }
 
 __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int64_t J, int64_t width, int out_bytes,
