@@ -21,11 +21,11 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
 // out_i = lhs_i [J,K] @ rhs_i[e] with rhs_i stored [E,N,K] (K-contiguous); no tail zeroing.
 int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,
                       const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype, void* stream);
-// Two ragged-contraction weight gradients in one launch: out_i[e] = lhsT_i[:, rows_e] @
-// doutT_i[:, rows_e]^T from job-contiguous [K,J] / [N,J] operands.
-int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out1, const void* lhsT2,
-                                const void* doutT2, void* out2, const int32_t* offsets, int64_t J, int E, int64_t K,
-                                int64_t N, int out_dtype, void* stream);
+// Two ragged-contraction weight gradients in one launch: out_i[e] = lhs_i[rows_e]^T @
+// dout_i[rows_e] from the row-major job-space operands lhs_i [J,K] and dout_i [J,N].
+int grouped_gemm_dw_pair(const void* lhs1, const void* dout1, void* out1, const void* lhs2, const void* dout2,
+                         void* out2, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype,
+                         void* stream);
 
 // pd_router_topk with the logits first rounded to bf16 when round_bf16 is set (the
 // reference's router product runs in the target's bf16 matmul dtype and is widened to

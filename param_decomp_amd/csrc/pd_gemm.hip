@@ -608,23 +608,22 @@ int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const voi
       dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), 2), (hipStream_t)stream);
 }
 
-int grouped_gemm_dw_kmajor_pair(const void* lhsT1, const void* doutT1, void* out1, const void* lhsT2,
-                                const void* doutT2, void* out2, const int32_t* offsets, int64_t J, int E, int64_t K,
-                                int64_t N, int out_dtype, void* stream) {
-  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhsT1 || !doutT1 || !out1 || !lhsT2 || !doutT2 || !out2 || !offsets)
-    return fail(PD_EINVAL, "grouped_gemm_dw_kmajor_pair: bad args");
-  if (!bf16_operand_ok(lhsT1, J, J) || !bf16_operand_ok(doutT1, J, J) || !bf16_operand_ok(lhsT2, J, J) ||
-      !bf16_operand_ok(doutT2, J, J))
-    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: J must be a multiple of 8 with 16B-aligned bases");
-  if (2 * (int64_t)E > 65535 || cdiv(K, CfgDtl::BM) > 65535)
-    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: size");
-  GemmArgs a{K, N, J, (const bf16_t*)lhsT1, J, (const bf16_t*)doutT1, J, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
-             (const bf16_t*)lhsT2, (const bf16_t*)doutT2, out2};
-  if (!dtl_fits(K, J, N, J)) return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_kmajor_pair: operands of 2 GiB or more");
-  // 128x128 tiles, two blocks per CU: with line-aligned stages they beat 256x256 on every
-  // paired weight-gradient shape (which the 256x256 tile won with 8-aligned starts)
+int grouped_gemm_dw_pair(const void* lhs1, const void* dout1, void* out1, const void* lhs2, const void* dout2,
+                         void* out2, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype,
+                         void* stream) {
+  if (J < 0 || E <= 0 || K <= 0 || N <= 0 || !lhs1 || !dout1 || !out1 || !lhs2 || !dout2 || !out2 || !offsets)
+    return fail(PD_EINVAL, "grouped_gemm_dw_pair: bad args");
+  if (!bf16_operand_ok(lhs1, K, K) || !bf16_operand_ok(dout1, N, N) || !bf16_operand_ok(lhs2, K, K) ||
+      !bf16_operand_ok(dout2, N, N))
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_pair: K and N must be multiples of 8 with 16B-aligned bases");
+  if (2 * (int64_t)E > 65535 || cdiv(K, CfgDtlRA::BM) > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_pair: size");
+  if (!dtl_fits_mn(J, K) || !dtl_fits_mn(J, N))
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_dw_pair: operands of 2 GiB or more");
+  // both operands MN-major (their rows are the contraction's jobs), 128x128 tiles
+  GemmArgs a{K, N, J, (const bf16_t*)lhs1, K, (const bf16_t*)dout1, N, out1, N, 1.f, 0.f, offsets, E, 0, K * N, 0,
+             (const bf16_t*)lhs2, (const bf16_t*)dout2, out2};
   dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(K, CfgDtlRA::BM), (unsigned)(2 * E));
-  return launch_dtl<CfgDtlRA, MODE_GROUPED_K>(a, out_dtype, true, grid, (hipStream_t)stream);
+  return launch_dtl<CfgDtlRA, MODE_GROUPED_K, true, true>(a, out_dtype, true, grid, (hipStream_t)stream);
 }
 
 }  // namespace pd

@@ -10,11 +10,14 @@
 // L_p imp-min over the selected upper CI, and the full backward (V/U of every site, the
 // CI preactivations, through routing weights, router softmax and the norm).
 //
-// Every grouped GEMM runs with both operands K-contiguous:
-//   forward  out = in @ W[e]      rhs = W^T copies [E, N, K] made once per step
+// Grouped GEMM operand layouts:
+//   forward  out = in @ W[e]      rhs = W^T copies [E, N, K] made once per step (K-contiguous:
+//                                  an MN-major rhs measured 6-13% slower per product)
 //   d_input  d_in = d_out @ W[e]^T rhs = W in its own layout [E, K_in, N_out]
-//   d_weight dW[e] = in^T @ d_out  both from job-contiguous copies [width, J] that the
-//                                  job-space producers write through 64x64 LDS tiles
+//   d_weight dW[e] = in^T @ d_out  both operands straight from the row-major job-space
+//                                  tensors [J, width], MN-major for the contraction over
+//                                  jobs (about 0.13 ms per step slower than K-major copies,
+//                                  which would cost ~2.4 GB of extra writes per step)
 #include <algorithm>
 #include <vector>
 
@@ -300,13 +303,12 @@ __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return 
 // Forward mask: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at the job's
 // token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16); acts =
 // bf16(h * (m - delta)) (the component coefficients m - d, pd/core/decomposed_linear.py:65-69;
-// d = 0 without the frozen channel) written as acts [J,c] and acts^T [c,J]; u stored as
-// its 7-bit integer; per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
+// d = 0 without the frozen channel) written as acts [J,c]; u stored as its 7-bit integer;
+// per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
 template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
-                                                       bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
-                                                       uint8_t* __restrict__ ubits, float* __restrict__ imp_partial) {
-  __shared__ TTile T;
+                                                       bf16_t* __restrict__ acts, uint8_t* __restrict__ ubits,
+                                                       float* __restrict__ imp_partial) {
   __shared__ float red[4];
   __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
   const int tid = threadIdx.x;
@@ -355,8 +357,6 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 #pragma unroll
       for (int e = 0; e < 4; ++e) SLv.ps[r][q4 + e] = 0.f;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
   if constexpr (PM == PM_SL0) {
     __syncthreads();
@@ -367,10 +367,9 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
     __syncthreads();
     if (tid == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
   }
-  ttile_store(T, actsT, a.J, j0, a.J, q0, a.c, tid);
 }
 
-// Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts, plus d_h^T [c,J]) and the
+// Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts) and the
 // CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
 // upper_vjp(pre, imp_scale * d upper^p), written token-major.
 // SRC: the sources are tables (MASK_SRC): u is read back from the table, and the tables'
@@ -378,9 +377,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 template <int PM, bool SRC>
 __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
-                                                       bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_hT,
-                                                       bf16_t* __restrict__ d_pre) {
-  __shared__ TTile T;
+                                                       bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_pre) {
   __shared__ typename std::conditional<SRC, Sl0Tile, NoSl0Tile>::type SG;
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
@@ -453,20 +450,17 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       dmsum += __shfl_xor(dmsum, 8, 64);
       if (j < a.J && (tid & 15) == 0) a.rowdm[j * gridDim.x + blockIdx.x] = dmsum;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
   }
-  __syncthreads();
   if constexpr (SRC) {
+    __syncthreads();
     if (a.rps > 1) sl0_tile_colsums(SG, blockIdx.y, q0, a.c, a.colsrc, tid);
   }
-  ttile_store(T, d_hT, a.J, j0, a.J, q0, a.c, tid);
 }
 
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math) and its job-contiguous copy;
-// wt NULL = the frozen arm (no weight, no copy needed). With the frozen channel (fg, fu
+// din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math); wt NULL = the frozen arm (no
+// weight). With the frozen channel (fg, fu
 // non-NULL) the site outputs first take their delta share, g = bf16(g + dg[t] * fg) and
 // u = bf16(u + du[t] * fu) for the job's token t = sort_idx[j] / k
 // (pd/targets/qwen36_moe.py:2810-2815), written back over g and u for the backward.
@@ -476,8 +470,7 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd_tile(bf16_t* __restrict__ g,
                                                          const int32_t* __restrict__ sort_idx, int64_t J, int f,
                                                          const bf16_t* __restrict__ fg, const bf16_t* __restrict__ fu,
                                                          const float* __restrict__ dg, const float* __restrict__ du,
-                                                         int k, bf16_t* __restrict__ din, bf16_t* __restrict__ dinT) {
-  __shared__ TTile T;
+                                                         int k, bf16_t* __restrict__ din) {
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
@@ -516,18 +509,11 @@ __global__ __launch_bounds__(256) void k_swiglu_fwd_tile(bf16_t* __restrict__ g,
       for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(gv[e] * sigm(gv[e]) * uv[e] * w);
       *(uint2*)(din + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     }
-    if (dinT) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) T.v[q4 + e][r] = o[e];
-    }
   }
-  if (!dinT) return;
-  __syncthreads();
-  ttile_store(T, dinT, J, j0, J, q0, f, tid);
 }
 
 // SwiGLU-fold backward on 64x64 tiles: d_g = bf16(d*u*w*silu'(g)), d_u = bf16(d*silu(g)*w)
-// with their job-contiguous copies, and the per-(job, tile) partial of
+// and the per-(job, tile) partial of
 // d_w[j] = sum_f d*silu(g)*u into d_w_part [J, tiles]. With the down site's frozen channel
 // (gd non-NULL) the cotangent of the down input is d = d_din + dd[t] * gd, gd = d_out @
 // W_down[e]^T of the job, t = sort_idx[j] / k.
@@ -536,10 +522,8 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
                                                          const float* __restrict__ wt,
                                                          const int32_t* __restrict__ sort_idx, int64_t J, int f,
                                                          const bf16_t* __restrict__ gd, const float* __restrict__ dd,
-                                                         int k, bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_gT,
-                                                         bf16_t* __restrict__ d_u, bf16_t* __restrict__ d_uT,
+                                                         int k, bf16_t* __restrict__ d_g, bf16_t* __restrict__ d_u,
                                                          float* __restrict__ d_w_part) {
-  __shared__ TTile Tg, Tu;
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
@@ -582,15 +566,7 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd_tile(const bf16_t* __restric
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
     if ((tid & 15) == 0 && j < J) d_w_part[j * gridDim.x + blockIdx.x] = part;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      Tg.v[q4 + e][r] = og[e];
-      Tu.v[q4 + e][r] = ou[e];
-    }
   }
-  __syncthreads();
-  ttile_store(Tg, d_gT, J, j0, J, q0, f, tid);
-  ttile_store(Tu, d_uT, J, j0, J, q0, f, tid);
 }
 
 // d_logits of one token in the lane-strided layout (dl[i] = expert lane + 64 i, 0 past
@@ -956,9 +932,9 @@ __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ out, int64
 }
 
 static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h, bf16_t* acts,
-                            bf16_t* actsT, uint8_t* ub, float* part) {
+                            uint8_t* ub, float* part) {
 #define PD_MF(LY, PMV) \
-  hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, actsT, ub, part)
+  hipLaunchKernelGGL((k_mask_fwd_tile<LY, PMV>), grid, dim3(256), 0, s, ma, h, acts, ub, part)
   if (ma.src) {
     if (pm == PM_SL0) PD_MF(MASK_SRC, PM_SL0);
     else if (pm == 2) PD_MF(MASK_SRC, 2);
@@ -984,9 +960,9 @@ static void launch_mask_fwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
 }
 
 static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream_t s, const bf16_t* h,
-                            const uint8_t* ub, float imp_scale, bf16_t* d_acts, bf16_t* d_hT, bf16_t* d_pre) {
+                            const uint8_t* ub, float imp_scale, bf16_t* d_acts, bf16_t* d_pre) {
 #define PD_MB(PMV, SRC) \
-  hipLaunchKernelGGL((k_mask_bwd_tile<PMV, SRC>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_hT, d_pre)
+  hipLaunchKernelGGL((k_mask_bwd_tile<PMV, SRC>), grid, dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_pre)
   if (ma.src) {
     if (pm == PM_SL0) PD_MB(PM_SL0, true);
     else if (pm == 2) PD_MB(2, true);
@@ -1029,12 +1005,12 @@ struct Arena {
 };
 
 struct LayerSave {
-  bf16_t *r, *h2, *xjT, *gout, *uout, *dinT;
+  bf16_t *r, *h2, *xj, *gout, *uout, *din;  // xj, din: the layer's job-space inputs of its products
   bf16_t *fg, *fu, *fd;  // the frozen channel's products x_jobs @ Wg/Wu[e], din @ Wd[e]
   float *rinv, *probs, *w;
   int32_t *idx, *sort_idx, *inv, *sizes, *offsets;
   bf16_t* h[3];
-  bf16_t* actsT[3];
+  bf16_t* acts[3];
   uint8_t* ub[3];
 };
 
@@ -1042,14 +1018,14 @@ struct MoEPlan {
   std::vector<LayerSave> layers;
   // weight copies [L, E, N, K] for the forward products
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xj, *acts[2], *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
   float *colsrc, *rowdm, *qjob;  // persistent sources: group column sums, job row sums, job delta cotangents
   int32_t* goff;
   float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
-  bf16_t *d_dout, *d_doutT, *d_acts[2], *d_hT[2], *d_din, *d_g, *d_gT, *d_u, *d_uT, *dxa, *dxb;
+  bf16_t *d_dout, *d_acts[2], *d_din, *d_g, *d_u, *dxa, *dxb;
   size_t imp_per_site, total;
 };
 
@@ -1071,16 +1047,16 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
     S.inv = A.take<int32_t>(J);
     S.sizes = A.take<int32_t>(D.E);
     S.offsets = A.take<int32_t>(D.E + 1);
-    S.xjT = A.take<bf16_t>(J * D.d);
+    S.xj = A.take<bf16_t>(J * D.d);
     S.gout = A.take<bf16_t>(J * D.f);
     S.uout = A.take<bf16_t>(J * D.f);
-    S.dinT = A.take<bf16_t>(J * D.f);
+    S.din = A.take<bf16_t>(J * D.f);
     S.fg = A.take<bf16_t>(J * D.f);
     S.fu = A.take<bf16_t>(J * D.f);
     S.fd = A.take<bf16_t>(J * D.d);
     for (int s = 0; s < 3; ++s) {
       S.h[s] = A.take<bf16_t>(J * D.c);
-      S.actsT[s] = A.take<bf16_t>(J * D.c);
+      S.acts[s] = A.take<bf16_t>(J * D.c);
       S.ub[s] = A.take<uint8_t>(J * D.c);
     }
   }
@@ -1097,9 +1073,6 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.rc_b = A.take<bf16_t>(T * D.d);
   P.r_final = A.take<bf16_t>(T * D.d);
   P.h2c = A.take<bf16_t>(T * D.d);
-  P.xj = A.take<bf16_t>(J * D.d);
-  P.acts[0] = A.take<bf16_t>(J * D.c);
-  P.acts[1] = A.take<bf16_t>(J * D.c);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
   P.din = A.take<bf16_t>(J * D.f);
@@ -1128,16 +1101,10 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.delta = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
-  P.d_doutT = A.take<bf16_t>(J * D.d);
-  for (int i = 0; i < 2; ++i) {
-    P.d_acts[i] = A.take<bf16_t>(J * D.c);
-    P.d_hT[i] = A.take<bf16_t>(J * D.c);
-  }
+  for (int i = 0; i < 2; ++i) P.d_acts[i] = A.take<bf16_t>(J * D.c);
   P.d_din = A.take<bf16_t>(J * D.f);
   P.d_g = A.take<bf16_t>(J * D.f);
-  P.d_gT = A.take<bf16_t>(J * D.f);
   P.d_u = A.take<bf16_t>(J * D.f);
-  P.d_uT = A.take<bf16_t>(J * D.f);
   P.dxa = A.take<bf16_t>(J * D.d);
   P.dxb = A.take<bf16_t>(J * D.d);
   P.total = A.off;
@@ -1353,9 +1320,9 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
                              pd_routed_jobs_workspace_size(J, E), stream)))
       return rc;
-    bf16_t* xjl = l == 0 ? P.xj : P.down;
+    bf16_t* xjl = l == 0 ? S.xj : P.down;
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, h2l, S.sort_idx, k, J, d, xjl,
-                       l == 0 ? S.xjT : (bf16_t*)nullptr);
+                       (bf16_t*)nullptr);
     bf16_t* gcl = l == 0 ? S.fg : P.gc;
     bf16_t* ucl = l == 0 ? S.fu : P.uc;
     if ((rc = grouped_gemm_pair(xjl, P.WgT + l * szW, gcl, xjl, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
@@ -1363,7 +1330,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, gcl, ucl, (const float*)nullptr,
                        S.sort_idx, J, f, (const bf16_t*)nullptr, (const bf16_t*)nullptr, (const float*)nullptr,
-                       (const float*)nullptr, k, P.din, (bf16_t*)nullptr);
+                       (const float*)nullptr, k, P.din);
     if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
       return rc;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
@@ -1388,10 +1355,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                         PD_DTYPE_F32, 1.f, 0.f, stream)))
         return rc;
       launch_router_pinned(P.logits, T, E, k, S.idx, S.probs, S.w, s);
-      hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, P.xj, S.xjT);
+      hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, S.h2, S.sort_idx, k, J, d, S.xj,
+                         (bf16_t*)nullptr);
     }
     set_delta(l);
-    auto mask_fwd = [&](int si, bf16_t* acts_out) {
+    auto mask_fwd = [&](int si) {
       SiteMaskArgs ma;
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       ma.sort_idx = S.sort_idx;
@@ -1406,7 +1374,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       sl0_fill(ma, S, l, si);
       src_fill(ma, l, si);
       float* part = P.imp_part + ((size_t)l * 3 + si) * P.imp_per_site;
-      launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], acts_out, S.actsT[si], S.ub[si], part);
+      launch_mask_fwd(ma, pm, tile_grid(J, c), s, S.h[si], S.acts[si], S.ub[si], part);
       if (sl0) {  // this site's frequencies, loss partials and backward slopes
         const size_t sl = (size_t)l * 3 + si;
         hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(E, c)), dim3(256), 0, s, ma.colpart, S.offsets, E, J, c,
@@ -1416,7 +1384,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     };
     // ---- gate and up sites: both products of each stage in one paired launch
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm_pair(P.xj, VT[0] + l * szV[0], S.h[0], P.xj, VT[1] + l * szV[1], S.h[1], S.offsets, J, E,
+    if ((rc = grouped_gemm_pair(S.xj, VT[0] + l * szV[0], S.h[0], S.xj, VT[1] + l * szV[1], S.h[1], S.offsets, J, E,
                                 d, c, PD_DTYPE_BF16, stream)))
       return rc;
     // frozen channel of gate and up: x_jobs @ W[e] (layer 0: the clean pass's products)
@@ -1426,31 +1394,31 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       fg = S.fg;
       fu = S.fu;
       if (l > 0 &&
-          (rc = grouped_gemm_pair(P.xj, P.WgT + l * szW, S.fg, P.xj, P.WuT + l * szW, S.fu, S.offsets, J, E, d, f,
+          (rc = grouped_gemm_pair(S.xj, P.WgT + l * szW, S.fg, S.xj, P.WuT + l * szW, S.fu, S.offsets, J, E, d, f,
                                   PD_DTYPE_BF16, stream)))
         return rc;
     }
     rec.mark(MOE_CAT_MASK_FWD);
-    mask_fwd(0, P.acts[0]);
-    mask_fwd(1, P.acts[1]);
+    mask_fwd(0);
+    mask_fwd(1);
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm_pair(P.acts[0], UT[0] + l * szU[0], S.gout, P.acts[1], UT[1] + l * szU[1], S.uout,
+    if ((rc = grouped_gemm_pair(S.acts[0], UT[0] + l * szU[0], S.gout, S.acts[1], UT[1] + l * szU[1], S.uout,
                                 S.offsets, J, E, c, f, PD_DTYPE_BF16, stream)))
       return rc;
     // ---- down site
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J, f,
-                       fg, fu, dlt[0], dlt[1], k, P.din, S.dinT);
+                       fg, fu, dlt[0], dlt[1], k, S.din);
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm(P.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
+    if ((rc = grouped_gemm(S.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
       return rc;
     if (use_delta &&
-        (rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, S.fd, PD_DTYPE_BF16, stream, false)))
+        (rc = grouped_gemm(S.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, S.fd, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_MASK_FWD);
-    mask_fwd(2, P.acts[0]);
+    mask_fwd(2);
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm(P.acts[0], UT[2] + l * szU[2], S.offsets, J, E, c, d, 1, P.down, PD_DTYPE_BF16, stream,
+    if ((rc = grouped_gemm(S.acts[2], UT[2] + l * szU[2], S.offsets, J, E, c, d, 1, P.down, PD_DTYPE_BF16, stream,
                            false)))
       return rc;
     rec.mark(MOE_CAT_COMBINE);
@@ -1481,7 +1449,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   for (int l = L - 1; l >= 0; --l) {
     LayerSave& S = P.layers[l];
     rec.mark(MOE_CAT_COMBINE);
-    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, dr, S.sort_idx, k, J, d, P.d_dout, P.d_doutT);
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, dr, S.sort_idx, k, J, d, P.d_dout,
+                       (bf16_t*)nullptr);
     SiteMaskArgs ma;
     ma.sort_idx = S.sort_idx;
     ma.J = J;
@@ -1521,8 +1490,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                            false)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads && (rc = pd_grouped_gemm_dw_kmajor(S.actsT[2], P.d_doutT, S.offsets, J, E, c, d, dUd + l * szUd,
-                                                       PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd,
+                                                PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
@@ -1531,12 +1500,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     sl0_fill(ma, S, l, 2);
     src_fill(ma, l, 2);
     src_zero(2);
-    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0], P.d_hT[0],
+    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0],
                     (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     src_grads(2, P.d_dout, S.fd, d);
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads && (rc = pd_grouped_gemm_dw_kmajor(S.dinT, P.d_hT[0], S.offsets, J, E, f, c, dVd + l * szVd,
-                                                       PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = pd_grouped_gemm_dw(S.din, P.d_acts[0], S.offsets, J, E, f, c, dVd + l * szVd,
+                                                PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm(P.d_acts[0], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
@@ -1548,8 +1517,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
-                       J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_gT, P.d_u, P.d_uT,
-                       P.d_w_part);
+                       J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_u, P.d_w_part);
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
@@ -1557,8 +1525,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
     if (want_wgrads &&
-        (rc = grouped_gemm_dw_kmajor_pair(S.actsT[0], P.d_gT, dUg + l * szUg, S.actsT[1], P.d_uT, dUu + l * szUg,
-                                          S.offsets, J, E, c, f, PD_DTYPE_F32, stream)))
+        (rc = grouped_gemm_dw_pair(S.acts[0], P.d_g, dUg + l * szUg, S.acts[1], P.d_u, dUu + l * szUg, S.offsets,
+                                   J, E, c, f, PD_DTYPE_F32, stream)))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     for (int si = 0; si < 2; ++si) {
@@ -1568,14 +1536,14 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       sl0_fill(ma, S, l, si);
       src_fill(ma, l, si);
       src_zero(si);
-      launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], P.d_hT[si],
+      launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si],
                       (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
       src_grads(si, si == 0 ? P.d_g : P.d_u, si == 0 ? S.fg : S.fu, f);
     }
     rec.mark(MOE_CAT_GEMM_DW);
     if (want_wgrads &&
-        (rc = grouped_gemm_dw_kmajor_pair(S.xjT, P.d_hT[0], dVg + l * szVg, S.xjT, P.d_hT[1], dVu + l * szVg,
-                                          S.offsets, J, E, d, c, PD_DTYPE_F32, stream)))
+        (rc = grouped_gemm_dw_pair(S.xj, P.d_acts[0], dVg + l * szVg, S.xj, P.d_acts[1], dVu + l * szVg, S.offsets,
+                                   J, E, d, c, PD_DTYPE_F32, stream)))
       return rc;
     // The stack input carries no parameter gradient: layer 0 stops at its weight
     // gradients (its gate/up input products and the token backward feed only d x0).
