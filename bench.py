@@ -172,6 +172,73 @@ def pmc_mfma_summary(csv1: str, csv2: str, command: str, n_xcd: int = 8, n_simd:
     return "\n".join(out) + "\n"
 
 
+def copy_calibration():
+    """Three device-to-device copies of 1 GiB (the plain copy kernel of known size that
+    calibrates the FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("copied", n)
+
+
+def pmc_traffic_summary(outdir: str, workloads) -> str:
+    """Calibrated HBM bytes per dispatch from `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs
+    (one counter per run) under OUTDIR: cal_<CTR> around `bench.py --copy-calibration`,
+    <workload>_<CTR> around `bench.py --workload W --steps 2 --warmup 1 --no-cpu-baseline`.
+    Each counter is scaled by what it reads for the 1 GiB copy (KiB per dispatch)."""
+    import collections
+    import csv
+
+    def load(path):
+        agg = collections.defaultdict(list)
+        for r in csv.DictReader(open(os.path.join(outdir, path, "run_counter_collection.csv"))):
+            agg[r["Kernel_Name"].split("(")[0].replace("void ", "")].append(float(r["Counter_Value"]))
+        return agg
+
+    cal = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        v = load(f"cal_{ctr}")["__amd_rocclr_copyBuffer"]
+        cal[ctr] = (1 << 20) / (sum(v) / len(v))  # KiB of the 1 GiB copy -> factor to bytes moved
+    out = ["# HBM traffic per dispatch (rocprofv3 PMC)", "",
+           "Two counter runs per workload (FETCH_SIZE, then WRITE_SIZE; one counter per run), plus the same counters",
+           "around three device-to-device copies of 1 GiB (`python3 bench.py --copy-calibration`, a plain copy",
+           "kernel of known size) to calibrate:", "",
+           f"- FETCH_SIZE reads {1 / cal['FETCH_SIZE']:.4f} GiB for the 1 GiB copy: factor **{cal['FETCH_SIZE']:.3f}** "
+           "to bytes read",
+           f"- WRITE_SIZE reads {1 / cal['WRITE_SIZE']:.4f} GiB for the 1 GiB copy: factor **{cal['WRITE_SIZE']:.3f}** "
+           "to bytes written", "", "commands (OUT = a fresh directory per run):", "", "```",
+           "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d OUT -o run --output-format csv -- python3 bench.py --copy-calibration",
+           "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d OUT -o run --output-format csv -- python3 bench.py --copy-calibration"]
+    for wl in workloads:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            out.append(f"cd /tmp && rocprofv3 --pmc {ctr} -d OUT -o run --output-format csv -- python3 bench.py "
+                       f"--workload {wl} --steps 2 --warmup 1 --no-cpu-baseline")
+    out += ["```", f"summarized with `python bench.py --pmc-traffic-summary OUTDIR {' '.join(workloads)}`", ""]
+    for wl in workloads:
+        f, w = load(f"{wl}_FETCH_SIZE"), load(f"{wl}_WRITE_SIZE")
+        out += [f"## {wl}", "",
+                "| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/dispatch (calibrated) |",
+                "|---|---|---|---|---|"]
+        rows = []
+        for k in f:
+            if k not in w or not k.startswith("pd::"):
+                continue
+            fa, wa = sum(f[k]) / len(f[k]), sum(w[k]) / len(w[k])
+            hbm = (fa * cal["FETCH_SIZE"] + wa * cal["WRITE_SIZE"]) * 1024
+            rows.append((hbm * len(f[k]), k, len(f[k]), fa, wa, hbm))
+        for _, k, n, fa, wa, hbm in sorted(rows, reverse=True)[:18]:
+            out.append(f"| `{k}` | {n} | {fa:.0f} | {wa:.0f} | {hbm:.4g} |")
+        out.append("")
+    return "\n".join(out) + "\n"
+
+
 # The kernel behind each phase, as named in profiles/hbm_traffic_pmc.md (a prefix of the
 # demangled name: the phases of one kernel template share its per-dispatch average).
 # Kernels of a timed phase (name prefixes as rocprofv3 prints them). A phase's traffic per
@@ -1161,6 +1228,13 @@ def main():
     if "--rocprof-csv-summary" in sys.argv:
         i = sys.argv.index("--rocprof-csv-summary")
         print(rocprof_csv_summary(sys.argv[i + 1], sys.argv[i + 2]))
+        return
+    if "--copy-calibration" in sys.argv:
+        copy_calibration()
+        return
+    if "--pmc-traffic-summary" in sys.argv:
+        i = sys.argv.index("--pmc-traffic-summary")
+        print(pmc_traffic_summary(sys.argv[i + 1], sys.argv[i + 2:]), end="")
         return
     if "--pmc-mfma-summary" in sys.argv:
         i = sys.argv.index("--pmc-mfma-summary")
