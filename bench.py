@@ -55,6 +55,7 @@ FAITH_MOE = "faith_qwen35moe4L"
 LLAMA = "llama4L"
 TMS = "tms5_2"
 RESID = "resid_mlp1L"
+GEMM_MOE = "gemm_qwen35moe4L"
 PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
@@ -90,6 +91,12 @@ WORKLOADS = {
     # faithfulness of the dense site, and of every expert matrix of the MoE stack (per kind:
     # 4 layers x 42 experts, each layer's experts one block-factored site)
     FAITH_DENSE: dict(groups=[dict(n=1, per=1, d_in=768, d_out=3072, C=4096)]),
+    # the MoE step's grouped products in isolation (J = 8192 x 8 jobs over 42 experts with
+    # ragged group sizes), each through the public grouped-GEMM entry points: the forward
+    # products with the rhs K-contiguous (the step's per-step copies) and as stored
+    # (MN-major), and the weight gradients from row-major (MN-major) and job-contiguous
+    # (K-major) operands
+    GEMM_MOE: dict(J=65536, E=42, d=512, f=256, c=512),
     FAITH_MOE: dict(groups=[dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
                             dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
                             dict(n=4 * 42, per=42, d_in=256, d_out=512, C=512)]),
@@ -236,6 +243,38 @@ def pmc_traffic_summary(outdir: str, workloads) -> str:
         for _, k, n, fa, wa, hbm in sorted(rows, reverse=True)[:18]:
             out.append(f"| `{k}` | {n} | {fa:.0f} | {wa:.0f} | {hbm:.4g} |")
         out.append("")
+    return "\n".join(out) + "\n"
+
+
+def pmc_l2_summary(csv_path: str, command: str, n_xcd: int = 8, n_ch: int = 16) -> str:
+    """Per-kernel L2 behaviour from one `--pmc TCC_HIT_sum TCC_MISS_sum TCC_BUSY_sum
+    TCC_EA0_RDREQ_sum GRBM_GUI_ACTIVE` run: hit rate, channel busy fraction (TCC_BUSY over
+    GPU-active cycles per XCD x 16 channels per XCD) and memory read requests."""
+    import collections
+    import csv
+
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    name = {}
+    for r in csv.DictReader(open(csv_path)):
+        dsp = int(r["Dispatch_Id"])
+        per[dsp][r["Counter_Name"]] += float(r["Counter_Value"])
+        per[dsp]["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        name[dsp] = r["Kernel_Name"].split("(")[0].replace("void ", "")
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    for dsp, v in per.items():
+        for c, x in v.items():
+            agg[name[dsp]][c] += x
+        agg[name[dsp]]["calls"] += 1
+    out = [f"command: `{command}`", "", "| kernel | calls | avg us | L2 hit % | L2 channel busy % | memory read requests / call |",
+           "|---|---|---|---|---|---|"]
+    for n, v in sorted(agg.items(), key=lambda kv: -kv[1]["ns"]):
+        if not n.startswith("pd::"):
+            continue
+        calls = int(v["calls"])
+        hm = v["TCC_HIT_sum"] + v["TCC_MISS_sum"]
+        busy = v["TCC_BUSY_sum"] / (v["GRBM_GUI_ACTIVE"] / n_xcd * n_xcd * n_ch) if v["GRBM_GUI_ACTIVE"] else 0
+        out.append(f"| `{n}` | {calls} | {v['ns'] / calls / 1e3:.1f} | {100 * v['TCC_HIT_sum'] / hm if hm else 0:.1f} | "
+                   f"{100 * busy:.0f} | {v['TCC_EA0_RDREQ_sum'] / calls:.3g} |")
     return "\n".join(out) + "\n"
 
 
@@ -827,6 +866,69 @@ def run_faith(args):
     return res
 
 
+def run_gemm_moe(args):
+    """Each grouped product of the MoE step timed alone (HIP events around the repeated
+    launches of one product); a step is one launch of every listed product."""
+    import torch
+
+    from param_decomp_amd import hip_events, ops
+
+    cfg = WORKLOADS[GEMM_MOE]
+    J, E, d, f, c = cfg["J"], cfg["E"], cfg["d"], cfg["f"], cfg["c"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    w = torch.rand(E, generator=g, device=dev) * 0.8 + 0.6
+    sizes = (w / w.sum() * J).floor().to(torch.int64)
+    sizes[-1] += J - int(sizes.sum())
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int64, device=dev), sizes.cumsum(0)]).to(torch.int32)
+
+    def rn(*shape):
+        return torch.randn(*shape, device=dev, generator=g).to(torch.bfloat16)
+
+    x, acts, din = rn(J, d), rn(J, c), rn(J, f)
+    V, U, Vd = rn(E, d, c), rn(E, c, f), rn(E, f, c)
+    Vt, Ut, Vdt = (t.transpose(1, 2).contiguous() for t in (V, U, Vd))
+    dh, dg = rn(J, c), rn(J, f)
+    xT, dhT, actsT, dgT = (t.t().contiguous() for t in (x, dh, acts, dg))
+    prods = {  # name: (launch, FLOPs)
+        "fwd_xV_K512_N512_rhsK": (lambda: ops.grouped_gemm(x, Vt, offsets, trans_rhs=True), 2 * J * d * c),
+        "fwd_xV_K512_N512_rhsMN": (lambda: ops.grouped_gemm(x, V, offsets), 2 * J * d * c),
+        "fwd_aU_K512_N256_rhsK": (lambda: ops.grouped_gemm(acts, Ut, offsets, trans_rhs=True), 2 * J * c * f),
+        "fwd_aU_K512_N256_rhsMN": (lambda: ops.grouped_gemm(acts, U, offsets), 2 * J * c * f),
+        "fwd_dinV_K256_N512_rhsK": (lambda: ops.grouped_gemm(din, Vdt, offsets, trans_rhs=True), 2 * J * f * c),
+        "fwd_dinV_K256_N512_rhsMN": (lambda: ops.grouped_gemm(din, Vd, offsets), 2 * J * f * c),
+        "dW_dV_512x512_MN": (lambda: ops.grouped_gemm_dw(x, dh, offsets, E, out_dtype=torch.float32), 2 * J * d * c),
+        "dW_dV_512x512_K": (lambda: ops.grouped_gemm_dw_kmajor(xT, dhT, offsets, E, out_dtype=torch.float32),
+                            2 * J * d * c),
+        "dW_dU_512x256_MN": (lambda: ops.grouped_gemm_dw(acts, dg, offsets, E, out_dtype=torch.float32),
+                             2 * J * c * f),
+        "dW_dU_512x256_K": (lambda: ops.grouped_gemm_dw_kmajor(actsT, dgT, offsets, E, out_dtype=torch.float32),
+                            2 * J * c * f),
+    }
+    stream = torch.cuda.current_stream().cuda_stream
+    reps = max(args.steps, 1)
+    phase, tflops = {}, {}
+    for name, (launch, fl) in prods.items():
+        for _ in range(max(args.warmup, 1)):
+            launch()
+        ev = hip_events.create(2)
+        torch.cuda.synchronize()
+        hip_events.record(ev[0], stream)
+        for _ in range(reps):
+            launch()
+        hip_events.record(ev[1], stream)
+        torch.cuda.synchronize()
+        phase[name] = hip_events.elapsed_ms(ev[0], ev[1]) / reps
+        hip_events.destroy(ev)
+        tflops[name] = fl / (phase[name] * 1e-3) / 1e12
+    dom = max(phase, key=phase.get)
+    return {"tokens": J, "ms_per_step": sum(phase.values()),
+            "config": {"workload": GEMM_MOE, **cfg, "group_sizes": "ragged, seeded (0.6 + 0.8 U) weights",
+                       "unit_of_value": "job rows per step of every listed product"},
+            "step_flops": sum(fl for _, fl in prods.values()), "phases_ms": phase, "tflops": tflops,
+            "roofline": roofline("flop", prods[dom][1], phase[dom], dom, 1)}
+
+
 # ============================================================== MoE stack
 def moe_site_flops(J, d, f, c):
     """Per-site (in_proj, out_proj) FLOPs: gate/up read width d and write f; down reads
@@ -1236,6 +1338,10 @@ def main():
         i = sys.argv.index("--pmc-traffic-summary")
         print(pmc_traffic_summary(sys.argv[i + 1], sys.argv[i + 2:]), end="")
         return
+    if "--pmc-l2-summary" in sys.argv:
+        i = sys.argv.index("--pmc-l2-summary")
+        print(pmc_l2_summary(sys.argv[i + 1], sys.argv[i + 2]), end="")
+        return
     if "--pmc-mfma-summary" in sys.argv:
         i = sys.argv.index("--pmc-mfma-summary")
         print(pmc_mfma_summary(sys.argv[i + 1], sys.argv[i + 2], sys.argv[i + 3]))
@@ -1271,6 +1377,8 @@ def main():
         res = run_ppgd_moe(args)
     elif args.workload == KL_STREAM:
         res = run_kl(args)
+    elif args.workload == GEMM_MOE:
+        res = run_gemm_moe(args)
     else:
         res = run_ci(args)
     ms = res["ms_per_step"]
@@ -1297,6 +1405,8 @@ def main():
     }
     if "launches_per_step" in res:
         out["launches_per_step"] = res["launches_per_step"]
+    if "tflops" in res:
+        out["tflops_per_product"] = res["tflops"]
     if "reference_rule_flops" in res:
         out["reference_rule_tflops"] = res["reference_rule_flops"] / (ms * 1e-3) / 1e12
     if "cpu_baseline" in res:
