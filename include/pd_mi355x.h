@@ -356,7 +356,12 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
  * values of dm (1 - lower) (unselected entries 0), and d_src_delta fp32 [L, 3, S] = the sum
  * over each row's tokens and their jobs of the delta cotangent sum_o g_out frozen -
  * sum_c dm. Every sum is in a fixed order. Workspace:
- * pd_moe_stack_sources_workspace_size. */
+ * pd_moe_stack_sources_workspace_size. reuse_clean = 1 takes the frozen clean pass (the
+ * clean routing of every layer, its final residual and the frozen weights' copies) from
+ * the workspace as the previous call on it left it: the adversary's warmup ascents and
+ * final step within one PGD step, where x0, ln, router, Wg, Wu, Wd and the dimensions are
+ * unchanged and no other call used the workspace in between (results are then identical
+ * to reuse_clean = 0). */
 size_t pd_moe_stack_sources_workspace_size(int64_t T, int d, int f, int E, int k, int c, int L,
                                            int64_t rows_per_source);
 int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
@@ -365,10 +370,10 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
                               const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
                               int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
                               int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
-                              float recon_coeff, int want_weight_grads, float* losses, float* dVg, float* dUg,
-                              float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, float* d_src,
-                              float* d_src_delta, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
-                              void* stream);
+                              float recon_coeff, int want_weight_grads, int reuse_clean, float* losses, float* dVg,
+                              float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                              float* d_src, float* d_src_delta, int32_t* top_idx_out, void* workspace,
+                              size_t workspace_bytes, void* stream);
 /* pd_moe_stack_step recording a hipEvent_t before each launch group and one at the
  * end; categories[i] labels the interval [i, i+1): 0 clean forward, 1 masked norm /
  * router / bucketing / gather, 2 grouped GEMMs fwd, 3 mask fwd, 4 SwiGLU fold,

@@ -83,7 +83,7 @@ _SIGNATURES = {
                                 _IMP_ARGS + [_c_f32] + [_c_p] * 9 + [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
     "pd_moe_stack_sources_workspace_size": (_c_sz, [_c_i64] + [_c_i32] * 6 + [_c_i64]),
     "pd_moe_stack_step_sources": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_p, _c_i32, _c_p, _c_i32, _c_i64] +
-                                  _IMP_ARGS + [_c_f32, _c_i32] + [_c_p] * 12 + [_c_sz, _c_p]),
+                                  _IMP_ARGS + [_c_f32, _c_i32, _c_i32] + [_c_p] * 12 + [_c_sz, _c_p]),
     "pd_tms_step_workspace_size": (_c_sz, [_c_i64, _c_i32, _c_i32, _c_i32]),
     "pd_tms_step_grads_size": (_c_i32, [_c_i32, _c_i32, _c_i32]),
     "pd_tms_step": (_c_i32, [_c_i64] + [_c_i32] * 3 + [_c_p] * 7 + [_c_p, _c_u32, _c_u32, _c_i32, _c_i32, _c_p] +

@@ -239,9 +239,9 @@ class MoEPPGDStep:
         if delta_adversary is not None and delta_adversary.n_warmup != adversary.n_warmup:
             raise ValueError("delta sources share the component sources' warmup count")
 
-    def _run(self, x0, w, ci_pre, final: bool):
+    def _run(self, x0, w, ci_pre, final: bool, reuse_clean: bool):
         self.step_fn.step_sources(x0, w, ci_pre, self.adv.sources, None if self.dadv is None else self.dadv.sources,
-                                  want_weight_grads=final)
+                                  want_weight_grads=final, reuse_clean=reuse_clean)
         return self.step_fn.losses[0].clone()
 
     def _ascend(self, lr, key):
@@ -255,10 +255,12 @@ class MoEPPGDStep:
         final_key = prng.fold_in(prng.fold_in(quantize_key, 0x51D), adv_index)
         warmup_losses = []
         n = self.adv.n_warmup
-        for ascent_key in prng.split(warm_key, n) if n else []:
-            warmup_losses.append(self._run(x0, w, ci_pre, final=False))
+        # the frozen clean pass depends only on x0 and the frozen weights: the first call of
+        # the step forms it, the later ones reuse it from the step's workspace
+        for i, ascent_key in enumerate(prng.split(warm_key, n) if n else []):
+            warmup_losses.append(self._run(x0, w, ci_pre, final=False, reuse_clean=i > 0))
             self._ascend(lr, ascent_key)
-        loss = self._run(x0, w, ci_pre, final=True)
+        loss = self._run(x0, w, ci_pre, final=True, reuse_clean=n > 0)
         self._ascend(lr, final_key)
         s = self.step_fn
         return PPGDStepResult(loss=loss, dV=s.dV, dU=s.dU, d_ci=s.d_ci_pre, warmup_losses=warmup_losses)

@@ -1184,7 +1184,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                          int layout, const ImpSpec& imp, float recon_coeff, float* losses, float* dVg, float* dUg,
                          float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                          void* workspace, size_t workspace_bytes, void* stream, Recorder& rec,
-                         const SrcArgs* srcs = nullptr) {
+                         const SrcArgs* srcs = nullptr, bool reuse_clean = false) {
   int rc0;
   if (T <= 0 || d <= 0 || f <= 0 || E <= 0 || E > 512 || k <= 0 || k > E || k > 64 || c <= 0 || L <= 0)
     return fail(PD_EINVAL, "pd_moe_stack_step: bad dims (E <= 512, k <= 64)");
@@ -1271,9 +1271,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
   const int64_t LE = (int64_t)L * E;
-  launch_batched_T(Wg, LE, d, f, P.WgT, s);
-  launch_batched_T(Wu, LE, d, f, P.WuT, s);
-  launch_batched_T(Wd, LE, f, d, P.WdT, s);
+  if (!reuse_clean) {  // the frozen weights' copies, else as the previous call left them
+    launch_batched_T(Wg, LE, d, f, P.WgT, s);
+    launch_batched_T(Wu, LE, d, f, P.WuT, s);
+    launch_batched_T(Wd, LE, f, d, P.WdT, s);
+  }
   launch_batched_T(Vg, LE, d, c, P.VgT, s);
   launch_batched_T(Ug, LE, c, f, P.UgT, s);
   launch_batched_T(Vu, LE, d, c, P.VuT, s);
@@ -1302,11 +1304,18 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // the masked pass's own input under the same routing, so its norm (h2, rinv), routing
   // weights, gathered x_jobs (and copy) and the gate/up products of the frozen channel
   // are written straight into the masked pass's buffers; later clean layers gather into
-  // a buffer the masked pass only uses afterwards.
-  hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
+  // a buffer the masked pass only uses afterwards. With reuse_clean the workspace still
+  // holds all of it from the previous call (nothing after the clean pass writes these
+  // buffers), and the clean final residual is the ping-pong buffer L layers end in.
   bf16_t* rcur = P.rc_a;
   bf16_t* rnext = P.rc_b;
-  for (int l = 0; l < L; ++l) {
+  if (!reuse_clean) hipMemcpyAsync(P.rc_a, x0, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
+  for (int l = 0; l < L && reuse_clean; ++l) {
+    std::swap(rcur, rnext);
+    if (top_idx_out)
+      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, P.layers[l].idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+  }
+  for (int l = 0; l < L && !reuse_clean; ++l) {
     LayerSave& S = P.layers[l];
     bf16_t* h2l = l == 0 ? S.h2 : P.h2c;
     hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
@@ -1590,10 +1599,10 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
                               const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
                               int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
                               int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
-                              float recon_coeff, int want_weight_grads, float* losses, float* dVg, float* dUg,
-                              float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, float* d_src,
-                              float* d_src_delta, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+                              float recon_coeff, int want_weight_grads, int reuse_clean, float* losses, float* dVg,
+                              float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                              float* d_src, float* d_src_delta, int32_t* top_idx_out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
   const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
   const SrcArgs sa{src, src_dtype, src_delta, delta_dtype, rows_per_source, want_weight_grads, d_src, d_src_delta};
@@ -1604,7 +1613,8 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
     return fail(PD_EWORKSPACE, "pd_moe_stack_step_sources: workspace too small");
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, 0, 0,
                        src_delta != nullptr, -1.f, PD_LAYOUT_PARTITIONABLE, imp, recon_coeff, losses, dVg, dUg, dVu,
-                       dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec, &sa);
+                       dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec, &sa,
+                       reuse_clean != 0);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,

@@ -93,11 +93,14 @@ class MoEStackStep:
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]
 
     def step_sources(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, src: torch.Tensor,
-                     src_delta: torch.Tensor | None = None, *, want_weight_grads: bool = True):
+                     src_delta: torch.Tensor | None = None, *, want_weight_grads: bool = True,
+                     reuse_clean: bool = False):
         """The step with persistent source tables in place of the draws: src [L, 3, S, E, c]
         and src_delta [L, 3, S] (float32, bfloat16 or uint16 storage; None = no delta
         channel). Fills `d_src`, `d_src_delta` (and the model gradients when
-        `want_weight_grads`)."""
+        `want_weight_grads`). `reuse_clean` takes the frozen clean pass from this object's
+        workspace as the previous call left it: only for repeated calls on the same x0 and
+        frozen weights (ln, router, Wg, Wu, Wd) with no other step on this object between."""
         if self.rows_per_source is None:
             raise L.PDError("MoEStackStep: construct with rows_per_source for source tables")
         T, d, f, E, k, c, Ln = self.dims
@@ -111,7 +114,8 @@ class MoEStackStep:
                L.ptr(w.Ud), L.ptr(ci_pre), L.ptr(src), L.dtype_code(src.dtype),
                None if src_delta is None else L.ptr(src_delta),
                L.F32 if src_delta is None else L.dtype_code(src_delta.dtype), self.rows_per_source,
-               *self.imp_min.c_args(), self.recon_coeff, int(g), L.ptr(self.losses), P(self.dV["gate"]),
+               *self.imp_min.c_args(), self.recon_coeff, int(g), int(reuse_clean), L.ptr(self.losses),
+               P(self.dV["gate"]),
                P(self.dU["gate"]), P(self.dV["up"]), P(self.dU["up"]), P(self.dV["down"]), P(self.dU["down"]),
                L.ptr(self.d_ci_pre), L.ptr(self.d_src), L.ptr(self.d_src_delta), L.ptr(self.top_idx),
                L.ptr(self.workspace), self.workspace.numel(), L.stream())

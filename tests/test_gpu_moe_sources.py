@@ -64,11 +64,20 @@ def test_moe_step_with_source_tables_matches_oracle(device, rps, dtype, with_del
             if with_delta:
                 _close(d_srcd[l, si], ref["d_src_delta"][l][s], 2e-2, 1e-2, f"d_src_delta[{l}][{s}]")
     # the warmup form: no weight gradients, the same source gradients bit for bit
+    first = {k: v.clone() for k, v in (("losses", step.losses), ("dVd", step.dV["down"]), ("dUg", step.dU["gate"]),
+                                        ("dci", step.d_ci_pre))}
     step.step_sources(x0_t, w, ci_t, t_src, t_d, want_weight_grads=False)
     torch.cuda.synchronize()
     assert np.array_equal(step.d_src.cpu().numpy(), d_src)
     if with_delta:
         assert np.array_equal(step.d_src_delta.cpu().numpy(), d_srcd)
+    # the clean pass taken from the workspace (same x0 and frozen weights): identical
+    step.step_sources(x0_t, w, ci_t, t_src, t_d, reuse_clean=True)
+    torch.cuda.synchronize()
+    assert torch.equal(step.losses, first["losses"]) and torch.equal(step.d_ci_pre, first["dci"])
+    assert torch.equal(step.dV["down"], first["dVd"]) and torch.equal(step.dU["gate"], first["dUg"])
+    assert np.array_equal(step.d_src.cpu().numpy(), d_src)
+    assert np.array_equal(step.top_idx.cpu().numpy(), got_idx)
 
 
 def test_moe_persistent_pgd_step(device):
