@@ -13,9 +13,13 @@ Pinning (what checks each function besides a retyped formula):
 - `threefry` key chain, original layout: the published JAX documentation value of
   `split(PRNGKey(0))`.
 - `threefry` key chain, partitionable layout: `split(k)[i] == fold_in(k, i)` and the
-  Random123 vector at key (0,0), counter (0,0). The bits→uniform conversion is restated
-  from JAX's published `_uniform`; no JAX is importable here, so the uniform draw itself
-  is "parity unpinned" against JAX beyond those checks.
+  Random123 vector at key (0,0), counter (0,0).
+- `threefry.uniform`, fp32 and partitionable: the reference's stored fp32
+  `jax.random.uniform` draws under `split(PRNGKey(3), 9)`
+  (`param_decomp/param_decomp/tests/targets/stacked_parity/gen_stacked_fixtures.py:102`),
+  bit for bit. The bf16 conversion (8 bits drawn, top 7 kept) is restated from JAX's
+  published `_uniform`; no JAX is importable here and no stored bf16 draw exists, so the
+  bf16 draw is "parity unpinned" against JAX beyond the range and grid checks.
 - `moe_oracle`: finite differences of its hand-written backward and the every-expert
   dense spelling of a routed layer.
 - squashing VJPs: the reference's 10 known-answer cotangents.

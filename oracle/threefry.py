@@ -133,7 +133,11 @@ def uniform_bits_to_float(bits: np.ndarray, dtype: str) -> np.ndarray:
 
 
 def uniform(key: tuple[int, int], shape, dtype: str = "float32", *, partitionable: bool = True) -> np.ndarray:
-    """`jax.random.uniform(key, shape, dtype)` on [0, 1), as exact float64 values."""
+    """`jax.random.uniform(key, shape, dtype)` on [0, 1), as exact float64 values.
+
+    The fp32 partitionable draw equals the reference's stored JAX draws
+    (`tests/targets/stacked_parity/stacked_fixtures.npz`, `src::*`) bit for bit; the
+    bf16 draw is parity unpinned against JAX (no stored bf16 draw exists)."""
     nbits = {"float32": 32, "bfloat16": 8}[dtype]
     return uniform_bits_to_float(random_bits(key, nbits, shape, partitionable=partitionable), dtype)
 

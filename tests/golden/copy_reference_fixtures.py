@@ -11,6 +11,11 @@ build container, where the reference is mounted read-only at /root/reference:
 - simple_mlp_tiny_fixture.npz:
   param_decomp/param_decomp/tests/targets/simple_mlp_equivalence/tiny_fixture.npz
   (a 3-layer LlamaSimpleMLP state dict, token ids and the torch fp32 logits).
+- stacked_sources.npz: the `src::*` arrays of
+  param_decomp/param_decomp/tests/targets/stacked_parity/stacked_fixtures.npz (the
+  persistent sources its generator drew with jax.random from PRNGKey(3): one fp32 uniform
+  draw of [1, 16, 9] per site under split(PRNGKey(3), 9), site order as stored), the only
+  arrays of that file the tests use.
 """
 
 import hashlib
@@ -26,12 +31,26 @@ FILES = [
 ]
 
 
+SUBSETS = [  # (reference file, destination, key prefix kept)
+    ("stacked_parity/stacked_fixtures.npz", "stacked_sources.npz", "src::"),
+]
+
+
 def main() -> None:
+    import numpy as np
+
     lines = []
     for src, dst in FILES:
         shutil.copyfile(os.path.join(REF, src), os.path.join(HERE, dst))
         digest = hashlib.sha256(open(os.path.join(HERE, dst), "rb").read()).hexdigest()
         lines.append(f"{dst}  sha256={digest}  from param_decomp/param_decomp/tests/targets/{src}")
+    for src, dst, prefix in SUBSETS:
+        z = np.load(os.path.join(REF, src), allow_pickle=False)
+        keep = {k: z[k] for k in z.keys() if k.startswith(prefix)}
+        np.savez(os.path.join(HERE, dst), **keep)
+        digest = hashlib.sha256(open(os.path.join(REF, src), "rb").read()).hexdigest()
+        lines.append(f"{dst}  arrays {prefix}* ({len(keep)}) of param_decomp/param_decomp/tests/targets/{src} "
+                     f"(sha256={digest})")
     with open(os.path.join(HERE, "MANIFEST.txt"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))

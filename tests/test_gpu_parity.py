@@ -58,6 +58,23 @@ def test_uniform_bit_exact(device, draw, layout, n):
     np.testing.assert_array_equal(got.cpu().numpy().astype(np.float64), want)
 
 
+def test_uniform_reproduces_reference_stored_jax_draws(device):
+    """pd_uniform (fp32 draw, partitionable layout) reproduces the reference's stored
+    fp32 `jax.random.uniform` sources under `split(PRNGKey(3), 9)`
+    (`tests/targets/stacked_parity/gen_stacked_fixtures.py:102`), bit for bit."""
+    import os
+
+    from param_decomp_amd import ops, prng
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "stacked_sources.npz"))
+    names = list(z.keys())
+    keys = prng.split(prng.PRNGKey(3), len(names), partitionable=True)
+    for key, name in zip(keys, names):
+        want = z[name]
+        got = ops.uniform(key, want.shape, torch.float32, device).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
+
+
 def test_prng_host_matches_oracle():
     from param_decomp_amd import prng
 

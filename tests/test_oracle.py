@@ -46,6 +46,24 @@ def test_split_partitionable_layout():
     assert got == [(1797259609, 2579123966), (928981903, 3453687069)]
 
 
+def test_fp32_uniform_matches_reference_stored_jax_draws():
+    """The reference's stored PPGD sources are fp32 `jax.random.uniform` draws, one per
+    site, under `split(PRNGKey(3), 9)` in site order
+    (`tests/targets/stacked_parity/gen_stacked_fixtures.py:102`, `core/adversary.py:283-303`):
+    they pin the partitionable split, the per-element counter layout and the fp32
+    bits->[0,1) map bit for bit."""
+    import os
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "stacked_sources.npz"))
+    names = list(z.keys())
+    assert len(names) == 9 and all(n.startswith("src::") for n in names)
+    keys = tf.split(tf.prng_key(3), len(names), partitionable=True)
+    for key, name in zip(keys, names):
+        want = z[name]
+        got = tf.uniform(key, want.shape, "float32", partitionable=True).astype(np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
+
+
 def test_partitionable_split_is_foldlike():
     key = tf.fold_in(tf.prng_key(7), 3)
     subs = tf.split(key, 5, partitionable=True)
