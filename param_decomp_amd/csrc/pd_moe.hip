@@ -19,6 +19,8 @@
 //                                  jobs (about 0.13 ms per step slower than K-major copies,
 //                                  which would cost ~2.4 GB of extra writes per step)
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "pd_common.hpp"
@@ -1018,10 +1020,10 @@ struct MoEPlan {
   std::vector<LayerSave> layers;
   // weight copies [L, E, N, K] for the forward products
   bf16_t *WgT, *WuT, *WdT, *VgT, *UgT, *VuT, *UuT, *VdT, *UdT;
-  bf16_t *rc_a, *rc_b, *r_final, *h2c, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
+  bf16_t *rc_a, *rc_b, *r_final, *h2c, *xjc, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
   float *colsrc, *rowdm, *qjob;  // persistent sources: group column sums, job row sums, job delta cotangents
   int32_t* goff;
-  float *logits, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
+  float *logits, *logitsc, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
@@ -1073,6 +1075,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.rc_b = A.take<bf16_t>(T * D.d);
   P.r_final = A.take<bf16_t>(T * D.d);
   P.h2c = A.take<bf16_t>(T * D.d);
+  P.xjc = A.take<bf16_t>(J * D.d);
   P.gc = A.take<bf16_t>(J * D.f);
   P.uc = A.take<bf16_t>(J * D.f);
   P.din = A.take<bf16_t>(J * D.f);
@@ -1081,6 +1084,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.dr_a = A.take<bf16_t>(T * D.d);
   P.dr_b = A.take<bf16_t>(T * D.d);
   P.logits = A.take<float>(T * D.E);
+  P.logitsc = A.take<float>(T * D.E);
   P.probsc = A.take<float>(T * D.E);
   P.wc = A.take<float>(T * D.k);
   P.rec_part = A.take<float>(REC_BLOCKS);
@@ -1177,6 +1181,45 @@ struct SrcArgs {
   float* d_src_delta; // fp32 [L, 3, S]
 };
 
+// Clean layers 1.. run on a second stream (default priority, like every stream here),
+// concurrently with the masked forward: the two chains are independent until masked layer
+// l reads clean layer l's routing, and the matrix-core phases of one overlap the VALU-bound
+// mask passes of the other. One such stream and its events (one per layer) per device,
+// created on first use with that device current and kept until the process ends. Calls that overlap
+// on one device share them (and a workspace) and race, as any two calls on one workspace do.
+struct CleanStream {
+  hipStream_t st = nullptr;
+  hipEvent_t start = nullptr, fork = nullptr, copies = nullptr;
+  std::vector<hipEvent_t> layer;  // layer[l]: clean layer l is complete
+};
+constexpr int MOE_MAX_DEVICES = 64;
+static std::mutex g_clean_mu;
+static CleanStream g_clean[MOE_MAX_DEVICES];
+
+static int clean_stream(int L, CleanStream& out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MOE_MAX_DEVICES)
+    return fail(PD_ELAUNCH, "pd_moe_stack_step: no current HIP device in range");
+  std::lock_guard<std::mutex> lock(g_clean_mu);
+  CleanStream& c = g_clean[dev];
+  hipError_t e = hipSuccess;
+  if (!c.st) {
+    e = hipStreamCreateWithFlags(&c.st, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.start, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.copies, hipEventDisableTiming);
+    if (e != hipSuccess) c.st = nullptr;
+  }
+  while (e == hipSuccess && (int)c.layer.size() < L) {
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) c.layer.push_back(ev);
+  }
+  if (e != hipSuccess) return fail(PD_ELAUNCH, std::string("pd_moe_stack_step: clean-pass stream: ") + hipGetErrorString(e));
+  out = c;
+  return PD_OK;
+}
+
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
@@ -1271,17 +1314,29 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
   const int64_t LE = (int64_t)L * E;
+  // The frozen weights' copies and clean layer 0 run on this stream (masked layer 0 needs
+  // all of it). With L > 1 the second stream copies the components' weights meanwhile,
+  // then runs clean layers 1.. once layer 0 is done.
+  CleanStream cs;
+  const bool side = !reuse_clean && L > 1;
+  if (side) {
+    if ((rc0 = clean_stream(L, cs))) return rc0;
+    hipEventRecord(cs.start, s);
+    hipStreamWaitEvent(cs.st, cs.start, 0);
+  }
   if (!reuse_clean) {  // the frozen weights' copies, else as the previous call left them
     launch_batched_T(Wg, LE, d, f, P.WgT, s);
     launch_batched_T(Wu, LE, d, f, P.WuT, s);
     launch_batched_T(Wd, LE, f, d, P.WdT, s);
   }
-  launch_batched_T(Vg, LE, d, c, P.VgT, s);
-  launch_batched_T(Ug, LE, c, f, P.UgT, s);
-  launch_batched_T(Vu, LE, d, c, P.VuT, s);
-  launch_batched_T(Uu, LE, c, f, P.UuT, s);
-  launch_batched_T(Vd, LE, f, c, P.VdT, s);
-  launch_batched_T(Ud, LE, c, d, P.UdT, s);
+  const hipStream_t scp = side ? cs.st : s;
+  launch_batched_T(Vg, LE, d, c, P.VgT, scp);
+  launch_batched_T(Ug, LE, c, f, P.UgT, scp);
+  launch_batched_T(Vu, LE, d, c, P.VuT, scp);
+  launch_batched_T(Uu, LE, c, f, P.UuT, scp);
+  launch_batched_T(Vd, LE, f, c, P.VdT, scp);
+  launch_batched_T(Ud, LE, c, d, P.UdT, scp);
+  if (side) hipEventRecord(cs.copies, cs.st);
   const bf16_t* VT[3] = {P.VgT, P.VuT, P.VdT};
   const bf16_t* UT[3] = {P.UgT, P.UuT, P.UdT};
   const size_t szV[3] = {szVg, szVg, szVd};
@@ -1317,44 +1372,52 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   }
   for (int l = 0; l < L && !reuse_clean; ++l) {
     LayerSave& S = P.layers[l];
+    if (l == 1) {
+      hipEventRecord(cs.fork, s);
+      hipStreamWaitEvent(cs.st, cs.fork, 0);
+    }
+    hipStream_t sc = l == 0 ? s : cs.st;
     bf16_t* h2l = l == 0 ? S.h2 : P.h2c;
-    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, T, d, ln + (size_t)l * d, 1e-6f,
+    hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, sc, rcur, T, d, ln + (size_t)l * d, 1e-6f,
                        h2l, l == 0 ? S.rinv : (float*)nullptr);
-    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, h2l, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logits, E,
-                      PD_DTYPE_F32, 1.f, 0.f, stream)))
+    if ((rc = pd_gemm(PD_DTYPE_BF16, T, E, d, h2l, d, 0, bf(router, (size_t)l * E * d), d, 1, P.logitsc, E,
+                      PD_DTYPE_F32, 1.f, 0.f, sc)))
       return rc;
-    if ((rc = router_topk(P.logits, T, E, k, true, P.probsc, S.idx, P.wc, stream))) return rc;
+    if ((rc = router_topk(P.logitsc, T, E, k, true, P.probsc, S.idx, P.wc, sc))) return rc;
     if (l == 0)
-      launch_router_pinned(P.logits, T, E, k, S.idx, S.probs, S.w, s);
+      launch_router_pinned(P.logitsc, T, E, k, S.idx, S.probs, S.w, sc);
     if ((rc = pd_routed_jobs(S.idx, T, k, E, S.sort_idx, S.inv, S.sizes, S.offsets, P.sort_ws,
-                             pd_routed_jobs_workspace_size(J, E), stream)))
+                             pd_routed_jobs_workspace_size(J, E), sc)))
       return rc;
-    bf16_t* xjl = l == 0 ? S.xj : P.down;
-    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, h2l, S.sort_idx, k, J, d, xjl,
+    bf16_t* xjl = l == 0 ? S.xj : P.xjc;
+    hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, sc, h2l, S.sort_idx, k, J, d, xjl,
                        (bf16_t*)nullptr);
     bf16_t* gcl = l == 0 ? S.fg : P.gc;
     bf16_t* ucl = l == 0 ? S.fu : P.uc;
     if ((rc = grouped_gemm_pair(xjl, P.WgT + l * szW, gcl, xjl, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
-                                PD_DTYPE_BF16, stream)))
+                                PD_DTYPE_BF16, sc)))
       return rc;
-    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, gcl, ucl, (const float*)nullptr,
+    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, sc, gcl, ucl, (const float*)nullptr,
                        S.sort_idx, J, f, (const bf16_t*)nullptr, (const bf16_t*)nullptr, (const float*)nullptr,
                        (const float*)nullptr, k, P.din);
-    if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, stream, false)))
+    if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, sc, false)))
       return rc;
-    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, rcur, P.downc, S.inv, P.wc, T, k, d,
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, sc, rcur, P.downc, S.inv, P.wc, T, k, d,
                        (const bf16_t*)nullptr, (const float*)nullptr, rnext);
     std::swap(rcur, rnext);
     if (top_idx_out)
-      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, s);
+      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, sc);
+    if (l > 0) hipEventRecord(cs.layer[l], sc);
   }
   bf16_t* rc_final = rcur;
   if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
 
   // ================= masked forward
+  if (side) hipStreamWaitEvent(s, cs.copies, 0);
   const bf16_t* r_in = (const bf16_t*)x0;
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
+    if (side && l > 0) hipStreamWaitEvent(s, cs.layer[l], 0);  // clean layer l's routing
     rec.mark(MOE_CAT_NORM_ROUTE);
     if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
     if (l > 0) {  // layer 0's were formed by the clean pass
@@ -1437,7 +1500,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
-  // ================= loss
+  // ================= loss (and everything after it) after the whole clean pass
+  if (side) hipStreamWaitEvent(s, cs.layer[L - 1], 0);
   const int64_t nres = T * d;
   hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
                      recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
