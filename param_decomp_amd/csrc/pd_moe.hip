@@ -1027,7 +1027,7 @@ struct MoEPlan {
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
-  bf16_t *d_dout, *d_acts[2], *d_din, *d_g, *d_u, *dxa, *dxb;
+  bf16_t *d_dout, *d_acts[3], *d_din, *d_g, *d_u, *dxa, *dxb;  // d_acts[si]: site si
   size_t imp_per_site, total;
 };
 
@@ -1105,7 +1105,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.delta = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
-  for (int i = 0; i < 2; ++i) P.d_acts[i] = A.take<bf16_t>(J * D.c);
+  for (int i = 0; i < 3; ++i) P.d_acts[i] = A.take<bf16_t>(J * D.c);
   P.d_din = A.take<bf16_t>(J * D.f);
   P.d_g = A.take<bf16_t>(J * D.f);
   P.d_u = A.take<bf16_t>(J * D.f);
@@ -1191,6 +1191,7 @@ struct CleanStream {
   hipStream_t st = nullptr;
   hipEvent_t start = nullptr, fork = nullptr, copies = nullptr;
   std::vector<hipEvent_t> layer;  // layer[l]: clean layer l is complete
+  hipEvent_t wg_in[4] = {}, wg_out[4] = {};  // backward: a weight gradient's inputs ready / product done
 };
 constexpr int MOE_MAX_DEVICES = 64;
 static std::mutex g_clean_mu;
@@ -1208,6 +1209,10 @@ static int clean_stream(int L, CleanStream& out) {
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c.start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c.fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c.copies, hipEventDisableTiming);
+    for (int i = 0; i < 4 && e == hipSuccess; ++i) {
+      e = hipEventCreateWithFlags(&c.wg_in[i], hipEventDisableTiming);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&c.wg_out[i], hipEventDisableTiming);
+    }
     if (e != hipSuccess) c.st = nullptr;
   }
   while (e == hipSuccess && (int)c.layer.size() < L) {
@@ -1319,8 +1324,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // then runs clean layers 1.. once layer 0 is done.
   CleanStream cs;
   const bool side = !reuse_clean && L > 1;
+  if ((side || want_wgrads) && (rc0 = clean_stream(L, cs))) return rc0;
   if (side) {
-    if ((rc0 = clean_stream(L, cs))) return rc0;
     hipEventRecord(cs.start, s);
     hipStreamWaitEvent(cs.st, cs.start, 0);
   }
@@ -1519,8 +1524,28 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   bf16_t* dr_next = P.dr_b;
   const float imp_scale = imp.coeff / (float)T;
   const int n_wpart = (int)cdiv(f, TILE);
+  // Weight gradients run on the second stream: each product starts once its inputs are
+  // ready on this stream (event wg_in[i]), and this stream waits for it (wg_out[i]) before
+  // it next overwrites one of those inputs, and before it returns. Nothing on this stream
+  // reads a weight gradient.
+  bool wpend[4] = {false, false, false, false};
+  auto wgrad = [&](int i, auto&& product) -> int {
+    if (!cs.st) return product((void*)s);
+    hipEventRecord(cs.wg_in[i], s);
+    hipStreamWaitEvent(cs.st, cs.wg_in[i], 0);
+    const int r = product((void*)cs.st);
+    hipEventRecord(cs.wg_out[i], cs.st);
+    wpend[i] = true;
+    return r;
+  };
+  auto wjoin = [&](int i) {
+    if (wpend[i]) hipStreamWaitEvent(s, cs.wg_out[i], 0);
+    wpend[i] = false;
+  };
   for (int l = L - 1; l >= 0; --l) {
     LayerSave& S = P.layers[l];
+    wjoin(0);  // the down site's dU reads d_dout, its dV d_acts[2]
+    wjoin(1);
     rec.mark(MOE_CAT_COMBINE);
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, s, dr, S.sort_idx, k, J, d, P.d_dout,
                        (bf16_t*)nullptr);
@@ -1559,12 +1584,14 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     };
     // ---- down site
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[0], PD_DTYPE_BF16, stream,
+    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[2], PD_DTYPE_BF16, stream,
                            false)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads && (rc = pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd,
-                                                PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = wgrad(0, [&](void* st) {
+                          return pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd,
+                                                    PD_DTYPE_F32, st);
+                        })))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
@@ -1573,15 +1600,17 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     sl0_fill(ma, S, l, 2);
     src_fill(ma, l, 2);
     src_zero(2);
-    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[0],
+    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[2],
                     (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
     src_grads(2, P.d_dout, S.fd, d);
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads && (rc = pd_grouped_gemm_dw(S.din, P.d_acts[0], S.offsets, J, E, f, c, dVd + l * szVd,
-                                                PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = wgrad(1, [&](void* st) {
+                          return pd_grouped_gemm_dw(S.din, P.d_acts[2], S.offsets, J, E, f, c, dVd + l * szVd,
+                                                    PD_DTYPE_F32, st);
+                        })))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_acts[0], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
+    if ((rc = grouped_gemm(P.d_acts[2], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
                            false)))
       return rc;
     // frozen channel of down: d_out @ W_down[e]^T, scaled by the token's delta in the fold
@@ -1589,17 +1618,20 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
         (rc = grouped_gemm(P.d_dout, bf(Wd, l * szW), S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_SWIGLU);
+    wjoin(2);  // dU of gate / up reads d_g, d_u
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
                        J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_u, P.d_w_part);
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_GEMM_DX);
+    wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
     if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
                                 J, E, f, c, PD_DTYPE_BF16, stream)))
       return rc;
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads &&
-        (rc = grouped_gemm_dw_pair(S.acts[0], P.d_g, dUg + l * szUg, S.acts[1], P.d_u, dUu + l * szUg, S.offsets,
-                                   J, E, c, f, PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = wgrad(2, [&](void* st) {
+                          return grouped_gemm_dw_pair(S.acts[0], P.d_g, dUg + l * szUg, S.acts[1], P.d_u,
+                                                      dUu + l * szUg, S.offsets, J, E, c, f, PD_DTYPE_F32, st);
+                        })))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     for (int si = 0; si < 2; ++si) {
@@ -1614,9 +1646,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       src_grads(si, si == 0 ? P.d_g : P.d_u, si == 0 ? S.fg : S.fu, f);
     }
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads &&
-        (rc = grouped_gemm_dw_pair(S.xj, P.d_acts[0], dVg + l * szVg, S.xj, P.d_acts[1], dVu + l * szVg, S.offsets,
-                                   J, E, d, c, PD_DTYPE_F32, stream)))
+    if (want_wgrads && (rc = wgrad(3, [&](void* st) {
+                          return grouped_gemm_dw_pair(S.xj, P.d_acts[0], dVg + l * szVg, S.xj, P.d_acts[1],
+                                                      dVu + l * szVg, S.offsets, J, E, d, c, PD_DTYPE_F32, st);
+                        })))
       return rc;
     // The stack input carries no parameter gradient: layer 0 stops at its weight
     // gradients (its gate/up input products and the token backward feed only d x0).
@@ -1638,6 +1671,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     }
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
   }
+  for (int i = 0; i < 4; ++i) wjoin(i);
   rec.mark(MOE_CAT_END);
   return PD_OK;
 }
