@@ -13,6 +13,18 @@ namespace pd {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+
+// A helper stream of the current device for running an independent chain of work beside
+// the caller's stream inside one entry point, with a pool of timing-free events for the
+// fork / join points. Default priority (like every stream here); created on first use with
+// the device current and kept until the process ends. `which` (0 or 1) selects one of two
+// such streams; at least n_events events are returned. Entry points that use them on one
+// device at the same time race, as two calls on one workspace do.
+struct AuxStream {
+  hipStream_t st = nullptr;
+  hipEvent_t* ev = nullptr;
+};
+int aux_stream(int which, int n_events, AuxStream& out);
 // pd_grouped_gemm without the launch that zeroes rows past the last group offset (for
 // callers whose groups cover every row).
 int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,

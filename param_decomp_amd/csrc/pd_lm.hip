@@ -604,6 +604,8 @@ struct LMPlan {
   std::vector<LMLayerSave> layers;
   bf16_t *VT[LM_NK], *BtF[LM_NK], *BtB[LM_NK];  // per layer blocks of the per-step weight copies
   bf16_t *rc_a, *rc_b, *rL, *act_m, *act_c, *hc, *qc, *kc, *vc, *ac, *Oh, *fcc, *gc;
+  bf16_t *cQh, *cKh, *cKhT, *cVh, *cVhT, *cP, *cOh;  // the clean pass's own attention buffers
+  float* cS;
   bf16_t *q, *k, *v;
   float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
   bf16_t *dr_a, *dr_b, *drT, *dacts, *dcat, *dxVT, *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
@@ -677,6 +679,14 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.v = A.take<bf16_t>(N * qd);
   P.rinvF = A.take<float>(N);
   P.S = A.take<float>(BH * T * T);
+  P.cQh = A.take<bf16_t>(BH * T * LM_HD);
+  P.cKh = A.take<bf16_t>(BH * T * LM_HD);
+  P.cKhT = A.take<bf16_t>(BH * T * LM_HD);
+  P.cVh = A.take<bf16_t>(BH * T * LM_HD);
+  P.cVhT = A.take<bf16_t>(BH * T * LM_HD);
+  P.cOh = A.take<bf16_t>(BH * T * LM_HD);
+  P.cP = A.take<bf16_t>(BH * T * T);
+  P.cS = A.take<float>(BH * T * T);
   P.delta = A.take<float>((size_t)D.L * LM_NK * N);
   P.imp_total = 0;
   for (int k = 0; k < LM_NK; ++k) {
@@ -861,6 +871,13 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     o1 = y1;
   };
 
+  // the clean pass's helper stream starts once the inputs are ready
+  AuxStream ax;
+  if ((rc = aux_stream(0, 2, ax))) return rc;
+  const hipStream_t sc = ax.st;
+  hipEventRecord(ax.ev[0], s);
+  hipStreamWaitEvent(sc, ax.ev[0], 0);
+
   // ================= per-step weight copies (every product K-contiguous)
   rec.mark(LM_CAT_PREP);
   for (int k = 0; k < LM_NK; ++k) {
@@ -885,50 +902,53 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   if ((rc = check_launch("pd_lm_stack_step prep"))) return rc;
 
   // ================= attention forward on head-major copies
+  // on stream st, with scores Sb and head-major output Ob as scratch
   auto attn_fwd = [&](const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* Qh, bf16_t* Kh, bf16_t* KhT,
-                      bf16_t* Vh, bf16_t* VhT, bf16_t* Pm, bf16_t* a) -> int {
-    hipLaunchKernelGGL(k_lm_attn_in, dim3((unsigned)(T / TILE), (unsigned)H, (unsigned)B), dim3(256), 0, s, q, k, v,
+                      bf16_t* Vh, bf16_t* VhT, bf16_t* Pm, bf16_t* a, float* Sb, bf16_t* Ob, hipStream_t st) -> int {
+    hipLaunchKernelGGL(k_lm_attn_in, dim3((unsigned)(T / TILE), (unsigned)H, (unsigned)B), dim3(256), 0, st, q, k, v,
                        T, H, KV, log2b, Qh, Kh, KhT, Vh, VhT);
     int r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, T, LM_HD, Qh, LM_HD, T * LM_HD, 0, Kh, LM_HD, T * LM_HD, 1,
-                                    P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s);
+                                    Sb, T, T * T, PD_DTYPE_F32, 1.f, 0.f, st);
     if (r) return r;
-    hipLaunchKernelGGL(k_lm_softmax_fwd, rows4(BH * T), dim3(256), 0, s, P.S, BH * T, (int)T, att_scale, Pm);
-    if ((r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, P.Oh,
-                                     LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+    hipLaunchKernelGGL(k_lm_softmax_fwd, rows4(BH * T), dim3(256), 0, st, Sb, BH * T, (int)T, att_scale, Pm);
+    if ((r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, Ob,
+                                     LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, st)))
       return r;
-    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, a, P.Oh, B, T, H, 0);
+    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, st, a, Ob, B, T, H, 0);
     return check_launch("pd_lm_stack_step attention");
   };
 
-  // ================= clean forward (frozen target): act_c
+  // ================= clean forward (frozen target): act_c. It is independent of the masked
+  // forward until the KL reads act_c, so it runs on a helper stream beside the per-step
+  // weight copies and the masked forward, with attention buffers of its own.
   rec.mark(LM_CAT_CLEAN);
-  hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, s, tokens, (const bf16_t*)wte, N, d, V, P.rc_a);
+  hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, sc, tokens, (const bf16_t*)wte, N, d, V, P.rc_a);
   {
     bf16_t* rcur = P.rc_a;
     bf16_t* rnext = P.rc_b;
     for (int l = 0; l < L; ++l) {
       auto Wk = [&](int k) { return bfp(W[k], (size_t)l * D.dout[k] * D.din[k]); };
-      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, ln1 + (size_t)l * d, eps, P.hc,
+      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, sc, rcur, N, d, ln1 + (size_t)l * d, eps, P.hc,
                          (float*)nullptr);
-      if ((rc = gemm_nt(N, qd, d, P.hc, d, Wk(LK_Q), d, P.qc, qd, PD_DTYPE_BF16, 0.f, s))) return rc;
-      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_K), d, P.kc, kvd, PD_DTYPE_BF16, 0.f, s))) return rc;
-      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_V), d, P.vc, kvd, PD_DTYPE_BF16, 0.f, s))) return rc;
-      // the clean pass borrows layer 0's attention saves, which the masked pass rewrites
-      LMLayerSave& S0 = P.layers[0];
-      if ((rc = attn_fwd(P.qc, P.kc, P.vc, S0.Qh, S0.Kh, S0.KhT, S0.Vh, S0.VhT, S0.P, P.ac))) return rc;
-      if ((rc = gemm_nt(N, d, qd, P.ac, qd, Wk(LK_O), qd, P.hc, d, PD_DTYPE_BF16, 0.f, s))) return rc;
-      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, rcur, P.hc, N * d, rnext);
+      if ((rc = gemm_nt(N, qd, d, P.hc, d, Wk(LK_Q), d, P.qc, qd, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_K), d, P.kc, kvd, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_V), d, P.vc, kvd, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      if ((rc = attn_fwd(P.qc, P.kc, P.vc, P.cQh, P.cKh, P.cKhT, P.cVh, P.cVhT, P.cP, P.ac, P.cS, P.cOh, sc)))
+        return rc;
+      if ((rc = gemm_nt(N, d, qd, P.ac, qd, Wk(LK_O), qd, P.hc, d, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, sc, rcur, P.hc, N * d, rnext);
       std::swap(rcur, rnext);
-      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, ln2 + (size_t)l * d, eps, P.hc,
+      hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, sc, rcur, N, d, ln2 + (size_t)l * d, eps, P.hc,
                          (float*)nullptr);
-      if ((rc = gemm_nt(N, f, d, P.hc, d, Wk(LK_FC), d, P.fcc, f, PD_DTYPE_BF16, 0.f, s))) return rc;
-      hipLaunchKernelGGL(k_lm_gelu_fwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, P.fcc, N * f, P.gc);
-      if ((rc = gemm_nt(N, d, f, P.gc, f, Wk(LK_DOWN), f, P.hc, d, PD_DTYPE_BF16, 0.f, s))) return rc;
-      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, rcur, P.hc, N * d, rnext);
+      if ((rc = gemm_nt(N, f, d, P.hc, d, Wk(LK_FC), d, P.fcc, f, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      hipLaunchKernelGGL(k_lm_gelu_fwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, sc, P.fcc, N * f, P.gc);
+      if ((rc = gemm_nt(N, d, f, P.gc, f, Wk(LK_DOWN), f, P.hc, d, PD_DTYPE_BF16, 0.f, sc))) return rc;
+      hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, sc, rcur, P.hc, N * d, rnext);
       std::swap(rcur, rnext);
     }
-    hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, rcur, N, d, norm, eps, P.act_c, (float*)nullptr);
+    hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, sc, rcur, N, d, norm, eps, P.act_c, (float*)nullptr);
   }
+  hipEventRecord(ax.ev[1], sc);  // act_c is ready
   if ((rc = check_launch("pd_lm_stack_step clean"))) return rc;
 
   // ================= masked forward
@@ -996,7 +1016,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if ((rc = site_fwd(LK_K, l, S.h, P.k))) return rc;
     if ((rc = site_fwd(LK_V, l, S.h, P.v))) return rc;
     rec.mark(LM_CAT_ATTN);
-    if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.KhT, S.Vh, S.VhT, S.P, S.a))) return rc;
+    if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.KhT, S.Vh, S.VhT, S.P, S.a, P.S, P.Oh, s))) return rc;
     rec.mark(LM_CAT_ELEM);
     transpose(S.a, N, qd, S.aT, N, s);
     if ((rc = site_fwd(LK_O, l, S.a, P.q))) return rc;  // o output into the q scratch
@@ -1018,6 +1038,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 
   // ================= streamed KL (clean || masked) over the tied head, and its cotangent
   rec.mark(LM_CAT_KL);
+  hipStreamWaitEvent(s, ax.ev[1], 0);  // the clean pass's act_c
   if ((rc = pd_streamed_kl_fwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.pos_kl, P.stats,
                                P.kl_ws, P.kl_ws_bytes, s)))
     return rc;

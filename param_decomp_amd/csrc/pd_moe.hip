@@ -19,8 +19,6 @@
 //                                  jobs (about 0.13 ms per step slower than K-major copies,
 //                                  which would cost ~2.4 GB of extra writes per step)
 #include <algorithm>
-#include <mutex>
-#include <string>
 #include <vector>
 
 #include "pd_common.hpp"
@@ -1181,50 +1179,6 @@ struct SrcArgs {
   float* d_src_delta; // fp32 [L, 3, S]
 };
 
-// Clean layers 1.. run on a second stream (default priority, like every stream here),
-// concurrently with the masked forward: the two chains are independent until masked layer
-// l reads clean layer l's routing, and the matrix-core phases of one overlap the VALU-bound
-// mask passes of the other. One such stream and its events (one per layer) per device,
-// created on first use with that device current and kept until the process ends. Calls that overlap
-// on one device share them (and a workspace) and race, as any two calls on one workspace do.
-struct CleanStream {
-  hipStream_t st = nullptr;
-  hipEvent_t start = nullptr, fork = nullptr, copies = nullptr;
-  std::vector<hipEvent_t> layer;  // layer[l]: clean layer l is complete
-  hipEvent_t wg_in[4] = {}, wg_out[4] = {};  // backward: a weight gradient's inputs ready / product done
-};
-constexpr int MOE_MAX_DEVICES = 64;
-static std::mutex g_clean_mu;
-static CleanStream g_clean[MOE_MAX_DEVICES];
-
-static int clean_stream(int L, CleanStream& out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MOE_MAX_DEVICES)
-    return fail(PD_ELAUNCH, "pd_moe_stack_step: no current HIP device in range");
-  std::lock_guard<std::mutex> lock(g_clean_mu);
-  CleanStream& c = g_clean[dev];
-  hipError_t e = hipSuccess;
-  if (!c.st) {
-    e = hipStreamCreateWithFlags(&c.st, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.start, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.fork, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.copies, hipEventDisableTiming);
-    for (int i = 0; i < 4 && e == hipSuccess; ++i) {
-      e = hipEventCreateWithFlags(&c.wg_in[i], hipEventDisableTiming);
-      if (e == hipSuccess) e = hipEventCreateWithFlags(&c.wg_out[i], hipEventDisableTiming);
-    }
-    if (e != hipSuccess) c.st = nullptr;
-  }
-  while (e == hipSuccess && (int)c.layer.size() < L) {
-    hipEvent_t ev = nullptr;
-    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-    if (e == hipSuccess) c.layer.push_back(ev);
-  }
-  if (e != hipSuccess) return fail(PD_ELAUNCH, std::string("pd_moe_stack_step: clean-pass stream: ") + hipGetErrorString(e));
-  out = c;
-  return PD_OK;
-}
-
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
@@ -1320,11 +1274,31 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   rec.mark(MOE_CAT_CLEAN);
   const int64_t LE = (int64_t)L * E;
   // The frozen weights' copies and clean layer 0 run on this stream (masked layer 0 needs
-  // all of it). With L > 1 the second stream copies the components' weights meanwhile,
-  // then runs clean layers 1.. once layer 0 is done.
-  CleanStream cs;
+  // all of it). With L > 1 a helper stream copies the components' weights meanwhile, then
+  // runs clean layers 1.. once layer 0 is done, beside the masked forward: the two chains
+  // are independent until masked layer l reads clean layer l's routing, and the matrix-core
+  // phases of one overlap the VALU-bound mask passes of the other. In the backward the
+  // helper stream runs the weight-gradient products. Its events: start, fork, copies,
+  // weight-gradient inputs ready [4] and done [4], clean layer l done (layer l % 64: a
+  // wait on a shared event waits for the last layer recorded on it, later than needed).
+  constexpr int LAYER_EVENTS = 64;
+  struct {
+    hipStream_t st = nullptr;
+    hipEvent_t start, fork, copies, *wg_in, *wg_out, *layer_ev;
+    hipEvent_t layer(int l) const { return layer_ev[l % LAYER_EVENTS]; }
+  } cs;
   const bool side = !reuse_clean && L > 1;
-  if ((side || want_wgrads) && (rc0 = clean_stream(L, cs))) return rc0;
+  if (side || want_wgrads) {
+    AuxStream ax;
+    if ((rc0 = aux_stream(0, 11 + std::min(L, LAYER_EVENTS), ax))) return rc0;
+    cs.st = ax.st;
+    cs.start = ax.ev[0];
+    cs.fork = ax.ev[1];
+    cs.copies = ax.ev[2];
+    cs.wg_in = ax.ev + 3;
+    cs.wg_out = ax.ev + 7;
+    cs.layer_ev = ax.ev + 11;
+  }
   if (side) {
     hipEventRecord(cs.start, s);
     hipStreamWaitEvent(cs.st, cs.start, 0);
@@ -1412,7 +1386,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     std::swap(rcur, rnext);
     if (top_idx_out)
       hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, sc);
-    if (l > 0) hipEventRecord(cs.layer[l], sc);
+    if (l > 0) hipEventRecord(cs.layer(l), sc);
   }
   bf16_t* rc_final = rcur;
   if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
@@ -1422,7 +1396,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   const bf16_t* r_in = (const bf16_t*)x0;
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
-    if (side && l > 0) hipStreamWaitEvent(s, cs.layer[l], 0);  // clean layer l's routing
+    if (side && l > 0) hipStreamWaitEvent(s, cs.layer(l), 0);  // clean layer l's routing
     rec.mark(MOE_CAT_NORM_ROUTE);
     if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
     if (l > 0) {  // layer 0's were formed by the clean pass
@@ -1506,7 +1480,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
   // ================= loss (and everything after it) after the whole clean pass
-  if (side) hipStreamWaitEvent(s, cs.layer[L - 1], 0);
+  if (side) hipStreamWaitEvent(s, cs.layer(L - 1), 0);
   const int64_t nres = T * d;
   hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
                      recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
