@@ -805,7 +805,8 @@ enum {
   LM_CAT_GEMM_DX = 7,  // d_acts and d_input products
   LM_CAT_GEMM_DW = 8,  // dU and dV products
   LM_CAT_MASK_BWD = 9, // mask passes (backward)
-  LM_CAT_END = 10
+  LM_CAT_WAIT = 10,    // waiting for the helper stream (the clean pass)
+  LM_CAT_END = 11
 };
 
 static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64_t V, int L, const int32_t* Cs,
@@ -1037,8 +1038,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   if ((rc = check_launch("pd_lm_stack_step masked forward"))) return rc;
 
   // ================= streamed KL (clean || masked) over the tied head, and its cotangent
-  rec.mark(LM_CAT_KL);
+  rec.mark(LM_CAT_WAIT);
   hipStreamWaitEvent(s, ax.ev[1], 0);  // the clean pass's act_c
+  rec.mark(LM_CAT_KL);
   if ((rc = pd_streamed_kl_fwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.pos_kl, P.stats,
                                P.kl_ws, P.kl_ws_bytes, s)))
     return rc;

@@ -1164,7 +1164,8 @@ enum {
   MOE_CAT_GEMM_DW = 7,     // grouped GEMMs d_weight (ragged contraction)
   MOE_CAT_MASK_BWD = 8,    // job-space mask passes, backward
   MOE_CAT_TOKEN_BWD = 9,   // router/norm token backward
-  MOE_CAT_END = 10
+  MOE_CAT_WAIT = 10,       // waiting for the helper stream (clean layers, weight gradients)
+  MOE_CAT_END = 11
 };
 
 // Persistent (adversarial) source tables for pd_moe_stack_step_sources.
@@ -1392,11 +1393,17 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
 
   // ================= masked forward
-  if (side) hipStreamWaitEvent(s, cs.copies, 0);
+  if (side) {
+    rec.mark(MOE_CAT_WAIT);
+    hipStreamWaitEvent(s, cs.copies, 0);
+  }
   const bf16_t* r_in = (const bf16_t*)x0;
   for (int l = 0; l < L; ++l) {
     LayerSave& S = P.layers[l];
-    if (side && l > 0) hipStreamWaitEvent(s, cs.layer(l), 0);  // clean layer l's routing
+    if (side && l > 0) {
+      rec.mark(MOE_CAT_WAIT);
+      hipStreamWaitEvent(s, cs.layer(l), 0);  // clean layer l's routing
+    }
     rec.mark(MOE_CAT_NORM_ROUTE);
     if (S.r != r_in) hipMemcpyAsync(S.r, r_in, (size_t)T * d * 2, hipMemcpyDeviceToDevice, s);
     if (l > 0) {  // layer 0's were formed by the clean pass
@@ -1480,7 +1487,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
   // ================= loss (and everything after it) after the whole clean pass
-  if (side) hipStreamWaitEvent(s, cs.layer(L - 1), 0);
+  if (side) {
+    rec.mark(MOE_CAT_WAIT);
+    hipStreamWaitEvent(s, cs.layer(L - 1), 0);
+  }
+  rec.mark(MOE_CAT_COMBINE);
   const int64_t nres = T * d;
   hipLaunchKernelGGL(k_moe_recon, dim3(REC_BLOCKS), dim3(256), 0, s, P.r_final, rc_final, nres,
                      recon_coeff * 2.f / (float)nres, P.dr_a, P.rec_part);
@@ -1518,6 +1529,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   };
   for (int l = L - 1; l >= 0; --l) {
     LayerSave& S = P.layers[l];
+    rec.mark(MOE_CAT_WAIT);
     wjoin(0);  // the down site's dU reads d_dout, its dV d_acts[2]
     wjoin(1);
     rec.mark(MOE_CAT_COMBINE);
@@ -1591,13 +1603,15 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if (use_delta &&
         (rc = grouped_gemm(P.d_dout, bf(Wd, l * szW), S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false)))
       return rc;
-    rec.mark(MOE_CAT_SWIGLU);
+    rec.mark(MOE_CAT_WAIT);
     wjoin(2);  // dU of gate / up reads d_g, d_u
+    rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
                        J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_u, P.d_w_part);
     // ---- gate and up sites: paired launches
-    rec.mark(MOE_CAT_GEMM_DX);
+    rec.mark(MOE_CAT_WAIT);
     wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
+    rec.mark(MOE_CAT_GEMM_DX);
     if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
                                 J, E, f, c, PD_DTYPE_BF16, stream)))
       return rc;
@@ -1645,6 +1659,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     }
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
   }
+  rec.mark(MOE_CAT_WAIT);
   for (int i = 0; i < 4; ++i) wjoin(i);
   rec.mark(MOE_CAT_END);
   return PD_OK;

@@ -23,7 +23,7 @@ from param_decomp_amd.prng import Key
 
 KINDS = ("q_proj", "k_proj", "v_proj", "o_proj", "c_fc", "down_proj")  # KIND_ORDER (pd/targets/llama_simple_mlp.py)
 CATEGORIES = ("prep", "clean_fwd", "gemm_fwd", "mask_fwd", "attention", "elementwise", "kl", "gemm_dx", "gemm_dw",
-              "mask_bwd")
+              "mask_bwd", "wait")
 HEAD_DIM = 64
 
 
