@@ -104,7 +104,7 @@ def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T,
 def test_lm_stack_step_full_size_properties(device):
     """The Llama-4L shape (d_model 768, 12 heads, d_mlp 3072, vocab 50277, C = 1024
     attention / 4096 MLP, 16 x 512 tokens): finite, positive losses and gradients,
-    bit-identical run to run."""
+    bit-identical run to run, also when calls with other tokens are queued back to back."""
     from param_decomp_amd.lm_step import KINDS as K, LMStackStep, LMWeights, site_dims
 
     B, T, d, H, f, V, Ln = 16, 512, 768, 12, 3072, 50277, 4
@@ -135,3 +135,16 @@ def test_lm_stack_step_full_size_properties(device):
         assert torch.isfinite(step.d_ci_pre[k].float()).all()
     assert torch.equal(step.losses, l1) and torch.equal(step.dV["c_fc"], dv1)
     assert torch.equal(step.d_ci_pre["q_proj"], dci1)
+    # back to back with other tokens and no host synchronization in between (the clean
+    # pass runs on a helper stream): each call's results are those of a call alone
+    tok2 = torch.randint(0, V, (B * T,), device=device, generator=g, dtype=torch.int32)
+    step.step(tok2, w, ci, (0, 2))
+    lb, dvb = step.losses.clone(), step.dV["c_fc"].clone()
+    step.step(tok, w, ci, (0, 1))
+    la, dva = step.losses.clone(), step.dV["c_fc"].clone()
+    torch.cuda.synchronize()
+    assert torch.equal(la, l1) and torch.equal(dva, dv1)
+    step.step(tok2, w, ci, (0, 2))
+    torch.cuda.synchronize()
+    assert torch.equal(step.losses, lb) and torch.equal(step.dV["c_fc"], dvb)
+    assert not torch.equal(lb, l1)

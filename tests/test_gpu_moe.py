@@ -98,8 +98,9 @@ def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, so
 def test_moe_stack_step_full_size_properties(device):
     """The Qwen3.5-MoE-shaped stack (T=8192, width 512, 42 experts top-8, SwiGLU
     512->256->512, c=512 per expert, 4 layers): finite losses, deterministic run to
-    run, and every expert's bucket size equals its routed job count (the per-layer
-    routing is a permutation: all T*k jobs land)."""
+    run (also when calls with other inputs are queued back to back), and every expert's
+    bucket size equals its routed job count (the per-layer routing is a permutation: all
+    T*k jobs land)."""
     from param_decomp_amd.moe_step import MoEStackStep, MoEWeights
 
     T, d, f, E, k, c, Ln = 8192, 512, 256, 42, 8, 512, 4
@@ -124,6 +125,20 @@ def test_moe_stack_step_full_size_properties(device):
     step.step(x0, w, ci, (0, 1))
     assert torch.isfinite(l1).all() and float(l1[1]) > 0 and float(l1[2]) > 0
     assert torch.equal(step.losses, l1) and torch.equal(step.dV["down"], dv1) and torch.equal(step.d_ci_pre, dci1)
+    # back to back with another input and no host synchronization in between: the helper
+    # stream's work of one call must neither see the other call's buffers nor be seen by it
+    x1 = rn(T, d, scale=1.0)
+    step.step(x1, w, ci, (0, 2))
+    lb, dvb, dcib = step.losses.clone(), step.dV["down"].clone(), step.d_ci_pre.clone()
+    step.step(x0, w, ci, (0, 1))
+    la, dva, dcia = step.losses.clone(), step.dV["down"].clone(), step.d_ci_pre.clone()
+    torch.cuda.synchronize()
+    assert torch.equal(la, l1) and torch.equal(dva, dv1) and torch.equal(dcia, dci1)
+    step.step(x1, w, ci, (0, 2))
+    torch.cuda.synchronize()
+    assert torch.equal(step.losses, lb) and torch.equal(step.dV["down"], dvb) and torch.equal(step.d_ci_pre, dcib)
+    assert not torch.equal(lb, l1)
+    step.step(x0, w, ci, (0, 1))
     for l in range(Ln):
         counts = torch.bincount(step.top_idx[l].reshape(-1).long(), minlength=E)
         assert int(counts.sum()) == T * k
