@@ -608,7 +608,7 @@ struct LMPlan {
   float* cS;
   bf16_t *q, *k, *v;
   float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
-  bf16_t *dr_a, *dr_b, *drT, *dacts, *dcat, *dxVT, *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
+  bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dcat, *dxVT[2], *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
   char *kl_ws, *sk_ws;
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
   float *sl0_act, *sl0_freq;  // every site's smooth-L0 loss partials, contiguous
@@ -717,10 +717,10 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.dhf = A.take<float>(N * maxw);
   P.dr_a = A.take<bf16_t>(N * d);
   P.dr_b = A.take<bf16_t>(N * d);
-  P.drT = A.take<bf16_t>(N * maxw);
+  for (int b = 0; b < 2; ++b) P.drT[b] = A.take<bf16_t>(N * maxw);
   P.dacts = A.take<bf16_t>(N * maxC);
   P.dcat = A.take<bf16_t>(N * maxcat2);
-  P.dxVT = A.take<bf16_t>(N * maxC);
+  for (int b = 0; b < 2; ++b) P.dxVT[b] = A.take<bf16_t>(N * maxC);
   for (int i = 0; i < 3; ++i) P.dqkv[i] = A.take<bf16_t>(N * qd);
   P.dqkvT = A.take<bf16_t>(N * qd);
   P.da = A.take<bf16_t>(N * qd);
@@ -874,7 +874,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 
   // the clean pass's helper stream starts once the inputs are ready
   AuxStream ax;
-  if ((rc = aux_stream(0, 2, ax))) return rc;
+  if ((rc = aux_stream(0, 5, ax))) return rc;  // inputs ready, act_c ready, dW fork, dW done [2]
   const hipStream_t sc = ax.st;
   hipEventRecord(ax.ev[0], s);
   hipStreamWaitEvent(sc, ax.ev[0], 0);
@@ -1065,6 +1065,16 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   // site backward: g [N, d_out] (the output cotangent), the site input's transpose xT
   // [d_in, N] -> dU, dV, d_ci_pre, and d_input (+)= into din_out (fp32 accumulate when
   // din_f32, else bf16 written).
+  // The weight gradients (split-contraction products) run on the helper stream: site call
+  // n writes g^T and d(xV)^T into buffer set n % 2, forks the helper stream once both are
+  // written, and call n + 2 waits for that call's products before it rewrites the set.
+  // Nothing on this stream reads a weight gradient; the step joins them all at its end.
+  int wg_call = 0;
+  bool wg_pend[2] = {false, false};
+  auto wg_join = [&](int b) {
+    if (wg_pend[b]) hipStreamWaitEvent(s, ax.ev[3 + b], 0);
+    wg_pend[b] = false;
+  };
   auto site_bwd = [&](int k, int l, const bf16_t* g, const bf16_t* xT, void* din_out, bool din_f32,
                       float din_beta) -> int {
     // din_out NULL: the site's input carries no gradient (layer 0's q/k/v read the
@@ -1075,30 +1085,38 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     const LMMaskArgs ma0 = mask_args(k, l);
     LMMaskArgs ma = ma0;
     ma.ld = kc2;
+    const int wb = wg_call++ & 1;
+    bf16_t* const drT = P.drT[wb];
+    bf16_t* const dxVT = P.dxVT[wb];
+    rec.mark(LM_CAT_WAIT);
+    wg_join(wb);
     rec.mark(LM_CAT_ELEM);
-    transpose(g, N, dout, P.drT, N, s);  // g^T [d_out, N]
+    transpose(g, N, dout, drT, N, s);  // g^T [d_out, N]
     if (D.use_delta && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s);
     rec.mark(LM_CAT_GEMM_DX);
     int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
-    rec.mark(LM_CAT_GEMM_DW);
-    if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, P.drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
-                            P.sk_ws, P.sk_ws_bytes, s)))
-      return r;
     rec.mark(LM_CAT_MASK_BWD);
     bf16_t* dpre = (bf16_t*)d_ci_pre[k] + (size_t)l * N * C;
 #define PD_LMB(PMV)                                                                                          \
   hipLaunchKernelGGL((k_lm_mask_bwd<PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
-                     P.dcat, P.dxVT, dpre)
+                     P.dcat, dxVT, dpre)
     if (pm == PM_SL0) PD_LMB(PM_SL0);
     else if (pm == 2) PD_LMB(2);
     else if (pm == 1) PD_LMB(1);
     else PD_LMB(0);
 #undef PD_LMB
     rec.mark(LM_CAT_GEMM_DW);
-    if ((r = gemm_nt_splitk(di, C, N, xT, N, P.dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
-                            P.sk_ws_bytes, s)))
+    hipEventRecord(ax.ev[2], s);  // g^T and d(xV)^T of this call are written
+    hipStreamWaitEvent(ax.st, ax.ev[2], 0);
+    if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
+                            P.sk_ws, P.sk_ws_bytes, ax.st)))
       return r;
+    if ((r = gemm_nt_splitk(di, C, N, xT, N, dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
+                            P.sk_ws_bytes, ax.st)))
+      return r;
+    hipEventRecord(ax.ev[3 + wb], ax.st);
+    wg_pend[wb] = true;
     if (!din_out) return PD_OK;
     rec.mark(LM_CAT_GEMM_DX);
     return gemm_nt(N, di, kc2, P.dcat, kc2, P.BtB[k] + (size_t)l * di * kc2, kc2, din_out, di,
@@ -1154,6 +1172,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
       std::swap(dr, dr_o);  // dr: cotangent of layer l's input
     }
   }
+  rec.mark(LM_CAT_WAIT);
+  wg_join(0);
+  wg_join(1);
   rec.mark(LM_CAT_END);
   return check_launch("pd_lm_stack_step backward");
 }
