@@ -56,6 +56,7 @@ LLAMA = "llama4L"
 TMS = "tms5_2"
 RESID = "resid_mlp1L"
 GEMM_MOE = "gemm_qwen35moe4L"
+GEMM_LM = "gemm_llama4L"
 PEAK_FP32_MFMA = 157.3e12
 WORKLOADS = {
     DENSE: dict(T=4096, d_in=768, d_out=3072, C=4096),
@@ -97,6 +98,12 @@ WORKLOADS = {
     # (MN-major), and the weight gradients from row-major (MN-major) and job-contiguous
     # (K-major) operands
     GEMM_MOE: dict(J=65536, E=42, d=512, f=256, c=512),
+    # the LM step's dense products (16 x 512 tokens, d 768, d_mlp 3072, C 1024 / 4096, the
+    # delta channel's concatenated contractions), C = A @ B^T with both operands
+    # K-contiguous, each through pd_gemm and through torch.matmul (hipBLASLt) as a
+    # library reference: (M, N, K, output dtype)
+    GEMM_LM: dict(shapes=[(8192, 1024, 768, "bf16"), (8192, 4096, 768, "bf16"), (8192, 4096, 3072, "bf16"),
+                          (8192, 768, 1792, "bf16"), (8192, 3072, 4864, "bf16"), (8192, 768, 7168, "bf16")]),
     FAITH_MOE: dict(groups=[dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
                             dict(n=4 * 42, per=42, d_in=512, d_out=256, C=512),
                             dict(n=4 * 42, per=42, d_in=256, d_out=512, C=512)]),
@@ -866,6 +873,56 @@ def run_faith(args):
     return res
 
 
+def run_gemm_lm(args):
+    """Each dense product of the LM step timed alone through pd_gemm, and the same product
+    through torch.matmul (hipBLASLt) for reference; a step is one pd_gemm launch of every
+    listed product. The two results are compared (max relative difference)."""
+    import torch
+
+    from param_decomp_amd import hip_events, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    reps = max(args.steps, 1)
+    phase, tflops, lib_tflops, diff, flops = {}, {}, {}, {}, {}
+
+    def timed(launch):
+        for _ in range(max(args.warmup, 1)):
+            launch()
+        ev = hip_events.create(2)
+        torch.cuda.synchronize()
+        hip_events.record(ev[0], stream)
+        for _ in range(reps):
+            launch()
+        hip_events.record(ev[1], stream)
+        torch.cuda.synchronize()
+        ms = hip_events.elapsed_ms(ev[0], ev[1]) / reps
+        hip_events.destroy(ev)
+        return ms
+
+    for M, N, K, _ in WORKLOADS[GEMM_LM]["shapes"]:
+        name = f"M{M}_N{N}_K{K}"
+        a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        b = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+        c_pd = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        c_lib = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        fl = 2 * M * N * K
+        phase[name] = timed(lambda: ops.gemm(a, b, trans_b=True, out=c_pd))
+        lib_ms = timed(lambda: torch.matmul(a, b.t(), out=c_lib))
+        flops[name] = fl
+        tflops[name] = fl / (phase[name] * 1e-3) / 1e12
+        lib_tflops[name] = fl / (lib_ms * 1e-3) / 1e12
+        diff[name] = float(((c_pd.float() - c_lib.float()).abs().max() / c_lib.float().abs().max()).item())
+    dom = max(phase, key=phase.get)
+    return {"tokens": 8192, "ms_per_step": sum(phase.values()),
+            "config": {"workload": GEMM_LM, "shapes": WORKLOADS[GEMM_LM]["shapes"],
+                       "unit_of_value": "token rows per step of every listed product"},
+            "step_flops": sum(flops.values()), "phases_ms": phase, "tflops": tflops,
+            "hipblaslt_tflops": lib_tflops, "max_rel_diff_vs_hipblaslt": diff,
+            "roofline": roofline("flop", flops[dom], phase[dom], dom, 1)}
+
+
 def run_gemm_moe(args):
     """Each grouped product of the MoE step timed alone (HIP events around the repeated
     launches of one product); a step is one launch of every listed product."""
@@ -1379,6 +1436,8 @@ def main():
         res = run_kl(args)
     elif args.workload == GEMM_MOE:
         res = run_gemm_moe(args)
+    elif args.workload == GEMM_LM:
+        res = run_gemm_lm(args)
     else:
         res = run_ci(args)
     ms = res["ms_per_step"]
@@ -1407,6 +1466,9 @@ def main():
         out["launches_per_step"] = res["launches_per_step"]
     if "tflops" in res:
         out["tflops_per_product"] = res["tflops"]
+    for key in ("hipblaslt_tflops", "max_rel_diff_vs_hipblaslt"):
+        if key in res:
+            out[key] = res[key]
     if "reference_rule_flops" in res:
         out["reference_rule_tflops"] = res["reference_rule_flops"] / (ms * 1e-3) / 1e12
     if "cpu_baseline" in res:
