@@ -49,6 +49,7 @@ SL0 = dict(kind="smooth_l0", coeff=0.5, gamma=0.3, normalize_at_one=True, freq_c
 
 @pytest.mark.parametrize("cfg,partitionable,use_delta,source_value,sl0", [
     (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, True, None, None),
+    (mo.MoEConfig(T=128, d=32, f=24, E=6, k=2, c=16, L=1), True, True, None, None),  # no clean layer on the helper stream
     (mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3), True, True, None, None),
     (mo.MoEConfig(T=120, d=32, f=24, E=6, k=3, c=40, L=2), False, True, None, None),
     (mo.MoEConfig(T=256, d=64, f=32, E=8, k=2, c=16, L=2), True, False, None, None),
