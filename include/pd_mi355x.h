@@ -13,7 +13,13 @@
  *    is given. Entry points that need scratch take a caller-provided `workspace` whose
  *    size comes from the matching *_workspace_size query; nothing allocates.
  *  - `stream` is a hipStream_t (NULL = the default stream). Calls only enqueue work;
- *    none synchronizes the host.
+ *    none synchronizes the host. The stack steps (pd_moe_stack_step*, pd_lm_stack_step*)
+ *    run independent parts of their work on a helper stream of the
+ *    same priority, one per device, created with its events on the first call on that
+ *    device (make that first call outside any stream capture); the helper stream waits
+ *    on `stream` before it starts and `stream` waits on it before the call's last work,
+ *    so anything later enqueued on `stream` sees every output. Calls that overlap on one
+ *    device race, as two calls sharing a workspace do.
  *  - Return PD_OK (0) or a PD_E* code; pd_last_error() gives the message (thread-local).
  *    Invalid shapes are rejected on the host before any launch.
  *  - Random keys are JAX threefry2x32 key words (k0, k1) as jax.random.PRNGKey /
