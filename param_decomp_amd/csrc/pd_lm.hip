@@ -379,6 +379,17 @@ __global__ __launch_bounds__(256) void k_lm_attn_in(const bf16_t* __restrict__ q
   ttile_store(Tv, VhT + bh * LM_HD * T, T, t0, T, 0, LM_HD, tid);
 }
 
+// The causal attention products work on 128-row tiles: a query tile's products read P and
+// dS only up to the end of its diagonal 128 x 128 block, and the key tiles' products read
+// them only from the block's first row, so the softmax passes write each row up to the end
+// of its diagonal block (zeros past the diagonal) and nothing beyond; S and dP exist only
+// on and below the diagonal blocks.
+constexpr int ATT_BLOCK = 128;
+__device__ inline int att_row_end(int i, int T) {
+  const int e = (i / ATT_BLOCK + 1) * ATT_BLOCK;
+  return e < T ? e : T;
+}
+
 // P = softmax(scale * S) over keys j <= i (causal), bf16; one wave per row of S [rows, T].
 __global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict__ S, int64_t rows, int T, float scale,
                                                         bf16_t* __restrict__ P) {
@@ -392,7 +403,8 @@ __global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict_
   float sum = 0.f;
   for (int j = lane; j <= i; j += 64) sum += __expf(s[j] * scale - mx);
   const float inv = 1.f / wave_sum(sum);
-  for (int j = lane; j < T; j += 64) P[row * T + j] = f32_to_bf16(j <= i ? __expf(s[j] * scale - mx) * inv : 0.f);
+  const int end = att_row_end(i, T);
+  for (int j = lane; j < end; j += 64) P[row * T + j] = f32_to_bf16(j <= i ? __expf(s[j] * scale - mx) * inv : 0.f);
 }
 
 // dS = bf16(P * (dP - sum_j P dP) * scale) (causal zeros stay zero); one wave per row.
@@ -404,10 +416,9 @@ __global__ __launch_bounds__(256) void k_lm_softmax_bwd(const bf16_t* __restrict
   float dot = 0.f;
   for (int j = lane; j <= i; j += 64) dot = fmaf(bf16_to_f32(P[row * T + j]), dP[row * T + j], dot);
   dot = wave_sum(dot);
-  for (int j = lane; j < T; j += 64) {
-    const float pj = bf16_to_f32(P[row * T + j]);
-    dS[row * T + j] = f32_to_bf16(j <= i ? pj * (dP[row * T + j] - dot) * scale : 0.f);
-  }
+  const int end = att_row_end(i, T);
+  for (int j = lane; j < end; j += 64)
+    dS[row * T + j] = f32_to_bf16(j <= i ? bf16_to_f32(P[row * T + j]) * (dP[row * T + j] - dot) * scale : 0.f);
 }
 
 // a[b*T + t, h*64 + c] = Oh[(b*H + h)*T + t, c] (dir = 0) or the inverse copy (dir = 1);
@@ -908,12 +919,14 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                       bf16_t* Vh, bf16_t* VhT, bf16_t* Pm, bf16_t* a, float* Sb, bf16_t* Ob, hipStream_t st) -> int {
     hipLaunchKernelGGL(k_lm_attn_in, dim3((unsigned)(T / TILE), (unsigned)H, (unsigned)B), dim3(256), 0, st, q, k, v,
                        T, H, KV, log2b, Qh, Kh, KhT, Vh, VhT);
-    int r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, T, LM_HD, Qh, LM_HD, T * LM_HD, 0, Kh, LM_HD, T * LM_HD, 1,
-                                    Sb, T, T * T, PD_DTYPE_F32, 1.f, 0.f, st);
+    // causal: score tiles above the diagonal are not formed, and P @ V contracts each
+    // query tile only over keys up to its last row
+    int r = gemm_batched_causal(1, PD_DTYPE_BF16, BH, T, T, LM_HD, Qh, LM_HD, T * LM_HD, 0, Kh, LM_HD, T * LM_HD, 1,
+                                Sb, T, T * T, PD_DTYPE_F32, 1.f, 0.f, st);
     if (r) return r;
     hipLaunchKernelGGL(k_lm_softmax_fwd, rows4(BH * T), dim3(256), 0, st, Sb, BH * T, (int)T, att_scale, Pm);
-    if ((r = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, Ob,
-                                     LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, st)))
+    if ((r = gemm_batched_causal(2, PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, Ob,
+                                 LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, st)))
       return r;
     hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, st, a, Ob, B, T, H, 0);
     return check_launch("pd_lm_stack_step attention");
@@ -1142,20 +1155,21 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     // attention backward
     rec.mark(LM_CAT_ATTN);
     hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, P.da, P.dOh, B, T, H, 1);
-    // dP = dO @ V^T (fp32), dS
-    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, T, LM_HD, P.dOh, LM_HD, T * LM_HD, 0, S.Vh, LM_HD,
-                                      T * LM_HD, 1, P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s)))
+    // dP = dO @ V^T (fp32, tiles on or below the diagonal), dS
+    if ((rc = gemm_batched_causal(1, PD_DTYPE_BF16, BH, T, T, LM_HD, P.dOh, LM_HD, T * LM_HD, 0, S.Vh, LM_HD,
+                                  T * LM_HD, 1, P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s)))
       return rc;
     hipLaunchKernelGGL(k_lm_softmax_bwd, rows4(BH * T), dim3(256), 0, s, S.P, P.S, BH * T, (int)T, att_scale, P.dS);
-    // dQ = dS @ K (B^T = K^T), dK = dS^T @ Q, dV = P^T @ dO
-    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 0, S.KhT, T, LM_HD * T, 1, P.dQh,
-                                      LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+    // dQ = dS @ K (B^T = K^T; keys up to the query tile's last row), dK = dS^T @ Q,
+    // dV = P^T @ dO (queries from the key tile's first row)
+    if ((rc = gemm_batched_causal(2, PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 0, S.KhT, T, LM_HD * T, 1, P.dQh,
+                                  LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
       return rc;
-    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 1, S.Qh, LM_HD, T * LM_HD, 0,
-                                      P.dKh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+    if ((rc = gemm_batched_causal(3, PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 1, S.Qh, LM_HD, T * LM_HD, 0,
+                                  P.dKh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
       return rc;
-    if ((rc = pd_gemm_strided_batched(PD_DTYPE_BF16, BH, T, LM_HD, T, S.P, T, T * T, 1, P.dOh, LM_HD, T * LM_HD, 0,
-                                      P.dVh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
+    if ((rc = gemm_batched_causal(3, PD_DTYPE_BF16, BH, T, LM_HD, T, S.P, T, T * T, 1, P.dOh, LM_HD, T * LM_HD, 0,
+                                  P.dVh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
       return rc;
     hipLaunchKernelGGL(k_lm_attn_out_grads, dim3((unsigned)(T / TILE), (unsigned)KV, (unsigned)B), dim3(256), 0, s,
                        P.dQh, P.dKh, P.dVh, T, H, KV, log2b, P.dqkv[0], P.dqkv[1], P.dqkv[2]);
