@@ -390,7 +390,9 @@ __device__ inline int att_row_end(int i, int T) {
   return e < T ? e : T;
 }
 
-// P = softmax(scale * S) over keys j <= i (causal), bf16; one wave per row of S [rows, T].
+// P = softmax(scale * S) over keys j <= i (causal), bf16; one wave per row of S [rows, T],
+// 4 consecutive keys per lane (T % 4 == 0: 16-byte score loads, 8-byte stores). The last
+// group a row reads may reach past i inside its diagonal block; those keys are excluded.
 __global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict__ S, int64_t rows, int T, float scale,
                                                         bf16_t* __restrict__ P) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
@@ -398,27 +400,67 @@ __global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict_
   const int i = (int)(row % T), lane = threadIdx.x & 63;
   const float* s = S + row * T;
   float mx = -INFINITY;
-  for (int j = lane; j <= i; j += 64) mx = fmaxf(mx, s[j] * scale);
+  for (int j = lane * 4; j <= i; j += 256) {
+    const float4 v = *(const float4*)(s + j);
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + q <= i) mx = fmaxf(mx, e[q] * scale);
+  }
   mx = wave_max(mx);
   float sum = 0.f;
-  for (int j = lane; j <= i; j += 64) sum += __expf(s[j] * scale - mx);
+  for (int j = lane * 4; j <= i; j += 256) {
+    const float4 v = *(const float4*)(s + j);
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + q <= i) sum += __expf(e[q] * scale - mx);
+  }
   const float inv = 1.f / wave_sum(sum);
   const int end = att_row_end(i, T);
-  for (int j = lane; j < end; j += 64) P[row * T + j] = f32_to_bf16(j <= i ? __expf(s[j] * scale - mx) * inv : 0.f);
+  for (int j = lane * 4; j < end; j += 256) {
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j <= i) {
+      const float4 v = *(const float4*)(s + j);
+      const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = j + q <= i ? __expf(e[q] * scale - mx) * inv : 0.f;
+    }
+    *(uint2*)(P + row * T + j) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  }
 }
 
-// dS = bf16(P * (dP - sum_j P dP) * scale) (causal zeros stay zero); one wave per row.
+// dS = bf16(P * (dP - sum_j P dP) * scale) (causal zeros stay zero); one wave per row, 4
+// consecutive keys per lane.
 __global__ __launch_bounds__(256) void k_lm_softmax_bwd(const bf16_t* __restrict__ P, const float* __restrict__ dP,
                                                         int64_t rows, int T, float scale, bf16_t* __restrict__ dS) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   if (row >= rows) return;
   const int i = (int)(row % T), lane = threadIdx.x & 63;
+  const bf16_t* pr = P + row * T;
+  const float* dpr = dP + row * T;
   float dot = 0.f;
-  for (int j = lane; j <= i; j += 64) dot = fmaf(bf16_to_f32(P[row * T + j]), dP[row * T + j], dot);
+  for (int j = lane * 4; j <= i; j += 256) {
+    const uint2 pw = *(const uint2*)(pr + j);
+    const float4 g = *(const float4*)(dpr + j);
+    const float pv[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)}, gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + q <= i) dot = fmaf(pv[q], gv[q], dot);
+  }
   dot = wave_sum(dot);
   const int end = att_row_end(i, T);
-  for (int j = lane; j < end; j += 64)
-    dS[row * T + j] = f32_to_bf16(j <= i ? bf16_to_f32(P[row * T + j]) * (dP[row * T + j] - dot) * scale : 0.f);
+  for (int j = lane * 4; j < end; j += 256) {
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j <= i) {
+      const uint2 pw = *(const uint2*)(pr + j);
+      const float4 g = *(const float4*)(dpr + j);
+      const float pv[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)}, gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = j + q <= i ? pv[q] * (gv[q] - dot) * scale : 0.f;
+    }
+    *(uint2*)(dS + row * T + j) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  }
 }
 
 // a[b*T + t, h*64 + c] = Oh[(b*H + h)*T + t, c] (dir = 0) or the inverse copy (dir = 1);
