@@ -322,17 +322,154 @@ __global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32(int64_t M, 
   }
 }
 
-// The fp32 block form: whole-contraction 64x64 tiles once they alone give >= 512 blocks,
-// else 32x32 tiles with the contraction split over 8 (K >= 1024) or 4 waves.
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// fp32 GEMM, direct form: the MFMA operands go from memory straight into registers, no
+// LDS stage. Within each 16-k batch the two lane halves take different k: half h supplies
+// k = kc + 8h + s on MFMA step s (the two k slots of v_mfma_f32_32x32x2_f32), so
+//   an MN-contiguous operand is one coalesced dword per lane and step (32 consecutive
+//     floats per half), loaded through a buffer descriptor: an element outside the matrix
+//     or the wave's k range gets an offset past the descriptor's end, which the hardware
+//     returns as 0, so no value select follows a load and nothing waits for one until the
+//     MFMA that reads it;
+//   a K-contiguous operand is 8 consecutive floats per lane: two 16-byte loads when
+//     `vec` says rows are 16-byte aligned and K % 4 == 0 (each 4-run then lies wholly
+//     inside or outside the k range), else 8 dwords through the descriptor.
+// The next batch's loads are in flight during this batch's 8 MFMAs. Block forms as in
+// k_gemm_f32 (KW waves splitting the contraction of a 32x32 tile, or 4 waves of a 64x64
+// tile); the summation order is fixed. Measured at the residual-MLP target's products
+// (2048 rows, d 1000 / 100 / 50) it takes 0.35-0.6x the time of the LDS-staged form: those
+// launches hold one or two waves per SIMD, and the LDS round trip per 16-k chunk was
+// exposed latency there. Each operand must span fewer than 2^31 bytes (checked on the host).
+template <int KW, bool TA, bool TB>
+__global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32_direct(
+    int64_t M, int64_t N, int64_t K, const float* __restrict__ A, int64_t lda, const float* __restrict__ B,
+    int64_t ldb, float* __restrict__ C, int64_t ldc, float alpha, float beta, int64_t sA, int64_t sB, int64_t sC,
+    int32_t bytes_a, int32_t bytes_b, int vec) {
+  constexpr bool SPLIT = KW > 1;
+  constexpr int NWV = SPLIT ? KW : 4, NT = 64 * NWV, S = 8;
+  __shared__ float red[SPLIT ? KW : 1][SPLIT ? FT * FT : 1];
+  A += (int64_t)blockIdx.z * sA;
+  B += (int64_t)blockIdx.z * sB;
+  C += (int64_t)blockIdx.z * sC;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5;
+  const int64_t bt = SPLIT ? FT : 2 * FT;
+  const int64_t m0 = (int64_t)blockIdx.y * bt + (SPLIT ? 0 : (w >> 1) * FT);
+  const int64_t n0 = (int64_t)blockIdx.x * bt + (SPLIT ? 0 : (w & 1) * FT);
+  int kb = 0, ke = (int)K;
+  if (SPLIT) {
+    const int kq = (int)((K + KW * FK - 1) / (KW * FK) * FK);
+    kb = w * kq;
+    ke = kb + kq < ke ? kb + kq : ke;
+  }
+  const uint32_t m = (uint32_t)(m0 + (lane & 31)), n = (uint32_t)(n0 + (lane & 31));
+  const bool mok = m < M, nok = n < N;
+  const uint32_t la = (uint32_t)lda, lb = (uint32_t)ldb;
+  const auto rsa = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), (short)0, bytes_a, 0x00020000);
+  const auto rsb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, bytes_b, 0x00020000);
+  // bit 31 set for an element outside the operand: offsets of in-range elements are < 2^31
+  auto oob = [](bool ok) { return (uint32_t)(!ok) << 31; };
+  auto load = [&](float (&a)[S], float (&b)[S], int kc) {
+    const int k0 = kc + h * S;
+    if (!TA && (vec & 1)) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float4 v = {0.f, 0.f, 0.f, 0.f};
+        if (mok && k0 + 4 * q < ke) v = *(const float4*)(A + (int64_t)m * lda + k0 + 4 * q);
+        a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const uint32_t k = (uint32_t)(k0 + s), e = TA ? k * la + m : m * la + k;
+        a[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, (e * 4u) | oob(mok & (k0 + s < ke)),
+                                                                              0, 0));
+      }
+    }
+    if (TB && (vec & 2)) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float4 v = {0.f, 0.f, 0.f, 0.f};
+        if (nok && k0 + 4 * q < ke) v = *(const float4*)(B + (int64_t)n * ldb + k0 + 4 * q);
+        b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const uint32_t k = (uint32_t)(k0 + s), e = TB ? n * lb + k : k * lb + n;
+        b[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsb, (e * 4u) | oob(nok & (k0 + s < ke)),
+                                                                              0, 0));
+      }
+    }
+  };
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+  auto mma = [&](const float (&a)[S], const float (&b)[S]) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
+  };
+  float a0[S], b0[S], a1[S], b1[S];
+  if (kb < ke) load(a0, b0, kb);
+  for (int kc = kb; kc < ke; kc += 2 * FK) {
+    if (kc + FK < ke) load(a1, b1, kc + FK);
+    mma(a0, b0);
+    if (kc + FK >= ke) break;
+    if (kc + 2 * FK < ke) load(a0, b0, kc + 2 * FK);
+    mma(a1, b1);
+  }
+  // lane holds column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4 of its tile
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) red[w][(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * FT + (lane & 31)] = acc[v];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < FT * FT / NT; ++q) {
+      const int i = q * NT + tid, r = i / FT, c = i % FT;
+      float sum = red[0][i];
+#pragma unroll
+      for (int x = 1; x < KW; ++x) sum += red[x][i];
+      const int64_t gr = m0 + r, gc = n0 + c;
+      if (gr < M && gc < N) C[gr * ldc + gc] = alpha * sum + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+    }
+  } else {
+    const int64_t gc = n0 + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t gr = m0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (gr < M && gc < N) C[gr * ldc + gc] = alpha * acc[v] + (beta != 0.f ? beta * C[gr * ldc + gc] : 0.f);
+    }
+  }
+}
+
+// The fp32 block form. Whole-contraction 64x64 tiles once they alone give >= 512 blocks
+// (direct form up to K = 256, the LDS-staged one beyond), else 32x32 tiles with the
+// contraction split over waves: the direct form with 16 waves from K = 512 on, else 8.
+// The LDS-staged form also serves operands of 2^31 bytes or more.
 template <bool TA, bool TB>
 static void launch_gemm_f32_l(int64_t batch, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
                               const float* B, int64_t ldb, float* C, int64_t ldc, float alpha, float beta, int64_t sA,
                               int64_t sB, int64_t sC, hipStream_t s) {
   const dim3 g32((unsigned)cdiv(N, FT), (unsigned)cdiv(M, FT), (unsigned)batch);
-  if (cdiv(M, 2 * FT) * cdiv(N, 2 * FT) * batch >= 512)
-    hipLaunchKernelGGL((k_gemm_f32<1, TA, TB>),
-                       dim3((unsigned)cdiv(N, 2 * FT), (unsigned)cdiv(M, 2 * FT), (unsigned)batch), dim3(256), 0, s, M,
-                       N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA, sB, sC);
+  const dim3 g64((unsigned)cdiv(N, 2 * FT), (unsigned)cdiv(M, 2 * FT), (unsigned)batch);
+  const int64_t ea = 4 * (TA ? (K - 1) * lda + M : (M - 1) * lda + K);  // bytes one operand spans
+  const int64_t eb = 4 * (TB ? (N - 1) * ldb + K : (K - 1) * ldb + N);
+  const bool direct = ea < (int64_t(1) << 31) && eb < (int64_t(1) << 31);
+  const bool big = cdiv(M, 2 * FT) * cdiv(N, 2 * FT) * batch >= 512;
+  if (direct && (!big || K <= 256)) {
+    const bool v4 = K % 4 == 0;
+    const int vec = (!TA && v4 && lda % 4 == 0 && sA % 4 == 0 && aligned16(A) ? 1 : 0) |
+                    (TB && v4 && ldb % 4 == 0 && sB % 4 == 0 && aligned16(B) ? 2 : 0);
+#define PD_FD(KW_, G_)                                                                                               \
+  hipLaunchKernelGGL((k_gemm_f32_direct<KW_, TA, TB>), G_, dim3(KW_ > 1 ? 64 * KW_ : 256), 0, s, M, N, K, A, lda, B, \
+                     ldb, C, ldc, alpha, beta, sA, sB, sC, (int32_t)ea, (int32_t)eb, vec)
+    if (big) PD_FD(1, g64);
+    else if (K >= 512) PD_FD(16, g32);
+    else PD_FD(8, g32);
+#undef PD_FD
+  } else if (big)
+    hipLaunchKernelGGL((k_gemm_f32<1, TA, TB>), g64, dim3(256), 0, s, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA,
+                       sB, sC);
   else if (K >= 1024)
     hipLaunchKernelGGL((k_gemm_f32<8, TA, TB>), g32, dim3(512), 0, s, M, N, K, A, lda, B, ldb, C, ldc, alpha, beta, sA,
                        sB, sC);
@@ -362,8 +499,6 @@ __global__ void k_zero_tail_rows(const int32_t* __restrict__ offsets, int E, int
       ((bf16_t*)out)[start * width + i] = 0;
   }
 }
-
-static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <class CFG, int MODE>
 static int launch_bf16(const GemmArgs& a, bool a_kmaj, bool b_kmaj, int c_dtype, dim3 grid, hipStream_t s) {

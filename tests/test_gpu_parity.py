@@ -280,6 +280,30 @@ def test_gemm_bf16_padded_leading_dims(device, ta, tb):
     assert torch.all(C[:, N:] == 7.0)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1), (0, 0)])
+@pytest.mark.parametrize("M,N,K", [(264, 200, 328), (70, 90, 1200), (40, 33, 3002)])
+@pytest.mark.parametrize("pad,off", [(24, 0), (3, 1)])
+def test_gemm_fp32_padded_and_offset(device, ta, tb, M, N, K, pad, off):
+    """fp32 operands inside wider tensors: padded leading dimensions, and (off = 1) base
+    pointers and leading dimensions that are not 16-byte multiples, where the direct form
+    reads K-contiguous rows as dwords instead of 16-byte vectors; contraction split over 8
+    and 16 waves, K % 4 != 0 at K = 3002."""
+    from param_decomp_amd import _lib as L
+
+    rng = np.random.default_rng(M + N + K + 2 * ta + tb + pad)
+    A = f32(rng.normal(size=(K, M + pad) if ta else (M, K + pad)), device)
+    B = f32(rng.normal(size=(N, K + pad) if tb else (K, N + pad)), device)
+    C = torch.full((M, N + 8), 7.0, dtype=torch.float32, device=device)
+    L.call("pd_gemm", L.F32, M, N, K, L.ptr(A) + 4 * off, A.shape[1], ta, L.ptr(B) + 4 * off, B.shape[1], tb, L.ptr(C),
+           N + 8, L.F32,
+           1.0, 0.0, L.stream())
+    a, b = np64(A)[:, off:], np64(B)[:, off:]
+    a = a[:, :M].T if ta else a[:, :K]
+    b = b[:, :K].T if tb else b[:, :N]
+    assert_close(np64(C)[:, :N], a @ b, 1e-5, 1e-6, f"padded fp32 gemm ta={ta} tb={tb} pad={pad} off={off}")
+    assert torch.all(C[:, N:] == 7.0)
+
+
 def test_gemm_alpha_beta_and_fp32(device):
     from param_decomp_amd import ops
 
