@@ -82,6 +82,13 @@ int pd_component_mask_fwd(const void* ci, int dtype, int64_t n, uint32_t k0, uin
 /* d_ci = g_mask * (1 - u). */
 int pd_component_mask_bwd(const void* g_mask, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype,
                           int layout, void* d_ci, void* stream);
+/* The same two with the key in device memory (two uint32 words, read when the kernel
+ * runs): the form a captured graph replays with a fresh key per step, written into that
+ * buffer before each replay (pd/core/masking.py:135-136 as above). */
+int pd_component_mask_fwd_dkey(const void* ci, int dtype, int64_t n, const uint32_t* key, int draw_dtype,
+                               int layout, void* mask, void* stream);
+int pd_component_mask_bwd_dkey(const void* g_mask, int dtype, int64_t n, const uint32_t* key, int draw_dtype,
+                               int layout, void* d_ci, void* stream);
 
 /* ---- per-component gate MLP (paper form, spd_paper.md appendix; engine GELU is exact
  *      erf, pd/core/ci_fn/implementations/mlp.py:77):

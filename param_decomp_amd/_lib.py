@@ -35,6 +35,8 @@ _SIGNATURES = {
     "pd_squash_bwd": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i64, _c_p, _c_p]),
     "pd_component_mask_fwd": (_c_i32, [_c_p, _c_i32, _c_i64, _c_u32, _c_u32, _c_i32, _c_i32, _c_p, _c_p]),
     "pd_component_mask_bwd": (_c_i32, [_c_p, _c_i32, _c_i64, _c_u32, _c_u32, _c_i32, _c_i32, _c_p, _c_p]),
+    "pd_component_mask_fwd_dkey": (_c_i32, [_c_p, _c_i32, _c_i64, _c_p, _c_i32, _c_i32, _c_p, _c_p]),
+    "pd_component_mask_bwd_dkey": (_c_i32, [_c_p, _c_i32, _c_i64, _c_p, _c_i32, _c_i32, _c_p, _c_p]),
     "pd_gate_fwd": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p]),
     "pd_gate_bwd_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i32]),
     "pd_gate_bwd": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,

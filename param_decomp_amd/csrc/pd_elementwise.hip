@@ -69,8 +69,12 @@ __global__ void k_squash_bwd(const T* pre, const T* gl, const T* gu, int64_t n, 
 }
 
 // ---------------------------------------------------------------- component mask
+// kd (device key, optional): the key read from device memory at launch time instead of
+// (k0, k1), so a captured graph draws fresh masks on each replay once the key is rewritten.
 template <typename T>
-__global__ void k_mask_fwd(const T* ci, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype, int layout, T* mask) {
+__global__ void k_mask_fwd(const T* ci, int64_t n, uint32_t k0, uint32_t k1, const uint32_t* kd, int draw_dtype,
+                           int layout, T* mask) {
+  if (kd) k0 = kd[0], k1 = kd[1];
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     float g = load_f<T>(ci, i);
     float u = draw_uniform(k0, k1, i, n, draw_dtype, layout);
@@ -79,7 +83,9 @@ __global__ void k_mask_fwd(const T* ci, int64_t n, uint32_t k0, uint32_t k1, int
 }
 
 template <typename T>
-__global__ void k_mask_bwd(const T* gm, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype, int layout, T* dci) {
+__global__ void k_mask_bwd(const T* gm, int64_t n, uint32_t k0, uint32_t k1, const uint32_t* kd, int draw_dtype,
+                           int layout, T* dci) {
+  if (kd) k0 = kd[0], k1 = kd[1];
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     float u = draw_uniform(k0, k1, i, n, draw_dtype, layout);
     store_f<T>(dci, i, load_f<T>(gm, i) * (1.f - u));
@@ -476,24 +482,46 @@ int pd_squash_bwd(const void* pre, const void* gl, const void* gu, int dtype, in
   return check_launch("pd_squash_bwd");
 }
 
-int pd_component_mask_fwd(const void* ci, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype, int layout,
-                          void* mask, void* stream) {
-  if (n < 0 || !ci || !mask) return fail(PD_EINVAL, "pd_component_mask_fwd: bad args");
+static int mask_fwd(const void* ci, int dtype, int64_t n, uint32_t k0, uint32_t k1, const uint32_t* kd,
+                    int draw_dtype, int layout, void* mask, void* stream, const char* who) {
+  if (n < 0 || !ci || !mask) return fail(PD_EINVAL, std::string(who) + ": bad args");
   if (n == 0) return PD_OK;
   PD_DISPATCH_DTYPE(dtype, T,
                     hipLaunchKernelGGL(k_mask_fwd<T>, dim3(ew_blocks(n)), dim3(EW_THREADS), 0, (hipStream_t)stream,
-                                       (const T*)ci, n, k0, k1, draw_dtype, layout, (T*)mask));
-  return check_launch("pd_component_mask_fwd");
+                                       (const T*)ci, n, k0, k1, kd, draw_dtype, layout, (T*)mask));
+  return check_launch(who);
+}
+
+static int mask_bwd(const void* gm, int dtype, int64_t n, uint32_t k0, uint32_t k1, const uint32_t* kd,
+                    int draw_dtype, int layout, void* dci, void* stream, const char* who) {
+  if (n < 0 || !gm || !dci) return fail(PD_EINVAL, std::string(who) + ": bad args");
+  if (n == 0) return PD_OK;
+  PD_DISPATCH_DTYPE(dtype, T,
+                    hipLaunchKernelGGL(k_mask_bwd<T>, dim3(ew_blocks(n)), dim3(EW_THREADS), 0, (hipStream_t)stream,
+                                       (const T*)gm, n, k0, k1, kd, draw_dtype, layout, (T*)dci));
+  return check_launch(who);
+}
+
+int pd_component_mask_fwd(const void* ci, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype, int layout,
+                          void* mask, void* stream) {
+  return mask_fwd(ci, dtype, n, k0, k1, nullptr, draw_dtype, layout, mask, stream, "pd_component_mask_fwd");
 }
 
 int pd_component_mask_bwd(const void* gm, int dtype, int64_t n, uint32_t k0, uint32_t k1, int draw_dtype, int layout,
                           void* dci, void* stream) {
-  if (n < 0 || !gm || !dci) return fail(PD_EINVAL, "pd_component_mask_bwd: bad args");
-  if (n == 0) return PD_OK;
-  PD_DISPATCH_DTYPE(dtype, T,
-                    hipLaunchKernelGGL(k_mask_bwd<T>, dim3(ew_blocks(n)), dim3(EW_THREADS), 0, (hipStream_t)stream,
-                                       (const T*)gm, n, k0, k1, draw_dtype, layout, (T*)dci));
-  return check_launch("pd_component_mask_bwd");
+  return mask_bwd(gm, dtype, n, k0, k1, nullptr, draw_dtype, layout, dci, stream, "pd_component_mask_bwd");
+}
+
+int pd_component_mask_fwd_dkey(const void* ci, int dtype, int64_t n, const uint32_t* key, int draw_dtype, int layout,
+                               void* mask, void* stream) {
+  if (!key) return fail(PD_EINVAL, "pd_component_mask_fwd_dkey: null key");
+  return mask_fwd(ci, dtype, n, 0, 0, key, draw_dtype, layout, mask, stream, "pd_component_mask_fwd_dkey");
+}
+
+int pd_component_mask_bwd_dkey(const void* gm, int dtype, int64_t n, const uint32_t* key, int draw_dtype, int layout,
+                               void* dci, void* stream) {
+  if (!key) return fail(PD_EINVAL, "pd_component_mask_bwd_dkey: null key");
+  return mask_bwd(gm, dtype, n, 0, 0, key, draw_dtype, layout, dci, stream, "pd_component_mask_bwd_dkey");
 }
 
 int pd_gate_fwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const float* w_in, const float* b_in,

@@ -70,13 +70,16 @@ class _ImpMin(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_act, g_freq):
         (ci,) = ctx.saved_tensors
-        kw = dict(ctx.kw)
-        # device scalars -> host coefficients (the backward is outside the hot loop of
-        # the fused steps, which call the C ABI directly)
-        kw["coeff_act"] = float(g_act) if g_act is not None else 0.0
-        kw["coeff_freq"] = float(g_freq) if g_freq is not None else 0.0
-        _, grad = ops.impmin(ci.contiguous(), want_grad=True, **kw)
-        return grad, None
+        # the gradient of each term at unit coefficient, scaled by the upstream device
+        # scalar: no host read of g_act / g_freq, so the backward can be graph-captured
+        grad = None
+        for g, unit in ((g_act, dict(coeff_act=1.0, coeff_freq=0.0)), (g_freq, dict(coeff_act=0.0, coeff_freq=1.0))):
+            if g is None or (unit["coeff_freq"] and ctx.kw["kind"] != L.IMPMIN_SMOOTH_L0):
+                continue  # only the smooth-L0 form has a frequency term
+            _, d = ops.impmin(ci.contiguous(), want_grad=True, **dict(ctx.kw, **unit))
+            d = d * g.to(d.dtype)
+            grad = d if grad is None else grad + d
+        return (grad if grad is not None else torch.zeros_like(ci)), None
 
 
 def importance_minimality_terms(ci_upper: dict, gamma: float, reference_datapoint_count: int | None, *,

@@ -33,18 +33,20 @@ def uniform_like(key: Key, reference: torch.Tensor, *, drop_last_axis: bool = Fa
 
 class _ComponentMask(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, ci, k0, k1):
-        ctx.key = (k0, k1)
+    def forward(ctx, ci, key):
+        ctx.key = key
         ctx.draw_dtype = ci.dtype
-        return ops.component_mask_fwd(ci.contiguous(), (k0, k1), ci.dtype, LAYOUT)
+        return ops.component_mask_fwd(ci.contiguous(), key, ci.dtype, LAYOUT)
 
     @staticmethod
     def backward(ctx, g):
-        return ops.component_mask_bwd(g.contiguous(), ctx.key, ctx.draw_dtype, LAYOUT), None, None
+        return ops.component_mask_bwd(g.contiguous(), ctx.key, ctx.draw_dtype, LAYOUT), None
 
 
-def sample_component_mask(ci: torch.Tensor, key: Key) -> torch.Tensor:
-    return _ComponentMask.apply(ci, key[0], key[1])
+def sample_component_mask(ci: torch.Tensor, key) -> torch.Tensor:
+    """`key`: a host pair, or a device tensor of two 32-bit words that the mask kernels read
+    when they run (what a captured graph rewrites before each replay)."""
+    return _ComponentMask.apply(ci, key if isinstance(key, torch.Tensor) else (int(key[0]), int(key[1])))
 
 
 def sample_delta_mask(ci: torch.Tensor, key: Key) -> torch.Tensor:

@@ -41,17 +41,35 @@ def squash_bwd(pre, g_lower, g_upper):
     return d
 
 
-def component_mask_fwd(ci, key: Key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
+def _device_key(key) -> bool:
+    """A key given as a device tensor of two 32-bit words (read when the kernel runs: the
+    form a captured graph replays with fresh keys) rather than a host pair."""
+    if isinstance(key, torch.Tensor):
+        if key.dtype not in (torch.int32, torch.uint32) or key.numel() != 2 or not key.is_cuda:
+            raise L.PDError("a device key is a CUDA tensor of two 32-bit words")
+        return True
+    return False
+
+
+def component_mask_fwd(ci, key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
     m = torch.empty_like(ci)
-    L.call("pd_component_mask_fwd", L.ptr(ci), L.dtype_code(ci.dtype), ci.numel(), key[0], key[1],
-           L.dtype_code(draw_dtype), layout, L.ptr(m), L.stream())
+    if _device_key(key):
+        L.call("pd_component_mask_fwd_dkey", L.ptr(ci), L.dtype_code(ci.dtype), ci.numel(), L.ptr(key),
+               L.dtype_code(draw_dtype), layout, L.ptr(m), L.stream())
+    else:
+        L.call("pd_component_mask_fwd", L.ptr(ci), L.dtype_code(ci.dtype), ci.numel(), key[0], key[1],
+               L.dtype_code(draw_dtype), layout, L.ptr(m), L.stream())
     return m
 
 
-def component_mask_bwd(g_mask, key: Key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
+def component_mask_bwd(g_mask, key, draw_dtype: torch.dtype, layout=L.LAYOUT_PARTITIONABLE):
     d = torch.empty_like(g_mask)
-    L.call("pd_component_mask_bwd", L.ptr(g_mask), L.dtype_code(g_mask.dtype), g_mask.numel(), key[0], key[1],
-           L.dtype_code(draw_dtype), layout, L.ptr(d), L.stream())
+    if _device_key(key):
+        L.call("pd_component_mask_bwd_dkey", L.ptr(g_mask), L.dtype_code(g_mask.dtype), g_mask.numel(), L.ptr(key),
+               L.dtype_code(draw_dtype), layout, L.ptr(d), L.stream())
+    else:
+        L.call("pd_component_mask_bwd", L.ptr(g_mask), L.dtype_code(g_mask.dtype), g_mask.numel(), key[0], key[1],
+               L.dtype_code(draw_dtype), layout, L.ptr(d), L.stream())
     return d
 
 

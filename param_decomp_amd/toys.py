@@ -174,15 +174,22 @@ class ToyDecompositionStep:
         for s in self.sites:
             for prm in s.parameters():
                 prm.grad = None
+        mask_key, delta_key = prng.split(draw_key)
+        n = len(self.sites)
+        deltas = [prng.fold_in(delta_key, i) for i in range(n)] if self.use_delta else None
+        return self._body(x, [prng.fold_in(mask_key, i) for i in range(n)], deltas, routes)
+
+    def _body(self, x, mask_keys, delta_keys, routes) -> dict:
+        """The step given each site's mask key (host pairs, or device key tensors) and
+        delta key (host pairs or None)."""
         clean, cin = clean_forward(self.target, self.sites, x)
         g = [s.gate(product(cin[i], s.V)) for i, s in enumerate(self.sites)]
         lower = [lower_leaky_hard_sigmoid(a) for a in g]
         upper = {s.name: upper_leaky_hard_sigmoid(a) for s, a in zip(self.sites, g)}
-        mask_key, delta_key = prng.split(draw_key)
-        masks = [masking.sample_component_mask(lo, prng.fold_in(mask_key, i)) for i, lo in enumerate(lower)]
+        masks = [masking.sample_component_mask(lo, mask_keys[i]) for i, lo in enumerate(lower)]
         deltas = None
-        if self.use_delta:
-            deltas = [masking.sample_delta_mask(lo, prng.fold_in(delta_key, i)) for i, lo in enumerate(lower)]
+        if delta_keys is not None:
+            deltas = [masking.sample_delta_mask(lo, delta_keys[i]) for i, lo in enumerate(lower)]
         out = masked_forward(self.target, self.sites, x, masks, deltas, routes)
         recon = losses.mse(out, clean)
         imp = losses.importance_minimality_pnorm(upper, self.p)
@@ -190,6 +197,64 @@ class ToyDecompositionStep:
         loss.backward()
         return {"loss": loss.detach(), "recon": recon.detach(), "imp": imp.detach(), "out": out.detach(),
                 "clean": clean, "g_raw": [a.detach() for a in g]}
+
+
+class GraphedToyStep:
+    """`ToyDecompositionStep` captured once into a HIP graph and replayed every step: the
+    host launches one graph instead of ~90 kernels through autograd (at the ResidMLP-1L
+    shape the eager step is bound by that host work, not by its GPU time).
+
+    Each step writes that step's per-site mask keys (`fold_in(split(draw_key)[0], site)`)
+    into a device buffer the mask kernels read when they run, and copies the batch into the
+    captured input buffer, so a replay draws that step's masks over that step's batch; the
+    kernels and their order are those of the eager step, so results are bit-identical to
+    it. The returned tensors and the parameters' `.grad` are the graph's own buffers,
+    overwritten by the next step. Not for the weight-delta channel or routes (their draws
+    take host keys)."""
+
+    def __init__(self, step: ToyDecompositionStep, x_example: torch.Tensor, *, warmup: int = 2):
+        if step.use_delta:
+            raise ValueError("GraphedToyStep: the weight-delta channel draws with host keys")
+        self.inner, self.warmup = step, warmup
+        self.x = x_example.detach().clone()
+        self.keys = torch.zeros((len(step.sites), 2), dtype=torch.int32, device=self.x.device)
+        self.params = [prm for s in step.sites for prm in s.parameters()]
+        self.graph = None
+
+    def _set_keys(self, draw_key: Key):
+        import numpy as np
+
+        mask_key, _ = prng.split(draw_key)
+        ks = np.array([prng.fold_in(mask_key, i) for i in range(len(self.inner.sites))], dtype=np.uint32)
+        self.keys.copy_(torch.from_numpy(ks.view(np.int32)))  # stream-ordered after the last replay
+
+    def _capture(self):
+        keys = [self.keys[i] for i in range(self.keys.shape[0])]
+        side = torch.cuda.Stream(device=self.x.device)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # autograd's own set-up happens outside the capture
+            for _ in range(self.warmup):
+                for prm in self.params:
+                    prm.grad = None
+                self.inner._body(self.x, keys, None, None)
+        torch.cuda.current_stream().wait_stream(side)
+        for prm in self.params:
+            prm.grad = None
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = self.inner._body(self.x, keys, None, None)
+        self.grads = [prm.grad for prm in self.params]
+
+    def step(self, x: torch.Tensor, draw_key: Key) -> dict:
+        self._set_keys(draw_key)
+        if x is not self.x:
+            self.x.copy_(x)
+        if self.graph is None:
+            self._capture()
+        self.graph.replay()
+        for prm, gr in zip(self.params, self.grads):
+            prm.grad = gr
+        return self.out
 
 
 class TMSFusedStep:
