@@ -251,6 +251,24 @@ __device__ inline float wave_max(float v) {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// sum_{k < n} p[k * stride] added in k order (a deterministic reduction of per-chunk
+// partials). The loads of 64 chunks are issued before their adds: with one dependent load
+// per chunk such a pass is bound by n round trips to L2.
+__device__ inline float pd_ordered_sum(const float* __restrict__ p, int64_t n, int64_t stride) {
+  constexpr int Q = 64;
+  float s = 0.f;
+  int64_t k = 0;
+  for (; k + Q <= n; k += Q) {
+    float v[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) v[i] = p[(k + i) * stride];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) s += v[i];
+  }
+  for (; k < n; ++k) s += p[k * stride];
+  return s;
+}
+
 // jax.random.split(key, 2) on the host: out = {key0.x0, key0.x1, key1.x0, key1.x1}.
 // partitionable: key i = block(key, (0, i)); original: the block outputs of the counter
 // pairs (0, 2) and (1, 3), concatenated word-wise and read as [2, 2].

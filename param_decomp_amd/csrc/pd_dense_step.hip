@@ -423,8 +423,7 @@ __global__ void k_step_gate_reduce(const float* __restrict__ partial, int64_t ch
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= 49 * C) return;
   const int64_t q = idx / C, c = idx % C;
-  float acc = 0.f;
-  for (int64_t k = 0; k < chunks; ++k) acc += partial[k * 49 * C + idx];
+  const float acc = pd_ordered_sum(partial + idx, chunks, 49 * C);
   if (q < 16)
     dw_in[c * 16 + q] = acc;
   else if (q < 32)

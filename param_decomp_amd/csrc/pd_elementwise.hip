@@ -180,27 +180,13 @@ __global__ __launch_bounds__(GATE_COLS) void k_gate_bwd(const T* __restrict__ h,
 
 // sum_{k < n} p[k * stride] added in k order; loads go out 16 at a time so a long chunk
 // list is not one serial chain of load latencies.
-__device__ inline float ordered_sum(const float* __restrict__ p, int64_t n, int64_t stride) {
-  float s = 0.f;
-  int64_t k = 0;
-  for (; k + 16 <= n; k += 16) {
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = p[(k + i) * stride];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s += v[i];
-  }
-  for (; k < n; ++k) s += p[k * stride];
-  return s;
-}
-
 __global__ void k_gate_bwd_reduce(const float* __restrict__ partial, int64_t chunks, int64_t C,
                                   float* __restrict__ dw_in, float* __restrict__ db_in, float* __restrict__ dw_out,
                                   float* __restrict__ db_out) {
   int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over 49*C
   if (idx >= 49 * C) return;
   int64_t q = idx / C, c = idx % C;
-  const float s = ordered_sum(partial + idx, chunks, 49 * C);
+  const float s = pd_ordered_sum(partial + idx, chunks, 49 * C);
   if (q < 16)
     dw_in[c * 16 + q] = s;
   else if (q < 32)
@@ -262,7 +248,7 @@ __global__ void k_imp_colsum_partial(const T* __restrict__ ci, int64_t rows, int
 __global__ void k_colsum_final(const float* __restrict__ partial, int64_t chunks, int64_t C, float* __restrict__ colsum) {
   int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
-  colsum[c] = ordered_sum(partial + c, chunks, C);
+  colsum[c] = pd_ordered_sum(partial + c, chunks, C);
 }
 
 // per-column slope dL/ds_c of the imp-min objective in terms of the column sum s_c

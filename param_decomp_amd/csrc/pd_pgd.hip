@@ -95,9 +95,7 @@ __global__ void k_source_grad_reduce(const float* __restrict__ part, int64_t n_s
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_src * C) return;
   const int64_t sr = i / C, c = i % C;
-  float acc = 0.f;
-  for (int64_t k = 0; k < chunks; ++k) acc += part[(sr * chunks + k) * C + c];
-  d_src[i] = acc;
+  d_src[i] = pd_ordered_sum(part + sr * chunks * C + c, chunks, C);
 }
 
 // ---- vector forms (C % 8 == 0, 16-byte aligned operands): 8 columns per lane.
