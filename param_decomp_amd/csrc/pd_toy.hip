@@ -18,7 +18,7 @@
 // the output pre-activation, the hidden's cotangent) go through LDS in component order.
 // A block is 16 rows x 20 components (5 waves, 256 blocks at B = 4096); each gradient slot
 // is summed over the block's rows in row order into a per-block partial, and
-// k_tms_reduce adds the blocks' partials in block order, so the result is deterministic.
+// k_tms_reduce adds the blocks' partials in a fixed order, so the result is deterministic.
 #include <algorithm>
 #include <type_traits>
 
@@ -298,36 +298,44 @@ __global__ __launch_bounds__(TMS_RS * C) void k_tms_step(TmsArgs a, int iters) {
   }
 }
 
-// Column i of the [nblk, P] partials summed in block order (double). The loads of 64
-// blocks are issued before their adds: one dependent load per block left the kernel
-// bound by ~nblk round trips to L2 (79 us at 256 blocks; 14 us with 16 loads in flight).
-__device__ inline double tms_colsum(const float* __restrict__ partial, int nblk, int P, int i) {
+// Column i of partials [b0, b1) of the [nblk, P] partials, in block order (double), the
+// loads of 64 blocks issued before their adds.
+__device__ inline double tms_colsum(const float* __restrict__ partial, int b0, int b1, int P, int i) {
   constexpr int Q = 64;
   double acc = 0.0;
-  int b = 0;
-  for (; b + Q <= nblk; b += Q) {
+  int b = b0;
+  for (; b + Q <= b1; b += Q) {
     float v[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) v[q] = partial[(int64_t)(b + q) * P + i];
 #pragma unroll
     for (int q = 0; q < Q; ++q) acc += v[q];
   }
-  for (; b < nblk; ++b) acc += partial[(int64_t)b * P + i];
+  for (; b < b1; ++b) acc += partial[(int64_t)b * P + i];
   return acc;
 }
 
-// grads[i] = sum over blocks of partial[b][i] in block order; losses = {loss, recon, imp}.
+// grads[i] = sum over blocks of partial[b][i]; losses = {loss, recon, imp}. Four
+// consecutive lanes take one slot, each summing a quarter of the blocks in block order,
+// and the quarters are added in order ((q0 + q1) + q2) + q3 (double): a fixed order, so
+// the result is deterministic, with a quarter of the dependent round trips of one lane
+// per slot (one lane per slot, one dependent load per block: 79 us at 256 blocks).
 __global__ __launch_bounds__(256) void k_tms_reduce(const float* __restrict__ partial, int nblk, int P, int64_t B,
                                                     int F, float imp_coeff, float recon_coeff,
                                                     float* __restrict__ grads, float* __restrict__ losses) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= P) return;
-  const double acc = tms_colsum(partial, nblk, P, i);
+  const int i = blockIdx.x * 64 + (threadIdx.x >> 2), part = threadIdx.x & 3, lead = threadIdx.x & ~3;
+  const int per = (nblk + 3) / 4, b0 = min(nblk, part * per), b1 = min(nblk, b0 + per);
+  const bool last = i == P - 1;  // the imp sum: the last entry; the recon sum precedes it
+  const double acc = i < P ? tms_colsum(partial, b0, b1, P, i) : 0.0;
+  const double rec = last ? tms_colsum(partial, b0, b1, P, P - 2) : 0.0;
+  const double a1 = __shfl(acc, lead + 1), a2 = __shfl(acc, lead + 2), a3 = __shfl(acc, lead + 3);
+  const double r1 = __shfl(rec, lead + 1), r2 = __shfl(rec, lead + 2), r3 = __shfl(rec, lead + 3);
+  if (part != 0 || i >= P) return;
+  const double total = ((acc + a1) + a2) + a3;
   if (i < P - 2) {
-    grads[i] = (float)acc;
-  } else if (i == P - 1) {  // the imp sum: the last entry; the recon sum precedes it
-    const double rec = tms_colsum(partial, nblk, P, P - 2);
-    const double recon = rec / (double)(B * F), impv = acc / (double)B;
+    grads[i] = (float)total;
+  } else if (last) {
+    const double recon = (((rec + r1) + r2) + r3) / (double)(B * F), impv = total / (double)B;
     losses[0] = (float)(recon_coeff * recon + imp_coeff * impv);
     losses[1] = (float)recon;
     losses[2] = (float)impv;
@@ -345,7 +353,7 @@ static int launch_tms(const TmsArgs& a, float* grads, float* losses, size_t ws_b
   const int nblk = (int)tms_blocks(a.B);
   if (ws_bytes < (size_t)nblk * LY::P * sizeof(float)) return fail(PD_EWORKSPACE, "pd_tms_step: workspace too small");
   hipLaunchKernelGGL((k_tms_step<F, H, C>), dim3((unsigned)nblk), dim3(TMS_RS * C), 0, s, a, tms_iters(a.B));
-  hipLaunchKernelGGL(k_tms_reduce, dim3((unsigned)cdiv(LY::P, 256)), dim3(256), 0, s, a.partial, nblk, LY::P, a.B, F,
+  hipLaunchKernelGGL(k_tms_reduce, dim3((unsigned)cdiv(LY::P, 64)), dim3(256), 0, s, a.partial, nblk, LY::P, a.B, F,
                      a.imp_coeff, a.recon_coeff, grads, losses);
   return check_launch("pd_tms_step");
 }
