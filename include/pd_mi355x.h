@@ -18,8 +18,15 @@
  *    same priority, one per device, created with its events on the first call on that
  *    device (make that first call outside any stream capture); the helper stream waits
  *    on `stream` before it starts and `stream` waits on it before the call's last work,
- *    so anything later enqueued on `stream` sees every output. Calls that overlap on one
- *    device race, as two calls sharing a workspace do.
+ *    so anything later enqueued on `stream` sees every output.
+ *  - Threading: every entry point is reentrant. Host threads may call any of them at the
+ *    same time, on one device or several, each with its own stream, outputs and
+ *    workspace. The stack steps hold a per-device lock while they enqueue (never while
+ *    the GPU runs), so concurrent stack-step calls on one device enqueue one after
+ *    another and their helper-stream work runs in that order; each call's results are
+ *    those of the call alone. Calls that share an output or a workspace, and calls of
+ *    pd_masked_linear_bwd_noalloc on one device (one shared scratch region), must be
+ *    ordered by the caller.
  *  - Return PD_OK (0) or a PD_E* code; pd_last_error() gives the message (thread-local).
  *    Invalid shapes are rejected on the host before any launch.
  *  - Random keys are JAX threefry2x32 key words (k0, k1) as jax.random.PRNGKey /
@@ -107,11 +114,14 @@ int pd_gate_bwd(const void* h, int dtype, int64_t rows, int64_t C, int H, const 
  *      world_size); PD_IMPMIN_SMOOTH_L0 uses gamma, normalize_at_one and, when
  *      ref_count > 0, the frequency term. out[0] = activity, out[1] = frequency term
  *      (fp32, overwritten). grad (nullable, dtype of ci) = coeff_act*d act/d ci +
- *      coeff_freq*d freq/d ci. ---- */
+ *      coeff_freq*d freq/d ci. freq_ema_in (nullable, fp32 [C]): the frequency term
+ *      reads the EMA estimate instead of the batch's (the rule under pd_dense_step;
+ *      out[2] = the batch penalty; freq_ema_out [C] receives the new estimate). ---- */
 size_t pd_impmin_workspace_size(int64_t rows, int64_t C);
 int pd_impmin(const void* ci_upper, int dtype, int64_t rows, int64_t C, int kind, float p, float eps, float beta,
-              float world_size, float gamma, int normalize_at_one, float ref_count, float coeff_act,
-              float coeff_freq, float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream);
+              float world_size, float gamma, int normalize_at_one, float ref_count, const float* freq_ema_in,
+              float* freq_ema_out, float ema_count, float ema_halflife, float coeff_act, float coeff_freq, float* out,
+              void* grad, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- recon losses ----
  * MSE: pd/targets/tms.py:380-388, pd/targets/resid_mlp.py:411-418: mean((a-b)^2).
@@ -225,15 +235,28 @@ int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_
  * pd/core/objective.py:101-131; ref_count 0 = no frequency term).
  * Gradients (overwritten, fp32 for the fp32 masters): dV [d_in,C], dU [C,d_out], gate grads.
  * losses[4] = {loss, recon, activity, frequency} fp32. mask_key / delta_key are the site's
- * keys (already split/folded). dtype bf16: x,W,V,U bf16. */
+ * keys (already split/folded). dtype bf16: x,W,V,U bf16.
+ * The EMA frequency estimate (this and every fused step; pd/core/losses.py:425-458,
+ * EmaFrequency :522-543, ema_halflife_steps pd/core/configs.py:165-182): freq_ema_in NULL
+ * is the single-batch estimate above. Otherwise (smooth-L0 with ref_count > 0 only) each
+ * component's estimate becomes new = in + alpha (f_c - in) and the frequency term reads
+ * f_hat = new / debias, alpha = -expm1(-ln 2 / ema_halflife), debias = -expm1(-ln 2 /
+ * ema_halflife * (ema_count + 1)) (ema_count = earlier observations >= 0, ema_halflife in
+ * (0, 1e6]): value sum Phi(f_hat), CI gradient freq_coeff Phi'(f_hat) df_c (the
+ * reference's first-order surrogate; no gradient reaches the estimate); losses then has a
+ * fifth entry, the batch penalty sum Phi(f_c) (EmaFrequencyPenalty.batch_value), and
+ * freq_ema_out (nullable, may equal freq_ema_in) receives new. Estimate layouts: dense
+ * step [C]; MoE stack [L, 3, E*c] (site order gate, up, down; expert-major components);
+ * LM stack [L][kind][C_kind], layer-major, kinds in KIND_ORDER. */
 size_t pd_dense_step_workspace_size(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H);
 int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x, const void* W,
                   const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
                   const float* b_out, uint32_t mask_k0, uint32_t mask_k1, uint32_t delta_k0, uint32_t delta_k1,
-                  int use_delta, int draw_dtype, int layout, int imp_kind, float p, float gamma,
-                  int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count, float recon_coeff,
-                  float* losses, float* dV, float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out,
-                  void* workspace, size_t workspace_bytes, void* stream);
+                  int use_delta, int draw_dtype, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                  float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
+                  float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dV, float* dU,
+                  float* dw_in, float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes,
+                  void* stream);
 
 /* pd_dense_step with phase timing for measurement harnesses: `events` holds
  * PD_DENSE_STEP_PHASES + 1 hipEvent_t handles recorded on `stream` at the phase
@@ -244,12 +267,13 @@ int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, 
 #define PD_DENSE_STEP_PHASES 12
 int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
-                        const float* w_out, const float* b_out, uint32_t mask_k0, uint32_t mask_k1,
-                        uint32_t delta_k0, uint32_t delta_k1, int use_delta, int draw_dtype, int layout,
-                        int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff, float freq_coeff,
-                        float ref_count, float recon_coeff, float* losses, float* dV, float* dU, float* dw_in,
-                        float* db_in, float* dw_out, float* db_out, void* workspace, size_t workspace_bytes,
-                        void* stream, void** events);
+                        const float* w_out, const float* b_out, uint32_t mask_k0, uint32_t mask_k1, uint32_t delta_k0,
+                        uint32_t delta_k1, int use_delta, int draw_dtype, int layout, int imp_kind, float p,
+                        float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                        const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                        float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
+                        float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
+                        void** events);
 
 /* ---- site routing samplers: pd/core/recon.py:218-252 (which sites take the decomposed
  *      output at each position; AllRouting = no routes array). routes: uint8
@@ -335,7 +359,7 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
  * log2(1 + ref_count f_c), f_c = sum psi(upper) / T over the site's [E*c] components
  * (values scattered to their expert's block, pd/core/losses.py:316-330), psi =
  * c^2/(c^2 + gamma^2) (times 1 + gamma^2 when normalize_at_one); ref_count = 0 drops
- * the frequency term (the single-batch estimate: no EMA state).
+ * the frequency term; freq_ema_in as under pd_dense_step ([L, 3, E*c]).
  * Layouts (all bf16 unless noted): x0 [T,d]; ln fp32 [L,d]; router [L,E,d];
  * Wg, Wu [L,E,d,f]; Wd [L,E,f,d]; Vg, Vu [L,E,d,c]; Ug, Uu [L,E,c,f]; Vd [L,E,f,c];
  * Ud [L,E,c,d]; ci_pre [L,3,T,k,c] (site order gate, up, down; slot s = the token's
@@ -351,7 +375,8 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                       const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
                       int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
-                      float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dVg, float* dUg,
+                      float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
+                      float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg, float* dUg,
                       float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                       void* workspace, size_t workspace_bytes, void* stream);
 /* pd_moe_stack_step with persistent (adversarial) source tables in place of the draws:
@@ -383,6 +408,7 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
                               const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
                               int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
                               int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                              const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                               float recon_coeff, int want_weight_grads, int reuse_clean, float* losses, float* dVg,
                               float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
                               float* d_src, float* d_src_delta, int32_t* top_idx_out, void* workspace,
@@ -395,13 +421,13 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
-                            float source_value, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                            float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, float* losses,
-                            float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
-                            int32_t* top_idx_out,
-                            void* workspace, size_t workspace_bytes, void* stream, void** events,
-                            int32_t* categories, int capacity, int* n_recorded);
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
+                            int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
+                            float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
+                            float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg,
+                            float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                            int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream,
+                            void** events, int32_t* categories, int capacity, int* n_recorded);
 
 /* ---- the TMS toy decomposition step as one fused launch (pd/targets/tms.py:254-388) ----
  * target hid = x W1^T, out = relu(hid W1 + b2); both sites (linear1: W1 [H,F], linear2:
@@ -437,7 +463,7 @@ int pd_tms_step(int64_t B, int F, int H, int C, const float* x, const float* W1,
  * imp-min term: PD_IMPMIN_PNORM: imp_coeff * sum_sites sum_c mean_tokens upper(ci)^p;
  * PD_IMPMIN_SMOOTH_L0: imp_coeff * sum_sites sum_c f_c + freq_coeff * sum f_c log2(1 +
  * ref_count f_c), f_c = mean_tokens psi(upper) (as pd_moe_stack_step, one component
- * block per site).
+ * block per site); freq_ema_in as under pd_dense_step ([L][kind][C_kind]).
  * Shapes: N = B*T tokens (int32 ids [N], T % 64 == 0); head_dim 64 (d = 64 n_head);
  * n_head % n_kv_head == 0; d, d_mlp % 64 == 0; C[6] each % 8 == 0; vocab % n_kl_chunks == 0.
  * wte [vocab, d] bf16 (embedding and head); ln1, ln2 [L, d], norm [d] fp32 (values the
@@ -452,7 +478,8 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
                      int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                     float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, int n_kl_chunks,
+                     float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                     float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, int n_kl_chunks,
                      float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
                      size_t workspace_bytes, void* stream);
 /* pd_lm_stack_step recording HIP events at phase boundaries (categories: 0 per-step weight
@@ -465,6 +492,7 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
                            uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
                            int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                            float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                            void** events, int32_t* categories, int capacity, int* n_recorded);

@@ -293,11 +293,16 @@ def site_keys(draw_key, cfg: LMConfig, kind: str, layer: int, partitionable=True
 
 
 def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
-                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64, imp_min=None):
+                  bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64, imp_min=None,
+                  freq_ema=None, ema_count=0.0):
     """One stochastic-recon KL + imp-min step, forward and backward. The imp-min term is
     L_p (p, imp_coeff) or `imp_min` (a `pd_oracle.ImpMin`; smooth-L0 with the frequency
     penalty as the reference writes it, `pd/core/losses.py:340-394`: per-site means of
-    psi over the tokens, differentiated by autograd).
+    psi over the tokens, differentiated by autograd). `freq_ema[l][kind]` ([C_kind], with
+    `imp_min.ema_halflife`) is the EMA frequency estimate before this step after
+    `ema_count` observations: the frequency term is then the reference's surrogate
+    `Phi(f_hat) + Phi'(f_hat) (f - sg(f))` (`pd/core/losses.py:425-458`), and the result
+    also holds the new estimates (`freq_ema`) and the batch penalty (`freq_batch`).
 
     params: wte [V, d] (the embedding and the tied head), norm [d], layers: list of
     dicts (ln1, ln2, W_<kind> [d_out, d_in], V_<kind> [d_in, C], U_<kind> [C, d_out])
@@ -328,6 +333,8 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
     masks, deltas, pres, us, ds = [], [], {}, {}, {}
     imp = torch.zeros((), dtype=dtype)
     freq = torch.zeros((), dtype=dtype)
+    freq_batch = 0.0
+    new_ema = None if freq_ema is None else [{} for _ in range(cfg.n_layers)]
     for l in range(cfg.n_layers):
         masks.append({})
         deltas.append({})
@@ -356,7 +363,19 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
                 fr = psi.mean(0)
                 imp = imp + fr.sum()
                 if spec.ref_count > 0:
-                    freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
+                    f_sg = fr.detach()
+                    freq_batch += float((f_sg * torch.log2(1.0 + spec.ref_count * f_sg)).sum())
+                    if freq_ema is None:
+                        freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
+                    else:
+                        alpha, debias = po.ema_decay_terms(ema_count, spec.ema_halflife)
+                        prev = torch.tensor(np.asarray(freq_ema[l][kind], np.float64), dtype=dtype)
+                        nxt = prev + alpha * (f_sg - prev)
+                        new_ema[l][kind] = nxt.numpy()
+                        f_hat = nxt / debias
+                        a_ = spec.ref_count
+                        slope = torch.log2(1.0 + a_ * f_hat) + a_ * f_hat / ((1.0 + a_ * f_hat) * math.log(2.0))
+                        freq = freq + (f_hat * torch.log2(1.0 + a_ * f_hat) + slope * (fr - f_sg)).sum()
             masks[l][kind] = (lo + (1.0 - lo) * T(u)).reshape(b, t, C)
             deltas[l][kind] = T(dl).reshape(b, t) if use_delta else None
     act_m = forward(cfg, prm, r0, masks, deltas, rb=rb)
@@ -367,7 +386,7 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
     grads = torch.autograd.grad(loss, wrt)
     n = len(leaves)
     out = dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()),
-               freq=float(freq.detach()),
+               freq=float(freq.detach()), freq_ema=new_ema, freq_batch=freq_batch,
                dV=[{} for _ in range(cfg.n_layers)],
                dU=[{} for _ in range(cfg.n_layers)], d_ci_pre=[{} for _ in range(cfg.n_layers)], u=us, delta=ds)
     for i, (l, k) in enumerate(leaves):

@@ -34,6 +34,7 @@ everything between is float64.
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import numpy as np
@@ -98,7 +99,7 @@ def grouped_T(lhs, rhs, sizes):
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                    bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None,
-                   pinned_top_idx=None, imp_min=None, sources=None):
+                   pinned_top_idx=None, imp_min=None, sources=None, freq_ema=None, ema_count=0.0):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
     given. `pinned_top_idx[l]` ([T, k]) replaces the clean pass's own expert selection
@@ -108,7 +109,10 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     imp, grads, d_ci_pre, top_idx, own_top_idx, logits_raw, logits_mag, r_final,
     rc_final, deltas). `imp_min` (a `pd_oracle.ImpMin`) replaces the L_p term given by
     p / imp_coeff; each site's selected values map to their expert's block of the
-    [E * c] component vector; `freq` is the frequency term.
+    [E * c] component vector; `freq` is the frequency term. `freq_ema` ([L, 3, E * c],
+    with `imp_min.ema_halflife`) is the EMA frequency estimate before this step after
+    `ema_count` observations: the frequency term then reads the debiased estimate, and the
+    result holds the new estimate (`freq_ema`) and the batch penalty (`freq_batch`).
 
     `sources = (src, src_delta, rows_per_source)` replaces the draws by persistent
     (adversarial) source tables, the reference's `SourceMaskIngredients` arm
@@ -152,6 +156,8 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     saved = []
     imp = 0.0
     freq = 0.0
+    freq_batch = 0.0
+    new_ema = None if freq_ema is None else np.zeros((cfg.L, len(SITES), E * c))
     for l in range(cfg.L):
         P = params[l]
         h2, rinv = rms_norm_zero_centered(r, P["ln"], cfg.eps)
@@ -169,9 +175,14 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             pre = ci_pre[l][s]
             lo = po.lower_leaky(pre)
             up = po.upper_leaky(pre)
-            a_, f_, dup = po.impmin_site_terms(up, spec, T, idx, E)
+            si = SITES.index(s)
+            a_, f_, dup, ne, fb = po.impmin_site_terms_ema(
+                up, spec, T, idx, E, ema=None if freq_ema is None else np.asarray(freq_ema)[l, si], count=ema_count)
             imp += a_
             freq += f_
+            freq_batch += fb
+            if new_ema is not None:
+                new_ema[l, si] = ne
             if sources is not None:
                 src_t, src_d, rps = sources
                 # the table is cast to the CI dtype before the select (pd/core/masking.py:57)
@@ -284,8 +295,8 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         d_h2 = po.gather_tokens_vjp(d_xj, jobs) + d_logits @ P["router"]
         dx = rms_norm_vjp(sv["r"], P["ln"], sv["rinv"], d_h2)
         dr = rb(dr + dx)
-    return dict(loss=loss, recon=recon, imp=imp, freq=freq, grads=grads, d_ci_pre=d_pre, top_idx=tops,
-                d_src=d_src, d_src_delta=d_src_delta, own_top_idx=own_tops,
+    return dict(loss=loss, recon=recon, imp=imp, freq=freq, freq_ema=new_ema, freq_batch=freq_batch, grads=grads,
+                d_ci_pre=d_pre, top_idx=tops, d_src=d_src, d_src_delta=d_src_delta, own_top_idx=own_tops,
                 logits_raw=raws, logits_mag=mags, r_final=r, rc_final=rc, dx0=dr,
                 deltas=[{s: sv["S"][s]["delta"] for s in SITES} for sv in saved])
 
@@ -350,15 +361,17 @@ def init_moe(cfg: MoEConfig, rng):
 
 def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                          use_delta=True, partitionable=True, dtype=None, threads=None, imp_min=None,
-                         sources=None):
+                         sources=None, freq_ema=None, ema_count=0.0):
     """The same step as `moe_stack_step` (no bf16 storage model) written as a torch
     forward whose backward is torch autograd: in float64 it pins `moe_stack_step`'s
     hand-written backward (tests/test_moe_oracle.py). The expert selection and Threefry
     draws are computed as in `moe_stack_step` (integer and bit-level work, outside
     autograd). The smooth-L0 imp-min (`imp_min`) is written as the reference writes it, a
     scatter-add of psi into the [E, c] component frequencies, so autograd differentiates
-    the frequency penalty through the scatter. Returns dict(loss, recon, imp, freq,
-    grads, d_ci_pre, top_idx)."""
+    the frequency penalty through the scatter; with `freq_ema` ([L, 3, E * c]) the
+    penalty is the reference's EMA surrogate `Phi(f_hat) + Phi'(f_hat) (f - sg(f))`
+    (`pd/core/losses.py:449-456`). Returns dict(loss, recon, imp, freq, grads, d_ci_pre,
+    top_idx)."""
     import torch
 
     spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
@@ -427,8 +440,16 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
                 F = torch.zeros(E, c, dtype=dt).index_add(0, idx.reshape(-1), psi.reshape(-1, c))
                 fr = F / T
                 imp = imp + fr.sum()
-                if spec.ref_count > 0:
+                if spec.ref_count > 0 and freq_ema is None:
                     freq = freq + (fr * torch.log2(1.0 + spec.ref_count * fr)).sum()
+                elif spec.ref_count > 0:
+                    alpha, debias = po.ema_decay_terms(ema_count, spec.ema_halflife)
+                    f_sg = fr.detach().reshape(-1)
+                    prev = t(np.asarray(freq_ema)[l, SITES.index(s)])
+                    f_hat = (prev + alpha * (f_sg - prev)) / debias
+                    a_ = spec.ref_count
+                    slope = torch.log2(1.0 + a_ * f_hat) + a_ * f_hat / ((1.0 + a_ * f_hat) * math.log(2.0))
+                    freq = freq + (f_hat * torch.log2(1.0 + a_ * f_hat) + slope * (fr.reshape(-1) - f_sg)).sum()
             if sources is not None:
                 u = src[l][s][doc[:, None], idx]
                 dlt = srcd[l][s][doc]

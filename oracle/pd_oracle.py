@@ -311,6 +311,45 @@ def importance_minimality_terms(ci_upper_sites, gamma, reference_datapoint_count
     return activity, freq
 
 
+def frequency_curve(f, reference_datapoint_count):
+    """`pd/core/losses.py:375-377`: `Phi(f) = f log2(1 + a' f)`."""
+    return f * np.log2(1.0 + reference_datapoint_count * f)
+
+
+def frequency_curve_slope(f, reference_datapoint_count):
+    """`pd/core/losses.py:380-386`: `Phi'(f) = log2(1 + a' f) + a' f / ((1 + a' f) ln 2)`."""
+    af = reference_datapoint_count * f
+    return np.log2(1.0 + af) + af / ((1.0 + af) * math.log(2.0))
+
+
+def ema_decay_terms(count: float, halflife_steps: float):
+    """`(alpha, debias) = (1 - decay, 1 - decay^(count + 1))`, `decay = 2^(-1/h)`, both
+    formed through `expm1` of `log(decay) = -ln 2 / h` (`pd/core/losses.py:449-451`)."""
+    log_decay = -math.log(2.0) / halflife_steps
+    return -math.expm1(log_decay), -math.expm1(log_decay * (count + 1.0))
+
+
+def ema_frequency_update(f_batch, ema, count: float, halflife_steps: float):
+    """One observation of the running estimate (`pd/core/losses.py:452-455`):
+    `new = ema + alpha (f - ema)`, `f_hat = new / debias`. Returns `(new, f_hat)`."""
+    alpha, debias = ema_decay_terms(count, halflife_steps)
+    new = ema + alpha * (np.asarray(f_batch, np.float64) - ema)
+    return new, new / debias
+
+
+def ema_frequency_penalty(frequencies: dict, ema: dict, count: float, halflife_steps: float,
+                          reference_datapoint_count):
+    """`pd/core/losses.py:425-458`: `(freq, new_ema)`, the penalty `sum Phi(f_hat)` at the
+    debiased estimate after this batch (its gradient, `Phi'(f_hat) df_batch`, is
+    `ema_frequency_slope`'s)."""
+    freq = 0.0
+    new_ema = {}
+    for name, f in frequencies.items():
+        new_ema[name], f_hat = ema_frequency_update(f, ema[name], count, halflife_steps)
+        freq += float(np.sum(frequency_curve(f_hat, reference_datapoint_count)))
+    return freq, new_ema
+
+
 @dataclass(frozen=True)
 class ImpMin:
     """The imp-min term of a fused step. `kind="pnorm"`: `coeff * sum upper^p / n` (the
@@ -318,7 +357,10 @@ class ImpMin:
     stand-in). `kind="smooth_l0"`: the engine's term (`pd/core/objective.py:101-131`):
     `coeff * sum_c f_c + freq_coeff * sum_c f_c log2(1 + ref_count f_c)` with
     `f_c = sum psi(upper) / n` (`pd/core/losses.py:316-330, 375-394`), the frequency term
-    off when `ref_count` is 0. `n` is the token count of the batch."""
+    off when `ref_count` is 0. `n` is the token count of the batch. `ema_halflife` (the
+    config's `ema_halflife_steps`, `pd/core/configs.py:182`) evaluates the frequency term
+    at the debiased running estimate (`ema_frequency_penalty`); the steps then take the
+    estimate before the batch and its observation count."""
 
     kind: str = "pnorm"
     p: float = 2.0
@@ -327,6 +369,7 @@ class ImpMin:
     normalize_at_one: bool = False
     freq_coeff: float = 0.0
     ref_count: float = 0.0
+    ema_halflife: float | None = None
 
     def loss(self, activity: float, frequency: float) -> float:
         return self.coeff * activity + (self.freq_coeff * frequency if self.kind == "smooth_l0" else 0.0)
@@ -341,9 +384,19 @@ def impmin_site_terms(up, spec: ImpMin, n: int, groups=None, n_groups: int = 1):
     coefficients: `coeff * p up^(p-1) / n` (L_p) or
     `(coeff + freq_coeff * Phi'(f_c)) / n * psi'(up)` (smooth-L0, `Phi'` of
     `pd/core/losses.py:380-386`)."""
+    return impmin_site_terms_ema(up, spec, n, groups, n_groups)[:3]
+
+
+def impmin_site_terms_ema(up, spec: ImpMin, n: int, groups=None, n_groups: int = 1, ema=None, count: float = 0.0):
+    """`impmin_site_terms` plus the EMA estimator: with `ema` (the site's `[n_groups * c]`
+    estimate before this batch; `spec.ema_halflife` set) the frequency term is
+    `sum Phi(f_hat)` and its slope `Phi'(f_hat)` (`pd/core/losses.py:425-458`: the
+    surrogate `Phi'(f_hat) (f - sg(f))` keeps the gradient at the batch penalty's scale).
+    Returns `(activity, frequency, grad, new_ema, batch_frequency)`; `new_ema` is None
+    and `batch_frequency` the frequency term without the EMA."""
     up = np.asarray(up, np.float64)
     if spec.kind == "pnorm":
-        return float(np.sum(up**spec.p)) / n, 0.0, spec.coeff * spec.p * up ** (spec.p - 1.0) / n
+        return float(np.sum(up**spec.p)) / n, 0.0, spec.coeff * spec.p * up ** (spec.p - 1.0) / n, None, 0.0
     if spec.kind != "smooth_l0":
         raise ValueError(spec.kind)
     c = up.shape[-1]
@@ -353,14 +406,24 @@ def impmin_site_terms(up, spec: ImpMin, n: int, groups=None, n_groups: int = 1):
     np.add.at(F, g, psi)
     f = F / n
     act = float(f.sum())
-    freq = 0.0
+    freq = batch = 0.0
+    new_ema = None
     slope = np.full_like(f, spec.coeff)
     if spec.ref_count > 0:
-        af = spec.ref_count * f
-        freq = float(np.sum(f * np.log2(1.0 + af)))
-        slope = slope + spec.freq_coeff * (np.log2(1.0 + af) + af / ((1.0 + af) * math.log(2.0)))
+        fe = f
+        batch = float(np.sum(frequency_curve(f, spec.ref_count)))
+        if ema is not None:
+            if spec.ema_halflife is None:
+                raise ValueError("an EMA estimate needs spec.ema_halflife")
+            new_ema, fe = ema_frequency_update(f.reshape(-1), np.asarray(ema, np.float64).reshape(-1), count,
+                                               spec.ema_halflife)
+            fe = fe.reshape(f.shape)
+        freq = float(np.sum(frequency_curve(fe, spec.ref_count)))
+        slope = slope + spec.freq_coeff * frequency_curve_slope(fe, spec.ref_count)
+    elif ema is not None:
+        raise ValueError("the EMA estimate needs the frequency term (ref_count > 0)")
     grad = (slope / n)[g].reshape(up.shape) * smooth_l0_psi_grad(up, spec.gamma, spec.normalize_at_one)
-    return act, freq, grad
+    return act, freq, grad, new_ema, batch
 
 
 def mse(masked, clean):
@@ -455,6 +518,8 @@ class DenseStepResult:
     dU: np.ndarray
     dgate: tuple
     freq: float = 0.0
+    freq_ema: np.ndarray | None = None  # the EMA estimate after this step (with freq_ema given)
+    freq_batch: float = 0.0  # the batch frequency penalty (the EMA's diagnostic)
 
 
 def round_bf16(a):
@@ -476,7 +541,7 @@ def round_bf16(a):
 
 def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0, imp_coeff=1.0,
                     recon_coeff=1.0, mask_dtype="bfloat16", use_delta=False, partitionable=True, bf16_storage=False,
-                    imp_min=None):
+                    imp_min=None, freq_ema=None, ema_count=0.0):
     """One stochastic-recon + importance-minimality fwd+bwd for ONE decomposed site whose
     input `x` is the clean input (the single-linear workload). It composes:
     clean target `x@W.T` (`pd/core/train.py:578-606`, detached), CI gate on `h = x@V`
@@ -491,7 +556,9 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     `x@V`, `(x@V)*coef`, `@U` and the clean output are bf16, and their cotangents come
     back in bf16); products and reductions are exact (float64) in between. The gate
     MLP itself is evaluated exactly on the bf16 `h` — finer than the reference's bf16
-    MLP arithmetic. `imp_min` (an `ImpMin`) replaces the L_p term of p / imp_coeff."""
+    MLP arithmetic. `imp_min` (an `ImpMin`) replaces the L_p term of p / imp_coeff;
+    `freq_ema` ([C], with `imp_min.ema_halflife`) is the EMA frequency estimate before
+    this step after `ema_count` observations."""
     rb = round_bf16 if bf16_storage else (lambda a: a)
     spec = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
     y_t = rb(x @ W.T)
@@ -505,7 +572,7 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     y = rb(acts @ U)
     y_masked = y if d is None else y + d[:, None] * y_t
     recon = mse(y_masked, y_t)
-    imp, freq, dup = impmin_site_terms(up, spec, up.shape[0])
+    imp, freq, dup, new_ema, freq_batch = impmin_site_terms_ema(up, spec, up.shape[0], ema=freq_ema, count=ema_count)
     loss = recon_coeff * recon + spec.loss(imp, freq)
     dy = rb(recon_coeff * 2.0 * (y_masked - y_t) / y.size)
     dU = acts.T @ dy
@@ -516,7 +583,8 @@ def dense_site_step(x, W, V, U, gate: GateParams, draw_key, *, site_idx=0, p=2.0
     dgraw = dgraw + upper_leaky_vjp(g_raw, dup)
     dh_gate, dwi, dbi, dwo, dbo = gate_backward(h, gate, dgraw)
     dV = x.T @ rb(dh_direct + dh_gate)
-    return DenseStepResult(loss, recon, imp, y_masked, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo), freq)
+    return DenseStepResult(loss, recon, imp, y_masked, h, g_raw, m, u, d, dV, dU, (dwi, dbi, dwo, dbo), freq, new_ema,
+                           freq_batch)
 
 
 # ---------------------------------------------------------------- MoE routing

@@ -24,8 +24,9 @@ _c_i64, _c_i32, _c_u32, _c_f32, _c_p, _c_sz = (ctypes.c_int64, ctypes.c_int, cty
                                                 ctypes.c_void_p, ctypes.c_size_t)
 
 # name -> (restype, argtypes)
-# imp-min arguments of the fused steps: kind, p, gamma, normalize_at_one, coeff, freq_coeff, ref_count
-_IMP_ARGS = [_c_i32, _c_f32, _c_f32, _c_i32, _c_f32, _c_f32, _c_f32]
+# imp-min arguments of the fused steps: kind, p, gamma, normalize_at_one, coeff, freq_coeff, ref_count,
+# freq_ema_in, freq_ema_out, ema_count, ema_halflife
+_IMP_ARGS = [_c_i32, _c_f32, _c_f32, _c_i32, _c_f32, _c_f32, _c_f32, _c_p, _c_p, _c_f32, _c_f32]
 
 _SIGNATURES = {
     "pd_last_error": (ctypes.c_char_p, []),
@@ -43,7 +44,7 @@ _SIGNATURES = {
                              _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "pd_impmin_workspace_size": (_c_sz, [_c_i64, _c_i64]),
     "pd_impmin": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_i32,
-                           _c_f32, _c_f32, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
+                           _c_f32, _c_p, _c_p, _c_f32, _c_f32, _c_f32, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "pd_mse_workspace_size": (_c_sz, [_c_i64]),
     "pd_mse": (_c_i32, [_c_p, _c_p, _c_i32, _c_i64, _c_f32, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "pd_kl_workspace_size": (_c_sz, [_c_i64]),

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+#include <mutex>
 #include <string>
 
 #include "../../include/pd_mi355x.h"
@@ -18,11 +20,16 @@ int check_launch(const char* what);
 // the caller's stream inside one entry point, with a pool of timing-free events for the
 // fork / join points. Default priority (like every stream here); created on first use with
 // the device current and kept until the process ends. `which` (0 or 1) selects one of two
-// such streams; at least n_events events are returned. Entry points that use them on one
-// device at the same time race, as two calls on one workspace do.
+// such streams; at least n_events events are returned. The lease holds the (device, which)
+// slot's lock until the AuxStream is destroyed: an entry point keeps it for its whole
+// fork / join enqueue sequence, so calls from several host threads on one device enqueue
+// one after another and no call re-records an event before another call's wait on it has
+// been enqueued (a wait binds to the record that precedes it on the host). The helper
+// stream's work of such calls runs in enqueue order; each call's dependencies are its own.
 struct AuxStream {
   hipStream_t st = nullptr;
   hipEvent_t* ev = nullptr;
+  std::unique_lock<std::mutex> lease;
 };
 int aux_stream(int which, int n_events, AuxStream& out);
 // pd_grouped_gemm without the launch that zeroes rows past the last group offset (for
@@ -284,6 +291,55 @@ inline void split2(uint32_t k0, uint32_t k1, int layout, uint32_t out[4]) {
     threefry2x32(k0, k1, b0, b1);
     out[0] = a0, out[1] = b0, out[2] = a1, out[3] = b1;
   }
+}
+
+// ---------------------------------------------------------------- EMA frequency estimate
+// The frequency penalty's running estimate of f_c (pd/core/losses.py:425-458 and
+// EmaFrequency :522-543): new = ema + alpha (f - ema), f_hat = new / debias, with
+// alpha = 1 - 2^(-1/h) = -expm1(-ln 2 / h) and debias = 1 - 2^(-(count + 1)/h) =
+// -expm1(-ln 2 / h * (count + 1)), both in the expm1 form that stays finite up to the
+// configuration's 1e6 half-life cap. alpha is the double-precision value rounded to fp32
+// and debias is formed in fp32, as the reference's fp32 array arithmetic forms them; the
+// update and the division run in fp32. `count` is the number of earlier observations.
+struct FreqEma {
+  const float* in = nullptr;  // [components] the estimate before this step; NULL = batch estimate
+  float* out = nullptr;       // [components] the estimate after it (may alias in; NULL = not written)
+  float alpha = 0.f, debias = 1.f;
+  __host__ __device__ bool on() const { return in != nullptr; }
+  // the same estimator over components [off, ...)
+  __host__ __device__ FreqEma at(int64_t off) const {
+    FreqEma e = *this;
+    if (e.in) e.in += off;
+    if (e.out) e.out += off;
+    return e;
+  }
+};
+
+inline int make_freq_ema(const char* what, const float* in, float* out, float count, float halflife, FreqEma& e) {
+  e = FreqEma{};
+  if (!in) {
+    if (out) return fail(PD_EINVAL, std::string(what) + ": freq_ema_out needs freq_ema_in");
+    return PD_OK;
+  }
+  if (!(halflife > 0.f) || !(halflife <= 1e6f))
+    return fail(PD_EINVAL, std::string(what) + ": EMA half-life must be in (0, 1e6]");
+  if (!(count >= 0.f) || !std::isfinite(count))
+    return fail(PD_EINVAL, std::string(what) + ": EMA observation count must be >= 0");
+  const double log_decay = -std::log(2.0) / (double)halflife;
+  e.in = in;
+  e.out = out;
+  e.alpha = (float)(-std::expm1(log_decay));
+  e.debias = -std::expm1((float)log_decay * (count + 1.f));
+  return PD_OK;
+}
+
+// f_hat of component i from this batch's frequency f; the thread that owns component i
+// passes write = true to store the new estimate.
+__device__ inline float ema_frequency(const FreqEma& e, int64_t i, float f, bool write) {
+  const float prev = e.in[i];
+  const float next = prev + e.alpha * (f - prev);
+  if (write && e.out) e.out[i] = next;
+  return next / e.debias;
 }
 
 }  // namespace pd

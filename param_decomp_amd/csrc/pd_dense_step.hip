@@ -435,32 +435,39 @@ __global__ void k_step_gate_reduce(const float* __restrict__ partial, int64_t ch
 }
 
 // losses[0..3] = {loss, recon, activity, frequency} from the partial arrays (one block,
-// fixed order): activity = imp_scale * sum(imp_part), frequency = sum(freq_part).
+// fixed order): activity = imp_scale * sum(imp_part), frequency = sum(freq_part); with
+// fb_part (the EMA estimator's batch penalty) losses[4] = sum(fb_part) over n_freq.
 __global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec, const float* __restrict__ imp_part,
-                              int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double rec_scale,
-                              double imp_scale, float recon_coeff, float imp_coeff, float freq_coeff,
-                              float* __restrict__ losses) {
-  __shared__ double sr[16], si[16], sq[16];
-  double r = 0.0, m = 0.0, fq = 0.0;
+                              int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq,
+                              const float* __restrict__ fb_part, double rec_scale, double imp_scale,
+                              float recon_coeff, float imp_coeff, float freq_coeff, float* __restrict__ losses) {
+  __shared__ double sr[16], si[16], sq[16], sb[16];
+  double r = 0.0, m = 0.0, fq = 0.0, fb = 0.0;
   for (int64_t i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
   for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
   for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
+  if (fb_part)
+    for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fb += fb_part[i];
   r = wave_sum_d(r);
   m = wave_sum_d(m);
   fq = wave_sum_d(fq);
+  fb = wave_sum_d(fb);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
     sq[threadIdx.x / 64] = fq;
+    sb[threadIdx.x / 64] = fb;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, b = 0, q = 0;
+    double a = 0, b = 0, q = 0, qb = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       b += si[i];
       q += sq[i];
+      qb += sb[i];
     }
+    if (fb_part) losses[4] = (float)qb;
     a *= rec_scale;
     b *= imp_scale;
     losses[0] = (float)(recon_coeff * a + imp_coeff * b + freq_coeff * q);
@@ -472,7 +479,7 @@ __global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec,
 
 struct StepWorkspace {
   size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, rng_part, rng, tab,
-      sl0_col, sl0_slope, sl0_act, sl0_freq, total;
+      sl0_col, sl0_slope, sl0_act, sl0_freq, sl0_fb, total;
 };
 
 static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C) {
@@ -509,6 +516,7 @@ static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_o
   take(w.sl0_slope, 4 * (size_t)C);
   take(w.sl0_act, 4 * (size_t)sl0_blocks(1, (int)C));
   take(w.sl0_freq, 4 * (size_t)sl0_blocks(1, (int)C));
+  take(w.sl0_fb, 4 * (size_t)sl0_blocks(1, (int)C));
   w.total = o;
   return w;
 }
@@ -556,6 +564,7 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   float* sl0_slope = (float*)(ws + L.sl0_slope);
   float* sl0_act = (float*)(ws + L.sl0_act);
   float* sl0_freq = (float*)(ws + L.sl0_freq);
+  float* sl0_fb = imp.ema.on() ? (float*)(ws + L.sl0_fb) : nullptr;
   StepParams sp{T, C, mk0, mk1, draw_dtype, layout, imp.p, imp.coeff / (float)T, delta, (uint8_t*)(ws + L.ubits),
                 sl0 ? 1 : 0, imp.g2(), imp.psi_scale(), (float*)(ws + L.sl0_col), sl0_slope};
   const dim3 cgrid((unsigned)cdiv(C, SITE_COLS), (unsigned)cdiv(T, SITE_ROWS));
@@ -598,7 +607,7 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   if (sl0)  // per-component frequencies, loss partials and backward slopes
     hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(1, (int)C)), dim3(256), 0, s, sp.colpart,
                        (const int32_t*)nullptr, 1, T, (int)C, 1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count,
-                       sl0_slope, sl0_act, sl0_freq);
+                       imp.ema, sl0_slope, sl0_act, sl0_freq, sl0_fb);
   if ((rc = check_launch("pd_dense_step fwd"))) return rc;
   PD_MARK(4);
   if ((rc = pd_gemm(dtype, T, d_out, C, acts, C, 0, UT, C, 1, y, d_out, dtype, 1.f, 0.f, stream))) return rc;
@@ -616,11 +625,12 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   const int64_t n_sl0 = sl0_blocks(1, (int)C);
   if (sl0)
     hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), sl0_act,
-                       n_sl0, sl0_freq, imp.ref_count > 0.f ? n_sl0 : (int64_t)0, 1.0 / (double)(T * d_out), 1.0,
+                       n_sl0, sl0_freq, imp.ref_count > 0.f ? n_sl0 : (int64_t)0, sl0_fb, 1.0 / (double)(T * d_out), 1.0,
                        recon_coeff, imp.coeff, imp.freq_coeff, losses);
   else
     hipLaunchKernelGGL(k_step_losses, dim3(1), dim3(1024), 0, s, rec_part, (int64_t)(rgrid.x * rgrid.y), imp_part,
-                       n_imp, (const float*)nullptr, (int64_t)0, 1.0 / (double)(T * d_out), 1.0 / (double)T,
+                       n_imp, (const float*)nullptr, (int64_t)0, (const float*)nullptr, 1.0 / (double)(T * d_out),
+                       1.0 / (double)T,
                        recon_coeff, imp.coeff, 0.f, losses);
   PD_MARK(7);
   if ((rc = pd_gemm(dtype, C, d_out, T, actsT, T, 0, dyT, T, 1, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
@@ -661,10 +671,14 @@ int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, 
                   const void* V, const void* U, const float* w_in, const float* b_in, const float* w_out,
                   const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0, uint32_t dk1, int use_delta,
                   int draw_dtype, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                  float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dV,
-                  float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out, void* workspace,
+                  float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                  float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, float* losses,
+                  float* dV, float* dU, float* dw_in, float* db_in, float* dw_out, float* db_out, void* workspace,
                   size_t workspace_bytes, void* stream) {
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_dense_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
+                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
                          use_delta, draw_dtype, layout, imp, recon_coeff, losses, dV, dU, dw_in, db_in, dw_out, db_out,
                          workspace, workspace_bytes, stream, nullptr);
@@ -674,11 +688,16 @@ int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,
                         const float* w_out, const float* b_out, uint32_t mk0, uint32_t mk1, uint32_t dk0,
                         uint32_t dk1, int use_delta, int draw_dtype, int layout, int imp_kind, float p, float gamma,
-                        int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count, float recon_coeff,
-                        float* losses, float* dV, float* dU, float* dw_in, float* db_in, float* dw_out,
-                        float* db_out, void* workspace, size_t workspace_bytes, void* stream, void** events) {
+                        int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                        const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                        float recon_coeff, float* losses, float* dV, float* dU, float* dw_in, float* db_in,
+                        float* dw_out, float* db_out, void* workspace, size_t workspace_bytes, void* stream,
+                        void** events) {
   if (!events) return fail(PD_EINVAL, "pd_dense_step_timed: events required");
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_dense_step_timed", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   return dense_step_impl(dtype, T, d_in, d_out, C, H, x, W, V, U, w_in, b_in, w_out, b_out, mk0, mk1, dk0, dk1,
                          use_delta, draw_dtype, layout, imp, recon_coeff, losses, dV, dU, dw_in, db_in, dw_out, db_out,
                          workspace, workspace_bytes, stream, events);

@@ -203,7 +203,15 @@ struct ImpParams {
   float p, eps, beta, world_size, gamma;
   int normalize_at_one;
   float ref_count, coeff_act, coeff_freq;
+  FreqEma ema;  // the frequency term's running estimate (off: the batch estimate)
 };
+
+// The frequency the smooth-L0 penalty reads for column c with column sum s: the batch
+// f = s / rows, or the debiased EMA estimate after this batch (stored when write).
+__device__ inline float imp_penalty_frequency(float s, int64_t rows, int64_t c, const ImpParams& q, bool write) {
+  const float f = s / (float)rows;
+  return q.ema.on() ? ema_frequency(q.ema, c, f, write) : f;
+}
 
 __device__ inline float imp_psi(float v, const ImpParams& q) {
   if (q.kind == PD_IMPMIN_PNORM) {
@@ -251,27 +259,30 @@ __global__ void k_colsum_final(const float* __restrict__ partial, int64_t chunks
   colsum[c] = pd_ordered_sum(partial + c, chunks, C);
 }
 
-// per-column slope dL/ds_c of the imp-min objective in terms of the column sum s_c
-__device__ inline float imp_col_slope(float s, int64_t rows, const ImpParams& q) {
+// per-column slope dL/ds_c of the imp-min objective in terms of the column sum s_c (the
+// frequency term's slope at the penalty's frequency: Phi'(f_hat) under the EMA estimate,
+// pd/core/losses.py:449-456)
+__device__ inline float imp_col_slope(float s, int64_t rows, int64_t c, const ImpParams& q) {
   float n = (float)rows;
   if (q.kind == PD_IMPMIN_PNORM) {
     float a = s * q.world_size;
     return q.coeff_act * (1.f / n * (1.f + q.beta * log2f(1.f + a)) +
                           q.beta * (s / n) * q.world_size / ((1.f + a) * 0.69314718055994531f));
   }
-  float f = s / n;
   float slope = q.coeff_act;
   if (q.ref_count > 0.f) {
-    float af = q.ref_count * f;
+    float af = q.ref_count * imp_penalty_frequency(s, rows, c, q, false);
     slope += q.coeff_freq * (log2f(1.f + af) + af / ((1.f + af) * 0.69314718055994531f));
   }
   return slope / n;
 }
 
+// out[0] = activity, out[1] = frequency penalty (at f_hat under the EMA estimate, which
+// this kernel also stores), out[2] = the batch penalty when the EMA estimate is on.
 __global__ void k_imp_scalar(const float* __restrict__ colsum, int64_t rows, int64_t C, ImpParams q,
                              float* __restrict__ out) {
-  __shared__ double sa[16], sf[16];
-  double act = 0.0, freq = 0.0;
+  __shared__ double sa[16], sf[16], sb[16];
+  double act = 0.0, freq = 0.0, fbat = 0.0;
   double n = (double)rows;
   for (int64_t c = threadIdx.x; c < C; c += blockDim.x) {
     double s = colsum[c], f = s / n;
@@ -279,25 +290,33 @@ __global__ void k_imp_scalar(const float* __restrict__ colsum, int64_t rows, int
       act += f + q.beta * f * log2(1.0 + s * q.world_size);
     } else {
       act += f;
-      if (q.ref_count > 0.f) freq += f * log2(1.0 + q.ref_count * f);
+      if (q.ref_count > 0.f) {
+        const double fe = q.ema.on() ? (double)imp_penalty_frequency(colsum[c], rows, c, q, true) : f;
+        freq += fe * log2(1.0 + q.ref_count * fe);
+        fbat += f * log2(1.0 + q.ref_count * f);
+      }
     }
   }
   act = wave_sum_d(act);
   freq = wave_sum_d(freq);
+  fbat = wave_sum_d(fbat);
   int w = threadIdx.x / 64, l = threadIdx.x % 64;
   if (l == 0) {
     sa[w] = act;
     sf[w] = freq;
+    sb[w] = fbat;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, f = 0;
+    double a = 0, f = 0, b = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sa[i];
       f += sf[i];
+      b += sb[i];
     }
     out[0] = (float)a;
     out[1] = (float)f;
+    if (q.ema.on()) out[2] = (float)b;
   }
 }
 
@@ -308,7 +327,7 @@ __global__ void k_imp_grad(const T* __restrict__ ci, const float* __restrict__ c
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     int64_t c = i % C;
     float v = load_f<T>(ci, i);
-    store_f<T>(grad, i, imp_col_slope(colsum[c], rows, q) * imp_dpsi(v, q));
+    store_f<T>(grad, i, imp_col_slope(colsum[c], rows, c, q) * imp_dpsi(v, q));
   }
 }
 
@@ -568,13 +587,17 @@ size_t pd_impmin_workspace_size(int64_t rows, int64_t C) {
 }
 
 int pd_impmin(const void* ci, int dtype, int64_t rows, int64_t C, int kind, float p, float eps, float beta,
-              float world_size, float gamma, int normalize_at_one, float ref_count, float coeff_act,
-              float coeff_freq, float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream) {
+              float world_size, float gamma, int normalize_at_one, float ref_count, const float* freq_ema_in,
+              float* freq_ema_out, float ema_count, float ema_halflife, float coeff_act, float coeff_freq,
+              float* out, void* grad, void* workspace, size_t workspace_bytes, void* stream) {
   if (rows <= 0 || C <= 0 || !ci || !out) return fail(PD_EINVAL, "pd_impmin: bad args");
   if (kind != PD_IMPMIN_PNORM && kind != PD_IMPMIN_SMOOTH_L0) return fail(PD_EINVAL, "pd_impmin: kind");
   if (!workspace || workspace_bytes < pd_impmin_workspace_size(rows, C))
     return fail(PD_EWORKSPACE, "pd_impmin: workspace too small");
-  ImpParams q{kind, p, eps, beta, world_size, gamma, normalize_at_one, ref_count, coeff_act, coeff_freq};
+  ImpParams q{kind, p, eps, beta, world_size, gamma, normalize_at_one, ref_count, coeff_act, coeff_freq, FreqEma{}};
+  if (int e = make_freq_ema("pd_impmin", freq_ema_in, freq_ema_out, ema_count, ema_halflife, q.ema)) return e;
+  if (q.ema.on() && !(kind == PD_IMPMIN_SMOOTH_L0 && ref_count > 0.f))
+    return fail(PD_EINVAL, "pd_impmin: the EMA estimate needs the smooth-L0 frequency term (ref_count > 0)");
   const int64_t cr = col_rows(rows), chunks = cdiv(rows, cr);
   if (chunks > 65535) return fail(PD_EUNSUPPORTED, "pd_impmin: too many rows");
   float* part = (float*)workspace;
@@ -584,12 +607,12 @@ int pd_impmin(const void* ci, int dtype, int64_t rows, int64_t C, int kind, floa
   PD_DISPATCH_DTYPE(dtype, T,
                     hipLaunchKernelGGL(k_imp_colsum_partial<T>, grid, dim3(256), 0, s, (const T*)ci, rows, C, q, part, cr));
   hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, s, part, chunks, C, colsum);
-  hipLaunchKernelGGL(k_imp_scalar, dim3(1), dim3(1024), 0, s, colsum, rows, C, q, out);
-  if (grad) {
+  if (grad) {  // before the scalar pass, which stores the new estimate (possibly over the old)
     PD_DISPATCH_DTYPE(dtype, T,
                       hipLaunchKernelGGL(k_imp_grad<T>, dim3(ew_blocks(rows * C)), dim3(EW_THREADS), 0, s,
                                          (const T*)ci, colsum, rows, C, q, (T*)grad));
   }
+  hipLaunchKernelGGL(k_imp_scalar, dim3(1), dim3(1024), 0, s, colsum, rows, C, q, out);
   return check_launch("pd_impmin");
 }
 

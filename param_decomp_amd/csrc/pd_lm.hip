@@ -576,31 +576,40 @@ __global__ __launch_bounds__(256) void k_lm_gelu_bwd(const bf16_t* __restrict__ 
 
 // losses[0..3] = (recon_coeff kl + imp_coeff act + freq_coeff freq, kl, act, freq) with
 // kl = mean of the position KLs, act = imp_scale * sum of the imp partials, freq = sum
-// of the frequency partials (none when n_freq = 0), each added in a fixed order in double.
+// of the frequency partials (none when n_freq = 0); with fb_part (the EMA estimator's
+// batch penalty) losses[4] = sum(fb_part) over n_freq; each added in a fixed order in
+// double.
 __global__ void k_lm_losses(const float* __restrict__ pos_kl, int64_t N, const float* __restrict__ imp_part,
-                            int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double imp_scale,
-                            float recon_coeff, float imp_coeff, float freq_coeff, float* __restrict__ losses) {
-  __shared__ double sr[16], si[16], sq[16];
-  double r = 0.0, m = 0.0, fq = 0.0;
+                            int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq,
+                            const float* __restrict__ fb_part, double imp_scale, float recon_coeff, float imp_coeff,
+                            float freq_coeff, float* __restrict__ losses) {
+  __shared__ double sr[16], si[16], sq[16], sb[16];
+  double r = 0.0, m = 0.0, fq = 0.0, fb = 0.0;
   for (int64_t i = threadIdx.x; i < N; i += blockDim.x) r += pos_kl[i];
   for (int64_t i = threadIdx.x; i < n_imp; i += blockDim.x) m += imp_part[i];
   for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
+  if (fb_part)
+    for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fb += fb_part[i];
   r = wave_sum_d(r);
   m = wave_sum_d(m);
   fq = wave_sum_d(fq);
+  fb = wave_sum_d(fb);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
     sq[threadIdx.x / 64] = fq;
+    sb[threadIdx.x / 64] = fb;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, c = 0, q = 0;
+    double a = 0, c = 0, q = 0, qb = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       c += si[i];
       q += sq[i];
+      qb += sb[i];
     }
+    if (fb_part) losses[4] = (float)qb;
     a /= (double)N;
     c *= imp_scale;
     losses[0] = (float)(recon_coeff * a + imp_coeff * c + freq_coeff * q);
@@ -642,8 +651,10 @@ struct Arena {
 struct LMSiteSave {
   bf16_t *xV, *acat, *actsT;
   uint8_t* ub;
-  // smooth-L0: tile column sums of psi, per-component slopes, loss partials (act, freq)
-  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;
+  // smooth-L0: tile column sums of psi, per-component slopes, loss partials (act, freq,
+  // the EMA estimator's batch penalty), and the site's offset in the EMA estimate
+  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq, *sl0_fb;
+  size_t ema_off;
 };
 
 struct LMLayerSave {
@@ -664,7 +675,7 @@ struct LMPlan {
   bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dcat, *dxVT[2], *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
   char *kl_ws, *sk_ws;
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
-  float *sl0_act, *sl0_freq;  // every site's smooth-L0 loss partials, contiguous
+  float *sl0_act, *sl0_freq, *sl0_fb;  // every site's smooth-L0 loss partials, contiguous
   size_t sl0_blocks_total;
 };
 
@@ -753,7 +764,9 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.sl0_blocks_total = nblk;
   P.sl0_act = A.take<float>(nblk);
   P.sl0_freq = A.take<float>(nblk);
+  P.sl0_fb = A.take<float>(nblk);
   nblk = 0;
+  size_t ema_off = 0;  // the EMA estimate is [L][kind][C_kind], layer-major
   for (int l = 0; l < D.L; ++l)
     for (int k = 0; k < LM_NK; ++k) {
       LMSiteSave& S = P.layers[l].site[k];
@@ -761,7 +774,10 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
       S.sl0_slope = A.take<float>(D.C[k]);
       S.sl0_act = P.sl0_act ? P.sl0_act + nblk : nullptr;
       S.sl0_freq = P.sl0_freq ? P.sl0_freq + nblk : nullptr;
+      S.sl0_fb = P.sl0_fb ? P.sl0_fb + nblk : nullptr;
+      S.ema_off = ema_off;
       nblk += sl0_blocks(1, D.C[k]);
+      ema_off += (size_t)D.C[k];
     }
   P.pos_kl = A.take<float>(N);
   P.stats = A.take<float>(N * 5);
@@ -1057,7 +1073,8 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if (sl0)  // the site's frequencies, loss partials and backward slopes
       hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(1, (int)C)), dim3(256), 0, s, S.sl0_col,
                          (const int32_t*)nullptr, 1, N, (int)C, 1.f / (float)N, imp.coeff, imp.freq_coeff,
-                         imp.ref_count, S.sl0_slope, S.sl0_act, S.sl0_freq);
+                         imp.ref_count, imp.ema.at((int64_t)S.ema_off), S.sl0_slope, S.sl0_act, S.sl0_freq,
+                         imp.ema.on() ? S.sl0_fb : nullptr);
     rec.mark(LM_CAT_GEMM_FWD);
     return gemm_nt(N, dout, kc, S.acat, kc, P.BtF[k] + (size_t)l * dout * kc, kc, out, dout, PD_DTYPE_BF16, 0.f, s);
   };
@@ -1101,11 +1118,13 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     return rc;
   if (sl0)
     hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.sl0_act, (int64_t)P.sl0_blocks_total,
-                       P.sl0_freq, imp.ref_count > 0.f ? (int64_t)P.sl0_blocks_total : (int64_t)0, 1.0, recon_coeff,
-                       imp.coeff, imp.freq_coeff, losses);
+                       P.sl0_freq, imp.ref_count > 0.f ? (int64_t)P.sl0_blocks_total : (int64_t)0,
+                       imp.ema.on() ? (const float*)P.sl0_fb : nullptr, 1.0, recon_coeff, imp.coeff, imp.freq_coeff,
+                       losses);
   else
     hipLaunchKernelGGL(k_lm_losses, dim3(1), dim3(1024), 0, s, P.pos_kl, N, P.imp_part, (int64_t)P.imp_total,
-                       (const float*)nullptr, (int64_t)0, 1.0 / (double)N, recon_coeff, imp.coeff, 0.f, losses);
+                       (const float*)nullptr, (int64_t)0, (const float*)nullptr, 1.0 / (double)N, recon_coeff,
+                       imp.coeff, 0.f, losses);
   hipLaunchKernelGGL(k_lm_fill, dim3(ew_blocks(N)), dim3(256), 0, s, P.gpos, N, recon_coeff / (float)N);
   if ((rc = pd_streamed_kl_bwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.stats, P.gpos,
                                P.d_act, P.kl_ws, P.kl_ws_bytes, s)))
@@ -1240,11 +1259,15 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
                      int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                     float imp_coeff, float freq_coeff, float ref_count, float recon_coeff, int n_kl_chunks,
+                     float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                     float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, int n_kl_chunks,
                      float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
                      size_t workspace_bytes, void* stream) {
   LMRecorder rec{nullptr, nullptr, 0, 0, nullptr};
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_lm_stack_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   return lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base, W,
                       V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses, dV, dU,
                       d_ci_pre, workspace, workspace_bytes, stream, rec);
@@ -1256,11 +1279,15 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
                            uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
                            int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                            float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                            void** events, int32_t* categories, int capacity, int* n_recorded) {
   LMRecorder rec{events, categories, capacity, 0, nullptr};
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_lm_stack_step_timed", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   int rc = lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base,
                         W, V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses,
                         dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);

@@ -770,16 +770,19 @@ static void launch_token_bwd(const float* d_w_part, int n_part, const int32_t* i
 
 // losses[0..3] = {loss, recon, activity, frequency}: recon = rec_scale * sum(rec_part),
 // activity = imp_scale * sum(imp_part), frequency = sum(freq_part) (n_freq = 0: none),
-// loss = recon_coeff recon + imp_coeff activity + freq_coeff frequency; every sum in a
+// loss = recon_coeff recon + imp_coeff activity + freq_coeff frequency; with fb_part (the
+// EMA estimator's batch penalty) losses[4] = sum(fb_part) over n_freq; every sum in a
 // fixed order in double.
 __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, const float* __restrict__ imp_part,
-                             int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq, double rec_scale,
-                             double imp_scale, float recon_coeff, float imp_coeff, float freq_coeff,
-                             float* __restrict__ losses) {
-  __shared__ double sr[16], si[16], sq[16];
-  double r = 0.0, m = 0.0, fq = 0.0;
+                             int64_t n_imp, const float* __restrict__ freq_part, int64_t n_freq,
+                             const float* __restrict__ fb_part, double rec_scale, double imp_scale, float recon_coeff,
+                             float imp_coeff, float freq_coeff, float* __restrict__ losses) {
+  __shared__ double sr[16], si[16], sq[16], sb[16];
+  double r = 0.0, m = 0.0, fq = 0.0, fb = 0.0;
   for (int i = threadIdx.x; i < n_rec; i += blockDim.x) r += rec_part[i];
   for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fq += freq_part[i];
+  if (fb_part)
+    for (int64_t i = threadIdx.x; i < n_freq; i += blockDim.x) fb += fb_part[i];
   // four independent chains keep four loads in flight per lane; combined in a fixed order
   double m4[4] = {0.0, 0.0, 0.0, 0.0};
   const int64_t step = blockDim.x;
@@ -793,19 +796,23 @@ __global__ void k_moe_losses(const float* __restrict__ rec_part, int n_rec, cons
   r = wave_sum_d(r);
   m = wave_sum_d(m);
   fq = wave_sum_d(fq);
+  fb = wave_sum_d(fb);
   if (threadIdx.x % 64 == 0) {
     sr[threadIdx.x / 64] = r;
     si[threadIdx.x / 64] = m;
     sq[threadIdx.x / 64] = fq;
+    sb[threadIdx.x / 64] = fb;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double a = 0, b = 0, q = 0;
+    double a = 0, b = 0, q = 0, qb = 0;
     for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
       a += sr[i];
       b += si[i];
       q += sq[i];
+      qb += sb[i];
     }
+    if (fb_part) losses[4] = (float)qb;
     a *= rec_scale;
     b *= imp_scale;
     losses[0] = (float)(recon_coeff * a + imp_coeff * b + freq_coeff * q);
@@ -1022,7 +1029,7 @@ struct MoEPlan {
   float *colsrc, *rowdm, *qjob;  // persistent sources: group column sums, job row sums, job delta cotangents
   int32_t* goff;
   float *logits, *logitsc, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
-  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq;  // smooth-L0: per site-layer regions
+  float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq, *sl0_fb;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
   bf16_t *d_dout, *d_acts[3], *d_din, *d_g, *d_u, *dxa, *dxb;  // d_acts[si]: site si
@@ -1095,6 +1102,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.sl0_slope = A.take<float>(P.sl0_slope_per_site * 3 * L);
   P.sl0_act = A.take<float>(P.sl0_blocks_per_site * 3 * L);
   P.sl0_freq = A.take<float>(P.sl0_blocks_per_site * 3 * L);
+  P.sl0_fb = A.take<float>(P.sl0_blocks_per_site * 3 * L);
   P.colsrc = A.take<float>(D.S && D.S < T ? (size_t)(cdiv(J, TILE) + (int64_t)D.E * D.S) * D.c : 1);
   P.rowdm = A.take<float>(D.S ? (size_t)J * cdiv(D.c, TILE) : 1);
   P.qjob = A.take<float>(D.S ? (size_t)J : 1);
@@ -1289,8 +1297,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     hipEvent_t layer(int l) const { return layer_ev[l % LAYER_EVENTS]; }
   } cs;
   const bool side = !reuse_clean && L > 1;
+  AuxStream ax;  // its lease is held until this call has enqueued all of its work
   if (side || want_wgrads) {
-    AuxStream ax;
     if ((rc0 = aux_stream(0, 11 + std::min(L, LAYER_EVENTS), ax))) return rc0;
     cs.st = ax.st;
     cs.start = ax.ev[0];
@@ -1436,8 +1444,10 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       if (sl0) {  // this site's frequencies, loss partials and backward slopes
         const size_t sl = (size_t)l * 3 + si;
         hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(E, c)), dim3(256), 0, s, ma.colpart, S.offsets, E, J, c,
-                           1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count, P.sl0_slope + sl * P.sl0_slope_per_site,
-                           P.sl0_act + sl * P.sl0_blocks_per_site, P.sl0_freq + sl * P.sl0_blocks_per_site);
+                           1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count,
+                           imp.ema.at((int64_t)sl * P.sl0_slope_per_site), P.sl0_slope + sl * P.sl0_slope_per_site,
+                           P.sl0_act + sl * P.sl0_blocks_per_site, P.sl0_freq + sl * P.sl0_blocks_per_site,
+                           imp.ema.on() ? P.sl0_fb + sl * P.sl0_blocks_per_site : nullptr);
       }
     };
     // ---- gate and up sites: both products of each stage in one paired launch
@@ -1499,11 +1509,12 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.sl0_act,
                        (int64_t)(P.sl0_blocks_per_site * 3 * L), P.sl0_freq,
                        imp.ref_count > 0.f ? (int64_t)(P.sl0_blocks_per_site * 3 * L) : (int64_t)0,
-                       1.0 / (double)nres, 1.0, recon_coeff, imp.coeff, imp.freq_coeff, losses);
+                       imp.ema.on() ? (const float*)P.sl0_fb : nullptr, 1.0 / (double)nres, 1.0, recon_coeff,
+                       imp.coeff, imp.freq_coeff, losses);
   else
     hipLaunchKernelGGL(k_moe_losses, dim3(1), dim3(1024), 0, s, P.rec_part, REC_BLOCKS, P.imp_part,
-                       (int64_t)(P.imp_per_site * 3 * L), (const float*)nullptr, (int64_t)0, 1.0 / (double)nres,
-                       1.0 / (double)T, recon_coeff, imp.coeff, 0.f, losses);
+                       (int64_t)(P.imp_per_site * 3 * L), (const float*)nullptr, (int64_t)0, (const float*)nullptr,
+                       1.0 / (double)nres, 1.0 / (double)T, recon_coeff, imp.coeff, 0.f, losses);
   // ================= backward
   bf16_t* dr = P.dr_a;
   bf16_t* dr_next = P.dr_b;
@@ -1670,11 +1681,15 @@ int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
                       uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value, int layout, int imp_kind,
                       float p, float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                      const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                       float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
                       float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
                       void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_moe_stack_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
+                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
                        draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd,
                        d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
@@ -1686,12 +1701,16 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
                               const void* ci_pre, const void* src, int src_dtype, const void* src_delta,
                               int delta_dtype, int64_t rows_per_source, int imp_kind, float p, float gamma,
                               int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                              const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                               float recon_coeff, int want_weight_grads, int reuse_clean, float* losses, float* dVg,
                               float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
                               float* d_src, float* d_src_delta, int32_t* top_idx_out, void* workspace,
                               size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_moe_stack_step_sources", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
+                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   const SrcArgs sa{src, src_dtype, src_delta, delta_dtype, rows_per_source, want_weight_grads, d_src, d_src_delta};
   if (rows_per_source <= 0 || T % rows_per_source)
     return fail(PD_EINVAL, "pd_moe_stack_step_sources: rows_per_source must divide T");
@@ -1709,14 +1728,18 @@ int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
                             const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
                             int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
-                            float freq_coeff, float ref_count, float recon_coeff, float* losses, float* dVg,
+                            float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
+                            float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg,
                             float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
                             int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream,
                             void** events, int32_t* categories, int capacity, int* n_recorded) {
   if (!events || !categories || capacity <= 0 || !n_recorded)
     return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
   Recorder rec{events, categories, capacity, 0, nullptr};
-  const ImpSpec imp{imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_moe_stack_step_timed", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
+                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
   int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
                          draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
                          dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);

@@ -13,6 +13,7 @@ constexpr int AUX_MAX_EVENTS = 256;  // reserved up front, so a pool never moves
 struct AuxSlot {
   hipStream_t st = nullptr;
   std::vector<hipEvent_t> ev;
+  std::mutex use;  // held by one entry point's enqueue sequence at a time
 };
 std::mutex g_aux_mu;
 AuxSlot g_aux[AUX_MAX_DEVICES][2];
@@ -24,8 +25,12 @@ int aux_stream(int which, int n_events, AuxStream& out) {
     return fail(PD_EINVAL, "aux_stream: bad arguments (at most 256 events)");
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= AUX_MAX_DEVICES)
     return fail(PD_ELAUNCH, "aux_stream: no current HIP device in range");
-  std::lock_guard<std::mutex> lock(g_aux_mu);
+  if (out.lease.owns_lock()) return fail(PD_EINVAL, "aux_stream: this AuxStream already holds a lease");
   AuxSlot& a = g_aux[dev][which];
+  // Take the slot for this call first (waiting for another thread's call to finish its
+  // enqueue), then grow its stream / event pool under the creation lock.
+  std::unique_lock<std::mutex> lease(a.use);
+  std::lock_guard<std::mutex> lock(g_aux_mu);
   hipError_t e = hipSuccess;
   if (!a.st) {
     hipStream_t st = nullptr;
@@ -43,6 +48,7 @@ int aux_stream(int which, int n_events, AuxStream& out) {
   if (e != hipSuccess) return fail(PD_ELAUNCH, std::string("aux_stream: ") + hipGetErrorString(e));
   out.st = a.st;
   out.ev = a.ev.data();
+  out.lease = std::move(lease);
   return PD_OK;
 }
 

@@ -32,7 +32,7 @@ class DenseStepGrads:
     db_in: torch.Tensor
     dw_out: torch.Tensor
     db_out: torch.Tensor
-    losses: torch.Tensor  # [4] fp32: loss, recon, activity, frequency
+    losses: torch.Tensor  # [4] fp32: loss, recon, activity, frequency (+ the batch frequency with the EMA)
 
 
 class DenseSiteStep:
@@ -50,9 +50,11 @@ class DenseSiteStep:
         self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
+        # the EMA frequency estimate over the site's C components (None: the batch estimate)
+        self.frequency = self.imp_min.new_estimate(C, dev)
         self.grads = DenseStepGrads(torch.empty(d_in, C, **f32), torch.empty(C, d_out, **f32), torch.empty(C, H, **f32),
                                     torch.empty(C, H, **f32), torch.empty(C, H, **f32), torch.empty(C, **f32),
-                                    torch.empty(4, **f32))
+                                    torch.empty(5 if self.frequency else 4, **f32))
         nbytes = L.load().pd_dense_step_workspace_size(self.dt, T, d_in, d_out, C, H)
         self.workspace = L.workspace(nbytes, dev)
 
@@ -66,13 +68,16 @@ class DenseSiteStep:
         g = self.grads
         args = [self.dt, self.T, self.d_in, self.d_out, self.C, self.H, L.ptr(x), L.ptr(W), L.ptr(V), L.ptr(U),
                 L.ptr(w_in), L.ptr(b_in), L.ptr(w_out), L.ptr(b_out), mask_key[0], mask_key[1], delta_key[0],
-                delta_key[1], int(self.use_delta), self.draw, self.layout, *self.imp_min.c_args(), self.recon_coeff,
+                delta_key[1], int(self.use_delta), self.draw, self.layout, *self.imp_min.c_args(self.frequency),
+                self.recon_coeff,
                 L.ptr(g.losses), L.ptr(g.dV), L.ptr(g.dU), L.ptr(g.dw_in), L.ptr(g.db_in), L.ptr(g.dw_out),
                 L.ptr(g.db_out), L.ptr(self.workspace), self.workspace.numel(), L.stream()]
         if events is None:
             L.call("pd_dense_step", *args)
         else:
             L.call("pd_dense_step_timed", *args, events)
+        if self.frequency is not None:
+            self.frequency.count += 1
         return g
 
     @staticmethod

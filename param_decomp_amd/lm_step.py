@@ -62,7 +62,10 @@ class LMStackStep:
         dev = torch.device(device)
         N = B * T
         f32 = dict(dtype=torch.float32, device=dev)
-        self.losses = torch.empty(4, **f32)  # total, kl, activity, frequency
+        # the EMA frequency estimate, [L][kind][C_kind] layer-major (None: the batch estimate)
+        self.frequency = self.imp_min.new_estimate(n_layers * sum(self.C.values()), dev)
+        # total, kl, activity, frequency (+ the batch frequency with the EMA)
+        self.losses = torch.empty(5 if self.frequency else 4, **f32)
         self.dV, self.dU, self.d_ci_pre = {}, {}, {}
         for k in KINDS:
             din, dout = site_dims(k, d, n_head, n_kv_head, d_mlp)
@@ -92,15 +95,21 @@ class LMStackStep:
         Wa, Va, Ua, Ca = self._keep
         return [B, T, d, H, KV, f, V, Ln, self._cs, L.ptr(tokens), L.ptr(w.wte), L.ptr(w.ln1), L.ptr(w.ln2),
                 L.ptr(w.norm), self.eps, self.rope_base, Wa, Va, Ua, Ca, draw_key[0], draw_key[1], int(self.use_delta),
-                self.layout, *self.imp_min.c_args(), self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
+                self.layout, *self.imp_min.c_args(self.frequency), self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
                 self._dU, self._dci, L.ptr(self.workspace), self.workspace.numel(), L.stream()]
 
     def step(self, tokens: torch.Tensor, w: LMWeights, ci_pre: dict, draw_key: Key):
         L.call("pd_lm_stack_step", *self._args(tokens, w, ci_pre, draw_key))
+        self._advance()
         return self
+
+    def _advance(self):
+        if self.frequency is not None:
+            self.frequency.count += 1
 
     def step_timed(self, tokens, w, ci_pre, draw_key, events: ctypes.Array, categories: torch.Tensor) -> int:
         n = ctypes.c_int(0)
         L.call("pd_lm_stack_step_timed", *self._args(tokens, w, ci_pre, draw_key), events,
                ctypes.c_void_p(categories.data_ptr()), len(events), ctypes.byref(n))
+        self._advance()
         return n.value

@@ -63,7 +63,12 @@ class MoEStackStep:
         dev = torch.device(device)
         f32 = dict(dtype=torch.float32, device=dev)
         Ln = n_layers
-        self.losses = torch.empty(4, **f32)  # loss, recon, activity, frequency
+        # the EMA frequency estimate over every site's [E * c] components, [L, 3, E * c]
+        # (None: the batch estimate); advanced by `step` and the final (weight-gradient)
+        # call of `step_sources`, not by the adversary's warmup ascents
+        self.frequency = self.imp_min.new_estimate(Ln * 3 * E * c, dev)
+        # loss, recon, activity, frequency (+ the batch frequency with the EMA)
+        self.losses = torch.empty(5 if self.frequency else 4, **f32)
         self.dV = {"gate": torch.empty(Ln, E, d, c, **f32), "up": torch.empty(Ln, E, d, c, **f32),
                    "down": torch.empty(Ln, E, f, c, **f32)}
         self.dU = {"gate": torch.empty(Ln, E, c, f, **f32), "up": torch.empty(Ln, E, c, f, **f32),
@@ -87,7 +92,7 @@ class MoEStackStep:
         return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
                 L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
                 draw_key[0], draw_key[1], int(self.use_delta), self.source_value, self.layout,
-                *self.imp_min.c_args(), self.recon_coeff, L.ptr(self.losses),
+                *self.imp_min.c_args(self.frequency), self.recon_coeff, L.ptr(self.losses),
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
                 L.ptr(self.workspace), self.workspace.numel(), L.stream()]
@@ -114,15 +119,23 @@ class MoEStackStep:
                L.ptr(w.Ud), L.ptr(ci_pre), L.ptr(src), L.dtype_code(src.dtype),
                None if src_delta is None else L.ptr(src_delta),
                L.F32 if src_delta is None else L.dtype_code(src_delta.dtype), self.rows_per_source,
-               *self.imp_min.c_args(), self.recon_coeff, int(g), int(reuse_clean), L.ptr(self.losses),
+               *self.imp_min.c_args(self.frequency if g else None), self.recon_coeff, int(g), int(reuse_clean),
+               L.ptr(self.losses),
                P(self.dV["gate"]),
                P(self.dU["gate"]), P(self.dV["up"]), P(self.dU["up"]), P(self.dV["down"]), P(self.dU["down"]),
                L.ptr(self.d_ci_pre), L.ptr(self.d_src), L.ptr(self.d_src_delta), L.ptr(self.top_idx),
                L.ptr(self.workspace), self.workspace.numel(), L.stream())
+        if g:
+            self._advance()
         return self
+
+    def _advance(self):
+        if self.frequency is not None:
+            self.frequency.count += 1
 
     def step(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, draw_key: Key):
         L.call("pd_moe_stack_step", *self._args(x0, w, ci_pre, draw_key))
+        self._advance()
         return self
 
     def step_timed(self, x0, w, ci_pre, draw_key, events: ctypes.Array, categories: torch.Tensor) -> int:
@@ -131,4 +144,5 @@ class MoEStackStep:
         n = ctypes.c_int(0)
         L.call("pd_moe_stack_step_timed", *self._args(x0, w, ci_pre, draw_key), events,
                ctypes.c_void_p(categories.data_ptr()), len(events), ctypes.byref(n))
+        self._advance()
         return n.value

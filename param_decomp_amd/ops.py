@@ -96,14 +96,18 @@ def gate_bwd(h, w_in, b_in, w_out, b_out, dg_raw, precise: bool):
 
 
 def impmin(ci_upper, *, kind: int, p=1.0, eps=0.0, beta=0.0, world_size=1.0, gamma=1.0, normalize_at_one=False,
-           ref_count=0.0, coeff_act=1.0, coeff_freq=0.0, want_grad=False):
+           ref_count=0.0, coeff_act=1.0, coeff_freq=0.0, want_grad=False, ema=None, ema_out=None, ema_count=0.0,
+           ema_halflife=0.0):
+    """out[0] = activity, out[1] = frequency penalty, out[2] = the batch penalty when
+    `ema` (the fp32 [C] estimate before this batch) is given; `ema_out` receives the new
+    estimate (may be `ema` itself)."""
     rows, C = _flat_rows(ci_upper)
-    out = torch.empty(2, dtype=torch.float32, device=ci_upper.device)
+    out = torch.zeros(3, dtype=torch.float32, device=ci_upper.device)
     grad = torch.empty_like(ci_upper) if want_grad else None
     ws = L.workspace(L.load().pd_impmin_workspace_size(rows, C), ci_upper.device)
     L.call("pd_impmin", L.ptr(ci_upper), L.dtype_code(ci_upper.dtype), rows, C, kind, p, eps, beta, world_size, gamma,
-           int(normalize_at_one), ref_count, coeff_act, coeff_freq, L.ptr(out), L.ptr(grad), L.ptr(ws), ws.numel(),
-           L.stream())
+           int(normalize_at_one), ref_count, L.ptr(ema), L.ptr(ema_out), float(ema_count), float(ema_halflife),
+           coeff_act, coeff_freq, L.ptr(out), L.ptr(grad), L.ptr(ws), ws.numel(), L.stream())
     return out, grad
 
 

@@ -218,3 +218,33 @@ def test_smooth_l0_terms_and_gradient_match_the_reference_formula():
             _, _, dup = po.impmin_site_terms(po.upper_leaky(ci[l][k]), spec, 10)
             want = po.upper_leaky_vjp(ci[l][k], dup)
             np.testing.assert_allclose(out["d_ci_pre"][l][k], want, rtol=1e-10, atol=1e-14)
+
+
+def test_smooth_l0_ema_step_reads_the_debiased_estimate():
+    """With the EMA estimate the LM step's frequency term is sum Phi(f_hat) over every
+    site (ema_frequency_penalty of the per-site frequencies, itself pinned by the
+    reference's closed forms), the new estimates are ema + alpha (f - ema), the batch
+    penalty is the batch arm's, and at count 0 from a zero estimate every output equals
+    the batch arm's (the first observation reproduces the un-smoothed penalty)."""
+    from oracle import pd_oracle as po
+
+    cfg, params, tokens, ci = _small()
+    spec = po.ImpMin("smooth_l0", coeff=0.7, gamma=0.25, normalize_at_one=True, freq_coeff=0.3, ref_count=50.0,
+                     ema_halflife=7.0)
+    rng = np.random.default_rng(3)
+    sites = [(l, k) for l in range(cfg.n_layers) for k in cfg.kinds if k in cfg.C]
+    ema = [{k: rng.uniform(0.0, 0.5, size=cfg.C[k]) for k in cfg.C} for _ in range(cfg.n_layers)]
+    out = lo.lm_stack_step(cfg, params, tokens, ci, (7, 11), recon_coeff=0.0, imp_min=spec, freq_ema=ema,
+                           ema_count=2.0)
+    freqs = {(l, k): po.smooth_l0_psi(po.upper_leaky(ci[l][k]), 0.25, True).mean(0) for l, k in sites}
+    want, new = po.ema_frequency_penalty(freqs, {(l, k): ema[l][k] for l, k in sites}, 2.0, 7.0, 50.0)
+    assert out["freq"] == pytest.approx(want, rel=1e-12)
+    for l, k in sites:
+        np.testing.assert_allclose(out["freq_ema"][l][k], new[(l, k)], rtol=1e-12)
+    batch = lo.lm_stack_step(cfg, params, tokens, ci, (7, 11), recon_coeff=0.0, imp_min=spec)
+    assert out["freq_batch"] == pytest.approx(batch["freq"], rel=1e-12)
+    zero = [{k: np.zeros(cfg.C[k]) for k in cfg.C} for _ in range(cfg.n_layers)]
+    first = lo.lm_stack_step(cfg, params, tokens, ci, (7, 11), recon_coeff=0.0, imp_min=spec, freq_ema=zero)
+    assert first["freq"] == pytest.approx(batch["freq"], rel=1e-12)
+    for l, k in sites:
+        np.testing.assert_allclose(first["d_ci_pre"][l][k], batch["d_ci_pre"][l][k], rtol=1e-10, atol=1e-15)

@@ -289,6 +289,37 @@ def test_smooth_l0_moe_step_matches_the_autograd_restatement():
             np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
 
 
+def test_smooth_l0_ema_moe_step_matches_the_autograd_restatement():
+    """With the EMA frequency estimate (mid-run: count 4, a nonzero estimate per expert
+    block) the NumPy oracle's slope Phi'(f_hat) equals torch autograd of the reference's
+    surrogate Phi(f_hat) + Phi'(f_hat) (f - sg(f)) through the scatter form, and the new
+    estimate is ema + alpha (f - ema) per (layer, site)."""
+    cfg = mo.MoEConfig(T=48, d=16, f=8, E=6, k=2, c=4, L=2)
+    rng = np.random.default_rng(17)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    spec = po.ImpMin("smooth_l0", coeff=0.5, gamma=0.2, normalize_at_one=True, freq_coeff=0.3, ref_count=96.0,
+                     ema_halflife=5.0)
+    ema = rng.uniform(0.0, 0.3, size=(cfg.L, 3, cfg.E * cfg.c))
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), recon_coeff=1.5, imp_min=spec, freq_ema=ema, ema_count=4.0)
+    b = mo.moe_stack_step_torch(cfg, params, x0, ci, (3, 4), recon_coeff=1.5, imp_min=spec, freq_ema=ema,
+                                ema_count=4.0)
+    batch = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), recon_coeff=1.5, imp_min=spec)
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-10) and b["freq"] == pytest.approx(a["freq"], rel=1e-10)
+    assert a["freq_batch"] == pytest.approx(batch["freq"], rel=1e-12) and abs(a["freq"] - batch["freq"]) > 1e-3
+    for l in range(cfg.L):
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            np.testing.assert_allclose(b["grads"][l][n], a["grads"][l][n], rtol=1e-8, atol=1e-12)
+        for si, s in enumerate(mo.SITES):
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
+            up = po.upper_leaky(ci[l][s])
+            F = np.zeros((cfg.E, cfg.c))
+            np.add.at(F, batch["top_idx"][l].reshape(-1), po.smooth_l0_psi(up, 0.2, True).reshape(-1, cfg.c))
+            alpha, _ = po.ema_decay_terms(4.0, 5.0)
+            np.testing.assert_allclose(a["freq_ema"][l, si], ema[l, si] + alpha * (F.reshape(-1) / cfg.T - ema[l, si]),
+                                       rtol=1e-12)
+
+
 @pytest.mark.parametrize("rps", [48, 12, 1])
 def test_persistent_sources_match_the_autograd_restatement(rps):
     """Persistent source tables (the `c`, `bc` and `bsc` shapes: 48, 12 and 1 tokens per
