@@ -103,7 +103,7 @@ def test_dense_step_ema_three_steps(device, dtype):
     gp64 = po.GateParams(*(np64(t) for t in gate))
     ema = np.zeros(C)
     bf = dtype == torch.bfloat16
-    rtol, floor = (2e-2, 1e-2) if bf else (1e-4, 1e-4)
+    rtol, floor = (2e-2, 1e-2) if bf else (1e-5, 1e-5)  # fp32: the smooth-L0 floor of the dense parity test
     for s in range(3):
         draw_key = tf.fold_in(tf.prng_key(5), 1 + s)
         mk, dk = step.site_keys(draw_key, 0)

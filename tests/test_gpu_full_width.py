@@ -7,10 +7,14 @@ those workloads select is compared against the oracle, not only checked for fini
   several k stages, and ragged per-expert contraction lengths;
 - the register-staged 256x256 dense tile (`k_gemm_bf16` on `TileCfg<256,256>`, taken
   for operands that are not both K-contiguous once the grid has >= 192 such tiles);
-- the public grouped products at K = N = 512 with ragged and empty groups.
+- the public grouped products at K = N = 512 with ragged and empty groups;
+- the LM stack at the Llama-4L widths (the streamed KL's dual products at V = 50277) and
+  the dense step at 768 -> 3072, C = 4096.
 
 Reference semantics: `pd/targets/qwen36_moe.py:2752-2837` (decomposed experts in job
-space), `pd/routed/experts.py:209-348` (grouped products and the ragged dW).
+space), `pd/routed/experts.py:209-348` (grouped products and the ragged dW),
+`pd/targets/transformer.py:1031-1140` and `pd/targets/losses.py:102-163` (the LM step),
+`pd/core/decomposed_linear.py:142-175` (the dense site).
 """
 
 import numpy as np
@@ -147,3 +151,80 @@ def test_grouped_products_at_k_n_512(device):
     _close(_np(dwk), want_dw, 1e-5, 1e-6, "dw kmajor fp32")
     for e in (3, 17, 41):
         assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dwk[e]) == 0
+
+
+def test_lm_stack_step_at_benchmark_widths_matches_oracle(device):
+    """The Llama-4L widths (d_model 768, 12 heads, d_mlp 3072, vocab 50277, C = 1024
+    attention / 4096 MLP, KL over 3 vocab chunks) on one 512-token sequence through 2
+    layers: the KL dual products at V = 50277 and d = 768, the tied head's input
+    gradient, and every site product at the benchmark's widths against the LM oracle's
+    bf16 storage model (elementwise 2e-2 plus a 2e-2 floor of each tensor's largest
+    magnitude, and 2e-2 in relative norm; test_gpu_lm.py states why). About 20 s of
+    oracle time."""
+    from test_gpu_lm import _close as lm_close
+    from test_gpu_lm import _setup
+
+    from oracle import lm_oracle as lo
+    from param_decomp_amd.lm_step import KINDS, LMStackStep
+
+    B, T = 1, 512
+    cfg = lo.LMConfig(n_layers=2, d=768, n_head=12, n_kv_head=12, d_mlp=3072, vocab=50277,
+                      C={"q_proj": 1024, "k_proj": 1024, "v_proj": 1024, "o_proj": 1024, "c_fc": 4096,
+                         "down_proj": 4096})
+    params, tokens, ci, w, ci_t, tok_t = _setup(cfg, B, T, 31, device)
+    key = (9, 41)
+    spec = po.ImpMin("pnorm", p=2.0, coeff=1e-3)
+    step = LMStackStep(B, T, cfg.d, cfg.n_head, cfg.n_kv_head, cfg.d_mlp, cfg.vocab, cfg.n_layers, cfg.C,
+                       device=device, n_kl_chunks=3, recon_coeff=3.0, p=2.0, imp_coeff=1e-3)
+    step.step(tok_t, w, ci_t, key)
+    torch.cuda.synchronize()
+    ref = lo.lm_stack_step(cfg, params, tokens, ci, key, bf16_storage=True, recon_coeff=3.0, imp_min=spec)
+    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"], ref["freq"]],
+                               rtol=2e-2, atol=1e-7)
+    stats = []
+    for l in range(cfg.n_layers):
+        for k in KINDS:
+            lm_close(_np(step.dV[k][l]), ref["dV"][l][k], f"dV[{l}][{k}]", stats)
+            lm_close(_np(step.dU[k][l]), ref["dU"][l][k], f"dU[{l}][{k}]", stats)
+            lm_close(_np(step.d_ci_pre[k][l]), ref["d_ci_pre"][l][k], f"d_ci_pre[{l}][{k}]", stats)
+    worst = max(stats, key=lambda x: x[1])
+    print(f"worst element/scale {worst[1]:.3e} ({worst[0]}), worst relative norm {max(x[2] for x in stats):.3e}")
+
+
+@pytest.mark.parametrize("sl0", [False, True])
+def test_dense_step_at_benchmark_widths_matches_oracle(device, sl0):
+    """The single-linear widths (768 -> 3072, C = 4096, bf16, the delta channel on) on
+    512 tokens: the 256x256 GEMM tiles the step selects at these widths, the tabulated
+    gate forward over 4096 components and the gate backward, against the oracle's bf16
+    storage model at rtol 2e-2 with a 1e-2 floor of each tensor's largest magnitude."""
+    from oracle import threefry as tf
+    from param_decomp_amd.dense_step import DenseSiteStep
+    from param_decomp_amd.losses import ImpMin
+
+    rng = np.random.default_rng(7)
+    T, d_in, d_out, C = 512, 768, 3072, 4096
+    x = rng.normal(size=(T, d_in))
+    W = rng.normal(size=(d_out, d_in)) / np.sqrt(d_in)
+    V = rng.normal(size=(d_in, C)) / np.sqrt(d_in)
+    U = rng.normal(size=(C, d_out)) / np.sqrt(C)
+    gp = po.GateParams(rng.normal(size=(C, 16)) * 1.4, np.zeros((C, 16)), rng.normal(size=(C, 16)) * 0.35,
+                       np.full(C, 0.3))
+    tx, tW, tV, tU = (_bf(a, device) for a in (x, W, V, U))
+    gate = tuple(torch.tensor(np.asarray(a, np.float32), device=device) for a in (gp.w_in, gp.b_in, gp.w_out,
+                                                                                   gp.b_out))
+    spec = (po.ImpMin("smooth_l0", coeff=0.7, gamma=0.2, normalize_at_one=True, freq_coeff=0.4, ref_count=4096.0)
+            if sl0 else po.ImpMin("pnorm", p=2.0, coeff=0.7))
+    imp = ImpMin(spec.kind, spec.p, spec.coeff, spec.gamma, spec.normalize_at_one, spec.freq_coeff, spec.ref_count)
+    step = DenseSiteStep(T, d_in, d_out, C, device=device, recon_coeff=1.3, use_delta=True, imp_min=imp)
+    draw_key = tf.fold_in(tf.prng_key(11), 2)
+    mk, dk = step.site_keys(draw_key, 0)
+    g = step.step(tx, tW, tV, tU, gate, mk, dk)
+    torch.cuda.synchronize()
+    gp64 = po.GateParams(*(_np(t) for t in gate))
+    r = po.dense_site_step(_np(tx), _np(tW), _np(tV), _np(tU), gp64, draw_key, recon_coeff=1.3,
+                           mask_dtype="bfloat16", use_delta=True, bf16_storage=True, imp_min=spec)
+    np.testing.assert_allclose(g.losses.cpu().numpy(), [r.loss, r.recon, r.imp, r.freq], rtol=BF16_RTOL, atol=1e-7)
+    _close(_np(g.dU), r.dU, BF16_RTOL, 1e-2, "dU")
+    _close(_np(g.dV), r.dV, BF16_RTOL, 1e-2, "dV")
+    for got, want, name in zip((g.dw_in, g.db_in, g.dw_out, g.db_out), r.dgate, ("dw_in", "db_in", "dw_out", "db_out")):
+        _close(_np(got), want, BF16_RTOL, 1e-2, name)

@@ -37,6 +37,10 @@ def assert_close(got, want, rtol, atol_frac=1e-3, what=""):
     want = np.asarray(want, np.float64)
     scale = max(np.abs(want).max(), 1e-30)
     err = np.abs(got - want)
+    if rtol <= 1e-4:  # fp32: the floor that rtol 1e-5 alone would need (0: 1e-5 holds as is)
+        need = max(0.0, float(((err - 1e-5 * np.abs(want)) / scale).max()))
+        print(f"[fp32] {what}: max rel {float((err / np.maximum(np.abs(want), 1e-30)).max()):.2e}, "
+              f"floor needed at rtol 1e-5 {need:.2e}")
     bound = rtol * np.abs(want) + atol_frac * scale
     bad = err > bound
     assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} off; worst {err.max():.3e} (scale {scale:.3e})"
@@ -151,7 +155,9 @@ def test_gate_fwd_bwd_fp32(device, precise):
     dh, dwi, dbi, dwo, dbo = ops.gate_bwd(f32(h, device), *tp, f32(dg, device), precise)
     w = po.gate_backward(h, gp, dg)
     for got, want_, name in zip((dh, dwi, dbi, dwo, dbo), w, ("dh", "dw_in", "db_in", "dw_out", "db_out")):
-        assert_close(np64(got), want_, 1e-4, 1e-5 if precise else 3e-5, name)
+        # precise: rtol 1e-5 with a 1e-6 floor (measured need <= 8e-8 of the largest
+        # magnitude); the fast path's erf (A&S 7.1.26, |error| <= 1.5e-7) keeps 3e-5
+        assert_close(np64(got), want_, 1e-5, 1e-6 if precise else 3e-5, name)
 
 
 def test_gate_bf16_h(device):
@@ -179,7 +185,7 @@ def test_impmin_pnorm(device, p, beta):
     out, grad = ops.impmin(f32(up, device), kind=L.IMPMIN_PNORM, p=p, eps=1e-3, beta=beta, world_size=2.0,
                            want_grad=True)
     assert float(out[0]) == pytest.approx(po.impmin_pnorm(up, p, 1e-3, beta, 2), rel=1e-5)
-    assert_close(np64(grad), po.impmin_pnorm_grad(up, p, 1e-3, beta, 2), 1e-4, 1e-6, "pnorm grad")
+    assert_close(np64(grad), po.impmin_pnorm_grad(up, p, 1e-3, beta, 2), 1e-5, 1e-6, "pnorm grad")
 
 
 @pytest.mark.parametrize("normalize", [False, True])
@@ -365,9 +371,11 @@ def test_site_forward_and_backward(device, dtype, with_delta, with_route, shape)
     xs, Ws, Vs, Us, ms = (np64(t) for t in (tx, tW, tV, tU, tm))
     ds = None if td is None else np64(td)
     want, want_xV = po.site_forward(xs, Ws, Vs, Us, ms, ds, r)
+    # fp32: rtol 1e-5 with a floor of 1e-6 of the tensor's largest magnitude, the rounding
+    # of an fp32 reduction against float64 (measured need <= 1.2e-7 on these shapes)
     rtol = 1e-5 if dtype == torch.float32 else BF16_RTOL
-    assert_close(np64(res.output), want, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "site out")
-    assert_close(np64(res.component_activation), want_xV, rtol, 1e-4 if dtype == torch.float32 else 4e-3, "xV")
+    assert_close(np64(res.output), want, rtol, 1e-6 if dtype == torch.float32 else 4e-3, "site out")
+    assert_close(np64(res.component_activation), want_xV, rtol, 1e-6 if dtype == torch.float32 else 4e-3, "xV")
     go = rng.normal(size=want.shape)
     inputs = (tx, tV, tU, tm) + (() if td is None else (td,))
     grads = torch.autograd.grad(res.output, inputs, cv(go))
@@ -376,7 +384,7 @@ def test_site_forward_and_backward(device, dtype, with_delta, with_route, shape)
     if td is not None:  # the weight-delta cotangent (the delta sources of adversarial masking)
         wants = wants + (po.site_delta_grad(xs, Ws, Vs, Us, ms, ds, r, np64(cv(go))),)
     for got, w, name in zip(grads, wants, ("dx", "dV", "dU", "dmask", "d_delta")):
-        assert_close(np64(got), w, rtol, 1e-4 if dtype == torch.float32 else 5e-3, name)
+        assert_close(np64(got), w, rtol, 1e-6 if dtype == torch.float32 else 5e-3, name)
 
 
 @pytest.mark.parametrize("blocked", [False, True])
@@ -456,10 +464,13 @@ def test_dense_step_matches_oracle(device, dtype, use_delta, sl0):
     r = po.dense_site_step(np64(tx), np64(tW), np64(tV), np64(tU), gp64, draw_key, recon_coeff=1.3,
                            mask_dtype="bfloat16" if dtype == torch.bfloat16 else "float32",
                            use_delta=use_delta, bf16_storage=dtype == torch.bfloat16, imp_min=spec)
-    rtol = 1e-4 if dtype == torch.float32 else BF16_RTOL
+    rtol = 1e-5 if dtype == torch.float32 else BF16_RTOL
     losses = g.losses.cpu().numpy()
     np.testing.assert_allclose(losses, [r.loss, r.recon, r.imp, r.freq], rtol=rtol, atol=1e-7)
-    floor = 1e-4 if dtype == torch.float32 else 1e-2
+    # fp32 floor: 1e-6 of the largest magnitude (fp32 reductions against float64; measured
+    # need <= 1.3e-7), 1e-5 with smooth-L0, where one dV entry measured 4.3e-6: a gate value
+    # within fp32 rounding of a squashing kink takes the other backward branch
+    floor = (1e-5 if sl0 else 1e-6) if dtype == torch.float32 else 1e-2
     assert_close(np64(g.dU), r.dU, rtol, floor, "dU")
     assert_close(np64(g.dV), r.dV, rtol, floor, "dV")
     for got, want, name in zip((g.dw_in, g.db_in, g.dw_out, g.db_out), r.dgate, ("dw_in", "db_in", "dw_out", "db_out")):
