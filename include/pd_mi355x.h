@@ -360,6 +360,11 @@ int pd_grouped_gemm_dw_kmajor(const void* lhsT, const void* doutT, const int32_t
  * (values scattered to their expert's block, pd/core/losses.py:316-330), psi =
  * c^2/(c^2 + gamma^2) (times 1 + gamma^2 when normalize_at_one); ref_count = 0 drops
  * the frequency term; freq_ema_in as under pd_dense_step ([L, 3, E*c]).
+ * routes (nullable) uint8 [L, 3, T]: per-token site routes (the recon term's routing,
+ * pd/core/recon.py:219-252); an unrouted token's jobs take the frozen output at that site
+ * (where(route, decomposed + d frozen, frozen), pd/targets/qwen36_moe.py:2822-2827), so
+ * the frozen channel runs with routes even without the delta draws; NULL = every token
+ * routed. pd_moe_stack_step_sources takes no routes.
  * Layouts (all bf16 unless noted): x0 [T,d]; ln fp32 [L,d]; router [L,E,d];
  * Wg, Wu [L,E,d,f]; Wd [L,E,f,d]; Vg, Vu [L,E,d,c]; Ug, Uu [L,E,c,f]; Vd [L,E,f,c];
  * Ud [L,E,c,d]; ci_pre [L,3,T,k,c] (site order gate, up, down; slot s = the token's
@@ -373,12 +378,12 @@ size_t pd_moe_stack_workspace_size(int64_t T, int d, int f, int E, int k, int c,
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                      const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                      int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
-                      float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
-                      float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg, float* dUg,
-                      float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, const uint8_t* routes,
+                      float source_value, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
+                      float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                      float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, float* losses,
+                      float* dVg, float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
+                      int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream);
 /* pd_moe_stack_step with persistent (adversarial) source tables in place of the draws:
  * the reference's SourceMaskIngredients arm (pd/targets/qwen36_moe.py:2151-2163,
  * pd/core/source_mask.py:56-63) over block-factored sources read at each selected value's
@@ -421,13 +426,14 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                            int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
-                            float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
-                            float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg,
-                            float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
-                            int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream,
-                            void** events, int32_t* categories, int capacity, int* n_recorded);
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
+                            const uint8_t* routes, float source_value, int layout, int imp_kind, float p, float gamma,
+                            int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                            const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                            float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu,
+                            float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
+                            size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
+                            int* n_recorded);
 
 /* ---- the TMS toy decomposition step as one fused launch (pd/targets/tms.py:254-388) ----
  * target hid = x W1^T, out = relu(hid W1 + b2); both sites (linear1: W1 [H,F], linear2:
@@ -458,6 +464,11 @@ int pd_tms_step(int64_t B, int F, int H, int C, const float* x, const float* W1,
  * m = lower(ci) + (1 - lower(ci)) uniform(fold_in(fold_in(split(draw_key)[0], kind),
  * layer), [N, C]) and d = uniform(fold_in(fold_in(split(draw_key)[1], kind), layer), [N])
  * in bf16 (pd/targets/transformer.py:1048-1058, 1424-1451); use_delta = 0 is d = 0.
+ * routes (nullable) uint8 [L, 6, N]: per-token site routes (the recon term's routing,
+ * pd/core/recon.py:219-252); an unrouted token's site output is the target's x @ W^T
+ * (where(route, masked, target), pd/core/decomposed_linear.py:72-85), so its masks take
+ * no recon gradient; NULL = every token routed (AllRouting). Size the workspace of a
+ * routed call with use_delta = 1 (the target segment of the site products).
  * Loss: recon_coeff * mean KL(softmax(clean logits) || softmax(masked logits)) (the
  * streamed form, pd/targets/losses.py:102-163, over n_kl_chunks vocab chunks) + the
  * imp-min term: PD_IMPMIN_PNORM: imp_coeff * sum_sites sum_c mean_tokens upper(ci)^p;
@@ -477,11 +488,11 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
-                     int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                     float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
-                     float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, int n_kl_chunks,
-                     float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     int use_delta, const uint8_t* routes, int layout, int imp_kind, float p, float gamma,
+                     int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                     const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                     float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                     void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream);
 /* pd_lm_stack_step recording HIP events at phase boundaries (categories: 0 per-step weight
  * copies and delta draws, 1 frozen forward, 2 site products fwd, 3 mask fwd, 4 attention,
  * 5 norms / adds / GELU / transposes, 6 streamed KL, 7 d_acts and d_input products, 8 dU
@@ -490,8 +501,8 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                            const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
                            const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
-                           uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
-                           int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           uint32_t draw_k1, int use_delta, const uint8_t* routes, int layout, int imp_kind, float p,
+                           float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
                            const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                            float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,

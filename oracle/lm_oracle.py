@@ -67,6 +67,9 @@ class LMConfig:
     mlp: str = "plain"  # "plain" (fc -> gelu_tanh -> down) or "glu" (silu(gate) * up -> down)
     eps: float = 1e-6
     rope_base: float = 10000.0
+    # Llama-3 RoPE scaling (factor, low_freq_factor, high_freq_factor, original context);
+    # None: the plain inverse frequencies
+    rope_scaling: tuple | None = None
 
     @property
     def head_dim(self) -> int:
@@ -152,10 +155,27 @@ def rms_norm(x, w, eps, rb=lambda t: t):
     return w * rb(x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps))
 
 
-def rope_cos_sin(T: int, head_dim: int, base: float):
-    """Rotate-half RoPE tables at positions 0..T-1 (`pd/target_ports/llama.py:100-105`
-    with `inv_freq = base^(-2i/head_dim)`)."""
+def rope_inv_freq(head_dim: int, base: float, scaling=None):
+    """`inv_freq = base^(-2i/head_dim)`, with Llama-3 scaling when `scaling = (factor, low,
+    high, old_ctx)` (`pd/target_ports/llama.py:71-87`): wavelengths above old_ctx / low
+    divide by factor, below old_ctx / high stay, and the band between interpolates with
+    `smooth = (old_ctx / wavelen - low) / (high - low)`."""
     inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=F64) / head_dim))
+    if scaling is None:
+        return inv_freq
+    factor, low, high, old_ctx = scaling
+    wavelen = 2.0 * math.pi / inv_freq
+    scaled = torch.where(wavelen > old_ctx / low, inv_freq / factor, inv_freq)
+    smooth = (old_ctx / wavelen - low) / (high - low)
+    smoothed = (1.0 - smooth) * scaled / factor + smooth * scaled
+    medium = ~(wavelen < old_ctx / high) & ~(wavelen > old_ctx / low)
+    return torch.where(medium, smoothed, scaled)
+
+
+def rope_cos_sin(T: int, head_dim: int, base: float, scaling=None):
+    """Rotate-half RoPE tables at positions 0..T-1 (`pd/target_ports/llama.py:100-105`)
+    over `rope_inv_freq`."""
+    inv_freq = rope_inv_freq(head_dim, base, scaling)
     freqs = torch.arange(T, dtype=F64)[:, None] * inv_freq[None, :]
     emb = torch.cat([freqs, freqs], dim=-1)
     return emb.cos(), emb.sin()
@@ -197,7 +217,7 @@ class _CausalCore(torch.autograd.Function):
         return rb(ds @ k), rb(ds.transpose(-1, -2) @ q), rb(p.transpose(-1, -2) @ do), None
 
 
-def causal_attention(q, k, v, n_head: int, n_kv_head: int, base: float, rb=lambda t: t):
+def causal_attention(q, k, v, n_head: int, n_kv_head: int, base: float, rb=lambda t: t, scaling=None):
     """q [b, t, H*hd], k/v [b, t, KV*hd] -> [b, t, H*hd]: RoPE on q and k, then causal
     softmax(q k^T / sqrt(hd)) v with each kv head serving H/KV query heads."""
     b, t, qd = q.shape
@@ -206,7 +226,7 @@ def causal_attention(q, k, v, n_head: int, n_kv_head: int, base: float, rb=lambd
     qh = q.reshape(b, t, n_head, hd).transpose(1, 2)
     kh = k.reshape(b, t, n_kv_head, hd).transpose(1, 2)
     vh = v.reshape(b, t, n_kv_head, hd).transpose(1, 2)
-    cos, sin = rope_cos_sin(t, hd, base)
+    cos, sin = rope_cos_sin(t, hd, base, scaling)
     cos, sin = rb(cos.to(q.dtype)), rb(sin.to(q.dtype))  # the tables are cast to the activation dtype
     qh, kh = rb(apply_rope(qh, cos, sin)), rb(apply_rope(kh, cos, sin))
     kh = kh.repeat_interleave(rep, dim=1)
@@ -220,35 +240,43 @@ def gelu_tanh(x):
     return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x**3)))
 
 
-def site(x, W, V=None, U=None, mask=None, delta=None, rb=lambda t: t):
+def site(x, W, V=None, U=None, mask=None, delta=None, rb=lambda t: t, route=None):
     """`((x@V) * (m - d)) @ U + d * (x @ W^T)` (`pd/core/decomposed_linear.py:142-175`);
-    the frozen `x @ W^T` when V is None."""
+    the frozen `x @ W^T` when V is None; with `route` ([..., bool]) the unrouted rows take
+    the frozen `x @ W^T` (`blend_target_output`, `:72-85`)."""
     if V is None:
         return rb(x @ W.T)
     xV = rb(x @ V)
     coef = mask if delta is None else mask - delta[..., None]
     acts = rb(xV * coef)
     if delta is None:
-        return rb(acts @ U)
-    # d * (x @ W^T) = (d * x) @ W^T per row: one accumulation with acts @ U, d * x stored bf16
-    return rb(acts @ U + rb(delta[..., None] * x) @ W.T)
+        out = rb(acts @ U)
+    else:
+        # d * (x @ W^T) = (d * x) @ W^T per row: one accumulation with acts @ U, d * x stored bf16
+        out = rb(acts @ U + rb(delta[..., None] * x) @ W.T)
+    if route is None:
+        return out
+    return torch.where(torch.as_tensor(route, dtype=torch.bool)[..., None], out, rb(x @ W.T))
 
 
-def block(cfg: LMConfig, P: dict, r, masks=None, deltas=None, rb=lambda t: t, layer=0):
+def block(cfg: LMConfig, P: dict, r, masks=None, deltas=None, rb=lambda t: t, layer=0, routes=None):
     """One transformer block (`pd/targets/transformer.py:1085-1140`). P holds ln1, ln2
     and W_<kind> [d_out, d_in] for every kind, plus V_<kind>/U_<kind> for decomposed
-    kinds; masks/deltas map kind -> [b, t, C] / [b, t] (absent kind: frozen)."""
+    kinds; masks/deltas/routes map kind -> [b, t, C] / [b, t] / [b, t] bool (absent kind:
+    frozen; absent route: every position routed)."""
     masks = masks or {}
     deltas = deltas or {}
+    routes = routes or {}
 
     def run(kind, x):
         if kind in masks:
-            return site(x, P["W_" + kind], P["V_" + kind], P["U_" + kind], masks[kind], deltas.get(kind), rb=rb)
+            return site(x, P["W_" + kind], P["V_" + kind], P["U_" + kind], masks[kind], deltas.get(kind), rb=rb,
+                        route=routes.get(kind))
         return site(x, P["W_" + kind], rb=rb)
 
     h = rb(rms_norm(r, P["ln1"], cfg.eps, rb))
     q, k, v = run("q_proj", h), run("k_proj", h), run("v_proj", h)
-    a = rb(causal_attention(q, k, v, cfg.n_head, cfg.n_kv_head, cfg.rope_base, rb=rb))
+    a = rb(causal_attention(q, k, v, cfg.n_head, cfg.n_kv_head, cfg.rope_base, rb=rb, scaling=cfg.rope_scaling))
     r = rb(r + run("o_proj", a))
     h2 = rb(rms_norm(r, P["ln2"], cfg.eps, rb))
     if cfg.mlp == "plain":
@@ -262,13 +290,13 @@ def final_act(cfg: LMConfig, params: dict, r, rb=lambda t: t):
     return rb(rms_norm(r, params["norm"], cfg.eps, rb))
 
 
-def forward(cfg: LMConfig, params: dict, r0, masks=None, deltas=None, rb=lambda t: t):
-    """Residual stream r0 [b, t, d] through every layer; masks[l] / deltas[l] per layer
-    (None: the frozen target). Returns the final normed activations [b, t, d]."""
+def forward(cfg: LMConfig, params: dict, r0, masks=None, deltas=None, rb=lambda t: t, routes=None):
+    """Residual stream r0 [b, t, d] through every layer; masks[l] / deltas[l] / routes[l]
+    per layer (None: the frozen target). Returns the final normed activations [b, t, d]."""
     r = r0
     for l, P in enumerate(params["layers"]):
         r = block(cfg, P, r, None if masks is None else masks[l], None if deltas is None else deltas[l], rb=rb,
-                  layer=l)
+                  layer=l, routes=None if routes is None else routes[l])
     return final_act(cfg, params, r, rb=rb)
 
 
@@ -294,7 +322,7 @@ def site_keys(draw_key, cfg: LMConfig, kind: str, layer: int, partitionable=True
 
 def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                   bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64, imp_min=None,
-                  freq_ema=None, ema_count=0.0):
+                  freq_ema=None, ema_count=0.0, routes=None):
     """One stochastic-recon KL + imp-min step, forward and backward. The imp-min term is
     L_p (p, imp_coeff) or `imp_min` (a `pd_oracle.ImpMin`; smooth-L0 with the frequency
     penalty as the reference writes it, `pd/core/losses.py:340-394`: per-site means of
@@ -308,6 +336,8 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
     dicts (ln1, ln2, W_<kind> [d_out, d_in], V_<kind> [d_in, C], U_<kind> [C, d_out])
     as float64 numpy arrays; tokens [b, t] int; ci_pre[l][kind] [b*t, C_kind].
     `uniforms[l][kind] = (u [b*t, C], d [b*t])` replaces the Threefry draws when given.
+    `routes[l][kind]` ([b*t] bool) routes the recon term per token: an unrouted token's
+    site output is the target's (`site`'s route arm).
     `dtype` torch.float32 runs the same arithmetic in fp32 (the CPU baseline's timing
     form; the float64 default is the checker).
     Returns dict(loss, recon, imp, freq, dV[l][kind], dU[l][kind], d_ci_pre[l][kind], u, delta)."""
@@ -378,7 +408,9 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
                         freq = freq + (f_hat * torch.log2(1.0 + a_ * f_hat) + slope * (fr - f_sg)).sum()
             masks[l][kind] = (lo + (1.0 - lo) * T(u)).reshape(b, t, C)
             deltas[l][kind] = T(dl).reshape(b, t) if use_delta else None
-    act_m = forward(cfg, prm, r0, masks, deltas, rb=rb)
+    rts = None if routes is None else [{k: np.asarray(v, bool).reshape(b, t) for k, v in layer.items()}
+                                       for layer in routes]
+    act_m = forward(cfg, prm, r0, masks, deltas, rb=rb, routes=rts)
     recon = kl_per_position(logits(prm, act_m), clean_logits)
     loss = recon_coeff * recon + spec.coeff * imp + (spec.freq_coeff * freq if spec.kind == "smooth_l0" else 0.0)
     wrt = [prm["layers"][l]["V_" + k] for l, k in leaves] + [prm["layers"][l]["U_" + k] for l, k in leaves] + [

@@ -99,7 +99,7 @@ def grouped_T(lhs, rhs, sizes):
 
 def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                    bf16_storage=False, partitionable=True, use_delta=True, deltas=None, source_value=None,
-                   pinned_top_idx=None, imp_min=None, sources=None, freq_ema=None, ema_count=0.0):
+                   pinned_top_idx=None, imp_min=None, sources=None, freq_ema=None, ema_count=0.0, routes=None):
     """params: list over layers of dicts {ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud};
     ci_pre[l][site]: [T, k, c]. `deltas[l][site]` ([T]) replaces the drawn delta when
     given. `pinned_top_idx[l]` ([T, k]) replaces the clean pass's own expert selection
@@ -113,6 +113,9 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     with `imp_min.ema_halflife`) is the EMA frequency estimate before this step after
     `ema_count` observations: the frequency term then reads the debiased estimate, and the
     result holds the new estimate (`freq_ema`) and the batch penalty (`freq_batch`).
+    `routes[l][site]` ([T] bool) routes the recon term per token: an unrouted token's jobs
+    take the frozen output, `where(route, decomposed + d frozen, frozen)`
+    (`pd/targets/qwen36_moe.py:2822-2827`).
 
     `sources = (src, src_delta, rows_per_source)` replaces the draws by persistent
     (adversarial) source tables, the reference's `SourceMaskIngredients` arm
@@ -203,9 +206,10 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             else:
                 dt = np.zeros(T)
             dj = dt[tok][:, None]
+            rj = np.ones((T * k, 1)) if routes is None else np.asarray(routes[l][s], bool)[tok][:, None].astype(float)
             S[s] = dict(pre=pre, lo=lo, up=up, dup=dup, u=ut, m=m_tok.reshape(T * k, c)[jobs.sort_idx], delta=dt,
-                        dj=dj)
-            S[s]["coef"] = S[s]["m"] - dj
+                        dj=dj, rj=rj, bl=np.where(rj > 0, dj, 1.0))
+            S[s]["coef"] = (S[s]["m"] - dj) * rj
         wj = w.reshape(-1)[jobs.sort_idx]
         for s in ("gate", "up"):
             S[s]["h"] = rb(po.grouped_matmul(xj, P["V" + s[0]], jobs.group_sizes))
@@ -213,14 +217,14 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             frozen = rb(po.grouped_matmul(xj, P["W" + s[0]], jobs.group_sizes))
             S[s]["frozen"] = frozen
             S[s]["out"] = rb(rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
-                             + S[s]["dj"] * frozen)
+                             + S[s]["bl"] * frozen)
         gq, uq = S["gate"]["out"], S["up"]["out"]
         din = rb(silu(gq) * uq * wj[:, None])
         S["down"]["h"] = rb(po.grouped_matmul(din, P["Vd"], jobs.group_sizes))
         S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["coef"])
         S["down"]["frozen"] = rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes))
         dout = (rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
-                + S["down"]["dj"] * S["down"]["frozen"])
+                + S["down"]["bl"] * S["down"]["frozen"])
         routed = rb(po.sum_jobs(dout, jobs))
         saved.append(dict(r=r, rinv=rinv, h2=h2, probs=probs, w=w, wj=wj, jobs=jobs, xj=xj, S=S, din=din, idx=idx))
         r = rb(r + routed)
@@ -243,10 +247,10 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         Sd["gout"] = d_dout
         d_acts = rb(grouped_T(d_dout, P["Ud"], sizes))
         grads[l]["Ud"] = po.transposed_grouped_matmul(Sd["acts"], d_dout, sizes)
-        Sd["dm"] = d_acts * Sd["h"]
+        Sd["dm"] = d_acts * Sd["h"] * Sd["rj"]
         d_h = rb(d_acts * Sd["coef"])
         grads[l]["Vd"] = po.transposed_grouped_matmul(sv["din"], d_h, sizes)
-        d_din = rb(grouped_T(d_h, P["Vd"], sizes)) + Sd["dj"] * rb(grouped_T(d_dout, P["Wd"], sizes))
+        d_din = rb(grouped_T(d_h, P["Vd"], sizes)) + Sd["bl"] * rb(grouped_T(d_dout, P["Wd"], sizes))
         # SwiGLU fold
         gq, uq, wj = S["gate"]["out"], S["up"]["out"], sv["wj"]
         sg = silu(gq)
@@ -259,11 +263,11 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             Ss["gout"] = dgo
             d_acts = rb(grouped_T(dgo, P["U" + s[0]], sizes))
             grads[l]["U" + s[0]] = po.transposed_grouped_matmul(Ss["acts"], dgo, sizes)
-            Ss["dm"] = d_acts * Ss["h"]
+            Ss["dm"] = d_acts * Ss["h"] * Ss["rj"]
             d_h = rb(d_acts * Ss["coef"])
             grads[l]["V" + s[0]] = po.transposed_grouped_matmul(sv["xj"], d_h, sizes)
             d_xj = (d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
-                    + Ss["dj"] * rb(grouped_T(dgo, P["W" + s[0]], sizes)))
+                    + Ss["bl"] * rb(grouped_T(dgo, P["W" + s[0]], sizes)))
         # mask pullback to the CI preactivations (token-major)
         for s in SITES:
             Ss = S[s]
@@ -361,7 +365,7 @@ def init_moe(cfg: MoEConfig, rng):
 
 def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                          use_delta=True, partitionable=True, dtype=None, threads=None, imp_min=None,
-                         sources=None, freq_ema=None, ema_count=0.0):
+                         sources=None, freq_ema=None, ema_count=0.0, routes=None):
     """The same step as `moe_stack_step` (no bf16 storage model) written as a torch
     forward whose backward is torch autograd: in float64 it pins `moe_stack_step`'s
     hand-written backward (tests/test_moe_oracle.py). The expert selection and Threefry
@@ -458,7 +462,11 @@ def moe_stack_step_torch(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0,
                 dlt = (t(tf.uniform(dkeys[s], (T,), "bfloat16", partitionable=partitionable)) if use_delta
                        else torch.zeros(T, dtype=dt))
             m = (lo + (1.0 - lo) * u).reshape(T * k, c)[sidx]
-            coef[s] = (m - dlt[tok][:, None], dlt[tok][:, None])
+            if routes is None:
+                coef[s] = (m - dlt[tok][:, None], dlt[tok][:, None])
+            else:  # unrouted tokens: the frozen output alone
+                rj = torch.as_tensor(np.asarray(routes[l][s], bool))[tok][:, None]
+                coef[s] = ((m - dlt[tok][:, None]) * rj, torch.where(rj, dlt[tok][:, None], torch.ones((), dtype=dt)))
         wj = w.reshape(-1)[sidx]
         out = {}
         for s in ("gate", "up"):

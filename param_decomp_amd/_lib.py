@@ -80,10 +80,12 @@ _SIGNATURES = {
     "pd_grouped_gemm_dw": (_c_i32, [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i32, _c_p]),
     "pd_grouped_gemm_dw_kmajor": (_c_i32, [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_i64, _c_p, _c_i32, _c_p]),
     "pd_moe_stack_workspace_size": (_c_sz, [_c_i64] + [_c_i32] * 6),
-    "pd_moe_stack_step": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_u32, _c_u32, _c_i32, _c_f32, _c_i32] +
-                          _IMP_ARGS + [_c_f32] + [_c_p] * 9 + [_c_p, _c_sz, _c_p]),
-    "pd_moe_stack_step_timed": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_u32, _c_u32, _c_i32, _c_f32, _c_i32] +
-                                _IMP_ARGS + [_c_f32] + [_c_p] * 9 + [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
+    "pd_moe_stack_step": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 +
+                          [_c_u32, _c_u32, _c_i32, _c_p, _c_f32, _c_i32] + _IMP_ARGS + [_c_f32] + [_c_p] * 9 +
+                          [_c_p, _c_sz, _c_p]),
+    "pd_moe_stack_step_timed": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 +
+                                [_c_u32, _c_u32, _c_i32, _c_p, _c_f32, _c_i32] + _IMP_ARGS + [_c_f32] + [_c_p] * 9 +
+                                [_c_p, _c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
     "pd_moe_stack_sources_workspace_size": (_c_sz, [_c_i64] + [_c_i32] * 6 + [_c_i64]),
     "pd_moe_stack_step_sources": (_c_i32, [_c_i64] + [_c_i32] * 6 + [_c_p] * 13 + [_c_p, _c_i32, _c_p, _c_i32, _c_i64] +
                                   _IMP_ARGS + [_c_f32, _c_i32, _c_i32] + [_c_p] * 12 + [_c_sz, _c_p]),
@@ -94,11 +96,11 @@ _SIGNATURES = {
     "pd_lm_stack_workspace_size": (_c_sz, [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32, _c_p, _c_i32, _c_i32]),
     "pd_lm_stack_step": (_c_i32,
                          [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
-                         [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] + [_c_p] * 5 +
-                         [_c_sz, _c_p]),
+                         [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_p, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] +
+                         [_c_p] * 5 + [_c_sz, _c_p]),
     "pd_lm_stack_step_timed": (_c_i32,
                                [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
-                               [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] +
+                               [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_p, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] +
                                [_c_p] * 5 + [_c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
     "pd_ci_mlp_workspace_size": (_c_sz, [_c_i32, _c_p, _c_i64]),
     "pd_ci_mlp_fwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 5 + [_c_sz, _c_p]),

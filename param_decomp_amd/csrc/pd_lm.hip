@@ -143,16 +143,19 @@ __global__ __launch_bounds__(256) void k_lm_transpose(const bf16_t* __restrict__
   ttile_store(Tt, dst, ld, r0, R, c0, Cc, tid);
 }
 
-// dst[r * ld + c] = s[r] * src[r * w + c] (s NULL: a plain copy) for r < R, c < w; w % 8
-// == 0, ld % 8 == 0. One wave per row.
+// dst[r * ld + c] = sc[r] * src[r * w + c] for r < R, c < w: sc = s[r] (0 when s is NULL)
+// on routed rows and 1 on rows whose route is 0 (route NULL: every row routed); with
+// neither s nor route, a plain copy. w % 8 == 0, ld % 8 == 0. One wave per row.
 __global__ __launch_bounds__(256) void k_lm_copy_rows(const bf16_t* __restrict__ src, int64_t R, int w,
-                                                      const float* __restrict__ s, bf16_t* __restrict__ dst,
+                                                      const float* __restrict__ s,
+                                                      const uint8_t* __restrict__ route, bf16_t* __restrict__ dst,
                                                       int64_t ld) {
   const int64_t r = (int64_t)blockIdx.x * 4 + wave_id();
   if (r >= R) return;
-  const float sc = s ? s[r] : 1.f;
+  const bool scaled = s || route;
+  const float sc = route && !route[r] ? 1.f : (s ? s[r] : (route ? 0.f : 1.f));
   for (int i = (threadIdx.x & 63) * 8; i < w; i += 512) {
-    if (s) {
+    if (scaled) {
       float v[8];
       load8(src + r * w + i, v);
 #pragma unroll
@@ -186,8 +189,9 @@ struct LMMaskArgs {
   int C;
   uint32_t k0, k1;
   float p;
-  const float* delta;  // [N] or NULL (d = 0)
-  int64_t ld;          // row stride of acts / d_xV (the concatenated operand)
+  const float* delta;    // [N] or NULL (d = 0)
+  const uint8_t* route;  // [N] or NULL (every token routed); unrouted tokens take the target
+  int64_t ld;            // row stride of acts / d_xV (the concatenated operand)
   // smooth-L0 imp-min (PM_SL0): psi = psis * v^2 / (v^2 + g2); per-tile column sums of
   // psi out (colpart), per-component slopes in (slope)
   float g2, psis;
@@ -199,8 +203,9 @@ struct LMMaskArgs {
 #define PD_LM_COL ((threadIdx.x & 15) * 4)
 
 // m = lower(ci) + (1 - lower(ci)) u (u drawn in bf16 over [N, C], counter n*C + c);
-// acts = bf16(xV * (m - d)) into acts[n * ld + c] and acts^T [C, N]; u kept as its 7-bit
-// integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0.
+// acts = bf16(xV * (m - d)) into acts[n * ld + c] and acts^T [C, N] (0 on unrouted tokens,
+// whose output is the target's x @ W^T, pd/core/decomposed_linear.py:72-85); u kept as its
+// 7-bit integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0.
 template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
                                                      bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
@@ -223,6 +228,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
     if (n < a.N && qok) {
       const int64_t idx = n * a.C + q0 + q4;
       const float dt = a.delta ? a.delta[n] : 0.f;
+      const bool routed = !a.route || a.route[n];
       const uint2 pw = *(const uint2*)(a.ci_pre + idx);
       const uint2 hw = *(const uint2*)(xV + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
         const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
         ub |= kb << (8 * e);
         const float u = (float)kb * (1.f / 128.f);
-        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt));
+        o[e] = routed ? f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt)) : (bf16_t)0;
       }
       *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
@@ -261,6 +267,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
 
 // d_xV = bf16(d_acts * (m - d)) into d_xV[n * ld + c] and d_xV^T [C, N]; the CI pullback
 // d_pre = lower_vjp(pre, d_acts * xV * (1 - u)) + upper_vjp(pre, imp_scale * d upper^p).
+// An unrouted token's masked product does not reach the output: d_acts counts as 0 there.
 template <int PM>
 __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
                                                      const uint8_t* __restrict__ ubits, float imp_scale,
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
       const float dt = a.delta ? a.delta[n] : 0.f;
       const uint2 pw = *(const uint2*)(a.ci_pre + idx);
       const uint2 hw = *(const uint2*)(xV + idx);
-      const uint2 dw = *(const uint2*)(d_acts + idx);
+      const uint2 dw = (!a.route || a.route[n]) ? *(const uint2*)(d_acts + idx) : make_uint2(0u, 0u);
       const uint32_t ub = *(const uint32_t*)(ubits + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
@@ -630,9 +637,12 @@ struct LMDims {
   int d, H, KV, f, L, n_chunks;
   int C[LM_NK], din[LM_NK], dout[LM_NK];
   bool use_delta;
+  bool routed = false;  // per-token routes: the target segment is needed without a delta too
   int64_t BH() const { return B * H; }
-  int64_t kcat(int k) const { return C[k] + (use_delta ? din[k] : 0); }   // forward product depth
-  int64_t kcat2(int k) const { return C[k] + (use_delta ? dout[k] : 0); } // d_input product depth
+  // the site products run over [acts | s x] . [U ; W^T] (s = d on routed rows, 1 on the rest)
+  bool cat() const { return use_delta || routed; }
+  int64_t kcat(int k) const { return C[k] + (cat() ? din[k] : 0); }   // forward product depth
+  int64_t kcat2(int k) const { return C[k] + (cat() ? dout[k] : 0); } // d_input product depth
 };
 
 struct Arena {
@@ -831,8 +841,9 @@ static void transpose(const bf16_t* src, int64_t R, int64_t Cc, bf16_t* dst, int
                      R, Cc, dst, ld);
 }
 
-static void copy_rows(const bf16_t* src, int64_t R, int w, const float* sc, bf16_t* dst, int64_t ld, hipStream_t s) {
-  hipLaunchKernelGGL(k_lm_copy_rows, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, src, R, w, sc, dst, ld);
+static void copy_rows(const bf16_t* src, int64_t R, int w, const float* sc, bf16_t* dst, int64_t ld, hipStream_t s,
+                      const uint8_t* route = nullptr) {
+  hipLaunchKernelGGL(k_lm_copy_rows, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, src, R, w, sc, route, dst, ld);
 }
 
 // C = A @ B^T with both operands K-contiguous (the buffer-fed kernel).
@@ -881,8 +892,9 @@ enum {
 static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64_t V, int L, const int32_t* Cs,
                         const int32_t* tokens, const void* wte, const float* ln1, const float* ln2, const float* norm,
                         float eps, float rope_base, const void* const* W, const void* const* Vf, const void* const* Uf,
-                        const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, int layout,
-                        const ImpSpec& imp, float recon_coeff, int n_chunks, float* losses, float* const* dV,
+                        const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
+                        const uint8_t* routes, int layout, const ImpSpec& imp, float recon_coeff, int n_chunks,
+                        float* losses, float* const* dV,
                         float* const* dU, void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
                         LMRecorder& rec) {
   const char* what = "pd_lm_stack_step";
@@ -904,6 +916,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
     return fail(PD_EINVAL, std::string(what) + ": unknown counter layout");
   LMDims D{B, T, B * T, V, d, H, KV, f, L, n_chunks, {}, {}, {}, use_delta != 0};
+  D.routed = routes != nullptr;
   const int qd = H * LM_HD, kvd = KV * LM_HD;
   {
     const int din[LM_NK] = {d, d, d, qd, d, f}, dout[LM_NK] = {qd, kvd, kvd, d, f, d};
@@ -914,7 +927,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     }
   }
   if (!workspace || workspace_bytes < lm_plan(D, nullptr, true).total)
-    return fail(PD_EWORKSPACE, std::string(what) + ": workspace too small");
+    return fail(PD_EWORKSPACE, std::string(what) + ": workspace too small (size routed calls with use_delta = 1)");
   if (D.N * (int64_t)std::max<int64_t>(f, 4096) > ((int64_t)1 << 31) / 2 || D.BH() * T * T > ((int64_t)1 << 31))
     return fail(PD_EUNSUPPORTED, std::string(what) + ": activations of 2 GiB or more");
   LMPlan P = lm_plan(D, (char*)workspace, false);
@@ -961,9 +974,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
       bf16_t* bb = P.BtB[k] + (size_t)l * di * kc2;
       transpose(Vl, di, C, vt, di, s);                       // V^T [C, d_in]
       transpose(Ul, C, dout, bf, kc, s);                     // U^T into [U^T | W]
-      if (D.use_delta) copy_rows(Wl, dout, (int)di, nullptr, bf + C, kc, s);  // W
+      if (D.cat()) copy_rows(Wl, dout, (int)di, nullptr, bf + C, kc, s);  // W
       copy_rows(Vl, di, (int)C, nullptr, bb, kc2, s);        // V into [V | W^T]
-      if (D.use_delta) transpose(Wl, dout, di, bb + C, kc2, s);  // W^T
+      if (D.cat()) transpose(Wl, dout, di, bb + C, kc2, s);  // W^T
     }
   }
   if (D.use_delta)
@@ -1032,6 +1045,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     site_key(k, l, ma.k0, ma.k1);
     ma.p = imp.p;
     ma.delta = D.use_delta ? P.delta + ((size_t)l * LM_NK + k) * N : nullptr;
+    ma.route = routes ? routes + ((size_t)l * LM_NK + k) * N : nullptr;
     ma.ld = D.kcat(k);
     ma.g2 = imp.g2();
     ma.psis = imp.psi_scale();
@@ -1048,7 +1062,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if (r) return r;
     rec.mark(LM_CAT_MASK_FWD);
     const LMMaskArgs ma = mask_args(k, l);
-    if (D.use_delta) copy_rows(x, N, (int)di, ma.delta, S.acat + C, kc, s);
+    if (D.cat()) copy_rows(x, N, (int)di, ma.delta, S.acat + C, kc, s, ma.route);
     float* part = P.imp_part + [&] {
       size_t o = 0;
       for (int ll = 0; ll < l; ++ll)
@@ -1166,7 +1180,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     wg_join(wb);
     rec.mark(LM_CAT_ELEM);
     transpose(g, N, dout, drT, N, s);  // g^T [d_out, N]
-    if (D.use_delta && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s);
+    if (D.cat() && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s, ma.route);
     rec.mark(LM_CAT_GEMM_DX);
     int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
@@ -1258,27 +1272,27 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1, const float* ln2,
                      const float* norm, float eps, float rope_base, const void* const* W, const void* const* V,
                      const void* const* U, const void* const* ci_pre, uint32_t draw_k0, uint32_t draw_k1,
-                     int use_delta, int layout, int imp_kind, float p, float gamma, int normalize_at_one,
-                     float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
-                     float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff, int n_kl_chunks,
-                     float* losses, float* const* dV, float* const* dU, void* const* d_ci_pre, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     int use_delta, const uint8_t* routes, int layout, int imp_kind, float p, float gamma,
+                     int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                     const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                     float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
+                     void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream) {
   LMRecorder rec{nullptr, nullptr, 0, 0, nullptr};
   ImpSpec imp;
   if (int e = make_imp_spec("pd_lm_stack_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
                             ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
     return e;
   return lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base, W,
-                      V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses, dV, dU,
-                      d_ci_pre, workspace, workspace_bytes, stream, rec);
+                      V, U, ci_pre, draw_k0, draw_k1, use_delta, routes, layout, imp, recon_coeff, n_kl_chunks, losses,
+                      dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
                            const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
                            const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
                            const void* const* V, const void* const* U, const void* const* ci_pre, uint32_t draw_k0,
-                           uint32_t draw_k1, int use_delta, int layout, int imp_kind, float p, float gamma,
-                           int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                           uint32_t draw_k1, int use_delta, const uint8_t* routes, int layout, int imp_kind, float p,
+                           float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
                            const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                            float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                            void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
@@ -1289,8 +1303,8 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                             ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
     return e;
   int rc = lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base,
-                        W, V, U, ci_pre, draw_k0, draw_k1, use_delta, layout, imp, recon_coeff, n_kl_chunks, losses,
-                        dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
+                        W, V, U, ci_pre, draw_k0, draw_k1, use_delta, routes, layout, imp, recon_coeff, n_kl_chunks,
+                        losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
   if (n_recorded) *n_recorded = rec.n;
   return rc;
 }

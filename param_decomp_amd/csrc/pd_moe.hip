@@ -247,8 +247,9 @@ struct SiteMaskArgs {
   uint32_t k0, k1;
   int layout;
   float p;
-  const float* delta;  // [T] the site's per-token delta draw, or NULL (d = 0)
-  int k;               // experts per token: job j belongs to token sort_idx[j] / k
+  const float* delta;    // [T] the site's per-token delta draw, or NULL (d = 0)
+  const uint8_t* route;  // [T] the site's per-token route, or NULL (every token routed)
+  int k;                 // experts per token: job j belongs to token sort_idx[j] / k
   float uconst;        // MASK_CONST: the constant source value standing in for u
   // smooth-L0 imp-min (PM_SL0): psi = psis * v^2 / (v^2 + g2); the forward writes the
   // per-(tile, expert) column sums of psi to colpart, the backward reads the per-(expert,
@@ -294,6 +295,9 @@ __device__ inline int64_t src_index(const SiteMaskArgs& a, int32_t slot, int e, 
 }
 
 __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
+// An unrouted token's jobs take the frozen output (pd/core/decomposed_linear.py:72-85):
+// their component coefficients are 0, so their masks get no recon gradient.
+__device__ inline bool job_routed(const SiteMaskArgs& a, int32_t slot) { return !a.route || a.route[slot / a.k]; }
 
 
 // Thread -> (row (tid >> 4) + 16 * pass, columns q4 .. q4 + 3) of a 64x64 job-space tile.
@@ -303,8 +307,8 @@ __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return 
 // Forward mask: m = lower(ci) + (1 - lower(ci)) u with ci and u taken at the job's
 // token-major position sort_idx[j]*c + q (u drawn over [T, k*c] in bf16); acts =
 // bf16(h * (m - delta)) (the component coefficients m - d, pd/core/decomposed_linear.py:65-69;
-// d = 0 without the frozen channel) written as acts [J,c]; u stored as its 7-bit integer;
-// per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
+// d = 0 without the frozen channel; 0 on unrouted tokens) written as acts [J,c]; u stored
+// as its 7-bit integer; per-block partial of upper(ci)^p. c % 8 == 0, J % 8 == 0.
 template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                        bf16_t* __restrict__ acts, uint8_t* __restrict__ ubits,
@@ -328,6 +332,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
       const int32_t slot = a.sort_idx[j];
       const int64_t src = (int64_t)slot * a.c + q0 + q4;
       const float dt = job_delta(a, slot);
+      const bool routed = job_routed(a, slot);
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
           ub |= kb << (8 * e);
           u = (float)kb * (1.f / 128.f);
         }
-        o[e] = f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt));
+        o[e] = routed ? f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt)) : (bf16_t)0;
       }
       if constexpr (LAYOUT != MASK_CONST && LAYOUT != MASK_SRC) *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + idx) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
@@ -371,7 +376,8 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
 
 // Backward mask: d_h = bf16(d_acts * (m - delta)) (in place over d_acts) and the
 // CI pullback d_pre[sort_idx[j]*c + q] = lower_vjp(pre, d_acts*h*(1-u)) +
-// upper_vjp(pre, imp_scale * d upper^p), written token-major.
+// upper_vjp(pre, imp_scale * d upper^p), written token-major; d_acts counts as 0 on an
+// unrouted token's jobs.
 // SRC: the sources are tables (MASK_SRC): u is read back from the table, and the tables'
 // gradient dm (1 - lower) (dm = d_acts h) and each job's row sums of dm are written.
 template <int PM, bool SRC>
@@ -402,7 +408,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       const float dt = job_delta(a, slot);
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
-      const uint2 dw = *(const uint2*)(d_acts + idx);
+      const uint2 dw = job_routed(a, slot) ? *(const uint2*)(d_acts + idx) : make_uint2(0u, 0u);
       const uint32_t ub = !SRC && a.uconst < 0.f ? *(const uint32_t*)(ubits + idx) : 0u;
       const int ej = SRC ? row_group(a.offsets, a.E, j) : 0;
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
@@ -985,6 +991,15 @@ static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
 }
 
 // delta[0, n) = v (the constant sources' delta mask).
+// blend[i] = route[i] ? delta[i] : 1 (delta NULL: 0), over every (layer, site, token): the
+// frozen output's share of a job's site output, where(route, decomposed + d frozen, frozen).
+__global__ __launch_bounds__(256) void k_route_blend(const float* __restrict__ delta,
+                                                     const uint8_t* __restrict__ route, int64_t n,
+                                                     float* __restrict__ blend) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    blend[i] = route[i] ? (delta ? delta[i] : 0.f) : 1.f;
+}
+
 __global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ out, int64_t n, float v) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = v;
 }
@@ -1028,7 +1043,7 @@ struct MoEPlan {
   bf16_t *rc_a, *rc_b, *r_final, *h2c, *xjc, *gc, *uc, *din, *downc, *down, *dr_a, *dr_b;
   float *colsrc, *rowdm, *qjob;  // persistent sources: group column sums, job row sums, job delta cotangents
   int32_t* goff;
-  float *logits, *logitsc, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta;
+  float *logits, *logitsc, *probsc, *wc, *rec_part, *imp_part, *d_w_part, *delta, *blend;
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq, *sl0_fb;  // smooth-L0: per site-layer regions
   size_t sl0_col_per_site, sl0_slope_per_site, sl0_blocks_per_site;
   int32_t* sort_ws;
@@ -1109,6 +1124,7 @@ static MoEPlan plan(const MoEDims& D, char* base, bool dry) {
   P.goff = A.take<int32_t>(D.S ? (size_t)D.E * D.S + 1 : 1);
   P.d_w_part = A.take<float>(J * cdiv(D.f, TILE));
   P.delta = A.take<float>((size_t)T * 3 * L);
+  P.blend = A.take<float>((size_t)T * 3 * L);
   P.sort_ws = A.take<int32_t>(pd_routed_jobs_workspace_size(J, D.E) / 4 + 1);
   P.d_dout = A.take<bf16_t>(J * D.d);
   for (int i = 0; i < 3; ++i) P.d_acts[i] = A.take<bf16_t>(J * D.c);
@@ -1191,7 +1207,8 @@ struct SrcArgs {
 static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                          const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                          const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
+                         const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
+                         const uint8_t* routes, float source_value,
                          int layout, const ImpSpec& imp, float recon_coeff, float* losses, float* dVg, float* dUg,
                          float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
                          void* workspace, size_t workspace_bytes, void* stream, Recorder& rec,
@@ -1220,7 +1237,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       if (dt != PD_DTYPE_F32 && dt != PD_DTYPE_BF16 && dt != PD_DTYPE_U16)
         return fail(PD_EINVAL, "pd_moe_stack_step_sources: source dtype");
     use_delta = srcs->delta ? 1 : 0;
+    if (routes) return fail(PD_EINVAL, "pd_moe_stack_step_sources: no per-token routes with source tables");
   }
+  // the frozen channel (x_jobs @ W[e] beside every site) runs with the delta draws, and
+  // with routes, whose unrouted tokens take the frozen output alone
+  const bool use_frozen = use_delta || routes;
   const bool want_wgrads = !srcs || srcs->want_wgrads;
   const MoEDims D{T, T * k, d, f, E, k, c, L, srcs ? T / srcs->rps : 0};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
@@ -1240,6 +1261,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   split2(draw_k0, draw_k1, layout, halves);
   const uint32_t sb0 = halves[0], sb1 = halves[1];
   const float* dlt[3] = {nullptr, nullptr, nullptr};  // the current layer's per-token delta draws
+  const float* bl[3] = {nullptr, nullptr, nullptr};   // ... the frozen outputs' shares (d, or route ? d : 1)
+  const uint8_t* rt[3] = {nullptr, nullptr, nullptr}; // ... per-token routes
   auto site_key = [&](int kind, int layer, uint32_t& o0, uint32_t& o1) {
     uint32_t x0_ = 0, x1_ = (uint32_t)kind;
     threefry2x32(sb0, sb1, x0_, x1_);
@@ -1339,8 +1362,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   else if (use_delta)
     hipLaunchKernelGGL(k_delta_sites, dim3((unsigned)cdiv(T, 256), (unsigned)(3 * L)), dim3(256), 0, s, halves[2],
                        halves[3], T, layout, P.delta);
+  if (routes)
+    hipLaunchKernelGGL(k_route_blend, dim3((unsigned)std::min<int64_t>(cdiv(3 * L * T, 256), 4096)), dim3(256), 0, s,
+                       use_delta ? (const float*)P.delta : nullptr, routes, (int64_t)3 * L * T, P.blend);
   auto set_delta = [&](int l) {
-    for (int si = 0; si < 3; ++si) dlt[si] = use_delta ? P.delta + ((size_t)l * 3 + si) * T : nullptr;
+    for (int si = 0; si < 3; ++si) {
+      const size_t o = ((size_t)l * 3 + si) * T;
+      dlt[si] = use_delta ? P.delta + o : nullptr;
+      bl[si] = routes ? P.blend + o : dlt[si];
+      rt[si] = routes ? routes + o : nullptr;
+    }
   };
 
   // ================= clean forward (frozen weights): pins the expert indices. Layer 0 sees
@@ -1435,6 +1466,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.layout = layout;
       ma.p = imp.p;
       ma.delta = dlt[si];
+      ma.route = rt[si];
       ma.k = k;
       ma.uconst = uconst;
       sl0_fill(ma, S, l, si);
@@ -1458,7 +1490,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     // frozen channel of gate and up: x_jobs @ W[e] (layer 0: the clean pass's products)
     const bf16_t* fg = nullptr;
     const bf16_t* fu = nullptr;
-    if (use_delta) {
+    if (use_frozen) {
       fg = S.fg;
       fu = S.fu;
       if (l > 0 &&
@@ -1476,11 +1508,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     // ---- down site
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J, f,
-                       fg, fu, dlt[0], dlt[1], k, S.din);
+                       fg, fu, bl[0], bl[1], k, S.din);
     rec.mark(MOE_CAT_GEMM_FWD);
     if ((rc = grouped_gemm(S.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
       return rc;
-    if (use_delta &&
+    if (use_frozen &&
         (rc = grouped_gemm(S.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, S.fd, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_MASK_FWD);
@@ -1492,7 +1524,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, P.down, S.inv,
-                       (const float*)nullptr, T, k, d, use_delta ? S.fd : (const bf16_t*)nullptr, dlt[2], r_out);
+                       (const float*)nullptr, T, k, d, use_frozen ? S.fd : (const bf16_t*)nullptr, bl[2], r_out);
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
@@ -1594,6 +1626,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
     site_key(kinds[2], l, ma.k0, ma.k1);
     ma.delta = dlt[2];
+    ma.route = rt[2];
     sl0_fill(ma, S, l, 2);
     src_fill(ma, l, 2);
     src_zero(2);
@@ -1611,14 +1644,14 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                            false)))
       return rc;
     // frozen channel of down: d_out @ W_down[e]^T, scaled by the token's delta in the fold
-    if (use_delta &&
+    if (use_frozen &&
         (rc = grouped_gemm(P.d_dout, bf(Wd, l * szW), S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_WAIT);
     wjoin(2);  // dU of gate / up reads d_g, d_u
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
-                       J, f, use_delta ? P.gc : (const bf16_t*)nullptr, dlt[2], k, P.d_g, P.d_u, P.d_w_part);
+                       J, f, use_frozen ? P.gc : (const bf16_t*)nullptr, bl[2], k, P.d_g, P.d_u, P.d_w_part);
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_WAIT);
     wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
@@ -1637,6 +1670,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
       site_key(kinds[si], l, ma.k0, ma.k1);
       ma.delta = dlt[si];
+      ma.route = rt[si];
       sl0_fill(ma, S, l, si);
       src_fill(ma, l, si);
       src_zero(si);
@@ -1658,14 +1692,14 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                                   S.offsets, J, E, c, d, PD_DTYPE_BF16, stream)))
         return rc;
       // frozen channel of gate and up: d_g @ Wg[e]^T, d_u @ Wu[e]^T
-      if (use_delta && (rc = grouped_gemm_pair(P.d_g, bf(Wg, l * szW), P.downc, P.d_u, bf(Wu, l * szW), P.down,
+      if (use_frozen && (rc = grouped_gemm_pair(P.d_g, bf(Wg, l * szW), P.downc, P.d_u, bf(Wu, l * szW), P.down,
                                                S.offsets, J, E, f, d, PD_DTYPE_BF16, stream)))
         return rc;
       // ---- routing weights, router, gather VJP and the norm
       rec.mark(MOE_CAT_TOKEN_BWD);
       launch_token_bwd(P.d_w_part, n_wpart, S.inv, S.idx, S.probs, S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb,
-                       S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, use_delta ? P.downc : (const bf16_t*)nullptr,
-                       P.down, dlt[0], dlt[1], dr_next, s);
+                       S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, use_frozen ? P.downc : (const bf16_t*)nullptr,
+                       P.down, bl[0], bl[1], dr_next, s);
       std::swap(dr, dr_next);
     }
     if ((rc = check_launch("pd_moe_stack_step bwd"))) return rc;
@@ -1679,20 +1713,20 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
 int pd_moe_stack_step(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                       const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                       const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud, const void* ci_pre,
-                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value, int layout, int imp_kind,
-                      float p, float gamma, int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
-                      const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
-                      float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu, float* dVd,
-                      float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+                      uint32_t draw_k0, uint32_t draw_k1, int use_delta, const uint8_t* routes, float source_value,
+                      int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
+                      float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
+                      float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg, float* dUg,
+                      float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
   ImpSpec imp;
-  if (int e = make_imp_spec("pd_moe_stack_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
-                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+  if (int e = make_imp_spec("pd_moe_stack_step", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
     return e;
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                       draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd, dUd,
-                       d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
+                       draw_k1, use_delta, routes, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu,
+                       dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
 }
 
 int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
@@ -1708,8 +1742,8 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
                               size_t workspace_bytes, void* stream) {
   Recorder rec{nullptr, nullptr, 0, 0, nullptr};
   ImpSpec imp;
-  if (int e = make_imp_spec("pd_moe_stack_step_sources", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
-                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+  if (int e = make_imp_spec("pd_moe_stack_step_sources", imp_kind, p, gamma, normalize_at_one, imp_coeff,
+                            freq_coeff, ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
     return e;
   const SrcArgs sa{src, src_dtype, src_delta, delta_dtype, rows_per_source, want_weight_grads, d_src, d_src_delta};
   if (rows_per_source <= 0 || T % rows_per_source)
@@ -1718,31 +1752,32 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
     return fail(PD_EWORKSPACE, "pd_moe_stack_step_sources: workspace too small");
   return moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, 0, 0,
-                       src_delta != nullptr, -1.f, PD_LAYOUT_PARTITIONABLE, imp, recon_coeff, losses, dVg, dUg, dVu,
-                       dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec, &sa,
+                       src_delta != nullptr, nullptr, -1.f, PD_LAYOUT_PARTITIONABLE, imp, recon_coeff, losses, dVg,
+                       dUg, dVu, dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec, &sa,
                        reuse_clean != 0);
 }
 
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,
-                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta, float source_value,
-                            int layout, int imp_kind, float p, float gamma, int normalize_at_one, float imp_coeff,
-                            float freq_coeff, float ref_count, const float* freq_ema_in, float* freq_ema_out,
-                            float ema_count, float ema_halflife, float recon_coeff, float* losses, float* dVg,
-                            float* dUg, float* dVu, float* dUu, float* dVd, float* dUd, void* d_ci_pre,
-                            int32_t* top_idx_out, void* workspace, size_t workspace_bytes, void* stream,
-                            void** events, int32_t* categories, int capacity, int* n_recorded) {
+                            const void* ci_pre, uint32_t draw_k0, uint32_t draw_k1, int use_delta,
+                            const uint8_t* routes, float source_value, int layout, int imp_kind, float p, float gamma,
+                            int normalize_at_one, float imp_coeff, float freq_coeff, float ref_count,
+                            const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
+                            float recon_coeff, float* losses, float* dVg, float* dUg, float* dVu, float* dUu,
+                            float* dVd, float* dUd, void* d_ci_pre, int32_t* top_idx_out, void* workspace,
+                            size_t workspace_bytes, void* stream, void** events, int32_t* categories, int capacity,
+                            int* n_recorded) {
   if (!events || !categories || capacity <= 0 || !n_recorded)
     return fail(PD_EINVAL, "pd_moe_stack_step_timed: events/categories required");
   Recorder rec{events, categories, capacity, 0, nullptr};
   ImpSpec imp;
-  if (int e = make_imp_spec("pd_moe_stack_step_timed", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff, ref_count,
-                            freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+  if (int e = make_imp_spec("pd_moe_stack_step_timed", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
     return e;
   int rc = moe_step_impl(T, d, f, E, k, c, L, x0, ln, router, Wg, Wu, Wd, Vg, Ug, Vu, Uu, Vd, Ud, ci_pre, draw_k0,
-                         draw_k1, use_delta, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu, dUu, dVd,
-                         dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
+                         draw_k1, use_delta, routes, source_value, layout, imp, recon_coeff, losses, dVg, dUg, dVu,
+                         dUu, dVd, dUd, d_ci_pre, top_idx_out, workspace, workspace_bytes, stream, rec);
   *n_recorded = rec.n;
   if (rc == PD_OK && rec.n >= capacity) return fail(PD_EINVAL, "pd_moe_stack_step_timed: event capacity too small");
   return rc;

@@ -50,7 +50,9 @@ class LMStackStep:
     def __init__(self, B: int, T: int, d: int, n_head: int, n_kv_head: int, d_mlp: int, vocab: int, n_layers: int,
                  C: dict, *, device="cuda", p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
                  layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, n_kl_chunks: int = 1,
-                 eps: float = 1e-6, rope_base: float = 10000.0, imp_min: ImpMin | None = None):
+                 eps: float = 1e-6, rope_base: float = 10000.0, imp_min: ImpMin | None = None,
+                 routed: bool = False):
+        """routed: the step takes per-token site routes (`step(..., routes=...)`)."""
         if d != n_head * HEAD_DIM:
             raise L.PDError(f"LMStackStep: head_dim must be {HEAD_DIM} (d = {HEAD_DIM} * n_head)")
         self.dims = (B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers)
@@ -59,6 +61,7 @@ class LMStackStep:
         self.imp_min = imp_min if imp_min is not None else ImpMin("pnorm", p=p, coeff=imp_coeff)
         self.recon_coeff, self.layout = recon_coeff, layout
         self.use_delta, self.n_kl_chunks, self.eps, self.rope_base = bool(use_delta), n_kl_chunks, eps, rope_base
+        self.routed = bool(routed)
         dev = torch.device(device)
         N = B * T
         f32 = dict(dtype=torch.float32, device=dev)
@@ -74,7 +77,7 @@ class LMStackStep:
             self.d_ci_pre[k] = torch.empty(n_layers, N, self.C[k], dtype=torch.bfloat16, device=dev)
         self._cs = L.host_array(ctypes.c_int32, [self.C[k] for k in KINDS])
         nbytes = L.load().pd_lm_stack_workspace_size(B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers, self._cs,
-                                                     int(self.use_delta), n_kl_chunks)
+                                                     int(self.use_delta or self.routed), n_kl_chunks)
         if nbytes == 0:
             raise L.PDError("pd_lm_stack_workspace_size: bad dimensions")
         self.workspace = L.workspace(nbytes, dev)
@@ -83,7 +86,7 @@ class LMStackStep:
         self._dU = L.host_array(P, [L.ptr(self.dU[k]) for k in KINDS])
         self._dci = L.host_array(P, [L.ptr(self.d_ci_pre[k]) for k in KINDS])
 
-    def _args(self, tokens, w: LMWeights, ci_pre: dict, draw_key: Key):
+    def _args(self, tokens, w: LMWeights, ci_pre: dict, draw_key: Key, routes=None):
         B, T, d, H, KV, f, V, Ln = self.dims
         P = ctypes.c_void_p
         for k in KINDS:
@@ -93,13 +96,25 @@ class LMStackStep:
                       L.host_array(P, [L.ptr(w.U[k]) for k in KINDS]),
                       L.host_array(P, [L.ptr(ci_pre[k]) for k in KINDS]))
         Wa, Va, Ua, Ca = self._keep
+        rt = None
+        if routes is not None:
+            if not self.routed:
+                raise L.PDError("LMStackStep: construct with routed=True to pass routes")
+            if isinstance(routes, dict):  # kind -> [L, N]
+                routes = torch.stack([routes[k] for k in KINDS], 1)
+            if tuple(routes.shape) != (Ln, len(KINDS), B * T):
+                raise L.PDError("LMStackStep: routes are [L, 6, N]")
+            rt = routes.to(torch.uint8).contiguous()
+            self._keep = self._keep + (rt,)
         return [B, T, d, H, KV, f, V, Ln, self._cs, L.ptr(tokens), L.ptr(w.wte), L.ptr(w.ln1), L.ptr(w.ln2),
                 L.ptr(w.norm), self.eps, self.rope_base, Wa, Va, Ua, Ca, draw_key[0], draw_key[1], int(self.use_delta),
-                self.layout, *self.imp_min.c_args(self.frequency), self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
+                L.ptr(rt), self.layout, *self.imp_min.c_args(self.frequency), self.recon_coeff, self.n_kl_chunks, L.ptr(self.losses), self._dV,
                 self._dU, self._dci, L.ptr(self.workspace), self.workspace.numel(), L.stream()]
 
-    def step(self, tokens: torch.Tensor, w: LMWeights, ci_pre: dict, draw_key: Key):
-        L.call("pd_lm_stack_step", *self._args(tokens, w, ci_pre, draw_key))
+    def step(self, tokens: torch.Tensor, w: LMWeights, ci_pre: dict, draw_key: Key, routes=None):
+        """routes: per-token site routes, uint8/bool [L, 6, N] or kind -> [L, N] (None:
+        every token routed); an unrouted token's site output is the target's."""
+        L.call("pd_lm_stack_step", *self._args(tokens, w, ci_pre, draw_key, routes))
         self._advance()
         return self
 

@@ -87,11 +87,19 @@ class MoEStackStep:
             self.d_src_delta = torch.empty(Ln, 3, S, **f32)
         self.workspace = L.workspace(nbytes, dev)
 
-    def _args(self, x0, w: MoEWeights, ci_pre, draw_key: Key):
+    def _args(self, x0, w: MoEWeights, ci_pre, draw_key: Key, routes=None):
         T, d, f, E, k, c, Ln = self.dims
+        rt = None
+        if routes is not None:
+            if isinstance(routes, dict):  # site -> [L, T]
+                routes = torch.stack([routes[s] for s in SITE_NAMES], 1)
+            if tuple(routes.shape) != (Ln, 3, T):
+                raise L.PDError("MoEStackStep: routes are [L, 3, T]")
+            rt = routes.to(torch.uint8).contiguous()
+            self._routes = rt  # kept alive until the next call
         return [T, d, f, E, k, c, Ln, L.ptr(x0), L.ptr(w.ln), L.ptr(w.router), L.ptr(w.Wg), L.ptr(w.Wu), L.ptr(w.Wd),
                 L.ptr(w.Vg), L.ptr(w.Ug), L.ptr(w.Vu), L.ptr(w.Uu), L.ptr(w.Vd), L.ptr(w.Ud), L.ptr(ci_pre),
-                draw_key[0], draw_key[1], int(self.use_delta), self.source_value, self.layout,
+                draw_key[0], draw_key[1], int(self.use_delta), L.ptr(rt), self.source_value, self.layout,
                 *self.imp_min.c_args(self.frequency), self.recon_coeff, L.ptr(self.losses),
                 L.ptr(self.dV["gate"]), L.ptr(self.dU["gate"]), L.ptr(self.dV["up"]), L.ptr(self.dU["up"]),
                 L.ptr(self.dV["down"]), L.ptr(self.dU["down"]), L.ptr(self.d_ci_pre), L.ptr(self.top_idx),
@@ -133,8 +141,10 @@ class MoEStackStep:
         if self.frequency is not None:
             self.frequency.count += 1
 
-    def step(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, draw_key: Key):
-        L.call("pd_moe_stack_step", *self._args(x0, w, ci_pre, draw_key))
+    def step(self, x0: torch.Tensor, w: MoEWeights, ci_pre: torch.Tensor, draw_key: Key, routes=None):
+        """routes: per-token site routes, uint8/bool [L, 3, T] or site -> [L, T] (None:
+        every token routed); an unrouted token's jobs take the frozen output."""
+        L.call("pd_moe_stack_step", *self._args(x0, w, ci_pre, draw_key, routes))
         self._advance()
         return self
 

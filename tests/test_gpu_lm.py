@@ -103,6 +103,61 @@ def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T,
           f"{max(x[2] for x in stats):.3e}")
 
 
+@pytest.mark.parametrize("use_delta", [True, False])
+def test_lm_stack_step_with_routes_matches_oracle(device, use_delta):
+    """Per-token site routes from the uniform-k-subset sampler (pd/core/recon.py:218-231)
+    over the step's 12 sites (site = layer * 6 + kind): unrouted tokens take the target's
+    x @ W^T at that site (pd/core/decomposed_linear.py:72-85), so their masks get no recon
+    gradient; without the delta channel the target segment still carries them. Against
+    the LM oracle's route arm (pinned by the reference's stacked-parity masked_subset
+    golden, tests/test_lm_oracle.py)."""
+    from param_decomp_amd import ops
+    from param_decomp_amd.lm_step import LMStackStep
+
+    B, T = 2, 128
+    cfg = lo.LMConfig(n_layers=2, d=128, n_head=2, n_kv_head=1, d_mlp=256, vocab=384,
+                      C={"q_proj": 64, "k_proj": 48, "v_proj": 64, "o_proj": 32, "c_fc": 128, "down_proj": 96})
+    params, tokens, ci, w, ci_t, tok_t = _setup(cfg, B, T, 8, device)
+    key = (6, 29)
+    n_sites = cfg.n_layers * len(KINDS)
+    routes = ops.route_uniform_k((11, 12), n_sites, B * T, device)  # [n_sites, N] uint8
+    rt = routes.reshape(cfg.n_layers, len(KINDS), B * T)
+    frac = float(rt.float().mean())
+    assert 0.2 < frac < 0.9, frac  # both arms taken
+    spec = po.ImpMin("pnorm", p=2.0, coeff=0.05)
+    step = LMStackStep(B, T, cfg.d, cfg.n_head, cfg.n_kv_head, cfg.d_mlp, cfg.vocab, cfg.n_layers, cfg.C,
+                       device=device, use_delta=use_delta, n_kl_chunks=3, recon_coeff=3.0, imp_coeff=0.05,
+                       routed=True)
+    step.step(tok_t, w, ci_t, key, routes=rt)
+    torch.cuda.synchronize()
+    rnp = rt.cpu().numpy().astype(bool)
+    ref = lo.lm_stack_step(cfg, params, tokens, ci, key, bf16_storage=True, use_delta=use_delta, recon_coeff=3.0,
+                           imp_min=spec,
+                           routes=[{k: rnp[l, i] for i, k in enumerate(KINDS)} for l in range(cfg.n_layers)])
+    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"], ref["freq"]],
+                               rtol=2e-2, atol=1e-7)
+    stats = []
+    for l in range(cfg.n_layers):
+        for k in KINDS:
+            _close(step.dV[k][l].cpu().numpy(), ref["dV"][l][k], f"dV[{l}][{k}]", stats)
+            _close(step.dU[k][l].cpu().numpy(), ref["dU"][l][k], f"dU[{l}][{k}]", stats)
+            _close(step.d_ci_pre[k][l].float().cpu().numpy(), ref["d_ci_pre"][l][k], f"d_ci_pre[{l}][{k}]", stats)
+    # an unrouted token's CI gradient is the imp-min pullback alone
+    l, k = 1, "c_fc"
+    un = ~rnp[l, KINDS.index(k)]
+    _, _, dup = po.impmin_site_terms(po.upper_leaky(ci[l][k]), spec, B * T)
+    want = po.upper_leaky_vjp(ci[l][k], dup)
+    got = step.d_ci_pre[k][l].float().cpu().numpy()
+    np.testing.assert_allclose(got[un], want[un], rtol=1e-2, atol=1e-6 * np.abs(want).max())
+    # the routes change the result
+    plain = LMStackStep(B, T, cfg.d, cfg.n_head, cfg.n_kv_head, cfg.d_mlp, cfg.vocab, cfg.n_layers, cfg.C,
+                        device=device, use_delta=use_delta, n_kl_chunks=3, recon_coeff=3.0, imp_coeff=0.05)
+    plain.step(tok_t, w, ci_t, key)
+    assert abs(float(plain.losses[1]) - float(step.losses[1])) > 1e-3 * float(plain.losses[1])
+    worst = max(stats, key=lambda x: x[1])
+    print(f"worst element/scale {worst[1]:.3e} ({worst[0]})")
+
+
 def test_lm_stack_step_full_size_properties(device):
     """The Llama-4L shape (d_model 768, 12 heads, d_mlp 3072, vocab 50277, C = 1024
     attention / 4096 MLP, 16 x 512 tokens): finite, positive losses and gradients,

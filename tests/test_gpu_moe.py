@@ -96,6 +96,51 @@ def test_moe_stack_step_matches_oracle(device, cfg, partitionable, use_delta, so
             _close(got[si], ref["d_ci_pre"][l][s], 2e-2, 1e-2, f"d_ci_pre[{l}][{s}]")
 
 
+@pytest.mark.parametrize("use_delta", [True, False])
+def test_moe_stack_step_with_routes_matches_oracle(device, use_delta):
+    """Per-token site routes from the uniform-k-subset sampler (pd/core/recon.py:218-231)
+    over the stack's 3L sites (site = layer * 3 + kind): an unrouted token's jobs take the
+    frozen output at that site (pd/targets/qwen36_moe.py:2822-2827), also without the
+    delta draws (the frozen channel then runs for the routes alone)."""
+    from param_decomp_amd import ops
+    from param_decomp_amd.moe_step import MoEStackStep
+
+    cfg = mo.MoEConfig(T=200, d=48, f=40, E=13, k=4, c=24, L=3)
+    params, x0, ci, w, ci_t, x0_t = _make(cfg, 2, device)
+    key = (0, 31)
+    rt = ops.route_uniform_k((5, 6), 3 * cfg.L, cfg.T, device).reshape(cfg.L, 3, cfg.T)
+    assert 0.2 < float(rt.float().mean()) < 0.9
+    step = MoEStackStep(cfg.T, cfg.d, cfg.f, cfg.E, cfg.k, cfg.c, cfg.L, device=device, recon_coeff=1.5, p=2.0,
+                        imp_coeff=0.5, use_delta=use_delta)
+    step.step(x0_t, w, ci_t, key, routes=rt)
+    torch.cuda.synchronize()
+    got_idx = step.top_idx.cpu().numpy()
+    rnp = rt.cpu().numpy().astype(bool)
+    ref = mo.moe_stack_step(cfg, params, x0, ci, key, p=2.0, imp_coeff=0.5, recon_coeff=1.5, bf16_storage=True,
+                            use_delta=use_delta, pinned_top_idx=got_idx,
+                            routes=[{s: rnp[l, i] for i, s in enumerate(mo.SITES)} for l in range(cfg.L)])
+    for l in range(cfg.L):
+        assert_routing_matches(got_idx[l], ref, l, cfg.k)
+    np.testing.assert_allclose(step.losses.cpu().numpy(), [ref["loss"], ref["recon"], ref["imp"], ref["freq"]],
+                               rtol=2e-2, atol=1e-7)
+    for l in range(cfg.L):
+        for s, vn, un in (("gate", "Vg", "Ug"), ("up", "Vu", "Uu"), ("down", "Vd", "Ud")):
+            _close(step.dV[s][l].cpu().numpy(), ref["grads"][l][vn], 2e-2, 1e-2, f"{vn}[{l}]")
+            _close(step.dU[s][l].cpu().numpy(), ref["grads"][l][un], 2e-2, 1e-2, f"{un}[{l}]")
+        got = step.d_ci_pre[l].float().cpu().numpy()
+        for si, s in enumerate(mo.SITES):
+            _close(got[si], ref["d_ci_pre"][l][s], 2e-2, 1e-2, f"d_ci_pre[{l}][{s}]")
+    # every route on is the unrouted step, bit for bit
+    ones = torch.ones_like(rt)
+    step.step(x0_t, w, ci_t, key, routes=ones)
+    l1, d1 = step.losses.clone(), step.dV["down"].clone()
+    step.step(x0_t, w, ci_t, key)
+    if use_delta:  # without the delta draws the routed call also runs the frozen channel (d = 0 blend)
+        assert torch.equal(step.losses, l1) and torch.equal(step.dV["down"], d1)
+    else:
+        torch.testing.assert_close(step.losses, l1, rtol=1e-6, atol=0.0)
+
+
 def test_moe_stack_step_full_size_properties(device):
     """The Qwen3.5-MoE-shaped stack (T=8192, width 512, 42 experts top-8, SwiGLU
     512->256->512, c=512 per expert, 4 layers): finite losses, deterministic run to

@@ -248,3 +248,72 @@ def test_smooth_l0_ema_step_reads_the_debiased_estimate():
     assert first["freq"] == pytest.approx(batch["freq"], rel=1e-12)
     for l, k in sites:
         np.testing.assert_allclose(first["d_ci_pre"][l][k], batch["d_ci_pre"][l][k], rtol=1e-10, atol=1e-15)
+
+
+def _stacked_model():
+    """The reference's stacked-parity target (`pd/tests/targets/stacked_parity/
+    stacked_fixtures.npz`, made by `gen_stacked_fixtures.py:95-150`): a residual-fed tiny
+    GLU Llama (`tiny_glu_cfg`, `pd/targets/testing.py:107-122`: d 32, 4 heads over 2 kv
+    heads, d_mlp 64, vocab 64, RoPE theta 5e5 with Llama-3 scaling (8, 1, 4, 128), eps
+    1e-5) from layer 3 to 7, the MLP sites of layers 3-5 decomposed with C = 8."""
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "stacked_forward.npz")
+    f = dict(np.load(path))
+    first, last = int(f["_scalar_FIRST_LAYER"]), int(f["_scalar_LAST_LAYER"])
+    cfg = lo.LMConfig(n_layers=8 - first, d=32, n_head=4, n_kv_head=2, d_mlp=64, vocab=64, mlp="glu", eps=1e-5,
+                      rope_base=500000.0, rope_scaling=(8.0, 1.0, 4.0, 128.0),
+                      C={k: int(f["_scalar_C"]) for k in ("gate_proj", "up_proj", "down_proj")})
+    T = lambda a: torch.tensor(np.asarray(a, np.float64))  # noqa: E731
+    names = {"q_proj": "wq", "k_proj": "wk", "v_proj": "wv", "o_proj": "wo", "gate_proj": "Wg", "up_proj": "Wu",
+             "down_proj": "Wd"}
+    layers, sites = [], []
+    for i in range(first, 8):
+        P = {"ln1": T(f[f"tgt::layers.{i}.ln1"]), "ln2": T(f[f"tgt::layers.{i}.ln2"])}
+        for kind, nm in names.items():
+            P["W_" + kind] = T(f[f"tgt::layers.{i}.{nm}"])
+        if i <= last:
+            for kind in ("gate_proj", "up_proj", "down_proj"):
+                name = f"layers.{i}.mlp.{kind}"
+                P["V_" + kind], P["U_" + kind] = T(f["vu::V::" + name]), T(f["vu::U::" + name])
+                sites.append((i - first, kind, name))
+        layers.append(P)
+    params = {"layers": layers, "norm": T(f["tgt::norm"]), "head": T(f["tgt::lm_head"])}
+    return f, cfg, params, sites
+
+
+def test_stacked_reference_forward_golden():
+    """The reference's frozen forward pins of that model in fp32 (its own test's bar: rtol
+    1e-4, atol 1e-5): the clean logits, the masked logits with every decomposed site live
+    (fixed masks and weight-delta masks), and the route arm, where only layer 3's sites
+    are live, each with per-token routes (`pd/core/decomposed_linear.py:72-85`: unrouted
+    positions take the target's x @ W^T) and the other sites run the target."""
+    f, cfg, params, sites = _stacked_model()
+    resid = torch.tensor(np.asarray(f["resid"], np.float64))
+    n = cfg.n_layers
+
+    def run(live, routes=None):
+        masks = [dict() for _ in range(n)]
+        deltas = [dict() for _ in range(n)]
+        rts = [dict() for _ in range(n)]
+        for l, kind, name in sites:
+            if name in live:
+                masks[l][kind] = torch.tensor(np.asarray(f["mask::" + name], np.float64))
+                deltas[l][kind] = torch.tensor(np.asarray(f["delta_mask::" + name], np.float64))
+                if routes is not None:
+                    rts[l][kind] = routes[name]
+        act = lo.forward(cfg, params, resid, masks, deltas, routes=rts)
+        return lo.logits(params, act).numpy()
+
+    clean = lo.logits(params, lo.forward(cfg, params, resid)).numpy()
+    np.testing.assert_allclose(clean, f["out::clean"], rtol=1e-4, atol=1e-5)
+    all_live = run({name for _, _, name in sites})
+    np.testing.assert_allclose(all_live, f["out::masked_all"], rtol=1e-4, atol=1e-5)
+    chunk0 = [name for _, _, name in sites][:3]
+    routes = {name: np.asarray(f["route0::" + name]) for name in chunk0}
+    assert set(routes) == {f"layers.3.mlp.{k}" for k in ("gate_proj", "up_proj", "down_proj")}
+    assert 0 < np.mean([r.mean() for r in routes.values()]) < 1  # both arms taken
+    subset = run(set(chunk0), routes)
+    np.testing.assert_allclose(subset, f["out::masked_subset"], rtol=1e-4, atol=1e-5)
+    # the pins separate the arms: without the routes the subset output moves off its golden
+    assert np.abs(run(set(chunk0)) - f["out::masked_subset"]).max() > 1e-3

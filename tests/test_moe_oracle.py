@@ -320,6 +320,41 @@ def test_smooth_l0_ema_moe_step_matches_the_autograd_restatement():
                                        rtol=1e-12)
 
 
+@pytest.mark.parametrize("use_delta", [True, False])
+def test_routed_moe_step_matches_the_autograd_restatement(use_delta):
+    """Per-token site routes (`where(route, decomposed + d frozen, frozen)` per job,
+    pd/targets/qwen36_moe.py:2822-2827): the NumPy oracle's hand-written backward equals
+    torch autograd of the routed forward in float64; every route on reproduces the unrouted
+    step, every route off reproduces the frozen model (recon 0, CI gradient = the imp-min
+    pullback alone)."""
+    cfg = mo.MoEConfig(T=48, d=16, f=8, E=6, k=2, c=4, L=2)
+    rng = np.random.default_rng(23)
+    params, x0, _ = mo.init_moe(cfg, rng)
+    ci = [{s: rng.uniform(0.05, 0.95, size=(cfg.T, cfg.k, cfg.c)) for s in mo.SITES} for _ in range(cfg.L)]
+    routes = [{s: rng.uniform(size=cfg.T) < 0.6 for s in mo.SITES} for _ in range(cfg.L)]
+    kw = dict(p=2.0, imp_coeff=0.5, recon_coeff=1.5, use_delta=use_delta)
+    a = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), routes=routes, **kw)
+    b = mo.moe_stack_step_torch(cfg, params, x0, ci, (3, 4), routes=routes, **kw)
+    assert b["loss"] == pytest.approx(a["loss"], rel=1e-10)
+    for l in range(cfg.L):
+        for n in ("Vg", "Ug", "Vu", "Uu", "Vd", "Ud"):
+            np.testing.assert_allclose(b["grads"][l][n], a["grads"][l][n], rtol=1e-8, atol=1e-12)
+        for s in mo.SITES:
+            np.testing.assert_allclose(b["d_ci_pre"][l][s], a["d_ci_pre"][l][s], rtol=1e-8, atol=1e-12)
+    plain = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), **kw)
+    on = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), routes=[{s: np.ones(cfg.T, bool) for s in mo.SITES}
+                                                                 for _ in range(cfg.L)], **kw)
+    assert on["loss"] == pytest.approx(plain["loss"], rel=1e-12)
+    off = mo.moe_stack_step(cfg, params, x0, ci, (3, 4), routes=[{s: np.zeros(cfg.T, bool) for s in mo.SITES}
+                                                                  for _ in range(cfg.L)], **kw)
+    assert off["recon"] == pytest.approx(0.0, abs=1e-24)
+    for l in range(cfg.L):
+        for s in mo.SITES:
+            up = po.upper_leaky(ci[l][s])
+            _, _, dup = po.impmin_site_terms(up, po.ImpMin("pnorm", p=2.0, coeff=0.5), cfg.T)
+            np.testing.assert_allclose(off["d_ci_pre"][l][s], po.upper_leaky_vjp(ci[l][s], dup), rtol=1e-12)
+
+
 @pytest.mark.parametrize("rps", [48, 12, 1])
 def test_persistent_sources_match_the_autograd_restatement(rps):
     """Persistent source tables (the `c`, `bc` and `bsc` shapes: 48, 12 and 1 tokens per
