@@ -463,6 +463,57 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
   }
 }
 
+// The same backward mask for drawn or constant sources (no tables) as a streaming pass:
+// each lane takes 8 consecutive components of one job (16-byte accesses of ci, h, d_acts,
+// d_pre, 8 u bytes), the grid walks the jobs' rows in order, so every row of every operand
+// is read and written whole. c % 8 == 0; ci_pre / d_pre 16-byte aligned.
+template <int PM>
+__global__ __launch_bounds__(256) void k_mask_bwd_vec(SiteMaskArgs a, const bf16_t* __restrict__ h,
+                                                      const uint8_t* __restrict__ ubits, float imp_scale,
+                                                      bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_pre) {
+  const uint32_t cpr = (uint32_t)a.c >> 3;  // 8-component chunks per row
+  const uint32_t nch = (uint32_t)a.J * cpr;
+  for (uint32_t ch = blockIdx.x * 256u + threadIdx.x; ch < nch; ch += gridDim.x * 256u) {
+    const uint32_t j = ch / cpr;
+    const int q = (int)(ch - j * cpr) * 8;
+    const int32_t slot = a.sort_idx[j];
+    const int64_t idx = (int64_t)j * a.c + q, src = (int64_t)slot * a.c + q;
+    const float dt = job_delta(a, slot);
+    float pre[8], hv[8], da[8];
+    load8(a.ci_pre + src, pre);
+    load8(h + idx, hv);
+    if (job_routed(a, slot)) {
+      load8(d_acts + idx, da);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) da[e] = 0.f;
+    }
+    const uint2 ub = a.uconst < 0.f ? *(const uint2*)(ubits + idx) : make_uint2(0u, 0u);
+    float slope8[8];
+    if constexpr (PM == PM_SL0) {
+      load8f(a.slope + (int64_t)row_group(a.offsets, a.E, j) * a.c + q, slope8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) slope8[e] = imp_scale;
+    }
+    float dp[8], o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
+      const uint32_t w = e < 4 ? ub.x : ub.y;
+      const float u = a.uconst < 0.f ? (float)((w >> (8 * (e & 3))) & 0xFFu) * (1.f / 128.f) : a.uconst;
+      const float m = lo + (1.f - lo) * u - dt;
+      float dimp;
+      if constexpr (PM == PM_SL0) dimp = slope8[e] * sl0_dpsi(up, a.g2, a.psis);
+      else dimp = imp_scale * dpowp<PM>(up, a.p);
+      dp[e] = lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp);
+      o[e] = da[e] * m;
+    }
+    store8(d_pre + src, dp);
+    store8(d_acts + idx, o);
+  }
+}
+
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
 // din[j,:] = bf16(silu(g) * u * w[sort_idx[j]]) (fp32 math); wt NULL = the frozen arm (no
@@ -981,6 +1032,16 @@ static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
     else if (pm == 2) PD_MB(2, true);
     else if (pm == 1) PD_MB(1, true);
     else PD_MB(0, true);
+  } else if (((uintptr_t)ma.ci_pre & 15) == 0 && ((uintptr_t)d_pre & 15) == 0 && ma.J * (int64_t)ma.c < (1ll << 34)) {
+    // the streaming pass: about 8 chunks of 8 components per lane in flight over the grid
+    const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(ma.J * (int64_t)(ma.c / 8), 256), 8192);
+#define PD_MBV(PMV) \
+  hipLaunchKernelGGL((k_mask_bwd_vec<PMV>), dim3(blocks), dim3(256), 0, s, ma, h, ub, imp_scale, d_acts, d_pre)
+    if (pm == PM_SL0) PD_MBV(PM_SL0);
+    else if (pm == 2) PD_MBV(2);
+    else if (pm == 1) PD_MBV(1);
+    else PD_MBV(0);
+#undef PD_MBV
   } else {
     if (pm == PM_SL0) PD_MB(PM_SL0, false);
     else if (pm == 2) PD_MB(2, false);
