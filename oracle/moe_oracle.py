@@ -29,7 +29,10 @@ streams plus the L_p imp-min over the selected upper CI values
 (`pd/core/losses.py:357-372` selected arm).
 
 `bf16_storage=True` rounds to bf16 exactly the tensors the GPU step stores in bf16;
-everything between is float64.
+everything between is float64. Without source tables the GPU step forms each frozen
+product inside its site's second product (one accumulation, `out = rb(acts @ U + bl
+frozen)`; gate and up of layer 0 take the clean pass's stored product instead), so the
+frozen product is stored, and rounded, only on the source-table path.
 """
 
 from __future__ import annotations
@@ -129,6 +132,7 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
     cotangent sum_o g_out frozen - sum_c dm of every job, summed over each source row's
     tokens)."""
     rb = po.round_bf16 if bf16_storage else (lambda a: a)
+    fused = sources is None  # frozen products accumulate with their site's product (see above)
     spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
     T, k, c, E = cfg.T, cfg.k, cfg.c, cfg.E
     # ---------------- clean forward (frozen weights)
@@ -214,17 +218,25 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         for s in ("gate", "up"):
             S[s]["h"] = rb(po.grouped_matmul(xj, P["V" + s[0]], jobs.group_sizes))
             S[s]["acts"] = rb(S[s]["h"] * S[s]["coef"])
-            frozen = rb(po.grouped_matmul(xj, P["W" + s[0]], jobs.group_sizes))
+            raw = po.grouped_matmul(xj, P["W" + s[0]], jobs.group_sizes)
+            frozen = rb(raw)
             S[s]["frozen"] = frozen
-            S[s]["out"] = rb(rb(po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes))
-                             + S[s]["bl"] * frozen)
+            prod = po.grouped_matmul(S[s]["acts"], P["U" + s[0]], jobs.group_sizes)
+            if fused and l > 0:
+                S[s]["out"] = rb(prod + S[s]["bl"] * raw)
+            else:
+                S[s]["out"] = rb(rb(prod) + S[s]["bl"] * frozen)
         gq, uq = S["gate"]["out"], S["up"]["out"]
         din = rb(silu(gq) * uq * wj[:, None])
         S["down"]["h"] = rb(po.grouped_matmul(din, P["Vd"], jobs.group_sizes))
         S["down"]["acts"] = rb(S["down"]["h"] * S["down"]["coef"])
-        S["down"]["frozen"] = rb(po.grouped_matmul(din, P["Wd"], jobs.group_sizes))
-        dout = (rb(po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes))
-                + S["down"]["bl"] * S["down"]["frozen"])
+        raw = po.grouped_matmul(din, P["Wd"], jobs.group_sizes)
+        S["down"]["frozen"] = rb(raw)
+        prod = po.grouped_matmul(S["down"]["acts"], P["Ud"], jobs.group_sizes)
+        if fused:
+            dout = rb(prod + S["down"]["bl"] * raw)
+        else:
+            dout = rb(prod) + S["down"]["bl"] * S["down"]["frozen"]
         routed = rb(po.sum_jobs(dout, jobs))
         saved.append(dict(r=r, rinv=rinv, h2=h2, probs=probs, w=w, wj=wj, jobs=jobs, xj=xj, S=S, din=din, idx=idx))
         r = rb(r + routed)
@@ -250,7 +262,10 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
         Sd["dm"] = d_acts * Sd["h"] * Sd["rj"]
         d_h = rb(d_acts * Sd["coef"])
         grads[l]["Vd"] = po.transposed_grouped_matmul(sv["din"], d_h, sizes)
-        d_din = rb(grouped_T(d_h, P["Vd"], sizes)) + Sd["bl"] * rb(grouped_T(d_dout, P["Wd"], sizes))
+        if fused:
+            d_din = rb(grouped_T(d_h, P["Vd"], sizes) + Sd["bl"] * grouped_T(d_dout, P["Wd"], sizes))
+        else:
+            d_din = rb(grouped_T(d_h, P["Vd"], sizes)) + Sd["bl"] * rb(grouped_T(d_dout, P["Wd"], sizes))
         # SwiGLU fold
         gq, uq, wj = S["gate"]["out"], S["up"]["out"], sv["wj"]
         sg = silu(gq)
@@ -266,8 +281,11 @@ def moe_stack_step(cfg: MoEConfig, params, x0, ci_pre, draw_key, *, p=2.0, imp_c
             Ss["dm"] = d_acts * Ss["h"] * Ss["rj"]
             d_h = rb(d_acts * Ss["coef"])
             grads[l]["V" + s[0]] = po.transposed_grouped_matmul(sv["xj"], d_h, sizes)
-            d_xj = (d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
-                    + Ss["bl"] * rb(grouped_T(dgo, P["W" + s[0]], sizes)))
+            if fused:
+                d_xj = d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes) + Ss["bl"] * grouped_T(dgo, P["W" + s[0]], sizes))
+            else:
+                d_xj = (d_xj + rb(grouped_T(d_h, P["V" + s[0]], sizes))
+                        + Ss["bl"] * rb(grouped_T(dgo, P["W" + s[0]], sizes)))
         # mask pullback to the CI preactivations (token-major)
         for s in SITES:
             Ss = S[s]

@@ -40,6 +40,15 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
 // out_i = lhs_i [J,K] @ rhs_i[e] with rhs_i stored [E,N,K] (K-contiguous); no tail zeroing.
 int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,
                       const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype, void* stream);
+// Grouped two-segment products in job space, one launch for a pair (lhs1b NULL: one):
+// out[j] = rs[sort_idx[j] / k] * (lhs1[j] @ rhs1[e]) + lhs2[j] @ rhs2[e] for job j of
+// expert e, every rhs stored [E, N, K_seg] (K-contiguous), fp32 accumulation through both
+// segments and one bf16 rounding; the second problem uses lhs1b / rhs1b / lhs2b / rhs2b /
+// outb and the same row scale rs2 (NULL: rs).
+int grouped_gemm_kcat(const void* lhs1, const void* rhs1, int64_t K1, const void* lhs2, const void* rhs2, int64_t K2,
+                      void* out, const float* rs, const void* lhs1b, const void* rhs1b, const void* lhs2b,
+                      const void* rhs2b, void* outb, const float* rs2, const int32_t* sort_idx, int k,
+                      const int32_t* offsets, int64_t J, int E, int64_t N, void* stream);
 // Two ragged-contraction weight gradients in one launch: out_i[e] = lhs_i[rows_e]^T @
 // dout_i[rows_e] from the row-major job-space operands lhs_i [J,K] and dout_i [J,N].
 int grouped_gemm_dw_pair(const void* lhs1, const void* dout1, void* out1, const void* lhs2, const void* dout2,

@@ -763,6 +763,47 @@ int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const voi
       dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), 2), (hipStream_t)stream);
 }
 
+int grouped_gemm_kcat(const void* lhs1, const void* rhs1, int64_t K1, const void* lhs2, const void* rhs2, int64_t K2,
+                      void* out, const float* rs, const void* lhs1b, const void* rhs1b, const void* lhs2b,
+                      const void* rhs2b, void* outb, const float* rs2, const int32_t* sort_idx, int k,
+                      const int32_t* offsets, int64_t J, int E, int64_t N, void* stream) {
+  const bool pair = lhs1b != nullptr;
+  if (J < 0 || E <= 0 || E > 65535 || K1 <= 0 || K2 <= 0 || N <= 0 || k <= 0 || !lhs1 || !rhs1 || !lhs2 || !rhs2 ||
+      !out || !rs || !sort_idx || !offsets || (pair && (!rhs1b || !lhs2b || !rhs2b || !outb)))
+    return fail(PD_EINVAL, "grouped_gemm_kcat: bad args");
+  if (J == 0) return PD_OK;
+  const void* ops[8] = {lhs1, rhs1, lhs2, rhs2, pair ? lhs1b : lhs1, pair ? rhs1b : rhs1, pair ? lhs2b : lhs2,
+                        pair ? rhs2b : rhs2};
+  for (int i = 0; i < 8; ++i)
+    if (!bf16_operand_ok(ops[i], (i & 2) ? K2 : K1, (i & 2) ? K2 : K1))
+      return fail(PD_EUNSUPPORTED, "grouped_gemm_kcat: K1, K2 must be multiples of 8 with 16B-aligned bases");
+  if (!aligned16(out) || (pair && !aligned16(outb)) || N % 8)
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_kcat: N % 8 and 16B-aligned outputs");
+  if (!dtl_fits(J, K1, N, K1) || !dtl_fits(J, K2, N, K2))
+    return fail(PD_EUNSUPPORTED, "grouped_gemm_kcat: operands of 2 GiB or more");
+  if (cdiv(J, CfgDtlRA::BM) + E > 65535) return fail(PD_EUNSUPPORTED, "grouped_gemm_kcat: too many rows");
+  GemmArgs a{J, N, K2, (const bf16_t*)lhs2, K2, (const bf16_t*)rhs2, K2, out, N, 1.f, 0.f, offsets, E, K2 * N, 0, 0,
+             pair ? (const bf16_t*)lhs2b : nullptr, pair ? (const bf16_t*)rhs2b : nullptr, pair ? outb : nullptr};
+  KcatArgs q{(const bf16_t*)lhs1, K1, (const bf16_t*)rhs1, K1, K1, nullptr, nullptr};
+  q.A1b = pair ? (const bf16_t*)lhs1b : nullptr;
+  q.B1b = pair ? (const bf16_t*)rhs1b : nullptr;
+  q.strideB1 = K1 * N;
+  q.rs_tok = rs;
+  q.rs_tok2 = rs2 ? rs2 : rs;
+  q.sort_idx = sort_idx;
+  q.k = k;
+  if (N >= 512) {  // 256x256 tiles, as for the paired N=512 products
+    const dim3 grid((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)(cdiv(J, CfgDtlBig::BM) + E), pair ? 2u : 1u);
+    hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlBig, bf16_t, false, false, EpiStore, MODE_GROUPED>), grid,
+                       dim3(CfgDtlBig::NT), 0, (hipStream_t)stream, a, q, EpiStore::Args{});
+  } else {
+    const dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), pair ? 2u : 1u);
+    hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlRA, bf16_t, false, false, EpiStore, MODE_GROUPED>), grid,
+                       dim3(CfgDtlRA::NT), 0, (hipStream_t)stream, a, q, EpiStore::Args{});
+  }
+  return check_launch("grouped_gemm_kcat");
+}
+
 int grouped_gemm_dw_pair(const void* lhs1, const void* dout1, void* out1, const void* lhs2, const void* dout2,
                          void* out2, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N, int out_dtype,
                          void* stream) {

@@ -130,6 +130,7 @@ struct TileJob {
   void* C;
   int prob;    // 0, or 1 for the second problem of a paired launch
   int64_t lin;  // GROUPED: the tile's index within its problem, < (J / BM + E) * ceil(N / BN)
+  int e;        // GROUPED / GROUPED_K: the tile's group (expert); 0 otherwise
 };
 
 // Maps this block to its tile (the four problem mappings); false = no work.
@@ -143,6 +144,7 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
   t.kend = p.K;
   t.prob = 0;
   t.lin = 0;
+  t.e = 0;
   if (MODE == MODE_DENSE) {
     int my, nx;
     dense_tile(my, nx);
@@ -210,6 +212,7 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     t.m0 = off + (int64_t)(tile - before) * BM;
     if (t.m0 < 0) return false;
     t.B += (int64_t)e * p.strideB;
+    t.e = e;
   } else if (MODE == MODE_SPLITK) {
     // a dense tile, over the contraction slice blockIdx.z of gridDim.z equal slices of
     // p.strideA k each (a multiple of 64); slice z writes its partial sum to
@@ -250,6 +253,7 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     t.kend = p.offsets[e + 1] < p.K ? p.offsets[e + 1] : p.K;  // clamped to J
     if (t.kend < t.kbeg) t.kend = t.kbeg;
     t.C = (TC*)t.C + (int64_t)e * p.strideC;
+    t.e = e;
   }
   return t.m0 < t.M && t.n0 < p.N;
 }
@@ -857,6 +861,11 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
 // A1 and A2 are K-contiguous; B1MN / B2MN: the B operand is MN-major. The LDS stage ring
 // runs straight through the segment boundary, so the second product's first stages
 // load while the first product's last stage is consumed.
+// MODE_GROUPED (job space of routed experts): rows are jobs sorted by expert, each B is an
+// expert-major [E, N, K] stack (B1 advances by strideB1 per expert, B2 by p.strideB), an
+// optional second problem of the same shape runs in the same launch (A1b, B1b with p.A2,
+// p.B2, p.C2), and the row scale is per token, rs(row) = rs_tok[sort_idx[row] / k] (the
+// second problem's from rs_tok2).
 struct KcatArgs {
   const bf16_t* A1;
   int64_t lda1;
@@ -865,9 +874,16 @@ struct KcatArgs {
   int64_t K1;
   const bf16_t* delta;
   const uint8_t* route;
+  const bf16_t* A1b = nullptr;
+  const bf16_t* B1b = nullptr;
+  int64_t strideB1 = 0;
+  const float* rs_tok = nullptr;
+  const float* rs_tok2 = nullptr;
+  const int32_t* sort_idx = nullptr;
+  int k = 1;
 };
 
-template <class CFG, typename TC, bool B1MN, bool B2MN, class EPI = EpiStore>
+template <class CFG, typename TC, bool B1MN, bool B2MN, class EPI = EpiStore, int MODE = MODE_DENSE>
 __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs q, typename EPI::Args ea) {
   constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NS = CFG::NS, NW = CFG::NW;
   constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
@@ -877,14 +893,26 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs 
   const int wm = wave / CFG::WN, wn = wave % CFG::WN;
 
   TileJob t;
-  if (!map_tile<BM, BN, MODE_DENSE, TC>(p, lane, t)) return;
+  if (!map_tile<BM, BN, MODE, TC>(p, lane, t)) return;
   const int64_t m0 = uni64(t.m0), n0 = uni64(t.n0);
   const int64_t K1 = q.K1, K2 = p.K;
   const int64_t nk1 = (K1 + BK - 1) / BK, nk = nk1 + (K2 + BK - 1) / BK;
-  const bf16_t* a1 = (const bf16_t*)uni64((int64_t)(q.A1 + m0 * q.lda1));
-  const bf16_t* b1 = (const bf16_t*)uni64((int64_t)(B1MN ? q.B1 + n0 : q.B1 + n0 * q.ldb1));
-  const bf16_t* a2 = (const bf16_t*)uni64((int64_t)(p.A + m0 * p.lda));
-  const bf16_t* b2 = (const bf16_t*)uni64((int64_t)(B2MN ? p.B + n0 : p.B + n0 * p.ldb));
+  // the tile's segment-1 operands (its problem's, its expert's) and segment-2 operands
+  // (map_tile placed t.A / t.B / t.C); selected by assignment, since a conditional over
+  // the argument fields would take their address and move the arguments to scratch
+  const bf16_t* A1 = q.A1;
+  const bf16_t* B1 = q.B1;
+  const float* rs_tok = q.rs_tok;
+  if (t.prob) {
+    A1 = q.A1b;
+    B1 = q.B1b;
+    rs_tok = q.rs_tok2;
+  }
+  B1 += (int64_t)t.e * q.strideB1;
+  const bf16_t* a1 = (const bf16_t*)uni64((int64_t)(A1 + m0 * q.lda1));
+  const bf16_t* b1 = (const bf16_t*)uni64((int64_t)(B1MN ? B1 + n0 : B1 + n0 * q.ldb1));
+  const bf16_t* a2 = (const bf16_t*)uni64((int64_t)(t.A + m0 * p.lda));
+  const bf16_t* b2 = (const bf16_t*)uni64((int64_t)(B2MN ? t.B + n0 : t.B + n0 * p.ldb));
   const int32_t a1bytes = buf_bytes((p.M - m0) * q.lda1 * 2), a2bytes = buf_bytes((p.M - m0) * p.lda * 2);
   const int32_t b1bytes = buf_bytes(B1MN ? (K1 * q.ldb1 - n0) * 2 : (p.N - n0) * q.ldb1 * 2);
   const int32_t b2bytes = buf_bytes(B2MN ? (K2 * p.ldb - n0) * 2 : (p.N - n0) * p.ldb * 2);
@@ -905,17 +933,20 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // One issue path whose operands are selected value by value: two calls under an
+  // if / else get merged into one call over selected array addresses, which moves the
+  // offset arrays to scratch and the descriptors into vector registers.
   auto issue = [&](int64_t kt) {
     char* st = smem + (int)(kt % NS) * CFG::STAGE_BYTES;
-    if (kt < nk1) {
-      const uint32_t kpos = (uint32_t)(kt * BK);
-      dtl_issue<BM, NW>(st, a1, a1bytes, oa1, kpos * 2, wave);
-      dtl_issue<BN, NW>(st + BM * ROWB, b1, b1bytes, ob1, kpos * ks1, wave);
-    } else {
-      const uint32_t kpos = (uint32_t)((kt - nk1) * BK);
-      dtl_issue<BM, NW>(st, a2, a2bytes, oa2, kpos * 2, wave);
-      dtl_issue<BN, NW>(st + BM * ROWB, b2, b2bytes, ob2, kpos * ks2, wave);
-    }
+    const bool s1 = kt < nk1;
+    const uint32_t kpos = (uint32_t)((s1 ? kt : kt - nk1) * BK);
+    uint32_t oa[CFG::A_INSTS], ob[CFG::B_INSTS];
+#pragma unroll
+    for (int i = 0; i < CFG::A_INSTS; ++i) oa[i] = s1 ? oa1[i] : oa2[i];
+#pragma unroll
+    for (int i = 0; i < CFG::B_INSTS; ++i) ob[i] = s1 ? ob1[i] : ob2[i];
+    dtl_issue<BM, NW>(st, s1 ? a1 : a2, s1 ? a1bytes : a2bytes, oa, kpos * 2, wave);
+    dtl_issue<BN, NW>(st + BM * ROWB, s1 ? b1 : b2, s1 ? b1bytes : b2bytes, ob, kpos * (s1 ? ks1 : ks2), wave);
   };
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
@@ -944,7 +975,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs 
   for (int i = 0; i < TM; ++i) {
     const int64_t row = m0 + wm * CFG::WTM + i * 32 + (lane & 31);
     float rs = 1.f;
-    if (row < p.M && (!q.route || q.route[row])) rs = q.delta ? bf16_to_f32(q.delta[row]) : 0.f;
+    if (rs_tok) rs = row < t.M ? rs_tok[q.sort_idx[row] / q.k] : 0.f;
+    else if (row < p.M && (!q.route || q.route[row])) rs = q.delta ? bf16_to_f32(q.delta[row]) : 0.f;
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll

@@ -1303,6 +1303,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // the frozen channel (x_jobs @ W[e] beside every site) runs with the delta draws, and
   // with routes, whose unrouted tokens take the frozen output alone
   const bool use_frozen = use_delta || routes;
+  // Without source tables the frozen products join their site's second product as a first
+  // contraction segment, scaled per token (one launch, one rounding): gate / up from layer
+  // 1 on (layer 0's come from the clean pass), down, and the backward's d_input products.
+  // The source-table path keeps them apart, since its delta gradient reads them.
+  const bool kc = use_frozen && !srcs;
   const bool want_wgrads = !srcs || srcs->want_wgrads;
   const MoEDims D{T, T * k, d, f, E, k, c, L, srcs ? T / srcs->rps : 0};
   if (!workspace || workspace_bytes < plan(D, nullptr, true).total)
@@ -1554,7 +1559,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     if (use_frozen) {
       fg = S.fg;
       fu = S.fu;
-      if (l > 0 &&
+      if (l > 0 && !kc &&
           (rc = grouped_gemm_pair(S.xj, P.WgT + l * szW, S.fg, S.xj, P.WuT + l * szW, S.fu, S.offsets, J, E, d, f,
                                   PD_DTYPE_BF16, stream)))
         return rc;
@@ -1563,9 +1568,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     mask_fwd(0);
     mask_fwd(1);
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm_pair(S.acts[0], UT[0] + l * szU[0], S.gout, S.acts[1], UT[1] + l * szU[1], S.uout,
-                                S.offsets, J, E, c, f, PD_DTYPE_BF16, stream)))
+    if (kc && l > 0) {  // g = bl_g (x_jobs @ Wg[e]) + acts_g @ Ug[e], u likewise: blended here
+      if ((rc = grouped_gemm_kcat(S.xj, P.WgT + l * szW, d, S.acts[0], UT[0] + l * szU[0], c, S.gout, bl[0], S.xj,
+                                  P.WuT + l * szW, S.acts[1], UT[1] + l * szU[1], S.uout, bl[1], S.sort_idx, k,
+                                  S.offsets, J, E, f, stream)))
+        return rc;
+      fg = fu = nullptr;
+    } else if ((rc = grouped_gemm_pair(S.acts[0], UT[0] + l * szU[0], S.gout, S.acts[1], UT[1] + l * szU[1], S.uout,
+                                       S.offsets, J, E, c, f, PD_DTYPE_BF16, stream))) {
       return rc;
+    }
     // ---- down site
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, s, S.gout, S.uout, S.w, S.sort_idx, J, f,
@@ -1573,19 +1585,26 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_GEMM_FWD);
     if ((rc = grouped_gemm(S.din, VT[2] + l * szV[2], S.offsets, J, E, f, c, 1, S.h[2], PD_DTYPE_BF16, stream, false)))
       return rc;
-    if (use_frozen &&
+    if (use_frozen && !kc &&
         (rc = grouped_gemm(S.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, S.fd, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(2);
     rec.mark(MOE_CAT_GEMM_FWD);
-    if ((rc = grouped_gemm(S.acts[2], UT[2] + l * szU[2], S.offsets, J, E, c, d, 1, P.down, PD_DTYPE_BF16, stream,
-                           false)))
+    if (kc) {  // down = bl_d (din @ Wd[e]) + acts_d @ Ud[e]
+      if ((rc = grouped_gemm_kcat(S.din, P.WdT + l * szW, f, S.acts[2], UT[2] + l * szU[2], c, P.down, bl[2], nullptr,
+                                  nullptr, nullptr, nullptr, nullptr, nullptr, S.sort_idx, k, S.offsets, J, E, d,
+                                  stream)))
+        return rc;
+    } else if ((rc = grouped_gemm(S.acts[2], UT[2] + l * szU[2], S.offsets, J, E, c, d, 1, P.down, PD_DTYPE_BF16,
+                                  stream, false))) {
       return rc;
+    }
     rec.mark(MOE_CAT_COMBINE);
     bf16_t* r_out = (l + 1 < L) ? P.layers[l + 1].r : P.r_final;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, s, S.r, P.down, S.inv,
-                       (const float*)nullptr, T, k, d, use_frozen ? S.fd : (const bf16_t*)nullptr, bl[2], r_out);
+                       (const float*)nullptr, T, k, d, use_frozen && !kc ? S.fd : (const bf16_t*)nullptr, bl[2],
+                       r_out);
     r_in = r_out;
     if ((rc = check_launch("pd_moe_stack_step masked fwd"))) return rc;
   }
@@ -1701,18 +1720,25 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                         })))
       return rc;
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_acts[2], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16, stream,
-                           false)))
+    if (kc) {  // d_din = bl_d (d_out @ Wd[e]^T) + d_h @ Vd[e]^T
+      if ((rc = grouped_gemm_kcat(P.d_dout, bf(Wd, l * szW), d, P.d_acts[2], bf(Vd, l * szVd), c, P.d_din, bl[2],
+                                  nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, S.sort_idx, k, S.offsets, J, E,
+                                  f, stream)))
+        return rc;
+    } else if ((rc = grouped_gemm(P.d_acts[2], bf(Vd, l * szVd), S.offsets, J, E, c, f, 1, P.d_din, PD_DTYPE_BF16,
+                                  stream, false))) {
       return rc;
+    }
     // frozen channel of down: d_out @ W_down[e]^T, scaled by the token's delta in the fold
-    if (use_frozen &&
+    if (use_frozen && !kc &&
         (rc = grouped_gemm(P.d_dout, bf(Wd, l * szW), S.offsets, J, E, d, f, 1, P.gc, PD_DTYPE_BF16, stream, false)))
       return rc;
     rec.mark(MOE_CAT_WAIT);
     wjoin(2);  // dU of gate / up reads d_g, d_u
     rec.mark(MOE_CAT_SWIGLU);
     hipLaunchKernelGGL(k_swiglu_bwd_tile, tile_grid(J, f), dim3(256), 0, s, P.d_din, S.gout, S.uout, S.w, S.sort_idx,
-                       J, f, use_frozen ? P.gc : (const bf16_t*)nullptr, bl[2], k, P.d_g, P.d_u, P.d_w_part);
+                       J, f, use_frozen && !kc ? P.gc : (const bf16_t*)nullptr, bl[2], k, P.d_g, P.d_u,
+                       P.d_w_part);
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_WAIT);
     wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
@@ -1749,17 +1775,25 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     // gradients (its gate/up input products and the token backward feed only d x0).
     if (l > 0) {
       rec.mark(MOE_CAT_GEMM_DX);
-      if ((rc = grouped_gemm_pair(P.d_acts[0], bf(Vg, l * szVg), P.dxa, P.d_acts[1], bf(Vu, l * szVg), P.dxb,
-                                  S.offsets, J, E, c, d, PD_DTYPE_BF16, stream)))
+      if (kc) {  // dx_g = bl_g (d_g @ Wg[e]^T) + d_h_g @ Vg[e]^T, dx_u likewise
+        if ((rc = grouped_gemm_kcat(P.d_g, bf(Wg, l * szW), f, P.d_acts[0], bf(Vg, l * szVg), c, P.dxa, bl[0], P.d_u,
+                                    bf(Wu, l * szW), P.d_acts[1], bf(Vu, l * szVg), P.dxb, bl[1], S.sort_idx, k,
+                                    S.offsets, J, E, d, stream)))
+          return rc;
+      } else if ((rc = grouped_gemm_pair(P.d_acts[0], bf(Vg, l * szVg), P.dxa, P.d_acts[1], bf(Vu, l * szVg), P.dxb,
+                                         S.offsets, J, E, c, d, PD_DTYPE_BF16, stream))) {
         return rc;
+      }
       // frozen channel of gate and up: d_g @ Wg[e]^T, d_u @ Wu[e]^T
-      if (use_frozen && (rc = grouped_gemm_pair(P.d_g, bf(Wg, l * szW), P.downc, P.d_u, bf(Wu, l * szW), P.down,
-                                               S.offsets, J, E, f, d, PD_DTYPE_BF16, stream)))
+      if (use_frozen && !kc &&
+          (rc = grouped_gemm_pair(P.d_g, bf(Wg, l * szW), P.downc, P.d_u, bf(Wu, l * szW), P.down, S.offsets, J, E, f,
+                                  d, PD_DTYPE_BF16, stream)))
         return rc;
       // ---- routing weights, router, gather VJP and the norm
       rec.mark(MOE_CAT_TOKEN_BWD);
       launch_token_bwd(P.d_w_part, n_wpart, S.inv, S.idx, S.probs, S.w, bf(router, (size_t)l * E * d), P.dxa, P.dxb,
-                       S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d, use_frozen ? P.downc : (const bf16_t*)nullptr,
+                       S.r, S.rinv, ln + (size_t)l * d, dr, T, E, k, d,
+                       use_frozen && !kc ? P.downc : (const bf16_t*)nullptr,
                        P.down, bl[0], bl[1], dr_next, s);
       std::swap(dr, dr_next);
     }
