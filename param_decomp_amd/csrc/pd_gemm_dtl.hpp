@@ -595,6 +595,38 @@ struct StagedStore {
   static constexpr bool OK = PASSES > 0 && ROWS % CFG::WTM == 0;  // a wave's rows fall in one pass
 };
 
+// Pass q of the staged image: the waves whose rows fall in it write alpha * acc (bf16
+// rounded for ES == 2) into the row-major LDS image; a barrier before (the k loop's last
+// reads, or the previous pass's reads of the image, are done) and after (the image is
+// complete).
+template <class CFG, int ES>
+__device__ inline void staged_image_pass(float alpha, int q, int wm, int wn, int lane,
+                                         f32x16 (&acc)[CFG::TM][CFG::TN], char* smem) {
+  typedef StagedStore<CFG, ES> SS;
+  lds_write_barrier();
+  const int r0 = wm * CFG::WTM - q * SS::ROWS;
+  if (r0 >= 0 && r0 < SS::ROWS) {
+#pragma unroll
+    for (int i = 0; i < CFG::TM; ++i) {
+      char* rowp = smem + (r0 + i * 32 + (lane & 31)) * SS::RSB;
+#pragma unroll
+      for (int j = 0; j < CFG::TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = wn * CFG::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+          const float v0 = alpha * acc[i][j][4 * g], v1 = alpha * acc[i][j][4 * g + 1];
+          const float v2 = alpha * acc[i][j][4 * g + 2], v3 = alpha * acc[i][j][4 * g + 3];
+          if constexpr (ES == 2) {
+            *(uint2*)(rowp + c * 2) = uint2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+          } else {
+            *(float4*)(rowp + c * 4) = float4{v0, v1, v2, v3};
+          }
+        }
+    }
+  }
+  lds_write_barrier();
+}
+
 template <class CFG, typename TC>
 __device__ inline void dtl_epilogue_staged(const GemmArgs& p, const TileJob& t, int wm, int wn, int tid,
                                            f32x16 (&acc)[CFG::TM][CFG::TN], char* smem) {
@@ -609,28 +641,7 @@ __device__ inline void dtl_epilogue_staged(const GemmArgs& p, const TileJob& t, 
   const int64_t col = t.n0 + cc * EPC;
 #pragma unroll
   for (int q = 0; q < SS::PASSES; ++q) {
-    lds_write_barrier();  // the k loop's last reads (or the previous pass's stores) are done
-    const int r0 = wm * CFG::WTM - q * SS::ROWS;
-    if (r0 >= 0 && r0 < SS::ROWS) {
-#pragma unroll
-      for (int i = 0; i < CFG::TM; ++i) {
-        char* rowp = smem + (r0 + i * 32 + (lane & 31)) * SS::RSB;
-#pragma unroll
-        for (int j = 0; j < CFG::TN; ++j)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int c = wn * CFG::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
-            const float v0 = p.alpha * acc[i][j][4 * g], v1 = p.alpha * acc[i][j][4 * g + 1];
-            const float v2 = p.alpha * acc[i][j][4 * g + 2], v3 = p.alpha * acc[i][j][4 * g + 3];
-            if constexpr (ES == 2) {
-              *(uint2*)(rowp + c * 2) = uint2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-            } else {
-              *(float4*)(rowp + c * 4) = float4{v0, v1, v2, v3};
-            }
-          }
-      }
-    }
-    lds_write_barrier();
+    staged_image_pass<CFG, ES>(p.alpha, q, wm, wn, lane, acc, smem);
 #pragma unroll
     for (int r = rr; r < SS::ROWS; r += RPP) {
       const int64_t row = t.m0 + q * SS::ROWS + r;

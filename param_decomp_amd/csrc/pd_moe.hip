@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "pd_common.hpp"
+#include "pd_gemm_dtl.hpp"
 #include "pd_impmin.hpp"
 
 namespace pd {
@@ -467,6 +468,48 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
 // each lane takes 8 consecutive components of one job (16-byte accesses of ci, h, d_acts,
 // d_pre, 8 u bytes), the grid walks the jobs' rows in order, so every row of every operand
 // is read and written whole. c % 8 == 0; ci_pre / d_pre 16-byte aligned.
+// One 8-component chunk of the backward mask for drawn or constant sources: job j (of
+// token slot / k, expert e), components q .. q + 7, da the chunk of d_acts (bf16 values;
+// counted as 0 on an unrouted job). Writes d_pre (token-major) and d_h = d_acts (m - d).
+template <int PM>
+__device__ inline void mask_bwd_chunk(const SiteMaskArgs& a, const bf16_t* __restrict__ h,
+                                      const uint8_t* __restrict__ ubits, float imp_scale, int64_t j, int32_t slot,
+                                      int e_row, int q, float (&da)[8], bf16_t* __restrict__ d_h,
+                                      bf16_t* __restrict__ d_pre) {
+  const int64_t idx = j * a.c + q, src = (int64_t)slot * a.c + q;
+  const float dt = job_delta(a, slot);
+  if (!job_routed(a, slot)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) da[e] = 0.f;
+  }
+  float pre[8], hv[8];
+  load8(a.ci_pre + src, pre);
+  load8(h + idx, hv);
+  const uint2 ub = a.uconst < 0.f ? *(const uint2*)(ubits + idx) : make_uint2(0u, 0u);
+  float slope8[8];
+  if constexpr (PM == PM_SL0) {
+    load8f(a.slope + (int64_t)e_row * a.c + q, slope8);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) slope8[e] = imp_scale;
+  }
+  float dp[8], o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
+    const uint32_t w = e < 4 ? ub.x : ub.y;
+    const float u = a.uconst < 0.f ? (float)((w >> (8 * (e & 3))) & 0xFFu) * (1.f / 128.f) : a.uconst;
+    const float m = lo + (1.f - lo) * u - dt;
+    float dimp;
+    if constexpr (PM == PM_SL0) dimp = slope8[e] * sl0_dpsi(up, a.g2, a.psis);
+    else dimp = imp_scale * dpowp<PM>(up, a.p);
+    dp[e] = lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp);
+    o[e] = da[e] * m;
+  }
+  store8(d_pre + src, dp);
+  store8(d_h + idx, o);
+}
+
 template <int PM>
 __global__ __launch_bounds__(256) void k_mask_bwd_vec(SiteMaskArgs a, const bf16_t* __restrict__ h,
                                                       const uint8_t* __restrict__ ubits, float imp_scale,
@@ -477,42 +520,69 @@ __global__ __launch_bounds__(256) void k_mask_bwd_vec(SiteMaskArgs a, const bf16
     const uint32_t j = ch / cpr;
     const int q = (int)(ch - j * cpr) * 8;
     const int32_t slot = a.sort_idx[j];
-    const int64_t idx = (int64_t)j * a.c + q, src = (int64_t)slot * a.c + q;
-    const float dt = job_delta(a, slot);
-    float pre[8], hv[8], da[8];
-    load8(a.ci_pre + src, pre);
-    load8(h + idx, hv);
-    if (job_routed(a, slot)) {
-      load8(d_acts + idx, da);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) da[e] = 0.f;
-    }
-    const uint2 ub = a.uconst < 0.f ? *(const uint2*)(ubits + idx) : make_uint2(0u, 0u);
-    float slope8[8];
-    if constexpr (PM == PM_SL0) {
-      load8f(a.slope + (int64_t)row_group(a.offsets, a.E, j) * a.c + q, slope8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) slope8[e] = imp_scale;
-    }
-    float dp[8], o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-      const uint32_t w = e < 4 ? ub.x : ub.y;
-      const float u = a.uconst < 0.f ? (float)((w >> (8 * (e & 3))) & 0xFFu) * (1.f / 128.f) : a.uconst;
-      const float m = lo + (1.f - lo) * u - dt;
-      float dimp;
-      if constexpr (PM == PM_SL0) dimp = slope8[e] * sl0_dpsi(up, a.g2, a.psis);
-      else dimp = imp_scale * dpowp<PM>(up, a.p);
-      dp[e] = lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp);
-      o[e] = da[e] * m;
-    }
-    store8(d_pre + src, dp);
-    store8(d_acts + idx, o);
+    float da[8];
+    load8(d_acts + (int64_t)j * a.c + q, da);
+    mask_bwd_chunk<PM>(a, h, ubits, imp_scale, j, slot, PM == PM_SL0 ? row_group(a.offsets, a.E, j) : 0, q, da,
+                       d_acts, d_pre);
   }
 }
+
+// The backward mask as the epilogue of the grouped d_acts = d_out @ U[e]^T product (one
+// problem, or a pair of sites): the tile goes through the staged LDS image rounded to
+// bf16, exactly as the product's store would write d_acts, then every lane takes an
+// 8-component chunk of an image row through mask_bwd_chunk, writing d_h over the
+// product's output (C) and d_pre token-major. The tile's rows all belong to its expert.
+template <int PM>
+struct EpiMaskBwd {
+  static constexpr int LDS_BYTES = 0;
+  struct Args {
+    SiteMaskArgs a0, a1;  // the sites of problem 0 and (paired) problem 1
+    const bf16_t* h0;
+    const bf16_t* h1;
+    const uint8_t* ub0;
+    const uint8_t* ub1;
+    bf16_t* dp0;
+    bf16_t* dp1;
+    float imp_scale;
+  };
+  template <class CFG, typename TC>
+  __device__ static void run(const GemmArgs& p, const Args& ea, const TileJob& t, int wm, int wn, int tid,
+                             f32x16 (&acc)[CFG::TM][CFG::TN], char* smem) {
+    static_assert(sizeof(TC) == 2, "d_h is bf16");
+    typedef StagedStore<CFG, 2> SS;
+    static_assert(SS::OK, "the tile's image fits the stage ring");
+    constexpr int CPR = CFG::BN / 8, RPP = CFG::NT / CPR;
+    static_assert(CFG::NT % CPR == 0 && SS::ROWS % RPP == 0, "image passes");
+    const int lane = tid & 63, rr = tid / CPR, cc = tid % CPR;
+    // the tile's site, selected by assignment (a conditional over the argument fields
+    // would take their address)
+    SiteMaskArgs a = ea.a0;
+    const bf16_t* h = ea.h0;
+    const uint8_t* ub = ea.ub0;
+    bf16_t* dp = ea.dp0;
+    if (t.prob) {
+      a = ea.a1;
+      h = ea.h1;
+      ub = ea.ub1;
+      dp = ea.dp1;
+    }
+    const int col = (int)t.n0 + cc * 8;
+#pragma unroll
+    for (int q = 0; q < SS::PASSES; ++q) {
+      staged_image_pass<CFG, 2>(1.f, q, wm, wn, lane, acc, smem);
+#pragma unroll 2
+      for (int r = rr; r < SS::ROWS; r += RPP) {
+        const int64_t row = t.m0 + q * SS::ROWS + r;
+        if (row >= t.M || col >= p.N) continue;
+        float da[8];
+        const uint4 v = *(const uint4*)(smem + r * SS::RSB + cc * 16);
+        da[0] = bf_lo(v.x), da[1] = bf_hi(v.x), da[2] = bf_lo(v.y), da[3] = bf_hi(v.y);
+        da[4] = bf_lo(v.z), da[5] = bf_hi(v.z), da[6] = bf_lo(v.w), da[7] = bf_hi(v.w);
+        mask_bwd_chunk<PM>(a, h, ub, ea.imp_scale, row, a.sort_idx[row], t.e, col, da, (bf16_t*)t.C, dp);
+      }
+    }
+  }
+};
 
 __device__ inline float sigm(float x) { return 1.f / (1.f + __expf(-x)); }
 
@@ -1049,6 +1119,50 @@ static void launch_mask_bwd(const SiteMaskArgs& ma, int pm, dim3 grid, hipStream
     else PD_MB(0, false);
   }
 #undef PD_MB
+}
+
+// The backward mask fused into the d_acts product's epilogue applies to drawn or constant
+// sources (no tables) with K a multiple of 64 and 16-byte aligned rows.
+static bool mask_bwd_fusable(const SiteMaskArgs& ma, const bf16_t* h, const uint8_t* ub, const bf16_t* d_pre,
+                             const bf16_t* out, int64_t K) {
+  auto al = [](const void* q, uintptr_t m) { return ((uintptr_t)q & m) == 0; };
+  return !ma.src && K % 64 == 0 && ma.c % 8 == 0 && al(ma.ci_pre, 15) && al(h, 15) && al(d_pre, 15) && al(out, 15) &&
+         (ma.uconst >= 0.f || al(ub, 7)) && ma.J * (int64_t)ma.c < (1ll << 31);
+}
+
+// d_acts = lhs [J, K] @ rhs[e]^T (rhs stored [E, N, K]) per expert group with the backward
+// mask of site m0 as the epilogue (d_h over out, d_pre0 token-major); with lhs2 non-NULL
+// a second site's product in the same launch. N = c.
+static int grouped_gemm_mask_bwd(const bf16_t* lhs, const bf16_t* rhs, bf16_t* out, const SiteMaskArgs& m0,
+                                 const bf16_t* h0, const uint8_t* ub0, bf16_t* d_pre0, const bf16_t* lhs2,
+                                 const bf16_t* rhs2, bf16_t* out2, const SiteMaskArgs* m1, const bf16_t* h1,
+                                 const uint8_t* ub1, bf16_t* d_pre1, const int32_t* offsets, int64_t J, int E,
+                                 int64_t K, int64_t N, int pm, float imp_scale, hipStream_t s) {
+  const bool pair = lhs2 != nullptr;
+  if (J == 0) return PD_OK;
+  if (!dtl_fits(J, K, N, K) || cdiv(J, CfgDtlRA::BM) + E > 65535)
+    return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d_acts product too large");
+  GemmArgs a{J, N, K, lhs, K, rhs, K, out, N, 1.f, 0.f, offsets, E, K * N, 0, 0, lhs2, rhs2, out2};
+  const bool big = pair && N >= 512;  // 256x256 tiles, as for the paired N=512 products
+  const dim3 grid = big ? dim3((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)(cdiv(J, CfgDtlBig::BM) + E), 2u)
+                        : dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), pair ? 2u : 1u);
+#define PD_FM(PMV)                                                                                                    \
+  {                                                                                                                   \
+    typename EpiMaskBwd<PMV>::Args ea{m0, pair ? *m1 : m0, h0, pair ? h1 : h0, ub0, pair ? ub1 : ub0, d_pre0,         \
+                                      pair ? d_pre1 : d_pre0, imp_scale};                                             \
+    if (big)                                                                                                          \
+      hipLaunchKernelGGL((k_gemm_dtl<CfgDtlBig, bf16_t, MODE_GROUPED, false, EpiMaskBwd<PMV>>), grid,                \
+                         dim3(CfgDtlBig::NT), 0, s, a, ea);                                                           \
+    else                                                                                                              \
+      hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, bf16_t, MODE_GROUPED, false, EpiMaskBwd<PMV>>), grid,                 \
+                         dim3(CfgDtlRA::NT), 0, s, a, ea);                                                            \
+  }
+  if (pm == PM_SL0) PD_FM(PM_SL0)
+  else if (pm == 2) PD_FM(2)
+  else if (pm == 1) PD_FM(1)
+  else PD_FM(0)
+#undef PD_FM
+  return check_launch("pd_moe_stack_step d_acts + mask backward");
 }
 
 // delta[0, n) = v (the constant sources' delta mask).
@@ -1691,11 +1805,29 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
         hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)std::min<int64_t>(cdiv((int64_t)src_site, 256), 8192)),
                            dim3(256), 0, s, srcs->d_src + ((size_t)l * 3 + si) * src_site, (int64_t)src_site);
     };
-    // ---- down site
+    // ---- down site: d_acts, with the backward mask as its epilogue where it applies
+    SiteMaskArgs mg[3];
+    for (int si = 0; si < 3; ++si) {
+      mg[si] = ma;
+      mg[si].ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
+      site_key(kinds[si], l, mg[si].k0, mg[si].k1);
+      mg[si].delta = dlt[si];
+      mg[si].route = rt[si];
+      sl0_fill(mg[si], S, l, si);
+      src_fill(mg[si], l, si);
+    }
+    bf16_t* dpre[3];
+    for (int si = 0; si < 3; ++si) dpre[si] = (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI;
+    const bool fuse_d = mask_bwd_fusable(mg[2], S.h[2], S.ub[2], dpre[2], P.d_acts[2], d);
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[2], PD_DTYPE_BF16, stream,
-                           false)))
-      return rc;
+    if (fuse_d)
+      rc = grouped_gemm_mask_bwd(P.d_dout, bf(Ud, l * szUd), P.d_acts[2], mg[2], S.h[2], S.ub[2], dpre[2], nullptr,
+                                 nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, S.offsets, J, E, d, c, pm,
+                                 imp_scale, s);
+    else
+      rc = grouped_gemm(P.d_dout, bf(Ud, l * szUd), S.offsets, J, E, d, c, 1, P.d_acts[2], PD_DTYPE_BF16, stream,
+                        false);
+    if (rc) return rc;
     rec.mark(MOE_CAT_GEMM_DW);
     if (want_wgrads && (rc = wgrad(0, [&](void* st) {
                           return pd_grouped_gemm_dw(S.acts[2], P.d_dout, S.offsets, J, E, c, d, dUd + l * szUd,
@@ -1703,15 +1835,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
                         })))
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
-    ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + 2) * szCI);
-    site_key(kinds[2], l, ma.k0, ma.k1);
-    ma.delta = dlt[2];
-    ma.route = rt[2];
-    sl0_fill(ma, S, l, 2);
-    src_fill(ma, l, 2);
     src_zero(2);
-    launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[2],
-                    (bf16_t*)d_ci_pre + ((size_t)l * 3 + 2) * szCI);
+    if (!fuse_d) launch_mask_bwd(mg[2], pm, tile_grid(J, c), s, S.h[2], S.ub[2], imp_scale, P.d_acts[2], dpre[2]);
     src_grads(2, P.d_dout, S.fd, d);
     rec.mark(MOE_CAT_GEMM_DW);
     if (want_wgrads && (rc = wgrad(1, [&](void* st) {
@@ -1743,9 +1868,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_WAIT);
     wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
     rec.mark(MOE_CAT_GEMM_DX);
-    if ((rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets,
-                                J, E, f, c, PD_DTYPE_BF16, stream)))
-      return rc;
+    const bool fuse_gu = mask_bwd_fusable(mg[0], S.h[0], S.ub[0], dpre[0], P.d_acts[0], f) &&
+                         mask_bwd_fusable(mg[1], S.h[1], S.ub[1], dpre[1], P.d_acts[1], f);
+    if (fuse_gu)
+      rc = grouped_gemm_mask_bwd(P.d_g, bf(Ug, l * szUg), P.d_acts[0], mg[0], S.h[0], S.ub[0], dpre[0], P.d_u,
+                                 bf(Uu, l * szUg), P.d_acts[1], &mg[1], S.h[1], S.ub[1], dpre[1], S.offsets, J, E, f, c,
+                                 pm, imp_scale, s);
+    else
+      rc = grouped_gemm_pair(P.d_g, bf(Ug, l * szUg), P.d_acts[0], P.d_u, bf(Uu, l * szUg), P.d_acts[1], S.offsets, J,
+                             E, f, c, PD_DTYPE_BF16, stream);
+    if (rc) return rc;
     rec.mark(MOE_CAT_GEMM_DW);
     if (want_wgrads && (rc = wgrad(2, [&](void* st) {
                           return grouped_gemm_dw_pair(S.acts[0], P.d_g, dUg + l * szUg, S.acts[1], P.d_u,
@@ -1754,15 +1886,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       return rc;
     rec.mark(MOE_CAT_MASK_BWD);
     for (int si = 0; si < 2; ++si) {
-      ma.ci_pre = bf(ci_pre, ((size_t)l * 3 + si) * szCI);
-      site_key(kinds[si], l, ma.k0, ma.k1);
-      ma.delta = dlt[si];
-      ma.route = rt[si];
-      sl0_fill(ma, S, l, si);
-      src_fill(ma, l, si);
       src_zero(si);
-      launch_mask_bwd(ma, pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si],
-                      (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI);
+      if (!fuse_gu) launch_mask_bwd(mg[si], pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], dpre[si]);
       src_grads(si, si == 0 ? P.d_g : P.d_u, si == 0 ? S.fg : S.fu, f);
     }
     rec.mark(MOE_CAT_GEMM_DW);
