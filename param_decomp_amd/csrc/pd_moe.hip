@@ -471,6 +471,38 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
 // One 8-component chunk of the backward mask for drawn or constant sources: job j (of
 // token slot / k, expert e), components q .. q + 7, da the chunk of d_acts (bf16 values;
 // counted as 0 on an unrouted job). Writes d_pre (token-major) and d_h = d_acts (m - d).
+// The values of one chunk: ci preactivations pre, h, the u bytes ub, the SL0 slopes (or
+// imp_scale), the job's delta dt and d_acts da (0 on an unrouted job) -> d_pre, d_h.
+// (uconst, g2, psis, p: the site's SiteMaskArgs fields of those names.)
+template <int PM>
+__device__ inline void mask_bwd_values(float uconst, float g2, float psis, float pexp, float imp_scale,
+                                       const float (&pre)[8], const float (&hv)[8], uint2 ub,
+                                       const float (&slope8)[8], float dt, const float (&da)[8], float (&dp)[8],
+                                       float (&o)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
+    const uint32_t w = e < 4 ? ub.x : ub.y;
+    const float u = uconst < 0.f ? (float)((w >> (8 * (e & 3))) & 0xFFu) * (1.f / 128.f) : uconst;
+    const float m = lo + (1.f - lo) * u - dt;
+    float dimp;
+    if constexpr (PM == PM_SL0) dimp = slope8[e] * sl0_dpsi(up, g2, psis);
+    else dimp = imp_scale * dpowp<PM>(up, pexp);
+    dp[e] = lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp);
+    o[e] = da[e] * m;
+  }
+}
+
+template <int PM>
+__device__ inline void slope_chunk(const SiteMaskArgs& a, float imp_scale, int e_row, int q, float (&slope8)[8]) {
+  if constexpr (PM == PM_SL0) {
+    load8f(a.slope + (int64_t)e_row * a.c + q, slope8);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) slope8[e] = imp_scale;
+  }
+}
+
 template <int PM>
 __device__ inline void mask_bwd_chunk(const SiteMaskArgs& a, const bf16_t* __restrict__ h,
                                       const uint8_t* __restrict__ ubits, float imp_scale, int64_t j, int32_t slot,
@@ -487,25 +519,9 @@ __device__ inline void mask_bwd_chunk(const SiteMaskArgs& a, const bf16_t* __res
   load8(h + idx, hv);
   const uint2 ub = a.uconst < 0.f ? *(const uint2*)(ubits + idx) : make_uint2(0u, 0u);
   float slope8[8];
-  if constexpr (PM == PM_SL0) {
-    load8f(a.slope + (int64_t)e_row * a.c + q, slope8);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) slope8[e] = imp_scale;
-  }
+  slope_chunk<PM>(a, imp_scale, e_row, q, slope8);
   float dp[8], o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-    const uint32_t w = e < 4 ? ub.x : ub.y;
-    const float u = a.uconst < 0.f ? (float)((w >> (8 * (e & 3))) & 0xFFu) * (1.f / 128.f) : a.uconst;
-    const float m = lo + (1.f - lo) * u - dt;
-    float dimp;
-    if constexpr (PM == PM_SL0) dimp = slope8[e] * sl0_dpsi(up, a.g2, a.psis);
-    else dimp = imp_scale * dpowp<PM>(up, a.p);
-    dp[e] = lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp);
-    o[e] = da[e] * m;
-  }
+  mask_bwd_values<PM>(a.uconst, a.g2, a.psis, a.p, imp_scale, pre, hv, ub, slope8, dt, da, dp, o);
   store8(d_pre + src, dp);
   store8(d_h + idx, o);
 }
@@ -554,31 +570,87 @@ struct EpiMaskBwd {
     constexpr int CPR = CFG::BN / 8, RPP = CFG::NT / CPR;
     static_assert(CFG::NT % CPR == 0 && SS::ROWS % RPP == 0, "image passes");
     const int lane = tid & 63, rr = tid / CPR, cc = tid % CPR;
-    // the tile's site, selected by assignment (a conditional over the argument fields
-    // would take their address)
-    SiteMaskArgs a = ea.a0;
-    const bf16_t* h = ea.h0;
-    const uint8_t* ub = ea.ub0;
-    bf16_t* dp = ea.dp0;
-    if (t.prob) {
-      a = ea.a1;
-      h = ea.h1;
-      ub = ea.ub1;
-      dp = ea.dp1;
-    }
+    // the tile's site: each field read as a value and selected (selecting between the
+    // argument structs, or copies of them, takes their addresses and puts them in scratch)
+    const bool p1 = t.prob != 0;
+    const SiteMaskArgs& A0 = ea.a0;
+    const SiteMaskArgs& A1 = ea.a1;
+    const bf16_t *ci0 = A0.ci_pre, *ci1 = A1.ci_pre, *h0 = ea.h0, *h1 = ea.h1;
+    const uint8_t *ub0 = ea.ub0, *ub1 = ea.ub1, *rt0 = A0.route, *rt1 = A1.route;
+    const float *dl0 = A0.delta, *dl1 = A1.delta, *sl0 = A0.slope, *sl1 = A1.slope;
+    bf16_t *dp0 = ea.dp0, *dp1 = ea.dp1;
+    const bf16_t* ci = p1 ? ci1 : ci0;
+    const bf16_t* h = p1 ? h1 : h0;
+    const uint8_t* ub = p1 ? ub1 : ub0;
+    const uint8_t* route = p1 ? rt1 : rt0;
+    const float* delta = p1 ? dl1 : dl0;
+    const float* slope = p1 ? sl1 : sl0;
+    bf16_t* dp = p1 ? dp1 : dp0;
+    const int32_t* sort_idx = A0.sort_idx;  // shared by the pair
+    const int c = A0.c, kk = A0.k;
+    const float uconst = A0.uconst, g2 = A0.g2, psis = A0.psis, pexp = A0.p;
     const int col = (int)t.n0 + cc * 8;
+    const bool cok = col < p.N;
+    bf16_t* dh = (bf16_t*)t.C;
+    // every row of the tile has the tile's expert: one slope chunk per lane
+    float slope8[8];
+    if constexpr (PM == PM_SL0) {
+      if (cok) load8f(slope + (int64_t)t.e * c + col, slope8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) slope8[e] = ea.imp_scale;
+    }
+    // a lane's chunks of one pass, one at a time (issuing several chunks' loads ahead of
+    // their math measured slower)
+    constexpr int IT = SS::ROWS / RPP, G = 1;
+    static_assert(IT % G == 0, "chunk groups");
 #pragma unroll
     for (int q = 0; q < SS::PASSES; ++q) {
       staged_image_pass<CFG, 2>(1.f, q, wm, wn, lane, acc, smem);
-#pragma unroll 2
-      for (int r = rr; r < SS::ROWS; r += RPP) {
-        const int64_t row = t.m0 + q * SS::ROWS + r;
-        if (row >= t.M || col >= p.N) continue;
-        float da[8];
-        const uint4 v = *(const uint4*)(smem + r * SS::RSB + cc * 16);
-        da[0] = bf_lo(v.x), da[1] = bf_hi(v.x), da[2] = bf_lo(v.y), da[3] = bf_hi(v.y);
-        da[4] = bf_lo(v.z), da[5] = bf_hi(v.z), da[6] = bf_lo(v.w), da[7] = bf_hi(v.w);
-        mask_bwd_chunk<PM>(a, h, ub, ea.imp_scale, row, a.sort_idx[row], t.e, col, da, (bf16_t*)t.C, dp);
+#pragma unroll
+      for (int g0 = 0; g0 < IT; g0 += G) {
+        int64_t row[G];
+        int32_t slot[G];
+        bool ok[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          row[i] = t.m0 + q * SS::ROWS + rr + (g0 + i) * RPP;
+          ok[i] = cok && row[i] < t.M;
+          slot[i] = ok[i] ? sort_idx[row[i]] : 0;
+        }
+        uint4 pw[G], hw[G];
+        uint2 uw[G];
+        float dt[G];
+        bool routed[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          if (!ok[i]) continue;
+          pw[i] = *(const uint4*)(ci + (int64_t)slot[i] * c + col);
+          hw[i] = *(const uint4*)(h + row[i] * c + col);
+          uw[i] = uconst < 0.f ? *(const uint2*)(ub + row[i] * c + col) : make_uint2(0u, 0u);
+          dt[i] = delta ? delta[slot[i] / kk] : 0.f;
+          routed[i] = !route || route[slot[i] / kk];
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+          if (!ok[i]) continue;
+          const int r = rr + (g0 + i) * RPP;
+          const uint4 v = *(const uint4*)(smem + r * SS::RSB + cc * 16);
+          float da[8], pre[8], hv[8], dpv[8], o[8];
+          da[0] = bf_lo(v.x), da[1] = bf_hi(v.x), da[2] = bf_lo(v.y), da[3] = bf_hi(v.y);
+          da[4] = bf_lo(v.z), da[5] = bf_hi(v.z), da[6] = bf_lo(v.w), da[7] = bf_hi(v.w);
+          if (!routed[i]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) da[e] = 0.f;
+          }
+          pre[0] = bf_lo(pw[i].x), pre[1] = bf_hi(pw[i].x), pre[2] = bf_lo(pw[i].y), pre[3] = bf_hi(pw[i].y);
+          pre[4] = bf_lo(pw[i].z), pre[5] = bf_hi(pw[i].z), pre[6] = bf_lo(pw[i].w), pre[7] = bf_hi(pw[i].w);
+          hv[0] = bf_lo(hw[i].x), hv[1] = bf_hi(hw[i].x), hv[2] = bf_lo(hw[i].y), hv[3] = bf_hi(hw[i].y);
+          hv[4] = bf_lo(hw[i].z), hv[5] = bf_hi(hw[i].z), hv[6] = bf_lo(hw[i].w), hv[7] = bf_hi(hw[i].w);
+          mask_bwd_values<PM>(uconst, g2, psis, pexp, ea.imp_scale, pre, hv, uw[i], slope8, dt[i], da, dpv, o);
+          store8(dp + (int64_t)slot[i] * c + col, dpv);
+          store8(dh + row[i] * c + col, o);
+        }
       }
     }
   }
