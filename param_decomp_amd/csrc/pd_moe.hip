@@ -1557,49 +1557,61 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // ================= K-contiguous weight copies for the forward products (once per step)
   rec.mark(MOE_CAT_CLEAN);
   const int64_t LE = (int64_t)L * E;
-  // The frozen weights' copies and clean layer 0 run on this stream (masked layer 0 needs
-  // all of it). With L > 1 a helper stream copies the components' weights meanwhile, then
-  // runs clean layers 1.. once layer 0 is done, beside the masked forward: the two chains
-  // are independent until masked layer l reads clean layer l's routing, and the matrix-core
-  // phases of one overlap the VALU-bound mask passes of the other. In the backward the
-  // helper stream runs the weight-gradient products. Its events: start, fork, copies,
-  // weight-gradient inputs ready [4] and done [4], clean layer l done (layer l % 64: a
-  // wait on a shared event waits for the last layer recorded on it, later than needed).
+  // With L > 1 a helper stream takes every weight copy and the clean pass after layer 0's
+  // routing: this stream forms layer 0's routing (the masked pass runs under it), then
+  // starts the masked forward while the helper finishes clean layer 0 and runs clean
+  // layers 1.. beside it. The two chains are independent until masked layer l reads clean
+  // layer l's routing (and masked layer 0 the clean gate / up products of the frozen
+  // channel), and the matrix-core phases of one overlap the VALU-bound mask passes of the
+  // other. In the backward the helper stream runs the weight-gradient products. Its
+  // events: start, the copies of Vg / Vu (masked layer 0's first product) and of the rest,
+  // weight-gradient inputs ready [4] and done [4], layer 0's routing formed, clean layer
+  // 0's gate / up products formed, clean layer l done (layer l % 64: a wait on a shared
+  // event waits for the last layer recorded on it, later than needed).
   constexpr int LAYER_EVENTS = 64;
   struct {
     hipStream_t st = nullptr;
-    hipEvent_t start, fork, copies, *wg_in, *wg_out, *layer_ev;
+    hipEvent_t start, vcopies, copies, *wg_in, *wg_out, route0, clean0, *layer_ev;
     hipEvent_t layer(int l) const { return layer_ev[l % LAYER_EVENTS]; }
   } cs;
   const bool side = !reuse_clean && L > 1;
   AuxStream ax;  // its lease is held until this call has enqueued all of its work
   if (side || want_wgrads) {
-    if ((rc0 = aux_stream(0, 11 + std::min(L, LAYER_EVENTS), ax))) return rc0;
+    if ((rc0 = aux_stream(0, 14 + std::min(L, LAYER_EVENTS), ax))) return rc0;
     cs.st = ax.st;
     cs.start = ax.ev[0];
-    cs.fork = ax.ev[1];
+    cs.vcopies = ax.ev[1];
     cs.copies = ax.ev[2];
     cs.wg_in = ax.ev + 3;
     cs.wg_out = ax.ev + 7;
-    cs.layer_ev = ax.ev + 11;
+    cs.route0 = ax.ev[11];
+    cs.clean0 = ax.ev[12];
+    cs.layer_ev = ax.ev + 14;
   }
   if (side) {
     hipEventRecord(cs.start, s);
     hipStreamWaitEvent(cs.st, cs.start, 0);
   }
-  if (!reuse_clean) {  // the frozen weights' copies, else as the previous call left them
-    launch_batched_T(Wg, LE, d, f, P.WgT, s);
-    launch_batched_T(Wu, LE, d, f, P.WuT, s);
-    launch_batched_T(Wd, LE, f, d, P.WdT, s);
-  }
+  // the frozen weights' copies (else as the previous call left them): on this stream
+  // ahead of everything without the helper, after the components' copies with it
+  auto frozen_copies = [&](hipStream_t st) {
+    launch_batched_T(Wg, LE, d, f, P.WgT, st);
+    launch_batched_T(Wu, LE, d, f, P.WuT, st);
+    launch_batched_T(Wd, LE, f, d, P.WdT, st);
+  };
+  if (!reuse_clean && !side) frozen_copies(s);
   const hipStream_t scp = side ? cs.st : s;
   launch_batched_T(Vg, LE, d, c, P.VgT, scp);
-  launch_batched_T(Ug, LE, c, f, P.UgT, scp);
   launch_batched_T(Vu, LE, d, c, P.VuT, scp);
+  if (side) hipEventRecord(cs.vcopies, cs.st);
+  launch_batched_T(Ug, LE, c, f, P.UgT, scp);
   launch_batched_T(Uu, LE, c, f, P.UuT, scp);
   launch_batched_T(Vd, LE, f, c, P.VdT, scp);
   launch_batched_T(Ud, LE, c, d, P.UdT, scp);
-  if (side) hipEventRecord(cs.copies, cs.st);
+  if (side) {
+    frozen_copies(cs.st);
+    hipEventRecord(cs.copies, cs.st);
+  }
   const bf16_t* VT[3] = {P.VgT, P.VuT, P.VdT};
   const bf16_t* UT[3] = {P.UgT, P.UuT, P.UdT};
   const size_t szV[3] = {szVg, szVg, szVd};
@@ -1630,7 +1642,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // the masked pass's own input under the same routing, so its norm (h2, rinv), routing
   // weights, gathered x_jobs (and copy) and the gate/up products of the frozen channel
   // are written straight into the masked pass's buffers; later clean layers gather into
-  // a buffer the masked pass only uses afterwards. With reuse_clean the workspace still
+  // a buffer the masked pass only uses afterwards. Layer 0's routing runs on this stream,
+  // the rest of the clean pass on the helper stream (when there is one). With reuse_clean the workspace still
   // holds all of it from the previous call (nothing after the clean pass writes these
   // buffers), and the clean final residual is the ping-pong buffer L layers end in.
   bf16_t* rcur = P.rc_a;
@@ -1643,11 +1656,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   }
   for (int l = 0; l < L && !reuse_clean; ++l) {
     LayerSave& S = P.layers[l];
-    if (l == 1) {
-      hipEventRecord(cs.fork, s);
-      hipStreamWaitEvent(cs.st, cs.fork, 0);
-    }
-    hipStream_t sc = l == 0 ? s : cs.st;
+    hipStream_t sc = l == 0 ? s : cs.st;  // the routing part
     bf16_t* h2l = l == 0 ? S.h2 : P.h2c;
     hipLaunchKernelGGL(k_rmsnorm_fwd, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, sc, rcur, T, d, ln + (size_t)l * d, 1e-6f,
                        h2l, l == 0 ? S.rinv : (float*)nullptr);
@@ -1663,22 +1672,28 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     bf16_t* xjl = l == 0 ? S.xj : P.xjc;
     hipLaunchKernelGGL(k_gather_tile, tile_grid(J, d), dim3(256), 0, sc, h2l, S.sort_idx, k, J, d, xjl,
                        (bf16_t*)nullptr);
+    if (top_idx_out)
+      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, sc);
+    const hipStream_t sr = side ? cs.st : s;  // the rest of the layer
+    if (l == 0 && side) {
+      hipEventRecord(cs.route0, s);
+      hipStreamWaitEvent(cs.st, cs.route0, 0);
+    }
     bf16_t* gcl = l == 0 ? S.fg : P.gc;
     bf16_t* ucl = l == 0 ? S.fu : P.uc;
     if ((rc = grouped_gemm_pair(xjl, P.WgT + l * szW, gcl, xjl, P.WuT + l * szW, ucl, S.offsets, J, E, d, f,
-                                PD_DTYPE_BF16, sc)))
+                                PD_DTYPE_BF16, sr)))
       return rc;
-    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, sc, gcl, ucl, (const float*)nullptr,
+    if (l == 0 && side) hipEventRecord(cs.clean0, cs.st);
+    hipLaunchKernelGGL(k_swiglu_fwd_tile, tile_grid(J, f), dim3(256), 0, sr, gcl, ucl, (const float*)nullptr,
                        S.sort_idx, J, f, (const bf16_t*)nullptr, (const bf16_t*)nullptr, (const float*)nullptr,
                        (const float*)nullptr, k, P.din);
-    if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, sc, false)))
+    if ((rc = grouped_gemm(P.din, P.WdT + l * szW, S.offsets, J, E, f, d, 1, P.downc, PD_DTYPE_BF16, sr, false)))
       return rc;
-    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, sc, rcur, P.downc, S.inv, P.wc, T, k, d,
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, sr, rcur, P.downc, S.inv, P.wc, T, k, d,
                        (const bf16_t*)nullptr, (const float*)nullptr, rnext);
     std::swap(rcur, rnext);
-    if (top_idx_out)
-      hipMemcpyAsync(top_idx_out + (size_t)l * T * k, S.idx, (size_t)T * k * 4, hipMemcpyDeviceToDevice, sc);
-    if (l > 0) hipEventRecord(cs.layer(l), sc);
+    if (l > 0) hipEventRecord(cs.layer(l), sr);
   }
   bf16_t* rc_final = rcur;
   if ((rc = check_launch("pd_moe_stack_step clean"))) return rc;
@@ -1686,7 +1701,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // ================= masked forward
   if (side) {
     rec.mark(MOE_CAT_WAIT);
-    hipStreamWaitEvent(s, cs.copies, 0);
+    hipStreamWaitEvent(s, cs.vcopies, 0);
   }
   const bf16_t* r_in = (const bf16_t*)x0;
   for (int l = 0; l < L; ++l) {
@@ -1753,6 +1768,11 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     rec.mark(MOE_CAT_MASK_FWD);
     mask_fwd(0);
     mask_fwd(1);
+    if (side && l == 0) {  // every other weight copy; the clean gate / up products
+      rec.mark(MOE_CAT_WAIT);
+      hipStreamWaitEvent(s, cs.copies, 0);
+      hipStreamWaitEvent(s, cs.clean0, 0);
+    }
     rec.mark(MOE_CAT_GEMM_FWD);
     if (kc && l > 0) {  // g = bl_g (x_jobs @ Wg[e]) + acts_g @ Ug[e], u likewise: blended here
       if ((rc = grouped_gemm_kcat(S.xj, P.WgT + l * szW, d, S.acts[0], UT[0] + l * szU[0], c, S.gout, bl[0], S.xj,
