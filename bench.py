@@ -978,11 +978,35 @@ def run_gemm_moe(args):
         phase[name] = hip_events.elapsed_ms(ev[0], ev[1]) / reps
         hip_events.destroy(ev)
         tflops[name] = fl / (phase[name] * 1e-3) / 1e12
+    # The bar: the dense equivalents (all J rows against one weight) through hipBLASLt
+    # (torch.matmul) and through pd_gemm; not part of the step.
+    dense_bar = {}
+    for M, K, N in ((J, d, c), (J, c, f), (J, f, c)):
+        a = rn(M, K)
+        bt = rn(N, K)
+        out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        times = {}
+        for lib, launch in (("hipblaslt", lambda: torch.matmul(a, bt.t(), out=out)),
+                            ("pd_gemm", lambda: ops.gemm(a, bt, trans_b=True, out=out))):
+            for _ in range(max(args.warmup, 1)):
+                launch()
+            ev = hip_events.create(2)
+            torch.cuda.synchronize()
+            hip_events.record(ev[0], stream)
+            for _ in range(reps):
+                launch()
+            hip_events.record(ev[1], stream)
+            torch.cuda.synchronize()
+            times[lib] = hip_events.elapsed_ms(ev[0], ev[1]) / reps
+            hip_events.destroy(ev)
+        dense_bar[f"M{M}_K{K}_N{N}"] = {lib: {"ms": t, "tflops": 2 * M * N * K / (t * 1e-3) / 1e12}
+                                        for lib, t in times.items()}
     dom = max(phase, key=phase.get)
     return {"tokens": J, "ms_per_step": sum(phase.values()),
             "config": {"workload": GEMM_MOE, **cfg, "group_sizes": "ragged, seeded (0.6 + 0.8 U) weights",
                        "unit_of_value": "job rows per step of every listed product"},
             "step_flops": sum(fl for _, fl in prods.values()), "phases_ms": phase, "tflops": tflops,
+            "dense_equivalents": dense_bar,
             "roofline": roofline("flop", prods[dom][1], phase[dom], dom, 1)}
 
 
@@ -1468,7 +1492,7 @@ def main():
         out["launches_per_step"] = res["launches_per_step"]
     if "tflops" in res:
         out["tflops_per_product"] = res["tflops"]
-    for key in ("hipblaslt_tflops", "max_rel_diff_vs_hipblaslt"):
+    for key in ("hipblaslt_tflops", "max_rel_diff_vs_hipblaslt", "dense_equivalents"):
         if key in res:
             out[key] = res[key]
     if "reference_rule_flops" in res:
