@@ -290,9 +290,18 @@ def pmc_l2_summary(csv_path: str, command: str, n_xcd: int = 8, n_ch: int = 16) 
 # Kernels of a timed phase (name prefixes as rocprofv3 prints them). A phase's traffic per
 # launch is the dispatch-weighted mean over its kernels in the committed PMC summary.
 PHASE_KERNEL = {
+    # (the GEMM kernels of a phase also run in other phases: the clean pass, the backward)
     MOE: {"gemm_dw": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, float, 2,",
                       "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 2,"),
-          "mask_fwd": ("pd::k_mask_fwd_tile",), "mask_bwd": ("pd::k_mask_bwd_tile",)},
+          "gemm_fwd": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, unsigned short, 1, false, pd::EpiStore",
+                       "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 1, false, pd::EpiStore",
+                       "pd::k_gemm_dtl_kcat<"),
+          "gemm_dx": ("pd::k_gemm_dtl_kcat<",),
+          "gemm_dx_mask": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, unsigned short, 1, false, "
+                           "pd::EpiMaskBwd",
+                           "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 1, false, "
+                           "pd::EpiMaskBwd"),
+          "mask_fwd": ("pd::k_mask_fwd_tile",), "mask_bwd": ("pd::k_mask_bwd_tile", "pd::k_mask_bwd_vec")},
     DENSE: {"gate_mask_fwd": ("pd::k_step_fwd_tab",), "gate_mask_bwd": ("pd::k_step_bwd",),
             "recon": ("pd::k_step_recon",)},
 }
@@ -1045,6 +1054,20 @@ def moe_step_flops(cfg):
     return sum(moe_gemm_flops(cfg).values())
 
 
+def moe_dacts_work(cfg):
+    """The d_acts products (g @ U^T per site and layer; part of gemm_dx's FLOPs) that run
+    with the mask backward as their epilogue: their FLOPs and algorithmic HBM bytes (read
+    g [J, K] and U; the epilogue reads ci, h, the u byte and writes d_h, d_ci: 9 bytes per
+    selected component)."""
+    J, d, f, c, E = cfg["T"] * cfg["k"], cfg["d"], cfg["f"], cfg["c"], cfg["E"]
+    flops = byts = 0
+    for _ in range(cfg["L"]):
+        for K in (f, f, d):  # gate, up (g has width f), down (width d)
+            flops += 2 * J * c * K
+            byts += 2 * J * K + 2 * E * K * c + 9 * J * c
+    return flops, byts
+
+
 def moe_cpu_baseline(cfg, T_sample, reps=5, warmup=2):
     """The compiled fp32 C/OpenMP restatement of the same step (`oracle/cpu_step.c`
     `or_moe_step`, checked against the NumPy oracle) on `T_sample` tokens at the full
@@ -1127,13 +1150,17 @@ def run_moe(args):
     # algorithmic work per category (per step) for the roofline of the dominant one
     J = T * k
     gf = moe_gemm_flops(cfg)
+    da_flops, da_bytes = moe_dacts_work(cfg)
+    fused = cat_n.get("gemm_dx_mask", 0) > 0  # the d_acts products carry the mask backward
     work = {
         "gemm_fwd": ("flop", gf["gemm_fwd"]),
-        "gemm_dx": ("flop", gf["gemm_dx"]),
+        "gemm_dx": ("flop", gf["gemm_dx"] - (da_flops if fused else 0)),
         "gemm_dw": ("flop", gf["gemm_dw"]),
         "mask_fwd": ("byte", Ln * 3 * J * c * (2 + 2 + 2 + 1)),   # read ci, h; write acts, u bits
-        "mask_bwd": ("byte", Ln * 3 * J * c * (2 + 2 + 1 + 2 + 2)),  # read ci, h, u, d_acts; write d_h, d_ci
+        "gemm_dx_mask": ("byte", da_bytes),  # HBM-bound: 9 B per element against ~2 flop/B
     }
+    if not fused:
+        work["mask_bwd"] = ("byte", Ln * 3 * J * c * (2 + 2 + 1 + 2 + 2))  # read ci, h, u, d_acts; write d_h, d_ci
     dom = max((n for n in cat_ms if n in work), key=cat_ms.get)
     kind, amount = work[dom]
     launches = cat_n[dom]

@@ -422,7 +422,9 @@ int pd_moe_stack_step_sources(int64_t T, int d, int f, int E, int k, int c, int 
  * end; categories[i] labels the interval [i, i+1): 0 clean forward, 1 masked norm /
  * router / bucketing / gather, 2 grouped GEMMs fwd, 3 mask fwd, 4 SwiGLU fold,
  * 5 combine / loss / gathers, 6 grouped GEMMs d_input, 7 grouped GEMMs d_weight,
- * 8 mask bwd, 9 router+norm token backward, 10 end. *n_recorded = events used. */
+ * 8 mask bwd, 9 router+norm token backward, 10 waiting for the helper stream, 11 grouped
+ * d_acts GEMMs with the mask backward as their epilogue; the last event ends the final
+ * interval. *n_recorded = events used. */
 int pd_moe_stack_step_timed(int64_t T, int d, int f, int E, int k, int c, int L, const void* x0, const float* ln,
                             const void* router, const void* Wg, const void* Wu, const void* Wd, const void* Vg,
                             const void* Ug, const void* Vu, const void* Uu, const void* Vd, const void* Ud,

@@ -1436,7 +1436,8 @@ enum {
   MOE_CAT_MASK_BWD = 8,    // job-space mask passes, backward
   MOE_CAT_TOKEN_BWD = 9,   // router/norm token backward
   MOE_CAT_WAIT = 10,       // waiting for the helper stream (clean layers, weight gradients)
-  MOE_CAT_END = 11
+  MOE_CAT_GEMM_MASK = 11,  // grouped GEMMs d_acts with the backward mask as their epilogue
+  MOE_CAT_END = 12
 };
 
 // Persistent (adversarial) source tables for pd_moe_stack_step_sources.
@@ -1911,7 +1912,7 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     bf16_t* dpre[3];
     for (int si = 0; si < 3; ++si) dpre[si] = (bf16_t*)d_ci_pre + ((size_t)l * 3 + si) * szCI;
     const bool fuse_d = mask_bwd_fusable(mg[2], S.h[2], S.ub[2], dpre[2], P.d_acts[2], d);
-    rec.mark(MOE_CAT_GEMM_DX);
+    rec.mark(fuse_d ? MOE_CAT_GEMM_MASK : MOE_CAT_GEMM_DX);
     if (fuse_d)
       rc = grouped_gemm_mask_bwd(P.d_dout, bf(Ud, l * szUd), P.d_acts[2], mg[2], S.h[2], S.ub[2], dpre[2], nullptr,
                                  nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, S.offsets, J, E, d, c, pm,
@@ -1959,9 +1960,9 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
     // ---- gate and up sites: paired launches
     rec.mark(MOE_CAT_WAIT);
     wjoin(3);  // the previous layer's gate / up dV read d_acts[0], d_acts[1]
-    rec.mark(MOE_CAT_GEMM_DX);
     const bool fuse_gu = mask_bwd_fusable(mg[0], S.h[0], S.ub[0], dpre[0], P.d_acts[0], f) &&
                          mask_bwd_fusable(mg[1], S.h[1], S.ub[1], dpre[1], P.d_acts[1], f);
+    rec.mark(fuse_gu ? MOE_CAT_GEMM_MASK : MOE_CAT_GEMM_DX);
     if (fuse_gu)
       rc = grouped_gemm_mask_bwd(P.d_g, bf(Ug, l * szUg), P.d_acts[0], mg[0], S.h[0], S.ub[0], dpre[0], P.d_u,
                                  bf(Uu, l * szUg), P.d_acts[1], &mg[1], S.h[1], S.ub[1], dpre[1], S.offsets, J, E, f, c,

@@ -25,7 +25,7 @@ from param_decomp_amd.prng import Key
 
 SITE_NAMES = ("gate", "up", "down")
 CATEGORIES = ("clean_fwd", "norm_route", "gemm_fwd", "mask_fwd", "swiglu", "combine_loss", "gemm_dx", "gemm_dw",
-              "mask_bwd", "token_bwd", "wait")
+              "mask_bwd", "token_bwd", "wait", "gemm_dx_mask")
 
 
 @dataclass
