@@ -95,22 +95,37 @@ class FaithfulnessLoss:
         return out
 
 
+def _names_by_stack(site_stack_indices) -> dict:
+    """Per stack group, its site names in stack order. Each group's indices must count
+    0, 1, 2, ... in the order the sites are listed."""
+    names: dict = {}
+    for name, group, index in site_stack_indices:
+        seq = names.setdefault(group, [])
+        if index != len(seq):
+            raise AssertionError(f"stack {group!r}: site {name!r} has stack index {index}, expected {len(seq)}")
+        seq.append(name)
+    return names
+
+
 def make_faithfulness_loss(site_stack_indices, target_sq_norms: dict, stack_pads: dict | None = None):
     """`pd/core/faithfulness.py:16-75`: validate and bind the per-stack-index `||W_s||^2`
     (finite and positive), pad persist-stack pads with 1.0 (their deltas are exactly
-    zero), and average over the real sites."""
-    stack_pads = dict(stack_pads or {})
-    stack_names: dict = {}
-    for name, group, index in site_stack_indices:
-        assert index == len(stack_names.setdefault(group, [])), site_stack_indices
-        stack_names[group].append(name)
-    assert target_sq_norms.keys() == stack_names.keys(), (sorted(target_sq_norms), sorted(stack_names))
+    zero), and average over the real sites. Bad inputs raise AssertionError, as the
+    reference's checks do (its test matches the words "finite positive")."""
+    pads = dict(stack_pads or {})
+    names = _names_by_stack(site_stack_indices)
+    if set(target_sq_norms) != set(names):
+        raise AssertionError(f"||W||^2 stack groups {sorted(target_sq_norms)} differ from the sites' {sorted(names)}")
     for group, norms in target_sq_norms.items():
-        assert len(norms) == len(stack_names[group]), (group, len(norms), stack_names[group])
-    bad = {name: value for group, norms in target_sq_norms.items()
-           for name, value in zip(stack_names[group], norms) if not math.isfinite(value) or value <= 0.0}
-    assert not bad, f"faithfulness needs finite positive ‖W_s‖²: {bad}"
-    assert stack_pads.keys() <= target_sq_norms.keys(), (sorted(stack_pads), sorted(stack_names))
-    padded = {group: tuple(float(v) for v in norms) + (1.0,) * stack_pads.get(group, 0)
+        values = [float(v) for v in norms]
+        if len(values) != len(names[group]):
+            raise AssertionError(f"stack {group!r}: {len(values)} norms for {len(names[group])} sites")
+        invalid = {n: v for n, v in zip(names[group], values) if not (math.isfinite(v) and v > 0.0)}
+        if invalid:
+            raise AssertionError(f"each ||W_s||^2 must be a finite positive number; stack {group!r} has {invalid}")
+    unknown = set(pads) - set(names)
+    if unknown:
+        raise AssertionError(f"pads for unknown stack groups {sorted(unknown)}")
+    padded = {group: tuple(float(v) for v in norms) + (1.0,) * int(pads.get(group, 0))
               for group, norms in target_sq_norms.items()}
-    return FaithfulnessLoss(stack_names, padded, len(site_stack_indices))
+    return FaithfulnessLoss(names, padded, len(site_stack_indices))
