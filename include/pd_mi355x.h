@@ -195,7 +195,11 @@ int pd_masked_linear_bwd(int dtype, int64_t T, int64_t d_in, int64_t d_out, int6
  * device on the first call and held until the process ends. Calls whose
  * pd_masked_linear_bwd_workspace_size exceeds it return PD_EUNSUPPORTED. No allocation
  * happens in the call. Every call on one GPU shares that GPU's region: calls that overlap
- * on one GPU (different streams, or host threads without ordering) race. */
+ * on one GPU (different streams, or host threads without ordering) race, and so do two
+ * captured graphs containing it whose replays overlap. Under graph capture, make one
+ * eager call on the device first (it looks the region up); the call itself launches
+ * kernels only (no memset, no host synchronization). Loading the library reserves the
+ * region on every GPU it runs on, whether or not the entry point is called. */
 #define PD_MASKED_LINEAR_BWD_NOALLOC_MAX_BYTES ((size_t)64 << 20)
 int pd_masked_linear_bwd_noalloc(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, const void* x,
                                  const void* V, const void* U, const void* W, const void* mask, const void* delta,

@@ -69,3 +69,58 @@ def test_noalloc_backward_refuses_requests_above_its_scratch(device):
     with pytest.raises(L.PDError, match="above the fixed"):
         L.call("pd_masked_linear_bwd_noalloc", L.BF16, T, 64, d_out, C, p, p, p, p, p, None, None, p, p, p, p, p, p,
                None, None, L.stream())
+
+
+def test_noalloc_backward_replays_under_graph_capture(device):
+    """Captured into a HIP graph (torch.cuda.graph) after one eager call on the device, the
+    allocation-free backward replays with new inputs written into the captured buffers;
+    every replay, with eager calls of the workspace entry point between them, is
+    bit-identical to pd_masked_linear_bwd on the same inputs."""
+    from param_decomp_amd import _lib as L
+
+    dtype, T, d_in, d_out, C = torch.bfloat16, 512, 256, 384, 1024
+    code = L.dtype_code(dtype)
+    rng = np.random.default_rng(7)
+    static = [t.clone() for t in _inputs(rng, T, d_in, d_out, C, device, dtype)]
+    x, V, U, W, mask, delta, route, g = static
+    xV = torch.empty(T, C, dtype=dtype, device=device)
+    acts = torch.empty(T, C, dtype=dtype, device=device)
+    out = torch.empty(T, d_out, dtype=dtype, device=device)
+    grads = [torch.zeros(shape, dtype=dtype, device=device) for shape in ((T, d_in), (d_in, C), (C, d_out), (T, C), (T,))]
+
+    def forward():
+        L.call("pd_masked_linear_fwd", code, T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), L.ptr(W), L.ptr(mask),
+               L.ptr(delta), L.ptr(route), L.ptr(out), L.ptr(xV), L.ptr(acts), L.stream())
+
+    def noalloc():
+        L.call("pd_masked_linear_bwd_noalloc", code, T, d_in, d_out, C, L.ptr(x), L.ptr(V), L.ptr(U), L.ptr(W),
+               L.ptr(mask), L.ptr(delta), L.ptr(route), L.ptr(xV), L.ptr(acts), L.ptr(g),
+               *[L.ptr(t) for t in grads], L.stream())
+
+    forward()
+    noalloc()  # the eager call that looks the scratch region up on this device
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=device)  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        noalloc()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        noalloc()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        for dst, src in zip(static, _inputs(rng, T, d_in, d_out, C, device, dtype)):
+            dst.copy_(src)
+        forward()
+        for t in grads:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in grads]
+        want = _backward(L, "pd_masked_linear_bwd", dtype, T, d_in, d_out, C, *static)
+        for name, a, b in zip(("dx", "dV", "dU", "dmask", "d_delta"), got, want):
+            assert torch.isfinite(b.float()).all(), name
+            assert torch.equal(a, b), f"{name} differs on replay {replay}"
