@@ -1215,19 +1215,15 @@ static int grouped_gemm_mask_bwd(const bf16_t* lhs, const bf16_t* rhs, bf16_t* o
   if (!dtl_fits(J, K, N, K) || cdiv(J, CfgDtlRA::BM) + E > 65535)
     return fail(PD_EUNSUPPORTED, "pd_moe_stack_step: d_acts product too large");
   GemmArgs a{J, N, K, lhs, K, rhs, K, out, N, 1.f, 0.f, offsets, E, K * N, 0, 0, lhs2, rhs2, out2};
-  const bool big = pair && N >= 512;  // 256x256 tiles, as for the paired N=512 products
-  const dim3 grid = big ? dim3((unsigned)cdiv(N, CfgDtlBig::BN), (unsigned)(cdiv(J, CfgDtlBig::BM) + E), 2u)
-                        : dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), pair ? 2u : 1u);
+  // 128x128 tiles for pairs too (unlike the plain paired N=512 products): two blocks per
+  // CU keep twice the waves to cover the epilogue's gathered loads (measured faster)
+  const dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)(cdiv(J, CfgDtlRA::BM) + E), pair ? 2u : 1u);
 #define PD_FM(PMV)                                                                                                    \
   {                                                                                                                   \
     typename EpiMaskBwd<PMV>::Args ea{m0, pair ? *m1 : m0, h0, pair ? h1 : h0, ub0, pair ? ub1 : ub0, d_pre0,         \
                                       pair ? d_pre1 : d_pre0, imp_scale};                                             \
-    if (big)                                                                                                          \
-      hipLaunchKernelGGL((k_gemm_dtl<CfgDtlBig, bf16_t, MODE_GROUPED, false, EpiMaskBwd<PMV>>), grid,                \
-                         dim3(CfgDtlBig::NT), 0, s, a, ea);                                                           \
-    else                                                                                                              \
-      hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, bf16_t, MODE_GROUPED, false, EpiMaskBwd<PMV>>), grid,                 \
-                         dim3(CfgDtlRA::NT), 0, s, a, ea);                                                            \
+    hipLaunchKernelGGL((k_gemm_dtl<CfgDtlRA, bf16_t, MODE_GROUPED, false, EpiMaskBwd<PMV>>), grid,                   \
+                       dim3(CfgDtlRA::NT), 0, s, a, ea);                                                              \
   }
   if (pm == PM_SL0) PD_FM(PM_SL0)
   else if (pm == 2) PD_FM(2)
