@@ -322,7 +322,7 @@ def site_keys(draw_key, cfg: LMConfig, kind: str, layer: int, partitionable=True
 
 def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.0, imp_coeff=1.0, recon_coeff=1.0,
                   bf16_storage=False, partitionable=True, use_delta=True, uniforms=None, dtype=F64, imp_min=None,
-                  freq_ema=None, ema_count=0.0, routes=None):
+                  freq_ema=None, ema_count=0.0, routes=None, sources=None):
     """One stochastic-recon KL + imp-min step, forward and backward. The imp-min term is
     L_p (p, imp_coeff) or `imp_min` (a `pd_oracle.ImpMin`; smooth-L0 with the frequency
     penalty as the reference writes it, `pd/core/losses.py:340-394`: per-site means of
@@ -340,6 +340,14 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
     site output is the target's (`site`'s route arm).
     `dtype` torch.float32 runs the same arithmetic in fp32 (the CPU baseline's timing
     form; the float64 default is the checker).
+    `sources = (src, src_delta, rows_per_source)` replaces the draws by persistent
+    (adversarial) source tables (`pd/core/source_mask.py:56-63`, `pd/core/masking.py:
+    260-272`): src[l][kind] [S, C_kind], src_delta[l][kind] [S] (or src_delta None: no
+    delta channel), every source row covering rows_per_source consecutive tokens of the
+    flattened [b*t] order (S = b*t / rows_per_source: the `c`, `bc` and `bsc` shapes). The
+    tables are cast to the CI dtype before use (bf16 with `bf16_storage`), m = lower +
+    (1 - lower) src[n // rps] and d = src_delta[n // rps]; the result then also holds the
+    tables' gradients d_src[l][kind] and d_src_delta[l][kind].
     Returns dict(loss, recon, imp, freq, dV[l][kind], dU[l][kind], d_ci_pre[l][kind], u, delta)."""
     rb = _rounder(bf16_storage)
     spec = imp_min if imp_min is not None else po.ImpMin("pnorm", p=p, coeff=imp_coeff)
@@ -361,6 +369,10 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
         act_c = forward(cfg, prm, r0, rb=rb)
         clean_logits = logits(prm, act_c)
     masks, deltas, pres, us, ds = [], [], {}, {}, {}
+    src_leaf, srcd_leaf = {}, {}
+    if sources is not None:
+        use_delta = sources[1] is not None
+        doc = torch.as_tensor(np.arange(N) // sources[2], dtype=torch.long)
     imp = torch.zeros((), dtype=dtype)
     freq = torch.zeros((), dtype=dtype)
     freq_batch = 0.0
@@ -374,7 +386,14 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
             C = cfg.C[kind]
             pre = T(ci_pre[l][kind], True)
             pres[(l, kind)] = pre
-            if uniforms is not None:
+            if sources is not None:  # the tables as autograd leaves, cast to the CI dtype
+                src_leaf[(l, kind)] = T(sources[0][l][kind], True)
+                u_t = rb(src_leaf[(l, kind)])[doc]
+                if use_delta:
+                    srcd_leaf[(l, kind)] = T(sources[1][l][kind], True)
+                    d_t = rb(srcd_leaf[(l, kind)])[doc]
+                u, dl = u_t.detach().numpy(), (d_t.detach().numpy() if use_delta else np.zeros(N))
+            elif uniforms is not None:
                 u, dl = uniforms[l][kind]
                 u = np.asarray(u, np.float64)
                 dl = np.asarray(dl, np.float64)
@@ -406,15 +425,19 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
                         a_ = spec.ref_count
                         slope = torch.log2(1.0 + a_ * f_hat) + a_ * f_hat / ((1.0 + a_ * f_hat) * math.log(2.0))
                         freq = freq + (f_hat * torch.log2(1.0 + a_ * f_hat) + slope * (fr - f_sg)).sum()
-            masks[l][kind] = (lo + (1.0 - lo) * T(u)).reshape(b, t, C)
-            deltas[l][kind] = T(dl).reshape(b, t) if use_delta else None
+            if sources is not None:
+                masks[l][kind] = (lo + (1.0 - lo) * u_t).reshape(b, t, C)
+                deltas[l][kind] = d_t.reshape(b, t) if use_delta else None
+            else:
+                masks[l][kind] = (lo + (1.0 - lo) * T(u)).reshape(b, t, C)
+                deltas[l][kind] = T(dl).reshape(b, t) if use_delta else None
     rts = None if routes is None else [{k: np.asarray(v, bool).reshape(b, t) for k, v in layer.items()}
                                        for layer in routes]
     act_m = forward(cfg, prm, r0, masks, deltas, rb=rb, routes=rts)
     recon = kl_per_position(logits(prm, act_m), clean_logits)
     loss = recon_coeff * recon + spec.coeff * imp + (spec.freq_coeff * freq if spec.kind == "smooth_l0" else 0.0)
     wrt = [prm["layers"][l]["V_" + k] for l, k in leaves] + [prm["layers"][l]["U_" + k] for l, k in leaves] + [
-        pres[key] for key in pres]
+        pres[key] for key in pres] + [src_leaf[key] for key in src_leaf] + [srcd_leaf[key] for key in srcd_leaf]
     grads = torch.autograd.grad(loss, wrt)
     n = len(leaves)
     out = dict(loss=float(loss.detach()), recon=float(recon.detach()), imp=float(imp.detach()),
@@ -426,6 +449,14 @@ def lm_stack_step(cfg: LMConfig, params: dict, tokens, ci_pre, draw_key, *, p=2.
         out["dU"][l][k] = grads[n + i].numpy()
     for i, key in enumerate(pres):
         out["d_ci_pre"][key[0]][key[1]] = grads[2 * n + i].numpy()
+    if sources is not None:
+        out["d_src"] = [{} for _ in range(cfg.n_layers)]
+        out["d_src_delta"] = [{} for _ in range(cfg.n_layers)]
+        base = 2 * n + len(pres)
+        for i, key in enumerate(src_leaf):
+            out["d_src"][key[0]][key[1]] = grads[base + i].numpy()
+        for i, key in enumerate(srcd_leaf):
+            out["d_src_delta"][key[0]][key[1]] = grads[base + len(src_leaf) + i].numpy()
     return out
 
 

@@ -317,3 +317,47 @@ def test_stacked_reference_forward_golden():
     np.testing.assert_allclose(subset, f["out::masked_subset"], rtol=1e-4, atol=1e-5)
     # the pins separate the arms: without the routes the subset output moves off its golden
     assert np.abs(run(set(chunk0)) - f["out::masked_subset"]).max() > 1e-3
+
+
+def test_source_tables_with_the_drawn_values_reproduce_the_draw_step():
+    """One token per source row (`bsc`), tables holding exactly the step's own drawn u and
+    d: loss and every gradient equal the draw path's (the source arm reads the same masks)."""
+    cfg, params, tokens, ci = _small()
+    key = (7, 11)
+    kw = dict(p=2.0, imp_coeff=0.3, recon_coeff=1.7, bf16_storage=True)
+    base = lo.lm_stack_step(cfg, params, tokens, ci, key, **kw)
+    src = [{k: base["u"][(l, k)] for k in cfg.C} for l in range(cfg.n_layers)]
+    srcd = [{k: base["delta"][(l, k)] for k in cfg.C} for l in range(cfg.n_layers)]
+    got = lo.lm_stack_step(cfg, params, tokens, ci, key, sources=(src, srcd, 1), **kw)
+    assert got["loss"] == base["loss"]
+    for l in range(cfg.n_layers):
+        for k in cfg.C:
+            np.testing.assert_array_equal(got["dV"][l][k], base["dV"][l][k])
+            np.testing.assert_array_equal(got["d_ci_pre"][l][k], base["d_ci_pre"][l][k])
+            assert got["d_src"][l][k].shape == src[l][k].shape and got["d_src_delta"][l][k].shape == (10,)
+
+
+@pytest.mark.parametrize("rps", [5, 10])
+def test_source_table_gradients_match_finite_differences(rps):
+    """float64: d_src and d_src_delta (rows of 5 tokens: one per sample, `bc`; 10: one
+    row for the batch, `c`) against central differences of the loss."""
+    cfg, params, tokens, ci = _small()
+    rng = np.random.default_rng(9)
+    S = 10 // rps
+    src = [{k: rng.uniform(0.1, 0.9, size=(S, C)) for k, C in cfg.C.items()} for _ in range(cfg.n_layers)]
+    srcd = [{k: rng.uniform(0.1, 0.9, size=S) for k in cfg.C} for _ in range(cfg.n_layers)]
+    kw = dict(p=2.0, imp_coeff=0.3, recon_coeff=1.7, sources=(src, srcd, rps))
+    base = lo.lm_stack_step(cfg, params, tokens, ci, (1, 2), **kw)
+    eps = 1e-6
+    for l, kind in ((0, "q_proj"), (1, "c_fc"), (1, "down_proj")):
+        for tables, grads in ((src, base["d_src"]), (srcd, base["d_src_delta"])):
+            arr = tables[l][kind]
+            for _ in range(2):
+                i = tuple(int(rng.integers(0, s)) for s in arr.shape)
+                old = arr[i]
+                arr[i] = old + eps
+                up = lo.lm_stack_step(cfg, params, tokens, ci, (1, 2), **kw)["loss"]
+                arr[i] = old - eps
+                dn = lo.lm_stack_step(cfg, params, tokens, ci, (1, 2), **kw)["loss"]
+                arr[i] = old
+                assert (up - dn) / (2 * eps) == pytest.approx(grads[l][kind][i], rel=1e-5, abs=1e-9), (l, kind, i)
