@@ -499,6 +499,37 @@ int pd_lm_stack_step(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int
                      const float* freq_ema_in, float* freq_ema_out, float ema_count, float ema_halflife,
                      float recon_coeff, int n_kl_chunks, float* losses, float* const* dV, float* const* dU,
                      void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream);
+/* pd_lm_stack_step with persistent (adversarial) source tables in place of the draws
+ * (pd/core/source_mask.py:56-63; pd/core/masking.py:260-272), the source half of
+ * persistent PGD (pd/core/train.py:693-811, pd/core/adversary.py:463-567). src[k] [L, S,
+ * C_k] per kind (src_dtype F32, BF16 or U16 = u / 65535), every source row covering
+ * rows_per_source consecutive tokens of the [B*T] order (S = B*T / rows_per_source:
+ * B*T is the `c` shape, T the positions of a sample `bc`, 1 `bsc`; a pooled adversary's
+ * per-sample draw of a pool particle is a `bc` table the caller gathers);
+ * m = lower + (1 - lower) bf16(src[n / rps]); src_delta [L, 6, S] (its own dtype; NULL =
+ * no delta channel) gives d = bf16(src_delta[n / rps]). No routes. Outputs as
+ * pd_lm_stack_step (dV, dU only when want_weight_grads; NULL allowed otherwise: the
+ * warmup ascents need only the sources' gradient), plus d_src[k] fp32 [L, S, C_k] = the
+ * sum over each row's tokens of dm (1 - lower), and d_src_delta fp32 [L, 6, S] = the sum
+ * over each row's tokens of sum_o g_out (x @ W^T) - sum_c dm; every sum in a fixed order.
+ * reuse_clean = 1 takes the frozen forward's final activations from the workspace as the
+ * previous call on it left them (the warmup ascents and final step of one PGD step:
+ * tokens, wte and the frozen weights unchanged). Workspace:
+ * pd_lm_stack_sources_workspace_size. */
+size_t pd_lm_stack_sources_workspace_size(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp,
+                                          int64_t vocab, int L, const int32_t* C, int use_delta, int n_kl_chunks,
+                                          int64_t rows_per_source);
+int pd_lm_stack_step_sources(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                             const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
+                             const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
+                             const void* const* V, const void* const* U, const void* const* ci_pre,
+                             const void* const* src, int src_dtype, const void* src_delta, int delta_dtype,
+                             int64_t rows_per_source, int imp_kind, float p, float gamma, int normalize_at_one,
+                             float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                             float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff,
+                             int n_kl_chunks, int want_weight_grads, int reuse_clean, float* losses, float* const* dV,
+                             float* const* dU, void* const* d_ci_pre, float* const* d_src, float* d_src_delta,
+                             void* workspace, size_t workspace_bytes, void* stream);
 /* pd_lm_stack_step recording HIP events at phase boundaries (categories: 0 per-step weight
  * copies and delta draws, 1 frozen forward, 2 site products fwd, 3 mask fwd, 4 attention,
  * 5 norms / adds / GELU / transposes, 6 streamed KL, 7 d_acts and d_input products, 8 dU

@@ -102,6 +102,12 @@ _SIGNATURES = {
                                [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
                                [_c_p] * 4 + [_c_u32, _c_u32, _c_i32, _c_p, _c_i32] + _IMP_ARGS + [_c_f32, _c_i32] +
                                [_c_p] * 5 + [_c_sz, _c_p, _c_p, _c_p, _c_i32, _c_p]),
+    "pd_lm_stack_sources_workspace_size": (_c_sz, [_c_i64, _c_i64] + [_c_i32] * 4 +
+                                           [_c_i64, _c_i32, _c_p, _c_i32, _c_i32, _c_i64]),
+    "pd_lm_stack_step_sources": (_c_i32,
+                                 [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +
+                                 [_c_p] * 4 + [_c_p, _c_i32, _c_p, _c_i32, _c_i64] + _IMP_ARGS +
+                                 [_c_f32, _c_i32, _c_i32, _c_i32] + [_c_p] * 7 + [_c_sz, _c_p]),
     "pd_ci_mlp_workspace_size": (_c_sz, [_c_i32, _c_p, _c_i64]),
     "pd_ci_mlp_fwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 5 + [_c_sz, _c_p]),
     "pd_ci_mlp_bwd": (_c_i32, [_c_i32, _c_p, _c_i64] + [_c_p] * 7 + [_c_sz, _c_p]),

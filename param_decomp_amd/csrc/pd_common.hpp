@@ -197,6 +197,38 @@ __device__ inline float draw_uniform(uint32_t k0, uint32_t k1, int64_t i, int64_
   return bits_to_uniform(draw_bits(k0, k1, i, n, draw_dtype == PD_DTYPE_BF16 ? 8 : 32, layout), draw_dtype);
 }
 
+// ---------------------------------------------------------------- mask sources
+// Mask-source variants of the mask kernels beside the two Threefry counter layouts
+// (PD_LAYOUT_*): MASK_CONST, every source value one constant (the reference's
+// ConstantSources; 0 is the CI-masked reconstruction); MASK_SRC, persistent (adversarial)
+// source tables, each row covering rps consecutive tokens (pd/core/masking.py:43-68,
+// 260-272). Neither draws nor keeps u bytes.
+static constexpr int MASK_CONST = 2;
+static constexpr int MASK_SRC = 3;
+
+// Source value i of a table stored as src_dtype (F32, BF16, or U16 = u / 65535), cast to
+// bf16 as the reference casts the table to the CI dtype before use.
+__device__ inline float src_value(const void* src, int dtype, int64_t i) {
+  float v;
+  if (dtype == PD_DTYPE_F32) v = ((const float*)src)[i];
+  else if (dtype == PD_DTYPE_BF16) v = bf16_to_f32(((const bf16_t*)src)[i]);
+  else v = (float)((const uint16_t*)src)[i] * (1.f / 65535.f);
+  return bf16_to_f32(f32_to_bf16(v));
+}
+
+// delta[site * T + t] = bf16(src_delta[site * S + t / rps]) over n_sites sites: each
+// token's delta is its source row's value, cast to the CI dtype as the reference casts the
+// delta table.
+static __global__ __launch_bounds__(256) void k_src_delta_fill(const void* __restrict__ src_delta, int dtype,
+                                                               int64_t S, int64_t rps, int64_t T, int n_sites,
+                                                               float* __restrict__ delta) {
+  const int64_t n = (int64_t)n_sites * T;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t site = i / T, t = i % T;
+    delta[i] = src_value(src_delta, dtype, site * S + t / rps);
+  }
+}
+
 // ---------------------------------------------------------------- squashing
 // lower: forward clip(x,0,1); VJP leaks 0.01*g below zero only for g<0.
 __device__ inline float lower_fwd(float x) { return fminf(fmaxf(x, 0.f), 1.f); }

@@ -197,6 +197,17 @@ struct LMMaskArgs {
   float g2, psis;
   float* colpart;
   const float* slope;
+  // persistent source tables (MASK_SRC): src [S, C] of this (layer, kind), S = N / rps; the
+  // backward writes the table's gradient dm (1 - lower) as per-(64-token tile, source row)
+  // column sums colsrc (rps > 1; tiles and rows both run in token order, so tile + row is
+  // unique) or straight into dsrc [N, C] (rps = 1), and each token's per-tile sums of dm
+  // into rowdm [N, tiles of C] (for the delta table's gradient)
+  const void* src = nullptr;
+  int src_dtype = PD_DTYPE_F32;
+  int64_t rps = 1;
+  float* colsrc = nullptr;
+  float* dsrc = nullptr;
+  float* rowdm = nullptr;
 };
 
 #define PD_LM_ROW(pass) ((threadIdx.x >> 4) + 16 * (pass))
@@ -205,7 +216,8 @@ struct LMMaskArgs {
 // m = lower(ci) + (1 - lower(ci)) u (u drawn in bf16 over [N, C], counter n*C + c);
 // acts = bf16(xV * (m - d)) into acts[n * ld + c] and acts^T [C, N] (0 on unrouted tokens,
 // whose output is the target's x @ W^T, pd/core/decomposed_linear.py:72-85); u kept as its
-// 7-bit integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0.
+// 7-bit integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0. LAYOUT ==
+// MASK_SRC reads u from the source table instead (u = bf16(src[n / rps, c])), no u bytes.
 template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
                                                      bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
@@ -239,12 +251,17 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
         const float lo = lower_fwd(pre[e]);
         if constexpr (PM == PM_SL0) SLv.ps[r][q4 + e] = sl0_psi(upper_fwd(pre[e]), a.g2, a.psis);
         else imp += powp<PM>(upper_fwd(pre[e]), a.p);
-        const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
-        ub |= kb << (8 * e);
-        const float u = (float)kb * (1.f / 128.f);
+        float u;
+        if constexpr (LAYOUT == MASK_SRC) {
+          u = src_value(a.src, a.src_dtype, (n / a.rps) * a.C + q0 + q4 + e);
+        } else {
+          const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
+          ub |= kb << (8 * e);
+          u = (float)kb * (1.f / 128.f);
+        }
         o[e] = routed ? f32_to_bf16(hv[e] * (lo + (1.f - lo) * u - dt)) : (bf16_t)0;
       }
-      *(uint32_t*)(ubits + idx) = ub;
+      if constexpr (LAYOUT != MASK_SRC) *(uint32_t*)(ubits + idx) = ub;
       *(uint2*)(acts + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
     } else if constexpr (PM == PM_SL0) {
 #pragma unroll
@@ -268,28 +285,36 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
 // d_xV = bf16(d_acts * (m - d)) into d_xV[n * ld + c] and d_xV^T [C, N]; the CI pullback
 // d_pre = lower_vjp(pre, d_acts * xV * (1 - u)) + upper_vjp(pre, imp_scale * d upper^p).
 // An unrouted token's masked product does not reach the output: d_acts counts as 0 there.
-template <int PM>
+// SRC: u is read back from the source table, whose gradient dm (1 - lower) (dm = d_acts xV)
+// goes to dsrc (rps = 1) or the tile's column sums per source row (colsrc), and each
+// token's row sum of dm over the tile to rowdm.
+template <int PM, bool SRC>
 __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
                                                      const uint8_t* __restrict__ ubits, float imp_scale,
                                                      const bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_xV,
                                                      bf16_t* __restrict__ d_xVT, bf16_t* __restrict__ d_pre) {
   __shared__ TTile Tt;
+  __shared__ typename std::conditional<SRC, Sl0Tile, NoSl0Tile>::type SG;
   const int tid = threadIdx.x;
   const int64_t n0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_LM_COL;
   const bool qok = q0 + q4 < a.C;
+  if constexpr (SRC) {
+    if (tid < 64) SG.grp[tid] = n0 + tid < a.N ? (int)((n0 + tid) / a.rps) : -1;  // each row's source row
+  }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int r = PD_LM_ROW(pass);
     const int64_t n = n0 + r;
     bf16_t o[4] = {0, 0, 0, 0};
+    float dmsum = 0.f;
     if (n < a.N && qok) {
       const int64_t idx = n * a.C + q0 + q4;
       const float dt = a.delta ? a.delta[n] : 0.f;
       const uint2 pw = *(const uint2*)(a.ci_pre + idx);
       const uint2 hw = *(const uint2*)(xV + idx);
       const uint2 dw = (!a.route || a.route[n]) ? *(const uint2*)(d_acts + idx) : make_uint2(0u, 0u);
-      const uint32_t ub = *(const uint32_t*)(ubits + idx);
+      const uint32_t ub = SRC ? 0u : *(const uint32_t*)(ubits + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
@@ -305,22 +330,94 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-        const float u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
+        const float u = SRC ? src_value(a.src, a.src_dtype, (n / a.rps) * a.C + q0 + q4 + e)
+                            : (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
         const float m = lo + (1.f - lo) * u - dt;
         float dimp;
         if constexpr (PM == PM_SL0) dimp = slope4[e] * sl0_dpsi(up, a.g2, a.psis);
         else dimp = imp_scale * dpowp<PM>(up, a.p);
-        dp[e] = f32_to_bf16(lower_vjp(pre[e], da[e] * hv[e] * (1.f - u)) + upper_vjp(pre[e], dimp));
+        const float dm = da[e] * hv[e];
+        dp[e] = f32_to_bf16(lower_vjp(pre[e], dm * (1.f - u)) + upper_vjp(pre[e], dimp));
         o[e] = f32_to_bf16(da[e] * m);
+        if constexpr (SRC) {
+          dmsum += dm;
+          const float gs = dm * (1.f - lo);
+          if (a.rps == 1) a.dsrc[idx + e] = gs;
+          else SG.ps[r][q4 + e] = gs;
+        }
       }
       *(uint2*)(d_pre + idx) = make_uint2(bf_pack(dp[0], dp[1]), bf_pack(dp[2], dp[3]));
       *(uint2*)(d_xV + n * a.ld + q0 + q4) = make_uint2(bf_pack(o[0], o[1]), bf_pack(o[2], o[3]));
+    } else if constexpr (SRC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) SG.ps[r][q4 + e] = 0.f;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
+    if constexpr (SRC) {  // the 16 lanes of a row add their columns in a fixed tree (all lanes)
+      dmsum += __shfl_xor(dmsum, 1, 64);
+      dmsum += __shfl_xor(dmsum, 2, 64);
+      dmsum += __shfl_xor(dmsum, 4, 64);
+      dmsum += __shfl_xor(dmsum, 8, 64);
+      if (n < a.N && (tid & 15) == 0 && a.rowdm) a.rowdm[n * gridDim.x + blockIdx.x] = dmsum;
+    }
   }
   __syncthreads();
   ttile_store(Tt, d_xVT, a.N, n0, a.N, q0, a.C, tid);
+  if constexpr (SRC) {
+    if (a.rps > 1) sl0_tile_colsums(SG, blockIdx.y, q0, a.C, a.colsrc, tid);
+  }
+}
+
+// The source table's gradient from the tiles' column sums (rps > 1): d_src[g C + q] = the
+// sum over the 64-token tiles covering source row g (tokens [g rps, (g + 1) rps)) of
+// colsrc[(tile + g) C + q], tiles in order.
+__global__ __launch_bounds__(256) void k_lm_src_finalize(const float* __restrict__ colsrc, int64_t N, int64_t rps,
+                                                         int64_t S, int C, float* __restrict__ dsrc) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= S * C) return;
+  const int64_t g = i / C, q = i % C;
+  const int64_t lo = g * rps, hi = lo + rps < N ? lo + rps : N;
+  float F = 0.f;
+  for (int64_t t = lo / TILE; t <= (hi - 1) / TILE; ++t) F += colsrc[(t + g) * C + q];
+  dsrc[i] = F;
+}
+
+// The delta cotangent of each token: qtok[n] = sum_o g[n, o] frozen[n, o] - sum_b
+// rowdm[n, b] (d enters as acts = xV (m - d) and as + d x @ W^T). One wave per token,
+// lanes striding o, then a fixed-order wave sum.
+__global__ __launch_bounds__(256) void k_lm_delta_cot(const bf16_t* __restrict__ g, const bf16_t* __restrict__ frozen,
+                                                      int64_t N, int dout, const float* __restrict__ rowdm, int nb,
+                                                      float* __restrict__ qtok) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + wave_id();
+  if (n >= N) return;
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int o = lane; o < dout; o += 64)
+    acc = fmaf(bf16_to_f32(g[n * dout + o]), bf16_to_f32(frozen[n * dout + o]), acc);
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    float dm = 0.f;
+    for (int b = 0; b < nb; ++b) dm += rowdm[n * nb + b];
+    qtok[n] = acc - dm;
+  }
+}
+
+// The delta table's gradient: dsd[gi] = the sum of qtok over the tokens of source row gi.
+// One block per row: each thread adds a strided share in order, then a fixed tree.
+__global__ __launch_bounds__(256) void k_lm_src_delta_sum(const float* __restrict__ qtok, int64_t N, int64_t rps,
+                                                          float* __restrict__ dsd) {
+  __shared__ float red[256];
+  const int64_t lo = (int64_t)blockIdx.x * rps, hi = lo + rps < N ? lo + rps : N;
+  float acc = 0.f;
+  for (int64_t n = lo + threadIdx.x; n < hi; n += 256) acc += qtok[n];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dsd[blockIdx.x] = red[0];
 }
 
 // ---------------------------------------------------------------- attention (hd = 64)
@@ -638,6 +735,8 @@ struct LMDims {
   int C[LM_NK], din[LM_NK], dout[LM_NK];
   bool use_delta;
   bool routed = false;  // per-token routes: the target segment is needed without a delta too
+  int64_t S = 0, rps = 0;  // persistent source tables: S rows of rps tokens (rps = 0: none)
+  bool srcs() const { return rps > 0; }
   int64_t BH() const { return B * H; }
   // the site products run over [acts | s x] . [U ; W^T] (s = d on routed rows, 1 on the rest)
   bool cat() const { return use_delta || routed; }
@@ -661,6 +760,7 @@ struct Arena {
 struct LMSiteSave {
   bf16_t *xV, *acat, *actsT;
   uint8_t* ub;
+  bf16_t* frozen;  // source tables with the delta channel: the site's x @ W^T [N, d_out]
   // smooth-L0: tile column sums of psi, per-component slopes, loss partials (act, freq,
   // the EMA estimator's batch penalty), and the site's offset in the EMA estimate
   float *sl0_col, *sl0_slope, *sl0_act, *sl0_freq, *sl0_fb;
@@ -687,6 +787,7 @@ struct LMPlan {
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
   float *sl0_act, *sl0_freq, *sl0_fb;  // every site's smooth-L0 loss partials, contiguous
   size_t sl0_blocks_total;
+  float *colsrc, *rowdm, *qtok;  // source tables: tile column sums, token row sums, delta cotangents
 };
 
 static size_t site_imp_blocks(const LMDims& D, int k) { return (size_t)cdiv(D.C[k], TILE) * cdiv(D.N, TILE); }
@@ -723,6 +824,7 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
       S.site[k].acat = A.take<bf16_t>(N * D.kcat(k));
       S.site[k].actsT = A.take<bf16_t>(N * D.C[k]);
       S.site[k].ub = A.take<uint8_t>(N * D.C[k]);
+      S.site[k].frozen = D.srcs() && D.use_delta ? A.take<bf16_t>(N * D.dout[k]) : nullptr;
     }
   }
   for (int k = 0; k < LM_NK; ++k) {
@@ -817,9 +919,24 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
     P.sk_ws_bytes = std::max({P.sk_ws_bytes, gemm_splitk_ws_bytes(D.C[k], D.dout[k], N),
                               gemm_splitk_ws_bytes(D.din[k], D.C[k], N)});
   P.sk_ws = A.take<char>(P.sk_ws_bytes);
+  P.colsrc = D.srcs() && D.rps > 1 ? A.take<float>((size_t)(cdiv(N, TILE) + D.S) * maxC) : nullptr;
+  P.rowdm = D.srcs() && D.use_delta ? A.take<float>((size_t)N * cdiv(maxC, TILE)) : nullptr;
+  P.qtok = D.srcs() && D.use_delta ? A.take<float>(N) : nullptr;
   P.total = A.off;
   return P;
 }
+
+// Persistent source tables of a pd_lm_stack_step_sources call.
+struct LMSources {
+  const void* const* src;  // [6] kinds: [L, S, C_k]
+  int src_dtype;
+  const void* delta;       // [L, 6, S] or NULL (no delta channel)
+  int delta_dtype;
+  int64_t rps;
+  float* const* d_src;     // [6] kinds: [L, S, C_k] fp32
+  float* d_src_delta;      // [L, 6, S] fp32
+  bool want_wgrads, reuse_clean;
+};
 
 struct LMRecorder {
   void** ev;
@@ -896,8 +1013,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                         const uint8_t* routes, int layout, const ImpSpec& imp, float recon_coeff, int n_chunks,
                         float* losses, float* const* dV,
                         float* const* dU, void* const* d_ci_pre, void* workspace, size_t workspace_bytes, void* stream,
-                        LMRecorder& rec) {
-  const char* what = "pd_lm_stack_step";
+                        LMRecorder& rec, const LMSources* srcs = nullptr) {
+  const char* what = srcs ? "pd_lm_stack_step_sources" : "pd_lm_stack_step";
+  const bool want_wgrads = !srcs || srcs->want_wgrads;
   if (int e = check_imp_spec(imp, what)) return e;
   if (B <= 0 || T <= 0 || d <= 0 || H <= 0 || KV <= 0 || f <= 0 || V <= 0 || L <= 0 || n_chunks <= 0 || !Cs)
     return fail(PD_EINVAL, std::string(what) + ": bad dims");
@@ -908,15 +1026,31 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                                                      "vocab % n_chunks == 0");
   for (int k = 0; k < LM_NK; ++k)
     if (Cs[k] <= 0 || Cs[k] % 8) return fail(PD_EUNSUPPORTED, std::string(what) + ": every C must be a positive multiple of 8");
-  if (!tokens || !wte || !ln1 || !ln2 || !norm || !W || !Vf || !Uf || !ci_pre || !losses || !dV || !dU || !d_ci_pre)
+  if (!tokens || !wte || !ln1 || !ln2 || !norm || !W || !Vf || !Uf || !ci_pre || !losses || !d_ci_pre ||
+      (want_wgrads && (!dV || !dU)))
     return fail(PD_EINVAL, std::string(what) + ": null pointer");
   for (int k = 0; k < LM_NK; ++k)
-    if (!W[k] || !Vf[k] || !Uf[k] || !ci_pre[k] || !dV[k] || !dU[k] || !d_ci_pre[k])
+    if (!W[k] || !Vf[k] || !Uf[k] || !ci_pre[k] || !d_ci_pre[k] || (want_wgrads && (!dV[k] || !dU[k])))
       return fail(PD_EINVAL, std::string(what) + ": null per-kind pointer");
+  if (srcs) {
+    if (routes) return fail(PD_EINVAL, std::string(what) + ": no per-token routes with source tables");
+    if (!srcs->src || !srcs->d_src || srcs->rps <= 0 || (B * T) % srcs->rps || (srcs->delta && !srcs->d_src_delta))
+      return fail(PD_EINVAL, std::string(what) + ": source tables, rows_per_source | B*T and outputs required");
+    for (int k = 0; k < LM_NK; ++k)
+      if (!srcs->src[k] || !srcs->d_src[k]) return fail(PD_EINVAL, std::string(what) + ": null source table");
+    for (int dt : {srcs->src_dtype, srcs->delta ? srcs->delta_dtype : PD_DTYPE_F32})
+      if (dt != PD_DTYPE_F32 && dt != PD_DTYPE_BF16 && dt != PD_DTYPE_U16)
+        return fail(PD_EINVAL, std::string(what) + ": source dtype");
+    use_delta = srcs->delta ? 1 : 0;
+  }
   if (layout != PD_LAYOUT_PARTITIONABLE && layout != PD_LAYOUT_ORIGINAL)
     return fail(PD_EINVAL, std::string(what) + ": unknown counter layout");
   LMDims D{B, T, B * T, V, d, H, KV, f, L, n_chunks, {}, {}, {}, use_delta != 0};
   D.routed = routes != nullptr;
+  if (srcs) {
+    D.rps = srcs->rps;
+    D.S = D.N / srcs->rps;
+  }
   const int qd = H * LM_HD, kvd = KV * LM_HD;
   {
     const int din[LM_NK] = {d, d, d, qd, d, f}, dout[LM_NK] = {qd, kvd, kvd, d, f, d};
@@ -979,7 +1113,10 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
       if (D.cat()) transpose(Wl, dout, di, bb + C, kc2, s);  // W^T
     }
   }
-  if (D.use_delta)
+  if (srcs && D.use_delta)  // each token's delta is its source row's
+    hipLaunchKernelGGL(k_src_delta_fill, dim3((unsigned)std::min<int64_t>(cdiv((int64_t)LM_NK * L * N, 256), 4096)),
+                       dim3(256), 0, s, srcs->delta, srcs->delta_dtype, D.S, D.rps, N, LM_NK * L, P.delta);
+  else if (D.use_delta)
     hipLaunchKernelGGL(k_lm_deltas, dim3((unsigned)cdiv(N, 256), (unsigned)(LM_NK * L)), dim3(256), 0, s, halves[2],
                        halves[3], N, layout, P.delta);
   if ((rc = check_launch("pd_lm_stack_step prep"))) return rc;
@@ -1006,9 +1143,11 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   // ================= clean forward (frozen target): act_c. It is independent of the masked
   // forward until the KL reads act_c, so it runs on a helper stream beside the per-step
   // weight copies and the masked forward, with attention buffers of its own.
+  // With reuse_clean (source tables) act_c is the one the previous call left in the workspace.
   rec.mark(LM_CAT_CLEAN);
-  hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, sc, tokens, (const bf16_t*)wte, N, d, V, P.rc_a);
-  {
+  const bool clean = !(srcs && srcs->reuse_clean);
+  if (clean) hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, sc, tokens, (const bf16_t*)wte, N, d, V, P.rc_a);
+  if (clean) {
     bf16_t* rcur = P.rc_a;
     bf16_t* rnext = P.rc_b;
     for (int l = 0; l < L; ++l) {
@@ -1033,7 +1172,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     }
     hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, sc, rcur, N, d, norm, eps, P.act_c, (float*)nullptr);
   }
-  hipEventRecord(ax.ev[1], sc);  // act_c is ready
+  if (clean) hipEventRecord(ax.ev[1], sc);  // act_c is ready
   if ((rc = check_launch("pd_lm_stack_step clean"))) return rc;
 
   // ================= masked forward
@@ -1051,6 +1190,15 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     ma.psis = imp.psi_scale();
     ma.colpart = P.layers[l].site[k].sl0_col;
     ma.slope = P.layers[l].site[k].sl0_slope;
+    if (srcs) {
+      const size_t es = srcs->src_dtype == PD_DTYPE_F32 ? 4 : 2;
+      ma.src = (const char*)srcs->src[k] + (size_t)l * D.S * D.C[k] * es;
+      ma.src_dtype = srcs->src_dtype;
+      ma.rps = D.rps;
+      ma.colsrc = P.colsrc;
+      ma.dsrc = srcs->d_src[k] + (size_t)l * D.S * D.C[k];
+      ma.rowdm = P.rowdm;
+    }
     return ma;
   };
   // site forward: x [N, d_in] (and the site's saves) -> out [N, d_out]
@@ -1072,7 +1220,12 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     }();
 #define PD_LMF(LY, PMV) \
   hipLaunchKernelGGL((k_lm_mask_fwd<LY, PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.acat, S.actsT, S.ub, part)
-    if (layout == PD_LAYOUT_PARTITIONABLE) {
+    if (srcs) {
+      if (pm == PM_SL0) PD_LMF(MASK_SRC, PM_SL0);
+      else if (pm == 2) PD_LMF(MASK_SRC, 2);
+      else if (pm == 1) PD_LMF(MASK_SRC, 1);
+      else PD_LMF(MASK_SRC, 0);
+    } else if (layout == PD_LAYOUT_PARTITIONABLE) {
       if (pm == PM_SL0) PD_LMF(PD_LAYOUT_PARTITIONABLE, PM_SL0);
       else if (pm == 2) PD_LMF(PD_LAYOUT_PARTITIONABLE, 2);
       else if (pm == 1) PD_LMF(PD_LAYOUT_PARTITIONABLE, 1);
@@ -1090,6 +1243,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                          imp.ref_count, imp.ema.at((int64_t)S.ema_off), S.sl0_slope, S.sl0_act, S.sl0_freq,
                          imp.ema.on() ? S.sl0_fb : nullptr);
     rec.mark(LM_CAT_GEMM_FWD);
+    if (S.frozen &&  // the target output the delta table's gradient reads
+        (r = gemm_nt(N, dout, di, x, di, bfp(W[k], (size_t)l * dout * di), di, S.frozen, dout, PD_DTYPE_BF16, 0.f, s)))
+      return r;
     return gemm_nt(N, dout, kc, S.acat, kc, P.BtF[k] + (size_t)l * dout * kc, kc, out, dout, PD_DTYPE_BF16, 0.f, s);
   };
 
@@ -1125,7 +1281,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 
   // ================= streamed KL (clean || masked) over the tied head, and its cotangent
   rec.mark(LM_CAT_WAIT);
-  hipStreamWaitEvent(s, ax.ev[1], 0);  // the clean pass's act_c
+  if (clean) hipStreamWaitEvent(s, ax.ev[1], 0);  // the clean pass's act_c
   rec.mark(LM_CAT_KL);
   if ((rc = pd_streamed_kl_fwd(PD_DTYPE_BF16, N, d, V, n_chunks, P.act_m, wte, P.act_c, wte, P.pos_kl, P.stats,
                                P.kl_ws, P.kl_ws_bytes, s)))
@@ -1179,32 +1335,52 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     rec.mark(LM_CAT_WAIT);
     wg_join(wb);
     rec.mark(LM_CAT_ELEM);
-    transpose(g, N, dout, drT, N, s);  // g^T [d_out, N]
+    if (want_wgrads) transpose(g, N, dout, drT, N, s);  // g^T [d_out, N]
     if (D.cat() && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s, ma.route);
     rec.mark(LM_CAT_GEMM_DX);
     int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
     rec.mark(LM_CAT_MASK_BWD);
     bf16_t* dpre = (bf16_t*)d_ci_pre[k] + (size_t)l * N * C;
-#define PD_LMB(PMV)                                                                                          \
-  hipLaunchKernelGGL((k_lm_mask_bwd<PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
+#define PD_LMB(PMV, SRC)                                                                                          \
+  hipLaunchKernelGGL((k_lm_mask_bwd<PMV, SRC>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
                      P.dcat, dxVT, dpre)
-    if (pm == PM_SL0) PD_LMB(PM_SL0);
-    else if (pm == 2) PD_LMB(2);
-    else if (pm == 1) PD_LMB(1);
-    else PD_LMB(0);
+    if (srcs) {
+      if (pm == PM_SL0) PD_LMB(PM_SL0, true);
+      else if (pm == 2) PD_LMB(2, true);
+      else if (pm == 1) PD_LMB(1, true);
+      else PD_LMB(0, true);
+      // the table's gradient (rows of several tokens: from the tiles' column sums), and the
+      // delta table's from each token's delta cotangent
+      if (D.rps > 1)
+        hipLaunchKernelGGL(k_lm_src_finalize, dim3((unsigned)cdiv(D.S * C, 256)), dim3(256), 0, s, P.colsrc, N, D.rps,
+                           D.S, (int)C, ma.dsrc);
+      if (D.use_delta) {
+        hipLaunchKernelGGL(k_lm_delta_cot, rows4(N), dim3(256), 0, s, g, S.frozen, N, (int)dout, P.rowdm,
+                           (int)cdiv(C, TILE), P.qtok);
+        hipLaunchKernelGGL(k_lm_src_delta_sum, dim3((unsigned)D.S), dim3(256), 0, s, P.qtok, N, D.rps,
+                           srcs->d_src_delta + ((size_t)l * LM_NK + k) * D.S);
+      }
+    } else {
+      if (pm == PM_SL0) PD_LMB(PM_SL0, false);
+      else if (pm == 2) PD_LMB(2, false);
+      else if (pm == 1) PD_LMB(1, false);
+      else PD_LMB(0, false);
+    }
 #undef PD_LMB
-    rec.mark(LM_CAT_GEMM_DW);
-    hipEventRecord(ax.ev[2], s);  // g^T and d(xV)^T of this call are written
-    hipStreamWaitEvent(ax.st, ax.ev[2], 0);
-    if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
-                            P.sk_ws, P.sk_ws_bytes, ax.st)))
-      return r;
-    if ((r = gemm_nt_splitk(di, C, N, xT, N, dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
-                            P.sk_ws_bytes, ax.st)))
-      return r;
-    hipEventRecord(ax.ev[3 + wb], ax.st);
-    wg_pend[wb] = true;
+    if (want_wgrads) {
+      rec.mark(LM_CAT_GEMM_DW);
+      hipEventRecord(ax.ev[2], s);  // g^T and d(xV)^T of this call are written
+      hipStreamWaitEvent(ax.st, ax.ev[2], 0);
+      if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
+                              P.sk_ws, P.sk_ws_bytes, ax.st)))
+        return r;
+      if ((r = gemm_nt_splitk(di, C, N, xT, N, dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
+                              P.sk_ws_bytes, ax.st)))
+        return r;
+      hipEventRecord(ax.ev[3 + wb], ax.st);
+      wg_pend[wb] = true;
+    }
     if (!din_out) return PD_OK;
     rec.mark(LM_CAT_GEMM_DX);
     return gemm_nt(N, di, kc2, P.dcat, kc2, P.BtB[k] + (size_t)l * di * kc2, kc2, din_out, di,
@@ -1307,6 +1483,48 @@ int pd_lm_stack_step_timed(int64_t B, int64_t T, int d, int n_head, int n_kv_hea
                         losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec);
   if (n_recorded) *n_recorded = rec.n;
   return rc;
+}
+
+size_t pd_lm_stack_sources_workspace_size(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp,
+                                          int64_t vocab, int L, const int32_t* C, int use_delta, int n_kl_chunks,
+                                          int64_t rows_per_source) {
+  if (B <= 0 || T <= 0 || d <= 0 || n_head <= 0 || n_kv_head <= 0 || d_mlp <= 0 || vocab <= 0 || L <= 0 || !C ||
+      n_kl_chunks <= 0 || rows_per_source <= 0 || (B * T) % rows_per_source)
+    return 0;
+  LMDims D{B, T, B * T, vocab, d, n_head, n_kv_head, d_mlp, L, n_kl_chunks, {}, {}, {}, use_delta != 0};
+  D.rps = rows_per_source;
+  D.S = B * T / rows_per_source;
+  const int qd = n_head * LM_HD, kvd = n_kv_head * LM_HD;
+  const int din[LM_NK] = {d, d, d, qd, d, d_mlp}, dout[LM_NK] = {qd, kvd, kvd, d, d_mlp, d};
+  for (int k = 0; k < LM_NK; ++k) {
+    D.C[k] = C[k];
+    D.din[k] = din[k];
+    D.dout[k] = dout[k];
+  }
+  return lm_plan(D, nullptr, true).total;
+}
+
+int pd_lm_stack_step_sources(int64_t B, int64_t T, int d, int n_head, int n_kv_head, int d_mlp, int64_t vocab, int L,
+                             const int32_t* C, const int32_t* tokens, const void* wte, const float* ln1,
+                             const float* ln2, const float* norm, float eps, float rope_base, const void* const* W,
+                             const void* const* V, const void* const* U, const void* const* ci_pre,
+                             const void* const* src, int src_dtype, const void* src_delta, int delta_dtype,
+                             int64_t rows_per_source, int imp_kind, float p, float gamma, int normalize_at_one,
+                             float imp_coeff, float freq_coeff, float ref_count, const float* freq_ema_in,
+                             float* freq_ema_out, float ema_count, float ema_halflife, float recon_coeff,
+                             int n_kl_chunks, int want_weight_grads, int reuse_clean, float* losses, float* const* dV,
+                             float* const* dU, void* const* d_ci_pre, float* const* d_src, float* d_src_delta,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  LMRecorder rec{nullptr, nullptr, 0, 0, nullptr};
+  ImpSpec imp;
+  if (int e = make_imp_spec("pd_lm_stack_step_sources", imp_kind, p, gamma, normalize_at_one, imp_coeff, freq_coeff,
+                            ref_count, freq_ema_in, freq_ema_out, ema_count, ema_halflife, imp))
+    return e;
+  const LMSources srcs{src, src_dtype, src_delta, delta_dtype, rows_per_source, d_src, d_src_delta,
+                       want_weight_grads != 0, reuse_clean != 0};
+  return lm_step_impl(B, T, d, n_head, n_kv_head, d_mlp, vocab, L, C, tokens, wte, ln1, ln2, norm, eps, rope_base, W,
+                      V, U, ci_pre, 0u, 0u, src_delta ? 1 : 0, nullptr, PD_LAYOUT_PARTITIONABLE, imp, recon_coeff,
+                      n_kl_chunks, losses, dV, dU, d_ci_pre, workspace, workspace_bytes, stream, rec, &srcs);
 }
 
 }  // extern "C"

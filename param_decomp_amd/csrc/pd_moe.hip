@@ -272,23 +272,9 @@ struct SiteMaskArgs {
   float* rowdm;
 };
 
-// Mask-source variant of the mask kernels beside the two Threefry layouts: every source
-// value is the constant SiteMaskArgs::uconst (the reference's ConstantSources; 0 is the
-// CI-masked reconstruction), nothing is drawn and no u bytes are kept.
-static constexpr int MASK_CONST = 2;
-// Persistent (adversarial) source tables: a selected value reads its expert's row of the
-// table, u = src[(t / rps) E c + e c + q] (the reference's SourceMaskIngredients,
-// pd/core/masking.py:43-68), cast to bf16 as the reference casts the table to the CI
-// dtype before the select; no u bytes are kept.
-static constexpr int MASK_SRC = 3;
-
-__device__ inline float src_value(const void* src, int dtype, int64_t i) {
-  float v;
-  if (dtype == PD_DTYPE_F32) v = ((const float*)src)[i];
-  else if (dtype == PD_DTYPE_BF16) v = bf16_to_f32(((const bf16_t*)src)[i]);
-  else v = (float)((const uint16_t*)src)[i] * (1.f / 65535.f);
-  return bf16_to_f32(f32_to_bf16(v));
-}
+// (MASK_CONST: every source value is SiteMaskArgs::uconst. MASK_SRC: a selected value
+// reads its expert's row of the table, u = src[(t / rps) E c + e c + q], the reference's
+// SourceMaskIngredients, pd/core/masking.py:43-68.)
 
 // The table index of job j's element (q): source row of its token, its expert.
 __device__ inline int64_t src_index(const SiteMaskArgs& a, int32_t slot, int e, int q) {
@@ -1038,17 +1024,6 @@ __global__ __launch_bounds__(256) void k_delta_sites(uint32_t b0, uint32_t b1, i
 }
 
 // ---------------------------------------------------------------- persistent sources
-// delta[(l*3 + s)*T + t] = bf16(src_delta[(l*3 + s)*S + t / rps]): each token's delta is
-// its source row's value, cast to the CI dtype as the reference casts the delta table.
-__global__ __launch_bounds__(256) void k_src_delta_fill(const void* __restrict__ src_delta, int dtype, int64_t S,
-                                                        int64_t rps, int64_t T, int n_sites,
-                                                        float* __restrict__ delta) {
-  const int64_t n = (int64_t)n_sites * T;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t site = i / T, t = i % T;
-    delta[i] = src_value(src_delta, dtype, site * S + t / rps);
-  }
-}
 
 // goff[g] for g = e * S + row: the first job of expert e whose token lies in source row
 // `row` or later (jobs of an expert are in token order), goff[E * S] = J.

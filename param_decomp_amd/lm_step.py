@@ -51,8 +51,10 @@ class LMStackStep:
                  C: dict, *, device="cuda", p: float = 2.0, imp_coeff: float = 1.0, recon_coeff: float = 1.0,
                  layout: int = L.LAYOUT_PARTITIONABLE, use_delta: bool = True, n_kl_chunks: int = 1,
                  eps: float = 1e-6, rope_base: float = 10000.0, imp_min: ImpMin | None = None,
-                 routed: bool = False):
-        """routed: the step takes per-token site routes (`step(..., routes=...)`)."""
+                 routed: bool = False, rows_per_source: int | None = None):
+        """routed: the step takes per-token site routes (`step(..., routes=...)`).
+        rows_per_source: tokens per row of persistent source tables (`step_sources`; B*T is
+        the `c` shape, T a sample's positions `bc`, 1 `bsc`)."""
         if d != n_head * HEAD_DIM:
             raise L.PDError(f"LMStackStep: head_dim must be {HEAD_DIM} (d = {HEAD_DIM} * n_head)")
         self.dims = (B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers)
@@ -76,8 +78,20 @@ class LMStackStep:
             self.dU[k] = torch.empty(n_layers, self.C[k], dout, **f32)
             self.d_ci_pre[k] = torch.empty(n_layers, N, self.C[k], dtype=torch.bfloat16, device=dev)
         self._cs = L.host_array(ctypes.c_int32, [self.C[k] for k in KINDS])
-        nbytes = L.load().pd_lm_stack_workspace_size(B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers, self._cs,
-                                                     int(self.use_delta or self.routed), n_kl_chunks)
+        self.rows_per_source = rows_per_source
+        if rows_per_source is None:
+            nbytes = L.load().pd_lm_stack_workspace_size(B, T, d, n_head, n_kv_head, d_mlp, vocab, n_layers,
+                                                         self._cs, int(self.use_delta or self.routed), n_kl_chunks)
+        else:
+            if rows_per_source <= 0 or N % rows_per_source:
+                raise L.PDError("LMStackStep: rows_per_source must divide B*T")
+            S = N // rows_per_source
+            nbytes = L.load().pd_lm_stack_sources_workspace_size(B, T, d, n_head, n_kv_head, d_mlp, vocab,
+                                                                 n_layers, self._cs, int(self.use_delta),
+                                                                 n_kl_chunks, rows_per_source)
+            self.d_src = {k: torch.empty(n_layers, S, self.C[k], **f32) for k in KINDS}
+            self.d_src_delta = torch.empty(n_layers, len(KINDS), S, **f32)
+            self._dsrc = L.host_array(ctypes.c_void_p, [L.ptr(self.d_src[k]) for k in KINDS])
         if nbytes == 0:
             raise L.PDError("pd_lm_stack_workspace_size: bad dimensions")
         self.workspace = L.workspace(nbytes, dev)
@@ -116,6 +130,43 @@ class LMStackStep:
         every token routed); an unrouted token's site output is the target's."""
         L.call("pd_lm_stack_step", *self._args(tokens, w, ci_pre, draw_key, routes))
         self._advance()
+        return self
+
+    def step_sources(self, tokens: torch.Tensor, w: LMWeights, ci_pre: dict, src: dict,
+                     src_delta: torch.Tensor | None = None, *, want_weight_grads: bool = True,
+                     reuse_clean: bool = False):
+        """The step with persistent source tables in place of the draws: src kind -> [L, S,
+        C_k] (one storage dtype: float32, bfloat16 or uint16) and src_delta [L, 6, S] (None =
+        no delta channel; construct with use_delta=True to size for one). Fills `d_src`,
+        `d_src_delta` (and the model gradients when `want_weight_grads`). `reuse_clean` takes
+        the frozen forward's final activations from this object's workspace as the previous
+        call left them: only for repeated calls on the same tokens, wte and frozen weights
+        with no other step on this object between."""
+        if self.rows_per_source is None:
+            raise L.PDError("LMStackStep: construct with rows_per_source for source tables")
+        B, T, d, H, KV, f, V, Ln = self.dims
+        S = B * T // self.rows_per_source
+        dts = {src[k].dtype for k in KINDS}
+        if len(dts) != 1 or any(tuple(src[k].shape) != (Ln, S, self.C[k]) for k in KINDS):
+            raise L.PDError("step_sources: src[kind] [L, S, C_kind], one dtype")
+        if src_delta is not None and (tuple(src_delta.shape) != (Ln, len(KINDS), S) or not self.use_delta):
+            raise L.PDError("step_sources: src_delta [L, 6, S], on a step constructed with use_delta=True")
+        g = want_weight_grads
+        P = ctypes.c_void_p
+        Wa = L.host_array(P, [L.ptr(w.W[k]) for k in KINDS])
+        Va = L.host_array(P, [L.ptr(w.V[k]) for k in KINDS])
+        Ua = L.host_array(P, [L.ptr(w.U[k]) for k in KINDS])
+        Ca = L.host_array(P, [L.ptr(ci_pre[k]) for k in KINDS])
+        Sa = L.host_array(P, [L.ptr(src[k]) for k in KINDS])
+        L.call("pd_lm_stack_step_sources", B, T, d, H, KV, f, V, Ln, self._cs, L.ptr(tokens), L.ptr(w.wte),
+               L.ptr(w.ln1), L.ptr(w.ln2), L.ptr(w.norm), self.eps, self.rope_base, Wa, Va, Ua, Ca, Sa,
+               L.dtype_code(dts.pop()), None if src_delta is None else L.ptr(src_delta),
+               L.F32 if src_delta is None else L.dtype_code(src_delta.dtype), self.rows_per_source,
+               *self.imp_min.c_args(self.frequency if g else None), self.recon_coeff, self.n_kl_chunks, int(g),
+               int(reuse_clean), L.ptr(self.losses), self._dV if g else None, self._dU if g else None, self._dci,
+               self._dsrc, L.ptr(self.d_src_delta), L.ptr(self.workspace), self.workspace.numel(), L.stream())
+        if g:
+            self._advance()
         return self
 
     def _advance(self):
