@@ -264,3 +264,61 @@ class MoEPPGDStep:
         self._ascend(lr, final_key)
         s = self.step_fn
         return PPGDStepResult(loss=loss, dV=s.dV, dU=s.dU, d_ci=s.d_ci_pre, warmup_losses=warmup_losses)
+
+
+class LMPPGDStep:
+    """The persistent-PGD reconstruction step over every decomposed matrix of the LM stack
+    (`pd/core/train.py:693-811`, `pd/core/adversary.py:463-567`), on
+    `pd_lm_stack_step_sources`: `n_warmup` ascents of the adversary on the detached KL
+    reconstruction loss (only the source gradients are formed), then the final step, whose
+    backward gives the model and CI gradients and the source gradients of the final ascent.
+
+    `adversaries[kind].sources` is that kind's component-source leaf [L, S, C_kind] (every
+    row covering `step.rows_per_source` tokens of the [B*T] order), `delta_adversary.sources`
+    the delta leaf [L, 6, S]; each leaf folds its own `leaf_index` into the uint16 rounding
+    draws. A pooled adversary (one particle per sample drawn from a pool,
+    `pd/core/masking.py:221-257`) gathers its drawn particles into `bc` tables (rows of T
+    tokens) before the step and scatters the gradients back. Keys as
+    `DenseSitePPGDStep.step`."""
+
+    def __init__(self, step, adversaries: dict, delta_adversary: PersistentAdversary | None = None):
+        from param_decomp_amd.lm_step import KINDS
+
+        self.step_fn = step
+        self.kinds = KINDS
+        self.adv = {k: adversaries[k] for k in KINDS}
+        self.dadv = delta_adversary
+        if step.rows_per_source is None:
+            raise ValueError("the LM step must be constructed with rows_per_source")
+        counts = {a.n_warmup for a in self.adv.values()} | ({delta_adversary.n_warmup} if delta_adversary else set())
+        if len(counts) != 1:
+            raise ValueError("every source leaf of the step shares one warmup count")
+        self.n_warmup = counts.pop()
+
+    def _run(self, tokens, w, ci_pre, final: bool, reuse_clean: bool):
+        self.step_fn.step_sources(tokens, w, ci_pre, {k: a.sources for k, a in self.adv.items()},
+                                  None if self.dadv is None else self.dadv.sources, want_weight_grads=final,
+                                  reuse_clean=reuse_clean)
+        return self.step_fn.losses[0].clone()
+
+    def _ascend(self, lr, key):
+        for k, a in self.adv.items():
+            a.after_one_ascent(self.step_fn.d_src[k], lr, key)
+        if self.dadv is not None:
+            self.dadv.after_one_ascent(self.step_fn.d_src_delta, lr, key)
+
+    def step(self, tokens, w, ci_pre, lr: float, key, adv_index: int = 0) -> PPGDStepResult:
+        quantize_key = prng.fold_in(key, 0x51C)
+        warm_key = prng.fold_in(quantize_key, adv_index)
+        final_key = prng.fold_in(prng.fold_in(quantize_key, 0x51D), adv_index)
+        warmup_losses = []
+        n = self.n_warmup
+        # the frozen forward depends only on the tokens and the frozen weights: the first
+        # call of the step forms it, the later ones reuse it from the step's workspace
+        for i, ascent_key in enumerate(prng.split(warm_key, n) if n else []):
+            warmup_losses.append(self._run(tokens, w, ci_pre, final=False, reuse_clean=i > 0))
+            self._ascend(lr, ascent_key)
+        loss = self._run(tokens, w, ci_pre, final=True, reuse_clean=n > 0)
+        self._ascend(lr, final_key)
+        s = self.step_fn
+        return PPGDStepResult(loss=loss, dV=s.dV, dU=s.dU, d_ci=s.d_ci_pre, warmup_losses=warmup_losses)

@@ -92,3 +92,53 @@ def test_lm_sources_step_matches_oracle(device, dtype, rps_kind, with_delta):
     assert torch.equal(step.losses, first["losses"])
     for k in KINDS:
         assert torch.equal(step.dV[k], first["dV"][k]) and torch.equal(step.d_ci_pre[k], first["dci"][k]), k
+
+
+def test_lm_persistent_pgd_step(device):
+    """Warmup ascents then the final step (Adam on fp32 `bc` tables, with the delta leaf):
+    the sources move inside [0, 1], the recon term does not fall over the warmups (ascent),
+    and the final gradients equal those of the same procedure spelled out call by call."""
+    from param_decomp_amd.adversary import AdamPGDConfig, LMPPGDStep, PersistentAdversary
+    from param_decomp_amd.lm_step import LMStackStep
+    from param_decomp_amd.losses import ImpMin
+
+    B, T = 2, 64
+    cfg = lo.LMConfig(n_layers=2, d=128, n_head=2, n_kv_head=2, d_mlp=256, vocab=384,
+                      C={"q_proj": 32, "k_proj": 32, "v_proj": 32, "o_proj": 32, "c_fc": 64, "down_proj": 48})
+    params, tokens, ci, w, ci_t, tok_t = _setup(cfg, B, T, 21, device)
+    _, src_t, _, dl_t = _tables(cfg, B * T, T, torch.float32, True, 5, device)
+
+    def make():
+        advs = {k: PersistentAdversary(src_t[k].clone(), AdamPGDConfig(), n_warmup=2, rows_per_source=T, leaf_index=i)
+                for i, k in enumerate(KINDS)}
+        dadv = PersistentAdversary(dl_t.clone(), AdamPGDConfig(), n_warmup=2, rows_per_source=T, leaf_index=len(KINDS))
+        return advs, dadv
+
+    step = LMStackStep(B, T, cfg.d, cfg.n_head, cfg.n_kv_head, cfg.d_mlp, cfg.vocab, cfg.n_layers, cfg.C,
+                       device=device, use_delta=True, n_kl_chunks=2, imp_min=ImpMin("pnorm", 2.0, 0.0),
+                       rows_per_source=T)
+    advs, dadv = make()
+    res = LMPPGDStep(step, advs, dadv).step(tok_t, w, ci_t, lr=0.05, key=(0, 9))
+    torch.cuda.synchronize()
+    wl = [float(x) for x in res.warmup_losses]
+    assert len(wl) == 2 and wl[-1] >= wl[0] * (1 - 1e-3), wl
+    for k in KINDS:
+        s = advs[k].sources
+        assert float(s.min()) >= 0.0 and float(s.max()) <= 1.0 and not torch.equal(s, src_t[k])
+    dV = {k: step.dV[k].clone() for k in KINDS}
+    dci = {k: step.d_ci_pre[k].clone() for k in KINDS}
+    # the same procedure spelled out: source-only calls and ascents, then the final call
+    advs2, dadv2 = make()
+    from param_decomp_amd import prng
+
+    warm_key = prng.fold_in(prng.fold_in((0, 9), 0x51C), 0)
+    for ascent_key in prng.split(warm_key, 2):
+        step.step_sources(tok_t, w, ci_t, {k: a.sources for k, a in advs2.items()}, dadv2.sources,
+                          want_weight_grads=False)
+        for k in KINDS:
+            advs2[k].after_one_ascent(step.d_src[k], 0.05, ascent_key)
+        dadv2.after_one_ascent(step.d_src_delta, 0.05, ascent_key)
+    step.step_sources(tok_t, w, ci_t, {k: a.sources for k, a in advs2.items()}, dadv2.sources)
+    torch.cuda.synchronize()
+    for k in KINDS:
+        assert torch.equal(step.dV[k], dV[k]) and torch.equal(step.d_ci_pre[k], dci[k]), k
