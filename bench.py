@@ -49,6 +49,7 @@ CI_MLP = "ci_mlp768_h1024_C4096"
 CI_READOUT = "ci_readout_llama4L"
 PPGD_DENSE = "ppgd_dense768x3072_C4096"
 PPGD_MOE = "ppgd_qwen35moe4L"
+PPGD_LLAMA = "ppgd_llama4L"
 KL_STREAM = "kl_stream_llama4L"
 FAITH_DENSE = "faith_dense768x3072_C4096"
 FAITH_MOE = "faith_qwen35moe4L"
@@ -89,6 +90,11 @@ WORKLOADS = {
     # tables of 16 samples x 512 positions, momentum SGD, 2 warmup ascents
     PPGD_MOE: dict(T=8192, d=512, f=256, E=42, k=8, c=512, L=4, rows_per_source=512, n_warmup=2,
                    source_dtype="uint16", optimizer="momentum_sgd", momentum=0.9, lr=0.01),
+    # persistent PGD over every decomposed matrix of the 4-layer Llama-style stack: one
+    # source row per sample (bc: the reference's pooled adversary draws one particle per
+    # sample), fp32 tables with the reference LM config's Adam (beta1 0.01, beta2 0.99,
+    # lr 0.02), the delta leaf, 2 warmup ascents
+    PPGD_LLAMA: dict(n_warmup=2, source_dtype="float32", optimizer="adam", beta1=0.01, beta2=0.99, lr=0.02),
     # faithfulness of the dense site, and of every expert matrix of the MoE stack (per kind:
     # 4 layers x 42 experts, each layer's experts one block-factored site)
     FAITH_DENSE: dict(groups=[dict(n=1, per=1, d_in=768, d_out=3072, C=4096)]),
@@ -792,6 +798,71 @@ def run_ppgd_moe(args):
                                  "the weight-gradient products) with the source-table mask passes and ascents", 1)}
 
 
+def run_ppgd_llama(args):
+    """One persistent-PGD step over every decomposed matrix of the LM stack (the llama4L
+    shape): n_warmup source-only steps (masked forward, KL, backward to the sources, no
+    weight gradients; the frozen forward formed once and reused) each followed by a
+    projected ascent of every source leaf, then the final step with every gradient and the
+    final ascent."""
+    import torch
+
+    from param_decomp_amd import adversary as A
+    from param_decomp_amd import hip_events, prng
+    from param_decomp_amd.lm_step import KINDS, LMStackStep, LMWeights
+
+    lc, cfg = WORKLOADS[LLAMA], WORKLOADS[PPGD_LLAMA]
+    B, T, d, H, KV, f, V, Ln = (lc[x] for x in ("B", "T", "d", "H", "KV", "f", "V", "L"))
+    C, N = lc["C"], lc["B"] * lc["T"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, scale):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(torch.bfloat16)
+
+    dims = lm_site_dims(lc)
+    w = LMWeights(wte=rn(V, d, scale=d**-0.5), ln1=torch.ones(Ln, d, device=dev), ln2=torch.ones(Ln, d, device=dev),
+                  norm=torch.ones(d, device=dev),
+                  W={k: rn(Ln, dims[k][1], dims[k][0], scale=dims[k][0]**-0.5) for k in KINDS},
+                  V={k: rn(Ln, dims[k][0], C[k], scale=dims[k][0]**-0.5) for k in KINDS},
+                  U={k: rn(Ln, C[k], dims[k][1], scale=C[k]**-0.5) for k in KINDS})
+    ci = {k: (torch.rand(Ln, N, C[k], device=dev, generator=g) * 1.6 - 0.3).to(torch.bfloat16) for k in KINDS}
+    tok = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+    step = LMStackStep(B, T, d, H, KV, f, V, Ln, C, device=dev, p=2.0, imp_coeff=0.0, recon_coeff=1.0,
+                       use_delta=True, n_kl_chunks=lc["n_chunks"], rows_per_source=T)
+    opt = A.AdamPGDConfig(cfg["beta1"], cfg["beta2"])
+    advs = {k: A.PersistentAdversary(torch.rand(Ln, B, C[k], device=dev, generator=g), opt, cfg["n_warmup"],
+                                     rows_per_source=T, leaf_index=i) for i, k in enumerate(KINDS)}
+    dadv = A.PersistentAdversary(torch.rand(Ln, len(KINDS), B, device=dev, generator=g), opt, cfg["n_warmup"],
+                                 rows_per_source=T, leaf_index=len(KINDS))
+    ppgd = A.LMPPGDStep(step, advs, dadv)
+    for i in range(args.warmup):
+        ppgd.step(tok, w, ci, cfg["lr"], prng.fold_in((0, 0), i))
+    stream = torch.cuda.current_stream().cuda_stream
+    start, stop = hip_events.create(2)
+    torch.cuda.synchronize()
+    hip_events.record(start, stream)
+    for i in range(args.steps):
+        res = ppgd.step(tok, w, ci, cfg["lr"], prng.fold_in((0, 0), args.warmup + i))
+    hip_events.record(stop, stream)
+    torch.cuda.synchronize()
+    ms = hip_events.elapsed_ms(start, stop) / args.steps
+    hip_events.destroy([start, stop])
+    assert torch.isfinite(res.loss).all()
+    gf = lm_gemm_flops(lc)
+    # a warmup step runs everything but the weight-gradient products (and reuses the frozen forward)
+    step_flops = cfg["n_warmup"] * (sum(gf.values()) - gf["gemm_dw"]) + sum(gf.values())
+    return {"tokens": N, "ms_per_step": ms,
+            "config": {"workload": PPGD_LLAMA, "batch": B, "seq_len": T, "d_model": d, "heads": H, "d_mlp": f,
+                       "vocab": V, "layers": Ln, "C": dict(C), "source_shape": "bc", "rows_per_source": T,
+                       "source_dtype": cfg["source_dtype"], "optimizer": cfg["optimizer"],
+                       "n_warmup": cfg["n_warmup"], "recon": "kl(clean || masked), streamed over 3 vocab chunks",
+                       "delta_source": True},
+            "step_flops": step_flops, "phases_ms": {"step": ms},
+            "roofline": roofline("flop", step_flops, ms, "the step's bf16 site, attention and KL GEMMs (warmup "
+                                 "steps without the weight-gradient products) with the source-table mask passes "
+                                 "and ascents", 1)}
+
+
 # ============================================================== faithfulness
 def faith_cpu_baseline(groups, reps=3):
     import numpy as np
@@ -1483,6 +1554,8 @@ def main():
         res = run_faith(args)
     elif args.workload == PPGD_DENSE:
         res = run_ppgd(args)
+    elif args.workload == PPGD_LLAMA:
+        res = run_ppgd_llama(args)
     elif args.workload == PPGD_MOE:
         res = run_ppgd_moe(args)
     elif args.workload == KL_STREAM:
