@@ -374,7 +374,7 @@ def dense_phase_work(name, T, d_in, d_out, C, es):
     return table[name]
 
 
-def dense_cpu_baseline(T_sample, d_in, d_out, C, reps=3):
+def dense_cpu_baseline(T_sample, d_in, d_out, C, reps=20, warmup=3):
     import numpy as np
 
     from oracle import cpu
@@ -388,7 +388,8 @@ def dense_cpu_baseline(T_sample, d_in, d_out, C, reps=3):
     gp = po.GateParams(rng.normal(size=(C, 16)).astype(np.float32) * 1.4, np.zeros((C, 16), np.float32),
                        rng.normal(size=(C, 16)).astype(np.float32) * 0.35, np.full(C, 0.3, np.float32))
     mk, dk = po.site_keys((0, 0), 0)
-    cpu.dense_step(x, W, V, U, gp, mk, dk)
+    for _ in range(warmup):
+        cpu.dense_step(x, W, V, U, gp, mk, dk)
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -397,7 +398,7 @@ def dense_cpu_baseline(T_sample, d_in, d_out, C, reps=3):
     med = statistics.median(times)
     return {"value": T_sample / med, "unit": "tokens/s", "cores": cpu.num_threads(), "kind": "port",
             "sample": f"{T_sample} of the workload's tokens (same d_in/d_out/C), fp32 C+OpenMP restatement of the "
-                      f"same step, median of {reps} after 1 warmup; {med * 1e3:.1f} ms per sample step"}
+                      f"same step, median of {reps} after {warmup} warmups; {med * 1e3:.1f} ms per sample step"}
 
 
 def run_dense(args):
@@ -1139,7 +1140,7 @@ def moe_dacts_work(cfg):
     return flops, byts
 
 
-def moe_cpu_baseline(cfg, T_sample, reps=5, warmup=2):
+def moe_cpu_baseline(cfg, T_sample, reps=20, warmup=3):
     """The compiled fp32 C/OpenMP restatement of the same step (`oracle/cpu_step.c`
     `or_moe_step`, checked against the NumPy oracle) on `T_sample` tokens at the full
     widths; inputs packed once outside the timed calls."""
@@ -1389,7 +1390,7 @@ def lm_gemm_flops(cfg):
             "kl": kl}
 
 
-def lm_cpu_baseline(cfg, n_sample, reps=3):
+def lm_cpu_baseline(cfg, n_sample, reps=20, warmup=3):
     """The LM oracle's step in fp32 (torch on the host cores) on `n_sample` tokens of one
     sequence at the workload's full widths."""
     import numpy as np
@@ -1409,7 +1410,8 @@ def lm_cpu_baseline(cfg, n_sample, reps=3):
     tokens = rng.integers(0, lc.vocab, size=(1, n_sample))
     ci = lo.init_ci(lc, n_sample, rng)
     run = lambda: lo.lm_stack_step(lc, params, tokens, ci, (0, 1), use_delta=cfg["use_delta"], dtype=torch.float32)
-    run()
+    for _ in range(warmup):
+        run()
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -1418,8 +1420,8 @@ def lm_cpu_baseline(cfg, n_sample, reps=3):
     med = statistics.median(times)
     return {"value": n_sample / med, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"one sequence of {n_sample} tokens at the full widths (4 layers, vocab 50277), the oracle's "
-                      f"torch fp32 CPU restatement of the same step (autograd backward), median of {reps} after 1 "
-                      f"warmup; {med * 1e3:.0f} ms per sample step"}
+                      f"torch fp32 CPU restatement of the same step (autograd backward), median of {reps} after "
+                      f"{warmup} warmups; {med * 1e3:.0f} ms per sample step"}
 
 
 def run_llama(args):
@@ -1540,7 +1542,7 @@ def main():
               "How the path would shard is a design note, not a measurement.", file=sys.stderr)
         sys.exit(2)
     if args.cpu_tokens is None:
-        args.cpu_tokens = {MOE: 2048, DENSE: 4096, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
+        args.cpu_tokens = {MOE: 1024, DENSE: 2048, CI_MLP: 512, CI_READOUT: 256, PPGD_DENSE: 256,
                            KL_STREAM: 64, LLAMA: 128}.get(args.workload, 0)
     if args.workload == MOE:
         res = run_moe(args)
