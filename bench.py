@@ -208,53 +208,81 @@ def copy_calibration():
     print("copied", n)
 
 
+RD_COUNTERS = ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_sum")
+
+
 def pmc_traffic_summary(outdir: str, workloads) -> str:
-    """Calibrated HBM bytes per dispatch from `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs
-    (one counter per run) under OUTDIR: cal_<CTR> around `bench.py --copy-calibration`,
-    <workload>_<CTR> around `bench.py --workload W --steps 2 --warmup 1 --no-cpu-baseline`.
-    Each counter is scaled by what it reads for the 1 GiB copy (KiB per dispatch)."""
+    """HBM bytes per dispatch from two PMC runs per workload under OUTDIR: <name>_RD with the
+    L2-to-memory read requests by size (bytes = 32 n32 + 64 n64 + 128 n128) and
+    <name>_WRITE_SIZE; cal_* are the same runs around `bench.py --copy-calibration` (three
+    1 GiB device copies), a check that the request-size sums give the bytes copied. The
+    derived FETCH_SIZE counter is not used: it counts 128-byte reads through TCC_BUBBLE,
+    which stays 0 on gfx950, so it reports half of every 128-byte read."""
     import collections
     import csv
 
     def load(path):
-        agg = collections.defaultdict(list)
-        for r in csv.DictReader(open(os.path.join(outdir, path, "run_counter_collection.csv"))):
-            agg[r["Kernel_Name"].split("(")[0].replace("void ", "")].append(float(r["Counter_Value"]))
+        """{label: {counter: [per-dispatch values]}}; a kernel launched with several grid
+        sizes (one GEMM template serving several phases) gets one row per grid, labelled
+        `name @work-items`."""
+        rows = list(csv.DictReader(open(os.path.join(outdir, path, "run_counter_collection.csv"))))
+        grids = collections.defaultdict(set)
+        for r in rows:
+            grids[r["Kernel_Name"].split("(")[0].replace("void ", "")].add(r["Grid_Size"])
+        agg = collections.defaultdict(lambda: collections.defaultdict(list))
+        for r in rows:
+            k = r["Kernel_Name"].split("(")[0].replace("void ", "")
+            if len(grids[k]) > 1:
+                k = f"{k} @{r['Grid_Size']}"
+            agg[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
         return agg
 
-    cal = {}
-    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
-        v = load(f"cal_{ctr}")["__amd_rocclr_copyBuffer"]
-        cal[ctr] = (1 << 20) / (sum(v) / len(v))  # KiB of the 1 GiB copy -> factor to bytes moved
+    def avg(d, c):
+        v = d.get(c, [])
+        return sum(v) / len(v) if v else 0.0
+
+    def read_bytes(d):
+        n32, n64, n128, n = (avg(d, c) for c in RD_COUNTERS)
+        return 32 * n32 + 64 * n64 + 128 * n128, n - n32 - n64 - n128
+
+    crd, cwr = load("cal_RD")["__amd_rocclr_copyBuffer"], load("cal_WRITE_SIZE")["__amd_rocclr_copyBuffer"]
+    cal_rd, cal_unsized = read_bytes(crd)
+    cal_wr = avg(cwr, "WRITE_SIZE") * 1024
+    rd_cmd = "rocprofv3 --pmc " + " ".join(RD_COUNTERS)
     out = ["# HBM traffic per dispatch (rocprofv3 PMC)", "",
-           "Two counter runs per workload (FETCH_SIZE, then WRITE_SIZE; one counter per run), plus the same counters",
-           "around three device-to-device copies of 1 GiB (`python3 bench.py --copy-calibration`, a plain copy",
-           "kernel of known size) to calibrate:", "",
-           f"- FETCH_SIZE reads {1 / cal['FETCH_SIZE']:.4f} GiB for the 1 GiB copy: factor **{cal['FETCH_SIZE']:.3f}** "
-           "to bytes read",
-           f"- WRITE_SIZE reads {1 / cal['WRITE_SIZE']:.4f} GiB for the 1 GiB copy: factor **{cal['WRITE_SIZE']:.3f}** "
-           "to bytes written", "", "commands (OUT = a fresh directory per run):", "", "```",
-           "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d OUT -o run --output-format csv -- python3 bench.py --copy-calibration",
-           "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d OUT -o run --output-format csv -- python3 bench.py --copy-calibration"]
+           "Two counter runs per workload: the L2-to-memory read requests by size (" + ", ".join(
+               f"`{c}`" for c in RD_COUNTERS) + "; read bytes = 32 n32 + 64 n64 + 128 n128), then `WRITE_SIZE`.",
+           "The derived `FETCH_SIZE` is not used: its formula counts 128-byte reads through `TCC_BUBBLE`, which",
+           "stays 0 on gfx950, so it reports half of every 128-byte read.", "",
+           "Check against three device-to-device copies of 1 GiB (`python3 bench.py --copy-calibration`):",
+           f"read {cal_rd / 2**30:.4f} GiB and wrote {cal_wr / 2**30:.4f} GiB per copy "
+           f"({cal_unsized:.0f} read requests of no listed size).", "",
+           "commands (OUT = a fresh directory per run):", "", "```",
+           f"cd /tmp && {rd_cmd} -d OUT -o run --output-format csv -- python3 bench.py --copy-calibration",
+           "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d OUT -o run --output-format csv -- python3 bench.py "
+           "--copy-calibration"]
     for wl in workloads:
-        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
-            out.append(f"cd /tmp && rocprofv3 --pmc {ctr} -d OUT -o run --output-format csv -- python3 bench.py "
-                       f"--workload {wl} --steps 2 --warmup 1 --no-cpu-baseline")
+        out.append(f"cd /tmp && {rd_cmd} -d OUT -o run --output-format csv -- python3 bench.py "
+                   f"--workload {wl} --steps 2 --warmup 1 --no-cpu-baseline")
+        out.append(f"cd /tmp && rocprofv3 --pmc WRITE_SIZE -d OUT -o run --output-format csv -- python3 bench.py "
+                   f"--workload {wl} --steps 2 --warmup 1 --no-cpu-baseline")
     out += ["```", f"summarized with `python bench.py --pmc-traffic-summary OUTDIR {' '.join(workloads)}`", ""]
     for wl in workloads:
-        f, w = load(f"{wl}_FETCH_SIZE"), load(f"{wl}_WRITE_SIZE")
+        f, w = load(f"{wl}_RD"), load(f"{wl}_WRITE_SIZE")
         out += [f"## {wl}", "",
-                "| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/dispatch (calibrated) |",
-                "|---|---|---|---|---|"]
+                "| kernel | dispatches | read MB/dispatch | 128-byte reads | write MB/dispatch | HBM bytes/dispatch |",
+                "|---|---|---|---|---|---|"]
         rows = []
         for k in f:
             if k not in w or not k.startswith("pd::"):
                 continue
-            fa, wa = sum(f[k]) / len(f[k]), sum(w[k]) / len(w[k])
-            hbm = (fa * cal["FETCH_SIZE"] + wa * cal["WRITE_SIZE"]) * 1024
-            rows.append((hbm * len(f[k]), k, len(f[k]), fa, wa, hbm))
-        for _, k, n, fa, wa, hbm in sorted(rows, reverse=True)[:18]:
-            out.append(f"| `{k}` | {n} | {fa:.0f} | {wa:.0f} | {hbm:.4g} |")
+            rb, _ = read_bytes(f[k])
+            n128, n = avg(f[k], RD_COUNTERS[2]), avg(f[k], RD_COUNTERS[3])
+            wb = avg(w[k], "WRITE_SIZE") * 1024
+            nd = len(f[k][RD_COUNTERS[3]])
+            rows.append(((rb + wb) * nd, k, nd, rb, n128 / max(n, 1), wb, rb + wb))
+        for _, k, nd, rb, f128, wb, hbm in sorted(rows, reverse=True)[:24]:
+            out.append(f"| `{k}` | {nd} | {rb / 1e6:.1f} | {100 * f128:.0f}% | {wb / 1e6:.1f} | {hbm:.4g} |")
         out.append("")
     return "\n".join(out) + "\n"
 
@@ -308,14 +336,29 @@ PHASE_KERNEL = {
                            "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 1, false, "
                            "pd::EpiMaskBwd"),
           "mask_fwd": ("pd::k_mask_fwd_tile",), "mask_bwd": ("pd::k_mask_bwd_tile", "pd::k_mask_bwd_vec")},
-    DENSE: {"gate_mask_fwd": ("pd::k_step_fwd_tab",), "gate_mask_bwd": ("pd::k_step_bwd",),
-            "recon": ("pd::k_step_recon",)},
+    # dense GEMM phases by template and grid (work-items of 128x128 tiles x 512 threads at
+    # T 4096, 768 -> 3072, C 4096)
+    DENSE: {"gate_mask_fwd": ("pd::k_step_fwd_tab", "pd::k_gate_range", "pd::k_gate_table"),
+            "gate_mask_bwd": ("pd::k_step_bwd",), "gate_grad_reduce": ("pd::k_gate_finalize",),
+            "recon": ("pd::k_step_recon",),
+            "gemm_target": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
+                            "pd::EpiStore, false, false> @393216",),
+            "gemm_xV": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
+                        "pd::EpiStore, false, true> @524288",),
+            "gemm_actsU": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
+                           "pd::EpiStore, false, true> @393216",),
+            "gemm_dU": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 0, false, "
+                        "pd::EpiStore, true, true> @393216",),
+            "gemm_da": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
+                        "pd::EpiStore, false, false> @524288",),
+            "gemm_dV": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 0, false, "
+                        "pd::EpiStore, true, true> @98304",)},
 }
 
 
 def pmc_traffic(workload, phase):
-    """Calibrated HBM bytes per launch of the phase's kernels from the committed PMC
-    summary (FETCH_SIZE and WRITE_SIZE runs scaled by a 1 GiB copy), or None."""
+    """HBM bytes per launch of the phase's kernels from the committed PMC summary (read
+    requests by size plus WRITE_SIZE), or None."""
     prefixes = PHASE_KERNEL.get(workload, {}).get(phase)
     path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
     if prefixes is None or not os.path.exists(path):
@@ -358,7 +401,7 @@ def dense_phase_work(name, T, d_in, d_out, C, es):
     fused elementwise passes (fwd reads h and writes h*m; bwd reads h and d(h*m) and
     writes dh; u is regenerated or byte-stored, never stored at full width)."""
     table = {
-        "transpose_inputs": ("byte", 2 * (T * d_in + d_in * C + C * d_out) * es),
+        "delta_draw": ("byte", 4 * T),
         "gemm_target": ("flop", 2 * T * d_in * d_out),
         "gemm_xV": ("flop", 2 * T * d_in * C),
         "gate_mask_fwd": ("byte", 2 * T * C * es),

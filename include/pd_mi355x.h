@@ -240,6 +240,13 @@ int pd_blocked_site_bwd(int dtype, int contraction, int64_t T, int64_t E, int64_
  * Gradients (overwritten, fp32 for the fp32 masters): dV [d_in,C], dU [C,d_out], gate grads.
  * losses[4] = {loss, recon, activity, frequency} fp32. mask_key / delta_key are the site's
  * keys (already split/folded). dtype bf16: x,W,V,U bf16.
+ * The bf16 step evaluates each component's gate from a per-step table (32 bins over the
+ * observed h range, degree-7 Chebyshev interpolant of g per bin: |g error| <= 8.3e-7 *
+ * sum_j |w_out_j|) and takes the gate-parameter gradients from 8 Chebyshev moments of the
+ * gate cotangent on 16 bins (the exact pullback of 128 weighted nodes per component;
+ * interpolation error <= 7.5e-4 of each summand's scale). A component for which some
+ * |w_in_j| * (moment-bin width) > 3 gets the exact per-element gate in both passes. The
+ * fp32 step evaluates the gate exactly everywhere.
  * The EMA frequency estimate (this and every fused step; pd/core/losses.py:425-458,
  * EmaFrequency :522-543, ema_halflife_steps pd/core/configs.py:165-182): freq_ema_in NULL
  * is the single-batch estimate above. Otherwise (smooth-L0 with ref_count > 0 only) each
@@ -264,10 +271,10 @@ int pd_dense_step(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, 
 
 /* pd_dense_step with phase timing for measurement harnesses: `events` holds
  * PD_DENSE_STEP_PHASES + 1 hipEvent_t handles recorded on `stream` at the phase
- * boundaries: 0 operand transposes (x, V, U), 1 target GEMM x@W^T, 2 GEMM h=x@V,
- * 3 gate/mask fwd, 4 GEMM (h*m)@U, 5 recon residual, 6 loss finalize, 7 GEMM dU,
- * 8 GEMM da=dy@U^T, 9 gate/mask bwd, 10 gate-grad reduce, 11 GEMM dV. Same arithmetic
- * as pd_dense_step. */
+ * boundaries: 0 delta draw, 1 target GEMM x@W^T, 2 GEMM h=x@V, 3 gate/mask fwd
+ * (bf16: h range, gate table, forward), 4 GEMM (h*m)@U, 5 recon residual, 6 loss
+ * finalize, 7 GEMM dU, 8 GEMM da=dy@U^T, 9 gate/mask bwd, 10 gate-parameter gradients
+ * (bf16: moment finalize), 11 GEMM dV. Same arithmetic as pd_dense_step. */
 #define PD_DENSE_STEP_PHASES 12
 int pd_dense_step_timed(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C, int H, const void* x,
                         const void* W, const void* V, const void* U, const float* w_in, const float* b_in,

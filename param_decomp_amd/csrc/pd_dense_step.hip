@@ -3,20 +3,20 @@
 // (pd/core/train.py:1126-1352 restricted to one site; pd/core/masking.py:148-167 draws;
 // pd/core/decomposed_linear.py:142-175; spd_paper.md appendix gate).
 //
-// Every GEMM of the step runs with both operands K-contiguous (the fastest MFMA
-// operand path): the inputs x, V, U are transposed once per step, and the elementwise
-// producers write the K-contiguous copies the weight-gradient GEMMs need (acts^T, dy^T,
-// dh^T) through 64x64 LDS tiles, so those stores stay coalesced.
+// Every operand is consumed in the layout it is stored in: the bf16 GEMM reads an
+// MN-contiguous operand through the transposing LDS read (ds_read_b64_tr_b16), so no
+// transposed copy of x, V, U, acts, dy or dh is ever written. Every tensor of the step
+// is token-major.
 //
-//   yt  = x @ W^T          A=x [T,d_in]      B=W  [d_out,d_in]
-//   h   = x @ V            A=x               B=V^T [C,d_in]
-//   fwd elementwise: g_raw, squash, u, acts = h*(m-d)  -> acts [T,C], acts^T [C,T]
-//   y   = acts @ U         A=acts [T,C]      B=U^T [d_out,C]
-//   recon: e = y + d*yt - yt, dy = scale*e            -> dy [T,d_out], dy^T [d_out,T]
-//   dU  = acts^T @ dy      A=acts^T [C,T]    B=dy^T [d_out,T]
-//   da  = dy @ U^T         A=dy [T,d_out]    B=U [C,d_out]
-//   bwd elementwise: dh = da*(m-d) + gate pullback     -> dh^T [C,T]
-//   dV  = x^T @ dh         A=x^T [d_in,T]    B=dh^T [C,T]
+//   yt  = x @ W^T          A=x [T,d_in] (K-contig)     B=W [d_out,d_in] (K-contig)
+//   h   = x @ V            A=x                         B=V [d_in,C] (N-contig)
+//   fwd elementwise: gate, squash, u, acts = h*(m-d)  -> acts [T,C]
+//   y   = acts @ U         A=acts [T,C]                B=U [C,d_out] (N-contig)
+//   recon: e = y + d*yt - yt, dy = scale*e            -> dy [T,d_out]
+//   dU  = acts^T @ dy      A=acts [T,C] (M-contig)     B=dy [T,d_out] (N-contig)
+//   da  = dy @ U^T         A=dy [T,d_out]              B=U [C,d_out] (K-contig)
+//   bwd elementwise: dh = da*(m-d) + gate pullback     -> dh [T,C]
+//   dV  = x^T @ dh         A=x [T,d_in] (M-contig)     B=dh [T,C] (N-contig)
 #include <algorithm>
 
 #include "pd_impmin.hpp"
@@ -25,7 +25,7 @@ namespace pd {
 
 static constexpr int SITE_COLS = 64;  // components per block in the column-mapped kernels
 static constexpr int SITE_ROWS = 64;  // tokens per block chunk
-static constexpr int TP = 64;         // transpose tile
+static constexpr int TP = 64;         // recon tile
 
 struct StepParams {
   int64_t T, C;
@@ -51,36 +51,6 @@ __global__ void k_delta_fill(uint32_t k0, uint32_t k1, int64_t T, int draw_dtype
     d[t] = draw_uniform(k0, k1, t, T, draw_dtype, layout);
 }
 
-// A lane's run of consecutive-token values of one component, emitted to dstT [C, T] as
-// 16-byte stores: a sliding window of 8 bf16 (shifted with v_alignbit) or 4 fp32.
-template <typename T>
-struct RowPack;
-template <>
-struct RowPack<bf16_t> {
-  static constexpr int N = 8;
-  uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
-  __device__ inline void push(float v) {
-    const uint32_t b = f32_to_bf16(v);
-    w0 = __builtin_amdgcn_alignbit(w1, w0, 16);
-    w1 = __builtin_amdgcn_alignbit(w2, w1, 16);
-    w2 = __builtin_amdgcn_alignbit(w3, w2, 16);
-    w3 = (w3 >> 16) | (b << 16);
-  }
-  __device__ inline void flush(bf16_t* dst) { *(uint4*)dst = make_uint4(w0, w1, w2, w3); }
-};
-template <>
-struct RowPack<float> {
-  static constexpr int N = 4;
-  float w0 = 0, w1 = 0, w2 = 0, w3 = 0;
-  __device__ inline void push(float v) {
-    w0 = w1;
-    w1 = w2;
-    w2 = w3;
-    w3 = v;
-  }
-  __device__ inline void flush(float* dst) { *(float4*)dst = make_float4(w0, w1, w2, w3); }
-};
-
 __device__ inline float pow_p(float b, float p) { return p == 2.f ? b * b : (p == 1.f ? b : powf(b, p)); }
 __device__ inline float dpow_p(float b, float p) {
   return p == 2.f ? 2.f * b : (p == 1.f ? 1.f : p * powf(b, p - 1.f));
@@ -92,24 +62,6 @@ __device__ inline float step_imp(const StepParams& s, float up) {
 }
 __device__ inline float step_dimp(const StepParams& s, int64_t c, float up) {
   return s.sl0 ? s.slope[c] * sl0_dpsi(up, s.g2, s.psis) : s.imp_scale * dpow_p(up, s.p);
-}
-
-// dst[c][r] = src[r][c] for a [R, Cc] matrix; 64x64 tiles through LDS.
-template <typename T>
-__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ src, int64_t R, int64_t Cc,
-                                                   T* __restrict__ dst) {
-  __shared__ float tile[TP][TP + 1];
-  const int64_t r0 = (int64_t)blockIdx.y * TP, c0 = (int64_t)blockIdx.x * TP;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < TP; i += 4) {
-    int64_t r = r0 + i, c = c0 + tx;
-    tile[i][tx] = (r < R && c < Cc) ? load_f<T>(src, r * Cc + c) : 0.f;
-  }
-  __syncthreads();
-  for (int i = ty; i < TP; i += 4) {
-    int64_t c = c0 + i, r = r0 + tx;
-    if (c < Cc && r < R) store_f<T>(dst, c * R + r, tile[tx][i]);
-  }
 }
 
 // The uniform of element i: bf16 draws are stored by the forward as the 7-bit integer
@@ -128,15 +80,14 @@ __device__ inline float step_uniform_bwd(const StepParams& s, int64_t i, int64_t
 }
 
 // Forward, one component per lane over a 64-token chunk: gate MLP on h, squash, draw u,
-// acts = h*(m-d), imp-min partial of upper^p. Writes g_raw (fp32), acts, acts^T (the
-// lane's consecutive tokens of its component, packed into 16-byte stores).
+// acts = h*(m-d), imp-min partial of upper^p. Writes g_raw (fp32) and acts.
 template <typename T, bool PRECISE>
 __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h, const float* __restrict__ w_in,
                                                         const float* __restrict__ b_in,
                                                         const float* __restrict__ w_out,
                                                         const float* __restrict__ b_out, StepParams s,
                                                         float* __restrict__ g_raw, T* __restrict__ acts,
-                                                        T* __restrict__ actsT, float* __restrict__ imp_partial) {
+                                                        float* __restrict__ imp_partial) {
   const int64_t c = (int64_t)blockIdx.x * SITE_COLS + threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.y * SITE_ROWS;
   const int64_t r1 = r0 + SITE_ROWS < s.T ? r0 + SITE_ROWS : s.T;
@@ -151,7 +102,6 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
     }
     const float bo = b_out[c];
     const int64_t n = s.T * s.C;
-    RowPack<T> pack;
     for (int64_t t = r0; t < r1; ++t) {
       const int64_t i = t * s.C + c;
       const float hv = load_f<T>(h, i);
@@ -165,10 +115,7 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
       col += iv;
       const float u = step_uniform_fwd(s, i, n);
       const float m = lo + (1.f - lo) * u;
-      const float a = hv * (m - step_delta(s, t));
-      store_f<T>(acts, i, a);
-      pack.push(a);
-      if (((t - r0) % RowPack<T>::N) == RowPack<T>::N - 1) pack.flush(actsT + c * s.T + t + 1 - RowPack<T>::N);
+      store_f<T>(acts, i, hv * (m - step_delta(s, t)));
     }
     if (s.sl0) s.colpart[(int64_t)blockIdx.y * s.C + c] = col;
   }
@@ -176,21 +123,50 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_fwd(const T* __restrict__ h,
   if (threadIdx.x == 0) imp_partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = imp;
 }
 
-// ---------------------------------------------------------------- tabulated gate (bf16 step)
+// ---------------------------------------------------------------- binned gate (bf16 step)
 // For one component c the gate preactivation g_c(h) = b_out + sum_j w_out_j GELU(w_in_j h +
-// b_in_j) is a smooth function of the scalar h, and the step draws all its h values
-// from x @ V before the forward pass. So the bf16 forward evaluates g_c from a per-step
-// table instead of 16 GELUs per element: GATE_KNOTS intervals spanning the component's
-// observed [min h, max h], exact g and g' at every knot, and the cubic Hermite
-// interpolant between knots. Its error is at most dx^4/384 max|g^(4)|, about 1e-5 of g
-// for unit-scale h and the paper's initialization (dx = range/128), far below bf16
-// resolution and below the reference's own bf16 arithmetic for this MLP. The forward
-// stores that g, so the backward's squashing branches agree with it; the backward keeps
-// the exact per-element pullback (it needs every hidden unit for the parameter
-// gradients anyway).
-static constexpr int GATE_KNOTS = 128;
+// b_in_j) is a smooth function of the scalar h, and the step has all of its h values
+// (from x @ V) before either elementwise pass. The bf16 step splits the component's
+// observed [min h, max h] into GATE_TBINS equal bins and represents g_c on each by its
+// degree-7 Chebyshev interpolant (exact g at the bin's 8 Chebyshev nodes), stored as
+// power-series coefficients in the bin coordinate tau in [-1, 1]. The forward and the
+// backward evaluate g and dg/dh from this one table with the same code, so the
+// backward's squashing branches see the forward's g bit for bit without it being stored.
+//
+// The gate-parameter gradients are token sums of dg_t f(h_t) for 48 functions f of h
+// (w_out_j GELU'(z_j) h, w_out_j GELU'(z_j), GELU(z_j), z_j = w_in_j h + b_in_j). The
+// backward accumulates, per component and moment bin (a pair of table bins), the
+// Chebyshev moments M_m = sum_t dg_t T_m(tau_t), m < 8. If p is the degree-7 Chebyshev
+// interpolant of f on the bin, sum_t dg_t p(tau_t) = sum_k w_k f(node_k) with node
+// weights w_k = (2/8) (M_0 / 2 + sum_{m>=1} cos(m theta_k) M_m), theta_k = (2k+1) pi / 16
+// (discrete orthogonality of T_m on the nodes). So each component's T-token pullback
+// becomes the exact pullback of 128 weighted virtual tokens (8 nodes per moment bin),
+// evaluated once per step; sum_k w_k = M_0 keeps the b_out gradient exact.
+//
+// Error: with dz = |w_in_j| * (moment-bin width) <= GATE_DZ_MAX = 3 for every hidden
+// unit, the moment interpolant of GELU, GELU' and h GELU' errs by at most 1.6e-4, 4.0e-4
+// and 7.5e-4 of their scale (worst bin position; sums over tokens average it further),
+// and the table (half as wide in z) by 8.3e-7 for GELU (so |g error| <= 8.3e-7 sum_j
+// |w_out_j|) and 6.9e-5 for its derivative. A component with a wider unit is flagged by
+// the table pass, and both passes evaluate its gate exactly, element by element, as the
+// fp32 step does.
+static constexpr int GATE_TBINS = 32;    // table bins over [min h, max h]
+static constexpr int GATE_MBINS = 16;    // moment bins (pairs of table bins)
+static constexpr int GATE_NC = 8;        // degree-7 table polynomials, 8 Chebyshev moments
+static constexpr int GATE_MOM = GATE_MBINS * GATE_NC;  // moment slots per component (>= 49)
+static constexpr float GATE_DZ_MAX = 3.f;
 static constexpr int RANGE_ROWS = 256;   // tokens per block of the range pass
-static constexpr int FWD_WAVES = 8;      // waves per tabulated-forward block (each 64 tokens)
+static constexpr int FWD_WAVES = 8;      // waves per binned-forward block (each 64 tokens)
+static constexpr int BWD_COLS = 32;      // components per binned-backward block
+static constexpr int BWD_WAVES = 4;      // waves per binned-backward block
+static constexpr int BWD_ROWS = 256;     // tokens per half-wave stream of the backward
+static constexpr int BWD_BLOCK_ROWS = 2 * BWD_WAVES * BWD_ROWS;  // tokens per backward block
+static_assert(GATE_MOM >= 49, "the exact-gate sums share the moment slots");
+
+// The Chebyshev nodes x_k = cos((2k+1) pi / 16), k < 8 (T_m(x_k) = cos(m (2k+1) pi / 16)
+// follows by the recurrence T_{m+1} = 2 x T_m - T_{m-1}).
+__constant__ float kChebNode[GATE_NC] = {0.980785280f,  0.831469612f,  0.555570233f,  0.195090322f,
+                                         -0.195090322f, -0.555570233f, -0.831469612f, -0.980785280f};
 
 // Partial per-component min/max of h over RANGE_ROWS tokens: rng_part[chunk][c] = (min, max).
 __global__ __launch_bounds__(256) void k_gate_range(const bf16_t* __restrict__ h, int64_t T, int64_t C,
@@ -222,64 +198,156 @@ __global__ __launch_bounds__(256) void k_gate_range(const bf16_t* __restrict__ h
   }
 }
 
-// One thread per (component, knot): tab[c][k] = (g(h_k), g'(h_k) * dx) with h_k = lo + k dx
-// evaluated exactly (device erff/expf), and rng[c] = (lo, 1 / dx, dx).
+// One thread per (component, table bin): the bin's degree-7 Chebyshev interpolant of g in
+// power form, tab[c][b][0..7] (tau = 2 (h - lo) / bw - 2b - 1, bw the table-bin width),
+// from exact g (device erff/expf) at the nodes tau_k = cos((2k+1) pi / 16); and
+// rng[c] = (lo, 1 / bw, bw, flag), flag = 1 when some |w_in_j| * 2 bw > GATE_DZ_MAX.
 __global__ __launch_bounds__(256) void k_gate_table(const float2* __restrict__ rng_part, int nchunk, int64_t C,
                                                     const float* __restrict__ w_in, const float* __restrict__ b_in,
                                                     const float* __restrict__ w_out, const float* __restrict__ b_out,
-                                                    float2* __restrict__ tab, float4* __restrict__ rng) {
+                                                    float* __restrict__ tab, float4* __restrict__ rng) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= C * (GATE_KNOTS + 1)) return;
-  const int64_t c = idx / (GATE_KNOTS + 1);
-  const int k = (int)(idx % (GATE_KNOTS + 1));
+  if (idx >= C * GATE_TBINS) return;
+  const int64_t c = idx / GATE_TBINS;
+  const int b = (int)(idx % GATE_TBINS);
   float lo = INFINITY, hi = -INFINITY;
   for (int i = 0; i < nchunk; ++i) {
     const float2 r = rng_part[(int64_t)i * C + c];
     lo = fminf(lo, r.x);
     hi = fmaxf(hi, r.y);
   }
-  const float dx = fmaxf((hi - lo) / GATE_KNOTS, 1e-6f * fmaxf(fabsf(lo), 1.f));
-  const float hk = lo + k * dx;
-  float g = b_out[c], gp = 0.f;
+  const float bw = fmaxf((hi - lo) / GATE_TBINS, 4e-6f * fmaxf(fabsf(lo), 1.f));
+  float wi[16], bi[16], wo[16], wmax = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float wi = w_in[c * 16 + j], wo = w_out[c * 16 + j];
-    const GeluOut go = gelu_and_grad<true>(fmaf(wi, hk, b_in[c * 16 + j]));
-    g = fmaf(wo, go.gelu, g);
-    gp = fmaf(wo * wi, go.grad, gp);
+    wi[j] = w_in[c * 16 + j];
+    bi[j] = b_in[c * 16 + j];
+    wo[j] = w_out[c * 16 + j];
+    wmax = fmaxf(wmax, fabsf(wi[j]));
   }
-  tab[idx] = make_float2(g, gp * dx);
-  if (k == 0) rng[c] = make_float4(lo, 1.f / dx, dx, 0.f);
+  // Chebyshev coefficients cm[m] = (2/8) sum_k g(x_k) T_m(x_k), cm[0] halved
+  double cm[GATE_NC] = {};
+  for (int k = 0; k < GATE_NC; ++k) {
+    const float xk = kChebNode[k];
+    const float hk = lo + bw * ((float)b + 0.5f + 0.5f * xk);
+    float g = b_out[c];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) g = fmaf(wo[j], gelu_and_grad<true>(fmaf(wi[j], hk, bi[j])).gelu, g);
+    double t0 = 1.0, t1 = xk;
+    cm[0] += g;
+    cm[1] += (double)g * t1;
+    for (int m = 2; m < GATE_NC; ++m) {
+      const double t2 = 2.0 * xk * t1 - t0;
+      cm[m] += (double)g * t2;
+      t0 = t1;
+      t1 = t2;
+    }
+  }
+  // power form: sum_m cm[m] T_m(tau), T_m's coefficients by T_{m+1} = 2 tau T_m - T_{m-1}
+  double a[GATE_NC] = {}, t0[GATE_NC] = {1.0}, t1[GATE_NC] = {0.0, 1.0};
+  for (int m = 0; m < GATE_NC; ++m) {
+    const double cmm = cm[m] * (m == 0 ? 0.125 : 0.25);
+    const double* tm = m == 0 ? t0 : t1;
+    for (int i = 0; i < GATE_NC; ++i) a[i] += cmm * tm[i];
+    if (m >= 1) {
+      double t2[GATE_NC];
+      for (int i = 0; i < GATE_NC; ++i) t2[i] = (i > 0 ? 2.0 * t1[i - 1] : 0.0) - t0[i];
+      for (int i = 0; i < GATE_NC; ++i) {
+        t0[i] = t1[i];
+        t1[i] = t2[i];
+      }
+    }
+  }
+  for (int i = 0; i < GATE_NC; ++i) tab[idx * GATE_NC + i] = (float)a[i];
+  if (b == 0) rng[c] = make_float4(lo, 1.f / bw, bw, wmax * 2.f * bw > GATE_DZ_MAX ? 1.f : 0.f);
 }
 
-// g_c(h) from the component's table row tl (interval k, fraction f): the cubic Hermite
-// interpolant in power form.
-__device__ inline float gate_eval(const float* tl, float tt) {
-  const int k = min(max((int)tt, 0), GATE_KNOTS - 1);
-  const float f = tt - (float)k;
-  const float2 q0 = *(const float2*)(tl + 2 * k);  // (g_k, s_k), s = g' dx
-  const float2 q1 = *(const float2*)(tl + 2 * k + 2);
-  const float d = q1.x - q0.x;
-  const float b = 3.f * d - 2.f * q0.y - q1.y, cc = q0.y + q1.y - 2.f * d;
-  return fmaf(f, fmaf(f, fmaf(f, cc, b), q0.y), q0.x);
+// Table bin and coordinate of h: s = (h - lo) / bw in [0, GATE_TBINS], b = floor(s)
+// clamped, tau = 2 (s - b) - 1.
+struct GateCoord {
+  float s, tau;
+  int b;
+};
+__device__ inline GateCoord gate_coord(float hv, float4 rg) {
+  const float s = (hv - rg.x) * rg.y;
+  const int b = min(max((int)s, 0), GATE_TBINS - 1);
+  return {s, fmaf(2.f, s - (float)b, -1.f), b};
 }
 
-// The bf16 forward with the tabulated gate: block = 64 components x (FWD_WAVES * 64)
-// tokens; the 64 components' tables sit in LDS; each wave walks 64 consecutive tokens,
-// one component per lane. Otherwise as k_step_fwd.
-__global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* __restrict__ h,
-                                                                 const float2* __restrict__ tab,
-                                                                 const float4* __restrict__ rng, StepParams s,
-                                                                 float* __restrict__ g_raw, bf16_t* __restrict__ acts,
-                                                                 bf16_t* __restrict__ actsT,
-                                                                 float* __restrict__ imp_partial) {
-  constexpr int KS = GATE_KNOTS + 1;
-  __shared__ __attribute__((aligned(16))) float2 lt[64 * KS];
+// g and dg/dtau from a table bin's power-form coefficients a0 = (a_0..a_3), a1 = (a_4..a_7)
+// (Horner; the forward uses only g, which this one code path gives bit for bit in both
+// passes).
+__device__ inline float2 gate_poly(float4 a0, float4 a1, float tau) {
+  // Horner for p, with the derivative carried along (d <- d tau + p before each step)
+  float g = a1.w, d = a1.w;
+  g = fmaf(g, tau, a1.z);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a1.y);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a1.x);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a0.w);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a0.z);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a0.y);
+  d = fmaf(d, tau, g);
+  g = fmaf(g, tau, a0.x);
+  return make_float2(g, d);
+}
+
+// A component's 49 gate weights at stride `st` (w_in[16], b_in[16], w_out[16], b_out).
+__device__ inline void gate_weights_load(int64_t c, const float* __restrict__ w_in, const float* __restrict__ b_in,
+                                         const float* __restrict__ w_out, const float* __restrict__ b_out, float* w,
+                                         int st) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    w[j * st] = w_in[c * 16 + j];
+    w[(16 + j) * st] = b_in[c * 16 + j];
+    w[(32 + j) * st] = w_out[c * 16 + j];
+  }
+  w[48 * st] = b_out[c];
+}
+
+// The exact gate of a flagged component (device erff/expf GELU) from its weights at stride
+// st, shared by both binned passes: returns g, sets gp = dg/dh and go[j] = (GELU,
+// GELU')(z_j).
+__device__ inline float gate_exact(const float* w, int st, float hv, GeluOut* go, float& gp) {
+  float g = w[48 * st];
+  gp = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float wi = w[j * st], wo = w[(32 + j) * st];
+    go[j] = gelu_and_grad<true>(fmaf(wi, hv, w[(16 + j) * st]));
+    g = fmaf(wo, go[j].gelu, g);
+    gp = fmaf(wo * wi, go[j].grad, gp);
+  }
+  return g;
+}
+
+// Moment slot q = 8 mb + m of lane l in a wave's region: float4 (2 mb + m / 4) of lane l,
+// component m % 4 (lane-contiguous 16-byte slots, so a wave's accesses are conflict-free
+// whatever the lanes' bins).
+__device__ inline int mom_index(int q, int lane) { return (((q >> 3) * 2 + ((q >> 2) & 1)) * 64 + lane) * 4 + (q & 3); }
+
+// The bf16 forward with the binned gate: block = 64 components x (FWD_WAVES * 64) tokens;
+// the 64 components' tables sit in LDS as lt[2b + half][lane] (16-byte slots, so a wave's
+// reads are conflict-free whatever the lanes' bins); each wave walks 64 consecutive
+// tokens, one component per lane. Otherwise as k_step_fwd; g is not stored (the backward
+// recomputes it from the same table).
+__global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(
+    const bf16_t* __restrict__ h, const float4* __restrict__ tab, const float4* __restrict__ rng,
+    const float* __restrict__ w_in, const float* __restrict__ b_in, const float* __restrict__ w_out,
+    const float* __restrict__ b_out, StepParams s, bf16_t* __restrict__ acts, float* __restrict__ imp_partial) {
+  __shared__ float4 lt[GATE_TBINS * 2 * 64];
+  __shared__ float wl[49 * 64];  // the components' gate weights, for flagged ones
   __shared__ float red[FWD_WAVES];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t c0 = (int64_t)blockIdx.x * 64;
   const int nc = (int)(s.C - c0 < 64 ? s.C - c0 : 64);
-  for (int i = threadIdx.x; i < nc * KS; i += blockDim.x) lt[i] = tab[c0 * KS + i];
+  for (int i = threadIdx.x; i < 64 * GATE_TBINS * 2; i += blockDim.x)
+    if ((i & 63) < nc) lt[i] = tab[(c0 + (i & 63)) * GATE_TBINS * 2 + (i >> 6)];
+  if (w == 0 && lane < nc) gate_weights_load(c0 + lane, w_in, b_in, w_out, b_out, wl + lane, 64);
   __syncthreads();
   const int64_t c = c0 + lane;
   const int64_t r0 = ((int64_t)blockIdx.y * FWD_WAVES + w) * 64;
@@ -287,9 +355,8 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
   float imp = 0.f, col = 0.f;
   if (c < s.C && r0 < s.T) {
     const float4 rg = rng[c];
-    const float* tl = (const float*)(lt + lane * KS);
+    const bool exact = rg.w != 0.f;
     const int64_t n = s.T * s.C;
-    RowPack<bf16_t> pack;
     // 8 tokens per step: their h loads go out together, then the 8 elements are computed
     for (int64_t t8 = r0; t8 < r1; t8 += 8) {
       float hv8[8];
@@ -299,19 +366,21 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
       for (int e = 0; e < 8; ++e) {
         const int64_t t = t8 + e, i = t * s.C + c;
         const float hv = hv8[e];
-        const float g = gate_eval(tl, (hv - rg.x) * rg.y);
-        g_raw[i] = g;  // the backward's squashing branches see this exact value
+        const GateCoord q = gate_coord(hv, rg);
+        float g = gate_poly(lt[(2 * q.b) * 64 + lane], lt[(2 * q.b + 1) * 64 + lane], q.tau).x;
+        if (exact) {
+          GeluOut go[16];
+          float gp;
+          g = gate_exact(wl + lane, 64, hv, go, gp);
+        }
         const float lo = lower_fwd(g);
         const float iv = step_imp(s, upper_fwd(g));
         imp += iv;
         col += iv;
         const float u = step_uniform_fwd(s, i, n);
         const float m = lo + (1.f - lo) * u;
-        const float a = hv * (m - step_delta(s, t));
-        acts[i] = f32_to_bf16(a);
-        pack.push(a);
+        acts[i] = f32_to_bf16(hv * (m - step_delta(s, t)));
       }
-      pack.flush(actsT + c * s.T + t8);
     }
     if (s.sl0) s.colpart[(r0 / 64) * s.C + c] = col;
   }
@@ -325,43 +394,34 @@ __global__ __launch_bounds__(64 * FWD_WAVES) void k_step_fwd_tab(const bf16_t* _
   }
 }
 
-// Recon residual on a 64x64 tile: e = y + d*yt - yt; partial of e^2; dy = gscale*e
-// written as dy [T, D] and dy^T [D, T].
+// Recon residual on a 64x64 tile: e = y + d*yt - yt; partial of e^2; dy = gscale*e.
 template <typename T>
 __global__ __launch_bounds__(256) void k_step_recon(const T* __restrict__ y, const T* __restrict__ yt, StepParams s,
                                                     int64_t D, float gscale, T* __restrict__ dy,
-                                                    T* __restrict__ dyT, float* __restrict__ partial) {
-  __shared__ float tile[TP][TP + 1];
+                                                    float* __restrict__ partial) {
   __shared__ float sw[4];
   const int64_t r0 = (int64_t)blockIdx.y * TP, c0 = (int64_t)blockIdx.x * TP;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   float acc = 0.f;
   for (int i = ty; i < TP; i += 4) {
     int64_t t = r0 + i, c = c0 + tx;
-    float g = 0.f;
     if (t < s.T && c < D) {
       const int64_t idx = t * D + c;
       const float tv = load_f<T>(yt, idx);
       const float e = load_f<T>(y, idx) + step_delta(s, t) * tv - tv;
       acc = fmaf(e, e, acc);
-      g = gscale * e;
-      store_f<T>(dy, idx, g);
+      store_f<T>(dy, idx, gscale * e);
     }
-    tile[i][tx] = g;
   }
   acc = wave_sum(acc);
   if (tx == 0) sw[ty] = acc;
   __syncthreads();
   if (threadIdx.x == 0) partial[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = sw[0] + sw[1] + sw[2] + sw[3];
-  for (int i = ty; i < TP; i += 4) {
-    int64_t c = c0 + i, t = r0 + tx;
-    if (c < D && t < s.T) store_f<T>(dyT, c * s.T + t, tile[tx][i]);
-  }
 }
 
 // Backward, one component per lane: from da = dy@U^T, h, g_raw and the regenerated u:
 // dh = da*(m-d) + gate pullback of dg_raw, where dg_raw = lower_vjp(g, da*h*(1-u))
-// + upper_vjp(g, imp_scale * d upper^p). Writes dh^T; gate parameter grads go to
+// + upper_vjp(g, imp_scale * d upper^p). Writes dh [T, C]; gate parameter grads go to
 // per-chunk partials [chunk][49][C].
 template <typename T, bool PRECISE>
 __global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da, const T* __restrict__ h,
@@ -369,12 +429,11 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da
                                                         const float* __restrict__ w_in,
                                                         const float* __restrict__ b_in,
                                                         const float* __restrict__ w_out, StepParams s,
-                                                        T* __restrict__ dhT, float* __restrict__ partial) {
+                                                        T* __restrict__ dh, float* __restrict__ partial) {
   const int64_t c = (int64_t)blockIdx.x * SITE_COLS + threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.y * SITE_ROWS;
   const int64_t r1 = r0 + SITE_ROWS < s.T ? r0 + SITE_ROWS : s.T;
   if (c < s.C) {
-    RowPack<T> pack;
     float wi[16], bi[16], wo[16], a_wi[16], a_bi[16], a_wo[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -403,8 +462,7 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da
         a_wo[j] = fmaf(dg, go.gelu, a_wo[j]);
       }
       a_bo += dg;
-      pack.push(dhv);
-      if (((t - r0) % RowPack<T>::N) == RowPack<T>::N - 1) pack.flush(dhT + c * s.T + t + 1 - RowPack<T>::N);
+      store_f<T>(dh, i, dhv);
     }
     float* pp = partial + (int64_t)blockIdx.y * 49 * s.C;
 #pragma unroll
@@ -414,6 +472,259 @@ __global__ __launch_bounds__(SITE_COLS) void k_step_bwd(const T* __restrict__ da
       pp[(int64_t)(32 + j) * s.C + c] = a_wo[j];
     }
     pp[(int64_t)48 * s.C + c] = a_bo;
+  }
+}
+
+// The bf16 backward with the binned gate. Block = BWD_COLS components x BWD_BLOCK_ROWS
+// tokens in BWD_WAVES waves; lane l of wave w takes component l % 32 and token stream
+// 2w + l / 32 (BWD_ROWS consecutive tokens). Per element: g and dg/dh from the table
+// (exactly, for a flagged component), the squashing pullback dg, dh = da (m - d) + dg g'
+// written token-major, and dg T_m(tau_m), m < 8, added into the lane's own LDS slots of its
+// moment bin mb (two 16-byte read-add-writes; one writer per slot and LDS operations of a
+// wave run in order, so the sums are deterministic). A flagged component's lanes keep the
+// 49 exact gate-parameter sums in registers and store them into their first 49 slots at
+// the end. The block then adds its 8 streams per slot in a fixed order: partial[row
+// block][q][c], q < GATE_MOM. LDS: the 32 components' tables (32 KB) and the 4 waves'
+// slots (128 KB).
+__global__ __launch_bounds__(64 * BWD_WAVES) void k_step_bwd_tab(
+    const bf16_t* __restrict__ da, const bf16_t* __restrict__ h, const float4* __restrict__ tab,
+    const float4* __restrict__ rng, const float* __restrict__ w_in, const float* __restrict__ b_in,
+    const float* __restrict__ w_out, const float* __restrict__ b_out, StepParams s, bf16_t* __restrict__ dh,
+    float* __restrict__ partial) {
+  __shared__ float4 lt[GATE_TBINS * 2 * BWD_COLS];
+  __shared__ float4 mom[BWD_WAVES * GATE_MOM / 4 * 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, cl = lane & (BWD_COLS - 1);
+  // XCD-aware block order: workgroups go to the 8 XCDs round-robin by linear id, so the
+  // 4 component groups that share 128-byte lines of h, da (2 groups) and the u bytes (4)
+  // are given 4 consecutive workgroups of one XCD, which then reads each line into its L2
+  // once.
+  const unsigned nbx = gridDim.x, nb = gridDim.x * gridDim.y, p = blockIdx.y * nbx + blockIdx.x;
+  const unsigned lb = (nb % 32 == 0 && nbx % 4 == 0) ? (p / 8 / 4) * 32 + (p % 8) * 4 + (p / 8) % 4 : p;
+  const unsigned bx = lb % nbx, by = lb / nbx;
+  const int64_t c0 = (int64_t)bx * BWD_COLS, c = c0 + cl;
+  const int nc = (int)(s.C - c0 < BWD_COLS ? s.C - c0 : BWD_COLS);
+  for (int i = threadIdx.x; i < BWD_COLS * GATE_TBINS * 2; i += blockDim.x)
+    if ((i & (BWD_COLS - 1)) < nc) lt[i] = tab[(c0 + (i & (BWD_COLS - 1))) * GATE_TBINS * 2 + i / BWD_COLS];
+  float4* my = mom + w * (GATE_MOM / 4) * 64 + lane;
+  for (int q = 0; q < GATE_MOM / 4; ++q) my[q * 64] = make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+  const int64_t r0 = (int64_t)by * BWD_BLOCK_ROWS + (2 * w + (lane >> 5)) * BWD_ROWS;
+  const int64_t r1 = r0 + BWD_ROWS < s.T ? r0 + BWD_ROWS : s.T;
+  if (c < s.C && r0 < s.T) {
+    const float4 rg = rng[c];
+    const bool exact = rg.w != 0.f;
+    const float dtau_dh = 2.f * rg.y;
+    const bool ubyte = s.draw_dtype == PD_DTYPE_BF16;
+    const int64_t n = s.T * s.C;
+    // Loads of 8 tokens; the next 8 tokens' loads are issued before this step's
+    // arithmetic (the last step reloads its own rows).
+    float hv8[8], da8[8], d8[8];
+    uint32_t ub8[8];
+    auto load8 = [&](int64_t t8, float* hv, float* dv, float* dl, uint32_t* ub) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t i = (t8 + e) * s.C + c;
+        hv[e] = bf16_to_f32(h[i]);
+        dv[e] = bf16_to_f32(da[i]);
+        dl[e] = step_delta(s, t8 + e);
+        ub[e] = ubyte ? (uint32_t)s.ubits[i] : 0u;
+      }
+    };
+    load8(r0, hv8, da8, d8, ub8);
+    for (int64_t t8 = r0; t8 < r1; t8 += 8) {
+      float hn[8], dn[8], dln[8];
+      uint32_t ubn[8];
+      load8(t8 + 8 < r1 ? t8 + 8 : t8, hn, dn, dln, ubn);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t t = t8 + e, i = t * s.C + c;
+        const float hv = hv8[e], dav = da8[e];
+        const GateCoord q = gate_coord(hv, rg);
+        const float2 gd = gate_poly(lt[(2 * q.b) * BWD_COLS + cl], lt[(2 * q.b + 1) * BWD_COLS + cl], q.tau);
+        const float g = gd.x, gp = gd.y * dtau_dh;
+        const float lo = lower_fwd(g);
+        float u;
+        if (ubyte)
+          u = (float)ub8[e] * (1.f / 128.f);
+        else
+          u = draw_uniform(s.mk0, s.mk1, i, n, s.draw_dtype, s.layout);
+        const float m = lo + (1.f - lo) * u;
+        const float dg = lower_vjp(g, dav * hv * (1.f - u)) + upper_vjp(g, step_dimp(s, c, upper_fwd(g)));
+        dh[i] = f32_to_bf16(fmaf(dg, gp, dav * (m - d8[e])));  // a flagged lane rewrites it below
+        if (!exact) {
+          // moment bin mb = b / 2 and its coordinate tau_m = s - 2 mb - 1 in [-1, 1]
+          const int mb = q.b >> 1;
+          const float tm = q.s - (float)(2 * mb) - 1.f, t2 = tm + tm;
+          float p[GATE_NC];
+          p[0] = dg;
+          p[1] = dg * tm;
+#pragma unroll
+          for (int k = 2; k < GATE_NC; ++k) p[k] = fmaf(t2, p[k - 1], -p[k - 2]);
+          float4* slot = my + (2 * mb) * 64;
+          float4 a = slot[0], b = slot[64];
+          a.x += p[0];
+          a.y += p[1];
+          a.z += p[2];
+          a.w += p[3];
+          b.x += p[4];
+          b.y += p[5];
+          b.z += p[6];
+          b.w += p[7];
+          slot[0] = a;
+          slot[64] = b;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hv8[e] = hn[e];
+        da8[e] = dn[e];
+        d8[e] = dln[e];
+        ub8[e] = ubn[e];
+      }
+    }
+    if (exact) {
+      // flagged component: the exact gate, element by element, rewriting dh, with the 49
+      // gate-parameter sums in registers, stored into the lane's first 49 slots
+      float wv[49], acc[49];
+      gate_weights_load(c, w_in, b_in, w_out, b_out, wv, 1);
+#pragma unroll
+      for (int k = 0; k < 49; ++k) acc[k] = 0.f;
+      for (int64_t t = r0; t < r1; ++t) {
+        const int64_t i = t * s.C + c;
+        const float hv = bf16_to_f32(h[i]), dav = bf16_to_f32(da[i]);
+        GeluOut go[16];
+        float gp;
+        const float g = gate_exact(wv, 1, hv, go, gp);
+        const float lo = lower_fwd(g);
+        const float u = step_uniform_bwd(s, i, n);
+        const float m = lo + (1.f - lo) * u;
+        const float dg = lower_vjp(g, dav * hv * (1.f - u)) + upper_vjp(g, step_dimp(s, c, upper_fwd(g)));
+        dh[i] = f32_to_bf16(fmaf(dg, gp, dav * (m - step_delta(s, t))));
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float dz = dg * wv[32 + j] * go[j].grad;
+          acc[j] = fmaf(dz, hv, acc[j]);
+          acc[16 + j] += dz;
+          acc[32 + j] = fmaf(dg, go[j].gelu, acc[32 + j]);
+        }
+        acc[48] += dg;
+      }
+      float* mf = (float*)(mom + w * (GATE_MOM / 4) * 64);
+#pragma unroll
+      for (int k = 0; k < 49; ++k) mf[mom_index(k, lane)] = acc[k];
+    }
+  }
+  __syncthreads();
+  // float4 f of a lane's region holds slots 4f .. 4f+3
+  for (int i = threadIdx.x; i < GATE_MOM / 4 * BWD_COLS; i += blockDim.x) {
+    const int f = i / BWD_COLS, cc = i % BWD_COLS;
+    if (cc < nc) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int ww = 0; ww < BWD_WAVES; ++ww) {
+        const float4* r = mom + (ww * (GATE_MOM / 4) + f) * 64;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const float4 a = r[cc + 32 * half];
+          v.x += a.x;
+          v.y += a.y;
+          v.z += a.z;
+          v.w += a.w;
+        }
+      }
+      float* dst = partial + ((int64_t)by * GATE_MOM + 4 * f) * s.C + c0 + cc;
+      dst[0] = v.x;
+      dst[s.C] = v.y;
+      dst[2 * s.C] = v.z;
+      dst[3 * s.C] = v.w;
+    }
+  }
+}
+
+// Gate-parameter gradients from the binned backward's slots. Block = FIN_COLS components;
+// thread = (component, hidden unit j, node quarter). Slots are summed over the row blocks
+// in order. A flagged component's slots hold its exact sums. Otherwise slot (mb, m) holds
+// the Chebyshev moment M_m of moment bin mb; its node weights w_k make 128 virtual tokens
+// (h_v, w_v), and each thread takes the exact pullback (GELU with the A&S 7.1.26 erf,
+// |error| <= 1.5e-7) of the 32 in its quarter; the quarters are added in order. db_out =
+// sum over bins of M_0 = sum_t dg_t.
+static constexpr int FIN_COLS = 4;
+__global__ __launch_bounds__(256) void k_gate_finalize(const float* __restrict__ partial, int64_t nchunk, int64_t C,
+                                                       const float4* __restrict__ rng, const float* __restrict__ w_in,
+                                                       const float* __restrict__ b_in, const float* __restrict__ w_out,
+                                                       float* __restrict__ dw_in, float* __restrict__ db_in,
+                                                       float* __restrict__ dw_out, float* __restrict__ db_out) {
+  __shared__ float M[FIN_COLS][GATE_MOM];
+  __shared__ float Wt[FIN_COLS][GATE_MOM];
+  __shared__ float red[FIN_COLS][16][4][3];
+  // XCD-aware block order: the 8 blocks whose components share 128-byte lines of the
+  // slots are 8 consecutive workgroups of one XCD (workgroups go to XCDs round-robin)
+  const unsigned nb = gridDim.x, p = blockIdx.x;
+  const unsigned lb = nb % 64 == 0 ? (p / 8 / 8) * 64 + (p % 8) * 8 + (p / 8) % 8 : p;
+  const int64_t c0 = (int64_t)lb * FIN_COLS;
+  for (int i = threadIdx.x; i < FIN_COLS * GATE_MOM; i += blockDim.x) {
+    const int cc = i % FIN_COLS, q = i / FIN_COLS;
+    M[cc][q] = c0 + cc < C ? pd_ordered_sum(partial + (int64_t)q * C + c0 + cc, nchunk, (int64_t)GATE_MOM * C) : 0.f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < FIN_COLS * GATE_MOM; i += blockDim.x) {
+    const int cc = i / GATE_MOM, v = i % GATE_MOM, mb = v / GATE_NC, k = v % GATE_NC;
+    const float* mm = &M[cc][mb * GATE_NC];
+    const float xk = kChebNode[k];
+    float t0 = 1.f, t1 = xk, acc = fmaf(xk, mm[1], 0.5f * mm[0]);
+#pragma unroll
+    for (int m = 2; m < GATE_NC; ++m) {
+      const float t2 = fmaf(2.f * xk, t1, -t0);
+      acc = fmaf(t2, mm[m], acc);
+      t0 = t1;
+      t1 = t2;
+    }
+    Wt[cc][v] = 0.25f * acc;
+  }
+  __syncthreads();
+  const int cc = threadIdx.x >> 6, j = (threadIdx.x >> 2) & 15, qq = threadIdx.x & 3;
+  const int64_t c = c0 + cc;
+  const bool live = c < C;
+  const float4 rg = live ? rng[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  float a_wi = 0.f, a_bi = 0.f, a_wo = 0.f;
+  if (live && rg.w == 0.f) {
+    const float wi = w_in[c * 16 + j], bi = b_in[c * 16 + j], wo = w_out[c * 16 + j];
+    const float lo = rg.x, bwm = 2.f * rg.z;
+    for (int v = qq * (GATE_MOM / 4); v < (qq + 1) * (GATE_MOM / 4); ++v) {
+      const int mb = v / GATE_NC, k = v % GATE_NC;
+      const float hv = lo + bwm * ((float)mb + 0.5f + 0.5f * kChebNode[k]);
+      const float wt = Wt[cc][v];
+      const GeluOut go = gelu_and_grad<false>(fmaf(wi, hv, bi));
+      const float dz = wt * wo * go.grad;
+      a_wi = fmaf(dz, hv, a_wi);
+      a_bi += dz;
+      a_wo = fmaf(wt, go.gelu, a_wo);
+    }
+  }
+  red[cc][j][qq][0] = a_wi;
+  red[cc][j][qq][1] = a_bi;
+  red[cc][j][qq][2] = a_wo;
+  __syncthreads();
+  if (!live || qq != 0) return;
+  if (rg.w != 0.f) {
+    a_wi = M[cc][j];
+    a_bi = M[cc][16 + j];
+    a_wo = M[cc][32 + j];
+  } else {
+    a_wi = ((red[cc][j][0][0] + red[cc][j][1][0]) + red[cc][j][2][0]) + red[cc][j][3][0];
+    a_bi = ((red[cc][j][0][1] + red[cc][j][1][1]) + red[cc][j][2][1]) + red[cc][j][3][1];
+    a_wo = ((red[cc][j][0][2] + red[cc][j][1][2]) + red[cc][j][2][2]) + red[cc][j][3][2];
+  }
+  dw_in[c * 16 + j] = a_wi;
+  db_in[c * 16 + j] = a_bi;
+  dw_out[c * 16 + j] = a_wo;
+  if (j == 0) {
+    float a_bo = 0.f;
+    if (rg.w != 0.f)
+      a_bo = M[cc][48];
+    else
+      for (int mb = 0; mb < GATE_MBINS; ++mb) a_bo += M[cc][mb * GATE_NC];
+    db_out[c] = a_bo;
   }
 }
 
@@ -478,12 +789,13 @@ __global__ void k_step_losses(const float* __restrict__ rec_part, int64_t n_rec,
 }
 
 struct StepWorkspace {
-  size_t xT, VT, UT, yt, h, graw, acts, actsT, y, dy, dyT, da, dhT, imp, rec, gate, delta, ubits, rng_part, rng, tab,
-      sl0_col, sl0_slope, sl0_act, sl0_freq, sl0_fb, total;
+  size_t yt, h, graw, acts, y, dy, da, dh, imp, rec, gate, delta, ubits, rng_part, rng, tab, sl0_col, sl0_slope,
+      sl0_act, sl0_freq, sl0_fb, total;
 };
 
 static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_out, int64_t C) {
-  const size_t es = dtype == PD_DTYPE_BF16 ? 2 : 4;
+  const bool bf = dtype == PD_DTYPE_BF16;
+  const size_t es = bf ? 2 : 4;
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   StepWorkspace w{};
   size_t o = 0;
@@ -491,27 +803,23 @@ static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_o
     field = o;
     o += al(bytes);
   };
-  take(w.xT, es * d_in * T);
-  take(w.VT, es * C * d_in);
-  take(w.UT, es * d_out * C);
+  (void)d_in;
   take(w.yt, es * T * d_out);
   take(w.h, es * T * C);
-  take(w.graw, 4 * T * C);
+  take(w.graw, bf ? 0 : 4 * T * C);  // the bf16 step recomputes g from the gate table
   take(w.acts, es * T * C);
-  take(w.actsT, es * C * T);
   take(w.y, es * T * d_out);
   take(w.dy, es * T * d_out);
-  take(w.dyT, es * d_out * T);
   take(w.da, es * T * C);
-  take(w.dhT, es * C * T);
+  take(w.dh, es * T * C);
   take(w.imp, 4 * cdiv(T, SITE_ROWS) * cdiv(C, SITE_COLS));
   take(w.rec, 4 * cdiv(T, TP) * cdiv(d_out, TP));
-  take(w.gate, 4 * cdiv(T, SITE_ROWS) * 49 * C);
+  take(w.gate, bf ? 4 * cdiv(T, BWD_BLOCK_ROWS) * GATE_MOM * C : 4 * cdiv(T, SITE_ROWS) * 49 * C);
   take(w.delta, 4 * T);
   take(w.ubits, (size_t)T * C);
   take(w.rng_part, 8 * cdiv(T, RANGE_ROWS) * C);
   take(w.rng, 16 * C);
-  take(w.tab, 8 * C * (GATE_KNOTS + 1));
+  take(w.tab, 4 * C * GATE_TBINS * GATE_NC);
   take(w.sl0_col, 4 * (size_t)(cdiv(T, 64) + 1) * C);
   take(w.sl0_slope, 4 * (size_t)C);
   take(w.sl0_act, 4 * (size_t)sl0_blocks(1, (int)C));
@@ -519,12 +827,6 @@ static StepWorkspace step_layout(int dtype, int64_t T, int64_t d_in, int64_t d_o
   take(w.sl0_fb, 4 * (size_t)sl0_blocks(1, (int)C));
   w.total = o;
   return w;
-}
-
-template <typename TT>
-static void launch_transpose(const void* src, int64_t R, int64_t Cc, void* dst, hipStream_t s) {
-  hipLaunchKernelGGL(k_transpose<TT>, dim3((unsigned)cdiv(Cc, TP), (unsigned)cdiv(R, TP)), dim3(256), 0, s,
-                     (const TT*)src, R, Cc, (TT*)dst);
 }
 
 // Phase boundaries recorded into caller events (events may be NULL); the phase order
@@ -552,8 +854,8 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   if (T % 8 != 0) return fail(PD_EUNSUPPORTED, "pd_dense_step: T must be a multiple of 8");
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  void *xT = ws + L.xT, *VT = ws + L.VT, *UT = ws + L.UT, *yt = ws + L.yt, *h = ws + L.h, *acts = ws + L.acts;
-  void *actsT = ws + L.actsT, *y = ws + L.y, *dy = ws + L.dy, *dyT = ws + L.dyT, *da = ws + L.da, *dhT = ws + L.dhT;
+  void *yt = ws + L.yt, *h = ws + L.h, *acts = ws + L.acts, *y = ws + L.y, *dy = ws + L.dy, *da = ws + L.da,
+       *dh = ws + L.dh;
   float* graw = (float*)(ws + L.graw);
   float* imp_part = (float*)(ws + L.imp);
   float* rec_part = (float*)(ws + L.rec);
@@ -570,55 +872,46 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
   const dim3 cgrid((unsigned)cdiv(C, SITE_COLS), (unsigned)cdiv(T, SITE_ROWS));
   const dim3 rgrid((unsigned)cdiv(d_out, TP), (unsigned)cdiv(T, TP));
   int rc;
+  float4* rng = (float4*)(ws + L.rng);
+  float4* tab = (float4*)(ws + L.tab);
   PD_MARK(0);
-  if (bf) {
-    launch_transpose<bf16_t>(x, T, d_in, xT, s);
-    launch_transpose<bf16_t>(V, d_in, C, VT, s);
-    launch_transpose<bf16_t>(U, C, d_out, UT, s);
-  } else {
-    launch_transpose<float>(x, T, d_in, xT, s);
-    launch_transpose<float>(V, d_in, C, VT, s);
-    launch_transpose<float>(U, C, d_out, UT, s);
-  }
   if (delta)
     hipLaunchKernelGGL(k_delta_fill, dim3((unsigned)std::min<int64_t>(cdiv(T, 256), 1024)), dim3(256), 0, s, dk0, dk1,
                        T, draw_dtype, layout, delta);
-  if ((rc = check_launch("pd_dense_step transpose"))) return rc;
+  if ((rc = check_launch("pd_dense_step delta"))) return rc;
   PD_MARK(1);
   if ((rc = pd_gemm(dtype, T, d_out, d_in, x, d_in, 0, W, d_in, 1, yt, d_out, dtype, 1.f, 0.f, stream))) return rc;
   PD_MARK(2);
-  if ((rc = pd_gemm(dtype, T, C, d_in, x, d_in, 0, VT, d_in, 1, h, C, dtype, 1.f, 0.f, stream))) return rc;
+  if ((rc = pd_gemm(dtype, T, C, d_in, x, d_in, 0, V, C, 0, h, C, dtype, 1.f, 0.f, stream))) return rc;
   PD_MARK(3);
   const dim3 fgrid((unsigned)cdiv(C, 64), (unsigned)cdiv(T, 64 * FWD_WAVES));
   if (bf) {
     float2* rng_part = (float2*)(ws + L.rng_part);
-    float4* rng = (float4*)(ws + L.rng);
-    float2* tab = (float2*)(ws + L.tab);
     const int nchunk = (int)cdiv(T, RANGE_ROWS);
     hipLaunchKernelGGL(k_gate_range, dim3((unsigned)cdiv(C, 64), (unsigned)nchunk), dim3(256), 0, s, (const bf16_t*)h,
                        T, C, rng_part);
-    hipLaunchKernelGGL(k_gate_table, dim3((unsigned)cdiv(C * (GATE_KNOTS + 1), 256)), dim3(256), 0, s, rng_part,
-                       nchunk, C, w_in, b_in, w_out, b_out, tab, rng);
-    hipLaunchKernelGGL(k_step_fwd_tab, fgrid, dim3(64 * FWD_WAVES), 0, s, (const bf16_t*)h, tab, rng, sp, graw,
-                       (bf16_t*)acts, (bf16_t*)actsT, imp_part);
+    hipLaunchKernelGGL(k_gate_table, dim3((unsigned)cdiv(C * GATE_TBINS, 256)), dim3(256), 0, s, rng_part, nchunk, C,
+                       w_in, b_in, w_out, b_out, (float*)tab, rng);
+    hipLaunchKernelGGL(k_step_fwd_tab, fgrid, dim3(64 * FWD_WAVES), 0, s, (const bf16_t*)h, (const float4*)tab,
+                       (const float4*)rng, w_in, b_in, w_out, b_out, sp, (bf16_t*)acts, imp_part);
   } else
     hipLaunchKernelGGL((k_step_fwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)h, w_in, b_in, w_out,
-                       b_out, sp, graw, (float*)acts, (float*)actsT, imp_part);
+                       b_out, sp, graw, (float*)acts, imp_part);
   if (sl0)  // per-component frequencies, loss partials and backward slopes
     hipLaunchKernelGGL(k_sl0_finalize, dim3(sl0_blocks(1, (int)C)), dim3(256), 0, s, sp.colpart,
                        (const int32_t*)nullptr, 1, T, (int)C, 1.f / (float)T, imp.coeff, imp.freq_coeff, imp.ref_count,
                        imp.ema, sl0_slope, sl0_act, sl0_freq, sl0_fb);
   if ((rc = check_launch("pd_dense_step fwd"))) return rc;
   PD_MARK(4);
-  if ((rc = pd_gemm(dtype, T, d_out, C, acts, C, 0, UT, C, 1, y, d_out, dtype, 1.f, 0.f, stream))) return rc;
+  if ((rc = pd_gemm(dtype, T, d_out, C, acts, C, 0, U, d_out, 0, y, d_out, dtype, 1.f, 0.f, stream))) return rc;
   PD_MARK(5);
   const float gscale = recon_coeff * 2.f / (float)(T * d_out);
   if (bf)
     hipLaunchKernelGGL(k_step_recon<bf16_t>, rgrid, dim3(256), 0, s, (const bf16_t*)y, (const bf16_t*)yt, sp, d_out,
-                       gscale, (bf16_t*)dy, (bf16_t*)dyT, rec_part);
+                       gscale, (bf16_t*)dy, rec_part);
   else
     hipLaunchKernelGGL(k_step_recon<float>, rgrid, dim3(256), 0, s, (const float*)y, (const float*)yt, sp, d_out,
-                       gscale, (float*)dy, (float*)dyT, rec_part);
+                       gscale, (float*)dy, rec_part);
   if ((rc = check_launch("pd_dense_step recon"))) return rc;
   PD_MARK(6);
   const int64_t n_imp = bf ? (int64_t)fgrid.x * fgrid.y : (int64_t)cgrid.x * cgrid.y;
@@ -633,24 +926,29 @@ static int dense_step_impl(int dtype, int64_t T, int64_t d_in, int64_t d_out, in
                        1.0 / (double)T,
                        recon_coeff, imp.coeff, 0.f, losses);
   PD_MARK(7);
-  if ((rc = pd_gemm(dtype, C, d_out, T, actsT, T, 0, dyT, T, 1, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
+  if ((rc = pd_gemm(dtype, C, d_out, T, acts, C, 1, dy, d_out, 0, dU, d_out, PD_DTYPE_F32, 1.f, 0.f, stream)))
     return rc;
   PD_MARK(8);
   if ((rc = pd_gemm(dtype, T, C, d_out, dy, d_out, 0, U, d_out, 1, da, C, dtype, 1.f, 0.f, stream))) return rc;
   PD_MARK(9);
+  const dim3 bgrid((unsigned)cdiv(C, BWD_COLS), (unsigned)cdiv(T, BWD_BLOCK_ROWS));
   if (bf)
-    hipLaunchKernelGGL((k_step_bwd<bf16_t, false>), cgrid, dim3(SITE_COLS), 0, s, (const bf16_t*)da, (const bf16_t*)h,
-                       graw, w_in, b_in, w_out, sp, (bf16_t*)dhT, gate_part);
+    hipLaunchKernelGGL(k_step_bwd_tab, bgrid, dim3(64 * BWD_WAVES), 0, s, (const bf16_t*)da, (const bf16_t*)h,
+                       (const float4*)tab, (const float4*)rng, w_in, b_in, w_out, b_out, sp, (bf16_t*)dh, gate_part);
   else
     hipLaunchKernelGGL((k_step_bwd<float, true>), cgrid, dim3(SITE_COLS), 0, s, (const float*)da, (const float*)h,
-                       graw, w_in, b_in, w_out, sp, (float*)dhT, gate_part);
+                       graw, w_in, b_in, w_out, sp, (float*)dh, gate_part);
   if ((rc = check_launch("pd_dense_step bwd"))) return rc;
   PD_MARK(10);
-  hipLaunchKernelGGL(k_step_gate_reduce, dim3((unsigned)cdiv(49 * C, 256)), dim3(256), 0, s, gate_part,
-                     (int64_t)cgrid.y, C, dw_in, db_in, dw_out, db_out);
+  if (bf)
+    hipLaunchKernelGGL(k_gate_finalize, dim3((unsigned)cdiv(C, FIN_COLS)), dim3(256), 0, s, gate_part, (int64_t)bgrid.y, C,
+                       (const float4*)rng, w_in, b_in, w_out, dw_in, db_in, dw_out, db_out);
+  else
+    hipLaunchKernelGGL(k_step_gate_reduce, dim3((unsigned)cdiv(49 * C, 256)), dim3(256), 0, s, gate_part,
+                       (int64_t)cgrid.y, C, dw_in, db_in, dw_out, db_out);
   if ((rc = check_launch("pd_dense_step gate reduce"))) return rc;
   PD_MARK(11);
-  if ((rc = pd_gemm(dtype, d_in, C, T, xT, T, 0, dhT, T, 1, dV, C, PD_DTYPE_F32, 1.f, 0.f, stream))) return rc;
+  if ((rc = pd_gemm(dtype, d_in, C, T, x, d_in, 1, dh, C, 0, dV, C, PD_DTYPE_F32, 1.f, 0.f, stream))) return rc;
   PD_MARK(12);
   return PD_OK;
 #undef PD_MARK

@@ -58,7 +58,7 @@ class DenseSiteStep:
         nbytes = L.load().pd_dense_step_workspace_size(self.dt, T, d_in, d_out, C, H)
         self.workspace = L.workspace(nbytes, dev)
 
-    PHASES = ("transpose_inputs", "gemm_target", "gemm_xV", "gate_mask_fwd", "gemm_actsU", "recon", "loss_final",
+    PHASES = ("delta_draw", "gemm_target", "gemm_xV", "gate_mask_fwd", "gemm_actsU", "recon", "loss_final",
               "gemm_dU", "gemm_da", "gate_mask_bwd", "gate_grad_reduce", "gemm_dV")
 
     def step(self, x, W, V, U, gate, mask_key: Key, delta_key: Key, *, events=None) -> DenseStepGrads:

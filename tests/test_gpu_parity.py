@@ -477,6 +477,41 @@ def test_dense_step_matches_oracle(device, dtype, use_delta, sl0):
         assert_close(np64(got), want, rtol, floor, name)
 
 
+def test_dense_step_bf16_exact_gate_components(device):
+    """The bf16 step's binned gate falls back to the exact per-element gate for components
+    with a hidden unit wider than 3 in z over one moment bin. Four components get w_in x8
+    (two share a 32-component block with unflagged ones, so flagged and unflagged lanes run
+    in one wave); the whole step must still match the oracle at the bf16 tolerance."""
+    from param_decomp_amd.dense_step import DenseSiteStep
+
+    rng = np.random.default_rng(21)
+    T, d_in, d_out, C = 256, 64, 96, 192
+    x, W, V, U, gp = _dense_inputs(rng, T, d_in, d_out, C)
+    wide = [0, 5, 33, 100]
+    gp.w_in[wide] *= 8.0
+    tx, tW, tV, tU = (bf(a, device) for a in (x, W, V, U))
+    gate = tuple(f32(a, device) for a in (gp.w_in, gp.b_in, gp.w_out, gp.b_out))
+    # which components the step flags (moment-bin width = range(h) / 16)
+    h = np64(tx) @ np64(tV)
+    dz = np.abs(np64(gate[0])).max(1) * (h.max(0) - h.min(0)) / 16
+    assert (dz[wide] > 4).all() and (np.delete(dz, wide) < 2.5).all(), dz
+    draw_key = tf.fold_in(tf.prng_key(9), 1)
+    step = DenseSiteStep(T, d_in, d_out, C, dtype=torch.bfloat16, device=device, recon_coeff=1.3, use_delta=True)
+    mk, dk = step.site_keys(draw_key, 0)
+    g = step.step(tx, tW, tV, tU, gate, mk, dk)
+    torch.cuda.synchronize()
+    gp64 = po.GateParams(*(np64(t) for t in gate))
+    r = po.dense_site_step(np64(tx), np64(tW), np64(tV), np64(tU), gp64, draw_key, recon_coeff=1.3,
+                           mask_dtype="bfloat16", use_delta=True, bf16_storage=True)
+    np.testing.assert_allclose(g.losses.cpu().numpy(), [r.loss, r.recon, r.imp, r.freq], rtol=BF16_RTOL, atol=1e-7)
+    assert_close(np64(g.dU), r.dU, BF16_RTOL, 1e-2, "dU")
+    assert_close(np64(g.dV), r.dV, BF16_RTOL, 1e-2, "dV")
+    for got, want, name in zip((g.dw_in, g.db_in, g.dw_out, g.db_out), r.dgate, ("dw_in", "db_in", "dw_out", "db_out")):
+        assert_close(np64(got), want, BF16_RTOL, 1e-2, name)
+        # the flagged components alone, at their own scale
+        assert_close(np64(got)[wide], want[wide], BF16_RTOL, 1e-2, name + "[flagged]")
+
+
 def test_dense_step_full_size_properties(device):
     """At the full single-linear shape (T=4096, 768->3072, C=4096): the step is
     deterministic run to run, losses are finite and positive, and the gradient of
