@@ -222,17 +222,12 @@ def pmc_traffic_summary(outdir: str, workloads) -> str:
     import csv
 
     def load(path):
-        """{label: {counter: [per-dispatch values]}}; a kernel launched with several grid
-        sizes (one GEMM template serving several phases) gets one row per grid, labelled
-        `name @work-items`."""
-        rows = list(csv.DictReader(open(os.path.join(outdir, path, "run_counter_collection.csv"))))
-        grids = collections.defaultdict(set)
-        for r in rows:
-            grids[r["Kernel_Name"].split("(")[0].replace("void ", "")].add(r["Grid_Size"])
+        """{label: {counter: [per-dispatch values]}}; a GEMM kernel (one template serves
+        several phases) gets one row per grid size, labelled `name @work-items`."""
         agg = collections.defaultdict(lambda: collections.defaultdict(list))
-        for r in rows:
+        for r in csv.DictReader(open(os.path.join(outdir, path, "run_counter_collection.csv"))):
             k = r["Kernel_Name"].split("(")[0].replace("void ", "")
-            if len(grids[k]) > 1:
+            if k.startswith("pd::k_gemm"):
                 k = f"{k} @{r['Grid_Size']}"
             agg[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
         return agg
@@ -336,21 +331,21 @@ PHASE_KERNEL = {
                            "pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 1, false, "
                            "pd::EpiMaskBwd"),
           "mask_fwd": ("pd::k_mask_fwd_tile",), "mask_bwd": ("pd::k_mask_bwd_tile", "pd::k_mask_bwd_vec")},
-    # dense GEMM phases by template and grid (work-items of 128x128 tiles x 512 threads at
-    # T 4096, 768 -> 3072, C 4096)
+    # dense GEMM phases by template and grid (work-items: tiles x 512 threads at T 4096,
+    # 768 -> 3072, C 4096; the 4096 x 4096 products run on 256x256 tiles)
     DENSE: {"gate_mask_fwd": ("pd::k_step_fwd_tab", "pd::k_gate_range", "pd::k_gate_table"),
             "gate_mask_bwd": ("pd::k_step_bwd",), "gate_grad_reduce": ("pd::k_gate_finalize",),
             "recon": ("pd::k_step_recon",),
             "gemm_target": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
                             "pd::EpiStore, false, false> @393216",),
-            "gemm_xV": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
-                        "pd::EpiStore, false, true> @524288",),
+            "gemm_xV": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, unsigned short, 0, false, "
+                        "pd::EpiStore, false, true> @131072",),
             "gemm_actsU": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
                            "pd::EpiStore, false, true> @393216",),
             "gemm_dU": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 0, false, "
                         "pd::EpiStore, true, true> @393216",),
-            "gemm_da": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, unsigned short, 0, false, "
-                        "pd::EpiStore, false, false> @524288",),
+            "gemm_da": ("pd::k_gemm_dtl<pd::DtlCfg<256, 256, 4, 2, 2, false>, unsigned short, 0, false, "
+                        "pd::EpiStore, false, false> @131072",),
             "gemm_dV": ("pd::k_gemm_dtl<pd::DtlCfg<128, 128, 4, 2, 2, true>, float, 0, false, "
                         "pd::EpiStore, true, true> @98304",)},
 }

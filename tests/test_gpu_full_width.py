@@ -5,8 +5,8 @@ those workloads select is compared against the oracle, not only checked for fini
   256x256 grouped tiles of the N=512 component products (`grouped_gemm_pair`) and of
   every paired weight gradient (`grouped_gemm_dw_kmajor_pair`), K=512 main loops over
   several k stages, and ragged per-expert contraction lengths;
-- the register-staged 256x256 dense tile (`k_gemm_bf16` on `TileCfg<256,256>`, taken
-  for operands that are not both K-contiguous once the grid has >= 192 such tiles);
+- the dense products' 256x256 buffer-fed tile (`CfgDtlBig`, taken once the grid has >= 256
+  such tiles) in every operand layout, and the 128x128 one just below that size;
 - the public grouped products at K = N = 512 with ragged and empty groups;
 - the LM stack at the Llama-4L widths (the streamed KL's dual products at V = 50277) and
   the dense step at 768 -> 3072, C = 4096.
@@ -94,13 +94,13 @@ def test_moe_stack_step_full_width_matches_oracle(device):
             _close(got[si], ref["d_ci_pre"][l][s], BF16_RTOL, 1e-2, f"d_ci_pre[{l}][{s}]")
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 3072, 768), (4000, 3000, 776)])
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (1, 1)])
-def test_gemm_register_staged_big_tile(device, ta, tb, M, N, K):
-    """The dense site's shapes with operand layouts the buffer-fed kernel does not take
-    (it needs both operands K-contiguous: ta=0, tb=1): >= 192 256x256 tiles select the
-    register-staged 256x256 kernel. fp32 output within fp32 accumulation-order error of
-    a float64 product; bf16 output within bf16 rounding."""
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 768), (4096, 4096, 776), (4000, 4104, 200)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_big_tile_layouts(device, ta, tb, M, N, K):
+    """The dense site's shapes in every operand layout: 192 256x256 tiles stay on the
+    128x128 buffer-fed kernel; >= 256 (one per CU) select the 256x256 one, here with a
+    k-tail stage and ragged M and N edges. fp32 output within fp32 accumulation-order
+    error of a float64 product; bf16 output within bf16 rounding."""
     from param_decomp_amd import ops
 
     assert -(-M // 256) * -(-N // 256) >= 192
