@@ -1815,8 +1815,8 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
   // it next overwrites one of those inputs, and before it returns. Nothing on this stream
   // reads a weight gradient.
   bool wpend[4] = {false, false, false, false};
-  auto wgrad = [&](int i, auto&& product) -> int {
-    if (!cs.st) return product((void*)s);
+  auto wgrad = [&](int i, auto&& product, bool on_caller = false) -> int {
+    if (!cs.st || on_caller) return product((void*)s);
     hipEventRecord(cs.wg_in[i], s);
     hipStreamWaitEvent(cs.st, cs.wg_in[i], 0);
     const int r = product((void*)cs.st);
@@ -1954,11 +1954,16 @@ static int moe_step_impl(int64_t T, int d, int f, int E, int k, int c, int L, co
       if (!fuse_gu) launch_mask_bwd(mg[si], pm, tile_grid(J, c), s, S.h[si], S.ub[si], imp_scale, P.d_acts[si], dpre[si]);
       src_grads(si, si == 0 ? P.d_g : P.d_u, si == 0 ? S.fg : S.fu, f);
     }
+    // layer 0's gate / up dV products are the step's last work: this stream has nothing
+    // else left, so they run here, beside the helper's dU products, instead of after them
     rec.mark(MOE_CAT_GEMM_DW);
-    if (want_wgrads && (rc = wgrad(3, [&](void* st) {
-                          return grouped_gemm_dw_pair(S.xj, P.d_acts[0], dVg + l * szVg, S.xj, P.d_acts[1],
-                                                      dVu + l * szVg, S.offsets, J, E, d, c, PD_DTYPE_F32, st);
-                        })))
+    if (want_wgrads && (rc = wgrad(
+                            3,
+                            [&](void* st) {
+                              return grouped_gemm_dw_pair(S.xj, P.d_acts[0], dVg + l * szVg, S.xj, P.d_acts[1],
+                                                          dVu + l * szVg, S.offsets, J, E, d, c, PD_DTYPE_F32, st);
+                            },
+                            l == 0)))
       return rc;
     // The stack input carries no parameter gradient: layer 0 stops at its weight
     // gradients (its gate/up input products and the token backward feed only d x0).
