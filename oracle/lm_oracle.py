@@ -252,8 +252,9 @@ def site(x, W, V=None, U=None, mask=None, delta=None, rb=lambda t: t, route=None
     if delta is None:
         out = rb(acts @ U)
     else:
-        # d * (x @ W^T) = (d * x) @ W^T per row: one accumulation with acts @ U, d * x stored bf16
-        out = rb(acts @ U + rb(delta[..., None] * x) @ W.T)
+        # d * (x @ W^T) scales its own fp32 accumulation before acts @ U joins it: one
+        # rounding of the sum, and neither d * x nor its cotangent d * g is stored
+        out = rb(acts @ U + delta[..., None] * (x @ W.T))
     if route is None:
         return out
     return torch.where(torch.as_tensor(route, dtype=torch.bool)[..., None], out, rb(x @ W.T))

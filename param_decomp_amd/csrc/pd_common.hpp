@@ -72,6 +72,9 @@ int gemm_batched_causal(int causal, int dtype, int64_t batch, int64_t M, int64_t
                         int trans_b, void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
                         void* stream);
 size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K);
+// The same for any operand layouts (trans_a / trans_b as pd_gemm's).
+int gemm_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B, int64_t ldb,
+                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream);
 int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
                    int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream);
 

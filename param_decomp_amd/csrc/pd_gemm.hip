@@ -1,10 +1,12 @@
 // GEMM kernels for the masked-component path (gfx950), v_mfma_f32_32x32x16_bf16.
 //
-// Both operands K-contiguous (every hot-path product): the buffer-fed kernel of
-// pd_gemm_dtl.hpp, 128x128x64 tiles, 8 waves of 32x64, operands loaded straight into
-// LDS, two stages, two blocks per CU.
+// bf16 products run on the buffer-fed kernel of pd_gemm_dtl.hpp in every operand layout
+// (an MN-contiguous operand is transposed on its way out of LDS): 128x128x64 tiles, 8
+// waves of 32x64, two stages, two blocks per CU; 256x256 tiles (one block per CU) once the
+// grid has at least 256 of them.
 //
-// Any other operand layout: the register-staged kernel below. LDS holds both operands
+// Operands beyond the buffer kernel's 31-bit addressing: the register-staged kernel
+// below. LDS holds both operands
 // K-contiguous ([rows][BK+8]; the 144-byte row stride makes a wave's 16-byte fragment
 // reads of 16 consecutive rows hit 16 distinct 4-bank groups); an operand whose global
 // layout is MN-contiguous is transposed in registers (4 k-rows x 8 elements per thread)
@@ -726,19 +728,21 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
   }
 }
 
-int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
-                   int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream) {
+int gemm_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B, int64_t ldb,
+                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream) {
   const int64_t kc = splitk_slice(M, N, K);
   if (!kc || N % 4 || ldc % 4 || !aligned16(C))
-    return pd_gemm(PD_DTYPE_BF16, M, N, K, A, lda, 0, Bt, ldb, 1, C, ldc, c_dtype, 1.f, beta, stream);
-  if (!bf16_operand_ok(A, lda, K) || !bf16_operand_ok(Bt, ldb, K) || !dtl_fits(M, lda, N, ldb))
-    return fail(PD_EUNSUPPORTED, "gemm_nt_splitk: operands");
+    return pd_gemm(PD_DTYPE_BF16, M, N, K, A, lda, trans_a, B, ldb, trans_b, C, ldc, c_dtype, 1.f, beta, stream);
+  const bool a_kmaj = !trans_a, b_kmaj = trans_b;
+  if (!bf16_operand_ok(A, lda, a_kmaj ? K : M) || !bf16_operand_ok(B, ldb, b_kmaj ? K : N) ||
+      !dtl_fits_any(M, N, K, lda, a_kmaj, ldb, b_kmaj))
+    return fail(PD_EUNSUPPORTED, "gemm_splitk: operands");
   const int splits = (int)cdiv(K, kc);
-  if (!ws || ws_bytes < (size_t)splits * M * N * sizeof(float)) return fail(PD_EWORKSPACE, "gemm_nt_splitk: scratch");
+  if (!ws || ws_bytes < (size_t)splits * M * N * sizeof(float)) return fail(PD_EWORKSPACE, "gemm_splitk: scratch");
   hipStream_t s = (hipStream_t)stream;
-  GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)Bt, ldb, ws, N, 1.f, 0.f, nullptr, 0, 0, M * N, kc};
+  GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, ws, N, 1.f, 0.f, nullptr, 0, 0, M * N, kc};
   const dim3 grid((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)splits);
-  int rc = launch_dtl<CfgDtlRA, MODE_SPLITK>(a, PD_DTYPE_F32, K % CfgDtlRA::BK != 0, grid, s);
+  int rc = launch_dtl_any<CfgDtlRA, MODE_SPLITK>(a, a_kmaj, b_kmaj, PD_DTYPE_F32, K % CfgDtlRA::BK != 0, grid, s);
   if (rc) return rc;
   const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(M * N / 4, 256), 8192));
   if (c_dtype == PD_DTYPE_F32)
@@ -747,7 +751,12 @@ int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, 
   else
     hipLaunchKernelGGL(k_splitk_reduce<bf16_t>, dim3(blocks), dim3(256), 0, s, (const float*)ws, M, N, splits,
                        (bf16_t*)C, ldc, beta);
-  return check_launch("gemm_nt_splitk reduce");
+  return check_launch("gemm_splitk reduce");
+}
+
+int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
+                   int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream) {
+  return gemm_splitk(M, N, K, A, lda, 0, Bt, ldb, 1, C, ldc, c_dtype, beta, ws, ws_bytes, stream);
 }
 
 int grouped_gemm_pair(const void* lhs1, const void* rhsT1, void* out1, const void* lhs2, const void* rhsT2, void* out2,

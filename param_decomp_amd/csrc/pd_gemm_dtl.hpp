@@ -867,7 +867,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
 // k loop runs over A1's K1 columns, then A2's K2 (p.K), with rs, the per-row scale of
 // the first product, applied to the accumulators in between. Every lane's 16 accumulators
 // of a 32x32 MFMA tile sit in one output row, so the scale is one multiply per register.
-// rs(t) = routed(t) ? (delta ? delta[t] : 0) : 1, routed(t) = !route || route[t]: the
+// rs(t) = routed(t) ? (delta ? delta[t] : 0) : 1, routed(t) = !route || route[t] (delta
+// bf16, or fp32 through delta_f): the
 // blend weight of the target output x @ W^T in the masked linear (and of its cotangent).
 // A1 and A2 are K-contiguous; B1MN / B2MN: the B operand is MN-major. The LDS stage ring
 // runs straight through the segment boundary, so the second product's first stages
@@ -892,6 +893,7 @@ struct KcatArgs {
   const float* rs_tok2 = nullptr;
   const int32_t* sort_idx = nullptr;
   int k = 1;
+  const float* delta_f = nullptr;  // fp32 per-row delta (dense mode; preferred over `delta`)
 };
 
 template <class CFG, typename TC, bool B1MN, bool B2MN, class EPI = EpiStore, int MODE = MODE_DENSE>
@@ -987,7 +989,8 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_kcat(GemmArgs p, KcatArgs 
     const int64_t row = m0 + wm * CFG::WTM + i * 32 + (lane & 31);
     float rs = 1.f;
     if (rs_tok) rs = row < t.M ? rs_tok[q.sort_idx[row] / q.k] : 0.f;
-    else if (row < p.M && (!q.route || q.route[row])) rs = q.delta ? bf16_to_f32(q.delta[row]) : 0.f;
+    else if (row < p.M && (!q.route || q.route[row]))
+      rs = q.delta_f ? q.delta_f[row] : (q.delta ? bf16_to_f32(q.delta[row]) : 0.f);
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -1034,8 +1037,16 @@ inline int launch_kcat_epi(const GemmArgs& a, const KcatArgs& q, const typename 
     return fail(PD_EUNSUPPORTED, std::string(what) + ": operands of 2 GiB or more");
   if ((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM > 65535 || (a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN > 65535)
     return fail(PD_EUNSUPPORTED, std::string(what) + ": too large");
-  const dim3 grid((unsigned)((a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN), (unsigned)((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM));
-  hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlRA, TC, B1MN, B2MN, EPI>), grid, dim3(CfgDtlRA::NT), 0, s, a, q, ea);
+  // 256x256 tiles once the grid has at least 256 of them (pd_gemm's rule)
+  const int64_t gbx = (a.N + CfgDtlBig::BN - 1) / CfgDtlBig::BN, gby = (a.M + CfgDtlBig::BM - 1) / CfgDtlBig::BM;
+  if (EPI::LDS_BYTES <= 2 * CfgDtlBig::STAGE_BYTES && gbx * gby >= 256)
+    hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlBig, TC, B1MN, B2MN, EPI>), dim3((unsigned)gbx, (unsigned)gby),
+                       dim3(CfgDtlBig::NT), 0, s, a, q, ea);
+  else
+    hipLaunchKernelGGL((k_gemm_dtl_kcat<CfgDtlRA, TC, B1MN, B2MN, EPI>),
+                       dim3((unsigned)((a.N + CfgDtlRA::BN - 1) / CfgDtlRA::BN),
+                            (unsigned)((a.M + CfgDtlRA::BM - 1) / CfgDtlRA::BM)),
+                       dim3(CfgDtlRA::NT), 0, s, a, q, ea);
   return check_launch(what);
 }
 

@@ -12,15 +12,19 @@
 // preactivations (the attention is frozen: gradients flow through it).
 //
 // Layouts: activations row-major [N = B*T, width] bf16. Every product runs on the
-// buffer-fed MFMA kernel with both operands K-contiguous:
-//   x @ V            B^T = V^T [C, d_in]                     (per-step transposed copy)
-//   out              [acts | d*x] @ [U ; W^T]: one product over K = C + d_in, its B^T =
-//                    [U^T | W] [d_out, C + d_in] (per-step copy); the weight-delta blend
-//                    d * (x @ W^T) rides in the same accumulation
-//   d_acts           g @ U^T: B^T = U as stored
-//   dU = acts^T g    A = acts^T [C, N] (written by the mask pass), B^T = g^T [d_out, N]
-//   dV = x^T dxV     A = x^T [d_in, N], B^T = dxV^T [C, N] (written by the mask pass)
-//   d_input          [dxV | d*g] @ [V^T ; W]: B^T = [V | W^T] [d_in, C + d_out]
+// buffer-fed MFMA kernel. The weights are read K-contiguous (an MN-contiguous operand
+// costs the product 6-20% here), from per-step transposed copies made by one batched
+// launch per (kind, matrix) for all layers; activations are read as stored, MN-contiguous
+// where the contraction runs over tokens:
+//   x @ V            B = V^T [C, d_in] (copy)
+//   out              s (.) (x @ W^T) + acts @ U in one two-segment product (W as stored,
+//                    U^T [d_out, C] copy), s = d on routed rows and 1 on the rest
+//   d_acts           g @ U^T: U as stored
+//   dU = acts^T g    A = acts [N, C] (MN-major), B = g^T [d_out, N] (a per-call copy the
+//                    helper stream reads while this stream moves on)
+//   dV = x^T dxV     A = x [N, d_in], B = dxV [N, C] (both MN-major)
+//   d_input          s (.) (g @ W) + dxV @ V^T in one two-segment product (W^T [d_in,
+//                    d_out] copy, V as stored)
 // Attention is materialized per (batch, head) at hd = 64: S = Q K^T (fp32), causal softmax
 // to bf16 P, O = P V; the backward forms dP, dS = P (dP - rowsum(P dP)) / sqrt(hd), dQ = dS K,
 // dK = dS^T Q, dV = P^T dO. It is about 1% of the step's work at the benchmark shape.
@@ -28,6 +32,7 @@
 #include <vector>
 
 #include "pd_common.hpp"
+#include "pd_gemm_dtl.hpp"
 #include "pd_impmin.hpp"
 
 namespace pd {
@@ -143,28 +148,28 @@ __global__ __launch_bounds__(256) void k_lm_transpose(const bf16_t* __restrict__
   ttile_store(Tt, dst, ld, r0, R, c0, Cc, tid);
 }
 
-// dst[r * ld + c] = sc[r] * src[r * w + c] for r < R, c < w: sc = s[r] (0 when s is NULL)
-// on routed rows and 1 on rows whose route is 0 (route NULL: every row routed); with
-// neither s nor route, a plain copy. w % 8 == 0, ld % 8 == 0. One wave per row.
-__global__ __launch_bounds__(256) void k_lm_copy_rows(const bf16_t* __restrict__ src, int64_t R, int w,
-                                                      const float* __restrict__ s,
-                                                      const uint8_t* __restrict__ route, bf16_t* __restrict__ dst,
-                                                      int64_t ld) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + wave_id();
-  if (r >= R) return;
-  const bool scaled = s || route;
-  const float sc = route && !route[r] ? 1.f : (s ? s[r] : (route ? 0.f : 1.f));
-  for (int i = (threadIdx.x & 63) * 8; i < w; i += 512) {
-    if (scaled) {
-      float v[8];
-      load8(src + r * w + i, v);
+// dst[b] = src[b]^T, b = blockIdx.z, for [R, Cc] matrices (R, Cc multiples of 8).
+__global__ __launch_bounds__(256) void k_lm_transpose_b(const bf16_t* __restrict__ src, int64_t R, int64_t Cc,
+                                                        bf16_t* __restrict__ dst) {
+  __shared__ TTile Tt;
+  const int64_t b = blockIdx.z;
+  const bf16_t* sb = src + b * R * Cc;
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const int tid = threadIdx.x, c8 = (tid & 7) * 8;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] *= sc;
-      store8(dst + r * ld + i, v);
-    } else {
-      *(uint4*)(dst + r * ld + i) = *(const uint4*)(src + r * w + i);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int r = (tid >> 3) + 32 * pass;
+    uint4 v = {0, 0, 0, 0};
+    if (r0 + r < R && c0 + c8 < Cc) v = *(const uint4*)(sb + (r0 + r) * Cc + c0 + c8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Tt.v[c8 + 2 * e][r] = (bf16_t)(w[e] & 0xFFFFu);
+      Tt.v[c8 + 2 * e + 1][r] = (bf16_t)(w[e] >> 16);
     }
   }
+  __syncthreads();
+  ttile_store(Tt, dst + b * R * Cc, R, r0, R, c0, Cc, tid);
 }
 
 // Per-token delta draws of every (layer, kind): delta[(l * 6 + k) * N + n] =
@@ -214,15 +219,14 @@ struct LMMaskArgs {
 #define PD_LM_COL ((threadIdx.x & 15) * 4)
 
 // m = lower(ci) + (1 - lower(ci)) u (u drawn in bf16 over [N, C], counter n*C + c);
-// acts = bf16(xV * (m - d)) into acts[n * ld + c] and acts^T [C, N] (0 on unrouted tokens,
+// acts = bf16(xV * (m - d)) into acts[n * ld + c] (0 on unrouted tokens,
 // whose output is the target's x @ W^T, pd/core/decomposed_linear.py:72-85); u kept as its
 // 7-bit integer; per-block partial of upper(ci)^p. C % 8 == 0, N % 8 == 0. LAYOUT ==
 // MASK_SRC reads u from the source table instead (u = bf16(src[n / rps, c])), no u bytes.
 template <int LAYOUT, int PM>
 __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
-                                                     bf16_t* __restrict__ acts, bf16_t* __restrict__ actsT,
-                                                     uint8_t* __restrict__ ubits, float* __restrict__ imp_part) {
-  __shared__ TTile Tt;
+                                                     bf16_t* __restrict__ acts, uint8_t* __restrict__ ubits,
+                                                     float* __restrict__ imp_part) {
   __shared__ float red[4];
   __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
   const int tid = threadIdx.x;
@@ -267,8 +271,6 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
 #pragma unroll
       for (int e = 0; e < 4; ++e) SLv.ps[r][q4 + e] = 0.f;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
   }
   if constexpr (PM == PM_SL0) {
     __syncthreads();
@@ -279,10 +281,9 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
     __syncthreads();
     if (tid == 0) imp_part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
   }
-  ttile_store(Tt, actsT, a.N, n0, a.N, q0, a.C, tid);
 }
 
-// d_xV = bf16(d_acts * (m - d)) into d_xV[n * ld + c] and d_xV^T [C, N]; the CI pullback
+// d_xV = bf16(d_acts * (m - d)) into d_xV[n * ld + c]; the CI pullback
 // d_pre = lower_vjp(pre, d_acts * xV * (1 - u)) + upper_vjp(pre, imp_scale * d upper^p).
 // An unrouted token's masked product does not reach the output: d_acts counts as 0 there.
 // SRC: u is read back from the source table, whose gradient dm (1 - lower) (dm = d_acts xV)
@@ -292,8 +293,7 @@ template <int PM, bool SRC>
 __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t* __restrict__ xV,
                                                      const uint8_t* __restrict__ ubits, float imp_scale,
                                                      const bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_xV,
-                                                     bf16_t* __restrict__ d_xVT, bf16_t* __restrict__ d_pre) {
-  __shared__ TTile Tt;
+                                                     bf16_t* __restrict__ d_pre) {
   __shared__ typename std::conditional<SRC, Sl0Tile, NoSl0Tile>::type SG;
   const int tid = threadIdx.x;
   const int64_t n0 = (int64_t)blockIdx.y * TILE;
@@ -352,8 +352,6 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
 #pragma unroll
       for (int e = 0; e < 4; ++e) SG.ps[r][q4 + e] = 0.f;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Tt.v[q4 + e][r] = o[e];
     if constexpr (SRC) {  // the 16 lanes of a row add their columns in a fixed tree (all lanes)
       dmsum += __shfl_xor(dmsum, 1, 64);
       dmsum += __shfl_xor(dmsum, 2, 64);
@@ -362,9 +360,8 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
       if (n < a.N && (tid & 15) == 0 && a.rowdm) a.rowdm[n * gridDim.x + blockIdx.x] = dmsum;
     }
   }
-  __syncthreads();
-  ttile_store(Tt, d_xVT, a.N, n0, a.N, q0, a.C, tid);
   if constexpr (SRC) {
+    __syncthreads();
     if (a.rps > 1) sl0_tile_colsums(SG, blockIdx.y, q0, a.C, a.colsrc, tid);
   }
 }
@@ -738,10 +735,9 @@ struct LMDims {
   int64_t S = 0, rps = 0;  // persistent source tables: S rows of rps tokens (rps = 0: none)
   bool srcs() const { return rps > 0; }
   int64_t BH() const { return B * H; }
-  // the site products run over [acts | s x] . [U ; W^T] (s = d on routed rows, 1 on the rest)
+  // the site products add a target segment, s (.) (x @ W^T) (s = d on routed rows, 1 on the
+  // rest), and its cotangent s (.) (g @ W) to the d_input
   bool cat() const { return use_delta || routed; }
-  int64_t kcat(int k) const { return C[k] + (cat() ? din[k] : 0); }   // forward product depth
-  int64_t kcat2(int k) const { return C[k] + (cat() ? dout[k] : 0); } // d_input product depth
 };
 
 struct Arena {
@@ -758,7 +754,7 @@ struct Arena {
 };
 
 struct LMSiteSave {
-  bf16_t *xV, *acat, *actsT;
+  bf16_t *xV, *acts;
   uint8_t* ub;
   bf16_t* frozen;  // source tables with the delta channel: the site's x @ W^T [N, d_out]
   // smooth-L0: tile column sums of psi, per-component slopes, loss partials (act, freq,
@@ -768,7 +764,7 @@ struct LMSiteSave {
 };
 
 struct LMLayerSave {
-  bf16_t *r, *h, *hT, *r1, *h2, *h2T, *a, *aT, *fc, *g, *gT;
+  bf16_t *r, *h, *r1, *h2, *a, *fc, *g;
   float *rinv1, *rinv2;
   bf16_t *Qh, *Kh, *KhT, *Vh, *VhT, *P;
   LMSiteSave site[LM_NK];
@@ -776,13 +772,13 @@ struct LMLayerSave {
 
 struct LMPlan {
   std::vector<LMLayerSave> layers;
-  bf16_t *VT[LM_NK], *BtF[LM_NK], *BtB[LM_NK];  // per layer blocks of the per-step weight copies
+  bf16_t *VT[LM_NK], *UT[LM_NK], *WT[LM_NK];  // per-step transposed weights, [L, ...] per kind
   bf16_t *rc_a, *rc_b, *rL, *act_m, *act_c, *hc, *qc, *kc, *vc, *ac, *Oh, *fcc, *gc;
   bf16_t *cQh, *cKh, *cKhT, *cVh, *cVhT, *cP, *cOh;  // the clean pass's own attention buffers
   float* cS;
   bf16_t *q, *k, *v;
   float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
-  bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dcat, *dxVT[2], *dqkv[3], *dqkvT, *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
+  bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dxV[2], *dqkv[3], *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
   char *kl_ws, *sk_ws;
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
   float *sl0_act, *sl0_freq, *sl0_fb;  // every site's smooth-L0 loss partials, contiguous
@@ -802,15 +798,11 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
     LMLayerSave& S = P.layers[l];
     S.r = A.take<bf16_t>(N * d);
     S.h = A.take<bf16_t>(N * d);
-    S.hT = A.take<bf16_t>(N * d);
     S.r1 = A.take<bf16_t>(N * d);
     S.h2 = A.take<bf16_t>(N * d);
-    S.h2T = A.take<bf16_t>(N * d);
     S.a = A.take<bf16_t>(N * qd);
-    S.aT = A.take<bf16_t>(N * qd);
     S.fc = A.take<bf16_t>(N * f);
     S.g = A.take<bf16_t>(N * f);
-    S.gT = A.take<bf16_t>(N * f);
     S.rinv1 = A.take<float>(N);
     S.rinv2 = A.take<float>(N);
     S.Qh = A.take<bf16_t>(BH * T * LM_HD);
@@ -821,22 +813,18 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
     S.P = A.take<bf16_t>(BH * T * T);
     for (int k = 0; k < LM_NK; ++k) {
       S.site[k].xV = A.take<bf16_t>(N * D.C[k]);
-      S.site[k].acat = A.take<bf16_t>(N * D.kcat(k));
-      S.site[k].actsT = A.take<bf16_t>(N * D.C[k]);
+      S.site[k].acts = A.take<bf16_t>(N * D.C[k]);
       S.site[k].ub = A.take<uint8_t>(N * D.C[k]);
       S.site[k].frozen = D.srcs() && D.use_delta ? A.take<bf16_t>(N * D.dout[k]) : nullptr;
     }
   }
   for (int k = 0; k < LM_NK; ++k) {
     P.VT[k] = A.take<bf16_t>((size_t)D.L * D.C[k] * D.din[k]);
-    P.BtF[k] = A.take<bf16_t>((size_t)D.L * D.dout[k] * D.kcat(k));
-    P.BtB[k] = A.take<bf16_t>((size_t)D.L * D.din[k] * D.kcat2(k));
+    P.UT[k] = A.take<bf16_t>((size_t)D.L * D.dout[k] * D.C[k]);
+    P.WT[k] = D.cat() ? A.take<bf16_t>((size_t)D.L * D.din[k] * D.dout[k]) : nullptr;
   }
-  int64_t maxw = std::max<int64_t>(d, f), maxC = 0, maxcat2 = 0;
-  for (int k = 0; k < LM_NK; ++k) {
-    maxC = std::max<int64_t>(maxC, D.C[k]);
-    maxcat2 = std::max<int64_t>(maxcat2, D.kcat2(k));
-  }
+  int64_t maxw = std::max<int64_t>(d, f), maxC = 0;
+  for (int k = 0; k < LM_NK; ++k) maxC = std::max<int64_t>(maxC, D.C[k]);
   P.rc_a = A.take<bf16_t>(N * d);
   P.rc_b = A.take<bf16_t>(N * d);
   P.rL = A.take<bf16_t>(N * d);
@@ -900,10 +888,8 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.dr_b = A.take<bf16_t>(N * d);
   for (int b = 0; b < 2; ++b) P.drT[b] = A.take<bf16_t>(N * maxw);
   P.dacts = A.take<bf16_t>(N * maxC);
-  P.dcat = A.take<bf16_t>(N * maxcat2);
-  for (int b = 0; b < 2; ++b) P.dxVT[b] = A.take<bf16_t>(N * maxC);
+  for (int b = 0; b < 2; ++b) P.dxV[b] = A.take<bf16_t>(N * maxC);
   for (int i = 0; i < 3; ++i) P.dqkv[i] = A.take<bf16_t>(N * qd);
-  P.dqkvT = A.take<bf16_t>(N * qd);
   P.da = A.take<bf16_t>(N * qd);
   P.dOh = A.take<bf16_t>(BH * T * LM_HD);
   P.dQh = A.take<bf16_t>(BH * T * LM_HD);
@@ -958,9 +944,40 @@ static void transpose(const bf16_t* src, int64_t R, int64_t Cc, bf16_t* dst, int
                      R, Cc, dst, ld);
 }
 
-static void copy_rows(const bf16_t* src, int64_t R, int w, const float* sc, bf16_t* dst, int64_t ld, hipStream_t s,
-                      const uint8_t* route = nullptr) {
-  hipLaunchKernelGGL(k_lm_copy_rows, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, s, src, R, w, sc, route, dst, ld);
+// A site's output s (.) (x @ W^T) + acts @ U (s: d on routed rows, 0 without a delta,
+// 1 on unrouted rows), every operand K-contiguous: x [N, d_in], W [d_out, d_in] as
+// stored, acts [N, C], UT = U^T [d_out, C]. Without the target segment, acts @ U alone.
+static int site_out(int64_t N, int64_t dout, int64_t di, int64_t C, const bf16_t* x, const bf16_t* W,
+                    const bf16_t* acts, const bf16_t* UT, const float* delta, const uint8_t* route, bool cat,
+                    bf16_t* out, hipStream_t s) {
+  if (!cat) return pd_gemm(PD_DTYPE_BF16, N, dout, C, acts, C, 0, UT, C, 1, out, dout, PD_DTYPE_BF16, 1.f, 0.f, s);
+  GemmArgs g{N, dout, C, acts, C, UT, C, out, dout, 1.f, 0.f, nullptr, 0, 0, 0};
+  KcatArgs q{x, di, W, di, di, nullptr, route};
+  q.delta_f = delta;
+  return launch_kcat_epi<EpiStore, bf16_t, false, false>(g, q, EpiStore::Args{}, s, "pd_lm_stack_step site out");
+}
+
+// A site's input cotangent s (.) (g @ W) + dxV @ V^T, every operand K-contiguous: g [N,
+// d_out], WT = W^T [d_in, d_out], dxV [N, C], V [d_in, C] as stored; fp32 (beta
+// accumulates into out) or bf16 out.
+static int site_din(int64_t N, int64_t dout, int64_t di, int64_t C, const bf16_t* g, const bf16_t* WT,
+                    const bf16_t* dxV, const bf16_t* V, const float* delta, const uint8_t* route, bool cat, void* out,
+                    bool f32, float beta, hipStream_t s) {
+  if (!cat)
+    return pd_gemm(PD_DTYPE_BF16, N, di, C, dxV, C, 0, V, C, 1, out, di, f32 ? PD_DTYPE_F32 : PD_DTYPE_BF16, 1.f,
+                   beta, s);
+  GemmArgs a{N, di, C, dxV, C, V, C, out, di, 1.f, beta, nullptr, 0, 0, 0};
+  KcatArgs q{g, dout, WT, dout, dout, nullptr, route};
+  q.delta_f = delta;
+  if (f32) return launch_kcat_epi<EpiStore, float, false, false>(a, q, EpiStore::Args{}, s, "pd_lm_stack_step site din");
+  return launch_kcat_epi<EpiStore, bf16_t, false, false>(a, q, EpiStore::Args{}, s, "pd_lm_stack_step site din");
+}
+
+// dst[b] = src[b]^T for B matrices [R, Cc] (R, Cc multiples of 8): every layer's copy of
+// one weight in one launch.
+static void transpose_layers(const void* src, int64_t B, int64_t R, int64_t Cc, bf16_t* dst, hipStream_t s) {
+  hipLaunchKernelGGL(k_lm_transpose_b, dim3((unsigned)cdiv(Cc, TILE), (unsigned)cdiv(R, TILE), (unsigned)B), dim3(256),
+                     0, s, (const bf16_t*)src, R, Cc, dst);
 }
 
 // C = A @ B^T with both operands K-contiguous (the buffer-fed kernel).
@@ -992,12 +1009,12 @@ size_t pd_lm_stack_workspace_size(int64_t B, int64_t T, int d, int n_head, int n
 }
 
 enum {
-  LM_CAT_PREP = 0,     // per-step weight copies, delta draws
+  LM_CAT_PREP = 0,     // delta draws
   LM_CAT_CLEAN = 1,    // frozen forward
   LM_CAT_GEMM_FWD = 2, // masked-forward site products
   LM_CAT_MASK_FWD = 3, // mask passes (forward)
   LM_CAT_ATTN = 4,     // attention forward and backward
-  LM_CAT_ELEM = 5,     // norms, residual adds, GELU, transposes
+  LM_CAT_ELEM = 5,     // norms, residual adds, GELU, the cotangent copies g^T
   LM_CAT_KL = 6,       // streamed KL forward and backward
   LM_CAT_GEMM_DX = 7,  // d_acts and d_input products
   LM_CAT_GEMM_DW = 8,  // dU and dV products
@@ -1095,23 +1112,13 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   hipEventRecord(ax.ev[0], s);
   hipStreamWaitEvent(sc, ax.ev[0], 0);
 
-  // ================= per-step weight copies (every product K-contiguous)
+  // ================= per-step transposed weights (one launch per kind and matrix) and the
+  // per-token deltas
   rec.mark(LM_CAT_PREP);
   for (int k = 0; k < LM_NK; ++k) {
-    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc = D.kcat(k), kc2 = D.kcat2(k);
-    for (int l = 0; l < L; ++l) {
-      const bf16_t* Vl = bfp(Vf[k], (size_t)l * di * C);
-      const bf16_t* Ul = bfp(Uf[k], (size_t)l * C * dout);
-      const bf16_t* Wl = bfp(W[k], (size_t)l * dout * di);
-      bf16_t* vt = P.VT[k] + (size_t)l * C * di;
-      bf16_t* bf = P.BtF[k] + (size_t)l * dout * kc;
-      bf16_t* bb = P.BtB[k] + (size_t)l * di * kc2;
-      transpose(Vl, di, C, vt, di, s);                       // V^T [C, d_in]
-      transpose(Ul, C, dout, bf, kc, s);                     // U^T into [U^T | W]
-      if (D.cat()) copy_rows(Wl, dout, (int)di, nullptr, bf + C, kc, s);  // W
-      copy_rows(Vl, di, (int)C, nullptr, bb, kc2, s);        // V into [V | W^T]
-      if (D.cat()) transpose(Wl, dout, di, bb + C, kc2, s);  // W^T
-    }
+    transpose_layers(Vf[k], L, D.din[k], D.C[k], P.VT[k], s);    // V^T [C, d_in]
+    transpose_layers(Uf[k], L, D.C[k], D.dout[k], P.UT[k], s);   // U^T [d_out, C]
+    if (D.cat()) transpose_layers(W[k], L, D.dout[k], D.din[k], P.WT[k], s);  // W^T [d_in, d_out]
   }
   if (srcs && D.use_delta)  // each token's delta is its source row's
     hipLaunchKernelGGL(k_src_delta_fill, dim3((unsigned)std::min<int64_t>(cdiv((int64_t)LM_NK * L * N, 256), 4096)),
@@ -1185,7 +1192,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     ma.p = imp.p;
     ma.delta = D.use_delta ? P.delta + ((size_t)l * LM_NK + k) * N : nullptr;
     ma.route = routes ? routes + ((size_t)l * LM_NK + k) * N : nullptr;
-    ma.ld = D.kcat(k);
+    ma.ld = D.C[k];
     ma.g2 = imp.g2();
     ma.psis = imp.psi_scale();
     ma.colpart = P.layers[l].site[k].sl0_col;
@@ -1204,13 +1211,12 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   // site forward: x [N, d_in] (and the site's saves) -> out [N, d_out]
   auto site_fwd = [&](int k, int l, const bf16_t* x, bf16_t* out) -> int {
     LMSiteSave& S = P.layers[l].site[k];
-    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc = D.kcat(k);
+    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k];
     rec.mark(LM_CAT_GEMM_FWD);
     int r = gemm_nt(N, C, di, x, di, P.VT[k] + (size_t)l * C * di, di, S.xV, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
     rec.mark(LM_CAT_MASK_FWD);
     const LMMaskArgs ma = mask_args(k, l);
-    if (D.cat()) copy_rows(x, N, (int)di, ma.delta, S.acat + C, kc, s, ma.route);
     float* part = P.imp_part + [&] {
       size_t o = 0;
       for (int ll = 0; ll < l; ++ll)
@@ -1219,7 +1225,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
       return o;
     }();
 #define PD_LMF(LY, PMV) \
-  hipLaunchKernelGGL((k_lm_mask_fwd<LY, PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.acat, S.actsT, S.ub, part)
+  hipLaunchKernelGGL((k_lm_mask_fwd<LY, PMV>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.acts, S.ub, part)
     if (srcs) {
       if (pm == PM_SL0) PD_LMF(MASK_SRC, PM_SL0);
       else if (pm == 2) PD_LMF(MASK_SRC, 2);
@@ -1243,10 +1249,12 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                          imp.ref_count, imp.ema.at((int64_t)S.ema_off), S.sl0_slope, S.sl0_act, S.sl0_freq,
                          imp.ema.on() ? S.sl0_fb : nullptr);
     rec.mark(LM_CAT_GEMM_FWD);
+    const bf16_t* Wl = bfp(W[k], (size_t)l * dout * di);
     if (S.frozen &&  // the target output the delta table's gradient reads
-        (r = gemm_nt(N, dout, di, x, di, bfp(W[k], (size_t)l * dout * di), di, S.frozen, dout, PD_DTYPE_BF16, 0.f, s)))
+        (r = gemm_nt(N, dout, di, x, di, Wl, di, S.frozen, dout, PD_DTYPE_BF16, 0.f, s)))
       return r;
-    return gemm_nt(N, dout, kc, S.acat, kc, P.BtF[k] + (size_t)l * dout * kc, kc, out, dout, PD_DTYPE_BF16, 0.f, s);
+    return site_out(N, dout, di, C, x, Wl, S.acts, P.UT[k] + (size_t)l * dout * C, ma.delta, ma.route, D.cat(), out,
+                    s);
   };
 
   hipLaunchKernelGGL(k_lm_embed, rows4(N), dim3(256), 0, s, tokens, (const bf16_t*)wte, N, d, V, P.layers[0].r);
@@ -1254,23 +1262,19 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     LMLayerSave& S = P.layers[l];
     rec.mark(LM_CAT_ELEM);
     hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, S.r, N, d, ln1 + (size_t)l * d, eps, S.h, S.rinv1);
-    transpose(S.h, N, d, S.hT, N, s);
     if ((rc = site_fwd(LK_Q, l, S.h, P.q))) return rc;
     if ((rc = site_fwd(LK_K, l, S.h, P.k))) return rc;
     if ((rc = site_fwd(LK_V, l, S.h, P.v))) return rc;
     rec.mark(LM_CAT_ATTN);
     if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.KhT, S.Vh, S.VhT, S.P, S.a, P.S, P.Oh, s))) return rc;
     rec.mark(LM_CAT_ELEM);
-    transpose(S.a, N, qd, S.aT, N, s);
     if ((rc = site_fwd(LK_O, l, S.a, P.q))) return rc;  // o output into the q scratch
     rec.mark(LM_CAT_ELEM);
     hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, s, S.r, P.q, N * d, S.r1);
     hipLaunchKernelGGL(k_lm_rms_fwd, rows4(N), dim3(256), 0, s, S.r1, N, d, ln2 + (size_t)l * d, eps, S.h2, S.rinv2);
-    transpose(S.h2, N, d, S.h2T, N, s);
     if ((rc = site_fwd(LK_FC, l, S.h2, S.fc))) return rc;
     rec.mark(LM_CAT_ELEM);
     hipLaunchKernelGGL(k_lm_gelu_fwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, S.fc, N * f, S.g);
-    transpose(S.g, N, f, S.gT, N, s);
     if ((rc = site_fwd(LK_DOWN, l, S.g, P.q))) return rc;
     rec.mark(LM_CAT_ELEM);
     bf16_t* rnext = l + 1 < L ? P.layers[l + 1].r : P.rL;
@@ -1306,11 +1310,11 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 
   // ================= backward
   const float imp_scale = imp.coeff / (float)N;
-  // site backward: g [N, d_out] (the output cotangent), the site input's transpose xT
-  // [d_in, N] -> dU, dV, d_ci_pre, and d_input (+)= into din_out (fp32 accumulate when
-  // din_f32, else bf16 written).
+  // site backward: g [N, d_out] (the output cotangent), the site input x [N, d_in] -> dU,
+  // dV, d_ci_pre, and d_input (+)= into din_out (fp32 accumulate when din_f32, else bf16
+  // written).
   // The weight gradients (split-contraction products) run on the helper stream: site call
-  // n writes g^T and d(xV)^T into buffer set n % 2, forks the helper stream once both are
+  // n writes g^T and d(xV) into buffer set n % 2, forks the helper stream once both are
   // written, and call n + 2 waits for that call's products before it rewrites the set.
   // Nothing on this stream reads a weight gradient; the step joins them all at its end.
   int wg_call = 0;
@@ -1319,24 +1323,21 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if (wg_pend[b]) hipStreamWaitEvent(s, ax.ev[3 + b], 0);
     wg_pend[b] = false;
   };
-  auto site_bwd = [&](int k, int l, const bf16_t* g, const bf16_t* xT, void* din_out, bool din_f32,
+  auto site_bwd = [&](int k, int l, const bf16_t* g, const bf16_t* x, void* din_out, bool din_f32,
                       float din_beta) -> int {
     // din_out NULL: the site's input carries no gradient (layer 0's q/k/v read the
     // embedding), so its d_input product is not formed (nor counted by the reference's
     // FLOP rule, pd/core/flops/target.py:53-93)
     LMSiteSave& S = P.layers[l].site[k];
-    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k], kc2 = D.kcat2(k);
-    const LMMaskArgs ma0 = mask_args(k, l);
-    LMMaskArgs ma = ma0;
-    ma.ld = kc2;
+    const int64_t C = D.C[k], di = D.din[k], dout = D.dout[k];
+    const LMMaskArgs ma = mask_args(k, l);
     const int wb = wg_call++ & 1;
     bf16_t* const drT = P.drT[wb];
-    bf16_t* const dxVT = P.dxVT[wb];
+    bf16_t* const dxV = P.dxV[wb];
     rec.mark(LM_CAT_WAIT);
     wg_join(wb);
     rec.mark(LM_CAT_ELEM);
     if (want_wgrads) transpose(g, N, dout, drT, N, s);  // g^T [d_out, N]
-    if (D.cat() && din_out) copy_rows(g, N, (int)dout, ma.delta, P.dcat + C, kc2, s, ma.route);
     rec.mark(LM_CAT_GEMM_DX);
     int r = gemm_nt(N, C, dout, g, dout, bfp(Uf[k], (size_t)l * C * dout), dout, P.dacts, C, PD_DTYPE_BF16, 0.f, s);
     if (r) return r;
@@ -1344,7 +1345,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     bf16_t* dpre = (bf16_t*)d_ci_pre[k] + (size_t)l * N * C;
 #define PD_LMB(PMV, SRC)                                                                                          \
   hipLaunchKernelGGL((k_lm_mask_bwd<PMV, SRC>), tgrid(N, C), dim3(256), 0, s, ma, S.xV, S.ub, imp_scale, P.dacts, \
-                     P.dcat, dxVT, dpre)
+                     dxV, dpre)
     if (srcs) {
       if (pm == PM_SL0) PD_LMB(PM_SL0, true);
       else if (pm == 2) PD_LMB(2, true);
@@ -1370,21 +1371,22 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
 #undef PD_LMB
     if (want_wgrads) {
       rec.mark(LM_CAT_GEMM_DW);
-      hipEventRecord(ax.ev[2], s);  // g^T and d(xV)^T of this call are written
+      hipEventRecord(ax.ev[2], s);  // g^T and d(xV) of this call are written
       hipStreamWaitEvent(ax.st, ax.ev[2], 0);
-      if ((r = gemm_nt_splitk(C, dout, N, S.actsT, N, drT, N, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
-                              P.sk_ws, P.sk_ws_bytes, ax.st)))
+      // dU = acts^T @ g (acts MN-major, g^T K-contiguous), dV = x^T @ d(xV) (both MN-major)
+      if ((r = gemm_splitk(C, dout, N, S.acts, C, 1, drT, N, 1, dU[k] + (size_t)l * C * dout, dout, PD_DTYPE_F32, 0.f,
+                           P.sk_ws, P.sk_ws_bytes, ax.st)))
         return r;
-      if ((r = gemm_nt_splitk(di, C, N, xT, N, dxVT, N, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
-                              P.sk_ws_bytes, ax.st)))
+      if ((r = gemm_splitk(di, C, N, x, di, 1, dxV, C, 0, dV[k] + (size_t)l * di * C, C, PD_DTYPE_F32, 0.f, P.sk_ws,
+                           P.sk_ws_bytes, ax.st)))
         return r;
       hipEventRecord(ax.ev[3 + wb], ax.st);
       wg_pend[wb] = true;
     }
     if (!din_out) return PD_OK;
     rec.mark(LM_CAT_GEMM_DX);
-    return gemm_nt(N, di, kc2, P.dcat, kc2, P.BtB[k] + (size_t)l * di * kc2, kc2, din_out, di,
-                   din_f32 ? PD_DTYPE_F32 : PD_DTYPE_BF16, din_beta, s);
+    return site_din(N, dout, di, C, g, D.cat() ? P.WT[k] + (size_t)l * di * dout : nullptr, dxV,
+                    bfp(Vf[k], (size_t)l * di * C), ma.delta, ma.route, D.cat(), din_out, din_f32, din_beta, s);
   };
 
   bf16_t* dr = P.dr_a;     // cotangent of the residual leaving layer l
@@ -1392,17 +1394,17 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   for (int l = L - 1; l >= 0; --l) {
     LMLayerSave& S = P.layers[l];
     // down site: input g, output cotangent dr
-    if ((rc = site_bwd(LK_DOWN, l, dr, S.gT, P.dg, false, 0.f))) return rc;
+    if ((rc = site_bwd(LK_DOWN, l, dr, S.g, P.dg, false, 0.f))) return rc;
     rec.mark(LM_CAT_ELEM);
     hipLaunchKernelGGL(k_lm_gelu_bwd, dim3(ew_blocks(N * f / 8)), dim3(256), 0, s, S.fc, P.dg, N * f, P.dfc);
     // fc site: input h2 -> d_h2 (fp32) -> norm pullback added to dr
-    if ((rc = site_bwd(LK_FC, l, P.dfc, S.h2T, P.dhf, true, 0.f))) return rc;
+    if ((rc = site_bwd(LK_FC, l, P.dfc, S.h2, P.dhf, true, 0.f))) return rc;
     rec.mark(LM_CAT_ELEM);
     hipLaunchKernelGGL(k_lm_rms_bwd, rows4(N), dim3(256), 0, s, P.dhf, S.r1, S.rinv2, ln2 + (size_t)l * d, N, d, dr,
                        dr_o);
     std::swap(dr, dr_o);  // dr: cotangent of r1
     // o site: input a, output cotangent dr -> d_a
-    if ((rc = site_bwd(LK_O, l, dr, S.aT, P.da, false, 0.f))) return rc;
+    if ((rc = site_bwd(LK_O, l, dr, S.a, P.da, false, 0.f))) return rc;
     // attention backward
     rec.mark(LM_CAT_ATTN);
     hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, P.da, P.dOh, B, T, H, 1);
@@ -1427,9 +1429,9 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if ((rc = check_launch("pd_lm_stack_step attention backward"))) return rc;
     // q, k, v sites: input h, d_h accumulated in fp32 (none for layer 0: the embedding)
     float* dh = l > 0 ? P.dhf : nullptr;
-    if ((rc = site_bwd(LK_Q, l, P.dqkv[0], S.hT, dh, true, 0.f))) return rc;
-    if ((rc = site_bwd(LK_K, l, P.dqkv[1], S.hT, dh, true, 1.f))) return rc;
-    if ((rc = site_bwd(LK_V, l, P.dqkv[2], S.hT, dh, true, 1.f))) return rc;
+    if ((rc = site_bwd(LK_Q, l, P.dqkv[0], S.h, dh, true, 0.f))) return rc;
+    if ((rc = site_bwd(LK_K, l, P.dqkv[1], S.h, dh, true, 1.f))) return rc;
+    if ((rc = site_bwd(LK_V, l, P.dqkv[2], S.h, dh, true, 1.f))) return rc;
     if (l > 0) {
       rec.mark(LM_CAT_ELEM);
       hipLaunchKernelGGL(k_lm_rms_bwd, rows4(N), dim3(256), 0, s, P.dhf, S.r, S.rinv1, ln1 + (size_t)l * d, N, d, dr,
