@@ -66,11 +66,6 @@ int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, f
 // the GPU: each slice's fp32 partial goes to `ws` and a second pass adds the slices in
 // order (deterministic), writing C (+ beta * C) in c_dtype. gemm_splitk_ws_bytes gives the
 // scratch the same call needs (0: no split; the call then needs no scratch).
-// pd_gemm_strided_batched with a causal mode for attention products (GemmArgs::causal).
-int gemm_batched_causal(int causal, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
-                        int64_t lda, int64_t stride_a, int trans_a, const void* B, int64_t ldb, int64_t stride_b,
-                        int trans_b, void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
-                        void* stream);
 size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K);
 // The same for any operand layouts (trans_a / trans_b as pd_gemm's).
 int gemm_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B, int64_t ldb,

@@ -607,19 +607,6 @@ int pd_gemm_strided_batched(int dtype, int64_t batch, int64_t M, int64_t N, int6
                             int64_t stride_a, int trans_a, const void* B, int64_t ldb, int64_t stride_b, int trans_b,
                             void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
                             void* stream) {
-  return gemm_batched_causal(0, dtype, batch, M, N, K, A, lda, stride_a, trans_a, B, ldb, stride_b, trans_b, C, ldc,
-                             stride_c, c_dtype, alpha, beta, stream);
-}
-
-}  // extern "C"
-
-namespace pd {
-
-int gemm_batched_causal(int causal, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
-                        int64_t lda, int64_t stride_a, int trans_a, const void* B, int64_t ldb, int64_t stride_b,
-                        int trans_b, void* C, int64_t ldc, int64_t stride_c, int c_dtype, float alpha, float beta,
-                        void* stream) {
-  if (causal < 0 || causal > 3) return fail(PD_EINVAL, "gemm_batched_causal: causal mode");
   if (batch < 0 || M < 0 || N < 0 || K < 0 || stride_a < 0 || stride_b < 0 || stride_c < 0 || !A || !B || !C)
     return fail(PD_EINVAL, "pd_gemm_strided_batched: bad args");
   if (batch == 0 || M == 0 || N == 0) return PD_OK;
@@ -640,21 +627,13 @@ int gemm_batched_causal(int causal, int dtype, int64_t batch, int64_t M, int64_t
                 "pd_gemm_strided_batched: bf16 operands need 16B alignment, ld and batch strides % 8 == 0");
   GemmArgs a{M, N, K, (const bf16_t*)A, lda, (const bf16_t*)B, ldb, C, ldc, alpha, beta, nullptr, 0, stride_b,
              stride_c, stride_a};
-  a.causal = causal;
-  static_assert(CfgDtlRA::BM == 128, "the causal modes assume 128-row tiles");
   if (dtl_fits_any(M, N, K, lda, a_kmaj, ldb, b_kmaj))
     return launch_dtl_any<CfgDtlRA, MODE_BATCHED>(
         a, a_kmaj, b_kmaj, c_dtype, K % CfgDtlRA::BK != 0,
-        dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)batch),
-        s);
-  if (causal) return fail(PD_EUNSUPPORTED, "gemm_batched_causal: operands past the buffer-fed kernel's range");
+        dim3((unsigned)cdiv(N, CfgDtlRA::BN), (unsigned)cdiv(M, CfgDtlRA::BM), (unsigned)batch), s);
   return launch_bf16<CfgSmall, MODE_BATCHED>(
       a, a_kmaj, b_kmaj, c_dtype, dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)batch), s);
 }
-
-}  // namespace pd
-
-extern "C" {
 
 int pd_grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64_t J, int E, int64_t K, int64_t N,
                     int trans_rhs, void* out, int out_dtype, void* stream) {

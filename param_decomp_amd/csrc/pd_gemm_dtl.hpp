@@ -73,12 +73,6 @@ struct GemmArgs {
   const bf16_t* A2;
   const bf16_t* B2;
   void* C2;
-  // BATCHED only, for causal attention products over square [T, T] score matrices (BM =
-  // 128 rows per tile): 1 = skip tiles wholly above the diagonal (columns past the tile's
-  // last row); 2 = contract only k < the tile's last row + 1, rounded up to the tile (a
-  // [T, T] operand read along its rows, zero past the diagonal within the diagonal tile);
-  // 3 = contract only k >= the tile's first row (a [T, T] operand read along its columns).
-  int causal;
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): give
@@ -229,9 +223,6 @@ __device__ inline bool map_tile(const GemmArgs& p, int lane, TileJob& t) {
     const int64_t z = blockIdx.z;
     t.m0 = (int64_t)blockIdx.y * BM;
     t.n0 = (int64_t)blockIdx.x * BN;
-    if (p.causal == 1 && t.n0 > t.m0 + BM - 1) return false;
-    if (p.causal == 2 && t.m0 + BM < t.kend) t.kend = t.m0 + BM;
-    if (p.causal == 3) t.kbeg = t.m0 < t.kend ? t.m0 : t.kend;
     t.A = p.A + z * p.strideA;
     t.B = p.B + z * p.strideB;
     t.C = (TC*)p.C + z * p.strideC;

@@ -25,9 +25,12 @@
 //   dV = x^T dxV     A = x [N, d_in], B = dxV [N, C] (both MN-major)
 //   d_input          s (.) (g @ W) + dxV @ V^T in one two-segment product (W^T [d_in,
 //                    d_out] copy, V as stored)
-// Attention is materialized per (batch, head) at hd = 64: S = Q K^T (fp32), causal softmax
-// to bf16 P, O = P V; the backward forms dP, dS = P (dP - rowsum(P dP)) / sqrt(hd), dQ = dS K,
-// dK = dS^T Q, dV = P^T dO. It is about 1% of the step's work at the benchmark shape.
+// Attention (hd = 64) is fused per (batch, head) with nothing T x T stored: the forward
+// forms each query row's softmax max and sum, then O = P V with P = bf16(softmax(Q K^T /
+// sqrt(hd))) over 32-key blocks in registers, keeping the row stats and the fp32 O; the
+// backward recomputes P from the stats and forms dS = bf16(P (dP - D) / sqrt(hd)) (dP =
+// dO V^T, D = rowsum(P dP) = rowsum(dO O)), dQ = dS K per query tile and dK = dS^T Q,
+// dV = P^T dO per key tile.
 #include <algorithm>
 #include <vector>
 
@@ -429,28 +432,25 @@ __device__ inline void rope_cs(int64_t t, int c, float log2_base, float& cs, flo
 }
 
 // Head-major copies of one (batch, head, 64-token) tile: Qh, Kh, Vh [B*H, T, 64] (q and k
-// rotated; a kv head serves H/KV query heads, so its k and v are repeated), and the
-// transposed Kh^T, Vh^T [B*H, 64, T] for the products that contract over tokens.
+// rotated; a kv head serves H/KV query heads, so its k and v are repeated).
 // Grid (T/64, H, B); thread = (token tid / 4, pairs 8 (tid % 4) .. +8).
 __global__ __launch_bounds__(256) void k_lm_attn_in(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                     const bf16_t* __restrict__ v, int64_t T, int H, int KV,
                                                     float log2_base, bf16_t* __restrict__ Qh, bf16_t* __restrict__ Kh,
-                                                    bf16_t* __restrict__ KhT, bf16_t* __restrict__ Vh,
-                                                    bf16_t* __restrict__ VhT) {
-  __shared__ TTile Tk, Tv;
+                                                    bf16_t* __restrict__ Vh) {
   const int tid = threadIdx.x;
   const int h = blockIdx.y, g = h / (H / KV);
   const int64_t b = blockIdx.z, t0 = (int64_t)blockIdx.x * TILE;
   const int r = tid >> 2, cp = (tid & 3) * 8;
   const int64_t t = t0 + r, n = b * T + t;
   const int64_t bh = b * H + h;
-  float q1[8], q2[8], k1[8], k2[8], v1[8], v2[8];
+  float q1[8], q2[8], k1[8], k2[8];
   load8(q + n * (int64_t)H * LM_HD + h * LM_HD + cp, q1);
   load8(q + n * (int64_t)H * LM_HD + h * LM_HD + cp + 32, q2);
   load8(k + n * (int64_t)KV * LM_HD + g * LM_HD + cp, k1);
   load8(k + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, k2);
-  load8(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp, v1);
-  load8(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32, v2);
+  const uint4 v1 = *(const uint4*)(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp);
+  const uint4 v2 = *(const uint4*)(v + n * (int64_t)KV * LM_HD + g * LM_HD + cp + 32);
   float qa[8], qb[8], ka[8], kb[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -466,118 +466,437 @@ __global__ __launch_bounds__(256) void k_lm_attn_in(const bf16_t* __restrict__ q
   store8(Qh + row + cp + 32, qb);
   store8(Kh + row + cp, ka);
   store8(Kh + row + cp + 32, kb);
-  store8(Vh + row + cp, v1);
-  store8(Vh + row + cp + 32, v2);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    Tk.v[cp + j][r] = f32_to_bf16(ka[j]);
-    Tk.v[cp + 32 + j][r] = f32_to_bf16(kb[j]);
-    Tv.v[cp + j][r] = f32_to_bf16(v1[j]);
-    Tv.v[cp + 32 + j][r] = f32_to_bf16(v2[j]);
-  }
-  __syncthreads();
-  ttile_store(Tk, KhT + bh * LM_HD * T, T, t0, T, 0, LM_HD, tid);
-  ttile_store(Tv, VhT + bh * LM_HD * T, T, t0, T, 0, LM_HD, tid);
+  *(uint4*)(Vh + row + cp) = v1;
+  *(uint4*)(Vh + row + cp + 32) = v2;
 }
 
-// The causal attention products work on 128-row tiles: a query tile's products read P and
-// dS only up to the end of its diagonal 128 x 128 block, and the key tiles' products read
-// them only from the block's first row, so the softmax passes write each row up to the end
-// of its diagonal block (zeros past the diagonal) and nothing beyond; S and dP exist only
-// on and below the diagonal blocks.
-constexpr int ATT_BLOCK = 128;
-__device__ inline int att_row_end(int i, int T) {
-  const int e = (i / ATT_BLOCK + 1) * ATT_BLOCK;
-  return e < T ? e : T;
-}
+// ---------------------------------------------------------------- fused causal attention
+// Nothing T x T is stored. A workgroup of 8 waves owns a span of up to 512 rows of one
+// (batch, head); wave w takes the span's 32-row tiles w and nt - 1 - w (nt tiles in the
+// span), so with causal masking every wave walks the same number of blocks. The other
+// side's rows are staged through LDS 512 rows at a time (one stage when T <= 512) and read
+// from there by every wave.
+//
+// MFMA operands: written mfma(X, Y) (X the first source of the 32x32x16 bf16 MFMA), lane
+// l = 32 hh + r supplies row r of X and of Y over k = 8 hh .. +8 of a 16-wide slice and
+// receives out[Y row r][X row 8 g + 4 hh + e] = sum_k X[.][k] Y[r][k] in accumulator
+// register 4 g + e. An accumulator tile reused as an operand (P or dS) therefore carries,
+// in slice kk, the positions 16 kk + 4 hh + 0..3 and 16 kk + 8 + 4 hh + 0..3; its partner
+// (V^T, K^T, Q^T or dO^T: channels as rows, positions as k) is read in that order straight
+// from the row-major LDS image by ds_read_b64_tr_b16. Within each 16-lane group that read
+// gives output lane 4 a + b element b of the 8 bytes source lanes a, a + 4, a + 8, a + 12
+// read; source lane 16 G + 4 e + a reads position row 16 kk + 8 h + 4 (G >> 1) + e (h = 0,
+// 1: the two halves of the slice), channels 32 cb + 16 (G & 1) + 4 a .. + 3, so output lane
+// l receives channel 32 cb + (l & 31) at the positions its own accumulator slice holds.
+//
+// LDS image of a row-major [rows, 64] bf16 block: 128-byte rows, the 16-byte chunk c of row
+// R at physical chunk c ^ fa_swz(R). Each half wave's reads are conflict-free: 16
+// consecutive rows at one chunk (row fragments: fa_swz is a permutation of 0..7 over the
+// even rows and over the odd rows of any 16) and 4 consecutive rows at 4 consecutive
+// chunks (transposing reads: rows 4q and 4q + 2 differ in bit 2 of fa_swz).
+constexpr int FA_SPAN = 512;
+constexpr int FA_THREADS = 512;
+constexpr float FA_SCALE = 0.125f;                        // 1 / sqrt(64)
+constexpr float FA_C2 = 0.125f * 1.4426950408889634f;     // scale * log2(e): P = 2^(s C2 - m)
 
-// P = softmax(scale * S) over keys j <= i (causal), bf16; one wave per row of S [rows, T],
-// 4 consecutive keys per lane (T % 4 == 0: 16-byte score loads, 8-byte stores). The last
-// group a row reads may reach past i inside its diagonal block; those keys are excluded.
-__global__ __launch_bounds__(256) void k_lm_softmax_fwd(const float* __restrict__ S, int64_t rows, int T, float scale,
-                                                        bf16_t* __restrict__ P) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
-  if (row >= rows) return;
-  const int i = (int)(row % T), lane = threadIdx.x & 63;
-  const float* s = S + row * T;
-  float mx = -INFINITY;
-  for (int j = lane * 4; j <= i; j += 256) {
-    const float4 v = *(const float4*)(s + j);
-    const float e[4] = {v.x, v.y, v.z, v.w};
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned att_u32x4;
+
+__device__ inline int fa_swz(int R) { return (((R >> 1) & 1) << 2) | ((R >> 2) & 3); }
+__device__ inline int fa_off(int R, int c) { return R * 128 + ((c ^ fa_swz(R)) << 4); }
+
+// Rows [0, n) of src (row stride ld elements) into the image at dst; n <= 512.
+__device__ inline void fa_stage(char* dst, const bf16_t* __restrict__ src, int64_t ld, int n, int tid) {
+  uint4 v[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (j + q <= i) mx = fmaxf(mx, e[q] * scale);
+  for (int k = 0; k < 8; ++k) {
+    const int i = tid + k * FA_THREADS;
+    if (i < n * 8) v[k] = *(const uint4*)(src + (int64_t)(i >> 3) * ld + (i & 7) * 8);
   }
-  mx = wave_max(mx);
-  float sum = 0.f;
-  for (int j = lane * 4; j <= i; j += 256) {
-    const float4 v = *(const float4*)(s + j);
-    const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (j + q <= i) sum += __expf(e[q] * scale - mx);
+  for (int k = 0; k < 8; ++k) {
+    const int i = tid + k * FA_THREADS;
+    if (i < n * 8) *(uint4*)(dst + fa_off(i >> 3, i & 7)) = v[k];
   }
-  const float inv = 1.f / wave_sum(sum);
-  const int end = att_row_end(i, T);
-  for (int j = lane * 4; j < end; j += 256) {
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    if (j <= i) {
-      const float4 v = *(const float4*)(s + j);
-      const float e[4] = {v.x, v.y, v.z, v.w};
+}
+// Row fragments (row R, the four 16-wide slices) from an image.
+__device__ inline void fa_rows(const char* img, int R, int hh, bf16x8 (&f)[4]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = j + q <= i ? __expf(e[q] * scale - mx) * inv : 0.f;
+  for (int kk = 0; kk < 4; ++kk) f[kk] = *(const bf16x8*)(img + fa_off(R, 2 * kk + hh));
+}
+// The transposed partner of accumulator slice kk over image rows R0 .. R0 + 31, channels
+// 32 cb + (lane & 31).
+__device__ inline bf16x8 fa_tr(const char* img, int R0, int kk, int cb, int lane) {
+  const int G = lane >> 4, e = (lane >> 2) & 3, a = lane & 3;
+  const int c = 4 * cb + 2 * (G & 1) + (a >> 1);
+  const int R = R0 + 16 * kk + 4 * (G >> 1) + e;
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(img + fa_off(R, c) + 8 * (a & 1)));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(img + fa_off(R + 8, c) + 8 * (a & 1)));
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// Row fragments from global memory (row-major, stride ld elements).
+__device__ inline void att_rows(const bf16_t* base, int64_t ld, int row, int hh, bf16x8 (&f)[4]) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) f[kk] = *(const bf16x8*)(base + (int64_t)row * ld + 16 * kk + 8 * hh);
+}
+// Accumulator registers v[0..7] as a bf16 operand slice (round to nearest even).
+__device__ inline bf16x8 att_pack(const float* v) {
+  return (bf16x8)(att_u32x4){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                             pack_bf16x2(v[6], v[7])};
+}
+__device__ inline float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+__device__ inline f32x16 att_mm(const bf16x8 (&x)[4], const bf16x8 (&y)[4]) {
+  f32x16 acc = {};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x[kk], y[kk], acc, 0, 0, 0);
+  return acc;
+}
+// Causal test inside a diagonal block: accumulator register i of lane (hh, r) pairs row r
+// of the Y side with row 8 (i >> 2) + 4 hh + (i & 3) of the X side.
+__device__ inline int att_xrow(int i, int hh) { return 8 * (i >> 2) + 4 * hh + (i & 3); }
+__device__ inline float att_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Forward: a = softmax(Q K^T / 8, causal) V written row-major into a [B*T, H*64] (bf16; P
+// rounded to bf16 before the product, as a materialized P is stored). Pass 1 forms each
+// query row's max and sum of exp over its keys (both halves of a wave carry the row's
+// running max, each its own partial sum); pass 2 forms P = 2^(s C2 - m) / l and
+// accumulates P V. With SAVE the row's m and 1/l (stats [2][B*H*T]) and the fp32 output
+// (Of [B*H, T, 64]) are kept for the backward. Grid (query spans, B*H), the spans with
+// the most keys first.
+template <bool SAVE>
+__global__ __launch_bounds__(FA_THREADS) void k_lm_flash_fwd(const bf16_t* __restrict__ Qh,
+                                                             const bf16_t* __restrict__ Kh,
+                                                             const bf16_t* __restrict__ Vh, int T, int H,
+                                                             bf16_t* __restrict__ a, float* __restrict__ stats,
+                                                             float* __restrict__ Of) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * FA_SPAN * 128];
+  char* Kl = lds;
+  char* Vl = lds + FA_SPAN * 128;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, hh = lane >> 5;
+  const int s = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int64_t bh = blockIdx.y, BHT = (int64_t)gridDim.y * T;
+  const int q0 = s * FA_SPAN, nt = min(FA_SPAN, T - q0) / 32;
+  const bool act = w < nt / 2;
+  const int tl[2] = {w, nt - 1 - w};
+  const bf16_t* K = Kh + bh * T * LM_HD;
+  const bf16_t* V = Vh + bh * T * LM_HD;
+  bf16x8 qf[2][4];
+  if (act) {
+    att_rows(Qh + bh * T * LM_HD, LM_HD, q0 + 32 * tl[0] + r, hh, qf[0]);
+    att_rows(Qh + bh * T * LM_HD, LM_HD, q0 + 32 * tl[1] + r, hh, qf[1]);
+  }
+  const bool one = s == 0;  // a single stage of keys: K and V stay resident for both passes
+  if (one) {
+    fa_stage(Kl, K, LM_HD, min(FA_SPAN, T), tid);
+    fa_stage(Vl, V, LM_HD, min(FA_SPAN, T), tid);
+    __syncthreads();
+  }
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  for (int c = 0; c <= s; ++c) {
+    if (!one) {
+      __syncthreads();
+      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+      __syncthreads();
     }
-    *(uint2*)(P + row * T + j) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-  }
-}
-
-// dS = bf16(P * (dP - sum_j P dP) * scale) (causal zeros stay zero); one wave per row, 4
-// consecutive keys per lane.
-__global__ __launch_bounds__(256) void k_lm_softmax_bwd(const bf16_t* __restrict__ P, const float* __restrict__ dP,
-                                                        int64_t rows, int T, float scale, bf16_t* __restrict__ dS) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
-  if (row >= rows) return;
-  const int i = (int)(row % T), lane = threadIdx.x & 63;
-  const bf16_t* pr = P + row * T;
-  const float* dpr = dP + row * T;
-  float dot = 0.f;
-  for (int j = lane * 4; j <= i; j += 256) {
-    const uint2 pw = *(const uint2*)(pr + j);
-    const float4 g = *(const float4*)(dpr + j);
-    const float pv[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)}, gv[4] = {g.x, g.y, g.z, g.w};
+    if (!act) continue;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (j + q <= i) dot = fmaf(pv[q], gv[q], dot);
-  }
-  dot = wave_sum(dot);
-  const int end = att_row_end(i, T);
-  for (int j = lane * 4; j < end; j += 256) {
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    if (j <= i) {
-      const uint2 pw = *(const uint2*)(pr + j);
-      const float4 g = *(const float4*)(dpr + j);
-      const float pv[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)}, gv[4] = {g.x, g.y, g.z, g.w};
+    for (int X = 0; X < 2; ++X) {
+      const int nb = c < s ? 16 : tl[X] + 1;
+      for (int j = 0; j < nb; ++j) {
+        bf16x8 kf[4];
+        fa_rows(Kl, 32 * j + r, hh, kf);
+        const f32x16 sc = att_mm(kf, qf[X]);
+        const bool diag = c == s && j == tl[X];
+        float bm = -INFINITY;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = j + q <= i ? pv[q] * (gv[q] - dot) * scale : 0.f;
+        for (int i = 0; i < 16; ++i)
+          if (!diag || att_xrow(i, hh) <= r) bm = fmaxf(bm, sc[i]);
+        const float mn = fmaxf(m[X], fmaxf(bm, __shfl_xor(bm, 32, 64)) * FA_C2);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (!diag || att_xrow(i, hh) <= r) acc += att_exp2(fmaf(sc[i], FA_C2, -mn));
+        l[X] = l[X] * att_exp2(m[X] - mn) + acc;  // the first block: m = -inf, l = 0
+        m[X] = mn;
+      }
     }
-    *(uint2*)(dS + row * T + j) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  }
+  float il[2];
+#pragma unroll
+  for (int X = 0; X < 2; ++X) il[X] = 1.f / (l[X] + __shfl_xor(l[X], 32, 64));
+  f32x16 o[2][2] = {};
+  for (int c = 0; c <= s; ++c) {
+    if (!one) {
+      __syncthreads();
+      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+      fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+      __syncthreads();
+    }
+    if (!act) continue;
+#pragma unroll
+    for (int X = 0; X < 2; ++X) {
+      const int nb = c < s ? 16 : tl[X] + 1;
+      for (int j = 0; j < nb; ++j) {
+        bf16x8 kf[4];
+        fa_rows(Kl, 32 * j + r, hh, kf);
+        const f32x16 sc = att_mm(kf, qf[X]);
+        const bool diag = c == s && j == tl[X];
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          p[i] = (!diag || att_xrow(i, hh) <= r) ? att_exp2(fmaf(sc[i], FA_C2, -m[X])) * il[X] : 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16x8 pf = att_pack(p + 8 * kk);
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            o[X][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Vl, 32 * j, kk, cb, lane), pf, o[X][cb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (!act) return;
+  const int64_t b = bh / H, hd = bh % H;
+#pragma unroll
+  for (int X = 0; X < 2; ++X) {
+    const int qi = q0 + 32 * tl[X] + r;
+    bf16_t* arow = a + ((b * T + qi) * H + hd) * LM_HD;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int ch = cb * 32 + 8 * g + 4 * hh;
+        const f32x16& ov = o[X][cb];
+        *(uint2*)(arow + ch) = make_uint2(pack_bf16x2(ov[4 * g], ov[4 * g + 1]), pack_bf16x2(ov[4 * g + 2], ov[4 * g + 3]));
+        if (SAVE)
+          *(float4*)(Of + (bh * T + qi) * LM_HD + ch) = make_float4(ov[4 * g], ov[4 * g + 1], ov[4 * g + 2], ov[4 * g + 3]);
+      }
+    if (SAVE && hh == 0) {
+      stats[bh * T + qi] = m[X];
+      stats[BHT + bh * T + qi] = il[X];
+    }
   }
 }
 
-// a[b*T + t, h*64 + c] = Oh[(b*H + h)*T + t, c] (dir = 0) or the inverse copy (dir = 1);
-// 8 elements per thread.
-__global__ __launch_bounds__(256) void k_lm_heads(bf16_t* __restrict__ rowmajor, bf16_t* __restrict__ headmajor,
-                                                  int64_t B, int64_t T, int H, int dir) {
-  const int64_t total = B * T * H * (LM_HD / 8);
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int c8 = (int)(i % (LM_HD / 8)) * 8;
-    const int64_t rest = i / (LM_HD / 8);
-    const int h = (int)(rest % H);
-    const int64_t n = rest / H, b = n / T, t = n % T;
-    bf16_t* rm = rowmajor + n * (int64_t)H * LM_HD + h * LM_HD + c8;
-    bf16_t* hm = headmajor + ((b * H + h) * T + t) * LM_HD + c8;
-    if (dir == 0) *(uint4*)rm = *(const uint4*)hm;
-    else *(uint4*)hm = *(const uint4*)rm;
+// dQ = dS K per query row, dS = bf16(P (dP - D) / 8), dP = dO V^T, P = bf16(2^(s C2 - m) / l)
+// from the forward's row stats, D = sum_c dO O over the forward's fp32 output (equal to
+// sum_j P dP for the same P; written to Dq for the key-side kernel). dO is read from the
+// cotangent da [B*T, H*64]. Spans and waves as the forward's; K and V staged through LDS.
+// dQh [B*H, T, 64] bf16.
+__global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dq(const bf16_t* __restrict__ Qh,
+                                                            const bf16_t* __restrict__ Kh,
+                                                            const bf16_t* __restrict__ Vh,
+                                                            const bf16_t* __restrict__ da,
+                                                            const float* __restrict__ Of,
+                                                            const float* __restrict__ stats, int T, int H,
+                                                            bf16_t* __restrict__ dQh, float* __restrict__ Dq) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * FA_SPAN * 128];
+  char* Kl = lds;
+  char* Vl = lds + FA_SPAN * 128;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, hh = lane >> 5;
+  const int s = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int64_t bh = blockIdx.y, BHT = (int64_t)gridDim.y * T;
+  const int64_t b = bh / H, hd = bh % H;
+  const int q0 = s * FA_SPAN, nt = min(FA_SPAN, T - q0) / 32;
+  const bool act = w < nt / 2;
+  const int tl[2] = {w, nt - 1 - w};
+  const bf16_t* K = Kh + bh * T * LM_HD;
+  const bf16_t* V = Vh + bh * T * LM_HD;
+  const bf16_t* dO = da + (b * T * H + hd) * LM_HD;
+  bf16x8 qf[2][4], df[2][4];
+  float m[2], il[2], Dv[2];
+  if (act) {
+#pragma unroll
+    for (int X = 0; X < 2; ++X) {
+      const int qi = q0 + 32 * tl[X] + r;
+      att_rows(Qh + bh * T * LM_HD, LM_HD, qi, hh, qf[X]);
+      att_rows(dO, (int64_t)H * LM_HD, qi, hh, df[X]);
+      m[X] = stats[bh * T + qi];
+      il[X] = stats[BHT + bh * T + qi];
+      // D over the channels this lane's dO fragments hold: 16 kk + 8 hh + 0..7
+      const float* orow = Of + (bh * T + qi) * LM_HD;
+      float dot = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float4 o0 = *(const float4*)(orow + 16 * kk + 8 * hh);
+        const float4 o1 = *(const float4*)(orow + 16 * kk + 8 * hh + 4);
+        const att_u32x4 dw = (att_u32x4)df[X][kk];
+        dot = fmaf(bf_lo(dw[0]), o0.x, dot);
+        dot = fmaf(bf_hi(dw[0]), o0.y, dot);
+        dot = fmaf(bf_lo(dw[1]), o0.z, dot);
+        dot = fmaf(bf_hi(dw[1]), o0.w, dot);
+        dot = fmaf(bf_lo(dw[2]), o1.x, dot);
+        dot = fmaf(bf_hi(dw[2]), o1.y, dot);
+        dot = fmaf(bf_lo(dw[3]), o1.z, dot);
+        dot = fmaf(bf_hi(dw[3]), o1.w, dot);
+      }
+      Dv[X] = dot + __shfl_xor(dot, 32, 64);
+      if (hh == 0) Dq[bh * T + qi] = Dv[X];
+    }
+  }
+  const bool one = s == 0;
+  if (one) {
+    fa_stage(Kl, K, LM_HD, min(FA_SPAN, T), tid);
+    fa_stage(Vl, V, LM_HD, min(FA_SPAN, T), tid);
+    __syncthreads();
+  }
+  f32x16 dq[2][2] = {};
+  for (int c = 0; c <= s; ++c) {
+    if (!one) {
+      __syncthreads();
+      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+      fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+      __syncthreads();
+    }
+    if (!act) continue;
+#pragma unroll
+    for (int X = 0; X < 2; ++X) {
+      const int nb = c < s ? 16 : tl[X] + 1;
+      for (int j = 0; j < nb; ++j) {
+        bf16x8 kf[4], vf[4];
+        fa_rows(Kl, 32 * j + r, hh, kf);
+        fa_rows(Vl, 32 * j + r, hh, vf);
+        const f32x16 sc = att_mm(kf, qf[X]);
+        const f32x16 dp = att_mm(vf, df[X]);
+        const bool diag = c == s && j == tl[X];
+        float ds[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = (!diag || att_xrow(i, hh) <= r) ? bf16r(att_exp2(fmaf(sc[i], FA_C2, -m[X])) * il[X]) : 0.f;
+          ds[i] = (dp[i] - Dv[X]) * (p * FA_SCALE);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16x8 sf = att_pack(ds + 8 * kk);
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            dq[X][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Kl, 32 * j, kk, cb, lane), sf, dq[X][cb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (!act) return;
+#pragma unroll
+  for (int X = 0; X < 2; ++X) {
+    bf16_t* out = dQh + (bh * T + q0 + 32 * tl[X] + r) * LM_HD;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x16& v = dq[X][cb];
+        *(uint2*)(out + cb * 32 + 8 * g + 4 * hh) =
+            make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
+      }
+  }
+}
+
+// dK = dS^T Q and dV = P^T dO per key row: the workgroup owns a span of up to 512 keys
+// (waves pair key tiles as the forward pairs query tiles, one tile after the other) and
+// stages the queries from the span on, 512 at a time, through LDS (Q and dO rows, each
+// query's m, 1/l and D).
+// S^T = K Q^T and dP^T = V dO^T are formed key-major: each lane one key row, its
+// registers 16 queries. dKh, dVh [B*H, T, 64] bf16. Grid (key spans, B*H), the spans with
+// the most queries first.
+__global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dkv(const bf16_t* __restrict__ Qh,
+                                                             const bf16_t* __restrict__ Kh,
+                                                             const bf16_t* __restrict__ Vh,
+                                                             const bf16_t* __restrict__ da,
+                                                             const float* __restrict__ stats,
+                                                             const float* __restrict__ Dq, int T, int H,
+                                                             bf16_t* __restrict__ dKh, bf16_t* __restrict__ dVh) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * FA_SPAN * 128];
+  __shared__ __attribute__((aligned(16))) float qs[3][FA_SPAN];  // m, 1/l, D of the staged queries
+  char* Ql = lds;
+  char* Ol = lds + FA_SPAN * 128;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, hh = lane >> 5;
+  const int s = blockIdx.x, ns = (T + FA_SPAN - 1) / FA_SPAN;
+  const int64_t bh = blockIdx.y, BHT = (int64_t)gridDim.y * T;
+  const int64_t b = bh / H, hd = bh % H;
+  const int k0 = s * FA_SPAN, nt = min(FA_SPAN, T - k0) / 32;
+  const bool act = w < nt / 2;
+  const int tl[2] = {w, nt - 1 - w};
+  const bf16_t* Q = Qh + bh * T * LM_HD;
+  const bf16_t* dO = da + (b * T * H + hd) * LM_HD;
+  // one key tile at a time; its queries in LDS stages (staged once when one stage holds them)
+  auto stage = [&](int c) {
+    const int c0 = c * FA_SPAN, n = min(FA_SPAN, T - c0);
+    fa_stage(Ql, Q + (int64_t)c0 * LM_HD, LM_HD, n, tid);
+    fa_stage(Ol, dO + (int64_t)c0 * H * LM_HD, (int64_t)H * LM_HD, n, tid);
+    if (tid < n) {
+      qs[0][tid] = stats[bh * T + c0 + tid];
+      qs[1][tid] = stats[BHT + bh * T + c0 + tid];
+      qs[2][tid] = Dq[bh * T + c0 + tid];
+    }
+  };
+  const bool one = ns - s == 1;
+  if (one) {
+    stage(s);
+    __syncthreads();
+  }
+#pragma unroll 1
+  for (int X = 0; X < 2; ++X) {
+    f32x16 dk[2] = {}, dv[2] = {};
+    bf16x8 kf[4], vf[4];
+    const int kj = k0 + 32 * tl[X] + r;
+    if (act) {
+      att_rows(Kh + bh * T * LM_HD, LM_HD, kj, hh, kf);
+      att_rows(Vh + bh * T * LM_HD, LM_HD, kj, hh, vf);
+    }
+    for (int c = s; c < ns; ++c) {
+      if (!one) {
+        __syncthreads();
+        stage(c);
+        __syncthreads();
+      }
+      if (!act) continue;
+      const int ib0 = c == s ? tl[X] : 0, nb = min(FA_SPAN, T - c * FA_SPAN) / 32;
+      for (int i = ib0; i < nb; ++i) {
+        bf16x8 qf[4], of[4];
+        fa_rows(Ql, 32 * i + r, hh, qf);
+        fa_rows(Ol, 32 * i + r, hh, of);
+        const f32x16 st = att_mm(qf, kf);
+        const f32x16 dpt = att_mm(of, vf);
+        const bool diag = c == s && i == tl[X];
+        float p[16], ds[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int qq = 32 * i + 8 * g + 4 * hh;
+          const float4 mq = *(const float4*)&qs[0][qq];
+          const float4 lq = *(const float4*)&qs[1][qq];
+          const float4 dq4 = *(const float4*)&qs[2][qq];
+          const float mv[4] = {mq.x, mq.y, mq.z, mq.w}, lv[4] = {lq.x, lq.y, lq.z, lq.w};
+          const float dv4[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ii = 4 * g + e;
+            const float pv =
+                (!diag || att_xrow(ii, hh) >= r) ? bf16r(att_exp2(fmaf(st[ii], FA_C2, -mv[e])) * lv[e]) : 0.f;
+            p[ii] = pv;
+            ds[ii] = (dpt[ii] - dv4[e]) * (pv * FA_SCALE);
+          }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16x8 pf = att_pack(p + 8 * kk), sf = att_pack(ds + 8 * kk);
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) {
+            dv[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Ol, 32 * i, kk, cb, lane), pf, dv[cb], 0, 0, 0);
+            dk[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Ql, 32 * i, kk, cb, lane), sf, dk[cb], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (!act) continue;
+    const int64_t row = (bh * T + kj) * LM_HD;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int ch = cb * 32 + 8 * g + 4 * hh;
+        *(uint2*)(dKh + row + ch) =
+            make_uint2(pack_bf16x2(dk[cb][4 * g], dk[cb][4 * g + 1]), pack_bf16x2(dk[cb][4 * g + 2], dk[cb][4 * g + 3]));
+        *(uint2*)(dVh + row + ch) =
+            make_uint2(pack_bf16x2(dv[cb][4 * g], dv[cb][4 * g + 1]), pack_bf16x2(dv[cb][4 * g + 2], dv[cb][4 * g + 3]));
+      }
   }
 }
 
@@ -766,7 +1085,8 @@ struct LMSiteSave {
 struct LMLayerSave {
   bf16_t *r, *h, *r1, *h2, *a, *fc, *g;
   float *rinv1, *rinv2;
-  bf16_t *Qh, *Kh, *KhT, *Vh, *VhT, *P;
+  bf16_t *Qh, *Kh, *Vh;   // the attention's head-major operands [B*H, T, 64]
+  float *att_stats, *Of;  // row max and 1/sum [2][B*H*T]; fp32 output [B*H, T, 64]
   LMSiteSave site[LM_NK];
 };
 
@@ -774,11 +1094,10 @@ struct LMPlan {
   std::vector<LMLayerSave> layers;
   bf16_t *VT[LM_NK], *UT[LM_NK], *WT[LM_NK];  // per-step transposed weights, [L, ...] per kind
   bf16_t *rc_a, *rc_b, *rL, *act_m, *act_c, *hc, *qc, *kc, *vc, *ac, *Oh, *fcc, *gc;
-  bf16_t *cQh, *cKh, *cKhT, *cVh, *cVhT, *cP, *cOh;  // the clean pass's own attention buffers
-  float* cS;
+  bf16_t *cQh, *cKh, *cVh;  // the clean pass's own attention operands
   bf16_t *q, *k, *v;
-  float *rinvF, *S, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
-  bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dxV[2], *dqkv[3], *da, *dOh, *dQh, *dKh, *dVh, *dS, *dg, *dfc;
+  float *rinvF, *att_D, *delta, *imp_part, *pos_kl, *stats, *gpos, *d_act, *dhf;
+  bf16_t *dr_a, *dr_b, *drT[2], *dacts, *dxV[2], *dqkv[3], *da, *dQh, *dKh, *dVh, *dg, *dfc;
   char *kl_ws, *sk_ws;
   size_t kl_ws_bytes, sk_ws_bytes, imp_per_site[LM_NK], imp_total, total;
   float *sl0_act, *sl0_freq, *sl0_fb;  // every site's smooth-L0 loss partials, contiguous
@@ -807,10 +1126,9 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
     S.rinv2 = A.take<float>(N);
     S.Qh = A.take<bf16_t>(BH * T * LM_HD);
     S.Kh = A.take<bf16_t>(BH * T * LM_HD);
-    S.KhT = A.take<bf16_t>(BH * T * LM_HD);
     S.Vh = A.take<bf16_t>(BH * T * LM_HD);
-    S.VhT = A.take<bf16_t>(BH * T * LM_HD);
-    S.P = A.take<bf16_t>(BH * T * T);
+    S.att_stats = A.take<float>(2 * BH * T);
+    S.Of = A.take<float>(BH * T * LM_HD);
     for (int k = 0; k < LM_NK; ++k) {
       S.site[k].xV = A.take<bf16_t>(N * D.C[k]);
       S.site[k].acts = A.take<bf16_t>(N * D.C[k]);
@@ -835,22 +1153,16 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   P.kc = A.take<bf16_t>(N * qd);
   P.vc = A.take<bf16_t>(N * qd);
   P.ac = A.take<bf16_t>(N * qd);
-  P.Oh = A.take<bf16_t>(BH * T * LM_HD);
   P.fcc = A.take<bf16_t>(N * f);
   P.gc = A.take<bf16_t>(N * f);
   P.q = A.take<bf16_t>(N * qd);
   P.k = A.take<bf16_t>(N * qd);
   P.v = A.take<bf16_t>(N * qd);
   P.rinvF = A.take<float>(N);
-  P.S = A.take<float>(BH * T * T);
+  P.att_D = A.take<float>(BH * T);
   P.cQh = A.take<bf16_t>(BH * T * LM_HD);
   P.cKh = A.take<bf16_t>(BH * T * LM_HD);
-  P.cKhT = A.take<bf16_t>(BH * T * LM_HD);
   P.cVh = A.take<bf16_t>(BH * T * LM_HD);
-  P.cVhT = A.take<bf16_t>(BH * T * LM_HD);
-  P.cOh = A.take<bf16_t>(BH * T * LM_HD);
-  P.cP = A.take<bf16_t>(BH * T * T);
-  P.cS = A.take<float>(BH * T * T);
   P.delta = A.take<float>((size_t)D.L * LM_NK * N);
   P.imp_total = 0;
   for (int k = 0; k < LM_NK; ++k) {
@@ -891,11 +1203,9 @@ static LMPlan lm_plan(const LMDims& D, char* base, bool dry) {
   for (int b = 0; b < 2; ++b) P.dxV[b] = A.take<bf16_t>(N * maxC);
   for (int i = 0; i < 3; ++i) P.dqkv[i] = A.take<bf16_t>(N * qd);
   P.da = A.take<bf16_t>(N * qd);
-  P.dOh = A.take<bf16_t>(BH * T * LM_HD);
   P.dQh = A.take<bf16_t>(BH * T * LM_HD);
   P.dKh = A.take<bf16_t>(BH * T * LM_HD);
   P.dVh = A.take<bf16_t>(BH * T * LM_HD);
-  P.dS = A.take<bf16_t>(BH * T * T);
   P.dg = A.take<bf16_t>(N * f);
   P.dfc = A.take<bf16_t>(N * f);
   P.kl_ws_bytes = pd_streamed_kl_workspace_size(PD_DTYPE_BF16, N, d, D.V, D.n_chunks);
@@ -1085,7 +1395,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
   hipStream_t s = (hipStream_t)stream;
   rec.s = s;
   const int64_t N = D.N, BH = D.BH();
-  const float log2b = log2f(rope_base), att_scale = 1.f / sqrtf((float)LM_HD);
+  const float log2b = log2f(rope_base);
   const int pm = imp_mode(imp);
   const bool sl0 = pm == PM_SL0;
   int rc;
@@ -1128,22 +1438,19 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
                        halves[3], N, layout, P.delta);
   if ((rc = check_launch("pd_lm_stack_step prep"))) return rc;
 
-  // ================= attention forward on head-major copies
-  // on stream st, with scores Sb and head-major output Ob as scratch
-  auto attn_fwd = [&](const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* Qh, bf16_t* Kh, bf16_t* KhT,
-                      bf16_t* Vh, bf16_t* VhT, bf16_t* Pm, bf16_t* a, float* Sb, bf16_t* Ob, hipStream_t st) -> int {
+  // ================= fused causal attention on head-major copies, output a row-major;
+  // Ls (a layer's saves) also receives the row stats and fp32 output the backward reads
+  const dim3 fa_grid((unsigned)cdiv(T, FA_SPAN), (unsigned)BH);
+  auto attn_fwd = [&](const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* Qh, bf16_t* Kh, bf16_t* Vh,
+                      LMLayerSave* Ls, bf16_t* a, hipStream_t st) -> int {
     hipLaunchKernelGGL(k_lm_attn_in, dim3((unsigned)(T / TILE), (unsigned)H, (unsigned)B), dim3(256), 0, st, q, k, v,
-                       T, H, KV, log2b, Qh, Kh, KhT, Vh, VhT);
-    // causal: score tiles above the diagonal are not formed, and P @ V contracts each
-    // query tile only over keys up to its last row
-    int r = gemm_batched_causal(1, PD_DTYPE_BF16, BH, T, T, LM_HD, Qh, LM_HD, T * LM_HD, 0, Kh, LM_HD, T * LM_HD, 1,
-                                Sb, T, T * T, PD_DTYPE_F32, 1.f, 0.f, st);
-    if (r) return r;
-    hipLaunchKernelGGL(k_lm_softmax_fwd, rows4(BH * T), dim3(256), 0, st, Sb, BH * T, (int)T, att_scale, Pm);
-    if ((r = gemm_batched_causal(2, PD_DTYPE_BF16, BH, T, LM_HD, T, Pm, T, T * T, 0, VhT, T, LM_HD * T, 1, Ob,
-                                 LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, st)))
-      return r;
-    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, st, a, Ob, B, T, H, 0);
+                       T, H, KV, log2b, Qh, Kh, Vh);
+    if (Ls)
+      hipLaunchKernelGGL(k_lm_flash_fwd<true>, fa_grid, dim3(FA_THREADS), 0, st, Qh, Kh, Vh, (int)T, H, a,
+                         Ls->att_stats, Ls->Of);
+    else
+      hipLaunchKernelGGL(k_lm_flash_fwd<false>, fa_grid, dim3(FA_THREADS), 0, st, Qh, Kh, Vh, (int)T, H, a,
+                         (float*)nullptr, (float*)nullptr);
     return check_launch("pd_lm_stack_step attention");
   };
 
@@ -1164,7 +1471,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
       if ((rc = gemm_nt(N, qd, d, P.hc, d, Wk(LK_Q), d, P.qc, qd, PD_DTYPE_BF16, 0.f, sc))) return rc;
       if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_K), d, P.kc, kvd, PD_DTYPE_BF16, 0.f, sc))) return rc;
       if ((rc = gemm_nt(N, kvd, d, P.hc, d, Wk(LK_V), d, P.vc, kvd, PD_DTYPE_BF16, 0.f, sc))) return rc;
-      if ((rc = attn_fwd(P.qc, P.kc, P.vc, P.cQh, P.cKh, P.cKhT, P.cVh, P.cVhT, P.cP, P.ac, P.cS, P.cOh, sc)))
+      if ((rc = attn_fwd(P.qc, P.kc, P.vc, P.cQh, P.cKh, P.cVh, nullptr, P.ac, sc)))
         return rc;
       if ((rc = gemm_nt(N, d, qd, P.ac, qd, Wk(LK_O), qd, P.hc, d, PD_DTYPE_BF16, 0.f, sc))) return rc;
       hipLaunchKernelGGL(k_lm_add, dim3(ew_blocks(N * d / 8)), dim3(256), 0, sc, rcur, P.hc, N * d, rnext);
@@ -1266,7 +1573,7 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if ((rc = site_fwd(LK_K, l, S.h, P.k))) return rc;
     if ((rc = site_fwd(LK_V, l, S.h, P.v))) return rc;
     rec.mark(LM_CAT_ATTN);
-    if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.KhT, S.Vh, S.VhT, S.P, S.a, P.S, P.Oh, s))) return rc;
+    if ((rc = attn_fwd(P.q, P.k, P.v, S.Qh, S.Kh, S.Vh, &S, S.a, s))) return rc;
     rec.mark(LM_CAT_ELEM);
     if ((rc = site_fwd(LK_O, l, S.a, P.q))) return rc;  // o output into the q scratch
     rec.mark(LM_CAT_ELEM);
@@ -1407,23 +1714,11 @@ static int lm_step_impl(int64_t B, int64_t T, int d, int H, int KV, int f, int64
     if ((rc = site_bwd(LK_O, l, dr, S.a, P.da, false, 0.f))) return rc;
     // attention backward
     rec.mark(LM_CAT_ATTN);
-    hipLaunchKernelGGL(k_lm_heads, dim3(ew_blocks(N * H * (LM_HD / 8))), dim3(256), 0, s, P.da, P.dOh, B, T, H, 1);
-    // dP = dO @ V^T (fp32, tiles on or below the diagonal), dS
-    if ((rc = gemm_batched_causal(1, PD_DTYPE_BF16, BH, T, T, LM_HD, P.dOh, LM_HD, T * LM_HD, 0, S.Vh, LM_HD,
-                                  T * LM_HD, 1, P.S, T, T * T, PD_DTYPE_F32, 1.f, 0.f, s)))
-      return rc;
-    hipLaunchKernelGGL(k_lm_softmax_bwd, rows4(BH * T), dim3(256), 0, s, S.P, P.S, BH * T, (int)T, att_scale, P.dS);
-    // dQ = dS @ K (B^T = K^T; keys up to the query tile's last row), dK = dS^T @ Q,
-    // dV = P^T @ dO (queries from the key tile's first row)
-    if ((rc = gemm_batched_causal(2, PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 0, S.KhT, T, LM_HD * T, 1, P.dQh,
-                                  LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
-      return rc;
-    if ((rc = gemm_batched_causal(3, PD_DTYPE_BF16, BH, T, LM_HD, T, P.dS, T, T * T, 1, S.Qh, LM_HD, T * LM_HD, 0,
-                                  P.dKh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
-      return rc;
-    if ((rc = gemm_batched_causal(3, PD_DTYPE_BF16, BH, T, LM_HD, T, S.P, T, T * T, 1, P.dOh, LM_HD, T * LM_HD, 0,
-                                  P.dVh, LM_HD, T * LM_HD, PD_DTYPE_BF16, 1.f, 0.f, s)))
-      return rc;
+    // dQ (query spans; also the softmax row sums D), then dK, dV (key spans)
+    hipLaunchKernelGGL(k_lm_flash_dq, fa_grid, dim3(FA_THREADS), 0, s, S.Qh, S.Kh, S.Vh, P.da, S.Of, S.att_stats,
+                       (int)T, H, P.dQh, P.att_D);
+    hipLaunchKernelGGL(k_lm_flash_dkv, fa_grid, dim3(FA_THREADS), 0, s, S.Qh, S.Kh, S.Vh, P.da, S.att_stats, P.att_D,
+                       (int)T, H, P.dKh, P.dVh);
     hipLaunchKernelGGL(k_lm_attn_out_grads, dim3((unsigned)(T / TILE), (unsigned)KV, (unsigned)B), dim3(256), 0, s,
                        P.dQh, P.dKh, P.dVh, T, H, KV, log2b, P.dqkv[0], P.dqkv[1], P.dqkv[2]);
     if ((rc = check_launch("pd_lm_stack_step attention backward"))) return rc;

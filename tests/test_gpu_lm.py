@@ -70,12 +70,14 @@ SL0 = dict(kind="smooth_l0", coeff=0.05, gamma=0.4, normalize_at_one=False, freq
 
 @pytest.mark.parametrize("n_kv,use_delta,partitionable,T,sl0", [(2, True, True, 64, None), (1, True, False, 64, None),
                                                                (2, False, True, 64, None), (2, True, True, 512, None),
-                                                               (2, True, True, 128, SL0), (1, True, True, 320, None)])
+                                                               (2, True, True, 128, SL0), (1, True, True, 320, None),
+                                                               (2, True, True, 576, None)])
 def test_lm_stack_step_matches_oracle(device, n_kv, use_delta, partitionable, T, sl0):
     """T = 512 (1024 tokens) puts the weight-gradient products on the split-contraction
-    path (slices of the token axis added in order); T = 320 ends in a partial 128-row
-    attention tile (the causal products skip tiles above the diagonal blocks); sl0 runs the
-    smooth-L0 term."""
+    path (slices of the token axis added in order); the fused attention works on spans of
+    up to 512 rows per workgroup: T = 320 fills 5 of a span's 8 waves, T = 576 runs two
+    spans (the second one 64 rows long) with the other side staged through LDS in two
+    stages; sl0 runs the smooth-L0 term."""
     from param_decomp_amd import _lib as L
     from param_decomp_amd.losses import ImpMin
     from param_decomp_amd.lm_step import LMStackStep
