@@ -1343,8 +1343,8 @@ def toy_cpu_baseline(workload, cfg, reps=5):
 def run_toy(args):
     """The toy decomposition step: clean forward, per-site gate MLPs and CI, Threefry
     masks (fp32 draws), masked forward, MSE + L_p imp-min and the backward. TMS runs as one
-    fused kernel (pd_tms_step); ResidMLP through the HIP primitives under torch autograd,
-    captured once into a HIP graph that each step replays with that step's mask keys."""
+    fused kernel (pd_tms_step); ResidMLP as one native call (pd_resid_mlp_step: the fp32
+    products and one fused CI / mask pass per site and direction)."""
     import torch
 
     from param_decomp_amd import hip_events, prng, toys
@@ -1360,9 +1360,8 @@ def run_toy(args):
     x = toys.sparse_features(cfg["B"], cfg["n_features"], cfg["p_feat"], cfg["low"], device=dev, generator=g)
     if args.workload == TMS:  # one fused launch (+ one reduction) per step
         step = toys.TMSFusedStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
-    else:  # one captured graph per step (the eager step is bound by its ~90 host-side launches)
-        step = toys.GraphedToyStep(toys.ToyDecompositionStep(target, sites, p=cfg["p"], imp_coeff=1.0,
-                                                             recon_coeff=1.0), x)
+    else:  # one native call per step
+        step = toys.ResidMLPFusedStep(target, sites, p=cfg["p"], imp_coeff=1.0, recon_coeff=1.0)
     for i in range(args.warmup):
         step.step(x, prng.fold_in((0, 0), i))
     keys = [prng.fold_in((0, 0), args.warmup + i) for i in range(args.steps)]  # the training loop's step keys
@@ -1383,13 +1382,13 @@ def run_toy(args):
                       "gate_hidden": 16, "recon": "mse", "mask_draw": "threefry fp32 (partitionable)"},
            "step_flops": flops, "phases_ms": {"step": ms},
            "roofline": dict(roofline("flop32", flops, ms, "whole step" if args.workload == TMS else
-                                     "whole step (fp32, one graph replay of ~90 small launches)", 1),
+                                     "whole step (fp32, one native call of 31 launches)", 1),
                             note="TMS: one fused launch (k_tms_step) plus one reduction per step, bound by the "
                                  "CI gates' exact-erf GELUs and the Threefry draws on the vector ALUs; the FLOPs "
                                  "counted (the reference rule) are only its tiny contractions" if args.workload == TMS
-                            else "one graph replay of ~90 small launches (GEMMs of 2048 rows over d 1000/100/50, "
-                                 "gate MLPs, masks, losses); its contractions are microseconds of fp32 MFMA work "
-                                 "each")}
+                            else "one native call (pd_resid_mlp_step): 17 fp32 GEMMs of 2048 rows over d "
+                                 "1000/100/50, one fused CI / mask pass per site forward and backward, relu, recon "
+                                 "and loss passes; its contractions are microseconds of fp32 MFMA work each")}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = toy_cpu_baseline(args.workload, cfg)
     return out

@@ -467,6 +467,27 @@ int pd_tms_step(int64_t B, int F, int H, int C, const float* x, const float* W1,
                 float recon_coeff, float* grads, float* losses, void* workspace, size_t workspace_bytes,
                 void* stream);
 
+/* ---- the ResidMLP toy decomposition step as one native call (pd/targets/resid_mlp.py:266-418) ----
+ * target r_0 = x W_E, per layer r += relu(r W_in[l]^T) W_out[l]^T (no biases), out = r W_U;
+ * every mlp_in (W_in [M,D]) and mlp_out (W_out [D,M]) decomposed (sites in the order
+ * layers.0.mlp_in, layers.0.mlp_out, ...) with the paper-form gate on the clean input's
+ * a @ V and fp32 Threefry masks m = lower + (1 - lower) u under the site keys
+ * fold_in(split(draw_key)[0], site) (pd/core/masking.py:148-167); loss = recon_coeff
+ * mse(out, clean) + imp_coeff sum_sites sum_c mean_b upper^p, fwd + bwd. x [B,F],
+ * W_E [F,D], W_U [D,F] fp32; W_in, W_out: L pointers each; V, U: 2L pointers (V [din,C],
+ * U [C,dout]); gates: 8L pointers (per site w_in [C,16], b_in [C,16], w_out [C,16],
+ * b_out [C]). grads fp32 (pd_resid_mlp_step_grads_size floats): per site dV | dU | gate
+ * (w_in, b_in, w_out, b_out); losses[3] = {loss, recon, imp}; out [B,F] (the masked
+ * output) or NULL. Deterministic. No weight-delta channel or routes (the composed step
+ * in param_decomp_amd/toys.py has them). */
+size_t pd_resid_mlp_step_workspace_size(int64_t B, int F, int D, int M, int C, int L);
+int64_t pd_resid_mlp_step_grads_size(int D, int M, int C, int L);
+int pd_resid_mlp_step(int64_t B, int F, int D, int M, int C, int L, const float* x, const float* W_E,
+                      const float* W_U, const float* const* W_in, const float* const* W_out, const float* const* V,
+                      const float* const* U, const float* const* gates, uint32_t draw_k0, uint32_t draw_k1,
+                      int layout, float p, float imp_coeff, float recon_coeff, float* grads, float* losses,
+                      float* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- the decomposed Llama-style LM step (one stochastic-recon KL step, fwd + bwd) -----
  * The pre-RMSNorm transformer of pd/targets/transformer.py:1031-1140 in its
  * LlamaSimpleMLP form (pd/targets/llama_simple_mlp.py: rotate-half RoPE, causal GQA

@@ -93,6 +93,10 @@ _SIGNATURES = {
     "pd_tms_step_grads_size": (_c_i32, [_c_i32, _c_i32, _c_i32]),
     "pd_tms_step": (_c_i32, [_c_i64] + [_c_i32] * 3 + [_c_p] * 7 + [_c_p, _c_u32, _c_u32, _c_i32, _c_i32, _c_p] +
                     [_c_f32] * 3 + [_c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "pd_resid_mlp_step_workspace_size": (_c_sz, [_c_i64] + [_c_i32] * 5),
+    "pd_resid_mlp_step_grads_size": (_c_i64, [_c_i32] * 4),
+    "pd_resid_mlp_step": (_c_i32, [_c_i64] + [_c_i32] * 5 + [_c_p] * 8 + [_c_u32, _c_u32, _c_i32] + [_c_f32] * 3 +
+                          [_c_p] * 4 + [_c_sz, _c_p]),
     "pd_lm_stack_workspace_size": (_c_sz, [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32, _c_p, _c_i32, _c_i32]),
     "pd_lm_stack_step": (_c_i32,
                          [_c_i64, _c_i64] + [_c_i32] * 4 + [_c_i64, _c_i32] + [_c_p] * 6 + [_c_f32, _c_f32] +

@@ -257,6 +257,80 @@ class GraphedToyStep:
         return self.out
 
 
+class ResidMLPFusedStep:
+    """The ResidMLP decomposition step of `ToyDecompositionStep` (same objective, draws and
+    gradients; bias-free blocks, no weight-delta channel or routes) as one native call
+    (`pd_resid_mlp_step`): the fp32 MFMA products plus one fused CI / mask pass per site
+    forward and one backward, about a third of the composed step's launches. The gradients
+    land in the sites' `.grad` as views of one flat buffer; `out` is the masked output."""
+
+    def __init__(self, target: ResidMLPTarget, sites, *, p: float = 1.0, imp_coeff: float = 1.0,
+                 recon_coeff: float = 1.0, layout: int | None = None):
+        from param_decomp_amd import _lib as L
+
+        if any(b is not None for b in target.b_in + target.b_out):
+            raise L.PDError("ResidMLPFusedStep: bias-free blocks only (the composed step takes biases)")
+        self.target, self.sites = target, sites
+        self.F, self.D = target.W_E.shape
+        self.L = len(sites) // 2
+        self.M = sites[0].W.shape[0]
+        self.C = sites[0].V.shape[1]
+        self.p, self.imp_coeff, self.recon_coeff = p, imp_coeff, recon_coeff
+        self.layout = L.LAYOUT_PARTITIONABLE if layout is None else layout
+        dev = target.W_E.device
+        D, M, C = self.D, self.M, self.C
+        self.flat = torch.zeros(L.load().pd_resid_mlp_step_grads_size(D, M, C, self.L), dtype=torch.float32,
+                                device=dev)
+        self.losses = torch.zeros(3, dtype=torch.float32, device=dev)
+        self.views = []
+        o = 0
+        for i in range(len(sites)):
+            din, dout = (M, D) if i % 2 else (D, M)
+            dV = self.flat[o:o + din * C].view(din, C)
+            o += din * C
+            dU = self.flat[o:o + C * dout].view(C, dout)
+            o += C * dout
+            gv = []
+            for shape in ((C, 16), (C, 16), (C, 16), (C,)):
+                k = shape[0] * (shape[1] if len(shape) > 1 else 1)
+                gv.append(self.flat[o:o + k].view(*shape))
+                o += k
+            self.views.append((dV, dU, gv))
+        self._ws = None
+        self._out = None
+        self._keep = None
+
+    def step(self, x: torch.Tensor, draw_key: Key) -> dict:
+        import ctypes
+
+        from param_decomp_amd import _lib as L
+
+        B = x.shape[0]
+        lib = L.load()
+        nbytes = lib.pd_resid_mlp_step_workspace_size(B, self.F, self.D, self.M, self.C, self.L)
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = L.workspace(nbytes, x.device)
+        if self._out is None or self._out.shape[0] != B:
+            self._out = torch.empty(B, self.F, dtype=torch.float32, device=x.device)
+        sites = self.sites
+        arrays = (L.host_array(ctypes.c_void_p, [L.ptr(sites[2 * i].W) for i in range(self.L)]),
+                  L.host_array(ctypes.c_void_p, [L.ptr(sites[2 * i + 1].W) for i in range(self.L)]),
+                  L.host_array(ctypes.c_void_p, [L.ptr(s.V) for s in sites]),
+                  L.host_array(ctypes.c_void_p, [L.ptr(s.U) for s in sites]),
+                  L.host_array(ctypes.c_void_p, [L.ptr(t) for s in sites for t in
+                                                 (s.gate.w_in, s.gate.b_in, s.gate.w_out, s.gate.b_out)]))
+        self._keep = arrays
+        L.call("pd_resid_mlp_step", B, self.F, self.D, self.M, self.C, self.L, L.ptr(x.contiguous()),
+               L.ptr(self.target.W_E), L.ptr(self.target.W_U), *arrays, draw_key[0], draw_key[1], self.layout,
+               self.p, self.imp_coeff, self.recon_coeff, L.ptr(self.flat), L.ptr(self.losses), L.ptr(self._out),
+               L.ptr(self._ws), self._ws.numel(), L.stream())
+        for s, (dV, dU, gv) in zip(sites, self.views):
+            s.V.grad, s.U.grad = dV, dU
+            for prm, g in zip(s.gate.parameters(), gv):
+                prm.grad = g
+        return {"loss": self.losses[0], "recon": self.losses[1], "imp": self.losses[2], "out": self._out}
+
+
 class TMSFusedStep:
     """The TMS decomposition step of `ToyDecompositionStep` (same objective, draws and
     gradients) as one fused launch plus one reduction (`pd_tms_step`): each wave owns 64

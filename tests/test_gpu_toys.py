@@ -139,6 +139,31 @@ def test_resid_mlp_1l_step_matches_oracle(device, use_delta):
     _compare(res, sites, want)
 
 
+@pytest.mark.parametrize("n_layers,B", [(1, 2048), (2, 1003)])
+def test_resid_mlp_fused_step_matches_oracle(device, n_layers, B):
+    """The native ResidMLP step (pd_resid_mlp_step) against the same oracle: the benchmark
+    shape, and two layers (the second mlp_in's masked input differs from its clean gate
+    input, and the residual cotangent flows through the first layer) with a batch that is
+    not a multiple of the site passes' 8-row chunks; then bit-identical on a second call."""
+    from param_decomp_amd import toys
+
+    g = torch.Generator(device=device).manual_seed(1)
+    target, sites = toys.init_resid_mlp(100, 1000, 50, n_layers, 100, device=device, generator=g)
+    _vary_gates(sites, g)
+    x = toys.sparse_features(B, 100, 0.01, -1.0, device=device, generator=g)
+    key = (5, 6)
+    step = toys.ResidMLPFusedStep(target, sites, p=2.0, imp_coeff=0.1, recon_coeff=1.0)
+    res = step.step(x, key)
+    torch.cuda.synchronize()
+    tgt = {"W_E": _np(target.W_E), "W_U": _np(target.W_U), "layers": [{"b_in": None, "b_out": None}] * n_layers}
+    want = to.toy_step("resid_mlp", tgt, _oracle_sites(sites), _np(x), key, p=2.0, imp_coeff=0.1, recon_coeff=1.0)
+    _compare(res, sites, want)
+    flat, out = step.flat.clone(), res["out"].clone()
+    res = step.step(x, key)
+    torch.cuda.synchronize()
+    assert torch.equal(step.flat, flat) and torch.equal(res["out"], out)
+
+
 def test_resid_mlp_graphed_step_matches_eager(device):
     """The ResidMLP-1L step captured into a HIP graph (mask keys read from a device buffer
     the host rewrites before each replay) against the eager step with the same draw keys:
