@@ -337,9 +337,7 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 //   a K-contiguous operand is 8 consecutive floats per lane: two 16-byte loads when
 //     `vec` says rows are 16-byte aligned and K % 4 == 0 (each 4-run then lies wholly
 //     inside or outside the k range), else 8 dwords through the descriptor.
-// The loads of the next three batches are in flight during this batch's 8 MFMAs (at these
-// products' one or two waves per SIMD one batch ahead left most of the load latency
-// exposed: 2.4x the time at the residual-MLP target's products). Block forms as in
+// The next batch's loads are in flight during this batch's 8 MFMAs. Block forms as in
 // k_gemm_f32 (KW waves splitting the contraction of a 32x32 tile, or 4 waves of a 64x64
 // tile); the summation order is fixed. Measured at the residual-MLP target's products
 // (2048 rows, d 1000 / 100 / 50) it takes 0.35-0.6x the time of the LDS-staged form: those
@@ -413,21 +411,14 @@ __global__ __launch_bounds__(KW > 1 ? 64 * KW : 256) void k_gemm_f32_direct(
 #pragma unroll
     for (int s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
   };
-  // a ring of NB chunks: chunk i sits in slot i % NB, loaded NB - 1 chunks ahead of its MFMAs
-  // (1024-thread blocks have 128 registers a lane: three slots)
-  constexpr int NB = KW >= 16 ? 3 : 4;
-  float a[NB][S], b[NB][S];
-#pragma unroll
-  for (int q = 0; q < NB - 1; ++q)
-    if (kb + q * FK < ke) load(a[q], b[q], kb + q * FK);
-  for (int kc = kb; kc < ke; kc += NB * FK) {
-#pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const int k = kc + q * FK;
-      if (k >= ke) break;
-      if (k + (NB - 1) * FK < ke) load(a[(q + NB - 1) % NB], b[(q + NB - 1) % NB], k + (NB - 1) * FK);
-      mma(a[q], b[q]);
-    }
+  float a0[S], b0[S], a1[S], b1[S];
+  if (kb < ke) load(a0, b0, kb);
+  for (int kc = kb; kc < ke; kc += 2 * FK) {
+    if (kc + FK < ke) load(a1, b1, kc + FK);
+    mma(a0, b0);
+    if (kc + FK >= ke) break;
+    if (kc + 2 * FK < ke) load(a0, b0, kc + 2 * FK);
+    mma(a1, b1);
   }
   // lane holds column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4 of its tile
   if constexpr (SPLIT) {

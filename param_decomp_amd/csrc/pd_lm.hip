@@ -555,13 +555,56 @@ __device__ inline f32x16 att_mm(const bf16x8 (&x)[4], const bf16x8 (&y)[4]) {
 __device__ inline int att_xrow(int i, int hh) { return 8 * (i >> 2) + 4 * hh + (i & 3); }
 __device__ inline float att_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Scores of one 32-row block of the image against the wave's Y fragments:
+// out[lane: Y row r][reg: image row R0 + 8 g + 4 hh + e].
+__device__ inline f32x16 fa_scores(const char* img, int R0, int r, int hh, const bf16x8 (&yf)[4]) {
+  bf16x8 xf[4];
+  fa_rows(img, R0 + r, hh, xf);
+  return att_mm(xf, yf);
+}
+// Forward pass 1 on one key block: the row's running max m (in 2^x units, taken over the
+// scaled scores, whose products are canonical) and this lane's partial sum l.
+template <bool DIAG>
+__device__ inline void fa_rowstats(const f32x16& sc, int r, int hh, float& m, float& l) {
+  float t[16], bm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    t[i] = sc[i] * FA_C2;
+    if (!DIAG || att_xrow(i, hh) <= r) bm = fmaxf(bm, t[i]);
+  }
+  const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (!DIAG || att_xrow(i, hh) <= r) acc += att_exp2(t[i] - mn);
+  l = l * att_exp2(m - mn) + acc;  // the first block: m = -inf, l = 0
+  m = mn;
+}
+// P = 2^(s C2 - m) / l on one block (0 above the diagonal).
+template <bool DIAG>
+__device__ inline void fa_probs(const f32x16& sc, int r, int hh, float m, float il, float (&p)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = (!DIAG || att_xrow(i, hh) <= r) ? att_exp2(fmaf(sc[i], FA_C2, -m)) * il : 0.f;
+}
+// dS = (dP - D) bf16(P) / 8 on one block of a query-major tile.
+template <bool DIAG>
+__device__ inline void fa_dscores(const f32x16& sc, const f32x16& dp, int r, int hh, float m, float il, float D,
+                                  float (&ds)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = (!DIAG || att_xrow(i, hh) <= r) ? bf16r(att_exp2(fmaf(sc[i], FA_C2, -m)) * il) : 0.f;
+    ds[i] = (dp[i] - D) * (p * FA_SCALE);
+  }
+}
+
 // Forward: a = softmax(Q K^T / 8, causal) V written row-major into a [B*T, H*64] (bf16; P
-// rounded to bf16 before the product, as a materialized P is stored). Pass 1 forms each
-// query row's max and sum of exp over its keys (both halves of a wave carry the row's
-// running max, each its own partial sum); pass 2 forms P = 2^(s C2 - m) / l and
-// accumulates P V. With SAVE the row's m and 1/l (stats [2][B*H*T]) and the fp32 output
-// (Of [B*H, T, 64]) are kept for the backward. Grid (query spans, B*H), the spans with
-// the most keys first.
+// rounded to bf16 before the product, as a materialized P is stored). Per tile, pass 1
+// forms each query row's max and sum of exp over its keys (both halves of a wave carry
+// the row's running max, each its own partial sum); pass 2 forms P = 2^(s C2 - m) / l and
+// accumulates P V. Each block's scores are formed one block ahead of its softmax math, and
+// the diagonal block (the tile's last) runs the masked variant. With SAVE the row's m and
+// 1/l (stats [2][B*H*T]) and the fp32 output (Of [B*H, T, 64]) are kept for the backward.
+// Grid (query spans, B*H), the spans with the most keys first.
 template <bool SAVE>
 __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_fwd(const bf16_t* __restrict__ Qh,
                                                              const bf16_t* __restrict__ Kh,
@@ -574,105 +617,83 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_fwd(const bf16_t* __res
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, hh = lane >> 5;
   const int s = (int)gridDim.x - 1 - (int)blockIdx.x;
   const int64_t bh = blockIdx.y, BHT = (int64_t)gridDim.y * T;
+  const int64_t b = bh / H, hd = bh % H;
   const int q0 = s * FA_SPAN, nt = min(FA_SPAN, T - q0) / 32;
   const bool act = w < nt / 2;
   const int tl[2] = {w, nt - 1 - w};
   const bf16_t* K = Kh + bh * T * LM_HD;
   const bf16_t* V = Vh + bh * T * LM_HD;
-  bf16x8 qf[2][4];
-  if (act) {
-    att_rows(Qh + bh * T * LM_HD, LM_HD, q0 + 32 * tl[0] + r, hh, qf[0]);
-    att_rows(Qh + bh * T * LM_HD, LM_HD, q0 + 32 * tl[1] + r, hh, qf[1]);
-  }
-  const bool one = s == 0;  // a single stage of keys: K and V stay resident for both passes
+  const bool one = s == 0;  // a single stage of keys: K and V stay resident throughout
   if (one) {
     fa_stage(Kl, K, LM_HD, min(FA_SPAN, T), tid);
     fa_stage(Vl, V, LM_HD, min(FA_SPAN, T), tid);
     __syncthreads();
   }
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  for (int c = 0; c <= s; ++c) {
-    if (!one) {
-      __syncthreads();
-      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
-      __syncthreads();
-    }
-    if (!act) continue;
-#pragma unroll
-    for (int X = 0; X < 2; ++X) {
-      const int nb = c < s ? 16 : tl[X] + 1;
+#pragma unroll 1
+  for (int X = 0; X < 2; ++X) {
+    const int t = tl[X], qi = q0 + 32 * t + r;
+    bf16x8 qf[4];
+    if (act) att_rows(Qh + bh * T * LM_HD, LM_HD, qi, hh, qf);
+    float m = -INFINITY, l = 0.f;
+    for (int c = 0; c <= s; ++c) {
+      if (!one) {
+        __syncthreads();
+        fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+        __syncthreads();
+      }
+      if (!act) continue;
+      const int nb = c < s ? 16 : t + 1;
+      f32x16 sc = fa_scores(Kl, 0, r, hh, qf);
       for (int j = 0; j < nb; ++j) {
-        bf16x8 kf[4];
-        fa_rows(Kl, 32 * j + r, hh, kf);
-        const f32x16 sc = att_mm(kf, qf[X]);
-        const bool diag = c == s && j == tl[X];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (!diag || att_xrow(i, hh) <= r) bm = fmaxf(bm, sc[i]);
-        const float mn = fmaxf(m[X], fmaxf(bm, __shfl_xor(bm, 32, 64)) * FA_C2);
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (!diag || att_xrow(i, hh) <= r) acc += att_exp2(fmaf(sc[i], FA_C2, -mn));
-        l[X] = l[X] * att_exp2(m[X] - mn) + acc;  // the first block: m = -inf, l = 0
-        m[X] = mn;
+        const f32x16 cur = sc;
+        sc = fa_scores(Kl, 32 * min(j + 1, nb - 1), r, hh, qf);
+        if (c == s && j == nb - 1) fa_rowstats<true>(cur, r, hh, m, l);
+        else fa_rowstats<false>(cur, r, hh, m, l);
       }
     }
-  }
-  float il[2];
-#pragma unroll
-  for (int X = 0; X < 2; ++X) il[X] = 1.f / (l[X] + __shfl_xor(l[X], 32, 64));
-  f32x16 o[2][2] = {};
-  for (int c = 0; c <= s; ++c) {
-    if (!one) {
-      __syncthreads();
-      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
-      fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
-      __syncthreads();
-    }
-    if (!act) continue;
-#pragma unroll
-    for (int X = 0; X < 2; ++X) {
-      const int nb = c < s ? 16 : tl[X] + 1;
+    const float il = 1.f / (l + __shfl_xor(l, 32, 64));
+    f32x16 o[2] = {};
+    for (int c = 0; c <= s; ++c) {
+      if (!one) {
+        __syncthreads();
+        fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+        fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+        __syncthreads();
+      }
+      if (!act) continue;
+      const int nb = c < s ? 16 : t + 1;
+      f32x16 sc = fa_scores(Kl, 0, r, hh, qf);
       for (int j = 0; j < nb; ++j) {
-        bf16x8 kf[4];
-        fa_rows(Kl, 32 * j + r, hh, kf);
-        const f32x16 sc = att_mm(kf, qf[X]);
-        const bool diag = c == s && j == tl[X];
+        const f32x16 cur = sc;
+        sc = fa_scores(Kl, 32 * min(j + 1, nb - 1), r, hh, qf);
         float p[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          p[i] = (!diag || att_xrow(i, hh) <= r) ? att_exp2(fmaf(sc[i], FA_C2, -m[X])) * il[X] : 0.f;
+        if (c == s && j == nb - 1) fa_probs<true>(cur, r, hh, m, il, p);
+        else fa_probs<false>(cur, r, hh, m, il, p);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const bf16x8 pf = att_pack(p + 8 * kk);
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb)
-            o[X][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Vl, 32 * j, kk, cb, lane), pf, o[X][cb], 0, 0, 0);
+            o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Vl, 32 * j, kk, cb, lane), pf, o[cb], 0, 0, 0);
         }
       }
     }
-  }
-  if (!act) return;
-  const int64_t b = bh / H, hd = bh % H;
-#pragma unroll
-  for (int X = 0; X < 2; ++X) {
-    const int qi = q0 + 32 * tl[X] + r;
+    if (!act) continue;
     bf16_t* arow = a + ((b * T + qi) * H + hd) * LM_HD;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int ch = cb * 32 + 8 * g + 4 * hh;
-        const f32x16& ov = o[X][cb];
-        *(uint2*)(arow + ch) = make_uint2(pack_bf16x2(ov[4 * g], ov[4 * g + 1]), pack_bf16x2(ov[4 * g + 2], ov[4 * g + 3]));
+        *(uint2*)(arow + ch) =
+            make_uint2(pack_bf16x2(o[cb][4 * g], o[cb][4 * g + 1]), pack_bf16x2(o[cb][4 * g + 2], o[cb][4 * g + 3]));
         if (SAVE)
-          *(float4*)(Of + (bh * T + qi) * LM_HD + ch) = make_float4(ov[4 * g], ov[4 * g + 1], ov[4 * g + 2], ov[4 * g + 3]);
+          *(float4*)(Of + (bh * T + qi) * LM_HD + ch) =
+              make_float4(o[cb][4 * g], o[cb][4 * g + 1], o[cb][4 * g + 2], o[cb][4 * g + 3]);
       }
     if (SAVE && hh == 0) {
-      stats[bh * T + qi] = m[X];
-      stats[BHT + bh * T + qi] = il[X];
+      stats[bh * T + qi] = m;
+      stats[BHT + bh * T + qi] = il;
     }
   }
 }
@@ -680,8 +701,8 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_fwd(const bf16_t* __res
 // dQ = dS K per query row, dS = bf16(P (dP - D) / 8), dP = dO V^T, P = bf16(2^(s C2 - m) / l)
 // from the forward's row stats, D = sum_c dO O over the forward's fp32 output (equal to
 // sum_j P dP for the same P; written to Dq for the key-side kernel). dO is read from the
-// cotangent da [B*T, H*64]. Spans and waves as the forward's; K and V staged through LDS.
-// dQh [B*H, T, 64] bf16.
+// cotangent da [B*T, H*64]. Spans and waves as the forward's (one tile after the other, K
+// and V staged through LDS, scores and dP one block ahead). dQh [B*H, T, 64] bf16.
 __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dq(const bf16_t* __restrict__ Qh,
                                                             const bf16_t* __restrict__ Kh,
                                                             const bf16_t* __restrict__ Vh,
@@ -702,16 +723,22 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dq(const bf16_t* __rest
   const bf16_t* K = Kh + bh * T * LM_HD;
   const bf16_t* V = Vh + bh * T * LM_HD;
   const bf16_t* dO = da + (b * T * H + hd) * LM_HD;
-  bf16x8 qf[2][4], df[2][4];
-  float m[2], il[2], Dv[2];
-  if (act) {
-#pragma unroll
-    for (int X = 0; X < 2; ++X) {
-      const int qi = q0 + 32 * tl[X] + r;
-      att_rows(Qh + bh * T * LM_HD, LM_HD, qi, hh, qf[X]);
-      att_rows(dO, (int64_t)H * LM_HD, qi, hh, df[X]);
-      m[X] = stats[bh * T + qi];
-      il[X] = stats[BHT + bh * T + qi];
+  const bool one = s == 0;
+  if (one) {
+    fa_stage(Kl, K, LM_HD, min(FA_SPAN, T), tid);
+    fa_stage(Vl, V, LM_HD, min(FA_SPAN, T), tid);
+    __syncthreads();
+  }
+#pragma unroll 1
+  for (int X = 0; X < 2; ++X) {
+    const int t = tl[X], qi = q0 + 32 * t + r;
+    bf16x8 qf[4], df[4];
+    float m = 0.f, il = 0.f, Dv = 0.f;
+    if (act) {
+      att_rows(Qh + bh * T * LM_HD, LM_HD, qi, hh, qf);
+      att_rows(dO, (int64_t)H * LM_HD, qi, hh, df);
+      m = stats[bh * T + qi];
+      il = stats[BHT + bh * T + qi];
       // D over the channels this lane's dO fragments hold: 16 kk + 8 hh + 0..7
       const float* orow = Of + (bh * T + qi) * LM_HD;
       float dot = 0.f;
@@ -719,7 +746,7 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dq(const bf16_t* __rest
       for (int kk = 0; kk < 4; ++kk) {
         const float4 o0 = *(const float4*)(orow + 16 * kk + 8 * hh);
         const float4 o1 = *(const float4*)(orow + 16 * kk + 8 * hh + 4);
-        const att_u32x4 dw = (att_u32x4)df[X][kk];
+        const att_u32x4 dw = (att_u32x4)df[kk];
         dot = fmaf(bf_lo(dw[0]), o0.x, dot);
         dot = fmaf(bf_hi(dw[0]), o0.y, dot);
         dot = fmaf(bf_lo(dw[1]), o0.z, dot);
@@ -729,73 +756,81 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dq(const bf16_t* __rest
         dot = fmaf(bf_lo(dw[3]), o1.z, dot);
         dot = fmaf(bf_hi(dw[3]), o1.w, dot);
       }
-      Dv[X] = dot + __shfl_xor(dot, 32, 64);
-      if (hh == 0) Dq[bh * T + qi] = Dv[X];
+      Dv = dot + __shfl_xor(dot, 32, 64);
+      if (hh == 0) Dq[bh * T + qi] = Dv;
     }
-  }
-  const bool one = s == 0;
-  if (one) {
-    fa_stage(Kl, K, LM_HD, min(FA_SPAN, T), tid);
-    fa_stage(Vl, V, LM_HD, min(FA_SPAN, T), tid);
-    __syncthreads();
-  }
-  f32x16 dq[2][2] = {};
-  for (int c = 0; c <= s; ++c) {
-    if (!one) {
-      __syncthreads();
-      fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
-      fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
-      __syncthreads();
-    }
-    if (!act) continue;
-#pragma unroll
-    for (int X = 0; X < 2; ++X) {
-      const int nb = c < s ? 16 : tl[X] + 1;
+    f32x16 dq[2] = {};
+    for (int c = 0; c <= s; ++c) {
+      if (!one) {
+        __syncthreads();
+        fa_stage(Kl, K + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+        fa_stage(Vl, V + (int64_t)c * FA_SPAN * LM_HD, LM_HD, min(FA_SPAN, T - c * FA_SPAN), tid);
+        __syncthreads();
+      }
+      if (!act) continue;
+      const int nb = c < s ? 16 : t + 1;
+      f32x16 sc = fa_scores(Kl, 0, r, hh, qf), dp = fa_scores(Vl, 0, r, hh, df);
       for (int j = 0; j < nb; ++j) {
-        bf16x8 kf[4], vf[4];
-        fa_rows(Kl, 32 * j + r, hh, kf);
-        fa_rows(Vl, 32 * j + r, hh, vf);
-        const f32x16 sc = att_mm(kf, qf[X]);
-        const f32x16 dp = att_mm(vf, df[X]);
-        const bool diag = c == s && j == tl[X];
+        const f32x16 cs = sc, cp = dp;
+        const int jn = 32 * min(j + 1, nb - 1);
+        sc = fa_scores(Kl, jn, r, hh, qf);
+        dp = fa_scores(Vl, jn, r, hh, df);
         float ds[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = (!diag || att_xrow(i, hh) <= r) ? bf16r(att_exp2(fmaf(sc[i], FA_C2, -m[X])) * il[X]) : 0.f;
-          ds[i] = (dp[i] - Dv[X]) * (p * FA_SCALE);
-        }
+        if (c == s && j == nb - 1) fa_dscores<true>(cs, cp, r, hh, m, il, Dv, ds);
+        else fa_dscores<false>(cs, cp, r, hh, m, il, Dv, ds);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const bf16x8 sf = att_pack(ds + 8 * kk);
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb)
-            dq[X][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Kl, 32 * j, kk, cb, lane), sf, dq[X][cb], 0, 0, 0);
+            dq[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Kl, 32 * j, kk, cb, lane), sf, dq[cb], 0, 0, 0);
         }
       }
     }
-  }
-  if (!act) return;
-#pragma unroll
-  for (int X = 0; X < 2; ++X) {
-    bf16_t* out = dQh + (bh * T + q0 + 32 * tl[X] + r) * LM_HD;
+    if (!act) continue;
+    bf16_t* out = dQh + (bh * T + qi) * LM_HD;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x16& v = dq[X][cb];
+      for (int g = 0; g < 4; ++g)
         *(uint2*)(out + cb * 32 + 8 * g + 4 * hh) =
-            make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
-      }
+            make_uint2(pack_bf16x2(dq[cb][4 * g], dq[cb][4 * g + 1]), pack_bf16x2(dq[cb][4 * g + 2], dq[cb][4 * g + 3]));
   }
+}
+
+// Half kk of one key-major block of the key-side backward: P^T and dS^T for the lane's
+// key row against the 8 queries registers 8 kk .. 8 kk + 7 hold (row stats and D from
+// LDS), as bf16 operand slices.
+template <bool DIAG>
+__device__ inline void fa_kblock(const f32x16& st, const f32x16& dpt, const float (*qs)[FA_SPAN], int i0, int kk,
+                                 int r, int hh, bf16x8& pf, bf16x8& sf) {
+  float p[8], ds[8];
+#pragma unroll
+  for (int gg = 0; gg < 2; ++gg) {
+    const int g = 2 * kk + gg, qq = i0 + 8 * g + 4 * hh;
+    const float4 mq = *(const float4*)&qs[0][qq];
+    const float4 lq = *(const float4*)&qs[1][qq];
+    const float4 dq4 = *(const float4*)&qs[2][qq];
+    const float mv[4] = {mq.x, mq.y, mq.z, mq.w}, lv[4] = {lq.x, lq.y, lq.z, lq.w};
+    const float dv4[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = 4 * g + e;
+      const float pv = (!DIAG || att_xrow(ii, hh) >= r) ? bf16r(att_exp2(fmaf(st[ii], FA_C2, -mv[e])) * lv[e]) : 0.f;
+      p[4 * gg + e] = pv;
+      ds[4 * gg + e] = (dpt[ii] - dv4[e]) * (pv * FA_SCALE);
+    }
+  }
+  pf = att_pack(p);
+  sf = att_pack(ds);
 }
 
 // dK = dS^T Q and dV = P^T dO per key row: the workgroup owns a span of up to 512 keys
 // (waves pair key tiles as the forward pairs query tiles, one tile after the other) and
 // stages the queries from the span on, 512 at a time, through LDS (Q and dO rows, each
-// query's m, 1/l and D).
-// S^T = K Q^T and dP^T = V dO^T are formed key-major: each lane one key row, its
-// registers 16 queries. dKh, dVh [B*H, T, 64] bf16. Grid (key spans, B*H), the spans with
-// the most queries first.
+// query's m, 1/l and D). S^T = K Q^T and dP^T = V dO^T are formed key-major (each lane one
+// key row, its registers 16 queries); the diagonal block is the tile's first. dKh, dVh [B*H, T, 64] bf16. Grid (key spans, B*H), the spans with the
+// most queries first.
 __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dkv(const bf16_t* __restrict__ Qh,
                                                              const bf16_t* __restrict__ Kh,
                                                              const bf16_t* __restrict__ Vh,
@@ -816,7 +851,6 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dkv(const bf16_t* __res
   const int tl[2] = {w, nt - 1 - w};
   const bf16_t* Q = Qh + bh * T * LM_HD;
   const bf16_t* dO = da + (b * T * H + hd) * LM_HD;
-  // one key tile at a time; its queries in LDS stages (staged once when one stage holds them)
   auto stage = [&](int c) {
     const int c0 = c * FA_SPAN, n = min(FA_SPAN, T - c0);
     fa_stage(Ql, Q + (int64_t)c0 * LM_HD, LM_HD, n, tid);
@@ -827,7 +861,7 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dkv(const bf16_t* __res
       qs[2][tid] = Dq[bh * T + c0 + tid];
     }
   };
-  const bool one = ns - s == 1;
+  const bool one = ns - s == 1;  // one stage holds every query the span's keys meet
   if (one) {
     stage(s);
     __syncthreads();
@@ -848,42 +882,23 @@ __global__ __launch_bounds__(FA_THREADS) void k_lm_flash_dkv(const bf16_t* __res
         __syncthreads();
       }
       if (!act) continue;
-      const int ib0 = c == s ? tl[X] : 0, nb = min(FA_SPAN, T - c * FA_SPAN) / 32;
-      for (int i = ib0; i < nb; ++i) {
-        bf16x8 qf[4], of[4];
-        fa_rows(Ql, 32 * i + r, hh, qf);
-        fa_rows(Ol, 32 * i + r, hh, of);
-        const f32x16 st = att_mm(qf, kf);
-        const f32x16 dpt = att_mm(of, vf);
-        const bool diag = c == s && i == tl[X];
-        float p[16], ds[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int qq = 32 * i + 8 * g + 4 * hh;
-          const float4 mq = *(const float4*)&qs[0][qq];
-          const float4 lq = *(const float4*)&qs[1][qq];
-          const float4 dq4 = *(const float4*)&qs[2][qq];
-          const float mv[4] = {mq.x, mq.y, mq.z, mq.w}, lv[4] = {lq.x, lq.y, lq.z, lq.w};
-          const float dv4[4] = {dq4.x, dq4.y, dq4.z, dq4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ii = 4 * g + e;
-            const float pv =
-                (!diag || att_xrow(ii, hh) >= r) ? bf16r(att_exp2(fmaf(st[ii], FA_C2, -mv[e])) * lv[e]) : 0.f;
-            p[ii] = pv;
-            ds[ii] = (dpt[ii] - dv4[e]) * (pv * FA_SCALE);
-          }
-        }
+      auto block = [&](int i, auto diag) {
+        const f32x16 cs = fa_scores(Ql, 32 * i, r, hh, kf), cp = fa_scores(Ol, 32 * i, r, hh, vf);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const bf16x8 pf = att_pack(p + 8 * kk), sf = att_pack(ds + 8 * kk);
+          bf16x8 pf, sf;
+          fa_kblock<decltype(diag)::value>(cs, cp, qs, 32 * i, kk, r, hh, pf, sf);
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb) {
             dv[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Ol, 32 * i, kk, cb, lane), pf, dv[cb], 0, 0, 0);
             dk[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa_tr(Ql, 32 * i, kk, cb, lane), sf, dk[cb], 0, 0, 0);
           }
         }
-      }
+      };
+      int i = 0;
+      if (c == s) block(i = tl[X], std::true_type{});
+      const int nb = min(FA_SPAN, T - c * FA_SPAN) / 32;
+      for (i = c == s ? tl[X] + 1 : 0; i < nb; ++i) block(i, std::false_type{});
     }
     if (!act) continue;
     const int64_t row = (bh * T + kj) * LM_HD;
