@@ -768,13 +768,14 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl(GemmArgs p, typename EPI::
 // Two products of one shape in one block, P1 = A @ B^T and P2 = A2 @ B2^T (dense, every
 // operand K-contiguous with the same lda / ldb), for epilogues that need both tiles of the
 // same (row, column) block at once. A stage holds A | B | A2 | B2 (B2 == B shares B's
-// rows and skips their loads). EPI::run(p, ea, tile, wm, wn, tid, acc1, acc2, smem).
-template <class CFG, bool KEDGE, class EPI>
+// rows and skips their loads; with SHARED_B the caller guarantees B2 == B and a stage
+// has no B2 region). EPI::run(p, ea, tile, wm, wn, tid, acc1, acc2, smem).
+template <class CFG, bool KEDGE, class EPI, bool SHARED_B = false>
 __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename EPI::Args ea) {
   static_assert(CFG::NS == 2, "two LDS stages");
   constexpr int BM = CFG::BM, BN = CFG::BN, TM = CFG::TM, TN = CFG::TN, NW = CFG::NW;
   constexpr int BK = CFG::BK, ROWB = CFG::ROWB;
-  constexpr int SB = 2 * (BM + BN) * ROWB;
+  constexpr int SB = (SHARED_B ? 2 * BM + BN : 2 * (BM + BN)) * ROWB;
   constexpr int LDS = 2 * SB > EPI::LDS_BYTES ? 2 * SB : EPI::LDS_BYTES;
   static_assert(2 * SB <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char smem[LDS];
@@ -787,7 +788,7 @@ __global__ __launch_bounds__(CFG::NT) void k_gemm_dtl_dual(GemmArgs p, typename 
   const int64_t kmin = uni64(t.kbeg), kend = uni64(t.kend);
   const int64_t kbeg = kmin & ~(int64_t)63;
   const int64_t nk = kend > kmin ? (kend - kbeg + BK - 1) / BK : 0;
-  const bool share_b = p.B2 == p.B;
+  const bool share_b = SHARED_B || p.B2 == p.B;
   const bf16_t* abase = (const bf16_t*)uni64((int64_t)(p.A + m0 * p.lda));
   const bf16_t* a2base = (const bf16_t*)uni64((int64_t)(p.A2 + m0 * p.lda));
   const bf16_t* bbase = (const bf16_t*)uni64((int64_t)(p.B + n0 * p.ldb));

@@ -362,6 +362,22 @@ static KLFused kl_fused_plan(int64_t N, int64_t d, int64_t V, int n_chunks, char
   return P;
 }
 
+// Tiles of the fused passes: with one head for both sides (a tied head, as in the LM
+// step) 128 positions x 256 vocab columns, whose stage (A | B | A2, 64 KB) carries half
+// the operand bytes per MFMA of the 128 x 128 tile; with two heads 128 x 128.
+typedef DtlCfg<128, 256, 4, 2, 2> CfgKLWide;
+static int64_t kl_tiles(const KLChunks& K, int64_t V, int bn) {
+  int64_t n = 0;
+  for (int64_t c = 0; c < K.nc; ++c) n += cdiv(K.width(c, V), bn);
+  return n;
+}
+template <class CFG, bool SHARED, class EPI>
+static void kl_dual_launch(const GemmArgs& a, const typename EPI::Args& ea, int64_t d, hipStream_t s) {
+  const dim3 grid((unsigned)cdiv(a.N, CFG::BN), (unsigned)cdiv(a.M, CFG::BM));
+  if (d % CFG::BK) hipLaunchKernelGGL((k_gemm_dtl_dual<CFG, true, EPI, SHARED>), grid, dim3(CFG::NT), 0, s, a, ea);
+  else hipLaunchKernelGGL((k_gemm_dtl_dual<CFG, false, EPI, SHARED>), grid, dim3(CFG::NT), 0, s, a, ea);
+}
+
 static int kl_fused_fits(int64_t N, int64_t d, int64_t V) {
   return cdiv(N, CfgDtl::BM) <= 65535 && dtl_fits(N, d, V, d) && cdiv(d, 64) <= 65535 && cdiv(V, 64) <= 65535;
 }
@@ -391,6 +407,9 @@ int pd_streamed_kl_fwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks,
     if (!workspace || workspace_bytes < kl_fused_plan(N, d, V, n_chunks, nullptr).total)
       return fail(PD_EWORKSPACE, "pd_streamed_kl_fwd: workspace too small");
     const KLFused F = kl_fused_plan(N, d, V, n_chunks, (char*)workspace);
+    const bool shared = head_masked == head_clean;
+    const int bn = shared ? CfgKLWide::BN : CfgDtl::BN;
+    const int64_t n_tiles = kl_tiles(K, V, bn);  // <= F.n_tiles (the plan counts 128-wide tiles)
     int64_t tile_base = 0;
     for (int64_t c = 0; c < K.nc; ++c) {
       const int64_t w = K.width(c, V);
@@ -398,15 +417,12 @@ int pd_streamed_kl_fwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks,
       const bf16_t* hm = (const bf16_t*)head_masked + c * K.cw * d;
       GemmArgs a{N, w, d, (const bf16_t*)act_clean, d, hc, d, nullptr, 0, 1.f, 0.f, nullptr, 0, 0, 0, 0,
                  (const bf16_t*)act_masked, hm, nullptr};
-      const dim3 grid((unsigned)cdiv(w, CfgDtl::BN), (unsigned)cdiv(N, CfgDtl::BM));
-      const EpiKLStats::Args ea{F.part, F.n_tiles, tile_base};
-      if (d % CfgDtl::BK)
-        hipLaunchKernelGGL((k_gemm_dtl_dual<CfgDtl, true, EpiKLStats>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
-      else
-        hipLaunchKernelGGL((k_gemm_dtl_dual<CfgDtl, false, EpiKLStats>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
-      tile_base += cdiv(w, CfgDtl::BN);
+      const EpiKLStats::Args ea{F.part, n_tiles, tile_base};
+      if (shared) kl_dual_launch<CfgKLWide, true, EpiKLStats>(a, ea, d, s);
+      else kl_dual_launch<CfgDtl, false, EpiKLStats>(a, ea, d, s);
+      tile_base += cdiv(w, bn);
     }
-    hipLaunchKernelGGL(k_kl_merge, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, F.part, N, F.n_tiles, stats,
+    hipLaunchKernelGGL(k_kl_merge, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, F.part, N, n_tiles, stats,
                        position_kl);
     return check_launch("pd_streamed_kl_fwd");
   }
@@ -452,12 +468,9 @@ int pd_streamed_kl_bwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks,
       const bf16_t* hm = (const bf16_t*)head_masked + c * K.cw * d;
       GemmArgs a{N, w, d, (const bf16_t*)act_clean, d, hc, d, nullptr, 0, 1.f, 0.f, nullptr, 0, 0, 0, 0,
                  (const bf16_t*)act_masked, hm, nullptr};
-      const dim3 grid((unsigned)cdiv(w, CfgDtl::BN), (unsigned)cdiv(N, CfgDtl::BM));
       const EpiKLGrad::Args ea{stats, g_position, F.G, K.cw, w, kpad};
-      if (d % CfgDtl::BK)
-        hipLaunchKernelGGL((k_gemm_dtl_dual<CfgDtl, true, EpiKLGrad>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
-      else
-        hipLaunchKernelGGL((k_gemm_dtl_dual<CfgDtl, false, EpiKLGrad>), grid, dim3(CfgDtl::NT), 0, s, a, ea);
+      if (head_masked == head_clean) kl_dual_launch<CfgKLWide, true, EpiKLGrad>(a, ea, d, s);
+      else kl_dual_launch<CfgDtl, false, EpiKLGrad>(a, ea, d, s);
       // d_act (+)= G [N, kpad] @ (head^T [d, c cw + kpad))^T
       if ((rc = pd_gemm(PD_DTYPE_BF16, N, d, kpad, F.G, K.cw, 0, F.hT + c * K.cw, F.Vp, 1, d_act_masked, d,
                         PD_DTYPE_F32, 1.f, c == 0 ? 0.f : 1.f, stream)))

@@ -748,17 +748,26 @@ def test_grouped_gemm_mn_rhs_multistage(device, K):
 # ------------------------------------------------------------------ streamed-vocab KL
 
 
-@pytest.mark.parametrize("dtype,n_chunks,V,d", [(torch.float32, 1, 1200, 64), (torch.float32, 3, 1200, 64),
-                                                (torch.float32, 8, 1200, 64), (torch.bfloat16, 8, 4096, 128),
-                                                (torch.bfloat16, 2, 4096, 128), (torch.bfloat16, 3, 4101, 128),
-                                                (torch.bfloat16, 1, 2011, 128), (torch.bfloat16, 3, 999, 72)])
-def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V, d):
+@pytest.mark.parametrize("dtype,n_chunks,V,d,shared", [(torch.float32, 1, 1200, 64, False),
+                                                       (torch.float32, 3, 1200, 64, False),
+                                                       (torch.float32, 8, 1200, 64, False),
+                                                       (torch.bfloat16, 8, 4096, 128, False),
+                                                       (torch.bfloat16, 2, 4096, 128, False),
+                                                       (torch.bfloat16, 3, 4101, 128, False),
+                                                       (torch.bfloat16, 1, 2011, 128, False),
+                                                       (torch.bfloat16, 3, 999, 72, False),
+                                                       (torch.bfloat16, 3, 4101, 128, True),
+                                                       (torch.bfloat16, 1, 2011, 128, True),
+                                                       (torch.bfloat16, 3, 999, 72, True)])
+def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V, d, shared):
     """Per-position KL and the masked-activation gradient against the float64 oracle on
     the same (dtype-rounded) inputs. fp32: |err| <= 1e-4 |want| + 2e-6 max|want| (fp32
     logits accumulated over d, exp/log in fp32). bf16: the gradient's (q - p) g passes
     through bf16 on its way into the GEMM, so rtol 2e-2. V = 4101 (3 x 1367) and 2011 (prime)
     give bf16 chunk widths that are not multiples of 8: the kernels stream 8-aligned chunks
-    and a ragged last one (the reference's LM vocab 50277 = 3 x 16759 is such a case)."""
+    and a ragged last one (the reference's LM vocab 50277 = 3 x 16759 is such a case).
+    `shared`: one head tensor for both sides (a tied head), the bf16 passes' 128 x 256
+    tiles."""
     from param_decomp_amd.losses import streamed_kl_per_position, streamed_position_kl
 
     rng = np.random.default_rng(n_chunks + V)
@@ -767,7 +776,7 @@ def test_streamed_kl_fwd_bwd(device, dtype, n_chunks, V, d):
     aq = cast(rng.normal(size=(N, d)) * 0.5).requires_grad_(True)
     ap = cast(rng.normal(size=(N, d)) * 0.5)
     hq = cast(rng.normal(size=(V, d)) * 0.3)
-    hp = cast(rng.normal(size=(V, d)) * 0.3)
+    hp = hq if shared else cast(rng.normal(size=(V, d)) * 0.3)
     kl = streamed_position_kl(aq, hq, ap, hp, n_chunks)
     want, _ = po.streamed_position_kl(np64(aq), np64(hq), np64(ap), np64(hp), n_chunks)
     if dtype == torch.float32:
