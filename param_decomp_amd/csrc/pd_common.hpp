@@ -65,11 +65,13 @@ int router_topk(const float* logits, int64_t T, int E, int k, bool round_bf16, f
 // the contraction split into slices when the output alone has too few tiles to occupy
 // the GPU: each slice's fp32 partial goes to `ws` and a second pass adds the slices in
 // order (deterministic), writing C (+ beta * C) in c_dtype. gemm_splitk_ws_bytes gives the
-// scratch the same call needs (0: no split; the call then needs no scratch).
-size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K);
+// scratch the same call needs (0: no split; the call then needs no scratch). `splits` > 0
+// asks for that many slices (each a multiple of 64 deep) instead of the tile-count rule.
+size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K, int splits = 0);
 // The same for any operand layouts (trans_a / trans_b as pd_gemm's).
 int gemm_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B, int64_t ldb,
-                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream);
+                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream,
+                int splits = 0);
 int gemm_nt_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* Bt, int64_t ldb, void* C,
                    int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream);
 

@@ -673,8 +673,10 @@ int grouped_gemm(const void* lhs, const void* rhs, const int32_t* offsets, int64
 
 // ---------------------------------------------------------------- split contraction
 // Slices: enough (tiles x slices >= 512, two blocks per CU) when the output has fewer than
-// 384 128x128 tiles, each slice at least 512 deep, at most 16 slices.
-static int64_t splitk_slice(int64_t M, int64_t N, int64_t K) {
+// 384 128x128 tiles, each slice at least 512 deep, at most 16 slices; or the caller's
+// count (`splits` > 0).
+static int64_t splitk_slice(int64_t M, int64_t N, int64_t K, int splits_req = 0) {
+  if (splits_req > 0) return splits_req < 2 || K < 2 * 64 ? 0 : cdiv(cdiv(K, splits_req), 64) * 64;
   const int64_t tiles = cdiv(M, CfgDtlRA::BM) * cdiv(N, CfgDtlRA::BN);
   if (tiles >= 384 || K < 1024) return 0;
   int64_t splits = std::min<int64_t>(std::min<int64_t>(cdiv(512, tiles), K / 512), 16);
@@ -682,8 +684,8 @@ static int64_t splitk_slice(int64_t M, int64_t N, int64_t K) {
   return cdiv(cdiv(K, splits), 64) * 64;
 }
 
-size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K) {
-  const int64_t kc = splitk_slice(M, N, K);
+size_t gemm_splitk_ws_bytes(int64_t M, int64_t N, int64_t K, int splits) {
+  const int64_t kc = splitk_slice(M, N, K, splits);
   return kc ? (size_t)cdiv(K, kc) * M * N * sizeof(float) : 0;
 }
 
@@ -708,8 +710,9 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 int gemm_splitk(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int trans_a, const void* B, int64_t ldb,
-                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream) {
-  const int64_t kc = splitk_slice(M, N, K);
+                int trans_b, void* C, int64_t ldc, int c_dtype, float beta, void* ws, size_t ws_bytes, void* stream,
+                int splits_req) {
+  const int64_t kc = splitk_slice(M, N, K, splits_req);
   if (!kc || N % 4 || ldc % 4 || !aligned16(C))
     return pd_gemm(PD_DTYPE_BF16, M, N, K, A, lda, trans_a, B, ldb, trans_b, C, ldc, c_dtype, 1.f, beta, stream);
   const bool a_kmaj = !trans_a, b_kmaj = trans_b;

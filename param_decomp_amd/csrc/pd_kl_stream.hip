@@ -338,9 +338,31 @@ struct KLFused {
   float* part;  // [N, n_tiles, 5]
   bf16_t* G;    // [N, cw]
   bf16_t* hT;   // [d, Vp], Vp = V rounded up to 8
+  float* sk;    // the input-gradient product's contraction slices
   int64_t n_tiles, Vp;
-  size_t total;
+  int splits;
+  size_t sk_bytes, total;
 };
+
+// Contraction slices of the input-gradient product d_act += G @ head: its N x d output has
+// few 128 x 128 tiles (384 at 8192 x 768: three quarters of one round of two blocks per
+// CU), so it is split into the fewest slices (at most 8, each at least 1024 deep) that
+// fill whole rounds to 90%.
+static int kl_dact_splits(int64_t N, int64_t d, int64_t kw) {
+  const int64_t tiles = cdiv(N, 128) * cdiv(d, 128);
+  int best = 1;
+  double best_eff = 0.0;
+  for (int sp = 1; sp <= 8 && (sp == 1 || kw / sp >= 1024); ++sp) {
+    const int64_t work = tiles * sp;
+    const double eff = (double)work / (double)(cdiv(work, 512) * 512);
+    if (eff > best_eff + 1e-9) {
+      best = sp;
+      best_eff = eff;
+    }
+    if (eff >= 0.9) break;
+  }
+  return best;
+}
 
 static KLFused kl_fused_plan(int64_t N, int64_t d, int64_t V, int n_chunks, char* base) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -358,6 +380,10 @@ static KLFused kl_fused_plan(int64_t N, int64_t d, int64_t V, int n_chunks, char
   // + 64 columns: the input-gradient product reads each chunk's k range in 64-wide
   // stages from a column offset, so its last row may read up to 63 elements past hT
   off += up((size_t)d * P.Vp * 2 + 64 * 2);
+  P.splits = kl_dact_splits(N, d, (K.cw + 7) & ~(int64_t)7);
+  P.sk_bytes = P.splits > 1 ? gemm_splitk_ws_bytes(N, d, (K.cw + 7) & ~(int64_t)7, P.splits) : 0;
+  P.sk = (float*)(base + off);
+  off += up(P.sk_bytes);
   P.total = off;
   return P;
 }
@@ -472,8 +498,8 @@ int pd_streamed_kl_bwd(int dtype, int64_t N, int64_t d, int64_t V, int n_chunks,
       if (head_masked == head_clean) kl_dual_launch<CfgKLWide, true, EpiKLGrad>(a, ea, d, s);
       else kl_dual_launch<CfgDtl, false, EpiKLGrad>(a, ea, d, s);
       // d_act (+)= G [N, kpad] @ (head^T [d, c cw + kpad))^T
-      if ((rc = pd_gemm(PD_DTYPE_BF16, N, d, kpad, F.G, K.cw, 0, F.hT + c * K.cw, F.Vp, 1, d_act_masked, d,
-                        PD_DTYPE_F32, 1.f, c == 0 ? 0.f : 1.f, stream)))
+      if ((rc = gemm_splitk(N, d, kpad, F.G, K.cw, 0, F.hT + c * K.cw, F.Vp, 1, d_act_masked, d, PD_DTYPE_F32,
+                            c == 0 ? 0.f : 1.f, F.sk, F.sk_bytes, stream, F.splits)))
         return rc;
     }
     return check_launch("pd_streamed_kl_bwd");
