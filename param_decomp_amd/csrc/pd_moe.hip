@@ -302,12 +302,26 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
                                                        float* __restrict__ imp_partial) {
   __shared__ float red[4];
   __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
+  // the tile's 64 rows: slot, the token's delta, routed flag and (source tables) the expert
+  // group, looked up once per row by the first wave instead of in every pass of every lane
+  __shared__ int4 rows[TILE];
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
   const int64_t n = a.J * a.c;
   const bool qok = q0 + q4 < a.c;
   if constexpr (PM == PM_SL0) sl0_tile_groups(SLv, a.offsets, a.E, j0, a.J, tid);
+  if (tid < TILE) {
+    const int64_t j = j0 + tid;
+    int4 v = make_int4(0, 0, 0, 0);
+    if (j < a.J) {
+      const int32_t slot = a.sort_idx[j];
+      v = make_int4(slot, __float_as_int(job_delta(a, slot)), job_routed(a, slot) ? 1 : 0,
+                    LAYOUT == MASK_SRC ? row_group(a.offsets, a.E, j) : 0);
+    }
+    rows[tid] = v;
+  }
+  __syncthreads();
   float imp = 0.f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
@@ -316,16 +330,17 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
     bf16_t o[4] = {0, 0, 0, 0};
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
-      const int32_t slot = a.sort_idx[j];
+      const int4 row = rows[r];
+      const int32_t slot = row.x;
       const int64_t src = (int64_t)slot * a.c + q0 + q4;
-      const float dt = job_delta(a, slot);
-      const bool routed = job_routed(a, slot);
+      const float dt = __int_as_float(row.y);
+      const bool routed = row.z != 0;
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       uint32_t ub = 0;
-      const int ej = LAYOUT == MASK_SRC ? row_group(a.offsets, a.E, j) : 0;
+      const int ej = row.w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
