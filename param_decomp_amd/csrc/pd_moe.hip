@@ -593,6 +593,18 @@ struct EpiMaskBwd {
     const int col = (int)t.n0 + cc * 8;
     const bool cok = col < p.N;
     bf16_t* dh = (bf16_t*)t.C;
+    // the tile's rows: slot, the token's delta and routed flag, looked up once per row
+    // (visible after the barrier that opens the first image pass)
+    __shared__ int4 jrow[CFG::BM];
+    for (int r = tid; r < CFG::BM; r += CFG::NT) {
+      const int64_t row = t.m0 + r;
+      int4 v = make_int4(0, 0, 0, 0);
+      if (row < t.M) {
+        const int32_t sl = sort_idx[row], tok = sl / kk;
+        v = make_int4(sl, __float_as_int(delta ? delta[tok] : 0.f), !route || route[tok] ? 1 : 0, 0);
+      }
+      jrow[r] = v;
+    }
     // every row of the tile has the tile's expert: one slope chunk per lane
     float slope8[8];
     if constexpr (PM == PM_SL0) {
@@ -617,7 +629,6 @@ struct EpiMaskBwd {
         for (int i = 0; i < G; ++i) {
           row[i] = t.m0 + q * SS::ROWS + rr + (g0 + i) * RPP;
           ok[i] = cok && row[i] < t.M;
-          slot[i] = ok[i] ? sort_idx[row[i]] : 0;
         }
         uint4 pw[G], hw[G];
         uint2 uw[G];
@@ -626,11 +637,13 @@ struct EpiMaskBwd {
 #pragma unroll
         for (int i = 0; i < G; ++i) {
           if (!ok[i]) continue;
+          const int4 jr = jrow[q * SS::ROWS + rr + (g0 + i) * RPP];
+          slot[i] = jr.x;
+          dt[i] = __int_as_float(jr.y);
+          routed[i] = jr.z != 0;
           pw[i] = *(const uint4*)(ci + (int64_t)slot[i] * c + col);
           hw[i] = *(const uint4*)(h + row[i] * c + col);
           uw[i] = uconst < 0.f ? *(const uint2*)(ub + row[i] * c + col) : make_uint2(0u, 0u);
-          dt[i] = delta ? delta[slot[i] / kk] : 0.f;
-          routed[i] = !route || route[slot[i] / kk];
         }
 #pragma unroll
         for (int i = 0; i < G; ++i) {
