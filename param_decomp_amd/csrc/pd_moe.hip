@@ -276,15 +276,38 @@ struct SiteMaskArgs {
 // reads its expert's row of the table, u = src[(t / rps) E c + e c + q], the reference's
 // SourceMaskIngredients, pd/core/masking.py:43-68.)
 
-// The table index of job j's element (q): source row of its token, its expert.
-__device__ inline int64_t src_index(const SiteMaskArgs& a, int32_t slot, int e, int q) {
-  return (((int64_t)(slot / a.k) / a.rps) * a.E + e) * a.c + q;
-}
-
 __device__ inline float job_delta(const SiteMaskArgs& a, int32_t slot) { return a.delta ? a.delta[slot / a.k] : 0.f; }
 // An unrouted token's jobs take the frozen output (pd/core/decomposed_linear.py:72-85):
 // their component coefficients are 0, so their masks get no recon gradient.
 __device__ inline bool job_routed(const SiteMaskArgs& a, int32_t slot) { return !a.route || a.route[slot / a.k]; }
+
+// One row of a 64-row mask tile, looked up once per block by the first wave (instead of
+// in every pass of every lane): the job's token-major slot, its token's delta and routed
+// flag and, with GROUP, its expert group ej and source-table row (t / rps) E + ej.
+struct MaskRow {
+  int32_t slot;
+  float dt;
+  int32_t routed;
+  int32_t ej;
+  int64_t srow;
+};
+template <bool GROUP>
+__device__ inline void fill_mask_rows(MaskRow* rows, const SiteMaskArgs& a, int64_t j0, int tid) {
+  if (tid >= TILE) return;
+  const int64_t j = j0 + tid;
+  MaskRow v{0, 0.f, 0, 0, 0};
+  if (j < a.J) {
+    const int32_t slot = a.sort_idx[j], tok = slot / a.k;
+    v.slot = slot;
+    v.dt = a.delta ? a.delta[tok] : 0.f;
+    v.routed = !a.route || a.route[tok] ? 1 : 0;
+    if constexpr (GROUP) {
+      v.ej = row_group(a.offsets, a.E, j);
+      v.srow = ((int64_t)tok / a.rps) * a.E + v.ej;
+    }
+  }
+  rows[tid] = v;
+}
 
 
 // Thread -> (row (tid >> 4) + 16 * pass, columns q4 .. q4 + 3) of a 64x64 job-space tile.
@@ -302,25 +325,14 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
                                                        float* __restrict__ imp_partial) {
   __shared__ float red[4];
   __shared__ typename std::conditional<PM == PM_SL0, Sl0Tile, NoSl0Tile>::type SLv;
-  // the tile's 64 rows: slot, the token's delta, routed flag and (source tables) the expert
-  // group, looked up once per row by the first wave instead of in every pass of every lane
-  __shared__ int4 rows[TILE];
+  __shared__ MaskRow rows[TILE];
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
   const int64_t n = a.J * a.c;
   const bool qok = q0 + q4 < a.c;
   if constexpr (PM == PM_SL0) sl0_tile_groups(SLv, a.offsets, a.E, j0, a.J, tid);
-  if (tid < TILE) {
-    const int64_t j = j0 + tid;
-    int4 v = make_int4(0, 0, 0, 0);
-    if (j < a.J) {
-      const int32_t slot = a.sort_idx[j];
-      v = make_int4(slot, __float_as_int(job_delta(a, slot)), job_routed(a, slot) ? 1 : 0,
-                    LAYOUT == MASK_SRC ? row_group(a.offsets, a.E, j) : 0);
-    }
-    rows[tid] = v;
-  }
+  fill_mask_rows<LAYOUT == MASK_SRC>(rows, a, j0, tid);
   __syncthreads();
   float imp = 0.f;
 #pragma unroll
@@ -330,17 +342,16 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
     bf16_t o[4] = {0, 0, 0, 0};
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
-      const int4 row = rows[r];
-      const int32_t slot = row.x;
+      const MaskRow row = rows[r];
+      const int32_t slot = row.slot;
       const int64_t src = (int64_t)slot * a.c + q0 + q4;
-      const float dt = __int_as_float(row.y);
-      const bool routed = row.z != 0;
+      const float dt = row.dt;
+      const bool routed = row.routed != 0;
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       uint32_t ub = 0;
-      const int ej = row.w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]);
@@ -350,7 +361,7 @@ __global__ __launch_bounds__(256) void k_mask_fwd_tile(SiteMaskArgs a, const bf1
         if constexpr (LAYOUT == MASK_CONST) {
           u = a.uconst;
         } else if constexpr (LAYOUT == MASK_SRC) {
-          u = src_value(a.src, a.src_dtype, src_index(a, slot, ej, q0 + q4 + e));
+          u = src_value(a.src, a.src_dtype, row.srow * a.c + q0 + q4 + e);
         } else {
           const uint32_t kb = (draw_bits(a.k0, a.k1, src + e, n, 8, LAYOUT) & 0xFFu) >> 1;
           ub |= kb << (8 * e);
@@ -387,6 +398,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
                                                        const uint8_t* __restrict__ ubits, float imp_scale,
                                                        bf16_t* __restrict__ d_acts, bf16_t* __restrict__ d_pre) {
   __shared__ typename std::conditional<SRC, Sl0Tile, NoSl0Tile>::type SG;
+  __shared__ MaskRow rows[TILE];
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.y * TILE;
   const int q0 = blockIdx.x * TILE, q4 = PD_TILE4_COL;
@@ -397,6 +409,8 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       SG.grp[tid] = j < a.J ? row_group(a.offsets, a.E, j) * (int)a.S + (int)((a.sort_idx[j] / a.k) / a.rps) : -1;
     }
   }
+  fill_mask_rows<SRC || PM == PM_SL0>(rows, a, j0, tid);
+  __syncthreads();
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int r = PD_TILE4_ROW(pass);
@@ -405,21 +419,21 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
     float dmsum = 0.f;
     if (j < a.J && qok) {
       const int64_t idx = j * a.c + q0 + q4;
-      const int32_t slot = a.sort_idx[j];
+      const MaskRow row = rows[r];
+      const int32_t slot = row.slot;
       const int64_t src = (int64_t)slot * a.c + q0 + q4;
-      const float dt = job_delta(a, slot);
+      const float dt = row.dt;
       const uint2 pw = *(const uint2*)(a.ci_pre + src);
       const uint2 hw = *(const uint2*)(h + idx);
-      const uint2 dw = job_routed(a, slot) ? *(const uint2*)(d_acts + idx) : make_uint2(0u, 0u);
+      const uint2 dw = row.routed ? *(const uint2*)(d_acts + idx) : make_uint2(0u, 0u);
       const uint32_t ub = !SRC && a.uconst < 0.f ? *(const uint32_t*)(ubits + idx) : 0u;
-      const int ej = SRC ? row_group(a.offsets, a.E, j) : 0;
       const float pre[4] = {bf_lo(pw.x), bf_hi(pw.x), bf_lo(pw.y), bf_hi(pw.y)};
       const float hv[4] = {bf_lo(hw.x), bf_hi(hw.x), bf_lo(hw.y), bf_hi(hw.y)};
       const float da[4] = {bf_lo(dw.x), bf_hi(dw.x), bf_lo(dw.y), bf_hi(dw.y)};
       bf16_t dp[4];
       float slope4[4] = {imp_scale, imp_scale, imp_scale, imp_scale};
       if constexpr (PM == PM_SL0) {
-        const float4 sl = *(const float4*)(a.slope + (int64_t)row_group(a.offsets, a.E, j) * a.c + q0 + q4);
+        const float4 sl = *(const float4*)(a.slope + (int64_t)row.ej * a.c + q0 + q4);
         slope4[0] = sl.x;
         slope4[1] = sl.y;
         slope4[2] = sl.z;
@@ -429,7 +443,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
         float u;
-        if constexpr (SRC) u = src_value(a.src, a.src_dtype, src_index(a, slot, ej, q0 + q4 + e));
+        if constexpr (SRC) u = src_value(a.src, a.src_dtype, row.srow * a.c + q0 + q4 + e);
         else u = a.uconst < 0.f ? (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f) : a.uconst;
         const float m = lo + (1.f - lo) * u - dt;
         float dimp;
@@ -441,7 +455,7 @@ __global__ __launch_bounds__(256) void k_mask_bwd_tile(SiteMaskArgs a, const bf1
         if constexpr (SRC) {
           dmsum += dm;
           const float gs = dm * (1.f - lo);
-          if (a.rps == 1) a.dsrc[src_index(a, slot, ej, q0 + q4 + e)] = gs;
+          if (a.rps == 1) a.dsrc[row.srow * a.c + q0 + q4 + e] = gs;
           else SG.ps[r][q4 + e] = gs;
         }
       }
