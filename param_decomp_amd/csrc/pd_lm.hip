@@ -238,6 +238,12 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
   const int64_t total = a.N * a.C;
   const bool qok = q0 + q4 < a.C;
   if constexpr (PM == PM_SL0) sl0_tile_groups(SLv, nullptr, 1, n0, a.N, tid);
+  // source tables: each row's table row n / rps, divided once per row instead of per pass
+  __shared__ int srow[LAYOUT == MASK_SRC ? TILE : 1];
+  if constexpr (LAYOUT == MASK_SRC) {
+    if (tid < TILE) srow[tid] = n0 + tid < a.N ? (int)((n0 + tid) / a.rps) : 0;
+    __syncthreads();
+  }
   float imp = 0.f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_fwd(LMMaskArgs a, const bf16_t*
         else imp += powp<PM>(upper_fwd(pre[e]), a.p);
         float u;
         if constexpr (LAYOUT == MASK_SRC) {
-          u = src_value(a.src, a.src_dtype, (n / a.rps) * a.C + q0 + q4 + e);
+          u = src_value(a.src, a.src_dtype, (int64_t)srow[r] * a.C + q0 + q4 + e);
         } else {
           const uint32_t kb = (draw_bits(a.k0, a.k1, idx + e, total, 8, LAYOUT) & 0xFFu) >> 1;
           ub |= kb << (8 * e);
@@ -304,6 +310,7 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
   const bool qok = q0 + q4 < a.C;
   if constexpr (SRC) {
     if (tid < 64) SG.grp[tid] = n0 + tid < a.N ? (int)((n0 + tid) / a.rps) : -1;  // each row's source row
+    __syncthreads();
   }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
@@ -333,8 +340,9 @@ __global__ __launch_bounds__(256) void k_lm_mask_bwd(LMMaskArgs a, const bf16_t*
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = lower_fwd(pre[e]), up = upper_fwd(pre[e]);
-        const float u = SRC ? src_value(a.src, a.src_dtype, (n / a.rps) * a.C + q0 + q4 + e)
-                            : (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
+        float u;
+        if constexpr (SRC) u = src_value(a.src, a.src_dtype, (int64_t)SG.grp[r] * a.C + q0 + q4 + e);
+        else u = (float)((ub >> (8 * e)) & 0xFFu) * (1.f / 128.f);
         const float m = lo + (1.f - lo) * u - dt;
         float dimp;
         if constexpr (PM == PM_SL0) dimp = slope4[e] * sl0_dpsi(up, a.g2, a.psis);
